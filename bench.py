@@ -1,0 +1,188 @@
+"""Decode benchmark: Llama-3.2-3B-architecture Q8_0, batch 1, one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config llama-3.2-3b] [--no-cpu-baseline]
+
+Workload: seeded synthetic N(0, 0.02) weights quantized to
+Q8_0, a 512-token random prompt prefilled (n-1 tokens, as the reference seam does), then
+greedy decode.  A "step" is one decode token through the resident engine's device-side
+loop (embedding gather -> 28 layers -> lm_head -> argmax fed back on the device).  The
+timed region is exactly K steps, bracketed by device synchronisation; weights, KV cache
+and the token live in HBM throughout.
+
+Prints one JSON line with the metric, the live roofline of the dominant kernel (the Q8_0
+GEMV, HIP events on the engine's stream over a second pass of the same K steps) and the
+CPU baseline (the C++ restatement of Camelid's CPU forward, timed on this host).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD published peak
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(model, cfg, prompt_len: int, n_steps: int, threads: int) -> dict:
+    """Oracle (C++ restatement of Camelid's CPU path) decode steps at the benchmark's
+    positions: KV for the prompt is seeded with f16-rounded random rows, then `n_steps`
+    greedy steps run from position prompt_len-1."""
+    from oracle.oracle import OracleModel
+    os.environ.setdefault("OMP_NUM_THREADS", str(threads))
+    orc = OracleModel(model, prompt_len + n_steps + 1)
+    rng = np.random.default_rng(0)
+    n = prompt_len - 1
+    for layer in range(cfg.n_layers):
+        k = rng.normal(0, 1, (cfg.n_kv_heads, n, cfg.head_dim)).astype(np.float32)
+        v = rng.normal(0, 1, (cfg.n_kv_heads, n, cfg.head_dim)).astype(np.float32)
+        orc.seed_kv(layer, k, v)
+    tok = 1
+    t0 = time.perf_counter()
+    for i in range(n_steps):
+        tok, _, _ = orc.forward(tok, n + i)
+    dt = time.perf_counter() - t0
+    orc.close()
+    return {"value": round(n_steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n_steps} greedy decode steps of the same {cfg.name} Q8_0 model at positions "
+                      f"{n}..{n + n_steps - 1} (KV history seeded), oracle/camelid_oracle.cpp, "
+                      f"{threads} OpenMP threads over output rows"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--config", default="llama-3.2-3b")
+    ap.add_argument("--prompt", type=int, default=None, help="prompt length (default: the config's)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=6)
+    ap.add_argument("--no-profile", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the resident decode path runs on a single MI355X with no "
+              "sharding or collectives (multi-GPU sharding is a design note, not a measured path).",
+              file=sys.stderr)
+        return 2
+
+    from camelid_amd.engine import device_info
+    from camelid_amd.model import CONFIGS, ResidentSession, SyntheticModel, prompt_tokens
+
+    cfg = CONFIGS[args.config]
+    P = args.prompt or cfg.prompt_len
+    K, W = args.steps, args.warmup
+    dev_name, n_cu = device_info()
+    log(f"device {dev_name}, {n_cu} CUs; config {cfg.name}: prompt {P}, warmup {W}, steps {K}")
+
+    t0 = time.perf_counter()
+    model = SyntheticModel.generate(cfg)
+    log(f"generated synthetic Q8_0 weights in {time.perf_counter() - t0:.1f}s")
+    prompt = prompt_tokens(cfg, P)
+    max_pos = P + W + K
+    t0 = time.perf_counter()
+    sess = ResidentSession(model, max_pos, device_loop=True)
+    eng = sess.engine
+    log(f"uploaded weights in {time.perf_counter() - t0:.1f}s")
+
+    # prefill of the first P-1 prompt tokens (inference.rs:4411), timed separately
+    t0 = time.perf_counter()
+    sess.prefill(prompt[:-1])
+    prefill_s = time.perf_counter() - t0
+    log(f"prefill {P - 1} tokens: {prefill_s:.3f}s")
+
+    pos0 = P - 1
+    warm = eng.generate(int(prompt[-1]), pos0, W, cfg.scale()) if W else np.array([prompt[-1]], np.uint32)
+    last = int(warm[-1]) if W else int(prompt[-1])
+    start_pos = pos0 + W
+    from camelid_amd import _native as N
+    N.check(N.lib().camelid_hip_synchronize())
+    t0 = time.perf_counter()
+    toks = eng.generate(last, start_pos, K, cfg.scale())
+    N.check(N.lib().camelid_hip_synchronize())
+    dt = time.perf_counter() - t0
+    tok_s = K / dt
+    log(f"decode {K} steps: {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
+
+    # algorithmic bytes of the timed steps (positions start_pos .. start_pos+K-1)
+    total_bytes = sum(cfg.decode_bytes(p) for p in range(start_pos, start_pos + K))
+    hbm_frac = total_bytes / dt / (HBM_PEAK_GBS * 1e9)
+
+    # parity: the stream must equal the oracle's golden stream when one exists
+    stream = [int(t) for t in (list(warm) if W else [])] + [int(t) for t in toks]
+    parity = None
+    gold = ROOT / "tests" / "golden" / f"{cfg.name}_p{P}_d{cfg.decode_len}.json"
+    if gold.exists():
+        g = json.loads(gold.read_text())
+        n = min(len(stream), len(g["tokens"]))
+        parity = {"golden": gold.name, "compared": n, "identical": stream[:n] == g["tokens"][:n]}
+        log(f"token parity vs golden: {parity}")
+
+    roofline = None
+    prof = None
+    if not args.no_profile:
+        eng.set_filled(start_pos)
+        eng.profile_begin()
+        toks2 = eng.generate(last, start_pos, K, cfg.scale())
+        prof = eng.profile_end()
+        assert [int(t) for t in toks2] == [int(t) for t in toks], "profiled pass diverged"
+        g = prof["gemv"]
+        achieved = g["bytes"] / (g["ms"] * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "kernel": "k_q8_gemv (all Q8_0 GEMV launches of the timed steps, bytes-weighted)",
+                    "avg_launch_us": round(g["ms"] * 1e3 / max(g["launches"], 1), 3),
+                    "launches": g["launches"]}
+        log("per-kernel (profiled pass): " + ", ".join(
+            f"{k} {v['ms']:.2f}ms/{v['launches']}" for k, v in prof.items()))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        log(f"CPU baseline: {args.cpu_steps} oracle decode steps on {threads} threads")
+        cpu = cpu_baseline(model, cfg, P, args.cpu_steps, threads)
+        log(f"CPU baseline {cpu['value']} tok/s")
+
+    out = {
+        "metric": "decode tok/s & % of HBM roofline, Llama-3.2-3B-arch Q8_0, batch 1, 1 MI355X",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(dt * 1e3 / K, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8xint8->int32, f32 accumulate (Q8_0)",
+        "data": "synthetic: seeded N(0,0.02) weights quantized to Q8_0, random prompt ids",
+        "config": {"workload": f"{cfg.name} Q8_0 greedy decode, batch 1, {P}-token prompt, "
+                               f"steps at positions {start_pos}..{start_pos + K - 1}",
+                   "prompt_len": P, "decode_steps": K, "device": dev_name},
+        "hbm_roofline_frac": round(hbm_frac, 4),
+        "bytes_per_token": round(total_bytes / K),
+        "prefill_tok_s": round((P - 1) / prefill_s, 2),
+        "parity": parity,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    if prof:
+        out["kernels_ms"] = {k: round(v["ms"], 3) for k, v in prof.items()}
+    print(json.dumps(out), flush=True)
+    sess.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

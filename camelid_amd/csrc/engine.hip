@@ -1,0 +1,863 @@
+// engine.hip -- resident decode engine for MI355X (gfx950) behind the C ABI of
+// include/camelid_hip.h.  Mirrors CudaResidentDecode (src/cuda_resident.rs:5398-8857):
+// weights and the f16 KV cache stay in HBM; one HIP stream; one host sync per call.
+//
+// Device memory layout (all resident for the engine's lifetime):
+//   per layer: Wqkv (Q8R, rows nq+2*nkv), Wo (Q8R), Wgate|up (Q8R, rows 2F), Wdown (Q8R),
+//              attn/ffn norm [H], optional q/k norm [hd]
+//   lm_head Q8R [V][H], final norm [H], optional token_embd Q8R [V][H]
+//   KV cache f16 [L][n_kv][max_pos][hd] (K and V separately)
+//   activations: h [H] (residual stream), qkv, qrot, att [nq], gu [2F], logits [V],
+//                one Q8_0 activation buffer (quants + f32 scales) reused by every GEMV
+#include <hip/hip_runtime.h>
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/camelid_hip.h"
+#include "kernels_decode.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Q8Mat {
+  int8_t* q = nullptr;
+  uint16_t* d = nullptr;
+  uint32_t rows = 0, k = 0;
+};
+
+struct LayerW {
+  Q8Mat qkv, o, gu, down;
+  float* attn_norm = nullptr;
+  float* ffn_norm = nullptr;
+  float* q_norm = nullptr;
+  float* k_norm = nullptr;
+  bool set = false;
+};
+
+constexpr int kGemvRW = 4;        // rows per wave in the faithful GEMV
+constexpr int kGemvRowsPerWG = 4 * kGemvRW;
+
+size_t gemv_lds_bytes(uint32_t k) { return (size_t)4 * kGemvRW * (k / 32 + 1) * sizeof(float); }
+
+}  // namespace
+
+struct camelid_hip_engine {
+  camelid_hip_dims d{};
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::vector<LayerW> layers;
+  Q8Mat out;
+  float* out_norm = nullptr;
+  bool out_set = false;
+  Q8Mat embd;
+  bool embd_set = false;
+  uint16_t* kc = nullptr;
+  uint16_t* vc = nullptr;
+  float *h = nullptr, *qkv = nullptr, *qrot = nullptr, *att = nullptr, *gu = nullptr;
+  float *logits = nullptr, *hidden_cap = nullptr, *xs = nullptr;
+  float *cos_cur = nullptr, *sin_cur = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
+  uint32_t rope_rows = 0;
+  int8_t* xq = nullptr;
+  uint32_t *d_pos = nullptr, *d_tok = nullptr, *d_tokens = nullptr;
+  // pinned host staging
+  float *p_emb = nullptr, *p_cos = nullptr, *p_sin = nullptr, *p_logits = nullptr;
+  uint32_t *p_tok = nullptr, *p_pos = nullptr;
+  uint32_t filled = 0;
+  uint32_t cur_pos = 0;  // host copy of the position being computed (profiling byte counts)
+  bool capture = false;
+  // optional per-launch HIP-event timing (camelid_hip_profile_*)
+  bool profiling = false;
+  struct Rec { int cat; double bytes; hipEvent_t a, b; };
+  std::vector<Rec> recs;
+  std::vector<hipEvent_t> event_pool;
+  size_t pool_next = 0;
+  std::string err;
+  std::vector<void*> dev_allocs;
+  std::vector<void*> host_allocs;
+};
+
+namespace {
+
+int fail(camelid_hip_engine* e, const std::string& msg) {
+  if (e) e->err = msg;
+  g_last_error = msg;
+  return 1;
+}
+
+#define HIP_TRY(eng, expr)                                                                \
+  do {                                                                                    \
+    hipError_t _st = (expr);                                                              \
+    if (_st != hipSuccess)                                                                \
+      return fail((eng), std::string(#expr) + " failed: " + hipGetErrorString(_st));      \
+  } while (0)
+
+template <typename T>
+int dev_alloc(camelid_hip_engine* e, T** p, size_t count) {
+  void* v = nullptr;
+  size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+  hipError_t st = hipMalloc(&v, bytes);
+  if (st != hipSuccess) return fail(e, std::string("hipMalloc(") + std::to_string(bytes) + ") failed: " + hipGetErrorString(st));
+  e->dev_allocs.push_back(v);
+  *p = static_cast<T*>(v);
+  return 0;
+}
+
+template <typename T>
+int host_alloc(camelid_hip_engine* e, T** p, size_t count) {
+  void* v = nullptr;
+  hipError_t st = hipHostMalloc(&v, std::max<size_t>(count * sizeof(T), 64), hipHostMallocDefault);
+  if (st != hipSuccess) return fail(e, std::string("hipHostMalloc failed: ") + hipGetErrorString(st));
+  e->host_allocs.push_back(v);
+  *p = static_cast<T*>(v);
+  return 0;
+}
+
+uint16_t read_le16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+// Repack rows [r0, r1) of a 34/36-byte-block Q8_0 matrix into the Q8R planes.
+void repack_rows(const uint8_t* src, size_t r0, size_t r1, size_t k, uint8_t layout, int8_t* q,
+                 uint16_t* d) {
+  const size_t nb = k / 32;
+  for (size_t r = r0; r < r1; ++r) {
+    for (size_t b = 0; b < nb; ++b) {
+      const uint8_t* blk = src + (r * nb + b) * layout;
+      uint16_t bits;
+      if (layout == 34) {
+        bits = read_le16(blk);
+      } else {
+        float f;
+        std::memcpy(&f, blk, 4);
+        bits = cm::f32_to_f16_bits(f);  // exact: the f32 scale was decoded from an f16
+      }
+      d[r * nb + b] = bits;
+      std::memcpy(q + r * k + b * 32, blk + (layout == 34 ? 2 : 4), 32);
+    }
+  }
+}
+
+void repack_parallel(const uint8_t* src, size_t rows, size_t k, uint8_t layout, int8_t* q,
+                     uint16_t* d) {
+  unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  if (rows < 4096) nt = 1;
+  std::vector<std::thread> th;
+  for (unsigned t = 0; t < nt; ++t) {
+    size_t r0 = rows * t / nt, r1 = rows * (t + 1) / nt;
+    th.emplace_back(repack_rows, src, r0, r1, k, layout, q, d);
+  }
+  for (auto& x : th) x.join();
+}
+
+// Upload `parts` (stacked row-wise) as one Q8R matrix.
+struct Part {
+  const uint8_t* src;
+  size_t len;
+  uint32_t rows;
+};
+
+int upload_q8(camelid_hip_engine* e, Q8Mat* m, const std::vector<Part>& parts, uint32_t k,
+              uint8_t layout) {
+  if (layout != 34 && layout != 36) return fail(e, "q8_layout must be 34 or 36");
+  if (k % 32 != 0) return fail(e, "Q8_0 row width must be a multiple of 32");
+  uint32_t rows = 0;
+  for (const Part& p : parts) {
+    if (!p.src) return fail(e, "missing projection bytes");
+    size_t want = (size_t)p.rows * (k / 32) * layout;
+    if (p.len != want)
+      return fail(e, "projection byte length " + std::to_string(p.len) + " != expected " + std::to_string(want));
+    rows += p.rows;
+  }
+  const size_t nb = k / 32;
+  std::vector<int8_t> q((size_t)rows * k);
+  std::vector<uint16_t> d((size_t)rows * nb);
+  size_t r = 0;
+  for (const Part& p : parts) {
+    repack_parallel(p.src, p.rows, k, layout, q.data() + r * k, d.data() + r * nb);
+    r += p.rows;
+  }
+  if (!m->q) {
+    if (dev_alloc(e, &m->q, q.size()) || dev_alloc(e, &m->d, d.size())) return 1;
+  } else if (m->rows != rows || m->k != k) {
+    return fail(e, "matrix shape changed on re-upload");
+  }
+  m->rows = rows;
+  m->k = k;
+  HIP_TRY(e, hipMemcpy(m->q, q.data(), q.size(), hipMemcpyHostToDevice));
+  HIP_TRY(e, hipMemcpy(m->d, d.data(), d.size() * 2, hipMemcpyHostToDevice));
+  return 0;
+}
+
+int upload_f32(camelid_hip_engine* e, float** dst, const float* src, size_t n) {
+  if (!*dst && dev_alloc(e, dst, n)) return 1;
+  HIP_TRY(e, hipMemcpy(*dst, src, n * 4, hipMemcpyHostToDevice));
+  return 0;
+}
+
+// ---------------------------------------------------------------- profiling
+hipEvent_t next_event(camelid_hip_engine* e) {
+  if (e->pool_next == e->event_pool.size()) {
+    hipEvent_t ev;
+    if (hipEventCreate(&ev) != hipSuccess) return nullptr;
+    e->event_pool.push_back(ev);
+  }
+  return e->event_pool[e->pool_next++];
+}
+
+// Brackets one launch with events when profiling; `bytes` = algorithmic bytes of the launch.
+struct ProfScope {
+  camelid_hip_engine* e;
+  int cat;
+  double bytes;
+  hipEvent_t a = nullptr;
+  ProfScope(camelid_hip_engine* eng, int c, double b) : e(eng), cat(c), bytes(b) {
+    if (e && e->profiling) {
+      a = next_event(e);
+      if (a) (void)hipEventRecord(a, e->stream);
+    }
+  }
+  ~ProfScope() {
+    if (a) {
+      hipEvent_t b = next_event(e);
+      if (b) {
+        (void)hipEventRecord(b, e->stream);
+        e->recs.push_back({cat, bytes, a, b});
+      }
+    }
+  }
+};
+
+double q8_bytes(const Q8Mat& m) { return (double)m.rows * m.k * 34.0 / 32.0 + m.k * 34.0 / 32.0 + m.rows * 4.0; }
+
+// ---------------------------------------------------------------- launches
+void launch_gemv(const Q8Mat& m, const int8_t* xq, const float* xs, float* y, const float* resid,
+                 hipStream_t s) {
+  const uint32_t grid = (m.rows + kGemvRowsPerWG - 1) / kGemvRowsPerWG;
+  hipLaunchKernelGGL(cm::k_q8_gemv<kGemvRW>, dim3(grid), dim3(256), gemv_lds_bytes(m.k), s, m.q, m.d,
+                     (int)m.rows, (int)m.k, xq, xs, y, resid);
+}
+
+void launch_rmsnorm_quant(const float* x, const float* w, uint32_t n, float eps, int8_t* xq, float* xs,
+                          float* y, hipStream_t s) {
+  hipLaunchKernelGGL(cm::k_rmsnorm_quant, dim3(1), dim3(1024), (size_t)n * 4, s, x, w, (int)n, eps, xq,
+                     xs, y);
+}
+
+size_t attn_lds_bytes(const camelid_hip_dims& d) { return ((size_t)d.max_pos + d.head_dim) * 4; }
+
+// One transformer layer at the position held in d_pos (cos/sin: that position's tables).
+// Profiling categories (camelid_hip_profile_read).
+enum { P_GEMV = 0, P_NORM, P_ROPE, P_ATTN, P_SILU, P_HEAD, P_EMBED, P_NCAT };
+
+void gemv(camelid_hip_engine* e, const Q8Mat& m, float* y, const float* resid) {
+  ProfScope ps(e, P_GEMV, q8_bytes(m) + (resid ? m.rows * 4.0 : 0.0));
+  launch_gemv(m, e->xq, e->xs, y, resid, e->stream);
+}
+
+void rmsnorm(camelid_hip_engine* e, const float* w) {
+  const uint32_t n = e->d.hidden;
+  ProfScope ps(e, P_NORM, n * 8.0 + n * 34.0 / 32.0);
+  launch_rmsnorm_quant(e->h, w, n, e->d.eps, e->xq, e->xs, nullptr, e->stream);
+}
+
+void run_layer(camelid_hip_engine* e, uint32_t l, const float* cosv, const float* sinv, float scale) {
+  const camelid_hip_dims& d = e->d;
+  const LayerW& L = e->layers[l];
+  hipStream_t s = e->stream;
+  const double nq = (double)d.n_heads * d.head_dim, nkv = (double)d.n_kv_heads * d.head_dim;
+  rmsnorm(e, L.attn_norm);
+  gemv(e, L.qkv, e->qkv, nullptr);
+  {
+    ProfScope ps(e, P_ROPE, (nq + 2 * nkv) * 4 + nq * 4 + 2 * nkv * 2);
+    hipLaunchKernelGGL(cm::k_rope_kv, dim3(d.n_heads + d.n_kv_heads), dim3(64), 0, s, e->qkv, (int)d.n_heads,
+                       (int)d.n_kv_heads, (int)d.head_dim, (int)d.rope_dim, (int)d.split_half_pairing, cosv, sinv,
+                       L.q_norm, L.k_norm, d.eps, e->qrot, e->kc, e->vc, (int)l, (int)d.max_pos, e->d_pos);
+  }
+  {
+    ProfScope ps(e, P_ATTN, nq * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * 34.0 / 32.0);
+    hipLaunchKernelGGL(cm::k_attn_decode, dim3(d.n_heads), dim3(256), attn_lds_bytes(d), s, e->qrot, e->kc,
+                       e->vc, (int)l, (int)d.n_heads, (int)d.n_kv_heads, (int)d.head_dim, (int)d.max_pos,
+                       e->d_pos, scale, e->att, e->xq, e->xs);
+  }
+  gemv(e, L.o, e->h, e->h);
+  rmsnorm(e, L.ffn_norm);
+  gemv(e, L.gu, e->gu, nullptr);
+  {
+    const uint32_t nbf = d.ffn_dim / 32;
+    ProfScope ps(e, P_SILU, d.ffn_dim * 8.0 + d.ffn_dim * 34.0 / 32.0);
+    hipLaunchKernelGGL(cm::k_silu_mul_quant, dim3((nbf + 63) / 64), dim3(64), 0, s, e->gu, (int)d.ffn_dim,
+                       e->xq, e->xs, nullptr);
+  }
+  gemv(e, L.down, e->h, e->h);
+}
+
+void run_stack(camelid_hip_engine* e, const float* cosv, const float* sinv, float scale) {
+  const camelid_hip_dims& d = e->d;
+  for (uint32_t l = 0; l < d.n_layers; ++l) {
+    if (e->capture)
+      (void)hipMemcpyAsync(e->hidden_cap + (size_t)l * d.hidden, e->h, d.hidden * 4, hipMemcpyDeviceToDevice,
+                           e->stream);
+    run_layer(e, l, cosv, sinv, scale);
+  }
+  if (e->capture)
+    (void)hipMemcpyAsync(e->hidden_cap + (size_t)d.n_layers * d.hidden, e->h, d.hidden * 4,
+                         hipMemcpyDeviceToDevice, e->stream);
+}
+
+void run_head(camelid_hip_engine* e) {
+  const camelid_hip_dims& d = e->d;
+  rmsnorm(e, e->out_norm);
+  gemv(e, e->out, e->logits, nullptr);
+  ProfScope ps(e, P_HEAD, d.vocab * 4.0);
+  hipLaunchKernelGGL(cm::k_argmax, dim3(1), dim3(1024), 0, e->stream, e->logits, (int)d.vocab, e->d_tok);
+}
+
+bool ready(const camelid_hip_engine* e) {
+  if (!e->out_set) return false;
+  for (const LayerW& L : e->layers)
+    if (!L.set) return false;
+  return true;
+}
+
+int check_launch(camelid_hip_engine* e) {
+  hipError_t st = hipGetLastError();
+  if (st != hipSuccess) return fail(e, std::string("kernel launch failed: ") + hipGetErrorString(st));
+  return 0;
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+extern "C" {
+
+const char* camelid_hip_last_error(const camelid_hip_engine* e) {
+  return e ? e->err.c_str() : g_last_error.c_str();
+}
+
+int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** out) {
+  if (!dims || !out) return fail(nullptr, "null argument");
+  *out = nullptr;
+  const camelid_hip_dims& d = *dims;
+  if (!d.n_layers || !d.n_heads || !d.n_kv_heads || !d.head_dim || !d.hidden || !d.ffn_dim || !d.vocab ||
+      !d.max_pos)
+    return fail(nullptr, "all dimensions must be nonzero");
+  if (d.n_heads % d.n_kv_heads) return fail(nullptr, "n_heads must be a multiple of n_kv_heads");
+  if (d.hidden % 32 || d.ffn_dim % 32 || d.head_dim % 32)
+    return fail(nullptr, "hidden, ffn_dim and head_dim must be multiples of 32");
+  if (d.head_dim > 512) return fail(nullptr, "head_dim > 512 is not supported");
+  if (d.rope_dim == 0 || d.rope_dim > d.head_dim || d.rope_dim % 2)
+    return fail(nullptr, "rope_dim must be even and within head_dim");
+  if ((size_t)d.n_heads * d.head_dim % 32) return fail(nullptr, "n_heads*head_dim must be a multiple of 32");
+  if (((size_t)d.max_pos + d.head_dim) * 4 > 160 * 1024)
+    return fail(nullptr, "max_pos too large for the single-pass decode attention");
+  auto* e = new camelid_hip_engine();
+  e->d = d;
+  if (const char* dev = std::getenv("CAMELID_HIP_DEVICE")) e->device = std::atoi(dev);
+  hipError_t st = hipSetDevice(e->device);
+  if (st != hipSuccess) {
+    fail(nullptr, std::string("hipSetDevice failed: ") + hipGetErrorString(st));
+    delete e;
+    return 1;
+  }
+  st = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
+  if (st != hipSuccess) {
+    fail(nullptr, std::string("hipStreamCreate failed: ") + hipGetErrorString(st));
+    delete e;
+    return 1;
+  }
+  e->layers.resize(d.n_layers);
+  const size_t nq = (size_t)d.n_heads * d.head_dim, nkv = (size_t)d.n_kv_heads * d.head_dim;
+  const size_t kv_elems = (size_t)d.n_layers * d.n_kv_heads * d.max_pos * d.head_dim;
+  const size_t act = std::max<size_t>({(size_t)d.hidden, (size_t)d.ffn_dim, nq});
+  const uint32_t half = d.rope_dim / 2;
+  int rc = dev_alloc(e, &e->kc, kv_elems) || dev_alloc(e, &e->vc, kv_elems) || dev_alloc(e, &e->h, d.hidden) ||
+           dev_alloc(e, &e->qkv, nq + 2 * nkv) || dev_alloc(e, &e->qrot, nq) || dev_alloc(e, &e->att, nq) ||
+           dev_alloc(e, &e->gu, 2 * (size_t)d.ffn_dim) || dev_alloc(e, &e->logits, d.vocab) ||
+           dev_alloc(e, &e->hidden_cap, (size_t)(d.n_layers + 1) * d.hidden) || dev_alloc(e, &e->xq, act) ||
+           dev_alloc(e, &e->xs, act / 32) || dev_alloc(e, &e->cos_cur, half) || dev_alloc(e, &e->sin_cur, half) ||
+           dev_alloc(e, &e->d_pos, 1) || dev_alloc(e, &e->d_tok, 1) ||
+           host_alloc(e, &e->p_emb, d.hidden) || host_alloc(e, &e->p_cos, half) || host_alloc(e, &e->p_sin, half) ||
+           host_alloc(e, &e->p_logits, d.vocab) || host_alloc(e, &e->p_tok, 1) || host_alloc(e, &e->p_pos, 1);
+  if (rc) {
+    std::string m = e->err;
+    camelid_hip_engine_free(e);
+    return fail(nullptr, m);
+  }
+  if (attn_lds_bytes(d) > 64 * 1024) {
+    st = hipFuncSetAttribute((const void*)cm::k_attn_decode, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)attn_lds_bytes(d));
+    if (st != hipSuccess) {
+      camelid_hip_engine_free(e);
+      return fail(nullptr, std::string("attention LDS attribute failed: ") + hipGetErrorString(st));
+    }
+  }
+  // A fresh cache reads as zeros (K/V past `filled` are never read).
+  (void)hipMemset(e->kc, 0, kv_elems * 2);
+  (void)hipMemset(e->vc, 0, kv_elems * 2);
+  *out = e;
+  return 0;
+}
+
+void camelid_hip_engine_free(camelid_hip_engine* e) {
+  if (!e) return;
+  (void)hipSetDevice(e->device);
+  if (e->stream) (void)hipStreamSynchronize(e->stream);
+  for (hipEvent_t ev : e->event_pool) (void)hipEventDestroy(ev);
+  for (void* p : e->dev_allocs) (void)hipFree(p);
+  for (void* p : e->host_allocs) (void)hipHostFree(p);
+  if (e->stream) (void)hipStreamDestroy(e->stream);
+  delete e;
+}
+
+int camelid_hip_set_layer(camelid_hip_engine* e, uint32_t layer, const uint8_t* const w[7], const size_t len[7],
+                          const uint8_t quant[7], uint8_t q8_layout, const float* attn_norm, const float* ffn_norm,
+                          const float* q_norm, const float* k_norm) {
+  if (!e) return fail(nullptr, "null engine");
+  if (layer >= e->d.n_layers) return fail(e, "layer index out of range");
+  if (!w || !len || !quant || !attn_norm || !ffn_norm) return fail(e, "null argument");
+  for (int i = 0; i < 7; ++i)
+    if (quant[i] != CAMELID_Q8_0) return fail(e, "only Q8_0 projections are supported by this build");
+  HIP_TRY(e, hipSetDevice(e->device));
+  const camelid_hip_dims& d = e->d;
+  const uint32_t nq = d.n_heads * d.head_dim, nkv = d.n_kv_heads * d.head_dim;
+  LayerW& L = e->layers[layer];
+  if (upload_q8(e, &L.qkv, {{w[0], len[0], nq}, {w[1], len[1], nkv}, {w[2], len[2], nkv}}, d.hidden, q8_layout) ||
+      upload_q8(e, &L.o, {{w[3], len[3], d.hidden}}, nq, q8_layout) ||
+      upload_q8(e, &L.gu, {{w[4], len[4], d.ffn_dim}, {w[5], len[5], d.ffn_dim}}, d.hidden, q8_layout) ||
+      upload_q8(e, &L.down, {{w[6], len[6], d.hidden}}, d.ffn_dim, q8_layout) ||
+      upload_f32(e, &L.attn_norm, attn_norm, d.hidden) || upload_f32(e, &L.ffn_norm, ffn_norm, d.hidden))
+    return 1;
+  if (q_norm && upload_f32(e, &L.q_norm, q_norm, d.head_dim)) return 1;
+  if (k_norm && upload_f32(e, &L.k_norm, k_norm, d.head_dim)) return 1;
+  L.set = true;
+  return 0;
+}
+
+int camelid_hip_set_output(camelid_hip_engine* e, const float* final_norm, const uint8_t* w, size_t len,
+                           uint8_t quant, uint8_t q8_layout) {
+  if (!e) return fail(nullptr, "null engine");
+  if (!final_norm || !w) return fail(e, "null argument");
+  if (quant != CAMELID_Q8_0) return fail(e, "only a Q8_0 output projection is supported by this build");
+  HIP_TRY(e, hipSetDevice(e->device));
+  if (upload_q8(e, &e->out, {{w, len, e->d.vocab}}, e->d.hidden, q8_layout) ||
+      upload_f32(e, &e->out_norm, final_norm, e->d.hidden))
+    return 1;
+  e->out_set = true;
+  return 0;
+}
+
+int camelid_hip_set_embedding(camelid_hip_engine* e, const uint8_t* w, size_t len, uint8_t quant, uint8_t q8_layout) {
+  if (!e) return fail(nullptr, "null engine");
+  if (!w) return fail(e, "null argument");
+  if (quant != CAMELID_Q8_0) return fail(e, "only a Q8_0 token embedding is supported by this build");
+  HIP_TRY(e, hipSetDevice(e->device));
+  if (upload_q8(e, &e->embd, {{w, len, e->d.vocab}}, e->d.hidden, q8_layout)) return 1;
+  e->embd_set = true;
+  return 0;
+}
+
+int camelid_hip_set_rope_table(camelid_hip_engine* e, const float* cos_all, const float* sin_all, uint32_t n_pos) {
+  if (!e) return fail(nullptr, "null engine");
+  if (!cos_all || !sin_all) return fail(e, "null argument");
+  if (n_pos > e->d.max_pos) return fail(e, "rope table longer than max_pos");
+  HIP_TRY(e, hipSetDevice(e->device));
+  const size_t half = e->d.rope_dim / 2;
+  if (!e->rope_cos && (dev_alloc(e, &e->rope_cos, (size_t)e->d.max_pos * half) ||
+                       dev_alloc(e, &e->rope_sin, (size_t)e->d.max_pos * half)))
+    return 1;
+  HIP_TRY(e, hipMemcpy(e->rope_cos, cos_all, (size_t)n_pos * half * 4, hipMemcpyHostToDevice));
+  HIP_TRY(e, hipMemcpy(e->rope_sin, sin_all, (size_t)n_pos * half * 4, hipMemcpyHostToDevice));
+  e->rope_rows = n_pos;
+  return 0;
+}
+
+int camelid_hip_weights_ready(const camelid_hip_engine* e) { return e && ready(e) ? 1 : 0; }
+uint32_t camelid_hip_filled(const camelid_hip_engine* e) { return e ? e->filled : 0; }
+int camelid_hip_set_filled(camelid_hip_engine* e, uint32_t filled) {
+  if (!e) return fail(nullptr, "null engine");
+  if (filled > e->d.max_pos) return fail(e, "filled beyond max_pos");
+  e->filled = filled;
+  return 0;
+}
+uint32_t camelid_hip_max_pos(const camelid_hip_engine* e) { return e ? e->d.max_pos : 0; }
+uint32_t camelid_hip_n_layers(const camelid_hip_engine* e) { return e ? e->d.n_layers : 0; }
+int camelid_hip_uses_kquant(const camelid_hip_engine*) { return 0; }
+
+int camelid_hip_seed_layer(camelid_hip_engine* e, uint32_t layer, const float* ck, const float* cv, uint32_t n_pos) {
+  if (!e) return fail(nullptr, "null engine");
+  if (layer >= e->d.n_layers || n_pos > e->d.max_pos) return fail(e, "seed_layer out of range");
+  if (!ck || !cv) return fail(e, "null argument");
+  HIP_TRY(e, hipSetDevice(e->device));
+  const camelid_hip_dims& d = e->d;
+  std::vector<uint16_t> hk((size_t)n_pos * d.head_dim), hv(hk.size());
+  for (uint32_t h = 0; h < d.n_kv_heads; ++h) {
+    const size_t src = (size_t)h * n_pos * d.head_dim;
+    for (size_t i = 0; i < hk.size(); ++i) {
+      hk[i] = cm::f32_to_f16_bits(ck[src + i]);
+      hv[i] = cm::f32_to_f16_bits(cv[src + i]);
+    }
+    const size_t dst = (((size_t)layer * d.n_kv_heads + h) * d.max_pos) * d.head_dim;
+    HIP_TRY(e, hipMemcpy(e->kc + dst, hk.data(), hk.size() * 2, hipMemcpyHostToDevice));
+    HIP_TRY(e, hipMemcpy(e->vc + dst, hv.data(), hv.size() * 2, hipMemcpyHostToDevice));
+  }
+  return 0;
+}
+
+int camelid_hip_read_kv_layer(camelid_hip_engine* e, uint32_t layer, uint32_t n, float* ck, float* cv) {
+  if (!e) return fail(nullptr, "null engine");
+  if (layer >= e->d.n_layers || n > e->d.max_pos) return fail(e, "read_kv_layer out of range");
+  if (!ck || !cv) return fail(e, "null argument");
+  HIP_TRY(e, hipSetDevice(e->device));
+  HIP_TRY(e, hipStreamSynchronize(e->stream));
+  const camelid_hip_dims& d = e->d;
+  std::vector<uint16_t> hk((size_t)n * d.head_dim), hv(hk.size());
+  for (uint32_t h = 0; h < d.n_kv_heads; ++h) {
+    const size_t src = (((size_t)layer * d.n_kv_heads + h) * d.max_pos) * d.head_dim;
+    HIP_TRY(e, hipMemcpy(hk.data(), e->kc + src, hk.size() * 2, hipMemcpyDeviceToHost));
+    HIP_TRY(e, hipMemcpy(hv.data(), e->vc + src, hv.size() * 2, hipMemcpyDeviceToHost));
+    const size_t dst = (size_t)h * n * d.head_dim;
+    for (size_t i = 0; i < hk.size(); ++i) {
+      ck[dst + i] = cm::f16_bits_to_f32(hk[i]);
+      cv[dst + i] = cm::f16_bits_to_f32(hv[i]);
+    }
+  }
+  return 0;
+}
+
+int camelid_hip_forward_token(camelid_hip_engine* e, const float* emb, const float* cos_tab, const float* sin_tab,
+                              uint32_t position, float scale, int want_logits, uint32_t* tok_out,
+                              float* logits_out) {
+  if (!e) return fail(nullptr, "null engine");
+  if (!ready(e)) return fail(e, "weights not ready");
+  if (!emb || !cos_tab || !sin_tab) return fail(e, "null argument");
+  if (position >= e->d.max_pos) return fail(e, "position beyond max_pos");
+  if (!std::isfinite(scale)) return fail(e, "attention score scale must be finite");
+  HIP_TRY(e, hipSetDevice(e->device));
+  const camelid_hip_dims& d = e->d;
+  const size_t half = d.rope_dim / 2;
+  std::memcpy(e->p_emb, emb, d.hidden * 4);
+  std::memcpy(e->p_cos, cos_tab, half * 4);
+  std::memcpy(e->p_sin, sin_tab, half * 4);
+  *e->p_pos = position;
+  e->cur_pos = position;
+  HIP_TRY(e, hipMemcpyAsync(e->h, e->p_emb, d.hidden * 4, hipMemcpyHostToDevice, e->stream));
+  HIP_TRY(e, hipMemcpyAsync(e->cos_cur, e->p_cos, half * 4, hipMemcpyHostToDevice, e->stream));
+  HIP_TRY(e, hipMemcpyAsync(e->sin_cur, e->p_sin, half * 4, hipMemcpyHostToDevice, e->stream));
+  HIP_TRY(e, hipMemcpyAsync(e->d_pos, e->p_pos, 4, hipMemcpyHostToDevice, e->stream));
+  run_stack(e, e->cos_cur, e->sin_cur, scale);
+  run_head(e);
+  if (check_launch(e)) { e->filled = 0; return 1; }
+  HIP_TRY(e, hipMemcpyAsync(e->p_tok, e->d_tok, 4, hipMemcpyDeviceToHost, e->stream));
+  if (want_logits && logits_out)
+    HIP_TRY(e, hipMemcpyAsync(e->p_logits, e->logits, (size_t)d.vocab * 4, hipMemcpyDeviceToHost, e->stream));
+  hipError_t st = hipStreamSynchronize(e->stream);
+  if (st != hipSuccess) { e->filled = 0; return fail(e, std::string("forward_token: ") + hipGetErrorString(st)); }
+  if (tok_out) *tok_out = *e->p_tok;
+  if (want_logits && logits_out) std::memcpy(logits_out, e->p_logits, (size_t)d.vocab * 4);
+  e->filled = position + 1;
+  return 0;
+}
+
+int camelid_hip_prefill(camelid_hip_engine* e, const float* embs, const float* cos_all, const float* sin_all,
+                        uint32_t n, float scale) {
+  if (!e) return fail(nullptr, "null engine");
+  if (!ready(e)) return fail(e, "weights not ready");
+  if (!embs || !cos_all || !sin_all) return fail(e, "null argument");
+  const camelid_hip_dims& d = e->d;
+  if ((size_t)e->filled + n > d.max_pos) return fail(e, "prefill beyond max_pos");
+  if (!std::isfinite(scale)) return fail(e, "attention score scale must be finite");
+  if (n == 0) return 0;
+  HIP_TRY(e, hipSetDevice(e->device));
+  const size_t half = d.rope_dim / 2;
+  // Stage every row once; the per-token layer stack reads its slice.
+  float *d_embs = nullptr, *d_cos = nullptr, *d_sin = nullptr;
+  uint32_t* d_posv = nullptr;
+  HIP_TRY(e, hipMalloc(&d_embs, (size_t)n * d.hidden * 4));
+  HIP_TRY(e, hipMalloc(&d_cos, (size_t)n * half * 4));
+  HIP_TRY(e, hipMalloc(&d_sin, (size_t)n * half * 4));
+  HIP_TRY(e, hipMalloc(&d_posv, (size_t)n * 4));
+  std::vector<uint32_t> pv(n);
+  for (uint32_t t = 0; t < n; ++t) pv[t] = e->filled + t;
+  int rc = 0;
+  do {
+    if (hipMemcpy(d_embs, embs, (size_t)n * d.hidden * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(d_cos, cos_all, (size_t)n * half * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(d_sin, sin_all, (size_t)n * half * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(d_posv, pv.data(), (size_t)n * 4, hipMemcpyHostToDevice) != hipSuccess) {
+      rc = fail(e, "prefill staging copy failed");
+      break;
+    }
+    for (uint32_t t = 0; t < n; ++t) {
+      (void)hipMemcpyAsync(e->h, d_embs + (size_t)t * d.hidden, d.hidden * 4, hipMemcpyDeviceToDevice, e->stream);
+      (void)hipMemcpyAsync(e->d_pos, d_posv + t, 4, hipMemcpyDeviceToDevice, e->stream);
+      e->cur_pos = pv[t];
+      run_stack(e, d_cos + (size_t)t * half, d_sin + (size_t)t * half, scale);
+    }
+    if (check_launch(e)) { rc = 1; break; }
+    hipError_t st = hipStreamSynchronize(e->stream);
+    if (st != hipSuccess) { rc = fail(e, std::string("prefill: ") + hipGetErrorString(st)); break; }
+  } while (0);
+  (void)hipFree(d_embs);
+  (void)hipFree(d_cos);
+  (void)hipFree(d_sin);
+  (void)hipFree(d_posv);
+  if (rc) { e->filled = 0; return rc; }
+  e->filled += n;
+  return 0;
+}
+
+int camelid_hip_generate(camelid_hip_engine* e, uint32_t token, uint32_t position, uint32_t n_steps, float scale,
+                         uint32_t* tokens_out) {
+  if (!e) return fail(nullptr, "null engine");
+  if (!ready(e) || !e->embd_set) return fail(e, "weights or embedding not ready");
+  if (!tokens_out) return fail(e, "null argument");
+  const camelid_hip_dims& d = e->d;
+  if ((size_t)position + n_steps > e->rope_rows) return fail(e, "rope table does not cover the requested steps");
+  if (token >= d.vocab) return fail(e, "token id out of range");
+  if (!std::isfinite(scale)) return fail(e, "attention score scale must be finite");
+  if (n_steps == 0) return 0;
+  HIP_TRY(e, hipSetDevice(e->device));
+  const size_t half = d.rope_dim / 2;
+  uint32_t *d_toks = nullptr, *d_posv = nullptr;
+  HIP_TRY(e, hipMalloc(&d_toks, (size_t)(n_steps + 1) * 4));
+  HIP_TRY(e, hipMalloc(&d_posv, (size_t)n_steps * 4));
+  std::vector<uint32_t> pv(n_steps);
+  for (uint32_t t = 0; t < n_steps; ++t) pv[t] = position + t;
+  int rc = 0;
+  do {
+    if (hipMemcpy(d_posv, pv.data(), (size_t)n_steps * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(d_toks, &token, 4, hipMemcpyHostToDevice) != hipSuccess) {
+      rc = fail(e, "generate staging copy failed");
+      break;
+    }
+    for (uint32_t t = 0; t < n_steps; ++t) {
+      (void)hipMemcpyAsync(e->d_pos, d_posv + t, 4, hipMemcpyDeviceToDevice, e->stream);
+      e->cur_pos = pv[t];
+      {
+        ProfScope ps(e, P_EMBED, d.hidden * (34.0 / 32.0 + 4.0));
+        hipLaunchKernelGGL(cm::k_embed_q8, dim3((d.hidden + 255) / 256), dim3(256), 0, e->stream, e->embd.q,
+                           e->embd.d, (int)d.hidden, d_toks + t, e->h);
+      }
+      const size_t p = position + t;
+      run_stack(e, e->rope_cos + p * half, e->rope_sin + p * half, scale);
+      run_head(e);
+      (void)hipMemcpyAsync(d_toks + t + 1, e->d_tok, 4, hipMemcpyDeviceToDevice, e->stream);
+    }
+    if (check_launch(e)) { rc = 1; break; }
+    hipError_t st = hipStreamSynchronize(e->stream);
+    if (st != hipSuccess) { rc = fail(e, std::string("generate: ") + hipGetErrorString(st)); break; }
+    if (hipMemcpy(tokens_out, d_toks + 1, (size_t)n_steps * 4, hipMemcpyDeviceToHost) != hipSuccess)
+      rc = fail(e, "generate token copy failed");
+  } while (0);
+  (void)hipFree(d_toks);
+  (void)hipFree(d_posv);
+  if (rc) { e->filled = 0; return rc; }
+  e->filled = position + n_steps;
+  return 0;
+}
+
+int camelid_hip_capture_hidden(camelid_hip_engine* e, int enable) {
+  if (!e) return fail(nullptr, "null engine");
+  e->capture = enable != 0;
+  return 0;
+}
+
+int camelid_hip_read_hidden(camelid_hip_engine* e, float* out) {
+  if (!e || !out) return fail(e, "null argument");
+  HIP_TRY(e, hipSetDevice(e->device));
+  HIP_TRY(e, hipStreamSynchronize(e->stream));
+  HIP_TRY(e, hipMemcpy(out, e->hidden_cap, (size_t)(e->d.n_layers + 1) * e->d.hidden * 4, hipMemcpyDeviceToHost));
+  return 0;
+}
+
+int camelid_hip_profile_begin(camelid_hip_engine* e) {
+  if (!e) return fail(nullptr, "null engine");
+  e->recs.clear();
+  e->pool_next = 0;
+  e->profiling = true;
+  return 0;
+}
+
+int camelid_hip_profile_end(camelid_hip_engine* e, double* ms, double* bytes, uint64_t* launches, uint32_t n_cat) {
+  if (!e) return fail(nullptr, "null engine");
+  e->profiling = false;
+  HIP_TRY(e, hipStreamSynchronize(e->stream));
+  for (uint32_t c = 0; c < n_cat; ++c) {
+    if (ms) ms[c] = 0;
+    if (bytes) bytes[c] = 0;
+    if (launches) launches[c] = 0;
+  }
+  for (const auto& r : e->recs) {
+    if ((uint32_t)r.cat >= n_cat) continue;
+    float t = 0.0f;
+    HIP_TRY(e, hipEventElapsedTime(&t, r.a, r.b));
+    if (ms) ms[r.cat] += t;
+    if (bytes) bytes[r.cat] += r.bytes;
+    if (launches) launches[r.cat] += 1;
+  }
+  e->recs.clear();
+  e->pool_next = 0;
+  return 0;
+}
+
+int camelid_hip_device_info(char* name, size_t name_len, int* n_cu) {
+  int dev = 0;
+  if (const char* s = std::getenv("CAMELID_HIP_DEVICE")) dev = std::atoi(s);
+  hipDeviceProp_t p;
+  hipError_t st = hipGetDeviceProperties(&p, dev);
+  if (st != hipSuccess) return fail(nullptr, std::string("hipGetDeviceProperties: ") + hipGetErrorString(st));
+  if (name && name_len) {
+    std::snprintf(name, name_len, "%s (%s)", p.name, p.gcnArchName);
+  }
+  if (n_cu) *n_cu = p.multiProcessorCount;
+  return 0;
+}
+
+// ------------------------------------------------------------------ kernel-level ABI
+#define G_TRY(expr)                                                                          \
+  do {                                                                                       \
+    hipError_t _st = (expr);                                                                 \
+    if (_st != hipSuccess) return fail(nullptr, std::string(#expr) + ": " + hipGetErrorString(_st)); \
+  } while (0)
+
+int camelid_hip_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return fail(nullptr, "null argument");
+  G_TRY(hipMalloc(ptr, std::max<size_t>(bytes, 256)));
+  return 0;
+}
+int camelid_hip_free(void* ptr) {
+  G_TRY(hipFree(ptr));
+  return 0;
+}
+int camelid_hip_memcpy_htod(void* dst, const void* src, size_t bytes) {
+  G_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  return 0;
+}
+int camelid_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+  G_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  return 0;
+}
+int camelid_hip_synchronize(void) {
+  G_TRY(hipDeviceSynchronize());
+  return 0;
+}
+
+int camelid_q8_0_repack(const uint8_t* src, size_t rows, size_t k, uint8_t layout, int8_t* quants_out,
+                        uint16_t* scales_out) {
+  if (!src || !quants_out || !scales_out) return fail(nullptr, "null argument");
+  if (layout != 34 && layout != 36) return fail(nullptr, "layout must be 34 or 36");
+  if (k % 32) return fail(nullptr, "k must be a multiple of 32");
+  repack_parallel(src, rows, k, layout, quants_out, scales_out);
+  return 0;
+}
+
+static int launch_status(const char* what) {
+  hipError_t st = hipGetLastError();
+  if (st != hipSuccess) return fail(nullptr, std::string(what) + ": " + hipGetErrorString(st));
+  return 0;
+}
+
+int camelid_hip_q8_0_gemv(const int8_t* wq, const uint16_t* wd, uint32_t rows, uint32_t k, const int8_t* xq,
+                          const float* xs, float* y, const float* resid, void* stream) {
+  if (!wq || !wd || !xq || !xs || !y) return fail(nullptr, "null argument");
+  if (k % 32 || rows == 0) return fail(nullptr, "k must be a nonzero multiple of 32 and rows > 0");
+  if (gemv_lds_bytes(k) > 64 * 1024) return fail(nullptr, "k too large for the GEMV LDS stage");
+  Q8Mat m;
+  m.q = const_cast<int8_t*>(wq);
+  m.d = const_cast<uint16_t*>(wd);
+  m.rows = rows;
+  m.k = k;
+  launch_gemv(m, xq, xs, y, resid, (hipStream_t)stream);
+  return launch_status("q8_0_gemv");
+}
+
+int camelid_hip_q8_0_block_dots(const int8_t* wq, uint32_t rows, uint32_t k, const int8_t* xq, int32_t* out,
+                                void* stream) {
+  if (!wq || !xq || !out) return fail(nullptr, "null argument");
+  if (k % 32 || rows == 0) return fail(nullptr, "k must be a nonzero multiple of 32 and rows > 0");
+  hipLaunchKernelGGL(cm::k_q8_block_dots, dim3(rows), dim3(64), 0, (hipStream_t)stream, wq, (int)k, xq, out);
+  return launch_status("q8_0_block_dots");
+}
+
+int camelid_hip_rmsnorm_quantize(const float* x, const float* w, uint32_t n, float eps, int8_t* xq, float* xs,
+                                 float* y, void* stream) {
+  if (!x || !w || !xq || !xs) return fail(nullptr, "null argument");
+  if (n == 0 || n % 32 || n > 16384) return fail(nullptr, "n must be a multiple of 32 in (0, 16384]");
+  launch_rmsnorm_quant(x, w, n, eps, xq, xs, y, (hipStream_t)stream);
+  return launch_status("rmsnorm_quantize");
+}
+
+int camelid_hip_quantize_q8_0(const float* x, uint32_t n, int8_t* xq, float* xs, void* stream) {
+  if (!x || !xq || !xs) return fail(nullptr, "null argument");
+  if (n % 32) return fail(nullptr, "n must be a multiple of 32");
+  const uint32_t nb = n / 32;
+  if (nb == 0) return 0;
+  hipLaunchKernelGGL(cm::k_quantize_q8_0, dim3((nb + 63) / 64), dim3(64), 0, (hipStream_t)stream, x, (int)n, xq, xs);
+  return launch_status("quantize_q8_0");
+}
+
+int camelid_hip_silu_mul_quantize(const float* gu, uint32_t n, int8_t* xq, float* xs, float* act, void* stream) {
+  if (!gu || !xq || !xs) return fail(nullptr, "null argument");
+  if (n % 32) return fail(nullptr, "n must be a multiple of 32");
+  const uint32_t nb = n / 32;
+  if (nb == 0) return 0;
+  hipLaunchKernelGGL(cm::k_silu_mul_quant, dim3((nb + 63) / 64), dim3(64), 0, (hipStream_t)stream, gu, (int)n, xq,
+                     xs, act);
+  return launch_status("silu_mul_quantize");
+}
+
+int camelid_hip_rope_kv(const float* qkv, uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t rope_dim,
+                        uint32_t split_half, const float* cos_tab, const float* sin_tab, const float* q_norm,
+                        const float* k_norm, float eps, float* qrot, uint16_t* kc, uint16_t* vc, uint32_t layer,
+                        uint32_t max_pos, const uint32_t* d_pos, void* stream) {
+  if (!qkv || !cos_tab || !sin_tab || !qrot || !kc || !vc || !d_pos) return fail(nullptr, "null argument");
+  if (!n_heads || !n_kv || n_heads % n_kv || hd == 0 || hd > 512 || rope_dim > hd || rope_dim % 2)
+    return fail(nullptr, "invalid head geometry");
+  hipLaunchKernelGGL(cm::k_rope_kv, dim3(n_heads + n_kv), dim3(64), 0, (hipStream_t)stream, qkv, (int)n_heads,
+                     (int)n_kv, (int)hd, (int)rope_dim, (int)split_half, cos_tab, sin_tab, q_norm, k_norm, eps, qrot,
+                     kc, vc, (int)layer, (int)max_pos, d_pos);
+  return launch_status("rope_kv");
+}
+
+int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const uint16_t* vc, uint32_t layer,
+                                 uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t max_pos,
+                                 const uint32_t* d_pos, float scale, float* att_out, int8_t* xq, float* xs,
+                                 void* stream) {
+  if (!qrot || !kc || !vc || !d_pos || !att_out || !xq || !xs) return fail(nullptr, "null argument");
+  if (!n_heads || !n_kv || n_heads % n_kv || hd % 32 || hd == 0 || hd > 512)
+    return fail(nullptr, "invalid head geometry");
+  const size_t lds = ((size_t)max_pos + hd) * 4;
+  if (lds > 160 * 1024) return fail(nullptr, "max_pos too large for the single-pass decode attention");
+  if (lds > 64 * 1024) {
+    hipError_t st = hipFuncSetAttribute((const void*)cm::k_attn_decode, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)lds);
+    if (st != hipSuccess) return fail(nullptr, std::string("attention LDS attribute: ") + hipGetErrorString(st));
+  }
+  hipLaunchKernelGGL(cm::k_attn_decode, dim3(n_heads), dim3(256), lds, (hipStream_t)stream, qrot, kc, vc,
+                     (int)layer, (int)n_heads, (int)n_kv, (int)hd, (int)max_pos, d_pos, scale, att_out, xq, xs);
+  return launch_status("attention_decode");
+}
+
+int camelid_hip_argmax(const float* x, uint32_t n, uint32_t* out, void* stream) {
+  if (!x || !out) return fail(nullptr, "null argument");
+  hipLaunchKernelGGL(cm::k_argmax, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, (int)n, out);
+  return launch_status("argmax");
+}
+
+int camelid_hip_expf(const float* x, float* y, size_t n, void* stream) {
+  if (!x || !y) return fail(nullptr, "null argument");
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(cm::k_expf, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x, y, n);
+  return launch_status("expf");
+}
+
+void camelid_expf_host(const float* x, float* y, size_t n) {
+  for (size_t i = 0; i < n; ++i) y[i] = cm::glibc_expf(x[i]);
+}
+
+}  // extern "C"

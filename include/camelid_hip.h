@@ -1,0 +1,181 @@
+/* camelid_hip.h -- C ABI of the MI355X (gfx950) resident decode/prefill backend.
+ *
+ * Drop-in boundary for Camelid's CUDA resident engine: every engine entry point
+ * mirrors one method of `CudaResidentDecode` (src/cuda_resident.rs) with the same
+ * argument meaning.  Conventions (mirroring the reference):
+ *   - every call returns 0 on success, nonzero on error; the message is available
+ *     from camelid_hip_last_error(engine) (engine-owned string).  A caller treats
+ *     any error as "decline -> CPU fallback" (inference.rs:3316-3371); after an
+ *     error in prefill/forward the engine sets filled = 0 (inference.rs:2484);
+ *   - inputs are borrowed for the call and copied to device memory; the engine owns
+ *     every device buffer (cuda_resident.rs:5601-5762);
+ *   - the engine is not internally synchronised: one caller at a time
+ *     (inference.rs:10952 single-slot mutex);
+ *   - one HIP stream, one host synchronisation per forward call
+ *     (cuda_resident.rs:7475-7476).
+ * Plain pointers and sizes only; no HIP or torch types cross this boundary.
+ */
+#ifndef CAMELID_HIP_H
+#define CAMELID_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct camelid_hip_engine camelid_hip_engine;
+
+/* Model dimensions: the arguments of CudaResidentDecode::new (cuda_resident.rs:5601). */
+typedef struct camelid_hip_dims {
+  uint32_t n_layers;
+  uint32_t n_heads;
+  uint32_t n_kv_heads;
+  uint32_t head_dim;
+  uint32_t hidden;
+  uint32_t ffn_dim;
+  uint32_t rope_dim;
+  uint32_t max_pos;
+  uint32_t vocab;
+  float eps;
+  uint32_t split_half_pairing; /* 0: adjacent pairs (llama), 1: split-half (qwen3) */
+} camelid_hip_dims;
+
+/* Weight formats: ProjQuant (cuda_resident.rs:5262). */
+enum { CAMELID_Q8_0 = 0, CAMELID_Q4_K = 1, CAMELID_Q6_K = 2 };
+/* Q8_0 byte layouts accepted by set_layer/set_output: 34 = GGUF wire block (f16 scale LE +
+ * 32 i8); 36 = Camelid's in-memory Q8_0Block (f32 scale + 32 i8, inference.rs:19992). */
+enum { CAMELID_Q8_WIRE34 = 34, CAMELID_Q8_BLOCK36 = 36 };
+/* Projection order inside set_layer's arrays: q, k, v, o, gate, up, down. */
+enum { CAMELID_PROJ_Q = 0, CAMELID_PROJ_K, CAMELID_PROJ_V, CAMELID_PROJ_O,
+       CAMELID_PROJ_GATE, CAMELID_PROJ_UP, CAMELID_PROJ_DOWN, CAMELID_N_PROJ };
+
+/* CudaResidentDecode::new (cuda_resident.rs:5601): allocates the f16 KV cache
+ * [L][n_kv][max_pos][hd] and all scratch on device 0 (or CAMELID_HIP_DEVICE). */
+int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** out);
+/* Drop (cuda_resident.rs:5398 Drop + cuda.rs:485 release_async_pool). */
+void camelid_hip_engine_free(camelid_hip_engine* e);
+/* Last error message of this engine ("" if none); NULL engine -> last global error. */
+const char* camelid_hip_last_error(const camelid_hip_engine* e);
+
+/* CudaResidentDecode::set_layer_located (cuda_resident.rs:5801). w[i]/len[i]: projection
+ * bytes in CAMELID_PROJ_* order; quant[i]: CAMELID_Q8_0 (only Q8_0 is accepted in this
+ * build); q8_layout: 34 or 36.  q_norm/k_norm may be NULL (no QK-norm). */
+int camelid_hip_set_layer(camelid_hip_engine* e, uint32_t layer, const uint8_t* const w[7],
+                          const size_t len[7], const uint8_t quant[7], uint8_t q8_layout,
+                          const float* attn_norm, const float* ffn_norm, const float* q_norm,
+                          const float* k_norm);
+/* CudaResidentDecode::set_output (cuda_resident.rs:6008): final norm [H] + lm_head [V][H]. */
+int camelid_hip_set_output(camelid_hip_engine* e, const float* final_norm, const uint8_t* w,
+                           size_t len, uint8_t quant, uint8_t q8_layout);
+/* weights_ready (cuda_resident.rs:6261): 1 when every layer and the output are set. */
+int camelid_hip_weights_ready(const camelid_hip_engine* e);
+/* filled / set_filled (cuda_resident.rs:6265-6271): positions of valid KV. */
+uint32_t camelid_hip_filled(const camelid_hip_engine* e);
+int camelid_hip_set_filled(camelid_hip_engine* e, uint32_t filled);
+/* max_pos / n_layers / uses_kquant (cuda_resident.rs:6285, :6292, :6220). */
+uint32_t camelid_hip_max_pos(const camelid_hip_engine* e);
+uint32_t camelid_hip_n_layers(const camelid_hip_engine* e);
+int camelid_hip_uses_kquant(const camelid_hip_engine* e);
+
+/* seed_layer (cuda_resident.rs:6305): upload CPU KV history of one layer, f32 values laid
+ * out [kv_head][pos][hd] for positions [0, n_pos) (rounded to f16 on upload). */
+int camelid_hip_seed_layer(camelid_hip_engine* e, uint32_t layer, const float* ck, const float* cv,
+                           uint32_t n_pos);
+/* read_kv_layer (cuda_resident.rs:6348): download positions [0, n) of one layer as f32,
+ * [kv_head][pos][hd]. */
+int camelid_hip_read_kv_layer(camelid_hip_engine* e, uint32_t layer, uint32_t n, float* ck,
+                              float* cv);
+
+/* forward_token (cuda_resident.rs:7430) / forward_token_logits (:7724): one decode step at
+ * `position` from the embedding row emb[H] with that position's RoPE tables cos/sin
+ * [rope_dim/2].  `scale` is the attention score scale (1/sqrt(hd)).  want_logits != 0
+ * copies the logits row to logits_out [vocab].  *tok_out receives the greedy token. */
+int camelid_hip_forward_token(camelid_hip_engine* e, const float* emb, const float* cos_tab,
+                              const float* sin_tab, uint32_t position, float scale,
+                              int want_logits, uint32_t* tok_out, float* logits_out);
+/* prefill / prefill_batched (cuda_resident.rs:7785, :8797): positions
+ * [filled, filled + n) from embs [n][H], cos_all/sin_all [n][rope_dim/2]. */
+int camelid_hip_prefill(camelid_hip_engine* e, const float* embs, const float* cos_all,
+                        const float* sin_all, uint32_t n, float scale);
+
+/* Device-side token loop (forward_token_device, cuda_resident.rs:7529; embed_gather_q8_0
+ * :2995; rope_select :3012).  set_embedding uploads token_embd (Q8_0); set_rope_table
+ * uploads cos/sin for positions [0, n_pos).  generate runs n_steps greedy steps starting
+ * with `token` at `position`, feeding each argmax back on the device; tokens_out[n_steps]. */
+int camelid_hip_set_embedding(camelid_hip_engine* e, const uint8_t* w, size_t len, uint8_t quant,
+                              uint8_t q8_layout);
+int camelid_hip_set_rope_table(camelid_hip_engine* e, const float* cos_all, const float* sin_all,
+                               uint32_t n_pos);
+int camelid_hip_generate(camelid_hip_engine* e, uint32_t token, uint32_t position, uint32_t n_steps,
+                         float scale, uint32_t* tokens_out);
+
+/* Test hooks.  capture_hidden: 1 enables recording the residual stream entering each layer
+ * and after the last ([L+1][H] f32) on every forward; read_hidden copies the last one. */
+int camelid_hip_capture_hidden(camelid_hip_engine* e, int enable);
+int camelid_hip_read_hidden(camelid_hip_engine* e, float* out);
+/* Per-launch HIP-event timing on the engine's stream (measurement hook).  Between begin and
+ * end every kernel launch is bracketed by events; end synchronises and returns, per category
+ * (0 GEMV, 1 RMSNorm+quantize, 2 RoPE+KV store, 3 attention, 4 SwiGLU+quantize, 5 argmax,
+ * 6 embedding gather), the summed kernel milliseconds, algorithmic bytes and launch count. */
+int camelid_hip_profile_begin(camelid_hip_engine* e);
+int camelid_hip_profile_end(camelid_hip_engine* e, double* ms, double* bytes, uint64_t* launches,
+                            uint32_t n_cat);
+/* Device name and compute units. */
+int camelid_hip_device_info(char* name, size_t name_len, int* n_cu);
+
+/* ---------------------------------------------------------------------------------------
+ * Kernel-level entry points (device pointers; `stream` is a hipStream_t or NULL for the
+ * default stream).  They are the units the engine composes; exported for parity tests and
+ * the isolated kernel sweep.  Weight matrices use the "Q8R" split layout produced by
+ * camelid_q8_0_repack: int8 quants [rows][K] + f16 scale bits [rows][K/32].
+ * Global errors are read with camelid_hip_last_error(NULL). */
+int camelid_hip_malloc(void** ptr, size_t bytes);
+int camelid_hip_free(void* ptr);
+int camelid_hip_memcpy_htod(void* dst, const void* src, size_t bytes);
+int camelid_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+int camelid_hip_synchronize(void);
+
+/* Host repack of a Q8_0 matrix [rows][k] from 34- or 36-byte blocks into Q8R. */
+int camelid_q8_0_repack(const uint8_t* src, size_t rows, size_t k, uint8_t layout,
+                        int8_t* quants_out, uint16_t* scales_out);
+/* q8_gemv (cuda_resident.rs:230; CPU inference.rs:19871-19905): y = resid + W.x, faithful
+ * block-ordered fold.  resid may be NULL; y may alias resid. */
+int camelid_hip_q8_0_gemv(const int8_t* wq, const uint16_t* wd, uint32_t rows, uint32_t k,
+                          const int8_t* xq, const float* xs, float* y, const float* resid,
+                          void* stream);
+/* Per-(row, block) int32 dots [rows][k/32] through the GEMV's dot path (test hook for the
+ * bit-exact block-dot contract, CPU inference.rs:20539-20566). */
+int camelid_hip_q8_0_block_dots(const int8_t* wq, uint32_t rows, uint32_t k, const int8_t* xq, int32_t* out,
+                                void* stream);
+/* rms_norm_quantize (cuda_resident.rs:177; CPU tensor/mod.rs:2083-2106 + inference.rs:16953). */
+int camelid_hip_rmsnorm_quantize(const float* x, const float* w, uint32_t n, float eps, int8_t* xq,
+                                 float* xs, float* y, void* stream);
+/* quantize_q8_0 (cuda_resident.rs:151; CPU inference.rs:16953-16971). */
+int camelid_hip_quantize_q8_0(const float* x, uint32_t n, int8_t* xq, float* xs, void* stream);
+/* silu_mul_quantize (cuda_resident.rs:1315; CPU tensor/mod.rs:1943-1967). gu = [gate|up]. */
+int camelid_hip_silu_mul_quantize(const float* gu, uint32_t n, int8_t* xq, float* xs, float* act,
+                                  void* stream);
+/* rope_rotate + kv_scatter (cuda_resident.rs:1545, :1569; CPU rope.rs:489-524,
+ * kv_cache.rs:573-600), with optional per-head QK RMSNorm (cuda_resident.rs:122). */
+int camelid_hip_rope_kv(const float* qkv, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
+                        uint32_t rope_dim, uint32_t split_half, const float* cos_tab,
+                        const float* sin_tab, const float* q_norm, const float* k_norm, float eps,
+                        float* qrot, uint16_t* kc, uint16_t* vc, uint32_t layer, uint32_t max_pos,
+                        const uint32_t* d_pos, void* stream);
+/* attention_decode (cuda_resident.rs:1587; CPU inference.rs:23945-24025), faithful order. */
+int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const uint16_t* vc,
+                                 uint32_t layer, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
+                                 uint32_t max_pos, const uint32_t* d_pos, float scale,
+                                 float* att_out, int8_t* xq, float* xs, void* stream);
+/* argmax_f32 (cuda_resident.rs:1847; CPU inference.rs:5912). */
+int camelid_hip_argmax(const float* x, uint32_t n, uint32_t* out, void* stream);
+/* glibc-identical expf on the device (test hook for the softmax/SiLU exponential). */
+int camelid_hip_expf(const float* x, float* y, size_t n, void* stream);
+/* The same expf restatement evaluated on the host (test hook). */
+void camelid_expf_host(const float* x, float* y, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CAMELID_HIP_H */

@@ -1,0 +1,153 @@
+"""Whole-model parity of the resident engine against the CPU oracle (GPU).
+
+Mirrors the reference's full_forward_token_matches_cpu (src/cuda_resident/tests.rs:173),
+prefill_then_decode_matches_sequential (:354) and the 128-step token gate
+(tests/cuda_cpu_parity.rs:32-62, ToleranceGate::bit_exact).  The bar here is stronger than
+the north star's 1e-2: hidden states and logits are bit-identical.
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from camelid_amd.model import CONFIGS, ResidentSession, SyntheticModel, prompt_tokens, rope_tables, tiny_config
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def _run_pair(cfg, n_decode, hidden=True):
+    from oracle.oracle import OracleModel
+    model = SyntheticModel.generate(cfg)
+    prompt = prompt_tokens(cfg)
+    max_pos = len(prompt) + n_decode
+    orc = OracleModel(model, max_pos)
+    sess = ResidentSession(model, max_pos)
+    eng = sess.engine
+    eng.capture_hidden(hidden)
+    orc.prefill(prompt[:-1])
+    sess.prefill(prompt[:-1])
+    assert eng.filled() == len(prompt) - 1
+    pos, tok_o, tok_g = len(prompt) - 1, int(prompt[-1]), int(prompt[-1])
+    max_rel = 0.0
+    for step in range(n_decode):
+        tok_o, hid_o, lg_o = orc.forward(tok_o, pos, hidden=True, logits=True)
+        tok_g = sess.step(tok_g, pos, logits=True)
+        lg_g = eng.last_logits
+        if hidden:
+            hid_g = eng.read_hidden()
+            rel = np.abs(hid_g.astype(np.float64) - hid_o) / (np.abs(hid_o) + 1e-6)
+            max_rel = max(max_rel, float(rel.max()))
+            assert np.array_equal(_bits(hid_g), _bits(hid_o)), f"hidden differs at step {step}"
+        assert np.array_equal(_bits(lg_g), _bits(lg_o)), f"logits differ at step {step}"
+        assert tok_g == tok_o
+        pos += 1
+    return sess, orc, max_rel
+
+
+@pytest.mark.parametrize("variant", ["llama", "gqa128", "qwen3_like", "tied"])
+def test_tiny_model_bit_exact(variant):
+    kw = {}
+    if variant == "gqa128":
+        kw = dict(hidden=384, n_heads=3, n_kv_heads=1, head_dim=128, ffn_dim=1024, rope_theta=500000.0,
+                  rope_scaling="llama3", rope_factor=32.0)
+    elif variant == "qwen3_like":
+        kw = dict(qk_norm=True, split_half=True, rope_theta=1e6)
+    elif variant == "tied":
+        kw = dict(tied=True, n_layers=3)
+    cfg = tiny_config(**kw)
+    sess, orc, max_rel = _run_pair(cfg, 12)
+    assert max_rel == 0.0
+    # KV written by prefill + decode equals the oracle's cache, layer by layer
+    n = sess.engine.filled()
+    for layer in range(cfg.n_layers):
+        kg, vg = sess.engine.read_kv_layer(layer, n)
+        ko, vo = orc.read_kv(layer, n)
+        assert np.array_equal(_bits(kg), _bits(ko)) and np.array_equal(_bits(vg), _bits(vo))
+    sess.close()
+
+
+def test_device_loop_matches_host_loop():
+    cfg = tiny_config(n_layers=3, prompt_len=10)
+    model = SyntheticModel.generate(cfg)
+    prompt = prompt_tokens(cfg)
+    host = ResidentSession(model, 40).generate(prompt, 24)
+    dev = ResidentSession(model, 40, device_loop=True).generate(prompt, 24)
+    assert host == dev
+
+
+def test_seed_read_roundtrip_and_errors():
+    from camelid_amd._native import HipError
+    cfg = tiny_config()
+    model = SyntheticModel.generate(cfg)
+    sess = ResidentSession(model, 20)
+    eng = sess.engine
+    rng = np.random.default_rng(0)
+    k = rng.normal(0, 1, (cfg.n_kv_heads, 7, cfg.head_dim)).astype(np.float32)
+    v = rng.normal(0, 1, k.shape).astype(np.float32)
+    eng.seed_layer(1, k, v, 7)
+    kg, vg = eng.read_kv_layer(1, 7)
+    assert np.array_equal(kg, k.astype(np.float16).astype(np.float32))
+    assert np.array_equal(vg, v.astype(np.float16).astype(np.float32))
+    cos, sin = rope_tables(cfg, 0, 1)
+    emb = model.embed([1])[0]
+    with pytest.raises(HipError, match="max_pos"):
+        eng.forward_token(emb, cos[0], sin[0], 20, cfg.scale())
+    with pytest.raises(HipError, match="max_pos"):
+        eng.set_filled(21)
+    assert eng.weights_ready() and eng.n_layers() == cfg.n_layers and eng.max_pos() == 20
+    assert not eng.uses_kquant()
+    sess.close()
+
+
+def test_seeded_history_matches_prefill():
+    """A CPU-seeded KV history (seed_layer) continues exactly like a GPU prefill (inference.rs:3243-3297)."""
+    from oracle.oracle import OracleModel
+    cfg = tiny_config(n_layers=2)
+    model = SyntheticModel.generate(cfg)
+    prompt = prompt_tokens(cfg)
+    orc = OracleModel(model, 40)
+    orc.prefill(prompt[:-1])
+    sess = ResidentSession(model, 40)
+    n = len(prompt) - 1
+    for layer in range(cfg.n_layers):
+        k, v = orc.read_kv(layer, n)
+        sess.engine.seed_layer(layer, k, v, n)
+    sess.engine.set_filled(n)
+    tok = sess.step(int(prompt[-1]), n)
+    want, _, _ = orc.forward(int(prompt[-1]), n)
+    assert tok == want
+
+
+def _golden(name):
+    files = sorted(GOLDEN.glob(f"{name}_p*_d*.json"))
+    if not files:
+        pytest.skip(f"no golden stream for {name}")
+    return json.loads(files[-1].read_text())
+
+
+def test_tinyllama_token_gate():
+    """TinyLlama-1.1B arch Q8_0, 128-token prompt, 128 greedy tokens,
+    token-identical to the oracle's stream (tests/golden, written by make_golden.py)."""
+    g = _golden("tinyllama-1.1b")
+    cfg = CONFIGS["tinyllama-1.1b"]
+    model = SyntheticModel.generate(cfg)
+    prompt = prompt_tokens(cfg, g["prompt_len"])
+    assert [int(t) for t in prompt] == g["prompt"]
+    sess = ResidentSession(model, g["prompt_len"] + g["decode_len"])
+    toks = sess.generate(prompt, g["decode_len"])
+    assert toks == g["tokens"]
+    sess.close()
+
+
+def test_tinyllama_hidden_states_first_steps():
+    """Per-layer hidden states at TinyLlama dims vs the live oracle for the first decode steps."""
+    cfg = CONFIGS["tinyllama-1.1b"].scaled(prompt_len=24)
+    sess, _, max_rel = _run_pair(cfg, 3)
+    assert max_rel == 0.0
+    sess.close()
