@@ -7,8 +7,16 @@
 //              attn/ffn norm [H], optional q/k norm [hd]
 //   lm_head Q8R [V][H], final norm [H], optional token_embd Q8R [V][H]
 //   KV cache f16 [L][n_kv][max_pos][hd] (K and V separately)
-//   activations: h [H] (residual stream), qkv, qrot, att [nq], gu [2F], logits [V],
-//                one Q8_0 activation buffer (quants + f32 scales) reused by every GEMV
+//   activations: h [H] (residual stream), qkv, att [nq], gu [2F], logits [V], one Q8_0
+//                activation buffer (quants + f32 scales) reused by every GEMV
+//   StepState {pos, tok, step, counter}: the decode loop's device-side state
+//
+// Per decode step (launch order on the one stream):
+//   [embed]  rmsnorm_quant -> gemv(QKV) -> attention(+QK-norm, RoPE, KV store) ->
+//   gemv(O, +residual) -> rmsnorm_quant -> gemv(gate|up) -> silu_quant ->
+//   gemv(down, +residual)   x L,   then rmsnorm_quant -> gemv_argmax(lm_head)
+// The device-side loop captures one step in a HIP graph and replays it; the step reads
+// the token and position from StepState and the argmax advances them.
 #include <hip/hip_runtime.h>
 #include <algorithm>
 #include <cmath>
@@ -41,10 +49,8 @@ struct LayerW {
   bool set = false;
 };
 
-constexpr int kGemvRW = 4;        // rows per wave in the faithful GEMV
-constexpr int kGemvRowsPerWG = 4 * kGemvRW;
-
-size_t gemv_lds_bytes(uint32_t k) { return (size_t)4 * kGemvRW * (k / 32 + 1) * sizeof(float); }
+// Profiling categories (camelid_hip_profile_end).
+enum { P_GEMV = 0, P_NORM, P_ATTN, P_SILU, P_HEAD, P_EMBED, P_NCAT };
 
 }  // namespace
 
@@ -60,21 +66,34 @@ struct camelid_hip_engine {
   bool embd_set = false;
   uint16_t* kc = nullptr;
   uint16_t* vc = nullptr;
-  float *h = nullptr, *qkv = nullptr, *qrot = nullptr, *att = nullptr, *gu = nullptr;
+  float *h = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr;
   float *logits = nullptr, *hidden_cap = nullptr, *xs = nullptr;
   float *cos_cur = nullptr, *sin_cur = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
   uint32_t rope_rows = 0;
   int8_t* xq = nullptr;
-  uint32_t *d_pos = nullptr, *d_tok = nullptr, *d_tokens = nullptr;
+  float* part_v = nullptr;
+  uint32_t* part_i = nullptr;
+  cm::StepState* st = nullptr;
+  uint32_t* tokens = nullptr;  // device ring of generated tokens (device-side loop)
+  uint32_t tokens_cap = 0;
   // pinned host staging
   float *p_emb = nullptr, *p_cos = nullptr, *p_sin = nullptr, *p_logits = nullptr;
-  uint32_t *p_tok = nullptr, *p_pos = nullptr;
+  cm::StepState* p_st = nullptr;
   uint32_t filled = 0;
   uint32_t cur_pos = 0;  // host copy of the position being computed (profiling byte counts)
   bool capture = false;
+  // device-side loop graph (one decode step)
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
+  float graph_scale = 0.0f;
+  bool use_graph = true;
   // optional per-launch HIP-event timing (camelid_hip_profile_*)
   bool profiling = false;
-  struct Rec { int cat; double bytes; hipEvent_t a, b; };
+  struct Rec {
+    int cat;
+    double bytes;
+    hipEvent_t a, b;
+  };
   std::vector<Rec> recs;
   std::vector<hipEvent_t> event_pool;
   size_t pool_next = 0;
@@ -91,11 +110,11 @@ int fail(camelid_hip_engine* e, const std::string& msg) {
   return 1;
 }
 
-#define HIP_TRY(eng, expr)                                                                \
-  do {                                                                                    \
-    hipError_t _st = (expr);                                                              \
-    if (_st != hipSuccess)                                                                \
-      return fail((eng), std::string(#expr) + " failed: " + hipGetErrorString(_st));      \
+#define HIP_TRY(eng, expr)                                                           \
+  do {                                                                               \
+    hipError_t _st = (expr);                                                         \
+    if (_st != hipSuccess)                                                           \
+      return fail((eng), std::string(#expr) + " failed: " + hipGetErrorString(_st)); \
   } while (0)
 
 template <typename T>
@@ -103,7 +122,8 @@ int dev_alloc(camelid_hip_engine* e, T** p, size_t count) {
   void* v = nullptr;
   size_t bytes = std::max<size_t>(count * sizeof(T), 256);
   hipError_t st = hipMalloc(&v, bytes);
-  if (st != hipSuccess) return fail(e, std::string("hipMalloc(") + std::to_string(bytes) + ") failed: " + hipGetErrorString(st));
+  if (st != hipSuccess)
+    return fail(e, std::string("hipMalloc(") + std::to_string(bytes) + ") failed: " + hipGetErrorString(st));
   e->dev_allocs.push_back(v);
   *p = static_cast<T*>(v);
   return 0;
@@ -122,8 +142,7 @@ int host_alloc(camelid_hip_engine* e, T** p, size_t count) {
 uint16_t read_le16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 
 // Repack rows [r0, r1) of a 34/36-byte-block Q8_0 matrix into the Q8R planes.
-void repack_rows(const uint8_t* src, size_t r0, size_t r1, size_t k, uint8_t layout, int8_t* q,
-                 uint16_t* d) {
+void repack_rows(const uint8_t* src, size_t r0, size_t r1, size_t k, uint8_t layout, int8_t* q, uint16_t* d) {
   const size_t nb = k / 32;
   for (size_t r = r0; r < r1; ++r) {
     for (size_t b = 0; b < nb; ++b) {
@@ -142,8 +161,7 @@ void repack_rows(const uint8_t* src, size_t r0, size_t r1, size_t k, uint8_t lay
   }
 }
 
-void repack_parallel(const uint8_t* src, size_t rows, size_t k, uint8_t layout, int8_t* q,
-                     uint16_t* d) {
+void repack_parallel(const uint8_t* src, size_t rows, size_t k, uint8_t layout, int8_t* q, uint16_t* d) {
   unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
   if (rows < 4096) nt = 1;
   std::vector<std::thread> th;
@@ -154,15 +172,14 @@ void repack_parallel(const uint8_t* src, size_t rows, size_t k, uint8_t layout, 
   for (auto& x : th) x.join();
 }
 
-// Upload `parts` (stacked row-wise) as one Q8R matrix.
 struct Part {
   const uint8_t* src;
   size_t len;
   uint32_t rows;
 };
 
-int upload_q8(camelid_hip_engine* e, Q8Mat* m, const std::vector<Part>& parts, uint32_t k,
-              uint8_t layout) {
+// Upload `parts` (stacked row-wise) as one Q8R matrix.
+int upload_q8(camelid_hip_engine* e, Q8Mat* m, const std::vector<Part>& parts, uint32_t k, uint8_t layout) {
   if (layout != 34 && layout != 36) return fail(e, "q8_layout must be 34 or 36");
   if (k % 32 != 0) return fail(e, "Q8_0 row width must be a multiple of 32");
   uint32_t rows = 0;
@@ -216,7 +233,7 @@ struct ProfScope {
   double bytes;
   hipEvent_t a = nullptr;
   ProfScope(camelid_hip_engine* eng, int c, double b) : e(eng), cat(c), bytes(b) {
-    if (e && e->profiling) {
+    if (e->profiling) {
       a = next_event(e);
       if (a) (void)hipEventRecord(a, e->stream);
     }
@@ -232,30 +249,28 @@ struct ProfScope {
   }
 };
 
-double q8_bytes(const Q8Mat& m) { return (double)m.rows * m.k * 34.0 / 32.0 + m.k * 34.0 / 32.0 + m.rows * 4.0; }
+// Algorithmic bytes of one Q8_0 GEMV launch: weights (34 B per 32 values), the quantized
+// activation, the f32 output (+ the residual read when fused).
+double q8_bytes(const Q8Mat& m, bool resid) {
+  return (double)m.rows * m.k * 34.0 / 32.0 + m.k * 34.0 / 32.0 + m.rows * (resid ? 8.0 : 4.0);
+}
 
 // ---------------------------------------------------------------- launches
-void launch_gemv(const Q8Mat& m, const int8_t* xq, const float* xs, float* y, const float* resid,
-                 hipStream_t s) {
-  const uint32_t grid = (m.rows + kGemvRowsPerWG - 1) / kGemvRowsPerWG;
-  hipLaunchKernelGGL(cm::k_q8_gemv<kGemvRW>, dim3(grid), dim3(256), gemv_lds_bytes(m.k), s, m.q, m.d,
+void launch_gemv(const Q8Mat& m, const int8_t* xq, const float* xs, float* y, const float* resid, hipStream_t s) {
+  const uint32_t grid = (m.rows + cm::GEMV_R - 1) / cm::GEMV_R;
+  hipLaunchKernelGGL(cm::k_gemv, dim3(grid), dim3(cm::GEMV_NT), cm::gemv_lds_bytes((int)m.k), s, m.q, m.d,
                      (int)m.rows, (int)m.k, xq, xs, y, resid);
 }
 
-void launch_rmsnorm_quant(const float* x, const float* w, uint32_t n, float eps, int8_t* xq, float* xs,
-                          float* y, hipStream_t s) {
-  hipLaunchKernelGGL(cm::k_rmsnorm_quant, dim3(1), dim3(1024), (size_t)n * 4, s, x, w, (int)n, eps, xq,
-                     xs, y);
+void launch_rmsnorm_quant(const float* x, const float* w, uint32_t n, float eps, int8_t* xq, float* xs, float* y,
+                          hipStream_t s) {
+  hipLaunchKernelGGL(cm::k_rmsnorm_quant, dim3(1), dim3(cm::RMS_NT), (size_t)n * 4, s, x, w, (int)n, eps, xq, xs, y);
 }
 
-size_t attn_lds_bytes(const camelid_hip_dims& d) { return ((size_t)d.max_pos + d.head_dim) * 4; }
-
-// One transformer layer at the position held in d_pos (cos/sin: that position's tables).
-// Profiling categories (camelid_hip_profile_read).
-enum { P_GEMV = 0, P_NORM, P_ROPE, P_ATTN, P_SILU, P_HEAD, P_EMBED, P_NCAT };
+size_t attn_lds_bytes(uint32_t max_pos) { return (((size_t)max_pos + 3) & ~(size_t)3) * 4; }
 
 void gemv(camelid_hip_engine* e, const Q8Mat& m, float* y, const float* resid) {
-  ProfScope ps(e, P_GEMV, q8_bytes(m) + (resid ? m.rows * 4.0 : 0.0));
+  ProfScope ps(e, P_GEMV, q8_bytes(m, resid != nullptr));
   launch_gemv(m, e->xq, e->xs, y, resid, e->stream);
 }
 
@@ -265,7 +280,9 @@ void rmsnorm(camelid_hip_engine* e, const float* w) {
   launch_rmsnorm_quant(e->h, w, n, e->d.eps, e->xq, e->xs, nullptr, e->stream);
 }
 
-void run_layer(camelid_hip_engine* e, uint32_t l, const float* cosv, const float* sinv, float scale) {
+// One transformer layer at StepState.pos; RoPE tables at cos_base + pos*rope_stride.
+void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const float* sin_base, int rope_stride,
+               float scale) {
   const camelid_hip_dims& d = e->d;
   const LayerW& L = e->layers[l];
   hipStream_t s = e->stream;
@@ -273,48 +290,51 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cosv, const float
   rmsnorm(e, L.attn_norm);
   gemv(e, L.qkv, e->qkv, nullptr);
   {
-    ProfScope ps(e, P_ROPE, (nq + 2 * nkv) * 4 + nq * 4 + 2 * nkv * 2);
-    hipLaunchKernelGGL(cm::k_rope_kv, dim3(d.n_heads + d.n_kv_heads), dim3(64), 0, s, e->qkv, (int)d.n_heads,
-                       (int)d.n_kv_heads, (int)d.head_dim, (int)d.rope_dim, (int)d.split_half_pairing, cosv, sinv,
-                       L.q_norm, L.k_norm, d.eps, e->qrot, e->kc, e->vc, (int)l, (int)d.max_pos, e->d_pos);
-  }
-  {
-    ProfScope ps(e, P_ATTN, nq * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * 34.0 / 32.0);
-    hipLaunchKernelGGL(cm::k_attn_decode, dim3(d.n_heads), dim3(256), attn_lds_bytes(d), s, e->qrot, e->kc,
-                       e->vc, (int)l, (int)d.n_heads, (int)d.n_kv_heads, (int)d.head_dim, (int)d.max_pos,
-                       e->d_pos, scale, e->att, e->xq, e->xs);
+    ProfScope ps(e, P_ATTN, (nq + 2 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0));
+    hipLaunchKernelGGL(cm::k_attention<true>, dim3(d.n_heads), dim3(cm::ATT_NT), attn_lds_bytes(d.max_pos), s,
+                       e->qkv, (int)d.n_heads, (int)d.n_kv_heads, (int)d.head_dim, (int)d.rope_dim,
+                       (int)d.split_half_pairing, cos_base, sin_base, rope_stride, L.q_norm, L.k_norm, d.eps, e->kc,
+                       e->vc, (int)l, (int)d.max_pos, &e->st->pos, scale, e->att, e->xq, e->xs);
   }
   gemv(e, L.o, e->h, e->h);
   rmsnorm(e, L.ffn_norm);
   gemv(e, L.gu, e->gu, nullptr);
   {
-    const uint32_t nbf = d.ffn_dim / 32;
     ProfScope ps(e, P_SILU, d.ffn_dim * 8.0 + d.ffn_dim * 34.0 / 32.0);
-    hipLaunchKernelGGL(cm::k_silu_mul_quant, dim3((nbf + 63) / 64), dim3(64), 0, s, e->gu, (int)d.ffn_dim,
+    hipLaunchKernelGGL(cm::k_silu_mul_quant, dim3((d.ffn_dim + 255) / 256), dim3(256), 0, s, e->gu, (int)d.ffn_dim,
                        e->xq, e->xs, nullptr);
   }
   gemv(e, L.down, e->h, e->h);
 }
 
-void run_stack(camelid_hip_engine* e, const float* cosv, const float* sinv, float scale) {
+void run_stack(camelid_hip_engine* e, const float* cos_base, const float* sin_base, int rope_stride, float scale) {
   const camelid_hip_dims& d = e->d;
   for (uint32_t l = 0; l < d.n_layers; ++l) {
     if (e->capture)
       (void)hipMemcpyAsync(e->hidden_cap + (size_t)l * d.hidden, e->h, d.hidden * 4, hipMemcpyDeviceToDevice,
                            e->stream);
-    run_layer(e, l, cosv, sinv, scale);
+    run_layer(e, l, cos_base, sin_base, rope_stride, scale);
   }
   if (e->capture)
-    (void)hipMemcpyAsync(e->hidden_cap + (size_t)d.n_layers * d.hidden, e->h, d.hidden * 4,
-                         hipMemcpyDeviceToDevice, e->stream);
+    (void)hipMemcpyAsync(e->hidden_cap + (size_t)d.n_layers * d.hidden, e->h, d.hidden * 4, hipMemcpyDeviceToDevice,
+                         e->stream);
 }
 
-void run_head(camelid_hip_engine* e) {
-  const camelid_hip_dims& d = e->d;
+// Final norm, lm_head and greedy argmax; advances StepState (pos+1, tok, tokens[step]).
+void run_head(camelid_hip_engine* e, uint32_t* tokens, uint32_t cap) {
   rmsnorm(e, e->out_norm);
-  gemv(e, e->out, e->logits, nullptr);
-  ProfScope ps(e, P_HEAD, d.vocab * 4.0);
-  hipLaunchKernelGGL(cm::k_argmax, dim3(1), dim3(1024), 0, e->stream, e->logits, (int)d.vocab, e->d_tok);
+  const Q8Mat& m = e->out;
+  ProfScope ps(e, P_GEMV, q8_bytes(m, false));
+  const uint32_t grid = (m.rows + cm::GEMV_R - 1) / cm::GEMV_R;
+  hipLaunchKernelGGL(cm::k_gemv_argmax, dim3(grid), dim3(cm::GEMV_NT), cm::gemv_lds_bytes((int)m.k), e->stream, m.q,
+                     m.d, (int)m.rows, (int)m.k, e->xq, e->xs, e->logits, e->part_v, e->part_i, e->st, tokens, cap);
+}
+
+void run_embed(camelid_hip_engine* e) {
+  const camelid_hip_dims& d = e->d;
+  ProfScope ps(e, P_EMBED, d.hidden * (34.0 / 32.0 + 4.0));
+  hipLaunchKernelGGL(cm::k_embed_q8, dim3((d.hidden + 255) / 256), dim3(256), 0, e->stream, e->embd.q, e->embd.d,
+                     (int)d.hidden, e->st, e->h);
 }
 
 bool ready(const camelid_hip_engine* e) {
@@ -330,34 +350,66 @@ int check_launch(camelid_hip_engine* e) {
   return 0;
 }
 
+void drop_graph(camelid_hip_engine* e) {
+  if (e->graph_exec) (void)hipGraphExecDestroy(e->graph_exec);
+  if (e->graph) (void)hipGraphDestroy(e->graph);
+  e->graph_exec = nullptr;
+  e->graph = nullptr;
+}
+
+// Device-side decode step (embed -> layers -> head) as launched work on e->stream.
+void enqueue_device_step(camelid_hip_engine* e, float scale) {
+  run_embed(e);
+  run_stack(e, e->rope_cos, e->rope_sin, (int)(e->d.rope_dim / 2), scale);
+  run_head(e, e->tokens, e->tokens_cap);
+}
+
+// Captures one device-side step into a graph (once per scale).
+int ensure_graph(camelid_hip_engine* e, float scale) {
+  if (e->graph_exec && e->graph_scale == scale) return 0;
+  drop_graph(e);
+  HIP_TRY(e, hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+  enqueue_device_step(e, scale);
+  hipGraph_t g = nullptr;
+  hipError_t st = hipStreamEndCapture(e->stream, &g);
+  if (st != hipSuccess) return fail(e, std::string("graph capture failed: ") + hipGetErrorString(st));
+  e->graph = g;
+  st = hipGraphInstantiate(&e->graph_exec, g, nullptr, nullptr, 0);
+  if (st != hipSuccess) {
+    drop_graph(e);
+    return fail(e, std::string("graph instantiate failed: ") + hipGetErrorString(st));
+  }
+  e->graph_scale = scale;
+  return 0;
+}
+
 }  // namespace
 
 // ====================================================================== C ABI
 extern "C" {
 
-const char* camelid_hip_last_error(const camelid_hip_engine* e) {
-  return e ? e->err.c_str() : g_last_error.c_str();
-}
+const char* camelid_hip_last_error(const camelid_hip_engine* e) { return e ? e->err.c_str() : g_last_error.c_str(); }
 
 int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** out) {
   if (!dims || !out) return fail(nullptr, "null argument");
   *out = nullptr;
   const camelid_hip_dims& d = *dims;
-  if (!d.n_layers || !d.n_heads || !d.n_kv_heads || !d.head_dim || !d.hidden || !d.ffn_dim || !d.vocab ||
-      !d.max_pos)
+  if (!d.n_layers || !d.n_heads || !d.n_kv_heads || !d.head_dim || !d.hidden || !d.ffn_dim || !d.vocab || !d.max_pos)
     return fail(nullptr, "all dimensions must be nonzero");
   if (d.n_heads % d.n_kv_heads) return fail(nullptr, "n_heads must be a multiple of n_kv_heads");
   if (d.hidden % 32 || d.ffn_dim % 32 || d.head_dim % 32)
     return fail(nullptr, "hidden, ffn_dim and head_dim must be multiples of 32");
   if (d.head_dim > 512) return fail(nullptr, "head_dim > 512 is not supported");
+  if (d.hidden > 8192) return fail(nullptr, "hidden > 8192 is not supported by the RMSNorm kernel");
   if (d.rope_dim == 0 || d.rope_dim > d.head_dim || d.rope_dim % 2)
     return fail(nullptr, "rope_dim must be even and within head_dim");
-  if ((size_t)d.n_heads * d.head_dim % 32) return fail(nullptr, "n_heads*head_dim must be a multiple of 32");
-  if (((size_t)d.max_pos + d.head_dim) * 4 > 160 * 1024)
-    return fail(nullptr, "max_pos too large for the single-pass decode attention");
+  if (attn_lds_bytes(d.max_pos) > 96 * 1024) return fail(nullptr, "max_pos too large for the decode attention");
+  if (cm::gemv_lds_bytes((int)std::max(d.ffn_dim, d.n_heads * d.head_dim)) > 64 * 1024)
+    return fail(nullptr, "row width too large for the GEMV");
   auto* e = new camelid_hip_engine();
   e->d = d;
   if (const char* dev = std::getenv("CAMELID_HIP_DEVICE")) e->device = std::atoi(dev);
+  if (const char* g = std::getenv("CAMELID_HIP_GRAPHS")) e->use_graph = std::atoi(g) != 0;
   hipError_t st = hipSetDevice(e->device);
   if (st != hipSuccess) {
     fail(nullptr, std::string("hipSetDevice failed: ") + hipGetErrorString(st));
@@ -375,30 +427,28 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   const size_t kv_elems = (size_t)d.n_layers * d.n_kv_heads * d.max_pos * d.head_dim;
   const size_t act = std::max<size_t>({(size_t)d.hidden, (size_t)d.ffn_dim, nq});
   const uint32_t half = d.rope_dim / 2;
+  const size_t nparts = (d.vocab + cm::GEMV_R - 1) / cm::GEMV_R;
+  e->tokens_cap = d.max_pos;
   int rc = dev_alloc(e, &e->kc, kv_elems) || dev_alloc(e, &e->vc, kv_elems) || dev_alloc(e, &e->h, d.hidden) ||
-           dev_alloc(e, &e->qkv, nq + 2 * nkv) || dev_alloc(e, &e->qrot, nq) || dev_alloc(e, &e->att, nq) ||
+           dev_alloc(e, &e->qkv, nq + 2 * nkv) || dev_alloc(e, &e->att, nq) ||
            dev_alloc(e, &e->gu, 2 * (size_t)d.ffn_dim) || dev_alloc(e, &e->logits, d.vocab) ||
            dev_alloc(e, &e->hidden_cap, (size_t)(d.n_layers + 1) * d.hidden) || dev_alloc(e, &e->xq, act) ||
            dev_alloc(e, &e->xs, act / 32) || dev_alloc(e, &e->cos_cur, half) || dev_alloc(e, &e->sin_cur, half) ||
-           dev_alloc(e, &e->d_pos, 1) || dev_alloc(e, &e->d_tok, 1) ||
-           host_alloc(e, &e->p_emb, d.hidden) || host_alloc(e, &e->p_cos, half) || host_alloc(e, &e->p_sin, half) ||
-           host_alloc(e, &e->p_logits, d.vocab) || host_alloc(e, &e->p_tok, 1) || host_alloc(e, &e->p_pos, 1);
+           dev_alloc(e, &e->part_v, nparts) || dev_alloc(e, &e->part_i, nparts) || dev_alloc(e, &e->st, 1) ||
+           dev_alloc(e, &e->tokens, e->tokens_cap) || host_alloc(e, &e->p_emb, d.hidden) ||
+           host_alloc(e, &e->p_cos, half) || host_alloc(e, &e->p_sin, half) || host_alloc(e, &e->p_logits, d.vocab) ||
+           host_alloc(e, &e->p_st, 1);
   if (rc) {
     std::string m = e->err;
     camelid_hip_engine_free(e);
     return fail(nullptr, m);
   }
-  if (attn_lds_bytes(d) > 64 * 1024) {
-    st = hipFuncSetAttribute((const void*)cm::k_attn_decode, hipFuncAttributeMaxDynamicSharedMemorySize,
-                             (int)attn_lds_bytes(d));
-    if (st != hipSuccess) {
-      camelid_hip_engine_free(e);
-      return fail(nullptr, std::string("attention LDS attribute failed: ") + hipGetErrorString(st));
-    }
+  // A fresh cache reads as zeros (K/V past `filled` are never read); StepState starts at 0.
+  if (hipMemset(e->kc, 0, kv_elems * 2) != hipSuccess || hipMemset(e->vc, 0, kv_elems * 2) != hipSuccess ||
+      hipMemset(e->st, 0, sizeof(cm::StepState)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+    camelid_hip_engine_free(e);
+    return fail(nullptr, "initial device memset failed");
   }
-  // A fresh cache reads as zeros (K/V past `filled` are never read).
-  (void)hipMemset(e->kc, 0, kv_elems * 2);
-  (void)hipMemset(e->vc, 0, kv_elems * 2);
   *out = e;
   return 0;
 }
@@ -407,6 +457,7 @@ void camelid_hip_engine_free(camelid_hip_engine* e) {
   if (!e) return;
   (void)hipSetDevice(e->device);
   if (e->stream) (void)hipStreamSynchronize(e->stream);
+  drop_graph(e);
   for (hipEvent_t ev : e->event_pool) (void)hipEventDestroy(ev);
   for (void* p : e->dev_allocs) (void)hipFree(p);
   for (void* p : e->host_allocs) (void)hipHostFree(p);
@@ -420,6 +471,7 @@ int camelid_hip_set_layer(camelid_hip_engine* e, uint32_t layer, const uint8_t* 
   if (!e) return fail(nullptr, "null engine");
   if (layer >= e->d.n_layers) return fail(e, "layer index out of range");
   if (!w || !len || !quant || !attn_norm || !ffn_norm) return fail(e, "null argument");
+  if ((q_norm == nullptr) != (k_norm == nullptr)) return fail(e, "q_norm and k_norm must be given together");
   for (int i = 0; i < 7; ++i)
     if (quant[i] != CAMELID_Q8_0) return fail(e, "only Q8_0 projections are supported by this build");
   HIP_TRY(e, hipSetDevice(e->device));
@@ -432,14 +484,15 @@ int camelid_hip_set_layer(camelid_hip_engine* e, uint32_t layer, const uint8_t* 
       upload_q8(e, &L.down, {{w[6], len[6], d.hidden}}, d.ffn_dim, q8_layout) ||
       upload_f32(e, &L.attn_norm, attn_norm, d.hidden) || upload_f32(e, &L.ffn_norm, ffn_norm, d.hidden))
     return 1;
-  if (q_norm && upload_f32(e, &L.q_norm, q_norm, d.head_dim)) return 1;
-  if (k_norm && upload_f32(e, &L.k_norm, k_norm, d.head_dim)) return 1;
+  if (q_norm && (upload_f32(e, &L.q_norm, q_norm, d.head_dim) || upload_f32(e, &L.k_norm, k_norm, d.head_dim)))
+    return 1;
   L.set = true;
+  drop_graph(e);
   return 0;
 }
 
-int camelid_hip_set_output(camelid_hip_engine* e, const float* final_norm, const uint8_t* w, size_t len,
-                           uint8_t quant, uint8_t q8_layout) {
+int camelid_hip_set_output(camelid_hip_engine* e, const float* final_norm, const uint8_t* w, size_t len, uint8_t quant,
+                           uint8_t q8_layout) {
   if (!e) return fail(nullptr, "null engine");
   if (!final_norm || !w) return fail(e, "null argument");
   if (quant != CAMELID_Q8_0) return fail(e, "only a Q8_0 output projection is supported by this build");
@@ -448,6 +501,7 @@ int camelid_hip_set_output(camelid_hip_engine* e, const float* final_norm, const
       upload_f32(e, &e->out_norm, final_norm, e->d.hidden))
     return 1;
   e->out_set = true;
+  drop_graph(e);
   return 0;
 }
 
@@ -458,6 +512,7 @@ int camelid_hip_set_embedding(camelid_hip_engine* e, const uint8_t* w, size_t le
   HIP_TRY(e, hipSetDevice(e->device));
   if (upload_q8(e, &e->embd, {{w, len, e->d.vocab}}, e->d.hidden, q8_layout)) return 1;
   e->embd_set = true;
+  drop_graph(e);
   return 0;
 }
 
@@ -473,6 +528,7 @@ int camelid_hip_set_rope_table(camelid_hip_engine* e, const float* cos_all, cons
   HIP_TRY(e, hipMemcpy(e->rope_cos, cos_all, (size_t)n_pos * half * 4, hipMemcpyHostToDevice));
   HIP_TRY(e, hipMemcpy(e->rope_sin, sin_all, (size_t)n_pos * half * 4, hipMemcpyHostToDevice));
   e->rope_rows = n_pos;
+  drop_graph(e);
   return 0;
 }
 
@@ -493,6 +549,7 @@ int camelid_hip_seed_layer(camelid_hip_engine* e, uint32_t layer, const float* c
   if (layer >= e->d.n_layers || n_pos > e->d.max_pos) return fail(e, "seed_layer out of range");
   if (!ck || !cv) return fail(e, "null argument");
   HIP_TRY(e, hipSetDevice(e->device));
+  HIP_TRY(e, hipStreamSynchronize(e->stream));
   const camelid_hip_dims& d = e->d;
   std::vector<uint16_t> hk((size_t)n_pos * d.head_dim), hv(hk.size());
   for (uint32_t h = 0; h < d.n_kv_heads; ++h) {
@@ -530,8 +587,7 @@ int camelid_hip_read_kv_layer(camelid_hip_engine* e, uint32_t layer, uint32_t n,
 }
 
 int camelid_hip_forward_token(camelid_hip_engine* e, const float* emb, const float* cos_tab, const float* sin_tab,
-                              uint32_t position, float scale, int want_logits, uint32_t* tok_out,
-                              float* logits_out) {
+                              uint32_t position, float scale, int want_logits, uint32_t* tok_out, float* logits_out) {
   if (!e) return fail(nullptr, "null engine");
   if (!ready(e)) return fail(e, "weights not ready");
   if (!emb || !cos_tab || !sin_tab) return fail(e, "null argument");
@@ -543,21 +599,27 @@ int camelid_hip_forward_token(camelid_hip_engine* e, const float* emb, const flo
   std::memcpy(e->p_emb, emb, d.hidden * 4);
   std::memcpy(e->p_cos, cos_tab, half * 4);
   std::memcpy(e->p_sin, sin_tab, half * 4);
-  *e->p_pos = position;
+  *e->p_st = cm::StepState{position, 0u, 0u, 0u};
   e->cur_pos = position;
   HIP_TRY(e, hipMemcpyAsync(e->h, e->p_emb, d.hidden * 4, hipMemcpyHostToDevice, e->stream));
   HIP_TRY(e, hipMemcpyAsync(e->cos_cur, e->p_cos, half * 4, hipMemcpyHostToDevice, e->stream));
   HIP_TRY(e, hipMemcpyAsync(e->sin_cur, e->p_sin, half * 4, hipMemcpyHostToDevice, e->stream));
-  HIP_TRY(e, hipMemcpyAsync(e->d_pos, e->p_pos, 4, hipMemcpyHostToDevice, e->stream));
-  run_stack(e, e->cos_cur, e->sin_cur, scale);
-  run_head(e);
-  if (check_launch(e)) { e->filled = 0; return 1; }
-  HIP_TRY(e, hipMemcpyAsync(e->p_tok, e->d_tok, 4, hipMemcpyDeviceToHost, e->stream));
+  HIP_TRY(e, hipMemcpyAsync(e->st, e->p_st, sizeof(cm::StepState), hipMemcpyHostToDevice, e->stream));
+  run_stack(e, e->cos_cur, e->sin_cur, 0, scale);
+  run_head(e, nullptr, 0);
+  if (check_launch(e)) {
+    e->filled = 0;
+    return 1;
+  }
+  HIP_TRY(e, hipMemcpyAsync(e->p_st, e->st, sizeof(cm::StepState), hipMemcpyDeviceToHost, e->stream));
   if (want_logits && logits_out)
     HIP_TRY(e, hipMemcpyAsync(e->p_logits, e->logits, (size_t)d.vocab * 4, hipMemcpyDeviceToHost, e->stream));
   hipError_t st = hipStreamSynchronize(e->stream);
-  if (st != hipSuccess) { e->filled = 0; return fail(e, std::string("forward_token: ") + hipGetErrorString(st)); }
-  if (tok_out) *tok_out = *e->p_tok;
+  if (st != hipSuccess) {
+    e->filled = 0;
+    return fail(e, std::string("forward_token: ") + hipGetErrorString(st));
+  }
+  if (tok_out) *tok_out = e->p_st->tok;
   if (want_logits && logits_out) std::memcpy(logits_out, e->p_logits, (size_t)d.vocab * 4);
   e->filled = position + 1;
   return 0;
@@ -574,39 +636,47 @@ int camelid_hip_prefill(camelid_hip_engine* e, const float* embs, const float* c
   if (n == 0) return 0;
   HIP_TRY(e, hipSetDevice(e->device));
   const size_t half = d.rope_dim / 2;
-  // Stage every row once; the per-token layer stack reads its slice.
   float *d_embs = nullptr, *d_cos = nullptr, *d_sin = nullptr;
-  uint32_t* d_posv = nullptr;
+  cm::StepState* d_sts = nullptr;
   HIP_TRY(e, hipMalloc(&d_embs, (size_t)n * d.hidden * 4));
   HIP_TRY(e, hipMalloc(&d_cos, (size_t)n * half * 4));
   HIP_TRY(e, hipMalloc(&d_sin, (size_t)n * half * 4));
-  HIP_TRY(e, hipMalloc(&d_posv, (size_t)n * 4));
-  std::vector<uint32_t> pv(n);
-  for (uint32_t t = 0; t < n; ++t) pv[t] = e->filled + t;
+  HIP_TRY(e, hipMalloc(&d_sts, (size_t)n * sizeof(cm::StepState)));
+  std::vector<cm::StepState> sv(n);
+  for (uint32_t t = 0; t < n; ++t) sv[t] = cm::StepState{e->filled + t, 0u, 0u, 0u};
   int rc = 0;
   do {
     if (hipMemcpy(d_embs, embs, (size_t)n * d.hidden * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(d_cos, cos_all, (size_t)n * half * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(d_sin, sin_all, (size_t)n * half * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(d_posv, pv.data(), (size_t)n * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        hipMemcpy(d_sts, sv.data(), (size_t)n * sizeof(cm::StepState), hipMemcpyHostToDevice) != hipSuccess) {
       rc = fail(e, "prefill staging copy failed");
       break;
     }
     for (uint32_t t = 0; t < n; ++t) {
       (void)hipMemcpyAsync(e->h, d_embs + (size_t)t * d.hidden, d.hidden * 4, hipMemcpyDeviceToDevice, e->stream);
-      (void)hipMemcpyAsync(e->d_pos, d_posv + t, 4, hipMemcpyDeviceToDevice, e->stream);
-      e->cur_pos = pv[t];
-      run_stack(e, d_cos + (size_t)t * half, d_sin + (size_t)t * half, scale);
+      (void)hipMemcpyAsync(e->st, d_sts + t, sizeof(cm::StepState), hipMemcpyDeviceToDevice, e->stream);
+      e->cur_pos = sv[t].pos;
+      run_stack(e, d_cos + (size_t)t * half, d_sin + (size_t)t * half, 0, scale);
     }
-    if (check_launch(e)) { rc = 1; break; }
+    if (check_launch(e)) {
+      rc = 1;
+      break;
+    }
     hipError_t st = hipStreamSynchronize(e->stream);
-    if (st != hipSuccess) { rc = fail(e, std::string("prefill: ") + hipGetErrorString(st)); break; }
+    if (st != hipSuccess) {
+      rc = fail(e, std::string("prefill: ") + hipGetErrorString(st));
+      break;
+    }
   } while (0);
   (void)hipFree(d_embs);
   (void)hipFree(d_cos);
   (void)hipFree(d_sin);
-  (void)hipFree(d_posv);
-  if (rc) { e->filled = 0; return rc; }
+  (void)hipFree(d_sts);
+  if (rc) {
+    e->filled = 0;
+    return rc;
+  }
   e->filled += n;
   return 0;
 }
@@ -618,45 +688,37 @@ int camelid_hip_generate(camelid_hip_engine* e, uint32_t token, uint32_t positio
   if (!tokens_out) return fail(e, "null argument");
   const camelid_hip_dims& d = e->d;
   if ((size_t)position + n_steps > e->rope_rows) return fail(e, "rope table does not cover the requested steps");
+  if (n_steps > e->tokens_cap) return fail(e, "more steps than the token ring holds");
   if (token >= d.vocab) return fail(e, "token id out of range");
   if (!std::isfinite(scale)) return fail(e, "attention score scale must be finite");
   if (n_steps == 0) return 0;
   HIP_TRY(e, hipSetDevice(e->device));
-  const size_t half = d.rope_dim / 2;
-  uint32_t *d_toks = nullptr, *d_posv = nullptr;
-  HIP_TRY(e, hipMalloc(&d_toks, (size_t)(n_steps + 1) * 4));
-  HIP_TRY(e, hipMalloc(&d_posv, (size_t)n_steps * 4));
-  std::vector<uint32_t> pv(n_steps);
-  for (uint32_t t = 0; t < n_steps; ++t) pv[t] = position + t;
-  int rc = 0;
-  do {
-    if (hipMemcpy(d_posv, pv.data(), (size_t)n_steps * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(d_toks, &token, 4, hipMemcpyHostToDevice) != hipSuccess) {
-      rc = fail(e, "generate staging copy failed");
-      break;
-    }
-    for (uint32_t t = 0; t < n_steps; ++t) {
-      (void)hipMemcpyAsync(e->d_pos, d_posv + t, 4, hipMemcpyDeviceToDevice, e->stream);
-      e->cur_pos = pv[t];
-      {
-        ProfScope ps(e, P_EMBED, d.hidden * (34.0 / 32.0 + 4.0));
-        hipLaunchKernelGGL(cm::k_embed_q8, dim3((d.hidden + 255) / 256), dim3(256), 0, e->stream, e->embd.q,
-                           e->embd.d, (int)d.hidden, d_toks + t, e->h);
+  const bool graph = e->use_graph && !e->profiling && !e->capture;
+  if (graph && ensure_graph(e, scale)) return 1;
+  *e->p_st = cm::StepState{position, token, 0u, 0u};
+  HIP_TRY(e, hipMemcpyAsync(e->st, e->p_st, sizeof(cm::StepState), hipMemcpyHostToDevice, e->stream));
+  for (uint32_t t = 0; t < n_steps; ++t) {
+    e->cur_pos = position + t;
+    if (graph) {
+      hipError_t st = hipGraphLaunch(e->graph_exec, e->stream);
+      if (st != hipSuccess) {
+        e->filled = 0;
+        return fail(e, std::string("graph launch failed: ") + hipGetErrorString(st));
       }
-      const size_t p = position + t;
-      run_stack(e, e->rope_cos + p * half, e->rope_sin + p * half, scale);
-      run_head(e);
-      (void)hipMemcpyAsync(d_toks + t + 1, e->d_tok, 4, hipMemcpyDeviceToDevice, e->stream);
+    } else {
+      enqueue_device_step(e, scale);
     }
-    if (check_launch(e)) { rc = 1; break; }
-    hipError_t st = hipStreamSynchronize(e->stream);
-    if (st != hipSuccess) { rc = fail(e, std::string("generate: ") + hipGetErrorString(st)); break; }
-    if (hipMemcpy(tokens_out, d_toks + 1, (size_t)n_steps * 4, hipMemcpyDeviceToHost) != hipSuccess)
-      rc = fail(e, "generate token copy failed");
-  } while (0);
-  (void)hipFree(d_toks);
-  (void)hipFree(d_posv);
-  if (rc) { e->filled = 0; return rc; }
+  }
+  if (check_launch(e)) {
+    e->filled = 0;
+    return 1;
+  }
+  hipError_t st = hipStreamSynchronize(e->stream);
+  if (st != hipSuccess) {
+    e->filled = 0;
+    return fail(e, std::string("generate: ") + hipGetErrorString(st));
+  }
+  HIP_TRY(e, hipMemcpy(tokens_out, e->tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost));
   e->filled = position + n_steps;
   return 0;
 }
@@ -711,17 +773,15 @@ int camelid_hip_device_info(char* name, size_t name_len, int* n_cu) {
   hipDeviceProp_t p;
   hipError_t st = hipGetDeviceProperties(&p, dev);
   if (st != hipSuccess) return fail(nullptr, std::string("hipGetDeviceProperties: ") + hipGetErrorString(st));
-  if (name && name_len) {
-    std::snprintf(name, name_len, "%s (%s)", p.name, p.gcnArchName);
-  }
+  if (name && name_len) std::snprintf(name, name_len, "%s%s%s", p.name, p.name[0] ? " " : "", p.gcnArchName);
   if (n_cu) *n_cu = p.multiProcessorCount;
   return 0;
 }
 
 // ------------------------------------------------------------------ kernel-level ABI
-#define G_TRY(expr)                                                                          \
-  do {                                                                                       \
-    hipError_t _st = (expr);                                                                 \
+#define G_TRY(expr)                                                                                    \
+  do {                                                                                                 \
+    hipError_t _st = (expr);                                                                           \
     if (_st != hipSuccess) return fail(nullptr, std::string(#expr) + ": " + hipGetErrorString(_st)); \
   } while (0)
 
@@ -765,8 +825,8 @@ static int launch_status(const char* what) {
 int camelid_hip_q8_0_gemv(const int8_t* wq, const uint16_t* wd, uint32_t rows, uint32_t k, const int8_t* xq,
                           const float* xs, float* y, const float* resid, void* stream) {
   if (!wq || !wd || !xq || !xs || !y) return fail(nullptr, "null argument");
-  if (k % 32 || rows == 0) return fail(nullptr, "k must be a nonzero multiple of 32 and rows > 0");
-  if (gemv_lds_bytes(k) > 64 * 1024) return fail(nullptr, "k too large for the GEMV LDS stage");
+  if (k % 32 || k == 0 || rows == 0) return fail(nullptr, "k must be a nonzero multiple of 32 and rows > 0");
+  if (cm::gemv_lds_bytes((int)k) > 64 * 1024) return fail(nullptr, "k too large for the GEMV LDS stage");
   Q8Mat m;
   m.q = const_cast<int8_t*>(wq);
   m.d = const_cast<uint16_t*>(wd);
@@ -779,15 +839,15 @@ int camelid_hip_q8_0_gemv(const int8_t* wq, const uint16_t* wd, uint32_t rows, u
 int camelid_hip_q8_0_block_dots(const int8_t* wq, uint32_t rows, uint32_t k, const int8_t* xq, int32_t* out,
                                 void* stream) {
   if (!wq || !xq || !out) return fail(nullptr, "null argument");
-  if (k % 32 || rows == 0) return fail(nullptr, "k must be a nonzero multiple of 32 and rows > 0");
+  if (k % 32 || k == 0 || rows == 0) return fail(nullptr, "k must be a nonzero multiple of 32 and rows > 0");
   hipLaunchKernelGGL(cm::k_q8_block_dots, dim3(rows), dim3(64), 0, (hipStream_t)stream, wq, (int)k, xq, out);
   return launch_status("q8_0_block_dots");
 }
 
-int camelid_hip_rmsnorm_quantize(const float* x, const float* w, uint32_t n, float eps, int8_t* xq, float* xs,
-                                 float* y, void* stream) {
+int camelid_hip_rmsnorm_quantize(const float* x, const float* w, uint32_t n, float eps, int8_t* xq, float* xs, float* y,
+                                 void* stream) {
   if (!x || !w || !xq || !xs) return fail(nullptr, "null argument");
-  if (n == 0 || n % 32 || n > 16384) return fail(nullptr, "n must be a multiple of 32 in (0, 16384]");
+  if (n == 0 || n % 32 || n > 8192) return fail(nullptr, "n must be a multiple of 32 in (0, 8192]");
   launch_rmsnorm_quant(x, w, n, eps, xq, xs, y, (hipStream_t)stream);
   return launch_status("rmsnorm_quantize");
 }
@@ -795,18 +855,17 @@ int camelid_hip_rmsnorm_quantize(const float* x, const float* w, uint32_t n, flo
 int camelid_hip_quantize_q8_0(const float* x, uint32_t n, int8_t* xq, float* xs, void* stream) {
   if (!x || !xq || !xs) return fail(nullptr, "null argument");
   if (n % 32) return fail(nullptr, "n must be a multiple of 32");
-  const uint32_t nb = n / 32;
-  if (nb == 0) return 0;
-  hipLaunchKernelGGL(cm::k_quantize_q8_0, dim3((nb + 63) / 64), dim3(64), 0, (hipStream_t)stream, x, (int)n, xq, xs);
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(cm::k_quantize_q8_0, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, x, (int)n, xq,
+                     xs);
   return launch_status("quantize_q8_0");
 }
 
 int camelid_hip_silu_mul_quantize(const float* gu, uint32_t n, int8_t* xq, float* xs, float* act, void* stream) {
   if (!gu || !xq || !xs) return fail(nullptr, "null argument");
   if (n % 32) return fail(nullptr, "n must be a multiple of 32");
-  const uint32_t nb = n / 32;
-  if (nb == 0) return 0;
-  hipLaunchKernelGGL(cm::k_silu_mul_quant, dim3((nb + 63) / 64), dim3(64), 0, (hipStream_t)stream, gu, (int)n, xq,
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(cm::k_silu_mul_quant, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, gu, (int)n, xq,
                      xs, act);
   return launch_status("silu_mul_quantize");
 }
@@ -825,21 +884,17 @@ int camelid_hip_rope_kv(const float* qkv, uint32_t n_heads, uint32_t n_kv, uint3
 }
 
 int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const uint16_t* vc, uint32_t layer,
-                                 uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t max_pos,
-                                 const uint32_t* d_pos, float scale, float* att_out, int8_t* xq, float* xs,
-                                 void* stream) {
+                                 uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t max_pos, const uint32_t* d_pos,
+                                 float scale, float* att_out, int8_t* xq, float* xs, void* stream) {
   if (!qrot || !kc || !vc || !d_pos || !att_out || !xq || !xs) return fail(nullptr, "null argument");
   if (!n_heads || !n_kv || n_heads % n_kv || hd % 32 || hd == 0 || hd > 512)
     return fail(nullptr, "invalid head geometry");
-  const size_t lds = ((size_t)max_pos + hd) * 4;
-  if (lds > 160 * 1024) return fail(nullptr, "max_pos too large for the single-pass decode attention");
-  if (lds > 64 * 1024) {
-    hipError_t st = hipFuncSetAttribute((const void*)cm::k_attn_decode, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        (int)lds);
-    if (st != hipSuccess) return fail(nullptr, std::string("attention LDS attribute: ") + hipGetErrorString(st));
-  }
-  hipLaunchKernelGGL(cm::k_attn_decode, dim3(n_heads), dim3(256), lds, (hipStream_t)stream, qrot, kc, vc,
-                     (int)layer, (int)n_heads, (int)n_kv, (int)hd, (int)max_pos, d_pos, scale, att_out, xq, xs);
+  if (attn_lds_bytes(max_pos) > 96 * 1024) return fail(nullptr, "max_pos too large for the decode attention");
+  hipLaunchKernelGGL(cm::k_attention<false>, dim3(n_heads), dim3(cm::ATT_NT), attn_lds_bytes(max_pos),
+                     (hipStream_t)stream, qrot, (int)n_heads, (int)n_kv, (int)hd, (int)hd, 0, (const float*)nullptr,
+                     (const float*)nullptr, 0, (const float*)nullptr, (const float*)nullptr, 0.0f,
+                     const_cast<uint16_t*>(kc), const_cast<uint16_t*>(vc), (int)layer, (int)max_pos, d_pos, scale,
+                     att_out, xq, xs);
   return launch_status("attention_decode");
 }
 

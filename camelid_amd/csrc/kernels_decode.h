@@ -1,14 +1,15 @@
 // kernels_decode.h -- HIP/CDNA4 kernels of the resident decode step (gfx950, wave64).
 //
-// Bit-exactness contract: every f32 value that reaches a Q8_0 quantizer, the KV
-// cache or the argmax is produced by the same sequence of IEEE f32 operations as
-// Camelid's CPU path.  Integer work (int8 dot4) is reassociated freely (exact);
-// f32 reductions are folded in the CPU's order by one lane per output.
+// Bit-exactness contract: every f32 value that reaches a Q8_0 quantizer, the KV cache or
+// the argmax is produced by the same sequence of IEEE f32 operations as Camelid's CPU
+// path.  Integer work (int8 dot4) and max/argmax are reassociated freely (exact); every
+// f32 sum is folded in the CPU's order by one lane per output.
 //
 // Weight layout in HBM ("Q8R", repacked from the 34-byte GGUF Q8_0 wire blocks):
-//   quants: int8 [rows][K] row-major, 16-byte aligned rows (K % 32 == 0)
+//   quants: int8 [rows][K] row-major (K % 32 == 0), so R consecutive rows are one
+//           contiguous R*K-byte slab
 //   scales: f16 bits [rows][K/32]
-// Total bytes = rows*K*34/32, the same as the wire format; the split keeps every
+// Total bytes = rows*K*34/32, the same as the wire format; the split makes every
 // wavefront load a 16-byte-aligned, fully coalesced dwordx4.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -30,74 +31,53 @@ __device__ __forceinline__ int dot4x4(int4 w, int4 x, int acc) {
   return acc;
 }
 
-// Exact int32 dot of one 32-value block, split over a lane pair: each lane of the pair
-// holds one 16-byte half (chunk c = 2*block + (lane & 1)); the pair sum is returned to both.
-__device__ __forceinline__ int pair_block_dot(const int4* w4, const int4* x4, int c) {
-  int s = dot4x4(w4[c], x4[c], 0);
-  return s + __shfl_xor(s, 1);
-}
-
-// Per-(row, block) int32 dots through the GEMV's own dot path (test hook).
-// grid = rows, block = 64.
-__global__ __launch_bounds__(64) void k_q8_block_dots(const int8_t* __restrict__ wq, int K,
-                                                      const int8_t* __restrict__ xq, int32_t* __restrict__ out) {
-  const int row = blockIdx.x, lane = threadIdx.x;
-  const int4* w4 = reinterpret_cast<const int4*>(wq + (size_t)row * K);
-  const int4* x4 = reinterpret_cast<const int4*>(xq);
-  for (int c = lane; c < (K >> 4); c += 64) {
-    const int s = pair_block_dot(w4, x4, c);
-    if ((lane & 1) == 0) out[(size_t)row * (K >> 5) + (c >> 1)] = s;
-  }
-}
-
 // ---------------------------------------------------------------------------
-// Q8_0 GEMV, faithful.  y[row] = (resid ? resid[row] : 0) + fold_b term(row, b),
-//   term = (float(int_dot(w_b, x_b)) * w_scale_b) * x_scale_b   (inference.rs:19871-19905)
-// Each wave owns RW rows.  Lanes stream a row's quants as 16-byte chunks (two lanes per
-// 32-value block, combined with a lane-pair shuffle: integer, exact), write the per-block
-// f32 terms to LDS, then lane r folds row r's terms in block order.
-// grid = ceil(rows / (4*RW)), block = 256, dynamic LDS = 4*RW*(nb+1)*4 bytes.
-template <int RW>
-__global__ __launch_bounds__(256) void k_q8_gemv(const int8_t* __restrict__ wq,
-                                                 const uint16_t* __restrict__ wd, int rows, int K,
-                                                 const int8_t* __restrict__ xq,
-                                                 const float* __restrict__ xs,
-                                                 float* y, const float* resid) {
-  extern __shared__ float lds[];
-  const int nb = K >> 5;
-  const int nchunk = K >> 4;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * 4 + wave) * RW;
-  float* t = lds + wave * RW * (nb + 1);
-  const int4* x4 = reinterpret_cast<const int4*>(xq);
+// Serial f32 fold of n LDS floats in index order (one lane), the CPU's summation order.
+// LDS reads run W float4 groups ahead of the dependent add chain so the chain issues
+// back to back.  p must be 16-byte aligned.
+template <int W = 8>
+__device__ __forceinline__ float fold_lds(const float* p, int n, float acc = 0.0f) {
+  const float4* q = reinterpret_cast<const float4*>(p);
+  const int g = n >> 2;
+  float4 buf[W];
 #pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    const int row = min(row0 + r, rows - 1);  // clamped: uniform control flow, result discarded
-    const int4* w4 = reinterpret_cast<const int4*>(wq + (size_t)row * K);
-    const uint16_t* d = wd + (size_t)row * nb;
-    for (int c = lane; c < nchunk; c += 64) {
-      const int s = pair_block_dot(w4, x4, c);
-      if ((lane & 1) == 0) {
-        const int b = c >> 1;
-        t[r * (nb + 1) + b] = ((float)s * half_bits_to_float(d[b])) * xs[b];
+  for (int i = 0; i < W; ++i)
+    if (i < g) buf[i] = q[i];
+  for (int base = 0; base < g; base += W) {
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      if (base + i < g) {
+        const float4 v = buf[i];
+        if (base + i + W < g) buf[i] = q[base + i + W];
+        acc += v.x;
+        acc += v.y;
+        acc += v.z;
+        acc += v.w;
       }
     }
   }
-  __syncthreads();
-  if (lane < RW) {
-    const int row = row0 + lane;
-    if (row < rows) {
-      const float* tr = t + lane * (nb + 1);
-      float acc = 0.0f;
-      for (int b = 0; b < nb; ++b) acc += tr[b];
-      y[row] = resid ? resid[row] + acc : acc;
-    }
-  }
+  for (int i = g << 2; i < n; ++i) acc += p[i];
+  return acc;
 }
 
-// ---------------------------------------------------------------------------
-// Block reductions (exact: max / argmax only).
+// Q8_0 quantization of one 32-value block held one value per lane by a 32-lane group
+// (lanes 0-31 or 32-63 of a wave).  Returns the block's f16-valued scale (same in every
+// lane); *q receives this lane's quant.  inference.rs:16953-16971.
+__device__ __forceinline__ float quantize_lane32(float v, int8_t* q) {
+  float amax = fabsf(v);
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  const float unrounded = amax / 127.0f;
+  const float scale = f16_bits_to_f32(f32_to_f16_bits(unrounded));
+  const float inv = unrounded == 0.0f ? 0.0f : 1.0f / unrounded;
+  float r = roundf(v * inv);
+  r = fminf(fmaxf(r, -128.0f), 127.0f);
+  *q = (int8_t)r;
+  return scale;
+}
+
 __device__ __forceinline__ float block_max(float v, float* red) {
+#pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
   __syncthreads();
@@ -108,111 +88,254 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return m;
 }
 
-// Quantize `n` (multiple of 32) f32 values in LDS to Q8_0, one thread per block.
-__device__ __forceinline__ void quantize_blocks_from_lds(const float* v, int n, int8_t* xq, float* xs) {
-  for (int b = threadIdx.x; b < (n >> 5); b += blockDim.x) {
-    int8_t q[32];
-    xs[b] = quantize_q8_0_block(v + b * 32, q);
-    int4* dst = reinterpret_cast<int4*>(xq + b * 32);
-    const int4* src = reinterpret_cast<const int4*>(q);
-    dst[0] = src[0];
-    dst[1] = src[1];
+// ---------------------------------------------------------------------------
+// Per-(row, block) int32 dots (test hook for the bit-exact block-dot contract): the
+// same lane-pair dot4 path as the GEMV.  grid = rows, block = 64.
+__global__ __launch_bounds__(64) void k_q8_block_dots(const int8_t* __restrict__ wq, int K,
+                                                      const int8_t* __restrict__ xq, int32_t* __restrict__ out) {
+  const int row = blockIdx.x, lane = threadIdx.x;
+  const int4* w4 = reinterpret_cast<const int4*>(wq + (size_t)row * K);
+  const int4* x4 = reinterpret_cast<const int4*>(xq);
+  for (int c = lane; c < (K >> 4); c += 64) {
+    int s = dot4x4(w4[c], x4[c], 0);
+    s += __shfl_xor(s, 1);
+    if ((lane & 1) == 0) out[(size_t)row * (K >> 5) + (c >> 1)] = s;
   }
 }
 
-// Sequential f32 sum of LDS values 0..n-1 (one thread), the CPU's fold order.
-__device__ __forceinline__ float serial_sum_lds(const float* v, int n) {
-  float acc = 0.0f;
-  int i = 0;
-  for (; i + 8 <= n; i += 8) {
-    const float4 a = *reinterpret_cast<const float4*>(v + i);
-    const float4 b = *reinterpret_cast<const float4*>(v + i + 4);
-    acc += a.x; acc += a.y; acc += a.z; acc += a.w;
-    acc += b.x; acc += b.y; acc += b.z; acc += b.w;
+// ---------------------------------------------------------------------------
+// Q8_0 GEMV, faithful:  y[row] = (resid ? resid[row] : 0) + fold_b term(row, b),
+//   term = (float(int_dot(w_b, x_b)) * w_scale_b) * x_scale_b  (inference.rs:19871-19905).
+// A workgroup of 256 threads owns GEMV_R consecutive rows = one contiguous slab of
+// GEMV_R*K quant bytes.  The slab's 16-byte chunks are dealt round-robin (thread t takes
+// chunks t, t+256, ...), so each workgroup-wide load is 4 KB contiguous.  Lane pairs
+// (2j, 2j+1) always hold the two halves of one 32-value block (chunks per row is even),
+// combined with one integer shuffle.  Even lanes turn the block dot into its f32 term in
+// LDS; then lane r of wave 0 folds row r's terms in block order.
+// Dynamic LDS: K bytes (x quants) + nb*4 (x scales) + GEMV_R*(nb+4)*4 (terms).
+constexpr int GEMV_R = 8;
+constexpr int GEMV_NT = 256;
+
+__host__ __device__ inline int gemv_term_stride(int nb) { return ((nb + 3) & ~3) + 4; }
+__host__ __device__ inline size_t gemv_term_offset(int K) { return ((size_t)K + (size_t)(K >> 5) * 4 + 15) & ~(size_t)15; }
+__host__ __device__ inline size_t gemv_lds_bytes(int K) {
+  return gemv_term_offset(K) + (size_t)GEMV_R * gemv_term_stride(K >> 5) * 4;
+}
+
+// Shared body; returns (in lanes 0..GEMV_R-1 of wave 0) the folded sum of row row0+lane.
+__device__ __forceinline__ float gemv_rows(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, int rows,
+                                           int K, const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                           int row0, unsigned char* smem) {
+  const int nb = K >> 5;
+  const int cpr = K >> 4;  // 16-byte chunks per row
+  int8_t* xl = reinterpret_cast<int8_t*>(smem);
+  float* xsl = reinterpret_cast<float*>(smem + K);
+  float* t = reinterpret_cast<float*>(smem + gemv_term_offset(K));  // [GEMV_R][stride], 16-byte aligned rows
+  const int tid = threadIdx.x;
+  // stage the activation (K quants + nb scales) in LDS
+  for (int c = tid; c < cpr; c += GEMV_NT)
+    reinterpret_cast<int4*>(xl)[c] = reinterpret_cast<const int4*>(xq)[c];
+  for (int b = tid; b < nb; b += GEMV_NT) xsl[b] = xs[b];
+  __syncthreads();
+  const int nrows = min(GEMV_R, rows - row0);
+  const int total = nrows * cpr;
+  const int4* slab = reinterpret_cast<const int4*>(wq + (size_t)row0 * K);
+  const uint16_t* dslab = wd + (size_t)row0 * nb;
+  const int stride = gemv_term_stride(nb);
+  // (r, c) of chunk f tracked incrementally (no integer division in the stream loop)
+  int r = tid / cpr;
+  int c = tid - r * cpr;
+#pragma unroll 4
+  for (int f = tid; f < total; f += GEMV_NT) {
+    int s = dot4x4(slab[f], reinterpret_cast<const int4*>(xl)[c], 0);
+    s += __shfl_xor(s, 1);
+    if ((tid & 1) == 0) {
+      const int b = c >> 1;
+      t[r * stride + b] = ((float)s * half_bits_to_float(dslab[r * nb + b])) * xsl[b];
+    }
+    c += GEMV_NT;
+    while (c >= cpr) {
+      c -= cpr;
+      ++r;
+    }
   }
-  for (; i < n; ++i) acc += v[i];
+  __syncthreads();
+  float acc = 0.0f;
+  if (tid < nrows) acc = fold_lds(t + tid * stride, nb);
   return acc;
+}
+
+__global__ __launch_bounds__(GEMV_NT) void k_gemv(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                                  int rows, int K, const int8_t* __restrict__ xq,
+                                                  const float* __restrict__ xs, float* y, const float* resid) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int row0 = blockIdx.x * GEMV_R;
+  const float acc = gemv_rows(wq, wd, rows, K, xq, xs, row0, smem);
+  const int tid = threadIdx.x;
+  if (tid < GEMV_R && row0 + tid < rows) {
+    const int row = row0 + tid;
+    y[row] = resid ? resid[row] + acc : acc;
+  }
+}
+
+// Decode-loop state shared by the step's kernels (device memory).
+struct StepState {
+  uint32_t pos;      // position of the token being computed
+  uint32_t tok;      // current token (input of the next step)
+  uint32_t step;     // index into the generated-token ring
+  uint32_t counter;  // last-workgroup counter of the lm_head GEMV (always returns to 0)
+};
+
+// lm_head GEMV fused with greedy argmax (inference.rs:5912-5925: first index of the max,
+// strict '>').  Each workgroup reduces its rows to (value, index) with ties to the lower
+// index; the last workgroup to finish (atomic ticket) reduces the partials in the same
+// way, writes the token, appends it to tokens[step] and advances the position.
+__global__ __launch_bounds__(GEMV_NT) void k_gemv_argmax(const int8_t* __restrict__ wq,
+                                                         const uint16_t* __restrict__ wd, int rows, int K,
+                                                         const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                                         float* __restrict__ logits, float* __restrict__ part_v,
+                                                         uint32_t* __restrict__ part_i, StepState* st,
+                                                         uint32_t* __restrict__ tokens, uint32_t tokens_cap) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int s_last;
+  __shared__ float rv[GEMV_NT / 64];
+  __shared__ uint32_t ri[GEMV_NT / 64];
+  const int row0 = blockIdx.x * GEMV_R;
+  const float acc = gemv_rows(wq, wd, rows, K, xq, xs, row0, smem);
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+    if (tid < GEMV_R && row0 + tid < rows) {
+      logits[row0 + tid] = acc;
+      if (acc > bv) { bv = acc; bi = (uint32_t)(row0 + tid); }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const uint32_t oi = __shfl_xor(bi, o);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if (tid == 0) {
+      part_v[blockIdx.x] = bv;
+      part_i[blockIdx.x] = bi;
+      __threadfence();
+      const uint32_t ticket = atomicAdd(&st->counter, 1u);
+      s_last = ticket == gridDim.x - 1;
+    }
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  float bv = -INFINITY;
+  uint32_t bi = 0xffffffffu;
+  for (int i = tid; i < (int)gridDim.x; i += GEMV_NT) {
+    const float v = part_v[i];
+    const uint32_t ix = part_i[i];
+    if (v > bv || (v == bv && ix < bi)) { bv = v; bi = ix; }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const uint32_t oi = __shfl_xor(bi, o);
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+  }
+  if ((tid & 63) == 0) { rv[tid >> 6] = bv; ri[tid >> 6] = bi; }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < GEMV_NT / 64; ++w)
+      if (rv[w] > bv || (rv[w] == bv && ri[w] < bi)) { bv = rv[w]; bi = ri[w]; }
+    const uint32_t tok = bi == 0xffffffffu ? 0u : bi;  // all -inf: index 0, as the CPU loop
+    st->tok = tok;
+    const uint32_t s = st->step;
+    if (tokens && s < tokens_cap) tokens[s] = tok;
+    st->step = s + 1;
+    st->pos = st->pos + 1;
+    st->counter = 0;
+  }
 }
 
 // ---------------------------------------------------------------------------
 // RMSNorm (tensor/mod.rs:2083-2106) fused with Q8_0 quantization of the result.
-// One workgroup; squares in parallel, the sum of squares folded serially by thread 0.
-// Dynamic LDS = n*4 bytes (n % 32 == 0).
-__global__ __launch_bounds__(1024) void k_rmsnorm_quant(const float* __restrict__ x,
-                                                        const float* __restrict__ w, int n, float eps,
-                                                        int8_t* __restrict__ xq, float* __restrict__ xs,
-                                                        float* __restrict__ y_out) {
-  extern __shared__ float s[];
+// One workgroup of 1024 threads; thread t holds x[t + 1024 j] in registers; squares go to
+// LDS and thread 0 folds them in order; each 32-lane group then quantizes one block.
+// Dynamic LDS = n*4 bytes.  n % 32 == 0, n <= 1024 * RMS_MAXJ.
+constexpr int RMS_NT = 1024;
+constexpr int RMS_MAXJ = 16;
+
+__global__ __launch_bounds__(RMS_NT) void k_rmsnorm_quant(const float* __restrict__ x, const float* __restrict__ w,
+                                                          int n, float eps, int8_t* __restrict__ xq,
+                                                          float* __restrict__ xs, float* __restrict__ y_out) {
+  extern __shared__ __align__(16) float sq[];
   __shared__ float s_scale;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const float v = x[i];
-    s[i] = v * v;
+  const int tid = threadIdx.x;
+  float xv[RMS_MAXJ];
+#pragma unroll
+  for (int j = 0; j < RMS_MAXJ; ++j) {
+    const int i = tid + j * RMS_NT;
+    if (i < n) {
+      xv[j] = x[i];
+      sq[i] = xv[j] * xv[j];
+    }
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const float ms = serial_sum_lds(s, n) / (float)n;
+  if (tid == 0) {
+    const float ms = fold_lds(sq, n) / (float)n;
     s_scale = 1.0f / sqrtf(ms + eps);
   }
   __syncthreads();
   const float scale = s_scale;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const float yv = (x[i] * scale) * w[i];
-    s[i] = yv;
-    if (y_out) y_out[i] = yv;
+#pragma unroll
+  for (int j = 0; j < RMS_MAXJ; ++j) {
+    const int i = tid + j * RMS_NT;
+    if (i < n) {  // uniform per 32-lane group (n % 32 == 0, RMS_NT % 32 == 0)
+      const float yv = (xv[j] * scale) * w[i];
+      if (y_out) y_out[i] = yv;
+      int8_t q;
+      const float d = quantize_lane32(yv, &q);
+      xq[i] = q;
+      if ((tid & 31) == 0) xs[i >> 5] = d;
+    }
   }
-  __syncthreads();
-  quantize_blocks_from_lds(s, n, xq, xs);
 }
 
-// Plain Q8_0 quantization of an f32 vector, one thread per block.
-__global__ void k_quantize_q8_0(const float* __restrict__ x, int n, int8_t* __restrict__ xq,
-                                float* __restrict__ xs) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= (n >> 5)) return;
-  float v[32];
-  for (int i = 0; i < 32; ++i) v[i] = x[b * 32 + i];
-  int8_t q[32];
-  xs[b] = quantize_q8_0_block(v, q);
-  int4* dst = reinterpret_cast<int4*>(xq + b * 32);
-  const int4* src = reinterpret_cast<const int4*>(q);
-  dst[0] = src[0];
-  dst[1] = src[1];
+// Plain Q8_0 quantization of an f32 vector: one element per lane, one block per 32 lanes.
+__global__ __launch_bounds__(256) void k_quantize_q8_0(const float* __restrict__ x, int n, int8_t* __restrict__ xq,
+                                                       float* __restrict__ xs) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;  // uniform per 32-lane group
+  int8_t q;
+  const float d = quantize_lane32(x[i], &q);
+  xq[i] = q;
+  if ((i & 31) == 0) xs[i >> 5] = d;
 }
 
-// SwiGLU + Q8_0 quantization.  gate = gu[0..n), up = gu[n..2n); one thread per block.
-__global__ void k_silu_mul_quant(const float* __restrict__ gu, int n, int8_t* __restrict__ xq,
-                                 float* __restrict__ xs, float* __restrict__ act_out) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= (n >> 5)) return;
-  float v[32];
-  for (int i = 0; i < 32; ++i) {
-    v[i] = silu_mul1(gu[b * 32 + i], gu[n + b * 32 + i]);
-    if (act_out) act_out[b * 32 + i] = v[i];
-  }
-  int8_t q[32];
-  xs[b] = quantize_q8_0_block(v, q);
-  int4* dst = reinterpret_cast<int4*>(xq + b * 32);
-  const int4* src = reinterpret_cast<const int4*>(q);
-  dst[0] = src[0];
-  dst[1] = src[1];
+// SwiGLU (tensor/mod.rs:1943-1967) + Q8_0 quantization.  gu = [gate(n) | up(n)].
+__global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict__ gu, int n, int8_t* __restrict__ xq,
+                                                        float* __restrict__ xs, float* __restrict__ act_out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;  // uniform per 32-lane group
+  const float a = silu_mul1(gu[i], gu[n + i]);
+  if (act_out) act_out[i] = a;
+  int8_t q;
+  const float d = quantize_lane32(a, &q);
+  xq[i] = q;
+  if ((i & 31) == 0) xs[i >> 5] = d;
 }
 
 // ---------------------------------------------------------------------------
-// Per-head QK RMSNorm (optional) + RoPE + f16 KV store for the token at *d_pos.
-// One workgroup per head: blocks [0, n_heads) are Q heads, [n_heads, n_heads+n_kv) K heads
-// (which also store that head's V row).  qkv = [q | k | v] rows of the fused projection.
-// RoPE math: rope.rs:489-524; f16 store: kv_cache.rs:573-600 (layout [L][n_kv][max_pos][hd]).
-__global__ __launch_bounds__(128) void k_rope_kv(const float* __restrict__ qkv, int n_heads, int n_kv,
-                                                 int hd, int rope_dim, int split_half,
-                                                 const float* __restrict__ cosv,
-                                                 const float* __restrict__ sinv,
-                                                 const float* __restrict__ q_norm,
-                                                 const float* __restrict__ k_norm, float eps,
-                                                 float* __restrict__ qrot, uint16_t* __restrict__ kc,
-                                                 uint16_t* __restrict__ vc, int layer, int max_pos,
-                                                 const uint32_t* __restrict__ d_pos) {
-  __shared__ float buf[512];
-  __shared__ float sq[512];
+// Per-head QK RMSNorm (optional) + RoPE + f16 KV store for the token at st->pos (test
+// entry point; the engine fuses this into the attention kernel).  One workgroup per head:
+// blocks [0, n_heads) are Q heads, [n_heads, n_heads + n_kv) K heads (which also store the
+// head's V row).  RoPE: rope.rs:489-524; f16 store: kv_cache.rs:573-600.
+__global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, int n_heads, int n_kv, int hd,
+                                                int rope_dim, int split_half, const float* __restrict__ cosv,
+                                                const float* __restrict__ sinv, const float* __restrict__ q_norm,
+                                                const float* __restrict__ k_norm, float eps, float* __restrict__ qrot,
+                                                uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int layer,
+                                                int max_pos, const uint32_t* __restrict__ d_pos) {
+  __shared__ __align__(16) float buf[512];
+  __shared__ __align__(16) float sq[512];
   __shared__ float s_scale;
   const int h = blockIdx.x;
   const bool isq = h < n_heads;
@@ -223,10 +346,7 @@ __global__ __launch_bounds__(128) void k_rope_kv(const float* __restrict__ qkv, 
     __syncthreads();
     for (int d = threadIdx.x; d < hd; d += blockDim.x) sq[d] = buf[d] * buf[d];
     __syncthreads();
-    if (threadIdx.x == 0) {
-      const float ms = serial_sum_lds(sq, hd) / (float)hd;
-      s_scale = 1.0f / sqrtf(ms + eps);
-    }
+    if (threadIdx.x == 0) s_scale = 1.0f / sqrtf(fold_lds(sq, hd) / (float)hd + eps);
     __syncthreads();
     for (int d = threadIdx.x; d < hd; d += blockDim.x) buf[d] = (buf[d] * s_scale) * nw[d];
   }
@@ -255,47 +375,129 @@ __global__ __launch_bounds__(128) void k_rope_kv(const float* __restrict__ qkv, 
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention, faithful (inference.rs:23945-24025), one workgroup per query head:
-//   score_p = dot_seq(q, k_p) * scale           (one thread per position, d in order)
-//   m = max_p score_p                           (exact)
-//   e_p = expf(score_p - m); sum = fold_p e_p   (serial fold by thread 0)
-//   out_d = fold_p (e_p * (1/sum)) * v_pd       (one thread per d, p in order)
-// The head's output is then quantized to Q8_0 (hd % 32 == 0: blocks never straddle heads).
-// Dynamic LDS = (max_pos + hd) * 4 bytes.
-__global__ __launch_bounds__(256) void k_attn_decode(const float* __restrict__ qrot,
-                                                     const uint16_t* __restrict__ kc,
-                                                     const uint16_t* __restrict__ vc, int layer,
-                                                     int n_heads, int n_kv, int hd, int max_pos,
-                                                     const uint32_t* __restrict__ d_pos, float scale,
-                                                     float* __restrict__ att_out,
-                                                     int8_t* __restrict__ xq, float* __restrict__ xs) {
-  extern __shared__ float sm[];
-  __shared__ float qs[512];
-  __shared__ float red[16];
-  __shared__ float s_inv;
-  float* out = sm;        // [hd]
-  float* sc = sm + hd;    // [P]
+// Decode attention, faithful (inference.rs:23945-24025), one workgroup per query head.
+//   score_p = dot_seq(q, k_p) * scale         one lane per position, d in order
+//   m = max_p score_p                          exact
+//   e_p = expf(score_p - m); sum = fold_p e_p  serial fold by one lane
+//   out_d = fold_p (e_p * (1/sum)) * v_pd      one lane per d, p in order
+// FUSED (the engine's path): the kernel first builds this token's q (and the kv head's k
+// and v) from the fused QKV projection: optional per-head QK RMSNorm (tensor/mod.rs:2112),
+// RoPE (rope.rs:489-524) with the tables at cos_base + pos*rope_stride, f16 rounding of k
+// and v (kv_cache.rs:573-600).  The first q head of each GQA group stores the new K/V row;
+// every head of the group uses its own LDS copy of that row for position pos.
+// Not FUSED (test entry point): q is taken from qsrc and K/V entirely from the cache.
+// The head's output is quantized to Q8_0 (hd % 32 == 0: blocks never straddle heads).
+// Dynamic LDS = align16(max_pos) * 4 bytes.
+constexpr int ATT_NT = 256;
+
+template <bool FUSED>
+__global__ __launch_bounds__(ATT_NT) void k_attention(
+    const float* __restrict__ qsrc, int n_heads, int n_kv, int hd, int rope_dim, int split_half,
+    const float* __restrict__ cos_base, const float* __restrict__ sin_base, int rope_stride,
+    const float* __restrict__ q_norm, const float* __restrict__ k_norm, float eps, uint16_t* __restrict__ kc,
+    uint16_t* __restrict__ vc, int layer, int max_pos, const uint32_t* __restrict__ d_pos, float scale,
+    float* __restrict__ att_out, int8_t* __restrict__ xq, float* __restrict__ xs) {
+  extern __shared__ __align__(16) float sc[];
+  __shared__ __align__(16) float qs[512];
+  __shared__ __align__(16) float kn[512];  // this position's k (f16-rounded), then scratch
+  __shared__ __align__(16) float vn[512];  // this position's v (f16-rounded)
+  __shared__ __align__(16) float out[512];
+  __shared__ __align__(16) float sq[1024];
+  __shared__ float red[ATT_NT / 64];
+  __shared__ float s_qscale, s_kscale, s_inv;
+  const int tid = threadIdx.x;
   const int h = blockIdx.x;
-  const int kvh = h / (n_heads / n_kv);
-  const int P = (int)*d_pos + 1;
+  const int rep = n_heads / n_kv;
+  const int kvh = h / rep;
+  const int pos = (int)*d_pos;
+  const int P = pos + 1;
   const size_t base = (((size_t)layer * n_kv + kvh) * max_pos) * hd;
-  for (int d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = qrot[(size_t)h * hd + d];
+
+  if (FUSED) {
+    const float* q = qsrc + (size_t)h * hd;
+    const float* k = qsrc + (size_t)n_heads * hd + (size_t)kvh * hd;
+    const float* v = qsrc + (size_t)(n_heads + n_kv) * hd + (size_t)kvh * hd;
+    for (int d = tid; d < hd; d += ATT_NT) {
+      qs[d] = q[d];
+      kn[d] = k[d];
+      vn[d] = half_bits_to_float(f32_to_f16_bits(v[d]));
+    }
+    if (q_norm) {  // per-head RMSNorm of q and k (two serial folds by two lanes)
+      __syncthreads();
+      for (int d = tid; d < hd; d += ATT_NT) {
+        sq[d] = qs[d] * qs[d];
+        sq[512 + d] = kn[d] * kn[d];
+      }
+      __syncthreads();
+      if (tid == 0) s_qscale = 1.0f / sqrtf(fold_lds(sq, hd) / (float)hd + eps);
+      if (tid == 64) s_kscale = 1.0f / sqrtf(fold_lds(sq + 512, hd) / (float)hd + eps);
+      __syncthreads();
+      for (int d = tid; d < hd; d += ATT_NT) {
+        qs[d] = (qs[d] * s_qscale) * q_norm[d];
+        kn[d] = (kn[d] * s_kscale) * k_norm[d];
+      }
+    }
+    __syncthreads();
+    const float* cosv = cos_base + (size_t)pos * rope_stride;
+    const float* sinv = sin_base + (size_t)pos * rope_stride;
+    const int half = rope_dim >> 1;
+    for (int p = tid; p < half; p += ATT_NT) {
+      const int d0 = split_half ? p : 2 * p;
+      const int d1 = split_half ? p + half : 2 * p + 1;
+      const float c = cosv[p], s = sinv[p];
+      float x0 = qs[d0], x1 = qs[d1];
+      qs[d0] = (x0 * c) - (x1 * s);
+      qs[d1] = (x0 * s) + (x1 * c);
+      x0 = kn[d0];
+      x1 = kn[d1];
+      kn[d0] = (x0 * c) - (x1 * s);
+      kn[d1] = (x0 * s) + (x1 * c);
+    }
+    __syncthreads();
+    const bool store = (h % rep) == 0;
+    for (int d = tid; d < hd; d += ATT_NT) {
+      const uint16_t kb = f32_to_f16_bits(kn[d]);
+      kn[d] = half_bits_to_float(kb);
+      if (store) {
+        kc[base + (size_t)pos * hd + d] = kb;
+        vc[base + (size_t)pos * hd + d] = f32_to_f16_bits(vn[d]);
+      }
+    }
+  } else {
+    for (int d = tid; d < hd; d += ATT_NT) {
+      qs[d] = qsrc[(size_t)h * hd + d];
+      kn[d] = half_bits_to_float(kc[base + (size_t)pos * hd + d]);
+      vn[d] = half_bits_to_float(vc[base + (size_t)pos * hd + d]);
+    }
+  }
   __syncthreads();
+
   if (P == 1) {
     // inference.rs:23564-23575: a single position copies the V row.
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) out[d] = half_bits_to_float(vc[base + d]);
+    for (int d = tid; d < hd; d += ATT_NT) out[d] = vn[d];
   } else {
+    // scores
     float lmax = -INFINITY;
-    for (int p = threadIdx.x; p < P; p += blockDim.x) {
-      const uint16_t* kr = kc + base + (size_t)p * hd;
+    for (int p = tid; p < P; p += ATT_NT) {
       float acc = 0.0f;
-      for (int d = 0; d < hd; d += 8) {
-        const uint4 raw = *reinterpret_cast<const uint4*>(kr + d);
-        const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+      if (p == pos) {
+        for (int d = 0; d < hd; ++d) acc += qs[d] * kn[d];
+      } else {
+        const uint4* kr = reinterpret_cast<const uint4*>(kc + base + (size_t)p * hd);
+        for (int d8 = 0; d8 < (hd >> 3); d8 += 4) {
+          uint4 raw[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc += qs[d + 2 * j] * half_bits_to_float((uint16_t)(wv[j] & 0xffffu));
-          acc += qs[d + 2 * j + 1] * half_bits_to_float((uint16_t)(wv[j] >> 16));
+          for (int u = 0; u < 4; ++u) raw[u] = kr[d8 + u];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const uint32_t wv[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+            const int d = (d8 + u) * 8;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              acc += qs[d + 2 * j] * half_bits_to_float((uint16_t)(wv[j] & 0xffffu));
+              acc += qs[d + 2 * j + 1] * half_bits_to_float((uint16_t)(wv[j] >> 16));
+            }
+          }
         }
       }
       const float s = acc * scale;
@@ -303,29 +505,48 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float* __restrict__ q
       lmax = fmaxf(lmax, s);
     }
     const float mx = block_max(lmax, red);
-    for (int p = threadIdx.x; p < P; p += blockDim.x) sc[p] = glibc_expf(sc[p] - mx);
+    for (int p = tid; p < P; p += ATT_NT) sc[p] = glibc_expf(sc[p] - mx);
     __syncthreads();
-    if (threadIdx.x == 0) s_inv = 1.0f / serial_sum_lds(sc, P);
+    if (tid == 0) s_inv = 1.0f / fold_lds(sc, P);
     __syncthreads();
     const float inv = s_inv;
-    for (int p = threadIdx.x; p < P; p += blockDim.x) sc[p] = sc[p] * inv;
+    for (int p = tid; p < P; p += ATT_NT) sc[p] = sc[p] * inv;
     __syncthreads();
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-      const uint16_t* vcol = vc + base + d;
+    if (tid < hd) {
+      // out_d = fold over p of prob_p * v_pd; V loads run one group of 8 positions ahead.
+      const uint16_t* vcol = vc + base + tid;
       float acc = 0.0f;
-      for (int p = 0; p < P; ++p) acc += sc[p] * half_bits_to_float(vcol[(size_t)p * hd]);
-      out[d] = acc;
+      const int npre = pos;  // positions read from the cache
+      uint16_t cur[8], nxt[8];
+      int p = 0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) cur[u] = (u < npre) ? vcol[(size_t)u * hd] : 0;
+      for (; p + 8 <= npre; p += 8) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) nxt[u] = (p + 8 + u < npre) ? vcol[(size_t)(p + 8 + u) * hd] : 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += sc[p + u] * half_bits_to_float(cur[u]);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
+      }
+      for (int u = 0; p < npre; ++p, ++u) acc += sc[p] * half_bits_to_float(cur[u]);
+      acc += sc[pos] * vn[tid];
+      out[tid] = acc;
     }
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < hd; d += blockDim.x) att_out[(size_t)h * hd + d] = out[d];
-  quantize_blocks_from_lds(out, hd, xq + (size_t)h * hd, xs + (size_t)h * (hd >> 5));
+  for (int d = tid; d < hd; d += ATT_NT) {
+    att_out[(size_t)h * hd + d] = out[d];
+    int8_t q;
+    const float dd = quantize_lane32(out[d], &q);
+    xq[(size_t)h * hd + d] = q;
+    if ((d & 31) == 0) xs[((size_t)h * hd + d) >> 5] = dd;
+  }
 }
 
 // ---------------------------------------------------------------------------
-// Greedy argmax (inference.rs:5912-5925): first index of the maximum, strict '>'.
-__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int n,
-                                                 uint32_t* __restrict__ out) {
+// Greedy argmax (inference.rs:5912-5925) over a vector: one workgroup (test entry point).
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int n, uint32_t* __restrict__ out) {
   __shared__ float bv_s[16];
   __shared__ uint32_t bi_s[16];
   float bv = -INFINITY;
@@ -334,6 +555,7 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, in
     const float v = x[i];
     if (v > bv) { bv = v; bi = (uint32_t)i; }
   }
+#pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(bv, o);
     const uint32_t oi = __shfl_xor(bi, o);
@@ -343,19 +565,19 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, in
   if (lane == 0) { bv_s[wave] = bv; bi_s[wave] = bi; }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) {
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
       if (bv_s[w] > bv || (bv_s[w] == bv && bi_s[w] < bi)) { bv = bv_s[w]; bi = bi_s[w]; }
-    }
     *out = bi == 0xffffffffu ? 0u : bi;
   }
 }
 
-// On-device Q8R embedding row gather: h[i] = scale_b * q_i (exact; tensor/mod.rs:2329-2398).
-__global__ void k_embed_q8(const int8_t* __restrict__ eq, const uint16_t* __restrict__ ed, int H,
-                           const uint32_t* __restrict__ tok, float* __restrict__ h) {
+// On-device Q8R embedding row gather of st->tok: h[i] = scale_b * q_i (exact;
+// tensor/mod.rs:2329-2398).
+__global__ __launch_bounds__(256) void k_embed_q8(const int8_t* __restrict__ eq, const uint16_t* __restrict__ ed,
+                                                  int H, const StepState* __restrict__ st, float* __restrict__ h) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= H) return;
-  const size_t t = *tok;
+  const size_t t = st->tok;
   h[i] = half_bits_to_float(ed[t * (H >> 5) + (i >> 5)]) * (float)eq[t * H + i];
 }
 

@@ -170,7 +170,7 @@ class HipResidentDecode:
         return out
 
     # -- measurement ------------------------------------------------------------------------
-    PROFILE_CATEGORIES = ("gemv", "rmsnorm_quant", "rope_kv", "attention", "silu_quant", "argmax", "embed")
+    PROFILE_CATEGORIES = ("gemv", "rmsnorm_quant", "attention", "silu_quant", "head", "embed")
 
     def profile_begin(self) -> None:
         self._chk(self._lib.camelid_hip_profile_begin(self._h))

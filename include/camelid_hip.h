@@ -115,9 +115,11 @@ int camelid_hip_generate(camelid_hip_engine* e, uint32_t token, uint32_t positio
 int camelid_hip_capture_hidden(camelid_hip_engine* e, int enable);
 int camelid_hip_read_hidden(camelid_hip_engine* e, float* out);
 /* Per-launch HIP-event timing on the engine's stream (measurement hook).  Between begin and
- * end every kernel launch is bracketed by events; end synchronises and returns, per category
- * (0 GEMV, 1 RMSNorm+quantize, 2 RoPE+KV store, 3 attention, 4 SwiGLU+quantize, 5 argmax,
- * 6 embedding gather), the summed kernel milliseconds, algorithmic bytes and launch count. */
+ * end every kernel launch is bracketed by events (the device-side loop then runs without
+ * its graph); end synchronises and returns, per category (0 Q8_0 GEMV incl. the lm_head +
+ * argmax launch, 1 RMSNorm+quantize, 2 attention incl. QK-norm/RoPE/KV store, 3 SwiGLU +
+ * quantize, 4 unused, 5 embedding gather), the summed kernel milliseconds, algorithmic bytes
+ * and launch count. */
 int camelid_hip_profile_begin(camelid_hip_engine* e);
 int camelid_hip_profile_end(camelid_hip_engine* e, double* ms, double* bytes, uint64_t* launches,
                             uint32_t n_cat);
