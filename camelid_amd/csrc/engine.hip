@@ -6,7 +6,8 @@
 //   per layer: Wqkv (Q8R, rows nq+2*nkv), Wo (Q8R), Wgate|up (Q8R, rows 2F), Wdown (Q8R),
 //              attn/ffn norm [H], optional q/k norm [hd]
 //   lm_head Q8R [V][H], final norm [H], optional token_embd Q8R [V][H]
-//   KV cache f16 [L][n_kv][max_pos][hd] (K and V separately)
+//   KV cache f16: K [L][n_kv][kvs][hd], V transposed [L][n_kv][hd][kvs], kvs = max_pos
+//   rounded up to a multiple of 8 (16-byte aligned V rows)
 //   activations: h [H] (residual stream), qkv, att [nq], gu [2F], logits [V], one Q8_0
 //                activation buffer (quants + f32 scales) reused by every GEMV
 //   StepState {pos, tok, step, counter}: the decode loop's device-side state
@@ -64,8 +65,9 @@ struct camelid_hip_engine {
   bool out_set = false;
   Q8Mat embd;
   bool embd_set = false;
-  uint16_t* kc = nullptr;
-  uint16_t* vc = nullptr;
+  uint16_t* kc = nullptr;  // K [L][n_kv][kvs][hd]
+  uint16_t* vc = nullptr;  // V [L][n_kv][hd][kvs] (transposed)
+  uint32_t kvs = 0;        // KV position stride: max_pos rounded up to a multiple of 8
   float *h = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr;
   float *logits = nullptr, *hidden_cap = nullptr, *xs = nullptr;
   float *cos_cur = nullptr, *sin_cur = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
@@ -258,8 +260,52 @@ double q8_bytes(const Q8Mat& m, bool resid) {
 // ---------------------------------------------------------------- launches
 void launch_gemv(const Q8Mat& m, const int8_t* xq, const float* xs, float* y, const float* resid, hipStream_t s) {
   const uint32_t grid = (m.rows + cm::GEMV_R - 1) / cm::GEMV_R;
-  hipLaunchKernelGGL(cm::k_gemv, dim3(grid), dim3(cm::GEMV_NT), cm::gemv_lds_bytes((int)m.k), s, m.q, m.d,
-                     (int)m.rows, (int)m.k, xq, xs, y, resid);
+  switch (m.k) {
+#define CM_GEMV_CASE(K)                                                                                      \
+  case K:                                                                                                    \
+    hipLaunchKernelGGL(cm::k_gemv_k<K>, dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, xq, xs, y, \
+                       resid);                                                                               \
+    return;
+    CM_GEMV_KS(CM_GEMV_CASE)
+#undef CM_GEMV_CASE
+    default:
+      hipLaunchKernelGGL(cm::k_gemv, dim3(grid), dim3(cm::GEMV_NT), cm::gemv_lds_bytes((int)m.k), s, m.q, m.d,
+                         (int)m.rows, (int)m.k, xq, xs, y, resid);
+  }
+}
+
+void launch_gemv_argmax(const Q8Mat& m, const int8_t* xq, const float* xs, float* logits, float* part_v,
+                        uint32_t* part_i, cm::StepState* st, uint32_t* tokens, uint32_t cap, hipStream_t s) {
+  const uint32_t grid = (m.rows + cm::GEMV_R - 1) / cm::GEMV_R;
+  switch (m.k) {
+#define CM_GEMV_CASE(K)                                                                                      \
+  case K:                                                                                                    \
+    hipLaunchKernelGGL(cm::k_gemv_argmax<K>, dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, K, xq, \
+                       xs, logits, part_v, part_i, st, tokens, cap);                                         \
+    return;
+    CM_GEMV_KS(CM_GEMV_CASE)
+#undef CM_GEMV_CASE
+    default:
+      hipLaunchKernelGGL(cm::k_gemv_argmax<0>, dim3(grid), dim3(cm::GEMV_NT), cm::gemv_lds_bytes((int)m.k), s, m.q,
+                         m.d, (int)m.rows, (int)m.k, xq, xs, logits, part_v, part_i, st, tokens, cap);
+  }
+}
+
+// Attention launch for the supported head widths.
+bool attention_hd_supported(uint32_t hd) { return hd == 64 || hd == 128 || hd == 256; }
+
+template <bool FUSED>
+void launch_attention(uint32_t hd, uint32_t n_heads, size_t lds, hipStream_t s, const float* qsrc, int nh, int nkv,
+                      int rope_dim, int split_half, const float* cb, const float* sb, int rs, const float* qn,
+                      const float* kn, float eps, uint16_t* kc, uint16_t* vc, int layer, int kvs, const uint32_t* pos,
+                      float scale, float* att, int8_t* xq, float* xs) {
+#define CM_ATT(HD)                                                                                                 \
+  hipLaunchKernelGGL((cm::k_attention<HD, FUSED>), dim3(n_heads), dim3(cm::ATT_NT), lds, s, qsrc, nh, nkv, rope_dim, \
+                     split_half, cb, sb, rs, qn, kn, eps, kc, vc, layer, kvs, pos, scale, att, xq, xs)
+  if (hd == 64) CM_ATT(64);
+  else if (hd == 128) CM_ATT(128);
+  else CM_ATT(256);
+#undef CM_ATT
 }
 
 void launch_rmsnorm_quant(const float* x, const float* w, uint32_t n, float eps, int8_t* xq, float* xs, float* y,
@@ -291,10 +337,10 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const f
   gemv(e, L.qkv, e->qkv, nullptr);
   {
     ProfScope ps(e, P_ATTN, (nq + 2 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0));
-    hipLaunchKernelGGL(cm::k_attention<true>, dim3(d.n_heads), dim3(cm::ATT_NT), attn_lds_bytes(d.max_pos), s,
-                       e->qkv, (int)d.n_heads, (int)d.n_kv_heads, (int)d.head_dim, (int)d.rope_dim,
-                       (int)d.split_half_pairing, cos_base, sin_base, rope_stride, L.q_norm, L.k_norm, d.eps, e->kc,
-                       e->vc, (int)l, (int)d.max_pos, &e->st->pos, scale, e->att, e->xq, e->xs);
+    launch_attention<true>(d.head_dim, d.n_heads, attn_lds_bytes(d.max_pos), s, e->qkv, (int)d.n_heads,
+                           (int)d.n_kv_heads, (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base,
+                           rope_stride, L.q_norm, L.k_norm, d.eps, e->kc, e->vc, (int)l, (int)e->kvs, &e->st->pos,
+                           scale, e->att, e->xq, e->xs);
   }
   gemv(e, L.o, e->h, e->h);
   rmsnorm(e, L.ffn_norm);
@@ -325,9 +371,7 @@ void run_head(camelid_hip_engine* e, uint32_t* tokens, uint32_t cap) {
   rmsnorm(e, e->out_norm);
   const Q8Mat& m = e->out;
   ProfScope ps(e, P_GEMV, q8_bytes(m, false));
-  const uint32_t grid = (m.rows + cm::GEMV_R - 1) / cm::GEMV_R;
-  hipLaunchKernelGGL(cm::k_gemv_argmax, dim3(grid), dim3(cm::GEMV_NT), cm::gemv_lds_bytes((int)m.k), e->stream, m.q,
-                     m.d, (int)m.rows, (int)m.k, e->xq, e->xs, e->logits, e->part_v, e->part_i, e->st, tokens, cap);
+  launch_gemv_argmax(m, e->xq, e->xs, e->logits, e->part_v, e->part_i, e->st, tokens, cap, e->stream);
 }
 
 void run_embed(camelid_hip_engine* e) {
@@ -399,7 +443,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   if (d.n_heads % d.n_kv_heads) return fail(nullptr, "n_heads must be a multiple of n_kv_heads");
   if (d.hidden % 32 || d.ffn_dim % 32 || d.head_dim % 32)
     return fail(nullptr, "hidden, ffn_dim and head_dim must be multiples of 32");
-  if (d.head_dim > 512) return fail(nullptr, "head_dim > 512 is not supported");
+  if (!attention_hd_supported(d.head_dim)) return fail(nullptr, "head_dim must be 64, 128 or 256");
   if (d.hidden > 8192) return fail(nullptr, "hidden > 8192 is not supported by the RMSNorm kernel");
   if (d.rope_dim == 0 || d.rope_dim > d.head_dim || d.rope_dim % 2)
     return fail(nullptr, "rope_dim must be even and within head_dim");
@@ -423,8 +467,9 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
     return 1;
   }
   e->layers.resize(d.n_layers);
+  e->kvs = (d.max_pos + 7u) & ~7u;
   const size_t nq = (size_t)d.n_heads * d.head_dim, nkv = (size_t)d.n_kv_heads * d.head_dim;
-  const size_t kv_elems = (size_t)d.n_layers * d.n_kv_heads * d.max_pos * d.head_dim;
+  const size_t kv_elems = (size_t)d.n_layers * d.n_kv_heads * e->kvs * d.head_dim;
   const size_t act = std::max<size_t>({(size_t)d.hidden, (size_t)d.ffn_dim, nq});
   const uint32_t half = d.rope_dim / 2;
   const size_t nparts = (d.vocab + cm::GEMV_R - 1) / cm::GEMV_R;
@@ -551,16 +596,19 @@ int camelid_hip_seed_layer(camelid_hip_engine* e, uint32_t layer, const float* c
   HIP_TRY(e, hipSetDevice(e->device));
   HIP_TRY(e, hipStreamSynchronize(e->stream));
   const camelid_hip_dims& d = e->d;
-  std::vector<uint16_t> hk((size_t)n_pos * d.head_dim), hv(hk.size());
+  const size_t hd = d.head_dim, kvs = e->kvs;
+  std::vector<uint16_t> hk((size_t)n_pos * hd), hv(hd * kvs);
   for (uint32_t h = 0; h < d.n_kv_heads; ++h) {
-    const size_t src = (size_t)h * n_pos * d.head_dim;
-    for (size_t i = 0; i < hk.size(); ++i) {
-      hk[i] = cm::f32_to_f16_bits(ck[src + i]);
-      hv[i] = cm::f32_to_f16_bits(cv[src + i]);
-    }
-    const size_t dst = (((size_t)layer * d.n_kv_heads + h) * d.max_pos) * d.head_dim;
-    HIP_TRY(e, hipMemcpy(e->kc + dst, hk.data(), hk.size() * 2, hipMemcpyHostToDevice));
-    HIP_TRY(e, hipMemcpy(e->vc + dst, hv.data(), hv.size() * 2, hipMemcpyHostToDevice));
+    const size_t src = (size_t)h * n_pos * hd;
+    const size_t base = ((size_t)layer * d.n_kv_heads + h) * kvs * hd;
+    HIP_TRY(e, hipMemcpy(hv.data(), e->vc + base, hv.size() * 2, hipMemcpyDeviceToHost));
+    for (size_t t = 0; t < n_pos; ++t)
+      for (size_t j = 0; j < hd; ++j) {
+        hk[t * hd + j] = cm::f32_to_f16_bits(ck[src + t * hd + j]);
+        hv[j * kvs + t] = cm::f32_to_f16_bits(cv[src + t * hd + j]);
+      }
+    HIP_TRY(e, hipMemcpy(e->kc + base, hk.data(), hk.size() * 2, hipMemcpyHostToDevice));
+    HIP_TRY(e, hipMemcpy(e->vc + base, hv.data(), hv.size() * 2, hipMemcpyHostToDevice));
   }
   return 0;
 }
@@ -572,16 +620,18 @@ int camelid_hip_read_kv_layer(camelid_hip_engine* e, uint32_t layer, uint32_t n,
   HIP_TRY(e, hipSetDevice(e->device));
   HIP_TRY(e, hipStreamSynchronize(e->stream));
   const camelid_hip_dims& d = e->d;
-  std::vector<uint16_t> hk((size_t)n * d.head_dim), hv(hk.size());
+  const size_t hd = d.head_dim, kvs = e->kvs;
+  std::vector<uint16_t> hk((size_t)n * hd), hv(hd * kvs);
   for (uint32_t h = 0; h < d.n_kv_heads; ++h) {
-    const size_t src = (((size_t)layer * d.n_kv_heads + h) * d.max_pos) * d.head_dim;
-    HIP_TRY(e, hipMemcpy(hk.data(), e->kc + src, hk.size() * 2, hipMemcpyDeviceToHost));
-    HIP_TRY(e, hipMemcpy(hv.data(), e->vc + src, hv.size() * 2, hipMemcpyDeviceToHost));
-    const size_t dst = (size_t)h * n * d.head_dim;
-    for (size_t i = 0; i < hk.size(); ++i) {
-      ck[dst + i] = cm::f16_bits_to_f32(hk[i]);
-      cv[dst + i] = cm::f16_bits_to_f32(hv[i]);
-    }
+    const size_t base = ((size_t)layer * d.n_kv_heads + h) * kvs * hd;
+    HIP_TRY(e, hipMemcpy(hk.data(), e->kc + base, hk.size() * 2, hipMemcpyDeviceToHost));
+    HIP_TRY(e, hipMemcpy(hv.data(), e->vc + base, hv.size() * 2, hipMemcpyDeviceToHost));
+    const size_t dst = (size_t)h * n * hd;
+    for (size_t t = 0; t < n; ++t)
+      for (size_t j = 0; j < hd; ++j) {
+        ck[dst + t * hd + j] = cm::f16_bits_to_f32(hk[t * hd + j]);
+        cv[dst + t * hd + j] = cm::f16_bits_to_f32(hv[j * kvs + t]);
+      }
   }
   return 0;
 }
@@ -887,14 +937,12 @@ int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const ui
                                  uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t max_pos, const uint32_t* d_pos,
                                  float scale, float* att_out, int8_t* xq, float* xs, void* stream) {
   if (!qrot || !kc || !vc || !d_pos || !att_out || !xq || !xs) return fail(nullptr, "null argument");
-  if (!n_heads || !n_kv || n_heads % n_kv || hd % 32 || hd == 0 || hd > 512)
-    return fail(nullptr, "invalid head geometry");
+  if (!n_heads || !n_kv || n_heads % n_kv || !attention_hd_supported(hd)) return fail(nullptr, "invalid head geometry");
+  if (max_pos % 8) return fail(nullptr, "the KV position stride (max_pos) must be a multiple of 8");
   if (attn_lds_bytes(max_pos) > 96 * 1024) return fail(nullptr, "max_pos too large for the decode attention");
-  hipLaunchKernelGGL(cm::k_attention<false>, dim3(n_heads), dim3(cm::ATT_NT), attn_lds_bytes(max_pos),
-                     (hipStream_t)stream, qrot, (int)n_heads, (int)n_kv, (int)hd, (int)hd, 0, (const float*)nullptr,
-                     (const float*)nullptr, 0, (const float*)nullptr, (const float*)nullptr, 0.0f,
-                     const_cast<uint16_t*>(kc), const_cast<uint16_t*>(vc), (int)layer, (int)max_pos, d_pos, scale,
-                     att_out, xq, xs);
+  launch_attention<false>(hd, n_heads, attn_lds_bytes(max_pos), (hipStream_t)stream, qrot, (int)n_heads, (int)n_kv,
+                          (int)hd, 0, nullptr, nullptr, 0, nullptr, nullptr, 0.0f, const_cast<uint16_t*>(kc),
+                          const_cast<uint16_t*>(vc), (int)layer, (int)max_pos, d_pos, scale, att_out, xq, xs);
   return launch_status("attention_decode");
 }
 

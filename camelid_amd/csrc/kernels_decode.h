@@ -32,33 +32,85 @@ __device__ __forceinline__ int dot4x4(int4 w, int4 x, int acc) {
 }
 
 // ---------------------------------------------------------------------------
-// Serial f32 fold of n LDS floats in index order (one lane), the CPU's summation order.
-// LDS reads run W float4 groups ahead of the dependent add chain so the chain issues
-// back to back.  p must be 16-byte aligned.
-template <int W = 8>
+// Serial f32 folds in index order (one lane): the CPU's summation order.  LDS reads run
+// 8 float4 groups (32 floats) ahead of the dependent add chain, with clamped (always in
+// bounds) addresses so the main loop is straight-line code.  p must be 16-byte aligned.
+__device__ __forceinline__ void add4(float& acc, const float4 v) {
+  acc += v.x;
+  acc += v.y;
+  acc += v.z;
+  acc += v.w;
+}
+
+__device__ __forceinline__ void load8(float4 (&r)[8], const float4* q) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = q[i];
+}
+__device__ __forceinline__ void add8(float& acc, const float4 (&r)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) add4(acc, r[i]);
+}
+
 __device__ __forceinline__ float fold_lds(const float* p, int n, float acc = 0.0f) {
   const float4* q = reinterpret_cast<const float4*>(p);
   const int g = n >> 2;
-  float4 buf[W];
-#pragma unroll
-  for (int i = 0; i < W; ++i)
-    if (i < g) buf[i] = q[i];
-  for (int base = 0; base < g; base += W) {
-#pragma unroll
-    for (int i = 0; i < W; ++i) {
-      if (base + i < g) {
-        const float4 v = buf[i];
-        if (base + i + W < g) buf[i] = q[base + i + W];
-        acc += v.x;
-        acc += v.y;
-        acc += v.z;
-        acc += v.w;
-      }
+  int base = 0;
+  if (g >= 8) {
+    // ping-pong between two register sets: the next 8 groups are always in flight
+    float4 a[8], b[8];
+    load8(a, q);
+    base = 8;
+    for (; base + 16 <= g; base += 16) {
+      load8(b, q + base);
+      __builtin_amdgcn_sched_barrier(0);
+      add8(acc, a);
+      load8(a, q + base + 8);
+      __builtin_amdgcn_sched_barrier(0);
+      add8(acc, b);
+    }
+    if (base + 8 <= g) {
+      load8(b, q + base);
+      __builtin_amdgcn_sched_barrier(0);
+      add8(acc, a);
+      add8(acc, b);
+      base += 8;
+    } else {
+      add8(acc, a);
     }
   }
+  for (; base < g; ++base) add4(acc, q[base]);
   for (int i = g << 2; i < n; ++i) acc += p[i];
   return acc;
 }
+
+// Compile-time length variant (N % 4 == 0): fully unrolled, same order.
+template <int N>
+__device__ __forceinline__ float fold_lds_n(const float* p, float acc = 0.0f) {
+  static_assert(N % 4 == 0, "fold length must be a multiple of 4");
+  constexpr int G = N / 4;
+  const float4* q = reinterpret_cast<const float4*>(p);
+  float4 a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < G) a[i] = q[i];
+#pragma unroll
+  for (int base = 0; base < G; base += 8) {
+    float4 b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (base + 8 + i < G) b[i] = q[base + 8 + i];
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the add chain
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (base + i < G) add4(acc, a[i]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = b[i];
+  }
+  return acc;
+}
+
+// Lane-pair exchange (xor 1) through DPP quad_perm [1,0,3,2]; all lanes must be active.
+__device__ __forceinline__ int dpp_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
 
 // Q8_0 quantization of one 32-value block held one value per lane by a 32-lane group
 // (lanes 0-31 or 32-63 of a wave).  Returns the block's f16-valued scale (same in every
@@ -106,35 +158,84 @@ __global__ __launch_bounds__(64) void k_q8_block_dots(const int8_t* __restrict__
 // ---------------------------------------------------------------------------
 // Q8_0 GEMV, faithful:  y[row] = (resid ? resid[row] : 0) + fold_b term(row, b),
 //   term = (float(int_dot(w_b, x_b)) * w_scale_b) * x_scale_b  (inference.rs:19871-19905).
-// A workgroup of 256 threads owns GEMV_R consecutive rows = one contiguous slab of
-// GEMV_R*K quant bytes.  The slab's 16-byte chunks are dealt round-robin (thread t takes
-// chunks t, t+256, ...), so each workgroup-wide load is 4 KB contiguous.  Lane pairs
-// (2j, 2j+1) always hold the two halves of one 32-value block (chunks per row is even),
-// combined with one integer shuffle.  Even lanes turn the block dot into its f32 term in
-// LDS; then lane r of wave 0 folds row r's terms in block order.
-// Dynamic LDS: K bytes (x quants) + nb*4 (x scales) + GEMV_R*(nb+4)*4 (terms).
+// A workgroup of 4 waves owns GEMV_R = 8 consecutive rows; wave w owns rows 2w and 2w+1.
+// Lane l streams 16-byte chunks l, l+64, ... of each of its wave's rows (a wave load is
+// 1 KB contiguous), so lane pairs (2j, 2j+1) hold the two halves of one 32-value block,
+// combined by a DPP exchange (integer, exact).  Every weight and scale load of a wave is
+// issued before the first dot.  Even lanes write the block's f32 term to LDS; then lane r
+// of wave 0 folds row r's terms in block order.
 constexpr int GEMV_R = 8;
 constexpr int GEMV_NT = 256;
+constexpr int GEMV_RPW = 2;  // rows per wave
 
-__host__ __device__ inline int gemv_term_stride(int nb) { return ((nb + 3) & ~3) + 4; }
+__host__ __device__ constexpr int gemv_term_stride(int nb) { return ((nb + 3) & ~3) + 4; }
+
+// Shared body for a compile-time row width K; returns (in lanes 0..7 of wave 0) the
+// folded sum of row row0 + lane.
+template <int K>
+__device__ __forceinline__ float gemv_rows_k(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, int rows,
+                                             const int8_t* __restrict__ xq, const float* __restrict__ xs, int row0) {
+  constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64, STRIDE = gemv_term_stride(NB);
+  static_assert(NB % 4 == 0, "compile-time GEMV widths are multiples of 128");
+  __shared__ __align__(16) int8_t xl[K];
+  __shared__ __align__(16) float xsl[NB];
+  __shared__ __align__(16) float t[GEMV_R * STRIDE];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // issue this wave's weight and scale loads first (rows clamped: results of rows past the
+  // end are computed but never stored)
+  int4 wv[GEMV_RPW][IT];
+  uint16_t dv[GEMV_RPW][IT];
+#pragma unroll
+  for (int k = 0; k < GEMV_RPW; ++k) {
+    const int row = min(row0 + wave * GEMV_RPW + k, rows - 1);
+    const int4* w4 = reinterpret_cast<const int4*>(wq + (size_t)row * K);
+    const uint16_t* d = wd + (size_t)row * NB;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int c = min(lane + 64 * i, CPR - 1);
+      wv[k][i] = w4[c];
+      dv[k][i] = d[c >> 1];
+    }
+  }
+  // stage the activation (K quants + NB scales) in LDS
+  for (int c = tid; c < CPR; c += GEMV_NT) reinterpret_cast<int4*>(xl)[c] = reinterpret_cast<const int4*>(xq)[c];
+  for (int b = tid; b < NB; b += GEMV_NT) xsl[b] = xs[b];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < GEMV_RPW; ++k) {
+    float* tr = t + (wave * GEMV_RPW + k) * STRIDE;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int c = lane + 64 * i;
+      const int cc = min(c, CPR - 1);
+      int s = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
+      s += dpp_xor1(s);
+      if ((lane & 1) == 0 && c < CPR) tr[c >> 1] = ((float)s * half_bits_to_float(dv[k][i])) * xsl[c >> 1];
+    }
+  }
+  __syncthreads();
+  float acc = 0.0f;
+  if (tid < GEMV_R) acc = fold_lds_n<NB>(t + tid * STRIDE);
+  return acc;
+}
+
+// Runtime-K fallback (any K % 32 == 0 whose LDS stage fits): same arithmetic, chunks dealt
+// round-robin over the workgroup.
 __host__ __device__ inline size_t gemv_term_offset(int K) { return ((size_t)K + (size_t)(K >> 5) * 4 + 15) & ~(size_t)15; }
 __host__ __device__ inline size_t gemv_lds_bytes(int K) {
   return gemv_term_offset(K) + (size_t)GEMV_R * gemv_term_stride(K >> 5) * 4;
 }
 
-// Shared body; returns (in lanes 0..GEMV_R-1 of wave 0) the folded sum of row row0+lane.
-__device__ __forceinline__ float gemv_rows(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, int rows,
-                                           int K, const int8_t* __restrict__ xq, const float* __restrict__ xs,
-                                           int row0, unsigned char* smem) {
+__device__ __forceinline__ float gemv_rows_rt(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, int rows,
+                                              int K, const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                              int row0, unsigned char* smem) {
   const int nb = K >> 5;
-  const int cpr = K >> 4;  // 16-byte chunks per row
+  const int cpr = K >> 4;
   int8_t* xl = reinterpret_cast<int8_t*>(smem);
   float* xsl = reinterpret_cast<float*>(smem + K);
-  float* t = reinterpret_cast<float*>(smem + gemv_term_offset(K));  // [GEMV_R][stride], 16-byte aligned rows
+  float* t = reinterpret_cast<float*>(smem + gemv_term_offset(K));
   const int tid = threadIdx.x;
-  // stage the activation (K quants + nb scales) in LDS
-  for (int c = tid; c < cpr; c += GEMV_NT)
-    reinterpret_cast<int4*>(xl)[c] = reinterpret_cast<const int4*>(xq)[c];
+  for (int c = tid; c < cpr; c += GEMV_NT) reinterpret_cast<int4*>(xl)[c] = reinterpret_cast<const int4*>(xq)[c];
   for (int b = tid; b < nb; b += GEMV_NT) xsl[b] = xs[b];
   __syncthreads();
   const int nrows = min(GEMV_R, rows - row0);
@@ -142,21 +243,17 @@ __device__ __forceinline__ float gemv_rows(const int8_t* __restrict__ wq, const 
   const int4* slab = reinterpret_cast<const int4*>(wq + (size_t)row0 * K);
   const uint16_t* dslab = wd + (size_t)row0 * nb;
   const int stride = gemv_term_stride(nb);
-  // (r, c) of chunk f tracked incrementally (no integer division in the stream loop)
-  int r = tid / cpr;
-  int c = tid - r * cpr;
-#pragma unroll 4
-  for (int f = tid; f < total; f += GEMV_NT) {
-    int s = dot4x4(slab[f], reinterpret_cast<const int4*>(xl)[c], 0);
-    s += __shfl_xor(s, 1);
-    if ((tid & 1) == 0) {
+  const int iters = (GEMV_R * cpr + GEMV_NT - 1) / GEMV_NT;
+  for (int it = 0; it < iters; ++it) {
+    const int f = tid + it * GEMV_NT;
+    const int fc = min(f, total - 1);
+    const int r = fc / cpr;
+    const int c = fc - r * cpr;
+    int s = dot4x4(slab[fc], reinterpret_cast<const int4*>(xl)[c], 0);
+    s += dpp_xor1(s);
+    if ((tid & 1) == 0 && f < total) {
       const int b = c >> 1;
       t[r * stride + b] = ((float)s * half_bits_to_float(dslab[r * nb + b])) * xsl[b];
-    }
-    c += GEMV_NT;
-    while (c >= cpr) {
-      c -= cpr;
-      ++r;
     }
   }
   __syncthreads();
@@ -165,12 +262,28 @@ __device__ __forceinline__ float gemv_rows(const int8_t* __restrict__ wq, const 
   return acc;
 }
 
+// K values with a compile-time specialisation (the configured model widths).
+#define CM_GEMV_KS(X) X(2048) X(3072) X(4096) X(5632) X(8192) X(12288) X(14336)
+
+template <int K>
+__global__ __launch_bounds__(GEMV_NT) void k_gemv_k(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                                    int rows, const int8_t* __restrict__ xq,
+                                                    const float* __restrict__ xs, float* y, const float* resid) {
+  const int row0 = blockIdx.x * GEMV_R;
+  const float acc = gemv_rows_k<K>(wq, wd, rows, xq, xs, row0);
+  const int tid = threadIdx.x;
+  if (tid < GEMV_R && row0 + tid < rows) {
+    const int row = row0 + tid;
+    y[row] = resid ? resid[row] + acc : acc;
+  }
+}
+
 __global__ __launch_bounds__(GEMV_NT) void k_gemv(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                   int rows, int K, const int8_t* __restrict__ xq,
                                                   const float* __restrict__ xs, float* y, const float* resid) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int row0 = blockIdx.x * GEMV_R;
-  const float acc = gemv_rows(wq, wd, rows, K, xq, xs, row0, smem);
+  const float acc = gemv_rows_rt(wq, wd, rows, K, xq, xs, row0, smem);
   const int tid = threadIdx.x;
   if (tid < GEMV_R && row0 + tid < rows) {
     const int row = row0 + tid;
@@ -190,8 +303,17 @@ struct StepState {
 // strict '>').  Each workgroup reduces its rows to (value, index) with ties to the lower
 // index; the last workgroup to finish (atomic ticket) reduces the partials in the same
 // way, writes the token, appends it to tokens[step] and advances the position.
+// K = 0 selects the runtime-width body.
+__device__ __forceinline__ void argmax_pair(float& bv, uint32_t& bi, float ov, uint32_t oi) {
+  if (ov > bv || (ov == bv && oi < bi)) {
+    bv = ov;
+    bi = oi;
+  }
+}
+
+template <int K>
 __global__ __launch_bounds__(GEMV_NT) void k_gemv_argmax(const int8_t* __restrict__ wq,
-                                                         const uint16_t* __restrict__ wd, int rows, int K,
+                                                         const uint16_t* __restrict__ wd, int rows, int k_rt,
                                                          const int8_t* __restrict__ xq, const float* __restrict__ xs,
                                                          float* __restrict__ logits, float* __restrict__ part_v,
                                                          uint32_t* __restrict__ part_i, StepState* st,
@@ -201,21 +323,22 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv_argmax(const int8_t* __restric
   __shared__ float rv[GEMV_NT / 64];
   __shared__ uint32_t ri[GEMV_NT / 64];
   const int row0 = blockIdx.x * GEMV_R;
-  const float acc = gemv_rows(wq, wd, rows, K, xq, xs, row0, smem);
+  float acc;
+  if constexpr (K > 0) {
+    acc = gemv_rows_k<K>(wq, wd, rows, xq, xs, row0);
+  } else {
+    acc = gemv_rows_rt(wq, wd, rows, k_rt, xq, xs, row0, smem);
+  }
   const int tid = threadIdx.x;
   if (tid < 64) {
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
     if (tid < GEMV_R && row0 + tid < rows) {
       logits[row0 + tid] = acc;
-      if (acc > bv) { bv = acc; bi = (uint32_t)(row0 + tid); }
+      argmax_pair(bv, bi, acc, (uint32_t)(row0 + tid));
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const uint32_t oi = __shfl_xor(bi, o);
-      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
+    for (int o = 32; o > 0; o >>= 1) argmax_pair(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
     if (tid == 0) {
       part_v[blockIdx.x] = bv;
       part_i[blockIdx.x] = bi;
@@ -229,22 +352,16 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv_argmax(const int8_t* __restric
   __threadfence();
   float bv = -INFINITY;
   uint32_t bi = 0xffffffffu;
-  for (int i = tid; i < (int)gridDim.x; i += GEMV_NT) {
-    const float v = part_v[i];
-    const uint32_t ix = part_i[i];
-    if (v > bv || (v == bv && ix < bi)) { bv = v; bi = ix; }
-  }
+  for (int i = tid; i < (int)gridDim.x; i += GEMV_NT) argmax_pair(bv, bi, part_v[i], part_i[i]);
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o);
-    const uint32_t oi = __shfl_xor(bi, o);
-    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+  for (int o = 32; o > 0; o >>= 1) argmax_pair(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
+  if ((tid & 63) == 0) {
+    rv[tid >> 6] = bv;
+    ri[tid >> 6] = bi;
   }
-  if ((tid & 63) == 0) { rv[tid >> 6] = bv; ri[tid >> 6] = bi; }
   __syncthreads();
   if (tid == 0) {
-    for (int w = 1; w < GEMV_NT / 64; ++w)
-      if (rv[w] > bv || (rv[w] == bv && ri[w] < bi)) { bv = rv[w]; bi = ri[w]; }
+    for (int w = 1; w < GEMV_NT / 64; ++w) argmax_pair(bv, bi, rv[w], ri[w]);
     const uint32_t tok = bi == 0xffffffffu ? 0u : bi;  // all -inf: index 0, as the CPU loop
     st->tok = tok;
     const uint32_t s = st->step;
@@ -327,7 +444,8 @@ __global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict_
 // Per-head QK RMSNorm (optional) + RoPE + f16 KV store for the token at st->pos (test
 // entry point; the engine fuses this into the attention kernel).  One workgroup per head:
 // blocks [0, n_heads) are Q heads, [n_heads, n_heads + n_kv) K heads (which also store the
-// head's V row).  RoPE: rope.rs:489-524; f16 store: kv_cache.rs:573-600.
+// head's V entries; V is stored transposed, [hd][max_pos]).  RoPE: rope.rs:489-524; f16
+// store: kv_cache.rs:573-600.
 __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, int n_heads, int n_kv, int hd,
                                                 int rope_dim, int split_half, const float* __restrict__ cosv,
                                                 const float* __restrict__ sinv, const float* __restrict__ q_norm,
@@ -365,11 +483,12 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, i
     for (int d = threadIdx.x; d < hd; d += blockDim.x) qrot[(size_t)h * hd + d] = buf[d];
   } else {
     const int kvh = h - n_heads;
-    const size_t dst = (((size_t)layer * n_kv + kvh) * max_pos + *d_pos) * hd;
+    const size_t dst = (((size_t)layer * n_kv + kvh) * max_pos + *d_pos) * hd;         // K [pos][hd]
+    const size_t vdst = (((size_t)layer * n_kv + kvh) * hd) * max_pos + *d_pos;       // V [hd][max_pos]
     const float* vsrc = qkv + (size_t)(n_heads + n_kv) * hd + (size_t)kvh * hd;
     for (int d = threadIdx.x; d < hd; d += blockDim.x) {
       kc[dst + d] = f32_to_f16_bits(buf[d]);
-      vc[dst + d] = f32_to_f16_bits(vsrc[d]);
+      vc[vdst + (size_t)d * max_pos] = f32_to_f16_bits(vsrc[d]);
     }
   }
 }
@@ -380,29 +499,34 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, i
 //   m = max_p score_p                          exact
 //   e_p = expf(score_p - m); sum = fold_p e_p  serial fold by one lane
 //   out_d = fold_p (e_p * (1/sum)) * v_pd      one lane per d, p in order
+// KV cache layout (per layer, per kv head): K rows [pos][HD] (a score lane streams one
+// contiguous 2*HD-byte row), V transposed [HD][max_pos] (an output lane streams its d's
+// values over positions, 8 per 16-byte load).
 // FUSED (the engine's path): the kernel first builds this token's q (and the kv head's k
 // and v) from the fused QKV projection: optional per-head QK RMSNorm (tensor/mod.rs:2112),
 // RoPE (rope.rs:489-524) with the tables at cos_base + pos*rope_stride, f16 rounding of k
-// and v (kv_cache.rs:573-600).  The first q head of each GQA group stores the new K/V row;
-// every head of the group uses its own LDS copy of that row for position pos.
+// and v (kv_cache.rs:573-600).  The first q head of each GQA group stores the new K/V
+// entries; every head of the group uses its own LDS copy of them for position pos.
 // Not FUSED (test entry point): q is taken from qsrc and K/V entirely from the cache.
-// The head's output is quantized to Q8_0 (hd % 32 == 0: blocks never straddle heads).
-// Dynamic LDS = align16(max_pos) * 4 bytes.
+// The head's output is quantized to Q8_0 (HD % 32 == 0: blocks never straddle heads).
+// Dynamic LDS = align4(max_pos) * 4 bytes.
 constexpr int ATT_NT = 256;
 
-template <bool FUSED>
+template <int HD, bool FUSED>
 __global__ __launch_bounds__(ATT_NT) void k_attention(
-    const float* __restrict__ qsrc, int n_heads, int n_kv, int hd, int rope_dim, int split_half,
+    const float* __restrict__ qsrc, int n_heads, int n_kv, int rope_dim, int split_half,
     const float* __restrict__ cos_base, const float* __restrict__ sin_base, int rope_stride,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm, float eps, uint16_t* __restrict__ kc,
     uint16_t* __restrict__ vc, int layer, int max_pos, const uint32_t* __restrict__ d_pos, float scale,
     float* __restrict__ att_out, int8_t* __restrict__ xq, float* __restrict__ xs) {
+  static_assert(HD % 32 == 0 && HD <= ATT_NT, "head_dim must be a multiple of 32 and at most 256");
+  constexpr int R8 = HD / 8;  // 16-byte loads per K row
   extern __shared__ __align__(16) float sc[];
-  __shared__ __align__(16) float qs[512];
-  __shared__ __align__(16) float kn[512];  // this position's k (f16-rounded), then scratch
-  __shared__ __align__(16) float vn[512];  // this position's v (f16-rounded)
-  __shared__ __align__(16) float out[512];
-  __shared__ __align__(16) float sq[1024];
+  __shared__ __align__(16) float qs[HD];
+  __shared__ __align__(16) float kn[HD];  // this position's k (f16-rounded)
+  __shared__ __align__(16) float vn[HD];  // this position's v (f16-rounded)
+  __shared__ __align__(16) float out[HD];
+  __shared__ __align__(16) float sq[2 * HD];
   __shared__ float red[ATT_NT / 64];
   __shared__ float s_qscale, s_kscale, s_inv;
   const int tid = threadIdx.x;
@@ -411,40 +535,41 @@ __global__ __launch_bounds__(ATT_NT) void k_attention(
   const int kvh = h / rep;
   const int pos = (int)*d_pos;
   const int P = pos + 1;
-  const size_t base = (((size_t)layer * n_kv + kvh) * max_pos) * hd;
+  const size_t kbase = (((size_t)layer * n_kv + kvh) * max_pos) * HD;  // K [pos][HD]
+  const size_t vbase = (((size_t)layer * n_kv + kvh) * HD) * max_pos;  // V [HD][max_pos]
 
   if (FUSED) {
-    const float* q = qsrc + (size_t)h * hd;
-    const float* k = qsrc + (size_t)n_heads * hd + (size_t)kvh * hd;
-    const float* v = qsrc + (size_t)(n_heads + n_kv) * hd + (size_t)kvh * hd;
-    for (int d = tid; d < hd; d += ATT_NT) {
-      qs[d] = q[d];
-      kn[d] = k[d];
-      vn[d] = half_bits_to_float(f32_to_f16_bits(v[d]));
+    const float* q = qsrc + (size_t)h * HD;
+    const float* k = qsrc + (size_t)n_heads * HD + (size_t)kvh * HD;
+    const float* v = qsrc + (size_t)(n_heads + n_kv) * HD + (size_t)kvh * HD;
+    if (tid < HD) {
+      qs[tid] = q[tid];
+      kn[tid] = k[tid];
+      vn[tid] = v[tid];
     }
     if (q_norm) {  // per-head RMSNorm of q and k (two serial folds by two lanes)
       __syncthreads();
-      for (int d = tid; d < hd; d += ATT_NT) {
-        sq[d] = qs[d] * qs[d];
-        sq[512 + d] = kn[d] * kn[d];
+      if (tid < HD) {
+        sq[tid] = qs[tid] * qs[tid];
+        sq[HD + tid] = kn[tid] * kn[tid];
       }
       __syncthreads();
-      if (tid == 0) s_qscale = 1.0f / sqrtf(fold_lds(sq, hd) / (float)hd + eps);
-      if (tid == 64) s_kscale = 1.0f / sqrtf(fold_lds(sq + 512, hd) / (float)hd + eps);
+      if (tid == 0) s_qscale = 1.0f / sqrtf(fold_lds_n<HD>(sq) / (float)HD + eps);
+      if (tid == 64) s_kscale = 1.0f / sqrtf(fold_lds_n<HD>(sq + HD) / (float)HD + eps);
       __syncthreads();
-      for (int d = tid; d < hd; d += ATT_NT) {
-        qs[d] = (qs[d] * s_qscale) * q_norm[d];
-        kn[d] = (kn[d] * s_kscale) * k_norm[d];
+      if (tid < HD) {
+        qs[tid] = (qs[tid] * s_qscale) * q_norm[tid];
+        kn[tid] = (kn[tid] * s_kscale) * k_norm[tid];
       }
     }
     __syncthreads();
     const float* cosv = cos_base + (size_t)pos * rope_stride;
     const float* sinv = sin_base + (size_t)pos * rope_stride;
     const int half = rope_dim >> 1;
-    for (int p = tid; p < half; p += ATT_NT) {
-      const int d0 = split_half ? p : 2 * p;
-      const int d1 = split_half ? p + half : 2 * p + 1;
-      const float c = cosv[p], s = sinv[p];
+    if (tid < half) {
+      const int d0 = split_half ? tid : 2 * tid;
+      const int d1 = split_half ? tid + half : 2 * tid + 1;
+      const float c = cosv[tid], s = sinv[tid];
       float x0 = qs[d0], x1 = qs[d1];
       qs[d0] = (x0 * c) - (x1 * s);
       qs[d1] = (x0 * s) + (x1 * c);
@@ -454,55 +579,70 @@ __global__ __launch_bounds__(ATT_NT) void k_attention(
       kn[d1] = (x0 * s) + (x1 * c);
     }
     __syncthreads();
-    const bool store = (h % rep) == 0;
-    for (int d = tid; d < hd; d += ATT_NT) {
-      const uint16_t kb = f32_to_f16_bits(kn[d]);
-      kn[d] = half_bits_to_float(kb);
-      if (store) {
-        kc[base + (size_t)pos * hd + d] = kb;
-        vc[base + (size_t)pos * hd + d] = f32_to_f16_bits(vn[d]);
+    if (tid < HD) {
+      const uint16_t kb = f32_to_f16_bits(kn[tid]);
+      const uint16_t vb = f32_to_f16_bits(vn[tid]);
+      kn[tid] = half_bits_to_float(kb);
+      vn[tid] = half_bits_to_float(vb);
+      if ((h % rep) == 0) {
+        kc[kbase + (size_t)pos * HD + tid] = kb;
+        vc[vbase + (size_t)tid * max_pos + pos] = vb;
       }
     }
   } else {
-    for (int d = tid; d < hd; d += ATT_NT) {
-      qs[d] = qsrc[(size_t)h * hd + d];
-      kn[d] = half_bits_to_float(kc[base + (size_t)pos * hd + d]);
-      vn[d] = half_bits_to_float(vc[base + (size_t)pos * hd + d]);
+    if (tid < HD) {
+      qs[tid] = qsrc[(size_t)h * HD + tid];
+      kn[tid] = half_bits_to_float(kc[kbase + (size_t)pos * HD + tid]);
+      vn[tid] = half_bits_to_float(vc[vbase + (size_t)tid * max_pos + pos]);
     }
   }
   __syncthreads();
 
   if (P == 1) {
     // inference.rs:23564-23575: a single position copies the V row.
-    for (int d = tid; d < hd; d += ATT_NT) out[d] = vn[d];
+    if (tid < HD) out[tid] = vn[tid];
   } else {
-    // scores
+    // ---- scores: cache positions 0..pos-1, one lane each, next row prefetched
     float lmax = -INFINITY;
-    for (int p = tid; p < P; p += ATT_NT) {
-      float acc = 0.0f;
-      if (p == pos) {
-        for (int d = 0; d < hd; ++d) acc += qs[d] * kn[d];
-      } else {
-        const uint4* kr = reinterpret_cast<const uint4*>(kc + base + (size_t)p * hd);
-        for (int d8 = 0; d8 < (hd >> 3); d8 += 4) {
-          uint4 raw[4];
+    const int ncache = pos;
+    {
+      const uint4* kr0 = reinterpret_cast<const uint4*>(kc + kbase);
+      uint4 cur[R8], nxt[R8];
+      int p = tid;
+      {
+        const int pc = min(p, ncache - 1);
 #pragma unroll
-          for (int u = 0; u < 4; ++u) raw[u] = kr[d8 + u];
+        for (int u = 0; u < R8; ++u) cur[u] = kr0[(size_t)pc * R8 + u];
+      }
+      for (; p < ncache; p += ATT_NT) {
+        const int pn = min(p + ATT_NT, ncache - 1);
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const uint32_t wv[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
-            const int d = (d8 + u) * 8;
+        for (int u = 0; u < R8; ++u) nxt[u] = kr0[(size_t)pn * R8 + u];
+        __builtin_amdgcn_sched_barrier(0);
+        float acc = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              acc += qs[d + 2 * j] * half_bits_to_float((uint16_t)(wv[j] & 0xffffu));
-              acc += qs[d + 2 * j + 1] * half_bits_to_float((uint16_t)(wv[j] >> 16));
-            }
+        for (int u = 0; u < R8; ++u) {
+          const uint32_t wv[4] = {cur[u].x, cur[u].y, cur[u].z, cur[u].w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc += qs[u * 8 + 2 * j] * half_bits_to_float((uint16_t)(wv[j] & 0xffffu));
+            acc += qs[u * 8 + 2 * j + 1] * half_bits_to_float((uint16_t)(wv[j] >> 16));
           }
         }
+        const float sv = acc * scale;
+        sc[p] = sv;
+        lmax = fmaxf(lmax, sv);
+#pragma unroll
+        for (int u = 0; u < R8; ++u) cur[u] = nxt[u];
       }
-      const float s = acc * scale;
-      sc[p] = s;
-      lmax = fmaxf(lmax, s);
+    }
+    if (tid == (pos & (ATT_NT - 1))) {  // this token's own key, from LDS
+      float acc = 0.0f;
+#pragma unroll
+      for (int d = 0; d < HD; ++d) acc += qs[d] * kn[d];
+      const float sv = acc * scale;
+      sc[pos] = sv;
+      lmax = fmaxf(lmax, sv);
     }
     const float mx = block_max(lmax, red);
     for (int p = tid; p < P; p += ATT_NT) sc[p] = glibc_expf(sc[p] - mx);
@@ -512,35 +652,56 @@ __global__ __launch_bounds__(ATT_NT) void k_attention(
     const float inv = s_inv;
     for (int p = tid; p < P; p += ATT_NT) sc[p] = sc[p] * inv;
     __syncthreads();
-    if (tid < hd) {
-      // out_d = fold over p of prob_p * v_pd; V loads run one group of 8 positions ahead.
-      const uint16_t* vcol = vc + base + tid;
+    // ---- out_d = fold_p prob_p * v_pd: lane d streams V^T row d, 8 positions per load,
+    // loads running 4 groups ahead.
+    if (tid < HD) {
+      const uint4* vrow = reinterpret_cast<const uint4*>(vc + vbase + (size_t)tid * max_pos);
+      const int ng = ncache >> 3;  // full groups of 8 cache positions
       float acc = 0.0f;
-      const int npre = pos;  // positions read from the cache
-      uint16_t cur[8], nxt[8];
-      int p = 0;
+      uint4 buf[4];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) cur[u] = (u < npre) ? vcol[(size_t)u * hd] : 0;
-      for (; p + 8 <= npre; p += 8) {
+      for (int u = 0; u < 4; ++u) buf[u] = vrow[min(u, max(ng - 1, 0))];
+      int g = 0;
+      for (; g + 4 <= ng; g += 4) {
 #pragma unroll
-        for (int u = 0; u < 8; ++u) nxt[u] = (p + 8 + u < npre) ? vcol[(size_t)(p + 8 + u) * hd] : 0;
-#pragma unroll
-        for (int u = 0; u < 8; ++u) acc += sc[p + u] * half_bits_to_float(cur[u]);
-#pragma unroll
-        for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
+        for (int u = 0; u < 4; ++u) {
+          const uint4 cur = buf[u];
+          buf[u] = vrow[min(g + 4 + u, max(ng - 1, 0))];
+          __builtin_amdgcn_sched_barrier(0);
+          const float4 pa = *reinterpret_cast<const float4*>(sc + (g + u) * 8);
+          const float4 pb = *reinterpret_cast<const float4*>(sc + (g + u) * 8 + 4);
+          acc += pa.x * half_bits_to_float((uint16_t)(cur.x & 0xffffu));
+          acc += pa.y * half_bits_to_float((uint16_t)(cur.x >> 16));
+          acc += pa.z * half_bits_to_float((uint16_t)(cur.y & 0xffffu));
+          acc += pa.w * half_bits_to_float((uint16_t)(cur.y >> 16));
+          acc += pb.x * half_bits_to_float((uint16_t)(cur.z & 0xffffu));
+          acc += pb.y * half_bits_to_float((uint16_t)(cur.z >> 16));
+          acc += pb.z * half_bits_to_float((uint16_t)(cur.w & 0xffffu));
+          acc += pb.w * half_bits_to_float((uint16_t)(cur.w >> 16));
+        }
       }
-      for (int u = 0; p < npre; ++p, ++u) acc += sc[p] * half_bits_to_float(cur[u]);
+      for (; g < ng; ++g) {
+        const uint4 cur = vrow[g];
+        const uint32_t wv[4] = {cur.x, cur.y, cur.z, cur.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc += sc[g * 8 + 2 * j] * half_bits_to_float((uint16_t)(wv[j] & 0xffffu));
+          acc += sc[g * 8 + 2 * j + 1] * half_bits_to_float((uint16_t)(wv[j] >> 16));
+        }
+      }
+      const uint16_t* vs = vc + vbase + (size_t)tid * max_pos;
+      for (int p = ng * 8; p < ncache; ++p) acc += sc[p] * half_bits_to_float(vs[p]);
       acc += sc[pos] * vn[tid];
       out[tid] = acc;
     }
   }
   __syncthreads();
-  for (int d = tid; d < hd; d += ATT_NT) {
-    att_out[(size_t)h * hd + d] = out[d];
+  if (tid < HD) {
+    att_out[(size_t)h * HD + tid] = out[tid];
     int8_t q;
-    const float dd = quantize_lane32(out[d], &q);
-    xq[(size_t)h * hd + d] = q;
-    if ((d & 31) == 0) xs[((size_t)h * hd + d) >> 5] = dd;
+    const float dd = quantize_lane32(out[tid], &q);
+    xq[(size_t)h * HD + tid] = q;
+    if ((tid & 31) == 0) xs[((size_t)h * HD + tid) >> 5] = dd;
   }
 }
 

@@ -50,8 +50,9 @@ enum { CAMELID_Q8_WIRE34 = 34, CAMELID_Q8_BLOCK36 = 36 };
 enum { CAMELID_PROJ_Q = 0, CAMELID_PROJ_K, CAMELID_PROJ_V, CAMELID_PROJ_O,
        CAMELID_PROJ_GATE, CAMELID_PROJ_UP, CAMELID_PROJ_DOWN, CAMELID_N_PROJ };
 
-/* CudaResidentDecode::new (cuda_resident.rs:5601): allocates the f16 KV cache
- * [L][n_kv][max_pos][hd] and all scratch on device 0 (or CAMELID_HIP_DEVICE). */
+/* CudaResidentDecode::new (cuda_resident.rs:5601): allocates the f16 KV cache (K [L][n_kv][kvs][hd],
+ * V transposed [L][n_kv][hd][kvs], kvs = max_pos rounded up to a multiple of 8) and all
+ * scratch on device 0 (or CAMELID_HIP_DEVICE).  head_dim must be 64, 128 or 256. */
 int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** out);
 /* Drop (cuda_resident.rs:5398 Drop + cuda.rs:485 release_async_pool). */
 void camelid_hip_engine_free(camelid_hip_engine* e);
@@ -159,13 +160,15 @@ int camelid_hip_quantize_q8_0(const float* x, uint32_t n, int8_t* xq, float* xs,
 int camelid_hip_silu_mul_quantize(const float* gu, uint32_t n, int8_t* xq, float* xs, float* act,
                                   void* stream);
 /* rope_rotate + kv_scatter (cuda_resident.rs:1545, :1569; CPU rope.rs:489-524,
- * kv_cache.rs:573-600), with optional per-head QK RMSNorm (cuda_resident.rs:122). */
+ * kv_cache.rs:573-600), with optional per-head QK RMSNorm (cuda_resident.rs:122).  Cache
+ * layout: K [L][n_kv][max_pos][hd], V transposed [L][n_kv][hd][max_pos]. */
 int camelid_hip_rope_kv(const float* qkv, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
                         uint32_t rope_dim, uint32_t split_half, const float* cos_tab,
                         const float* sin_tab, const float* q_norm, const float* k_norm, float eps,
                         float* qrot, uint16_t* kc, uint16_t* vc, uint32_t layer, uint32_t max_pos,
                         const uint32_t* d_pos, void* stream);
-/* attention_decode (cuda_resident.rs:1587; CPU inference.rs:23945-24025), faithful order. */
+/* attention_decode (cuda_resident.rs:1587; CPU inference.rs:23945-24025), faithful order.
+ * Cache layout as camelid_hip_rope_kv; max_pos (the position stride) % 8 == 0; hd in {64,128,256}. */
 int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const uint16_t* vc,
                                  uint32_t layer, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
                                  uint32_t max_pos, const uint32_t* d_pos, float scale,

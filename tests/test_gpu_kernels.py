@@ -143,7 +143,7 @@ def test_silu_mul_quantize_bit_exact(native, orc):
                                                 (32, 8, 128, True, True)])
 def test_rope_kv_bit_exact(native, orc, nh, nkv, hd, split, qk):
     rng = np.random.default_rng(nh + hd)
-    L, max_pos, layer, pos = 2, 40, 1, 33
+    L, max_pos, layer, pos = 2, 40, 1, 33  # max_pos (the position stride) is a multiple of 8
     qkv = rng.normal(0, 2, (nh + 2 * nkv) * hd).astype(np.float32)
     c, s = orc.rope_tables(hd, 500000.0, 2, 32.0, 8192.0, 1.0, 4.0, None, pos, 1)
     qn = rng.normal(1, 0.3, hd).astype(np.float32) if qk else None
@@ -167,22 +167,24 @@ def test_rope_kv_bit_exact(native, orc, nh, nkv, hd, split, qk):
     want_k = orc.apply_rope(k, nkv, hd, hd, c[0], s[0], split)
     assert np.array_equal(_bits(qrot.download(np.float32, nh * hd)), _bits(want_q))
     kk = kc.download(np.uint16, L * nkv * max_pos * hd).reshape(L, nkv, max_pos, hd)
-    vv = vc.download(np.uint16, L * nkv * max_pos * hd).reshape(L, nkv, max_pos, hd)
+    vv = vc.download(np.uint16, L * nkv * max_pos * hd).reshape(L, nkv, hd, max_pos)  # V transposed
     assert np.array_equal(kk[layer, :, pos], orc.f32_to_f16(want_k).reshape(nkv, hd))
-    assert np.array_equal(vv[layer, :, pos], orc.f32_to_f16(v).reshape(nkv, hd))
+    assert np.array_equal(vv[layer, :, :, pos], orc.f32_to_f16(v).reshape(nkv, hd))
 
 
 @pytest.mark.parametrize("nh,nkv,hd,P", [(24, 8, 128, 1), (24, 8, 128, 2), (24, 8, 128, 511), (24, 8, 128, 767),
                                          (32, 4, 64, 129), (8, 8, 64, 300), (32, 8, 128, 1280)])
 def test_attention_decode_bit_exact(native, orc, nh, nkv, hd, P):
     rng = np.random.default_rng(P + nh)
-    L, layer, max_pos = 2, 1, max(P, 2) + 3
+    L, layer, max_pos = 2, 1, (max(P, 2) + 3 + 7) // 8 * 8  # position stride: multiple of 8
     kf = rng.normal(0, 1.5, (L, nkv, max_pos, hd)).astype(np.float32)
     vf = rng.normal(0, 1, (L, nkv, max_pos, hd)).astype(np.float32)
     kb, vb = orc.f32_to_f16(kf), orc.f32_to_f16(vf)
     q = rng.normal(0, 1, nh * hd).astype(np.float32)
     scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
-    dq, dk, dv, dpos = _dev(q), _dev(kb), _dev(vb), _dev(np.array([P - 1], np.uint32))
+    # device layout: K [L][nkv][pos][hd], V transposed [L][nkv][hd][pos]
+    dq, dk, dv = _dev(q), _dev(kb), _dev(np.ascontiguousarray(vb.transpose(0, 1, 3, 2)))
+    dpos = _dev(np.array([P - 1], np.uint32))
     out, xq, xs = _buf(nh * hd * 4), _buf(nh * hd), _buf(nh * hd // 32 * 4)
     _ok(native.camelid_hip_attention_decode(dq.ptr, dk.ptr, dv.ptr, layer, nh, nkv, hd, max_pos, dpos.ptr, scale,
                                             out.ptr, xq.ptr, xs.ptr, None))
