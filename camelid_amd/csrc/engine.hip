@@ -10,7 +10,7 @@
 //   rounded up to a multiple of 8 (16-byte aligned V rows)
 //   activations: h [H] (residual stream), qkv, att [nq], gu [2F], logits [V], one Q8_0
 //                activation buffer (quants + f32 scales) reused by every GEMV
-//   StepState {pos, tok, step, counter}: the decode loop's device-side state
+//   StepState {pos, tok, step}: the decode loop's device-side state
 //
 // Per decode step (launch order on the one stream):
 //   [embed]  rmsnorm_quant -> gemv(QKV) -> attention(+QK-norm, RoPE, KV store) ->
@@ -258,13 +258,29 @@ double q8_bytes(const Q8Mat& m, bool resid) {
 }
 
 // ---------------------------------------------------------------- launches
-void launch_gemv(const Q8Mat& m, const int8_t* xq, const float* xs, float* y, const float* resid, hipStream_t s) {
-  const uint32_t grid = (m.rows + cm::GEMV_R - 1) / cm::GEMV_R;
+uint32_t gemv_rows_per_wg(const Q8Mat& m) {
   switch (m.k) {
-#define CM_GEMV_CASE(K)                                                                                      \
-  case K:                                                                                                    \
-    hipLaunchKernelGGL(cm::k_gemv_k<K>, dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, xq, xs, y, \
-                       resid);                                                                               \
+#define CM_GEMV_CASE(K) \
+  case K:               \
+    return 4 * cm::gemv_rpw(K, (int)m.rows);
+    CM_GEMV_KS(CM_GEMV_CASE)
+#undef CM_GEMV_CASE
+    default:
+      return cm::GEMV_R;
+  }
+}
+
+void launch_gemv(const Q8Mat& m, const int8_t* xq, const float* xs, float* y, const float* resid, hipStream_t s) {
+  const uint32_t grid = (m.rows + gemv_rows_per_wg(m) - 1) / gemv_rows_per_wg(m);
+  switch (m.k) {
+#define CM_GEMV_CASE(K)                                                                                             \
+  case K:                                                                                                           \
+    if (cm::gemv_rpw(K, (int)m.rows) == 2)                                                                          \
+      hipLaunchKernelGGL((cm::k_gemv_k<K, 2>), dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, xq, xs, y, \
+                         resid);                                                                                    \
+    else                                                                                                            \
+      hipLaunchKernelGGL((cm::k_gemv_k<K, 1>), dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, xq, xs, y, \
+                         resid);                                                                                    \
     return;
     CM_GEMV_KS(CM_GEMV_CASE)
 #undef CM_GEMV_CASE
@@ -274,20 +290,27 @@ void launch_gemv(const Q8Mat& m, const int8_t* xq, const float* xs, float* y, co
   }
 }
 
-void launch_gemv_argmax(const Q8Mat& m, const int8_t* xq, const float* xs, float* logits, float* part_v,
-                        uint32_t* part_i, cm::StepState* st, uint32_t* tokens, uint32_t cap, hipStream_t s) {
-  const uint32_t grid = (m.rows + cm::GEMV_R - 1) / cm::GEMV_R;
+// lm_head GEMV with per-workgroup argmax partials; returns the number of partials.
+uint32_t launch_gemv_argmax(const Q8Mat& m, const int8_t* xq, const float* xs, float* logits, float* part_v,
+                            uint32_t* part_i, hipStream_t s) {
+  const uint32_t R = gemv_rows_per_wg(m);
+  const uint32_t grid = (m.rows + R - 1) / R;
   switch (m.k) {
-#define CM_GEMV_CASE(K)                                                                                      \
-  case K:                                                                                                    \
-    hipLaunchKernelGGL(cm::k_gemv_argmax<K>, dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, K, xq, \
-                       xs, logits, part_v, part_i, st, tokens, cap);                                         \
-    return;
+#define CM_GEMV_CASE(K)                                                                                               \
+  case K:                                                                                                             \
+    if (cm::gemv_rpw(K, (int)m.rows) == 2)                                                                            \
+      hipLaunchKernelGGL((cm::k_gemv_argmax<K, 2>), dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, K, xq, \
+                         xs, logits, part_v, part_i);                                                                 \
+    else                                                                                                              \
+      hipLaunchKernelGGL((cm::k_gemv_argmax<K, 1>), dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, K, xq, \
+                         xs, logits, part_v, part_i);                                                                 \
+    return grid;
     CM_GEMV_KS(CM_GEMV_CASE)
 #undef CM_GEMV_CASE
     default:
-      hipLaunchKernelGGL(cm::k_gemv_argmax<0>, dim3(grid), dim3(cm::GEMV_NT), cm::gemv_lds_bytes((int)m.k), s, m.q,
-                         m.d, (int)m.rows, (int)m.k, xq, xs, logits, part_v, part_i, st, tokens, cap);
+      hipLaunchKernelGGL((cm::k_gemv_argmax<0, 1>), dim3(grid), dim3(cm::GEMV_NT), cm::gemv_lds_bytes((int)m.k), s,
+                         m.q, m.d, (int)m.rows, (int)m.k, xq, xs, logits, part_v, part_i);
+      return grid;
   }
 }
 
@@ -371,7 +394,9 @@ void run_head(camelid_hip_engine* e, uint32_t* tokens, uint32_t cap) {
   rmsnorm(e, e->out_norm);
   const Q8Mat& m = e->out;
   ProfScope ps(e, P_GEMV, q8_bytes(m, false));
-  launch_gemv_argmax(m, e->xq, e->xs, e->logits, e->part_v, e->part_i, e->st, tokens, cap, e->stream);
+  const uint32_t nparts = launch_gemv_argmax(m, e->xq, e->xs, e->logits, e->part_v, e->part_i, e->stream);
+  hipLaunchKernelGGL(cm::k_argmax_finish, dim3(1), dim3(1024), 0, e->stream, e->part_v, e->part_i, (int)nparts, e->st,
+                     tokens, cap);
 }
 
 void run_embed(camelid_hip_engine* e) {
@@ -472,7 +497,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   const size_t kv_elems = (size_t)d.n_layers * d.n_kv_heads * e->kvs * d.head_dim;
   const size_t act = std::max<size_t>({(size_t)d.hidden, (size_t)d.ffn_dim, nq});
   const uint32_t half = d.rope_dim / 2;
-  const size_t nparts = (d.vocab + cm::GEMV_R - 1) / cm::GEMV_R;
+  const size_t nparts = (d.vocab + 3) / 4;  // at least 4 rows per lm_head workgroup
   e->tokens_cap = d.max_pos;
   int rc = dev_alloc(e, &e->kc, kv_elems) || dev_alloc(e, &e->vc, kv_elems) || dev_alloc(e, &e->h, d.hidden) ||
            dev_alloc(e, &e->qkv, nq + 2 * nkv) || dev_alloc(e, &e->att, nq) ||

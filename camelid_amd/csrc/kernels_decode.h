@@ -158,36 +158,36 @@ __global__ __launch_bounds__(64) void k_q8_block_dots(const int8_t* __restrict__
 // ---------------------------------------------------------------------------
 // Q8_0 GEMV, faithful:  y[row] = (resid ? resid[row] : 0) + fold_b term(row, b),
 //   term = (float(int_dot(w_b, x_b)) * w_scale_b) * x_scale_b  (inference.rs:19871-19905).
-// A workgroup of 4 waves owns GEMV_R = 8 consecutive rows; wave w owns rows 2w and 2w+1.
+// A workgroup of 4 waves owns 4*RPW consecutive rows; wave w owns rows RPW*w .. RPW*w+RPW-1.
 // Lane l streams 16-byte chunks l, l+64, ... of each of its wave's rows (a wave load is
 // 1 KB contiguous), so lane pairs (2j, 2j+1) hold the two halves of one 32-value block,
 // combined by a DPP exchange (integer, exact).  Every weight and scale load of a wave is
 // issued before the first dot.  Even lanes write the block's f32 term to LDS; then lane r
 // of wave 0 folds row r's terms in block order.
-constexpr int GEMV_R = 8;
-constexpr int GEMV_NT = 256;
-constexpr int GEMV_RPW = 2;  // rows per wave
+constexpr int GEMV_R = 8;     // rows per workgroup of the runtime-width fallback
+constexpr int GEMV_NT = 256;  // 4 waves
 
 __host__ __device__ constexpr int gemv_term_stride(int nb) { return ((nb + 3) & ~3) + 4; }
 
-// Shared body for a compile-time row width K; returns (in lanes 0..7 of wave 0) the
-// folded sum of row row0 + lane.
-template <int K>
+// Shared body for a compile-time row width K and RPW rows per wave; returns (in lanes
+// 0..4*RPW-1 of wave 0) the folded sum of row row0 + lane.
+template <int K, int RPW>
 __device__ __forceinline__ float gemv_rows_k(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, int rows,
                                              const int8_t* __restrict__ xq, const float* __restrict__ xs, int row0) {
   constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64, STRIDE = gemv_term_stride(NB);
+  constexpr int R = 4 * RPW;
   static_assert(NB % 4 == 0, "compile-time GEMV widths are multiples of 128");
   __shared__ __align__(16) int8_t xl[K];
   __shared__ __align__(16) float xsl[NB];
-  __shared__ __align__(16) float t[GEMV_R * STRIDE];
+  __shared__ __align__(16) float t[R * STRIDE];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   // issue this wave's weight and scale loads first (rows clamped: results of rows past the
   // end are computed but never stored)
-  int4 wv[GEMV_RPW][IT];
-  uint16_t dv[GEMV_RPW][IT];
+  int4 wv[RPW][IT];
+  uint16_t dv[RPW][IT];
 #pragma unroll
-  for (int k = 0; k < GEMV_RPW; ++k) {
-    const int row = min(row0 + wave * GEMV_RPW + k, rows - 1);
+  for (int k = 0; k < RPW; ++k) {
+    const int row = min(row0 + wave * RPW + k, rows - 1);
     const int4* w4 = reinterpret_cast<const int4*>(wq + (size_t)row * K);
     const uint16_t* d = wd + (size_t)row * NB;
 #pragma unroll
@@ -202,8 +202,8 @@ __device__ __forceinline__ float gemv_rows_k(const int8_t* __restrict__ wq, cons
   for (int b = tid; b < NB; b += GEMV_NT) xsl[b] = xs[b];
   __syncthreads();
 #pragma unroll
-  for (int k = 0; k < GEMV_RPW; ++k) {
-    float* tr = t + (wave * GEMV_RPW + k) * STRIDE;
+  for (int k = 0; k < RPW; ++k) {
+    float* tr = t + (wave * RPW + k) * STRIDE;
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int c = lane + 64 * i;
@@ -215,7 +215,7 @@ __device__ __forceinline__ float gemv_rows_k(const int8_t* __restrict__ wq, cons
   }
   __syncthreads();
   float acc = 0.0f;
-  if (tid < GEMV_R) acc = fold_lds_n<NB>(t + tid * STRIDE);
+  if (tid < R) acc = fold_lds_n<NB>(t + tid * STRIDE);
   return acc;
 }
 
@@ -262,17 +262,20 @@ __device__ __forceinline__ float gemv_rows_rt(const int8_t* __restrict__ wq, con
   return acc;
 }
 
-// K values with a compile-time specialisation (the configured model widths).
+// K values with a compile-time specialisation (the configured model widths), and the
+// rows per wave used for each: one row per wave keeps >= ~4 workgroups per CU on the
+// smaller projections; two rows per wave halve the workgroup count of the large ones.
 #define CM_GEMV_KS(X) X(2048) X(3072) X(4096) X(5632) X(8192) X(12288) X(14336)
+__host__ __device__ constexpr int gemv_rpw(int K, int rows) { return (rows >= 16384 && K <= 4096) ? 2 : 1; }
 
-template <int K>
+template <int K, int RPW>
 __global__ __launch_bounds__(GEMV_NT) void k_gemv_k(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                     int rows, const int8_t* __restrict__ xq,
                                                     const float* __restrict__ xs, float* y, const float* resid) {
-  const int row0 = blockIdx.x * GEMV_R;
-  const float acc = gemv_rows_k<K>(wq, wd, rows, xq, xs, row0);
+  const int row0 = blockIdx.x * (4 * RPW);
+  const float acc = gemv_rows_k<K, RPW>(wq, wd, rows, xq, xs, row0);
   const int tid = threadIdx.x;
-  if (tid < GEMV_R && row0 + tid < rows) {
+  if (tid < 4 * RPW && row0 + tid < rows) {
     const int row = row0 + tid;
     y[row] = resid ? resid[row] + acc : acc;
   }
@@ -296,7 +299,7 @@ struct StepState {
   uint32_t pos;      // position of the token being computed
   uint32_t tok;      // current token (input of the next step)
   uint32_t step;     // index into the generated-token ring
-  uint32_t counter;  // last-workgroup counter of the lm_head GEMV (always returns to 0)
+  uint32_t pad;
 };
 
 // lm_head GEMV fused with greedy argmax (inference.rs:5912-5925: first index of the max,
@@ -311,21 +314,22 @@ __device__ __forceinline__ void argmax_pair(float& bv, uint32_t& bi, float ov, u
   }
 }
 
-template <int K>
+// lm_head: the GEMV writes the logits and, per workgroup, its (value, index) argmax
+// partial; k_argmax_finish (one workgroup, the next launch) reduces the partials, writes
+// the token, appends it to tokens[step] and advances the position.  K = 0 selects the
+// runtime-width body.
+template <int K, int RPW>
 __global__ __launch_bounds__(GEMV_NT) void k_gemv_argmax(const int8_t* __restrict__ wq,
                                                          const uint16_t* __restrict__ wd, int rows, int k_rt,
                                                          const int8_t* __restrict__ xq, const float* __restrict__ xs,
                                                          float* __restrict__ logits, float* __restrict__ part_v,
-                                                         uint32_t* __restrict__ part_i, StepState* st,
-                                                         uint32_t* __restrict__ tokens, uint32_t tokens_cap) {
+                                                         uint32_t* __restrict__ part_i) {
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int s_last;
-  __shared__ float rv[GEMV_NT / 64];
-  __shared__ uint32_t ri[GEMV_NT / 64];
-  const int row0 = blockIdx.x * GEMV_R;
+  const int R = K > 0 ? 4 * RPW : GEMV_R;
+  const int row0 = blockIdx.x * R;
   float acc;
   if constexpr (K > 0) {
-    acc = gemv_rows_k<K>(wq, wd, rows, xq, xs, row0);
+    acc = gemv_rows_k<K, RPW>(wq, wd, rows, xq, xs, row0);
   } else {
     acc = gemv_rows_rt(wq, wd, rows, k_rt, xq, xs, row0, smem);
   }
@@ -333,7 +337,7 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv_argmax(const int8_t* __restric
   if (tid < 64) {
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
-    if (tid < GEMV_R && row0 + tid < rows) {
+    if (tid < R && row0 + tid < rows) {
       logits[row0 + tid] = acc;
       argmax_pair(bv, bi, acc, (uint32_t)(row0 + tid));
     }
@@ -342,17 +346,19 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv_argmax(const int8_t* __restric
     if (tid == 0) {
       part_v[blockIdx.x] = bv;
       part_i[blockIdx.x] = bi;
-      __threadfence();
-      const uint32_t ticket = atomicAdd(&st->counter, 1u);
-      s_last = ticket == gridDim.x - 1;
     }
   }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+}
+
+__global__ __launch_bounds__(1024) void k_argmax_finish(const float* __restrict__ part_v,
+                                                        const uint32_t* __restrict__ part_i, int nparts, StepState* st,
+                                                        uint32_t* __restrict__ tokens, uint32_t tokens_cap) {
+  __shared__ float rv[16];
+  __shared__ uint32_t ri[16];
+  const int tid = threadIdx.x;
   float bv = -INFINITY;
   uint32_t bi = 0xffffffffu;
-  for (int i = tid; i < (int)gridDim.x; i += GEMV_NT) argmax_pair(bv, bi, part_v[i], part_i[i]);
+  for (int i = tid; i < nparts; i += 1024) argmax_pair(bv, bi, part_v[i], part_i[i]);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) argmax_pair(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
   if ((tid & 63) == 0) {
@@ -361,14 +367,13 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv_argmax(const int8_t* __restric
   }
   __syncthreads();
   if (tid == 0) {
-    for (int w = 1; w < GEMV_NT / 64; ++w) argmax_pair(bv, bi, rv[w], ri[w]);
+    for (int w = 1; w < 16; ++w) argmax_pair(bv, bi, rv[w], ri[w]);
     const uint32_t tok = bi == 0xffffffffu ? 0u : bi;  // all -inf: index 0, as the CPU loop
     st->tok = tok;
     const uint32_t s = st->step;
     if (tokens && s < tokens_cap) tokens[s] = tok;
     st->step = s + 1;
     st->pos = st->pos + 1;
-    st->counter = 0;
   }
 }
 
