@@ -977,6 +977,15 @@ int camelid_hip_argmax(const float* x, uint32_t n, uint32_t* out, void* stream) 
   return launch_status("argmax");
 }
 
+int camelid_hip_inorder_sum_rows(const float* x, uint32_t rows, uint32_t n, uint32_t m_seq, float* out,
+                                 void* stream) {
+  if (!x || !out) return fail(nullptr, "null argument");
+  if (n == 0 || n > 8192 || rows == 0) return fail(nullptr, "n must be in (0, 8192] and rows > 0");
+  hipLaunchKernelGGL(cm::k_inorder_sum_rows, dim3(rows), dim3(1024), 0, (hipStream_t)stream, x, (int)n, (int)m_seq,
+                     out);
+  return launch_status("inorder_sum_rows");
+}
+
 int camelid_hip_expf(const float* x, float* y, size_t n, void* stream) {
   if (!x || !y) return fail(nullptr, "null argument");
   if (n == 0) return 0;

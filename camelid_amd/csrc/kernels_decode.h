@@ -83,6 +83,154 @@ __device__ __forceinline__ float fold_lds(const float* p, int n, float acc = 0.0
   return acc;
 }
 
+// ---------------------------------------------------------------------------
+// Exact in-order sum of n non-negative f32 values, evaluated by a whole workgroup.
+//
+// The CPU folds s_i = RNE(s_{i-1} + t_i) one term at a time.  While the running sum stays
+// in one binade [2^e, 2^(e+1)) its ulp u = 2^(e-23) is fixed and s_{i-1} is a multiple of
+// u, so each step adds the integer d_i = round(t_i / u) (ulps) exactly -- unless t_i / u
+// is an exact half (round-half-even then depends on the running parity) or the step
+// leaves the binade.  A segment of the fold is therefore an integer prefix sum: the
+// workgroup computes the d_i in parallel, prefix-sums them, finds the first index where a
+// tie or a binade change occurs, applies that single step with a real f32 add, and
+// continues from there.  The first m_seq terms (where binade changes are frequent) are
+// folded sequentially by one lane.  The result is bit-identical to the sequential fold.
+// Every thread of the workgroup must call; v is in LDS; the sum is returned to all.
+struct SegDelta {
+  int d;   // ulps added by the step (when valid)
+  int j;   // floor(t / u)
+  bool stop;  // tie, or t too large for the binade, or not a finite non-negative value
+};
+
+__device__ __forceinline__ SegDelta seg_delta(float t, int E) {
+  const uint32_t b = __float_as_uint(t);
+  int et = (int)((b >> 23) & 0xffu);
+  uint32_t mt = b & 0x7fffffu;
+  SegDelta r{0, 0, false};
+  if ((b >> 31) != 0u || et == 255) {  // negative or non-finite: apply as a plain add
+    r.stop = b != 0x80000000u;  // -0 adds nothing
+    return r;
+  }
+  if (et == 0) {
+    et = 1;  // subnormal: value = mt * 2^-149
+  } else {
+    mt |= 0x800000u;
+  }
+  if (mt == 0u) return r;  // +0
+  if (et >= E) {           // t >= 2^e: the step surely leaves the binade
+    r.stop = true;
+    return r;
+  }
+  const int sh = E - et;  // t / u = mt * 2^-sh, sh >= 1
+  if (sh >= 26) return r;  // t < u/4: adds nothing, cannot tie
+  const uint32_t j = mt >> sh;
+  const uint32_t rem = mt & ((1u << sh) - 1u);
+  const uint32_t half = 1u << (sh - 1);
+  r.j = (int)j;
+  r.d = (int)j + (rem > half ? 1 : 0);
+  r.stop = rem == half;
+  return r;
+}
+
+template <int NT>
+__device__ float inorder_sum_nonneg(const float* v, int n, int m_seq) {
+  constexpr int NW = NT / 64;
+  constexpr int CAP = 1 << 25;  // saturating prefix: exact below CAP, and CAP > 2^24
+  constexpr int LIM = 1 << 24;  // 2^24 ulps = the top of the binade
+  __shared__ float sh_s;
+  __shared__ int sh_k;
+  __shared__ int sh_tot[NW];
+  __shared__ int sh_min[NW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int C = (n + NT - 1) / NT;  // contiguous chunk per thread
+  const int i0 = tid * C;
+  if (tid == 0) {
+    const int m = min(n, m_seq);
+    sh_s = fold_lds(v, m);
+    sh_k = m;
+  }
+  __syncthreads();
+  while (true) {
+    const float s = sh_s;
+    const int k = sh_k;
+    if (k >= n) break;
+    const uint32_t sb = __float_as_uint(s);
+    const int E = (int)((sb >> 23) & 0xffu);
+    if (E == 0 || E >= 254) {  // zero/subnormal/huge running sum: one plain step
+      __syncthreads();
+      if (tid == 0) {
+        sh_s = s + v[k];
+        sh_k = k + 1;
+      }
+      __syncthreads();
+      continue;
+    }
+    const int M = (int)((sb & 0x7fffffu) | 0x800000u);
+    // pass 1: chunk total of the deltas (saturating)
+    int T = 0;
+    for (int c = 0; c < C; ++c) {
+      const int i = i0 + c;
+      if (i >= k && i < n) T = min(T + seg_delta(v[i], E).d, CAP);
+    }
+    // block exclusive scan of the chunk totals
+    int incl = T;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o);
+      if (lane >= o) incl = min(incl + y, CAP);
+    }
+    int excl = __shfl_up(incl, 1);
+    if (lane == 0) excl = 0;
+    if (lane == 63) sh_tot[wave] = incl;
+    __syncthreads();
+    int wpre = 0;
+    for (int w = 0; w < wave; ++w) wpre = min(wpre + sh_tot[w], CAP);
+    const int X = min(wpre + excl, CAP);
+    // pass 2: first stop of this chunk (tie/too-large/leaving the binade, or landing on 2^(e+1))
+    int key = 0x7fffffff;
+    int P = X;
+    for (int c = 0; c < C; ++c) {
+      const int i = i0 + c;
+      if (i < k || i >= n) continue;
+      const SegDelta st = seg_delta(v[i], E);
+      if (st.stop || M + P + st.j >= LIM) {
+        key = i * 2;
+        break;
+      }
+      P = min(P + st.d, CAP);
+      if (M + P == LIM) {
+        key = i * 2 + 1;
+        break;
+      }
+    }
+    int kmin = key;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) kmin = min(kmin, __shfl_xor(kmin, o));
+    if (lane == 0) sh_min[wave] = kmin;
+    __syncthreads();
+    int gmin = sh_min[0];
+    for (int w = 1; w < NW; ++w) gmin = min(gmin, sh_min[w]);
+    if (gmin == 0x7fffffff) {
+      if (tid == NT - 1) {  // no stop: the block total completes the sum in this binade
+        const int total = min(X + T, CAP);
+        sh_s = __uint_as_float((sb & 0xff800000u) | ((uint32_t)(M + total) & 0x7fffffu));
+        sh_k = n;
+      }
+    } else if (key == gmin) {  // the owner of the first stop applies it
+      const int i = gmin >> 1;
+      if (gmin & 1) {
+        sh_s = __uint_as_float((uint32_t)(E + 1) << 23);  // landed exactly on 2^(e+1)
+      } else {
+        const float sp = __uint_as_float((sb & 0xff800000u) | ((uint32_t)(M + P) & 0x7fffffu));
+        sh_s = sp + v[i];
+      }
+      sh_k = i + 1;
+    }
+    __syncthreads();
+  }
+  return sh_s;
+}
+
 // Compile-time length variant (N % 4 == 0): fully unrolled, same order.
 template <int N>
 __device__ __forceinline__ float fold_lds_n(const float* p, float acc = 0.0f) {
@@ -380,10 +528,12 @@ __global__ __launch_bounds__(1024) void k_argmax_finish(const float* __restrict_
 // ---------------------------------------------------------------------------
 // RMSNorm (tensor/mod.rs:2083-2106) fused with Q8_0 quantization of the result.
 // One workgroup of 1024 threads; thread t holds x[t + 1024 j] in registers; squares go to
-// LDS and thread 0 folds them in order; each 32-lane group then quantizes one block.
+// LDS and are summed in order (inorder_sum_nonneg: bit-identical to the sequential fold);
+// each 32-lane group then quantizes one block.
 // Dynamic LDS = n*4 bytes.  n % 32 == 0, n <= 1024 * RMS_MAXJ.
 constexpr int RMS_NT = 1024;
 constexpr int RMS_MAXJ = 16;
+constexpr int RMS_SEQ_HEAD = 128;  // terms folded sequentially before the segmented sum
 
 __global__ __launch_bounds__(RMS_NT) void k_rmsnorm_quant(const float* __restrict__ x, const float* __restrict__ w,
                                                           int n, float eps, int8_t* __restrict__ xq,
@@ -401,10 +551,8 @@ __global__ __launch_bounds__(RMS_NT) void k_rmsnorm_quant(const float* __restric
     }
   }
   __syncthreads();
-  if (tid == 0) {
-    const float ms = fold_lds(sq, n) / (float)n;
-    s_scale = 1.0f / sqrtf(ms + eps);
-  }
+  const float ss = inorder_sum_nonneg<RMS_NT>(sq, n, RMS_SEQ_HEAD);
+  if (tid == 0) s_scale = 1.0f / sqrtf(ss / (float)n + eps);
   __syncthreads();
   const float scale = s_scale;
 #pragma unroll
@@ -745,6 +893,18 @@ __global__ __launch_bounds__(256) void k_embed_q8(const int8_t* __restrict__ eq,
   if (i >= H) return;
   const size_t t = st->tok;
   h[i] = half_bits_to_float(ed[t * (H >> 5) + (i >> 5)]) * (float)eq[t * H + i];
+}
+
+// In-order sums of non-negative rows (test hook for inorder_sum_nonneg): one workgroup
+// per row, row length n <= 8192 staged in LDS.
+__global__ __launch_bounds__(1024) void k_inorder_sum_rows(const float* __restrict__ x, int n, int m_seq,
+                                                           float* __restrict__ out) {
+  __shared__ __align__(16) float v[8192];
+  const float* row = x + (size_t)blockIdx.x * n;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) v[i] = row[i];
+  __syncthreads();
+  const float sum = inorder_sum_nonneg<1024>(v, n, m_seq);
+  if (threadIdx.x == 0) out[blockIdx.x] = sum;
 }
 
 // glibc-identical expf over a vector (test hook).

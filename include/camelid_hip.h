@@ -175,6 +175,11 @@ int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const ui
                                  float* att_out, int8_t* xq, float* xs, void* stream);
 /* argmax_f32 (cuda_resident.rs:1847; CPU inference.rs:5912). */
 int camelid_hip_argmax(const float* x, uint32_t n, uint32_t* out, void* stream);
+/* Sequential-order f32 sums of non-negative rows [rows][n] (n <= 8192), evaluated with the
+ * workgroup-parallel exact method the RMSNorm uses (test hook; CPU order: the Σx² fold of
+ * tensor/mod.rs:2083-2106); m_seq leading terms are folded sequentially. */
+int camelid_hip_inorder_sum_rows(const float* x, uint32_t rows, uint32_t n, uint32_t m_seq, float* out,
+                                 void* stream);
 /* glibc-identical expf on the device (test hook for the softmax/SiLU exponential). */
 int camelid_hip_expf(const float* x, float* y, size_t n, void* stream);
 /* The same expf restatement evaluated on the host (test hook). */

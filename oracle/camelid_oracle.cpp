@@ -498,3 +498,13 @@ OX void oracle_model_seed_kv(void* p, uint32_t l, uint32_t n, const float* k_in,
       }
     }
 }
+
+// Sequential f32 fold of each row, sum = 0; sum += x[i] (the `.sum::<f32>()` order of
+// tensor/mod.rs:2083-2106 and the softmax denominator of inference.rs:23990-23994).
+OX void oracle_serial_sum_rows(const float* x, size_t rows, size_t n, float* out) {
+  for (size_t r = 0; r < rows; ++r) {
+    float acc = 0.0f;
+    for (size_t i = 0; i < n; ++i) acc += x[r * n + i];
+    out[r] = acc;
+  }
+}

@@ -50,6 +50,7 @@ _SIG = {
     "oracle_model_forward": (C.c_int, [vp, f32p, C.c_uint32, f32p, f32p, f32p, f32p, u32p]),
     "oracle_model_read_kv": (None, [vp, C.c_uint32, C.c_uint32, f32p, f32p]),
     "oracle_model_seed_kv": (None, [vp, C.c_uint32, C.c_uint32, f32p, f32p]),
+    "oracle_serial_sum_rows": (None, [f32p, C.c_size_t, C.c_size_t, f32p]),
 }
 
 _lib = None
@@ -148,6 +149,14 @@ def q8_0_gemm(wire, rows, k, xs, xq) -> np.ndarray:
     out = np.empty((T, rows), np.float32)
     lib().oracle_q8_0_gemm(P(np.ascontiguousarray(wire, np.uint8), C.c_uint8), rows, k, T, P(xs, C.c_float),
                            P(xq, C.c_int8), P(out, C.c_float))
+    return out
+
+
+def serial_sum_rows(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    rows, n = x.shape
+    out = np.empty(rows, np.float32)
+    lib().oracle_serial_sum_rows(P(x, C.c_float), rows, n, P(out, C.c_float))
     return out
 
 

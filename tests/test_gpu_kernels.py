@@ -97,6 +97,59 @@ def test_q8_gemv_extreme_quants(native, orc):
     assert np.array_equal(_bits(y.download(np.float32, rows)), _bits(orc.q8_0_gemv(wire, rows, k, xs, xq)))
 
 
+def _adversarial_rows(rng, rows, n):
+    """Non-negative rows of the kinds that stress the segmented in-order sum: squares of
+    normals at many scales, softmax-like exps, constants (round-half-even ties at every
+    binade), powers of two, zeros mixed in, subnormal magnitudes, huge leading terms, and
+    small integers (exact stretches), plus a few rows with a negative or infinite term."""
+    out = np.empty((rows, n), np.float32)
+    for r in range(rows):
+        kind = r % 10
+        scale = np.float32(2.0 ** rng.integers(-30, 30))
+        x = rng.normal(0, 1, n).astype(np.float32) * scale
+        if kind == 0:
+            row = x * x
+        elif kind == 1:
+            row = np.exp(-np.abs(rng.normal(0, 3, n))).astype(np.float32)
+        elif kind == 2:
+            row = np.full(n, np.float32(0.75) * scale, np.float32)
+        elif kind == 3:
+            row = (2.0 ** rng.integers(0, 20, n)).astype(np.float32) * scale
+        elif kind == 4:
+            row = np.where(rng.random(n) < 0.25, 0, np.abs(x)).astype(np.float32)
+        elif kind == 5:
+            row = (np.abs(x) * np.float32(2.0 ** -140)).astype(np.float32)
+        elif kind == 6:
+            row = np.abs(x)
+            row[:5] *= np.float32(1e6)
+        elif kind == 7:
+            row = (rng.integers(0, 64, n) * 2.0 ** rng.integers(0, 8, n)).astype(np.float32)
+        elif kind == 8:
+            row = x * x
+            row[n // 2] = -row[n // 2] if n > 1 else row[0]
+        else:
+            row = x * x
+            if n > 3:
+                row[n - 3] = np.inf
+        out[r] = row
+    return out
+
+
+@pytest.mark.parametrize("n", [3072, 2048, 4096, 8192, 768, 129, 7, 1])
+def test_inorder_sum_segmented_bit_exact(native, orc, n):
+    """The workgroup-parallel exact in-order sum equals the sequential fold bit for bit."""
+    rng = np.random.default_rng(n)
+    rows = 200 if n <= 4096 else 60
+    x = _adversarial_rows(rng, rows, n)
+    want = orc.serial_sum_rows(x)
+    dx, out = _dev(x), _buf(rows * 4)
+    for m_seq in (128, 0, 1):
+        _ok(native.camelid_hip_inorder_sum_rows(dx.ptr, rows, n, m_seq, out.ptr, None))
+        got = out.download(np.float32, rows)
+        same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+        assert same.all(), (m_seq, np.nonzero(~same)[0][:5])
+
+
 @pytest.mark.parametrize("n", [2048, 3072, 4096, 8192, 96])
 def test_rmsnorm_quantize_bit_exact(native, orc, n):
     rng = np.random.default_rng(n)
