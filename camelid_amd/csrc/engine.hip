@@ -333,7 +333,14 @@ void launch_attention(uint32_t hd, uint32_t n_heads, size_t lds, hipStream_t s, 
 
 void launch_rmsnorm_quant(const float* x, const float* w, uint32_t n, float eps, int8_t* xq, float* xs, float* y,
                           hipStream_t s) {
-  hipLaunchKernelGGL(cm::k_rmsnorm_quant, dim3(1), dim3(cm::RMS_NT), (size_t)n * 4, s, x, w, (int)n, eps, xq, xs, y);
+  switch (cm::seg_chunk((int)n)) {
+#define CM_RMS(C)                                                                                         \
+  case C:                                                                                                 \
+    hipLaunchKernelGGL(cm::k_rmsnorm_quant<C>, dim3(1), dim3(cm::RMS_NT), 0, s, x, w, (int)n, eps, xq, xs, y); \
+    break;
+    CM_SEG_CHUNKS(CM_RMS)
+#undef CM_RMS
+  }
 }
 
 size_t attn_lds_bytes(uint32_t max_pos) { return (((size_t)max_pos + 3) & ~(size_t)3) * 4; }
@@ -469,7 +476,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   if (d.hidden % 32 || d.ffn_dim % 32 || d.head_dim % 32)
     return fail(nullptr, "hidden, ffn_dim and head_dim must be multiples of 32");
   if (!attention_hd_supported(d.head_dim)) return fail(nullptr, "head_dim must be 64, 128 or 256");
-  if (d.hidden > 8192) return fail(nullptr, "hidden > 8192 is not supported by the RMSNorm kernel");
+  if (d.hidden > (uint32_t)cm::SEG_MAX_N) return fail(nullptr, "hidden > 16384 is not supported by the RMSNorm kernel");
   if (d.rope_dim == 0 || d.rope_dim > d.head_dim || d.rope_dim % 2)
     return fail(nullptr, "rope_dim must be even and within head_dim");
   if (attn_lds_bytes(d.max_pos) > 96 * 1024) return fail(nullptr, "max_pos too large for the decode attention");
@@ -922,7 +929,9 @@ int camelid_hip_q8_0_block_dots(const int8_t* wq, uint32_t rows, uint32_t k, con
 int camelid_hip_rmsnorm_quantize(const float* x, const float* w, uint32_t n, float eps, int8_t* xq, float* xs, float* y,
                                  void* stream) {
   if (!x || !w || !xq || !xs) return fail(nullptr, "null argument");
-  if (n == 0 || n % 32 || n > 8192) return fail(nullptr, "n must be a multiple of 32 in (0, 8192]");
+  if (n == 0 || n % 32 || n > (uint32_t)cm::SEG_MAX_N) return fail(nullptr, "n must be a multiple of 32 in (0, 16384]");
+  if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)xq | (uintptr_t)y) & 15u)
+    return fail(nullptr, "x, w, xq and y must be 16-byte aligned");
   launch_rmsnorm_quant(x, w, n, eps, xq, xs, y, (hipStream_t)stream);
   return launch_status("rmsnorm_quantize");
 }
@@ -980,9 +989,16 @@ int camelid_hip_argmax(const float* x, uint32_t n, uint32_t* out, void* stream) 
 int camelid_hip_inorder_sum_rows(const float* x, uint32_t rows, uint32_t n, uint32_t m_seq, float* out,
                                  void* stream) {
   if (!x || !out) return fail(nullptr, "null argument");
-  if (n == 0 || n > 8192 || rows == 0) return fail(nullptr, "n must be in (0, 8192] and rows > 0");
-  hipLaunchKernelGGL(cm::k_inorder_sum_rows, dim3(rows), dim3(1024), 0, (hipStream_t)stream, x, (int)n, (int)m_seq,
-                     out);
+  if (n == 0 || n > (uint32_t)cm::SEG_MAX_N || rows == 0) return fail(nullptr, "n must be in (0, 16384] and rows > 0");
+  switch (cm::seg_chunk((int)n)) {
+#define CM_SUM(C)                                                                                                \
+  case C:                                                                                                        \
+    hipLaunchKernelGGL(cm::k_inorder_sum_rows<C>, dim3(rows), dim3(256), 0, (hipStream_t)stream, x, (int)n,      \
+                       (int)m_seq, out);                                                                         \
+    break;
+    CM_SEG_CHUNKS(CM_SUM)
+#undef CM_SUM
+  }
   return launch_status("inorder_sum_rows");
 }
 

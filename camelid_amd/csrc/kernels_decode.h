@@ -84,66 +84,72 @@ __device__ __forceinline__ float fold_lds(const float* p, int n, float acc = 0.0
 }
 
 // ---------------------------------------------------------------------------
-// Exact in-order sum of n non-negative f32 values, evaluated by a whole workgroup.
+// Exact in-order sum of n f32 values (non-negative in the intended use), evaluated by a
+// whole workgroup; bit-identical to the sequential fold s_i = RNE(s_{i-1} + t_i).
 //
-// The CPU folds s_i = RNE(s_{i-1} + t_i) one term at a time.  While the running sum stays
-// in one binade [2^e, 2^(e+1)) its ulp u = 2^(e-23) is fixed and s_{i-1} is a multiple of
-// u, so each step adds the integer d_i = round(t_i / u) (ulps) exactly -- unless t_i / u
-// is an exact half (round-half-even then depends on the running parity) or the step
-// leaves the binade.  A segment of the fold is therefore an integer prefix sum: the
-// workgroup computes the d_i in parallel, prefix-sums them, finds the first index where a
-// tie or a binade change occurs, applies that single step with a real f32 add, and
-// continues from there.  The first m_seq terms (where binade changes are frequent) are
-// folded sequentially by one lane.  The result is bit-identical to the sequential fold.
-// Every thread of the workgroup must call; v is in LDS; the sum is returned to all.
-struct SegDelta {
-  int d;   // ulps added by the step (when valid)
-  int j;   // floor(t / u)
-  bool stop;  // tie, or t too large for the binade, or not a finite non-negative value
-};
+// While the running sum stays in one binade [2^e, 2^(e+1)) (or in [0, 2^-125), where
+// the ulp is 2^-149 throughout), its ulp u is fixed and s_{i-1} is a multiple of u, so a
+// step adds exactly the integer d_i = RNE(t_i / u) ulps -- unless t_i / u is an exact half
+// (round-half-even then depends on the running parity), t_i >= 2^e, t_i is negative or
+// not finite, or the step leaves the binade.
+//   pass  (all threads, once per binade entered): d_i for every remaining term, with the
+//         exceptional terms ("flagged") given d = 2^25, larger than any in-binade step;
+//         a saturating workgroup prefix sum of d goes to ps[0..n] in LDS.
+//   round (wave 0, while the binade is unchanged): from the running mantissa N (in ulps)
+//         at term k, the first index i >= k whose step reaches 2^24 ulps or is flagged is
+//         the first p with ps[p] >= 2^24 - N + ps[k] (ps is monotone), minus one; found by
+//         a 64-way ballot search.  Terms k..i-1 are summed exactly by the integer
+//         difference; term i is applied as a real f32 add (flag or binade change), or --
+//         when it rounds up onto exactly 2^(e+1) -- written directly.
+// The first m_seq terms, where binade changes are frequent, are folded sequentially.
+// Negative or huge (>= 2^126) running sums take plain sequential steps.  Every thread
+// of the workgroup must call; v (n floats) and ps (n + 1 words) are in LDS; NT * C >= n.
+constexpr uint32_t SEG_LIM = 1u << 24;   // ulps in a binade
+constexpr uint32_t SEG_FLAG = 1u << 25;  // step given to a flagged term
+constexpr uint32_t SEG_GUARD = 0xffffffffu - 2u * SEG_FLAG;  // prefix values the rounds accept
 
-__device__ __forceinline__ SegDelta seg_delta(float t, int E) {
-  const uint32_t b = __float_as_uint(t);
-  int et = (int)((b >> 23) & 0xffu);
-  uint32_t mt = b & 0x7fffffu;
-  SegDelta r{0, 0, false};
-  if ((b >> 31) != 0u || et == 255) {  // negative or non-finite: apply as a plain add
-    r.stop = b != 0x80000000u;  // -0 adds nothing
-    return r;
-  }
-  if (et == 0) {
-    et = 1;  // subnormal: value = mt * 2^-149
-  } else {
-    mt |= 0x800000u;
-  }
-  if (mt == 0u) return r;  // +0
-  if (et >= E) {           // t >= 2^e: the step surely leaves the binade
-    r.stop = true;
-    return r;
-  }
-  const int sh = E - et;  // t / u = mt * 2^-sh, sh >= 1
-  if (sh >= 26) return r;  // t < u/4: adds nothing, cannot tie
-  const uint32_t j = mt >> sh;
-  const uint32_t rem = mt & ((1u << sh) - 1u);
-  const uint32_t half = 1u << (sh - 1);
-  r.j = (int)j;
-  r.d = (int)j + (rem > half ? 1 : 0);
-  r.stop = rem == half;
-  return r;
+__device__ __forceinline__ uint32_t sat_add(uint32_t a, uint32_t b) { return __builtin_elementwise_add_sat(a, b); }
+
+// Step (in ulps of the binade with exponent field Ep >= 1, u = 2^(Ep - 150)) of term t;
+// SEG_FLAG when t / u is a tie, >= 2^23, negative (-0 included), or not finite.
+__device__ __forceinline__ uint32_t seg_d(float t, int Ep, float* q_out = nullptr) {
+  const float q = ldexpf(t, 150 - Ep);  // t / u, exact whenever it is >= 2^-126
+  const float r = rintf(q);
+  if (q_out) *q_out = q;
+  const bool ok = __float_as_uint(q) < 0x4b000000u && fabsf(q - r) != 0.5f;
+  return ok ? (uint32_t)r : SEG_FLAG;
 }
 
-template <int NT>
-__device__ float inorder_sum_nonneg(const float* v, int n, int m_seq) {
+// f32 with value Nv ulps in the binade Ep (Nv < 2^24; Nv == 2^24 gives 2^(e+1)).
+__device__ __forceinline__ float seg_value(int Ep, uint32_t Nv) {
+  return __uint_as_float(((uint32_t)(Ep - 1) << 23) + Nv);
+}
+
+// Saturating wave-wide inclusive scan: DPP row shifts within each 16-lane row, then row
+// broadcasts across rows.
+#define CM_DPP(x, ctrl, rmask) ((uint32_t)__builtin_amdgcn_update_dpp(0, (int)(x), ctrl, rmask, 0xf, false))
+__device__ __forceinline__ uint32_t wave_scan_incl_sat(uint32_t x) {
+  x = sat_add(x, CM_DPP(x, 0x111, 0xf));  // row_shr:1
+  x = sat_add(x, CM_DPP(x, 0x112, 0xf));  // row_shr:2
+  x = sat_add(x, CM_DPP(x, 0x114, 0xf));  // row_shr:4
+  x = sat_add(x, CM_DPP(x, 0x118, 0xf));  // row_shr:8
+  x = sat_add(x, CM_DPP(x, 0x142, 0xa));  // row_bcast:15 -> rows 1, 3
+  x = sat_add(x, CM_DPP(x, 0x143, 0xc));  // row_bcast:31 -> rows 2, 3
+  return x;
+}
+
+template <int NT, int C>
+__device__ __forceinline__ float inorder_sum_nonneg(const float* v, uint32_t* ps, int n, int m_seq) {
   constexpr int NW = NT / 64;
-  constexpr int CAP = 1 << 25;  // saturating prefix: exact below CAP, and CAP > 2^24
-  constexpr int LIM = 1 << 24;  // 2^24 ulps = the top of the binade
+  static_assert(NT % 64 == 0 && NW <= 16, "the cross-wave scan runs in one 16-lane DPP row");
   __shared__ float sh_s;
   __shared__ int sh_k;
-  __shared__ int sh_tot[NW];
-  __shared__ int sh_min[NW];
+  __shared__ uint32_t sh_tot[NW];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int C = (n + NT - 1) / NT;  // contiguous chunk per thread
-  const int i0 = tid * C;
+  const int i0 = tid * C;  // this thread's contiguous chunk
+  float t[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) t[c] = i0 + c < n ? v[i0 + c] : 0.0f;
   if (tid == 0) {
     const int m = min(n, m_seq);
     sh_s = fold_lds(v, m);
@@ -151,80 +157,123 @@ __device__ float inorder_sum_nonneg(const float* v, int n, int m_seq) {
   }
   __syncthreads();
   while (true) {
-    const float s = sh_s;
-    const int k = sh_k;
+    float s = sh_s;
+    int k = sh_k;
     if (k >= n) break;
-    const uint32_t sb = __float_as_uint(s);
-    const int E = (int)((sb >> 23) & 0xffu);
-    if (E == 0 || E >= 254) {  // zero/subnormal/huge running sum: one plain step
-      __syncthreads();
-      if (tid == 0) {
-        sh_s = s + v[k];
-        sh_k = k + 1;
-      }
-      __syncthreads();
-      continue;
-    }
-    const int M = (int)((sb & 0x7fffffu) | 0x800000u);
-    // pass 1: chunk total of the deltas (saturating)
-    int T = 0;
-    for (int c = 0; c < C; ++c) {
-      const int i = i0 + c;
-      if (i >= k && i < n) T = min(T + seg_delta(v[i], E).d, CAP);
-    }
-    // block exclusive scan of the chunk totals
-    int incl = T;
+    const uint32_t sb0 = __float_as_uint(s);
+    const int E0 = (int)((sb0 >> 23) & 0xffu);
+    const int Ep = max(E0, 1);
+    const bool plain = (sb0 >> 31) != 0u || E0 >= 254;
+    if (!plain) {  // pass for binade Ep over the terms k..n-1 (terms before k count 0)
+      uint32_t dv[C];
+      uint32_t T = 0;
+      if (i0 + C > k) {
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(incl, o);
-      if (lane >= o) incl = min(incl + y, CAP);
-    }
-    int excl = __shfl_up(incl, 1);
-    if (lane == 0) excl = 0;
-    if (lane == 63) sh_tot[wave] = incl;
-    __syncthreads();
-    int wpre = 0;
-    for (int w = 0; w < wave; ++w) wpre = min(wpre + sh_tot[w], CAP);
-    const int X = min(wpre + excl, CAP);
-    // pass 2: first stop of this chunk (tie/too-large/leaving the binade, or landing on 2^(e+1))
-    int key = 0x7fffffff;
-    int P = X;
-    for (int c = 0; c < C; ++c) {
-      const int i = i0 + c;
-      if (i < k || i >= n) continue;
-      const SegDelta st = seg_delta(v[i], E);
-      if (st.stop || M + P + st.j >= LIM) {
-        key = i * 2;
-        break;
-      }
-      P = min(P + st.d, CAP);
-      if (M + P == LIM) {
-        key = i * 2 + 1;
-        break;
-      }
-    }
-    int kmin = key;
+        for (int c = 0; c < C; ++c) dv[c] = seg_d(t[c], Ep);
+        if (i0 < k) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) kmin = min(kmin, __shfl_xor(kmin, o));
-    if (lane == 0) sh_min[wave] = kmin;
-    __syncthreads();
-    int gmin = sh_min[0];
-    for (int w = 1; w < NW; ++w) gmin = min(gmin, sh_min[w]);
-    if (gmin == 0x7fffffff) {
-      if (tid == NT - 1) {  // no stop: the block total completes the sum in this binade
-        const int total = min(X + T, CAP);
-        sh_s = __uint_as_float((sb & 0xff800000u) | ((uint32_t)(M + total) & 0x7fffffu));
-        sh_k = n;
-      }
-    } else if (key == gmin) {  // the owner of the first stop applies it
-      const int i = gmin >> 1;
-      if (gmin & 1) {
-        sh_s = __uint_as_float((uint32_t)(E + 1) << 23);  // landed exactly on 2^(e+1)
+          for (int c = 0; c < C; ++c) dv[c] = i0 + c < k ? 0u : dv[c];
+        }
       } else {
-        const float sp = __uint_as_float((sb & 0xff800000u) | ((uint32_t)(M + P) & 0x7fffffu));
-        sh_s = sp + v[i];
+#pragma unroll
+        for (int c = 0; c < C; ++c) dv[c] = 0u;
       }
-      sh_k = i + 1;
+#pragma unroll
+      for (int c = 0; c < C; ++c) T = sat_add(T, dv[c]);
+      const uint32_t incl = wave_scan_incl_sat(T);
+      if (lane == 63) sh_tot[wave] = incl;
+      __syncthreads();
+      uint32_t wt = lane < NW ? sh_tot[lane] : 0u;
+      wt = sat_add(wt, CM_DPP(wt, 0x111, 0xf));
+      wt = sat_add(wt, CM_DPP(wt, 0x112, 0xf));
+      wt = sat_add(wt, CM_DPP(wt, 0x114, 0xf));
+      wt = sat_add(wt, CM_DPP(wt, 0x118, 0xf));
+      const uint32_t wpre = (uint32_t)__builtin_amdgcn_readlane((int)CM_DPP(wt, 0x111, 0xf), wave);
+      uint32_t P = sat_add(wpre, CM_DPP(incl, 0x138, 0xf));  // wave_shr:1 -> exclusive prefix
+      uint32_t pv[C];
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        pv[c] = P;
+        P = sat_add(P, dv[c]);
+      }
+      if constexpr (C % 4 == 0) {
+        if (i0 + C <= n) {
+#pragma unroll
+          for (int c = 0; c < C; c += 4)
+            *reinterpret_cast<uint4*>(ps + i0 + c) = make_uint4(pv[c], pv[c + 1], pv[c + 2], pv[c + 3]);
+        } else {
+#pragma unroll
+          for (int c = 0; c < C; ++c)
+            if (i0 + c < n) ps[i0 + c] = pv[c];
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+          if (i0 + c < n) ps[i0 + c] = pv[c];
+      }
+      if (i0 <= n - 1 && n - 1 < i0 + C) ps[n] = P;
+    }
+    __syncthreads();
+    if (wave == 0) {  // rounds: uniform control flow over the wave
+      const uint32_t tot = plain ? 0u : ps[n];
+      uint32_t base = 0;  // ps[k]: the pass counted nothing before k
+      bool base_ok = true;
+      while (k < n) {
+        const uint32_t sb = __float_as_uint(s);
+        const int E = (int)((sb >> 23) & 0xffu);
+        if ((sb >> 31) != 0u || E >= 254) {  // negative or huge running sum: plain step
+          s = s + v[k];
+          ++k;
+          base_ok = false;
+          continue;
+        }
+        if (plain || max(E, 1) != Ep) break;  // a new binade needs a new pass
+        if (!base_ok) {
+          base = ps[k];
+          base_ok = true;
+        }
+        if (base > SEG_GUARD) break;  // keep the prefix sums unsaturated
+        const uint32_t N = sb - ((uint32_t)(Ep - 1) << 23);
+        const uint32_t X = SEG_LIM - N + base;
+        if (tot < X) {  // no stop: the rest sums exactly in this binade
+          s = seg_value(Ep, N + (tot - base));
+          k = n;
+          break;
+        }
+        // first p in [k + 1, n] with ps[p] >= X (ps[n] >= X)
+        int lo = k + 1, hi = n;
+        while (hi - lo >= 63) {
+          const int stride = (hi - lo + 64) >> 6;
+          const int p = min(lo + lane * stride + stride - 1, hi);
+          const unsigned long long bm = __ballot(ps[p] >= X);
+          const int nlo = lo + (__ffsll((long long)bm) - 1) * stride;
+          hi = min(nlo + stride - 1, hi);
+          lo = nlo;
+        }
+        // lane l holds position lo - 1 + l (lane 0: the term before the range)
+        const int q = min(lo - 1 + lane, hi);
+        const uint32_t pq = ps[q];
+        const float tq = v[min(q, n - 1)];
+        const unsigned long long bm = __ballot(lane >= 1 && lo - 1 + lane <= hi && pq >= X);
+        const int li = __ffsll((long long)bm) - 2;  // lane holding the stopping term i = p - 1
+        const int i = lo - 1 + li;
+        const uint32_t pi = (uint32_t)__builtin_amdgcn_readlane((int)pq, li);
+        const float ti = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tq), li));
+        float qi;
+        const uint32_t di = seg_d(ti, Ep, &qi);
+        const uint32_t Ni = N + (pi - base);  // running sum before term i, exact
+        if (di == SEG_FLAG || Ni + (uint32_t)floorf(qi) >= SEG_LIM) {
+          s = seg_value(Ep, Ni) + ti;  // flagged term or a binade change: real add
+        } else {
+          s = seg_value(Ep, SEG_LIM);  // rounds up onto exactly 2^(e+1)
+        }
+        base = sat_add(pi, di);  // ps[i + 1]
+        k = i + 1;
+      }
+      if (lane == 0) {
+        sh_s = s;
+        sh_k = k;
+      }
     }
     __syncthreads();
   }
@@ -527,46 +576,101 @@ __global__ __launch_bounds__(1024) void k_argmax_finish(const float* __restrict_
 
 // ---------------------------------------------------------------------------
 // RMSNorm (tensor/mod.rs:2083-2106) fused with Q8_0 quantization of the result.
-// One workgroup of 1024 threads; thread t holds x[t + 1024 j] in registers; squares go to
-// LDS and are summed in order (inorder_sum_nonneg: bit-identical to the sequential fold);
-// each 32-lane group then quantizes one block.
-// Dynamic LDS = n*4 bytes.  n % 32 == 0, n <= 1024 * RMS_MAXJ.
-constexpr int RMS_NT = 1024;
-constexpr int RMS_MAXJ = 16;
-constexpr int RMS_SEQ_HEAD = 128;  // terms folded sequentially before the segmented sum
+// One workgroup of RMS_NT threads.  Thread t owns the 32-element blocks t + RMS_NT b: it
+// loads their x and w values up front (16-byte loads, all in flight together), writes the
+// squares to LDS for the in-order sum (inorder_sum_nonneg: bit-identical to the
+// sequential fold), then normalises and quantizes its blocks from registers, with no
+// cross-lane traffic.  n % 32 == 0, n <= RMS_NT * C.
+constexpr int RMS_NT = 256;
+constexpr int RMS_SEQ_HEAD = 384;  // terms folded sequentially before the segmented sum
 
+__device__ __forceinline__ float4 mul4(const float4 a, const float4 b) {
+  return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
+}
+
+// Q8_0 quantization of one 32-element block held by one lane (inference.rs:16953-16971):
+// returns the f16-rounded scale, writes the 32 quants as 8 packed words.
+__device__ __forceinline__ float quantize_block_regs(const float (&y)[32], uint32_t (&packed)[8]) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(y[e]));
+  const float unrounded = amax / 127.0f;
+  const float scale = f16_bits_to_f32(f32_to_f16_bits(unrounded));
+  const float inv = unrounded == 0.0f ? 0.0f : 1.0f / unrounded;
+#pragma unroll
+  for (int w4 = 0; w4 < 8; ++w4) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float r = roundf(y[w4 * 4 + e] * inv);
+      r = fminf(fmaxf(r, -128.0f), 127.0f);
+      word |= ((uint32_t)(int32_t)r & 0xffu) << (8 * e);
+    }
+    packed[w4] = word;
+  }
+  return scale;
+}
+
+template <int C>
 __global__ __launch_bounds__(RMS_NT) void k_rmsnorm_quant(const float* __restrict__ x, const float* __restrict__ w,
                                                           int n, float eps, int8_t* __restrict__ xq,
                                                           float* __restrict__ xs, float* __restrict__ y_out) {
-  extern __shared__ __align__(16) float sq[];
-  __shared__ float s_scale;
+  constexpr int BPT = (C + 31) / 32;  // blocks per thread
+  __shared__ __align__(16) float sq[RMS_NT * C];
+  __shared__ __align__(16) uint32_t ps[RMS_NT * C + 4];
   const int tid = threadIdx.x;
-  float xv[RMS_MAXJ];
+  const int nb = n >> 5;
+  float4 xv[BPT][8], wv[BPT][8];
 #pragma unroll
-  for (int j = 0; j < RMS_MAXJ; ++j) {
-    const int i = tid + j * RMS_NT;
-    if (i < n) {
-      xv[j] = x[i];
-      sq[i] = xv[j] * xv[j];
+  for (int b = 0; b < BPT; ++b) {
+    const int blk = tid + b * RMS_NT;
+    if (blk < nb) {
+      const float4* xp = reinterpret_cast<const float4*>(x + blk * 32);
+      const float4* wp = reinterpret_cast<const float4*>(w + blk * 32);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        xv[b][u] = xp[u];
+        wv[b][u] = wp[u];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) reinterpret_cast<float4*>(sq + blk * 32)[u] = mul4(xv[b][u], xv[b][u]);
     }
   }
   __syncthreads();
-  const float ss = inorder_sum_nonneg<RMS_NT>(sq, n, RMS_SEQ_HEAD);
-  if (tid == 0) s_scale = 1.0f / sqrtf(ss / (float)n + eps);
-  __syncthreads();
-  const float scale = s_scale;
+  const float ss = inorder_sum_nonneg<RMS_NT, C>(sq, ps, n, RMS_SEQ_HEAD);
+  const float scale = 1.0f / sqrtf(ss / (float)n + eps);
 #pragma unroll
-  for (int j = 0; j < RMS_MAXJ; ++j) {
-    const int i = tid + j * RMS_NT;
-    if (i < n) {  // uniform per 32-lane group (n % 32 == 0, RMS_NT % 32 == 0)
-      const float yv = (xv[j] * scale) * w[i];
-      if (y_out) y_out[i] = yv;
-      int8_t q;
-      const float d = quantize_lane32(yv, &q);
-      xq[i] = q;
-      if ((tid & 31) == 0) xs[i >> 5] = d;
+  for (int b = 0; b < BPT; ++b) {
+    const int blk = tid + b * RMS_NT;
+    if (blk < nb) {
+      float y[32];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        y[u * 4 + 0] = (xv[b][u].x * scale) * wv[b][u].x;
+        y[u * 4 + 1] = (xv[b][u].y * scale) * wv[b][u].y;
+        y[u * 4 + 2] = (xv[b][u].z * scale) * wv[b][u].z;
+        y[u * 4 + 3] = (xv[b][u].w * scale) * wv[b][u].w;
+      }
+      if (y_out) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          reinterpret_cast<float4*>(y_out + blk * 32)[u] = make_float4(y[u * 4], y[u * 4 + 1], y[u * 4 + 2], y[u * 4 + 3]);
+      }
+      uint32_t packed[8];
+      xs[blk] = quantize_block_regs(y, packed);
+      uint4* qp = reinterpret_cast<uint4*>(xq + blk * 32);
+      qp[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+      qp[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
     }
   }
+}
+
+// Chunk sizes instantiated for the 256-thread segmented sum (n <= 256 * C).
+#define CM_SEG_CHUNKS(X) X(1) X(2) X(4) X(8) X(12) X(16) X(20) X(24) X(32) X(48) X(64)
+constexpr int SEG_MAX_N = 256 * 64;
+__host__ __device__ constexpr int seg_chunk(int n) {
+  return n <= 256 ? 1 : n <= 512 ? 2 : n <= 1024 ? 4 : n <= 2048 ? 8 : n <= 3072 ? 12 : n <= 4096 ? 16
+       : n <= 5120 ? 20 : n <= 6144 ? 24 : n <= 8192 ? 32 : n <= 12288 ? 48 : 64;
 }
 
 // Plain Q8_0 quantization of an f32 vector: one element per lane, one block per 32 lanes.
@@ -895,15 +999,17 @@ __global__ __launch_bounds__(256) void k_embed_q8(const int8_t* __restrict__ eq,
   h[i] = half_bits_to_float(ed[t * (H >> 5) + (i >> 5)]) * (float)eq[t * H + i];
 }
 
-// In-order sums of non-negative rows (test hook for inorder_sum_nonneg): one workgroup
-// per row, row length n <= 8192 staged in LDS.
-__global__ __launch_bounds__(1024) void k_inorder_sum_rows(const float* __restrict__ x, int n, int m_seq,
-                                                           float* __restrict__ out) {
-  __shared__ __align__(16) float v[8192];
+// In-order sums of rows (test hook for inorder_sum_nonneg): one 256-thread workgroup per
+// row of n values, the first m_seq folded sequentially.  n <= 256 * C.
+template <int C>
+__global__ __launch_bounds__(256) void k_inorder_sum_rows(const float* __restrict__ x, int n, int m_seq,
+                                                          float* __restrict__ out) {
+  __shared__ __align__(16) float v[256 * C];
+  __shared__ __align__(16) uint32_t ps[256 * C + 4];
   const float* row = x + (size_t)blockIdx.x * n;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) v[i] = row[i];
+  for (int i = threadIdx.x; i < n; i += 256) v[i] = row[i];
   __syncthreads();
-  const float sum = inorder_sum_nonneg<1024>(v, n, m_seq);
+  const float sum = inorder_sum_nonneg<256, C>(v, ps, n, m_seq);
   if (threadIdx.x == 0) out[blockIdx.x] = sum;
 }
 

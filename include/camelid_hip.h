@@ -151,7 +151,8 @@ int camelid_hip_q8_0_gemv(const int8_t* wq, const uint16_t* wd, uint32_t rows, u
  * bit-exact block-dot contract, CPU inference.rs:20539-20566). */
 int camelid_hip_q8_0_block_dots(const int8_t* wq, uint32_t rows, uint32_t k, const int8_t* xq, int32_t* out,
                                 void* stream);
-/* rms_norm_quantize (cuda_resident.rs:177; CPU tensor/mod.rs:2083-2106 + inference.rs:16953). */
+/* rms_norm_quantize (cuda_resident.rs:177; CPU tensor/mod.rs:2083-2106 + inference.rs:16953).
+ * n % 32 == 0, n <= 16384; x, w, xq and y (when given) 16-byte aligned. */
 int camelid_hip_rmsnorm_quantize(const float* x, const float* w, uint32_t n, float eps, int8_t* xq,
                                  float* xs, float* y, void* stream);
 /* quantize_q8_0 (cuda_resident.rs:151; CPU inference.rs:16953-16971). */
@@ -175,7 +176,7 @@ int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const ui
                                  float* att_out, int8_t* xq, float* xs, void* stream);
 /* argmax_f32 (cuda_resident.rs:1847; CPU inference.rs:5912). */
 int camelid_hip_argmax(const float* x, uint32_t n, uint32_t* out, void* stream);
-/* Sequential-order f32 sums of non-negative rows [rows][n] (n <= 8192), evaluated with the
+/* Sequential-order f32 sums of rows [rows][n] (n <= 16384), evaluated with the
  * workgroup-parallel exact method the RMSNorm uses (test hook; CPU order: the Σx² fold of
  * tensor/mod.rs:2083-2106); m_seq leading terms are folded sequentially. */
 int camelid_hip_inorder_sum_rows(const float* x, uint32_t rows, uint32_t n, uint32_t m_seq, float* out,

@@ -101,10 +101,11 @@ def _adversarial_rows(rng, rows, n):
     """Non-negative rows of the kinds that stress the segmented in-order sum: squares of
     normals at many scales, softmax-like exps, constants (round-half-even ties at every
     binade), powers of two, zeros mixed in, subnormal magnitudes, huge leading terms, and
-    small integers (exact stretches), plus a few rows with a negative or infinite term."""
+    small integers (exact stretches), plus rows with a negative, infinite or NaN term, all
+    zeros, and many negative terms (the plain-step path)."""
     out = np.empty((rows, n), np.float32)
     for r in range(rows):
-        kind = r % 10
+        kind = r % 13
         scale = np.float32(2.0 ** rng.integers(-30, 30))
         x = rng.normal(0, 1, n).astype(np.float32) * scale
         if kind == 0:
@@ -127,30 +128,38 @@ def _adversarial_rows(rng, rows, n):
         elif kind == 8:
             row = x * x
             row[n // 2] = -row[n // 2] if n > 1 else row[0]
-        else:
+        elif kind == 9:
             row = x * x
             if n > 3:
                 row[n - 3] = np.inf
+        elif kind == 10:
+            row = x * x
+            row[rng.integers(0, n)] = np.nan
+        elif kind == 11:
+            row = np.zeros(n, np.float32)
+            row[n - 1] = np.float32(1e-45)  # zeros, then the smallest subnormal
+        else:
+            row = np.where(rng.random(n) < 0.3, -(x * x), x * x).astype(np.float32)
         out[r] = row
     return out
 
 
-@pytest.mark.parametrize("n", [3072, 2048, 4096, 8192, 768, 129, 7, 1])
+@pytest.mark.parametrize("n", [3072, 2048, 4096, 8192, 16384, 12288, 5000, 768, 257, 256, 129, 7, 1])
 def test_inorder_sum_segmented_bit_exact(native, orc, n):
     """The workgroup-parallel exact in-order sum equals the sequential fold bit for bit."""
     rng = np.random.default_rng(n)
-    rows = 200 if n <= 4096 else 60
+    rows = 260 if n <= 4096 else 65
     x = _adversarial_rows(rng, rows, n)
     want = orc.serial_sum_rows(x)
     dx, out = _dev(x), _buf(rows * 4)
-    for m_seq in (128, 0, 1):
+    for m_seq in (384, 128, 0, 1):
         _ok(native.camelid_hip_inorder_sum_rows(dx.ptr, rows, n, m_seq, out.ptr, None))
         got = out.download(np.float32, rows)
         same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
         assert same.all(), (m_seq, np.nonzero(~same)[0][:5])
 
 
-@pytest.mark.parametrize("n", [2048, 3072, 4096, 8192, 96])
+@pytest.mark.parametrize("n", [2048, 3072, 4096, 5120, 8192, 16384, 96])
 def test_rmsnorm_quantize_bit_exact(native, orc, n):
     rng = np.random.default_rng(n)
     x = (rng.normal(0, 1, n) * rng.uniform(0.1, 30, n)).astype(np.float32)
