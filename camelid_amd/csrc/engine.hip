@@ -6,7 +6,8 @@
 //   per layer: Wqkv (Q8R, rows nq+2*nkv), Wo (Q8R), Wgate|up (Q8R, rows 2F), Wdown (Q8R),
 //              attn/ffn norm [H], optional q/k norm [hd]
 //   lm_head Q8R [V][H], final norm [H], optional token_embd Q8R [V][H]
-//   KV cache f16: K [L][n_kv][kvs][hd], V transposed [L][n_kv][hd][kvs], kvs = max_pos
+//   KV cache: per (layer, kv head) regions of hd * kvs elements, K f16 as [hd/8][kvs][8] and
+//   V f16-rounded f32 as [kvs/4][hd][4] (cm::kv_k_index / cm::kv_v_index), kvs = max_pos
 //   rounded up to a multiple of 8 (16-byte aligned V rows)
 //   activations: h [H] (residual stream), qkv, att [nq], gu [2F], logits [V], one Q8_0
 //                activation buffer (quants + f32 scales) reused by every GEMV
@@ -65,8 +66,8 @@ struct camelid_hip_engine {
   bool out_set = false;
   Q8Mat embd;
   bool embd_set = false;
-  uint16_t* kc = nullptr;  // K [L][n_kv][kvs][hd]
-  uint16_t* vc = nullptr;  // V [L][n_kv][hd][kvs] (transposed)
+  uint16_t* kc = nullptr;  // K, granules of 8 dims per position (cm::kv_k_index)
+  float* vc = nullptr;     // V (f16-rounded f32), granules of 4 positions per dim (cm::kv_v_index)
   uint32_t kvs = 0;        // KV position stride: max_pos rounded up to a multiple of 8
   float *h = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr;
   float *logits = nullptr, *hidden_cap = nullptr, *xs = nullptr;
@@ -320,10 +321,10 @@ bool attention_hd_supported(uint32_t hd) { return hd == 64 || hd == 128 || hd ==
 template <bool FUSED>
 void launch_attention(uint32_t hd, uint32_t n_heads, size_t lds, hipStream_t s, const float* qsrc, int nh, int nkv,
                       int rope_dim, int split_half, const float* cb, const float* sb, int rs, const float* qn,
-                      const float* kn, float eps, uint16_t* kc, uint16_t* vc, int layer, int kvs, const uint32_t* pos,
+                      const float* kn, float eps, uint16_t* kc, float* vc, int layer, int kvs, const uint32_t* pos,
                       float scale, float* att, int8_t* xq, float* xs) {
 #define CM_ATT(HD)                                                                                                 \
-  hipLaunchKernelGGL((cm::k_attention<HD, FUSED>), dim3(n_heads), dim3(cm::ATT_NT), lds, s, qsrc, nh, nkv, rope_dim, \
+  hipLaunchKernelGGL((cm::k_attention<HD, FUSED>), dim3(n_heads), dim3(cm::att_nt(HD)), lds, s, qsrc, nh, nkv, rope_dim, \
                      split_half, cb, sb, rs, qn, kn, eps, kc, vc, layer, kvs, pos, scale, att, xq, xs)
   if (hd == 64) CM_ATT(64);
   else if (hd == 128) CM_ATT(128);
@@ -521,7 +522,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
     return fail(nullptr, m);
   }
   // A fresh cache reads as zeros (K/V past `filled` are never read); StepState starts at 0.
-  if (hipMemset(e->kc, 0, kv_elems * 2) != hipSuccess || hipMemset(e->vc, 0, kv_elems * 2) != hipSuccess ||
+  if (hipMemset(e->kc, 0, kv_elems * 2) != hipSuccess || hipMemset(e->vc, 0, kv_elems * 4) != hipSuccess ||
       hipMemset(e->st, 0, sizeof(cm::StepState)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
     camelid_hip_engine_free(e);
     return fail(nullptr, "initial device memset failed");
@@ -628,19 +629,21 @@ int camelid_hip_seed_layer(camelid_hip_engine* e, uint32_t layer, const float* c
   HIP_TRY(e, hipSetDevice(e->device));
   HIP_TRY(e, hipStreamSynchronize(e->stream));
   const camelid_hip_dims& d = e->d;
-  const size_t hd = d.head_dim, kvs = e->kvs;
-  std::vector<uint16_t> hk((size_t)n_pos * hd), hv(hd * kvs);
+  const int hd = (int)d.head_dim, kvs = (int)e->kvs;
+  std::vector<uint16_t> hk((size_t)hd * kvs);
+  std::vector<float> hv((size_t)hd * kvs);
   for (uint32_t h = 0; h < d.n_kv_heads; ++h) {
     const size_t src = (size_t)h * n_pos * hd;
-    const size_t base = ((size_t)layer * d.n_kv_heads + h) * kvs * hd;
-    HIP_TRY(e, hipMemcpy(hv.data(), e->vc + base, hv.size() * 2, hipMemcpyDeviceToHost));
-    for (size_t t = 0; t < n_pos; ++t)
-      for (size_t j = 0; j < hd; ++j) {
-        hk[t * hd + j] = cm::f32_to_f16_bits(ck[src + t * hd + j]);
-        hv[j * kvs + t] = cm::f32_to_f16_bits(cv[src + t * hd + j]);
+    const size_t base = cm::kv_head_base((int)layer, (int)d.n_kv_heads, (int)h, hd, kvs);
+    HIP_TRY(e, hipMemcpy(hk.data(), e->kc + base, hk.size() * 2, hipMemcpyDeviceToHost));
+    HIP_TRY(e, hipMemcpy(hv.data(), e->vc + base, hv.size() * 4, hipMemcpyDeviceToHost));
+    for (int t = 0; t < (int)n_pos; ++t)
+      for (int j = 0; j < hd; ++j) {
+        hk[cm::kv_k_index(kvs, t, j)] = cm::f32_to_f16_bits(ck[src + (size_t)t * hd + j]);
+        hv[cm::kv_v_index(hd, t, j)] = cm::f16_bits_to_f32(cm::f32_to_f16_bits(cv[src + (size_t)t * hd + j]));
       }
     HIP_TRY(e, hipMemcpy(e->kc + base, hk.data(), hk.size() * 2, hipMemcpyHostToDevice));
-    HIP_TRY(e, hipMemcpy(e->vc + base, hv.data(), hv.size() * 2, hipMemcpyHostToDevice));
+    HIP_TRY(e, hipMemcpy(e->vc + base, hv.data(), hv.size() * 4, hipMemcpyHostToDevice));
   }
   return 0;
 }
@@ -652,17 +655,18 @@ int camelid_hip_read_kv_layer(camelid_hip_engine* e, uint32_t layer, uint32_t n,
   HIP_TRY(e, hipSetDevice(e->device));
   HIP_TRY(e, hipStreamSynchronize(e->stream));
   const camelid_hip_dims& d = e->d;
-  const size_t hd = d.head_dim, kvs = e->kvs;
-  std::vector<uint16_t> hk((size_t)n * hd), hv(hd * kvs);
+  const int hd = (int)d.head_dim, kvs = (int)e->kvs;
+  std::vector<uint16_t> hk((size_t)hd * kvs);
+  std::vector<float> hv((size_t)hd * kvs);
   for (uint32_t h = 0; h < d.n_kv_heads; ++h) {
-    const size_t base = ((size_t)layer * d.n_kv_heads + h) * kvs * hd;
+    const size_t base = cm::kv_head_base((int)layer, (int)d.n_kv_heads, (int)h, hd, kvs);
     HIP_TRY(e, hipMemcpy(hk.data(), e->kc + base, hk.size() * 2, hipMemcpyDeviceToHost));
-    HIP_TRY(e, hipMemcpy(hv.data(), e->vc + base, hv.size() * 2, hipMemcpyDeviceToHost));
+    HIP_TRY(e, hipMemcpy(hv.data(), e->vc + base, hv.size() * 4, hipMemcpyDeviceToHost));
     const size_t dst = (size_t)h * n * hd;
-    for (size_t t = 0; t < n; ++t)
-      for (size_t j = 0; j < hd; ++j) {
-        ck[dst + t * hd + j] = cm::f16_bits_to_f32(hk[t * hd + j]);
-        cv[dst + t * hd + j] = cm::f16_bits_to_f32(hv[j * kvs + t]);
+    for (int t = 0; t < (int)n; ++t)
+      for (int j = 0; j < hd; ++j) {
+        ck[dst + (size_t)t * hd + j] = cm::f16_bits_to_f32(hk[cm::kv_k_index(kvs, t, j)]);
+        cv[dst + (size_t)t * hd + j] = hv[cm::kv_v_index(hd, t, j)];
       }
   }
   return 0;
@@ -956,7 +960,7 @@ int camelid_hip_silu_mul_quantize(const float* gu, uint32_t n, int8_t* xq, float
 
 int camelid_hip_rope_kv(const float* qkv, uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t rope_dim,
                         uint32_t split_half, const float* cos_tab, const float* sin_tab, const float* q_norm,
-                        const float* k_norm, float eps, float* qrot, uint16_t* kc, uint16_t* vc, uint32_t layer,
+                        const float* k_norm, float eps, float* qrot, uint16_t* kc, float* vc, uint32_t layer,
                         uint32_t max_pos, const uint32_t* d_pos, void* stream) {
   if (!qkv || !cos_tab || !sin_tab || !qrot || !kc || !vc || !d_pos) return fail(nullptr, "null argument");
   if (!n_heads || !n_kv || n_heads % n_kv || hd == 0 || hd > 512 || rope_dim > hd || rope_dim % 2)
@@ -967,7 +971,7 @@ int camelid_hip_rope_kv(const float* qkv, uint32_t n_heads, uint32_t n_kv, uint3
   return launch_status("rope_kv");
 }
 
-int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const uint16_t* vc, uint32_t layer,
+int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const float* vc, uint32_t layer,
                                  uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t max_pos, const uint32_t* d_pos,
                                  float scale, float* att_out, int8_t* xq, float* xs, void* stream) {
   if (!qrot || !kc || !vc || !d_pos || !att_out || !xq || !xs) return fail(nullptr, "null argument");
@@ -976,7 +980,7 @@ int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const ui
   if (attn_lds_bytes(max_pos) > 96 * 1024) return fail(nullptr, "max_pos too large for the decode attention");
   launch_attention<false>(hd, n_heads, attn_lds_bytes(max_pos), (hipStream_t)stream, qrot, (int)n_heads, (int)n_kv,
                           (int)hd, 0, nullptr, nullptr, 0, nullptr, nullptr, 0.0f, const_cast<uint16_t*>(kc),
-                          const_cast<uint16_t*>(vc), (int)layer, (int)max_pos, d_pos, scale, att_out, xq, xs);
+                          const_cast<float*>(vc), (int)layer, (int)max_pos, d_pos, scale, att_out, xq, xs);
   return launch_status("attention_decode");
 }
 

@@ -60,6 +60,8 @@ __device__ __forceinline__ float fold_lds(const float* p, int n, float acc = 0.0
     float4 a[8], b[8];
     load8(a, q);
     base = 8;
+    // not unrolled: a fully unrolled fold would hold every term in registers at once
+#pragma unroll 1
     for (; base + 16 <= g; base += 16) {
       load8(b, q + base);
       __builtin_amdgcn_sched_barrier(0);
@@ -280,30 +282,15 @@ __device__ __forceinline__ float inorder_sum_nonneg(const float* v, uint32_t* ps
   return sh_s;
 }
 
-// Compile-time length variant (N % 4 == 0): fully unrolled, same order.
+// Compile-time length variant (N % 4 == 0), same order.  The length is hidden from the
+// optimiser (an empty asm statement) so that the fold stays a loop instead of straight-line
+// code that hoists every term into registers (register count sets the workgroups per CU).
 template <int N>
 __device__ __forceinline__ float fold_lds_n(const float* p, float acc = 0.0f) {
   static_assert(N % 4 == 0, "fold length must be a multiple of 4");
-  constexpr int G = N / 4;
-  const float4* q = reinterpret_cast<const float4*>(p);
-  float4 a[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if (i < G) a[i] = q[i];
-#pragma unroll
-  for (int base = 0; base < G; base += 8) {
-    float4 b[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (base + 8 + i < G) b[i] = q[base + 8 + i];
-    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the add chain
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (base + i < G) add4(acc, a[i]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) a[i] = b[i];
-  }
-  return acc;
+  int n = N;
+  asm volatile("" : "+s"(n));
+  return fold_lds(p, n, acc);
 }
 
 // Lane-pair exchange (xor 1) through DPP quad_perm [1,0,3,2]; all lanes must be active.
@@ -403,6 +390,9 @@ __device__ __forceinline__ float gemv_rows_k(const int8_t* __restrict__ wq, cons
     float* tr = t + (wave * RPW + k) * STRIDE;
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
+      // one chunk at a time: keeps the activation reads from being hoisted into registers
+      // next to the in-flight weights (register count sets the workgroups per CU)
+      __builtin_amdgcn_sched_barrier(0);
       const int c = lane + 64 * i;
       const int cc = min(c, CPR - 1);
       int s = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
@@ -698,17 +688,36 @@ __global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------
+// KV cache layout.  Per layer and kv head a region of hd * kvs elements (kvs: the position
+// stride, a multiple of 8) at kv_head_base; inside it
+//   K (f16 bits): [hd/8][kvs][8]  -- 16-byte granule = 8 dims of one position,
+//   V (f32 holding f16-rounded values): [kvs/4][hd][4]  -- 16-byte granule = 4 positions
+//   of one dim,
+// so that lanes over consecutive positions (scores) or consecutive dims (the output sum)
+// read consecutive granules.  V is kept widened so that the output sum spends two VALU
+// operations (multiply, add) per position, which is what its serial add chain allows.
+__host__ __device__ __forceinline__ size_t kv_head_base(int layer, int n_kv, int kvh, int hd, int kvs) {
+  return ((size_t)layer * n_kv + kvh) * (size_t)hd * kvs;
+}
+__host__ __device__ __forceinline__ size_t kv_k_index(int kvs, int p, int d) {
+  return ((size_t)(d >> 3) * kvs + p) * 8 + (d & 7);
+}
+__host__ __device__ __forceinline__ size_t kv_v_index(int hd, int p, int d) {
+  return ((size_t)(p >> 2) * hd + d) * 4 + (p & 3);
+}
+
+// ---------------------------------------------------------------------------
 // Per-head QK RMSNorm (optional) + RoPE + f16 KV store for the token at st->pos (test
 // entry point; the engine fuses this into the attention kernel).  One workgroup per head:
 // blocks [0, n_heads) are Q heads, [n_heads, n_heads + n_kv) K heads (which also store the
-// head's V entries; V is stored transposed, [hd][max_pos]).  RoPE: rope.rs:489-524; f16
+// head's V entries).  Cache layout: kv_k_index / kv_v_index.  RoPE: rope.rs:489-524; f16
 // store: kv_cache.rs:573-600.
 __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, int n_heads, int n_kv, int hd,
                                                 int rope_dim, int split_half, const float* __restrict__ cosv,
                                                 const float* __restrict__ sinv, const float* __restrict__ q_norm,
                                                 const float* __restrict__ k_norm, float eps, float* __restrict__ qrot,
-                                                uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int layer,
-                                                int max_pos, const uint32_t* __restrict__ d_pos) {
+                                                uint16_t* __restrict__ kc, float* __restrict__ vc, int layer,
+                                                int kvs, const uint32_t* __restrict__ d_pos) {
   __shared__ __align__(16) float buf[512];
   __shared__ __align__(16) float sq[512];
   __shared__ float s_scale;
@@ -740,12 +749,12 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, i
     for (int d = threadIdx.x; d < hd; d += blockDim.x) qrot[(size_t)h * hd + d] = buf[d];
   } else {
     const int kvh = h - n_heads;
-    const size_t dst = (((size_t)layer * n_kv + kvh) * max_pos + *d_pos) * hd;         // K [pos][hd]
-    const size_t vdst = (((size_t)layer * n_kv + kvh) * hd) * max_pos + *d_pos;       // V [hd][max_pos]
+    const int pos = (int)*d_pos;
+    const size_t hbase = kv_head_base(layer, n_kv, kvh, hd, kvs);
     const float* vsrc = qkv + (size_t)(n_heads + n_kv) * hd + (size_t)kvh * hd;
     for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-      kc[dst + d] = f32_to_f16_bits(buf[d]);
-      vc[vdst + (size_t)d * max_pos] = f32_to_f16_bits(vsrc[d]);
+      kc[hbase + kv_k_index(kvs, pos, d)] = f32_to_f16_bits(buf[d]);
+      vc[hbase + kv_v_index(hd, pos, d)] = half_bits_to_float(f32_to_f16_bits(vsrc[d]));
     }
   }
 }
@@ -756,9 +765,11 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, i
 //   m = max_p score_p                          exact
 //   e_p = expf(score_p - m); sum = fold_p e_p  serial fold by one lane
 //   out_d = fold_p (e_p * (1/sum)) * v_pd      one lane per d, p in order
-// KV cache layout (per layer, per kv head): K rows [pos][HD] (a score lane streams one
-// contiguous 2*HD-byte row), V transposed [HD][max_pos] (an output lane streams its d's
-// values over positions, 8 per 16-byte load).
+// KV cache layout: kv_k_index / kv_v_index (16-byte granules; a wave's loads are contiguous
+// both for the score lanes, one position each, and for the output lanes, one d each).
+// Timeline: the score lanes issue their K loads first; lanes without a score position
+// touch the head's V granules so that they sit in L2 when the output lanes stream them;
+// the output lanes issue their first V loads before the softmax.
 // FUSED (the engine's path): the kernel first builds this token's q (and the kv head's k
 // and v) from the fused QKV projection: optional per-head QK RMSNorm (tensor/mod.rs:2112),
 // RoPE (rope.rs:489-524) with the tables at cos_base + pos*rope_stride, f16 rounding of k
@@ -766,18 +777,21 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, i
 // entries; every head of the group uses its own LDS copy of them for position pos.
 // Not FUSED (test entry point): q is taken from qsrc and K/V entirely from the cache.
 // The head's output is quantized to Q8_0 (HD % 32 == 0: blocks never straddle heads).
-// Dynamic LDS = align4(max_pos) * 4 bytes.
-constexpr int ATT_NT = 256;
+// kvs (the position stride) % 8 == 0.  Dynamic LDS = align4(kvs) * 4 bytes.
+// Threads per workgroup: 1024 (16 waves) up to head_dim 128; 512 for head_dim 256, whose
+// 512-byte K rows need twice the registers.
+__host__ __device__ constexpr int att_nt(int hd) { return hd <= 128 ? 1024 : 512; }
 
 template <int HD, bool FUSED>
-__global__ __launch_bounds__(ATT_NT) void k_attention(
+__global__ __launch_bounds__(att_nt(HD)) void k_attention(
     const float* __restrict__ qsrc, int n_heads, int n_kv, int rope_dim, int split_half,
     const float* __restrict__ cos_base, const float* __restrict__ sin_base, int rope_stride,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm, float eps, uint16_t* __restrict__ kc,
-    uint16_t* __restrict__ vc, int layer, int max_pos, const uint32_t* __restrict__ d_pos, float scale,
+    float* __restrict__ vc, int layer, int kvs, const uint32_t* __restrict__ d_pos, float scale,
     float* __restrict__ att_out, int8_t* __restrict__ xq, float* __restrict__ xs) {
-  static_assert(HD % 32 == 0 && HD <= ATT_NT, "head_dim must be a multiple of 32 and at most 256");
-  constexpr int R8 = HD / 8;  // 16-byte loads per K row
+  constexpr int ATT_NT = att_nt(HD);
+  static_assert(HD % 32 == 0 && HD <= 256, "head_dim must be a multiple of 32 and at most 256");
+  constexpr int R8 = HD / 8;  // 16-byte granules per K row
   extern __shared__ __align__(16) float sc[];
   __shared__ __align__(16) float qs[HD];
   __shared__ __align__(16) float kn[HD];  // this position's k (f16-rounded)
@@ -792,8 +806,19 @@ __global__ __launch_bounds__(ATT_NT) void k_attention(
   const int kvh = h / rep;
   const int pos = (int)*d_pos;
   const int P = pos + 1;
-  const size_t kbase = (((size_t)layer * n_kv + kvh) * max_pos) * HD;  // K [pos][HD]
-  const size_t vbase = (((size_t)layer * n_kv + kvh) * HD) * max_pos;  // V [HD][max_pos]
+  const int ncache = pos;
+  const size_t hbase = kv_head_base(layer, n_kv, kvh, HD, kvs);
+  const uint4* kg = reinterpret_cast<const uint4*>(kc + hbase);  // K granule (u, p): u * kvs + p
+  const float4* vg = reinterpret_cast<const float4*>(vc + hbase);  // V granule (g, d): g * HD + d
+
+  if (tid >= ncache) {
+    // no score position: touch the head's V granules (one load per 128-byte line) so the
+    // output lanes find them in L2
+    const int nlines = (ncache >> 2) * HD / 8;
+    float sink = 0.0f;
+    for (int i = tid - ncache; i < nlines; i += ATT_NT - ncache) sink += vg[(size_t)i * 8].x;
+    if (sink == 1.5f && scale == 0.0f) red[0] = 0.0f;  // keeps the loads (red is rewritten later)
+  }
 
   if (FUSED) {
     const float* q = qsrc + (size_t)h * HD;
@@ -842,15 +867,15 @@ __global__ __launch_bounds__(ATT_NT) void k_attention(
       kn[tid] = half_bits_to_float(kb);
       vn[tid] = half_bits_to_float(vb);
       if ((h % rep) == 0) {
-        kc[kbase + (size_t)pos * HD + tid] = kb;
-        vc[vbase + (size_t)tid * max_pos + pos] = vb;
+        kc[hbase + kv_k_index(kvs, pos, tid)] = kb;
+        vc[hbase + kv_v_index(HD, pos, tid)] = vn[tid];
       }
     }
   } else {
     if (tid < HD) {
       qs[tid] = qsrc[(size_t)h * HD + tid];
-      kn[tid] = half_bits_to_float(kc[kbase + (size_t)pos * HD + tid]);
-      vn[tid] = half_bits_to_float(vc[vbase + (size_t)tid * max_pos + pos]);
+      kn[tid] = half_bits_to_float(kc[hbase + kv_k_index(kvs, pos, tid)]);
+      vn[tid] = vc[hbase + kv_v_index(HD, pos, tid)];
     }
   }
   __syncthreads();
@@ -859,39 +884,32 @@ __global__ __launch_bounds__(ATT_NT) void k_attention(
     // inference.rs:23564-23575: a single position copies the V row.
     if (tid < HD) out[tid] = vn[tid];
   } else {
-    // ---- scores: cache positions 0..pos-1, one lane each, next row prefetched
+    // ---- scores: cache positions 0..pos-1, one lane each
     float lmax = -INFINITY;
-    const int ncache = pos;
-    {
-      const uint4* kr0 = reinterpret_cast<const uint4*>(kc + kbase);
-      uint4 cur[R8], nxt[R8];
-      int p = tid;
-      {
-        const int pc = min(p, ncache - 1);
+    for (int p = tid; p < ncache; p += ATT_NT) {
+      uint4 row[R8];
 #pragma unroll
-        for (int u = 0; u < R8; ++u) cur[u] = kr0[(size_t)pc * R8 + u];
-      }
-      for (; p < ncache; p += ATT_NT) {
-        const int pn = min(p + ATT_NT, ncache - 1);
+      for (int u = 0; u < R8; ++u) row[u] = kg[(size_t)u * kvs + p];
+      float acc = 0.0f;
 #pragma unroll
-        for (int u = 0; u < R8; ++u) nxt[u] = kr0[(size_t)pn * R8 + u];
+      for (int u = 0; u < R8; ++u) {
+        // q is read from LDS 8 values at a time (fencing the schedule keeps the whole of
+        // q from being hoisted into registers next to the in-flight row)
         __builtin_amdgcn_sched_barrier(0);
-        float acc = 0.0f;
-#pragma unroll
-        for (int u = 0; u < R8; ++u) {
-          const uint32_t wv[4] = {cur[u].x, cur[u].y, cur[u].z, cur[u].w};
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            acc += qs[u * 8 + 2 * j] * half_bits_to_float((uint16_t)(wv[j] & 0xffffu));
-            acc += qs[u * 8 + 2 * j + 1] * half_bits_to_float((uint16_t)(wv[j] >> 16));
-          }
-        }
-        const float sv = acc * scale;
-        sc[p] = sv;
-        lmax = fmaxf(lmax, sv);
-#pragma unroll
-        for (int u = 0; u < R8; ++u) cur[u] = nxt[u];
+        const float4 qa = reinterpret_cast<const float4*>(qs)[2 * u];
+        const float4 qb = reinterpret_cast<const float4*>(qs)[2 * u + 1];
+        acc += qa.x * half_bits_to_float((uint16_t)(row[u].x & 0xffffu));
+        acc += qa.y * half_bits_to_float((uint16_t)(row[u].x >> 16));
+        acc += qa.z * half_bits_to_float((uint16_t)(row[u].y & 0xffffu));
+        acc += qa.w * half_bits_to_float((uint16_t)(row[u].y >> 16));
+        acc += qb.x * half_bits_to_float((uint16_t)(row[u].z & 0xffffu));
+        acc += qb.y * half_bits_to_float((uint16_t)(row[u].z >> 16));
+        acc += qb.z * half_bits_to_float((uint16_t)(row[u].w & 0xffffu));
+        acc += qb.w * half_bits_to_float((uint16_t)(row[u].w >> 16));
       }
+      const float sv = acc * scale;
+      sc[p] = sv;
+      lmax = fmaxf(lmax, sv);
     }
     if (tid == (pos & (ATT_NT - 1))) {  // this token's own key, from LDS
       float acc = 0.0f;
@@ -902,6 +920,16 @@ __global__ __launch_bounds__(ATT_NT) void k_attention(
       lmax = fmaxf(lmax, sv);
     }
     const float mx = block_max(lmax, red);
+    // The output lanes start streaming their V granules now: the loads do not depend on
+    // the probabilities and land while the softmax below runs.
+    constexpr int VPF = HD <= 128 ? 12 : 8;  // granules (4 positions each) in flight per lane
+    const int ng = ncache >> 2;              // full groups of 4 cache positions
+    const float4* vd = vg + min(tid, HD - 1);
+    float4 vbuf[VPF];
+    if (tid < HD) {
+#pragma unroll
+      for (int u = 0; u < VPF; ++u) vbuf[u] = vd[(size_t)min(u, max(ng - 1, 0)) * HD];
+    }
     for (int p = tid; p < P; p += ATT_NT) sc[p] = glibc_expf(sc[p] - mx);
     __syncthreads();
     if (tid == 0) s_inv = 1.0f / fold_lds(sc, P);
@@ -909,45 +937,36 @@ __global__ __launch_bounds__(ATT_NT) void k_attention(
     const float inv = s_inv;
     for (int p = tid; p < P; p += ATT_NT) sc[p] = sc[p] * inv;
     __syncthreads();
-    // ---- out_d = fold_p prob_p * v_pd: lane d streams V^T row d, 8 positions per load,
-    // loads running 4 groups ahead.
+    // ---- out_d = fold_p prob_p * v_pd: lane d streams its granules, VPF ahead.
     if (tid < HD) {
-      const uint4* vrow = reinterpret_cast<const uint4*>(vc + vbase + (size_t)tid * max_pos);
-      const int ng = ncache >> 3;  // full groups of 8 cache positions
       float acc = 0.0f;
-      uint4 buf[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) buf[u] = vrow[min(u, max(ng - 1, 0))];
       int g = 0;
-      for (; g + 4 <= ng; g += 4) {
+      for (; g + VPF <= ng; g += VPF) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const uint4 cur = buf[u];
-          buf[u] = vrow[min(g + 4 + u, max(ng - 1, 0))];
+        for (int u = 0; u < VPF; ++u) {
+          const float4 cur = vbuf[u];
+          vbuf[u] = vd[(size_t)min(g + VPF + u, max(ng - 1, 0)) * HD];
           __builtin_amdgcn_sched_barrier(0);
-          const float4 pa = *reinterpret_cast<const float4*>(sc + (g + u) * 8);
-          const float4 pb = *reinterpret_cast<const float4*>(sc + (g + u) * 8 + 4);
-          acc += pa.x * half_bits_to_float((uint16_t)(cur.x & 0xffffu));
-          acc += pa.y * half_bits_to_float((uint16_t)(cur.x >> 16));
-          acc += pa.z * half_bits_to_float((uint16_t)(cur.y & 0xffffu));
-          acc += pa.w * half_bits_to_float((uint16_t)(cur.y >> 16));
-          acc += pb.x * half_bits_to_float((uint16_t)(cur.z & 0xffffu));
-          acc += pb.y * half_bits_to_float((uint16_t)(cur.z >> 16));
-          acc += pb.z * half_bits_to_float((uint16_t)(cur.w & 0xffffu));
-          acc += pb.w * half_bits_to_float((uint16_t)(cur.w >> 16));
+          const float4 pr = *reinterpret_cast<const float4*>(sc + (g + u) * 4);
+          acc += pr.x * cur.x;
+          acc += pr.y * cur.y;
+          acc += pr.z * cur.z;
+          acc += pr.w * cur.w;
         }
       }
-      for (; g < ng; ++g) {
-        const uint4 cur = vrow[g];
-        const uint32_t wv[4] = {cur.x, cur.y, cur.z, cur.w};
+      // the last (< VPF) full groups are already in vbuf[0 .. ng - g)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc += sc[g * 8 + 2 * j] * half_bits_to_float((uint16_t)(wv[j] & 0xffffu));
-          acc += sc[g * 8 + 2 * j + 1] * half_bits_to_float((uint16_t)(wv[j] >> 16));
+      for (int u = 0; u < VPF; ++u) {
+        if (g + u < ng) {
+          const float4 cur = vbuf[u];
+          const float4 pr = *reinterpret_cast<const float4*>(sc + (g + u) * 4);
+          acc += pr.x * cur.x;
+          acc += pr.y * cur.y;
+          acc += pr.z * cur.z;
+          acc += pr.w * cur.w;
         }
       }
-      const uint16_t* vs = vc + vbase + (size_t)tid * max_pos;
-      for (int p = ng * 8; p < ncache; ++p) acc += sc[p] * half_bits_to_float(vs[p]);
+      for (int p = ng * 4; p < ncache; ++p) acc += sc[p] * vc[hbase + kv_v_index(HD, p, tid)];
       acc += sc[pos] * vn[tid];
       out[tid] = acc;
     }

@@ -162,15 +162,19 @@ int camelid_hip_silu_mul_quantize(const float* gu, uint32_t n, int8_t* xq, float
                                   void* stream);
 /* rope_rotate + kv_scatter (cuda_resident.rs:1545, :1569; CPU rope.rs:489-524,
  * kv_cache.rs:573-600), with optional per-head QK RMSNorm (cuda_resident.rs:122).  Cache
- * layout: K [L][n_kv][max_pos][hd], V transposed [L][n_kv][hd][max_pos]. */
+ * layout: per (layer, kv head) a region of hd * max_pos elements at element offset
+ * (layer * n_kv + kv_head) * hd * max_pos; K holds f16 bits, element (p, d) at
+ * ((d / 8) * max_pos + p) * 8 + d % 8; V holds the f16-rounded values as f32, element (p, d)
+ * at ((p / 4) * hd + d) * 4 + p % 4 (16-byte granules: 8 dims of one position for K,
+ * 4 positions of one dim for V).  max_pos (the position stride) % 8 == 0. */
 int camelid_hip_rope_kv(const float* qkv, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
                         uint32_t rope_dim, uint32_t split_half, const float* cos_tab,
                         const float* sin_tab, const float* q_norm, const float* k_norm, float eps,
-                        float* qrot, uint16_t* kc, uint16_t* vc, uint32_t layer, uint32_t max_pos,
+                        float* qrot, uint16_t* kc, float* vc, uint32_t layer, uint32_t max_pos,
                         const uint32_t* d_pos, void* stream);
 /* attention_decode (cuda_resident.rs:1587; CPU inference.rs:23945-24025), faithful order.
  * Cache layout as camelid_hip_rope_kv; max_pos (the position stride) % 8 == 0; hd in {64,128,256}. */
-int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const uint16_t* vc,
+int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const float* vc,
                                  uint32_t layer, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
                                  uint32_t max_pos, const uint32_t* d_pos, float scale,
                                  float* att_out, int8_t* xq, float* xs, void* stream);
