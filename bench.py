@@ -154,7 +154,8 @@ def main() -> int:
         achieved = g["bytes"] / (g["ms"] * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                    "kernel": "k_q8_gemv (all Q8_0 GEMV launches of the timed steps, bytes-weighted)",
+                    "kernel": "Q8_0 GEMV: k_gemv_k + k_gemv_argmax, all launches of K steps "
+                              "(algorithmic bytes / summed dispatch durations)",
                     "avg_launch_us": round(g["ms"] * 1e3 / max(g["launches"], 1), 3),
                     "launches": g["launches"]}
         log("per-kernel (profiled pass): " + ", ".join(

@@ -20,6 +20,7 @@
 // The device-side loop captures one step in a HIP graph and replays it; the step reads
 // the token and position from StepState and the argmax advances them.
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -69,6 +70,7 @@ struct camelid_hip_engine {
   uint16_t* kc = nullptr;  // K, granules of 8 dims per position (cm::kv_k_index)
   float* vc = nullptr;     // V (f16-rounded f32), granules of 4 positions per dim (cm::kv_v_index)
   uint32_t kvs = 0;        // KV position stride: max_pos rounded up to a multiple of 8
+  int att_slots = 0;       // V ring chunks of the attention kernel
   float *h = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr;
   float *logits = nullptr, *hidden_cap = nullptr, *xs = nullptr;
   float *cos_cur = nullptr, *sin_cur = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
@@ -229,28 +231,44 @@ hipEvent_t next_event(camelid_hip_engine* e) {
   return e->event_pool[e->pool_next++];
 }
 
-// Brackets one launch with events when profiling; `bytes` = algorithmic bytes of the launch.
+// Profiling: while a ProfScope is open on the calling thread, each engine launch goes out
+// through hipExtLaunchKernelGGL with a start/stop event pair, which the runtime stamps at
+// the dispatch's own begin and end (the kernel's duration, as a kernel trace reports it).
+// The scope's algorithmic bytes are credited to its first launch.
+struct ProfScope;
+thread_local ProfScope* g_prof = nullptr;
+
 struct ProfScope {
   camelid_hip_engine* e;
   int cat;
   double bytes;
-  hipEvent_t a = nullptr;
+  bool first = true;
   ProfScope(camelid_hip_engine* eng, int c, double b) : e(eng), cat(c), bytes(b) {
-    if (e->profiling) {
-      a = next_event(e);
-      if (a) (void)hipEventRecord(a, e->stream);
-    }
+    if (e->profiling) g_prof = this;
   }
   ~ProfScope() {
-    if (a) {
-      hipEvent_t b = next_event(e);
-      if (b) {
-        (void)hipEventRecord(b, e->stream);
-        e->recs.push_back({cat, bytes, a, b});
-      }
-    }
+    if (g_prof == this) g_prof = nullptr;
+  }
+  // Event pair for the next launch of this scope (false when none can be created).
+  bool take(hipEvent_t* a, hipEvent_t* b) {
+    *a = next_event(e);
+    *b = *a ? next_event(e) : nullptr;
+    if (!*b) return false;
+    e->recs.push_back({cat, first ? bytes : 0.0, *a, *b});
+    first = false;
+    return true;
   }
 };
+
+// Launch through the profiler when a scope is open, plainly otherwise.
+#define CM_LAUNCH(K, G, B, S, STREAM, ...)                                                 \
+  do {                                                                                    \
+    hipEvent_t cm_a_, cm_b_;                                                              \
+    if (g_prof && g_prof->take(&cm_a_, &cm_b_))                                           \
+      hipExtLaunchKernelGGL(K, G, B, S, STREAM, cm_a_, cm_b_, 0, __VA_ARGS__);            \
+    else                                                                                  \
+      hipLaunchKernelGGL(K, G, B, S, STREAM, __VA_ARGS__);                        \
+  } while (0)
 
 // Algorithmic bytes of one Q8_0 GEMV launch: weights (34 B per 32 values), the quantized
 // activation, the f32 output (+ the residual read when fused).
@@ -277,16 +295,16 @@ void launch_gemv(const Q8Mat& m, const int8_t* xq, const float* xs, float* y, co
 #define CM_GEMV_CASE(K)                                                                                             \
   case K:                                                                                                           \
     if (cm::gemv_rpw(K, (int)m.rows) == 2)                                                                          \
-      hipLaunchKernelGGL((cm::k_gemv_k<K, 2>), dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, xq, xs, y, \
+      CM_LAUNCH((cm::k_gemv_k<K, 2>), dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, xq, xs, y, \
                          resid);                                                                                    \
     else                                                                                                            \
-      hipLaunchKernelGGL((cm::k_gemv_k<K, 1>), dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, xq, xs, y, \
+      CM_LAUNCH((cm::k_gemv_k<K, 1>), dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, xq, xs, y, \
                          resid);                                                                                    \
     return;
     CM_GEMV_KS(CM_GEMV_CASE)
 #undef CM_GEMV_CASE
     default:
-      hipLaunchKernelGGL(cm::k_gemv, dim3(grid), dim3(cm::GEMV_NT), cm::gemv_lds_bytes((int)m.k), s, m.q, m.d,
+      CM_LAUNCH(cm::k_gemv, dim3(grid), dim3(cm::GEMV_NT), cm::gemv_lds_bytes((int)m.k), s, m.q, m.d,
                          (int)m.rows, (int)m.k, xq, xs, y, resid);
   }
 }
@@ -300,16 +318,16 @@ uint32_t launch_gemv_argmax(const Q8Mat& m, const int8_t* xq, const float* xs, f
 #define CM_GEMV_CASE(K)                                                                                               \
   case K:                                                                                                             \
     if (cm::gemv_rpw(K, (int)m.rows) == 2)                                                                            \
-      hipLaunchKernelGGL((cm::k_gemv_argmax<K, 2>), dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, K, xq, \
+      CM_LAUNCH((cm::k_gemv_argmax<K, 2>), dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, K, xq, \
                          xs, logits, part_v, part_i);                                                                 \
     else                                                                                                              \
-      hipLaunchKernelGGL((cm::k_gemv_argmax<K, 1>), dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, K, xq, \
+      CM_LAUNCH((cm::k_gemv_argmax<K, 1>), dim3(grid), dim3(cm::GEMV_NT), 0, s, m.q, m.d, (int)m.rows, K, xq, \
                          xs, logits, part_v, part_i);                                                                 \
     return grid;
     CM_GEMV_KS(CM_GEMV_CASE)
 #undef CM_GEMV_CASE
     default:
-      hipLaunchKernelGGL((cm::k_gemv_argmax<0, 1>), dim3(grid), dim3(cm::GEMV_NT), cm::gemv_lds_bytes((int)m.k), s,
+      CM_LAUNCH((cm::k_gemv_argmax<0, 1>), dim3(grid), dim3(cm::GEMV_NT), cm::gemv_lds_bytes((int)m.k), s,
                          m.q, m.d, (int)m.rows, (int)m.k, xq, xs, logits, part_v, part_i);
       return grid;
   }
@@ -318,14 +336,19 @@ uint32_t launch_gemv_argmax(const Q8Mat& m, const int8_t* xq, const float* xs, f
 // Attention launch for the supported head widths.
 bool attention_hd_supported(uint32_t hd) { return hd == 64 || hd == 128 || hd == 256; }
 
+size_t attn_sc_bytes(uint32_t kvs) { return (((size_t)kvs + 3) & ~(size_t)3) * 4; }
+int attn_ring_slots(uint32_t kvs);
+
 template <bool FUSED>
-void launch_attention(uint32_t hd, uint32_t n_heads, size_t lds, hipStream_t s, const float* qsrc, int nh, int nkv,
+void launch_attention(uint32_t hd, uint32_t n_heads, int slots, hipStream_t s, const float* qsrc, int nh, int nkv,
                       int rope_dim, int split_half, const float* cb, const float* sb, int rs, const float* qn,
                       const float* kn, float eps, uint16_t* kc, float* vc, int layer, int kvs, const uint32_t* pos,
                       float scale, float* att, int8_t* xq, float* xs) {
-#define CM_ATT(HD)                                                                                                 \
-  hipLaunchKernelGGL((cm::k_attention<HD, FUSED>), dim3(n_heads), dim3(cm::att_nt(HD)), lds, s, qsrc, nh, nkv, rope_dim, \
-                     split_half, cb, sb, rs, qn, kn, eps, kc, vc, layer, kvs, pos, scale, att, xq, xs)
+  const size_t lds = (size_t)slots * cm::ATT_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs);
+#define CM_ATT(HD)                                                                                                  \
+  CM_LAUNCH((cm::k_attention<HD, FUSED>), dim3(n_heads), dim3(cm::att_nt(HD)), lds, s, qsrc, nh, nkv,  \
+                     rope_dim, split_half, cb, sb, rs, qn, kn, eps, kc, vc, layer, kvs, pos, scale, att, xq, xs, \
+                     slots)
   if (hd == 64) CM_ATT(64);
   else if (hd == 128) CM_ATT(128);
   else CM_ATT(256);
@@ -337,14 +360,27 @@ void launch_rmsnorm_quant(const float* x, const float* w, uint32_t n, float eps,
   switch (cm::seg_chunk((int)n)) {
 #define CM_RMS(C)                                                                                         \
   case C:                                                                                                 \
-    hipLaunchKernelGGL(cm::k_rmsnorm_quant<C>, dim3(1), dim3(cm::RMS_NT), 0, s, x, w, (int)n, eps, xq, xs, y); \
+    CM_LAUNCH(cm::k_rmsnorm_quant<C>, dim3(1), dim3(cm::RMS_NT), 0, s, x, w, (int)n, eps, xq, xs, y); \
     break;
     CM_SEG_CHUNKS(CM_RMS)
 #undef CM_RMS
   }
 }
 
-size_t attn_lds_bytes(uint32_t max_pos) { return (((size_t)max_pos + 3) & ~(size_t)3) * 4; }
+// LDS of the attention kernel: the score vector (align4(kvs) floats) plus a V ring of 2..4
+// chunks of 32 KB; 0 when even two chunks do not fit beside the scores.
+int attn_ring_slots(uint32_t kvs) {
+  static int limit = -1;
+  if (limit < 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      v = 65536;
+    limit = v;
+  }
+  const long room = (long)limit - (long)cm::att_static_lds_max() - (long)attn_sc_bytes(kvs);
+  const long slots = std::min<long>(4, room / (cm::ATT_RING_GRANULES * 16));
+  return slots >= 2 ? (int)slots : 0;
+}
 
 void gemv(camelid_hip_engine* e, const Q8Mat& m, float* y, const float* resid) {
   ProfScope ps(e, P_GEMV, q8_bytes(m, resid != nullptr));
@@ -368,7 +404,7 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const f
   gemv(e, L.qkv, e->qkv, nullptr);
   {
     ProfScope ps(e, P_ATTN, (nq + 2 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0));
-    launch_attention<true>(d.head_dim, d.n_heads, attn_lds_bytes(d.max_pos), s, e->qkv, (int)d.n_heads,
+    launch_attention<true>(d.head_dim, d.n_heads, e->att_slots, s, e->qkv, (int)d.n_heads,
                            (int)d.n_kv_heads, (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base,
                            rope_stride, L.q_norm, L.k_norm, d.eps, e->kc, e->vc, (int)l, (int)e->kvs, &e->st->pos,
                            scale, e->att, e->xq, e->xs);
@@ -378,7 +414,7 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const f
   gemv(e, L.gu, e->gu, nullptr);
   {
     ProfScope ps(e, P_SILU, d.ffn_dim * 8.0 + d.ffn_dim * 34.0 / 32.0);
-    hipLaunchKernelGGL(cm::k_silu_mul_quant, dim3((d.ffn_dim + 255) / 256), dim3(256), 0, s, e->gu, (int)d.ffn_dim,
+    CM_LAUNCH(cm::k_silu_mul_quant, dim3((d.ffn_dim + 255) / 256), dim3(256), 0, s, e->gu, (int)d.ffn_dim,
                        e->xq, e->xs, nullptr);
   }
   gemv(e, L.down, e->h, e->h);
@@ -401,16 +437,20 @@ void run_stack(camelid_hip_engine* e, const float* cos_base, const float* sin_ba
 void run_head(camelid_hip_engine* e, uint32_t* tokens, uint32_t cap) {
   rmsnorm(e, e->out_norm);
   const Q8Mat& m = e->out;
-  ProfScope ps(e, P_GEMV, q8_bytes(m, false));
-  const uint32_t nparts = launch_gemv_argmax(m, e->xq, e->xs, e->logits, e->part_v, e->part_i, e->stream);
-  hipLaunchKernelGGL(cm::k_argmax_finish, dim3(1), dim3(1024), 0, e->stream, e->part_v, e->part_i, (int)nparts, e->st,
+  uint32_t nparts;
+  {
+    ProfScope ps(e, P_GEMV, q8_bytes(m, false));
+    nparts = launch_gemv_argmax(m, e->xq, e->xs, e->logits, e->part_v, e->part_i, e->stream);
+  }
+  ProfScope ps(e, P_HEAD, 0.0);
+  CM_LAUNCH(cm::k_argmax_finish, dim3(1), dim3(1024), 0, e->stream, e->part_v, e->part_i, (int)nparts, e->st,
                      tokens, cap);
 }
 
 void run_embed(camelid_hip_engine* e) {
   const camelid_hip_dims& d = e->d;
   ProfScope ps(e, P_EMBED, d.hidden * (34.0 / 32.0 + 4.0));
-  hipLaunchKernelGGL(cm::k_embed_q8, dim3((d.hidden + 255) / 256), dim3(256), 0, e->stream, e->embd.q, e->embd.d,
+  CM_LAUNCH(cm::k_embed_q8, dim3((d.hidden + 255) / 256), dim3(256), 0, e->stream, e->embd.q, e->embd.d,
                      (int)d.hidden, e->st, e->h);
 }
 
@@ -480,7 +520,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   if (d.hidden > (uint32_t)cm::SEG_MAX_N) return fail(nullptr, "hidden > 16384 is not supported by the RMSNorm kernel");
   if (d.rope_dim == 0 || d.rope_dim > d.head_dim || d.rope_dim % 2)
     return fail(nullptr, "rope_dim must be even and within head_dim");
-  if (attn_lds_bytes(d.max_pos) > 96 * 1024) return fail(nullptr, "max_pos too large for the decode attention");
+  if (attn_ring_slots((d.max_pos + 7u) & ~7u) == 0) return fail(nullptr, "max_pos too large for the decode attention");
   if (cm::gemv_lds_bytes((int)std::max(d.ffn_dim, d.n_heads * d.head_dim)) > 64 * 1024)
     return fail(nullptr, "row width too large for the GEMV");
   auto* e = new camelid_hip_engine();
@@ -501,6 +541,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   }
   e->layers.resize(d.n_layers);
   e->kvs = (d.max_pos + 7u) & ~7u;
+  e->att_slots = attn_ring_slots(e->kvs);
   const size_t nq = (size_t)d.n_heads * d.head_dim, nkv = (size_t)d.n_kv_heads * d.head_dim;
   const size_t kv_elems = (size_t)d.n_layers * d.n_kv_heads * e->kvs * d.head_dim;
   const size_t act = std::max<size_t>({(size_t)d.hidden, (size_t)d.ffn_dim, nq});
@@ -977,8 +1018,9 @@ int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const fl
   if (!qrot || !kc || !vc || !d_pos || !att_out || !xq || !xs) return fail(nullptr, "null argument");
   if (!n_heads || !n_kv || n_heads % n_kv || !attention_hd_supported(hd)) return fail(nullptr, "invalid head geometry");
   if (max_pos % 8) return fail(nullptr, "the KV position stride (max_pos) must be a multiple of 8");
-  if (attn_lds_bytes(max_pos) > 96 * 1024) return fail(nullptr, "max_pos too large for the decode attention");
-  launch_attention<false>(hd, n_heads, attn_lds_bytes(max_pos), (hipStream_t)stream, qrot, (int)n_heads, (int)n_kv,
+  const int slots = attn_ring_slots(max_pos);
+  if (slots == 0) return fail(nullptr, "max_pos too large for the decode attention");
+  launch_attention<false>(hd, n_heads, slots, (hipStream_t)stream, qrot, (int)n_heads, (int)n_kv,
                           (int)hd, 0, nullptr, nullptr, 0, nullptr, nullptr, 0.0f, const_cast<uint16_t*>(kc),
                           const_cast<float*>(vc), (int)layer, (int)max_pos, d_pos, scale, att_out, xq, xs);
   return launch_status("attention_decode");

@@ -767,9 +767,9 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, i
 //   out_d = fold_p (e_p * (1/sum)) * v_pd      one lane per d, p in order
 // KV cache layout: kv_k_index / kv_v_index (16-byte granules; a wave's loads are contiguous
 // both for the score lanes, one position each, and for the output lanes, one d each).
-// Timeline: the score lanes issue their K loads first; lanes without a score position
-// touch the head's V granules so that they sit in L2 when the output lanes stream them;
-// the output lanes issue their first V loads before the softmax.
+// V for the output sum goes through an LDS ring (ring_slots chunks of 32 KB, filled by
+// staging waves with direct global->LDS loads, the first ring_slots-1 chunks issued before
+// the softmax); the output lanes read granules from LDS, two VALU operations per position.
 // FUSED (the engine's path): the kernel first builds this token's q (and the kv head's k
 // and v) from the fused QKV projection: optional per-head QK RMSNorm (tensor/mod.rs:2112),
 // RoPE (rope.rs:489-524) with the tables at cos_base + pos*rope_stride, f16 rounding of k
@@ -777,10 +777,34 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, i
 // entries; every head of the group uses its own LDS copy of them for position pos.
 // Not FUSED (test entry point): q is taken from qsrc and K/V entirely from the cache.
 // The head's output is quantized to Q8_0 (HD % 32 == 0: blocks never straddle heads).
-// kvs (the position stride) % 8 == 0.  Dynamic LDS = align4(kvs) * 4 bytes.
+// kvs (the position stride) % 8 == 0.  Dynamic LDS = ring_slots * 32 KB + align4(kvs) * 4 bytes,
+// ring_slots >= 2.
 // Threads per workgroup: 1024 (16 waves) up to head_dim 128; 512 for head_dim 256, whose
 // 512-byte K rows need twice the registers.
 __host__ __device__ constexpr int att_nt(int hd) { return hd <= 128 ? 1024 : 512; }
+
+// V staging ring: chunks of 32 KB (2048 16-byte granules), 32 wave-loads of 1 KB each.
+constexpr int ATT_RING_GRANULES = 2048;
+constexpr int ATT_RING_LOADS = 32;
+__host__ __device__ constexpr size_t att_static_lds_max() { return 8192; }  // bound on the kernel's static LDS
+
+// Waits until at most n of this wave's vector memory operations are outstanding (gfx9
+// s_waitcnt encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+#define CM_VMW(N)                                                                          \
+  case N:                                                                                  \
+    __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8)); \
+    break;
+  switch (n) {
+    CM_VMW(0) CM_VMW(1) CM_VMW(2) CM_VMW(3) CM_VMW(4) CM_VMW(5) CM_VMW(6) CM_VMW(7)
+    CM_VMW(8) CM_VMW(9) CM_VMW(10) CM_VMW(11) CM_VMW(12) CM_VMW(13) CM_VMW(14) CM_VMW(15)
+    CM_VMW(16) CM_VMW(17) CM_VMW(18) CM_VMW(19) CM_VMW(20) CM_VMW(21) CM_VMW(22) CM_VMW(23)
+    CM_VMW(24)
+    default:
+      __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+  }
+#undef CM_VMW
+}
 
 template <int HD, bool FUSED>
 __global__ __launch_bounds__(att_nt(HD)) void k_attention(
@@ -788,11 +812,18 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
     const float* __restrict__ cos_base, const float* __restrict__ sin_base, int rope_stride,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm, float eps, uint16_t* __restrict__ kc,
     float* __restrict__ vc, int layer, int kvs, const uint32_t* __restrict__ d_pos, float scale,
-    float* __restrict__ att_out, int8_t* __restrict__ xq, float* __restrict__ xs) {
+    float* __restrict__ att_out, int8_t* __restrict__ xq, float* __restrict__ xs, int ring_slots) {
   constexpr int ATT_NT = att_nt(HD);
-  static_assert(HD % 32 == 0 && HD <= 256, "head_dim must be a multiple of 32 and at most 256");
+  static_assert(HD % 64 == 0 && HD <= 256, "head_dim must be 64, 128 or 256");
   constexpr int R8 = HD / 8;  // 16-byte granules per K row
-  extern __shared__ __align__(16) float sc[];
+  constexpr int NW = ATT_NT / 64;
+  constexpr int CW = HD / 64;                        // output waves: one lane per dim
+  constexpr int NH = (NW - CW) >= 8 ? 8 : 4;         // V-staging waves (divides the 32 loads)
+  constexpr int LH = ATT_RING_LOADS / NH;            // 1 KB wave loads per staging wave per chunk
+  constexpr int CG = ATT_RING_GRANULES / HD;         // 4-position groups per ring chunk
+  extern __shared__ __align__(16) float4 dyn[];
+  float4* ring = dyn;  // ring_slots chunks of ATT_RING_GRANULES V granules
+  float* sc = reinterpret_cast<float*>(dyn + (size_t)ring_slots * ATT_RING_GRANULES);
   __shared__ __align__(16) float qs[HD];
   __shared__ __align__(16) float kn[HD];  // this position's k (f16-rounded)
   __shared__ __align__(16) float vn[HD];  // this position's v (f16-rounded)
@@ -810,15 +841,6 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   const size_t hbase = kv_head_base(layer, n_kv, kvh, HD, kvs);
   const uint4* kg = reinterpret_cast<const uint4*>(kc + hbase);  // K granule (u, p): u * kvs + p
   const float4* vg = reinterpret_cast<const float4*>(vc + hbase);  // V granule (g, d): g * HD + d
-
-  if (tid >= ncache) {
-    // no score position: touch the head's V granules (one load per 128-byte line) so the
-    // output lanes find them in L2
-    const int nlines = (ncache >> 2) * HD / 8;
-    float sink = 0.0f;
-    for (int i = tid - ncache; i < nlines; i += ATT_NT - ncache) sink += vg[(size_t)i * 8].x;
-    if (sink == 1.5f && scale == 0.0f) red[0] = 0.0f;  // keeps the loads (red is rewritten later)
-  }
 
   if (FUSED) {
     const float* q = qsrc + (size_t)h * HD;
@@ -920,52 +942,89 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
       lmax = fmaxf(lmax, sv);
     }
     const float mx = block_max(lmax, red);
-    // The output lanes start streaming their V granules now: the loads do not depend on
-    // the probabilities and land while the softmax below runs.
-    constexpr int VPF = HD <= 128 ? 12 : 8;  // granules (4 positions each) in flight per lane
-    const int ng = ncache >> 2;              // full groups of 4 cache positions
-    const float4* vd = vg + min(tid, HD - 1);
-    float4 vbuf[VPF];
-    if (tid < HD) {
+    // V staging: the cache positions' V granules (full 4-position groups) are copied into
+    // an LDS ring of ring_slots chunks by NH staging waves with direct global->LDS loads;
+    // the output lanes read them from LDS.  A chunk is contiguous in the cache layout.
+    const int ng = ncache >> 2;  // full groups of 4 cache positions
+    const int nchunks = (ng + CG - 1) / CG;
+    const int R = ring_slots;
+    const int hw = (tid >> 6) - CW;
+    const bool stager = hw >= 0 && hw < NH;
+    const size_t last_granule = (size_t)max(ng, 1) * HD - 1;
+    auto stage = [&](int c) {  // chunk c into slot c % R
+      float4* slot = ring + (size_t)(c % R) * ATT_RING_GRANULES;
 #pragma unroll
-      for (int u = 0; u < VPF; ++u) vbuf[u] = vd[(size_t)min(u, max(ng - 1, 0)) * HD];
-    }
+      for (int j = 0; j < LH; ++j) {
+        const int i = hw + NH * j;  // 1 KB piece of the chunk
+        const size_t gsrc = min((size_t)c * ATT_RING_GRANULES + (size_t)i * 64 + (tid & 63), last_granule);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(vg + gsrc),
+                                         (__attribute__((address_space(3))) void*)(slot + i * 64), 16, 0, 0);
+      }
+    };
     for (int p = tid; p < P; p += ATT_NT) sc[p] = glibc_expf(sc[p] - mx);
+    if (stager) {  // after the exponentials, whose table loads would otherwise queue behind
+      for (int c = 0; c < min(R - 1, nchunks); ++c) stage(c);
+    }
     __syncthreads();
     if (tid == 0) s_inv = 1.0f / fold_lds(sc, P);
     __syncthreads();
     const float inv = s_inv;
     for (int p = tid; p < P; p += ATT_NT) sc[p] = sc[p] * inv;
-    __syncthreads();
-    // ---- out_d = fold_p prob_p * v_pd: lane d streams its granules, VPF ahead.
+    // ---- out_d = fold_p prob_p * v_pd: lane d walks the ring chunk by chunk.
+    float acc = 0.0f;
+    for (int c = 0; c < nchunks; ++c) {
+      if (stager) wait_vmcnt(LH * (min(c + R - 2, nchunks - 1) - c));  // chunk c has landed
+      __syncthreads();  // chunk c visible; the slot of chunk c - 1 is free
+      if (stager && c + R - 1 < nchunks) stage(c + R - 1);
+      if (tid < HD) {
+        const float4* slot = ring + (size_t)(c % R) * ATT_RING_GRANULES + tid;
+        const float4* pr4 = reinterpret_cast<const float4*>(sc) + (size_t)c * CG;
+        const int gn = min(CG, ng - c * CG);
+        if (gn == CG) {
+          // LDS reads ping-pong between two batches of 4 granules (16 positions) so that
+          // the add chain never waits on LDS latency
+          static_assert(CG % 8 == 0, "ring chunks hold a multiple of 8 groups");
+          float4 va[4], pa[4], vb[4], pb[4];
+          auto ld = [&](float4(&v)[4], float4(&pq)[4], int j0) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              v[u] = slot[(j0 + u) * HD];
+              pq[u] = pr4[j0 + u];
+            }
+          };
+          auto mac = [&](const float4(&v)[4], const float4(&pq)[4]) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              acc += pq[u].x * v[u].x;
+              acc += pq[u].y * v[u].y;
+              acc += pq[u].z * v[u].z;
+              acc += pq[u].w * v[u].w;
+            }
+          };
+          ld(va, pa, 0);
+#pragma unroll
+          for (int j = 0; j < CG; j += 8) {
+            ld(vb, pb, j + 4);
+            __builtin_amdgcn_sched_barrier(0);
+            mac(va, pa);
+            if (j + 8 < CG) ld(va, pa, j + 8);
+            __builtin_amdgcn_sched_barrier(0);
+            mac(vb, pb);
+          }
+        } else {
+          for (int j = 0; j < gn; ++j) {
+            const float4 v = slot[j * HD];
+            const float4 pr = pr4[j];
+            acc += pr.x * v.x;
+            acc += pr.y * v.y;
+            acc += pr.z * v.z;
+            acc += pr.w * v.w;
+          }
+        }
+      }
+    }
+    __syncthreads();  // the normalised probabilities past the ring (and with no chunks at all)
     if (tid < HD) {
-      float acc = 0.0f;
-      int g = 0;
-      for (; g + VPF <= ng; g += VPF) {
-#pragma unroll
-        for (int u = 0; u < VPF; ++u) {
-          const float4 cur = vbuf[u];
-          vbuf[u] = vd[(size_t)min(g + VPF + u, max(ng - 1, 0)) * HD];
-          __builtin_amdgcn_sched_barrier(0);
-          const float4 pr = *reinterpret_cast<const float4*>(sc + (g + u) * 4);
-          acc += pr.x * cur.x;
-          acc += pr.y * cur.y;
-          acc += pr.z * cur.z;
-          acc += pr.w * cur.w;
-        }
-      }
-      // the last (< VPF) full groups are already in vbuf[0 .. ng - g)
-#pragma unroll
-      for (int u = 0; u < VPF; ++u) {
-        if (g + u < ng) {
-          const float4 cur = vbuf[u];
-          const float4 pr = *reinterpret_cast<const float4*>(sc + (g + u) * 4);
-          acc += pr.x * cur.x;
-          acc += pr.y * cur.y;
-          acc += pr.z * cur.z;
-          acc += pr.w * cur.w;
-        }
-      }
       for (int p = ng * 4; p < ncache; ++p) acc += sc[p] * vc[hbase + kv_v_index(HD, p, tid)];
       acc += sc[pos] * vn[tid];
       out[tid] = acc;
