@@ -71,6 +71,7 @@ struct camelid_hip_engine {
   float* vc = nullptr;     // V (f16-rounded f32), granules of 4 positions per dim (cm::kv_v_index)
   uint32_t kvs = 0;        // KV position stride: max_pos rounded up to a multiple of 8
   int att_slots = 0;       // V ring chunks of the attention kernel
+  bool read_ahead = true;  // spare workgroups of the norm kernels read ahead the next weights
   float *h = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr;
   float *logits = nullptr, *hidden_cap = nullptr, *xs = nullptr;
   float *cos_cur = nullptr, *sin_cur = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
@@ -336,6 +337,19 @@ uint32_t launch_gemv_argmax(const Q8Mat& m, const int8_t* xq, const float* xs, f
 // Attention launch for the supported head widths.
 bool attention_hd_supported(uint32_t hd) { return hd == 64 || hd == 128 || hd == 256; }
 
+// Read-ahead descriptor of a Q8R matrix (quants and scales, in 128-byte lines).
+cm::Prefetch prefetch_of(const Q8Mat* m) {
+  cm::Prefetch pf{nullptr, 0, nullptr, 0};
+  if (m && m->q) {
+    pf.a = reinterpret_cast<const uint32_t*>(m->q);
+    pf.a_lines = (size_t)m->rows * m->k / 128;
+    pf.b = reinterpret_cast<const uint32_t*>(m->d);
+    pf.b_lines = (size_t)m->rows * (m->k / 32) * 2 / 128;
+  }
+  return pf;
+}
+constexpr uint32_t PREFETCH_WGS = 256;  // spare workgroups added to a kernel that reads ahead
+
 size_t attn_sc_bytes(uint32_t kvs) { return (((size_t)kvs + 3) & ~(size_t)3) * 4; }
 int attn_ring_slots(uint32_t kvs);
 
@@ -343,12 +357,14 @@ template <bool FUSED>
 void launch_attention(uint32_t hd, uint32_t n_heads, int slots, hipStream_t s, const float* qsrc, int nh, int nkv,
                       int rope_dim, int split_half, const float* cb, const float* sb, int rs, const float* qn,
                       const float* kn, float eps, uint16_t* kc, float* vc, int layer, int kvs, const uint32_t* pos,
-                      float scale, float* att, int8_t* xq, float* xs) {
+                      float scale, float* att, int8_t* xq, float* xs, const Q8Mat* next = nullptr) {
   const size_t lds = (size_t)slots * cm::ATT_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs);
+  const cm::Prefetch pf = prefetch_of(next);
+  const uint32_t grid = n_heads + (pf.a_lines ? PREFETCH_WGS : 0);
 #define CM_ATT(HD)                                                                                                  \
-  CM_LAUNCH((cm::k_attention<HD, FUSED>), dim3(n_heads), dim3(cm::att_nt(HD)), lds, s, qsrc, nh, nkv,  \
+  CM_LAUNCH((cm::k_attention<HD, FUSED>), dim3(grid), dim3(cm::att_nt(HD)), lds, s, qsrc, nh, nkv,  \
                      rope_dim, split_half, cb, sb, rs, qn, kn, eps, kc, vc, layer, kvs, pos, scale, att, xq, xs, \
-                     slots)
+                     slots, pf)
   if (hd == 64) CM_ATT(64);
   else if (hd == 128) CM_ATT(128);
   else CM_ATT(256);
@@ -356,11 +372,13 @@ void launch_attention(uint32_t hd, uint32_t n_heads, int slots, hipStream_t s, c
 }
 
 void launch_rmsnorm_quant(const float* x, const float* w, uint32_t n, float eps, int8_t* xq, float* xs, float* y,
-                          hipStream_t s) {
+                          hipStream_t s, const Q8Mat* next = nullptr) {
+  const cm::Prefetch pf = prefetch_of(next);
+  const uint32_t grid = 1 + (pf.a_lines ? PREFETCH_WGS : 0);
   switch (cm::seg_chunk((int)n)) {
-#define CM_RMS(C)                                                                                         \
-  case C:                                                                                                 \
-    CM_LAUNCH(cm::k_rmsnorm_quant<C>, dim3(1), dim3(cm::RMS_NT), 0, s, x, w, (int)n, eps, xq, xs, y); \
+#define CM_RMS(C)                                                                                             \
+  case C:                                                                                                     \
+    CM_LAUNCH(cm::k_rmsnorm_quant<C>, dim3(grid), dim3(cm::RMS_NT), 0, s, x, w, (int)n, eps, xq, xs, y, pf); \
     break;
     CM_SEG_CHUNKS(CM_RMS)
 #undef CM_RMS
@@ -387,10 +405,10 @@ void gemv(camelid_hip_engine* e, const Q8Mat& m, float* y, const float* resid) {
   launch_gemv(m, e->xq, e->xs, y, resid, e->stream);
 }
 
-void rmsnorm(camelid_hip_engine* e, const float* w) {
+void rmsnorm(camelid_hip_engine* e, const float* w, const Q8Mat* next) {
   const uint32_t n = e->d.hidden;
   ProfScope ps(e, P_NORM, n * 8.0 + n * 34.0 / 32.0);
-  launch_rmsnorm_quant(e->h, w, n, e->d.eps, e->xq, e->xs, nullptr, e->stream);
+  launch_rmsnorm_quant(e->h, w, n, e->d.eps, e->xq, e->xs, nullptr, e->stream, e->read_ahead ? next : nullptr);
 }
 
 // One transformer layer at StepState.pos; RoPE tables at cos_base + pos*rope_stride.
@@ -400,22 +418,23 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const f
   const LayerW& L = e->layers[l];
   hipStream_t s = e->stream;
   const double nq = (double)d.n_heads * d.head_dim, nkv = (double)d.n_kv_heads * d.head_dim;
-  rmsnorm(e, L.attn_norm);
+  rmsnorm(e, L.attn_norm, &L.qkv);
   gemv(e, L.qkv, e->qkv, nullptr);
   {
     ProfScope ps(e, P_ATTN, (nq + 2 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0));
     launch_attention<true>(d.head_dim, d.n_heads, e->att_slots, s, e->qkv, (int)d.n_heads,
                            (int)d.n_kv_heads, (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base,
                            rope_stride, L.q_norm, L.k_norm, d.eps, e->kc, e->vc, (int)l, (int)e->kvs, &e->st->pos,
-                           scale, e->att, e->xq, e->xs);
+                           scale, e->att, e->xq, e->xs, e->read_ahead ? &L.o : nullptr);
   }
   gemv(e, L.o, e->h, e->h);
-  rmsnorm(e, L.ffn_norm);
+  rmsnorm(e, L.ffn_norm, &L.gu);
   gemv(e, L.gu, e->gu, nullptr);
   {
     ProfScope ps(e, P_SILU, d.ffn_dim * 8.0 + d.ffn_dim * 34.0 / 32.0);
-    CM_LAUNCH(cm::k_silu_mul_quant, dim3((d.ffn_dim + 255) / 256), dim3(256), 0, s, e->gu, (int)d.ffn_dim,
-                       e->xq, e->xs, nullptr);
+    const cm::Prefetch pf = prefetch_of(e->read_ahead ? &L.down : nullptr);
+    const uint32_t grid = (d.ffn_dim + 255) / 256 + (pf.a_lines ? PREFETCH_WGS : 0);
+    CM_LAUNCH(cm::k_silu_mul_quant, dim3(grid), dim3(256), 0, s, e->gu, (int)d.ffn_dim, e->xq, e->xs, nullptr, pf);
   }
   gemv(e, L.down, e->h, e->h);
 }
@@ -435,7 +454,7 @@ void run_stack(camelid_hip_engine* e, const float* cos_base, const float* sin_ba
 
 // Final norm, lm_head and greedy argmax; advances StepState (pos+1, tok, tokens[step]).
 void run_head(camelid_hip_engine* e, uint32_t* tokens, uint32_t cap) {
-  rmsnorm(e, e->out_norm);
+  rmsnorm(e, e->out_norm, nullptr);
   const Q8Mat& m = e->out;
   uint32_t nparts;
   {
@@ -527,6 +546,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   e->d = d;
   if (const char* dev = std::getenv("CAMELID_HIP_DEVICE")) e->device = std::atoi(dev);
   if (const char* g = std::getenv("CAMELID_HIP_GRAPHS")) e->use_graph = std::atoi(g) != 0;
+  if (const char* r = std::getenv("CAMELID_HIP_READ_AHEAD")) e->read_ahead = std::atoi(r) != 0;
   hipError_t st = hipSetDevice(e->device);
   if (st != hipSuccess) {
     fail(nullptr, std::string("hipSetDevice failed: ") + hipGetErrorString(st));
@@ -995,7 +1015,7 @@ int camelid_hip_silu_mul_quantize(const float* gu, uint32_t n, int8_t* xq, float
   if (n % 32) return fail(nullptr, "n must be a multiple of 32");
   if (n == 0) return 0;
   hipLaunchKernelGGL(cm::k_silu_mul_quant, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, gu, (int)n, xq,
-                     xs, act);
+                     xs, act, prefetch_of(nullptr));
   return launch_status("silu_mul_quantize");
 }
 

@@ -565,8 +565,40 @@ __global__ __launch_bounds__(1024) void k_argmax_finish(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------
+// Read-ahead of the next projection's weights by the spare workgroups of a latency-bound
+// kernel (the RMSNorm and attention kernels use one or a few CUs for several
+// microseconds): one 4-byte load per 128-byte line pulls the lines into the L2 / MALL
+// caches, so that the GEMV that follows streams them from cache.  Two regions (the int8
+// quants and the f16 scales of a Q8R matrix); worker `wg` of `nwg`.  Loads only.
+struct Prefetch {
+  const uint32_t* a;
+  size_t a_lines;
+  const uint32_t* b;
+  size_t b_lines;
+};
+
+__device__ __forceinline__ void prefetch_lines(const Prefetch& pf, int wg, int nwg, float* sink_lds) {
+  const size_t stride = (size_t)nwg * blockDim.x;
+  uint32_t acc = 0;
+  const size_t total = pf.a_lines + pf.b_lines;
+  size_t i = (size_t)wg * blockDim.x + threadIdx.x;
+  for (; i + 7 * stride < total; i += 8 * stride) {
+    uint32_t v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const size_t l = i + u * stride;
+      v[u] = l < pf.a_lines ? pf.a[l * 32] : pf.b[(l - pf.a_lines) * 32];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= v[u];
+  }
+  for (; i < total; i += stride) acc ^= i < pf.a_lines ? pf.a[i * 32] : pf.b[(i - pf.a_lines) * 32];
+  if (acc == 0x9e3779b9u && pf.a_lines == 1) sink_lds[0] = 0.0f;  // keeps the loads
+}
+
+// ---------------------------------------------------------------------------
 // RMSNorm (tensor/mod.rs:2083-2106) fused with Q8_0 quantization of the result.
-// One workgroup of RMS_NT threads.  Thread t owns the 32-element blocks t + RMS_NT b: it
+// Workgroup 0 (RMS_NT threads) computes it; any further workgroups read ahead `pf`.  Thread t owns the 32-element blocks t + RMS_NT b: it
 // loads their x and w values up front (16-byte loads, all in flight together), writes the
 // squares to LDS for the in-order sum (inorder_sum_nonneg: bit-identical to the
 // sequential fold), then normalises and quantizes its blocks from registers, with no
@@ -604,10 +636,15 @@ __device__ __forceinline__ float quantize_block_regs(const float (&y)[32], uint3
 template <int C>
 __global__ __launch_bounds__(RMS_NT) void k_rmsnorm_quant(const float* __restrict__ x, const float* __restrict__ w,
                                                           int n, float eps, int8_t* __restrict__ xq,
-                                                          float* __restrict__ xs, float* __restrict__ y_out) {
+                                                          float* __restrict__ xs, float* __restrict__ y_out,
+                                                          Prefetch pf) {
   constexpr int BPT = (C + 31) / 32;  // blocks per thread
   __shared__ __align__(16) float sq[RMS_NT * C];
   __shared__ __align__(16) uint32_t ps[RMS_NT * C + 4];
+  if (blockIdx.x > 0) {  // spare workgroups: read ahead the next projection's weights
+    prefetch_lines(pf, blockIdx.x - 1, gridDim.x - 1, sq);
+    return;
+  }
   const int tid = threadIdx.x;
   const int nb = n >> 5;
   float4 xv[BPT][8], wv[BPT][8];
@@ -676,7 +713,14 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float* __restrict__
 
 // SwiGLU (tensor/mod.rs:1943-1967) + Q8_0 quantization.  gu = [gate(n) | up(n)].
 __global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict__ gu, int n, int8_t* __restrict__ xq,
-                                                        float* __restrict__ xs, float* __restrict__ act_out) {
+                                                        float* __restrict__ xs, float* __restrict__ act_out,
+                                                        Prefetch pf) {
+  const int nwork = (n + 255) / 256;
+  if ((int)blockIdx.x >= nwork) {  // spare workgroups: read ahead the down projection
+    __shared__ float sink[1];
+    prefetch_lines(pf, blockIdx.x - nwork, gridDim.x - nwork, sink);
+    return;
+  }
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;  // uniform per 32-lane group
   const float a = silu_mul1(gu[i], gu[n + i]);
@@ -812,7 +856,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
     const float* __restrict__ cos_base, const float* __restrict__ sin_base, int rope_stride,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm, float eps, uint16_t* __restrict__ kc,
     float* __restrict__ vc, int layer, int kvs, const uint32_t* __restrict__ d_pos, float scale,
-    float* __restrict__ att_out, int8_t* __restrict__ xq, float* __restrict__ xs, int ring_slots) {
+    float* __restrict__ att_out, int8_t* __restrict__ xq, float* __restrict__ xs, int ring_slots, Prefetch pf) {
   constexpr int ATT_NT = att_nt(HD);
   static_assert(HD % 64 == 0 && HD <= 256, "head_dim must be 64, 128 or 256");
   constexpr int R8 = HD / 8;  // 16-byte granules per K row
@@ -824,6 +868,10 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   extern __shared__ __align__(16) float4 dyn[];
   float4* ring = dyn;  // ring_slots chunks of ATT_RING_GRANULES V granules
   float* sc = reinterpret_cast<float*>(dyn + (size_t)ring_slots * ATT_RING_GRANULES);
+  if ((int)blockIdx.x >= n_heads) {  // spare workgroups: read ahead the output projection
+    prefetch_lines(pf, blockIdx.x - n_heads, gridDim.x - n_heads, sc);
+    return;
+  }
   __shared__ __align__(16) float qs[HD];
   __shared__ __align__(16) float kn[HD];  // this position's k (f16-rounded)
   __shared__ __align__(16) float vn[HD];  // this position's v (f16-rounded)
