@@ -94,10 +94,11 @@ __device__ __forceinline__ float fold_lds(const float* p, int n, float acc = 0.0
 // step adds exactly the integer d_i = RNE(t_i / u) ulps -- unless t_i / u is an exact half
 // (round-half-even then depends on the running parity), t_i >= 2^e, t_i is negative or
 // not finite, or the step leaves the binade.
-//   pass  (all threads, once per binade entered): d_i for every remaining term, with the
-//         exceptional terms ("flagged") given d = 2^25, larger than any in-binade step;
-//         a saturating workgroup prefix sum of d goes to ps[0..n] in LDS.
-//   round (wave 0, while the binade is unchanged): from the running mantissa N (in ulps)
+//   pass  (all threads): for each of seg_binades(C) consecutive binades from the current
+//         one, d_i for every remaining term, with the exceptional terms ("flagged") given
+//         d = 2^25, larger than any in-binade step; a saturating workgroup prefix sum of d
+//         per binade goes to LDS.  A new pass is needed only past the last of them.
+//   round (wave 0, per stop): in the running sum's binade, from the mantissa N (in ulps)
 //         at term k, the first index i >= k whose step reaches 2^24 ulps or is flagged is
 //         the first p with ps[p] >= 2^24 - N + ps[k] (ps is monotone), minus one; found by
 //         a 64-way ballot search.  Terms k..i-1 are summed exactly by the integer
@@ -105,7 +106,8 @@ __device__ __forceinline__ float fold_lds(const float* p, int n, float acc = 0.0
 //         when it rounds up onto exactly 2^(e+1) -- written directly.
 // The first m_seq terms, where binade changes are frequent, are folded sequentially.
 // Negative or huge (>= 2^126) running sums take plain sequential steps.  Every thread
-// of the workgroup must call; v (n floats) and ps (n + 1 words) are in LDS; NT * C >= n.
+// of the workgroup must call; v (n floats) and ps (seg_binades(C) * (NT * C + 4) words) are
+// in LDS; NT * C >= n.
 constexpr uint32_t SEG_LIM = 1u << 24;   // ulps in a binade
 constexpr uint32_t SEG_FLAG = 1u << 25;  // step given to a flagged term
 constexpr uint32_t SEG_GUARD = 0xffffffffu - 2u * SEG_FLAG;  // prefix values the rounds accept
@@ -140,13 +142,18 @@ __device__ __forceinline__ uint32_t wave_scan_incl_sat(uint32_t x) {
   return x;
 }
 
+// Binades covered by one pass (prefix arrays of n + 4 words each in LDS), by chunk size.
+__host__ __device__ constexpr int seg_binades(int C) { return C <= 16 ? 4 : C <= 32 ? 3 : 1; }
+
 template <int NT, int C>
 __device__ __forceinline__ float inorder_sum_nonneg(const float* v, uint32_t* ps, int n, int m_seq) {
   constexpr int NW = NT / 64;
+  constexpr int NB = seg_binades(C);  // consecutive binades per pass
+  constexpr int PSTRIDE = NT * C + 4;  // words per prefix array
   static_assert(NT % 64 == 0 && NW <= 16, "the cross-wave scan runs in one 16-lane DPP row");
   __shared__ float sh_s;
   __shared__ int sh_k;
-  __shared__ uint32_t sh_tot[NW];
+  __shared__ uint32_t sh_tot[NB][NW];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i0 = tid * C;  // this thread's contiguous chunk
   float t[C];
@@ -164,75 +171,96 @@ __device__ __forceinline__ float inorder_sum_nonneg(const float* v, uint32_t* ps
     if (k >= n) break;
     const uint32_t sb0 = __float_as_uint(s);
     const int E0 = (int)((sb0 >> 23) & 0xffu);
-    const int Ep = max(E0, 1);
+    const int Eb = max(E0, 1);  // first binade of this pass
     const bool plain = (sb0 >> 31) != 0u || E0 >= 254;
-    if (!plain) {  // pass for binade Ep over the terms k..n-1 (terms before k count 0)
-      uint32_t dv[C];
-      uint32_t T = 0;
+    if (!plain) {  // pass for binades Eb .. Eb+NB-1 over the terms k..n-1 (terms before k count 0)
+      uint32_t dv[NB][C];
+      uint32_t T[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) T[b] = 0;
       if (i0 + C > k) {
 #pragma unroll
-        for (int c = 0; c < C; ++c) dv[c] = seg_d(t[c], Ep);
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+          for (int b = 0; b < NB; ++b) dv[b][c] = seg_d(t[c], Eb + b);
         if (i0 < k) {
 #pragma unroll
-          for (int c = 0; c < C; ++c) dv[c] = i0 + c < k ? 0u : dv[c];
-        }
-      } else {
-#pragma unroll
-        for (int c = 0; c < C; ++c) dv[c] = 0u;
-      }
-#pragma unroll
-      for (int c = 0; c < C; ++c) T = sat_add(T, dv[c]);
-      const uint32_t incl = wave_scan_incl_sat(T);
-      if (lane == 63) sh_tot[wave] = incl;
-      __syncthreads();
-      uint32_t wt = lane < NW ? sh_tot[lane] : 0u;
-      wt = sat_add(wt, CM_DPP(wt, 0x111, 0xf));
-      wt = sat_add(wt, CM_DPP(wt, 0x112, 0xf));
-      wt = sat_add(wt, CM_DPP(wt, 0x114, 0xf));
-      wt = sat_add(wt, CM_DPP(wt, 0x118, 0xf));
-      const uint32_t wpre = (uint32_t)__builtin_amdgcn_readlane((int)CM_DPP(wt, 0x111, 0xf), wave);
-      uint32_t P = sat_add(wpre, CM_DPP(incl, 0x138, 0xf));  // wave_shr:1 -> exclusive prefix
-      uint32_t pv[C];
-#pragma unroll
-      for (int c = 0; c < C; ++c) {
-        pv[c] = P;
-        P = sat_add(P, dv[c]);
-      }
-      if constexpr (C % 4 == 0) {
-        if (i0 + C <= n) {
-#pragma unroll
-          for (int c = 0; c < C; c += 4)
-            *reinterpret_cast<uint4*>(ps + i0 + c) = make_uint4(pv[c], pv[c + 1], pv[c + 2], pv[c + 3]);
-        } else {
-#pragma unroll
           for (int c = 0; c < C; ++c)
-            if (i0 + c < n) ps[i0 + c] = pv[c];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) dv[b][c] = i0 + c < k ? 0u : dv[b][c];
         }
       } else {
 #pragma unroll
         for (int c = 0; c < C; ++c)
-          if (i0 + c < n) ps[i0 + c] = pv[c];
+#pragma unroll
+          for (int b = 0; b < NB; ++b) dv[b][c] = 0u;
       }
-      if (i0 <= n - 1 && n - 1 < i0 + C) ps[n] = P;
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int c = 0; c < C; ++c) T[b] = sat_add(T[b], dv[b][c]);
+      uint32_t incl[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        incl[b] = wave_scan_incl_sat(T[b]);
+        if (lane == 63) sh_tot[b][wave] = incl[b];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        uint32_t wt = lane < NW ? sh_tot[b][lane] : 0u;
+        wt = sat_add(wt, CM_DPP(wt, 0x111, 0xf));
+        wt = sat_add(wt, CM_DPP(wt, 0x112, 0xf));
+        wt = sat_add(wt, CM_DPP(wt, 0x114, 0xf));
+        wt = sat_add(wt, CM_DPP(wt, 0x118, 0xf));
+        const uint32_t wpre = (uint32_t)__builtin_amdgcn_readlane((int)CM_DPP(wt, 0x111, 0xf), wave);
+        uint32_t P = sat_add(wpre, CM_DPP(incl[b], 0x138, 0xf));  // wave_shr:1 -> exclusive prefix
+        uint32_t* psb = ps + b * PSTRIDE;
+        uint32_t pv[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          pv[c] = P;
+          P = sat_add(P, dv[b][c]);
+        }
+        if constexpr (C % 4 == 0) {
+          if (i0 + C <= n) {
+#pragma unroll
+            for (int c = 0; c < C; c += 4)
+              *reinterpret_cast<uint4*>(psb + i0 + c) = make_uint4(pv[c], pv[c + 1], pv[c + 2], pv[c + 3]);
+          } else {
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+              if (i0 + c < n) psb[i0 + c] = pv[c];
+          }
+        } else {
+#pragma unroll
+          for (int c = 0; c < C; ++c)
+            if (i0 + c < n) psb[i0 + c] = pv[c];
+        }
+        if (i0 <= n - 1 && n - 1 < i0 + C) psb[n] = P;
+      }
     }
     __syncthreads();
     if (wave == 0) {  // rounds: uniform control flow over the wave
-      const uint32_t tot = plain ? 0u : ps[n];
-      uint32_t base = 0;  // ps[k]: the pass counted nothing before k
-      bool base_ok = true;
+      int cur = -1;            // prefix array in use (binade Eb + cur)
+      uint32_t base = 0, tot = 0;  // its values at k and at n
       while (k < n) {
         const uint32_t sb = __float_as_uint(s);
         const int E = (int)((sb >> 23) & 0xffu);
         if ((sb >> 31) != 0u || E >= 254) {  // negative or huge running sum: plain step
           s = s + v[k];
           ++k;
-          base_ok = false;
+          cur = -1;
           continue;
         }
-        if (plain || max(E, 1) != Ep) break;  // a new binade needs a new pass
-        if (!base_ok) {
-          base = ps[k];
-          base_ok = true;
+        const int Ep = max(E, 1);
+        const int b = Ep - Eb;
+        if (plain || b < 0 || b >= NB) break;  // outside this pass's binades: new pass
+        const uint32_t* psb = ps + b * PSTRIDE;
+        if (b != cur) {
+          base = psb[k];
+          tot = psb[n];
+          cur = b;
         }
         if (base > SEG_GUARD) break;  // keep the prefix sums unsaturated
         const uint32_t N = sb - ((uint32_t)(Ep - 1) << 23);
@@ -242,19 +270,19 @@ __device__ __forceinline__ float inorder_sum_nonneg(const float* v, uint32_t* ps
           k = n;
           break;
         }
-        // first p in [k + 1, n] with ps[p] >= X (ps[n] >= X)
+        // first p in [k + 1, n] with psb[p] >= X (psb[n] >= X)
         int lo = k + 1, hi = n;
         while (hi - lo >= 63) {
           const int stride = (hi - lo + 64) >> 6;
           const int p = min(lo + lane * stride + stride - 1, hi);
-          const unsigned long long bm = __ballot(ps[p] >= X);
+          const unsigned long long bm = __ballot(psb[p] >= X);
           const int nlo = lo + (__ffsll((long long)bm) - 1) * stride;
           hi = min(nlo + stride - 1, hi);
           lo = nlo;
         }
         // lane l holds position lo - 1 + l (lane 0: the term before the range)
         const int q = min(lo - 1 + lane, hi);
-        const uint32_t pq = ps[q];
+        const uint32_t pq = psb[q];
         const float tq = v[min(q, n - 1)];
         const unsigned long long bm = __ballot(lane >= 1 && lo - 1 + lane <= hi && pq >= X);
         const int li = __ffsll((long long)bm) - 2;  // lane holding the stopping term i = p - 1
@@ -269,7 +297,7 @@ __device__ __forceinline__ float inorder_sum_nonneg(const float* v, uint32_t* ps
         } else {
           s = seg_value(Ep, SEG_LIM);  // rounds up onto exactly 2^(e+1)
         }
-        base = sat_add(pi, di);  // ps[i + 1]
+        base = sat_add(pi, di);  // psb[i + 1]
         k = i + 1;
       }
       if (lane == 0) {
@@ -640,7 +668,7 @@ __global__ __launch_bounds__(RMS_NT) void k_rmsnorm_quant(const float* __restric
                                                           Prefetch pf) {
   constexpr int BPT = (C + 31) / 32;  // blocks per thread
   __shared__ __align__(16) float sq[RMS_NT * C];
-  __shared__ __align__(16) uint32_t ps[RMS_NT * C + 4];
+  __shared__ __align__(16) uint32_t ps[seg_binades(C) * (RMS_NT * C + 4)];
   if (blockIdx.x > 0) {  // spare workgroups: read ahead the next projection's weights
     prefetch_lines(pf, blockIdx.x - 1, gridDim.x - 1, sq);
     return;
@@ -1131,7 +1159,7 @@ template <int C>
 __global__ __launch_bounds__(256) void k_inorder_sum_rows(const float* __restrict__ x, int n, int m_seq,
                                                           float* __restrict__ out) {
   __shared__ __align__(16) float v[256 * C];
-  __shared__ __align__(16) uint32_t ps[256 * C + 4];
+  __shared__ __align__(16) uint32_t ps[seg_binades(C) * (256 * C + 4)];
   const float* row = x + (size_t)blockIdx.x * n;
   for (int i = threadIdx.x; i < n; i += 256) v[i] = row[i];
   __syncthreads();
