@@ -72,11 +72,14 @@ struct camelid_hip_engine {
   uint32_t kvs = 0;        // KV position stride: max_pos rounded up to a multiple of 8
   int att_slots = 0;       // V ring chunks of the attention kernel
   bool read_ahead = true;  // spare workgroups of the norm kernels read ahead the next weights
+  bool gu_fused = false;   // gate/up rows interleaved by 32, SwiGLU fused into their GEMV
   float *h = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr;
   float *logits = nullptr, *hidden_cap = nullptr, *xs = nullptr;
   float *cos_cur = nullptr, *sin_cur = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
   uint32_t rope_rows = 0;
   int8_t* xq = nullptr;
+  int8_t* aq = nullptr;      // SwiGLU activation quants (fused gate/up path), [ffn]
+  float* as = nullptr;       // its block scales, [ffn / 32]
   float* part_v = nullptr;
   uint32_t* part_i = nullptr;
   cm::StepState* st = nullptr;
@@ -185,7 +188,10 @@ struct Part {
 };
 
 // Upload `parts` (stacked row-wise) as one Q8R matrix.
-int upload_q8(camelid_hip_engine* e, Q8Mat* m, const std::vector<Part>& parts, uint32_t k, uint8_t layout) {
+// group > 0 (two parts of equal rows): interleave them in groups of `group` rows, part 0's
+// group first (the fused gate/up layout).
+int upload_q8(camelid_hip_engine* e, Q8Mat* m, const std::vector<Part>& parts, uint32_t k, uint8_t layout,
+              uint32_t group = 0) {
   if (layout != 34 && layout != 36) return fail(e, "q8_layout must be 34 or 36");
   if (k % 32 != 0) return fail(e, "Q8_0 row width must be a multiple of 32");
   uint32_t rows = 0;
@@ -203,6 +209,21 @@ int upload_q8(camelid_hip_engine* e, Q8Mat* m, const std::vector<Part>& parts, u
   for (const Part& p : parts) {
     repack_parallel(p.src, p.rows, k, layout, q.data() + r * k, d.data() + r * nb);
     r += p.rows;
+  }
+  if (group) {
+    if (parts.size() != 2 || parts[0].rows != parts[1].rows || parts[0].rows % group)
+      return fail(e, "interleaved upload needs two parts of equal rows, a multiple of the group");
+    const size_t half = parts[0].rows;
+    std::vector<int8_t> q2(q.size());
+    std::vector<uint16_t> d2(d.size());
+    for (size_t g = 0; g < half / group; ++g)
+      for (size_t h = 0; h < 2; ++h) {
+        const size_t src = h * half + g * group, dst = (2 * g + h) * group;
+        std::memcpy(q2.data() + dst * k, q.data() + src * k, group * k);
+        std::memcpy(d2.data() + dst * nb, d.data() + src * nb, group * nb * 2);
+      }
+    q.swap(q2);
+    d.swap(d2);
   }
   if (!m->q) {
     if (dev_alloc(e, &m->q, q.size()) || dev_alloc(e, &m->d, d.size())) return 1;
@@ -400,9 +421,10 @@ int attn_ring_slots(uint32_t kvs) {
   return slots >= 2 ? (int)slots : 0;
 }
 
-void gemv(camelid_hip_engine* e, const Q8Mat& m, float* y, const float* resid) {
+void gemv(camelid_hip_engine* e, const Q8Mat& m, float* y, const float* resid, const int8_t* xq = nullptr,
+          const float* xs = nullptr) {
   ProfScope ps(e, P_GEMV, q8_bytes(m, resid != nullptr));
-  launch_gemv(m, e->xq, e->xs, y, resid, e->stream);
+  launch_gemv(m, xq ? xq : e->xq, xs ? xs : e->xs, y, resid, e->stream);
 }
 
 void rmsnorm(camelid_hip_engine* e, const float* w, const Q8Mat* next) {
@@ -429,14 +451,29 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const f
   }
   gemv(e, L.o, e->h, e->h);
   rmsnorm(e, L.ffn_norm, &L.gu);
-  gemv(e, L.gu, e->gu, nullptr);
-  {
+  if (e->gu_fused) {
+    ProfScope ps(e, P_GEMV, q8_bytes(L.gu, false) - L.gu.rows * 4.0 + d.ffn_dim * 34.0 / 32.0);
+    const uint32_t groups = d.ffn_dim / 32;
+    switch (d.hidden) {
+#define CM_GU(K)                                                                                                 \
+  case K:                                                                                                        \
+    CM_LAUNCH(cm::k_gemv_gu_silu<K>, dim3(groups), dim3(cm::GU_NT), 0, s, L.gu.q, L.gu.d, e->xq, e->xs, e->aq, \
+              e->as);                                                                                            \
+    break;
+      CM_GU(2048) CM_GU(3072) CM_GU(4096)
+#undef CM_GU
+    }
+  } else {
+    gemv(e, L.gu, e->gu, nullptr);
     ProfScope ps(e, P_SILU, d.ffn_dim * 8.0 + d.ffn_dim * 34.0 / 32.0);
     const cm::Prefetch pf = prefetch_of(e->read_ahead ? &L.down : nullptr);
     const uint32_t grid = (d.ffn_dim + 255) / 256 + (pf.a_lines ? PREFETCH_WGS : 0);
     CM_LAUNCH(cm::k_silu_mul_quant, dim3(grid), dim3(256), 0, s, e->gu, (int)d.ffn_dim, e->xq, e->xs, nullptr, pf);
   }
-  gemv(e, L.down, e->h, e->h);
+  if (e->gu_fused)
+    gemv(e, L.down, e->h, e->h, e->aq, e->as);  // the activation quantized by the fused gate/up kernel
+  else
+    gemv(e, L.down, e->h, e->h);
 }
 
 void run_stack(camelid_hip_engine* e, const float* cos_base, const float* sin_base, int rope_stride, float scale) {
@@ -561,6 +598,8 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   }
   e->layers.resize(d.n_layers);
   e->kvs = (d.max_pos + 7u) & ~7u;
+  e->gu_fused = cm::gu_fused_k((int)d.hidden);
+  if (const char* f = std::getenv("CAMELID_HIP_FUSED_GU")) e->gu_fused = e->gu_fused && std::atoi(f) != 0;
   e->att_slots = attn_ring_slots(e->kvs);
   const size_t nq = (size_t)d.n_heads * d.head_dim, nkv = (size_t)d.n_kv_heads * d.head_dim;
   const size_t kv_elems = (size_t)d.n_layers * d.n_kv_heads * e->kvs * d.head_dim;
@@ -571,6 +610,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   int rc = dev_alloc(e, &e->kc, kv_elems) || dev_alloc(e, &e->vc, kv_elems) || dev_alloc(e, &e->h, d.hidden) ||
            dev_alloc(e, &e->qkv, nq + 2 * nkv) || dev_alloc(e, &e->att, nq) ||
            dev_alloc(e, &e->gu, 2 * (size_t)d.ffn_dim) || dev_alloc(e, &e->logits, d.vocab) ||
+           dev_alloc(e, &e->aq, d.ffn_dim) || dev_alloc(e, &e->as, d.ffn_dim / 32) ||
            dev_alloc(e, &e->hidden_cap, (size_t)(d.n_layers + 1) * d.hidden) || dev_alloc(e, &e->xq, act) ||
            dev_alloc(e, &e->xs, act / 32) || dev_alloc(e, &e->cos_cur, half) || dev_alloc(e, &e->sin_cur, half) ||
            dev_alloc(e, &e->part_v, nparts) || dev_alloc(e, &e->part_i, nparts) || dev_alloc(e, &e->st, 1) ||
@@ -619,7 +659,8 @@ int camelid_hip_set_layer(camelid_hip_engine* e, uint32_t layer, const uint8_t* 
   LayerW& L = e->layers[layer];
   if (upload_q8(e, &L.qkv, {{w[0], len[0], nq}, {w[1], len[1], nkv}, {w[2], len[2], nkv}}, d.hidden, q8_layout) ||
       upload_q8(e, &L.o, {{w[3], len[3], d.hidden}}, nq, q8_layout) ||
-      upload_q8(e, &L.gu, {{w[4], len[4], d.ffn_dim}, {w[5], len[5], d.ffn_dim}}, d.hidden, q8_layout) ||
+      upload_q8(e, &L.gu, {{w[4], len[4], d.ffn_dim}, {w[5], len[5], d.ffn_dim}}, d.hidden, q8_layout,
+                e->gu_fused ? 32u : 0u) ||
       upload_q8(e, &L.down, {{w[6], len[6], d.hidden}}, d.ffn_dim, q8_layout) ||
       upload_f32(e, &L.attn_norm, attn_norm, d.hidden) || upload_f32(e, &L.ffn_norm, ffn_norm, d.hidden))
     return 1;

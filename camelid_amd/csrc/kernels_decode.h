@@ -340,6 +340,29 @@ __device__ __forceinline__ float quantize_lane32(float v, int8_t* q) {
   return scale;
 }
 
+// Q8_0 quantization of one 32-element block held by one lane (inference.rs:16953-16971):
+// returns the f16-rounded scale, writes the 32 quants as 8 packed words.
+__device__ __forceinline__ float quantize_block_regs(const float (&y)[32], uint32_t (&packed)[8]) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(y[e]));
+  const float unrounded = amax / 127.0f;
+  const float scale = f16_bits_to_f32(f32_to_f16_bits(unrounded));
+  const float inv = unrounded == 0.0f ? 0.0f : 1.0f / unrounded;
+#pragma unroll
+  for (int w4 = 0; w4 < 8; ++w4) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float r = roundf(y[w4 * 4 + e] * inv);
+      r = fminf(fmaxf(r, -128.0f), 127.0f);
+      word |= ((uint32_t)(int32_t)r & 0xffu) << (8 * e);
+    }
+    packed[w4] = word;
+  }
+  return scale;
+}
+
 __device__ __forceinline__ float block_max(float v, float* red) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
@@ -509,6 +532,82 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv(const int8_t* __restrict__ wq,
   }
 }
 
+// Gate/up projection fused with SwiGLU (tensor/mod.rs:1943-1967) and the Q8_0 quantization
+// of the activation.  The matrix rows are interleaved in groups of 32: group g holds gate
+// rows 32g..32g+31 followed by up rows 32g..32g+31, so one workgroup (8 waves, 8 rows each)
+// computes both halves of one 32-value block of the activation: the same per-row block
+// dots and in-order folds as k_gemv_k, then silu(gate) * up and the block's quantization.
+constexpr int GU_NT = 512;
+constexpr int GU_ROWS = 64;  // rows per workgroup: 32 gate + 32 up
+__host__ __device__ constexpr bool gu_fused_k(int K) { return K == 2048 || K == 3072 || K == 4096; }
+
+template <int K>
+__global__ __launch_bounds__(GU_NT) void k_gemv_gu_silu(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                                       const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                                       int8_t* __restrict__ aq, float* __restrict__ as) {
+  constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64, STRIDE = gemv_term_stride(NB);
+  constexpr int RPW = GU_ROWS / (GU_NT / 64);  // 8 rows per wave
+  static_assert(NB % 4 == 0, "compile-time GEMV widths are multiples of 128");
+  __shared__ __align__(16) int8_t xl[K];
+  __shared__ __align__(16) float xsl[NB];
+  __shared__ __align__(16) float t[GU_ROWS * STRIDE];
+  __shared__ __align__(16) float vals[GU_ROWS];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const size_t row0 = (size_t)blockIdx.x * GU_ROWS;
+  // all of this wave's weight and scale loads first
+  int4 wv[RPW][IT];
+  uint16_t dv[RPW][IT];
+#pragma unroll
+  for (int k = 0; k < RPW; ++k) {
+    const size_t row = row0 + wave * RPW + k;
+    const int4* w4 = reinterpret_cast<const int4*>(wq + row * K);
+    const uint16_t* d = wd + row * NB;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int c = min(lane + 64 * i, CPR - 1);
+      wv[k][i] = w4[c];
+      dv[k][i] = d[c >> 1];
+    }
+  }
+  for (int c = tid; c < CPR; c += GU_NT) reinterpret_cast<int4*>(xl)[c] = reinterpret_cast<const int4*>(xq)[c];
+  for (int b = tid; b < NB; b += GU_NT) xsl[b] = xs[b];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < RPW; ++k) {
+    float* tr = t + (wave * RPW + k) * STRIDE;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int c = lane + 64 * i;
+      const int cc = min(c, CPR - 1);
+      int sacc = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
+      sacc += dpp_xor1(sacc);
+      if ((lane & 1) == 0 && c < CPR) tr[c >> 1] = ((float)sacc * half_bits_to_float(dv[k][i])) * xsl[c >> 1];
+    }
+  }
+  __syncthreads();
+  if (tid < GU_ROWS) vals[tid] = fold_lds_n<NB>(t + tid * STRIDE);  // one lane per row
+  __syncthreads();
+  if (tid < 32) vals[tid] = silu_mul1(vals[tid], vals[32 + tid]);
+  __syncthreads();
+  if (tid == 0) {  // the block's quantization, from registers
+    float y[32];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float4 v = reinterpret_cast<const float4*>(vals)[u];
+      y[u * 4] = v.x;
+      y[u * 4 + 1] = v.y;
+      y[u * 4 + 2] = v.z;
+      y[u * 4 + 3] = v.w;
+    }
+    uint32_t packed[8];
+    as[blockIdx.x] = quantize_block_regs(y, packed);
+    uint4* qp = reinterpret_cast<uint4*>(aq + (size_t)blockIdx.x * 32);
+    qp[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    qp[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+  }
+}
+
 // Decode-loop state shared by the step's kernels (device memory).
 struct StepState {
   uint32_t pos;      // position of the token being computed
@@ -636,29 +735,6 @@ constexpr int RMS_SEQ_HEAD = 384;  // terms folded sequentially before the segme
 
 __device__ __forceinline__ float4 mul4(const float4 a, const float4 b) {
   return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
-}
-
-// Q8_0 quantization of one 32-element block held by one lane (inference.rs:16953-16971):
-// returns the f16-rounded scale, writes the 32 quants as 8 packed words.
-__device__ __forceinline__ float quantize_block_regs(const float (&y)[32], uint32_t (&packed)[8]) {
-  float amax = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(y[e]));
-  const float unrounded = amax / 127.0f;
-  const float scale = f16_bits_to_f32(f32_to_f16_bits(unrounded));
-  const float inv = unrounded == 0.0f ? 0.0f : 1.0f / unrounded;
-#pragma unroll
-  for (int w4 = 0; w4 < 8; ++w4) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float r = roundf(y[w4 * 4 + e] * inv);
-      r = fminf(fmaxf(r, -128.0f), 127.0f);
-      word |= ((uint32_t)(int32_t)r & 0xffu) << (8 * e);
-    }
-    packed[w4] = word;
-  }
-  return scale;
 }
 
 template <int C>
