@@ -672,7 +672,18 @@ __global__ __launch_bounds__(1024) void k_argmax_finish(const float* __restrict_
   const int tid = threadIdx.x;
   float bv = -INFINITY;
   uint32_t bi = 0xffffffffu;
-  for (int i = tid; i < nparts; i += 1024) argmax_pair(bv, bi, part_v[i], part_i[i]);
+  for (int base = 0; base < nparts; base += 1024 * 8) {  // 8 pairs per lane in flight
+    float v[8];
+    uint32_t ix[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + tid + u * 1024;
+      v[u] = i < nparts ? part_v[i] : -INFINITY;
+      ix[u] = i < nparts ? part_i[i] : 0xffffffffu;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) argmax_pair(bv, bi, v[u], ix[u]);
+  }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) argmax_pair(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
   if ((tid & 63) == 0) {
