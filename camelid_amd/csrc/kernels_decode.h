@@ -23,6 +23,20 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t b) {
   return (float)h;  // v_cvt_f32_f16: exact widening (f16 denormals are enabled on gfx9)
 }
 
+// q * f32(h) for the f16 h in the low / high half of w, rounded once to f32: one
+// mixed-precision FMA with a -0 addend (exactly the f32 product, signed zeros included),
+// in place of a conversion and a multiply.
+__device__ __forceinline__ float mul_f16_lo(float q, uint32_t w) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(q), "v"(w), "v"(-0.0f));
+  return r;
+}
+__device__ __forceinline__ float mul_f16_hi(float q, uint32_t w) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(q), "v"(w), "v"(-0.0f));
+  return r;
+}
+
 __device__ __forceinline__ int dot4x4(int4 w, int4 x, int acc) {
   acc = __builtin_amdgcn_sdot4(w.x, x.x, acc, false);
   acc = __builtin_amdgcn_sdot4(w.y, x.y, acc, false);
@@ -1083,14 +1097,14 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
         __builtin_amdgcn_sched_barrier(0);
         const float4 qa = reinterpret_cast<const float4*>(qs)[2 * u];
         const float4 qb = reinterpret_cast<const float4*>(qs)[2 * u + 1];
-        acc += qa.x * half_bits_to_float((uint16_t)(row[u].x & 0xffffu));
-        acc += qa.y * half_bits_to_float((uint16_t)(row[u].x >> 16));
-        acc += qa.z * half_bits_to_float((uint16_t)(row[u].y & 0xffffu));
-        acc += qa.w * half_bits_to_float((uint16_t)(row[u].y >> 16));
-        acc += qb.x * half_bits_to_float((uint16_t)(row[u].z & 0xffffu));
-        acc += qb.y * half_bits_to_float((uint16_t)(row[u].z >> 16));
-        acc += qb.z * half_bits_to_float((uint16_t)(row[u].w & 0xffffu));
-        acc += qb.w * half_bits_to_float((uint16_t)(row[u].w >> 16));
+        acc += mul_f16_lo(qa.x, row[u].x);
+        acc += mul_f16_hi(qa.y, row[u].x);
+        acc += mul_f16_lo(qa.z, row[u].y);
+        acc += mul_f16_hi(qa.w, row[u].y);
+        acc += mul_f16_lo(qb.x, row[u].z);
+        acc += mul_f16_hi(qb.y, row[u].z);
+        acc += mul_f16_lo(qb.z, row[u].w);
+        acc += mul_f16_hi(qb.w, row[u].w);
       }
       const float sv = acc * scale;
       sc[p] = sv;
