@@ -78,6 +78,9 @@ SIGNATURES: dict[str, tuple] = {
                                       vp, C.c_float, vp, vp, vp, C.c_uint32, C.c_uint32, vp, vp]),
     "camelid_hip_attention_decode": (C.c_int, [vp, vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                                C.c_uint32, vp, C.c_float, vp, vp, vp, vp]),
+    "camelid_hip_q8_0_gemm": (C.c_int, [vp, vp, C.c_uint32, C.c_uint32, vp, vp, C.c_uint32, vp, vp, vp]),
+    "camelid_hip_attention_prefill": (C.c_int, [vp, vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                                C.c_uint32, C.c_uint32, C.c_uint32, C.c_float, vp, vp, vp, vp]),
     "camelid_hip_argmax": (C.c_int, [vp, C.c_uint32, vp, vp]),
     "camelid_hip_inorder_sum_rows": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp]),
     "camelid_hip_expf": (C.c_int, [vp, vp, C.c_size_t, vp]),

@@ -32,6 +32,7 @@
 
 #include "../../include/camelid_hip.h"
 #include "kernels_decode.h"
+#include "kernels_prefill.h"
 
 namespace {
 
@@ -88,6 +89,11 @@ struct camelid_hip_engine {
   // pinned host staging
   float *p_emb = nullptr, *p_cos = nullptr, *p_sin = nullptr, *p_logits = nullptr;
   cm::StepState* p_st = nullptr;
+  // batched prefill: per-chunk activations of up to PREFILL_CHUNK tokens (allocated on the
+  // first prefill): residual rows, QKV rows, rotated q rows, gate|up rows, Q8_0 activations
+  bool prefill_batched = true;
+  float *pf_h = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_gu = nullptr, *pf_xs = nullptr;
+  int8_t* pf_xq = nullptr;
   uint32_t filled = 0;
   uint32_t cur_pos = 0;  // host copy of the position being computed (profiling byte counts)
   bool capture = false;
@@ -392,14 +398,15 @@ void launch_attention(uint32_t hd, uint32_t n_heads, int slots, hipStream_t s, c
 #undef CM_ATT
 }
 
+// rows > 1: a [rows][n] batch, one workgroup per row (no read-ahead).
 void launch_rmsnorm_quant(const float* x, const float* w, uint32_t n, float eps, int8_t* xq, float* xs, float* y,
-                          hipStream_t s, const Q8Mat* next = nullptr) {
-  const cm::Prefetch pf = prefetch_of(next);
+                          hipStream_t s, const Q8Mat* next = nullptr, uint32_t rows = 1) {
+  const cm::Prefetch pf = prefetch_of(rows == 1 ? next : nullptr);
   const uint32_t grid = 1 + (pf.a_lines ? PREFETCH_WGS : 0);
   switch (cm::seg_chunk((int)n)) {
-#define CM_RMS(C)                                                                                             \
-  case C:                                                                                                     \
-    CM_LAUNCH(cm::k_rmsnorm_quant<C>, dim3(grid), dim3(cm::RMS_NT), 0, s, x, w, (int)n, eps, xq, xs, y, pf); \
+#define CM_RMS(C)                                                                                                   \
+  case C:                                                                                                           \
+    CM_LAUNCH(cm::k_rmsnorm_quant<C>, dim3(grid, rows), dim3(cm::RMS_NT), 0, s, x, w, (int)n, eps, xq, xs, y, pf); \
     break;
     CM_SEG_CHUNKS(CM_RMS)
 #undef CM_RMS
@@ -510,6 +517,65 @@ void run_embed(camelid_hip_engine* e) {
                      (int)d.hidden, e->st, e->h);
 }
 
+// ---------------------------------------------------------------- batched prefill
+constexpr uint32_t PREFILL_CHUNK = 512;  // tokens per pass over the layers
+
+int ensure_prefill_buffers(camelid_hip_engine* e) {
+  if (e->pf_h) return 0;
+  const camelid_hip_dims& d = e->d;
+  const size_t tc = PREFILL_CHUNK;
+  const size_t nq = (size_t)d.n_heads * d.head_dim, nkv = (size_t)d.n_kv_heads * d.head_dim;
+  const size_t act = std::max<size_t>({(size_t)d.hidden, (size_t)d.ffn_dim, nq});
+  return dev_alloc(e, &e->pf_h, tc * d.hidden) || dev_alloc(e, &e->pf_qkv, tc * (nq + 2 * nkv)) ||
+         dev_alloc(e, &e->pf_q, tc * nq) || dev_alloc(e, &e->pf_gu, tc * 2 * d.ffn_dim) ||
+         dev_alloc(e, &e->pf_xq, tc * act) || dev_alloc(e, &e->pf_xs, tc * act / 32);
+}
+
+void launch_gemm(const Q8Mat& m, uint32_t T, const int8_t* xq, const float* xs, float* y, const float* resid,
+                 hipStream_t s) {
+  CM_LAUNCH(cm::k_gemm_q8, dim3(cm::gemm_grid((int)m.rows, (int)T)), dim3(cm::GM_NT), 0, s, m.q, m.d, (int)m.rows,
+            (int)m.k, xq, xs, (int)T, y, resid);
+}
+
+void launch_attn_prefill(uint32_t hd, uint32_t n_heads, uint32_t n_kv, uint32_t T, const float* q, const uint16_t* kc,
+                         const float* vc, int layer, int kvs, int pos0, float scale, float* att, int8_t* xq, float* xs,
+                         hipStream_t s) {
+  const size_t lds = (((size_t)pos0 + T + 3) & ~(size_t)3) * 4;
+#define CM_AP(HD)                                                                                                  \
+  CM_LAUNCH(cm::k_attn_prefill<HD>, dim3(n_heads, T), dim3(cm::AP_NT), lds, s, q, (int)n_heads, (int)n_kv, kc, vc, \
+            layer, kvs, pos0, scale, att, xq, xs)
+  if (hd == 64) CM_AP(64);
+  else if (hd == 128) CM_AP(128);
+  else CM_AP(256);
+#undef CM_AP
+}
+
+// One chunk of T prompt tokens at positions pos0.. through every layer; the residual rows
+// are in e->pf_h, the RoPE rows of the chunk at cosv / sinv.
+void prefill_chunk(camelid_hip_engine* e, const float* cosv, const float* sinv, uint32_t T, uint32_t pos0,
+                   float scale) {
+  const camelid_hip_dims& d = e->d;
+  hipStream_t s = e->stream;
+  const uint32_t half = d.rope_dim / 2;
+  for (uint32_t l = 0; l < d.n_layers; ++l) {
+    const LayerW& L = e->layers[l];
+    launch_rmsnorm_quant(e->pf_h, L.attn_norm, d.hidden, d.eps, e->pf_xq, e->pf_xs, nullptr, s, nullptr, T);
+    launch_gemm(L.qkv, T, e->pf_xq, e->pf_xs, e->pf_qkv, nullptr, s);
+    CM_LAUNCH(cm::k_rope_kv, dim3(d.n_heads + d.n_kv_heads, T), dim3(64), 0, s, e->pf_qkv, (int)d.n_heads,
+              (int)d.n_kv_heads, (int)d.head_dim, (int)d.rope_dim, (int)d.split_half_pairing, cosv, sinv, L.q_norm,
+              L.k_norm, d.eps, e->pf_q, e->kc, e->vc, (int)l, (int)e->kvs, (const uint32_t*)nullptr, (int)pos0,
+              (int)half);
+    launch_attn_prefill(d.head_dim, d.n_heads, d.n_kv_heads, T, e->pf_q, e->kc, e->vc, (int)l, (int)e->kvs,
+                        (int)pos0, scale, nullptr, e->pf_xq, e->pf_xs, s);
+    launch_gemm(L.o, T, e->pf_xq, e->pf_xs, e->pf_h, e->pf_h, s);
+    launch_rmsnorm_quant(e->pf_h, L.ffn_norm, d.hidden, d.eps, e->pf_xq, e->pf_xs, nullptr, s, nullptr, T);
+    launch_gemm(L.gu, T, e->pf_xq, e->pf_xs, e->pf_gu, nullptr, s);
+    CM_LAUNCH(cm::k_silu_rows, dim3((d.ffn_dim + 255) / 256, T), dim3(256), 0, s, e->pf_gu, (int)d.ffn_dim,
+              (int)e->gu_fused, e->pf_xq, e->pf_xs);
+    launch_gemm(L.down, T, e->pf_xq, e->pf_xs, e->pf_h, e->pf_h, s);
+  }
+}
+
 bool ready(const camelid_hip_engine* e) {
   if (!e->out_set) return false;
   for (const LayerW& L : e->layers)
@@ -584,6 +650,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   if (const char* dev = std::getenv("CAMELID_HIP_DEVICE")) e->device = std::atoi(dev);
   if (const char* g = std::getenv("CAMELID_HIP_GRAPHS")) e->use_graph = std::atoi(g) != 0;
   if (const char* r = std::getenv("CAMELID_HIP_READ_AHEAD")) e->read_ahead = std::atoi(r) != 0;
+  if (const char* p = std::getenv("CAMELID_HIP_PREFILL")) e->prefill_batched = std::strcmp(p, "token") != 0;
   hipError_t st = hipSetDevice(e->device);
   if (st != hipSuccess) {
     fail(nullptr, std::string("hipSetDevice failed: ") + hipGetErrorString(st));
@@ -841,11 +908,26 @@ int camelid_hip_prefill(camelid_hip_engine* e, const float* embs, const float* c
       rc = fail(e, "prefill staging copy failed");
       break;
     }
-    for (uint32_t t = 0; t < n; ++t) {
-      (void)hipMemcpyAsync(e->h, d_embs + (size_t)t * d.hidden, d.hidden * 4, hipMemcpyDeviceToDevice, e->stream);
-      (void)hipMemcpyAsync(e->st, d_sts + t, sizeof(cm::StepState), hipMemcpyDeviceToDevice, e->stream);
-      e->cur_pos = sv[t].pos;
-      run_stack(e, d_cos + (size_t)t * half, d_sin + (size_t)t * half, 0, scale);
+    if (e->prefill_batched) {
+      // chunks of PREFILL_CHUNK tokens, every layer over the whole chunk
+      if (ensure_prefill_buffers(e)) {
+        rc = 1;
+        break;
+      }
+      for (uint32_t c0 = 0; c0 < n; c0 += PREFILL_CHUNK) {
+        const uint32_t T = std::min(PREFILL_CHUNK, n - c0);
+        (void)hipMemcpyAsync(e->pf_h, d_embs + (size_t)c0 * d.hidden, (size_t)T * d.hidden * 4,
+                             hipMemcpyDeviceToDevice, e->stream);
+        prefill_chunk(e, d_cos + (size_t)c0 * half, d_sin + (size_t)c0 * half, T, e->filled + c0, scale);
+      }
+    } else {
+      // one decode step per token
+      for (uint32_t t = 0; t < n; ++t) {
+        (void)hipMemcpyAsync(e->h, d_embs + (size_t)t * d.hidden, d.hidden * 4, hipMemcpyDeviceToDevice, e->stream);
+        (void)hipMemcpyAsync(e->st, d_sts + t, sizeof(cm::StepState), hipMemcpyDeviceToDevice, e->stream);
+        e->cur_pos = sv[t].pos;
+        run_stack(e, d_cos + (size_t)t * half, d_sin + (size_t)t * half, 0, scale);
+      }
     }
     if (check_launch(e)) {
       rc = 1;
@@ -1069,7 +1151,7 @@ int camelid_hip_rope_kv(const float* qkv, uint32_t n_heads, uint32_t n_kv, uint3
     return fail(nullptr, "invalid head geometry");
   hipLaunchKernelGGL(cm::k_rope_kv, dim3(n_heads + n_kv), dim3(64), 0, (hipStream_t)stream, qkv, (int)n_heads,
                      (int)n_kv, (int)hd, (int)rope_dim, (int)split_half, cos_tab, sin_tab, q_norm, k_norm, eps, qrot,
-                     kc, vc, (int)layer, (int)max_pos, d_pos);
+                     kc, vc, (int)layer, (int)max_pos, d_pos, 0, 0);
   return launch_status("rope_kv");
 }
 
@@ -1085,6 +1167,33 @@ int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const fl
                           (int)hd, 0, nullptr, nullptr, 0, nullptr, nullptr, 0.0f, const_cast<uint16_t*>(kc),
                           const_cast<float*>(vc), (int)layer, (int)max_pos, d_pos, scale, att_out, xq, xs);
   return launch_status("attention_decode");
+}
+
+int camelid_hip_q8_0_gemm(const int8_t* wq, const uint16_t* wd, uint32_t rows, uint32_t k, const int8_t* xq,
+                          const float* xs, uint32_t tokens, float* y, const float* resid, void* stream) {
+  if (!wq || !wd || !xq || !xs || !y) return fail(nullptr, "null argument");
+  if (k % 32 || k == 0 || rows == 0 || tokens == 0) return fail(nullptr, "k must be a nonzero multiple of 32, rows and tokens > 0");
+  if (rows % 4) return fail(nullptr, "rows must be a multiple of 4");
+  Q8Mat m;
+  m.q = const_cast<int8_t*>(wq);
+  m.d = const_cast<uint16_t*>(wd);
+  m.rows = rows;
+  m.k = k;
+  launch_gemm(m, tokens, xq, xs, y, resid, (hipStream_t)stream);
+  return launch_status("q8_0_gemm");
+}
+
+int camelid_hip_attention_prefill(const float* qrot, const uint16_t* kc, const float* vc, uint32_t layer,
+                                  uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t max_pos, uint32_t pos0,
+                                  uint32_t tokens, float scale, float* att_out, int8_t* xq, float* xs, void* stream) {
+  if (!qrot || !kc || !vc || !xq || !xs) return fail(nullptr, "null argument");
+  if (!n_heads || !n_kv || n_heads % n_kv || !attention_hd_supported(hd)) return fail(nullptr, "invalid head geometry");
+  if (max_pos % 8) return fail(nullptr, "the KV position stride (max_pos) must be a multiple of 8");
+  if (tokens == 0 || (size_t)pos0 + tokens > max_pos) return fail(nullptr, "positions beyond max_pos");
+  if (((size_t)pos0 + tokens) * 4 > 64 * 1024) return fail(nullptr, "more than 16384 positions");
+  launch_attn_prefill(hd, n_heads, n_kv, tokens, qrot, kc, vc, (int)layer, (int)max_pos, (int)pos0, scale, att_out,
+                      xq, xs, (hipStream_t)stream);
+  return launch_status("attention_prefill");
 }
 
 int camelid_hip_argmax(const float* x, uint32_t n, uint32_t* out, void* stream) {

@@ -774,6 +774,13 @@ __global__ __launch_bounds__(RMS_NT) void k_rmsnorm_quant(const float* __restric
     prefetch_lines(pf, blockIdx.x - 1, gridDim.x - 1, sq);
     return;
   }
+  {  // row blockIdx.y of a [rows][n] batch (prefill); row 0 in the decode step
+    const size_t row = blockIdx.y;
+    x += row * n;
+    xq += row * n;
+    xs += row * (n >> 5);
+    if (y_out) y_out += row * n;
+  }
   const int tid = threadIdx.x;
   const int nb = n >> 5;
   float4 xv[BPT][8], wv[BPT][8];
@@ -880,8 +887,10 @@ __host__ __device__ __forceinline__ size_t kv_v_index(int hd, int p, int d) {
 }
 
 // ---------------------------------------------------------------------------
-// Per-head QK RMSNorm (optional) + RoPE + f16 KV store for the token at st->pos (test
-// entry point; the engine fuses this into the attention kernel).  One workgroup per head:
+// Per-head QK RMSNorm (optional) + RoPE + f16 KV store for the token at *d_pos (or pos0
+// when d_pos is null).  The decode step fuses this into the attention kernel; prefill runs
+// it over a chunk of tokens, token blockIdx.y at position pos + blockIdx.y with its RoPE
+// row at cos/sin + blockIdx.y * rope_stride.  One workgroup per head:
 // blocks [0, n_heads) are Q heads, [n_heads, n_heads + n_kv) K heads (which also store the
 // head's V entries).  Cache layout: kv_k_index / kv_v_index.  RoPE: rope.rs:489-524; f16
 // store: kv_cache.rs:573-600.
@@ -890,12 +899,20 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, i
                                                 const float* __restrict__ sinv, const float* __restrict__ q_norm,
                                                 const float* __restrict__ k_norm, float eps, float* __restrict__ qrot,
                                                 uint16_t* __restrict__ kc, float* __restrict__ vc, int layer,
-                                                int kvs, const uint32_t* __restrict__ d_pos) {
+                                                int kvs, const uint32_t* __restrict__ d_pos, int pos0,
+                                                int rope_stride) {
   __shared__ __align__(16) float buf[512];
   __shared__ __align__(16) float sq[512];
   __shared__ float s_scale;
   const int h = blockIdx.x;
   const bool isq = h < n_heads;
+  {  // token blockIdx.y of a prefill chunk: its QKV row, q row, RoPE row and position
+    const size_t t = blockIdx.y;
+    qkv += t * (size_t)(n_heads + 2 * n_kv) * hd;
+    qrot += t * (size_t)n_heads * hd;
+    cosv += t * (size_t)rope_stride;
+    sinv += t * (size_t)rope_stride;
+  }
   const float* src = isq ? qkv + (size_t)h * hd : qkv + (size_t)n_heads * hd + (size_t)(h - n_heads) * hd;
   for (int d = threadIdx.x; d < hd; d += blockDim.x) buf[d] = src[d];
   const float* nw = isq ? q_norm : k_norm;
@@ -922,7 +939,7 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, i
     for (int d = threadIdx.x; d < hd; d += blockDim.x) qrot[(size_t)h * hd + d] = buf[d];
   } else {
     const int kvh = h - n_heads;
-    const int pos = (int)*d_pos;
+    const int pos = (d_pos ? (int)*d_pos : pos0) + (int)blockIdx.y;
     const size_t hbase = kv_head_base(layer, n_kv, kvh, hd, kvs);
     const float* vsrc = qkv + (size_t)(n_heads + n_kv) * hd + (size_t)kvh * hd;
     for (int d = threadIdx.x; d < hd; d += blockDim.x) {

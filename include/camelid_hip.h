@@ -178,6 +178,22 @@ int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const fl
                                  uint32_t layer, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
                                  uint32_t max_pos, const uint32_t* d_pos, float scale,
                                  float* att_out, int8_t* xq, float* xs, void* stream);
+/* q8_gemm_batched (cuda_resident.rs:1494; CPU: the row dot of inference.rs:19871-19905 for
+ * each token): y[t][n] = resid[t][n] + W[n].X[t] for T = tokens activation rows X [tokens][k]
+ * (Q8_0 quants, f32 block scales [tokens][k/32]); output [tokens][rows]; the same
+ * block-ordered fold as the GEMV.  rows % 4 == 0; resid may be NULL; y may alias resid. */
+int camelid_hip_q8_0_gemm(const int8_t* wq, const uint16_t* wd, uint32_t rows, uint32_t k,
+                          const int8_t* xq, const float* xs, uint32_t tokens, float* y,
+                          const float* resid, void* stream);
+/* attention_batched (cuda_resident.rs:1994; CPU inference.rs:23945-24025 per token): causal
+ * attention of `tokens` query rows qrot [tokens][n_heads*hd], row t at position pos0 + t,
+ * over the cache positions [0, pos0 + t] (already stored).  Cache layout as
+ * camelid_hip_rope_kv.  Outputs [tokens][n_heads*hd] (att_out may be NULL) and their Q8_0
+ * quantization.  pos0 + tokens <= max_pos, <= 16384. */
+int camelid_hip_attention_prefill(const float* qrot, const uint16_t* kc, const float* vc,
+                                  uint32_t layer, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
+                                  uint32_t max_pos, uint32_t pos0, uint32_t tokens, float scale,
+                                  float* att_out, int8_t* xq, float* xs, void* stream);
 /* argmax_f32 (cuda_resident.rs:1847; CPU inference.rs:5912). */
 int camelid_hip_argmax(const float* x, uint32_t n, uint32_t* out, void* stream);
 /* Sequential-order f32 sums of rows [rows][n] (n <= 16384), evaluated with the

@@ -80,6 +80,47 @@ def test_q8_gemv_bit_exact(native, orc, rows, k):
                           orc.q8_0_block_dots(wire, rows, k, xq))
 
 
+@pytest.mark.parametrize("rows,k,tokens", [(5120, 3072, 130), (3072, 8192, 64), (2048, 5632, 65), (36, 96, 70),
+                                           (128, 14336, 3), (1000, 2048, 1), (16384, 3072, 33)])
+def test_q8_gemm_bit_exact(native, orc, rows, k, tokens):
+    """Prefill GEMM on the matrix cores == the per-token GEMV fold of the CPU path."""
+    rng = np.random.default_rng(rows + 3 * k + tokens)
+    wire = orc.quantize_q8_0_wire(rng.normal(0, 0.02, rows * k).astype(np.float32))
+    q, d = _repack(native, wire, rows, k)
+    xs = np.empty((tokens, k // 32), np.float32)
+    xq = np.empty((tokens, k), np.int8)
+    for t in range(tokens):
+        xs[t], xq[t] = orc.quantize_q8_0(rng.normal(0, 1 + t % 5, k).astype(np.float32))
+    resid = rng.normal(0, 1, (tokens, rows)).astype(np.float32)
+    wq, wd, dxq, dxs, dres = _dev(q), _dev(d), _dev(xq), _dev(xs), _dev(resid)
+    y = _buf(tokens * rows * 4)
+    _ok(native.camelid_hip_q8_0_gemm(wq.ptr, wd.ptr, rows, k, dxq.ptr, dxs.ptr, tokens, y.ptr, None, None))
+    got = y.download(np.float32, tokens * rows).reshape(tokens, rows)
+    want = np.stack([orc.q8_0_gemv(wire, rows, k, xs[t], xq[t]) for t in range(tokens)])
+    assert np.array_equal(_bits(got), _bits(want))
+    _ok(native.camelid_hip_q8_0_gemm(wq.ptr, wd.ptr, rows, k, dxq.ptr, dxs.ptr, tokens, dres.ptr, dres.ptr, None))
+    assert np.array_equal(_bits(dres.download(np.float32, tokens * rows).reshape(tokens, rows)), _bits(resid + want))
+
+
+def test_q8_gemm_extreme_quants(native, orc):
+    """All -128 quants (largest |int32| block dot), zero-scale rows, through the matrix cores."""
+    rows, k, tokens = 64, 1024, 20
+    wire = np.zeros((rows, k // 32, 34), np.uint8)
+    wire[:, :, :2] = orc.f32_to_f16(np.full((rows, k // 32), 0.5, np.float32)).view(np.uint8).reshape(rows, k // 32, 2)
+    wire[:, :, 2:] = np.uint8(0x80)
+    wire[::3, :, :2] = 0
+    wire = wire.ravel()
+    q, d = _repack(native, wire, rows, k)
+    xq = np.full((tokens, k), -128, np.int8)
+    xq[1::2] = 127
+    xs = np.full((tokens, k // 32), 0.25, np.float32)
+    wq, wd, dxq, dxs = _dev(q), _dev(d), _dev(xq), _dev(xs)
+    y = _buf(rows * tokens * 4)
+    _ok(native.camelid_hip_q8_0_gemm(wq.ptr, wd.ptr, rows, k, dxq.ptr, dxs.ptr, tokens, y.ptr, None, None))
+    want = np.stack([orc.q8_0_gemv(wire, rows, k, xs[t], xq[t]) for t in range(tokens)])
+    assert np.array_equal(_bits(y.download(np.float32, rows * tokens).reshape(tokens, rows)), _bits(want))
+
+
 def test_q8_gemv_extreme_quants(native, orc):
     """All -128 quants on both sides (largest |int32| block dot) and zero scales."""
     rows, k = 64, 1024
@@ -287,6 +328,34 @@ def test_attention_decode_bit_exact(native, orc, nh, nkv, hd, P):
     ws, wq = orc.quantize_q8_0(want)
     assert np.array_equal(_bits(xs.download(np.float32, nh * hd // 32)), _bits(ws))
     assert np.array_equal(xq.download(np.int8, nh * hd), wq)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,pos0,T", [(24, 8, 128, 0, 70), (24, 8, 128, 500, 11), (32, 4, 64, 3, 130),
+                                             (8, 4, 256, 40, 9), (4, 4, 64, 0, 1)])
+def test_attention_prefill_bit_exact(native, orc, nh, nkv, hd, pos0, T):
+    """Causal attention of a prefill chunk == the decode attention of each of its tokens."""
+    rng = np.random.default_rng(pos0 * 31 + T + hd)
+    L, layer = 2, 1
+    max_pos = (pos0 + T + 5 + 7) // 8 * 8
+    kf = rng.normal(0, 1.5, (L, nkv, max_pos, hd)).astype(np.float32)
+    vf = rng.normal(0, 1, (L, nkv, max_pos, hd)).astype(np.float32)
+    kb, vb = orc.f32_to_f16(kf), orc.f32_to_f16(vf)
+    q = rng.normal(0, 1, (T, nh * hd)).astype(np.float32)
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+    kd, vd = _kv_device(kb, orc.f16_to_f32(vb))
+    dq, dk, dv = _dev(q), _dev(kd), _dev(vd)
+    out, xq, xs = _buf(T * nh * hd * 4), _buf(T * nh * hd), _buf(T * nh * hd // 32 * 4)
+    _ok(native.camelid_hip_attention_prefill(dq.ptr, dk.ptr, dv.ptr, layer, nh, nkv, hd, max_pos, pos0, T, scale,
+                                             out.ptr, xq.ptr, xs.ptr, None))
+    got = out.download(np.float32, T * nh * hd).reshape(T, nh * hd)
+    gxq = xq.download(np.int8, T * nh * hd).reshape(T, nh * hd)
+    gxs = xs.download(np.float32, T * nh * hd // 32).reshape(T, nh * hd // 32)
+    kl, vl = orc.f16_to_f32(kb[layer]).ravel(), orc.f16_to_f32(vb[layer]).ravel()
+    for t in range(T):
+        want = orc.attention(q[t], kl, vl, nh, nkv, hd, max_pos, pos0 + t + 1)
+        assert np.array_equal(_bits(got[t]), _bits(want)), f"token {t}"
+        ws, wq = orc.quantize_q8_0(want)
+        assert np.array_equal(_bits(gxs[t]), _bits(ws)) and np.array_equal(gxq[t], wq)
 
 
 @pytest.mark.parametrize("n", [1, 1000, 32000, 128256, 151936])
