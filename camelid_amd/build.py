@@ -32,6 +32,8 @@ HIPCC_FLAGS = [
     "-Wno-unused-result",
     # packed FP32 (v_pk_*_f32) code generation is disabled for every HIP object
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # matrix-core results in VGPRs (the GEMM folds them with VALU code right away)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 GXX_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-pthread", "-Wall"]
 

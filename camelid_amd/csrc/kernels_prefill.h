@@ -27,15 +27,20 @@ typedef int v4i_t __attribute__((ext_vector_type(4)));
 // Workgroup: 4 waves over a 64-row x 64-token tile, each wave 32 x 32 (2 x 2 fragments).
 // Lane l of a fragment supplies row / token l % 16, bytes 8*(l/16) .. +7 of the block, and
 // receives the outputs of rows 4*(l/16) + i (i = 0..3) for token l % 16.
-// Scales are staged in LDS for 32 blocks at a time (transposed: [block][row], [block][token]).
+// Operands move in steps of 4 blocks (128 bytes of every row and token): coalesced 16-byte
+// global loads into registers one step ahead, then into a double-buffered LDS tile laid out
+// [block][8-byte piece][row] (a fragment read is 16 consecutive 8-byte pieces per piece
+// index: no bank conflicts).  Scales are staged in LDS 32 blocks at a time (transposed:
+// [block][row], [block][token]), the next group's held in registers meanwhile.
 // Tiles are dealt so that each XCD (workgroup id mod 8) runs a contiguous range of tiles,
 // token tiles innermost: the row tile's weights are read once per XCD and re-read from its L2.
-// N % 4 == 0 (16-byte output stores); y may alias resid.
+// N % 4 == 0 (16-byte output stores); K % 32 == 0; y may alias resid.
 constexpr int GM_NT = 256;
 constexpr int GM_RN = 64;  // rows per workgroup tile
 constexpr int GM_RT = 64;  // tokens per workgroup tile
 constexpr int GM_BG = 32;  // blocks per scale-staging group
-constexpr int GM_PD = 4;   // operand prefetch distance, blocks
+constexpr int GM_SB = 4;   // blocks per operand step
+constexpr int GM_PS = 80;  // 8-byte pieces per [block][piece] row of the LDS tile (64 + 16 pad)
 
 __host__ __device__ inline int gemm_tiles(int N, int T) {
   return ((N + GM_RN - 1) / GM_RN) * ((T + GM_RT - 1) / GM_RT);
@@ -46,9 +51,13 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq
                                                    int N, int K, const int8_t* __restrict__ xq,
                                                    const float* __restrict__ xs, int T, float* y,
                                                    const float* resid) {
+  static_assert(GM_RN == 64 && GM_RT == 64 && GM_NT == 256 && GM_SB == 4 && GM_BG % GM_SB == 0, "tile layout");
+  __shared__ __align__(16) uint2 sa[2][GM_SB][4][GM_PS];
+  __shared__ __align__(16) uint2 sb[2][GM_SB][4][GM_PS];
   __shared__ __align__(16) uint16_t swd[GM_BG][GM_RN + 4];
   __shared__ __align__(16) float sxs[GM_BG][GM_RT + 1];
   const int NB = K >> 5;
+  const int nsteps = (NB + GM_SB - 1) / GM_SB;
   const int ntt = (T + GM_RT - 1) / GM_RT;
   const int tiles = gemm_tiles(N, T);
   const int per = (tiles + 7) >> 3;
@@ -58,13 +67,61 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int r = lane & 15, g = lane >> 4;
   const int wn = (wave & 1) * 32, wt = (wave >> 1) * 32;
-  const int8_t* ap[2];
-  const int8_t* bp[2];
+
+  // global -> register loads of one step: chunk j of thread tid is 16 bytes of row / token
+  // (tid + 256 j) / 8 at byte (tid % 8) * 16 of the step's 128
+  const int crow = tid >> 3, cc = tid & 7;
+  const int8_t* ga[2];
+  const int8_t* gb[2];
 #pragma unroll
-  for (int f = 0; f < 2; ++f) {
-    ap[f] = wq + (size_t)min(n_base + wn + 16 * f + r, N - 1) * K + 8 * g;
-    bp[f] = xq + (size_t)min(t_base + wt + 16 * f + r, T - 1) * K + 8 * g;
+  for (int j = 0; j < 2; ++j) {
+    ga[j] = wq + (size_t)min(n_base + crow + 32 * j, N - 1) * K;
+    gb[j] = xq + (size_t)min(t_base + crow + 32 * j, T - 1) * K;
   }
+  uint4 ra[2], rb[2];
+  auto gload = [&](int step) {
+    const int off = min(step * 128 + cc * 16, K - 16);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      ra[j] = *reinterpret_cast<const uint4*>(ga[j] + off);
+      rb[j] = *reinterpret_cast<const uint4*>(gb[j] + off);
+    }
+  };
+  auto lds_put = [&](int buf) {  // bytes 0..7 -> piece 2(cc%2), 8..15 -> piece 2(cc%2)+1
+    const int bl = cc >> 1, pc = (cc & 1) * 2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int row = crow + 32 * j;
+      sa[buf][bl][pc][row] = make_uint2(ra[j].x, ra[j].y);
+      sa[buf][bl][pc + 1][row] = make_uint2(ra[j].z, ra[j].w);
+      sb[buf][bl][pc][row] = make_uint2(rb[j].x, rb[j].y);
+      sb[buf][bl][pc + 1][row] = make_uint2(rb[j].z, rb[j].w);
+    }
+  };
+
+  // scale staging: thread tid carries block tid % 32 of rows / tokens tid / 32 + 8 i
+  constexpr int SPT = GM_BG * GM_RN / GM_NT;
+  uint32_t pw[SPT];
+  float px[SPT];
+  auto stage_load = [&](int g0) {
+    const int blk = min(g0 + (tid & 31), NB - 1);
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+      const int row = (tid >> 5) + 8 * i;
+      pw[i] = wd[(size_t)min(n_base + row, N - 1) * NB + blk];
+      px[i] = xs[(size_t)min(t_base + row, T - 1) * NB + blk];
+    }
+  };
+  auto stage_store = [&]() {
+    const int bb = tid & 31;
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+      const int row = (tid >> 5) + 8 * i;
+      swd[bb][row] = (uint16_t)pw[i];
+      sxs[bb][row] = px[i];
+    }
+  };
+
   float acc[2][2][4];
 #pragma unroll
   for (int nf = 0; nf < 2; ++nf)
@@ -72,61 +129,66 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq
     for (int tf = 0; tf < 2; ++tf)
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[nf][tf][i] = 0.0f;
-  long av[GM_PD][2], bv[GM_PD][2];
-  auto load = [&](int s, int b) {  // operands of block b (clamped) into slot s
-    const int bb = min(b, NB - 1) * 32;
+
+  auto block = [&](int buf, int bl, int b) {  // block b = step block bl, from LDS buffer buf
+    long av[2], bv[2];
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
-      av[s][f] = *reinterpret_cast<const long*>(ap[f] + bb);
-      bv[s][f] = *reinterpret_cast<const long*>(bp[f] + bb);
+      av[f] = *reinterpret_cast<const long*>(&sa[buf][bl][g][wn + 16 * f + r]);
+      bv[f] = *reinterpret_cast<const long*>(&sb[buf][bl][g][wt + 16 * f + r]);
     }
+    v4i_t c[2][2];
+#pragma unroll
+    for (int nf = 0; nf < 2; ++nf)
+#pragma unroll
+      for (int tf = 0; tf < 2; ++tf)
+        c[nf][tf] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[nf], bv[tf], v4i_t{0, 0, 0, 0}, 0, 0, 0);
+    const int sl = b & (GM_BG - 1);
+    uint2 w2[2];
+    float xv[2];
+#pragma unroll
+    for (int nf = 0; nf < 2; ++nf) w2[nf] = *reinterpret_cast<const uint2*>(&swd[sl][wn + 16 * nf + 4 * g]);
+#pragma unroll
+    for (int tf = 0; tf < 2; ++tf) xv[tf] = sxs[sl][wt + 16 * tf + r];
+#pragma unroll
+    for (int nf = 0; nf < 2; ++nf)
+#pragma unroll
+      for (int tf = 0; tf < 2; ++tf) {
+        acc[nf][tf][0] += mul_f16_lo((float)c[nf][tf][0], w2[nf].x) * xv[tf];
+        acc[nf][tf][1] += mul_f16_hi((float)c[nf][tf][1], w2[nf].x) * xv[tf];
+        acc[nf][tf][2] += mul_f16_lo((float)c[nf][tf][2], w2[nf].y) * xv[tf];
+        acc[nf][tf][3] += mul_f16_hi((float)c[nf][tf][3], w2[nf].y) * xv[tf];
+      }
   };
-#pragma unroll
-  for (int s = 0; s < GM_PD; ++s) load(s, s);
-  for (int b0 = 0; b0 < NB; b0 += GM_PD) {
-    if (b0 % GM_BG == 0) {
-      __syncthreads();  // the previous group's scales are consumed
-      for (int e = tid; e < GM_BG * GM_RN; e += GM_NT) {
-        const int row = e / GM_BG, bb = e % GM_BG;
-        const int blk = min(b0 + bb, NB - 1);
-        swd[bb][row] = wd[(size_t)min(n_base + row, N - 1) * NB + blk];
-      }
-      for (int e = tid; e < GM_BG * GM_RT; e += GM_NT) {
-        const int tok = e / GM_BG, bb = e % GM_BG;
-        const int blk = min(b0 + bb, NB - 1);
-        sxs[bb][tok] = xs[(size_t)min(t_base + tok, T - 1) * NB + blk];
-      }
-      __syncthreads();
+
+  stage_load(0);
+  gload(0);
+  stage_store();
+  if (GM_BG < NB) stage_load(GM_BG);
+  lds_put(0);
+  __syncthreads();
+  for (int s = 0; s < nsteps; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < nsteps) gload(s + 1);
+    const int b0 = s * GM_SB;
+    if (b0 + GM_SB <= NB) {
+      block(buf, 0, b0);
+      block(buf, 1, b0 + 1);
+      block(buf, 2, b0 + 2);
+      block(buf, 3, b0 + 3);
+    } else {  // the last, partial step
+      for (int bl = 0; bl < NB - b0; ++bl) block(buf, bl, b0 + bl);
     }
-#pragma unroll
-    for (int s = 0; s < GM_PD; ++s) {
-      const int b = b0 + s;
-      if (b < NB) {
-        v4i_t c[2][2];
-#pragma unroll
-        for (int nf = 0; nf < 2; ++nf)
-#pragma unroll
-          for (int tf = 0; tf < 2; ++tf)
-            c[nf][tf] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[s][nf], bv[s][tf], v4i_t{0, 0, 0, 0}, 0, 0, 0);
-        load(s, b + GM_PD);
-        const int bl = b % GM_BG;
-        uint2 w2[2];
-        float xv[2];
-#pragma unroll
-        for (int nf = 0; nf < 2; ++nf) w2[nf] = *reinterpret_cast<const uint2*>(&swd[bl][wn + 16 * nf + 4 * g]);
-#pragma unroll
-        for (int tf = 0; tf < 2; ++tf) xv[tf] = sxs[bl][wt + 16 * tf + r];
-#pragma unroll
-        for (int nf = 0; nf < 2; ++nf)
-#pragma unroll
-          for (int tf = 0; tf < 2; ++tf) {
-            acc[nf][tf][0] += mul_f16_lo((float)c[nf][tf][0], w2[nf].x) * xv[tf];
-            acc[nf][tf][1] += mul_f16_hi((float)c[nf][tf][1], w2[nf].x) * xv[tf];
-            acc[nf][tf][2] += mul_f16_lo((float)c[nf][tf][2], w2[nf].y) * xv[tf];
-            acc[nf][tf][3] += mul_f16_hi((float)c[nf][tf][3], w2[nf].y) * xv[tf];
-          }
+    if (s + 1 < nsteps) {
+      lds_put(buf ^ 1);
+      if (((s + 1) * GM_SB) % GM_BG == 0) {  // next step opens a new scale group
+        __syncthreads();  // every wave is done with this group's scales
+        stage_store();
+        const int g_next = (s + 1) * GM_SB + GM_BG;
+        if (g_next < NB) stage_load(g_next);
       }
     }
+    __syncthreads();
   }
 #pragma unroll
   for (int nf = 0; nf < 2; ++nf)
