@@ -81,6 +81,10 @@ SIGNATURES: dict[str, tuple] = {
     "camelid_hip_q8_0_gemm": (C.c_int, [vp, vp, C.c_uint32, C.c_uint32, vp, vp, C.c_uint32, vp, vp, vp]),
     "camelid_hip_attention_prefill": (C.c_int, [vp, vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                                 C.c_uint32, C.c_uint32, C.c_uint32, C.c_float, vp, vp, vp, vp]),
+    "camelid_hip_quantize_q8_k": (C.c_int, [vp, C.c_uint32, vp, vp, vp, vp]),
+    "camelid_kquant_repack": (C.c_int, [C.c_uint8, u8p, C.c_size_t, C.c_size_t, u8p, u8p, i8p, u16p]),
+    "camelid_hip_kquant_gemv": (C.c_int, [C.c_uint8, vp, vp, vp, vp, C.c_uint32, C.c_uint32, vp, vp, vp, vp, vp,
+                                          vp]),
     "camelid_hip_argmax": (C.c_int, [vp, C.c_uint32, vp, vp]),
     "camelid_hip_inorder_sum_rows": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp]),
     "camelid_hip_expf": (C.c_int, [vp, vp, C.c_size_t, vp]),
@@ -92,6 +96,8 @@ SIGNATURES: dict[str, tuple] = {
     "camelid_synth_normal_f32": (None, [C.c_char_p, C.c_uint64, C.c_float, f32p, C.c_uint64]),
     "camelid_synth_q8_0_wire": (C.c_int, [C.c_char_p, C.c_uint64, C.c_float, C.c_uint64, u8p]),
     "camelid_synth_tokens": (None, [C.c_uint64, C.c_uint32, C.c_uint32, u32p]),
+    "camelid_synth_kquant_wire": (C.c_int, [C.c_char_p, C.c_uint64, C.c_float, C.c_uint64, C.c_int, u8p]),
+    "camelid_embed_kquant": (C.c_int, [C.c_int, u8p, C.c_uint32, C.c_uint32, u32p, C.c_uint32, f32p]),
 }
 
 _lib = None

@@ -33,6 +33,7 @@
 #include "../../include/camelid_hip.h"
 #include "kernels_decode.h"
 #include "kernels_prefill.h"
+#include "kernels_kquant.h"
 
 namespace {
 
@@ -44,8 +45,30 @@ struct Q8Mat {
   uint32_t rows = 0, k = 0;
 };
 
+// A K-quant matrix as planes split out of its GGUF superblocks (kernels_kquant.h):
+// Q4_K: a = nibbles [rows][k/2], b = headers [rows][k/256][16];
+// Q6_K: a = ql [rows][k/2], b = qh [rows][k/4], sc = scales [rows][k/256][16], d = f16 [rows][k/256].
+struct KMat {
+  uint8_t quant = 0;
+  uint8_t* a = nullptr;
+  uint8_t* b = nullptr;
+  int8_t* sc = nullptr;
+  uint16_t* d = nullptr;
+  uint32_t rows = 0, k = 0;
+};
+
+// One projection in its own format (the layers with any K-quant projection keep all seven
+// separately; all-Q8_0 layers use the fused QKV / gate|up matrices below).
+struct Proj {
+  uint8_t quant = CAMELID_Q8_0;
+  Q8Mat q8;
+  KMat kq;
+};
+
 struct LayerW {
   Q8Mat qkv, o, gu, down;
+  bool generic = false;  // some projection is a K-quant: seven separate projections in p
+  Proj p[7];
   float* attn_norm = nullptr;
   float* ffn_norm = nullptr;
   float* q_norm = nullptr;
@@ -64,10 +87,21 @@ struct camelid_hip_engine {
   hipStream_t stream = nullptr;
   std::vector<LayerW> layers;
   Q8Mat out;
+  KMat out_k;                 // K-quant lm_head (out_quant != Q8_0)
+  uint8_t out_quant = CAMELID_Q8_0;
   float* out_norm = nullptr;
   bool out_set = false;
   Q8Mat embd;
+  KMat embd_k;                // K-quant token table (embd_quant != Q8_0)
+  uint8_t embd_quant = CAMELID_Q8_0;
   bool embd_set = false;
+  bool any_kquant = false;
+  // K-quant activations: the f32 input of the next projection and its Q8_K quantization
+  float* xn = nullptr;        // [max(H, F, nq)]
+  float* actf = nullptr;      // SwiGLU output [F]
+  float* kd = nullptr;        // Q8_K block scales
+  int8_t* kq = nullptr;       // Q8_K quants
+  int32_t* kbs = nullptr;     // per-32 quant sums
   uint16_t* kc = nullptr;  // K, granules of 8 dims per position (cm::kv_k_index)
   float* vc = nullptr;     // V (f16-rounded f32), granules of 4 positions per dim (cm::kv_v_index)
   uint32_t kvs = 0;        // KV position stride: max_pos rounded up to a multiple of 8
@@ -240,6 +274,65 @@ int upload_q8(camelid_hip_engine* e, Q8Mat* m, const std::vector<Part>& parts, u
   m->k = k;
   HIP_TRY(e, hipMemcpy(m->q, q.data(), q.size(), hipMemcpyHostToDevice));
   HIP_TRY(e, hipMemcpy(m->d, d.data(), d.size() * 2, hipMemcpyHostToDevice));
+  return 0;
+}
+
+// Split rows of K-quant wire superblocks into the KMat planes (host).
+void kq_split_rows(uint8_t quant, const uint8_t* src, size_t r0, size_t r1, size_t k, uint8_t* a, uint8_t* b,
+                   int8_t* sc, uint16_t* d) {
+  const size_t nsb = k / 256, bb = quant == CAMELID_Q4_K ? 144 : 210;
+  for (size_t r = r0; r < r1; ++r)
+    for (size_t s = 0; s < nsb; ++s) {
+      const uint8_t* blk = src + (r * nsb + s) * bb;
+      const size_t sb = r * nsb + s;
+      if (quant == CAMELID_Q4_K) {
+        std::memcpy(b + sb * 16, blk, 16);
+        std::memcpy(a + sb * 128, blk + 16, 128);
+      } else {
+        std::memcpy(a + sb * 128, blk, 128);
+        std::memcpy(b + sb * 64, blk + 128, 64);
+        std::memcpy(sc + sb * 16, blk + 192, 16);
+        d[sb] = read_le16(blk + 208);
+      }
+    }
+}
+
+size_t kq_block_bytes(uint8_t quant) { return quant == CAMELID_Q4_K ? 144 : 210; }
+
+int upload_kq(camelid_hip_engine* e, KMat* m, const uint8_t* src, size_t len, uint32_t rows, uint32_t k,
+              uint8_t quant) {
+  if (quant != CAMELID_Q4_K && quant != CAMELID_Q6_K) return fail(e, "unknown weight format");
+  if (!src) return fail(e, "missing projection bytes");
+  if (k % 256) return fail(e, "K-quant row width must be a multiple of 256");
+  const size_t nsb = k / 256, want = (size_t)rows * nsb * kq_block_bytes(quant);
+  if (len != want) return fail(e, "K-quant byte length " + std::to_string(len) + " != expected " + std::to_string(want));
+  std::vector<uint8_t> a((size_t)rows * k / 2), b((size_t)rows * nsb * (quant == CAMELID_Q4_K ? 16 : 64));
+  std::vector<int8_t> sc(quant == CAMELID_Q6_K ? (size_t)rows * nsb * 16 : 0);
+  std::vector<uint16_t> d(quant == CAMELID_Q6_K ? (size_t)rows * nsb : 0);
+  {
+    unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    if (rows < 4096) nt = 1;
+    std::vector<std::thread> th;
+    for (unsigned t = 0; t < nt; ++t)
+      th.emplace_back(kq_split_rows, quant, src, (size_t)rows * t / nt, (size_t)rows * (t + 1) / nt, (size_t)k,
+                      a.data(), b.data(), sc.data(), d.data());
+    for (auto& x : th) x.join();
+  }
+  if (!m->a) {
+    if (dev_alloc(e, &m->a, a.size()) || dev_alloc(e, &m->b, b.size())) return 1;
+    if (quant == CAMELID_Q6_K && (dev_alloc(e, &m->sc, sc.size()) || dev_alloc(e, &m->d, d.size()))) return 1;
+  } else if (m->rows != rows || m->k != k || m->quant != quant) {
+    return fail(e, "matrix shape changed on re-upload");
+  }
+  m->quant = quant;
+  m->rows = rows;
+  m->k = k;
+  HIP_TRY(e, hipMemcpy(m->a, a.data(), a.size(), hipMemcpyHostToDevice));
+  HIP_TRY(e, hipMemcpy(m->b, b.data(), b.size(), hipMemcpyHostToDevice));
+  if (quant == CAMELID_Q6_K) {
+    HIP_TRY(e, hipMemcpy(m->sc, sc.data(), sc.size(), hipMemcpyHostToDevice));
+    HIP_TRY(e, hipMemcpy(m->d, d.data(), d.size() * 2, hipMemcpyHostToDevice));
+  }
   return 0;
 }
 
@@ -428,6 +521,39 @@ int attn_ring_slots(uint32_t kvs) {
   return slots >= 2 ? (int)slots : 0;
 }
 
+// Algorithmic bytes of one K-quant GEMV launch: superblocks (144 or 210 B per 256 values),
+// the Q8_K activation (K + K/256 * 4 + K/32 * 4 bytes), the output (+ residual).
+double kq_bytes(const KMat& m, bool resid) {
+  return (double)m.rows * (m.k / 256) * kq_block_bytes(m.quant) + m.k * (1.0 + 4.0 / 256 + 4.0 / 32) +
+         m.rows * (resid ? 8.0 : 4.0);
+}
+
+// K-quant GEMV (+ residual, + per-workgroup argmax partials when part_v is set); returns
+// the number of workgroups.
+uint32_t launch_kgemv(const KMat& m, const float* yd, const int8_t* yq, const int32_t* ybs, float* y,
+                      const float* resid, float* part_v, uint32_t* part_i, hipStream_t s) {
+  const int rpw = m.rows >= 16384 ? 2 : 1;
+  const uint32_t R = 4 * rpw, grid = (m.rows + R - 1) / R;
+  if (m.quant == CAMELID_Q4_K) {
+    const size_t lds = cm::kq4_lds_bytes((int)m.k, (int)R);
+    if (rpw == 2)
+      CM_LAUNCH(cm::k_gemv_q4k<2>, dim3(grid), dim3(cm::KQ_NT), lds, s, m.a, m.b, (int)m.rows, (int)m.k, yd, yq, ybs,
+                y, resid, part_v, part_i);
+    else
+      CM_LAUNCH(cm::k_gemv_q4k<1>, dim3(grid), dim3(cm::KQ_NT), lds, s, m.a, m.b, (int)m.rows, (int)m.k, yd, yq, ybs,
+                y, resid, part_v, part_i);
+  } else {
+    const size_t lds = cm::kq6_lds_bytes((int)m.k, (int)R);
+    if (rpw == 2)
+      CM_LAUNCH(cm::k_gemv_q6k<2>, dim3(grid), dim3(cm::KQ_NT), lds, s, m.a, m.b, m.sc, m.d, (int)m.rows, (int)m.k,
+                yd, yq, y, resid, part_v, part_i);
+    else
+      CM_LAUNCH(cm::k_gemv_q6k<1>, dim3(grid), dim3(cm::KQ_NT), lds, s, m.a, m.b, m.sc, m.d, (int)m.rows, (int)m.k,
+                yd, yq, y, resid, part_v, part_i);
+  }
+  return grid;
+}
+
 void gemv(camelid_hip_engine* e, const Q8Mat& m, float* y, const float* resid, const int8_t* xq = nullptr,
           const float* xs = nullptr) {
   ProfScope ps(e, P_GEMV, q8_bytes(m, resid != nullptr));
@@ -440,11 +566,75 @@ void rmsnorm(camelid_hip_engine* e, const float* w, const Q8Mat* next) {
   launch_rmsnorm_quant(e->h, w, n, e->d.eps, e->xq, e->xs, nullptr, e->stream, e->read_ahead ? next : nullptr);
 }
 
+// Q8_K quantization of n values (the K-quant projections' activation).
+void quant_q8k(camelid_hip_engine* e, const float* x, uint32_t n) {
+  ProfScope ps(e, P_NORM, n * 4.0 + n * (1.0 + 4.0 / 256 + 4.0 / 32));
+  CM_LAUNCH(cm::k_quantize_q8k, dim3(n / 256), dim3(256), 0, e->stream, x, e->kd, e->kq, e->kbs);
+}
+
+// One projection in its own format: Q8_0 from the Q8_0 activation, K-quants from the Q8_K one.
+void proj(camelid_hip_engine* e, const Proj& p, float* y, const float* resid) {
+  if (p.quant == CAMELID_Q8_0) {
+    gemv(e, p.q8, y, resid);
+  } else {
+    ProfScope ps(e, P_GEMV, kq_bytes(p.kq, resid != nullptr));
+    launch_kgemv(p.kq, e->kd, e->kq, e->kbs, y, resid, nullptr, nullptr, e->stream);
+  }
+}
+
+// A layer with K-quant projections (forward_layer_timed, inference.rs:6228-6807): the same
+// order as run_layer, with each projection in its own format; the RMSNorm kernel also writes
+// the normalized row, which is quantized to Q8_K when a K-quant projection reads it.
+void run_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cos_base, const float* sin_base,
+                       int rope_stride, float scale) {
+  const camelid_hip_dims& d = e->d;
+  const LayerW& L = e->layers[l];
+  hipStream_t s = e->stream;
+  const uint32_t nq = d.n_heads * d.head_dim, nkv = d.n_kv_heads * d.head_dim;
+  auto is_k = [&](int i) { return L.p[i].quant != CAMELID_Q8_0; };
+  {
+    ProfScope ps(e, P_NORM, d.hidden * 12.0 + d.hidden * 34.0 / 32.0);
+    launch_rmsnorm_quant(e->h, L.attn_norm, d.hidden, d.eps, e->xq, e->xs, e->xn, s);
+  }
+  if (is_k(0) || is_k(1) || is_k(2)) quant_q8k(e, e->xn, d.hidden);
+  proj(e, L.p[0], e->qkv, nullptr);
+  proj(e, L.p[1], e->qkv + nq, nullptr);
+  proj(e, L.p[2], e->qkv + nq + nkv, nullptr);
+  {
+    ProfScope ps(e, P_ATTN, (nq + 2.0 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0));
+    launch_attention<true>(d.head_dim, d.n_heads, e->att_slots, s, e->qkv, (int)d.n_heads, (int)d.n_kv_heads,
+                           (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base, rope_stride, L.q_norm,
+                           L.k_norm, d.eps, e->kc, e->vc, (int)l, (int)e->kvs, &e->st->pos, scale, e->att, e->xq,
+                           e->xs, nullptr);
+  }
+  if (is_k(3)) quant_q8k(e, e->att, nq);
+  proj(e, L.p[3], e->h, e->h);
+  {
+    ProfScope ps(e, P_NORM, d.hidden * 12.0 + d.hidden * 34.0 / 32.0);
+    launch_rmsnorm_quant(e->h, L.ffn_norm, d.hidden, d.eps, e->xq, e->xs, e->xn, s);
+  }
+  if (is_k(4) || is_k(5)) quant_q8k(e, e->xn, d.hidden);
+  proj(e, L.p[4], e->gu, nullptr);
+  proj(e, L.p[5], e->gu + d.ffn_dim, nullptr);
+  {
+    ProfScope ps(e, P_SILU, d.ffn_dim * 12.0 + d.ffn_dim * 34.0 / 32.0);
+    const cm::Prefetch pf{nullptr, 0, nullptr, 0};
+    CM_LAUNCH(cm::k_silu_mul_quant, dim3((d.ffn_dim + 255) / 256), dim3(256), 0, s, e->gu, (int)d.ffn_dim, e->xq,
+              e->xs, e->actf, pf);
+  }
+  if (is_k(6)) quant_q8k(e, e->actf, d.ffn_dim);
+  proj(e, L.p[6], e->h, e->h);
+}
+
 // One transformer layer at StepState.pos; RoPE tables at cos_base + pos*rope_stride.
 void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const float* sin_base, int rope_stride,
                float scale) {
   const camelid_hip_dims& d = e->d;
   const LayerW& L = e->layers[l];
+  if (L.generic) {
+    run_layer_generic(e, l, cos_base, sin_base, rope_stride, scale);
+    return;
+  }
   hipStream_t s = e->stream;
   const double nq = (double)d.n_heads * d.head_dim, nkv = (double)d.n_kv_heads * d.head_dim;
   rmsnorm(e, L.attn_norm, &L.qkv);
@@ -498,12 +688,20 @@ void run_stack(camelid_hip_engine* e, const float* cos_base, const float* sin_ba
 
 // Final norm, lm_head and greedy argmax; advances StepState (pos+1, tok, tokens[step]).
 void run_head(camelid_hip_engine* e, uint32_t* tokens, uint32_t cap) {
-  rmsnorm(e, e->out_norm, nullptr);
-  const Q8Mat& m = e->out;
   uint32_t nparts;
-  {
+  if (e->out_quant == CAMELID_Q8_0) {
+    rmsnorm(e, e->out_norm, nullptr);
+    const Q8Mat& m = e->out;
     ProfScope ps(e, P_GEMV, q8_bytes(m, false));
     nparts = launch_gemv_argmax(m, e->xq, e->xs, e->logits, e->part_v, e->part_i, e->stream);
+  } else {
+    {
+      ProfScope ps(e, P_NORM, e->d.hidden * 12.0 + e->d.hidden * 34.0 / 32.0);
+      launch_rmsnorm_quant(e->h, e->out_norm, e->d.hidden, e->d.eps, e->xq, e->xs, e->xn, e->stream);
+    }
+    quant_q8k(e, e->xn, e->d.hidden);
+    ProfScope ps(e, P_GEMV, kq_bytes(e->out_k, false));
+    nparts = launch_kgemv(e->out_k, e->kd, e->kq, e->kbs, e->logits, nullptr, e->part_v, e->part_i, e->stream);
   }
   ProfScope ps(e, P_HEAD, 0.0);
   CM_LAUNCH(cm::k_argmax_finish, dim3(1), dim3(1024), 0, e->stream, e->part_v, e->part_i, (int)nparts, e->st,
@@ -513,8 +711,15 @@ void run_head(camelid_hip_engine* e, uint32_t* tokens, uint32_t cap) {
 void run_embed(camelid_hip_engine* e) {
   const camelid_hip_dims& d = e->d;
   ProfScope ps(e, P_EMBED, d.hidden * (34.0 / 32.0 + 4.0));
-  CM_LAUNCH(cm::k_embed_q8, dim3((d.hidden + 255) / 256), dim3(256), 0, e->stream, e->embd.q, e->embd.d,
-                     (int)d.hidden, e->st, e->h);
+  if (e->embd_quant == CAMELID_Q4_K)
+    CM_LAUNCH(cm::k_embed_q4k, dim3(d.hidden / 256), dim3(256), 0, e->stream, e->embd_k.a, e->embd_k.b,
+              (int)d.hidden, e->st, e->h);
+  else if (e->embd_quant == CAMELID_Q6_K)
+    CM_LAUNCH(cm::k_embed_q6k, dim3(d.hidden / 256), dim3(256), 0, e->stream, e->embd_k.a, e->embd_k.b,
+              e->embd_k.sc, e->embd_k.d, (int)d.hidden, e->st, e->h);
+  else
+    CM_LAUNCH(cm::k_embed_q8, dim3((d.hidden + 255) / 256), dim3(256), 0, e->stream, e->embd.q, e->embd.d,
+              (int)d.hidden, e->st, e->h);
 }
 
 // ---------------------------------------------------------------- batched prefill
@@ -681,7 +886,9 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
            dev_alloc(e, &e->hidden_cap, (size_t)(d.n_layers + 1) * d.hidden) || dev_alloc(e, &e->xq, act) ||
            dev_alloc(e, &e->xs, act / 32) || dev_alloc(e, &e->cos_cur, half) || dev_alloc(e, &e->sin_cur, half) ||
            dev_alloc(e, &e->part_v, nparts) || dev_alloc(e, &e->part_i, nparts) || dev_alloc(e, &e->st, 1) ||
-           dev_alloc(e, &e->tokens, e->tokens_cap) || host_alloc(e, &e->p_emb, d.hidden) ||
+           dev_alloc(e, &e->tokens, e->tokens_cap) || dev_alloc(e, &e->xn, act) || dev_alloc(e, &e->actf, d.ffn_dim) ||
+           dev_alloc(e, &e->kd, act / 256 + 1) || dev_alloc(e, &e->kq, act) || dev_alloc(e, &e->kbs, act / 32) ||
+           host_alloc(e, &e->p_emb, d.hidden) ||
            host_alloc(e, &e->p_cos, half) || host_alloc(e, &e->p_sin, half) || host_alloc(e, &e->p_logits, d.vocab) ||
            host_alloc(e, &e->p_st, 1);
   if (rc) {
@@ -718,12 +925,38 @@ int camelid_hip_set_layer(camelid_hip_engine* e, uint32_t layer, const uint8_t* 
   if (layer >= e->d.n_layers) return fail(e, "layer index out of range");
   if (!w || !len || !quant || !attn_norm || !ffn_norm) return fail(e, "null argument");
   if ((q_norm == nullptr) != (k_norm == nullptr)) return fail(e, "q_norm and k_norm must be given together");
-  for (int i = 0; i < 7; ++i)
-    if (quant[i] != CAMELID_Q8_0) return fail(e, "only Q8_0 projections are supported by this build");
+  bool all_q8 = true;
+  for (int i = 0; i < 7; ++i) {
+    if (quant[i] != CAMELID_Q8_0 && quant[i] != CAMELID_Q4_K && quant[i] != CAMELID_Q6_K)
+      return fail(e, "unknown projection format");
+    all_q8 = all_q8 && quant[i] == CAMELID_Q8_0;
+  }
   HIP_TRY(e, hipSetDevice(e->device));
   const camelid_hip_dims& d = e->d;
   const uint32_t nq = d.n_heads * d.head_dim, nkv = d.n_kv_heads * d.head_dim;
   LayerW& L = e->layers[layer];
+  if (L.set && L.generic == all_q8) return fail(e, "a layer's formats cannot change after upload");
+  if (!all_q8) {
+    // seven separate projections, each in its own format
+    const uint32_t rows[7] = {nq, nkv, nkv, d.hidden, d.ffn_dim, d.ffn_dim, d.hidden};
+    const uint32_t ks[7] = {d.hidden, d.hidden, d.hidden, nq, d.hidden, d.hidden, d.ffn_dim};
+    for (int i = 0; i < 7; ++i) {
+      Proj& P = L.p[i];
+      if (L.set && P.quant != quant[i]) return fail(e, "a layer's formats cannot change after upload");
+      P.quant = quant[i];
+      const int rc = quant[i] == CAMELID_Q8_0 ? upload_q8(e, &P.q8, {{w[i], len[i], rows[i]}}, ks[i], q8_layout)
+                                              : upload_kq(e, &P.kq, w[i], len[i], rows[i], ks[i], quant[i]);
+      if (rc) return 1;
+    }
+    if (upload_f32(e, &L.attn_norm, attn_norm, d.hidden) || upload_f32(e, &L.ffn_norm, ffn_norm, d.hidden)) return 1;
+    if (q_norm && (upload_f32(e, &L.q_norm, q_norm, d.head_dim) || upload_f32(e, &L.k_norm, k_norm, d.head_dim)))
+      return 1;
+    L.generic = true;
+    L.set = true;
+    e->any_kquant = true;
+    drop_graph(e);
+    return 0;
+  }
   if (upload_q8(e, &L.qkv, {{w[0], len[0], nq}, {w[1], len[1], nkv}, {w[2], len[2], nkv}}, d.hidden, q8_layout) ||
       upload_q8(e, &L.o, {{w[3], len[3], d.hidden}}, nq, q8_layout) ||
       upload_q8(e, &L.gu, {{w[4], len[4], d.ffn_dim}, {w[5], len[5], d.ffn_dim}}, d.hidden, q8_layout,
@@ -742,11 +975,15 @@ int camelid_hip_set_output(camelid_hip_engine* e, const float* final_norm, const
                            uint8_t q8_layout) {
   if (!e) return fail(nullptr, "null engine");
   if (!final_norm || !w) return fail(e, "null argument");
-  if (quant != CAMELID_Q8_0) return fail(e, "only a Q8_0 output projection is supported by this build");
+  if (quant != CAMELID_Q8_0 && quant != CAMELID_Q4_K && quant != CAMELID_Q6_K)
+    return fail(e, "unknown output projection format");
+  if (e->out_set && quant != e->out_quant) return fail(e, "the output format cannot change after upload");
   HIP_TRY(e, hipSetDevice(e->device));
-  if (upload_q8(e, &e->out, {{w, len, e->d.vocab}}, e->d.hidden, q8_layout) ||
-      upload_f32(e, &e->out_norm, final_norm, e->d.hidden))
-    return 1;
+  const int rc = quant == CAMELID_Q8_0 ? upload_q8(e, &e->out, {{w, len, e->d.vocab}}, e->d.hidden, q8_layout)
+                                       : upload_kq(e, &e->out_k, w, len, e->d.vocab, e->d.hidden, quant);
+  if (rc || upload_f32(e, &e->out_norm, final_norm, e->d.hidden)) return 1;
+  e->out_quant = quant;
+  if (quant != CAMELID_Q8_0) e->any_kquant = true;
   e->out_set = true;
   drop_graph(e);
   return 0;
@@ -755,9 +992,14 @@ int camelid_hip_set_output(camelid_hip_engine* e, const float* final_norm, const
 int camelid_hip_set_embedding(camelid_hip_engine* e, const uint8_t* w, size_t len, uint8_t quant, uint8_t q8_layout) {
   if (!e) return fail(nullptr, "null engine");
   if (!w) return fail(e, "null argument");
-  if (quant != CAMELID_Q8_0) return fail(e, "only a Q8_0 token embedding is supported by this build");
+  if (quant != CAMELID_Q8_0 && quant != CAMELID_Q4_K && quant != CAMELID_Q6_K)
+    return fail(e, "unknown embedding format");
+  if (e->embd_set && quant != e->embd_quant) return fail(e, "the embedding format cannot change after upload");
   HIP_TRY(e, hipSetDevice(e->device));
-  if (upload_q8(e, &e->embd, {{w, len, e->d.vocab}}, e->d.hidden, q8_layout)) return 1;
+  const int rc = quant == CAMELID_Q8_0 ? upload_q8(e, &e->embd, {{w, len, e->d.vocab}}, e->d.hidden, q8_layout)
+                                       : upload_kq(e, &e->embd_k, w, len, e->d.vocab, e->d.hidden, quant);
+  if (rc) return 1;
+  e->embd_quant = quant;
   e->embd_set = true;
   drop_graph(e);
   return 0;
@@ -789,7 +1031,7 @@ int camelid_hip_set_filled(camelid_hip_engine* e, uint32_t filled) {
 }
 uint32_t camelid_hip_max_pos(const camelid_hip_engine* e) { return e ? e->d.max_pos : 0; }
 uint32_t camelid_hip_n_layers(const camelid_hip_engine* e) { return e ? e->d.n_layers : 0; }
-int camelid_hip_uses_kquant(const camelid_hip_engine*) { return 0; }
+int camelid_hip_uses_kquant(const camelid_hip_engine* e) { return e && e->any_kquant ? 1 : 0; }
 
 int camelid_hip_seed_layer(camelid_hip_engine* e, uint32_t layer, const float* ck, const float* cv, uint32_t n_pos) {
   if (!e) return fail(nullptr, "null engine");
@@ -908,7 +1150,9 @@ int camelid_hip_prefill(camelid_hip_engine* e, const float* embs, const float* c
       rc = fail(e, "prefill staging copy failed");
       break;
     }
-    if (e->prefill_batched) {
+    bool generic = false;
+    for (const LayerW& L : e->layers) generic = generic || L.generic;
+    if (e->prefill_batched && !generic) {
       // chunks of PREFILL_CHUNK tokens, every layer over the whole chunk
       if (ensure_prefill_buffers(e)) {
         rc = 1;
@@ -921,7 +1165,8 @@ int camelid_hip_prefill(camelid_hip_engine* e, const float* embs, const float* c
         prefill_chunk(e, d_cos + (size_t)c0 * half, d_sin + (size_t)c0 * half, T, e->filled + c0, scale);
       }
     } else {
-      // one decode step per token
+      // one decode step per token (the path of layers with K-quant projections, whose CPU
+      // prefill is likewise a per-token loop of block dots, inference.rs:2462-2473)
       for (uint32_t t = 0; t < n; ++t) {
         (void)hipMemcpyAsync(e->h, d_embs + (size_t)t * d.hidden, d.hidden * 4, hipMemcpyDeviceToDevice, e->stream);
         (void)hipMemcpyAsync(e->st, d_sts + t, sizeof(cm::StepState), hipMemcpyDeviceToDevice, e->stream);
@@ -1194,6 +1439,42 @@ int camelid_hip_attention_prefill(const float* qrot, const uint16_t* kc, const f
   launch_attn_prefill(hd, n_heads, n_kv, tokens, qrot, kc, vc, (int)layer, (int)max_pos, (int)pos0, scale, att_out,
                       xq, xs, (hipStream_t)stream);
   return launch_status("attention_prefill");
+}
+
+int camelid_hip_quantize_q8_k(const float* x, uint32_t n, float* yd, int8_t* yq, int32_t* ybs, void* stream) {
+  if (!x || !yd || !yq || !ybs) return fail(nullptr, "null argument");
+  if (n == 0 || n % 256) return fail(nullptr, "n must be a nonzero multiple of 256");
+  hipLaunchKernelGGL(cm::k_quantize_q8k, dim3(n / 256), dim3(256), 0, (hipStream_t)stream, x, yd, yq, ybs);
+  return launch_status("quantize_q8_k");
+}
+
+int camelid_kquant_repack(uint8_t quant, const uint8_t* src, size_t rows, size_t k, uint8_t* a, uint8_t* b,
+                          int8_t* sc, uint16_t* d) {
+  if (!src || !a || !b) return fail(nullptr, "null argument");
+  if (quant != CAMELID_Q4_K && quant != CAMELID_Q6_K) return fail(nullptr, "quant must be Q4_K or Q6_K");
+  if (quant == CAMELID_Q6_K && (!sc || !d)) return fail(nullptr, "null argument");
+  if (k % 256) return fail(nullptr, "k must be a multiple of 256");
+  kq_split_rows(quant, src, 0, rows, k, a, b, sc, d);
+  return 0;
+}
+
+int camelid_hip_kquant_gemv(uint8_t quant, const uint8_t* a, const uint8_t* b, const int8_t* sc, const uint16_t* d,
+                            uint32_t rows, uint32_t k, const float* yd, const int8_t* yq, const int32_t* ybs,
+                            float* y, const float* resid, void* stream) {
+  if (!a || !b || !yd || !yq || !ybs || !y) return fail(nullptr, "null argument");
+  if (quant != CAMELID_Q4_K && quant != CAMELID_Q6_K) return fail(nullptr, "quant must be Q4_K or Q6_K");
+  if (quant == CAMELID_Q6_K && (!sc || !d)) return fail(nullptr, "null argument");
+  if (rows == 0 || k == 0 || k % 256 || k > 16384) return fail(nullptr, "k must be a multiple of 256, at most 16384");
+  KMat m;
+  m.quant = quant;
+  m.a = const_cast<uint8_t*>(a);
+  m.b = const_cast<uint8_t*>(b);
+  m.sc = const_cast<int8_t*>(sc);
+  m.d = const_cast<uint16_t*>(d);
+  m.rows = rows;
+  m.k = k;
+  launch_kgemv(m, yd, yq, ybs, y, resid, nullptr, nullptr, (hipStream_t)stream);
+  return launch_status("kquant_gemv");
 }
 
 int camelid_hip_argmax(const float* x, uint32_t n, uint32_t* out, void* stream) {

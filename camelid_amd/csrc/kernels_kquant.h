@@ -1,0 +1,363 @@
+// kernels_kquant.h -- HIP/CDNA4 kernels of the K-quant decode path (Q4_K / Q6_K weights,
+// Q8_K activations; gfx950, wave64).
+//
+// Weights are kept in HBM as planes split out of the GGUF superblocks (same bytes, so the
+// algorithmic bytes stay 144 B / 256 for Q4_K and 210 B / 256 for Q6_K):
+//   Q4_K: nibbles [rows][K/2], header [rows][K/256][16] = (f16 d, f16 dmin, 12 scale bytes)
+//   Q6_K: ql [rows][K/2], qh [rows][K/4], scales [rows][K/256][16] (i8), d [rows][K/256] (f16)
+// so that a lane streams 16-byte pieces of one plane and the headers arrive once per
+// superblock.  The activation is quantized to Q8_K by k_quantize_q8k and staged in LDS.
+#pragma once
+#include "kernels_decode.h"
+
+namespace cm {
+
+// ---------------------------------------------------------------------------
+// Q8_K quantization (inference.rs:17564-17599 quantize_q8_k_blocks), one workgroup per
+// 256-value block: max = the signed value of the first largest |x| (a strict '>' scan),
+// iscale = -127/max, q = min(nearest_int(iscale*x), 127), d = 1/iscale; a block whose |x|
+// never exceeds 0 gives d = 0 and zero quants.  Also writes the per-32 sums of the quants
+// (the Q4_K mins side).  nearest_int: inference.rs:17555-17561.
+__device__ __forceinline__ int nearest_int_ref(float f) {
+  const float v = f + 12582912.0f;
+  return (int)(__float_as_uint(v) & 0x007fffffu) - 0x00400000;
+}
+
+__global__ __launch_bounds__(256) void k_quantize_q8k(const float* __restrict__ x, float* __restrict__ yd,
+                                                      int8_t* __restrict__ yq, int32_t* __restrict__ ybs) {
+  __shared__ float sa[4];
+  __shared__ int si[4];
+  const int s = blockIdx.x, tid = threadIdx.x;
+  const float v = x[(size_t)s * 256 + tid];
+  float a = fabsf(v);
+  if (!(a > 0.0f)) a = 0.0f;  // zeros and NaN never win against the scan's initial 0
+  int idx = tid;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float oa = __shfl_xor(a, o);
+    const int oi = __shfl_xor(idx, o);
+    if (oa > a || (oa == a && oi < idx)) {
+      a = oa;
+      idx = oi;
+    }
+  }
+  if ((tid & 63) == 0) {
+    sa[tid >> 6] = a;
+    si[tid >> 6] = idx;
+  }
+  __syncthreads();
+  a = sa[0];
+  idx = si[0];
+  for (int w = 1; w < 4; ++w)
+    if (sa[w] > a) {  // waves are in index order: equal values keep the earlier wave
+      a = sa[w];
+      idx = si[w];
+    }
+  int q = 0;
+  float d = 0.0f;
+  if (a > 0.0f) {
+    const float mx = x[(size_t)s * 256 + idx];
+    const float iscale = -127.0f / mx;
+    q = min(nearest_int_ref(iscale * v), 127);
+    d = 1.0f / iscale;
+  }
+  const int8_t q8 = (int8_t)q;
+  yq[(size_t)s * 256 + tid] = q8;
+  int bs = q8;
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) bs += __shfl_xor(bs, o);
+  if ((tid & 31) == 0) ybs[(size_t)s * 8 + (tid >> 5)] = bs;
+  if (tid == 0) yd[s] = d;
+}
+
+// Integer sum over lane groups of 2^m consecutive lanes (xor butterflies; exact).
+template <int W>
+__device__ __forceinline__ int group_sum(int v) {
+#pragma unroll
+  for (int o = 1; o < W; o <<= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+constexpr int KQ_NT = 256;  // 4 waves
+__host__ __device__ inline int kq_rows_per_wg(int rpw) { return 4 * rpw; }
+
+// ---------------------------------------------------------------------------
+// Q4_K GEMV (q4k_gemv, cuda_resident.rs:601; CPU: q4_k_dot_arm, refmath.rs:424-561, the
+// Q4_K decode dot of inference.rs:17906-17965), faithful:
+//   per superblock s: prod = sum_g bsum32_g * min_g, sumi = sum_j (lo_j*sc_2j + hi_j*sc_2j+1)
+//   (exact integers), then  sumf = fma(-(y.d*dmin), prod, sumf); sumf = fma(y.d*d, sumi, sumf)
+//   in superblock order from 0;  y[row] = (resid ? resid[row] : 0) + sumf.
+// Lane work unit: one 16-byte nibble piece (32 weights: piece j of superblock s pairs its low
+// nibbles with q8[64(j/2) + 16(j%2) ..] and its high nibbles 32 values further); the 8
+// lanes of a superblock reduce their integers with butterflies, the first writes the
+// superblock's four fold operands to LDS, and one lane per row folds them in order.
+// Dynamic LDS: K quants + K/256 scales + K/32 sums + rows * K/256 * 16 bytes.
+__host__ __device__ inline size_t kq4_terms_offset(int K) {
+  return ((size_t)K + (size_t)(K / 256) * 4 + (size_t)(K / 32) * 4 + 15) & ~(size_t)15;
+}
+__host__ __device__ inline size_t kq4_lds_bytes(int K, int R) {
+  return kq4_terms_offset(K) + (size_t)R * (K / 256) * 16;
+}
+
+template <int RPW>
+__global__ __launch_bounds__(KQ_NT) void k_gemv_q4k(const uint8_t* __restrict__ nib, const uint8_t* __restrict__ hdr,
+                                                    int rows, int K, const float* __restrict__ yd,
+                                                    const int8_t* __restrict__ yq, const int32_t* __restrict__ ybs,
+                                                    float* y, const float* resid, float* __restrict__ part_v,
+                                                    uint32_t* __restrict__ part_i) {
+  constexpr int R = 4 * RPW;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int NSB = K >> 8, NC = K >> 5;
+  int8_t* xq = reinterpret_cast<int8_t*>(smem);
+  float* xd = reinterpret_cast<float*>(smem + K);
+  int* xbs = reinterpret_cast<int*>(smem + K + NSB * 4);
+  float4* terms = reinterpret_cast<float4*>(smem + kq4_terms_offset(K));
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int row0 = blockIdx.x * R;
+  for (int c = tid; c < (K >> 4); c += KQ_NT) reinterpret_cast<int4*>(xq)[c] = reinterpret_cast<const int4*>(yq)[c];
+  for (int i = tid; i < NSB; i += KQ_NT) xd[i] = yd[i];
+  for (int i = tid; i < NC; i += KQ_NT) xbs[i] = ybs[i];
+  __syncthreads();
+  const uint32_t K1 = 0x3f3f3f3fu, K2 = 0x0f0f0f0fu, K3 = 0x03030303u;
+#pragma unroll
+  for (int k = 0; k < RPW; ++k) {
+    const int rl = wave * RPW + k;
+    const int row = min(row0 + rl, rows - 1);
+    const uint4* np = reinterpret_cast<const uint4*>(nib + (size_t)row * (K >> 1));
+    const uint4* hp = reinterpret_cast<const uint4*>(hdr + (size_t)row * NSB * 16);
+    for (int c0 = 0; c0 < NC; c0 += 64) {
+      const int c = c0 + lane;
+      const bool valid = c < NC;  // uniform per 8-lane superblock group (NC % 8 == 0)
+      const int cc = min(c, NC - 1);
+      const uint4 w = np[cc];
+      const int s = cc >> 3, j = cc & 7, c4 = j >> 1, h = j & 1;
+      const uint4 hd = hp[s];
+      const uint32_t scw = (c4 < 2) ? (hd.y & K1) : ((hd.w & K2) | (((hd.y >> 6) & K3) << 4));
+      const uint32_t mnw = (j < 4) ? (hd.z & K1) : (((hd.w >> 4) & K2) | (((hd.z >> 6) & K3) << 4));
+      const int sc_lo = (scw >> (8 * ((2 * c4) & 3))) & 0xff;
+      const int sc_hi = (scw >> (8 * ((2 * c4 + 1) & 3))) & 0xff;
+      const int mn = (mnw >> (8 * (j & 3))) & 0xff;
+      const int base = (s << 8) + 64 * c4 + 16 * h;
+      const int4 qa = *reinterpret_cast<const int4*>(xq + base);
+      const int4 qb = *reinterpret_cast<const int4*>(xq + base + 32);
+      int lo = 0, hi = 0;
+      lo = __builtin_amdgcn_sdot4((int)(w.x & K2), qa.x, lo, false);
+      lo = __builtin_amdgcn_sdot4((int)(w.y & K2), qa.y, lo, false);
+      lo = __builtin_amdgcn_sdot4((int)(w.z & K2), qa.z, lo, false);
+      lo = __builtin_amdgcn_sdot4((int)(w.w & K2), qa.w, lo, false);
+      hi = __builtin_amdgcn_sdot4((int)((w.x >> 4) & K2), qb.x, hi, false);
+      hi = __builtin_amdgcn_sdot4((int)((w.y >> 4) & K2), qb.y, hi, false);
+      hi = __builtin_amdgcn_sdot4((int)((w.z >> 4) & K2), qb.z, hi, false);
+      hi = __builtin_amdgcn_sdot4((int)((w.w >> 4) & K2), qb.w, hi, false);
+      const int sumi = group_sum<8>(lo * sc_lo + hi * sc_hi);
+      const int prod = group_sum<8>(xbs[s * 8 + j] * mn);
+      if (valid && j == 0) {
+        const float ydv = xd[s];
+        const float dw = half_bits_to_float((uint16_t)(hd.x & 0xffffu));
+        const float dmw = half_bits_to_float((uint16_t)(hd.x >> 16));
+        terms[rl * NSB + s] = make_float4(-(ydv * dmw), (float)prod, ydv * dw, (float)sumi);
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < 64) {
+    float acc = 0.0f;
+    if (tid < R) {
+      const float4* t = terms + tid * NSB;
+      for (int s = 0; s < NSB; ++s) {
+        const float4 v = t[s];
+        acc = fmaf(v.x, v.y, acc);
+        acc = fmaf(v.z, v.w, acc);
+      }
+    }
+    const int row = row0 + tid;
+    const bool live = tid < R && row < rows;
+    if (live) y[row] = resid ? resid[row] + acc : acc;
+    if (part_v) {  // lm_head: this workgroup's argmax partial (first index of the max)
+      float bv = live ? acc : -INFINITY;
+      uint32_t bi = live ? (uint32_t)row : 0xffffffffu;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) argmax_pair(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
+      if (tid == 0) {
+        part_v[blockIdx.x] = bv;
+        part_i[blockIdx.x] = bi;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Q6_K GEMV (q6k_gemv, cuda_resident.rs:925; CPU: q6_k_wire_row_dot, inference.rs:19240-19295,
+// the Q6_K decode dot of inference.rs:19148-19195), faithful:
+//   per superblock s: aux[l] = sum over positions p = l (mod 8) of sc[p/16] * q8[p] * w[p]
+//   (exact integers); sums[l] += (f16(d_w) * y.d) * aux[l] in superblock order;
+//   result = left fold of sums[0..8] from -0.0;  y[row] = (resid ? resid[row] : 0) + result.
+// Lane work unit: 64 weights that share 16 bytes of qh (half n, offset q0 in {0, 16}): the
+// 16-value groups q0 + 32k (k = 0..3) of the half, rebuilt from two 16-byte ql pieces.
+// For each group the 8 position classes are separated with byte permutes: class l takes
+// the group's values l and 8 + l, paired with the activation dword (q_l, q_8+l, q_l, q_8+l)
+// prepared once per workgroup in LDS, and bytes 2-3 of the weight dword set to -32, so one
+// dot4 gives sum (w - 32) * q over the class.  The 4 lanes of a superblock reduce their 8
+// class sums with butterflies; the superblock's 8 products d * aux go to LDS; then 8 lanes
+// per row run the 8 class chains and the first folds them.
+// Dynamic LDS: K/256 * 512 bytes of activation pairs + K/256 scales + rows * K/256 * 32 bytes.
+__host__ __device__ inline size_t kq6_terms_offset(int K) {
+  return ((size_t)(K / 256) * 516 + 15) & ~(size_t)15;
+}
+__host__ __device__ inline size_t kq6_lds_bytes(int K, int R) {
+  return kq6_terms_offset(K) + (size_t)R * (K / 256) * 32;
+}
+
+template <int RPW>
+__global__ __launch_bounds__(KQ_NT) void k_gemv_q6k(const uint8_t* __restrict__ ql, const uint8_t* __restrict__ qh,
+                                                    const int8_t* __restrict__ scl, const uint16_t* __restrict__ dw,
+                                                    int rows, int K, const float* __restrict__ yd,
+                                                    const int8_t* __restrict__ yq, float* y, const float* resid,
+                                                    float* __restrict__ part_v, uint32_t* __restrict__ part_i) {
+  constexpr int R = 4 * RPW;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int NSB = K >> 8, NU = K >> 6;
+  uint32_t* xp = reinterpret_cast<uint32_t*>(smem);  // [s][group j][class l] activation pairs
+  float* xd = reinterpret_cast<float*>(smem + NSB * 512);
+  float* terms = reinterpret_cast<float*>(smem + kq6_terms_offset(K));  // [row][s][l]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int row0 = blockIdx.x * R;
+  // activation pairs: entry (s, j, l) = bytes (q[16j+l], q[16j+8+l], q[16j+l], q[16j+8+l])
+  for (int e = tid; e < NSB * 128; e += KQ_NT) {
+    const int l = e & 7, g = e >> 3;  // g = s * 16 + j
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(yq + (size_t)g * 16);
+    const uint32_t a = src[l >> 2], b = src[(l >> 2) + 2];
+    const uint32_t bl = l & 3;
+    // bytes: 0 <- a.byte(bl), 1 <- b.byte(bl), 2 <- a.byte(bl), 3 <- b.byte(bl)
+    const uint32_t sel = bl | ((4 + bl) << 8) | (bl << 16) | ((4 + bl) << 24);
+    xp[e] = __builtin_amdgcn_perm(b, a, sel);
+  }
+  for (int i = tid; i < NSB; i += KQ_NT) xd[i] = yd[i];
+  __syncthreads();
+  const uint32_t M4 = 0x0f0f0f0fu, M2 = 0x03030303u;
+#pragma unroll
+  for (int k = 0; k < RPW; ++k) {
+    const int rl = wave * RPW + k;
+    const int row = min(row0 + rl, rows - 1);
+    const uint8_t* qlr = ql + (size_t)row * (K >> 1);
+    const uint8_t* qhr = qh + (size_t)row * (K >> 2);
+    const int8_t* scr = scl + (size_t)row * NSB * 16;
+    for (int u0 = 0; u0 < NU; u0 += 64) {
+      const int u = u0 + lane;
+      const bool valid = u < NU;  // uniform per 4-lane superblock group (NU % 4 == 0)
+      const int uu = min(u, NU - 1);
+      const int s = uu >> 2, n = (uu >> 1) & 1, q0 = (uu & 1) * 16;
+      const uint4 l0 = *reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + q0);
+      const uint4 l1 = *reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + 32 + q0);
+      const uint4 hh = *reinterpret_cast<const uint4*>(qhr + s * 64 + n * 32 + q0);
+      const uint4 scv = *reinterpret_cast<const uint4*>(scr + s * 16);
+      const uint32_t L0[4] = {l0.x, l0.y, l0.z, l0.w}, L1[4] = {l1.x, l1.y, l1.z, l1.w};
+      const uint32_t HH[4] = {hh.x, hh.y, hh.z, hh.w};
+      const uint32_t SC[4] = {scv.x, scv.y, scv.z, scv.w};
+      int aux[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int j = n * 8 + (q0 >> 4) + 2 * kk;  // the group's index (scale index)
+        const int sc = (int)(int8_t)((SC[j >> 2] >> (8 * (j & 3))) & 0xff);
+        uint32_t v[4];
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+          const uint32_t lq = (kk & 1) ? L1[t4] : L0[t4];
+          const uint32_t lo = (kk < 2) ? (lq & M4) : ((lq >> 4) & M4);
+          v[t4] = lo | (((HH[t4] >> (2 * kk)) & M2) << 4);
+        }
+        const uint32_t* xg = xp + (size_t)(s * 16 + j) * 8;
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+          const uint32_t bl = l & 3;
+          const uint32_t a = v[l >> 2], b = v[(l >> 2) + 2];
+          const uint32_t wpair = __builtin_amdgcn_perm(b, a, bl | ((4 + bl) << 8) | (0x0c << 16) | (0x0cu << 24)) |
+                                 0xe0e00000u;
+          aux[l] += sc * __builtin_amdgcn_sdot4((int)wpair, (int)xg[l], 0, false);
+        }
+      }
+#pragma unroll
+      for (int l = 0; l < 8; ++l) aux[l] = group_sum<4>(aux[l]);
+      if (valid && (uu & 3) == 0) {
+        const float d = half_bits_to_float(dw[(size_t)row * NSB + s]) * xd[s];
+        float* tp = terms + ((size_t)rl * NSB + s) * 8;
+        *reinterpret_cast<float4*>(tp) = make_float4(d * (float)aux[0], d * (float)aux[1], d * (float)aux[2],
+                                                     d * (float)aux[3]);
+        *reinterpret_cast<float4*>(tp + 4) = make_float4(d * (float)aux[4], d * (float)aux[5], d * (float)aux[6],
+                                                         d * (float)aux[7]);
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < 64) {
+    // lanes 8r .. 8r+7: the 8 class chains of row r (R <= 8)
+    const int r = tid >> 3, l = tid & 7;
+    float sl = 0.0f;
+    if (r < R) {
+      const float* t = terms + (size_t)r * NSB * 8 + l;
+      for (int s = 0; s < NSB; ++s) sl += t[s * 8];
+    }
+    float acc = -0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc += __shfl(sl, (tid & ~7) + i);
+    const int row = row0 + r;
+    const bool live = l == 0 && r < R && row < rows;
+    if (live) y[row] = resid ? resid[row] + acc : acc;
+    if (part_v) {  // lm_head: this workgroup's argmax partial (first index of the max)
+      float bv = live ? acc : -INFINITY;
+      uint32_t bi = live ? (uint32_t)row : 0xffffffffu;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) argmax_pair(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
+      if (tid == 0) {
+        part_v[blockIdx.x] = bv;
+        part_i[blockIdx.x] = bi;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Embedding row of a K-quant token table (the block dequantizers of tensor/mod.rs:4682-4703
+// Q4_K: (d*sc)*q - dmin*m; :4818-4845 Q6_K: (d*sc)*q), for the token in StepState.
+// One thread per value, grid H/256.
+__global__ __launch_bounds__(256) void k_embed_q4k(const uint8_t* __restrict__ nib, const uint8_t* __restrict__ hdr,
+                                                   int H, const StepState* __restrict__ st, float* __restrict__ out) {
+  const int s = blockIdx.x, i = threadIdx.x;
+  const int NSB = H >> 8;
+  const size_t tok = st->tok;
+  const uint8_t* hp = hdr + (tok * NSB + s) * 16;
+  const uint8_t* sc = hp + 4;
+  const int pair = i >> 6, hi = (i >> 5) & 1, l = i & 31;
+  const int idx = 2 * pair + hi;
+  int scale, mn;
+  if (idx < 4) {
+    scale = sc[idx] & 63;
+    mn = sc[idx + 4] & 63;
+  } else {
+    scale = (sc[idx + 4] & 0x0f) | ((sc[idx - 4] >> 6) << 4);
+    mn = (sc[idx + 4] >> 4) | ((sc[idx] >> 6) << 4);
+  }
+  const float d = half_bits_to_float((uint16_t)(hp[0] | (hp[1] << 8)));
+  const float dmin = half_bits_to_float((uint16_t)(hp[2] | (hp[3] << 8)));
+  const uint8_t byte = nib[(tok * NSB + s) * 128 + pair * 32 + l];
+  const int q = hi ? (byte >> 4) : (byte & 0x0f);
+  out[s * 256 + i] = (d * (float)scale) * (float)q - dmin * (float)mn;
+}
+
+__global__ __launch_bounds__(256) void k_embed_q6k(const uint8_t* __restrict__ ql, const uint8_t* __restrict__ qh,
+                                                   const int8_t* __restrict__ scl, const uint16_t* __restrict__ dw,
+                                                   int H, const StepState* __restrict__ st, float* __restrict__ out) {
+  const int s = blockIdx.x, i = threadIdx.x;
+  const int NSB = H >> 8;
+  const size_t tok = st->tok;
+  const size_t sb = tok * NSB + s;
+  const int n = i >> 7, r = i & 127, k = r >> 5, l = r & 31;
+  const uint8_t lq = ql[sb * 128 + n * 64 + (k & 1) * 32 + l];
+  const uint8_t hq = qh[sb * 64 + n * 32 + l];
+  const int lo = (k < 2) ? (lq & 0xf) : (lq >> 4);
+  const int q = (lo | (((hq >> (2 * k)) & 3) << 4)) - 32;
+  const float d = half_bits_to_float(dw[sb]);
+  out[s * 256 + i] = d * (float)scl[sb * 16 + i / 16] * (float)q;
+}
+
+}  // namespace cm

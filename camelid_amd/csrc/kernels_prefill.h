@@ -40,7 +40,10 @@ constexpr int GM_RN = 64;  // rows per workgroup tile
 constexpr int GM_RT = 64;  // tokens per workgroup tile
 constexpr int GM_BG = 32;  // blocks per scale-staging group
 constexpr int GM_SB = 4;   // blocks per operand step
-constexpr int GM_PS = 80;  // 8-byte pieces per [block][piece] row of the LDS tile (64 + 16 pad)
+// 8-byte pieces per [block][piece] row of the LDS tile: 64 + 1 pad, so that the planes
+// start 2 banks apart (130 dwords) and the 8 pieces a row's 16-byte chunks scatter to
+// land in different banks (the tile writes are otherwise 8-way bank conflicts)
+constexpr int GM_PS = 65;
 
 __host__ __device__ inline int gemm_tiles(int N, int T) {
   return ((N + GM_RN - 1) / GM_RN) * ((T + GM_RT - 1) / GM_RT);

@@ -83,3 +83,49 @@ CX int camelid_embed_q8_0(const uint8_t* wire, uint32_t vocab, uint32_t hidden, 
   }
   return 0;
 }
+
+// K-quant embedding rows (the block dequantizers: tensor/mod.rs:4682-4703 Q4_K,
+// (d*sc)*q - dmin*m; :4818-4845 Q6_K, (d*sc)*q).  quant 1 = Q4_K, 2 = Q6_K.
+CX int camelid_embed_kquant(int quant, const uint8_t* wire, uint32_t vocab, uint32_t hidden, const uint32_t* tokens,
+                            uint32_t n, float* out) {
+  if (hidden % 256 || (quant != 1 && quant != 2)) return 1;
+  const size_t nsb = hidden / 256, bb = quant == 1 ? 144 : 210;
+  for (uint32_t t = 0; t < n; ++t) {
+    if (tokens[t] >= vocab) return 1;
+    for (size_t s = 0; s < nsb; ++s) {
+      const uint8_t* b = wire + ((size_t)tokens[t] * nsb + s) * bb;
+      float* o = out + (size_t)t * hidden + s * 256;
+      if (quant == 1) {
+        const float d = cm::f16_bits_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+        const float dmin = cm::f16_bits_to_f32((uint16_t)(b[2] | (b[3] << 8)));
+        const uint8_t* sc = b + 4;
+        for (int idx = 0; idx < 8; ++idx) {
+          int scale, mn;
+          if (idx < 4) {
+            scale = sc[idx] & 63;
+            mn = sc[idx + 4] & 63;
+          } else {
+            scale = (sc[idx + 4] & 0x0f) | ((sc[idx - 4] >> 6) << 4);
+            mn = (sc[idx + 4] >> 4) | ((sc[idx] >> 6) << 4);
+          }
+          const float ds = d * (float)scale, dm = dmin * (float)mn;
+          const int pair = idx / 2, hi = idx % 2;
+          for (int l = 0; l < 32; ++l) {
+            const uint8_t byte = b[16 + pair * 32 + l];
+            o[pair * 64 + hi * 32 + l] = ds * (float)(hi ? (byte >> 4) : (byte & 0x0f)) - dm;
+          }
+        }
+      } else {
+        const float d = cm::f16_bits_to_f32((uint16_t)(b[208] | (b[209] << 8)));
+        for (int p = 0; p < 256; ++p) {
+          const int nn = p / 128, k = (p % 128) / 32, l = p % 32;
+          const uint8_t lq = b[nn * 64 + (k & 1) * 32 + l];
+          const int lo = k < 2 ? (lq & 0x0f) : (lq >> 4);
+          const int q = (lo | (((b[128 + nn * 32 + l] >> (2 * k)) & 3) << 4)) - 32;
+          o[p] = d * (float)(int8_t)b[192 + p / 16] * (float)q;
+        }
+      }
+    }
+  }
+  return 0;
+}

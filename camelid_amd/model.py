@@ -15,9 +15,11 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import _native as N
-from .engine import EngineDims, HipResidentDecode, PROJ_NAMES
+from .engine import EngineDims, HipResidentDecode, PROJ_NAMES, Q4_K, Q6_K, Q8_0
 
 Q8_BLOCK_BYTES = 34
+# bytes per value of each weight format (Q8_0 34 B / 32, Q4_K 144 B / 256, Q6_K 210 B / 256)
+QUANT_BYTES = {Q8_0: 34 / 32, Q4_K: 144 / 256, Q6_K: 210 / 256}
 
 
 @dataclass(frozen=True)
@@ -45,6 +47,20 @@ class ModelConfig:
     prompt_len: int = 128
     decode_len: int = 128
     weight_std: float = 0.02
+    # "q8_0": every tensor Q8_0.  "q4_k_m": Q4_K for q, k, o, gate, up, down and the token
+    # table; Q6_K for v and the output projection (the llama.cpp Q4_K_M mix).
+    quant_scheme: str = "q8_0"
+
+    def proj_quant(self, proj: str) -> int:
+        if self.quant_scheme == "q8_0":
+            return Q8_0
+        return Q6_K if proj == "v" else Q4_K
+
+    def output_quant(self) -> int:
+        return Q8_0 if self.quant_scheme == "q8_0" else Q6_K
+
+    def embd_quant(self) -> int:
+        return Q8_0 if self.quant_scheme == "q8_0" else Q4_K
 
     @property
     def rope_dim(self) -> int:
@@ -65,12 +81,12 @@ class ModelConfig:
                 "gate": (F, H), "up": (F, H), "down": (H, F)}
 
     def weight_bytes(self) -> int:
-        """Q8_0 weight + norm bytes touched per decode token (lm_head + norms, no embedding)."""
-        per_layer = sum(r * k for r, k in self.proj_shapes().values()) * Q8_BLOCK_BYTES // 32
+        """Weight + norm bytes touched per decode token (lm_head + norms, no embedding)."""
+        per_layer = sum(int(r * k * QUANT_BYTES[self.proj_quant(p)]) for p, (r, k) in self.proj_shapes().items())
         norms = 4 * (2 * self.n_layers + 1) * self.hidden
         if self.qk_norm:
             norms += 4 * 2 * self.n_layers * self.head_dim
-        lm = self.vocab * self.hidden * Q8_BLOCK_BYTES // 32
+        lm = int(self.vocab * self.hidden * QUANT_BYTES[self.output_quant()])
         return per_layer * self.n_layers + norms + lm
 
     def kv_bytes_per_pos(self) -> int:
@@ -78,7 +94,7 @@ class ModelConfig:
 
     def decode_bytes(self, pos: int) -> int:
         """Algorithmic HBM bytes of one decode step at position `pos` (reads pos+1 KV rows)."""
-        emb = self.hidden * Q8_BLOCK_BYTES // 32
+        emb = int(self.hidden * QUANT_BYTES[self.embd_quant()])
         return self.weight_bytes() + emb + self.kv_bytes_per_pos() * (pos + 1) + self.kv_bytes_per_pos()
 
     def engine_dims(self, max_pos: int | None = None) -> EngineDims:
@@ -107,6 +123,10 @@ CONFIGS = {
     # Mistral-7B-v0.3 architecture, long context 8192 + 256.
     "mistral-7b-v0.3": ModelConfig("mistral-7b-v0.3", 32, 4096, 14336, 32, 8, 128, 32768, 1e6, seed=4,
                                    prompt_seed=4 + 1000, prompt_len=8192, decode_len=256),
+    # Qwen3-8B architecture, Q4_K_M (Q6_K v / output), QK-norm, split-half RoPE.
+    "qwen3-8b": ModelConfig("qwen3-8b", 36, 4096, 12288, 32, 8, 128, 151936, 1e6, eps=1e-6, qk_norm=True,
+                            split_half=True, seed=5, prompt_seed=5 + 1000, prompt_len=1024, decode_len=256,
+                            quant_scheme="q4_k_m"),
 }
 
 
@@ -139,6 +159,19 @@ def synth_q8_0(name: str, seed: int, rows: int, k: int, std: float = 0.02) -> np
     return out
 
 
+def synth_kquant(name: str, seed: int, rows: int, k: int, quant: int, std: float = 0.02) -> np.ndarray:
+    """N(0, std) weights [rows][k] as Q4_K / Q6_K wire superblocks."""
+    out = np.empty(int(rows * k * QUANT_BYTES[quant]), np.uint8)
+    rc = N.lib().camelid_synth_kquant_wire(name.encode(), seed, std, rows * k, quant, N.ptr(out, C.c_uint8))
+    if rc:
+        raise ValueError("K-quant tensor size must be a multiple of 256")
+    return out
+
+
+def synth_weight(name: str, seed: int, rows: int, k: int, quant: int, std: float = 0.02) -> np.ndarray:
+    return synth_q8_0(name, seed, rows, k, std) if quant == Q8_0 else synth_kquant(name, seed, rows, k, quant, std)
+
+
 def synth_f32(name: str, seed: int, n: int, std: float) -> np.ndarray:
     out = np.empty(n, np.float32)
     N.lib().camelid_synth_normal_f32(name.encode(), seed, std, N.ptr(out, C.c_float), n)
@@ -147,7 +180,7 @@ def synth_f32(name: str, seed: int, n: int, std: float) -> np.ndarray:
 
 @dataclass
 class SyntheticModel:
-    """Seeded N(0, std) weights quantized to GGUF Q8_0 wire bytes; norms = 1.0."""
+    """Seeded N(0, std) weights as GGUF wire bytes (Q8_0, or the config's K-quant mix); norms = 1.0."""
 
     cfg: ModelConfig
     layers: list = field(default_factory=list)
@@ -162,33 +195,43 @@ class SyntheticModel:
         gguf = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output", "gate": "ffn_gate",
                 "up": "ffn_up", "down": "ffn_down"}
         for i in range(cfg.n_layers):
-            projs = {p: synth_q8_0(f"blk.{i}.{gguf[p]}.weight", cfg.seed, r, k, cfg.weight_std)
+            projs = {p: synth_weight(f"blk.{i}.{gguf[p]}.weight", cfg.seed, r, k, cfg.proj_quant(p), cfg.weight_std)
                      for p, (r, k) in cfg.proj_shapes().items()}
-            layer = {"projs": projs, "attn_norm": np.ones(H, np.float32), "ffn_norm": np.ones(H, np.float32)}
+            layer = {"projs": projs, "attn_norm": np.ones(H, np.float32), "ffn_norm": np.ones(H, np.float32),
+                     "quant": [cfg.proj_quant(p) for p in PROJ_NAMES]}
             if cfg.qk_norm:
                 layer["q_norm"] = np.ones(cfg.head_dim, np.float32)
                 layer["k_norm"] = np.ones(cfg.head_dim, np.float32)
             m.layers.append(layer)
-        m.token_embd = synth_q8_0("token_embd.weight", cfg.seed, cfg.vocab, H, cfg.weight_std)
-        m.output = m.token_embd if cfg.tied else synth_q8_0("output.weight", cfg.seed, cfg.vocab, H, cfg.weight_std)
+        m.token_embd = synth_weight("token_embd.weight", cfg.seed, cfg.vocab, H, cfg.embd_quant(), cfg.weight_std)
+        if cfg.tied and cfg.embd_quant() == cfg.output_quant():
+            m.output = m.token_embd
+        else:
+            m.output = synth_weight("output.weight", cfg.seed, cfg.vocab, H, cfg.output_quant(), cfg.weight_std)
         m.output_norm = np.ones(H, np.float32)
         return m
 
     def embed(self, tokens) -> np.ndarray:
         toks = np.ascontiguousarray(tokens, np.uint32)
         out = np.empty((len(toks), self.cfg.hidden), np.float32)
-        rc = N.lib().camelid_embed_q8_0(N.ptr(self.token_embd, C.c_uint8), self.cfg.vocab, self.cfg.hidden,
-                                        N.ptr(toks, C.c_uint32), len(toks), N.ptr(out, C.c_float))
+        q = self.cfg.embd_quant()
+        if q == Q8_0:
+            rc = N.lib().camelid_embed_q8_0(N.ptr(self.token_embd, C.c_uint8), self.cfg.vocab, self.cfg.hidden,
+                                            N.ptr(toks, C.c_uint32), len(toks), N.ptr(out, C.c_float))
+        else:
+            rc = N.lib().camelid_embed_kquant(q, N.ptr(self.token_embd, C.c_uint8), self.cfg.vocab, self.cfg.hidden,
+                                              N.ptr(toks, C.c_uint32), len(toks), N.ptr(out, C.c_float))
         if rc:
             raise ValueError("token id out of range")
         return out
 
     def load_into(self, eng: HipResidentDecode, device_embedding: bool = False) -> None:
         for i, L in enumerate(self.layers):
-            eng.set_layer(i, L["projs"], L["attn_norm"], L["ffn_norm"], L.get("q_norm"), L.get("k_norm"))
-        eng.set_output(self.output_norm, self.output)
+            eng.set_layer(i, L["projs"], L["attn_norm"], L["ffn_norm"], L.get("q_norm"), L.get("k_norm"),
+                          quants=L.get("quant"))
+        eng.set_output(self.output_norm, self.output, quant=self.cfg.output_quant())
         if device_embedding:
-            eng.set_embedding(self.token_embd)
+            eng.set_embedding(self.token_embd, quant=self.cfg.embd_quant())
 
 
 class ResidentSession:

@@ -194,6 +194,25 @@ int camelid_hip_attention_prefill(const float* qrot, const uint16_t* kc, const f
                                   uint32_t layer, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
                                   uint32_t max_pos, uint32_t pos0, uint32_t tokens, float scale,
                                   float* att_out, int8_t* xq, float* xs, void* stream);
+/* quantize_q8k (cuda_resident.rs:1416-1490; CPU inference.rs:17564-17599): n (multiple of 256)
+ * f32 values -> Q8_K blocks: scales yd [n/256], quants yq [n], per-32 quant sums ybs [n/32]. */
+int camelid_hip_quantize_q8_k(const float* x, uint32_t n, float* yd, int8_t* yq, int32_t* ybs,
+                              void* stream);
+/* Host split of K-quant wire rows [rows][k/256 superblocks] into the device planes the
+ * K-quant GEMV reads: Q4_K (quant 1): a = nibbles [rows][k/2], b = superblock headers
+ * [rows][k/256][16] (sc, d unused); Q6_K (quant 2): a = ql [rows][k/2], b = qh [rows][k/4],
+ * sc = scales [rows][k/256][16], d = f16 scales [rows][k/256]. */
+int camelid_kquant_repack(uint8_t quant, const uint8_t* src, size_t rows, size_t k, uint8_t* a,
+                          uint8_t* b, int8_t* sc, uint16_t* d);
+/* q4k_gemv / q6k_gemv (cuda_resident.rs:601, :925; CPU q4_k_dot_arm refmath.rs:424-561 via
+ * inference.rs:17906-17965, q6_k_wire_row_dot inference.rs:19240-19295 via :19148-19195):
+ * y = resid + W.x for a Q8_K activation (camelid_hip_quantize_q8_k) and planes from
+ * camelid_kquant_repack; faithful per-row order.  k % 256 == 0, k <= 16384; resid may be
+ * NULL; y may alias resid. */
+int camelid_hip_kquant_gemv(uint8_t quant, const uint8_t* a, const uint8_t* b, const int8_t* sc,
+                            const uint16_t* d, uint32_t rows, uint32_t k, const float* yd,
+                            const int8_t* yq, const int32_t* ybs, float* y, const float* resid,
+                            void* stream);
 /* argmax_f32 (cuda_resident.rs:1847; CPU inference.rs:5912). */
 int camelid_hip_argmax(const float* x, uint32_t n, uint32_t* out, void* stream);
 /* Sequential-order f32 sums of rows [rows][n] (n <= 16384), evaluated with the

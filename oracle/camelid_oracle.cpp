@@ -130,6 +130,158 @@ float q8_0_row_dot_wire(const uint8_t* row, const float* xs, const int8_t* xq, s
   return sum;
 }
 
+// ---------------------------------------------------------------- K-quants
+// Projection formats (the C ABI's ProjQuant codes).
+enum { Q_Q8_0 = 0, Q_Q4_K = 1, Q_Q6_K = 2 };
+inline uint32_t le32(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24); }
+inline uint16_t le16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+// inference.rs:17555-17561 nearest_int_reference: adding 1.5*2^23 rounds to nearest even
+// into the mantissa.
+int32_t nearest_int(float fval) {
+  const float val = fval + 12582912.0f;
+  return (int32_t)(f2u(val) & 0x007fffffu) - 0x00400000;
+}
+
+// inference.rs:17564-17599 quantize_q8_k_blocks, one 256-value block: max = the signed
+// value of the first largest |x| (strict >), iscale = -127/max, q = min(nearest_int(iscale*x),
+// 127) (wrapped to i8), d = 1/iscale; an all-zero block gives d = 0, q = 0.
+void quantize_q8_k_block(const float* x, float* d, int8_t* qs) {
+  float amax = 0.0f, mx = 0.0f;
+  for (int i = 0; i < 256; ++i)
+    if (std::fabs(x[i]) > amax) { amax = std::fabs(x[i]); mx = x[i]; }
+  if (amax == 0.0f) {
+    *d = 0.0f;
+    std::memset(qs, 0, 256);
+    return;
+  }
+  const float iscale = -127.0f / mx;
+  for (int i = 0; i < 256; ++i) qs[i] = (int8_t)std::min(nearest_int(iscale * x[i]), 127);
+  *d = 1.0f / iscale;
+}
+
+// tensor/mod.rs:4776-4785 q4_k_scale_min: 6-bit (scale, min) of sub-block idx.
+void q4_k_scale_min(int idx, const uint8_t* sc, uint8_t* scale, uint8_t* mn) {
+  if (idx < 4) {
+    *scale = sc[idx] & 63;
+    *mn = sc[idx + 4] & 63;
+  } else {
+    *scale = (uint8_t)((sc[idx + 4] & 0x0f) | ((sc[idx - 4] >> 6) << 4));
+    *mn = (uint8_t)((sc[idx + 4] >> 4) | ((sc[idx] >> 6) << 4));
+  }
+}
+
+// tensor/mod.rs:4682-4703 Q4KBlock::dequantize (144-byte superblock: f16 d, f16 dmin,
+// 12 packed scale/min bytes, 128 nibble bytes): out = (d*sc)*q - dmin*m.
+void dequant_q4_k_block(const uint8_t* b, float* out) {
+  const float d = f16_bits_to_f32(le16(b)), dmin = f16_bits_to_f32(le16(b + 2));
+  for (int pair = 0; pair < 4; ++pair) {
+    uint8_t ls, lm, hs, hm;
+    q4_k_scale_min(2 * pair, b + 4, &ls, &lm);
+    q4_k_scale_min(2 * pair + 1, b + 4, &hs, &hm);
+    const float lo_s = d * (float)ls, hi_s = d * (float)hs, lo_m = dmin * (float)lm, hi_m = dmin * (float)hm;
+    for (int l = 0; l < 32; ++l) {
+      const uint8_t byte = b[16 + pair * 32 + l];
+      out[pair * 64 + l] = lo_s * (float)(byte & 0x0f) - lo_m;
+      out[pair * 64 + 32 + l] = hi_s * (float)(byte >> 4) - hi_m;
+    }
+  }
+}
+
+// The signed 6-bit weights of a Q6_K superblock (210 bytes: ql[128], qh[64], i8 scales[16],
+// f16 d), in value order (inference.rs:19256-19276; tensor/mod.rs:4818-4845).
+void q6_k_values(const uint8_t* b, int8_t* a) {
+  for (int n = 0; n < 2; ++n) {
+    const uint8_t* ql = b + 64 * n;
+    const uint8_t* qh = b + 128 + 32 * n;
+    int8_t* w = a + 128 * n;
+    for (int l = 0; l < 32; ++l) {
+      w[l] = (int8_t)(((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32);
+      w[l + 32] = (int8_t)(((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32);
+      w[l + 64] = (int8_t)(((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32);
+      w[l + 96] = (int8_t)(((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32);
+    }
+  }
+}
+
+// tensor/mod.rs:4818-4845 Q6KBlock::dequantize: out = (d*sc)*q.
+void dequant_q6_k_block(const uint8_t* b, float* out) {
+  const float d = f16_bits_to_f32(le16(b + 208));
+  int8_t a[256];
+  q6_k_values(b, a);
+  for (int i = 0; i < 256; ++i) out[i] = d * (float)(int8_t)b[192 + i / 16] * (float)a[i];
+}
+
+// refmath.rs:503-561 q4_k_dot_scalar (= q4_k_dot_arm, the CPU decode's Q4_K dot via
+// inference.rs:17906-17965): per superblock exact integer mins product and scaled nibble
+// dots, then sumf = fma(-dmin, prod, sumf); sumf = fma(d, sumi1 + sumi2, sumf), with
+// d = y.d * f16(d_w), dmin = y.d * f16(dmin_w).
+float q4_k_row_dot(const uint8_t* row, const float* yd, const int8_t* yqs, size_t nsb) {
+  const uint32_t K1 = 0x3f3f3f3f, K2 = 0x0f0f0f0f, K3 = 0x03030303;
+  float sumf = 0.0f;
+  for (size_t s = 0; s < nsb; ++s) {
+    const uint8_t* b = row + s * 144;
+    const float d = yd[s] * f16_bits_to_f32(le16(b));
+    const float dmin = yd[s] * f16_bits_to_f32(le16(b + 2));
+    const uint32_t u0 = le32(b + 4), u1 = le32(b + 8), u2 = le32(b + 12);
+    const uint32_t mins8[2] = {u1 & K1, ((u2 >> 4) & K2) | (((u1 >> 6) & K3) << 4)};
+    const uint32_t scw[2] = {u0 & K1, (u2 & K2) | (((u0 >> 6) & K3) << 4)};
+    auto scale_at = [&](int g) { return (int64_t)((scw[g / 4] >> (8 * (g % 4))) & 0xff); };
+    auto min_at = [&](int g) { return (int64_t)((mins8[g / 4] >> (8 * (g % 4))) & 0xff); };
+    const int8_t* q8 = yqs + s * 256;
+    int64_t prod = 0;
+    for (int g = 0; g < 8; ++g) {
+      int64_t bs = 0;
+      for (int t = 0; t < 32; ++t) bs += q8[32 * g + t];
+      prod += bs * min_at(g);
+    }
+    sumf = std::fma(-dmin, (float)prod, sumf);
+    int64_t sumi1 = 0, sumi2 = 0;
+    for (int j = 0; j < 4; ++j) {
+      const uint8_t* q4 = b + 16 + 32 * j;
+      int64_t lo = 0, hi = 0;
+      for (int t = 0; t < 32; ++t) {
+        lo += (int64_t)(q4[t] & 0xf) * q8[64 * j + t];
+        hi += (int64_t)(q4[t] >> 4) * q8[64 * j + 32 + t];
+      }
+      sumi1 += lo * scale_at(2 * j);
+      sumi2 += hi * scale_at(2 * j + 1);
+    }
+    sumf = std::fma(d, (float)(sumi1 + sumi2), sumf);
+  }
+  return sumf;
+}
+
+// inference.rs:19240-19295 q6_k_wire_row_dot (the CPU decode's Q6_K dot via
+// inference.rs:19148-19195): per superblock 8 integer lanes aux[l] (l = position mod 8)
+// += scale_j * q8 * a; sums[l] += (f16(d_w) * y.d) * aux[l]; the result is the left fold of
+// sums[0..8] (Rust's f32 Sum, whose initial value is -0.0).
+float q6_k_row_dot(const uint8_t* row, const float* yd, const int8_t* yqs, size_t nsb) {
+  float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int8_t a[256];
+  for (size_t s = 0; s < nsb; ++s) {
+    const uint8_t* b = row + s * 210;
+    const float d = f16_bits_to_f32(le16(b + 208)) * yd[s];
+    q6_k_values(b, a);
+    const int8_t* q8 = yqs + s * 256;
+    int32_t aux[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int j = 0; j < 16; ++j) {
+      const int32_t scale = (int8_t)b[192 + j];
+      const int off = j * 16;
+      for (int l = 0; l < 8; ++l) aux[l] += scale * (int32_t)q8[off + l] * (int32_t)a[off + l];
+      for (int l = 0; l < 8; ++l) aux[l] += scale * (int32_t)q8[off + 8 + l] * (int32_t)a[off + 8 + l];
+    }
+    for (int l = 0; l < 8; ++l) sums[l] += d * (float)aux[l];
+  }
+  float r = -0.0f;
+  for (int l = 0; l < 8; ++l) r += sums[l];
+  return r;
+}
+
+size_t quant_row_bytes(int quant, size_t k) {
+  return quant == Q_Q8_0 ? k / 32 * 34 : quant == Q_Q4_K ? k / 256 * 144 : k / 256 * 210;
+}
+
 // tensor/mod.rs:2083-2106 rms_norm_into (scalar branch): sequential sum of squares,
 // /n, scale = 1/sqrt(ms+eps), out = (x*scale)*w.
 void rms_norm_row(const float* x, const float* w, size_t n, float eps, float* out) {
@@ -222,8 +374,11 @@ struct Model {
   uint32_t L, n_heads, n_kv, hd, H, F, V, max_pos;
   float eps;
   int split_half;
-  // per layer wire pointers (Q8_0, 34 B blocks), borrowed from the caller
+  // per layer wire pointers (Q8_0 34 B blocks, Q4_K 144 B or Q6_K 210 B superblocks),
+  // borrowed from the caller; qt[l*7 + proj] = the projection's format (q,k,v,o,gate,up,down)
   std::vector<const uint8_t*> wq, wk, wv, wo, wg, wu, wd;
+  std::vector<uint8_t> qt;
+  int out_quant = Q_Q8_0, embd_quant = Q_Q8_0;
   std::vector<const float*> attn_norm, ffn_norm, q_norm, k_norm;
   const float* out_norm = nullptr;
   const uint8_t* out_w = nullptr;   // lm_head (may equal token_embd when tied)
@@ -233,6 +388,7 @@ struct Model {
   // scratch
   std::vector<float> h, xn, q, k, v, ctx, tmp, g, u, act, logits;
   std::vector<float> xs; std::vector<int8_t> xq;
+  std::vector<float> kd; std::vector<int8_t> kq;  // Q8_K activation
 };
 
 void quantize_row(const float* x, size_t n, std::vector<float>& xs, std::vector<int8_t>& xq) {
@@ -251,6 +407,25 @@ void linear_q8(const uint8_t* w, size_t rows, size_t k, const float* x, float* o
 #pragma omp parallel for schedule(static)
   for (long r = 0; r < (long)rows; ++r)
     out[r] = q8_0_row_dot_wire(w + (size_t)r * nb * 34, xsp, xqp, nb);
+}
+
+// A linear layer in the projection's format: Q8_0 as above; K-quants quantize the input
+// row to Q8_K once, then dot every wire row (inference.rs:17906-17965 Q4_K,
+// :19148-19195 Q6_K).
+void linear(Model& m, const uint8_t* w, int quant, size_t rows, size_t k, const float* x, float* out) {
+  if (quant == Q_Q8_0) {
+    linear_q8(w, rows, k, x, out, m.xs, m.xq);
+    return;
+  }
+  const size_t nsb = k / 256, rb = quant_row_bytes(quant, k);
+  m.kd.resize(nsb);
+  m.kq.resize(k);
+  for (size_t sb = 0; sb < nsb; ++sb) quantize_q8_k_block(x + 256 * sb, &m.kd[sb], &m.kq[256 * sb]);
+  const float* kd = m.kd.data();
+  const int8_t* kq = m.kq.data();
+#pragma omp parallel for schedule(static)
+  for (long r = 0; r < (long)rows; ++r)
+    out[r] = quant == Q_Q4_K ? q4_k_row_dot(w + (size_t)r * rb, kd, kq, nsb) : q6_k_row_dot(w + (size_t)r * rb, kd, kq, nsb);
 }
 
 // inference.rs:23945-24025 attention_context_for_head_into_with_kernels (F32 KV dtype,
@@ -283,9 +458,10 @@ void forward_layer(Model& m, uint32_t l, uint32_t pos, const float* cosv, const 
   const uint32_t H = m.H, hd = m.hd, nq = m.n_heads * hd, nkv = m.n_kv * hd;
   rms_norm_row(m.h.data(), m.attn_norm[l], H, m.eps, m.xn.data());
   // Q/K/V share one quantized input (the row is quantized identically for each linear).
-  linear_q8(m.wq[l], nq, H, m.xn.data(), m.q.data(), m.xs, m.xq);
-  linear_q8(m.wk[l], nkv, H, m.xn.data(), m.k.data(), m.xs, m.xq);
-  linear_q8(m.wv[l], nkv, H, m.xn.data(), m.v.data(), m.xs, m.xq);
+  const uint8_t* qt = &m.qt[(size_t)l * 7];
+  linear(m, m.wq[l], qt[0], nq, H, m.xn.data(), m.q.data());
+  linear(m, m.wk[l], qt[1], nkv, H, m.xn.data(), m.k.data());
+  linear(m, m.wv[l], qt[2], nkv, H, m.xn.data(), m.v.data());
   // per-head QK RMSNorm (tensor/mod.rs:2112-2136) before RoPE (inference.rs:6369-6386).
   if (m.q_norm[l]) for (uint32_t h = 0; h < m.n_heads; ++h) rms_norm_row(&m.q[h * hd], m.q_norm[l], hd, m.eps, &m.q[h * hd]);
   if (m.k_norm[l]) for (uint32_t h = 0; h < m.n_kv; ++h) rms_norm_row(&m.k[h * hd], m.k_norm[l], hd, m.eps, &m.k[h * hd]);
@@ -310,13 +486,13 @@ void forward_layer(Model& m, uint32_t l, uint32_t pos, const float* cosv, const 
     for (long h = 0; h < (long)m.n_heads; ++h)
       attention_head(m, l, (uint32_t)h / rep, &m.q[h * hd], pos + 1, scale, &m.ctx[h * hd], sc);
   }
-  linear_q8(m.wo[l], H, nq, m.ctx.data(), m.tmp.data(), m.xs, m.xq);
+  linear(m, m.wo[l], qt[3], H, nq, m.ctx.data(), m.tmp.data());
   for (uint32_t i = 0; i < H; ++i) m.h[i] = m.h[i] + m.tmp[i];   // pooled_add residual
   rms_norm_row(m.h.data(), m.ffn_norm[l], H, m.eps, m.xn.data());
-  linear_q8(m.wg[l], m.F, H, m.xn.data(), m.g.data(), m.xs, m.xq);
-  linear_q8(m.wu[l], m.F, H, m.xn.data(), m.u.data(), m.xs, m.xq);
+  linear(m, m.wg[l], qt[4], m.F, H, m.xn.data(), m.g.data());
+  linear(m, m.wu[l], qt[5], m.F, H, m.xn.data(), m.u.data());
   for (uint32_t i = 0; i < m.F; ++i) m.act[i] = silu_mul1(m.g[i], m.u[i]);
-  linear_q8(m.wd[l], H, m.F, m.act.data(), m.tmp.data(), m.xs, m.xq);
+  linear(m, m.wd[l], qt[6], H, m.F, m.act.data(), m.tmp.data());
   for (uint32_t i = 0; i < H; ++i) m.h[i] = m.h[i] + m.tmp[i];
 }
 
@@ -380,6 +556,26 @@ OX void oracle_q8_0_gemm(const uint8_t* wire, size_t rows, size_t k, size_t T, c
     for (size_t t = 0; t < T; ++t)
       out[t * rows + r] = q8_0_row_dot_wire(wire + (size_t)r * nb * 34, xs + t * nb, xq + t * k, nb);
 }
+// K-quant kernels: Q8_K activation quantizer, wire dequantizers, row dots.
+OX void oracle_quantize_q8_k(const float* x, size_t n, float* d, int8_t* qs) {
+  for (size_t b = 0; b < n / 256; ++b) quantize_q8_k_block(x + 256 * b, &d[b], &qs[256 * b]);
+}
+OX int32_t oracle_nearest_int(float x) { return nearest_int(x); }
+OX void oracle_dequant_q4_k(const uint8_t* wire, size_t nsb, float* out) {
+  for (size_t b = 0; b < nsb; ++b) dequant_q4_k_block(wire + b * 144, out + b * 256);
+}
+OX void oracle_dequant_q6_k(const uint8_t* wire, size_t nsb, float* out) {
+  for (size_t b = 0; b < nsb; ++b) dequant_q6_k_block(wire + b * 210, out + b * 256);
+}
+// rows x k K-quant GEMV (quant 1 Q4_K, 2 Q6_K) against a Q8_K activation row.
+OX void oracle_kquant_gemv(int quant, const uint8_t* wire, size_t rows, size_t k, const float* yd, const int8_t* yqs,
+                           float* out) {
+  const size_t nsb = k / 256, rb = quant_row_bytes(quant, k);
+#pragma omp parallel for schedule(static)
+  for (long r = 0; r < (long)rows; ++r)
+    out[r] = quant == Q_Q4_K ? q4_k_row_dot(wire + (size_t)r * rb, yd, yqs, nsb)
+                             : q6_k_row_dot(wire + (size_t)r * rb, yd, yqs, nsb);
+}
 OX void oracle_rms_norm(const float* x, const float* w, size_t rows, size_t n, float eps, float* out) {
   for (size_t r = 0; r < rows; ++r) rms_norm_row(x + r * n, w, n, eps, out + r * n);
 }
@@ -422,6 +618,7 @@ OX void* oracle_model_new(uint32_t L, uint32_t n_heads, uint32_t n_kv, uint32_t 
   Model* m = new Model();
   m->L = L; m->n_heads = n_heads; m->n_kv = n_kv; m->hd = hd; m->H = H; m->F = F; m->V = V;
   m->max_pos = max_pos; m->eps = eps; m->split_half = split_half;
+  m->qt.assign((size_t)L * 7, (uint8_t)Q_Q8_0);
   m->wq.assign(L, nullptr); m->wk = m->wq; m->wv = m->wq; m->wo = m->wq; m->wg = m->wq; m->wu = m->wq; m->wd = m->wq;
   m->attn_norm.assign(L, nullptr); m->ffn_norm = m->attn_norm; m->q_norm = m->attn_norm; m->k_norm = m->attn_norm;
   m->kc.assign((size_t)L * n_kv * max_pos * hd, 0.0f);
@@ -444,11 +641,31 @@ OX void oracle_model_set_output(void* p, const float* out_norm, const uint8_t* o
   Model* m = (Model*)p;
   m->out_norm = out_norm; m->out_w = out_w; m->embd = embd;
 }
-// tensor/mod.rs:2329-2398 Q8_0 embedding row: scale * q (exact).
+// Formats of one layer's seven projections (q, k, v, o, gate, up, down), of the output
+// projection and of the token embedding (0 Q8_0, 1 Q4_K, 2 Q6_K).
+OX void oracle_model_set_quant(void* p, uint32_t l, const uint8_t* quant7) {
+  Model* m = (Model*)p;
+  std::memcpy(&m->qt[(size_t)l * 7], quant7, 7);
+}
+OX void oracle_model_set_output_quant(void* p, int out_quant, int embd_quant) {
+  Model* m = (Model*)p;
+  m->out_quant = out_quant;
+  m->embd_quant = embd_quant;
+}
+// Embedding row (tensor/mod.rs:2329-2398 Q8_0: scale * q, exact; K-quant rows through the
+// block dequantizers).
 OX void oracle_model_embed(void* p, uint32_t token, float* out) {
   Model* m = (Model*)p;
-  size_t nb = m->H / 32;
-  oracle_dequant_q8_0_wire(m->embd + (size_t)token * nb * 34, nb, out);
+  const size_t rb = quant_row_bytes(m->embd_quant, m->H);
+  const uint8_t* row = m->embd + (size_t)token * rb;
+  if (m->embd_quant == Q_Q8_0) {
+    oracle_dequant_q8_0_wire(row, m->H / 32, out);
+  } else {
+    for (size_t sb = 0; sb < m->H / 256; ++sb) {
+      if (m->embd_quant == Q_Q4_K) dequant_q4_k_block(row + sb * 144, out + sb * 256);
+      else dequant_q6_k_block(row + sb * 210, out + sb * 256);
+    }
+  }
 }
 // One forward step at `pos` from an embedding row.  Optional captures:
 //   hidden_out [L+1][H]: the residual stream entering each layer and after the last;
@@ -466,7 +683,7 @@ OX int oracle_model_forward(void* p, const float* emb, uint32_t pos, const float
   if (hidden_out) std::memcpy(hidden_out + (size_t)m->L * m->H, m->h.data(), m->H * sizeof(float));
   if (logits_out || tok_out) {
     rms_norm_row(m->h.data(), m->out_norm, m->H, m->eps, m->xn.data());
-    linear_q8(m->out_w, m->V, m->H, m->xn.data(), m->logits.data(), m->xs, m->xq);
+    linear(*m, m->out_w, m->out_quant, m->V, m->H, m->xn.data(), m->logits.data());
     if (logits_out) std::memcpy(logits_out, m->logits.data(), m->V * sizeof(float));
     if (tok_out) *tok_out = oracle_argmax(m->logits.data(), m->V);
   }

@@ -51,6 +51,13 @@ _SIG = {
     "oracle_model_read_kv": (None, [vp, C.c_uint32, C.c_uint32, f32p, f32p]),
     "oracle_model_seed_kv": (None, [vp, C.c_uint32, C.c_uint32, f32p, f32p]),
     "oracle_serial_sum_rows": (None, [f32p, C.c_size_t, C.c_size_t, f32p]),
+    "oracle_quantize_q8_k": (None, [f32p, C.c_size_t, f32p, i8p]),
+    "oracle_nearest_int": (C.c_int32, [C.c_float]),
+    "oracle_dequant_q4_k": (None, [u8p, C.c_size_t, f32p]),
+    "oracle_dequant_q6_k": (None, [u8p, C.c_size_t, f32p]),
+    "oracle_kquant_gemv": (None, [C.c_int, u8p, C.c_size_t, C.c_size_t, f32p, i8p, f32p]),
+    "oracle_model_set_quant": (None, [vp, C.c_uint32, u8p]),
+    "oracle_model_set_output_quant": (None, [vp, C.c_int, C.c_int]),
 }
 
 _lib = None
@@ -152,6 +159,36 @@ def q8_0_gemm(wire, rows, k, xs, xq) -> np.ndarray:
     return out
 
 
+def quantize_q8_k(x):
+    """-> (scales f32 [n/256], quants i8 [n]) (inference.rs:17564-17599)."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    d = np.empty(x.size // 256, np.float32)
+    q = np.empty(x.size, np.int8)
+    lib().oracle_quantize_q8_k(P(x, C.c_float), x.size, P(d, C.c_float), P(q, C.c_int8))
+    return d, q
+
+
+def nearest_int(x: float) -> int:
+    return int(lib().oracle_nearest_int(float(x)))
+
+
+def dequant_kquant(quant: int, wire) -> np.ndarray:
+    wire = np.ascontiguousarray(wire, np.uint8)
+    nsb = wire.size // (144 if quant == 1 else 210)
+    out = np.empty(nsb * 256, np.float32)
+    fn = lib().oracle_dequant_q4_k if quant == 1 else lib().oracle_dequant_q6_k
+    fn(P(wire, C.c_uint8), nsb, P(out, C.c_float))
+    return out
+
+
+def kquant_gemv(quant: int, wire, rows, k, yd, yq) -> np.ndarray:
+    out = np.empty(rows, np.float32)
+    lib().oracle_kquant_gemv(quant, P(np.ascontiguousarray(wire, np.uint8), C.c_uint8), rows, k,
+                             P(np.ascontiguousarray(yd, np.float32), C.c_float),
+                             P(np.ascontiguousarray(yq, np.int8), C.c_int8), P(out, C.c_float))
+    return out
+
+
 def serial_sum_rows(x) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32)
     rows, n = x.shape
@@ -227,8 +264,12 @@ class OracleModel:
             norms = [layer["attn_norm"], layer["ffn_norm"], layer.get("q_norm"), layer.get("k_norm")]
             nptr = [P(a, C.c_float) if a is not None else None for a in norms]
             L.oracle_model_set_layer(self.h, i, *ws, *nptr)
+            q7 = np.ascontiguousarray(layer.get("quant", [0] * 7), np.uint8)
+            self._keep.append(q7)
+            L.oracle_model_set_quant(self.h, i, P(q7, C.c_uint8))
         L.oracle_model_set_output(self.h, P(model.output_norm, C.c_float), P(model.output, C.c_uint8),
                                   P(model.token_embd, C.c_uint8))
+        L.oracle_model_set_output_quant(self.h, cfg.output_quant(), cfg.embd_quant())
         kind = {"none": 0, "linear": 1, "llama3": 2}[cfg.rope_scaling]
         self.cos, self.sin = rope_tables(cfg.rope_dim, cfg.rope_theta, kind, cfg.rope_factor, cfg.rope_orig_ctx,
                                          cfg.rope_low, cfg.rope_high, None, 0, max_pos)

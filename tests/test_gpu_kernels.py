@@ -358,6 +358,77 @@ def test_attention_prefill_bit_exact(native, orc, nh, nkv, hd, pos0, T):
         assert np.array_equal(_bits(gxs[t]), _bits(ws)) and np.array_equal(gxq[t], wq)
 
 
+def test_quantize_q8_k_bit_exact(native, orc):
+    """Q8_K activation quantizer == quantize_q8_k_blocks, incl. zero blocks, |max| ties (first
+    wins), one-hot and huge/tiny blocks; per-32 sums of the quants."""
+    rng = np.random.default_rng(41)
+    nb = 64
+    x = rng.normal(0, 1, nb * 256).astype(np.float32)
+    b = x.reshape(nb, 256)
+    b[1] = 0.0
+    b[2] = rng.uniform(-1, 1, 256); b[2, 7], b[2, 200] = -3.0, 3.0
+    b[3] = rng.uniform(-1, 1, 256); b[3, 100], b[3, 20] = 3.0, -3.0
+    b[4] = 0.0; b[4, 255] = 1e-30
+    b[5] *= 1e30
+    b[6] = np.round(rng.normal(0, 40, 256)) / 127.0      # many exact .5 products: round-half-even
+    b[7] = -1.0
+    dx = _dev(x)
+    yd, yq, ybs = _buf(nb * 4), _buf(nb * 256), _buf(nb * 8 * 4)
+    _ok(native.camelid_hip_quantize_q8_k(dx.ptr, nb * 256, yd.ptr, yq.ptr, ybs.ptr, None))
+    wd, wq = orc.quantize_q8_k(x)
+    assert np.array_equal(_bits(yd.download(np.float32, nb)), _bits(wd))
+    gq = yq.download(np.int8, nb * 256)
+    assert np.array_equal(gq, wq)
+    assert np.array_equal(ybs.download(np.int32, nb * 8), wq.astype(np.int64).reshape(-1, 32).sum(1))
+
+
+def _kquant_wire(orc, rng, quant, rows, k):
+    """Random superblocks with finite f16 scales (every other byte uniformly random)."""
+    nsb, bb = k // 256, (144 if quant == 1 else 210)
+    wire = rng.integers(0, 256, (rows, nsb, bb), dtype=np.uint8)
+    if quant == 1:
+        wire[:, :, 0:4] = orc.f32_to_f16(rng.uniform(-2e-3, 2e-3, (rows, nsb, 2)).astype(np.float32)).view(
+            np.uint8).reshape(rows, nsb, 4)
+    else:
+        wire[:, :, 208:210] = orc.f32_to_f16(rng.uniform(-2e-3, 2e-3, (rows, nsb)).astype(np.float32)).view(
+            np.uint8).reshape(rows, nsb, 2)
+    return wire.ravel()
+
+
+def _kquant_planes(native, quant, wire, rows, k):
+    from camelid_amd._native import ptr
+    nsb = k // 256
+    a = np.empty(rows * k // 2, np.uint8)
+    b = np.empty(rows * nsb * (16 if quant == 1 else 64), np.uint8)
+    sc = np.empty(max(rows * nsb * 16, 1), np.int8)
+    d = np.empty(max(rows * nsb, 1), np.uint16)
+    _ok(native.camelid_kquant_repack(quant, ptr(wire, C.c_uint8), rows, k, ptr(a, C.c_uint8), ptr(b, C.c_uint8),
+                                     ptr(sc, C.c_int8), ptr(d, C.c_uint16)))
+    return _dev(a), _dev(b), _dev(sc), _dev(d)
+
+
+@pytest.mark.parametrize("quant,rows,k", [(1, 4096, 4096), (1, 12288, 4096), (1, 4096, 12288), (1, 36, 256),
+                                          (1, 16384, 2048), (2, 1024, 4096), (2, 20000, 4096), (2, 37, 512),
+                                          (2, 4096, 12288)])
+def test_kquant_gemv_bit_exact(native, orc, quant, rows, k):
+    """Q4_K (q4_k_dot_arm order) / Q6_K (8-lane q6_k_wire_row_dot order) GEMV == the CPU dots."""
+    rng = np.random.default_rng(rows + k + quant)
+    wire = _kquant_wire(orc, rng, quant, rows, k)
+    ydh, yqh = orc.quantize_q8_k(rng.normal(0, 1, k).astype(np.float32))
+    bsh = yqh.astype(np.int32).reshape(-1, 32).sum(1).astype(np.int32)
+    a, b, sc, d = _kquant_planes(native, quant, wire, rows, k)
+    yd, yq, ybs = _dev(ydh), _dev(yqh), _dev(bsh)
+    resid = rng.normal(0, 1, rows).astype(np.float32)
+    dres, y = _dev(resid), _buf(rows * 4)
+    _ok(native.camelid_hip_kquant_gemv(quant, a.ptr, b.ptr, sc.ptr, d.ptr, rows, k, yd.ptr, yq.ptr, ybs.ptr, y.ptr,
+                                       None, None))
+    want = orc.kquant_gemv(quant, wire, rows, k, ydh, yqh)
+    assert np.array_equal(_bits(y.download(np.float32, rows)), _bits(want))
+    _ok(native.camelid_hip_kquant_gemv(quant, a.ptr, b.ptr, sc.ptr, d.ptr, rows, k, yd.ptr, yq.ptr, ybs.ptr,
+                                       dres.ptr, dres.ptr, None))
+    assert np.array_equal(_bits(dres.download(np.float32, rows)), _bits(resid + want))
+
+
 @pytest.mark.parametrize("n", [1, 1000, 32000, 128256, 151936])
 def test_argmax_matches_first_max(native, orc, n):
     rng = np.random.default_rng(n)

@@ -72,6 +72,28 @@ def test_tiny_model_bit_exact(variant):
     sess.close()
 
 
+@pytest.mark.parametrize("kw", [dict(), dict(tied=True, n_layers=3)])
+def test_kquant_model_bit_exact(kw):
+    """A Qwen3-shaped Q4_K_M model (Q4_K projections and token table, Q6_K v and output,
+    QK-norm, split-half RoPE): hidden states, logits and tokens equal the CPU path's, the KV
+    cache too; the device-side loop (device K-quant embedding) gives the host loop's tokens."""
+    cfg = tiny_config(hidden=512, ffn_dim=768, n_heads=4, n_kv_heads=2, head_dim=128, vocab=1024, qk_norm=True,
+                      split_half=True, rope_theta=1e6, quant_scheme="q4_k_m", **kw)
+    sess, orc, max_rel = _run_pair(cfg, 10)
+    assert max_rel == 0.0 and sess.engine.uses_kquant()
+    n = sess.engine.filled()
+    for layer in range(cfg.n_layers):
+        kg, vg = sess.engine.read_kv_layer(layer, n)
+        ko, vo = orc.read_kv(layer, n)
+        assert np.array_equal(_bits(kg), _bits(ko)) and np.array_equal(_bits(vg), _bits(vo))
+    sess.close()
+    model = SyntheticModel.generate(cfg)
+    prompt = prompt_tokens(cfg)
+    host = ResidentSession(model, 40).generate(prompt, 12)
+    dev = ResidentSession(model, 40, device_loop=True).generate(prompt, 12)
+    assert host == dev
+
+
 def test_device_loop_matches_host_loop():
     cfg = tiny_config(n_layers=3, prompt_len=10)
     model = SyntheticModel.generate(cfg)

@@ -314,3 +314,96 @@ def test_oracle_expf_is_glibc(orc):
     y = orc.expf(x).astype(np.float64)
     want = np.exp(x.astype(np.float64))
     assert np.all(np.abs(y - want) <= 1.0001 * np.spacing(np.float32(want).astype(np.float32)).astype(np.float64) + 1e-45)
+
+
+# ------------------------------------------------------------------ K-quants (Q8_K, Q4_K, Q6_K)
+def test_q4_k_q6_k_dequant_fixtures_match_reference(orc):
+    """Q4_K / Q6_K superblock decode vs the reference's gguf==0.19.0 fixtures."""
+    for name, quant in (("Q4_K.json", 1), ("Q6_K.json", 2)):
+        _, raw, ref = _fixture(name)
+        got = orc.dequant_kquant(quant, raw).view(np.uint32)
+        assert np.array_equal(got, ref), name
+
+
+def test_nearest_int_is_round_half_even(orc):
+    """nearest_int_reference (inference.rs:17555-17561) == IEEE round-half-even (numpy rint)."""
+    xs = np.concatenate([np.arange(-300, 300) + 0.5, np.arange(-300, 300) + 0.25, np.arange(-300, 300) - 0.75,
+                         np.random.default_rng(5).uniform(-4e6, 4e6, 2000)]).astype(np.float32)
+    got = np.array([orc.nearest_int(v) for v in xs])
+    assert np.array_equal(got, np.rint(xs.astype(np.float64)).astype(np.int64))
+
+
+def test_quantize_q8_k_properties(orc):
+    rng = np.random.default_rng(6)
+    x = rng.normal(0, 1, 256 * 40).astype(np.float32)
+    x[256 * 3: 256 * 4] = 0.0                                    # all-zero block
+    blk = x[256 * 5: 256 * 6]
+    blk[:] = rng.uniform(-1, 1, 256)
+    blk[5], blk[9] = -2.0, 2.0                                   # |max| tie: the first (negative) wins
+    d, q = orc.quantize_q8_k(x)
+    q = q.reshape(-1, 256).astype(np.int64)
+    xb = x.reshape(-1, 256)
+    assert d[3] == 0.0 and not q[3].any()
+    assert q[5, 5] == -127 and q[5, 9] == 127 and d[5] > 0
+    for b in range(len(d)):
+        if b == 3:
+            continue
+        i = int(np.argmax(np.abs(xb[b])))
+        assert q[b, i] == -127                                   # the max maps to -127 (iscale = -127/max)
+        assert np.all(np.abs(q[b]) <= 127)
+        err = np.abs(d[b].astype(np.float64) * q[b] - xb[b])
+        assert np.all(err <= abs(float(d[b])) * 0.5 * (1 + 1e-5))
+
+
+def _kquant_exact_case(orc, rng, quant, rows, nsb):
+    """Wire bytes with power-of-two scales and small activations: every product and sum of the
+    dot is exact in f32, so the dot must equal the float64 sum over the (fixture-pinned)
+    dequantized weights."""
+    bb = 144 if quant == 1 else 210
+    wire = rng.integers(0, 256, (rows, nsb, bb), dtype=np.uint8)
+    if quant == 1:
+        d = (2.0 ** rng.integers(-6, -4, (rows, nsb, 2))).astype(np.float32)
+        wire[:, :, 0:4] = orc.f32_to_f16(d).view(np.uint8).reshape(rows, nsb, 4)
+    else:
+        d = (2.0 ** rng.integers(-6, -4, (rows, nsb))).astype(np.float32)
+        wire[:, :, 208:210] = orc.f32_to_f16(d).view(np.uint8).reshape(rows, nsb, 2)
+        wire[:, :, 192:208] = rng.integers(-8, 9, (rows, nsb, 16)).astype(np.int8).view(np.uint8)
+    wire = wire.ravel()
+    yd = (2.0 ** rng.integers(-1, 1, nsb)).astype(np.float32)
+    yq = rng.integers(-3, 4, nsb * 256).astype(np.int8)
+    return wire, yd, yq
+
+
+@pytest.mark.parametrize("quant", [1, 2])
+def test_kquant_dot_exact_case_equals_dequant_sum(orc, quant):
+    rng = np.random.default_rng(10 + quant)
+    rows, nsb = 64, 2
+    wire, yd, yq = _kquant_exact_case(orc, rng, quant, rows, nsb)
+    got = orc.kquant_gemv(quant, wire, rows, nsb * 256, yd, yq)
+    w = orc.dequant_kquant(quant, wire).reshape(rows, nsb * 256).astype(np.float64)
+    x = yq.astype(np.float64) * np.repeat(yd.astype(np.float64), 256)
+    assert np.array_equal(got.astype(np.float64), (w * x[None, :]).sum(1))
+
+
+@pytest.mark.parametrize("quant", [1, 2])
+def test_kquant_dot_float64_bound(orc, quant):
+    """Random superblocks (finite scales): the f32 dot is within a float64 error bound of the
+    exact dequantized sum."""
+    rng = np.random.default_rng(20 + quant)
+    rows, nsb = 128, 8
+    bb = 144 if quant == 1 else 210
+    wire = rng.integers(0, 256, (rows, nsb, bb), dtype=np.uint8)
+    if quant == 1:
+        wire[:, :, 0:4] = orc.f32_to_f16(rng.uniform(1e-3, 1e-2, (rows, nsb, 2)).astype(np.float32)).view(
+            np.uint8).reshape(rows, nsb, 4)
+    else:
+        wire[:, :, 208:210] = orc.f32_to_f16(rng.uniform(1e-3, 1e-2, (rows, nsb)).astype(np.float32)).view(
+            np.uint8).reshape(rows, nsb, 2)
+    wire = wire.ravel()
+    yd, yq = orc.quantize_q8_k(rng.normal(0, 1, nsb * 256).astype(np.float32))
+    got = orc.kquant_gemv(quant, wire, rows, nsb * 256, yd, yq).astype(np.float64)
+    w = orc.dequant_kquant(quant, wire).reshape(rows, nsb * 256).astype(np.float64)
+    x = yq.astype(np.float64) * np.repeat(yd.astype(np.float64), 256)
+    exact = (w * x[None, :]).sum(1)
+    bound = 1e-5 * (np.abs(w) * np.abs(x)[None, :]).sum(1) + 1e-6
+    assert np.all(np.abs(got - exact) <= bound)
