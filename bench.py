@@ -1,6 +1,8 @@
 """Decode benchmark: Llama-3.2-3B-architecture Q8_0, batch 1, one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config llama-3.2-3b] [--no-cpu-baseline]
+    python bench.py --config qwen3-8b | mistral-7b-v0.3 | tinyllama-1.1b   (the other decode configs)
+    python bench.py --sweep                                             (the Q8_0 kernel sweep)
 
 Workload: seeded synthetic N(0, 0.02) weights quantized to
 Q8_0, a 512-token random prompt prefilled (n-1 tokens, as the reference seam does), then
@@ -28,6 +30,15 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD published peak
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix-core peak, AMD published
+HEADLINE = "llama-3.2-3b"
+ARCH = {"llama-3.2-3b": "Llama-3.2-3B-arch Q8_0", "tinyllama-1.1b": "TinyLlama-1.1B-arch Q8_0",
+        "mistral-7b-v0.3": "Mistral-7B-v0.3-arch Q8_0 (8K context)", "qwen3-8b": "Qwen3-8B-arch Q4_K_M"}
+# Measured HBM bytes per launch of the dominant kernel (rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE passes scaled by a copy kernel's reading, profiles/); None until measured.
+TRAFFIC: dict = {}
+# Q8_0 [N, K] shapes, weights N(0, 0.02) and activations N(0, 1), seed 2
+SWEEP_SHAPES = [(2048, 2048), (5632, 2048), (2048, 5632), (32000, 2048), (128256, 3072)]
 
 
 def log(msg: str) -> None:
@@ -54,9 +65,58 @@ def cpu_baseline(model, cfg, prompt_len: int, n_steps: int, threads: int) -> dic
     dt = time.perf_counter() - t0
     orc.close()
     return {"value": round(n_steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n_steps} greedy decode steps of the same {cfg.name} Q8_0 model at positions "
+            "sample": f"{n_steps} greedy decode steps of the same {ARCH[cfg.name]} model at positions "
                       f"{n}..{n + n_steps - 1} (KV history seeded), oracle/camelid_oracle.cpp, "
                       f"{threads} OpenMP threads over output rows"}
+
+
+def run_sweep(iters_min: int = 200) -> dict:
+    """each [N, K] Q8_0 matrix as a batch-1 GEMV (GB/s against HBM peak) and as the
+    512-token prefill GEMM (int8 TOP/s against the matrix-core peak).  Weight copies rotate
+    over more than 1 GB so that no launch finds its matrix in L2 or MALL; the activations are
+    quantized on the device."""
+    import ctypes as C
+    from camelid_amd import _native as N
+    from camelid_amd.engine import DeviceBuffer
+    from camelid_amd.model import synth_f32, synth_q8_0
+    L = N.lib()
+    T = 512
+    out = []
+    for rows, k in SWEEP_SHAPES:
+        wire = synth_q8_0(f"sweep.{rows}x{k}.weight", 2, rows, k)
+        q = np.empty(rows * k, np.int8)
+        d = np.empty(rows * k // 32, np.uint16)
+        N.check(L.camelid_q8_0_repack(N.ptr(wire, C.c_uint8), rows, k, 34, N.ptr(q, C.c_int8), N.ptr(d, C.c_uint16)))
+        wbytes = rows * k * 34 / 32
+        copies = int(min(48, max(2, np.ceil(1.2e9 / wbytes))))
+        qb = [DeviceBuffer.from_array(q) for _ in range(copies)]
+        db = [DeviceBuffer.from_array(d) for _ in range(copies)]
+        x = DeviceBuffer.from_array(synth_f32(f"sweep.{rows}x{k}.x", 2, T * k, 1.0))
+        xq, xs = DeviceBuffer(T * k), DeviceBuffer(T * k // 32 * 4)
+        N.check(L.camelid_hip_quantize_q8_0(x.ptr, T * k, xq.ptr, xs.ptr, None))
+        y = DeviceBuffer(T * rows * 4)
+        qp = (N.vp * copies)(*[b.ptr for b in qb])
+        dp = (N.vp * copies)(*[b.ptr for b in db])
+        ms = C.c_float(0)
+        it = max(iters_min, 4 * copies)
+        N.check(L.camelid_hip_time_q8_0(0, qp, dp, copies, rows, k, xq.ptr, xs.ptr, 1, y.ptr, it, C.byref(ms)))
+        gemv_us = ms.value * 1e3 / it
+        gbytes = wbytes + k * 34 / 32 + rows * 4
+        itg = max(10, 2 * copies)
+        N.check(L.camelid_hip_time_q8_0(1, qp, dp, copies, rows, k, xq.ptr, xs.ptr, T, y.ptr, itg, C.byref(ms)))
+        gemm_us = ms.value * 1e3 / itg
+        ops = 2.0 * rows * k * T
+        out.append({"shape": [rows, k], "gemv_us": round(gemv_us, 2),
+                    "gemv_gbs": round(gbytes / gemv_us / 1e3, 1), "gemv_hbm_frac": round(gbytes / gemv_us / 1e3 / HBM_PEAK_GBS, 4),
+                    "gemm_tokens": T, "gemm_us": round(gemm_us, 1), "gemm_tops": round(ops / gemm_us / 1e6, 1),
+                    "gemm_mfma_frac": round(ops / gemm_us / 1e6 / INT8_PEAK_TOPS, 4), "weight_copies": copies})
+        log(f"sweep {rows}x{k}: GEMV {gemv_us:.2f} us {out[-1]['gemv_gbs']} GB/s; "
+            f"GEMM(T={T}) {gemm_us:.1f} us {out[-1]['gemm_tops']} TOP/s")
+        del qb, db, x, xq, xs, y
+    return {"metric": "Q8_0 GEMV GB/s and prefill GEMM int8 TOP/s, isolated kernel sweep, 1 MI355X",
+            "config": {"workload": "BASELINE configs[1]: Q8_0 [N,K] weights N(0,0.02) seed 2, activations N(0,1) "
+                                   "quantized on device; GEMV batch 1, GEMM batch 512"},
+            "peaks": {"hbm_gbs": HBM_PEAK_GBS, "int8_tops": INT8_PEAK_TOPS}, "shapes": out}
 
 
 def main() -> int:
@@ -69,6 +129,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=6)
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--sweep", action="store_true", help="run the isolated Q8_0 GEMV/GEMM sweep (configs[1])")
     ap.add_argument("--seed-kv", action="store_true",
                     help="seed the prompt's KV rows with random f16 values instead of running the prefill "
                          "(kernel profiling of the decode steps alone; skips the parity check)")
@@ -83,6 +144,14 @@ def main() -> int:
     from camelid_amd.engine import device_info
     from camelid_amd.model import CONFIGS, ResidentSession, SyntheticModel, prompt_tokens
 
+    if args.sweep:
+        dev_name, n_cu = device_info()
+        log(f"device {dev_name}, {n_cu} CUs; Q8_0 kernel sweep")
+        res = run_sweep()
+        res["config"]["device"] = dev_name
+        print(json.dumps(res), flush=True)
+        return 0
+
     cfg = CONFIGS[args.config]
     P = args.prompt or cfg.prompt_len
     K, W = args.steps, args.warmup
@@ -91,7 +160,7 @@ def main() -> int:
 
     t0 = time.perf_counter()
     model = SyntheticModel.generate(cfg)
-    log(f"generated synthetic Q8_0 weights in {time.perf_counter() - t0:.1f}s")
+    log(f"generated synthetic {ARCH[cfg.name]} weights in {time.perf_counter() - t0:.1f}s")
     prompt = prompt_tokens(cfg, P)
     max_pos = P + W + K
     t0 = time.perf_counter()
@@ -152,10 +221,11 @@ def main() -> int:
         assert [int(t) for t in toks2] == [int(t) for t in toks], "profiled pass diverged"
         g = prof["gemv"]
         achieved = g["bytes"] / (g["ms"] * 1e-3) / 1e9
+        kname = ("Q8_0 GEMV: k_gemv_k + k_gemv_gu_silu + k_gemv_argmax" if cfg.quant_scheme == "q8_0" else
+                 "K-quant GEMV: k_gemv_q4k + k_gemv_q6k (incl. lm_head)")
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                    "kernel": "Q8_0 GEMV: k_gemv_k + k_gemv_argmax, all launches of K steps "
-                              "(algorithmic bytes / summed dispatch durations)",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get(cfg.name),
+                    "kernel": kname + ", all launches of K steps (algorithmic bytes / summed dispatch durations)",
                     "avg_launch_us": round(g["ms"] * 1e3 / max(g["launches"], 1), 3),
                     "launches": g["launches"]}
         log("per-kernel (profiled pass): " + ", ".join(
@@ -169,7 +239,7 @@ def main() -> int:
         log(f"CPU baseline {cpu['value']} tok/s")
 
     out = {
-        "metric": "decode tok/s & % of HBM roofline, Llama-3.2-3B-arch Q8_0, batch 1, 1 MI355X",
+        "metric": f"decode tok/s & % of HBM roofline, {ARCH[cfg.name]}, batch 1, 1 MI355X",
         "value": round(tok_s, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -179,9 +249,10 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8xint8->int32, f32 accumulate (Q8_0)",
-        "data": "synthetic: seeded N(0,0.02) weights quantized to Q8_0, random prompt ids",
-        "config": {"workload": f"{cfg.name} Q8_0 greedy decode, batch 1, {P}-token prompt, "
+        "dtype": ("int8xint8->int32, f32 accumulate (Q8_0)" if cfg.quant_scheme == "q8_0" else
+                  "Q4_K/Q6_K x Q8_K -> int32, f32 accumulate"),
+        "data": f"synthetic: seeded N(0,0.02) weights quantized to {cfg.quant_scheme.upper()}, random prompt ids",
+        "config": {"workload": f"{ARCH[cfg.name]} greedy decode, batch 1, {P}-token prompt, "
                                f"steps at positions {start_pos}..{start_pos + K - 1}",
                    "prompt_len": P, "decode_steps": K, "device": dev_name},
         "hbm_roofline_frac": round(hbm_frac, 4),

@@ -1477,6 +1477,44 @@ int camelid_hip_kquant_gemv(uint8_t quant, const uint8_t* a, const uint8_t* b, c
   return launch_status("kquant_gemv");
 }
 
+int camelid_hip_time_q8_0(int batched, const int8_t* const* wq, const uint16_t* const* wd, uint32_t copies,
+                          uint32_t rows, uint32_t k, const int8_t* xq, const float* xs, uint32_t tokens, float* y,
+                          uint32_t iters, float* ms_out) {
+  if (!wq || !wd || !xq || !xs || !y || !ms_out || copies == 0 || iters == 0) return fail(nullptr, "null argument");
+  if (k % 32 || k == 0 || rows == 0 || (batched && (tokens == 0 || rows % 4)))
+    return fail(nullptr, "invalid shape");
+  hipStream_t s = nullptr;
+  if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return fail(nullptr, "stream create failed");
+  hipEvent_t a = nullptr, b = nullptr;
+  int rc = 0;
+  if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) {
+    rc = fail(nullptr, "event create failed");
+  } else {
+    auto launch = [&](uint32_t i) {
+      Q8Mat m;
+      m.q = const_cast<int8_t*>(wq[i % copies]);
+      m.d = const_cast<uint16_t*>(wd[i % copies]);
+      m.rows = rows;
+      m.k = k;
+      if (batched)
+        launch_gemm(m, tokens, xq, xs, y, nullptr, s);
+      else
+        launch_gemv(m, xq, xs, y, nullptr, s);
+    };
+    for (uint32_t i = 0; i < std::min(copies, 4u); ++i) launch(i);  // warm-up
+    (void)hipEventRecord(a, s);
+    for (uint32_t i = 0; i < iters; ++i) launch(i);
+    (void)hipEventRecord(b, s);
+    if (hipEventSynchronize(b) != hipSuccess || hipEventElapsedTime(ms_out, a, b) != hipSuccess)
+      rc = fail(nullptr, "timing failed");
+    if (!rc && hipGetLastError() != hipSuccess) rc = fail(nullptr, "launch failed");
+  }
+  if (a) (void)hipEventDestroy(a);
+  if (b) (void)hipEventDestroy(b);
+  (void)hipStreamDestroy(s);
+  return rc;
+}
+
 int camelid_hip_argmax(const float* x, uint32_t n, uint32_t* out, void* stream) {
   if (!x || !out) return fail(nullptr, "null argument");
   hipLaunchKernelGGL(cm::k_argmax, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, (int)n, out);

@@ -213,6 +213,14 @@ int camelid_hip_kquant_gemv(uint8_t quant, const uint8_t* a, const uint8_t* b, c
                             const uint16_t* d, uint32_t rows, uint32_t k, const float* yd,
                             const int8_t* yq, const int32_t* ybs, float* y, const float* resid,
                             void* stream);
+/* Measurement hook (no reference counterpart; the kernel sweep of the benchmark): `iters`
+ * launches of the Q8_0 GEMV (batched = 0) or of the prefill GEMM over `tokens` activation
+ * rows (batched = 1), rotating over `copies` weight matrices, timed with HIP events on a
+ * stream of its own; *ms_out = total milliseconds. */
+int camelid_hip_time_q8_0(int batched, const int8_t* const* wq, const uint16_t* const* wd,
+                          uint32_t copies, uint32_t rows, uint32_t k, const int8_t* xq,
+                          const float* xs, uint32_t tokens, float* y, uint32_t iters,
+                          float* ms_out);
 /* argmax_f32 (cuda_resident.rs:1847; CPU inference.rs:5912). */
 int camelid_hip_argmax(const float* x, uint32_t n, uint32_t* out, void* stream);
 /* Sequential-order f32 sums of rows [rows][n] (n <= 16384), evaluated with the
