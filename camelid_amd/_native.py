@@ -82,6 +82,8 @@ SIGNATURES: dict[str, tuple] = {
     "camelid_hip_attention_prefill": (C.c_int, [vp, vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                                 C.c_uint32, C.c_uint32, C.c_uint32, C.c_float, vp, vp, vp, vp]),
     "camelid_hip_quantize_q8_k": (C.c_int, [vp, C.c_uint32, vp, vp, vp, vp]),
+    "camelid_hip_rmsnorm_q8_k": (C.c_int, [vp, vp, C.c_uint32, C.c_float, vp, vp, vp, vp]),
+    "camelid_hip_silu_mul_q8_k": (C.c_int, [vp, C.c_uint32, vp, vp, vp, vp]),
     "camelid_kquant_repack": (C.c_int, [C.c_uint8, u8p, C.c_size_t, C.c_size_t, u8p, u8p, i8p, u16p]),
     "camelid_hip_kquant_gemv": (C.c_int, [C.c_uint8, vp, vp, vp, vp, C.c_uint32, C.c_uint32, vp, vp, vp, vp, vp,
                                           vp]),

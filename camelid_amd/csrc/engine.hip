@@ -69,6 +69,8 @@ struct LayerW {
   Q8Mat qkv, o, gu, down;
   bool generic = false;  // some projection is a K-quant: seven separate projections in p
   Proj p[7];
+  bool qk_stacked = false;  // generic layer: p[0] holds q|k stacked (same K-quant format)
+  bool gu_stacked = false;  // generic layer: p[4] holds gate|up stacked
   float* attn_norm = nullptr;
   float* ffn_norm = nullptr;
   float* q_norm = nullptr;
@@ -468,6 +470,16 @@ cm::Prefetch prefetch_of(const Q8Mat* m) {
   }
   return pf;
 }
+cm::Prefetch prefetch_of(const KMat* m) {
+  cm::Prefetch pf{nullptr, 0, nullptr, 0};
+  if (m && m->a) {
+    pf.a = reinterpret_cast<const uint32_t*>(m->a);
+    pf.a_lines = (size_t)m->rows * m->k / 2 / 128;
+    pf.b = reinterpret_cast<const uint32_t*>(m->b);
+    pf.b_lines = (size_t)m->rows * (m->k / 256) * (m->quant == CAMELID_Q4_K ? 16 : 64) / 128;
+  }
+  return pf;
+}
 constexpr uint32_t PREFETCH_WGS = 256;  // spare workgroups added to a kernel that reads ahead
 
 size_t attn_sc_bytes(uint32_t kvs) { return (((size_t)kvs + 3) & ~(size_t)3) * 4; }
@@ -477,9 +489,8 @@ template <bool FUSED>
 void launch_attention(uint32_t hd, uint32_t n_heads, int slots, hipStream_t s, const float* qsrc, int nh, int nkv,
                       int rope_dim, int split_half, const float* cb, const float* sb, int rs, const float* qn,
                       const float* kn, float eps, uint16_t* kc, float* vc, int layer, int kvs, const uint32_t* pos,
-                      float scale, float* att, int8_t* xq, float* xs, const Q8Mat* next = nullptr) {
+                      float scale, float* att, int8_t* xq, float* xs, cm::Prefetch pf) {
   const size_t lds = (size_t)slots * cm::ATT_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs);
-  const cm::Prefetch pf = prefetch_of(next);
   const uint32_t grid = n_heads + (pf.a_lines ? PREFETCH_WGS : 0);
 #define CM_ATT(HD)                                                                                                  \
   CM_LAUNCH((cm::k_attention<HD, FUSED>), dim3(grid), dim3(cm::att_nt(HD)), lds, s, qsrc, nh, nkv,  \
@@ -492,14 +503,18 @@ void launch_attention(uint32_t hd, uint32_t n_heads, int slots, hipStream_t s, c
 }
 
 // rows > 1: a [rows][n] batch, one workgroup per row (no read-ahead).
+// kd/kq/kbs (optional, n % 256 == 0): also the Q8_K quantization of the normalized rows.
 void launch_rmsnorm_quant(const float* x, const float* w, uint32_t n, float eps, int8_t* xq, float* xs, float* y,
-                          hipStream_t s, const Q8Mat* next = nullptr, uint32_t rows = 1) {
-  const cm::Prefetch pf = prefetch_of(rows == 1 ? next : nullptr);
+                          hipStream_t s, cm::Prefetch pf = cm::Prefetch{nullptr, 0, nullptr, 0}, uint32_t rows = 1,
+                          float* kd = nullptr,
+                          int8_t* kq = nullptr, int32_t* kbs = nullptr) {
+  if (rows != 1) pf = cm::Prefetch{nullptr, 0, nullptr, 0};
   const uint32_t grid = 1 + (pf.a_lines ? PREFETCH_WGS : 0);
   switch (cm::seg_chunk((int)n)) {
 #define CM_RMS(C)                                                                                                   \
   case C:                                                                                                           \
-    CM_LAUNCH(cm::k_rmsnorm_quant<C>, dim3(grid, rows), dim3(cm::RMS_NT), 0, s, x, w, (int)n, eps, xq, xs, y, pf); \
+    CM_LAUNCH(cm::k_rmsnorm_quant<C>, dim3(grid, rows), dim3(cm::RMS_NT), 0, s, x, w, (int)n, eps, xq, xs, y, pf, \
+              kd, kq, kbs);                                                                                         \
     break;
     CM_SEG_CHUNKS(CM_RMS)
 #undef CM_RMS
@@ -530,18 +545,26 @@ double kq_bytes(const KMat& m, bool resid) {
 
 // K-quant GEMV (+ residual, + per-workgroup argmax partials when part_v is set); returns
 // the number of workgroups.
+// xf (Q4_K only): the activation in f32, quantized to Q8_K inside the GEMV.
 uint32_t launch_kgemv(const KMat& m, const float* yd, const int8_t* yq, const int32_t* ybs, float* y,
-                      const float* resid, float* part_v, uint32_t* part_i, hipStream_t s) {
+                      const float* resid, float* part_v, uint32_t* part_i, hipStream_t s,
+                      const float* xf = nullptr) {
   const int rpw = m.rows >= 16384 ? 2 : 1;
   const uint32_t R = 4 * rpw, grid = (m.rows + R - 1) / R;
   if (m.quant == CAMELID_Q4_K) {
     const size_t lds = cm::kq4_lds_bytes((int)m.k, (int)R);
-    if (rpw == 2)
-      CM_LAUNCH(cm::k_gemv_q4k<2>, dim3(grid), dim3(cm::KQ_NT), lds, s, m.a, m.b, (int)m.rows, (int)m.k, yd, yq, ybs,
-                y, resid, part_v, part_i);
-    else
-      CM_LAUNCH(cm::k_gemv_q4k<1>, dim3(grid), dim3(cm::KQ_NT), lds, s, m.a, m.b, (int)m.rows, (int)m.k, yd, yq, ybs,
-                y, resid, part_v, part_i);
+    const int it = (int)(m.k / 32 + 63) / 64;  // 16-byte pieces per lane and row (k <= 16384: <= 8)
+    switch (it * 2 + (rpw == 2)) {
+#define CM_Q4(IT, RPW)                                                                                           \
+  case IT * 2 + (RPW == 2):                                                                                      \
+    CM_LAUNCH((cm::k_gemv_q4k<IT, RPW>), dim3(grid), dim3(cm::KQ_NT), lds, s, m.a, m.b, (int)m.rows, (int)m.k, yd, \
+              yq, ybs, y, resid, part_v, part_i, xf);                                                            \
+    break;
+      CM_Q4(1, 1) CM_Q4(1, 2) CM_Q4(2, 1) CM_Q4(2, 2) CM_Q4(3, 1) CM_Q4(3, 2) CM_Q4(4, 1) CM_Q4(4, 2)
+      CM_Q4(5, 1) CM_Q4(6, 1) CM_Q4(7, 1) CM_Q4(8, 1)
+      CM_Q4(5, 2) CM_Q4(6, 2) CM_Q4(7, 2) CM_Q4(8, 2)
+#undef CM_Q4
+    }
   } else {
     const size_t lds = cm::kq6_lds_bytes((int)m.k, (int)R);
     if (rpw == 2)
@@ -563,7 +586,8 @@ void gemv(camelid_hip_engine* e, const Q8Mat& m, float* y, const float* resid, c
 void rmsnorm(camelid_hip_engine* e, const float* w, const Q8Mat* next) {
   const uint32_t n = e->d.hidden;
   ProfScope ps(e, P_NORM, n * 8.0 + n * 34.0 / 32.0);
-  launch_rmsnorm_quant(e->h, w, n, e->d.eps, e->xq, e->xs, nullptr, e->stream, e->read_ahead ? next : nullptr);
+  launch_rmsnorm_quant(e->h, w, n, e->d.eps, e->xq, e->xs, nullptr, e->stream,
+                       prefetch_of(e->read_ahead ? next : nullptr));
 }
 
 // Q8_K quantization of n values (the K-quant projections' activation).
@@ -572,14 +596,19 @@ void quant_q8k(camelid_hip_engine* e, const float* x, uint32_t n) {
   CM_LAUNCH(cm::k_quantize_q8k, dim3(n / 256), dim3(256), 0, e->stream, x, e->kd, e->kq, e->kbs);
 }
 
-// One projection in its own format: Q8_0 from the Q8_0 activation, K-quants from the Q8_K one.
-void proj(camelid_hip_engine* e, const Proj& p, float* y, const float* resid) {
+// One projection in its own format: Q8_0 from the Q8_0 activation, K-quants from the Q8_K
+// one, or (xf given) from the f32 activation, which a Q4_K GEMV quantizes itself.
+void proj(camelid_hip_engine* e, const Proj& p, float* y, const float* resid, const float* xf = nullptr) {
   if (p.quant == CAMELID_Q8_0) {
     gemv(e, p.q8, y, resid);
-  } else {
-    ProfScope ps(e, P_GEMV, kq_bytes(p.kq, resid != nullptr));
-    launch_kgemv(p.kq, e->kd, e->kq, e->kbs, y, resid, nullptr, nullptr, e->stream);
+    return;
   }
+  if (xf && p.quant == CAMELID_Q6_K) {
+    quant_q8k(e, xf, p.kq.k);
+    xf = nullptr;
+  }
+  ProfScope ps(e, P_GEMV, kq_bytes(p.kq, resid != nullptr));
+  launch_kgemv(p.kq, e->kd, e->kq, e->kbs, y, resid, nullptr, nullptr, e->stream, xf);
 }
 
 // A layer with K-quant projections (forward_layer_timed, inference.rs:6228-6807): the same
@@ -592,37 +621,40 @@ void run_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cos_base,
   hipStream_t s = e->stream;
   const uint32_t nq = d.n_heads * d.head_dim, nkv = d.n_kv_heads * d.head_dim;
   auto is_k = [&](int i) { return L.p[i].quant != CAMELID_Q8_0; };
-  {
-    ProfScope ps(e, P_NORM, d.hidden * 12.0 + d.hidden * 34.0 / 32.0);
-    launch_rmsnorm_quant(e->h, L.attn_norm, d.hidden, d.eps, e->xq, e->xs, e->xn, s);
-  }
-  if (is_k(0) || is_k(1) || is_k(2)) quant_q8k(e, e->xn, d.hidden);
-  proj(e, L.p[0], e->qkv, nullptr);
-  proj(e, L.p[1], e->qkv + nq, nullptr);
+  // the RMSNorm kernel writes the Q8_K activation itself when a K-quant projection reads it
+  // read-ahead of the projection that runs next, in its own format
+  auto ahead = [&](const Proj& p) {
+    if (!e->read_ahead) return prefetch_of((const Q8Mat*)nullptr);
+    return p.quant == CAMELID_Q8_0 ? prefetch_of(&p.q8) : prefetch_of(&p.kq);
+  };
+  auto norm = [&](const float* w, bool k8, cm::Prefetch pf) {
+    ProfScope ps(e, P_NORM, d.hidden * 8.0 + d.hidden * 34.0 / 32.0 + (k8 ? d.hidden * (1.0 + 4.0 / 256 + 4.0 / 32) : 0.0));
+    launch_rmsnorm_quant(e->h, w, d.hidden, d.eps, e->xq, e->xs, nullptr, s, pf, 1, k8 ? e->kd : nullptr,
+                         k8 ? e->kq : nullptr, k8 ? e->kbs : nullptr);
+  };
+  norm(L.attn_norm, is_k(0) || is_k(1) || is_k(2), ahead(L.p[0]));
+  proj(e, L.p[0], e->qkv, nullptr);  // q, or q|k stacked
+  if (!L.qk_stacked) proj(e, L.p[1], e->qkv + nq, nullptr);
   proj(e, L.p[2], e->qkv + nq + nkv, nullptr);
   {
     ProfScope ps(e, P_ATTN, (nq + 2.0 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0));
     launch_attention<true>(d.head_dim, d.n_heads, e->att_slots, s, e->qkv, (int)d.n_heads, (int)d.n_kv_heads,
                            (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base, rope_stride, L.q_norm,
                            L.k_norm, d.eps, e->kc, e->vc, (int)l, (int)e->kvs, &e->st->pos, scale, e->att, e->xq,
-                           e->xs, nullptr);
+                           e->xs, ahead(L.p[3]));
   }
-  if (is_k(3)) quant_q8k(e, e->att, nq);
-  proj(e, L.p[3], e->h, e->h);
-  {
-    ProfScope ps(e, P_NORM, d.hidden * 12.0 + d.hidden * 34.0 / 32.0);
-    launch_rmsnorm_quant(e->h, L.ffn_norm, d.hidden, d.eps, e->xq, e->xs, e->xn, s);
-  }
-  if (is_k(4) || is_k(5)) quant_q8k(e, e->xn, d.hidden);
-  proj(e, L.p[4], e->gu, nullptr);
-  proj(e, L.p[5], e->gu + d.ffn_dim, nullptr);
+  proj(e, L.p[3], e->h, e->h, is_k(3) ? e->att : nullptr);
+  norm(L.ffn_norm, is_k(4) || is_k(5), ahead(L.p[4]));
+  proj(e, L.p[4], e->gu, nullptr);  // gate, or gate|up stacked
+  if (!L.gu_stacked) proj(e, L.p[5], e->gu + d.ffn_dim, nullptr);
   {
     ProfScope ps(e, P_SILU, d.ffn_dim * 12.0 + d.ffn_dim * 34.0 / 32.0);
-    const cm::Prefetch pf{nullptr, 0, nullptr, 0};
-    CM_LAUNCH(cm::k_silu_mul_quant, dim3((d.ffn_dim + 255) / 256), dim3(256), 0, s, e->gu, (int)d.ffn_dim, e->xq,
-              e->xs, e->actf, pf);
+    const cm::Prefetch pf = ahead(L.p[6]);
+    const bool k8 = is_k(6);
+    CM_LAUNCH(cm::k_silu_mul_quant, dim3((d.ffn_dim + 255) / 256 + (pf.a_lines ? PREFETCH_WGS : 0)), dim3(256), 0, s,
+              e->gu, (int)d.ffn_dim, e->xq,
+              e->xs, (float*)nullptr, pf, k8 ? e->kd : nullptr, k8 ? e->kq : nullptr, k8 ? e->kbs : nullptr);
   }
-  if (is_k(6)) quant_q8k(e, e->actf, d.ffn_dim);
   proj(e, L.p[6], e->h, e->h);
 }
 
@@ -644,7 +676,8 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const f
     launch_attention<true>(d.head_dim, d.n_heads, e->att_slots, s, e->qkv, (int)d.n_heads,
                            (int)d.n_kv_heads, (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base,
                            rope_stride, L.q_norm, L.k_norm, d.eps, e->kc, e->vc, (int)l, (int)e->kvs, &e->st->pos,
-                           scale, e->att, e->xq, e->xs, e->read_ahead ? &L.o : nullptr);
+                           scale, e->att, e->xq, e->xs,
+                           prefetch_of(e->read_ahead ? &L.o : nullptr));
   }
   gemv(e, L.o, e->h, e->h);
   rmsnorm(e, L.ffn_norm, &L.gu);
@@ -665,7 +698,8 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const f
     ProfScope ps(e, P_SILU, d.ffn_dim * 8.0 + d.ffn_dim * 34.0 / 32.0);
     const cm::Prefetch pf = prefetch_of(e->read_ahead ? &L.down : nullptr);
     const uint32_t grid = (d.ffn_dim + 255) / 256 + (pf.a_lines ? PREFETCH_WGS : 0);
-    CM_LAUNCH(cm::k_silu_mul_quant, dim3(grid), dim3(256), 0, s, e->gu, (int)d.ffn_dim, e->xq, e->xs, nullptr, pf);
+    CM_LAUNCH(cm::k_silu_mul_quant, dim3(grid), dim3(256), 0, s, e->gu, (int)d.ffn_dim, e->xq, e->xs, nullptr, pf,
+              (float*)nullptr, (int8_t*)nullptr, (int32_t*)nullptr);
   }
   if (e->gu_fused)
     gemv(e, L.down, e->h, e->h, e->aq, e->as);  // the activation quantized by the fused gate/up kernel
@@ -696,10 +730,12 @@ void run_head(camelid_hip_engine* e, uint32_t* tokens, uint32_t cap) {
     nparts = launch_gemv_argmax(m, e->xq, e->xs, e->logits, e->part_v, e->part_i, e->stream);
   } else {
     {
-      ProfScope ps(e, P_NORM, e->d.hidden * 12.0 + e->d.hidden * 34.0 / 32.0);
-      launch_rmsnorm_quant(e->h, e->out_norm, e->d.hidden, e->d.eps, e->xq, e->xs, e->xn, e->stream);
+      const double H = e->d.hidden;
+      ProfScope ps(e, P_NORM, H * 8.0 + H * 34.0 / 32.0 + H * (1.0 + 4.0 / 256 + 4.0 / 32));
+      launch_rmsnorm_quant(e->h, e->out_norm, e->d.hidden, e->d.eps, e->xq, e->xs, nullptr, e->stream,
+                           prefetch_of(e->read_ahead ? &e->out_k : nullptr), 1,
+                           e->kd, e->kq, e->kbs);
     }
-    quant_q8k(e, e->xn, e->d.hidden);
     ProfScope ps(e, P_GEMV, kq_bytes(e->out_k, false));
     nparts = launch_kgemv(e->out_k, e->kd, e->kq, e->kbs, e->logits, nullptr, e->part_v, e->part_i, e->stream);
   }
@@ -764,7 +800,7 @@ void prefill_chunk(camelid_hip_engine* e, const float* cosv, const float* sinv, 
   const uint32_t half = d.rope_dim / 2;
   for (uint32_t l = 0; l < d.n_layers; ++l) {
     const LayerW& L = e->layers[l];
-    launch_rmsnorm_quant(e->pf_h, L.attn_norm, d.hidden, d.eps, e->pf_xq, e->pf_xs, nullptr, s, nullptr, T);
+    launch_rmsnorm_quant(e->pf_h, L.attn_norm, d.hidden, d.eps, e->pf_xq, e->pf_xs, nullptr, s, cm::Prefetch{}, T);
     launch_gemm(L.qkv, T, e->pf_xq, e->pf_xs, e->pf_qkv, nullptr, s);
     CM_LAUNCH(cm::k_rope_kv, dim3(d.n_heads + d.n_kv_heads, T), dim3(64), 0, s, e->pf_qkv, (int)d.n_heads,
               (int)d.n_kv_heads, (int)d.head_dim, (int)d.rope_dim, (int)d.split_half_pairing, cosv, sinv, L.q_norm,
@@ -773,7 +809,7 @@ void prefill_chunk(camelid_hip_engine* e, const float* cosv, const float* sinv, 
     launch_attn_prefill(d.head_dim, d.n_heads, d.n_kv_heads, T, e->pf_q, e->kc, e->vc, (int)l, (int)e->kvs,
                         (int)pos0, scale, nullptr, e->pf_xq, e->pf_xs, s);
     launch_gemm(L.o, T, e->pf_xq, e->pf_xs, e->pf_h, e->pf_h, s);
-    launch_rmsnorm_quant(e->pf_h, L.ffn_norm, d.hidden, d.eps, e->pf_xq, e->pf_xs, nullptr, s, nullptr, T);
+    launch_rmsnorm_quant(e->pf_h, L.ffn_norm, d.hidden, d.eps, e->pf_xq, e->pf_xs, nullptr, s, cm::Prefetch{}, T);
     launch_gemm(L.gu, T, e->pf_xq, e->pf_xs, e->pf_gu, nullptr, s);
     CM_LAUNCH(cm::k_silu_rows, dim3((d.ffn_dim + 255) / 256, T), dim3(256), 0, s, e->pf_gu, (int)d.ffn_dim,
               (int)e->gu_fused, e->pf_xq, e->pf_xs);
@@ -940,14 +976,33 @@ int camelid_hip_set_layer(camelid_hip_engine* e, uint32_t layer, const uint8_t* 
     // seven separate projections, each in its own format
     const uint32_t rows[7] = {nq, nkv, nkv, d.hidden, d.ffn_dim, d.ffn_dim, d.hidden};
     const uint32_t ks[7] = {d.hidden, d.hidden, d.hidden, nq, d.hidden, d.hidden, d.ffn_dim};
+    // q|k and gate|up of one K-quant format go up as one stacked matrix (one launch each)
+    const bool qk = quant[0] == quant[1] && quant[0] != CAMELID_Q8_0;
+    const bool gu = quant[4] == quant[5] && quant[4] != CAMELID_Q8_0;
+    if (L.set && (qk != L.qk_stacked || gu != L.gu_stacked)) return fail(e, "a layer's formats cannot change after upload");
     for (int i = 0; i < 7; ++i) {
       Proj& P = L.p[i];
       if (L.set && P.quant != quant[i]) return fail(e, "a layer's formats cannot change after upload");
       P.quant = quant[i];
-      const int rc = quant[i] == CAMELID_Q8_0 ? upload_q8(e, &P.q8, {{w[i], len[i], rows[i]}}, ks[i], q8_layout)
-                                              : upload_kq(e, &P.kq, w[i], len[i], rows[i], ks[i], quant[i]);
+      if ((i == 1 && qk) || (i == 5 && gu)) continue;  // uploaded with its partner
+      int rc;
+      if ((i == 0 && qk) || (i == 4 && gu)) {
+        if (!w[i] || !w[i + 1]) return fail(e, "missing projection bytes");
+        std::vector<uint8_t> both(len[i] + len[i + 1]);
+        std::memcpy(both.data(), w[i], len[i]);
+        std::memcpy(both.data() + len[i], w[i + 1], len[i + 1]);
+        const size_t per_row = (size_t)(ks[i] / 256) * kq_block_bytes(quant[i]);
+        if (len[i] != (size_t)rows[i] * per_row || len[i + 1] != (size_t)rows[i + 1] * per_row)
+          return fail(e, "K-quant byte length does not match the projection shape");
+        rc = upload_kq(e, &P.kq, both.data(), both.size(), rows[i] + rows[i + 1], ks[i], quant[i]);
+      } else {
+        rc = quant[i] == CAMELID_Q8_0 ? upload_q8(e, &P.q8, {{w[i], len[i], rows[i]}}, ks[i], q8_layout)
+                                      : upload_kq(e, &P.kq, w[i], len[i], rows[i], ks[i], quant[i]);
+      }
       if (rc) return 1;
     }
+    L.qk_stacked = qk;
+    L.gu_stacked = gu;
     if (upload_f32(e, &L.attn_norm, attn_norm, d.hidden) || upload_f32(e, &L.ffn_norm, ffn_norm, d.hidden)) return 1;
     if (q_norm && (upload_f32(e, &L.q_norm, q_norm, d.head_dim) || upload_f32(e, &L.k_norm, k_norm, d.head_dim)))
       return 1;
@@ -1383,8 +1438,46 @@ int camelid_hip_silu_mul_quantize(const float* gu, uint32_t n, int8_t* xq, float
   if (n % 32) return fail(nullptr, "n must be a multiple of 32");
   if (n == 0) return 0;
   hipLaunchKernelGGL(cm::k_silu_mul_quant, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, gu, (int)n, xq,
-                     xs, act, prefetch_of(nullptr));
+                     xs, act, prefetch_of((const Q8Mat*)nullptr), (float*)nullptr, (int8_t*)nullptr, (int32_t*)nullptr);
   return launch_status("silu_mul_quantize");
+}
+
+int camelid_hip_rmsnorm_q8_k(const float* x, const float* w, uint32_t n, float eps, float* yd, int8_t* yq,
+                             int32_t* ybs, void* stream) {
+  if (!x || !w || !yd || !yq || !ybs) return fail(nullptr, "null argument");
+  if (n == 0 || n % 256 || n > (uint32_t)cm::SEG_MAX_N) return fail(nullptr, "n must be a multiple of 256, <= 16384");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15)
+    return fail(nullptr, "x and w must be 16-byte aligned");
+  int8_t* xq = nullptr;
+  float* xs = nullptr;
+  if (hipMalloc(&xq, n) != hipSuccess || hipMalloc(&xs, n / 32 * 4) != hipSuccess) {
+    (void)hipFree(xq);
+    return fail(nullptr, "scratch allocation failed");
+  }
+  launch_rmsnorm_quant(x, w, n, eps, xq, xs, nullptr, (hipStream_t)stream, cm::Prefetch{}, 1, yd, yq, ybs);
+  const int rc = launch_status("rmsnorm_q8_k");
+  (void)hipStreamSynchronize((hipStream_t)stream);
+  (void)hipFree(xq);
+  (void)hipFree(xs);
+  return rc;
+}
+
+int camelid_hip_silu_mul_q8_k(const float* gu, uint32_t n, float* yd, int8_t* yq, int32_t* ybs, void* stream) {
+  if (!gu || !yd || !yq || !ybs) return fail(nullptr, "null argument");
+  if (n == 0 || n % 256) return fail(nullptr, "n must be a multiple of 256");
+  int8_t* xq = nullptr;
+  float* xs = nullptr;
+  if (hipMalloc(&xq, n) != hipSuccess || hipMalloc(&xs, n / 32 * 4) != hipSuccess) {
+    (void)hipFree(xq);
+    return fail(nullptr, "scratch allocation failed");
+  }
+  hipLaunchKernelGGL(cm::k_silu_mul_quant, dim3(n / 256), dim3(256), 0, (hipStream_t)stream, gu, (int)n, xq, xs,
+                     (float*)nullptr, prefetch_of((const Q8Mat*)nullptr), yd, yq, ybs);
+  const int rc = launch_status("silu_mul_q8_k");
+  (void)hipStreamSynchronize((hipStream_t)stream);
+  (void)hipFree(xq);
+  (void)hipFree(xs);
+  return rc;
 }
 
 int camelid_hip_rope_kv(const float* qkv, uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t rope_dim,
@@ -1410,7 +1503,8 @@ int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const fl
   if (slots == 0) return fail(nullptr, "max_pos too large for the decode attention");
   launch_attention<false>(hd, n_heads, slots, (hipStream_t)stream, qrot, (int)n_heads, (int)n_kv,
                           (int)hd, 0, nullptr, nullptr, 0, nullptr, nullptr, 0.0f, const_cast<uint16_t*>(kc),
-                          const_cast<float*>(vc), (int)layer, (int)max_pos, d_pos, scale, att_out, xq, xs);
+                          const_cast<float*>(vc), (int)layer, (int)max_pos, d_pos, scale, att_out, xq, xs,
+                          prefetch_of((const Q8Mat*)nullptr));
   return launch_status("attention_decode");
 }
 

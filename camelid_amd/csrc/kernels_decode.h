@@ -377,6 +377,93 @@ __device__ __forceinline__ float quantize_block_regs(const float (&y)[32], uint3
   return scale;
 }
 
+// ---------------------------------------------------------------------------
+// Q8_K quantization (inference.rs:17564-17599 quantize_q8_k_blocks): per 256-value block,
+// max = the signed value of the first largest |x| (a strict '>' scan from 0), iscale =
+// -127/max, q = min(nearest_int(iscale*x), 127), d = 1/iscale; a block whose |x| never
+// exceeds 0 gives d = 0 and zero quants.  nearest_int: inference.rs:17555-17561.
+__device__ __forceinline__ int nearest_int_ref(float f) {
+  const float v = f + 12582912.0f;
+  return (int)(__float_as_uint(v) & 0x007fffffu) - 0x00400000;
+}
+
+// (|x|, index, x) of the first largest |x|: keep the incumbent unless the challenger is
+// larger, or equal with a smaller index.
+__device__ __forceinline__ void amax_pick(float& a, int& i, float& v, float oa, int oi, float ov) {
+  if (oa > a || (oa == a && oi < i)) {
+    a = oa;
+    i = oi;
+    v = ov;
+  }
+}
+
+// Q8_K block held as eight 32-value pieces by eight consecutive lanes (piece j = values
+// 32j..32j+31 of the block, in lane j of the group): each lane writes its 32 quants and their
+// sum; the group's first lane writes the block scale.
+__device__ __forceinline__ void quantize_q8k_lanes8(const float (&y)[32], int8_t* __restrict__ q32,
+                                                    int32_t* __restrict__ bsum, float* __restrict__ d_out) {
+  const int j = threadIdx.x & 7;
+  float a = 0.0f, v = 0.0f;
+  int idx = 0x7fffffff;
+#pragma unroll
+  for (int e = 0; e < 32; ++e)
+    if (fabsf(y[e]) > a) {
+      a = fabsf(y[e]);
+      v = y[e];
+      idx = 32 * j + e;
+    }
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) amax_pick(a, idx, v, __shfl_xor(a, o), __shfl_xor(idx, o), __shfl_xor(v, o));
+  const float iscale = a > 0.0f ? -127.0f / v : 0.0f;
+  int sum = 0;
+#pragma unroll
+  for (int w4 = 0; w4 < 8; ++w4) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int q = a > 0.0f ? min(nearest_int_ref(iscale * y[w4 * 4 + e]), 127) : 0;
+      sum += (int8_t)q;
+      word |= ((uint32_t)q & 0xffu) << (8 * e);
+    }
+    reinterpret_cast<uint32_t*>(q32)[w4] = word;
+  }
+  *bsum = sum;
+  if (j == 0) *d_out = a > 0.0f ? 1.0f / iscale : 0.0f;
+}
+
+// Q8_K block of a 256-thread workgroup, one value per thread (thread t = value t): writes
+// the quants, the per-32 sums and the scale.  Every thread of the workgroup must call it.
+__device__ __forceinline__ void quantize_q8k_wg256(float x, int8_t* __restrict__ yq, int32_t* __restrict__ ybs,
+                                                   float* __restrict__ yd) {
+  __shared__ float s_a[4], s_v[4];
+  __shared__ int s_i[4];
+  const int tid = threadIdx.x;
+  float a = fabsf(x), v = x;
+  int idx = tid;
+  if (!(a > 0.0f)) a = 0.0f;  // zeros and NaN never win against the scan's initial 0
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) amax_pick(a, idx, v, __shfl_xor(a, o), __shfl_xor(idx, o), __shfl_xor(v, o));
+  if ((tid & 63) == 0) {
+    s_a[tid >> 6] = a;
+    s_i[tid >> 6] = idx;
+    s_v[tid >> 6] = v;
+  }
+  __syncthreads();
+  a = s_a[0];
+  idx = s_i[0];
+  v = s_v[0];
+  for (int w = 1; w < 4; ++w) amax_pick(a, idx, v, s_a[w], s_i[w], s_v[w]);
+  const float iscale = a > 0.0f ? -127.0f / v : 0.0f;
+  const int q = a > 0.0f ? min(nearest_int_ref(iscale * x), 127) : 0;
+  const int8_t q8 = (int8_t)q;
+  yq[tid] = q8;
+  int bs = q8;
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) bs += __shfl_xor(bs, o);
+  if ((tid & 31) == 0) ybs[tid >> 5] = bs;
+  if (tid == 0) *yd = a > 0.0f ? 1.0f / iscale : 0.0f;
+}
+
 __device__ __forceinline__ float block_max(float v, float* red) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
@@ -766,7 +853,8 @@ template <int C>
 __global__ __launch_bounds__(RMS_NT) void k_rmsnorm_quant(const float* __restrict__ x, const float* __restrict__ w,
                                                           int n, float eps, int8_t* __restrict__ xq,
                                                           float* __restrict__ xs, float* __restrict__ y_out,
-                                                          Prefetch pf) {
+                                                          Prefetch pf, float* __restrict__ kd,
+                                                          int8_t* __restrict__ kq, int32_t* __restrict__ kbs) {
   constexpr int BPT = (C + 31) / 32;  // blocks per thread
   __shared__ __align__(16) float sq[RMS_NT * C];
   __shared__ __align__(16) uint32_t ps[seg_binades(C) * (RMS_NT * C + 4)];
@@ -780,6 +868,11 @@ __global__ __launch_bounds__(RMS_NT) void k_rmsnorm_quant(const float* __restric
     xq += row * n;
     xs += row * (n >> 5);
     if (y_out) y_out += row * n;
+    if (kd) {
+      kd += row * (n >> 8);
+      kq += row * n;
+      kbs += row * (n >> 5);
+    }
   }
   const int tid = threadIdx.x;
   const int nb = n >> 5;
@@ -824,6 +917,8 @@ __global__ __launch_bounds__(RMS_NT) void k_rmsnorm_quant(const float* __restric
       uint4* qp = reinterpret_cast<uint4*>(xq + blk * 32);
       qp[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
       qp[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+      // Q8_K for K-quant consumers (n % 256 == 0: a 256-block is 8 consecutive lanes' blocks)
+      if (kd) quantize_q8k_lanes8(y, kq + blk * 32, kbs + blk, kd + (blk >> 3));
     }
   }
 }
@@ -848,9 +943,12 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float* __restrict__
 }
 
 // SwiGLU (tensor/mod.rs:1943-1967) + Q8_0 quantization.  gu = [gate(n) | up(n)].
+// kd (optional, n % 256 == 0): also the Q8_K quantization of the activation, one block per
+// workgroup.
 __global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict__ gu, int n, int8_t* __restrict__ xq,
                                                         float* __restrict__ xs, float* __restrict__ act_out,
-                                                        Prefetch pf) {
+                                                        Prefetch pf, float* __restrict__ kd,
+                                                        int8_t* __restrict__ kq, int32_t* __restrict__ kbs) {
   const int nwork = (n + 255) / 256;
   if ((int)blockIdx.x >= nwork) {  // spare workgroups: read ahead the down projection
     __shared__ float sink[1];
@@ -865,6 +963,7 @@ __global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict_
   const float d = quantize_lane32(a, &q);
   xq[i] = q;
   if ((i & 31) == 0) xs[i >> 5] = d;
+  if (kd) quantize_q8k_wg256(a, kq + (size_t)blockIdx.x * 256, kbs + (size_t)blockIdx.x * 8, kd + blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------

@@ -13,61 +13,13 @@
 namespace cm {
 
 // ---------------------------------------------------------------------------
-// Q8_K quantization (inference.rs:17564-17599 quantize_q8_k_blocks), one workgroup per
-// 256-value block: max = the signed value of the first largest |x| (a strict '>' scan),
-// iscale = -127/max, q = min(nearest_int(iscale*x), 127), d = 1/iscale; a block whose |x|
-// never exceeds 0 gives d = 0 and zero quants.  Also writes the per-32 sums of the quants
-// (the Q4_K mins side).  nearest_int: inference.rs:17555-17561.
-__device__ __forceinline__ int nearest_int_ref(float f) {
-  const float v = f + 12582912.0f;
-  return (int)(__float_as_uint(v) & 0x007fffffu) - 0x00400000;
-}
-
+// Q8_K quantization of n values (quantize_q8k, cuda_resident.rs:1416-1490), one workgroup per
+// 256-value block (quantize_q8k_wg256: inference.rs:17564-17599), with the per-32 quant sums
+// the Q4_K mins side reads.
 __global__ __launch_bounds__(256) void k_quantize_q8k(const float* __restrict__ x, float* __restrict__ yd,
                                                       int8_t* __restrict__ yq, int32_t* __restrict__ ybs) {
-  __shared__ float sa[4];
-  __shared__ int si[4];
-  const int s = blockIdx.x, tid = threadIdx.x;
-  const float v = x[(size_t)s * 256 + tid];
-  float a = fabsf(v);
-  if (!(a > 0.0f)) a = 0.0f;  // zeros and NaN never win against the scan's initial 0
-  int idx = tid;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float oa = __shfl_xor(a, o);
-    const int oi = __shfl_xor(idx, o);
-    if (oa > a || (oa == a && oi < idx)) {
-      a = oa;
-      idx = oi;
-    }
-  }
-  if ((tid & 63) == 0) {
-    sa[tid >> 6] = a;
-    si[tid >> 6] = idx;
-  }
-  __syncthreads();
-  a = sa[0];
-  idx = si[0];
-  for (int w = 1; w < 4; ++w)
-    if (sa[w] > a) {  // waves are in index order: equal values keep the earlier wave
-      a = sa[w];
-      idx = si[w];
-    }
-  int q = 0;
-  float d = 0.0f;
-  if (a > 0.0f) {
-    const float mx = x[(size_t)s * 256 + idx];
-    const float iscale = -127.0f / mx;
-    q = min(nearest_int_ref(iscale * v), 127);
-    d = 1.0f / iscale;
-  }
-  const int8_t q8 = (int8_t)q;
-  yq[(size_t)s * 256 + tid] = q8;
-  int bs = q8;
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) bs += __shfl_xor(bs, o);
-  if ((tid & 31) == 0) ybs[(size_t)s * 8 + (tid >> 5)] = bs;
-  if (tid == 0) yd[s] = d;
+  const size_t s = blockIdx.x;
+  quantize_q8k_wg256(x[s * 256 + threadIdx.x], yq + s * 256, ybs + s * 8, yd + s);
 }
 
 // Integer sum over lane groups of 2^m consecutive lanes (xor butterflies; exact).
@@ -76,6 +28,38 @@ __device__ __forceinline__ int group_sum(int v) {
 #pragma unroll
   for (int o = 1; o < W; o <<= 1) v += __shfl_xor(v, o);
   return v;
+}
+
+// Q8_K quantization of one 256-value block by one wave (lane l holds values 4l..4l+3) into
+// LDS: quants, per-32 sums and the scale (inference.rs:17564-17599, as quantize_q8k_wg256).
+__device__ __forceinline__ void quantize_q8k_wave(const float* __restrict__ x, int8_t* q, int* bs, float* d) {
+  const int lane = threadIdx.x & 63;
+  const float4 v4 = reinterpret_cast<const float4*>(x)[lane];
+  const float vals[4] = {v4.x, v4.y, v4.z, v4.w};
+  float a = 0.0f, v = 0.0f;
+  int idx = 0x7fffffff;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (fabsf(vals[e]) > a) {
+      a = fabsf(vals[e]);
+      v = vals[e];
+      idx = 4 * lane + e;
+    }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) amax_pick(a, idx, v, __shfl_xor(a, o), __shfl_xor(idx, o), __shfl_xor(v, o));
+  const float iscale = a > 0.0f ? -127.0f / v : 0.0f;
+  uint32_t word = 0;
+  int sum = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int qv = a > 0.0f ? min(nearest_int_ref(iscale * vals[e]), 127) : 0;
+    sum += (int8_t)qv;
+    word |= ((uint32_t)qv & 0xffu) << (8 * e);
+  }
+  reinterpret_cast<uint32_t*>(q)[lane] = word;
+  sum = group_sum<8>(sum);
+  if ((lane & 7) == 0) bs[lane >> 3] = sum;
+  if (lane == 0) *d = a > 0.0f ? 1.0f / iscale : 0.0f;
 }
 
 constexpr int KQ_NT = 256;  // 4 waves
@@ -88,9 +72,13 @@ __host__ __device__ inline int kq_rows_per_wg(int rpw) { return 4 * rpw; }
 //   (exact integers), then  sumf = fma(-(y.d*dmin), prod, sumf); sumf = fma(y.d*d, sumi, sumf)
 //   in superblock order from 0;  y[row] = (resid ? resid[row] : 0) + sumf.
 // Lane work unit: one 16-byte nibble piece (32 weights: piece j of superblock s pairs its low
-// nibbles with q8[64(j/2) + 16(j%2) ..] and its high nibbles 32 values further); the 8
-// lanes of a superblock reduce their integers with butterflies, the first writes the
-// superblock's four fold operands to LDS, and one lane per row folds them in order.
+// nibbles with q8[64(j/2) + 16(j%2) ..] and its high nibbles 32 values further); IT pieces
+// per lane and row, every load of a wave issued before the first dot; the 8 lanes of a
+// superblock reduce their integers with butterflies, the first writes the superblock's four
+// fold operands to LDS, and one lane per row folds them in order.
+// xf (optional): the activation in f32, quantized to Q8_K by the workgroup itself (one wave
+// per 256-value block) instead of read from yd/yq/ybs: a K-quant projection of the attention
+// output needs no separate quantizer launch.
 // Dynamic LDS: K quants + K/256 scales + K/32 sums + rows * K/256 * 16 bytes.
 __host__ __device__ inline size_t kq4_terms_offset(int K) {
   return ((size_t)K + (size_t)(K / 256) * 4 + (size_t)(K / 32) * 4 + 15) & ~(size_t)15;
@@ -99,12 +87,12 @@ __host__ __device__ inline size_t kq4_lds_bytes(int K, int R) {
   return kq4_terms_offset(K) + (size_t)R * (K / 256) * 16;
 }
 
-template <int RPW>
+template <int IT, int RPW>
 __global__ __launch_bounds__(KQ_NT) void k_gemv_q4k(const uint8_t* __restrict__ nib, const uint8_t* __restrict__ hdr,
                                                     int rows, int K, const float* __restrict__ yd,
                                                     const int8_t* __restrict__ yq, const int32_t* __restrict__ ybs,
                                                     float* y, const float* resid, float* __restrict__ part_v,
-                                                    uint32_t* __restrict__ part_i) {
+                                                    uint32_t* __restrict__ part_i, const float* __restrict__ xf) {
   constexpr int R = 4 * RPW;
   extern __shared__ __align__(16) unsigned char smem[];
   const int NSB = K >> 8, NC = K >> 5;
@@ -114,24 +102,41 @@ __global__ __launch_bounds__(KQ_NT) void k_gemv_q4k(const uint8_t* __restrict__ 
   float4* terms = reinterpret_cast<float4*>(smem + kq4_terms_offset(K));
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int row0 = blockIdx.x * R;
-  for (int c = tid; c < (K >> 4); c += KQ_NT) reinterpret_cast<int4*>(xq)[c] = reinterpret_cast<const int4*>(yq)[c];
-  for (int i = tid; i < NSB; i += KQ_NT) xd[i] = yd[i];
-  for (int i = tid; i < NC; i += KQ_NT) xbs[i] = ybs[i];
+  // every weight and header load of this wave first (pieces lane + 64 i of each row; past
+  // NC clamped, their results never stored)
+  uint4 wv[RPW][IT], hv[RPW][IT];
+#pragma unroll
+  for (int k = 0; k < RPW; ++k) {
+    const int row = min(row0 + wave * RPW + k, rows - 1);
+    const uint4* np = reinterpret_cast<const uint4*>(nib + (size_t)row * (K >> 1));
+    const uint4* hp = reinterpret_cast<const uint4*>(hdr + (size_t)row * NSB * 16);
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int cc = min(lane + 64 * i, NC - 1);
+      wv[k][i] = np[cc];
+      hv[k][i] = hp[cc >> 3];
+    }
+  }
+  if (xf) {  // the activation given in f32: each wave quantizes blocks wave, wave + 4, ... to Q8_K
+    for (int b = wave; b < NSB; b += KQ_NT / 64) quantize_q8k_wave(xf + 256 * b, xq + 256 * b, xbs + 8 * b, xd + b);
+  } else {
+    for (int c = tid; c < (K >> 4); c += KQ_NT) reinterpret_cast<int4*>(xq)[c] = reinterpret_cast<const int4*>(yq)[c];
+    for (int i = tid; i < NSB; i += KQ_NT) xd[i] = yd[i];
+    for (int i = tid; i < NC; i += KQ_NT) xbs[i] = ybs[i];
+  }
   __syncthreads();
   const uint32_t K1 = 0x3f3f3f3fu, K2 = 0x0f0f0f0fu, K3 = 0x03030303u;
 #pragma unroll
   for (int k = 0; k < RPW; ++k) {
     const int rl = wave * RPW + k;
-    const int row = min(row0 + rl, rows - 1);
-    const uint4* np = reinterpret_cast<const uint4*>(nib + (size_t)row * (K >> 1));
-    const uint4* hp = reinterpret_cast<const uint4*>(hdr + (size_t)row * NSB * 16);
-    for (int c0 = 0; c0 < NC; c0 += 64) {
-      const int c = c0 + lane;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int c = lane + 64 * i;
       const bool valid = c < NC;  // uniform per 8-lane superblock group (NC % 8 == 0)
       const int cc = min(c, NC - 1);
-      const uint4 w = np[cc];
+      const uint4 w = wv[k][i], hd = hv[k][i];
       const int s = cc >> 3, j = cc & 7, c4 = j >> 1, h = j & 1;
-      const uint4 hd = hp[s];
       const uint32_t scw = (c4 < 2) ? (hd.y & K1) : ((hd.w & K2) | (((hd.y >> 6) & K3) << 4));
       const uint32_t mnw = (j < 4) ? (hd.z & K1) : (((hd.w >> 4) & K2) | (((hd.z >> 6) & K3) << 4));
       const int sc_lo = (scw >> (8 * ((2 * c4) & 3))) & 0xff;

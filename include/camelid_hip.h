@@ -198,6 +198,15 @@ int camelid_hip_attention_prefill(const float* qrot, const uint16_t* kc, const f
  * f32 values -> Q8_K blocks: scales yd [n/256], quants yq [n], per-32 quant sums ybs [n/32]. */
 int camelid_hip_quantize_q8_k(const float* x, uint32_t n, float* yd, int8_t* yq, int32_t* ybs,
                               void* stream);
+/* rms_norm + quantize_q8k (CPU tensor/mod.rs:2083-2106 then inference.rs:17564-17599): the
+ * RMSNorm kernel writing the Q8_K activation of a K-quant projection.  n % 256 == 0,
+ * n <= 16384; x, w 16-byte aligned.  (Test hook; allocates its own Q8_0 scratch.) */
+int camelid_hip_rmsnorm_q8_k(const float* x, const float* w, uint32_t n, float eps, float* yd,
+                             int8_t* yq, int32_t* ybs, void* stream);
+/* silu_mul + quantize_q8k (CPU tensor/mod.rs:1943-1967 then inference.rs:17564-17599), gu =
+ * [gate|up], n % 256 == 0.  (Test hook; allocates its own Q8_0 scratch.) */
+int camelid_hip_silu_mul_q8_k(const float* gu, uint32_t n, float* yd, int8_t* yq, int32_t* ybs,
+                              void* stream);
 /* Host split of K-quant wire rows [rows][k/256 superblocks] into the device planes the
  * K-quant GEMV reads: Q4_K (quant 1): a = nibbles [rows][k/2], b = superblock headers
  * [rows][k/256][16] (sc, d unused); Q6_K (quant 2): a = ql [rows][k/2], b = qh [rows][k/4],

@@ -382,6 +382,30 @@ def test_quantize_q8_k_bit_exact(native, orc):
     assert np.array_equal(ybs.download(np.int32, nb * 8), wq.astype(np.int64).reshape(-1, 32).sum(1))
 
 
+@pytest.mark.parametrize("n", [4096, 3072, 256, 16384])
+def test_rmsnorm_and_silu_q8_k_bit_exact(native, orc, n):
+    """The Q8_K activation written by the RMSNorm and SwiGLU kernels == the CPU norm / SwiGLU
+    followed by quantize_q8_k_blocks."""
+    rng = np.random.default_rng(n + 7)
+    x = rng.normal(0, 1, n).astype(np.float32)
+    x[:256] *= 1e-3
+    w = rng.normal(1, 0.1, n).astype(np.float32)
+    yd, yq, ybs = _buf(n // 256 * 4), _buf(n), _buf(n // 32 * 4)
+    dx, dw = _dev(x), _dev(w)  # the buffers must outlive the launch
+    _ok(native.camelid_hip_rmsnorm_q8_k(dx.ptr, dw.ptr, n, 1e-5, yd.ptr, yq.ptr, ybs.ptr, None))
+    wd, wq = orc.quantize_q8_k(orc.rms_norm(x, w, 1e-5))
+    assert np.array_equal(_bits(yd.download(np.float32, n // 256)), _bits(wd))
+    assert np.array_equal(yq.download(np.int8, n), wq)
+    assert np.array_equal(ybs.download(np.int32, n // 32), wq.astype(np.int64).reshape(-1, 32).sum(1))
+    gu = rng.normal(0, 2, 2 * n).astype(np.float32)
+    dgu = _dev(gu)
+    _ok(native.camelid_hip_silu_mul_q8_k(dgu.ptr, n, yd.ptr, yq.ptr, ybs.ptr, None))
+    wd, wq = orc.quantize_q8_k(orc.silu_mul(gu[:n], gu[n:]))
+    assert np.array_equal(_bits(yd.download(np.float32, n // 256)), _bits(wd))
+    assert np.array_equal(yq.download(np.int8, n), wq)
+    assert np.array_equal(ybs.download(np.int32, n // 32), wq.astype(np.int64).reshape(-1, 32).sum(1))
+
+
 def _kquant_wire(orc, rng, quant, rows, k):
     """Random superblocks with finite f16 scales (every other byte uniformly random)."""
     nsb, bb = k // 256, (144 if quant == 1 else 210)
