@@ -307,7 +307,9 @@ def test_rope_kv_bit_exact(native, orc, nh, nkv, hd, split, qk):
 
 @pytest.mark.parametrize("nh,nkv,hd,P", [(24, 8, 128, 1), (24, 8, 128, 2), (24, 8, 128, 9), (24, 8, 128, 511),
                                          (24, 8, 128, 767), (32, 4, 64, 129), (8, 8, 64, 300), (32, 8, 128, 1280),
-                                         (32, 8, 128, 2100), (8, 4, 256, 700), (8, 4, 256, 40)])
+                                         (32, 8, 128, 2100), (8, 4, 256, 700), (8, 4, 256, 40),
+                                         (32, 8, 128, 5000), (32, 8, 128, 8448), (8, 4, 256, 3000),
+                                         (32, 8, 64, 12000)])
 def test_attention_decode_bit_exact(native, orc, nh, nkv, hd, P):
     rng = np.random.default_rng(P + nh)
     L, layer, max_pos = 2, 1, (max(P, 2) + 3 + 7) // 8 * 8  # position stride: multiple of 8
