@@ -6,9 +6,9 @@
 //   per layer: Wqkv (Q8R, rows nq+2*nkv), Wo (Q8R), Wgate|up (Q8R, rows 2F), Wdown (Q8R),
 //              attn/ffn norm [H], optional q/k norm [hd]
 //   lm_head Q8R [V][H], final norm [H], optional token_embd Q8R [V][H]
-//   KV cache: per (layer, kv head) regions of hd * kvs elements, K f16 as [hd/8][kvs][8] and
-//   V f16-rounded f32 as [kvs/4][hd][4] (cm::kv_k_index / cm::kv_v_index), kvs = max_pos
-//   rounded up to a multiple of 8 (16-byte aligned V rows)
+//   KV cache: per (layer, kv head) regions of hd * kvs f16 elements, K as [hd/8][kvs][8] and
+//   V as [kvs/8][hd][8] (cm::kv_k_index / cm::kv_v_index), kvs = max_pos rounded up to a
+//   multiple of 8
 //   activations: h [H] (residual stream), qkv, att [nq], gu [2F], logits [V], one Q8_0
 //                activation buffer (quants + f32 scales) reused by every GEMV
 //   StepState {pos, tok, step}: the decode loop's device-side state
@@ -105,7 +105,7 @@ struct camelid_hip_engine {
   int8_t* kq = nullptr;       // Q8_K quants
   int32_t* kbs = nullptr;     // per-32 quant sums
   uint16_t* kc = nullptr;  // K, granules of 8 dims per position (cm::kv_k_index)
-  float* vc = nullptr;     // V (f16-rounded f32), granules of 4 positions per dim (cm::kv_v_index)
+  uint16_t* vc = nullptr;  // V, granules of 8 positions per dim (cm::kv_v_index)
   uint32_t kvs = 0;        // KV position stride: max_pos rounded up to a multiple of 8
   int att_slots = 0;       // V ring chunks of the attention kernel
   bool read_ahead = true;  // spare workgroups of the norm kernels read ahead the next weights
@@ -488,7 +488,7 @@ int attn_ring_slots(uint32_t kvs);
 template <bool FUSED>
 void launch_attention(uint32_t hd, uint32_t n_heads, int slots, hipStream_t s, const float* qsrc, int nh, int nkv,
                       int rope_dim, int split_half, const float* cb, const float* sb, int rs, const float* qn,
-                      const float* kn, float eps, uint16_t* kc, float* vc, int layer, int kvs, const uint32_t* pos,
+                      const float* kn, float eps, uint16_t* kc, uint16_t* vc, int layer, int kvs, const uint32_t* pos,
                       float scale, float* att, int8_t* xq, float* xs, cm::Prefetch pf) {
   const size_t lds = (size_t)slots * cm::ATT_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs);
   const uint32_t grid = n_heads + (pf.a_lines ? PREFETCH_WGS : 0);
@@ -779,7 +779,7 @@ void launch_gemm(const Q8Mat& m, uint32_t T, const int8_t* xq, const float* xs, 
 }
 
 void launch_attn_prefill(uint32_t hd, uint32_t n_heads, uint32_t n_kv, uint32_t T, const float* q, const uint16_t* kc,
-                         const float* vc, int layer, int kvs, int pos0, float scale, float* att, int8_t* xq, float* xs,
+                         const uint16_t* vc, int layer, int kvs, int pos0, float scale, float* att, int8_t* xq, float* xs,
                          hipStream_t s) {
   const size_t lds = (((size_t)pos0 + T + 3) & ~(size_t)3) * 4;
 #define CM_AP(HD)                                                                                                  \
@@ -933,7 +933,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
     return fail(nullptr, m);
   }
   // A fresh cache reads as zeros (K/V past `filled` are never read); StepState starts at 0.
-  if (hipMemset(e->kc, 0, kv_elems * 2) != hipSuccess || hipMemset(e->vc, 0, kv_elems * 4) != hipSuccess ||
+  if (hipMemset(e->kc, 0, kv_elems * 2) != hipSuccess || hipMemset(e->vc, 0, kv_elems * 2) != hipSuccess ||
       hipMemset(e->st, 0, sizeof(cm::StepState)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
     camelid_hip_engine_free(e);
     return fail(nullptr, "initial device memset failed");
@@ -1096,20 +1096,19 @@ int camelid_hip_seed_layer(camelid_hip_engine* e, uint32_t layer, const float* c
   HIP_TRY(e, hipStreamSynchronize(e->stream));
   const camelid_hip_dims& d = e->d;
   const int hd = (int)d.head_dim, kvs = (int)e->kvs;
-  std::vector<uint16_t> hk((size_t)hd * kvs);
-  std::vector<float> hv((size_t)hd * kvs);
+  std::vector<uint16_t> hk((size_t)hd * kvs), hv((size_t)hd * kvs);
   for (uint32_t h = 0; h < d.n_kv_heads; ++h) {
     const size_t src = (size_t)h * n_pos * hd;
     const size_t base = cm::kv_head_base((int)layer, (int)d.n_kv_heads, (int)h, hd, kvs);
     HIP_TRY(e, hipMemcpy(hk.data(), e->kc + base, hk.size() * 2, hipMemcpyDeviceToHost));
-    HIP_TRY(e, hipMemcpy(hv.data(), e->vc + base, hv.size() * 4, hipMemcpyDeviceToHost));
+    HIP_TRY(e, hipMemcpy(hv.data(), e->vc + base, hv.size() * 2, hipMemcpyDeviceToHost));
     for (int t = 0; t < (int)n_pos; ++t)
       for (int j = 0; j < hd; ++j) {
         hk[cm::kv_k_index(kvs, t, j)] = cm::f32_to_f16_bits(ck[src + (size_t)t * hd + j]);
-        hv[cm::kv_v_index(hd, t, j)] = cm::f16_bits_to_f32(cm::f32_to_f16_bits(cv[src + (size_t)t * hd + j]));
+        hv[cm::kv_v_index(hd, t, j)] = cm::f32_to_f16_bits(cv[src + (size_t)t * hd + j]);
       }
     HIP_TRY(e, hipMemcpy(e->kc + base, hk.data(), hk.size() * 2, hipMemcpyHostToDevice));
-    HIP_TRY(e, hipMemcpy(e->vc + base, hv.data(), hv.size() * 4, hipMemcpyHostToDevice));
+    HIP_TRY(e, hipMemcpy(e->vc + base, hv.data(), hv.size() * 2, hipMemcpyHostToDevice));
   }
   return 0;
 }
@@ -1122,17 +1121,16 @@ int camelid_hip_read_kv_layer(camelid_hip_engine* e, uint32_t layer, uint32_t n,
   HIP_TRY(e, hipStreamSynchronize(e->stream));
   const camelid_hip_dims& d = e->d;
   const int hd = (int)d.head_dim, kvs = (int)e->kvs;
-  std::vector<uint16_t> hk((size_t)hd * kvs);
-  std::vector<float> hv((size_t)hd * kvs);
+  std::vector<uint16_t> hk((size_t)hd * kvs), hv((size_t)hd * kvs);
   for (uint32_t h = 0; h < d.n_kv_heads; ++h) {
     const size_t base = cm::kv_head_base((int)layer, (int)d.n_kv_heads, (int)h, hd, kvs);
     HIP_TRY(e, hipMemcpy(hk.data(), e->kc + base, hk.size() * 2, hipMemcpyDeviceToHost));
-    HIP_TRY(e, hipMemcpy(hv.data(), e->vc + base, hv.size() * 4, hipMemcpyDeviceToHost));
+    HIP_TRY(e, hipMemcpy(hv.data(), e->vc + base, hv.size() * 2, hipMemcpyDeviceToHost));
     const size_t dst = (size_t)h * n * hd;
     for (int t = 0; t < (int)n; ++t)
       for (int j = 0; j < hd; ++j) {
         ck[dst + (size_t)t * hd + j] = cm::f16_bits_to_f32(hk[cm::kv_k_index(kvs, t, j)]);
-        cv[dst + (size_t)t * hd + j] = hv[cm::kv_v_index(hd, t, j)];
+        cv[dst + (size_t)t * hd + j] = cm::f16_bits_to_f32(hv[cm::kv_v_index(hd, t, j)]);
       }
   }
   return 0;
@@ -1482,7 +1480,7 @@ int camelid_hip_silu_mul_q8_k(const float* gu, uint32_t n, float* yd, int8_t* yq
 
 int camelid_hip_rope_kv(const float* qkv, uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t rope_dim,
                         uint32_t split_half, const float* cos_tab, const float* sin_tab, const float* q_norm,
-                        const float* k_norm, float eps, float* qrot, uint16_t* kc, float* vc, uint32_t layer,
+                        const float* k_norm, float eps, float* qrot, uint16_t* kc, uint16_t* vc, uint32_t layer,
                         uint32_t max_pos, const uint32_t* d_pos, void* stream) {
   if (!qkv || !cos_tab || !sin_tab || !qrot || !kc || !vc || !d_pos) return fail(nullptr, "null argument");
   if (!n_heads || !n_kv || n_heads % n_kv || hd == 0 || hd > 512 || rope_dim > hd || rope_dim % 2)
@@ -1493,7 +1491,7 @@ int camelid_hip_rope_kv(const float* qkv, uint32_t n_heads, uint32_t n_kv, uint3
   return launch_status("rope_kv");
 }
 
-int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const float* vc, uint32_t layer,
+int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const uint16_t* vc, uint32_t layer,
                                  uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t max_pos, const uint32_t* d_pos,
                                  float scale, float* att_out, int8_t* xq, float* xs, void* stream) {
   if (!qrot || !kc || !vc || !d_pos || !att_out || !xq || !xs) return fail(nullptr, "null argument");
@@ -1503,7 +1501,7 @@ int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const fl
   if (slots == 0) return fail(nullptr, "max_pos too large for the decode attention");
   launch_attention<false>(hd, n_heads, slots, (hipStream_t)stream, qrot, (int)n_heads, (int)n_kv,
                           (int)hd, 0, nullptr, nullptr, 0, nullptr, nullptr, 0.0f, const_cast<uint16_t*>(kc),
-                          const_cast<float*>(vc), (int)layer, (int)max_pos, d_pos, scale, att_out, xq, xs,
+                          const_cast<uint16_t*>(vc), (int)layer, (int)max_pos, d_pos, scale, att_out, xq, xs,
                           prefetch_of((const Q8Mat*)nullptr));
   return launch_status("attention_decode");
 }
@@ -1522,7 +1520,7 @@ int camelid_hip_q8_0_gemm(const int8_t* wq, const uint16_t* wd, uint32_t rows, u
   return launch_status("q8_0_gemm");
 }
 
-int camelid_hip_attention_prefill(const float* qrot, const uint16_t* kc, const float* vc, uint32_t layer,
+int camelid_hip_attention_prefill(const float* qrot, const uint16_t* kc, const uint16_t* vc, uint32_t layer,
                                   uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t max_pos, uint32_t pos0,
                                   uint32_t tokens, float scale, float* att_out, int8_t* xq, float* xs, void* stream) {
   if (!qrot || !kc || !vc || !xq || !xs) return fail(nullptr, "null argument");

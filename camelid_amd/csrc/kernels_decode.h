@@ -969,13 +969,12 @@ __global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict_
 
 // ---------------------------------------------------------------------------
 // KV cache layout.  Per layer and kv head a region of hd * kvs elements (kvs: the position
-// stride, a multiple of 8) at kv_head_base; inside it
-//   K (f16 bits): [hd/8][kvs][8]  -- 16-byte granule = 8 dims of one position,
-//   V (f32 holding f16-rounded values): [kvs/4][hd][4]  -- 16-byte granule = 4 positions
-//   of one dim,
+// stride, a multiple of 8) at kv_head_base; inside it, f16 bits,
+//   K: [hd/8][kvs][8]  -- 16-byte granule = 8 dims of one position,
+//   V: [kvs/8][hd][8]  -- 16-byte granule = 8 positions of one dim,
 // so that lanes over consecutive positions (scores) or consecutive dims (the output sum)
-// read consecutive granules.  V is kept widened so that the output sum spends two VALU
-// operations (multiply, add) per position, which is what its serial add chain allows.
+// read consecutive granules.  Both products (q * k, p * v) are one mixed-precision FMA on
+// the f16 value, so each position costs the serial add chain two VALU operations.
 __host__ __device__ __forceinline__ size_t kv_head_base(int layer, int n_kv, int kvh, int hd, int kvs) {
   return ((size_t)layer * n_kv + kvh) * (size_t)hd * kvs;
 }
@@ -983,7 +982,7 @@ __host__ __device__ __forceinline__ size_t kv_k_index(int kvs, int p, int d) {
   return ((size_t)(d >> 3) * kvs + p) * 8 + (d & 7);
 }
 __host__ __device__ __forceinline__ size_t kv_v_index(int hd, int p, int d) {
-  return ((size_t)(p >> 2) * hd + d) * 4 + (p & 3);
+  return ((size_t)(p >> 3) * hd + d) * 8 + (p & 7);
 }
 
 // ---------------------------------------------------------------------------
@@ -998,7 +997,7 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, i
                                                 int rope_dim, int split_half, const float* __restrict__ cosv,
                                                 const float* __restrict__ sinv, const float* __restrict__ q_norm,
                                                 const float* __restrict__ k_norm, float eps, float* __restrict__ qrot,
-                                                uint16_t* __restrict__ kc, float* __restrict__ vc, int layer,
+                                                uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int layer,
                                                 int kvs, const uint32_t* __restrict__ d_pos, int pos0,
                                                 int rope_stride) {
   __shared__ __align__(16) float buf[512];
@@ -1044,7 +1043,7 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, i
     const float* vsrc = qkv + (size_t)(n_heads + n_kv) * hd + (size_t)kvh * hd;
     for (int d = threadIdx.x; d < hd; d += blockDim.x) {
       kc[hbase + kv_k_index(kvs, pos, d)] = f32_to_f16_bits(buf[d]);
-      vc[hbase + kv_v_index(hd, pos, d)] = half_bits_to_float(f32_to_f16_bits(vsrc[d]));
+      vc[hbase + kv_v_index(hd, pos, d)] = f32_to_f16_bits(vsrc[d]);
     }
   }
 }
@@ -1126,7 +1125,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
     const float* __restrict__ qsrc, int n_heads, int n_kv, int rope_dim, int split_half,
     const float* __restrict__ cos_base, const float* __restrict__ sin_base, int rope_stride,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm, float eps, uint16_t* __restrict__ kc,
-    float* __restrict__ vc, int layer, int kvs, const uint32_t* __restrict__ d_pos, float scale,
+    uint16_t* __restrict__ vc, int layer, int kvs, const uint32_t* __restrict__ d_pos, float scale,
     float* __restrict__ att_out, int8_t* __restrict__ xq, float* __restrict__ xs, int ring_slots, Prefetch pf) {
   constexpr int ATT_NT = att_nt(HD);
   static_assert(HD % 64 == 0 && HD <= 256, "head_dim must be 64, 128 or 256");
@@ -1135,7 +1134,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   constexpr int CW = HD / 64;                        // output waves: one lane per dim
   constexpr int NH = (NW - CW) >= 8 ? 8 : 4;         // V-staging waves (divides the 32 loads)
   constexpr int LH = ATT_RING_LOADS / NH;            // 1 KB wave loads per staging wave per chunk
-  constexpr int CG = ATT_RING_GRANULES / HD;         // 4-position groups per ring chunk
+  constexpr int CG = ATT_RING_GRANULES / HD;         // 8-position groups per ring chunk
   extern __shared__ __align__(16) float4 dyn[];
   float4* ring = dyn;  // ring_slots chunks of ATT_RING_GRANULES V granules
   float* sc = reinterpret_cast<float*>(dyn + (size_t)ring_slots * ATT_RING_GRANULES);
@@ -1159,7 +1158,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   const int ncache = pos;
   const size_t hbase = kv_head_base(layer, n_kv, kvh, HD, kvs);
   const uint4* kg = reinterpret_cast<const uint4*>(kc + hbase);  // K granule (u, p): u * kvs + p
-  const float4* vg = reinterpret_cast<const float4*>(vc + hbase);  // V granule (g, d): g * HD + d
+  const uint4* vg = reinterpret_cast<const uint4*>(vc + hbase);  // V granule (g, d): g * HD + d
 
   if (FUSED) {
     const float* q = qsrc + (size_t)h * HD;
@@ -1209,14 +1208,14 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
       vn[tid] = half_bits_to_float(vb);
       if ((h % rep) == 0) {
         kc[hbase + kv_k_index(kvs, pos, tid)] = kb;
-        vc[hbase + kv_v_index(HD, pos, tid)] = vn[tid];
+        vc[hbase + kv_v_index(HD, pos, tid)] = vb;
       }
     }
   } else {
     if (tid < HD) {
       qs[tid] = qsrc[(size_t)h * HD + tid];
       kn[tid] = half_bits_to_float(kc[hbase + kv_k_index(kvs, pos, tid)]);
-      vn[tid] = vc[hbase + kv_v_index(HD, pos, tid)];
+      vn[tid] = half_bits_to_float(vc[hbase + kv_v_index(HD, pos, tid)]);
     }
   }
   __syncthreads();
@@ -1266,10 +1265,10 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
       lmax = fmaxf(lmax, sv);
     }
     const float mx = block_max(lmax, red);
-    // V staging: the cache positions' V granules (full 4-position groups) are copied into
+    // V staging: the cache positions' V granules (full 8-position groups) are copied into
     // an LDS ring of ring_slots chunks by NH staging waves with direct global->LDS loads;
     // the output lanes read them from LDS.  A chunk is contiguous in the cache layout.
-    const int ng = ncache >> 2;  // full groups of 4 cache positions
+    const int ng = ncache >> 3;  // full groups of 8 cache positions
     const int nchunks = (ng + CG - 1) / CG;
     const int R = ring_slots;
     const int hw = (tid >> 6) - CW;
@@ -1306,72 +1305,76 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
     __syncthreads();
     const float inv = s_inv;
     for (int p = tid; p < P; p += ATT_NT) sc[p] = sc[p] * inv;
-    // ---- out_d = fold_p prob_p * v_pd: lane d walks the ring chunk by chunk.
+    // ---- out_d = fold_p prob_p * v_pd: lane d walks the ring chunk by chunk (granules of
+    // 8 positions; each product is one mixed-precision FMA on the f16 value).
     float acc = 0.0f;
     for (int c = 0; c < nchunks; ++c) {
       if (stager) wait_vmcnt(LH * (min(c + R - 2, nchunks - 1) - c));  // chunk c has landed
       __syncthreads();  // chunk c visible; the slot of chunk c - 1 is free
       if (stager && c + R - 1 < nchunks) stage(c + R - 1);
       if (tid < HD) {
-        const float4* slot = ring + (size_t)(c % R) * ATT_RING_GRANULES + tid;
-        const float4* pr4 = reinterpret_cast<const float4*>(sc) + (size_t)c * CG;
+        const uint4* slot = reinterpret_cast<const uint4*>(ring + (size_t)(c % R) * ATT_RING_GRANULES) + tid;
+        const float4* pr4 = reinterpret_cast<const float4*>(sc) + (size_t)c * CG * 2;
         const int gn = min(CG, ng - c * CG);
+        // granule g (8 positions) with its probabilities p0 (positions 0-3), p1 (4-7): the 8
+        // products, then the 8 dependent adds (no add waits on its own product)
+        auto granule = [&](const uint4& g, const float4& p0, const float4& p1, float (&pr)[8]) {
+          pr[0] = mul_f16_lo(p0.x, g.x);
+          pr[1] = mul_f16_hi(p0.y, g.x);
+          pr[2] = mul_f16_lo(p0.z, g.y);
+          pr[3] = mul_f16_hi(p0.w, g.y);
+          pr[4] = mul_f16_lo(p1.x, g.z);
+          pr[5] = mul_f16_hi(p1.y, g.z);
+          pr[6] = mul_f16_lo(p1.z, g.w);
+          pr[7] = mul_f16_hi(p1.w, g.w);
+        };
         if (gn == CG) {
-          // LDS reads ping-pong between two batches of 4 granules (16 positions) so that
+          // LDS reads ping-pong between two batches of 2 granules (16 positions) so that
           // the add chain never waits on LDS latency
-          static_assert(CG % 8 == 0, "ring chunks hold a multiple of 8 groups");
-          float4 va[4], pa[4], vb[4], pb[4];
-          auto ld = [&](float4(&v)[4], float4(&pq)[4], int j0) {
+          static_assert(CG % 4 == 0, "ring chunks hold a multiple of 4 granule groups");
+          uint4 va[2], vb[2];
+          float4 pa[4], pb[4];
+          auto ld = [&](uint4(&v)[2], float4(&pq)[4], int j0) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < 2; ++u) {
               v[u] = slot[(j0 + u) * HD];
-              pq[u] = pr4[j0 + u];
+              pq[2 * u] = pr4[2 * (j0 + u)];
+              pq[2 * u + 1] = pr4[2 * (j0 + u) + 1];
             }
           };
-          // the 16 products first (in place), then the 16 dependent adds: no add waits on
-          // its own multiply
-          auto mac = [&](float4(&v)[4], const float4(&pq)[4]) {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              v[u].x = pq[u].x * v[u].x;
-              v[u].y = pq[u].y * v[u].y;
-              v[u].z = pq[u].z * v[u].z;
-              v[u].w = pq[u].w * v[u].w;
-            }
+          auto mac = [&](const uint4(&v)[2], const float4(&pq)[4]) {
+            float pr[2][8];
+            granule(v[0], pq[0], pq[1], pr[0]);
+            granule(v[1], pq[2], pq[3], pr[1]);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              acc += v[u].x;
-              acc += v[u].y;
-              acc += v[u].z;
-              acc += v[u].w;
-            }
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+              for (int e = 0; e < 8; ++e) acc += pr[u][e];
           };
           ld(va, pa, 0);
 #pragma unroll
-          for (int j = 0; j < CG; j += 8) {
-            ld(vb, pb, j + 4);
+          for (int j = 0; j < CG; j += 4) {
+            ld(vb, pb, j + 2);
             __builtin_amdgcn_sched_barrier(0);
             mac(va, pa);
-            if (j + 8 < CG) ld(va, pa, j + 8);
+            if (j + 4 < CG) ld(va, pa, j + 4);
             __builtin_amdgcn_sched_barrier(0);
             mac(vb, pb);
           }
         } else {
           for (int j = 0; j < gn; ++j) {
-            const float4 v = slot[j * HD];
-            const float4 pr = pr4[j];
-            acc += pr.x * v.x;
-            acc += pr.y * v.y;
-            acc += pr.z * v.z;
-            acc += pr.w * v.w;
+            float pr[8];
+            granule(slot[j * HD], pr4[2 * j], pr4[2 * j + 1], pr);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc += pr[e];
           }
         }
       }
     }
     __syncthreads();  // the normalised probabilities past the ring (and with no chunks at all)
     if (tid < HD) {
-      for (int p = ng * 4; p < ncache; ++p) acc += sc[p] * vc[hbase + kv_v_index(HD, p, tid)];
+      for (int p = ng * 8; p < ncache; ++p) acc += sc[p] * half_bits_to_float(vc[hbase + kv_v_index(HD, p, tid)]);
       acc += sc[pos] * vn[tid];
       out[tid] = acc;
     }

@@ -223,7 +223,7 @@ constexpr int AP_NT = 256;
 
 template <int HD>
 __global__ __launch_bounds__(AP_NT) void k_attn_prefill(const float* __restrict__ qrot, int n_heads, int n_kv,
-                                                        const uint16_t* __restrict__ kc, const float* __restrict__ vc,
+                                                        const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
                                                         int layer, int kvs, int pos0, float scale,
                                                         float* __restrict__ att_out, int8_t* __restrict__ xq,
                                                         float* __restrict__ xs) {
@@ -240,13 +240,13 @@ __global__ __launch_bounds__(AP_NT) void k_attn_prefill(const float* __restrict_
   const int kvh = h / (n_heads / n_kv);
   const size_t hbase = kv_head_base(layer, n_kv, kvh, HD, kvs);
   const uint4* kg = reinterpret_cast<const uint4*>(kc + hbase);
-  const float4* vg = reinterpret_cast<const float4*>(vc + hbase);
+  const uint4* vg = reinterpret_cast<const uint4*>(vc + hbase);
   const size_t row = (size_t)t * n_heads * HD + (size_t)h * HD;
   if (tid < HD) qs[tid] = qrot[row + tid];
   __syncthreads();
   float o = 0.0f;
   if (P == 1) {
-    if (tid < HD) o = vc[hbase + kv_v_index(HD, 0, tid)];
+    if (tid < HD) o = half_bits_to_float(vc[hbase + kv_v_index(HD, 0, tid)]);
   } else {
     float lmax = -INFINITY;
     for (int p = tid; p < P; p += AP_NT) {
@@ -281,32 +281,34 @@ __global__ __launch_bounds__(AP_NT) void k_attn_prefill(const float* __restrict_
     for (int p = tid; p < P; p += AP_NT) sc[p] = sc[p] * inv;
     __syncthreads();
     if (tid < HD) {
-      const int ng = P >> 2;
+      const int ng = P >> 3;  // full granules of 8 positions (f16 V, one FMA-mix product each)
       const float4* pr4 = reinterpret_cast<const float4*>(sc);
       float a = 0.0f;
+      auto granule = [&](const uint4& g, int j) {
+        const float4 p0 = pr4[2 * j], p1 = pr4[2 * j + 1];
+        const float r0 = mul_f16_lo(p0.x, g.x), r1 = mul_f16_hi(p0.y, g.x);
+        const float r2 = mul_f16_lo(p0.z, g.y), r3 = mul_f16_hi(p0.w, g.y);
+        const float r4 = mul_f16_lo(p1.x, g.z), r5 = mul_f16_hi(p1.y, g.z);
+        const float r6 = mul_f16_lo(p1.z, g.w), r7 = mul_f16_hi(p1.w, g.w);
+        a += r0;
+        a += r1;
+        a += r2;
+        a += r3;
+        a += r4;
+        a += r5;
+        a += r6;
+        a += r7;
+      };
       int j = 0;
-      for (; j + 8 <= ng; j += 8) {
-        float4 v[8];
+      for (; j + 4 <= ng; j += 4) {
+        uint4 v[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = vg[(size_t)(j + u) * HD + tid];
+        for (int u = 0; u < 4; ++u) v[u] = vg[(size_t)(j + u) * HD + tid];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const float4 pr = pr4[j + u];
-          a += pr.x * v[u].x;
-          a += pr.y * v[u].y;
-          a += pr.z * v[u].z;
-          a += pr.w * v[u].w;
-        }
+        for (int u = 0; u < 4; ++u) granule(v[u], j + u);
       }
-      for (; j < ng; ++j) {
-        const float4 v = vg[(size_t)j * HD + tid];
-        const float4 pr = pr4[j];
-        a += pr.x * v.x;
-        a += pr.y * v.y;
-        a += pr.z * v.z;
-        a += pr.w * v.w;
-      }
-      for (int p = ng * 4; p < P; ++p) a += sc[p] * vc[hbase + kv_v_index(HD, p, tid)];
+      for (; j < ng; ++j) granule(vg[(size_t)j * HD + tid], j);
+      for (int p = ng * 8; p < P; ++p) a += sc[p] * half_bits_to_float(vc[hbase + kv_v_index(HD, p, tid)]);
       o = a;
     }
   }

@@ -50,8 +50,9 @@ enum { CAMELID_Q8_WIRE34 = 34, CAMELID_Q8_BLOCK36 = 36 };
 enum { CAMELID_PROJ_Q = 0, CAMELID_PROJ_K, CAMELID_PROJ_V, CAMELID_PROJ_O,
        CAMELID_PROJ_GATE, CAMELID_PROJ_UP, CAMELID_PROJ_DOWN, CAMELID_N_PROJ };
 
-/* CudaResidentDecode::new (cuda_resident.rs:5601): allocates the f16 KV cache (K [L][n_kv][kvs][hd],
- * V transposed [L][n_kv][hd][kvs], kvs = max_pos rounded up to a multiple of 8) and all
+/* CudaResidentDecode::new (cuda_resident.rs:5601): allocates the f16 KV cache (per layer and
+ * kv head, K in granules of 8 dims of one position, V in granules of 8 positions of one dim,
+ * as camelid_hip_rope_kv documents; position stride kvs = max_pos rounded up to 8) and all
  * scratch on device 0 (or CAMELID_HIP_DEVICE).  head_dim must be 64, 128 or 256. */
 int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** out);
 /* Drop (cuda_resident.rs:5398 Drop + cuda.rs:485 release_async_pool). */
@@ -162,19 +163,18 @@ int camelid_hip_silu_mul_quantize(const float* gu, uint32_t n, int8_t* xq, float
                                   void* stream);
 /* rope_rotate + kv_scatter (cuda_resident.rs:1545, :1569; CPU rope.rs:489-524,
  * kv_cache.rs:573-600), with optional per-head QK RMSNorm (cuda_resident.rs:122).  Cache
- * layout: per (layer, kv head) a region of hd * max_pos elements at element offset
- * (layer * n_kv + kv_head) * hd * max_pos; K holds f16 bits, element (p, d) at
- * ((d / 8) * max_pos + p) * 8 + d % 8; V holds the f16-rounded values as f32, element (p, d)
- * at ((p / 4) * hd + d) * 4 + p % 4 (16-byte granules: 8 dims of one position for K,
- * 4 positions of one dim for V).  max_pos (the position stride) % 8 == 0. */
+ * layout: per (layer, kv head) a region of hd * max_pos f16 elements at element offset
+ * (layer * n_kv + kv_head) * hd * max_pos; K element (p, d) at ((d / 8) * max_pos + p) * 8
+ * + d % 8; V element (p, d) at ((p / 8) * hd + d) * 8 + p % 8 (16-byte granules: 8 dims of
+ * one position for K, 8 positions of one dim for V).  max_pos (the position stride) % 8 == 0. */
 int camelid_hip_rope_kv(const float* qkv, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
                         uint32_t rope_dim, uint32_t split_half, const float* cos_tab,
                         const float* sin_tab, const float* q_norm, const float* k_norm, float eps,
-                        float* qrot, uint16_t* kc, float* vc, uint32_t layer, uint32_t max_pos,
+                        float* qrot, uint16_t* kc, uint16_t* vc, uint32_t layer, uint32_t max_pos,
                         const uint32_t* d_pos, void* stream);
 /* attention_decode (cuda_resident.rs:1587; CPU inference.rs:23945-24025), faithful order.
  * Cache layout as camelid_hip_rope_kv; max_pos (the position stride) % 8 == 0; hd in {64,128,256}. */
-int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const float* vc,
+int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const uint16_t* vc,
                                  uint32_t layer, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
                                  uint32_t max_pos, const uint32_t* d_pos, float scale,
                                  float* att_out, int8_t* xq, float* xs, void* stream);
@@ -190,7 +190,7 @@ int camelid_hip_q8_0_gemm(const int8_t* wq, const uint16_t* wd, uint32_t rows, u
  * over the cache positions [0, pos0 + t] (already stored).  Cache layout as
  * camelid_hip_rope_kv.  Outputs [tokens][n_heads*hd] (att_out may be NULL) and their Q8_0
  * quantization.  pos0 + tokens <= max_pos, <= 16384. */
-int camelid_hip_attention_prefill(const float* qrot, const uint16_t* kc, const float* vc,
+int camelid_hip_attention_prefill(const float* qrot, const uint16_t* kc, const uint16_t* vc,
                                   uint32_t layer, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
                                   uint32_t max_pos, uint32_t pos0, uint32_t tokens, float scale,
                                   float* att_out, int8_t* xq, float* xs, void* stream);

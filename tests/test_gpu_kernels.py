@@ -243,31 +243,31 @@ def test_silu_mul_quantize_bit_exact(native, orc):
 
 
 def _kv_device(k, v):
-    """[L][n_kv][kvs][hd] K (f16 bits) and V (f32) -> the device layout: K granules of 8
-    dims per position ([hd/8][kvs][8]), V granules of 4 positions per dim ([kvs/4][hd][4])."""
+    """[L][n_kv][kvs][hd] K and V (f16 bits) -> the device layout: K granules of 8 dims per
+    position ([hd/8][kvs][8]), V granules of 8 positions per dim ([kvs/8][hd][8])."""
     L, nkv, kvs, hd = k.shape
     kd = k.reshape(L, nkv, kvs, hd // 8, 8).transpose(0, 1, 3, 2, 4)
-    vd = v.reshape(L, nkv, kvs // 4, 4, hd).transpose(0, 1, 2, 4, 3)
+    vd = v.reshape(L, nkv, kvs // 8, 8, hd).transpose(0, 1, 2, 4, 3)
     return np.ascontiguousarray(kd), np.ascontiguousarray(vd)
 
 
 def _kv_host(kd, vd, L, nkv, kvs, hd):
     """Inverse of _kv_device, from the flat device arrays."""
     k = kd.reshape(L, nkv, hd // 8, kvs, 8).transpose(0, 1, 3, 2, 4).reshape(L, nkv, kvs, hd)
-    v = vd.reshape(L, nkv, kvs // 4, hd, 4).transpose(0, 1, 2, 4, 3).reshape(L, nkv, kvs, hd)
+    v = vd.reshape(L, nkv, kvs // 8, hd, 8).transpose(0, 1, 2, 4, 3).reshape(L, nkv, kvs, hd)
     return k, v
 
 
 def test_kv_layout_helpers_roundtrip():
     rng = np.random.default_rng(0)
     k = rng.integers(0, 65535, (2, 3, 16, 64)).astype(np.uint16)
-    v = rng.normal(0, 1, (2, 3, 16, 64)).astype(np.float32)
+    v = rng.integers(0, 65535, (2, 3, 16, 64)).astype(np.uint16)
     kd, vd = _kv_device(k, v)
-    # spot-check the index formulas: K (p, d) at ((d/8)*kvs + p)*8 + d%8, V at ((p/4)*hd + d)*4 + p%4
+    # spot-check the index formulas: K (p, d) at ((d/8)*kvs + p)*8 + d%8, V at ((p/8)*hd + d)*8 + p%8
     kf, vf = kd.reshape(2, 3, -1), vd.reshape(2, 3, -1)
-    for p_, d_ in [(0, 0), (5, 13), (15, 63), (8, 7)]:
+    for p_, d_ in [(0, 0), (5, 13), (15, 63), (8, 7), (9, 1)]:
         assert kf[1, 2, ((d_ // 8) * 16 + p_) * 8 + d_ % 8] == k[1, 2, p_, d_]
-        assert vf[1, 2, ((p_ // 4) * 64 + d_) * 4 + p_ % 4] == v[1, 2, p_, d_]
+        assert vf[1, 2, ((p_ // 8) * 64 + d_) * 8 + p_ % 8] == v[1, 2, p_, d_]
     k2, v2 = _kv_host(kd.ravel(), vd.ravel(), 2, 3, 16, 64)
     assert np.array_equal(k2, k) and np.array_equal(v2, v)
 
@@ -282,7 +282,7 @@ def test_rope_kv_bit_exact(native, orc, nh, nkv, hd, split, qk):
     qn = rng.normal(1, 0.3, hd).astype(np.float32) if qk else None
     kn = rng.normal(1, 0.3, hd).astype(np.float32) if qk else None
     kc = _buf(L * nkv * max_pos * hd * 2)
-    vc = _buf(L * nkv * max_pos * hd * 4)
+    vc = _buf(L * nkv * max_pos * hd * 2)
     qrot = _buf(nh * hd * 4)
     dq, dc, ds, dpos = _dev(qkv), _dev(c[0]), _dev(s[0]), _dev(np.array([pos], np.uint32))
     dqn = _dev(qn) if qk else None
@@ -299,10 +299,10 @@ def test_rope_kv_bit_exact(native, orc, nh, nkv, hd, split, qk):
     want_q = orc.apply_rope(q, nh, hd, hd, c[0], s[0], split)
     want_k = orc.apply_rope(k, nkv, hd, hd, c[0], s[0], split)
     assert np.array_equal(_bits(qrot.download(np.float32, nh * hd)), _bits(want_q))
-    kk, vv = _kv_host(kc.download(np.uint16, L * nkv * max_pos * hd), vc.download(np.float32, L * nkv * max_pos * hd),
+    kk, vv = _kv_host(kc.download(np.uint16, L * nkv * max_pos * hd), vc.download(np.uint16, L * nkv * max_pos * hd),
                       L, nkv, max_pos, hd)
     assert np.array_equal(kk[layer, :, pos], orc.f32_to_f16(want_k).reshape(nkv, hd))
-    assert np.array_equal(_bits(vv[layer, :, pos]), _bits(orc.f16_to_f32(orc.f32_to_f16(v)).reshape(nkv, hd)))
+    assert np.array_equal(vv[layer, :, pos], orc.f32_to_f16(v).reshape(nkv, hd))
 
 
 @pytest.mark.parametrize("nh,nkv,hd,P", [(24, 8, 128, 1), (24, 8, 128, 2), (24, 8, 128, 9), (24, 8, 128, 511),
@@ -318,7 +318,7 @@ def test_attention_decode_bit_exact(native, orc, nh, nkv, hd, P):
     kb, vb = orc.f32_to_f16(kf), orc.f32_to_f16(vf)
     q = rng.normal(0, 1, nh * hd).astype(np.float32)
     scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
-    kd, vd = _kv_device(kb, orc.f16_to_f32(vb))
+    kd, vd = _kv_device(kb, vb)
     dq, dk, dv = _dev(q), _dev(kd), _dev(vd)
     dpos = _dev(np.array([P - 1], np.uint32))
     out, xq, xs = _buf(nh * hd * 4), _buf(nh * hd), _buf(nh * hd // 32 * 4)
@@ -344,7 +344,7 @@ def test_attention_prefill_bit_exact(native, orc, nh, nkv, hd, pos0, T):
     kb, vb = orc.f32_to_f16(kf), orc.f32_to_f16(vf)
     q = rng.normal(0, 1, (T, nh * hd)).astype(np.float32)
     scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
-    kd, vd = _kv_device(kb, orc.f16_to_f32(vb))
+    kd, vd = _kv_device(kb, vb)
     dq, dk, dv = _dev(q), _dev(kd), _dev(vd)
     out, xq, xs = _buf(T * nh * hd * 4), _buf(T * nh * hd), _buf(T * nh * hd // 32 * 4)
     _ok(native.camelid_hip_attention_prefill(dq.ptr, dk.ptr, dv.ptr, layer, nh, nkv, hd, max_pos, pos0, T, scale,
