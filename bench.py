@@ -34,9 +34,11 @@ INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix-core peak, AMD published
 HEADLINE = "llama-3.2-3b"
 ARCH = {"llama-3.2-3b": "Llama-3.2-3B-arch Q8_0", "tinyllama-1.1b": "TinyLlama-1.1B-arch Q8_0",
         "mistral-7b-v0.3": "Mistral-7B-v0.3-arch Q8_0 (8K context)", "qwen3-8b": "Qwen3-8B-arch Q4_K_M"}
-# Measured HBM bytes per launch of the dominant kernel (rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE passes scaled by a copy kernel's reading, profiles/); None until measured.
-TRAFFIC: dict = {}
+# Measured HBM bytes per launch of the dominant kernel: rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE passes over `bench.py --probe-traffic`, FETCH_SIZE scaled by 2.0 (what it reads
+# for a 256 MiB device copy: 128 MiB; WRITE_SIZE reads 256 MiB), averaged over the 113 GEMV
+# launches of one C3 step (profiles/traffic_gemv_llama-3.2-3b_q8_0.md).
+TRAFFIC: dict = {"llama-3.2-3b": 30414176}
 # Q8_0 [N, K] shapes, weights N(0, 0.02) and activations N(0, 1), seed 2
 SWEEP_SHAPES = [(2048, 2048), (5632, 2048), (2048, 5632), (32000, 2048), (128256, 3072)]
 
@@ -119,6 +121,36 @@ def run_sweep(iters_min: int = 200) -> dict:
             "peaks": {"hbm_gbs": HBM_PEAK_GBS, "int8_tops": INT8_PEAK_TOPS}, "shapes": out}
 
 
+def probe_traffic() -> int:
+    """The workload of the traffic counter passes: a 256 MiB device-to-device copy (the
+    counters' scale reference), then three C3 decode steps launched without graphs on a
+    seeded 511-position KV history."""
+    import ctypes as C
+    os.environ["CAMELID_HIP_GRAPHS"] = "0"
+    from camelid_amd.engine import DeviceBuffer
+    from camelid_amd.model import CONFIGS, ResidentSession, SyntheticModel
+    hip = C.CDLL("libamdhip64.so")
+    n = 256 << 20
+    a, b = DeviceBuffer(n), DeviceBuffer(n)
+    for _ in range(3):
+        if hip.hipMemcpy(b.ptr, a.ptr, C.c_size_t(n), 3) != 0:
+            raise RuntimeError("device copy failed")
+    cfg = CONFIGS[HEADLINE]
+    model = SyntheticModel.generate(cfg)
+    P = cfg.prompt_len
+    sess = ResidentSession(model, P + 16, device_loop=True)
+    eng = sess.engine
+    rng = np.random.default_rng(0)
+    for layer in range(cfg.n_layers):
+        k = rng.normal(0, 1, (cfg.n_kv_heads, P - 1, cfg.head_dim)).astype(np.float32)
+        v = rng.normal(0, 1, (cfg.n_kv_heads, P - 1, cfg.head_dim)).astype(np.float32)
+        eng.seed_layer(layer, k, v, P - 1)
+    eng.set_filled(P - 1)
+    log(f"probe: 3 copies of 256 MiB, then decode tokens {list(eng.generate(1, P - 1, 3, cfg.scale()))}")
+    sess.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -130,6 +162,8 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=6)
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--sweep", action="store_true", help="run the isolated Q8_0 GEMV/GEMM sweep (configs[1])")
+    ap.add_argument("--probe-traffic", action="store_true",
+                    help="the workload of the rocprofv3 FETCH_SIZE/WRITE_SIZE passes (no JSON line)")
     ap.add_argument("--seed-kv", action="store_true",
                     help="seed the prompt's KV rows with random f16 values instead of running the prefill "
                          "(kernel profiling of the decode steps alone; skips the parity check)")
@@ -144,6 +178,8 @@ def main() -> int:
     from camelid_amd.engine import device_info
     from camelid_amd.model import CONFIGS, ResidentSession, SyntheticModel, prompt_tokens
 
+    if args.probe_traffic:
+        return probe_traffic()
     if args.sweep:
         dev_name, n_cu = device_info()
         log(f"device {dev_name}, {n_cu} CUs; Q8_0 kernel sweep")
