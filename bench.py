@@ -240,8 +240,11 @@ def main() -> int:
     # parity: the stream must equal the oracle's golden stream when one exists
     stream = [int(t) for t in (list(warm) if W else [])] + [int(t) for t in toks]
     parity = None
-    gold = ROOT / "tests" / "golden" / f"{cfg.name}_p{P}_d{cfg.decode_len}.json"
-    if gold.exists() and not args.seed_kv:
+    # the longest committed stream for this prompt length (a shorter one is a prefix check)
+    golds = sorted((ROOT / "tests" / "golden").glob(f"{cfg.name}_p{P}_d*.json"),
+                   key=lambda f: int(f.stem.rsplit("_d", 1)[1]))
+    gold = golds[-1] if golds else None
+    if gold is not None and not args.seed_kv:
         g = json.loads(gold.read_text())
         n = min(len(stream), len(g["tokens"]))
         parity = {"golden": gold.name, "compared": n, "identical": stream[:n] == g["tokens"][:n]}

@@ -510,13 +510,13 @@ void launch_rmsnorm_quant(const float* x, const float* w, uint32_t n, float eps,
                           int8_t* kq = nullptr, int32_t* kbs = nullptr) {
   if (rows != 1) pf = cm::Prefetch{nullptr, 0, nullptr, 0};
   const uint32_t grid = 1 + (pf.a_lines ? PREFETCH_WGS : 0);
-  switch (cm::seg_chunk((int)n)) {
+  switch (cm::rms_chunk((int)n)) {
 #define CM_RMS(C)                                                                                                   \
   case C:                                                                                                           \
     CM_LAUNCH(cm::k_rmsnorm_quant<C>, dim3(grid, rows), dim3(cm::RMS_NT), 0, s, x, w, (int)n, eps, xq, xs, y, pf, \
               kd, kq, kbs);                                                                                         \
     break;
-    CM_SEG_CHUNKS(CM_RMS)
+    CM_RMS_CHUNKS(CM_RMS)
 #undef CM_RMS
   }
 }
@@ -1613,10 +1613,23 @@ int camelid_hip_argmax(const float* x, uint32_t n, uint32_t* out, void* stream) 
   return launch_status("argmax");
 }
 
-int camelid_hip_inorder_sum_rows(const float* x, uint32_t rows, uint32_t n, uint32_t m_seq, float* out,
-                                 void* stream) {
+int camelid_hip_inorder_sum_rows(const float* x, uint32_t rows, uint32_t n, uint32_t m_seq, uint32_t method,
+                                 float* out, void* stream) {
   if (!x || !out) return fail(nullptr, "null argument");
   if (n == 0 || n > (uint32_t)cm::SEG_MAX_N || rows == 0) return fail(nullptr, "n must be in (0, 16384] and rows > 0");
+  if (method > 1) return fail(nullptr, "method must be 0 (segmented passes) or 1 (one pass)");
+  if (method == 1) {
+    switch (cm::rms_chunk((int)n)) {
+#define CM_SUM(C)                                                                                                  \
+  case C:                                                                                                          \
+    hipLaunchKernelGGL(cm::k_inorder_sum_rows_onepass<C>, dim3(rows), dim3(cm::RMS_NT), 0, (hipStream_t)stream, x, \
+                       (int)n, out);                                                                               \
+    break;
+      CM_RMS_CHUNKS(CM_SUM)
+#undef CM_SUM
+    }
+    return launch_status("inorder_sum_rows");
+  }
   switch (cm::seg_chunk((int)n)) {
 #define CM_SUM(C)                                                                                                \
   case C:                                                                                                        \

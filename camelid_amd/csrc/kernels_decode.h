@@ -325,6 +325,222 @@ __device__ __forceinline__ float inorder_sum_nonneg(const float* v, uint32_t* ps
   return sh_s;
 }
 
+// ---------------------------------------------------------------------------
+// One-pass exact in-order sum of n f32 values held C per thread (thread t: terms t*C ..
+// t*C+C-1, zero past n), bit-identical to the sequential fold s_i = RNE(s_{i-1} + t_i).
+//
+// The binade of every running sum s_i is predicted from an f64 prefix sum R_i of the terms:
+// for non-negative terms each step rounds by at most 2^-24 of the new sum, so
+// |s_i - R_i| <= i * 2^-24 * s_i, and R_i's binade is s_i's unless R_i lies within about
+// (i+1) * 2^-23 (relative) of a binade boundary ("uncertain").  A step whose running sum is
+// predicted to stay in one certain binade adds exactly d_i = RNE(t_i / u) ulps (seg_d:
+// ties, terms of 2^23 ulps or more, negative and non-finite terms are excluded); every other
+// step is "special".  Between two special steps the sum moves by the integer total of the
+// d_i (a segmented scan over the workgroup).  Wave 0 then replays the special steps in order
+// as real f32 adds, applying each run's integer total first -- after checking that the run
+// starts in its predicted binade and ends below the binade's top: the d_i are
+// non-negative, so the run then stayed in that binade and every step rounded as assumed.
+// A failed check, or more than FS_CAP special steps, falls back to the sequential fold of v
+// (the same n terms, in LDS): the result never depends on the prediction being right.
+// Every thread of the workgroup must call; NT * C >= n.
+constexpr int FS_CAP = 256;  // special steps the replay takes before falling back
+
+// Predicted binade (f32 exponent field, at least 1) of a running sum estimated as R after b
+// terms; 0 when the sum may lie in a neighbouring binade (or R is negative or huge).
+__device__ __forceinline__ int fs_binade(double R, int b) {
+  const uint32_t hi = (uint32_t)__double2hiint(R);
+  const int field = (int)(hi >> 20) - 896;  // f64 exponent rebased to f32's
+  const uint32_t m20 = hi & 0xfffffu;       // leading 20 mantissa bits
+  const uint32_t slack = ((uint32_t)(b + 1) >> 3) + 2;  // (b+1) * 2^-23 relative, in 2^-20 units
+  if (field <= 0) return 1;  // below 2^-126: one binade (ulp 2^-149) down to zero
+  if (field >= 254 || m20 >= 0xfffffu - slack || (field >= 2 && m20 < slack)) return 0;
+  return field;
+}
+
+// A special step's replay data: the run of V ulps before it is valid iff the running sum's
+// bits sb satisfy (sb - lo) < lim (unsigned), i.e. sb lies in the run's predicted binade
+// E and sb + V stays below its top; the run then moves the sum to the bits sb + V.
+__device__ __forceinline__ void fs_entry(uint32_t V, int E, uint32_t& lo, uint32_t& lim) {
+  if (V == 0u) {  // nothing to apply, nothing to check
+    lo = 0u;
+    lim = 0xffffffffu;
+    return;
+  }
+  lo = E <= 1 ? 0u : (uint32_t)E << 23;            // lowest bits of the binade (E = 0: invalid)
+  const uint32_t span = ((uint32_t)(E + 1) << 23) - lo;  // bits in the binade
+  lim = (E >= 1 && V < span) ? span - V : 0u;
+}
+
+template <int CTRL, int RMASK>
+__device__ __forceinline__ double dpp_f64(double x) {
+  const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(x), CTRL, RMASK, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(x), CTRL, RMASK, 0xf, false);
+  return __hiloint2double(hi, lo);
+}
+
+// Segmented-scan step: (rs, b) absorbs the earlier element (rp, bp): b restarts after a
+// special step (rs set), else accumulates; cnt is a plain sum.
+#define CM_FS_STEP(ctrl, rmask)                                                                            \
+  {                                                                                                         \
+    const uint32_t rp = CM_DPP(rs, ctrl, rmask), bp = CM_DPP(b, ctrl, rmask), cp = CM_DPP(cnt, ctrl, rmask); \
+    b = rs ? b : sat_add(bp, b);                                                                            \
+    rs |= rp;                                                                                               \
+    cnt += cp;                                                                                              \
+  }
+
+template <int NT, int C>
+__device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const float* v, int n) {
+  constexpr int NW = NT / 64;
+  static_assert(NT % 64 == 0 && NW <= 16 && C <= 32, "one 16-lane row holds the wave totals");
+  __shared__ double sh_r[NW];
+  __shared__ uint32_t sh_rs[NW], sh_b[NW], sh_c[NW];
+  __shared__ float sh_et[FS_CAP];
+  __shared__ uint32_t sh_ev[FS_CAP], sh_lo[FS_CAP], sh_lim[FS_CAP];
+  __shared__ uint32_t sh_end[3];
+  __shared__ float sh_sum;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave: a scalar lane index
+  const int i0 = tid * C;
+  // f64 prefix of the terms before this thread's chunk: wave scan, then the wave totals
+  // scanned in one 16-lane row
+  double r = 0.0;
+#pragma unroll
+  for (int c = 0; c < C; ++c) r += (double)t[c];
+  double incl = r;
+  incl += dpp_f64<0x111, 0xf>(incl);  // row_shr:1
+  incl += dpp_f64<0x112, 0xf>(incl);  // row_shr:2
+  incl += dpp_f64<0x114, 0xf>(incl);  // row_shr:4
+  incl += dpp_f64<0x118, 0xf>(incl);  // row_shr:8
+  incl += dpp_f64<0x142, 0xa>(incl);  // row_bcast:15
+  incl += dpp_f64<0x143, 0xc>(incl);  // row_bcast:31
+  if (lane == 63) sh_r[wave] = incl;
+  double R = dpp_f64<0x138, 0xf>(incl);  // wave_shr:1 -> exclusive
+  __syncthreads();
+  if (NW > 1) {
+    double wt = lane < NW ? sh_r[lane] : 0.0;
+    wt += dpp_f64<0x111, 0xf>(wt);
+    wt += dpp_f64<0x112, 0xf>(wt);
+    wt += dpp_f64<0x114, 0xf>(wt);
+    wt += dpp_f64<0x118, 0xf>(wt);
+    const double wx = dpp_f64<0x111, 0xf>(wt);  // exclusive over the waves
+    R += __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(wx), wave),
+                          __builtin_amdgcn_readlane(__double2loint(wx), wave));
+  }
+  // classify the steps; d = ulps of an in-binade step, 0 for a special one
+  uint32_t d[C];
+  int eb_of[C];
+  uint32_t spm = 0;
+  int eb = fs_binade(R, i0), e_end = 1;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int i = i0 + c;
+    const double Ra = R + (double)t[c];
+    const int ea = fs_binade(Ra, i + 1);
+    uint32_t dc = SEG_FLAG;
+    if (eb != 0 && eb == ea) dc = seg_d(t[c], eb);
+    const bool special = i < n && dc == SEG_FLAG;
+    d[c] = (i < n && !special) ? dc : 0u;
+    spm |= (uint32_t)special << c;
+    eb_of[c] = eb;
+    if (i == n - 1) e_end = ea;
+    eb = ea;
+    R = Ra;
+  }
+  // segmented scan: the run total entering each chunk (a special step resets it), and the
+  // count of special steps before it
+  uint32_t b = 0;
+#pragma unroll
+  for (int c = 0; c < C; ++c) b = ((spm >> c) & 1u) ? 0u : sat_add(b, d[c]);
+  uint32_t rs = spm != 0u, cnt = (uint32_t)__builtin_popcount(spm);
+  CM_FS_STEP(0x111, 0xf)
+  CM_FS_STEP(0x112, 0xf)
+  CM_FS_STEP(0x114, 0xf)
+  CM_FS_STEP(0x118, 0xf)
+  CM_FS_STEP(0x142, 0xa)
+  CM_FS_STEP(0x143, 0xc)
+  if (lane == 63) {
+    sh_rs[wave] = rs;
+    sh_b[wave] = b;
+    sh_c[wave] = cnt;
+  }
+  uint32_t run = CM_DPP(b, 0x138, 0xf), pos = CM_DPP(cnt, 0x138, 0xf);
+  const uint32_t rs_x = CM_DPP(rs, 0x138, 0xf);
+  __syncthreads();
+  uint32_t total;
+  {
+    const uint32_t wr = lane < NW ? sh_rs[lane] : 0u, wbv = lane < NW ? sh_b[lane] : 0u,
+                   wc = lane < NW ? sh_c[lane] : 0u;
+    {  // the wave totals' segmented scan in row 0
+      uint32_t rs = wr, b = wbv, cnt = wc;
+      CM_FS_STEP(0x111, 0xf)
+      CM_FS_STEP(0x112, 0xf)
+      CM_FS_STEP(0x114, 0xf)
+      CM_FS_STEP(0x118, 0xf)
+      total = (uint32_t)__builtin_amdgcn_readlane((int)cnt, NW - 1);
+      const uint32_t bx = CM_DPP(b, 0x111, 0xf), cx = CM_DPP(cnt, 0x111, 0xf);
+      const uint32_t bw = (uint32_t)__builtin_amdgcn_readlane((int)bx, wave);
+      pos += (uint32_t)__builtin_amdgcn_readlane((int)cx, wave);
+      run = rs_x ? run : sat_add(bw, run);
+    }
+  }
+  // the special steps, in order: the term, and the run before it with its check
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    if ((spm >> c) & 1u) {
+      if (pos < (uint32_t)FS_CAP) {
+        uint32_t lo, lim;
+        fs_entry(run, eb_of[c], lo, lim);
+        sh_et[pos] = t[c];
+        sh_ev[pos] = run;
+        sh_lo[pos] = lo;
+        sh_lim[pos] = lim;
+      }
+      ++pos;
+      run = 0u;
+    } else {
+      run = sat_add(run, d[c]);
+    }
+  }
+  if (i0 <= n - 1 && n - 1 < i0 + C) {
+    uint32_t lo, lim;
+    fs_entry(run, e_end, lo, lim);
+    sh_end[0] = run;
+    sh_end[1] = lo;
+    sh_end[2] = lim;
+  }
+  __syncthreads();
+  if (wave == 0) {  // replay, branch-free per step: the sum's chain is one integer and one f32 add
+    const int tot = __builtin_amdgcn_readfirstlane((int)total);
+    float s = 0.0f;
+    uint32_t bad = tot > FS_CAP;
+    for (int base = 0; !bad && base < tot; base += 64) {
+      const int e = min(base + lane, tot - 1);
+      const float et = sh_et[e];
+      const uint32_t ev = sh_ev[e], elo = sh_lo[e], elim = sh_lim[e];
+      const int m = min(64, tot - base);
+      for (int j = 0; j < m; ++j) {
+        const uint32_t V = (uint32_t)__builtin_amdgcn_readlane((int)ev, j);
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)elo, j);
+        const uint32_t lim = (uint32_t)__builtin_amdgcn_readlane((int)elim, j);
+        const float tj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(et), j));
+        const uint32_t sb = __float_as_uint(s);
+        bad |= (uint32_t)!(sb - lo < lim);
+        s = __uint_as_float(sb + V) + tj;
+      }
+    }
+    {
+      const uint32_t sb = __float_as_uint(s);
+      bad |= (uint32_t)!(sb - sh_end[1] < sh_end[2]);
+      s = __uint_as_float(sb + sh_end[0]);
+    }
+    if (bad) s = fold_lds(v, n);
+    if (lane == 0) sh_sum = s;
+  }
+  __syncthreads();
+  return sh_sum;
+}
+#undef CM_FS_STEP
+
 // Compile-time length variant (N % 4 == 0), same order.  The length is hidden from the
 // optimiser (an empty asm statement) so that the fold stays a loop instead of straight-line
 // code that hoists every term into registers (register count sets the workgroups per CU).
@@ -838,13 +1054,19 @@ __device__ __forceinline__ void prefetch_lines(const Prefetch& pf, int wg, int n
 
 // ---------------------------------------------------------------------------
 // RMSNorm (tensor/mod.rs:2083-2106) fused with Q8_0 quantization of the result.
-// Workgroup 0 (RMS_NT threads) computes it; any further workgroups read ahead `pf`.  Thread t owns the 32-element blocks t + RMS_NT b: it
-// loads their x and w values up front (16-byte loads, all in flight together), writes the
-// squares to LDS for the in-order sum (inorder_sum_nonneg: bit-identical to the
-// sequential fold), then normalises and quantizes its blocks from registers, with no
-// cross-lane traffic.  n % 32 == 0, n <= RMS_NT * C.
-constexpr int RMS_NT = 256;
-constexpr int RMS_SEQ_HEAD = 384;  // terms folded sequentially before the segmented sum
+// Workgroup 0 (RMS_NT threads) computes it; any further workgroups read ahead `pf`.  Thread t
+// owns the 32-element blocks t + RMS_NT b: it loads their x and w values up front (16-byte
+// loads, all in flight together), writes the squares to LDS for the in-order sum
+// (inorder_sum_onepass, C consecutive terms per thread: bit-identical to the sequential
+// fold), then normalises and quantizes its blocks from registers, with no cross-lane
+// traffic.  1024 threads: the sum's per-thread work is short and four waves per SIMD hide
+// each other's latencies.  n % 32 == 0, n <= RMS_NT * C.
+constexpr int RMS_NT = 1024;
+#define CM_RMS_CHUNKS(X) X(1) X(2) X(3) X(4) X(5) X(6) X(8) X(12) X(16)
+__host__ __device__ constexpr int rms_chunk(int n) {
+  return n <= 1024 ? 1 : n <= 2048 ? 2 : n <= 3072 ? 3 : n <= 4096 ? 4 : n <= 5120 ? 5 : n <= 6144 ? 6
+       : n <= 8192 ? 8 : n <= 12288 ? 12 : 16;
+}
 
 __device__ __forceinline__ float4 mul4(const float4 a, const float4 b) {
   return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
@@ -858,7 +1080,7 @@ __global__ __launch_bounds__(RMS_NT) void k_rmsnorm_quant(const float* __restric
                                                           int8_t* __restrict__ kq, int32_t* __restrict__ kbs) {
   constexpr int BPT = (C + 31) / 32;  // blocks per thread
   __shared__ __align__(16) float sq[RMS_NT * C];
-  __shared__ __align__(16) uint32_t ps[seg_binades(C) * (RMS_NT * C + 4)];
+  __shared__ __align__(16) float wl[RMS_NT * C];  // w waits here during the sum (registers are short)
   if (blockIdx.x > 0) {  // spare workgroups: read ahead the next projection's weights
     prefetch_lines(pf, blockIdx.x - 1, gridDim.x - 1, sq);
     return;
@@ -890,16 +1112,24 @@ __global__ __launch_bounds__(RMS_NT) void k_rmsnorm_quant(const float* __restric
         wv[b][u] = wp[u];
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) reinterpret_cast<float4*>(sq + blk * 32)[u] = mul4(xv[b][u], xv[b][u]);
+      for (int u = 0; u < 8; ++u) {
+        reinterpret_cast<float4*>(sq + blk * 32)[u] = mul4(xv[b][u], xv[b][u]);
+        reinterpret_cast<float4*>(wl + blk * 32)[u] = wv[b][u];
+      }
     }
   }
   __syncthreads();
-  const float ss = inorder_sum_nonneg<RMS_NT, C>(sq, ps, n, RMS_SEQ_HEAD);
+  float tv[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) tv[c] = tid * C + c < n ? sq[tid * C + c] : 0.0f;
+  const float ss = inorder_sum_onepass<RMS_NT, C>(tv, sq, n);
   const float scale = 1.0f / sqrtf(ss / (float)n + eps);
 #pragma unroll
   for (int b = 0; b < BPT; ++b) {
     const int blk = tid + b * RMS_NT;
     if (blk < nb) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) wv[b][u] = reinterpret_cast<const float4*>(wl + blk * 32)[u];
       float y[32];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
@@ -1426,8 +1656,10 @@ __global__ __launch_bounds__(256) void k_embed_q8(const int8_t* __restrict__ eq,
   h[i] = half_bits_to_float(ed[t * (H >> 5) + (i >> 5)]) * (float)eq[t * H + i];
 }
 
-// In-order sums of rows (test hook for inorder_sum_nonneg): one 256-thread workgroup per
-// row of n values, the first m_seq folded sequentially.  n <= 256 * C.
+// In-order sums of rows (test hooks): one workgroup per row of n values.  k_inorder_sum_rows:
+// the segmented passes (256 threads, n <= 256 * C), the first m_seq terms folded
+// sequentially; k_inorder_sum_rows_onepass: the one-pass method as the RMSNorm runs it
+// (RMS_NT threads, n <= RMS_NT * C).
 template <int C>
 __global__ __launch_bounds__(256) void k_inorder_sum_rows(const float* __restrict__ x, int n, int m_seq,
                                                           float* __restrict__ out) {
@@ -1437,6 +1669,20 @@ __global__ __launch_bounds__(256) void k_inorder_sum_rows(const float* __restric
   for (int i = threadIdx.x; i < n; i += 256) v[i] = row[i];
   __syncthreads();
   const float sum = inorder_sum_nonneg<256, C>(v, ps, n, m_seq);
+  if (threadIdx.x == 0) out[blockIdx.x] = sum;
+}
+
+template <int C>
+__global__ __launch_bounds__(RMS_NT) void k_inorder_sum_rows_onepass(const float* __restrict__ x, int n,
+                                                                     float* __restrict__ out) {
+  __shared__ __align__(16) float v[RMS_NT * C];
+  const float* row = x + (size_t)blockIdx.x * n;
+  for (int i = threadIdx.x; i < n; i += RMS_NT) v[i] = row[i];
+  __syncthreads();
+  float t[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) t[c] = (int)threadIdx.x * C + c < n ? v[threadIdx.x * C + c] : 0.0f;
+  const float sum = inorder_sum_onepass<RMS_NT, C>(t, v, n);
   if (threadIdx.x == 0) out[blockIdx.x] = sum;
 }
 

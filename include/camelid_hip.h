@@ -232,11 +232,13 @@ int camelid_hip_time_q8_0(int batched, const int8_t* const* wq, const uint16_t* 
                           float* ms_out);
 /* argmax_f32 (cuda_resident.rs:1847; CPU inference.rs:5912). */
 int camelid_hip_argmax(const float* x, uint32_t n, uint32_t* out, void* stream);
-/* Sequential-order f32 sums of rows [rows][n] (n <= 16384), evaluated with the
- * workgroup-parallel exact method the RMSNorm uses (test hook; CPU order: the Σx² fold of
- * tensor/mod.rs:2083-2106); m_seq leading terms are folded sequentially. */
-int camelid_hip_inorder_sum_rows(const float* x, uint32_t rows, uint32_t n, uint32_t m_seq, float* out,
-                                 void* stream);
+/* Sequential-order f32 sums of rows [rows][n] (n <= 16384), evaluated by a workgroup-parallel
+ * exact method (test hook; CPU order: the Σx² fold of tensor/mod.rs:2083-2106).  method 0:
+ * segmented passes (the long-context softmax denominator), m_seq leading terms folded
+ * sequentially; method 1: the one-pass binade-prediction method the RMSNorm uses (m_seq
+ * unused). */
+int camelid_hip_inorder_sum_rows(const float* x, uint32_t rows, uint32_t n, uint32_t m_seq, uint32_t method,
+                                 float* out, void* stream);
 /* glibc-identical expf on the device (test hook for the softmax/SiLU exponential). */
 int camelid_hip_expf(const float* x, float* y, size_t n, void* stream);
 /* The same expf restatement evaluated on the host (test hook). */

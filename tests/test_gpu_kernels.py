@@ -193,11 +193,12 @@ def test_inorder_sum_segmented_bit_exact(native, orc, n):
     x = _adversarial_rows(rng, rows, n)
     want = orc.serial_sum_rows(x)
     dx, out = _dev(x), _buf(rows * 4)
-    for m_seq in (384, 128, 0, 1):
-        _ok(native.camelid_hip_inorder_sum_rows(dx.ptr, rows, n, m_seq, out.ptr, None))
+    methods = [(0, m) for m in (384, 128, 0, 1)] + [(1, 0)]
+    for method, m_seq in methods:
+        _ok(native.camelid_hip_inorder_sum_rows(dx.ptr, rows, n, m_seq, method, out.ptr, None))
         got = out.download(np.float32, rows)
         same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
-        assert same.all(), (m_seq, np.nonzero(~same)[0][:5])
+        assert same.all(), (method, m_seq, np.nonzero(~same)[0][:5])
 
 
 @pytest.mark.parametrize("n", [2048, 3072, 4096, 5120, 8192, 16384, 96])
