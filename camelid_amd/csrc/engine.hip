@@ -110,6 +110,7 @@ struct camelid_hip_engine {
   int att_slots = 0;       // V ring chunks of the attention kernel
   bool read_ahead = true;  // spare workgroups of the norm kernels read ahead the next weights
   bool gu_fused = false;   // gate/up rows interleaved by 32, SwiGLU fused into their GEMV
+  bool norm_fused = true;  // RMSNorms computed inside the qkv and gate/up GEMVs (Q8_0 layers)
   float *h = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr;
   float *logits = nullptr, *hidden_cap = nullptr, *xs = nullptr;
   float *cos_cur = nullptr, *sin_cur = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
@@ -432,6 +433,28 @@ void launch_gemv(const Q8Mat& m, const int8_t* xq, const float* xs, float* y, co
   }
 }
 
+// y = W · rmsnorm(x; nw) for a Q8_0 W whose width is a fused-norm width (2048, 3072, 4096):
+// at most 32 rows per workgroup, spread over up to 256 workgroups.
+void launch_gemv_norm(const Q8Mat& m, const float* x, const float* nw, float eps, float* y, hipStream_t s) {
+  const uint32_t per = std::min(32u, std::max(1u, (m.rows + 255u) / 256u));
+  const uint32_t grid = (m.rows + per - 1) / per;
+  switch (m.k) {
+#define CM_GN(K)                                                                                                    \
+  case K:                                                                                                           \
+    if (per > 16)                                                                                                   \
+      CM_LAUNCH((cm::k_gemv_norm<K, 2>), dim3(grid), dim3(cm::GN_NT), 0, s, m.q, m.d, (int)m.rows, (int)per, x, nw, \
+                eps, y);                                                                                            \
+    else                                                                                                            \
+      CM_LAUNCH((cm::k_gemv_norm<K, 1>), dim3(grid), dim3(cm::GN_NT), 0, s, m.q, m.d, (int)m.rows, (int)per, x, nw, \
+                eps, y);                                                                                            \
+    return;
+    CM_GN(2048) CM_GN(3072) CM_GN(4096)
+#undef CM_GN
+    default:  // not reached: callers admit only these widths (cm::gu_fused_k)
+      break;
+  }
+}
+
 // lm_head GEMV with per-workgroup argmax partials; returns the number of partials.
 uint32_t launch_gemv_argmax(const Q8Mat& m, const int8_t* xq, const float* xs, float* logits, float* part_v,
                             uint32_t* part_i, hipStream_t s) {
@@ -669,8 +692,16 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const f
   }
   hipStream_t s = e->stream;
   const double nq = (double)d.n_heads * d.head_dim, nkv = (double)d.n_kv_heads * d.head_dim;
-  rmsnorm(e, L.attn_norm, &L.qkv);
-  gemv(e, L.qkv, e->qkv, nullptr);
+  // the RMSNorms inside the qkv and gate/up GEMVs (norm_q8_lds) for the widths instantiated
+  const bool norm_fused = e->norm_fused && cm::gu_fused_k((int)d.hidden);
+  const bool gu_norm = norm_fused && e->gu_fused && cm::gu_norm_k((int)d.hidden);
+  if (norm_fused) {
+    ProfScope ps(e, P_GEMV, q8_bytes(L.qkv, false) + d.hidden * 8.0);
+    launch_gemv_norm(L.qkv, e->h, L.attn_norm, d.eps, e->qkv, s);
+  } else {
+    rmsnorm(e, L.attn_norm, &L.qkv);
+    gemv(e, L.qkv, e->qkv, nullptr);
+  }
   {
     ProfScope ps(e, P_ATTN, (nq + 2 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0));
     launch_attention<true>(d.head_dim, d.n_heads, e->att_slots, s, e->qkv, (int)d.n_heads,
@@ -680,15 +711,21 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const f
                            prefetch_of(e->read_ahead ? &L.o : nullptr));
   }
   gemv(e, L.o, e->h, e->h);
-  rmsnorm(e, L.ffn_norm, &L.gu);
+  if (!gu_norm) rmsnorm(e, L.ffn_norm, &L.gu);
   if (e->gu_fused) {
-    ProfScope ps(e, P_GEMV, q8_bytes(L.gu, false) - L.gu.rows * 4.0 + d.ffn_dim * 34.0 / 32.0);
+    ProfScope ps(e, P_GEMV, q8_bytes(L.gu, false) - L.gu.rows * 4.0 + d.ffn_dim * 34.0 / 32.0 +
+                                (gu_norm ? d.hidden * 8.0 - d.hidden * 34.0 / 32.0 : 0.0));
     const uint32_t groups = d.ffn_dim / 32;
     switch (d.hidden) {
 #define CM_GU(K)                                                                                                 \
   case K:                                                                                                        \
-    CM_LAUNCH(cm::k_gemv_gu_silu<K>, dim3(groups), dim3(cm::GU_NT), 0, s, L.gu.q, L.gu.d, e->xq, e->xs, e->aq, \
-              e->as);                                                                                            \
+    if (cm::gu_norm_k(K) && gu_norm)                                                                           \
+      CM_LAUNCH((cm::k_gemv_gu_silu<K, cm::GN_NT, cm::gu_norm_k(K)>), dim3(groups), dim3(cm::GN_NT), 0, s,       \
+                L.gu.q, L.gu.d, (const int8_t*)nullptr, (const float*)nullptr, e->h, L.ffn_norm, d.eps, e->aq,  \
+                e->as);                                                                                        \
+    else                                                                                                       \
+      CM_LAUNCH((cm::k_gemv_gu_silu<K, cm::GU_NT, false>), dim3(groups), dim3(cm::GU_NT), 0, s, L.gu.q, L.gu.d,  \
+                e->xq, e->xs, (const float*)nullptr, (const float*)nullptr, 0.0f, e->aq, e->as);               \
     break;
       CM_GU(2048) CM_GU(3072) CM_GU(4096)
 #undef CM_GU
@@ -908,6 +945,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   e->kvs = (d.max_pos + 7u) & ~7u;
   e->gu_fused = cm::gu_fused_k((int)d.hidden);
   if (const char* f = std::getenv("CAMELID_HIP_FUSED_GU")) e->gu_fused = e->gu_fused && std::atoi(f) != 0;
+  if (const char* f = std::getenv("CAMELID_HIP_FUSED_NORM")) e->norm_fused = std::atoi(f) != 0;
   e->att_slots = attn_ring_slots(e->kvs);
   const size_t nq = (size_t)d.n_heads * d.head_dim, nkv = (size_t)d.n_kv_heads * d.head_dim;
   const size_t kv_elems = (size_t)d.n_layers * d.n_kv_heads * e->kvs * d.head_dim;
@@ -1504,6 +1542,42 @@ int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const ui
                           const_cast<uint16_t*>(vc), (int)layer, (int)max_pos, d_pos, scale, att_out, xq, xs,
                           prefetch_of((const Q8Mat*)nullptr));
   return launch_status("attention_decode");
+}
+
+int camelid_hip_rmsnorm_q8_0_gemv(const int8_t* wq, const uint16_t* wd, uint32_t rows, uint32_t k, const float* x,
+                                  const float* nw, float eps, float* y, void* stream) {
+  if (!wq || !wd || !x || !nw || !y) return fail(nullptr, "null argument");
+  if (!cm::gu_fused_k((int)k) || rows == 0) return fail(nullptr, "k must be 2048, 3072 or 4096 and rows > 0");
+  Q8Mat m;
+  m.q = const_cast<int8_t*>(wq);
+  m.d = const_cast<uint16_t*>(wd);
+  m.rows = rows;
+  m.k = k;
+  launch_gemv_norm(m, x, nw, eps, y, (hipStream_t)stream);
+  return launch_status("rmsnorm_q8_0_gemv");
+}
+
+int camelid_hip_gate_up_silu(const int8_t* wq, const uint16_t* wd, uint32_t ffn, uint32_t k, const int8_t* xq,
+                             const float* xs, const float* x, const float* nw, float eps, int8_t* aq, float* as,
+                             void* stream) {
+  if (!wq || !wd || !aq || !as || (x ? !nw : (!xq || !xs))) return fail(nullptr, "null argument");
+  if (!cm::gu_fused_k((int)k) || ffn == 0 || ffn % 32) return fail(nullptr, "k must be 2048, 3072 or 4096; ffn a nonzero multiple of 32");
+  if (x && !cm::gu_norm_k((int)k)) return fail(nullptr, "the in-kernel RMSNorm takes k = 2048 or 3072");
+  const hipStream_t s = (hipStream_t)stream;
+  switch (k) {
+#define CM_GU(K)                                                                                                   \
+  case K:                                                                                                          \
+    if (x && cm::gu_norm_k(K))                                                                                     \
+      hipLaunchKernelGGL((cm::k_gemv_gu_silu<K, cm::GN_NT, cm::gu_norm_k(K)>), dim3(ffn / 32), dim3(cm::GN_NT), 0, \
+                         s, wq, wd, (const int8_t*)nullptr, (const float*)nullptr, x, nw, eps, aq, as);            \
+    else                                                                                                           \
+      hipLaunchKernelGGL((cm::k_gemv_gu_silu<K, cm::GU_NT, false>), dim3(ffn / 32), dim3(cm::GU_NT), 0, s, wq, wd, \
+                         xq, xs, (const float*)nullptr, (const float*)nullptr, 0.0f, aq, as);                      \
+    break;
+    CM_GU(2048) CM_GU(3072) CM_GU(4096)
+#undef CM_GU
+  }
+  return launch_status("gate_up_silu");
 }
 
 int camelid_hip_q8_0_gemm(const int8_t* wq, const uint16_t* wd, uint32_t rows, uint32_t k, const int8_t* xq,

@@ -850,6 +850,122 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv(const int8_t* __restrict__ wq,
   }
 }
 
+// ---------------------------------------------------------------------------
+// RMSNorm fused into the GEMV that consumes it: every workgroup normalises the activation
+// itself (the arithmetic of k_rmsnorm_quant) into LDS while its weight loads are in flight,
+// so the norm needs no launch of its own and its latency overlaps the weight stream.
+constexpr int GN_NT = 1024;
+
+// Copies n16 16-byte pieces from global src to LDS dst by direct global->LDS loads (no
+// registers held: the weight scales of a workgroup's rows wait there while the norm runs).
+// dst holds n16 rounded up to 64 pieces (a wave load writes 64 pieces; surplus lanes re-read
+// the last piece).  Completion: vmcnt(0) in every wave, then a barrier.
+template <int NT>
+__device__ __forceinline__ void stage_lds16(const uint4* src, int n16, uint4* dst) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int base = wave * 64; base < n16; base += NT)
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src + min(base + lane, n16 - 1)),
+                                     (__attribute__((address_space(3))) void*)(dst + base), 16, 0, 0);
+}
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
+
+// RMSNorm of x (n values, global) with weights w (tensor/mod.rs:2083-2106), Q8_0-quantized
+// into LDS: xl (n quants), xsl (n/32 scales); yl: NT*C floats of LDS.  Thread t holds the
+// C consecutive values t*C.. (the layout of inorder_sum_onepass).  The whole workgroup
+// calls; ends with a barrier.
+template <int NT, int C>
+__device__ __forceinline__ void norm_q8_lds(const float* __restrict__ x, const float* __restrict__ w, int n,
+                                            float eps, int8_t* xl, float* xsl, float* yl) {
+  const int tid = threadIdx.x, i0 = tid * C;
+  float xv[C], wv[C], t[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const bool in = i0 + c < n;
+    xv[c] = in ? x[i0 + c] : 0.0f;
+    wv[c] = in ? w[i0 + c] : 0.0f;
+  }
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    t[c] = xv[c] * xv[c];
+    if (i0 + c < n) yl[i0 + c] = t[c];  // the sum's fallback reads the squares here
+  }
+  const float ss = inorder_sum_onepass<NT, C>(t, yl, n);
+  const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+    if (i0 + c < n) yl[i0 + c] = (xv[c] * scale) * wv[c];
+  __syncthreads();
+  for (int b = tid; b < (n >> 5); b += NT) {
+    float y[32];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float4 v = reinterpret_cast<const float4*>(yl + b * 32)[u];
+      y[u * 4] = v.x;
+      y[u * 4 + 1] = v.y;
+      y[u * 4 + 2] = v.z;
+      y[u * 4 + 3] = v.w;
+    }
+    uint32_t packed[8];
+    xsl[b] = quantize_block_regs(y, packed);
+    uint4* qp = reinterpret_cast<uint4*>(xl + b * 32);
+    qp[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    qp[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+  }
+  __syncthreads();
+}
+
+// y = W · rmsnorm(x) for a Q8_0 W [rows][K]: workgroup b takes rows b*rows_per_wg .. (at most
+// 16 * RPW; wave w the local rows w, w + 16, ..), issues its weight loads, computes the norm,
+// then the same per-row block dots and in-order folds as k_gemv_k.
+template <int K, int RPW>
+__global__ __launch_bounds__(GN_NT) void k_gemv_norm(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                                     int rows, int rows_per_wg, const float* __restrict__ x,
+                                                     const float* __restrict__ nw, float eps, float* __restrict__ y) {
+  constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64, STRIDE = gemv_term_stride(NB);
+  constexpr int NWV = GN_NT / 64, R = NWV * RPW, C = (K + GN_NT - 1) / GN_NT;
+  constexpr int S16 = (R * NB / 8 + 63) / 64 * 64;  // LDS pieces for the scales of R rows
+  static_assert(NB % 8 == 0, "a row's scales are whole 16-byte pieces");
+  __shared__ __align__(16) int8_t xl[K];
+  __shared__ __align__(16) float xsl[NB];
+  __shared__ __align__(16) float t[R * STRIDE];
+  __shared__ __align__(16) float yl[GN_NT * C];
+  __shared__ __align__(16) uint4 sdl[S16];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int row0 = blockIdx.x * rows_per_wg;
+  const int nrows = min(rows_per_wg, rows - row0);
+  // the rows' scales (contiguous) to LDS, then the weights to registers
+  stage_lds16<GN_NT>(reinterpret_cast<const uint4*>(wd + (size_t)row0 * NB), nrows * NB / 8, sdl);
+  int4 wv[RPW][IT];
+#pragma unroll
+  for (int k = 0; k < RPW; ++k) {
+    const int row = row0 + min(wave + NWV * k, nrows - 1);  // surplus local rows repeat the last one
+    const int4* w4 = reinterpret_cast<const int4*>(wq + (size_t)row * K);
+#pragma unroll
+    for (int i = 0; i < IT; ++i) wv[k][i] = w4[min(lane + 64 * i, CPR - 1)];
+  }
+  norm_q8_lds<GN_NT, C>(x, nw, K, eps, xl, xsl, yl);
+  wait_vm_all();
+  __syncthreads();
+  const uint16_t* sd = reinterpret_cast<const uint16_t*>(sdl);
+#pragma unroll
+  for (int k = 0; k < RPW; ++k) {
+    const int j = min(wave + NWV * k, nrows - 1);
+    float* tr = t + (wave + NWV * k) * STRIDE;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int c = lane + 64 * i;
+      const int cc = min(c, CPR - 1);
+      int sacc = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
+      sacc += dpp_xor1(sacc);
+      if ((lane & 1) == 0 && c < CPR)
+        tr[c >> 1] = ((float)sacc * half_bits_to_float(sd[j * NB + (c >> 1)])) * xsl[c >> 1];
+    }
+  }
+  __syncthreads();
+  if (tid < nrows) y[row0 + tid] = fold_lds_n<NB>(t + tid * STRIDE);
+}
+
 // Gate/up projection fused with SwiGLU (tensor/mod.rs:1943-1967) and the Q8_0 quantization
 // of the activation.  The matrix rows are interleaved in groups of 32: group g holds gate
 // rows 32g..32g+31 followed by up rows 32g..32g+31, so one workgroup (8 waves, 8 rows each)
@@ -858,21 +974,33 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv(const int8_t* __restrict__ wq,
 constexpr int GU_NT = 512;
 constexpr int GU_ROWS = 64;  // rows per workgroup: 32 gate + 32 up
 __host__ __device__ constexpr bool gu_fused_k(int K) { return K == 2048 || K == 3072 || K == 4096; }
+// widths whose gate/up kernel also takes the RMSNorm (at 4096 the 1024-thread kernel would
+// spill registers)
+__host__ __device__ constexpr bool gu_norm_k(int K) { return K == 2048 || K == 3072; }
 
-template <int K>
-__global__ __launch_bounds__(GU_NT) void k_gemv_gu_silu(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
-                                                       const int8_t* __restrict__ xq, const float* __restrict__ xs,
-                                                       int8_t* __restrict__ aq, float* __restrict__ as) {
+// NORM: the activation is the RMSNorm of x (weights nw), computed by every workgroup in its
+// prologue (norm_q8_lds) instead of read quantized from xq/xs.
+template <int K, int NT, bool NORM>
+__global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                                    const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                                    const float* __restrict__ x, const float* __restrict__ nw,
+                                                    float eps, int8_t* __restrict__ aq, float* __restrict__ as) {
   constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64, STRIDE = gemv_term_stride(NB);
-  constexpr int RPW = GU_ROWS / (GU_NT / 64);  // 8 rows per wave
-  static_assert(NB % 4 == 0, "compile-time GEMV widths are multiples of 128");
+  constexpr int RPW = GU_ROWS / (NT / 64);  // 8 rows per wave at 512 threads, 4 at 1024
+  constexpr int C = (K + NT - 1) / NT;      // norm values per thread
+  static_assert(NB % 4 == 0 && GU_ROWS % (NT / 64) == 0, "compile-time GEMV widths are multiples of 128");
   __shared__ __align__(16) int8_t xl[K];
   __shared__ __align__(16) float xsl[NB];
   __shared__ __align__(16) float t[GU_ROWS * STRIDE];
   __shared__ __align__(16) float vals[GU_ROWS];
+  __shared__ __align__(16) float yl[NORM ? NT * C : 4];
+  // NORM: the rows' scales wait in LDS (registers are short), GU_ROWS * NB / 8 pieces
+  __shared__ __align__(16) uint4 sdl[NORM ? GU_ROWS * NB / 8 : 1];
+  static_assert(!NORM || (GU_ROWS * NB / 8) % 64 == 0, "whole wave loads of scales");
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const size_t row0 = (size_t)blockIdx.x * GU_ROWS;
-  // all of this wave's weight and scale loads first
+  if constexpr (NORM) stage_lds16<NT>(reinterpret_cast<const uint4*>(wd + row0 * NB), GU_ROWS * NB / 8, sdl);
+  // all of this wave's weight (and, without NORM, scale) loads first
   int4 wv[RPW][IT];
   uint16_t dv[RPW][IT];
 #pragma unroll
@@ -884,12 +1012,18 @@ __global__ __launch_bounds__(GU_NT) void k_gemv_gu_silu(const int8_t* __restrict
     for (int i = 0; i < IT; ++i) {
       const int c = min(lane + 64 * i, CPR - 1);
       wv[k][i] = w4[c];
-      dv[k][i] = d[c >> 1];
+      if constexpr (!NORM) dv[k][i] = d[c >> 1];
     }
   }
-  for (int c = tid; c < CPR; c += GU_NT) reinterpret_cast<int4*>(xl)[c] = reinterpret_cast<const int4*>(xq)[c];
-  for (int b = tid; b < NB; b += GU_NT) xsl[b] = xs[b];
-  __syncthreads();
+  if constexpr (NORM) {
+    norm_q8_lds<NT, C>(x, nw, K, eps, xl, xsl, yl);
+    wait_vm_all();
+    __syncthreads();
+  } else {
+    for (int c = tid; c < CPR; c += NT) reinterpret_cast<int4*>(xl)[c] = reinterpret_cast<const int4*>(xq)[c];
+    for (int b = tid; b < NB; b += NT) xsl[b] = xs[b];
+    __syncthreads();
+  }
 #pragma unroll
   for (int k = 0; k < RPW; ++k) {
     float* tr = t + (wave * RPW + k) * STRIDE;
@@ -900,7 +1034,14 @@ __global__ __launch_bounds__(GU_NT) void k_gemv_gu_silu(const int8_t* __restrict
       const int cc = min(c, CPR - 1);
       int sacc = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
       sacc += dpp_xor1(sacc);
-      if ((lane & 1) == 0 && c < CPR) tr[c >> 1] = ((float)sacc * half_bits_to_float(dv[k][i])) * xsl[c >> 1];
+      if ((lane & 1) == 0 && c < CPR) {
+        uint16_t db;
+        if constexpr (NORM)
+          db = reinterpret_cast<const uint16_t*>(sdl)[(wave * RPW + k) * NB + (c >> 1)];
+        else
+          db = dv[k][i];
+        tr[c >> 1] = ((float)sacc * half_bits_to_float(db)) * xsl[c >> 1];
+      }
     }
   }
   __syncthreads();

@@ -152,6 +152,20 @@ int camelid_hip_q8_0_gemv(const int8_t* wq, const uint16_t* wd, uint32_t rows, u
  * bit-exact block-dot contract, CPU inference.rs:20539-20566). */
 int camelid_hip_q8_0_block_dots(const int8_t* wq, uint32_t rows, uint32_t k, const int8_t* xq, int32_t* out,
                                 void* stream);
+/* rms_norm_quantize followed by q8_gemv (cuda_resident.rs:177 + :230; CPU tensor/mod.rs:2083-2106,
+ * inference.rs:16953, 19871-19905), with the norm computed inside the GEMV: y = W.Q8_0(rmsnorm(x; nw)),
+ * bit-identical to camelid_hip_rmsnorm_quantize + camelid_hip_q8_0_gemv (the decode step's qkv
+ * projection).  k (the hidden width) in {2048, 3072, 4096}. */
+int camelid_hip_rmsnorm_q8_0_gemv(const int8_t* wq, const uint16_t* wd, uint32_t rows, uint32_t k, const float* x,
+                                  const float* nw, float eps, float* y, void* stream);
+/* Gate/up projection + SwiGLU + Q8_0 quantization of the activation (CPU tensor/mod.rs:1943-1967,
+ * inference.rs:16953): W holds gate and up rows interleaved in groups of 32 (group g: gate rows
+ * 32g..32g+31, then up rows 32g..32g+31; ffn groups), aq/as = Q8_0(silu(gate.x) * up.x).  The
+ * activation is Q8_0(rmsnorm(x; nw)) computed in-kernel when x is given (k in {2048, 3072}),
+ * else xq/xs.  k in {2048, 3072, 4096}; ffn % 32 == 0. */
+int camelid_hip_gate_up_silu(const int8_t* wq, const uint16_t* wd, uint32_t ffn, uint32_t k, const int8_t* xq,
+                             const float* xs, const float* x, const float* nw, float eps, int8_t* aq, float* as,
+                             void* stream);
 /* rms_norm_quantize (cuda_resident.rs:177; CPU tensor/mod.rs:2083-2106 + inference.rs:16953).
  * n % 32 == 0, n <= 16384; x, w, xq and y (when given) 16-byte aligned. */
 int camelid_hip_rmsnorm_quantize(const float* x, const float* w, uint32_t n, float eps, int8_t* xq,

@@ -243,6 +243,49 @@ def test_silu_mul_quantize_bit_exact(native, orc):
     assert np.array_equal(xq.download(np.int8, n), wq)
 
 
+@pytest.mark.parametrize("rows,k", [(5120, 3072), (2560, 2048), (6144, 4096), (37, 3072), (8200, 2048)])
+def test_rmsnorm_q8_gemv_bit_exact(native, orc, rows, k):
+    """The norm computed inside the GEMV == rmsnorm, Q8_0 quantization, then the GEMV."""
+    rng = np.random.default_rng(rows + k)
+    wire = orc.quantize_q8_0_wire(rng.normal(0, 0.02, rows * k).astype(np.float32))
+    q, d = _repack(native, wire, rows, k)
+    x = (rng.normal(0, 1, k) * rng.uniform(0.1, 30, k)).astype(np.float32)
+    w = rng.normal(1, 0.2, k).astype(np.float32)
+    wq, wd, dx, dw, y = _dev(q), _dev(d), _dev(x), _dev(w), _buf(rows * 4)
+    _ok(native.camelid_hip_rmsnorm_q8_0_gemv(wq.ptr, wd.ptr, rows, k, dx.ptr, dw.ptr, 1e-5, y.ptr, None))
+    xs, xq = orc.quantize_q8_0(orc.rms_norm(x, w, 1e-5))
+    assert np.array_equal(_bits(y.download(np.float32, rows)), _bits(orc.q8_0_gemv(wire, rows, k, xs, xq)))
+
+
+@pytest.mark.parametrize("ffn,k,norm", [(8192, 3072, True), (8192, 3072, False), (5632, 2048, True),
+                                        (96, 4096, False), (64, 2048, False), (96, 3072, True)])
+def test_gate_up_silu_bit_exact(native, orc, ffn, k, norm):
+    """Fused gate/up GEMV + SwiGLU + Q8_0 of the activation (rows interleaved by 32)."""
+    rng = np.random.default_rng(ffn + k + norm)
+    gate = rng.normal(0, 0.02, (ffn, k)).astype(np.float32)
+    up = rng.normal(0, 0.02, (ffn, k)).astype(np.float32)
+    inter = np.concatenate([gate.reshape(ffn // 32, 32, k), up.reshape(ffn // 32, 32, k)], axis=1)
+    wire = orc.quantize_q8_0_wire(inter.reshape(-1))
+    q, d = _repack(native, wire, 2 * ffn, k)
+    x = (rng.normal(0, 1, k) * rng.uniform(0.1, 30, k)).astype(np.float32)
+    w = rng.normal(1, 0.2, k).astype(np.float32)
+    xs, xq = orc.quantize_q8_0(orc.rms_norm(x, w, 1e-5))
+    wq, wd, aq, as_ = _dev(q), _dev(d), _buf(ffn), _buf(ffn // 32 * 4)
+    if norm:
+        dx, dw = _dev(x), _dev(w)
+        _ok(native.camelid_hip_gate_up_silu(wq.ptr, wd.ptr, ffn, k, None, None, dx.ptr, dw.ptr, 1e-5, aq.ptr,
+                                            as_.ptr, None))
+    else:
+        dxq, dxs = _dev(xq), _dev(xs)
+        _ok(native.camelid_hip_gate_up_silu(wq.ptr, wd.ptr, ffn, k, dxq.ptr, dxs.ptr, None, None, 0.0, aq.ptr,
+                                            as_.ptr, None))
+    rows_out = orc.q8_0_gemv(wire, 2 * ffn, k, xs, xq).reshape(ffn // 32, 2, 32)
+    act = orc.silu_mul(rows_out[:, 0].reshape(-1), rows_out[:, 1].reshape(-1))
+    ws, wq8 = orc.quantize_q8_0(act)
+    assert np.array_equal(_bits(as_.download(np.float32, ffn // 32)), _bits(ws))
+    assert np.array_equal(aq.download(np.int8, ffn), wq8)
+
+
 def _kv_device(k, v):
     """[L][n_kv][kvs][hd] K and V (f16 bits) -> the device layout: K granules of 8 dims per
     position ([hd/8][kvs][8]), V granules of 8 positions per dim ([kvs/8][hd][8])."""
