@@ -92,7 +92,8 @@ constexpr uint64_t kExp2Tab[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
 // glibc-identical expf (see the header comment).
-CM_HD float glibc_expf(float x) {
+// tab: kExp2Tab or a copy of it (the decode attention keeps one in LDS)
+CM_HD float glibc_expf_t(float x, const uint64_t* tab) {
   const double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
   const double kShift = 0x1.8p+52;
   const double C0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0);
@@ -111,7 +112,7 @@ CM_HD float glibc_expf(float x) {
   uint64_t ki = d2u(kd);
   kd -= kShift;
   double r = fma(kInvLn2N, xd, -kd);
-  uint64_t t = kExp2Tab[ki & 31u] + (ki << 47);
+  uint64_t t = tab[ki & 31u] + (ki << 47);
   double s = u2d(t);
   double z = fma(C0, r, C1);
   double r2 = r * r;
@@ -120,6 +121,8 @@ CM_HD float glibc_expf(float x) {
   y = y * s;
   return (float)y;
 }
+
+CM_HD float glibc_expf(float x) { return glibc_expf_t(x, kExp2Tab); }
 
 // Q8_0 block quantizer (inference.rs:16953-16971): amax fold, scale = f16(amax/127),
 // quants from the UNROUNDED inverse, round half away from zero, clamp [-128, 127].

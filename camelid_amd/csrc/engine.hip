@@ -546,6 +546,26 @@ void launch_rmsnorm_quant(const float* x, const float* w, uint32_t n, float eps,
 
 // LDS of the attention kernel: the score vector (align4(kvs) floats) plus a V ring of 2..4
 // chunks of 32 KB; 0 when even two chunks do not fit beside the scores.
+// The largest static LDS of the decode attention kernels (the dynamic ring and score vector
+// come on top of it), read from the compiled kernels.
+long attn_static_lds() {
+  static long bytes = -1;
+  if (bytes < 0) {
+    long m = 0;
+    hipFuncAttributes a;
+#define CM_ATT_LDS(HD, F)                                                                          \
+  if (hipFuncGetAttributes(&a, reinterpret_cast<const void*>(&cm::k_attention<HD, F>)) == hipSuccess) \
+    m = std::max<long>(m, (long)a.sharedSizeBytes);                                                 \
+  else                                                                                              \
+    m = std::max<long>(m, 32768);
+    CM_ATT_LDS(64, true) CM_ATT_LDS(64, false) CM_ATT_LDS(128, true) CM_ATT_LDS(128, false)
+    CM_ATT_LDS(256, true) CM_ATT_LDS(256, false)
+#undef CM_ATT_LDS
+    bytes = m;
+  }
+  return bytes;
+}
+
 int attn_ring_slots(uint32_t kvs) {
   static int limit = -1;
   if (limit < 0) {
@@ -554,7 +574,7 @@ int attn_ring_slots(uint32_t kvs) {
       v = 65536;
     limit = v;
   }
-  const long room = (long)limit - (long)cm::att_static_lds_max() - (long)attn_sc_bytes(kvs);
+  const long room = (long)limit - attn_static_lds() - (long)attn_sc_bytes(kvs);
   const long slots = std::min<long>(4, room / (cm::ATT_RING_GRANULES * 16));
   return slots >= 2 ? (int)slots : 0;
 }

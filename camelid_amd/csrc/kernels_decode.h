@@ -99,6 +99,39 @@ __device__ __forceinline__ float fold_lds(const float* p, int n, float acc = 0.0
   return acc;
 }
 
+// The same sequential fold with a small register footprint (two groups of 4 float4 in
+// flight): the fallback of inorder_sum_onepass, which runs inside kernels whose registers
+// are already committed.  p must be 16-byte aligned.
+__device__ __forceinline__ float fold_lds_lean(const float* p, int n) {
+  const float4* q = reinterpret_cast<const float4*>(p);
+  const int g = n >> 2;
+  float acc = 0.0f;
+  int base = 0;
+  if (g >= 4) {
+    float4 a[4], b[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a[u] = q[u];
+    base = 4;
+#pragma unroll 1
+    for (; base + 4 <= g; base += 4) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) b[u] = q[base + u];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        add4(acc, a[u]);
+        a[u] = b[u];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) add4(acc, a[u]);
+  }
+  for (; base < g; ++base) add4(acc, q[base]);
+  for (int i = g << 2; i < n; ++i) acc += p[i];
+  return acc;
+}
+
 // ---------------------------------------------------------------------------
 // Exact in-order sum of n f32 values (non-negative in the intended use), evaluated by a
 // whole workgroup; bit-identical to the sequential fold s_i = RNE(s_{i-1} + t_i).
@@ -176,7 +209,7 @@ __device__ __forceinline__ float inorder_sum_nonneg(const float* v, uint32_t* ps
   for (int c = 0; c < C; ++c) t[c] = i0 + c < n ? v[i0 + c] : 0.0f;
   if (tid == 0) {
     const int m = min(n, m_seq);
-    sh_s = fold_lds(v, m);
+    sh_s = fold_lds_lean(v, m);  // (the chunk's terms are held in registers meanwhile)
     sh_k = m;
   }
   __syncthreads();
@@ -342,8 +375,18 @@ __device__ __forceinline__ float inorder_sum_nonneg(const float* v, uint32_t* ps
 // non-negative, so the run then stayed in that binade and every step rounded as assumed.
 // A failed check, or more than FS_CAP special steps, falls back to the sequential fold of v
 // (the same n terms, in LDS): the result never depends on the prediction being right.
-// Every thread of the workgroup must call; NT * C >= n.
-constexpr int FS_CAP = 256;  // special steps the replay takes before falling back
+// Every thread of the workgroup must call; NT * C >= n; fs: the caller's LDS workspace (one
+// per kernel, shared by every chunk size the kernel instantiates).
+constexpr int FS_CAP = 128;  // special steps the replay takes before falling back
+template <int NT>
+struct FsLds {
+  double r[NT / 64];                   // wave totals of the f64 prefix
+  uint32_t rs[NT / 64], b[NT / 64], c[NT / 64];  // wave totals of the segmented scan
+  float et[FS_CAP];                    // the special steps: term,
+  uint32_t ev[FS_CAP], lo[FS_CAP], lim[FS_CAP];  // run before it and its check
+  uint32_t end[3];                     // the final run and its check
+  float sum;
+};
 
 // Predicted binade (f32 exponent field, at least 1) of a running sum estimated as R after b
 // terms; 0 when the sum may lie in a neighbouring binade (or R is negative or huge).
@@ -389,15 +432,14 @@ __device__ __forceinline__ double dpp_f64(double x) {
   }
 
 template <int NT, int C>
-__device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const float* v, int n) {
+__device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const float* v, int n, FsLds<NT>& fs) {
   constexpr int NW = NT / 64;
   static_assert(NT % 64 == 0 && NW <= 16 && C <= 32, "one 16-lane row holds the wave totals");
-  __shared__ double sh_r[NW];
-  __shared__ uint32_t sh_rs[NW], sh_b[NW], sh_c[NW];
-  __shared__ float sh_et[FS_CAP];
-  __shared__ uint32_t sh_ev[FS_CAP], sh_lo[FS_CAP], sh_lim[FS_CAP];
-  __shared__ uint32_t sh_end[3];
-  __shared__ float sh_sum;
+  double* sh_r = fs.r;
+  uint32_t *sh_rs = fs.rs, *sh_b = fs.b, *sh_c = fs.c;
+  float* sh_et = fs.et;
+  uint32_t *sh_ev = fs.ev, *sh_lo = fs.lo, *sh_lim = fs.lim, *sh_end = fs.end;
+  float& sh_sum = fs.sum;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave: a scalar lane index
   const int i0 = tid * C;
@@ -533,7 +575,7 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
       bad |= (uint32_t)!(sb - sh_end[1] < sh_end[2]);
       s = __uint_as_float(sb + sh_end[0]);
     }
-    if (bad) s = fold_lds(v, n);
+    if (bad) s = fold_lds_lean(v, n);
     if (lane == 0) sh_sum = s;
   }
   __syncthreads();
@@ -855,41 +897,48 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv(const int8_t* __restrict__ wq,
 // itself (the arithmetic of k_rmsnorm_quant) into LDS while its weight loads are in flight,
 // so the norm needs no launch of its own and its latency overlaps the weight stream.
 constexpr int GN_NT = 1024;
-
-// Copies n16 16-byte pieces from global src to LDS dst by direct global->LDS loads (no
-// registers held: the weight scales of a workgroup's rows wait there while the norm runs).
-// dst holds n16 rounded up to 64 pieces (a wave load writes 64 pieces; surplus lanes re-read
-// the last piece).  Completion: vmcnt(0) in every wave, then a barrier.
-template <int NT>
-__device__ __forceinline__ void stage_lds16(const uint4* src, int n16, uint4* dst) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int base = wave * 64; base < n16; base += NT)
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src + min(base + lane, n16 - 1)),
-                                     (__attribute__((address_space(3))) void*)(dst + base), 16, 0, 0);
-}
-__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
+#ifndef CM_GU_PRE
+#define CM_GU_PRE 1
+#endif
+#ifndef CM_GN_PRE
+#define CM_GN_PRE 1
+#endif
+constexpr int GU_PRE = CM_GU_PRE;  // rows per wave loaded before the in-kernel norm (gate/up)
+constexpr int GN_PRE = CM_GN_PRE;  // the same for k_gemv_norm
 
 // RMSNorm of x (n values, global) with weights w (tensor/mod.rs:2083-2106), Q8_0-quantized
 // into LDS: xl (n quants), xsl (n/32 scales); yl: NT*C floats of LDS.  Thread t holds the
-// C consecutive values t*C.. (the layout of inorder_sum_onepass).  The whole workgroup
-// calls; ends with a barrier.
-template <int NT, int C>
-__device__ __forceinline__ void norm_q8_lds(const float* __restrict__ x, const float* __restrict__ w, int n,
-                                            float eps, int8_t* xl, float* xsl, float* yl) {
-  const int tid = threadIdx.x, i0 = tid * C;
-  float xv[C], wv[C], t[C];
+// C consecutive values t*C.. (the layout of inorder_sum_onepass).  norm_load issues the
+// loads and ends with a barrier, so that every wave's norm loads enter the CU's memory
+// pipeline ahead of any weight load (the pipeline serves the workgroup's requests in
+// order; the norm must not wait behind the weights); norm_q8_lds computes.  The whole
+// workgroup calls both; norm_q8_lds ends with a barrier.
+template <int C>
+__device__ __forceinline__ void norm_load(const float* __restrict__ x, const float* __restrict__ w, int n,
+                                          float (&xv)[C], float (&wv)[C]) {
+  const int i0 = threadIdx.x * C;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const bool in = i0 + c < n;
     xv[c] = in ? x[i0 + c] : 0.0f;
     wv[c] = in ? w[i0 + c] : 0.0f;
   }
+  __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the caller's next ones
+  __builtin_amdgcn_s_barrier();       // (issued, not completed: no wait on the loads)
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int NT, int C>
+__device__ __forceinline__ void norm_q8_lds(const float (&xv)[C], const float (&wv)[C], int n, float eps,
+                                            int8_t* xl, float* xsl, float* yl, FsLds<NT>& fs) {
+  const int tid = threadIdx.x, i0 = tid * C;
+  float t[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     t[c] = xv[c] * xv[c];
     if (i0 + c < n) yl[i0 + c] = t[c];  // the sum's fallback reads the squares here
   }
-  const float ss = inorder_sum_onepass<NT, C>(t, yl, n);
+  const float ss = inorder_sum_onepass<NT, C>(t, yl, n, fs);
   const float scale = 1.0f / sqrtf(ss / (float)n + eps);
 #pragma unroll
   for (int c = 0; c < C; ++c)
@@ -923,33 +972,38 @@ __global__ __launch_bounds__(GN_NT) void k_gemv_norm(const int8_t* __restrict__ 
                                                      const float* __restrict__ nw, float eps, float* __restrict__ y) {
   constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64, STRIDE = gemv_term_stride(NB);
   constexpr int NWV = GN_NT / 64, R = NWV * RPW, C = (K + GN_NT - 1) / GN_NT;
-  constexpr int S16 = (R * NB / 8 + 63) / 64 * 64;  // LDS pieces for the scales of R rows
-  static_assert(NB % 8 == 0, "a row's scales are whole 16-byte pieces");
   __shared__ __align__(16) int8_t xl[K];
   __shared__ __align__(16) float xsl[NB];
   __shared__ __align__(16) float t[R * STRIDE];
   __shared__ __align__(16) float yl[GN_NT * C];
-  __shared__ __align__(16) uint4 sdl[S16];
+  __shared__ FsLds<GN_NT> fs;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int row0 = blockIdx.x * rows_per_wg;
   const int nrows = min(rows_per_wg, rows - row0);
-  // the rows' scales (contiguous) to LDS, then the weights to registers
-  stage_lds16<GN_NT>(reinterpret_cast<const uint4*>(wd + (size_t)row0 * NB), nrows * NB / 8, sdl);
+  // the norm's inputs, then the weights and their scales
+  float nxv[C], nwv[C];
+  norm_load<C>(x, nw, K, nxv, nwv);
   int4 wv[RPW][IT];
-#pragma unroll
-  for (int k = 0; k < RPW; ++k) {
+  uint16_t dv[RPW][IT];
+  auto load_row = [&](int k) {
     const int row = row0 + min(wave + NWV * k, nrows - 1);  // surplus local rows repeat the last one
     const int4* w4 = reinterpret_cast<const int4*>(wq + (size_t)row * K);
+    const uint16_t* d = wd + (size_t)row * NB;
 #pragma unroll
-    for (int i = 0; i < IT; ++i) wv[k][i] = w4[min(lane + 64 * i, CPR - 1)];
-  }
-  norm_q8_lds<GN_NT, C>(x, nw, K, eps, xl, xsl, yl);
-  wait_vm_all();
-  __syncthreads();
-  const uint16_t* sd = reinterpret_cast<const uint16_t*>(sdl);
+    for (int i = 0; i < IT; ++i) {
+      const int c = min(lane + 64 * i, CPR - 1);
+      wv[k][i] = w4[c];
+      dv[k][i] = d[c >> 1];
+    }
+  };
+  constexpr int PRE = GN_PRE < RPW ? GN_PRE : RPW;  // rows loaded before the norm, as in k_gemv_gu_silu
+#pragma unroll
+  for (int k = 0; k < PRE; ++k) load_row(k);
+  norm_q8_lds<GN_NT, C>(nxv, nwv, K, eps, xl, xsl, yl, fs);
+#pragma unroll
+  for (int k = PRE; k < RPW; ++k) load_row(k);
 #pragma unroll
   for (int k = 0; k < RPW; ++k) {
-    const int j = min(wave + NWV * k, nrows - 1);
     float* tr = t + (wave + NWV * k) * STRIDE;
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
@@ -958,8 +1012,7 @@ __global__ __launch_bounds__(GN_NT) void k_gemv_norm(const int8_t* __restrict__ 
       const int cc = min(c, CPR - 1);
       int sacc = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
       sacc += dpp_xor1(sacc);
-      if ((lane & 1) == 0 && c < CPR)
-        tr[c >> 1] = ((float)sacc * half_bits_to_float(sd[j * NB + (c >> 1)])) * xsl[c >> 1];
+      if ((lane & 1) == 0 && c < CPR) tr[c >> 1] = ((float)sacc * half_bits_to_float(dv[k][i])) * xsl[c >> 1];
     }
   }
   __syncthreads();
@@ -994,17 +1047,16 @@ __global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ 
   __shared__ __align__(16) float t[GU_ROWS * STRIDE];
   __shared__ __align__(16) float vals[GU_ROWS];
   __shared__ __align__(16) float yl[NORM ? NT * C : 4];
-  // NORM: the rows' scales wait in LDS (registers are short), GU_ROWS * NB / 8 pieces
-  __shared__ __align__(16) uint4 sdl[NORM ? GU_ROWS * NB / 8 : 1];
-  static_assert(!NORM || (GU_ROWS * NB / 8) % 64 == 0, "whole wave loads of scales");
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const size_t row0 = (size_t)blockIdx.x * GU_ROWS;
-  if constexpr (NORM) stage_lds16<NT>(reinterpret_cast<const uint4*>(wd + row0 * NB), GU_ROWS * NB / 8, sdl);
-  // all of this wave's weight (and, without NORM, scale) loads first
+  float nxv[NORM ? C : 1], nwv[NORM ? C : 1];
+  if constexpr (NORM) norm_load<C>(x, nw, K, nxv, nwv);  // ahead of the weights
+  // the wave's weight and scale loads: all up front, or with NORM the first GU_PRE rows
+  // before the norm and the rest after it (a wave stalls when it issues into a full memory
+  // queue, and the norm's barriers would wait for it)
   int4 wv[RPW][IT];
   uint16_t dv[RPW][IT];
-#pragma unroll
-  for (int k = 0; k < RPW; ++k) {
+  auto load_row = [&](int k) {
     const size_t row = row0 + wave * RPW + k;
     const int4* w4 = reinterpret_cast<const int4*>(wq + row * K);
     const uint16_t* d = wd + row * NB;
@@ -1012,13 +1064,17 @@ __global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ 
     for (int i = 0; i < IT; ++i) {
       const int c = min(lane + 64 * i, CPR - 1);
       wv[k][i] = w4[c];
-      if constexpr (!NORM) dv[k][i] = d[c >> 1];
+      dv[k][i] = d[c >> 1];
     }
-  }
+  };
+  constexpr int PRE = NORM ? (GU_PRE < RPW ? GU_PRE : RPW) : RPW;
+#pragma unroll
+  for (int k = 0; k < PRE; ++k) load_row(k);
   if constexpr (NORM) {
-    norm_q8_lds<NT, C>(x, nw, K, eps, xl, xsl, yl);
-    wait_vm_all();
-    __syncthreads();
+    __shared__ FsLds<NT> fs;
+    norm_q8_lds<NT, C>(nxv, nwv, K, eps, xl, xsl, yl, fs);
+#pragma unroll
+    for (int k = PRE; k < RPW; ++k) load_row(k);
   } else {
     for (int c = tid; c < CPR; c += NT) reinterpret_cast<int4*>(xl)[c] = reinterpret_cast<const int4*>(xq)[c];
     for (int b = tid; b < NB; b += NT) xsl[b] = xs[b];
@@ -1034,14 +1090,7 @@ __global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ 
       const int cc = min(c, CPR - 1);
       int sacc = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
       sacc += dpp_xor1(sacc);
-      if ((lane & 1) == 0 && c < CPR) {
-        uint16_t db;
-        if constexpr (NORM)
-          db = reinterpret_cast<const uint16_t*>(sdl)[(wave * RPW + k) * NB + (c >> 1)];
-        else
-          db = dv[k][i];
-        tr[c >> 1] = ((float)sacc * half_bits_to_float(db)) * xsl[c >> 1];
-      }
+      if ((lane & 1) == 0 && c < CPR) tr[c >> 1] = ((float)sacc * half_bits_to_float(dv[k][i])) * xsl[c >> 1];
     }
   }
   __syncthreads();
@@ -1174,6 +1223,10 @@ struct Prefetch {
   size_t b_lines;
 };
 
+__device__ __forceinline__ uint32_t prefetch_line(const Prefetch& pf, size_t l) {
+  return l < pf.a_lines ? pf.a[l * 32] : pf.b[(l - pf.a_lines) * 32];
+}
+
 __device__ __forceinline__ void prefetch_lines(const Prefetch& pf, int wg, int nwg, float* sink_lds) {
   const size_t stride = (size_t)nwg * blockDim.x;
   uint32_t acc = 0;
@@ -1182,14 +1235,11 @@ __device__ __forceinline__ void prefetch_lines(const Prefetch& pf, int wg, int n
   for (; i + 7 * stride < total; i += 8 * stride) {
     uint32_t v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const size_t l = i + u * stride;
-      v[u] = l < pf.a_lines ? pf.a[l * 32] : pf.b[(l - pf.a_lines) * 32];
-    }
+    for (int u = 0; u < 8; ++u) v[u] = prefetch_line(pf, i + u * stride);
 #pragma unroll
     for (int u = 0; u < 8; ++u) acc ^= v[u];
   }
-  for (; i < total; i += stride) acc ^= i < pf.a_lines ? pf.a[i * 32] : pf.b[(i - pf.a_lines) * 32];
+  for (; i < total; i += stride) acc ^= prefetch_line(pf, i);
   if (acc == 0x9e3779b9u && pf.a_lines == 1) sink_lds[0] = 0.0f;  // keeps the loads
 }
 
@@ -1260,10 +1310,11 @@ __global__ __launch_bounds__(RMS_NT) void k_rmsnorm_quant(const float* __restric
     }
   }
   __syncthreads();
+  __shared__ FsLds<RMS_NT> fs;
   float tv[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) tv[c] = tid * C + c < n ? sq[tid * C + c] : 0.0f;
-  const float ss = inorder_sum_onepass<RMS_NT, C>(tv, sq, n);
+  const float ss = inorder_sum_onepass<RMS_NT, C>(tv, sq, n, fs);
   const float scale = 1.0f / sqrtf(ss / (float)n + eps);
 #pragma unroll
   for (int b = 0; b < BPT; ++b) {
@@ -1446,7 +1497,6 @@ __host__ __device__ constexpr int att_nt(int hd) { return hd <= 128 ? 1024 : 512
 // V staging ring: chunks of 32 KB (2048 16-byte granules), 32 wave-loads of 1 KB each.
 constexpr int ATT_RING_GRANULES = 2048;
 constexpr int ATT_RING_LOADS = 32;
-__host__ __device__ constexpr size_t att_static_lds_max() { return 8192; }  // bound on the kernel's static LDS
 
 // Waits until at most n of this wave's vector memory operations are outstanding (gfx9
 // s_waitcnt encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
@@ -1491,6 +1541,27 @@ __device__ __forceinline__ float att_seg_sum(const float* v, uint32_t* ps, int P
   }
 }
 
+// Softmax denominator by the one-pass exact in-order sum for ATT_FOLD_MAX <= P <= NT *
+// ATT_ONEPASS_C positions (C = P / NT rounded up to a power of two); below, a serial fold
+// by one lane is faster (measured: 2.0 us fold vs 2.9 us one-pass at P = 560).
+constexpr int ATT_ONEPASS_C = 8;
+constexpr int ATT_FOLD_MAX = 1024;
+template <int NT>
+__device__ __forceinline__ float att_onepass_sum(const float* v, int P, FsLds<NT>& fs) {
+  const int tid = threadIdx.x;
+#define CM_AOP(C)                                                               \
+  {                                                                             \
+    float t[C];                                                                 \
+    _Pragma("unroll") for (int c = 0; c < C; ++c) t[c] = tid * C + c < P ? v[tid * C + c] : 0.0f; \
+    return inorder_sum_onepass<NT, C>(t, v, P, fs);                             \
+  }
+  if (P <= NT) CM_AOP(1)
+  if (P <= NT * 2) CM_AOP(2)
+  if (P <= NT * 4) CM_AOP(4)
+  CM_AOP(8)
+#undef CM_AOP
+}
+
 template <int HD, bool FUSED>
 __global__ __launch_bounds__(att_nt(HD)) void k_attention(
     const float* __restrict__ qsrc, int n_heads, int n_kv, int rope_dim, int split_half,
@@ -1520,26 +1591,83 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   __shared__ __align__(16) float sq[2 * HD];
   __shared__ float red[ATT_NT / 64];
   __shared__ float s_qscale, s_kscale, s_inv;
+  __shared__ uint64_t etab[32];  // the expf table, read from LDS by the exponentials
+  __shared__ FsLds<ATT_NT> fs;
   const int tid = threadIdx.x;
   const int h = blockIdx.x;
   const int rep = n_heads / n_kv;
   const int kvh = h / rep;
-  const int pos = (int)*d_pos;
-  const int P = pos + 1;
-  const int ncache = pos;
   const size_t hbase = kv_head_base(layer, n_kv, kvh, HD, kvs);
   const uint4* kg = reinterpret_cast<const uint4*>(kc + hbase);  // K granule (u, p): u * kvs + p
   const uint4* vg = reinterpret_cast<const uint4*>(vc + hbase);  // V granule (g, d): g * HD + d
+  const int pos = (int)*d_pos;
+  const int P = pos + 1;
+  const int ncache = pos;
+  // Loads in the order they are needed (a wave's loads complete in order): this token's q, k
+  // and v, the expf table, then the K rows of the first score pass, then (staging waves)
+  // the first V chunks.
+  float qv = 0.0f, kv = 0.0f, vv = 0.0f;
+  uint64_t et = 0;
+  if (tid < HD) {
+    if (FUSED) {
+      qv = qsrc[(size_t)h * HD + tid];
+      kv = qsrc[(size_t)n_heads * HD + (size_t)kvh * HD + tid];
+      vv = qsrc[(size_t)(n_heads + n_kv) * HD + (size_t)kvh * HD + tid];
+    } else {
+      qv = qsrc[(size_t)h * HD + tid];
+      kv = half_bits_to_float(kc[hbase + kv_k_index(kvs, pos, tid)]);
+      vv = half_bits_to_float(vc[hbase + kv_v_index(HD, pos, tid)]);
+    }
+  }
+  if (tid < 32) et = kExp2Tab[tid];
+  // every wave past this point: q, k, v enter the CU's memory pipeline ahead of the K rows
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  // K rows of the first score pass (rows at or past the position are loaded and dropped;
+  // the addresses stay inside the head's region)
+  uint4 krow0[R8];
+  {
+    const int pl = min(tid, kvs - 1);
+#pragma unroll
+    for (int u = 0; u < R8; ++u) krow0[u] = kg[(size_t)u * kvs + pl];
+  }
+  // V staging: the cache positions' V granules (full 8-position groups) are copied into an
+  // LDS ring of ring_slots chunks by NH staging waves with direct global->LDS loads; the
+  // output lanes read them from LDS.  A chunk is contiguous in the cache layout.  Up to the
+  // one-pass limit the first chunks go out now; longer contexts use the ring for the
+  // denominator's prefix arrays first.
+  const int ng = ncache >> 3;  // full groups of 8 cache positions
+  const int nchunks = (ng + CG - 1) / CG;
+  const int R = ring_slots;
+  const int hw = (tid >> 6) - CW;
+  const bool stager = hw >= 0 && hw < NH;
+  const size_t last_granule = (size_t)max(ng, 1) * HD - 1;
+  auto stage = [&](int c) {  // chunk c into slot c % R
+    float4* slot = ring + (size_t)(c % R) * ATT_RING_GRANULES;
+#pragma unroll
+    for (int j = 0; j < LH; ++j) {
+      const int i = hw + NH * j;  // 1 KB piece of the chunk
+      const size_t gsrc = min((size_t)c * ATT_RING_GRANULES + (size_t)i * 64 + (tid & 63), last_granule);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(vg + gsrc),
+                                       (__attribute__((address_space(3))) void*)(slot + i * 64), 16, 0, 0);
+    }
+  };
+  // the denominator: a serial fold below ATT_FOLD_MAX positions, the one-pass exact sum up
+  // to ATT_NT * ATT_ONEPASS_C, the segmented passes beyond (which use the ring first)
+  const bool onepass = P >= ATT_FOLD_MAX && P <= ATT_NT * ATT_ONEPASS_C;
+  const bool early = P > 1 && P <= ATT_NT * ATT_ONEPASS_C;
+  if (stager && early) {
+    for (int c = 0; c < min(R - 1, nchunks); ++c) stage(c);
+  }
+  if (tid < 32) etab[tid] = et;
+  if (tid < HD) {
+    qs[tid] = qv;
+    kn[tid] = kv;
+    vn[tid] = vv;
+  }
 
   if (FUSED) {
-    const float* q = qsrc + (size_t)h * HD;
-    const float* k = qsrc + (size_t)n_heads * HD + (size_t)kvh * HD;
-    const float* v = qsrc + (size_t)(n_heads + n_kv) * HD + (size_t)kvh * HD;
-    if (tid < HD) {
-      qs[tid] = q[tid];
-      kn[tid] = k[tid];
-      vn[tid] = v[tid];
-    }
     if (q_norm) {  // per-head RMSNorm of q and k (two serial folds by two lanes)
       __syncthreads();
       if (tid < HD) {
@@ -1547,8 +1675,9 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
         sq[HD + tid] = kn[tid] * kn[tid];
       }
       __syncthreads();
-      if (tid == 0) s_qscale = 1.0f / sqrtf(fold_lds_n<HD>(sq) / (float)HD + eps);
-      if (tid == 64) s_kscale = 1.0f / sqrtf(fold_lds_n<HD>(sq + HD) / (float)HD + eps);
+      // (lean folds: the first score pass's K rows are in flight in registers)
+      if (tid == 0) s_qscale = 1.0f / sqrtf(fold_lds_lean(sq, HD) / (float)HD + eps);
+      if (tid == 64) s_kscale = 1.0f / sqrtf(fold_lds_lean(sq + HD, HD) / (float)HD + eps);
       __syncthreads();
       if (tid < HD) {
         qs[tid] = (qs[tid] * s_qscale) * q_norm[tid];
@@ -1582,12 +1711,6 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
         vc[hbase + kv_v_index(HD, pos, tid)] = vb;
       }
     }
-  } else {
-    if (tid < HD) {
-      qs[tid] = qsrc[(size_t)h * HD + tid];
-      kn[tid] = half_bits_to_float(kc[hbase + kv_k_index(kvs, pos, tid)]);
-      vn[tid] = half_bits_to_float(vc[hbase + kv_v_index(HD, pos, tid)]);
-    }
   }
   __syncthreads();
 
@@ -1597,10 +1720,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   } else {
     // ---- scores: cache positions 0..pos-1, one lane each
     float lmax = -INFINITY;
-    for (int p = tid; p < ncache; p += ATT_NT) {
-      uint4 row[R8];
-#pragma unroll
-      for (int u = 0; u < R8; ++u) row[u] = kg[(size_t)u * kvs + p];
+    auto score = [&](const uint4(&row)[R8], int p) {
       float acc = 0.0f;
 #pragma unroll
       for (int u = 0; u < R8; ++u) {
@@ -1626,6 +1746,13 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
       const float sv = acc * scale;
       sc[p] = sv;
       lmax = fmaxf(lmax, sv);
+    };
+    if (tid < ncache) score(krow0, tid);
+    for (int p = tid + ATT_NT; p < ncache; p += ATT_NT) {
+      uint4 row[R8];
+#pragma unroll
+      for (int u = 0; u < R8; ++u) row[u] = kg[(size_t)u * kvs + p];
+      score(row, p);
     }
     if (tid == (pos & (ATT_NT - 1))) {  // this token's own key, from LDS
       float acc = 0.0f;
@@ -1636,45 +1763,32 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
       lmax = fmaxf(lmax, sv);
     }
     const float mx = block_max(lmax, red);
-    // V staging: the cache positions' V granules (full 8-position groups) are copied into
-    // an LDS ring of ring_slots chunks by NH staging waves with direct global->LDS loads;
-    // the output lanes read them from LDS.  A chunk is contiguous in the cache layout.
-    const int ng = ncache >> 3;  // full groups of 8 cache positions
-    const int nchunks = (ng + CG - 1) / CG;
-    const int R = ring_slots;
-    const int hw = (tid >> 6) - CW;
-    const bool stager = hw >= 0 && hw < NH;
-    const size_t last_granule = (size_t)max(ng, 1) * HD - 1;
-    auto stage = [&](int c) {  // chunk c into slot c % R
-      float4* slot = ring + (size_t)(c % R) * ATT_RING_GRANULES;
-#pragma unroll
-      for (int j = 0; j < LH; ++j) {
-        const int i = hw + NH * j;  // 1 KB piece of the chunk
-        const size_t gsrc = min((size_t)c * ATT_RING_GRANULES + (size_t)i * 64 + (tid & 63), last_granule);
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(vg + gsrc),
-                                         (__attribute__((address_space(3))) void*)(slot + i * 64), 16, 0, 0);
-      }
-    };
-    for (int p = tid; p < P; p += ATT_NT) sc[p] = glibc_expf(sc[p] - mx);
-    // Long contexts: the denominator by the exact segmented in-order sum (one binade per
-    // pass), its prefix array in the V ring, which is staged only afterwards.  Shorter ones:
-    // a serial fold by one lane, with the first V chunks already in flight.
-    const bool seg = att_seg_chunk<ATT_NT>(P) > 0 && att_seg_bytes<ATT_NT>(P) <= (size_t)R * ATT_RING_GRANULES * 16;
-    if (stager && !seg) {  // after the exponentials, whose table loads would otherwise queue behind
+    for (int p = tid; p < P; p += ATT_NT) sc[p] = glibc_expf_t(sc[p] - mx, etab);
+    // The denominator: the one-pass exact in-order sum; beyond its limit the exact segmented
+    // sum (one binade per pass) with its prefix array in the V ring, staged only afterwards,
+    // or (when even that does not fit) a serial fold by one lane.
+    const bool seg = !early && att_seg_chunk<ATT_NT>(P) > 0 &&
+                     att_seg_bytes<ATT_NT>(P) <= (size_t)R * ATT_RING_GRANULES * 16;
+    if (stager && !early && !seg) {
       for (int c = 0; c < min(R - 1, nchunks); ++c) stage(c);
     }
     __syncthreads();
-    if (seg) {
-      const float ssum = att_seg_sum<ATT_NT>(sc, reinterpret_cast<uint32_t*>(ring), P);
-      if (tid == 0) s_inv = 1.0f / ssum;
-      if (stager) {
-        for (int c = 0; c < min(R - 1, nchunks); ++c) stage(c);
+    float inv;
+    if (onepass) {
+      inv = 1.0f / att_onepass_sum<ATT_NT>(sc, P, fs);
+    } else {
+      if (seg) {
+        const float ssum = att_seg_sum<ATT_NT>(sc, reinterpret_cast<uint32_t*>(ring), P);
+        if (tid == 0) s_inv = 1.0f / ssum;
+        if (stager) {
+          for (int c = 0; c < min(R - 1, nchunks); ++c) stage(c);
+        }
+      } else if (tid == 0) {
+        s_inv = 1.0f / fold_lds(sc, P);
       }
-    } else if (tid == 0) {
-      s_inv = 1.0f / fold_lds(sc, P);
+      __syncthreads();
+      inv = s_inv;
     }
-    __syncthreads();
-    const float inv = s_inv;
     for (int p = tid; p < P; p += ATT_NT) sc[p] = sc[p] * inv;
     // ---- out_d = fold_p prob_p * v_pd: lane d walks the ring chunk by chunk (granules of
     // 8 positions; each product is one mixed-precision FMA on the f16 value).
@@ -1820,10 +1934,11 @@ __global__ __launch_bounds__(RMS_NT) void k_inorder_sum_rows_onepass(const float
   const float* row = x + (size_t)blockIdx.x * n;
   for (int i = threadIdx.x; i < n; i += RMS_NT) v[i] = row[i];
   __syncthreads();
+  __shared__ FsLds<RMS_NT> fs;
   float t[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) t[c] = (int)threadIdx.x * C + c < n ? v[threadIdx.x * C + c] : 0.0f;
-  const float sum = inorder_sum_onepass<RMS_NT, C>(t, v, n);
+  const float sum = inorder_sum_onepass<RMS_NT, C>(t, v, n, fs);
   if (threadIdx.x == 0) out[blockIdx.x] = sum;
 }
 
