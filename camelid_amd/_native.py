@@ -92,6 +92,7 @@ SIGNATURES: dict[str, tuple] = {
     "camelid_hip_argmax": (C.c_int, [vp, C.c_uint32, vp, vp]),
     "camelid_hip_rmsnorm_q8_0_gemv": (C.c_int, [vp, vp, C.c_uint32, C.c_uint32, vp, vp, C.c_float, vp, vp]),
     "camelid_hip_gate_up_silu": (C.c_int, [vp, vp, C.c_uint32, C.c_uint32, vp, vp, vp, vp, C.c_float, vp, vp, vp]),
+    "camelid_hip_verify": (C.c_int, [vp, vp, vp, vp, C.c_uint32, C.c_uint32, C.c_float, vp]),
     "camelid_hip_inorder_sum_rows": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp]),
     "camelid_hip_expf": (C.c_int, [vp, vp, C.c_size_t, vp]),
     "camelid_expf_host": (None, [f32p, f32p, C.c_size_t]),

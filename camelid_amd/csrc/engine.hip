@@ -131,6 +131,10 @@ struct camelid_hip_engine {
   bool prefill_batched = true;
   float *pf_h = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_gu = nullptr, *pf_xs = nullptr;
   int8_t* pf_xq = nullptr;
+  // verify scratch (allocated on first use): inputs of up to CAMELID_MAX_VERIFY_K tokens,
+  // their logits and greedy tokens
+  float *v_embs = nullptr, *v_cos = nullptr, *v_sin = nullptr, *v_logits = nullptr;
+  uint32_t* v_tok = nullptr;
   uint32_t filled = 0;
   uint32_t cur_pos = 0;  // host copy of the position being computed (profiling byte counts)
   bool capture = false;
@@ -1304,6 +1308,65 @@ int camelid_hip_prefill(camelid_hip_engine* e, const float* embs, const float* c
     return rc;
   }
   e->filled += n;
+  return 0;
+}
+
+int camelid_hip_verify(camelid_hip_engine* e, const float* embs, const float* cos_all, const float* sin_all,
+                       uint32_t base_position, uint32_t k, float scale, uint32_t* tokens_out) {
+  if (!e) return fail(nullptr, "null engine");
+  if (!ready(e)) return fail(e, "weights not ready");
+  if (!embs || !cos_all || !sin_all || !tokens_out) return fail(e, "null argument");
+  const camelid_hip_dims& d = e->d;
+  if (k == 0 || k > CAMELID_MAX_VERIFY_K) return fail(e, "verify: k out of 1..=8");
+  if ((size_t)base_position + k > d.max_pos) return fail(e, "verify beyond max_pos");
+  if (base_position > e->filled) return fail(e, "verify: base_position past the filled cache");
+  if (!std::isfinite(scale)) return fail(e, "attention score scale must be finite");
+  HIP_TRY(e, hipSetDevice(e->device));
+  const size_t half = d.rope_dim / 2, K = CAMELID_MAX_VERIFY_K;
+  if (!e->v_embs && (dev_alloc(e, &e->v_embs, K * d.hidden) || dev_alloc(e, &e->v_cos, K * half) ||
+                     dev_alloc(e, &e->v_sin, K * half) || dev_alloc(e, &e->v_logits, K * (size_t)d.vocab) ||
+                     dev_alloc(e, &e->v_tok, K)))
+    return 1;
+  HIP_TRY(e, hipMemcpy(e->v_embs, embs, (size_t)k * d.hidden * 4, hipMemcpyHostToDevice));
+  HIP_TRY(e, hipMemcpy(e->v_cos, cos_all, (size_t)k * half * 4, hipMemcpyHostToDevice));
+  HIP_TRY(e, hipMemcpy(e->v_sin, sin_all, (size_t)k * half * 4, hipMemcpyHostToDevice));
+  bool generic = false;
+  for (const LayerW& L : e->layers) generic = generic || L.generic;
+  const bool batched = e->prefill_batched && !generic && e->out_quant == CAMELID_Q8_0 && e->out.rows % 4 == 0;
+  if (batched) {
+    // one batched forward (the prefill chunk path: bit-identical to token steps), then the
+    // final norm, lm_head GEMM and one argmax per token
+    if (ensure_prefill_buffers(e)) return 1;
+    HIP_TRY(e, hipMemcpyAsync(e->pf_h, e->v_embs, (size_t)k * d.hidden * 4, hipMemcpyDeviceToDevice, e->stream));
+    prefill_chunk(e, e->v_cos, e->v_sin, k, base_position, scale);
+    launch_rmsnorm_quant(e->pf_h, e->out_norm, d.hidden, d.eps, e->pf_xq, e->pf_xs, nullptr, e->stream,
+                         cm::Prefetch{}, k);
+    launch_gemm(e->out, k, e->pf_xq, e->pf_xs, e->v_logits, nullptr, e->stream);
+    for (uint32_t t = 0; t < k; ++t)
+      CM_LAUNCH(cm::k_argmax, dim3(1), dim3(1024), 0, e->stream, e->v_logits + (size_t)t * d.vocab, (int)d.vocab,
+                e->v_tok + t);
+  } else {
+    // k single-token steps; the head writes each greedy token to v_tok[step]
+    *e->p_st = cm::StepState{base_position, 0u, 0u, 0u};
+    HIP_TRY(e, hipMemcpyAsync(e->st, e->p_st, sizeof(cm::StepState), hipMemcpyHostToDevice, e->stream));
+    for (uint32_t t = 0; t < k; ++t) {
+      HIP_TRY(e, hipMemcpyAsync(e->h, e->v_embs + (size_t)t * d.hidden, d.hidden * 4, hipMemcpyDeviceToDevice,
+                                e->stream));
+      e->cur_pos = base_position + t;
+      run_stack(e, e->v_cos + (size_t)t * half, e->v_sin + (size_t)t * half, 0, scale);
+      run_head(e, e->v_tok, k);
+    }
+  }
+  if (check_launch(e)) {
+    e->filled = 0;
+    return 1;
+  }
+  hipError_t st = hipStreamSynchronize(e->stream);
+  if (st != hipSuccess) {
+    e->filled = 0;
+    return fail(e, std::string("verify: ") + hipGetErrorString(st));
+  }
+  HIP_TRY(e, hipMemcpy(tokens_out, e->v_tok, (size_t)k * 4, hipMemcpyDeviceToHost));
   return 0;
 }
 

@@ -163,6 +163,18 @@ class HipResidentDecode:
 
     prefill_batched = prefill
 
+    MAX_VERIFY_K = 8
+
+    def verify_batch(self, embeddings, cos_all, sin_all, base_position: int, scale: float) -> np.ndarray:
+        """k tokens at [base_position, base_position + k) in one batched forward; the greedy
+        token after each (cuda_resident.rs:7821).  filled is left to the caller."""
+        e, c, s = _f32(embeddings), _f32(cos_all), _f32(sin_all)
+        k = e.shape[0]
+        out = np.empty(k, np.uint32)
+        self._chk(self._lib.camelid_hip_verify(self._h, N.ptr(e, C.c_float), N.ptr(c, C.c_float), N.ptr(s, C.c_float),
+                                               base_position, k, scale, N.ptr(out, C.c_uint32)))
+        return out
+
     def generate(self, token: int, position: int, n_steps: int, scale: float) -> np.ndarray:
         """Device-side greedy loop (forward_token_device, cuda_resident.rs:7529)."""
         out = np.empty(n_steps, np.uint32)

@@ -100,6 +100,15 @@ int camelid_hip_forward_token(camelid_hip_engine* e, const float* emb, const flo
  * [filled, filled + n) from embs [n][H], cos_all/sin_all [n][rope_dim/2]. */
 int camelid_hip_prefill(camelid_hip_engine* e, const float* embs, const float* cos_all,
                         const float* sin_all, uint32_t n, float scale);
+/* verify_batch (cuda_resident.rs:7821; MAX_VERIFY_K :5524; seam inference.rs:2752-2876):
+ * the k tokens of embs [k][H] at positions [base_position, base_position + k) in one batched
+ * forward (their K/V are written), tokens_out[k] = the greedy token after each, bit-identical
+ * to k single-token steps.  1 <= k <= CAMELID_MAX_VERIFY_K; base_position <= filled.
+ * filled is not changed: the caller sets it to base_position + the accepted length
+ * (inference.rs:2873). */
+#define CAMELID_MAX_VERIFY_K 8
+int camelid_hip_verify(camelid_hip_engine* e, const float* embs, const float* cos_all, const float* sin_all,
+                       uint32_t base_position, uint32_t k, float scale, uint32_t* tokens_out);
 
 /* Device-side token loop (forward_token_device, cuda_resident.rs:7529; embed_gather_q8_0
  * :2995; rope_select :3012).  set_embedding uploads token_embd (Q8_0); set_rope_table

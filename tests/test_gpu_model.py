@@ -135,6 +135,65 @@ def test_batched_prefill_matches_token_steps(monkeypatch, kw):
     assert toks["token"] == toks["batched"]
 
 
+@pytest.mark.parametrize("kw,prefill", [(dict(), "batched"), (dict(), "token"),
+                                        (dict(hidden=384, n_heads=3, n_kv_heads=1, head_dim=128, ffn_dim=1024), "batched")])
+def test_verify_batch_matches_token_steps(monkeypatch, kw, prefill):
+    """verify_batch (cuda_resident.rs:7821): k tokens in one batched forward give, bit for bit,
+    the greedy tokens of k single-token steps over the same inputs (the reference's
+    decode == verify contract, cuda_resident/tests.rs:1136), whatever the drafts are; the
+    seam's accept rule (inference.rs:2864-2873) then continues the engine's own greedy stream,
+    and the oracle's."""
+    from oracle.oracle import OracleModel
+    monkeypatch.setenv("CAMELID_HIP_PREFILL", prefill)
+    cfg = tiny_config(prompt_len=40, **kw)
+    model = SyntheticModel.generate(cfg)
+    prompt = prompt_tokens(cfg)
+    base = len(prompt) - 1
+    # the true greedy continuation (single-token steps) and the oracle's
+    ref = ResidentSession(model, 64)
+    ref.prefill(prompt[:-1])
+    tok, truth = int(prompt[-1]), []
+    for i in range(8):
+        tok = ref.step(tok, base + i)
+        truth.append(tok)
+    ref.close()
+    orc = OracleModel(model, 64)
+    orc_stream = orc.generate(prompt, 8, [])
+    assert [int(t) for t in orc_stream] == truth
+    rng = np.random.default_rng(3)
+    sess = ResidentSession(model, 64)
+    sess.prefill(prompt[:-1])
+    eng = sess.engine
+    for k in (1, 5, 8):
+        for drafts_kind in ("right", "wrong", "half"):
+            drafts = list(truth[:k - 1])
+            if drafts_kind == "wrong":
+                drafts = [int(t) for t in rng.integers(0, cfg.vocab, k - 1)]
+            elif drafts_kind == "half" and k > 2:
+                drafts[k // 2] = (drafts[k // 2] + 1) % cfg.vocab
+            inputs = [int(prompt[-1])] + drafts
+            cos, sin = rope_tables(cfg, base, k)
+            eng.set_filled(base)
+            pred = [int(t) for t in eng.verify_batch(model.embed(inputs), cos, sin, base, cfg.scale())]
+            # the same inputs as single-token steps
+            eng.set_filled(base)
+            steps = [int(sess.step(t, base + i)) for i, t in enumerate(inputs)]
+            assert pred == steps, (k, drafts_kind)
+            # accept rule: predicted[0], then the bonus after each confirmed draft
+            accepted, j = [pred[0]], 0
+            while j < len(drafts) and drafts[j] == pred[j]:
+                accepted.append(pred[j + 1])
+                j += 1
+            assert accepted == truth[:len(accepted)], (k, drafts_kind)
+    from camelid_amd._native import HipError
+    with pytest.raises(HipError):
+        eng.verify_batch(model.embed([1] * 9), *rope_tables(cfg, base, 9), base, cfg.scale())
+    with pytest.raises(HipError):
+        eng.set_filled(3)
+        eng.verify_batch(model.embed([1]), *rope_tables(cfg, 10, 1), 10, cfg.scale())
+    sess.close()
+
+
 def test_seed_read_roundtrip_and_errors():
     from camelid_amd._native import HipError
     cfg = tiny_config()
