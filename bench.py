@@ -176,7 +176,7 @@ def main() -> int:
         return 2
 
     from camelid_amd.engine import device_info
-    from camelid_amd.model import CONFIGS, ResidentSession, SyntheticModel, prompt_tokens
+    from camelid_amd.model import CONFIGS, ResidentSession, SyntheticModel, prompt_tokens, rope_tables
 
     if args.probe_traffic:
         return probe_traffic()
@@ -260,7 +260,8 @@ def main() -> int:
         assert [int(t) for t in toks2] == [int(t) for t in toks], "profiled pass diverged"
         g = prof["gemv"]
         achieved = g["bytes"] / (g["ms"] * 1e-3) / 1e9
-        kname = ("Q8_0 GEMV: k_gemv_k + k_gemv_gu_silu + k_gemv_argmax" if cfg.quant_scheme == "q8_0" else
+        kname = ("Q8_0 GEMV: k_gemv_norm (RMSNorm + qkv) + k_gemv_k (o, down; + residual) + k_gemv_gu_silu "
+                 "(RMSNorm + gate/up + SwiGLU + Q8_0) + k_gemv_argmax (lm_head)" if cfg.quant_scheme == "q8_0" else
                  "K-quant GEMV: k_gemv_q4k + k_gemv_q6k (incl. lm_head)")
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get(cfg.name),
@@ -269,6 +270,23 @@ def main() -> int:
                     "launches": g["launches"]}
         log("per-kernel (profiled pass): " + ", ".join(
             f"{k} {v['ms']:.2f}ms/{v['launches']}" for k, v in prof.items()))
+
+    # speculative verify (verify_batch): the first 8 timed steps' inputs in one batched
+    # forward; its tokens must be the decode loop's.  Host call incl. input staging.
+    verify = None
+    if K >= 8 and not args.seed_kv:
+        inputs = [last] + [int(t) for t in toks[:7]]
+        vcos, vsin = rope_tables(cfg, start_pos, 8)
+        embs = model.embed(inputs)
+        eng.set_filled(start_pos)
+        pred = eng.verify_batch(embs, vcos, vsin, start_pos, cfg.scale())
+        t0 = time.perf_counter()
+        for _ in range(5):
+            pred = eng.verify_batch(embs, vcos, vsin, start_pos, cfg.scale())
+        vdt = (time.perf_counter() - t0) / 5
+        verify = {"k": 8, "ms": round(vdt * 1e3, 3), "tokens_identical": [int(t) for t in pred] == [int(t) for t in toks[:8]],
+                  "tok_s_if_all_accepted": round(8 / vdt, 1)}
+        log(f"verify k=8: {vdt * 1e3:.2f} ms, tokens identical to the decode loop: {verify['tokens_identical']}")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -300,6 +318,7 @@ def main() -> int:
         "parity": parity,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "verify": verify,
     }
     if prof:
         out["kernels_ms"] = {k: round(v["ms"], 3) for k, v in prof.items()}

@@ -835,6 +835,20 @@ int ensure_prefill_buffers(camelid_hip_engine* e) {
 
 void launch_gemm(const Q8Mat& m, uint32_t T, const int8_t* xq, const float* xs, float* y, const float* resid,
                  hipStream_t s) {
+  if (T <= (uint32_t)cm::GMT_MAX && m.k <= 8192) {  // a few tokens: weights streamed once by GEMV-shaped workgroups
+    const uint32_t grid = (m.rows + cm::GMT_ROWS - 1) / cm::GMT_ROWS;
+    const size_t lds = cm::gemv_multi_lds_bytes((int)m.k, (int)T);
+    switch (m.k) {
+#define CM_GMT(K)                                                                                                  \
+  case K:                                                                                                          \
+    CM_LAUNCH(cm::k_gemv_multi<K>, dim3(grid), dim3(256), lds, s, m.q, m.d, (int)m.rows, xq, xs, (int)T, y, resid); \
+    return;
+      CM_GMT(2048) CM_GMT(3072) CM_GMT(4096) CM_GMT(5632) CM_GMT(8192)
+#undef CM_GMT
+      default:
+        break;
+    }
+  }
   CM_LAUNCH(cm::k_gemm_q8, dim3(cm::gemm_grid((int)m.rows, (int)T)), dim3(cm::GM_NT), 0, s, m.q, m.d, (int)m.rows,
             (int)m.k, xq, xs, (int)T, y, resid);
 }

@@ -211,6 +211,78 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq
 }
 
 // ---------------------------------------------------------------------------
+// Y[t] = W . X[t] (+ resid[t]) for 1 <= T <= GMT_MAX tokens (speculative verify, short
+// prefill chunks): the single-token GEMV's arithmetic for every (row, token) -- exact int32
+// block dots, terms ((float)dot * d_w) * d_x, the in-order fold over blocks -- with each
+// weight chunk loaded once and dotted with all T activations (a 64-token matrix-core tile
+// would leave most CUs idle at this size).  4 waves x GMT_RPW rows per workgroup.
+// Dynamic LDS: gemv_multi_lds_bytes(K, T).
+constexpr int GMT_MAX = 8;
+constexpr int GMT_RPW = 2;
+constexpr int GMT_ROWS = 4 * GMT_RPW;
+__host__ __device__ inline size_t gemv_multi_lds_bytes(int K, int T) {
+  return (size_t)T * K + (size_t)T * (K / 32) * 4 + (size_t)GMT_ROWS * T * gemv_term_stride(K / 32) * 4;
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void k_gemv_multi(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                                    int rows, const int8_t* __restrict__ xq,
+                                                    const float* __restrict__ xs, int T, float* y,
+                                                    const float* resid) {
+  constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64, STRIDE = gemv_term_stride(NB);
+  static_assert(NB % 4 == 0, "compile-time GEMV widths are multiples of 128");
+  extern __shared__ __align__(16) unsigned char gmt_lds[];
+  int8_t* xl = reinterpret_cast<int8_t*>(gmt_lds);                    // [T][K]
+  float* xsl = reinterpret_cast<float*>(gmt_lds + (size_t)T * K);     // [T][NB]
+  float* t = xsl + (size_t)T * NB;                                     // [GMT_ROWS][T][STRIDE]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int row0 = blockIdx.x * GMT_ROWS;
+  int4 wv[GMT_RPW][IT];
+  uint16_t dv[GMT_RPW][IT];
+#pragma unroll
+  for (int k = 0; k < GMT_RPW; ++k) {
+    const int row = min(row0 + wave * GMT_RPW + k, rows - 1);
+    const int4* w4 = reinterpret_cast<const int4*>(wq + (size_t)row * K);
+    const uint16_t* d = wd + (size_t)row * NB;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int c = min(lane + 64 * i, CPR - 1);
+      wv[k][i] = w4[c];
+      dv[k][i] = d[c >> 1];
+    }
+  }
+  for (int c = tid; c < T * CPR; c += 256) reinterpret_cast<int4*>(xl)[c] = reinterpret_cast<const int4*>(xq)[c];
+  for (int b = tid; b < T * NB; b += 256) xsl[b] = xs[b];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < GMT_RPW; ++k) {
+    const int lr = wave * GMT_RPW + k;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int c = lane + 64 * i;
+      const int cc = min(c, CPR - 1);
+      const float dw = half_bits_to_float(dv[k][i]);
+      for (int tk = 0; tk < T; ++tk) {
+        int sacc = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl + (size_t)tk * K)[cc], 0);
+        sacc += dpp_xor1(sacc);
+        if ((lane & 1) == 0 && c < CPR)
+          t[((size_t)lr * T + tk) * STRIDE + (c >> 1)] = ((float)sacc * dw) * xsl[tk * NB + (c >> 1)];
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < GMT_ROWS * T) {
+    const int lr = tid / T, tk = tid - lr * T;
+    const int row = row0 + lr;
+    if (row < rows) {
+      const float acc = fold_lds(t + (size_t)tid * STRIDE, NB);
+      const size_t o = (size_t)tk * rows + row;
+      y[o] = resid ? resid[o] + acc : acc;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Causal attention of a prefill chunk (attention_batched, cuda_resident.rs:1994; CPU
 // inference.rs:23945-24025 per token): one workgroup per (query head, token); token t of
 // the chunk sits at position pos0 + t and attends positions [0, pos0 + t], all already in

@@ -81,7 +81,8 @@ def test_q8_gemv_bit_exact(native, orc, rows, k):
 
 
 @pytest.mark.parametrize("rows,k,tokens", [(5120, 3072, 130), (3072, 8192, 64), (2048, 5632, 65), (36, 96, 70),
-                                           (128, 14336, 3), (1000, 2048, 1), (16384, 3072, 33)])
+                                           (128, 14336, 3), (1000, 2048, 1), (16384, 3072, 33),
+                                           (5120, 3072, 8), (3072, 8192, 5), (36, 2048, 2), (4100, 5632, 7)])
 def test_q8_gemm_bit_exact(native, orc, rows, k, tokens):
     """Prefill GEMM on the matrix cores == the per-token GEMV fold of the CPU path."""
     rng = np.random.default_rng(rows + 3 * k + tokens)
