@@ -133,8 +133,8 @@ struct camelid_hip_engine {
   int8_t* pf_xq = nullptr;
   // verify scratch (allocated on first use): inputs of up to CAMELID_MAX_VERIFY_K tokens,
   // their logits and greedy tokens
-  float *v_embs = nullptr, *v_cos = nullptr, *v_sin = nullptr, *v_logits = nullptr;
-  uint32_t* v_tok = nullptr;
+  float *v_embs = nullptr, *v_cos = nullptr, *v_sin = nullptr, *v_logits = nullptr, *v_pv = nullptr;
+  uint32_t *v_tok = nullptr, *v_pi = nullptr;
   uint32_t filled = 0;
   uint32_t cur_pos = 0;  // host copy of the position being computed (profiling byte counts)
   bool capture = false;
@@ -1339,7 +1339,8 @@ int camelid_hip_verify(camelid_hip_engine* e, const float* embs, const float* co
   const size_t half = d.rope_dim / 2, K = CAMELID_MAX_VERIFY_K;
   if (!e->v_embs && (dev_alloc(e, &e->v_embs, K * d.hidden) || dev_alloc(e, &e->v_cos, K * half) ||
                      dev_alloc(e, &e->v_sin, K * half) || dev_alloc(e, &e->v_logits, K * (size_t)d.vocab) ||
-                     dev_alloc(e, &e->v_tok, K)))
+                     dev_alloc(e, &e->v_tok, K) || dev_alloc(e, &e->v_pv, K * cm::AMR_PARTS) ||
+                     dev_alloc(e, &e->v_pi, K * cm::AMR_PARTS)))
     return 1;
   HIP_TRY(e, hipMemcpy(e->v_embs, embs, (size_t)k * d.hidden * 4, hipMemcpyHostToDevice));
   HIP_TRY(e, hipMemcpy(e->v_cos, cos_all, (size_t)k * half * 4, hipMemcpyHostToDevice));
@@ -1356,9 +1357,9 @@ int camelid_hip_verify(camelid_hip_engine* e, const float* embs, const float* co
     launch_rmsnorm_quant(e->pf_h, e->out_norm, d.hidden, d.eps, e->pf_xq, e->pf_xs, nullptr, e->stream,
                          cm::Prefetch{}, k);
     launch_gemm(e->out, k, e->pf_xq, e->pf_xs, e->v_logits, nullptr, e->stream);
-    for (uint32_t t = 0; t < k; ++t)
-      CM_LAUNCH(cm::k_argmax, dim3(1), dim3(1024), 0, e->stream, e->v_logits + (size_t)t * d.vocab, (int)d.vocab,
-                e->v_tok + t);
+    CM_LAUNCH(cm::k_argmax_rows_part, dim3(cm::AMR_PARTS, k), dim3(256), 0, e->stream, e->v_logits, (int)d.vocab,
+              e->v_pv, e->v_pi);
+    CM_LAUNCH(cm::k_argmax_rows_finish, dim3(k), dim3(64), 0, e->stream, e->v_pv, e->v_pi, e->v_tok);
   } else {
     // k single-token steps; the head writes each greedy token to v_tok[step]
     *e->p_st = cm::StepState{base_position, 0u, 0u, 0u};

@@ -211,6 +211,53 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq
 }
 
 // ---------------------------------------------------------------------------
+// Greedy argmax (inference.rs:5912-5925: first index of the max, strict '>') of T rows of n
+// logits: workgroup (p, t) reduces slice p of row t to a (value, index) pair, then one
+// wave per row reduces the AMR_PARTS pairs; a row with no value above -inf gives 0.
+constexpr int AMR_PARTS = 64;
+__global__ __launch_bounds__(256) void k_argmax_rows_part(const float* __restrict__ x, int n,
+                                                          float* __restrict__ pv, uint32_t* __restrict__ pi) {
+  __shared__ float rv[4];
+  __shared__ uint32_t ri[4];
+  const int t = blockIdx.y, p = blockIdx.x, tid = threadIdx.x;
+  const int per = (n + AMR_PARTS - 1) / AMR_PARTS;
+  const int lo = p * per, hi = min(n, lo + per);
+  const float* row = x + (size_t)t * n;
+  float bv = -INFINITY;
+  uint32_t bi = 0xffffffffu;
+  for (int i = lo + tid; i < hi; i += 256) {
+    const float v = row[i];
+    if (v > bv) {
+      bv = v;
+      bi = (uint32_t)i;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) argmax_pair(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
+  if ((tid & 63) == 0) {
+    rv[tid >> 6] = bv;
+    ri[tid >> 6] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 4; ++w) argmax_pair(bv, bi, rv[w], ri[w]);
+    pv[t * AMR_PARTS + p] = bv;
+    pi[t * AMR_PARTS + p] = bi;
+  }
+}
+
+__global__ __launch_bounds__(64) void k_argmax_rows_finish(const float* __restrict__ pv,
+                                                           const uint32_t* __restrict__ pi,
+                                                           uint32_t* __restrict__ out) {
+  const int t = blockIdx.x, lane = threadIdx.x;
+  float bv = pv[t * AMR_PARTS + lane];
+  uint32_t bi = pi[t * AMR_PARTS + lane];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) argmax_pair(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
+  if (lane == 0) out[t] = bi == 0xffffffffu ? 0u : bi;
+}
+
+// ---------------------------------------------------------------------------
 // Y[t] = W . X[t] (+ resid[t]) for 1 <= T <= GMT_MAX tokens (speculative verify, short
 // prefill chunks): the single-token GEMV's arithmetic for every (row, token) -- exact int32
 // block dots, terms ((float)dot * d_w) * d_x, the in-order fold over blocks -- with each
@@ -220,8 +267,13 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq
 constexpr int GMT_MAX = 8;
 constexpr int GMT_RPW = 2;
 constexpr int GMT_ROWS = 4 * GMT_RPW;
+// LDS: the activations [T][K] i8, their scales [T][K/32] f32 rounded up to whole 1 KB wave
+// loads, the terms [GMT_ROWS][T][stride] f32
+__host__ __device__ inline size_t gemv_multi_xs_bytes(int K, int T) {
+  return (((size_t)T * (K / 32) * 4 + 1023) / 1024) * 1024;
+}
 __host__ __device__ inline size_t gemv_multi_lds_bytes(int K, int T) {
-  return (size_t)T * K + (size_t)T * (K / 32) * 4 + (size_t)GMT_ROWS * T * gemv_term_stride(K / 32) * 4;
+  return (size_t)T * K + gemv_multi_xs_bytes(K, T) + (size_t)GMT_ROWS * T * gemv_term_stride(K / 32) * 4;
 }
 
 template <int K>
@@ -234,9 +286,24 @@ __global__ __launch_bounds__(256) void k_gemv_multi(const int8_t* __restrict__ w
   extern __shared__ __align__(16) unsigned char gmt_lds[];
   int8_t* xl = reinterpret_cast<int8_t*>(gmt_lds);                    // [T][K]
   float* xsl = reinterpret_cast<float*>(gmt_lds + (size_t)T * K);     // [T][NB]
-  float* t = xsl + (size_t)T * NB;                                     // [GMT_ROWS][T][STRIDE]
+  float* t = reinterpret_cast<float*>(gmt_lds + (size_t)T * K + gemv_multi_xs_bytes(K, T));  // [GMT_ROWS][T][STRIDE]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int row0 = blockIdx.x * GMT_ROWS;
+  // the activations and their scales go to LDS by direct loads (1 KB per wave load; the
+  // scales' last load may overrun into the rounded-up pad, re-reading the last piece)
+  {
+    const uint4* sx = reinterpret_cast<const uint4*>(xq);
+    const uint4* ss = reinterpret_cast<const uint4*>(xs);
+    uint4* dx = reinterpret_cast<uint4*>(xl);
+    uint4* ds = reinterpret_cast<uint4*>(xsl);
+    const int nx = T * CPR, ns = (T * NB * 4 + 15) / 16;
+    for (int b = wave * 64; b < nx; b += 256)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(sx + min(b + lane, nx - 1)),
+                                       (__attribute__((address_space(3))) void*)(dx + b), 16, 0, 0);
+    for (int b = wave * 64; b < ns; b += 256)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(ss + min(b + lane, ns - 1)),
+                                       (__attribute__((address_space(3))) void*)(ds + b), 16, 0, 0);
+  }
   int4 wv[GMT_RPW][IT];
   uint16_t dv[GMT_RPW][IT];
 #pragma unroll
@@ -251,8 +318,7 @@ __global__ __launch_bounds__(256) void k_gemv_multi(const int8_t* __restrict__ w
       dv[k][i] = d[c >> 1];
     }
   }
-  for (int c = tid; c < T * CPR; c += 256) reinterpret_cast<int4*>(xl)[c] = reinterpret_cast<const int4*>(xq)[c];
-  for (int b = tid; b < T * NB; b += 256) xsl[b] = xs[b];
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0): this wave's direct loads have landed
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < GMT_RPW; ++k) {
