@@ -38,7 +38,7 @@ ARCH = {"llama-3.2-3b": "Llama-3.2-3B-arch Q8_0", "tinyllama-1.1b": "TinyLlama-1
 # WRITE_SIZE passes over `bench.py --probe-traffic`, FETCH_SIZE scaled by 2.0 (what it reads
 # for a 256 MiB device copy: 128 MiB; WRITE_SIZE reads 256 MiB), averaged over the 113 GEMV
 # launches of one C3 step (profiles/traffic_gemv_llama-3.2-3b_q8_0.md).
-TRAFFIC: dict = {"llama-3.2-3b": 30414176}
+TRAFFIC: dict = {"llama-3.2-3b": 30571736}
 # Q8_0 [N, K] shapes, weights N(0, 0.02) and activations N(0, 1), seed 2
 SWEEP_SHAPES = [(2048, 2048), (5632, 2048), (2048, 5632), (32000, 2048), (128256, 3072)]
 
