@@ -1604,8 +1604,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   const int P = pos + 1;
   const int ncache = pos;
   // Loads in the order they are needed (a wave's loads complete in order): this token's q, k
-  // and v, the expf table, then the K rows of the first score pass, then (staging waves)
-  // the first V chunks.
+  // and v and the expf table first.
   float qv = 0.0f, kv = 0.0f, vv = 0.0f;
   uint64_t et = 0;
   if (tid < HD) {
@@ -1620,23 +1619,22 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
     }
   }
   if (tid < 32) et = kExp2Tab[tid];
-  // every wave past this point: q, k, v enter the CU's memory pipeline ahead of the K rows
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_sched_barrier(0);
-  // K rows of the first score pass (rows at or past the position are loaded and dropped;
-  // the addresses stay inside the head's region)
-  uint4 krow0[R8];
-  {
-    const int pl = min(tid, kvs - 1);
+  // The output lanes also load now the (up to 7) V values of the positions past the last
+  // full 8-position granule, which their output chain adds from registers at the end.  (The
+  // K rows and V chunks wait for the score phase: a wave issuing hundreds of KB stalls until
+  // the CU's memory queue drains, and the RoPE barriers would wait for it.)
+  uint16_t vtail[7];
+  if (tid < HD) {
+    const int tail0 = (pos >> 3) << 3;  // first position past the full granules of [0, pos)
 #pragma unroll
-    for (int u = 0; u < R8; ++u) krow0[u] = kg[(size_t)u * kvs + pl];
+    for (int u = 0; u < 7; ++u)
+      vtail[u] = tail0 + u < pos ? vc[hbase + kv_v_index(HD, tail0 + u, tid)] : (uint16_t)0;
   }
   // V staging: the cache positions' V granules (full 8-position groups) are copied into an
   // LDS ring of ring_slots chunks by NH staging waves with direct global->LDS loads; the
-  // output lanes read them from LDS.  A chunk is contiguous in the cache layout.  Up to the
-  // one-pass limit the first chunks go out now; longer contexts use the ring for the
-  // denominator's prefix arrays first.
+  // output lanes read them from LDS.  A chunk is contiguous in the cache layout.  The first
+  // chunks go out after the exponentials (longer contexts with the segmented denominator use
+  // the ring for its prefix arrays first).
   const int ng = ncache >> 3;  // full groups of 8 cache positions
   const int nchunks = (ng + CG - 1) / CG;
   const int R = ring_slots;
@@ -1657,9 +1655,6 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   // to ATT_NT * ATT_ONEPASS_C, the segmented passes beyond (which use the ring first)
   const bool onepass = P >= ATT_FOLD_MAX && P <= ATT_NT * ATT_ONEPASS_C;
   const bool early = P > 1 && P <= ATT_NT * ATT_ONEPASS_C;
-  if (stager && early) {
-    for (int c = 0; c < min(R - 1, nchunks); ++c) stage(c);
-  }
   if (tid < 32) etab[tid] = et;
   if (tid < HD) {
     qs[tid] = qv;
@@ -1747,8 +1742,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
       sc[p] = sv;
       lmax = fmaxf(lmax, sv);
     };
-    if (tid < ncache) score(krow0, tid);
-    for (int p = tid + ATT_NT; p < ncache; p += ATT_NT) {
+    for (int p = tid; p < ncache; p += ATT_NT) {
       uint4 row[R8];
 #pragma unroll
       for (int u = 0; u < R8; ++u) row[u] = kg[(size_t)u * kvs + p];
@@ -1769,10 +1763,13 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
     // or (when even that does not fit) a serial fold by one lane.
     const bool seg = !early && att_seg_chunk<ATT_NT>(P) > 0 &&
                      att_seg_bytes<ATT_NT>(P) <= (size_t)R * ATT_RING_GRANULES * 16;
-    if (stager && !early && !seg) {
+    __syncthreads();
+    // the first V chunks go out now: the staging waves' issue (a wave stalls while the CU's
+    // memory queue is full) overlaps the denominator's serial fold by one lane, and no
+    // barrier waits on it before that
+    if (stager && !seg) {
       for (int c = 0; c < min(R - 1, nchunks); ++c) stage(c);
     }
-    __syncthreads();
     float inv;
     if (onepass) {
       inv = 1.0f / att_onepass_sum<ATT_NT>(sc, P, fs);
@@ -1859,7 +1856,9 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
     }
     __syncthreads();  // the normalised probabilities past the ring (and with no chunks at all)
     if (tid < HD) {
-      for (int p = ng * 8; p < ncache; ++p) acc += sc[p] * half_bits_to_float(vc[hbase + kv_v_index(HD, p, tid)]);
+#pragma unroll
+      for (int u = 0; u < 7; ++u)
+        if (ng * 8 + u < ncache) acc += sc[ng * 8 + u] * half_bits_to_float(vtail[u]);
       acc += sc[pos] * vn[tid];
       out[tid] = acc;
     }
