@@ -131,6 +131,11 @@ struct camelid_hip_engine {
   bool prefill_batched = true;
   float *pf_h = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_gu = nullptr, *pf_xs = nullptr;
   int8_t* pf_xq = nullptr;
+  // layers with K-quant projections: Q8_K activation rows, f32 attention rows, and the rows of
+  // a Q8_0 projection before they are scattered into the QKV / gate|up rows
+  float *pf_kd = nullptr, *pf_att = nullptr, *pf_tmp = nullptr;
+  int8_t* pf_kq = nullptr;
+  int32_t* pf_kbs = nullptr;
   // verify scratch (allocated on first use): inputs of up to CAMELID_MAX_VERIFY_K tokens,
   // their logits and greedy tokens
   float *v_embs = nullptr, *v_cos = nullptr, *v_sin = nullptr, *v_logits = nullptr, *v_pv = nullptr;
@@ -828,9 +833,42 @@ int ensure_prefill_buffers(camelid_hip_engine* e) {
   const size_t tc = PREFILL_CHUNK;
   const size_t nq = (size_t)d.n_heads * d.head_dim, nkv = (size_t)d.n_kv_heads * d.head_dim;
   const size_t act = std::max<size_t>({(size_t)d.hidden, (size_t)d.ffn_dim, nq});
-  return dev_alloc(e, &e->pf_h, tc * d.hidden) || dev_alloc(e, &e->pf_qkv, tc * (nq + 2 * nkv)) ||
-         dev_alloc(e, &e->pf_q, tc * nq) || dev_alloc(e, &e->pf_gu, tc * 2 * d.ffn_dim) ||
-         dev_alloc(e, &e->pf_xq, tc * act) || dev_alloc(e, &e->pf_xs, tc * act / 32);
+  if (dev_alloc(e, &e->pf_h, tc * d.hidden) || dev_alloc(e, &e->pf_qkv, tc * (nq + 2 * nkv)) ||
+      dev_alloc(e, &e->pf_q, tc * nq) || dev_alloc(e, &e->pf_gu, tc * 2 * d.ffn_dim) ||
+      dev_alloc(e, &e->pf_xq, tc * act) || dev_alloc(e, &e->pf_xs, tc * act / 32))
+    return 1;
+  if (!e->any_kquant) return 0;
+  return dev_alloc(e, &e->pf_kd, tc * act / 256) || dev_alloc(e, &e->pf_kq, tc * act) ||
+         dev_alloc(e, &e->pf_kbs, tc * act / 32) || dev_alloc(e, &e->pf_att, tc * nq) ||
+         dev_alloc(e, &e->pf_tmp, tc * act);
+}
+
+// Tokens per launch of the multi-token Q6_K GEMV at width K (its activations and terms
+// within 64 KB of LDS).
+uint32_t q6m_tokens(uint32_t K) {
+  uint32_t t = cm::Q6M_MAX;
+  while (t > 1 && cm::gemv_q6k_multi_lds_bytes((int)K, (int)t) > 65536) --t;
+  return t;
+}
+
+// A K-quant projection over T tokens with Q8_K activation rows (kd [T][k/256], kq [T][k]):
+// y[t * ldy + row] (+ resid, same stride).  Q4_K: the matrix-core GEMM; Q6_K: the multi-token
+// GEMV over groups of up to Q6M_MAX tokens.
+void launch_kgemm(const KMat& m, uint32_t T, const float* kd, const int8_t* kq, float* y, uint32_t ldy,
+                  const float* resid, hipStream_t s) {
+  if (m.quant == CAMELID_Q4_K) {
+    CM_LAUNCH(cm::k_gemm_q4k, dim3(cm::gemm_q4k_grid((int)m.rows, (int)T)), dim3(cm::G4_NT), 0, s, m.a, m.b,
+              (int)m.rows, (int)m.k, kd, kq, (int)T, y, (int)ldy, resid);
+    return;
+  }
+  const uint32_t tt = q6m_tokens(m.k), nsb = m.k / 256;
+  for (uint32_t t0 = 0; t0 < T; t0 += tt) {
+    const uint32_t n = std::min(tt, T - t0);
+    CM_LAUNCH(cm::k_gemv_q6k_multi, dim3((m.rows + cm::Q6M_ROWS - 1) / cm::Q6M_ROWS), dim3(cm::KQ_NT),
+              cm::gemv_q6k_multi_lds_bytes((int)m.k, (int)n), s, m.a, m.b, m.sc, m.d, (int)m.rows, (int)m.k,
+              kd + (size_t)t0 * nsb, kq + (size_t)t0 * m.k, (int)n, y + (size_t)t0 * ldy, (int)ldy,
+              resid ? resid + (size_t)t0 * ldy : nullptr);
+  }
 }
 
 void launch_gemm(const Q8Mat& m, uint32_t T, const int8_t* xq, const float* xs, float* y, const float* resid,
@@ -868,6 +906,55 @@ void launch_attn_prefill(uint32_t hd, uint32_t n_heads, uint32_t n_kv, uint32_t 
 
 // One chunk of T prompt tokens at positions pos0.. through every layer; the residual rows
 // are in e->pf_h, the RoPE rows of the chunk at cosv / sinv.
+// A layer with K-quant projections over the chunk (the order of run_layer_generic per token):
+// RMSNorm rows to Q8_0 and Q8_K, each projection in its own format (Q4_K: k_gemm_q4k, Q6_K:
+// k_gemv_q6k_multi, Q8_0: launch_gemm), the attention rows also in f32 for a K-quant O.
+void prefill_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cosv, const float* sinv, uint32_t T,
+                           uint32_t pos0, float scale) {
+  const camelid_hip_dims& d = e->d;
+  const LayerW& L = e->layers[l];
+  hipStream_t s = e->stream;
+  const uint32_t half = d.rope_dim / 2;
+  const uint32_t nq = d.n_heads * d.head_dim, nkv = d.n_kv_heads * d.head_dim, F = d.ffn_dim, H = d.hidden;
+  // projection i into rows [T][ldy] at y (+ resid)
+  auto proj_rows = [&](const Proj& p, float* y, uint32_t ldy, const float* resid) {
+    if (p.quant != CAMELID_Q8_0) {
+      launch_kgemm(p.kq, T, e->pf_kd, e->pf_kq, y, ldy, resid, s);
+    } else if (ldy == p.q8.rows) {
+      launch_gemm(p.q8, T, e->pf_xq, e->pf_xs, y, resid, s);
+    } else {  // (no residual on the strided projections)
+      launch_gemm(p.q8, T, e->pf_xq, e->pf_xs, e->pf_tmp, nullptr, s);
+      (void)hipMemcpy2DAsync(y, (size_t)ldy * 4, e->pf_tmp, (size_t)p.q8.rows * 4, (size_t)p.q8.rows * 4, T,
+                             hipMemcpyDeviceToDevice, s);
+    }
+  };
+  const uint32_t W = nq + 2 * nkv;
+  launch_rmsnorm_quant(e->pf_h, L.attn_norm, H, d.eps, e->pf_xq, e->pf_xs, nullptr, s, cm::Prefetch{}, T, e->pf_kd,
+                       e->pf_kq, e->pf_kbs);
+  proj_rows(L.p[0], e->pf_qkv, W, nullptr);
+  if (!L.qk_stacked) proj_rows(L.p[1], e->pf_qkv + nq, W, nullptr);
+  proj_rows(L.p[2], e->pf_qkv + nq + nkv, W, nullptr);
+  CM_LAUNCH(cm::k_rope_kv, dim3(d.n_heads + d.n_kv_heads, T), dim3(64), 0, s, e->pf_qkv, (int)d.n_heads,
+            (int)d.n_kv_heads, (int)d.head_dim, (int)d.rope_dim, (int)d.split_half_pairing, cosv, sinv, L.q_norm,
+            L.k_norm, d.eps, e->pf_q, e->kc, e->vc, (int)l, (int)e->kvs, (const uint32_t*)nullptr, (int)pos0,
+            (int)half);
+  launch_attn_prefill(d.head_dim, d.n_heads, d.n_kv_heads, T, e->pf_q, e->kc, e->vc, (int)l, (int)e->kvs, (int)pos0,
+                      scale, e->pf_att, e->pf_xq, e->pf_xs, s);
+  if (L.p[3].quant != CAMELID_Q8_0)
+    CM_LAUNCH(cm::k_quantize_q8k, dim3(T * nq / 256), dim3(256), 0, s, e->pf_att, e->pf_kd, e->pf_kq,
+              e->pf_kbs);
+  proj_rows(L.p[3], e->pf_h, H, e->pf_h);
+  launch_rmsnorm_quant(e->pf_h, L.ffn_norm, H, d.eps, e->pf_xq, e->pf_xs, nullptr, s, cm::Prefetch{}, T, e->pf_kd,
+                       e->pf_kq, e->pf_kbs);
+  proj_rows(L.p[4], e->pf_gu, 2 * F, nullptr);
+  if (!L.gu_stacked) proj_rows(L.p[5], e->pf_gu + F, 2 * F, nullptr);
+  const bool k8 = L.p[6].quant != CAMELID_Q8_0;
+  CM_LAUNCH(cm::k_silu_mul_quant, dim3((F + 255) / 256, T), dim3(256), 0, s, e->pf_gu, (int)F, e->pf_xq, e->pf_xs,
+            (float*)nullptr, cm::Prefetch{}, k8 ? e->pf_kd : nullptr, k8 ? e->pf_kq : nullptr,
+            k8 ? e->pf_kbs : nullptr);
+  proj_rows(L.p[6], e->pf_h, H, e->pf_h);
+}
+
 void prefill_chunk(camelid_hip_engine* e, const float* cosv, const float* sinv, uint32_t T, uint32_t pos0,
                    float scale) {
   const camelid_hip_dims& d = e->d;
@@ -875,6 +962,10 @@ void prefill_chunk(camelid_hip_engine* e, const float* cosv, const float* sinv, 
   const uint32_t half = d.rope_dim / 2;
   for (uint32_t l = 0; l < d.n_layers; ++l) {
     const LayerW& L = e->layers[l];
+    if (L.generic) {
+      prefill_layer_generic(e, l, cosv, sinv, T, pos0, scale);
+      continue;
+    }
     launch_rmsnorm_quant(e->pf_h, L.attn_norm, d.hidden, d.eps, e->pf_xq, e->pf_xs, nullptr, s, cm::Prefetch{}, T);
     launch_gemm(L.qkv, T, e->pf_xq, e->pf_xs, e->pf_qkv, nullptr, s);
     CM_LAUNCH(cm::k_rope_kv, dim3(d.n_heads + d.n_kv_heads, T), dim3(64), 0, s, e->pf_qkv, (int)d.n_heads,
@@ -1279,9 +1370,7 @@ int camelid_hip_prefill(camelid_hip_engine* e, const float* embs, const float* c
       rc = fail(e, "prefill staging copy failed");
       break;
     }
-    bool generic = false;
-    for (const LayerW& L : e->layers) generic = generic || L.generic;
-    if (e->prefill_batched && !generic) {
+    if (e->prefill_batched) {
       // chunks of PREFILL_CHUNK tokens, every layer over the whole chunk
       if (ensure_prefill_buffers(e)) {
         rc = 1;
@@ -1294,8 +1383,8 @@ int camelid_hip_prefill(camelid_hip_engine* e, const float* embs, const float* c
         prefill_chunk(e, d_cos + (size_t)c0 * half, d_sin + (size_t)c0 * half, T, e->filled + c0, scale);
       }
     } else {
-      // one decode step per token (the path of layers with K-quant projections, whose CPU
-      // prefill is likewise a per-token loop of block dots, inference.rs:2462-2473)
+      // one decode step per token (CAMELID_HIP_PREFILL=token; the reference's CPU prefill of
+      // K-quant layers is likewise a per-token loop of row dots, inference.rs:2462-2473)
       for (uint32_t t = 0; t < n; ++t) {
         (void)hipMemcpyAsync(e->h, d_embs + (size_t)t * d.hidden, d.hidden * 4, hipMemcpyDeviceToDevice, e->stream);
         (void)hipMemcpyAsync(e->st, d_sts + t, sizeof(cm::StepState), hipMemcpyDeviceToDevice, e->stream);
@@ -1345,18 +1434,21 @@ int camelid_hip_verify(camelid_hip_engine* e, const float* embs, const float* co
   HIP_TRY(e, hipMemcpy(e->v_embs, embs, (size_t)k * d.hidden * 4, hipMemcpyHostToDevice));
   HIP_TRY(e, hipMemcpy(e->v_cos, cos_all, (size_t)k * half * 4, hipMemcpyHostToDevice));
   HIP_TRY(e, hipMemcpy(e->v_sin, sin_all, (size_t)k * half * 4, hipMemcpyHostToDevice));
-  bool generic = false;
-  for (const LayerW& L : e->layers) generic = generic || L.generic;
-  const bool batched = e->prefill_batched && !generic && e->out_quant == CAMELID_Q8_0 && e->out.rows % 4 == 0;
+  const bool batched = e->prefill_batched && (e->out_quant != CAMELID_Q8_0 || e->out.rows % 4 == 0);
   if (batched) {
     // one batched forward (the prefill chunk path: bit-identical to token steps), then the
     // final norm, lm_head GEMM and one argmax per token
     if (ensure_prefill_buffers(e)) return 1;
     HIP_TRY(e, hipMemcpyAsync(e->pf_h, e->v_embs, (size_t)k * d.hidden * 4, hipMemcpyDeviceToDevice, e->stream));
     prefill_chunk(e, e->v_cos, e->v_sin, k, base_position, scale);
+    const bool kout = e->out_quant != CAMELID_Q8_0;
     launch_rmsnorm_quant(e->pf_h, e->out_norm, d.hidden, d.eps, e->pf_xq, e->pf_xs, nullptr, e->stream,
-                         cm::Prefetch{}, k);
-    launch_gemm(e->out, k, e->pf_xq, e->pf_xs, e->v_logits, nullptr, e->stream);
+                         cm::Prefetch{}, k, kout ? e->pf_kd : nullptr, kout ? e->pf_kq : nullptr,
+                         kout ? e->pf_kbs : nullptr);
+    if (kout)
+      launch_kgemm(e->out_k, k, e->pf_kd, e->pf_kq, e->v_logits, d.vocab, nullptr, e->stream);
+    else
+      launch_gemm(e->out, k, e->pf_xq, e->pf_xs, e->v_logits, nullptr, e->stream);
     CM_LAUNCH(cm::k_argmax_rows_part, dim3(cm::AMR_PARTS, k), dim3(256), 0, e->stream, e->v_logits, (int)d.vocab,
               e->v_pv, e->v_pi);
     CM_LAUNCH(cm::k_argmax_rows_finish, dim3(k), dim3(64), 0, e->stream, e->v_pv, e->v_pi, e->v_tok);
@@ -1739,6 +1831,26 @@ int camelid_hip_kquant_gemv(uint8_t quant, const uint8_t* a, const uint8_t* b, c
   m.k = k;
   launch_kgemv(m, yd, yq, ybs, y, resid, nullptr, nullptr, (hipStream_t)stream);
   return launch_status("kquant_gemv");
+}
+
+int camelid_hip_kquant_gemm(uint8_t quant, const uint8_t* a, const uint8_t* b, const int8_t* sc, const uint16_t* d,
+                            uint32_t rows, uint32_t k, uint32_t tokens, const float* yd, const int8_t* yq, float* y,
+                            uint32_t ldy, const float* resid, void* stream) {
+  if (!a || !b || !yd || !yq || !y) return fail(nullptr, "null argument");
+  if (quant != CAMELID_Q4_K && quant != CAMELID_Q6_K) return fail(nullptr, "quant must be Q4_K or Q6_K");
+  if (quant == CAMELID_Q6_K && (!sc || !d)) return fail(nullptr, "null argument");
+  if (rows == 0 || k == 0 || k % 256 || k > 16384) return fail(nullptr, "k must be a multiple of 256, at most 16384");
+  if (tokens == 0 || ldy < rows) return fail(nullptr, "tokens must be nonzero and ldy >= rows");
+  KMat m;
+  m.quant = quant;
+  m.a = const_cast<uint8_t*>(a);
+  m.b = const_cast<uint8_t*>(b);
+  m.sc = const_cast<int8_t*>(sc);
+  m.d = const_cast<uint16_t*>(d);
+  m.rows = rows;
+  m.k = k;
+  launch_kgemm(m, tokens, yd, yq, y, ldy, resid, (hipStream_t)stream);
+  return launch_status("kquant_gemm");
 }
 
 int camelid_hip_time_q8_0(int batched, const int8_t* const* wq, const uint16_t* const* wd, uint32_t copies,

@@ -1367,7 +1367,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float* __restrict__
 
 // SwiGLU (tensor/mod.rs:1943-1967) + Q8_0 quantization.  gu = [gate(n) | up(n)].
 // kd (optional, n % 256 == 0): also the Q8_K quantization of the activation, one block per
-// workgroup.
+// workgroup.  gridDim.y rows (prefill chunks): row y at gu + y * 2n, outputs likewise.
 __global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict__ gu, int n, int8_t* __restrict__ xq,
                                                         float* __restrict__ xs, float* __restrict__ act_out,
                                                         Prefetch pf, float* __restrict__ kd,
@@ -1377,6 +1377,18 @@ __global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict_
     __shared__ float sink[1];
     prefetch_lines(pf, blockIdx.x - nwork, gridDim.x - nwork, sink);
     return;
+  }
+  {  // row blockIdx.y of a [rows][2n] batch (prefill); row 0 in the decode step
+    const size_t row = blockIdx.y;
+    gu += row * 2 * n;
+    xq += row * n;
+    xs += row * (n >> 5);
+    if (act_out) act_out += row * n;
+    if (kd) {
+      kd += row * (n >> 8);
+      kq += row * n;
+      kbs += row * (n >> 5);
+    }
   }
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;  // uniform per 32-lane group

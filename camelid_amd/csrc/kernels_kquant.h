@@ -9,6 +9,7 @@
 // superblock.  The activation is quantized to Q8_K by k_quantize_q8k and staged in LDS.
 #pragma once
 #include "kernels_decode.h"
+#include "kernels_prefill.h"
 
 namespace cm {
 
@@ -363,6 +364,331 @@ __global__ __launch_bounds__(256) void k_embed_q6k(const uint8_t* __restrict__ q
   const int q = (lo | (((hq >> (2 * k)) & 3) << 4)) - 32;
   const float d = half_bits_to_float(dw[sb]);
   out[s * 256 + i] = d * (float)scl[sb * 16 + i / 16] * (float)q;
+}
+
+// ---------------------------------------------------------------------------
+// Q4_K GEMM for prefill chunks and batched verify.  The reference has none: its CPU path
+// (and its CUDA path for K-quant layers) prefills one token at a time through the row dot
+// (inference.rs:2462-2473); this kernel gives every (token, row) exactly that dot's result:
+//   per superblock s: sumi = sum_j sc_j * D_j,  D_j = sum over sub-block j of q4 * q8,
+//                     prod = sum_j mn_j * bsum_j   (exact integers)
+//   acc = fma(-(y.d * dmin), prod, acc); acc = fma(y.d * d, sumi, acc), s = 0, 1, ...
+//   y[t][n] = (resid ? resid[t][n] : 0) + acc
+// The integer parts run on the matrix cores: per sub-block (32 values) one
+// v_mfma_i32_16x16x32_i8 gives D_j for a 16-token x 16-row fragment (the activation is the A
+// operand, so a lane's 4 outputs are 4 tokens of one row and need that row's scales only),
+// scaled by sc_j on the vector ALUs; prod comes from a second MFMA per sub-block whose row
+// operand is mn_j repeated (sum_k q8[k] * mn_j = mn_j * bsum_j), accumulated over the
+// superblock.  Lane l of a fragment supplies token / row l % 16, values 8*(l/16) .. +7 of
+// the sub-block; 8 nibble bytes of a row give the row operands of both sub-blocks of a
+// 64-value chunk (low nibbles: sub-block 2c, high: 2c + 1).
+// Workgroup: 4 waves over a 64-row x 64-token tile, each wave 32 x 32 (2 x 2 fragments).
+// One superblock per step: 128 nibble bytes of every row and 256 activation bytes of every
+// token, loaded one step ahead into registers, then into a double-buffered LDS tile
+// [chunk or sub-block][8-byte piece][row or token] (65-entry planes: no bank conflicts);
+// headers and activation scales go straight to registers one step ahead.
+// Tiles are dealt so that each XCD runs a contiguous range, token tiles innermost.
+// K % 256 == 0; y may alias resid (same row stride ldy).
+constexpr int G4_NT = 256;
+constexpr int G4_RN = 64;
+constexpr int G4_RT = 64;
+constexpr int G4_PS = 65;
+constexpr int G4_MAX_SB = 64;  // K <= 16384
+__host__ __device__ inline int gemm_q4k_tiles(int N, int T) {
+  return ((N + G4_RN - 1) / G4_RN) * ((T + G4_RT - 1) / G4_RT);
+}
+__host__ __device__ inline int gemm_q4k_grid(int N, int T) { return ((gemm_q4k_tiles(N, T) + 7) / 8) * 8; }
+
+__global__ __launch_bounds__(G4_NT, 2) void k_gemm_q4k(const uint8_t* __restrict__ nib,
+                                                       const uint8_t* __restrict__ hdr, int N, int K,
+                                                       const float* __restrict__ xd,
+                                                       const int8_t* __restrict__ xq, int T, float* y, int ldy,
+                                                       const float* resid) {
+  __shared__ __align__(16) uint2 sw[2][4][4][G4_PS];  // weights: [buf][64-value chunk][piece][row]
+  __shared__ __align__(16) uint2 sx[2][8][4][G4_PS];  // activations: [buf][sub-block][piece][token]
+  __shared__ __align__(16) float sxd[G4_MAX_SB][G4_RT];  // activation scales: [superblock][token]
+  const int NSB = K >> 8;
+  const int ntt = (T + G4_RT - 1) / G4_RT;
+  const int tiles = gemm_q4k_tiles(N, T);
+  const int per = (tiles + 7) >> 3;
+  const int L = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (L >= tiles) return;
+  const int n_base = (L / ntt) * G4_RN, t_base = (L % ntt) * G4_RT;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int r = lane & 15, g = lane >> 4;
+  const int wn = (wave & 1) * 32, wt = (wave >> 1) * 32;
+  for (int i = tid; i < NSB * G4_RT; i += G4_NT) {
+    const int sb = i / G4_RT, t = i - sb * G4_RT;
+    sxd[sb][t] = xd[(size_t)min(t_base + t, T - 1) * NSB + sb];
+  }
+
+  // global -> register loads of one superblock step (32-bit offsets from the matrix bases)
+  const int wrow = tid >> 3, wc = tid & 7;   // weights: rows wrow + 32 j, 16 bytes at wc * 16
+  const int xrow = tid >> 4, xc = tid & 15;  // activations: tokens xrow + 16 j, 16 bytes at xc * 16
+  uint32_t ow[2], ox[4], oh[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) ow[j] = (uint32_t)min(n_base + wrow + 32 * j, N - 1) * (uint32_t)(K >> 1) + wc * 16;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ox[j] = (uint32_t)min(t_base + xrow + 16 * j, T - 1) * (uint32_t)K + xc * 16;
+#pragma unroll
+  for (int f = 0; f < 2; ++f) oh[f] = (uint32_t)min(n_base + wn + 16 * f + r, N - 1) * (uint32_t)NSB;
+  uint4 rw[2], rx[4], rh[2];
+  auto gload = [&](int s) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) rw[j] = *reinterpret_cast<const uint4*>(nib + ow[j] + (size_t)s * 128);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) rx[j] = *reinterpret_cast<const uint4*>(xq + ox[j] + (size_t)s * 256);
+#pragma unroll
+    for (int f = 0; f < 2; ++f) rh[f] = reinterpret_cast<const uint4*>(hdr)[oh[f] + s];
+  };
+  auto lds_put = [&](int buf) {
+    const int wchunk = wc >> 1, wp = (wc & 1) * 2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      sw[buf][wchunk][wp][wrow + 32 * j] = make_uint2(rw[j].x, rw[j].y);
+      sw[buf][wchunk][wp + 1][wrow + 32 * j] = make_uint2(rw[j].z, rw[j].w);
+    }
+    const int xsb = xc >> 1, xp = (xc & 1) * 2;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      sx[buf][xsb][xp][xrow + 16 * j] = make_uint2(rx[j].x, rx[j].y);
+      sx[buf][xsb][xp + 1][xrow + 16 * j] = make_uint2(rx[j].z, rx[j].w);
+    }
+  };
+
+  float acc[2][2][4];  // [token fragment][row fragment][token 4g + i]
+#pragma unroll
+  for (int tf = 0; tf < 2; ++tf)
+#pragma unroll
+    for (int nf = 0; nf < 2; ++nf)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[tf][nf][i] = 0.0f;
+
+  const uint32_t K1 = 0x3f3f3f3fu, K2 = 0x0f0f0f0fu, K3 = 0x03030303u;
+  auto step = [&](int buf, int sb, const uint4 (&hd)[2]) {
+    // the rows' 6-bit scales and mins, 4 per dword (sub-blocks 0-3, 4-7)
+    uint32_t scp[2][2], mnp[2][2];
+#pragma unroll
+    for (int nf = 0; nf < 2; ++nf) {
+      scp[nf][0] = hd[nf].y & K1;
+      scp[nf][1] = (hd[nf].w & K2) | (((hd[nf].y >> 6) & K3) << 4);
+      mnp[nf][0] = hd[nf].z & K1;
+      mnp[nf][1] = ((hd[nf].w >> 4) & K2) | (((hd[nf].z >> 6) & K3) << 4);
+    }
+    int sumi[2][2][4];
+    v4i_t cmn[2][2];
+#pragma unroll
+    for (int tf = 0; tf < 2; ++tf)
+#pragma unroll
+      for (int nf = 0; nf < 2; ++nf) {
+        cmn[tf][nf] = v4i_t{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sumi[tf][nf][i] = 0;
+      }
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+      __builtin_amdgcn_sched_barrier(0);  // one 64-value chunk at a time (register pressure)
+      uint2 wv[2];
+#pragma unroll
+      for (int nf = 0; nf < 2; ++nf) wv[nf] = sw[buf][c4][g][wn + 16 * nf + r];
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        const int j = 2 * c4 + hb;
+        long av[2], bw[2], bm[2];
+        int scj[2];
+#pragma unroll
+        for (int tf = 0; tf < 2; ++tf) av[tf] = *reinterpret_cast<const long*>(&sx[buf][j][g][wt + 16 * tf + r]);
+#pragma unroll
+        for (int nf = 0; nf < 2; ++nf) {
+          const uint32_t lo = hb ? ((wv[nf].x >> 4) & K2) : (wv[nf].x & K2);
+          const uint32_t hi = hb ? ((wv[nf].y >> 4) & K2) : (wv[nf].y & K2);
+          bw[nf] = (long)(((uint64_t)hi << 32) | lo);
+          const uint32_t sel = (uint32_t)(j & 3) * 0x01010101u;  // byte j % 4 into all four bytes
+          const uint32_t mrep = __builtin_amdgcn_perm(0u, mnp[nf][j >> 2], sel);
+          bm[nf] = (long)(((uint64_t)mrep << 32) | mrep);
+          scj[nf] = (int)((scp[nf][j >> 2] >> (8 * (j & 3))) & 0xffu);
+        }
+#pragma unroll
+        for (int tf = 0; tf < 2; ++tf)
+#pragma unroll
+          for (int nf = 0; nf < 2; ++nf) {
+            const v4i_t c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[tf], bw[nf], v4i_t{0, 0, 0, 0}, 0, 0, 0);
+            cmn[tf][nf] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[tf], bm[nf], cmn[tf][nf], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sumi[tf][nf][i] += scj[nf] * c[i];
+          }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int tf = 0; tf < 2; ++tf) {
+      const float4 y4 = *reinterpret_cast<const float4*>(&sxd[sb][wt + 16 * tf + 4 * g]);
+      const float ydv[4] = {y4.x, y4.y, y4.z, y4.w};
+#pragma unroll
+      for (int nf = 0; nf < 2; ++nf) {
+        const float dw = half_bits_to_float((uint16_t)(hd[nf].x & 0xffffu));
+        const float dmw = half_bits_to_float((uint16_t)(hd[nf].x >> 16));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[tf][nf][i] = fmaf(-(ydv[i] * dmw), (float)cmn[tf][nf][i], acc[tf][nf][i]);
+          acc[tf][nf][i] = fmaf(ydv[i] * dw, (float)sumi[tf][nf][i], acc[tf][nf][i]);
+        }
+      }
+    }
+  };
+
+  gload(0);
+  lds_put(0);
+  __syncthreads();
+  for (int sb = 0; sb < NSB; ++sb) {
+    const int buf = sb & 1;
+    const uint4 hd[2] = {rh[0], rh[1]};
+    if (sb + 1 < NSB) gload(sb + 1);
+    step(buf, sb, hd);
+    if (sb + 1 < NSB) lds_put(buf ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int tf = 0; tf < 2; ++tf)
+#pragma unroll
+    for (int nf = 0; nf < 2; ++nf) {
+      const int n = n_base + wn + 16 * nf + r;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t_base + wt + 16 * tf + 4 * g + i;
+        if (t < T && n < N) {
+          const size_t o = (size_t)t * ldy + n;
+          y[o] = resid ? resid[o] + acc[tf][nf][i] : acc[tf][nf][i];
+        }
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Q6_K GEMV over T tokens at once (speculative verify, prefill chunks): each token's result
+// is k_gemv_q6k's, in the same order (the Q6_K decode dot of inference.rs:19148-19195); the
+// weights of a lane's 64-value unit are loaded and split into their 8 position classes once
+// and used for every token.  The activations stay in LDS as raw Q8_K quants (the class
+// pairs are formed per use).  y[t * ldy + row] (+ resid, same stride).
+// Dynamic LDS: gemv_q6k_multi_lds_bytes(K, T).
+constexpr int Q6M_MAX = 8;
+constexpr int Q6M_RPW = 2;
+constexpr int Q6M_ROWS = 4 * Q6M_RPW;
+__host__ __device__ inline size_t q6m_terms_offset(int K, int T) {
+  return ((size_t)T * K + (size_t)T * (K / 256) * 4 + 15) & ~(size_t)15;
+}
+__host__ __device__ inline size_t gemv_q6k_multi_lds_bytes(int K, int T) {
+  return q6m_terms_offset(K, T) + (size_t)Q6M_ROWS * T * (K / 256) * 32;
+}
+
+__global__ __launch_bounds__(KQ_NT) void k_gemv_q6k_multi(const uint8_t* __restrict__ ql,
+                                                          const uint8_t* __restrict__ qh,
+                                                          const int8_t* __restrict__ scl,
+                                                          const uint16_t* __restrict__ dw, int rows, int K,
+                                                          const float* __restrict__ yd,
+                                                          const int8_t* __restrict__ yq, int T, float* y, int ldy,
+                                                          const float* resid) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int NSB = K >> 8, NU = K >> 6;
+  int8_t* xq = reinterpret_cast<int8_t*>(smem);                  // [T][K]
+  float* xd = reinterpret_cast<float*>(smem + (size_t)T * K);    // [T][NSB]
+  float* terms = reinterpret_cast<float*>(smem + q6m_terms_offset(K, T));  // [row][t][s][class]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int row0 = blockIdx.x * Q6M_ROWS;
+  for (int c = tid; c < (T * K) >> 4; c += KQ_NT) reinterpret_cast<int4*>(xq)[c] = reinterpret_cast<const int4*>(yq)[c];
+  for (int i = tid; i < T * NSB; i += KQ_NT) xd[i] = yd[i];
+  __syncthreads();
+  const uint32_t M4 = 0x0f0f0f0fu, M2 = 0x03030303u;
+#pragma unroll
+  for (int k = 0; k < Q6M_RPW; ++k) {
+    const int rl = wave * Q6M_RPW + k;
+    const int row = min(row0 + rl, rows - 1);
+    const uint8_t* qlr = ql + (size_t)row * (K >> 1);
+    const uint8_t* qhr = qh + (size_t)row * (K >> 2);
+    const int8_t* scr = scl + (size_t)row * NSB * 16;
+    for (int u0 = 0; u0 < NU; u0 += 64) {
+      const int u = u0 + lane;
+      const bool valid = u < NU;  // uniform per 4-lane superblock group (NU % 4 == 0)
+      const int uu = min(u, NU - 1);
+      const int s = uu >> 2, n = (uu >> 1) & 1, q0 = (uu & 1) * 16;
+      const uint4 l0 = *reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + q0);
+      const uint4 l1 = *reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + 32 + q0);
+      const uint4 hh = *reinterpret_cast<const uint4*>(qhr + s * 64 + n * 32 + q0);
+      const uint4 scv = *reinterpret_cast<const uint4*>(scr + s * 16);
+      const float dsb = half_bits_to_float(dw[(size_t)row * NSB + s]);
+      const uint32_t L0[4] = {l0.x, l0.y, l0.z, l0.w}, L1[4] = {l1.x, l1.y, l1.z, l1.w};
+      const uint32_t HH[4] = {hh.x, hh.y, hh.z, hh.w};
+      const uint32_t SC[4] = {scv.x, scv.y, scv.z, scv.w};
+      // the unit's weights as class pairs (bytes 2-3 = -32: one dot4 gives sum (w - 32) * q)
+      uint32_t wp[4][8];
+      int scg[4];
+      int jg[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int j = n * 8 + (q0 >> 4) + 2 * kk;
+        jg[kk] = j;
+        scg[kk] = (int)(int8_t)((SC[j >> 2] >> (8 * (j & 3))) & 0xff);
+        uint32_t v[4];
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+          const uint32_t lq = (kk & 1) ? L1[t4] : L0[t4];
+          const uint32_t lo = (kk < 2) ? (lq & M4) : ((lq >> 4) & M4);
+          v[t4] = lo | (((HH[t4] >> (2 * kk)) & M2) << 4);
+        }
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+          const uint32_t bl = l & 3;
+          wp[kk][l] = __builtin_amdgcn_perm(v[(l >> 2) + 2], v[l >> 2], bl | ((4 + bl) << 8) | (0x0c << 16) | (0x0cu << 24)) |
+                      0xe0e00000u;
+        }
+      }
+      for (int t = 0; t < T; ++t) {
+        int aux[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const uint4 xg = *reinterpret_cast<const uint4*>(xq + (size_t)t * K + s * 256 + 16 * jg[kk]);
+          const uint32_t X[4] = {xg.x, xg.y, xg.z, xg.w};
+#pragma unroll
+          for (int l = 0; l < 8; ++l) {
+            const uint32_t bl = l & 3;
+            // bytes (q[l], q[8 + l], q[l], q[8 + l]) of the 16-value group
+            const uint32_t xpair = __builtin_amdgcn_perm(X[(l >> 2) + 2], X[l >> 2], bl | ((4 + bl) << 8) | (bl << 16) | ((4 + bl) << 24));
+            aux[l] += scg[kk] * __builtin_amdgcn_sdot4((int)wp[kk][l], (int)xpair, 0, false);
+          }
+        }
+#pragma unroll
+        for (int l = 0; l < 8; ++l) aux[l] = group_sum<4>(aux[l]);
+        if (valid && (uu & 3) == 0) {
+          const float d = dsb * xd[t * NSB + s];
+          float* tp = terms + (((size_t)rl * T + t) * NSB + s) * 8;
+          *reinterpret_cast<float4*>(tp) = make_float4(d * (float)aux[0], d * (float)aux[1], d * (float)aux[2],
+                                                       d * (float)aux[3]);
+          *reinterpret_cast<float4*>(tp + 4) = make_float4(d * (float)aux[4], d * (float)aux[5], d * (float)aux[6],
+                                                           d * (float)aux[7]);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // 8 lanes per (row, token): the 8 class chains, then the left fold by the first
+  for (int base = 0; base < Q6M_ROWS * T * 8; base += KQ_NT) {
+    const int id = base + tid;
+    const int pair = id >> 3, l = id & 7;
+    const int rl = pair / T, t = pair - rl * T;
+    float sl = 0.0f;
+    if (pair < Q6M_ROWS * T) {
+      const float* tp = terms + ((size_t)rl * T + t) * NSB * 8 + l;
+      for (int s = 0; s < NSB; ++s) sl += tp[s * 8];
+    }
+    float acc = -0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc += __shfl(sl, (lane & ~7) + i);
+    const int row = row0 + rl;
+    if (l == 0 && pair < Q6M_ROWS * T && row < rows) {
+      const size_t o = (size_t)t * ldy + row;
+      y[o] = resid ? resid[o] + acc : acc;
+    }
+  }
 }
 
 }  // namespace cm

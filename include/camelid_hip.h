@@ -245,6 +245,16 @@ int camelid_hip_kquant_gemv(uint8_t quant, const uint8_t* a, const uint8_t* b, c
                             const uint16_t* d, uint32_t rows, uint32_t k, const float* yd,
                             const int8_t* yq, const int32_t* ybs, float* y, const float* resid,
                             void* stream);
+/* K-quant projection over `tokens` Q8_K activation rows (yd [tokens][k/256], yq [tokens][k]):
+ * y[t * ldy + r] = resid[t * ldy + r] + W[r].x[t], each (token, row) bit-identical to
+ * camelid_hip_kquant_gemv on that token.  Replaces the reference's per-token K-quant prefill
+ * loop (inference.rs:2462-2473; the reference has no K-quant GEMM): Q4_K on the int8 matrix
+ * cores, Q6_K by a multi-token GEMV.  k % 256 == 0, k <= 16384, ldy >= rows; resid may be
+ * NULL; y may alias resid. */
+int camelid_hip_kquant_gemm(uint8_t quant, const uint8_t* a, const uint8_t* b, const int8_t* sc,
+                            const uint16_t* d, uint32_t rows, uint32_t k, uint32_t tokens,
+                            const float* yd, const int8_t* yq, float* y, uint32_t ldy,
+                            const float* resid, void* stream);
 /* Measurement hook (no reference counterpart; the kernel sweep of the benchmark): `iters`
  * launches of the Q8_0 GEMV (batched = 0) or of the prefill GEMM over `tokens` activation
  * rows (batched = 1), rotating over `copies` weight matrices, timed with HIP events on a

@@ -500,6 +500,46 @@ def test_kquant_gemv_bit_exact(native, orc, quant, rows, k):
     assert np.array_equal(_bits(dres.download(np.float32, rows)), _bits(resid + want))
 
 
+@pytest.mark.parametrize("quant,rows,k,T,ldy", [(1, 64, 256, 1, 64), (1, 100, 512, 5, 100), (1, 1024, 4096, 8, 1024),
+                                                 (1, 4096, 4096, 70, 4100), (1, 300, 12288, 3, 300),
+                                                 (1, 2048, 4096, 130, 2048), (1, 36, 16384, 65, 40),
+                                                 (2, 1024, 4096, 8, 1024), (2, 37, 512, 13, 50),
+                                                 (2, 300, 12288, 5, 300), (2, 2048, 4096, 20, 2048)])
+def test_kquant_gemm_bit_exact(native, orc, quant, rows, k, T, ldy):
+    """Multi-token K-quant projection (Q4_K on the matrix cores, Q6_K multi-token GEMV): every
+    (token, row) equals the single-token GEMV on that token bit for bit (and the CPU dot on
+    the first and last token), with a strided, residual-carrying output; ragged row and token
+    tiles, K up to 16384."""
+    rng = np.random.default_rng(rows * 7 + k + T + quant)
+    wire = _kquant_wire(orc, rng, quant, rows, k)
+    a, b, sc, d = _kquant_planes(native, quant, wire, rows, k)
+    x = rng.normal(0, 1, (T, k)).astype(np.float32)
+    x[T // 2, : k // 3] = 0.0  # a token with all-zero Q8_K blocks
+    yds, yqs = zip(*(orc.quantize_q8_k(x[t]) for t in range(T)))
+    ydh, yqh = np.stack(yds).astype(np.float32), np.stack(yqs).astype(np.int8)
+    yd, yq = _dev(ydh), _dev(yqh)
+    resid = rng.normal(0, 1, (T, ldy)).astype(np.float32)
+    dres, y = _dev(resid), _buf(T * ldy * 4)
+    _ok(native.camelid_hip_kquant_gemm(quant, a.ptr, b.ptr, sc.ptr, d.ptr, rows, k, T, yd.ptr, yq.ptr, y.ptr, ldy,
+                                       None, None))
+    got = y.download(np.float32, T * ldy).reshape(T, ldy)[:, :rows]
+    _ok(native.camelid_hip_kquant_gemm(quant, a.ptr, b.ptr, sc.ptr, d.ptr, rows, k, T, yd.ptr, yq.ptr, dres.ptr, ldy,
+                                       dres.ptr, None))
+    got_r = dres.download(np.float32, T * ldy).reshape(T, ldy)
+    one, ybs = _buf(rows * 4), _buf(k // 32 * 4)
+    for t in range(T):
+        tyd, tyq = _dev(ydh[t]), _dev(yqh[t])
+        dbs = _dev(yqh[t].astype(np.int32).reshape(-1, 32).sum(1).astype(np.int32))
+        _ok(native.camelid_hip_kquant_gemv(quant, a.ptr, b.ptr, sc.ptr, d.ptr, rows, k, tyd.ptr, tyq.ptr, dbs.ptr,
+                                           one.ptr, None, None))
+        want = one.download(np.float32, rows)
+        assert np.array_equal(_bits(got[t]), _bits(want)), f"token {t}"
+        assert np.array_equal(_bits(got_r[t, :rows]), _bits(resid[t, :rows] + want)), f"token {t} (resid)"
+        assert np.array_equal(_bits(got_r[t, rows:]), _bits(resid[t, rows:])), "past the rows"
+        if t in (0, T - 1):
+            assert np.array_equal(_bits(want), _bits(orc.kquant_gemv(quant, wire, rows, k, ydh[t], yqh[t])))
+
+
 @pytest.mark.parametrize("n", [1, 1000, 32000, 128256, 151936])
 def test_argmax_matches_first_max(native, orc, n):
     rng = np.random.default_rng(n)

@@ -103,12 +103,18 @@ def test_device_loop_matches_host_loop():
     assert host == dev
 
 
+KQUANT_TINY = dict(hidden=512, ffn_dim=768, n_heads=4, n_kv_heads=2, head_dim=128, vocab=1024, qk_norm=True,
+                   split_half=True, rope_theta=1e6, quant_scheme="q4_k_m")
+
+
 @pytest.mark.parametrize("kw", [dict(), dict(qk_norm=True, split_half=True, rope_theta=1e6),
-                                dict(hidden=384, n_heads=3, n_kv_heads=1, head_dim=128, ffn_dim=1024)])
+                                dict(hidden=384, n_heads=3, n_kv_heads=1, head_dim=128, ffn_dim=1024),
+                                KQUANT_TINY])
 def test_batched_prefill_matches_token_steps(monkeypatch, kw):
-    """The batched prefill (matrix-core GEMMs, causal attention over a chunk) writes the same
-    KV cache as one decode step per token, across chunks of 512 and calls that start at
-    filled > 0; the decode that follows produces the same tokens."""
+    """The batched prefill (matrix-core GEMMs -- Q8_0, or Q4_K with Q6_K multi-token GEMVs --
+    causal attention over a chunk) writes the same KV cache as one decode step per token,
+    across chunks of 512 and calls that start at filled > 0; the decode that follows produces
+    the same tokens."""
     cfg = tiny_config(prompt_len=700, **kw)
     model = SyntheticModel.generate(cfg)
     prompt = prompt_tokens(cfg)
@@ -136,7 +142,8 @@ def test_batched_prefill_matches_token_steps(monkeypatch, kw):
 
 
 @pytest.mark.parametrize("kw,prefill", [(dict(), "batched"), (dict(), "token"),
-                                        (dict(hidden=384, n_heads=3, n_kv_heads=1, head_dim=128, ffn_dim=1024), "batched")])
+                                        (dict(hidden=384, n_heads=3, n_kv_heads=1, head_dim=128, ffn_dim=1024), "batched"),
+                                        (KQUANT_TINY, "batched")])
 def test_verify_batch_matches_token_steps(monkeypatch, kw, prefill):
     """verify_batch (cuda_resident.rs:7821): k tokens in one batched forward give, bit for bit,
     the greedy tokens of k single-token steps over the same inputs (the reference's
