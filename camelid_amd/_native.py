@@ -36,6 +36,33 @@ class Dims(C.Structure):
     ]
 
 
+class GgufTensor(C.Structure):
+    """camelid_gguf_tensor: one entry of a mapped GGUF file's tensor directory."""
+
+    _fields_ = [
+        ("data", vp),
+        ("n_bytes", C.c_uint64),
+        ("offset", C.c_uint64),
+        ("dims", C.c_uint64 * 4),
+        ("n_dims", C.c_uint32),
+        ("type", C.c_int32),
+    ]
+
+
+class GgufRope(C.Structure):
+    """camelid_gguf_rope: a model's RoPE parameters in camelid_rope_tables' argument form."""
+
+    _fields_ = [
+        ("freq_base", C.c_float),
+        ("scaling_kind", C.c_int32),
+        ("factor", C.c_float),
+        ("orig_ctx", C.c_float),
+        ("low", C.c_float),
+        ("high", C.c_float),
+        ("freqs", vp),
+    ]
+
+
 # name -> (restype, argtypes)
 SIGNATURES: dict[str, tuple] = {
     "camelid_hip_engine_new": (C.c_int, [C.POINTER(Dims), C.POINTER(vp)]),
@@ -87,6 +114,19 @@ SIGNATURES: dict[str, tuple] = {
     "camelid_kquant_repack": (C.c_int, [C.c_uint8, u8p, C.c_size_t, C.c_size_t, u8p, u8p, i8p, u16p]),
     "camelid_hip_kquant_gemv": (C.c_int, [C.c_uint8, vp, vp, vp, vp, C.c_uint32, C.c_uint32, vp, vp, vp, vp, vp,
                                           vp]),
+    "camelid_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(vp)]),
+    "camelid_gguf_close": (None, [vp]),
+    "camelid_gguf_last_error": (C.c_char_p, []),
+    "camelid_gguf_version": (C.c_uint32, [vp]),
+    "camelid_gguf_alignment": (C.c_uint64, [vp]),
+    "camelid_gguf_tensor_count": (C.c_uint64, [vp]),
+    "camelid_gguf_tensor_name": (C.c_char_p, [vp, C.c_uint64]),
+    "camelid_gguf_find": (C.c_int, [vp, C.c_char_p, C.POINTER(GgufTensor)]),
+    "camelid_gguf_meta_u32": (C.c_int, [vp, C.c_char_p, C.POINTER(C.c_uint32)]),
+    "camelid_gguf_meta_f32": (C.c_int, [vp, C.c_char_p, C.POINTER(C.c_float)]),
+    "camelid_gguf_meta_str": (C.c_char_p, [vp, C.c_char_p]),
+    "camelid_gguf_model": (C.c_int, [vp, C.c_uint32, C.POINTER(Dims), C.POINTER(GgufRope)]),
+    "camelid_hip_load_gguf": (C.c_int, [vp, vp, C.c_int]),
     "camelid_hip_kquant_gemm": (C.c_int, [C.c_uint8, vp, vp, vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp,
                                           vp, C.c_uint32, vp, vp]),
     "camelid_hip_time_q8_0": (C.c_int, [C.c_int, C.POINTER(vp), C.POINTER(vp), C.c_uint32, C.c_uint32,

@@ -19,7 +19,7 @@ BUILD_DIR = PKG / "_build"
 LIB = LIB_DIR / "libcamelid_hip.so"
 
 HIP_SOURCES = ["engine.hip"]
-HOST_SOURCES = ["seam.cpp", "synth.cpp"]
+HOST_SOURCES = ["seam.cpp", "synth.cpp", "gguf.cpp"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -11,6 +11,7 @@ from __future__ import annotations
 import ctypes as C
 import math
 from dataclasses import dataclass, field
+from pathlib import Path
 
 import numpy as np
 
@@ -130,14 +131,16 @@ CONFIGS = {
 }
 
 
-def rope_tables(cfg: ModelConfig, pos0: int, n_pos: int):
-    """Host RoPE tables [n_pos][rope_dim/2] (rope.rs:568-685), via the native seam."""
+def rope_tables(cfg: ModelConfig, pos0: int, n_pos: int, freqs: np.ndarray | None = None):
+    """Host RoPE tables [n_pos][rope_dim/2] (rope.rs:568-685), via the native seam; freqs: a
+    model's rope_freqs factors [rope_dim/2] (rope.rs:526-560), if it has them."""
     half = cfg.rope_dim // 2
     cos = np.empty((n_pos, half), np.float32)
     sin = np.empty((n_pos, half), np.float32)
     kind = {"none": 0, "linear": 1, "llama3": 2}[cfg.rope_scaling]
+    fp = None if freqs is None else N.ptr(np.ascontiguousarray(freqs, np.float32), C.c_float)
     rc = N.lib().camelid_rope_tables(cfg.rope_dim, cfg.rope_theta, kind, cfg.rope_factor, cfg.rope_orig_ctx,
-                                     cfg.rope_low, cfg.rope_high, None, pos0, n_pos, N.ptr(cos, C.c_float),
+                                     cfg.rope_low, cfg.rope_high, fp, pos0, n_pos, N.ptr(cos, C.c_float),
                                      N.ptr(sin, C.c_float))
     if rc:
         raise ValueError("invalid RoPE metadata")
@@ -225,6 +228,9 @@ class SyntheticModel:
             raise ValueError("token id out of range")
         return out
 
+    def rope_tables(self, pos0: int, n_pos: int):
+        return rope_tables(self.cfg, pos0, n_pos)
+
     def load_into(self, eng: HipResidentDecode, device_embedding: bool = False) -> None:
         for i, L in enumerate(self.layers):
             eng.set_layer(i, L["projs"], L["attn_norm"], L["ffn_norm"], L.get("q_norm"), L.get("k_norm"),
@@ -232,6 +238,102 @@ class SyntheticModel:
         eng.set_output(self.output_norm, self.output, quant=self.cfg.output_quant())
         if device_embedding:
             eng.set_embedding(self.token_embd, quant=self.cfg.embd_quant())
+
+
+GGML_TO_QUANT = {8: Q8_0, 12: Q4_K, 14: Q6_K}
+
+
+class GgufModel:
+    """A GGUF model file, mapped read-only by the native loader (camelid_gguf_open:
+    GgufWireMmap::map, wire_mmap.rs:78, and read_metadata, gguf/reader.rs:346): its config
+    (ModelConfig::from_gguf, model.rs:137-230), the seam's embedding rows read from the
+    mapped token table, and the upload of every tensor straight from the mapping
+    (camelid_hip_load_gguf).  Same interface as SyntheticModel."""
+
+    def __init__(self, path, max_pos: int = 0):
+        lib = N.lib()
+        self._lib = lib
+        h = N.vp()
+        if lib.camelid_gguf_open(str(path).encode(), C.byref(h)):
+            raise ValueError(lib.camelid_gguf_last_error().decode())
+        self._h = h
+        dims, rope = N.Dims(), N.GgufRope()
+        if lib.camelid_gguf_model(h, max_pos, C.byref(dims), C.byref(rope)):
+            msg = lib.camelid_gguf_last_error().decode()
+            self.close()
+            raise ValueError(msg)
+        if dims.rope_dim != dims.head_dim:
+            self.close()
+            raise ValueError("partial RoPE (rope.dimension_count != head_dim) is not on the resident path")
+        emb = self.tensor("token_embd.weight")
+        out = self.tensor("output.weight") if self.has_tensor("output.weight") else emb
+        kinds = {0: "none", 1: "linear", 2: "llama3"}
+        self.cfg = ModelConfig(
+            name=Path(str(path)).stem, n_layers=dims.n_layers, hidden=dims.hidden, ffn_dim=dims.ffn_dim,
+            n_heads=dims.n_heads, n_kv_heads=dims.n_kv_heads, head_dim=dims.head_dim, vocab=dims.vocab,
+            rope_theta=float(rope.freq_base), eps=float(dims.eps), tied=not self.has_tensor("output.weight"),
+            qk_norm=self.has_tensor("blk.0.attn_q_norm.weight"), split_half=bool(dims.split_half_pairing),
+            rope_scaling=kinds[rope.scaling_kind], rope_factor=float(rope.factor), rope_orig_ctx=float(rope.orig_ctx),
+            rope_low=float(rope.low), rope_high=float(rope.high),
+            # (the byte accounting of the benchmark; the engine takes each tensor's own format)
+            quant_scheme="q8_0" if emb.type == 8 and out.type == 8 else "q4_k_m")
+        self._embd = emb
+        self._embd_quant = GGML_TO_QUANT.get(emb.type)
+        self._freqs = None
+        if rope.freqs:
+            self._freqs = np.ctypeslib.as_array(C.cast(rope.freqs, C.POINTER(C.c_float)),
+                                                (dims.rope_dim // 2,)).copy()
+
+    def has_tensor(self, name: str) -> bool:
+        t = N.GgufTensor()
+        return self._lib.camelid_gguf_find(self._h, name.encode(), C.byref(t)) == 0
+
+    def tensor(self, name: str) -> "N.GgufTensor":
+        t = N.GgufTensor()
+        if self._lib.camelid_gguf_find(self._h, name.encode(), C.byref(t)):
+            raise KeyError(name)
+        return t
+
+    def tensor_bytes(self, name: str) -> np.ndarray:
+        """A tensor's bytes as a read-only view of the mapping (valid until close)."""
+        t = self.tensor(name)
+        a = np.ctypeslib.as_array(C.cast(t.data, C.POINTER(C.c_uint8)), (t.n_bytes,))
+        a.flags.writeable = False
+        return a
+
+    def rope_tables(self, pos0: int, n_pos: int):
+        return rope_tables(self.cfg, pos0, n_pos, self._freqs)
+
+    def embed(self, tokens) -> np.ndarray:
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        out = np.empty((len(toks), self.cfg.hidden), np.float32)
+        data = C.cast(self._embd.data, C.POINTER(C.c_uint8))
+        if self._embd_quant == Q8_0:
+            rc = self._lib.camelid_embed_q8_0(data, self.cfg.vocab, self.cfg.hidden, N.ptr(toks, C.c_uint32),
+                                              len(toks), N.ptr(out, C.c_float))
+        elif self._embd_quant in (Q4_K, Q6_K):
+            rc = self._lib.camelid_embed_kquant(self._embd_quant, data, self.cfg.vocab, self.cfg.hidden,
+                                                N.ptr(toks, C.c_uint32), len(toks), N.ptr(out, C.c_float))
+        else:
+            raise ValueError(f"token_embd GGML type {self._embd.type} is not supported")
+        if rc:
+            raise ValueError("token id out of range")
+        return out
+
+    def load_into(self, eng: HipResidentDecode, device_embedding: bool = False) -> None:
+        if self._lib.camelid_hip_load_gguf(eng._h, self._h, int(device_embedding)):
+            raise N.HipError(self._lib.camelid_gguf_last_error().decode())
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.camelid_gguf_close(self._h)
+            self._h = None
+
+    def __del__(self):  # pragma: no cover - best effort
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class ResidentSession:
@@ -244,7 +346,7 @@ class ResidentSession:
         model.load_into(self.engine, device_embedding=device_loop)
         self.device_loop = device_loop
         if device_loop:
-            cos, sin = rope_tables(self.cfg, 0, self.engine.max_pos())
+            cos, sin = model.rope_tables(0, self.engine.max_pos())
             self.engine.set_rope_table(cos, sin)
 
     def prefill(self, tokens) -> None:
@@ -252,11 +354,11 @@ class ResidentSession:
         if n == 0:
             return
         base = self.engine.filled()
-        cos, sin = rope_tables(self.cfg, base, n)
+        cos, sin = self.model.rope_tables(base, n)
         self.engine.prefill(self.model.embed(tokens), cos, sin, self.cfg.scale())
 
     def step(self, token: int, pos: int, logits: bool = False):
-        cos, sin = rope_tables(self.cfg, pos, 1)
+        cos, sin = self.model.rope_tables(pos, 1)
         emb = self.model.embed([token])[0]
         return self.engine.forward_token(emb, cos[0], sin[0], pos, self.cfg.scale(), compute_logits=logits)
 

@@ -61,8 +61,9 @@ void camelid_hip_engine_free(camelid_hip_engine* e);
 const char* camelid_hip_last_error(const camelid_hip_engine* e);
 
 /* CudaResidentDecode::set_layer_located (cuda_resident.rs:5801). w[i]/len[i]: projection
- * bytes in CAMELID_PROJ_* order; quant[i]: CAMELID_Q8_0 (only Q8_0 is accepted in this
- * build); q8_layout: 34 or 36.  q_norm/k_norm may be NULL (no QK-norm). */
+ * bytes in CAMELID_PROJ_* order; quant[i]: CAMELID_Q8_0, CAMELID_Q4_K or CAMELID_Q6_K (K-quants
+ * as GGUF wire superblocks); q8_layout: 34 or 36 (Q8_0 projections).  q_norm/k_norm may be
+ * NULL (no QK-norm). */
 int camelid_hip_set_layer(camelid_hip_engine* e, uint32_t layer, const uint8_t* const w[7],
                           const size_t len[7], const uint8_t quant[7], uint8_t q8_layout,
                           const float* attn_norm, const float* ffn_norm, const float* q_norm,

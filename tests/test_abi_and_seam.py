@@ -9,12 +9,15 @@ import numpy as np
 import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
-HEADER = ROOT / "include" / "camelid_hip.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 def _declared_symbols():
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"\b(camelid_\w+)\s*\(", text)))
+    syms = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        syms.update(re.findall(r"\b(camelid_\w+)\s*\(", text))
+    return sorted(syms)
 
 
 def test_library_exports_every_declared_symbol(native):

@@ -16,6 +16,9 @@ from camelid_amd.model import CONFIGS, ResidentSession, SyntheticModel, prompt_t
 pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
+KQUANT_TINY = dict(hidden=512, ffn_dim=768, n_heads=4, n_kv_heads=2, head_dim=128, vocab=1024, qk_norm=True,
+                   split_half=True, rope_theta=1e6, quant_scheme="q4_k_m")
+
 
 def _bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
@@ -94,6 +97,34 @@ def test_kquant_model_bit_exact(kw):
     assert host == dev
 
 
+@pytest.mark.parametrize("kw,arch", [(dict(tied=True, rope_scaling="llama3", rope_factor=32.0, rope_theta=500000.0,
+                                          n_layers=3), "llama"),
+                                     (KQUANT_TINY, "qwen3")])
+def test_gguf_file_model_matches_synthetic(tmp_path, kw, arch):
+    """A model loaded from a GGUF file (mapped read-only, every tensor uploaded straight from
+    the mapping by camelid_hip_load_gguf) generates the synthetic model's tokens -- host loop,
+    device loop (token table from the file), batched prefill and verify alike."""
+    from gguf_writer import model_gguf
+    from camelid_amd.model import GgufModel
+    cfg = tiny_config(prompt_len=40, **kw)
+    model = SyntheticModel.generate(cfg)
+    path = tmp_path / "model.gguf"
+    path.write_bytes(model_gguf(model, arch))
+    g = GgufModel(path, 96)
+    prompt = prompt_tokens(cfg)
+    want = ResidentSession(model, 96).generate(prompt, 12)
+    assert ResidentSession(g, 96).generate(prompt, 12) == want
+    assert ResidentSession(g, 96, device_loop=True).generate(prompt, 12) == want
+    sess = ResidentSession(g, 96)
+    sess.prefill(prompt[:-1])
+    base = len(prompt) - 1
+    inputs = [int(prompt[-1])] + want[:7]
+    cos, sin = g.rope_tables(base, 8)
+    assert [int(t) for t in sess.engine.verify_batch(g.embed(inputs), cos, sin, base, g.cfg.scale())] == want[:8]
+    sess.close()
+    g.close()
+
+
 def test_device_loop_matches_host_loop():
     cfg = tiny_config(n_layers=3, prompt_len=10)
     model = SyntheticModel.generate(cfg)
@@ -101,10 +132,6 @@ def test_device_loop_matches_host_loop():
     host = ResidentSession(model, 40).generate(prompt, 24)
     dev = ResidentSession(model, 40, device_loop=True).generate(prompt, 24)
     assert host == dev
-
-
-KQUANT_TINY = dict(hidden=512, ffn_dim=768, n_heads=4, n_kv_heads=2, head_dim=128, vocab=1024, qk_norm=True,
-                   split_half=True, rope_theta=1e6, quant_scheme="q4_k_m")
 
 
 @pytest.mark.parametrize("kw", [dict(), dict(qk_norm=True, split_half=True, rope_theta=1e6),
