@@ -108,6 +108,12 @@ struct camelid_hip_engine {
   uint16_t* vc = nullptr;  // V, granules of 8 positions per dim (cm::kv_v_index)
   uint32_t kvs = 0;        // KV position stride: max_pos rounded up to a multiple of 8
   int att_slots = 0;       // V ring chunks of the attention kernel
+  // long contexts: the split attention (k_att_scores + k_att_out) from att_split_min positions
+  // on (CAMELID_HIP_ATT_SPLIT; 0 = never); its scores [n_heads][kvs] and slice maxima
+  uint32_t att_split_min = 2048;
+  float* att_sc = nullptr;
+  float* att_mx = nullptr;
+  int att_mode = -1;       // -1: by position; 0 / 1: single / split (graph capture)
   bool read_ahead = true;  // spare workgroups of the norm kernels read ahead the next weights
   bool gu_fused = false;   // gate/up rows interleaved by 32, SwiGLU fused into their GEMV
   bool norm_fused = true;  // RMSNorms computed inside the qkv and gate/up GEMVs (Q8_0 layers)
@@ -144,9 +150,9 @@ struct camelid_hip_engine {
   uint32_t cur_pos = 0;  // host copy of the position being computed (profiling byte counts)
   bool capture = false;
   // device-side loop graph (one decode step)
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t graph_exec = nullptr;
-  float graph_scale = 0.0f;
+  hipGraph_t graph[2] = {nullptr, nullptr};  // [0]: single-workgroup attention, [1]: split
+  hipGraphExec_t graph_exec[2] = {nullptr, nullptr};
+  float graph_scale[2] = {0.0f, 0.0f};
   bool use_graph = true;
   // optional per-launch HIP-event timing (camelid_hip_profile_*)
   bool profiling = false;
@@ -534,6 +540,29 @@ void launch_attention(uint32_t hd, uint32_t n_heads, int slots, hipStream_t s, c
 #undef CM_ATT
 }
 
+// The split attention for long contexts (k_att_scores + k_att_out): slices of ATT_NT
+// positions for the scores (grid sized for kvs; slices past the position exit), 32-dim
+// output workgroups (+ read-ahead workgroups) for the softmax and output sum.
+template <bool FUSED>
+void launch_attention_split(uint32_t hd, uint32_t n_heads, int slots, hipStream_t s, const float* qsrc, int nh,
+                            int nkv, int rope_dim, int split_half, const float* cb, const float* sb, int rs,
+                            const float* qn, const float* kn, float eps, uint16_t* kc, uint16_t* vc, int layer,
+                            int kvs, const uint32_t* pos, float scale, float* g_sc, float* g_mx, float* att,
+                            int8_t* xq, float* xs, cm::Prefetch pf) {
+  const size_t lds = (size_t)slots * cm::ATT_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs);
+#define CM_ATTS(HD)                                                                                                 {                                                                                                                   const int nsl = (kvs + cm::att_nt(HD) - 1) / cm::att_nt(HD);                                                     CM_LAUNCH((cm::k_att_scores<HD, FUSED>), dim3(n_heads, nsl), dim3(cm::att_nt(HD)), 0, s, qsrc, nh, nkv,                    rope_dim, split_half, cb, sb, rs, qn, kn, eps, kc, vc, layer, kvs, pos, scale, g_sc, g_mx);            const uint32_t grid = n_heads * (HD / 32) + (pf.a_lines ? PREFETCH_WGS : 0);                                      CM_LAUNCH((cm::k_att_out<HD>), dim3(grid), dim3(cm::att_nt(HD)), lds, s, vc, nh, nkv, layer, kvs, pos, g_sc,               g_mx, nsl, att, xq, xs, slots, pf);                                                                   }
+  if (hd == 64) CM_ATTS(64)
+  else if (hd == 128) CM_ATTS(128)
+  else CM_ATTS(256)
+#undef CM_ATTS
+}
+
+// The attention of this step: the split kernels from att_split_min positions on.
+bool att_split(const camelid_hip_engine* e) {
+  if (e->att_mode >= 0) return e->att_mode == 1;
+  return e->att_split_min && (uint64_t)e->cur_pos + 1 >= e->att_split_min;
+}
+
 // rows > 1: a [rows][n] batch, one workgroup per row (no read-ahead).
 // kd/kq/kbs (optional, n % 256 == 0): also the Q8_K quantization of the normalized rows.
 void launch_rmsnorm_quant(const float* x, const float* w, uint32_t n, float eps, int8_t* xq, float* xs, float* y,
@@ -570,6 +599,13 @@ long attn_static_lds() {
     CM_ATT_LDS(64, true) CM_ATT_LDS(64, false) CM_ATT_LDS(128, true) CM_ATT_LDS(128, false)
     CM_ATT_LDS(256, true) CM_ATT_LDS(256, false)
 #undef CM_ATT_LDS
+#define CM_ATTO_LDS(HD)                                                                      \
+  if (hipFuncGetAttributes(&a, reinterpret_cast<const void*>(&cm::k_att_out<HD>)) == hipSuccess) \
+    m = std::max<long>(m, (long)a.sharedSizeBytes);                                           \
+  else                                                                                        \
+    m = std::max<long>(m, 32768);
+    CM_ATTO_LDS(64) CM_ATTO_LDS(128) CM_ATTO_LDS(256)
+#undef CM_ATTO_LDS
     bytes = m;
   }
   return bytes;
@@ -663,6 +699,24 @@ void proj(camelid_hip_engine* e, const Proj& p, float* y, const float* resid, co
   launch_kgemv(p.kq, e->kd, e->kq, e->kbs, y, resid, nullptr, nullptr, e->stream, xf);
 }
 
+// The decode attention of layer l for the token at StepState.pos (QK-norm, RoPE and the K/V
+// store fused): one workgroup per head, or the split kernels for long contexts.
+void decode_attention(camelid_hip_engine* e, uint32_t l, const float* cos_base, const float* sin_base,
+                      int rope_stride, float scale, cm::Prefetch pf) {
+  const camelid_hip_dims& d = e->d;
+  const LayerW& L = e->layers[l];
+  if (att_split(e))
+    launch_attention_split<true>(d.head_dim, d.n_heads, e->att_slots, e->stream, e->qkv, (int)d.n_heads,
+                                 (int)d.n_kv_heads, (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base,
+                                 rope_stride, L.q_norm, L.k_norm, d.eps, e->kc, e->vc, (int)l, (int)e->kvs,
+                                 &e->st->pos, scale, e->att_sc, e->att_mx, e->att, e->xq, e->xs, pf);
+  else
+    launch_attention<true>(d.head_dim, d.n_heads, e->att_slots, e->stream, e->qkv, (int)d.n_heads,
+                           (int)d.n_kv_heads, (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base,
+                           rope_stride, L.q_norm, L.k_norm, d.eps, e->kc, e->vc, (int)l, (int)e->kvs, &e->st->pos,
+                           scale, e->att, e->xq, e->xs, pf);
+}
+
 // A layer with K-quant projections (forward_layer_timed, inference.rs:6228-6807): the same
 // order as run_layer, with each projection in its own format; the RMSNorm kernel also writes
 // the normalized row, which is quantized to Q8_K when a K-quant projection reads it.
@@ -690,10 +744,7 @@ void run_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cos_base,
   proj(e, L.p[2], e->qkv + nq + nkv, nullptr);
   {
     ProfScope ps(e, P_ATTN, (nq + 2.0 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0));
-    launch_attention<true>(d.head_dim, d.n_heads, e->att_slots, s, e->qkv, (int)d.n_heads, (int)d.n_kv_heads,
-                           (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base, rope_stride, L.q_norm,
-                           L.k_norm, d.eps, e->kc, e->vc, (int)l, (int)e->kvs, &e->st->pos, scale, e->att, e->xq,
-                           e->xs, ahead(L.p[3]));
+    decode_attention(e, l, cos_base, sin_base, rope_stride, scale, ahead(L.p[3]));
   }
   proj(e, L.p[3], e->h, e->h, is_k(3) ? e->att : nullptr);
   norm(L.ffn_norm, is_k(4) || is_k(5), ahead(L.p[4]));
@@ -733,11 +784,7 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const f
   }
   {
     ProfScope ps(e, P_ATTN, (nq + 2 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0));
-    launch_attention<true>(d.head_dim, d.n_heads, e->att_slots, s, e->qkv, (int)d.n_heads,
-                           (int)d.n_kv_heads, (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base,
-                           rope_stride, L.q_norm, L.k_norm, d.eps, e->kc, e->vc, (int)l, (int)e->kvs, &e->st->pos,
-                           scale, e->att, e->xq, e->xs,
-                           prefetch_of(e->read_ahead ? &L.o : nullptr));
+    decode_attention(e, l, cos_base, sin_base, rope_stride, scale, prefetch_of(e->read_ahead ? &L.o : nullptr));
   }
   gemv(e, L.o, e->h, e->h);
   if (!gu_norm) rmsnorm(e, L.ffn_norm, &L.gu);
@@ -997,10 +1044,12 @@ int check_launch(camelid_hip_engine* e) {
 }
 
 void drop_graph(camelid_hip_engine* e) {
-  if (e->graph_exec) (void)hipGraphExecDestroy(e->graph_exec);
-  if (e->graph) (void)hipGraphDestroy(e->graph);
-  e->graph_exec = nullptr;
-  e->graph = nullptr;
+  for (int m = 0; m < 2; ++m) {
+    if (e->graph_exec[m]) (void)hipGraphExecDestroy(e->graph_exec[m]);
+    if (e->graph[m]) (void)hipGraphDestroy(e->graph[m]);
+    e->graph_exec[m] = nullptr;
+    e->graph[m] = nullptr;
+  }
 }
 
 // Device-side decode step (embed -> layers -> head) as launched work on e->stream.
@@ -1010,22 +1059,28 @@ void enqueue_device_step(camelid_hip_engine* e, float scale) {
   run_head(e, e->tokens, e->tokens_cap);
 }
 
-// Captures one device-side step into a graph (once per scale).
-int ensure_graph(camelid_hip_engine* e, float scale) {
-  if (e->graph_exec && e->graph_scale == scale) return 0;
-  drop_graph(e);
+// Captures one device-side step into a graph (once per scale and attention mode: the
+// position is read on the device, so the graph for the split attention is a second graph).
+int ensure_graph(camelid_hip_engine* e, float scale, int mode) {
+  if (e->graph_exec[mode] && e->graph_scale[mode] == scale) return 0;
+  if (e->graph_exec[mode]) (void)hipGraphExecDestroy(e->graph_exec[mode]);
+  if (e->graph[mode]) (void)hipGraphDestroy(e->graph[mode]);
+  e->graph_exec[mode] = nullptr;
+  e->graph[mode] = nullptr;
   HIP_TRY(e, hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+  e->att_mode = mode;
   enqueue_device_step(e, scale);
+  e->att_mode = -1;
   hipGraph_t g = nullptr;
   hipError_t st = hipStreamEndCapture(e->stream, &g);
   if (st != hipSuccess) return fail(e, std::string("graph capture failed: ") + hipGetErrorString(st));
-  e->graph = g;
-  st = hipGraphInstantiate(&e->graph_exec, g, nullptr, nullptr, 0);
+  e->graph[mode] = g;
+  st = hipGraphInstantiate(&e->graph_exec[mode], g, nullptr, nullptr, 0);
   if (st != hipSuccess) {
     drop_graph(e);
     return fail(e, std::string("graph instantiate failed: ") + hipGetErrorString(st));
   }
-  e->graph_scale = scale;
+  e->graph_scale[mode] = scale;
   return 0;
 }
 
@@ -1076,6 +1131,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   if (const char* f = std::getenv("CAMELID_HIP_FUSED_GU")) e->gu_fused = e->gu_fused && std::atoi(f) != 0;
   if (const char* f = std::getenv("CAMELID_HIP_FUSED_NORM")) e->norm_fused = std::atoi(f) != 0;
   e->att_slots = attn_ring_slots(e->kvs);
+  if (const char* f = std::getenv("CAMELID_HIP_ATT_SPLIT")) e->att_split_min = (uint32_t)std::strtoul(f, nullptr, 10);
   const size_t nq = (size_t)d.n_heads * d.head_dim, nkv = (size_t)d.n_kv_heads * d.head_dim;
   const size_t kv_elems = (size_t)d.n_layers * d.n_kv_heads * e->kvs * d.head_dim;
   const size_t act = std::max<size_t>({(size_t)d.hidden, (size_t)d.ffn_dim, nq});
@@ -1091,6 +1147,8 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
            dev_alloc(e, &e->part_v, nparts) || dev_alloc(e, &e->part_i, nparts) || dev_alloc(e, &e->st, 1) ||
            dev_alloc(e, &e->tokens, e->tokens_cap) || dev_alloc(e, &e->xn, act) || dev_alloc(e, &e->actf, d.ffn_dim) ||
            dev_alloc(e, &e->kd, act / 256 + 1) || dev_alloc(e, &e->kq, act) || dev_alloc(e, &e->kbs, act / 32) ||
+           dev_alloc(e, &e->att_sc, (size_t)d.n_heads * e->kvs) ||
+           dev_alloc(e, &e->att_mx, (size_t)d.n_heads * ((e->kvs + 255) / 256)) ||
            host_alloc(e, &e->p_emb, d.hidden) ||
            host_alloc(e, &e->p_cos, half) || host_alloc(e, &e->p_sin, half) || host_alloc(e, &e->p_logits, d.vocab) ||
            host_alloc(e, &e->p_st, 1);
@@ -1490,13 +1548,19 @@ int camelid_hip_generate(camelid_hip_engine* e, uint32_t token, uint32_t positio
   if (n_steps == 0) return 0;
   HIP_TRY(e, hipSetDevice(e->device));
   const bool graph = e->use_graph && !e->profiling && !e->capture;
-  if (graph && ensure_graph(e, scale)) return 1;
   *e->p_st = cm::StepState{position, token, 0u, 0u};
   HIP_TRY(e, hipMemcpyAsync(e->st, e->p_st, sizeof(cm::StepState), hipMemcpyHostToDevice, e->stream));
+  if (graph) {  // the graphs this call's positions need (the split attention from att_split_min on)
+    const uint64_t first = (uint64_t)position + 1, last = (uint64_t)position + n_steps;
+    const bool split_used = e->att_split_min && last >= e->att_split_min;
+    const bool single_used = !e->att_split_min || first < e->att_split_min;
+    if ((single_used && ensure_graph(e, scale, 0)) || (split_used && ensure_graph(e, scale, 1))) return 1;
+  }
   for (uint32_t t = 0; t < n_steps; ++t) {
     e->cur_pos = position + t;
     if (graph) {
-      hipError_t st = hipGraphLaunch(e->graph_exec, e->stream);
+      const int mode = att_split(e) ? 1 : 0;
+      hipError_t st = hipGraphLaunch(e->graph_exec[mode], e->stream);
       if (st != hipSuccess) {
         e->filled = 0;
         return fail(e, std::string("graph launch failed: ") + hipGetErrorString(st));
@@ -1732,6 +1796,33 @@ int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const ui
                           const_cast<uint16_t*>(vc), (int)layer, (int)max_pos, d_pos, scale, att_out, xq, xs,
                           prefetch_of((const Q8Mat*)nullptr));
   return launch_status("attention_decode");
+}
+
+int camelid_hip_attention_decode_split(const float* qrot, const uint16_t* kc, const uint16_t* vc, uint32_t layer,
+                                       uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t max_pos,
+                                       const uint32_t* d_pos, float scale, float* att_out, int8_t* xq, float* xs,
+                                       void* stream) {
+  if (!qrot || !kc || !vc || !d_pos || !att_out || !xq || !xs) return fail(nullptr, "null argument");
+  if (!n_heads || !n_kv || n_heads % n_kv || !attention_hd_supported(hd)) return fail(nullptr, "invalid head geometry");
+  if (max_pos % 8) return fail(nullptr, "the KV position stride (max_pos) must be a multiple of 8");
+  const int slots = attn_ring_slots(max_pos);
+  if (slots == 0) return fail(nullptr, "max_pos too large for the decode attention");
+  float *g_sc = nullptr, *g_mx = nullptr;
+  if (hipMalloc(&g_sc, (size_t)n_heads * max_pos * 4) != hipSuccess ||
+      hipMalloc(&g_mx, (size_t)n_heads * ((max_pos + 255) / 256) * 4) != hipSuccess) {
+    (void)hipFree(g_sc);
+    return fail(nullptr, "attention_decode_split: scratch allocation failed");
+  }
+  launch_attention_split<false>(hd, n_heads, slots, (hipStream_t)stream, qrot, (int)n_heads, (int)n_kv, (int)hd, 0,
+                                nullptr, nullptr, 0, nullptr, nullptr, 0.0f, const_cast<uint16_t*>(kc),
+                                const_cast<uint16_t*>(vc), (int)layer, (int)max_pos, d_pos, scale, g_sc, g_mx, att_out,
+                                xq, xs, prefetch_of((const Q8Mat*)nullptr));
+  const int rc = launch_status("attention_decode_split");
+  const hipError_t st = hipStreamSynchronize((hipStream_t)stream);
+  (void)hipFree(g_sc);
+  (void)hipFree(g_mx);
+  if (!rc && st != hipSuccess) return fail(nullptr, std::string("attention_decode_split: ") + hipGetErrorString(st));
+  return rc;
 }
 
 int camelid_hip_rmsnorm_q8_0_gemv(const int8_t* wq, const uint16_t* wd, uint32_t rows, uint32_t k, const float* x,

@@ -1886,6 +1886,299 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
 }
 
 // ---------------------------------------------------------------------------
+// Decode attention for long contexts, split over workgroups: k_attention's arithmetic, in
+// the same order, with a head's K and V streamed through many CUs instead of one (at 8K
+// positions one CU's loads in flight, not the arithmetic, bound the single-workgroup kernel).
+//   k_att_scores  grid (heads, ceil(kvs / ATT_NT)): workgroup (h, s) builds q (and, for s = 0
+//                 of a group's first head, stores this position's K/V, as k_attention does),
+//                 then the scores of positions [s ATT_NT, (s + 1) ATT_NT) ∩ [0, pos] into
+//                 g_sc[h][p] and their max into g_max[h][s]; slices past pos exit at once.
+//   k_att_out     grid (heads * HD / 32 [+ read-ahead workgroups]): workgroup (h, w) reads the
+//                 head's scores, softmax as k_attention (max, expf, the in-order denominator,
+//                 normalise), then out_d for d in [32 w, 32 w + 32) through a V ring whose 32 KB
+//                 chunks hold 512 positions of those 32 dims, and quantizes them (one Q8_0
+//                 block).  Every position's V comes from the cache (k_att_scores stored pos).
+template <int HD, bool FUSED>
+__global__ __launch_bounds__(att_nt(HD)) void k_att_scores(
+    const float* __restrict__ qsrc, int n_heads, int n_kv, int rope_dim, int split_half,
+    const float* __restrict__ cos_base, const float* __restrict__ sin_base, int rope_stride,
+    const float* __restrict__ q_norm, const float* __restrict__ k_norm, float eps, uint16_t* __restrict__ kc,
+    uint16_t* __restrict__ vc, int layer, int kvs, const uint32_t* __restrict__ d_pos, float scale,
+    float* __restrict__ g_sc, float* __restrict__ g_max) {
+  constexpr int ATT_NT = att_nt(HD);
+  static_assert(HD % 64 == 0 && HD <= 256, "head_dim must be 64, 128 or 256");
+  constexpr int R8 = HD / 8;
+  __shared__ __align__(16) float qs[HD];
+  __shared__ __align__(16) float kn[HD];
+  __shared__ __align__(16) float vn[HD];
+  __shared__ __align__(16) float sq[2 * HD];
+  __shared__ float red[ATT_NT / 64];
+  __shared__ float s_qscale, s_kscale;
+  const int tid = threadIdx.x, h = blockIdx.x, s = blockIdx.y;
+  const int pos = (int)*d_pos;
+  const int p0 = s * ATT_NT;
+  if (p0 > pos) return;  // (uniform) a slice past the current position
+  const int rep = n_heads / n_kv;
+  const int kvh = h / rep;
+  const size_t hbase = kv_head_base(layer, n_kv, kvh, HD, kvs);
+  const uint4* kg = reinterpret_cast<const uint4*>(kc + hbase);
+  if (tid < HD) {
+    qs[tid] = qsrc[(size_t)h * HD + tid];
+    if (FUSED) {
+      kn[tid] = qsrc[(size_t)n_heads * HD + (size_t)kvh * HD + tid];
+      vn[tid] = qsrc[(size_t)(n_heads + n_kv) * HD + (size_t)kvh * HD + tid];
+    } else {
+      kn[tid] = half_bits_to_float(kc[hbase + kv_k_index(kvs, pos, tid)]);
+    }
+  }
+  if (FUSED) {
+    if (q_norm) {  // per-head RMSNorm of q and k (serial folds, as k_attention)
+      __syncthreads();
+      if (tid < HD) {
+        sq[tid] = qs[tid] * qs[tid];
+        sq[HD + tid] = kn[tid] * kn[tid];
+      }
+      __syncthreads();
+      if (tid == 0) s_qscale = 1.0f / sqrtf(fold_lds_lean(sq, HD) / (float)HD + eps);
+      if (tid == 64) s_kscale = 1.0f / sqrtf(fold_lds_lean(sq + HD, HD) / (float)HD + eps);
+      __syncthreads();
+      if (tid < HD) {
+        qs[tid] = (qs[tid] * s_qscale) * q_norm[tid];
+        kn[tid] = (kn[tid] * s_kscale) * k_norm[tid];
+      }
+    }
+    __syncthreads();
+    const float* cosv = cos_base + (size_t)pos * rope_stride;
+    const float* sinv = sin_base + (size_t)pos * rope_stride;
+    const int half = rope_dim >> 1;
+    if (tid < half) {
+      const int d0 = split_half ? tid : 2 * tid;
+      const int d1 = split_half ? tid + half : 2 * tid + 1;
+      const float c = cosv[tid], sn = sinv[tid];
+      float x0 = qs[d0], x1 = qs[d1];
+      qs[d0] = (x0 * c) - (x1 * sn);
+      qs[d1] = (x0 * sn) + (x1 * c);
+      x0 = kn[d0];
+      x1 = kn[d1];
+      kn[d0] = (x0 * c) - (x1 * sn);
+      kn[d1] = (x0 * sn) + (x1 * c);
+    }
+    __syncthreads();
+    if (tid < HD) {
+      const uint16_t kb = f32_to_f16_bits(kn[tid]);
+      kn[tid] = half_bits_to_float(kb);
+      if ((h % rep) == 0 && s == 0) {
+        kc[hbase + kv_k_index(kvs, pos, tid)] = kb;
+        vc[hbase + kv_v_index(HD, pos, tid)] = f32_to_f16_bits(vn[tid]);
+      }
+    }
+  }
+  __syncthreads();
+  float lmax = -INFINITY;
+  const int p = p0 + tid;
+  if (p < pos) {
+    uint4 row[R8];
+#pragma unroll
+    for (int u = 0; u < R8; ++u) row[u] = kg[(size_t)u * kvs + p];
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < R8; ++u) {
+      __builtin_amdgcn_sched_barrier(0);
+      const float4 qa = reinterpret_cast<const float4*>(qs)[2 * u];
+      const float4 qb = reinterpret_cast<const float4*>(qs)[2 * u + 1];
+      const float e0 = mul_f16_lo(qa.x, row[u].x), e1 = mul_f16_hi(qa.y, row[u].x);
+      const float e2 = mul_f16_lo(qa.z, row[u].y), e3 = mul_f16_hi(qa.w, row[u].y);
+      const float e4 = mul_f16_lo(qb.x, row[u].z), e5 = mul_f16_hi(qb.y, row[u].z);
+      const float e6 = mul_f16_lo(qb.z, row[u].w), e7 = mul_f16_hi(qb.w, row[u].w);
+      acc += e0;
+      acc += e1;
+      acc += e2;
+      acc += e3;
+      acc += e4;
+      acc += e5;
+      acc += e6;
+      acc += e7;
+    }
+    const float sv = acc * scale;
+    g_sc[(size_t)h * kvs + p] = sv;
+    lmax = sv;
+  } else if (p == pos) {  // this token's own key, from LDS
+    float acc = 0.0f;
+#pragma unroll
+    for (int d = 0; d < HD; ++d) acc += qs[d] * kn[d];
+    const float sv = acc * scale;
+    g_sc[(size_t)h * kvs + p] = sv;
+    lmax = sv;
+  }
+  const float mx = block_max(lmax, red);
+  if (tid == 0) g_max[(size_t)h * gridDim.y + s] = mx;
+}
+
+template <int HD>
+__global__ __launch_bounds__(att_nt(HD)) void k_att_out(
+    const uint16_t* __restrict__ vc, int n_heads, int n_kv, int layer, int kvs, const uint32_t* __restrict__ d_pos,
+    const float* __restrict__ g_sc, const float* __restrict__ g_max, int n_slices, float* __restrict__ att_out,
+    int8_t* __restrict__ xq, float* __restrict__ xs, int ring_slots, Prefetch pf) {
+  constexpr int ATT_NT = att_nt(HD);
+  constexpr int NW = ATT_NT / 64;
+  constexpr int DW = 32;                       // output dims per workgroup: one Q8_0 block
+  constexpr int NDW = HD / DW;
+  constexpr int NH = (NW - 1) >= 8 ? 8 : 4;    // V-staging waves 1..NH
+  constexpr int LH = ATT_RING_LOADS / NH;      // 1 KB wave loads per staging wave per chunk
+  constexpr int CG = ATT_RING_GRANULES / DW;   // 8-position groups per ring chunk
+  static_assert(CG % 4 == 0, "ring chunks hold a multiple of 4 granule groups");
+  extern __shared__ __align__(16) float4 dyn[];
+  float4* ring = dyn;
+  float* sc = reinterpret_cast<float*>(dyn + (size_t)ring_slots * ATT_RING_GRANULES);
+  const int nwork = n_heads * NDW;
+  if ((int)blockIdx.x >= nwork) {  // spare workgroups: read ahead the output projection
+    prefetch_lines(pf, blockIdx.x - nwork, gridDim.x - nwork, sc);
+    return;
+  }
+  __shared__ float red[NW];
+  __shared__ float s_inv;
+  __shared__ uint64_t etab[32];
+  __shared__ FsLds<ATT_NT> fs;
+  const int tid = threadIdx.x;
+  const int h = (int)blockIdx.x / NDW, w = (int)blockIdx.x % NDW;
+  const int rep = n_heads / n_kv;
+  const size_t hbase = kv_head_base(layer, n_kv, h / rep, HD, kvs);
+  const uint4* vg = reinterpret_cast<const uint4*>(vc + hbase);  // V granule (g, d): g * HD + d
+  const int pos = (int)*d_pos;
+  const int P = pos + 1;
+  const int d = w * DW + tid;  // output lanes: tid < DW
+  float acc = 0.0f;
+  if (P == 1) {
+    // inference.rs:23564-23575: a single position copies the V row
+    if (tid < DW) acc = half_bits_to_float(vc[hbase + kv_v_index(HD, pos, d)]);
+  } else {
+    if (tid < 32) etab[tid] = kExp2Tab[tid];
+    const float* gs = g_sc + (size_t)h * kvs;
+    for (int p = tid; p < P; p += ATT_NT) sc[p] = gs[p];
+    float lm = -INFINITY;
+    const int nsl = (P + ATT_NT - 1) / ATT_NT;
+    for (int i = tid; i < nsl; i += ATT_NT) lm = fmaxf(lm, g_max[(size_t)h * n_slices + i]);
+    const float mx = block_max(lm, red);  // (its barriers also publish sc and etab)
+    for (int p = tid; p < P; p += ATT_NT) sc[p] = glibc_expf_t(sc[p] - mx, etab);
+    const int R = ring_slots;
+    const int ng = pos >> 3;  // full groups of 8 positions before pos
+    const int nchunks = (ng + CG - 1) / CG;
+    const int hw = (tid >> 6) - 1;
+    const bool stager = hw >= 0 && hw < NH;
+    const size_t last_group = (size_t)max(ng, 1) - 1;
+    auto stage = [&](int c) {  // chunk c into slot c % R: 1 KB wave load i = groups 2i, 2i+1
+      float4* slot = ring + (size_t)(c % R) * ATT_RING_GRANULES;
+#pragma unroll
+      for (int j = 0; j < LH; ++j) {
+        const int i = hw + NH * j;
+        const int lane = tid & 63;
+        const size_t grp = min((size_t)c * CG + 2 * i + (lane >> 5), last_group);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(vg + grp * HD + w * DW + (lane & 31)),
+                                         (__attribute__((address_space(3))) void*)(slot + i * 64), 16, 0, 0);
+      }
+    };
+    const bool onepass = P >= ATT_FOLD_MAX && P <= ATT_NT * ATT_ONEPASS_C;
+    const bool early = P <= ATT_NT * ATT_ONEPASS_C;
+    const bool seg = !early && att_seg_chunk<ATT_NT>(P) > 0 &&
+                     att_seg_bytes<ATT_NT>(P) <= (size_t)R * ATT_RING_GRANULES * 16;
+    __syncthreads();
+    if (stager && !seg) {
+      for (int c = 0; c < min(R - 1, nchunks); ++c) stage(c);
+    }
+    float inv;
+    if (onepass) {
+      inv = 1.0f / att_onepass_sum<ATT_NT>(sc, P, fs);
+    } else {
+      if (seg) {
+        const float ssum = att_seg_sum<ATT_NT>(sc, reinterpret_cast<uint32_t*>(ring), P);
+        if (tid == 0) s_inv = 1.0f / ssum;
+        if (stager) {
+          for (int c = 0; c < min(R - 1, nchunks); ++c) stage(c);
+        }
+      } else if (tid == 0) {
+        s_inv = 1.0f / fold_lds(sc, P);
+      }
+      __syncthreads();
+      inv = s_inv;
+    }
+    for (int p = tid; p < P; p += ATT_NT) sc[p] = sc[p] * inv;
+    for (int c = 0; c < nchunks; ++c) {
+      if (stager) wait_vmcnt(LH * (min(c + R - 2, nchunks - 1) - c));  // chunk c has landed
+      __syncthreads();  // chunk c visible; the slot of chunk c - 1 is free
+      if (stager && c + R - 1 < nchunks) stage(c + R - 1);
+      if (tid < DW) {
+        const uint4* slot = reinterpret_cast<const uint4*>(ring + (size_t)(c % R) * ATT_RING_GRANULES) + tid;
+        const float4* pr4 = reinterpret_cast<const float4*>(sc) + (size_t)c * CG * 2;
+        const int gn = min(CG, ng - c * CG);
+        auto granule = [&](const uint4& g, const float4& q0, const float4& q1, float(&pr)[8]) {
+          pr[0] = mul_f16_lo(q0.x, g.x);
+          pr[1] = mul_f16_hi(q0.y, g.x);
+          pr[2] = mul_f16_lo(q0.z, g.y);
+          pr[3] = mul_f16_hi(q0.w, g.y);
+          pr[4] = mul_f16_lo(q1.x, g.z);
+          pr[5] = mul_f16_hi(q1.y, g.z);
+          pr[6] = mul_f16_lo(q1.z, g.w);
+          pr[7] = mul_f16_hi(q1.w, g.w);
+        };
+        if (gn == CG) {
+          uint4 va[2], vb[2];
+          float4 pa[4], pb[4];
+          auto ld = [&](uint4(&v)[2], float4(&pq)[4], int j0) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              v[u] = slot[(j0 + u) * DW];
+              pq[2 * u] = pr4[2 * (j0 + u)];
+              pq[2 * u + 1] = pr4[2 * (j0 + u) + 1];
+            }
+          };
+          auto mac = [&](const uint4(&v)[2], const float4(&pq)[4]) {
+            float pr[2][8];
+            granule(v[0], pq[0], pq[1], pr[0]);
+            granule(v[1], pq[2], pq[3], pr[1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+              for (int e = 0; e < 8; ++e) acc += pr[u][e];
+          };
+          // blocks of 16 groups, each fully unrolled (the LDS reads run one batch ahead)
+          for (int j0 = 0; j0 < CG; j0 += 16) {
+            ld(va, pa, j0);
+#pragma unroll
+            for (int j = j0; j < j0 + 16; j += 4) {
+              ld(vb, pb, j + 2);
+              __builtin_amdgcn_sched_barrier(0);
+              mac(va, pa);
+              if (j + 4 < j0 + 16) ld(va, pa, j + 4);
+              __builtin_amdgcn_sched_barrier(0);
+              mac(vb, pb);
+            }
+          }
+        } else {
+          for (int j = 0; j < gn; ++j) {
+            float pr[8];
+            granule(slot[j * DW], pr4[2 * j], pr4[2 * j + 1], pr);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc += pr[e];
+          }
+        }
+      }
+    }
+    __syncthreads();  // the normalised probabilities past the ring (and with no chunks at all)
+    if (tid < DW) {
+      for (int p = ng * 8; p < P; ++p) acc += sc[p] * half_bits_to_float(vc[hbase + kv_v_index(HD, p, d)]);
+    }
+  }
+  if (tid < DW) {
+    att_out[(size_t)h * HD + d] = acc;
+    int8_t q;
+    const float dd = quantize_lane32(acc, &q);
+    xq[(size_t)h * HD + d] = q;
+    if (tid == 0) xs[((size_t)h * HD + d) >> 5] = dd;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Greedy argmax (inference.rs:5912-5925) over a vector: one workgroup (test entry point).
 __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int n, uint32_t* __restrict__ out) {
   __shared__ float bv_s[16];

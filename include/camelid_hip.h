@@ -202,6 +202,14 @@ int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const ui
                                  uint32_t layer, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
                                  uint32_t max_pos, const uint32_t* d_pos, float scale,
                                  float* att_out, int8_t* xq, float* xs, void* stream);
+/* The same attention split over workgroups for long contexts (the engine's path from
+ * CAMELID_HIP_ATT_SPLIT positions on, default 2048): scores by slices of positions, softmax and
+ * output sum by 32-dim slices; bit-identical to camelid_hip_attention_decode.  Allocates its
+ * score scratch and synchronizes the stream (test entry point). */
+int camelid_hip_attention_decode_split(const float* qrot, const uint16_t* kc, const uint16_t* vc,
+                                       uint32_t layer, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
+                                       uint32_t max_pos, const uint32_t* d_pos, float scale,
+                                       float* att_out, int8_t* xq, float* xs, void* stream);
 /* q8_gemm_batched (cuda_resident.rs:1494; CPU: the row dot of inference.rs:19871-19905 for
  * each token): y[t][n] = resid[t][n] + W[n].X[t] for T = tokens activation rows X [tokens][k]
  * (Q8_0 quants, f32 block scales [tokens][k/32]); output [tokens][rows]; the same

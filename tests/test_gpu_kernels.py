@@ -367,14 +367,15 @@ def test_attention_decode_bit_exact(native, orc, nh, nkv, hd, P):
     dq, dk, dv = _dev(q), _dev(kd), _dev(vd)
     dpos = _dev(np.array([P - 1], np.uint32))
     out, xq, xs = _buf(nh * hd * 4), _buf(nh * hd), _buf(nh * hd // 32 * 4)
-    _ok(native.camelid_hip_attention_decode(dq.ptr, dk.ptr, dv.ptr, layer, nh, nkv, hd, max_pos, dpos.ptr, scale,
-                                            out.ptr, xq.ptr, xs.ptr, None))
     want = orc.attention(q, orc.f16_to_f32(kb[layer]).ravel(), orc.f16_to_f32(vb[layer]).ravel(), nh, nkv, hd,
                          max_pos, P)
-    assert np.array_equal(_bits(out.download(np.float32, nh * hd)), _bits(want))
     ws, wq = orc.quantize_q8_0(want)
-    assert np.array_equal(_bits(xs.download(np.float32, nh * hd // 32)), _bits(ws))
-    assert np.array_equal(xq.download(np.int8, nh * hd), wq)
+    # one workgroup per head, and the long-context split over workgroups
+    for entry in (native.camelid_hip_attention_decode, native.camelid_hip_attention_decode_split):
+        _ok(entry(dq.ptr, dk.ptr, dv.ptr, layer, nh, nkv, hd, max_pos, dpos.ptr, scale, out.ptr, xq.ptr, xs.ptr, None))
+        assert np.array_equal(_bits(out.download(np.float32, nh * hd)), _bits(want))
+        assert np.array_equal(_bits(xs.download(np.float32, nh * hd // 32)), _bits(ws))
+        assert np.array_equal(xq.download(np.int8, nh * hd), wq)
 
 
 @pytest.mark.parametrize("nh,nkv,hd,pos0,T", [(24, 8, 128, 0, 70), (24, 8, 128, 500, 11), (32, 4, 64, 3, 130),

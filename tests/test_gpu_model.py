@@ -125,6 +125,29 @@ def test_gguf_file_model_matches_synthetic(tmp_path, kw, arch):
     g.close()
 
 
+@pytest.mark.parametrize("kw", [dict(), dict(qk_norm=True, split_half=True, rope_theta=1e6), KQUANT_TINY])
+def test_split_attention_crossing_matches_oracle(monkeypatch, kw):
+    """With the long-context split attention switched on from 24 positions, a generation that
+    crosses that position (host loop and graph-replayed device loop) stays bit-identical to
+    the CPU path: hidden states, logits, tokens and the KV cache."""
+    monkeypatch.setenv("CAMELID_HIP_ATT_SPLIT", "24")
+    cfg = tiny_config(prompt_len=20, **kw)
+    sess, orc, max_rel = _run_pair(cfg, 12)
+    assert max_rel == 0.0
+    n = sess.engine.filled()
+    for layer in range(cfg.n_layers):
+        kg, vg = sess.engine.read_kv_layer(layer, n)
+        ko, vo = orc.read_kv(layer, n)
+        assert np.array_equal(_bits(kg), _bits(ko)) and np.array_equal(_bits(vg), _bits(vo))
+    sess.close()
+    model = SyntheticModel.generate(cfg)
+    prompt = prompt_tokens(cfg)
+    host = ResidentSession(model, 48).generate(prompt, 16)
+    assert ResidentSession(model, 48, device_loop=True).generate(prompt, 16) == host
+    monkeypatch.setenv("CAMELID_HIP_ATT_SPLIT", "0")
+    assert ResidentSession(model, 48, device_loop=True).generate(prompt, 16) == host
+
+
 def test_device_loop_matches_host_loop():
     cfg = tiny_config(n_layers=3, prompt_len=10)
     model = SyntheticModel.generate(cfg)
