@@ -3,6 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config llama-3.2-3b] [--no-cpu-baseline]
     python bench.py --config qwen3-8b | mistral-7b-v0.3 | tinyllama-1.1b   (the other decode configs)
     python bench.py --sweep                                             (the Q8_0 kernel sweep)
+    python bench.py --sweep-kquant                                      (the K-quant prefill projections)
 
 Workload: seeded synthetic N(0, 0.02) weights quantized to
 Q8_0, a 512-token random prompt prefilled (n-1 tokens, as the reference seam does), then
@@ -121,6 +122,60 @@ def run_sweep(iters_min: int = 200) -> dict:
             "peaks": {"hbm_gbs": HBM_PEAK_GBS, "int8_tops": INT8_PEAK_TOPS}, "shapes": out}
 
 
+KQUANT_SWEEP_SHAPES = [(1, 4096, 4096), (1, 5120, 4096), (1, 24576, 4096), (1, 4096, 12288), (2, 1024, 4096)]
+
+
+def run_sweep_kquant(tokens: int = 512, iters: int = 20) -> dict:
+    """The K-quant prefill projections of configs[4] (Qwen3-8B Q4_K_M: q, q|k, gate|up, down as
+    Q4_K; v as Q6_K) over a 512-token chunk: k_gemm_q4k on the int8 matrix cores, or the
+    multi-token Q6_K GEMV, timed on the host over `iters` launches after one warm-up (each
+    launch is 0.1-3 ms, launch overhead is below 1 %).  int8 TOP/s = 2 N K T / time, against
+    the matrix-core peak."""
+    import ctypes as C
+    from camelid_amd import _native as N
+    from camelid_amd.engine import DeviceBuffer
+    from camelid_amd.model import synth_f32, synth_kquant
+    L = N.lib()
+    T = tokens
+    out = []
+    for quant, rows, k in KQUANT_SWEEP_SHAPES:
+        wire = synth_kquant(f"ksweep.{rows}x{k}.weight", 2, rows, k, quant)
+        nsb = k // 256
+        a = np.empty(rows * k // 2, np.uint8)
+        b = np.empty(rows * nsb * (16 if quant == 1 else 64), np.uint8)
+        sc = np.empty(max(rows * nsb * 16, 1), np.int8)
+        d = np.empty(max(rows * nsb, 1), np.uint16)
+        N.check(L.camelid_kquant_repack(quant, N.ptr(wire, C.c_uint8), rows, k, N.ptr(a, C.c_uint8),
+                                        N.ptr(b, C.c_uint8), N.ptr(sc, C.c_int8), N.ptr(d, C.c_uint16)))
+        da, db, dsc, dd = (DeviceBuffer.from_array(v) for v in (a, b, sc, d))
+        x = DeviceBuffer.from_array(synth_f32(f"ksweep.{rows}x{k}.x", 2, T * k, 1.0))
+        yd, yq, ybs = DeviceBuffer(T * nsb * 4), DeviceBuffer(T * k), DeviceBuffer(T * k // 32 * 4)
+        N.check(L.camelid_hip_quantize_q8_k(x.ptr, T * k, yd.ptr, yq.ptr, ybs.ptr, None))
+        y = DeviceBuffer(T * rows * 4)
+
+        def launch():
+            N.check(L.camelid_hip_kquant_gemm(quant, da.ptr, db.ptr, dsc.ptr, dd.ptr, rows, k, T, yd.ptr, yq.ptr,
+                                              y.ptr, rows, None, None))
+        launch()
+        N.check(L.camelid_hip_synchronize())
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            launch()
+        N.check(L.camelid_hip_synchronize())
+        us = (time.perf_counter() - t0) / iters * 1e6
+        ops = 2.0 * rows * k * T
+        name = "k_gemm_q4k" if quant == 1 else "k_gemv_q6k_multi"
+        out.append({"quant": "Q4_K" if quant == 1 else "Q6_K", "kernel": name, "shape": [rows, k], "tokens": T,
+                    "us": round(us, 1), "tops": round(ops / us / 1e6, 1),
+                    "mfma_frac": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4)})
+        log(f"kquant sweep {out[-1]['quant']} {rows}x{k} T={T}: {name} {us:.1f} us, {out[-1]['tops']} TOP/s")
+        del da, db, dsc, dd, x, yd, yq, ybs, y
+    return {"metric": "K-quant prefill projection int8 TOP/s over a 512-token chunk, 1 MI355X",
+            "config": {"workload": "configs[4] Qwen3-8B Q4_K_M projection shapes, weights N(0,0.02) seed 2, "
+                                   "activations N(0,1) quantized to Q8_K on device"},
+            "peaks": {"int8_tops": INT8_PEAK_TOPS}, "shapes": out}
+
+
 def probe_traffic() -> int:
     """The workload of the traffic counter passes: a 256 MiB device-to-device copy (the
     counters' scale reference), then three C3 decode steps launched without graphs on a
@@ -162,6 +217,8 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=6)
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--sweep", action="store_true", help="run the isolated Q8_0 GEMV/GEMM sweep (configs[1])")
+    ap.add_argument("--sweep-kquant", action="store_true",
+                    help="time the K-quant prefill projections (Q4_K GEMM, Q6_K multi-token GEMV) of configs[4]")
     ap.add_argument("--probe-traffic", action="store_true",
                     help="the workload of the rocprofv3 FETCH_SIZE/WRITE_SIZE passes (no JSON line)")
     ap.add_argument("--seed-kv", action="store_true",
@@ -184,6 +241,14 @@ def main() -> int:
         dev_name, n_cu = device_info()
         log(f"device {dev_name}, {n_cu} CUs; Q8_0 kernel sweep")
         res = run_sweep()
+        res["config"]["device"] = dev_name
+        print(json.dumps(res), flush=True)
+        return 0
+
+    if args.sweep_kquant:
+        dev_name, n_cu = device_info()
+        log(f"device {dev_name}, {n_cu} CUs; K-quant prefill projection sweep")
+        res = run_sweep_kquant()
         res["config"]["device"] = dev_name
         print(json.dumps(res), flush=True)
         return 0

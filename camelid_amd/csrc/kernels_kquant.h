@@ -572,7 +572,7 @@ __global__ __launch_bounds__(G4_NT, 2) void k_gemm_q4k(const uint8_t* __restrict
 // pairs are formed per use).  y[t * ldy + row] (+ resid, same stride).
 // Dynamic LDS: gemv_q6k_multi_lds_bytes(K, T).
 constexpr int Q6M_MAX = 8;
-constexpr int Q6M_RPW = 2;
+constexpr int Q6M_RPW = 1;
 constexpr int Q6M_ROWS = 4 * Q6M_RPW;
 __host__ __device__ inline size_t q6m_terms_offset(int K, int T) {
   return ((size_t)T * K + (size_t)T * (K / 256) * 4 + 15) & ~(size_t)15;
