@@ -127,8 +127,8 @@ KQUANT_SWEEP_SHAPES = [(1, 4096, 4096), (1, 5120, 4096), (1, 24576, 4096), (1, 4
 
 def run_sweep_kquant(tokens: int = 512, iters: int = 20) -> dict:
     """The K-quant prefill projections of configs[4] (Qwen3-8B Q4_K_M: q, q|k, gate|up, down as
-    Q4_K; v as Q6_K) over a 512-token chunk: k_gemm_q4k on the int8 matrix cores, or the
-    multi-token Q6_K GEMV, timed on the host over `iters` launches after one warm-up (each
+    Q4_K; v as Q6_K) over a 512-token chunk: k_gemm_q4k / k_gemm_q6k on the int8 matrix cores,
+    timed on the host over `iters` launches after one warm-up (each
     launch is 0.1-3 ms, launch overhead is below 1 %).  int8 TOP/s = 2 N K T / time, against
     the matrix-core peak."""
     import ctypes as C
@@ -164,7 +164,7 @@ def run_sweep_kquant(tokens: int = 512, iters: int = 20) -> dict:
         N.check(L.camelid_hip_synchronize())
         us = (time.perf_counter() - t0) / iters * 1e6
         ops = 2.0 * rows * k * T
-        name = "k_gemm_q4k" if quant == 1 else "k_gemv_q6k_multi"
+        name = "k_gemm_q4k" if quant == 1 else ("k_gemm_q6k" if T > 8 else "k_gemv_q6k_multi")
         out.append({"quant": "Q4_K" if quant == 1 else "Q6_K", "kernel": name, "shape": [rows, k], "tokens": T,
                     "us": round(us, 1), "tops": round(ops / us / 1e6, 1),
                     "mfma_frac": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4)})

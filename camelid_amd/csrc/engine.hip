@@ -899,13 +899,18 @@ uint32_t q6m_tokens(uint32_t K) {
 }
 
 // A K-quant projection over T tokens with Q8_K activation rows (kd [T][k/256], kq [T][k]):
-// y[t * ldy + row] (+ resid, same stride).  Q4_K: the matrix-core GEMM; Q6_K: the multi-token
-// GEMV over groups of up to Q6M_MAX tokens.
+// y[t * ldy + row] (+ resid, same stride).  Q4_K: the matrix-core GEMM; Q6_K: the matrix-core
+// GEMM for more than Q6M_MAX tokens, else the multi-token GEMV.
 void launch_kgemm(const KMat& m, uint32_t T, const float* kd, const int8_t* kq, float* y, uint32_t ldy,
                   const float* resid, hipStream_t s) {
   if (m.quant == CAMELID_Q4_K) {
     CM_LAUNCH(cm::k_gemm_q4k, dim3(cm::gemm_q4k_grid((int)m.rows, (int)T)), dim3(cm::G4_NT), 0, s, m.a, m.b,
               (int)m.rows, (int)m.k, kd, kq, (int)T, y, (int)ldy, resid);
+    return;
+  }
+  if (T > (uint32_t)cm::Q6M_MAX) {  // a chunk: the matrix-core GEMM
+    CM_LAUNCH(cm::k_gemm_q6k, dim3((m.rows + cm::G6_RN - 1) / cm::G6_RN, (T + cm::G6_RT - 1) / cm::G6_RT),
+              dim3(cm::G6_NT), 0, s, m.a, m.b, m.sc, m.d, (int)m.rows, (int)m.k, kd, kq, (int)T, y, (int)ldy, resid);
     return;
   }
   const uint32_t tt = q6m_tokens(m.k), nsb = m.k / 256;

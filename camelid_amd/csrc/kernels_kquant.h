@@ -691,4 +691,128 @@ __global__ __launch_bounds__(KQ_NT) void k_gemv_q6k_multi(const uint8_t* __restr
   }
 }
 
+// ---------------------------------------------------------------------------
+// Q6_K GEMM for prefill chunks: each (token, row) is k_gemv_q6k's result (the Q6_K decode dot
+// of inference.rs:19148-19195):  aux[l] = sum over positions p = l (mod 8) of
+// sc[p/16] * q8[p] * w[p] per superblock (exact integers), sums[l] += (f16(d) * y.d) * aux[l]
+// in superblock order, result = left fold of sums[0..8] from -0.0.
+// On the matrix cores, per 16-value scale group and token pair: one v_mfma_i32_16x16x32_i8
+// whose K holds the group's 16 positions (the other 16 are zero) and whose 16 columns are
+// (token, class) pairs -- column (t, l) carries q8[t][p] only at the group's two positions
+// of class l -- so each output is one (group, class) partial sum w[l] q[l] + w[8+l] q[8+l],
+// scaled by that group's sc on the vector ALUs and accumulated into aux.
+// Workgroup: 4 waves x 16 rows, 16 tokens; one superblock of the 64 rows' ql/qh/scales and
+// the 16 tokens' quants staged in LDS per step.  K % 256 == 0; y may alias resid.
+constexpr int G6_NT = 256;
+constexpr int G6_RN = 64;
+constexpr int G6_RT = 16;
+
+__global__ __launch_bounds__(G6_NT) void k_gemm_q6k(const uint8_t* __restrict__ ql, const uint8_t* __restrict__ qh,
+                                                    const int8_t* __restrict__ scl, const uint16_t* __restrict__ dw,
+                                                    int N, int K, const float* __restrict__ xd,
+                                                    const int8_t* __restrict__ xq, int T, float* y, int ldy,
+                                                    const float* resid) {
+  __shared__ __align__(16) uint8_t sql[G6_RN][128];
+  __shared__ __align__(16) uint8_t sqh[G6_RN][64];
+  __shared__ __align__(16) int8_t ssc[G6_RN][16];
+  __shared__ __align__(16) int8_t sxq[G6_RT][256];
+  __shared__ float sd[G6_RN], sxd[G6_RT];
+  const int NSB = K >> 8;
+  const int n_base = blockIdx.x * G6_RN, t_base = blockIdx.y * G6_RT;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int r = lane & 15, k8 = lane >> 4;  // operand row / column, 8-position slice of K
+  const int tl = r >> 3, cls = r & 7;       // this lane's output column: token of the pair, class
+  int aux[8][4];
+  float sums[8][4];
+#pragma unroll
+  for (int tp = 0; tp < 8; ++tp)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sums[tp][i] = 0.0f;
+  const uint32_t M4 = 0x0f0f0f0fu, M2 = 0x03030303u;
+  for (int s = 0; s < NSB; ++s) {
+    __syncthreads();  // the previous superblock's tile is consumed
+    {  // stage: 64 rows x (128 + 64 + 16) bytes, 16 tokens x 256 bytes, scales
+      const int row = tid >> 2, part = tid & 3;  // 4 threads per row
+      const size_t gr = (size_t)min(n_base + row, N - 1);
+      const uint4* qlp = reinterpret_cast<const uint4*>(ql + gr * (K >> 1) + (size_t)s * 128);
+      const uint4* qhp = reinterpret_cast<const uint4*>(qh + gr * (K >> 2) + (size_t)s * 64);
+      reinterpret_cast<uint4*>(sql[row])[part * 2] = qlp[part * 2];
+      reinterpret_cast<uint4*>(sql[row])[part * 2 + 1] = qlp[part * 2 + 1];
+      reinterpret_cast<uint4*>(sqh[row])[part] = qhp[part];
+      if (part == 0) {
+        reinterpret_cast<uint4*>(ssc[row])[0] = *reinterpret_cast<const uint4*>(scl + (gr * NSB + s) * 16);
+        sd[row] = half_bits_to_float(dw[gr * NSB + s]);
+      }
+      const int tok = tid >> 4, piece = tid & 15;  // 16 threads per token
+      const size_t gt = (size_t)min(t_base + tok, T - 1);
+      reinterpret_cast<uint4*>(sxq[tok])[piece] =
+          *reinterpret_cast<const uint4*>(xq + gt * K + (size_t)s * 256 + piece * 16);
+      if (piece == 0) sxd[tok] = xd[gt * NSB + s];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int tp = 0; tp < 8; ++tp)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) aux[tp][i] = 0;
+    const int arow = wave * 16 + r;
+#pragma unroll 2
+    for (int g = 0; g < 16; ++g) {
+      const int n = g >> 3, kk = (g & 7) >> 1, q0 = (g & 1) * 16;
+      // A: the row's weights at positions 16 g + 8 k8 .. +7 (k8 < 2), as int8 (q - 32)
+      long av = 0;
+      if (k8 < 2) {
+        const uint2 lq = *reinterpret_cast<const uint2*>(&sql[arow][n * 64 + (kk & 1) * 32 + q0 + 8 * k8]);
+        const uint2 hq = *reinterpret_cast<const uint2*>(&sqh[arow][n * 32 + q0 + 8 * k8]);
+        uint32_t w[2];
+        const uint32_t L[2] = {lq.x, lq.y}, H[2] = {hq.x, hq.y};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t lo = (kk < 2) ? (L[h] & M4) : ((L[h] >> 4) & M4);
+          const uint32_t v = lo | (((H[h] >> (2 * kk)) & M2) << 4);  // 0..63 per byte
+          w[h] = (v & 0x1f1f1f1fu) | ((~v & 0x20202020u) * 7u);      // v - 32 per byte
+        }
+        av = (long)(((uint64_t)w[1] << 32) | w[0]);
+      }
+      int scr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) scr[i] = ssc[wave * 16 + 4 * k8 + i][g];
+#pragma unroll
+      for (int tp = 0; tp < 8; ++tp) {
+        // B: column (token 2 tp + tl, class cls): its quant at position 16 g + 8 k8 + cls only
+        long bv = 0;
+        if (k8 < 2) {
+          const uint32_t q = (uint8_t)sxq[2 * tp + tl][16 * g + 8 * k8 + cls];
+          bv = (long)((uint64_t)q << (8 * cls));
+        }
+        const v4i_t c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) aux[tp][i] += scr[i] * c[i];
+      }
+    }
+#pragma unroll
+    for (int tp = 0; tp < 8; ++tp) {
+      const float ydv = sxd[2 * tp + tl];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float d = sd[wave * 16 + 4 * k8 + i] * ydv;
+        sums[tp][i] += d * (float)aux[tp][i];
+      }
+    }
+  }
+  // left fold of the 8 class chains (lanes 8 (lane / 8) .. +7), from -0.0
+#pragma unroll
+  for (int tp = 0; tp < 8; ++tp)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float acc = -0.0f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc += __shfl(sums[tp][i], (lane & ~7) + c);
+      const int row = n_base + wave * 16 + 4 * k8 + i, t = t_base + 2 * tp + tl;
+      if (cls == 0 && row < N && t < T) {
+        const size_t o = (size_t)t * ldy + row;
+        y[o] = resid ? resid[o] + acc : acc;
+      }
+    }
+}
+
 }  // namespace cm

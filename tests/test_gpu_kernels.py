@@ -505,9 +505,11 @@ def test_kquant_gemv_bit_exact(native, orc, quant, rows, k):
                                                  (1, 4096, 4096, 70, 4100), (1, 300, 12288, 3, 300),
                                                  (1, 2048, 4096, 130, 2048), (1, 36, 16384, 65, 40),
                                                  (2, 1024, 4096, 8, 1024), (2, 37, 512, 13, 50),
-                                                 (2, 300, 12288, 5, 300), (2, 2048, 4096, 20, 2048)])
+                                                 (2, 300, 12288, 5, 300), (2, 2048, 4096, 20, 2048),
+                                                 (2, 1024, 4096, 130, 1024), (2, 100, 12288, 33, 104)])
 def test_kquant_gemm_bit_exact(native, orc, quant, rows, k, T, ldy):
-    """Multi-token K-quant projection (Q4_K on the matrix cores, Q6_K multi-token GEMV): every
+    """Multi-token K-quant projection (Q4_K on the matrix cores; Q6_K on the matrix cores above 8
+    tokens, by the multi-token GEMV up to 8): every
     (token, row) equals the single-token GEMV on that token bit for bit (and the CPU dot on
     the first and last token), with a strided, residual-carrying output; ragged row and token
     tiles, K up to 16384."""
