@@ -267,13 +267,17 @@ __global__ __launch_bounds__(64) void k_argmax_rows_finish(const float* __restri
 constexpr int GMT_MAX = 8;
 constexpr int GMT_RPW = 2;
 constexpr int GMT_ROWS = 4 * GMT_RPW;
-// LDS: the activations [T][K] i8, their scales [T][K/32] f32 rounded up to whole 1 KB wave
-// loads, the terms [GMT_ROWS][T][stride] f32
+// LDS: the activations [T][K] i8 and their scales [T][K/32] f32, each rounded up to whole
+// 1 KB wave loads (a direct load writes all 64 lanes' 16 bytes, the last one past the data),
+// then the terms [GMT_ROWS][T][stride] f32
+__host__ __device__ inline size_t gemv_multi_xq_bytes(int K, int T) {
+  return (((size_t)T * K + 1023) / 1024) * 1024;
+}
 __host__ __device__ inline size_t gemv_multi_xs_bytes(int K, int T) {
   return (((size_t)T * (K / 32) * 4 + 1023) / 1024) * 1024;
 }
 __host__ __device__ inline size_t gemv_multi_lds_bytes(int K, int T) {
-  return (size_t)T * K + gemv_multi_xs_bytes(K, T) + (size_t)GMT_ROWS * T * gemv_term_stride(K / 32) * 4;
+  return gemv_multi_xq_bytes(K, T) + gemv_multi_xs_bytes(K, T) + (size_t)GMT_ROWS * T * gemv_term_stride(K / 32) * 4;
 }
 
 template <int K>
@@ -285,12 +289,12 @@ __global__ __launch_bounds__(256) void k_gemv_multi(const int8_t* __restrict__ w
   static_assert(NB % 4 == 0, "compile-time GEMV widths are multiples of 128");
   extern __shared__ __align__(16) unsigned char gmt_lds[];
   int8_t* xl = reinterpret_cast<int8_t*>(gmt_lds);                    // [T][K]
-  float* xsl = reinterpret_cast<float*>(gmt_lds + (size_t)T * K);     // [T][NB]
-  float* t = reinterpret_cast<float*>(gmt_lds + (size_t)T * K + gemv_multi_xs_bytes(K, T));  // [GMT_ROWS][T][STRIDE]
+  float* xsl = reinterpret_cast<float*>(gmt_lds + gemv_multi_xq_bytes(K, T));  // [T][NB]
+  float* t = reinterpret_cast<float*>(gmt_lds + gemv_multi_xq_bytes(K, T) + gemv_multi_xs_bytes(K, T));  // [GMT_ROWS][T][STRIDE]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int row0 = blockIdx.x * GMT_ROWS;
-  // the activations and their scales go to LDS by direct loads (1 KB per wave load; the
-  // scales' last load may overrun into the rounded-up pad, re-reading the last piece)
+  // the activations and their scales go to LDS by direct loads (1 KB per wave load; a last
+  // load may overrun into its region's rounded-up pad, re-reading the last piece)
   {
     const uint4* sx = reinterpret_cast<const uint4*>(xq);
     const uint4* ss = reinterpret_cast<const uint4*>(xs);
