@@ -265,7 +265,7 @@ __global__ __launch_bounds__(64) void k_argmax_rows_finish(const float* __restri
 // would leave most CUs idle at this size).  4 waves x GMT_RPW rows per workgroup.
 // Dynamic LDS: gemv_multi_lds_bytes(K, T).
 constexpr int GMT_MAX = 8;
-constexpr int GMT_RPW = 2;
+constexpr int GMT_RPW = 1;
 constexpr int GMT_ROWS = 4 * GMT_RPW;
 // LDS: the activations [T][K] i8 and their scales [T][K/32] f32, each rounded up to whole
 // 1 KB wave loads (a direct load writes all 64 lanes' 16 bytes, the last one past the data),
