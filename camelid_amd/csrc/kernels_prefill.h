@@ -269,7 +269,7 @@ constexpr int GMT_RPW = 1;
 constexpr int GMT_ROWS = 4 * GMT_RPW;
 // LDS: the activations [T][K] i8 and their scales [T][K/32] f32, each rounded up to whole
 // 1 KB wave loads (a direct load writes all 64 lanes' 16 bytes, the last one past the data),
-// then the terms [GMT_ROWS][T][stride] f32
+// then per wave the terms of one 32-block slice [GMT_RPW][T][32] f32
 __host__ __device__ inline size_t gemv_multi_xq_bytes(int K, int T) {
   return (((size_t)T * K + 1023) / 1024) * 1024;
 }
@@ -277,7 +277,7 @@ __host__ __device__ inline size_t gemv_multi_xs_bytes(int K, int T) {
   return (((size_t)T * (K / 32) * 4 + 1023) / 1024) * 1024;
 }
 __host__ __device__ inline size_t gemv_multi_lds_bytes(int K, int T) {
-  return gemv_multi_xq_bytes(K, T) + gemv_multi_xs_bytes(K, T) + (size_t)GMT_ROWS * T * gemv_term_stride(K / 32) * 4;
+  return gemv_multi_xq_bytes(K, T) + gemv_multi_xs_bytes(K, T) + (size_t)GMT_ROWS * T * 32 * 4;
 }
 
 template <int K>
@@ -285,12 +285,14 @@ __global__ __launch_bounds__(256) void k_gemv_multi(const int8_t* __restrict__ w
                                                     int rows, const int8_t* __restrict__ xq,
                                                     const float* __restrict__ xs, int T, float* y,
                                                     const float* resid) {
-  constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64, STRIDE = gemv_term_stride(NB);
+  constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64;
   static_assert(NB % 4 == 0, "compile-time GEMV widths are multiples of 128");
   extern __shared__ __align__(16) unsigned char gmt_lds[];
   int8_t* xl = reinterpret_cast<int8_t*>(gmt_lds);                    // [T][K]
   float* xsl = reinterpret_cast<float*>(gmt_lds + gemv_multi_xq_bytes(K, T));  // [T][NB]
-  float* t = reinterpret_cast<float*>(gmt_lds + gemv_multi_xq_bytes(K, T) + gemv_multi_xs_bytes(K, T));  // [GMT_ROWS][T][STRIDE]
+  // this wave's slice terms [GMT_RPW][T][32]
+  float* tw = reinterpret_cast<float*>(gmt_lds + gemv_multi_xq_bytes(K, T) + gemv_multi_xs_bytes(K, T)) +
+              (size_t)(threadIdx.x >> 6) * GMT_RPW * T * 32;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int row0 = blockIdx.x * GMT_ROWS;
   // the activations and their scales go to LDS by direct loads (1 KB per wave load; a last
@@ -324,28 +326,40 @@ __global__ __launch_bounds__(256) void k_gemv_multi(const int8_t* __restrict__ w
   }
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0): this wave's direct loads have landed
   __syncthreads();
+  // slice i = blocks 32 i .. 32 i + 31 of every (row, token): lane pairs form the block terms
+  // into LDS, then lane f (< GMT_RPW * T) continues the in-order fold of (row f / T, token
+  // f % T) over them (wave-level ordering only: the slice buffer is this wave's)
+  auto wave_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  float acc = 0.0f;
 #pragma unroll
-  for (int k = 0; k < GMT_RPW; ++k) {
-    const int lr = wave * GMT_RPW + k;
+  for (int i = 0; i < IT; ++i) {
+    const int c = lane + 64 * i;
+    const int cc = min(c, CPR - 1);
 #pragma unroll
-    for (int i = 0; i < IT; ++i) {
-      const int c = lane + 64 * i;
-      const int cc = min(c, CPR - 1);
+    for (int k = 0; k < GMT_RPW; ++k) {
       const float dw = half_bits_to_float(dv[k][i]);
       for (int tk = 0; tk < T; ++tk) {
         int sacc = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl + (size_t)tk * K)[cc], 0);
         sacc += dpp_xor1(sacc);
         if ((lane & 1) == 0 && c < CPR)
-          t[((size_t)lr * T + tk) * STRIDE + (c >> 1)] = ((float)sacc * dw) * xsl[tk * NB + (c >> 1)];
+          tw[(k * T + tk) * 32 + (lane >> 1)] = ((float)sacc * dw) * xsl[tk * NB + (c >> 1)];
       }
     }
+    wave_sync();
+    if (lane < GMT_RPW * T) {
+      const int nb = min(32, NB - 32 * i);
+      acc = fold_lds(tw + (size_t)lane * 32, nb, acc);
+    }
+    wave_sync();
   }
-  __syncthreads();
-  if (tid < GMT_ROWS * T) {
-    const int lr = tid / T, tk = tid - lr * T;
+  if (lane < GMT_RPW * T) {
+    const int lr = wave * GMT_RPW + lane / T, tk = lane - (lane / T) * T;
     const int row = row0 + lr;
     if (row < rows) {
-      const float acc = fold_lds(t + (size_t)tid * STRIDE, NB);
       const size_t o = (size_t)tk * rows + row;
       y[o] = resid ? resid[o] + acc : acc;
     }
