@@ -903,6 +903,26 @@ uint32_t q6m_tokens(uint32_t K) {
 // GEMM for more than Q6M_MAX tokens, else the multi-token GEMV.
 void launch_kgemm(const KMat& m, uint32_t T, const float* kd, const int8_t* kq, float* y, uint32_t ldy,
                   const float* resid, hipStream_t s) {
+  if (m.quant == CAMELID_Q4_K && T <= (uint32_t)cm::Q4M_MAX) {  // a few tokens (verify)
+    uint32_t tt = T;
+    while (tt > 1 && cm::gemv_q4k_multi_lds_bytes((int)m.k, (int)tt) > 65536) --tt;
+    const uint32_t nsb = m.k / 256, it = (m.k / 32 + 63) / 64;
+    for (uint32_t t0 = 0; t0 < T; t0 += tt) {
+      const uint32_t n = std::min(tt, T - t0);
+      const size_t lds = cm::gemv_q4k_multi_lds_bytes((int)m.k, (int)n);
+      switch (it) {
+#define CM_Q4M(IT)                                                                                                \
+  case IT:                                                                                                        \
+    CM_LAUNCH(cm::k_gemv_q4k_multi<IT>, dim3((m.rows + 3) / 4), dim3(cm::KQ_NT), lds, s, m.a, m.b, (int)m.rows,   \
+              (int)m.k, kd + (size_t)t0 * nsb, kq + (size_t)t0 * m.k, (int)n,                                     \
+              y + (size_t)t0 * ldy, (int)ldy, resid ? resid + (size_t)t0 * ldy : nullptr);                        \
+    break;
+        CM_Q4M(1) CM_Q4M(2) CM_Q4M(3) CM_Q4M(4) CM_Q4M(5) CM_Q4M(6) CM_Q4M(7) CM_Q4M(8)
+#undef CM_Q4M
+      }
+    }
+    return;
+  }
   if (m.quant == CAMELID_Q4_K) {
     CM_LAUNCH(cm::k_gemm_q4k, dim3(cm::gemm_q4k_grid((int)m.rows, (int)T)), dim3(cm::G4_NT), 0, s, m.a, m.b,
               (int)m.rows, (int)m.k, kd, kq, (int)T, y, (int)ldy, resid);

@@ -815,4 +815,118 @@ __global__ __launch_bounds__(G6_NT) void k_gemm_q6k(const uint8_t* __restrict__ 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K GEMV over T tokens at once (speculative verify): each token's result is k_gemv_q4k's,
+// in the same order; a lane's weight pieces and their headers are loaded once and dotted with
+// every token's Q8_K activation, staged in LDS ([T][K] quants, [T][K/256] scales, and the
+// [T][K/32] quant sums formed there).  4 rows per workgroup; y[t * ldy + row] (+ resid, same stride).
+// Dynamic LDS: gemv_q4k_multi_lds_bytes(K, T).
+constexpr int Q4M_MAX = 8;
+__host__ __device__ inline size_t q4m_terms_offset(int K, int T) {
+  return ((size_t)T * (K + (K / 256) * 4 + (K / 32) * 4) + 15) & ~(size_t)15;
+}
+__host__ __device__ inline size_t gemv_q4k_multi_lds_bytes(int K, int T) {
+  return q4m_terms_offset(K, T) + (size_t)4 * T * (K / 256) * 16;
+}
+
+template <int IT>
+__global__ __launch_bounds__(KQ_NT) void k_gemv_q4k_multi(const uint8_t* __restrict__ nib,
+                                                          const uint8_t* __restrict__ hdr, int rows, int K,
+                                                          const float* __restrict__ yd,
+                                                          const int8_t* __restrict__ yq, int T, float* y, int ldy,
+                                                          const float* resid) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int NSB = K >> 8, NC = K >> 5;
+  int8_t* xq = reinterpret_cast<int8_t*>(smem);                                          // [T][K]
+  float* xd = reinterpret_cast<float*>(smem + (size_t)T * K);                           // [T][NSB]
+  int* xbs = reinterpret_cast<int*>(smem + (size_t)T * K + (size_t)T * NSB * 4);        // [T][NC]
+  float4* terms = reinterpret_cast<float4*>(smem + q4m_terms_offset(K, T));             // [row][t][s]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int row = min((int)blockIdx.x * 4 + wave, rows - 1);
+  uint4 wv[IT], hv[IT];
+  {
+    const uint4* np = reinterpret_cast<const uint4*>(nib + (size_t)row * (K >> 1));
+    const uint4* hp = reinterpret_cast<const uint4*>(hdr + (size_t)row * NSB * 16);
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int cc = min(lane + 64 * i, NC - 1);
+      wv[i] = np[cc];
+      hv[i] = hp[cc >> 3];
+    }
+  }
+  for (int c = tid; c < (T * K) >> 4; c += KQ_NT) reinterpret_cast<int4*>(xq)[c] = reinterpret_cast<const int4*>(yq)[c];
+  for (int i = tid; i < T * NSB; i += KQ_NT) xd[i] = yd[i];
+  __syncthreads();
+  for (int i = tid; i < T * NC; i += KQ_NT) {  // the per-32 quant sums (exact), from LDS
+    const int4* q = reinterpret_cast<const int4*>(xq + (size_t)i * 32);
+    int sum = 0;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int4 v = q[u];
+      sum = __builtin_amdgcn_sdot4(v.x, 0x01010101, sum, false);
+      sum = __builtin_amdgcn_sdot4(v.y, 0x01010101, sum, false);
+      sum = __builtin_amdgcn_sdot4(v.z, 0x01010101, sum, false);
+      sum = __builtin_amdgcn_sdot4(v.w, 0x01010101, sum, false);
+    }
+    xbs[i] = sum;
+  }
+  __syncthreads();
+  const uint32_t K1 = 0x3f3f3f3fu, K2 = 0x0f0f0f0fu, K3 = 0x03030303u;
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int c = lane + 64 * i;
+    const bool valid = c < NC;  // uniform per 8-lane superblock group (NC % 8 == 0)
+    const int cc = min(c, NC - 1);
+    const uint4 w = wv[i], hd = hv[i];
+    const int s = cc >> 3, j = cc & 7, c4 = j >> 1, h = j & 1;
+    const uint32_t scw = (c4 < 2) ? (hd.y & K1) : ((hd.w & K2) | (((hd.y >> 6) & K3) << 4));
+    const uint32_t mnw = (j < 4) ? (hd.z & K1) : (((hd.w >> 4) & K2) | (((hd.z >> 6) & K3) << 4));
+    const int sc_lo = (scw >> (8 * ((2 * c4) & 3))) & 0xff;
+    const int sc_hi = (scw >> (8 * ((2 * c4 + 1) & 3))) & 0xff;
+    const int mn = (mnw >> (8 * (j & 3))) & 0xff;
+    const int base = (s << 8) + 64 * c4 + 16 * h;
+    const int wl[4] = {(int)(w.x & K2), (int)(w.y & K2), (int)(w.z & K2), (int)(w.w & K2)};
+    const int wh[4] = {(int)((w.x >> 4) & K2), (int)((w.y >> 4) & K2), (int)((w.z >> 4) & K2),
+                       (int)((w.w >> 4) & K2)};
+    const float dw = half_bits_to_float((uint16_t)(hd.x & 0xffffu));
+    const float dmw = half_bits_to_float((uint16_t)(hd.x >> 16));
+    for (int t = 0; t < T; ++t) {
+      const int8_t* xt = xq + (size_t)t * K;
+      const int4 qa = *reinterpret_cast<const int4*>(xt + base);
+      const int4 qb = *reinterpret_cast<const int4*>(xt + base + 32);
+      int lo = 0, hi = 0;
+      lo = __builtin_amdgcn_sdot4(wl[0], qa.x, lo, false);
+      lo = __builtin_amdgcn_sdot4(wl[1], qa.y, lo, false);
+      lo = __builtin_amdgcn_sdot4(wl[2], qa.z, lo, false);
+      lo = __builtin_amdgcn_sdot4(wl[3], qa.w, lo, false);
+      hi = __builtin_amdgcn_sdot4(wh[0], qb.x, hi, false);
+      hi = __builtin_amdgcn_sdot4(wh[1], qb.y, hi, false);
+      hi = __builtin_amdgcn_sdot4(wh[2], qb.z, hi, false);
+      hi = __builtin_amdgcn_sdot4(wh[3], qb.w, hi, false);
+      const int sumi = group_sum<8>(lo * sc_lo + hi * sc_hi);
+      const int prod = group_sum<8>(xbs[t * NC + s * 8 + j] * mn);
+      if (valid && j == 0) {
+        const float ydv = xd[t * NSB + s];
+        terms[((size_t)wave * T + t) * NSB + s] = make_float4(-(ydv * dmw), (float)prod, ydv * dw, (float)sumi);
+      }
+    }
+  }
+  __syncthreads();
+  for (int f = tid; f < 4 * T; f += KQ_NT) {  // one lane per (row, token): the in-order fold
+    const int rl = f / T, t = f - rl * T;
+    const int r = blockIdx.x * 4 + rl;
+    if (r < rows) {
+      const float4* tp = terms + (size_t)f * NSB;
+      float acc = 0.0f;
+      for (int s = 0; s < NSB; ++s) {
+        const float4 v = tp[s];
+        acc = fmaf(v.x, v.y, acc);
+        acc = fmaf(v.z, v.w, acc);
+      }
+      const size_t o = (size_t)t * ldy + r;
+      y[o] = resid ? resid[o] + acc : acc;
+    }
+  }
+}
+
 }  // namespace cm
