@@ -117,6 +117,7 @@ struct camelid_hip_engine {
   bool read_ahead = true;  // spare workgroups of the norm kernels read ahead the next weights
   bool gu_fused = false;   // gate/up rows interleaved by 32, SwiGLU fused into their GEMV
   bool norm_fused = true;  // RMSNorms computed inside the qkv and gate/up GEMVs (Q8_0 layers)
+  bool qkv_merged = true;  // Q4_K q|k and Q6_K v projections in one launch (k_gemv_qk4_v6)
   float *h = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr;
   float *logits = nullptr, *hidden_cap = nullptr, *xs = nullptr;
   float *cos_cur = nullptr, *sin_cur = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
@@ -497,10 +498,17 @@ uint32_t launch_gemv_argmax(const Q8Mat& m, const int8_t* xq, const float* xs, f
 // Attention launch for the supported head widths.
 bool attention_hd_supported(uint32_t hd) { return hd == 64 || hd == 128 || hd == 256; }
 
+constexpr uint32_t PREFETCH_WGS = 256;  // spare workgroups added to a kernel that reads ahead
+// Largest matrix worth reading ahead: beyond a fraction of the 256 MB last-level cache the
+// lines are evicted before their GEMV reads them and the read-ahead only adds HBM traffic and
+// launch time (measured: reading the 510 MB Q6_K lm_head ahead made the final RMSNorm launch
+// 77 us instead of ~10 us, with no gain in the lm_head GEMV).
+constexpr size_t PREFETCH_MAX_BYTES = (size_t)128 << 20;
+
 // Read-ahead descriptor of a Q8R matrix (quants and scales, in 128-byte lines).
 cm::Prefetch prefetch_of(const Q8Mat* m) {
   cm::Prefetch pf{nullptr, 0, nullptr, 0};
-  if (m && m->q) {
+  if (m && m->q && (size_t)m->rows * m->k * 34 / 32 <= PREFETCH_MAX_BYTES) {
     pf.a = reinterpret_cast<const uint32_t*>(m->q);
     pf.a_lines = (size_t)m->rows * m->k / 128;
     pf.b = reinterpret_cast<const uint32_t*>(m->d);
@@ -510,7 +518,7 @@ cm::Prefetch prefetch_of(const Q8Mat* m) {
 }
 cm::Prefetch prefetch_of(const KMat* m) {
   cm::Prefetch pf{nullptr, 0, nullptr, 0};
-  if (m && m->a) {
+  if (m && m->a && (size_t)m->rows * (m->k / 256) * kq_block_bytes(m->quant) <= PREFETCH_MAX_BYTES) {
     pf.a = reinterpret_cast<const uint32_t*>(m->a);
     pf.a_lines = (size_t)m->rows * m->k / 2 / 128;
     pf.b = reinterpret_cast<const uint32_t*>(m->b);
@@ -518,7 +526,6 @@ cm::Prefetch prefetch_of(const KMat* m) {
   }
   return pf;
 }
-constexpr uint32_t PREFETCH_WGS = 256;  // spare workgroups added to a kernel that reads ahead
 
 size_t attn_sc_bytes(uint32_t kvs) { return (((size_t)kvs + 3) & ~(size_t)3) * 4; }
 int attn_ring_slots(uint32_t kvs);
@@ -739,9 +746,29 @@ void run_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cos_base,
                          k8 ? e->kq : nullptr, k8 ? e->kbs : nullptr);
   };
   norm(L.attn_norm, is_k(0) || is_k(1) || is_k(2), ahead(L.p[0]));
-  proj(e, L.p[0], e->qkv, nullptr);  // q, or q|k stacked
-  if (!L.qk_stacked) proj(e, L.p[1], e->qkv + nq, nullptr);
-  proj(e, L.p[2], e->qkv + nq + nkv, nullptr);
+  const KMat& qk = L.p[0].kq;
+  const KMat& v6 = L.p[2].kq;
+  if (e->qkv_merged && L.qk_stacked && L.p[0].quant == CAMELID_Q4_K && L.p[2].quant == CAMELID_Q6_K &&
+      qk.rows < 16384 && v6.rows < 16384 && qk.k == v6.k && qk.k / 32 <= 8 * 64) {
+    // q|k and v in one launch (both from the Q8_K activation the norm wrote)
+    ProfScope ps(e, P_GEMV, kq_bytes(qk, false) + kq_bytes(v6, false) - qk.k * (1.0 + 4.0 / 256 + 4.0 / 32));
+    const uint32_t g4 = (qk.rows + 3) / 4, g6 = (v6.rows + 3) / 4;
+    const size_t lds = std::max(cm::kq4_lds_bytes((int)qk.k, 4), cm::kq6_lds_bytes((int)qk.k, 4));
+    const int it = (int)(qk.k / 32 + 63) / 64;
+    switch (it) {
+#define CM_QKV(IT)                                                                                            \
+  case IT:                                                                                                    \
+    CM_LAUNCH(cm::k_gemv_qk4_v6<IT>, dim3(g4 + g6), dim3(cm::KQ_NT), lds, s, qk.a, qk.b, (int)qk.rows, e->qkv, \
+              (int)g4, v6.a, v6.b, v6.sc, v6.d, (int)v6.rows, e->qkv + nq + nkv, (int)qk.k, e->kd, e->kq, e->kbs); \
+    break;
+      CM_QKV(1) CM_QKV(2) CM_QKV(3) CM_QKV(4) CM_QKV(5) CM_QKV(6) CM_QKV(7) CM_QKV(8)
+#undef CM_QKV
+    }
+  } else {
+    proj(e, L.p[0], e->qkv, nullptr);  // q, or q|k stacked
+    if (!L.qk_stacked) proj(e, L.p[1], e->qkv + nq, nullptr);
+    proj(e, L.p[2], e->qkv + nq + nkv, nullptr);
+  }
   {
     ProfScope ps(e, P_ATTN, (nq + 2.0 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0));
     decode_attention(e, l, cos_base, sin_base, rope_stride, scale, ahead(L.p[3]));
@@ -1155,6 +1182,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   e->gu_fused = cm::gu_fused_k((int)d.hidden);
   if (const char* f = std::getenv("CAMELID_HIP_FUSED_GU")) e->gu_fused = e->gu_fused && std::atoi(f) != 0;
   if (const char* f = std::getenv("CAMELID_HIP_FUSED_NORM")) e->norm_fused = std::atoi(f) != 0;
+  if (const char* f = std::getenv("CAMELID_HIP_QKV_MERGED")) e->qkv_merged = std::atoi(f) != 0;
   e->att_slots = attn_ring_slots(e->kvs);
   if (const char* f = std::getenv("CAMELID_HIP_ATT_SPLIT")) e->att_split_min = (uint32_t)std::strtoul(f, nullptr, 10);
   const size_t nq = (size_t)d.n_heads * d.head_dim, nkv = (size_t)d.n_kv_heads * d.head_dim;

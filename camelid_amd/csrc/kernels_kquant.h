@@ -89,7 +89,7 @@ __host__ __device__ inline size_t kq4_lds_bytes(int K, int R) {
 }
 
 template <int IT, int RPW>
-__global__ __launch_bounds__(KQ_NT) void k_gemv_q4k(const uint8_t* __restrict__ nib, const uint8_t* __restrict__ hdr,
+__device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __restrict__ nib, const uint8_t* __restrict__ hdr,
                                                     int rows, int K, const float* __restrict__ yd,
                                                     const int8_t* __restrict__ yq, const int32_t* __restrict__ ybs,
                                                     float* y, const float* resid, float* __restrict__ part_v,
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(KQ_NT) void k_gemv_q4k(const uint8_t* __restrict__ 
   int* xbs = reinterpret_cast<int*>(smem + K + NSB * 4);
   float4* terms = reinterpret_cast<float4*>(smem + kq4_terms_offset(K));
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int row0 = blockIdx.x * R;
+  const int row0 = bid * R;
   // every weight and header load of this wave first (pieces lane + 64 i of each row; past
   // NC clamped, their results never stored)
   uint4 wv[RPW][IT], hv[RPW][IT];
@@ -185,11 +185,20 @@ __global__ __launch_bounds__(KQ_NT) void k_gemv_q4k(const uint8_t* __restrict__ 
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) argmax_pair(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
       if (tid == 0) {
-        part_v[blockIdx.x] = bv;
-        part_i[blockIdx.x] = bi;
+        part_v[bid] = bv;
+        part_i[bid] = bi;
       }
     }
   }
+}
+
+template <int IT, int RPW>
+__global__ __launch_bounds__(KQ_NT) void k_gemv_q4k(const uint8_t* __restrict__ nib, const uint8_t* __restrict__ hdr,
+                                                    int rows, int K, const float* __restrict__ yd,
+                                                    const int8_t* __restrict__ yq, const int32_t* __restrict__ ybs,
+                                                    float* y, const float* resid, float* __restrict__ part_v,
+                                                    uint32_t* __restrict__ part_i, const float* __restrict__ xf) {
+  gemv_q4k_body<IT, RPW>((int)blockIdx.x, nib, hdr, rows, K, yd, yq, ybs, y, resid, part_v, part_i, xf);
 }
 
 // ---------------------------------------------------------------------------
@@ -215,7 +224,7 @@ __host__ __device__ inline size_t kq6_lds_bytes(int K, int R) {
 }
 
 template <int RPW>
-__global__ __launch_bounds__(KQ_NT) void k_gemv_q6k(const uint8_t* __restrict__ ql, const uint8_t* __restrict__ qh,
+__device__ __forceinline__ void gemv_q6k_body(const int bid, const uint8_t* __restrict__ ql, const uint8_t* __restrict__ qh,
                                                     const int8_t* __restrict__ scl, const uint16_t* __restrict__ dw,
                                                     int rows, int K, const float* __restrict__ yd,
                                                     const int8_t* __restrict__ yq, float* y, const float* resid,
@@ -227,7 +236,7 @@ __global__ __launch_bounds__(KQ_NT) void k_gemv_q6k(const uint8_t* __restrict__ 
   float* xd = reinterpret_cast<float*>(smem + NSB * 512);
   float* terms = reinterpret_cast<float*>(smem + kq6_terms_offset(K));  // [row][s][l]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int row0 = blockIdx.x * R;
+  const int row0 = bid * R;
   // activation pairs: entry (s, j, l) = bytes (q[16j+l], q[16j+8+l], q[16j+l], q[16j+8+l])
   for (int e = tid; e < NSB * 128; e += KQ_NT) {
     const int l = e & 7, g = e >> 3;  // g = s * 16 + j
@@ -315,11 +324,39 @@ __global__ __launch_bounds__(KQ_NT) void k_gemv_q6k(const uint8_t* __restrict__ 
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) argmax_pair(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
       if (tid == 0) {
-        part_v[blockIdx.x] = bv;
-        part_i[blockIdx.x] = bi;
+        part_v[bid] = bv;
+        part_i[bid] = bi;
       }
     }
   }
+}
+
+template <int RPW>
+__global__ __launch_bounds__(KQ_NT) void k_gemv_q6k(const uint8_t* __restrict__ ql, const uint8_t* __restrict__ qh,
+                                                    const int8_t* __restrict__ scl, const uint16_t* __restrict__ dw,
+                                                    int rows, int K, const float* __restrict__ yd,
+                                                    const int8_t* __restrict__ yq, float* y, const float* resid,
+                                                    float* __restrict__ part_v, uint32_t* __restrict__ part_i) {
+  gemv_q6k_body<RPW>((int)blockIdx.x, ql, qh, scl, dw, rows, K, yd, yq, y, resid, part_v, part_i);
+}
+
+// ---------------------------------------------------------------------------
+// The q|k (Q4_K, stacked) and v (Q6_K) projections of a Q4_K_M layer in one launch: both
+// read the same Q8_K activation, so workgroups [0, g4) run the Q4_K GEMV over the q|k rows
+// and workgroups [g4, gridDim.x) the Q6_K GEMV over the v rows (one row per wave each, no
+// residual).  Each output row is computed exactly as by k_gemv_q4k / k_gemv_q6k; the launch
+// saves the v projection's own dispatch.  Dynamic LDS: the larger of the two kernels' needs.
+template <int IT>
+__global__ __launch_bounds__(KQ_NT) void k_gemv_qk4_v6(const uint8_t* __restrict__ nib, const uint8_t* __restrict__ hdr,
+                                                       int rows4, float* y4, int g4, const uint8_t* __restrict__ ql,
+                                                       const uint8_t* __restrict__ qh, const int8_t* __restrict__ scl,
+                                                       const uint16_t* __restrict__ dw, int rows6, float* y6, int K,
+                                                       const float* __restrict__ yd, const int8_t* __restrict__ yq,
+                                                       const int32_t* __restrict__ ybs) {
+  if ((int)blockIdx.x < g4)
+    gemv_q4k_body<IT, 1>((int)blockIdx.x, nib, hdr, rows4, K, yd, yq, ybs, y4, nullptr, nullptr, nullptr, nullptr);
+  else
+    gemv_q6k_body<1>((int)blockIdx.x - g4, ql, qh, scl, dw, rows6, K, yd, yq, y6, nullptr, nullptr, nullptr);
 }
 
 // ---------------------------------------------------------------------------
