@@ -67,6 +67,7 @@ class GgufRope(C.Structure):
 SIGNATURES: dict[str, tuple] = {
     "camelid_hip_engine_new": (C.c_int, [C.POINTER(Dims), C.POINTER(vp)]),
     "camelid_hip_engine_free": (None, [vp]),
+    "camelid_hip_check_model": (C.c_int, [C.POINTER(Dims), u8p, C.c_uint8]),
     "camelid_hip_last_error": (C.c_char_p, [vp]),
     "camelid_hip_set_layer": (C.c_int, [vp, C.c_uint32, C.POINTER(u8p), C.POINTER(C.c_size_t), u8p, C.c_uint8,
                                         f32p, f32p, f32p, f32p]),

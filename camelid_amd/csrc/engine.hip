@@ -318,11 +318,22 @@ void kq_split_rows(uint8_t quant, const uint8_t* src, size_t r0, size_t r1, size
 
 size_t kq_block_bytes(uint8_t quant) { return quant == CAMELID_Q4_K ? 144 : 210; }
 
+// Widest K-quant row the GEMV/GEMM kernels take (k_gemv_q4k<IT> is instantiated for IT <= 8
+// 16-byte pieces per lane: (k / 32 + 63) / 64 <= 8).
+constexpr uint32_t KQ_MAX_K = 16384;
+
+// A launch the host could not map to a kernel instantiation (reported by check_launch; set
+// by launch helpers that have no engine to fail on).
+thread_local std::string g_launch_error;
+
 int upload_kq(camelid_hip_engine* e, KMat* m, const uint8_t* src, size_t len, uint32_t rows, uint32_t k,
               uint8_t quant) {
   if (quant != CAMELID_Q4_K && quant != CAMELID_Q6_K) return fail(e, "unknown weight format");
   if (!src) return fail(e, "missing projection bytes");
   if (k % 256) return fail(e, "K-quant row width must be a multiple of 256");
+  // the K-quant GEMVs hold a row's activation in LDS and instantiate up to 8 pieces per lane
+  if (k > (uint32_t)KQ_MAX_K)
+    return fail(e, "K-quant row width " + std::to_string(k) + " > " + std::to_string(KQ_MAX_K) + " is not supported");
   const size_t nsb = k / 256, want = (size_t)rows * nsb * kq_block_bytes(quant);
   if (len != want) return fail(e, "K-quant byte length " + std::to_string(len) + " != expected " + std::to_string(want));
   std::vector<uint8_t> a((size_t)rows * k / 2), b((size_t)rows * nsb * (quant == CAMELID_Q4_K ? 16 : 64));
@@ -593,6 +604,11 @@ void launch_rmsnorm_quant(const float* x, const float* w, uint32_t n, float eps,
 // chunks of 32 KB; 0 when even two chunks do not fit beside the scores.
 // The largest static LDS of the decode attention kernels (the dynamic ring and score vector
 // come on top of it), read from the compiled kernels.
+// Without a device (the host-only preflight), the static LDS of the attention kernels is taken
+// as this bound (the compiled kernels use at most 8832 bytes) and the LDS of a workgroup as
+// gfx950's 160 KB.
+constexpr long ATT_STATIC_LDS_BOUND = 16384;
+constexpr int GFX950_LDS_PER_WORKGROUP = 160 * 1024;
 long attn_static_lds() {
   static long bytes = -1;
   if (bytes < 0) {
@@ -602,7 +618,7 @@ long attn_static_lds() {
   if (hipFuncGetAttributes(&a, reinterpret_cast<const void*>(&cm::k_attention<HD, F>)) == hipSuccess) \
     m = std::max<long>(m, (long)a.sharedSizeBytes);                                                 \
   else                                                                                              \
-    m = std::max<long>(m, 32768);
+    m = std::max<long>(m, ATT_STATIC_LDS_BOUND);
     CM_ATT_LDS(64, true) CM_ATT_LDS(64, false) CM_ATT_LDS(128, true) CM_ATT_LDS(128, false)
     CM_ATT_LDS(256, true) CM_ATT_LDS(256, false)
 #undef CM_ATT_LDS
@@ -610,7 +626,7 @@ long attn_static_lds() {
   if (hipFuncGetAttributes(&a, reinterpret_cast<const void*>(&cm::k_att_out<HD>)) == hipSuccess) \
     m = std::max<long>(m, (long)a.sharedSizeBytes);                                           \
   else                                                                                        \
-    m = std::max<long>(m, 32768);
+    m = std::max<long>(m, ATT_STATIC_LDS_BOUND);
     CM_ATTO_LDS(64) CM_ATTO_LDS(128) CM_ATTO_LDS(256)
 #undef CM_ATTO_LDS
     bytes = m;
@@ -623,7 +639,7 @@ int attn_ring_slots(uint32_t kvs) {
   if (limit < 0) {
     int dev = 0, v = 0;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
-      v = 65536;
+      v = GFX950_LDS_PER_WORKGROUP;
     limit = v;
   }
   const long room = (long)limit - attn_static_lds() - (long)attn_sc_bytes(kvs);
@@ -659,6 +675,9 @@ uint32_t launch_kgemv(const KMat& m, const float* yd, const int8_t* yq, const in
       CM_Q4(5, 1) CM_Q4(6, 1) CM_Q4(7, 1) CM_Q4(8, 1)
       CM_Q4(5, 2) CM_Q4(6, 2) CM_Q4(7, 2) CM_Q4(8, 2)
 #undef CM_Q4
+      default:
+        g_launch_error = "Q4_K GEMV: row width " + std::to_string(m.k) + " has no kernel instantiation";
+        return 0;
     }
   } else {
     const size_t lds = cm::kq6_lds_bytes((int)m.k, (int)R);
@@ -763,6 +782,9 @@ void run_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cos_base,
     break;
       CM_QKV(1) CM_QKV(2) CM_QKV(3) CM_QKV(4) CM_QKV(5) CM_QKV(6) CM_QKV(7) CM_QKV(8)
 #undef CM_QKV
+      default:
+        g_launch_error = "Q4_K|Q6_K qkv GEMV: row width " + std::to_string(qk.k) + " has no kernel instantiation";
+        break;
     }
   } else {
     proj(e, L.p[0], e->qkv, nullptr);  // q, or q|k stacked
@@ -946,6 +968,9 @@ void launch_kgemm(const KMat& m, uint32_t T, const float* kd, const int8_t* kq, 
     break;
         CM_Q4M(1) CM_Q4M(2) CM_Q4M(3) CM_Q4M(4) CM_Q4M(5) CM_Q4M(6) CM_Q4M(7) CM_Q4M(8)
 #undef CM_Q4M
+        default:
+          g_launch_error = "Q4_K multi-token GEMV: row width " + std::to_string(m.k) + " has no kernel instantiation";
+          return;
       }
     }
     return;
@@ -1092,6 +1117,11 @@ bool ready(const camelid_hip_engine* e) {
 int check_launch(camelid_hip_engine* e) {
   hipError_t st = hipGetLastError();
   if (st != hipSuccess) return fail(e, std::string("kernel launch failed: ") + hipGetErrorString(st));
+  if (!g_launch_error.empty()) {
+    const std::string m = g_launch_error;
+    g_launch_error.clear();
+    return fail(e, m);
+  }
   return 0;
 }
 
@@ -1136,6 +1166,33 @@ int ensure_graph(camelid_hip_engine* e, float scale, int mode) {
   return 0;
 }
 
+// Why the engine would refuse these dimensions ("" when it takes them).  Host-only: callable
+// without a device (camelid_hip_check_model).
+std::string dims_problem(const camelid_hip_dims& d) {
+  if (!d.n_layers || !d.n_heads || !d.n_kv_heads || !d.head_dim || !d.hidden || !d.ffn_dim || !d.vocab || !d.max_pos)
+    return "all dimensions must be nonzero";
+  if (d.n_heads % d.n_kv_heads) return "n_heads must be a multiple of n_kv_heads";
+  if (d.hidden % 32 || d.ffn_dim % 32 || d.head_dim % 32) return "hidden, ffn_dim and head_dim must be multiples of 32";
+  if (!attention_hd_supported(d.head_dim)) return "head_dim must be 64, 128 or 256";
+  if (d.hidden > (uint32_t)cm::SEG_MAX_N) return "hidden > 16384 is not supported by the RMSNorm kernel";
+  if (d.rope_dim == 0 || d.rope_dim > d.head_dim || d.rope_dim % 2) return "rope_dim must be even and within head_dim";
+  if (attn_ring_slots((d.max_pos + 7u) & ~7u) == 0) return "max_pos too large for the decode attention";
+  if (cm::gemv_lds_bytes((int)std::max(d.ffn_dim, d.n_heads * d.head_dim)) > 64 * 1024)
+    return "row width too large for the GEMV";
+  return "";
+}
+
+// Why set_layer / set_output would refuse a projection of `quant` with row width k ("" when
+// they take it).  The byte length is checked at upload.
+std::string proj_problem(uint8_t quant, uint32_t k) {
+  if (quant == CAMELID_Q8_0) return k % 32 ? "Q8_0 row width must be a multiple of 32" : "";
+  if (quant != CAMELID_Q4_K && quant != CAMELID_Q6_K) return "unknown weight format";
+  if (k % 256) return "K-quant row width must be a multiple of 256";
+  if (k > KQ_MAX_K)
+    return "K-quant row width " + std::to_string(k) + " > " + std::to_string(KQ_MAX_K) + " is not supported";
+  return "";
+}
+
 }  // namespace
 
 // ====================================================================== C ABI
@@ -1143,22 +1200,30 @@ extern "C" {
 
 const char* camelid_hip_last_error(const camelid_hip_engine* e) { return e ? e->err.c_str() : g_last_error.c_str(); }
 
+int camelid_hip_check_model(const camelid_hip_dims* dims, const uint8_t layer_quant[7], uint8_t out_quant) {
+  if (!dims) return fail(nullptr, "null argument");
+  const camelid_hip_dims& d = *dims;
+  std::string bad = dims_problem(d);
+  if (!bad.empty()) return fail(nullptr, bad);
+  const uint32_t nq = d.n_heads * d.head_dim;
+  const uint32_t ks[7] = {d.hidden, d.hidden, d.hidden, nq, d.hidden, d.hidden, d.ffn_dim};
+  static const char* names[7] = {"q", "k", "v", "o", "gate", "up", "down"};
+  if (layer_quant)
+    for (int i = 0; i < 7; ++i) {
+      bad = proj_problem(layer_quant[i], ks[i]);
+      if (!bad.empty()) return fail(nullptr, std::string(names[i]) + " projection: " + bad);
+    }
+  bad = proj_problem(out_quant, d.hidden);
+  if (!bad.empty()) return fail(nullptr, "output projection: " + bad);
+  return 0;
+}
+
 int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** out) {
   if (!dims || !out) return fail(nullptr, "null argument");
   *out = nullptr;
   const camelid_hip_dims& d = *dims;
-  if (!d.n_layers || !d.n_heads || !d.n_kv_heads || !d.head_dim || !d.hidden || !d.ffn_dim || !d.vocab || !d.max_pos)
-    return fail(nullptr, "all dimensions must be nonzero");
-  if (d.n_heads % d.n_kv_heads) return fail(nullptr, "n_heads must be a multiple of n_kv_heads");
-  if (d.hidden % 32 || d.ffn_dim % 32 || d.head_dim % 32)
-    return fail(nullptr, "hidden, ffn_dim and head_dim must be multiples of 32");
-  if (!attention_hd_supported(d.head_dim)) return fail(nullptr, "head_dim must be 64, 128 or 256");
-  if (d.hidden > (uint32_t)cm::SEG_MAX_N) return fail(nullptr, "hidden > 16384 is not supported by the RMSNorm kernel");
-  if (d.rope_dim == 0 || d.rope_dim > d.head_dim || d.rope_dim % 2)
-    return fail(nullptr, "rope_dim must be even and within head_dim");
-  if (attn_ring_slots((d.max_pos + 7u) & ~7u) == 0) return fail(nullptr, "max_pos too large for the decode attention");
-  if (cm::gemv_lds_bytes((int)std::max(d.ffn_dim, d.n_heads * d.head_dim)) > 64 * 1024)
-    return fail(nullptr, "row width too large for the GEMV");
+  const std::string bad = dims_problem(d);
+  if (!bad.empty()) return fail(nullptr, bad);
   auto* e = new camelid_hip_engine();
   e->d = d;
   if (const char* dev = std::getenv("CAMELID_HIP_DEVICE")) e->device = std::atoi(dev);
@@ -1240,10 +1305,14 @@ int camelid_hip_set_layer(camelid_hip_engine* e, uint32_t layer, const uint8_t* 
   if (!w || !len || !quant || !attn_norm || !ffn_norm) return fail(e, "null argument");
   if ((q_norm == nullptr) != (k_norm == nullptr)) return fail(e, "q_norm and k_norm must be given together");
   bool all_q8 = true;
-  for (int i = 0; i < 7; ++i) {
-    if (quant[i] != CAMELID_Q8_0 && quant[i] != CAMELID_Q4_K && quant[i] != CAMELID_Q6_K)
-      return fail(e, "unknown projection format");
-    all_q8 = all_q8 && quant[i] == CAMELID_Q8_0;
+  {
+    const uint32_t nq0 = e->d.n_heads * e->d.head_dim;
+    const uint32_t ks0[7] = {e->d.hidden, e->d.hidden, e->d.hidden, nq0, e->d.hidden, e->d.hidden, e->d.ffn_dim};
+    for (int i = 0; i < 7; ++i) {
+      const std::string bad = proj_problem(quant[i], ks0[i]);
+      if (!bad.empty()) return fail(e, bad);
+      all_q8 = all_q8 && quant[i] == CAMELID_Q8_0;
+    }
   }
   HIP_TRY(e, hipSetDevice(e->device));
   const camelid_hip_dims& d = e->d;
@@ -1310,6 +1379,10 @@ int camelid_hip_set_output(camelid_hip_engine* e, const float* final_norm, const
   if (!final_norm || !w) return fail(e, "null argument");
   if (quant != CAMELID_Q8_0 && quant != CAMELID_Q4_K && quant != CAMELID_Q6_K)
     return fail(e, "unknown output projection format");
+  {
+    const std::string bad = proj_problem(quant, e->d.hidden);
+    if (!bad.empty()) return fail(e, "output projection: " + bad);
+  }
   if (e->out_set && quant != e->out_quant) return fail(e, "the output format cannot change after upload");
   HIP_TRY(e, hipSetDevice(e->device));
   const int rc = quant == CAMELID_Q8_0 ? upload_q8(e, &e->out, {{w, len, e->d.vocab}}, e->d.hidden, q8_layout)
@@ -1732,6 +1805,11 @@ int camelid_q8_0_repack(const uint8_t* src, size_t rows, size_t k, uint8_t layou
 static int launch_status(const char* what) {
   hipError_t st = hipGetLastError();
   if (st != hipSuccess) return fail(nullptr, std::string(what) + ": " + hipGetErrorString(st));
+  if (!g_launch_error.empty()) {
+    const std::string m = g_launch_error;
+    g_launch_error.clear();
+    return fail(nullptr, std::string(what) + ": " + m);
+  }
   return 0;
 }
 
@@ -1823,6 +1901,29 @@ int camelid_hip_silu_mul_q8_k(const float* gu, uint32_t n, float* yd, int8_t* yq
   return rc;
 }
 
+// The kernel-level entry points that read the position from device memory (d_pos): the
+// position is read on the host first and refused unless it lies inside the cache (pos <
+// max_pos); the kernels' own guard (cm::kv_pos_bad) is cleared before the launch and read
+// after it, so a position changed on the device in between is reported, not used.
+static int kv_pos_check(const uint32_t* d_pos, uint32_t max_pos, hipStream_t s, const char* what) {
+  uint32_t pos = 0;
+  G_TRY(hipStreamSynchronize(s));
+  G_TRY(hipMemcpy(&pos, d_pos, 4, hipMemcpyDeviceToHost));
+  if (pos >= max_pos)
+    return fail(nullptr, std::string(what) + ": position " + std::to_string(pos) + " is outside the KV cache (" +
+                             std::to_string(max_pos) + " positions)");
+  const uint32_t zero = 0;
+  G_TRY(hipMemcpyToSymbol(HIP_SYMBOL(cm::g_kv_pos_error), &zero, 4, 0, hipMemcpyHostToDevice));
+  return 0;
+}
+static int kv_pos_result(hipStream_t s, const char* what) {
+  uint32_t bad = 0;
+  G_TRY(hipStreamSynchronize(s));
+  G_TRY(hipMemcpyFromSymbol(&bad, HIP_SYMBOL(cm::g_kv_pos_error), 4, 0, hipMemcpyDeviceToHost));
+  if (bad) return fail(nullptr, std::string(what) + ": the device-side position is outside the KV cache");
+  return 0;
+}
+
 int camelid_hip_rope_kv(const float* qkv, uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t rope_dim,
                         uint32_t split_half, const float* cos_tab, const float* sin_tab, const float* q_norm,
                         const float* k_norm, float eps, float* qrot, uint16_t* kc, uint16_t* vc, uint32_t layer,
@@ -1830,10 +1931,13 @@ int camelid_hip_rope_kv(const float* qkv, uint32_t n_heads, uint32_t n_kv, uint3
   if (!qkv || !cos_tab || !sin_tab || !qrot || !kc || !vc || !d_pos) return fail(nullptr, "null argument");
   if (!n_heads || !n_kv || n_heads % n_kv || hd == 0 || hd > 512 || rope_dim > hd || rope_dim % 2)
     return fail(nullptr, "invalid head geometry");
+  if (max_pos % 8) return fail(nullptr, "the KV position stride (max_pos) must be a multiple of 8");
+  if (kv_pos_check(d_pos, max_pos, (hipStream_t)stream, "rope_kv")) return 1;
   hipLaunchKernelGGL(cm::k_rope_kv, dim3(n_heads + n_kv), dim3(64), 0, (hipStream_t)stream, qkv, (int)n_heads,
                      (int)n_kv, (int)hd, (int)rope_dim, (int)split_half, cos_tab, sin_tab, q_norm, k_norm, eps, qrot,
                      kc, vc, (int)layer, (int)max_pos, d_pos, 0, 0);
-  return launch_status("rope_kv");
+  if (launch_status("rope_kv")) return 1;
+  return kv_pos_result((hipStream_t)stream, "rope_kv");
 }
 
 int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const uint16_t* vc, uint32_t layer,
@@ -1844,11 +1948,13 @@ int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const ui
   if (max_pos % 8) return fail(nullptr, "the KV position stride (max_pos) must be a multiple of 8");
   const int slots = attn_ring_slots(max_pos);
   if (slots == 0) return fail(nullptr, "max_pos too large for the decode attention");
+  if (kv_pos_check(d_pos, max_pos, (hipStream_t)stream, "attention_decode")) return 1;
   launch_attention<false>(hd, n_heads, slots, (hipStream_t)stream, qrot, (int)n_heads, (int)n_kv,
                           (int)hd, 0, nullptr, nullptr, 0, nullptr, nullptr, 0.0f, const_cast<uint16_t*>(kc),
                           const_cast<uint16_t*>(vc), (int)layer, (int)max_pos, d_pos, scale, att_out, xq, xs,
                           prefetch_of((const Q8Mat*)nullptr));
-  return launch_status("attention_decode");
+  if (launch_status("attention_decode")) return 1;
+  return kv_pos_result((hipStream_t)stream, "attention_decode");
 }
 
 int camelid_hip_attention_decode_split(const float* qrot, const uint16_t* kc, const uint16_t* vc, uint32_t layer,
@@ -1860,6 +1966,7 @@ int camelid_hip_attention_decode_split(const float* qrot, const uint16_t* kc, co
   if (max_pos % 8) return fail(nullptr, "the KV position stride (max_pos) must be a multiple of 8");
   const int slots = attn_ring_slots(max_pos);
   if (slots == 0) return fail(nullptr, "max_pos too large for the decode attention");
+  if (kv_pos_check(d_pos, max_pos, (hipStream_t)stream, "attention_decode_split")) return 1;
   float *g_sc = nullptr, *g_mx = nullptr;
   if (hipMalloc(&g_sc, (size_t)n_heads * max_pos * 4) != hipSuccess ||
       hipMalloc(&g_mx, (size_t)n_heads * ((max_pos + 255) / 256) * 4) != hipSuccess) {
@@ -1875,7 +1982,7 @@ int camelid_hip_attention_decode_split(const float* qrot, const uint16_t* kc, co
   (void)hipFree(g_sc);
   (void)hipFree(g_mx);
   if (!rc && st != hipSuccess) return fail(nullptr, std::string("attention_decode_split: ") + hipGetErrorString(st));
-  return rc;
+  return rc ? rc : kv_pos_result((hipStream_t)stream, "attention_decode_split");
 }
 
 int camelid_hip_rmsnorm_q8_0_gemv(const int8_t* wq, const uint16_t* wd, uint32_t rows, uint32_t k, const float* x,

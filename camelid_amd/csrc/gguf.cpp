@@ -272,8 +272,20 @@ bool parse(camelid_gguf* g, std::string* why) {
              " is not divisible by block size " + std::to_string(bs);
       return false;
     }
+    // element count with a per-dimension overflow check past 2^64 (reader.rs:553-557 checked_mul)
     unsigned __int128 elems = 1;
-    for (uint64_t d : r.dims) elems *= d;
+    bool overflow = false;
+    for (uint64_t d : r.dims) {
+      elems *= d;
+      if (elems >> 64) {
+        overflow = true;
+        break;
+      }
+    }
+    if (overflow) {
+      *why = "tensor " + r.name + " element count overflows";
+      return false;
+    }
     const unsigned __int128 nb = elems / bs * ts;
     const unsigned __int128 end = (unsigned __int128)g->data_start + r.off + nb;
     if (nb >> 64 || end > g->len) {
@@ -456,8 +468,11 @@ CX int camelid_gguf_model(const camelid_gguf* g, uint32_t max_pos, camelid_hip_d
   r.low = meta_f32(g, key("rope.scaling.low_freq_factor"), &f) ? f : 1.0f;
   r.high = meta_f32(g, key("rope.scaling.high_freq_factor"), &f) ? f : 4.0f;
   const camelid_gguf_tensor* rf = tensor(g, "rope_freqs.weight");
-  r.freqs = (rf && rf->type == 0 && rf->dims[0] == d.rope_dim / 2) ? reinterpret_cast<const float*>(rf->data)
-                                                                      : nullptr;
+  // rope_freqs: an F32 tensor holding at least rope_dim/2 factors (its byte count checked too,
+  // so a tensor with a zero trailing dimension is never read past its end)
+  r.freqs = (rf && rf->type == 0 && rf->dims[0] == d.rope_dim / 2 && rf->n_bytes >= (uint64_t)d.rope_dim / 2 * 4)
+                ? reinterpret_cast<const float*>(rf->data)
+                : nullptr;
   *dims = d;
   *rope = r;
   return 0;

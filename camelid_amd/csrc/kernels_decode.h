@@ -1419,6 +1419,17 @@ __host__ __device__ __forceinline__ size_t kv_v_index(int hd, int p, int d) {
   return ((size_t)(p >> 3) * hd + d) * 8 + (p & 7);
 }
 
+// Position guard of the decode kernels that read their position from device memory: a
+// position outside the KV cache (pos >= kvs) makes the kernel touch no cache entry and write
+// no output; it sets this word to 1 instead.  The kernel-level entry points clear and read it
+// (the engine validates every position on the host before it is written to device memory).
+__device__ uint32_t g_kv_pos_error;
+__device__ __forceinline__ bool kv_pos_bad(int pos, int kvs) {
+  if ((unsigned)pos < (unsigned)kvs) return false;
+  if (threadIdx.x == 0) g_kv_pos_error = 1u;
+  return true;
+}
+
 // ---------------------------------------------------------------------------
 // Per-head QK RMSNorm (optional) + RoPE + f16 KV store for the token at *d_pos (or pos0
 // when d_pos is null).  The decode step fuses this into the attention kernel; prefill runs
@@ -1473,6 +1484,7 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, i
   } else {
     const int kvh = h - n_heads;
     const int pos = (d_pos ? (int)*d_pos : pos0) + (int)blockIdx.y;
+    if (kv_pos_bad(pos, kvs)) return;
     const size_t hbase = kv_head_base(layer, n_kv, kvh, hd, kvs);
     const float* vsrc = qkv + (size_t)(n_heads + n_kv) * hd + (size_t)kvh * hd;
     for (int d = threadIdx.x; d < hd; d += blockDim.x) {
@@ -1613,6 +1625,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   const uint4* kg = reinterpret_cast<const uint4*>(kc + hbase);  // K granule (u, p): u * kvs + p
   const uint4* vg = reinterpret_cast<const uint4*>(vc + hbase);  // V granule (g, d): g * HD + d
   const int pos = (int)*d_pos;
+  if (kv_pos_bad(pos, kvs)) return;  // (uniform, before any barrier)
   const int P = pos + 1;
   const int ncache = pos;
   // Loads in the order they are needed (a wave's loads complete in order): this token's q, k
@@ -1916,6 +1929,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_scores(
   __shared__ float s_qscale, s_kscale;
   const int tid = threadIdx.x, h = blockIdx.x, s = blockIdx.y;
   const int pos = (int)*d_pos;
+  if (kv_pos_bad(pos, kvs)) return;  // (uniform, before any barrier)
   const int p0 = s * ATT_NT;
   if (p0 > pos) return;  // (uniform) a slice past the current position
   const int rep = n_heads / n_kv;
@@ -2045,6 +2059,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
   const size_t hbase = kv_head_base(layer, n_kv, h / rep, HD, kvs);
   const uint4* vg = reinterpret_cast<const uint4*>(vc + hbase);  // V granule (g, d): g * HD + d
   const int pos = (int)*d_pos;
+  if (kv_pos_bad(pos, kvs)) return;  // (uniform, before any barrier)
   const int P = pos + 1;
   const int d = w * DW + tid;  // output lanes: tid < DW
   float acc = 0.0f;

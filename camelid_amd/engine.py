@@ -47,6 +47,24 @@ def _u8(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.uint8)
 
 
+def _sized(a: np.ndarray, count: int, what: str) -> np.ndarray:
+    """a, refused unless it holds exactly `count` values: the C side copies fixed sizes
+    derived from the model dims (the reference's prefill checks these lengths,
+    cuda_resident.rs:7795)."""
+    if a.size != count:
+        raise ValueError(f"{what}: {a.size} values, expected {count}")
+    return a
+
+
+def _rows(a: np.ndarray, width: int, what: str) -> int:
+    """Number of rows of width `width` in a (a 1-D array is one row); refuses other shapes."""
+    if a.ndim == 1:
+        a = a.reshape(1, -1)
+    if a.ndim != 2 or a.shape[1] != width:
+        raise ValueError(f"{what}: shape {a.shape}, expected [n][{width}]")
+    return a.shape[0]
+
+
 class HipResidentDecode:
     """Resident weights + f16 KV cache on one MI355X; one stream, one sync per call."""
 
@@ -86,15 +104,17 @@ class HipResidentDecode:
         ptrs = (N.u8p * 7)(*[N.ptr(a, C.c_uint8) for a in arrs])
         lens = (C.c_size_t * 7)(*[a.nbytes for a in arrs])
         qs = (C.c_uint8 * 7)(*(quants or [Q8_0] * 7))
-        an, fn = _f32(attn_norm), _f32(ffn_norm)
-        qn = _f32(q_norm) if q_norm is not None else None
-        kn = _f32(k_norm) if k_norm is not None else None
+        d = self.dims
+        an = _sized(_f32(attn_norm), d.hidden, "attn_norm")
+        fn = _sized(_f32(ffn_norm), d.hidden, "ffn_norm")
+        qn = _sized(_f32(q_norm), d.head_dim, "q_norm") if q_norm is not None else None
+        kn = _sized(_f32(k_norm), d.head_dim, "k_norm") if k_norm is not None else None
         self._chk(self._lib.camelid_hip_set_layer(
             self._h, layer, ptrs, lens, qs, q8_layout, N.ptr(an, C.c_float), N.ptr(fn, C.c_float),
             N.ptr(qn, C.c_float) if qn is not None else None, N.ptr(kn, C.c_float) if kn is not None else None))
 
     def set_output(self, final_norm, weight, quant: int = Q8_0, q8_layout: int = WIRE34) -> None:
-        fn, w = _f32(final_norm), _u8(weight)
+        fn, w = _sized(_f32(final_norm), self.dims.hidden, "final_norm"), _u8(weight)
         self._chk(self._lib.camelid_hip_set_output(self._h, N.ptr(fn, C.c_float), N.ptr(w, C.c_uint8), w.nbytes,
                                                    quant, q8_layout))
 
@@ -104,7 +124,10 @@ class HipResidentDecode:
 
     def set_rope_table(self, cos_all, sin_all) -> None:
         c, s = _f32(cos_all), _f32(sin_all)
-        n = c.shape[0]
+        half = self.dims.rope_dim // 2
+        n = _rows(c, half, "cos_all")
+        if _rows(s, half, "sin_all") != n:
+            raise ValueError("cos_all and sin_all must have the same number of rows")
         self._chk(self._lib.camelid_hip_set_rope_table(self._h, N.ptr(c, C.c_float), N.ptr(s, C.c_float), n))
 
     # -- state (cuda_resident.rs:6261-6292) ------------------------------------------------
@@ -128,7 +151,9 @@ class HipResidentDecode:
 
     # -- KV handoff (cuda_resident.rs:6305 seed_layer, :6348 read_kv_layer) ----------------
     def seed_layer(self, layer: int, ck, cv, n_pos: int) -> None:
-        k, v = _f32(ck), _f32(cv)
+        d = self.dims
+        k = _sized(_f32(ck), d.n_kv_heads * n_pos * d.head_dim, "ck")
+        v = _sized(_f32(cv), d.n_kv_heads * n_pos * d.head_dim, "cv")
         self._chk(self._lib.camelid_hip_seed_layer(self._h, layer, N.ptr(k, C.c_float), N.ptr(v, C.c_float), n_pos))
 
     def read_kv_layer(self, layer: int, n: int):
@@ -141,7 +166,10 @@ class HipResidentDecode:
     # -- forward (cuda_resident.rs:7430 forward_token, :7724 forward_token_logits) ---------
     def forward_token(self, embedding, cos, sin, position: int, scale: float, compute_logits: bool = True):
         """Returns the greedy token (and fills self.last_logits when compute_logits)."""
-        e, c, s = _f32(embedding), _f32(cos), _f32(sin)
+        d = self.dims
+        e = _sized(_f32(embedding), d.hidden, "embedding")
+        c = _sized(_f32(cos), d.rope_dim // 2, "cos")
+        s = _sized(_f32(sin), d.rope_dim // 2, "sin")
         tok = C.c_uint32(0)
         logits = np.empty(self.dims.vocab, np.float32) if compute_logits else None
         self._chk(self._lib.camelid_hip_forward_token(
@@ -156,20 +184,29 @@ class HipResidentDecode:
 
     def prefill(self, embeddings, cos_all, sin_all, scale: float) -> None:
         """Positions [filled, filled+n) (cuda_resident.rs:7785 prefill / :8797 prefill_batched)."""
+        n = self._rows_checked(embeddings, cos_all, sin_all)
         e, c, s = _f32(embeddings), _f32(cos_all), _f32(sin_all)
-        n = e.shape[0]
         self._chk(self._lib.camelid_hip_prefill(self._h, N.ptr(e, C.c_float), N.ptr(c, C.c_float),
                                                 N.ptr(s, C.c_float), n, scale))
 
     prefill_batched = prefill
+
+    def _rows_checked(self, embeddings, cos_all, sin_all) -> int:
+        """Rows of the [n][H] embeddings, refused unless cos/sin hold [n][rope_dim/2]."""
+        d = self.dims
+        n = _rows(np.asarray(embeddings), d.hidden, "embeddings")
+        half = d.rope_dim // 2
+        if _rows(np.asarray(cos_all), half, "cos_all") != n or _rows(np.asarray(sin_all), half, "sin_all") != n:
+            raise ValueError(f"cos_all / sin_all must hold {n} rows of {half}")
+        return n
 
     MAX_VERIFY_K = 8
 
     def verify_batch(self, embeddings, cos_all, sin_all, base_position: int, scale: float) -> np.ndarray:
         """k tokens at [base_position, base_position + k) in one batched forward; the greedy
         token after each (cuda_resident.rs:7821).  filled is left to the caller."""
+        k = self._rows_checked(embeddings, cos_all, sin_all)
         e, c, s = _f32(embeddings), _f32(cos_all), _f32(sin_all)
-        k = e.shape[0]
         out = np.empty(k, np.uint32)
         self._chk(self._lib.camelid_hip_verify(self._h, N.ptr(e, C.c_float), N.ptr(c, C.c_float), N.ptr(s, C.c_float),
                                                base_position, k, scale, N.ptr(out, C.c_uint32)))

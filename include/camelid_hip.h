@@ -55,6 +55,13 @@ enum { CAMELID_PROJ_Q = 0, CAMELID_PROJ_K, CAMELID_PROJ_V, CAMELID_PROJ_O,
  * as camelid_hip_rope_kv documents; position stride kvs = max_pos rounded up to 8) and all
  * scratch on device 0 (or CAMELID_HIP_DEVICE).  head_dim must be 64, 128 or 256. */
 int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** out);
+/* Host-only preflight of build_resident_cuda_engine's decline (inference.rs:11245-11678 returns
+ * None, and the caller runs the model on the CPU path, for a model the resident engine cannot
+ * take): 0 when engine_new would accept `dims` and set_layer / set_output would accept a layer
+ * whose projections have the formats layer_quant[7] (CAMELID_PROJ_* order; NULL: no layer
+ * check) and an lm_head of format out_quant; nonzero otherwise, with the reason in
+ * camelid_hip_last_error(NULL).  Needs no device. */
+int camelid_hip_check_model(const camelid_hip_dims* dims, const uint8_t layer_quant[7], uint8_t out_quant);
 /* Drop (cuda_resident.rs:5398 Drop + cuda.rs:485 release_async_pool). */
 void camelid_hip_engine_free(camelid_hip_engine* e);
 /* Last error message of this engine ("" if none); NULL engine -> last global error. */
@@ -190,14 +197,19 @@ int camelid_hip_silu_mul_quantize(const float* gu, uint32_t n, int8_t* xq, float
  * layout: per (layer, kv head) a region of hd * max_pos f16 elements at element offset
  * (layer * n_kv + kv_head) * hd * max_pos; K element (p, d) at ((d / 8) * max_pos + p) * 8
  * + d % 8; V element (p, d) at ((p / 8) * hd + d) * 8 + p % 8 (16-byte granules: 8 dims of
- * one position for K, 8 positions of one dim for V).  max_pos (the position stride) % 8 == 0. */
+ * one position for K, 8 positions of one dim for V).  max_pos (the position stride) % 8 == 0.
+ * Position contract (the engine's filled/max_pos, cuda_resident.rs:6265-6292): *d_pos is read
+ * on the host and refused unless *d_pos < max_pos; the kernel also skips every cache access
+ * for a position outside the cache and the call then returns an error.  Synchronizes the
+ * stream. */
 int camelid_hip_rope_kv(const float* qkv, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
                         uint32_t rope_dim, uint32_t split_half, const float* cos_tab,
                         const float* sin_tab, const float* q_norm, const float* k_norm, float eps,
                         float* qrot, uint16_t* kc, uint16_t* vc, uint32_t layer, uint32_t max_pos,
                         const uint32_t* d_pos, void* stream);
 /* attention_decode (cuda_resident.rs:1587; CPU inference.rs:23945-24025), faithful order.
- * Cache layout as camelid_hip_rope_kv; max_pos (the position stride) % 8 == 0; hd in {64,128,256}. */
+ * Cache layout and position contract as camelid_hip_rope_kv (synchronizes the stream);
+ * max_pos (the position stride) % 8 == 0; hd in {64,128,256}. */
 int camelid_hip_attention_decode(const float* qrot, const uint16_t* kc, const uint16_t* vc,
                                  uint32_t layer, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
                                  uint32_t max_pos, const uint32_t* d_pos, float scale,

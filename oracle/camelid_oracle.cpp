@@ -21,10 +21,15 @@
 //   quantize_q8_0          - reference KAT q8_0_input_quantization_uses_unrounded_scale
 //                            + brute-force properties (round-half-away, clamp)
 //   block int dot          - brute force int64 sums
-//   rms_norm               - closed form on constant rows; float64 bound
+//   Q8_0 row fold          - exact integer case; order/FMA/association known answers
+//   rms_norm               - closed form on constant rows; float64 bound; sum-order and
+//                            rounded-square known answers
 //   rope                   - pos 0 identity, norm preservation, llama3 KAT
-//   attention              - single-position copy, uniform keys -> mean of V
+//   attention              - single-position copy, uniform keys -> mean of V; score-dot,
+//                            softmax-sum and AV order / rounded-product known answers
 //   silu_mul / argmax      - closed forms / brute force incl. ties
+//   Q4_K / Q6_K row dots   - fixture-pinned dequant sums; FMA chain and class-chain
+//                            left-fold known answers
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>

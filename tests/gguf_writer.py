@@ -56,9 +56,11 @@ def gguf_bytes(meta: list, tensors: list, alignment: int = 32, version: int = 3,
     return bytes(out)
 
 
-def model_gguf(model, arch: str = "llama", alignment: int = 32, extra_meta: list | None = None) -> bytes:
+def model_gguf(model, arch: str = "llama", alignment: int = 32, extra_meta: list | None = None,
+               extra_tensors: list | None = None) -> bytes:
     """A SyntheticModel as a GGUF file: the GGUF tensor names, weights as their wire bytes,
-    norms as F32, dims [k, rows] (the contiguous dimension first)."""
+    norms as F32, dims [k, rows] (the contiguous dimension first); extra_tensors are appended
+    as given ([(name, dims, ggml_type, data bytes)])."""
     cfg = model.cfg
     a = arch
     meta = [("general.architecture", STR, a), ("general.name", STR, cfg.name), ("general.alignment", U32, alignment),
@@ -95,4 +97,5 @@ def model_gguf(model, arch: str = "llama", alignment: int = 32, extra_meta: list
     tensors.append(("output_norm.weight", [H], 0, f32(model.output_norm)))
     if model.output is not model.token_embd:
         tensors.append(("output.weight", [H, cfg.vocab], GGML[cfg.output_quant()], model.output.tobytes()))
+    tensors += extra_tensors or []
     return gguf_bytes(meta, tensors, alignment)

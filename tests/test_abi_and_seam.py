@@ -118,3 +118,79 @@ def test_q8_repack_layouts(native, orc):
     assert native.camelid_q8_0_repack(ptr(b36.ravel(), C.c_uint8), rows, k, 36, ptr(q2, C.c_int8),
                                       ptr(d2, C.c_uint16)) == 0
     assert np.array_equal(q, q2) and np.array_equal(d, d2)
+
+
+def test_check_model_refuses_unsupported_shapes_without_gpu(native):
+    """camelid_hip_check_model: the host preflight of the resident engine's decline
+    (build_resident_cuda_engine returns None, inference.rs:11245).  K-quant rows wider than the
+    GEMV kernels take (ffn_down of a Q4_K qwen2-7B, ffn 18944) are refused with a reason, as are
+    rows whose width is no multiple of the block; the benchmark configs are taken."""
+    from camelid_amd import _native as N
+    from camelid_amd.engine import Q4_K, Q6_K, Q8_0
+    from camelid_amd.model import CONFIGS
+
+    def check(dims, quant, out):
+        q = (C.c_uint8 * 7)(*quant) if quant is not None else None
+        rc = native.camelid_hip_check_model(C.byref(dims), C.cast(q, N.u8p) if q is not None else None, out)
+        return rc, N.last_error()
+
+    def dims_of(cfg, max_pos=2048, **over):
+        d = N.Dims(cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.hidden, cfg.ffn_dim, cfg.rope_dim,
+                   max_pos, cfg.vocab, cfg.eps, int(cfg.split_half))
+        for k, v in over.items():
+            setattr(d, k, v)
+        return d
+
+    q8 = [Q8_0] * 7
+    qkm = [Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q4_K]
+    for name, cfg in CONFIGS.items():
+        quant = q8 if cfg.quant_scheme == "q8_0" else qkm
+        out = Q8_0 if cfg.quant_scheme == "q8_0" else Q6_K
+        assert check(dims_of(cfg, cfg.prompt_len + cfg.decode_len), quant, out)[0] == 0, name
+    qwen = CONFIGS["qwen3-8b"]
+    rc, msg = check(dims_of(qwen, ffn_dim=18944), qkm, Q6_K)
+    assert rc != 0 and "down projection" in msg and "18944 > 16384" in msg
+    # the same width in Q8_0 is taken (its GEMV stages the row in LDS up to the limit checked here)
+    assert check(dims_of(qwen, ffn_dim=18944), [Q4_K] * 6 + [Q8_0], Q6_K)[0] == 0
+    rc, msg = check(dims_of(qwen, hidden=4096 + 32), qkm, Q6_K)
+    assert rc != 0 and "multiple of 256" in msg
+    rc, msg = check(dims_of(qwen), qkm, 7)
+    assert rc != 0 and "output projection" in msg
+    assert check(dims_of(qwen), None, Q8_0)[0] == 0
+    rc, msg = check(dims_of(qwen, n_kv_heads=3), None, Q8_0)
+    assert rc != 0 and "multiple of n_kv_heads" in msg
+
+
+def test_engine_wrapper_refuses_short_arrays_without_gpu(native):
+    """The Python mirror checks every host array against the model dims before the C side
+    copies its fixed sizes (cuda_resident.rs:7795 checks prefill's lengths the same way):
+    short or mis-shaped arrays raise ValueError and no native call is made."""
+    from camelid_amd.engine import EngineDims, HipResidentDecode
+    d = EngineDims(2, 4, 2, 64, 256, 512, 64, 32, 100, 1e-5)
+    eng = object.__new__(HipResidentDecode)  # no device: only the host-side checks run
+    eng.dims, eng._lib, eng._h = d, None, None
+    H, half = d.hidden, d.rope_dim // 2
+    z = np.zeros
+    with pytest.raises(ValueError, match="embedding"):
+        eng.forward_token(z(H - 1), z(half), z(half), 0, 0.125)
+    with pytest.raises(ValueError, match="cos"):
+        eng.forward_token(z(H), z(half - 1), z(half), 0, 0.125)
+    with pytest.raises(ValueError, match="sin"):
+        eng.forward_token(z(H), z(half), z(half + 1), 0, 0.125)
+    with pytest.raises(ValueError, match="embeddings"):
+        eng.prefill(z((3, H - 32)), z((3, half)), z((3, half)), 0.125)
+    with pytest.raises(ValueError, match="rows"):
+        eng.prefill(z((3, H)), z((2, half)), z((3, half)), 0.125)
+    with pytest.raises(ValueError, match="rows"):
+        eng.verify_batch(z((4, H)), z((4, half)), z((3, half)), 0, 0.125)
+    with pytest.raises(ValueError, match="cos_all"):
+        eng.set_rope_table(z((8, half + 1)), z((8, half + 1)))
+    with pytest.raises(ValueError, match="ck"):
+        eng.seed_layer(0, z(d.n_kv_heads * 5 * d.head_dim - 1), z(d.n_kv_heads * 5 * d.head_dim), 5)
+    with pytest.raises(ValueError, match="final_norm"):
+        eng.set_output(z(H + 1), z(10, np.uint8))
+    projs = {n: z(8, np.uint8) for n in ("q", "k", "v", "o", "gate", "up", "down")}
+    with pytest.raises(ValueError, match="attn_norm"):
+        eng.set_layer(0, projs, z(H - 1), z(H))
+    with pytest.raises(ValueError, match="k_norm"):
+        eng.set_layer(0, projs, z(H), z(H), z(d.head_dim), z(d.head_dim - 1))

@@ -159,3 +159,38 @@ def test_model_round_trip(tmp_path, kw, arch):
         assert N.lib().camelid_gguf_alignment(g._h) == 64
     finally:
         g.close()
+
+
+def test_element_count_overflow_is_refused(tmp_path):
+    """reader.rs:553-557 (checked_mul of the dims): a tensor whose element count passes 2^64
+    is refused, not wrapped to a small byte count."""
+    ok_meta = [("general.architecture", STR, "llama")]
+    msg = _refusal(tmp_path, gguf_bytes(ok_meta, [("a.weight", [2 ** 32, 2 ** 32, 2 ** 32, 2 ** 32], 0, b"")]))
+    assert "element count overflows" in msg
+    msg = _refusal(tmp_path, gguf_bytes(ok_meta, [("a.weight", [2 ** 32, 2 ** 32], 0, b"")]))
+    assert "element count overflows" in msg
+    # just below 2^64 elements: not an overflow, but far beyond the file
+    assert "beyond end of file" in _refusal(tmp_path, gguf_bytes(ok_meta, [("a.weight", [2 ** 32, 2 ** 31], 0, b"")]))
+
+
+def test_short_rope_freqs_is_not_read(tmp_path):
+    """A rope_freqs tensor with the right first dimension but no bytes ([rope_dim/2, 0]) is
+    ignored: the model reader hands out no pointer to read rope_dim/2 factors from."""
+    cfg = tiny_config()
+    model = SyntheticModel.generate(cfg)
+    half = cfg.rope_dim // 2
+    for dims, data, expect in (([half, 0], b"", False), ([half], np.full(half, 2.0, np.float32).tobytes(), True)):
+        p = tmp_path / "rf.gguf"
+        p.write_bytes(model_gguf(model, "llama", extra_tensors=[("rope_freqs.weight", dims, 0, data)]))
+        rc, h, msg = _open(p)
+        assert rc == 0, msg
+        lib = N.lib()
+        try:
+            d, rope = N.Dims(), N.GgufRope()
+            assert lib.camelid_gguf_model(h, 64, C.byref(d), C.byref(rope)) == 0
+            assert bool(rope.freqs) == expect
+            if expect:
+                got = np.ctypeslib.as_array(C.cast(rope.freqs, C.POINTER(C.c_float)), (half,))
+                assert np.all(got == 2.0)
+        finally:
+            lib.camelid_gguf_close(h)

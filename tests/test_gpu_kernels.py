@@ -58,10 +58,16 @@ def test_expf_device_all_inputs(native, orc):
 
 
 @pytest.mark.parametrize("rows,k", [(2048, 2048), (5632, 2048), (2048, 5632), (1000, 3072), (3072, 8192),
-                                    (37, 96), (33, 14336)])
+                                    (37, 96), (33, 14336),
+                                    # the isolated sweep's two widest shapes: two rows per
+                                    # wave (k_gemv_k<K, 2>, rows >= 16384), the lm_head shapes of C1 and C3
+                                    (32000, 2048), (128256, 3072), (16385, 4096)])
 def test_q8_gemv_bit_exact(native, orc, rows, k):
+    from camelid_amd.model import synth_q8_0
     rng = np.random.default_rng(rows * 7 + k)
-    wire = orc.quantize_q8_0_wire(rng.normal(0, 0.02, rows * k).astype(np.float32))
+    # N(0, 0.02) weights as Q8_0 wire blocks (the seeded multi-threaded generator: the widest
+    # shapes hold 394M values)
+    wire = synth_q8_0(f"gemv{rows}x{k}", 2, rows, k, 0.02)
     q, d = _repack(native, wire, rows, k)
     xs, xq = orc.quantize_q8_0(rng.normal(0, 1, k).astype(np.float32))
     resid = rng.normal(0, 1, rows).astype(np.float32)
@@ -82,7 +88,9 @@ def test_q8_gemv_bit_exact(native, orc, rows, k):
 
 @pytest.mark.parametrize("rows,k,tokens", [(5120, 3072, 130), (3072, 8192, 64), (2048, 5632, 65), (36, 96, 70),
                                            (128, 14336, 3), (1000, 2048, 1), (16384, 3072, 33),
-                                           (5120, 3072, 8), (3072, 8192, 5), (36, 2048, 2), (4100, 5632, 7)])
+                                           (5120, 3072, 8), (3072, 8192, 5), (36, 2048, 2), (4100, 5632, 7),
+                                           # the sweep's prefill batch (512 tokens) and C3's prefill chunk (511)
+                                           (2048, 2048, 512), (5632, 2048, 512), (3072, 8192, 511)])
 def test_q8_gemm_bit_exact(native, orc, rows, k, tokens):
     """Prefill GEMM on the matrix cores == the per-token GEMV fold of the CPU path."""
     rng = np.random.default_rng(rows + 3 * k + tokens)
