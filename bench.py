@@ -176,6 +176,51 @@ def run_sweep_kquant(tokens: int = 512, iters: int = 20) -> dict:
             "peaks": {"int8_tops": INT8_PEAK_TOPS}, "shapes": out}
 
 
+ATT_PHASES = ("qkv_rope_kvstore", "scores_max", "exp", "denominator", "output_sums", "quantize_store")
+
+
+def attention_phases(cfg) -> dict:
+    """Per-phase times of the decode attention in the last timed step, from the measurement
+    build's in-kernel timestamps (100 MHz counter, thread 0 of every head's workgroup): the
+    mean over layers and heads of each phase, the workgroups' start spread within a launch
+    and the launch span (first start to last end), in microseconds."""
+    import ctypes as C
+    from camelid_amd import _native as N
+    na, ng = 64 * 64 * 7, 2 * 256 * 8
+    buf = (C.c_uint64 * (na + ng))()
+    got = C.c_size_t(0)
+    N.check(N.lib().camelid_hip_phase_stamps(buf, na + ng, C.byref(got)))
+    allst = np.frombuffer(buf, np.uint64).astype(np.int64)
+    st = allst[:na].reshape(64, 64, 7)[:cfg.n_layers, :cfg.n_heads]
+    d = np.diff(st, axis=2) * 0.01  # 100 MHz ticks -> us
+    res = {name: round(float(d[:, :, i].mean()), 3) for i, name in enumerate(ATT_PHASES)}
+    res["workgroup_total"] = round(float((st[:, :, 6] - st[:, :, 0]).mean() * 0.01), 3)
+    res["start_spread"] = round(float((st[:, :, 0].max(1) - st[:, :, 0].min(1)).mean() * 0.01), 3)
+    res["launch_span"] = round(float((st[:, :, 6].max(1) - st[:, :, 0].min(1)).mean() * 0.01), 3)
+    log("attention phases (us, mean over layers and heads): " + ", ".join(f"{k} {v}" for k, v in res.items()))
+    # the norm-fused GEMVs of the last layer (mean over the workgroups that recorded)
+    gs = allst[na:].reshape(2, 256, 8)
+    for kind, name in enumerate(("qkv_norm_gemv", "gate_up_norm_gemv")):
+        g = gs[kind]
+        g = g[g[:, 0] > 0]
+        if not len(g):
+            continue
+        t0 = g[:, 0]
+        ph = {"norm_inputs_arrived": float((g[:, 6] - t0).mean() * 0.01),
+              "sum_of_squares_done": float((g[:, 7] - t0).mean() * 0.01),
+              "norm_done": float((g[:, 1] - t0).mean() * 0.01),
+              "weight_loads_issued": float((g[:, 2] - t0).mean() * 0.01),
+              "past_norm_barrier": float((g[:, 3] - t0).mean() * 0.01),
+              "dots_done": float((g[:, 4] - t0).mean() * 0.01),
+              "end": float((g[:, 5] - t0).mean() * 0.01),
+              "start_spread": float((t0.max() - t0.min()) * 0.01),
+              "launch_span": float((g[:, 5].max() - t0.min()) * 0.01),
+              "workgroups": int(len(g))}
+        res[name] = {k: round(v, 3) for k, v in ph.items()}
+        log(f"{name} phases (us from each workgroup's start): " + ", ".join(f"{k} {v:.3f}" for k, v in ph.items()))
+    return res
+
+
 def probe_traffic() -> int:
     """The workload of the traffic counter passes: a 256 MiB device-to-device copy (the
     counters' scale reference), then three C3 decode steps launched without graphs on a
@@ -221,11 +266,17 @@ def main() -> int:
                     help="time the K-quant prefill projections (Q4_K GEMM, Q6_K multi-token GEMV) of configs[4]")
     ap.add_argument("--probe-traffic", action="store_true",
                     help="the workload of the rocprofv3 FETCH_SIZE/WRITE_SIZE passes (no JSON line)")
+    ap.add_argument("--phase-stamps", action="store_true",
+                    help="load the measurement build (libcamelid_hip_stamps.so, built by `python -m "
+                         "camelid_amd.build --stamps`) and report the decode attention's per-phase times "
+                         "from in-kernel timestamps of the last timed step")
     ap.add_argument("--seed-kv", action="store_true",
                     help="seed the prompt's KV rows with random f16 values instead of running the prefill "
                          "(kernel profiling of the decode steps alone; skips the parity check)")
     args = ap.parse_args()
 
+    if args.phase_stamps:  # (before the library is loaded)
+        os.environ["CAMELID_HIP_LIB"] = "libcamelid_hip_stamps.so"
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the resident decode path runs on a single MI355X with no "
               "sharding or collectives (multi-GPU sharding is a design note, not a measured path).",
@@ -315,6 +366,8 @@ def main() -> int:
         parity = {"golden": gold.name, "compared": n, "identical": stream[:n] == g["tokens"][:n]}
         log(f"token parity vs golden: {parity}")
 
+    phases = attention_phases(cfg) if args.phase_stamps else None
+
     roofline = None
     prof = None
     if not args.no_profile:
@@ -387,6 +440,8 @@ def main() -> int:
     }
     if prof:
         out["kernels_ms"] = {k: round(v["ms"], 3) for k, v in prof.items()}
+    if phases:
+        out["attention_phases_us"] = phases
     print(json.dumps(out), flush=True)
     sess.close()
     return 0

@@ -6,9 +6,13 @@ missing: there is no CPU fallback on the product path.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libcamelid_hip.so"
+LIB_DIR = Path(__file__).resolve().parent / "_lib"
+# The product library; CAMELID_HIP_LIB names another build of it in the same directory (the
+# measurement build libcamelid_hip_stamps.so, which also records phase timestamps).
+LIB_PATH = LIB_DIR / os.environ.get("CAMELID_HIP_LIB", "libcamelid_hip.so")
 
 u8p = C.POINTER(C.c_uint8)
 i8p = C.POINTER(C.c_int8)
@@ -91,6 +95,7 @@ SIGNATURES: dict[str, tuple] = {
     "camelid_hip_profile_end": (C.c_int, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                           C.POINTER(C.c_uint64), C.c_uint32]),
     "camelid_hip_device_info": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(C.c_int)]),
+    "camelid_hip_phase_stamps": (C.c_int, [C.POINTER(C.c_uint64), C.c_size_t, C.POINTER(C.c_size_t)]),
     "camelid_hip_malloc": (C.c_int, [C.POINTER(vp), C.c_size_t]),
     "camelid_hip_free": (C.c_int, [vp]),
     "camelid_hip_memcpy_htod": (C.c_int, [vp, vp, C.c_size_t]),

@@ -52,27 +52,34 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd[:6])} ...")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every source and link the shared library; returns its path."""
+STAMPS_LIB = LIB_DIR / "libcamelid_hip_stamps.so"
+
+
+def build(verbose: bool = False, stamps: bool = False) -> Path:
+    """Compile every source and link the shared library; returns its path.  stamps: the
+    measurement build instead (-DCM_STAMPS: the decode attention also records phase
+    timestamps), linked as libcamelid_hip_stamps.so beside the product library."""
     BUILD_DIR.mkdir(exist_ok=True)
     LIB_DIR.mkdir(exist_ok=True)
     hipcc = _hipcc()
     objs: list[str] = []
     for src in HIP_SOURCES:
-        obj = BUILD_DIR / (Path(src).stem + ".hip.o")
-        _run([hipcc, *HIPCC_FLAGS, "-I", str(CSRC), "-c", str(CSRC / src), "-o", str(obj)])
+        obj = BUILD_DIR / (Path(src).stem + (".stamps" if stamps else "") + ".hip.o")
+        _run([hipcc, *HIPCC_FLAGS, *(["-DCM_STAMPS"] if stamps else []), "-I", str(CSRC), "-c", str(CSRC / src),
+              "-o", str(obj)])
         objs.append(str(obj))
     for src in HOST_SOURCES:
         obj = BUILD_DIR / (Path(src).stem + ".o")
         _run(["g++", *GXX_FLAGS, "-I", str(CSRC), "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(str(obj))
-    tmp = LIB.with_suffix(".so.tmp")
+    out = STAMPS_LIB if stamps else LIB
+    tmp = out.with_suffix(".so.tmp")
     _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-pthread", *objs, "-o", str(tmp)])
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {out}")
+    return out
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, stamps="--stamps" in sys.argv[1:])

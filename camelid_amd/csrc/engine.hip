@@ -461,23 +461,24 @@ void launch_gemv(const Q8Mat& m, const int8_t* xq, const float* xs, float* y, co
 }
 
 // y = W · rmsnorm(x; nw) for a Q8_0 W whose width is a fused-norm width (2048, 3072, 4096):
-// at most 32 rows per workgroup, spread over up to 256 workgroups.
+// at most 32 rows per workgroup, spread over up to 256 workgroups; the 8 weight waves hold
+// ceil(rows per workgroup / 8) rows each.
 void launch_gemv_norm(const Q8Mat& m, const float* x, const float* nw, float eps, float* y, hipStream_t s) {
   const uint32_t per = std::min(32u, std::max(1u, (m.rows + 255u) / 256u));
   const uint32_t grid = (m.rows + per - 1) / per;
-  switch (m.k) {
-#define CM_GN(K)                                                                                                    \
-  case K:                                                                                                           \
-    if (per > 16)                                                                                                   \
-      CM_LAUNCH((cm::k_gemv_norm<K, 2>), dim3(grid), dim3(cm::GN_NT), 0, s, m.q, m.d, (int)m.rows, (int)per, x, nw, \
-                eps, y);                                                                                            \
-    else                                                                                                            \
-      CM_LAUNCH((cm::k_gemv_norm<K, 1>), dim3(grid), dim3(cm::GN_NT), 0, s, m.q, m.d, (int)m.rows, (int)per, x, nw, \
-                eps, y);                                                                                            \
+  const uint32_t rpw = (per + 7) / 8;
+  switch (m.k * 8 + rpw) {
+#define CM_GN(K, RPW)                                                                                                 \
+  case K * 8 + RPW:                                                                                                   \
+    CM_LAUNCH((cm::k_gemv_norm<K, RPW>), dim3(grid), dim3(cm::GN_NT), 0, s, m.q, m.d, (int)m.rows, (int)per, x, nw, \
+              eps, y);                                                                                                \
     return;
-    CM_GN(2048) CM_GN(3072) CM_GN(4096)
+    CM_GN(2048, 1) CM_GN(2048, 2) CM_GN(2048, 3) CM_GN(2048, 4)
+    CM_GN(3072, 1) CM_GN(3072, 2) CM_GN(3072, 3) CM_GN(3072, 4)
+    CM_GN(4096, 1) CM_GN(4096, 2) CM_GN(4096, 3) CM_GN(4096, 4)
 #undef CM_GN
-    default:  // not reached: callers admit only these widths (cm::gu_fused_k)
+    default:  // not reached: callers admit only these widths (cm::gu_fused_k), per <= 32
+      g_launch_error = "qkv GEMV: no kernel for row width " + std::to_string(m.k);
       break;
   }
 }
@@ -1753,6 +1754,34 @@ int camelid_hip_profile_end(camelid_hip_engine* e, double* ms, double* bytes, ui
   return 0;
 }
 
+#define G_TRY(expr)                                                                                    \
+  do {                                                                                                 \
+    hipError_t _st = (expr);                                                                           \
+    if (_st != hipSuccess) return fail(nullptr, std::string(#expr) + ": " + hipGetErrorString(_st)); \
+  } while (0)
+
+int camelid_hip_phase_stamps(uint64_t* out, size_t n, size_t* n_out) {
+  if (!out || !n_out) return fail(nullptr, "null argument");
+  const size_t na = (size_t)cm::ATT_STAMP_LAYERS * cm::ATT_STAMP_HEADS * cm::ATT_NSTAMP;
+  const size_t ng = (size_t)2 * cm::GEMV_STAMP_WGS * cm::GEMV_NSTAMP;
+  const size_t total = na + ng;
+#ifdef CM_STAMPS
+  G_TRY(hipDeviceSynchronize());
+  const size_t m1 = std::min(n, na), m2 = std::min(n - m1, ng);
+  G_TRY(hipMemcpyFromSymbol(out, HIP_SYMBOL(cm::g_att_stamps), m1 * sizeof(uint64_t), 0, hipMemcpyDeviceToHost));
+  if (m2)
+    G_TRY(hipMemcpyFromSymbol(out + m1, HIP_SYMBOL(cm::g_gemv_stamps), m2 * sizeof(uint64_t), 0,
+                              hipMemcpyDeviceToHost));
+  *n_out = m1 + m2;
+  return 0;
+#else
+  (void)n;
+  (void)total;
+  *n_out = 0;
+  return fail(nullptr, "phase stamps are recorded only by the measurement build (libcamelid_hip_stamps.so)");
+#endif
+}
+
 int camelid_hip_device_info(char* name, size_t name_len, int* n_cu) {
   int dev = 0;
   if (const char* s = std::getenv("CAMELID_HIP_DEVICE")) dev = std::atoi(s);
@@ -1765,11 +1794,6 @@ int camelid_hip_device_info(char* name, size_t name_len, int* n_cu) {
 }
 
 // ------------------------------------------------------------------ kernel-level ABI
-#define G_TRY(expr)                                                                                    \
-  do {                                                                                                 \
-    hipError_t _st = (expr);                                                                           \
-    if (_st != hipSuccess) return fail(nullptr, std::string(#expr) + ": " + hipGetErrorString(_st)); \
-  } while (0)
 
 int camelid_hip_malloc(void** ptr, size_t bytes) {
   if (!ptr) return fail(nullptr, "null argument");
@@ -2003,7 +2027,7 @@ int camelid_hip_gate_up_silu(const int8_t* wq, const uint16_t* wd, uint32_t ffn,
                              void* stream) {
   if (!wq || !wd || !aq || !as || (x ? !nw : (!xq || !xs))) return fail(nullptr, "null argument");
   if (!cm::gu_fused_k((int)k) || ffn == 0 || ffn % 32) return fail(nullptr, "k must be 2048, 3072 or 4096; ffn a nonzero multiple of 32");
-  if (x && !cm::gu_norm_k((int)k)) return fail(nullptr, "the in-kernel RMSNorm takes k = 2048 or 3072");
+  if (x && !cm::gu_norm_k((int)k)) return fail(nullptr, "the in-kernel RMSNorm takes k = 2048, 3072 or 4096");
   const hipStream_t s = (hipStream_t)stream;
   switch (k) {
 #define CM_GU(K)                                                                                                   \

@@ -431,8 +431,43 @@ __device__ __forceinline__ double dpp_f64(double x) {
     cnt += cp;                                                                                              \
   }
 
-template <int NT, int C>
-__device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const float* v, int n, FsLds<NT>& fs) {
+// Barrier policies of the one-pass sum and the in-kernel norm: the whole workgroup
+// (__syncthreads), or a team of the workgroup's first waves synchronising through an LDS
+// counter (TeamBar), so that the other waves can stream weights meanwhile without taking part.
+struct WgBar {
+  __device__ __forceinline__ void operator()() const { __syncthreads(); }
+};
+
+// Software barrier of waves 0 .. nw-1 (threads 0 .. 64*nw-1) of a workgroup.  `ctr` is a
+// zeroed LDS word (zeroed before a workgroup barrier that precedes the first use); each call
+// adds one per wave and waits, with the team's LDS writes made visible first, until every
+// team wave has arrived.  The wait is bounded: past about 2^22 polls (far beyond any
+// schedule) the call returns with *bad set, so a broken schedule cannot hang the device; the
+// caller then takes its fallback.
+struct TeamBar {
+  uint32_t* ctr;
+  uint32_t* bad;
+  uint32_t nw;
+  uint32_t target;
+  __device__ __forceinline__ void operator()() {
+    target += nw;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    uint32_t polls = 0;
+    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++polls == (1u << 22)) {
+        *bad = 1u;
+        break;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  }
+};
+
+template <int NT, int C, typename Bar = WgBar>
+__device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const float* v, int n, FsLds<NT>& fs,
+                                                     Bar&& bar = Bar{}) {
   constexpr int NW = NT / 64;
   static_assert(NT % 64 == 0 && NW <= 16 && C <= 32, "one 16-lane row holds the wave totals");
   double* sh_r = fs.r;
@@ -457,7 +492,7 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
   incl += dpp_f64<0x143, 0xc>(incl);  // row_bcast:31
   if (lane == 63) sh_r[wave] = incl;
   double R = dpp_f64<0x138, 0xf>(incl);  // wave_shr:1 -> exclusive
-  __syncthreads();
+  bar();
   if (NW > 1) {
     double wt = lane < NW ? sh_r[lane] : 0.0;
     wt += dpp_f64<0x111, 0xf>(wt);
@@ -507,7 +542,7 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
   }
   uint32_t run = CM_DPP(b, 0x138, 0xf), pos = CM_DPP(cnt, 0x138, 0xf);
   const uint32_t rs_x = CM_DPP(rs, 0x138, 0xf);
-  __syncthreads();
+  bar();
   uint32_t total;
   {
     const uint32_t wr = lane < NW ? sh_rs[lane] : 0u, wbv = lane < NW ? sh_b[lane] : 0u,
@@ -550,7 +585,7 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
     sh_end[1] = lo;
     sh_end[2] = lim;
   }
-  __syncthreads();
+  bar();
   if (wave == 0) {  // replay, branch-free per step: the sum's chain is one integer and one f32 add
     const int tot = __builtin_amdgcn_readfirstlane((int)total);
     float s = 0.0f;
@@ -578,7 +613,7 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
     if (bad) s = fold_lds_lean(v, n);
     if (lane == 0) sh_sum = s;
   }
-  __syncthreads();
+  bar();
   return sh_sum;
 }
 #undef CM_FS_STEP
@@ -592,6 +627,35 @@ __device__ __forceinline__ float fold_lds_n(const float* p, float acc = 0.0f) {
   int n = N;
   asm volatile("" : "+s"(n));
   return fold_lds(p, n, acc);
+}
+
+// Serial fold in index order of N terms spaced `stride` floats apart in LDS (one lane; the
+// block-major term layout [block][row] of the norm-fused GEMVs, whose lanes - one per row -
+// then read consecutive words).  Reads run 8 terms ahead of the dependent add chain.
+template <int N>
+__device__ __forceinline__ float fold_lds_strided(const float* p, int stride) {
+  static_assert(N % 8 == 0 && N >= 8, "strided fold length must be a multiple of 8");
+  float a[8], b[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) a[u] = p[u * stride];
+  float acc = 0.0f;
+  int n = N;
+  asm volatile("" : "+s"(n));  // keep the fold a loop (registers set the occupancy)
+#pragma unroll 1
+  for (int base = 8; base < n; base += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) b[u] = p[(base + u) * stride];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      acc += a[u];
+      a[u] = b[u];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int u = 0; u < 8; ++u) acc += a[u];
+  return acc;
 }
 
 // Lane-pair exchange (xor 1) through DPP quad_perm [1,0,3,2]; all lanes must be active.
@@ -610,6 +674,34 @@ __device__ __forceinline__ float quantize_lane32(float v, int8_t* q) {
   float r = roundf(v * inv);
   r = fminf(fmaxf(r, -128.0f), 127.0f);
   *q = (int8_t)r;
+  return scale;
+}
+
+// Q8_0 quantization of one 32-value block held 8 values per lane by a quad of lanes (lanes
+// 4b..4b+3, values 8j..8j+7 in lane 4b+j; all four lanes active): the block's absolute
+// maximum by two quad exchanges (exact), then each lane quantizes its 8 values; returns the
+// f16-valued scale (every lane of the quad), packs the 8 quants into q[0..1].
+// inference.rs:16953-16971.
+__device__ __forceinline__ float quantize_quad8(const float (&y)[8], uint32_t (&q)[2]) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(y[e]));
+  amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0xB1, 0xF, 0xF, false)));  // xor 1
+  amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0x4E, 0xF, 0xF, false)));  // xor 2
+  const float unrounded = amax / 127.0f;
+  const float scale = f16_bits_to_f32(f32_to_f16_bits(unrounded));
+  const float inv = unrounded == 0.0f ? 0.0f : 1.0f / unrounded;
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float r = roundf(y[w * 4 + e] * inv);
+      r = fminf(fmaxf(r, -128.0f), 127.0f);
+      word |= ((uint32_t)(int32_t)r & 0xffu) << (8 * e);
+    }
+    q[w] = word;
+  }
   return scale;
 }
 
@@ -894,28 +986,35 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv(const int8_t* __restrict__ wq,
 
 // ---------------------------------------------------------------------------
 // RMSNorm fused into the GEMV that consumes it: every workgroup normalises the activation
-// itself (the arithmetic of k_rmsnorm_quant) into LDS while its weight loads are in flight,
-// so the norm needs no launch of its own and its latency overlaps the weight stream.
+// itself (the arithmetic of k_rmsnorm_quant) into LDS, so the norm needs no launch of its own.
+// The workgroup splits into two teams.  The norm team (waves 0..GN_TEAM/64-1) loads x and the
+// norm weights first, computes the norm with team-only synchronisation (TeamBar) and only
+// then loads its own weight rows; the other waves issue all their weight loads at once.  The
+// CU's share of HBM bandwidth, not the norm, then sets the kernel's time: a wave that issues
+// into a full memory queue stalls, but no norm barrier waits for the weight waves.
 constexpr int GN_NT = 1024;
-#ifndef CM_GU_PRE
-#define CM_GU_PRE 1
-#endif
-#ifndef CM_GN_PRE
-#define CM_GN_PRE 1
-#endif
-constexpr int GU_PRE = CM_GU_PRE;  // rows per wave loaded before the in-kernel norm (gate/up)
-constexpr int GN_PRE = CM_GN_PRE;  // the same for k_gemv_norm
+constexpr int GN_TEAM = 256;      // threads of the gate/up kernel's norm team
+constexpr int GN_TEAM_QKV = 512;  // threads of the qkv kernel's norm team (its weight waves hold every row)
 
-// RMSNorm of x (n values, global) with weights w (tensor/mod.rs:2083-2106), Q8_0-quantized
-// into LDS: xl (n quants), xsl (n/32 scales); yl: NT*C floats of LDS.  Thread t holds the
-// C consecutive values t*C.. (the layout of inorder_sum_onepass).  norm_load issues the
-// loads and ends with a barrier, so that every wave's norm loads enter the CU's memory
-// pipeline ahead of any weight load (the pipeline serves the workgroup's requests in
-// order; the norm must not wait behind the weights); norm_q8_lds computes.  The whole
-// workgroup calls both; norm_q8_lds ends with a barrier.
+// Phase timestamps of the two norm-fused GEMVs (measurement build only, as g_att_stamps):
+// kind 0 k_gemv_norm, 1 k_gemv_gu_silu; per workgroup (< 256; the last launch overwrites):
+// 0 start (thread 0), 1 norm done (thread 0), 2 a weight wave's loads issued (thread 256),
+// 3 past the workgroup barrier after the norm, 4 block dots done, 5 end.
+constexpr int GEMV_NSTAMP = 8, GEMV_STAMP_WGS = 256;
+#ifdef CM_STAMPS
+__device__ uint64_t g_gemv_stamps[2 * GEMV_STAMP_WGS * GEMV_NSTAMP];
+#define CM_GEMV_STAMP(kind, i, t)                                                                        \
+  if (threadIdx.x == (t) && blockIdx.x < GEMV_STAMP_WGS)                                                 \
+    g_gemv_stamps[((kind) * GEMV_STAMP_WGS + blockIdx.x) * GEMV_NSTAMP + (i)] = __builtin_amdgcn_s_memrealtime();
+#else
+#define CM_GEMV_STAMP(kind, i, t)
+#endif
+
+// The norm team's share of x and w: thread t holds the C consecutive values t*C.. (the layout
+// of inorder_sum_onepass).
 template <int C>
-__device__ __forceinline__ void norm_load(const float* __restrict__ x, const float* __restrict__ w, int n,
-                                          float (&xv)[C], float (&wv)[C]) {
+__device__ __forceinline__ void norm_load_team(const float* __restrict__ x, const float* __restrict__ w, int n,
+                                               float (&xv)[C], float (&wv)[C]) {
   const int i0 = threadIdx.x * C;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
@@ -923,72 +1022,120 @@ __device__ __forceinline__ void norm_load(const float* __restrict__ x, const flo
     xv[c] = in ? x[i0 + c] : 0.0f;
     wv[c] = in ? w[i0 + c] : 0.0f;
   }
-  __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the caller's next ones
-  __builtin_amdgcn_s_barrier();       // (issued, not completed: no wait on the loads)
-  __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int NT, int C>
-__device__ __forceinline__ void norm_q8_lds(const float (&xv)[C], const float (&wv)[C], int n, float eps,
-                                            int8_t* xl, float* xsl, float* yl, FsLds<NT>& fs) {
+// The RMSNorm's scale (tensor/mod.rs:2083-2106): the in-order sum of the squares of the n
+// values xv (thread t holds t*C..), scale = 1/sqrt(ss/n + eps), written to *s_scale by thread
+// 0.  Called by the NT threads that hold the values, synchronised by `bar` (the whole
+// workgroup or a TeamBar; no bar() after the sum: the caller's workgroup barrier publishes
+// the scale).  x and w are also copied to the LDS arrays xf and wf for norm_quantize_all; yl
+// (NT*C floats) holds the squares for the sum's fallback.
+template <int NT, int C, typename Bar = WgBar>
+__device__ __forceinline__ void norm_scale(const float (&xv)[C], const float (&wv)[C], int n, float eps, float* xf,
+                                           float* wf, float* yl, FsLds<NT>& fs, float* s_scale, Bar&& bar = Bar{},
+                                           int stamp_kind = -1) {
   const int tid = threadIdx.x, i0 = tid * C;
+  (void)stamp_kind;
   float t[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     t[c] = xv[c] * xv[c];
-    if (i0 + c < n) yl[i0 + c] = t[c];  // the sum's fallback reads the squares here
-  }
-  const float ss = inorder_sum_onepass<NT, C>(t, yl, n, fs);
-  const float scale = 1.0f / sqrtf(ss / (float)n + eps);
-#pragma unroll
-  for (int c = 0; c < C; ++c)
-    if (i0 + c < n) yl[i0 + c] = (xv[c] * scale) * wv[c];
-  __syncthreads();
-  for (int b = tid; b < (n >> 5); b += NT) {
-    float y[32];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float4 v = reinterpret_cast<const float4*>(yl + b * 32)[u];
-      y[u * 4] = v.x;
-      y[u * 4 + 1] = v.y;
-      y[u * 4 + 2] = v.z;
-      y[u * 4 + 3] = v.w;
+    if (i0 + c < n) {
+      yl[i0 + c] = t[c];  // the sum's fallback reads the squares here
+      xf[i0 + c] = xv[c];
+      wf[i0 + c] = wv[c];
     }
-    uint32_t packed[8];
-    xsl[b] = quantize_block_regs(y, packed);
-    uint4* qp = reinterpret_cast<uint4*>(xl + b * 32);
-    qp[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-    qp[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
   }
-  __syncthreads();
+  if (stamp_kind >= 0) {
+    CM_GEMV_STAMP(stamp_kind, 6, 0)  // (the measurement build: x and w have arrived)
+  }
+  const float ss = inorder_sum_onepass<NT, C>(t, yl, n, fs, bar);
+  if (tid == 0) *s_scale = 1.0f / sqrtf(ss / (float)n + eps);
+  if (stamp_kind >= 0) {
+    CM_GEMV_STAMP(stamp_kind, 7, 0)  // the sum of squares is known
+  }
 }
 
+// The normalised values y = (x * scale) * w of xf/wf (LDS, 16-byte aligned, n % 32 == 0),
+// Q8_0-quantized into LDS (xl: n quants, xsl: n/32 scales) by the whole workgroup (NTALL
+// threads, a multiple of 64): each quad of lanes quantizes one 32-value block, 8 values per
+// lane (quantize_quad8).  The caller synchronises before (scale, xf, wf written) and after
+// (xl, xsl read).
+template <int NTALL>
+__device__ __forceinline__ void norm_quantize_all(const float* xf, const float* wf, int n, float scale, int8_t* xl,
+                                                  float* xsl) {
+  for (int p = threadIdx.x; p < (n >> 3); p += NTALL) {  // (uniform per quad: n % 32 == 0)
+    const float4* xp = reinterpret_cast<const float4*>(xf) + 2 * p;
+    const float4* wp = reinterpret_cast<const float4*>(wf) + 2 * p;
+    const float4 x0 = xp[0], x1 = xp[1], w0 = wp[0], w1 = wp[1];
+    const float y[8] = {(x0.x * scale) * w0.x, (x0.y * scale) * w0.y, (x0.z * scale) * w0.z, (x0.w * scale) * w0.w,
+                        (x1.x * scale) * w1.x, (x1.y * scale) * w1.y, (x1.z * scale) * w1.z, (x1.w * scale) * w1.w};
+    uint32_t q[2];
+    const float d = quantize_quad8(y, q);
+    reinterpret_cast<uint2*>(xl)[p] = make_uint2(q[0], q[1]);
+    if ((p & 3) == 0) xsl[p >> 2] = d;
+  }
+}
+
+// The norm team's LDS: its counter and failure word (TeamBar), its one-pass-sum workspace.
+template <int NTEAM>
+struct NormTeamLds {
+  uint32_t ctr;
+  uint32_t bad;
+  float scale;
+  FsLds<NTEAM> fs;
+};
+
+// Row stride of the block-major term layout [block][row] of the norm-fused GEMVs: an odd word
+// count, so that the lanes writing one row's terms (one block each) and the lanes folding the
+// rows (one row each) both touch distinct LDS banks.
+__host__ __device__ constexpr int gemv_row_stride(int rows) { return rows | 1; }
+
 // y = W · rmsnorm(x) for a Q8_0 W [rows][K]: workgroup b takes rows b*rows_per_wg .. (at most
-// 16 * RPW; wave w the local rows w, w + 16, ..), issues its weight loads, computes the norm,
-// then the same per-row block dots and in-order folds as k_gemv_k.
+// 8 * RPW, all held by the 8 weight waves): the norm team (8 waves) computes the norm while
+// the weight waves' loads stream, then the same per-row block dots and in-order folds as
+// k_gemv_k.
 template <int K, int RPW>
 __global__ __launch_bounds__(GN_NT) void k_gemv_norm(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                      int rows, int rows_per_wg, const float* __restrict__ x,
                                                      const float* __restrict__ nw, float eps, float* __restrict__ y) {
-  constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64, STRIDE = gemv_term_stride(NB);
-  constexpr int NWV = GN_NT / 64, R = NWV * RPW, C = (K + GN_NT - 1) / GN_NT;
+  constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64;
+  constexpr int NT = GN_TEAM_QKV;  // the norm team: waves 0..TW-1; waves TW.. hold the rows
+  constexpr int NWV = GN_NT / 64, R = NWV * RPW, C = (K + NT - 1) / NT, TW = NT / 64;
+  constexpr int RS = gemv_row_stride(R);  // terms block-major: t[block * RS + slot]
   __shared__ __align__(16) int8_t xl[K];
   __shared__ __align__(16) float xsl[NB];
-  __shared__ __align__(16) float t[R * STRIDE];
-  __shared__ __align__(16) float yl[GN_NT * C];
-  __shared__ FsLds<GN_NT> fs;
+  __shared__ __align__(16) float t[NB * RS];
+  __shared__ __align__(16) float yl[NT * C];
+  __shared__ __align__(16) float xf[NT * C];
+  __shared__ __align__(16) float wf[NT * C];
+  __shared__ NormTeamLds<NT> team;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const bool in_team = wave < TW;  // (wave-uniform)
   const int row0 = blockIdx.x * rows_per_wg;
   const int nrows = min(rows_per_wg, rows - row0);
-  // the norm's inputs, then the weights and their scales
+  CM_GEMV_STAMP(0, 0, 0)
   float nxv[C], nwv[C];
-  norm_load<C>(x, nw, K, nxv, nwv);
+  if (in_team) norm_load_team<C>(x, nw, K, nxv, nwv);
+  if (tid == 0) {
+    team.ctr = 0u;
+    team.bad = 0u;
+  }
+  // the norm's loads are issued ahead of every weight load; the team counter is zeroed
+  __syncthreads();
+  // local row slots: the weight waves' first (slot (wave - TW) + k (NWV - TW)), the norm
+  // team's last, so that rows_per_wg <= (NWV - TW) * RPW rows all stream during the norm;
+  // slots past nrows load nothing and store nothing
+  auto slot_of = [&](int k) {
+    return in_team ? (NWV - TW) * RPW + wave + TW * k : (wave - TW) + (NWV - TW) * k;
+  };
   int4 wv[RPW][IT];
   uint16_t dv[RPW][IT];
   auto load_row = [&](int k) {
-    const int row = row0 + min(wave + NWV * k, nrows - 1);  // surplus local rows repeat the last one
-    const int4* w4 = reinterpret_cast<const int4*>(wq + (size_t)row * K);
-    const uint16_t* d = wd + (size_t)row * NB;
+    const int sl = slot_of(k);
+    if (sl >= nrows) return;  // (wave-uniform)
+    const int4* w4 = reinterpret_cast<const int4*>(wq + (size_t)(row0 + sl) * K);
+    const uint16_t* d = wd + (size_t)(row0 + sl) * NB;
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int c = min(lane + 64 * i, CPR - 1);
@@ -996,15 +1143,21 @@ __global__ __launch_bounds__(GN_NT) void k_gemv_norm(const int8_t* __restrict__ 
       dv[k][i] = d[c >> 1];
     }
   };
-  constexpr int PRE = GN_PRE < RPW ? GN_PRE : RPW;  // rows loaded before the norm, as in k_gemv_gu_silu
+  if (in_team) {
+    norm_scale<NT, C>(nxv, nwv, K, eps, xf, wf, yl, team.fs, &team.scale, TeamBar{&team.ctr, &team.bad, TW, 0u}, 0);
+    CM_GEMV_STAMP(0, 1, 0)
+  }
 #pragma unroll
-  for (int k = 0; k < PRE; ++k) load_row(k);
-  norm_q8_lds<GN_NT, C>(nxv, nwv, K, eps, xl, xsl, yl, fs);
-#pragma unroll
-  for (int k = PRE; k < RPW; ++k) load_row(k);
+  for (int k = 0; k < RPW; ++k) load_row(k);
+  CM_GEMV_STAMP(0, 2, NT)
+  __syncthreads();  // the scale and x, w are in LDS for every wave
+  norm_quantize_all<GN_NT>(xf, wf, K, team.scale, xl, xsl);
+  __syncthreads();  // the normalised activation (Q8_0) is in LDS
+  CM_GEMV_STAMP(0, 3, 0)
 #pragma unroll
   for (int k = 0; k < RPW; ++k) {
-    float* tr = t + (wave + NWV * k) * STRIDE;
+    const int sl = slot_of(k);
+    if (sl >= nrows) continue;  // (wave-uniform)
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       __builtin_amdgcn_sched_barrier(0);
@@ -1012,11 +1165,14 @@ __global__ __launch_bounds__(GN_NT) void k_gemv_norm(const int8_t* __restrict__ 
       const int cc = min(c, CPR - 1);
       int sacc = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
       sacc += dpp_xor1(sacc);
-      if ((lane & 1) == 0 && c < CPR) tr[c >> 1] = ((float)sacc * half_bits_to_float(dv[k][i])) * xsl[c >> 1];
+      if ((lane & 1) == 0 && c < CPR)
+        t[(c >> 1) * RS + sl] = ((float)sacc * half_bits_to_float(dv[k][i])) * xsl[c >> 1];
     }
   }
+  CM_GEMV_STAMP(0, 4, 0)
   __syncthreads();
-  if (tid < nrows) y[row0 + tid] = fold_lds_n<NB>(t + tid * STRIDE);
+  if (tid < nrows) y[row0 + tid] = team.bad ? __builtin_nanf("") : fold_lds_strided<NB>(t + tid, RS);
+  CM_GEMV_STAMP(0, 5, 0)
 }
 
 // Gate/up projection fused with SwiGLU (tensor/mod.rs:1943-1967) and the Q8_0 quantization
@@ -1027,37 +1183,61 @@ __global__ __launch_bounds__(GN_NT) void k_gemv_norm(const int8_t* __restrict__ 
 constexpr int GU_NT = 512;
 constexpr int GU_ROWS = 64;  // rows per workgroup: 32 gate + 32 up
 __host__ __device__ constexpr bool gu_fused_k(int K) { return K == 2048 || K == 3072 || K == 4096; }
-// widths whose gate/up kernel also takes the RMSNorm (at 4096 the 1024-thread kernel would
-// spill registers)
-__host__ __device__ constexpr bool gu_norm_k(int K) { return K == 2048 || K == 3072; }
+// widths whose gate/up kernel also takes the RMSNorm
+__host__ __device__ constexpr bool gu_norm_k(int K) { return K == 2048 || K == 3072 || K == 4096; }
 
 // NORM: the activation is the RMSNorm of x (weights nw), computed by every workgroup in its
-// prologue (norm_q8_lds) instead of read quantized from xq/xs.
+// prologue (norm_scale by the norm team, norm_quantize_all) instead of read quantized from
+// xq/xs.
 template <int K, int NT, bool NORM>
 __global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                     const int8_t* __restrict__ xq, const float* __restrict__ xs,
                                                     const float* __restrict__ x, const float* __restrict__ nw,
                                                     float eps, int8_t* __restrict__ aq, float* __restrict__ as) {
-  constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64, STRIDE = gemv_term_stride(NB);
-  constexpr int RPW = GU_ROWS / (NT / 64);  // 8 rows per wave at 512 threads, 4 at 1024
-  constexpr int C = (K + NT - 1) / NT;      // norm values per thread
-  static_assert(NB % 4 == 0 && GU_ROWS % (NT / 64) == 0, "compile-time GEMV widths are multiples of 128");
+  constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64;
+  constexpr int RS = gemv_row_stride(GU_ROWS);  // terms block-major: t[block * RS + row]
+  // row slots per wave: 8 at 512 threads; with NORM the weight waves' slots come first (up to
+  // K = 3072 six each: all 64 rows stream during the norm; at 4096, where six rows of
+  // registers do not fit, four each and the norm team's slots take the last 16 rows)
+  constexpr int TW = NORM ? GN_TEAM / 64 : 0;  // norm-team waves
+  constexpr int NWW = NT / 64 - TW;           // weight waves
+  constexpr int RPW = NORM ? (K <= 3072 ? 6 : 4) : GU_ROWS / (NT / 64);
+  constexpr int CT = (K + GN_TEAM - 1) / GN_TEAM;  // norm values per norm-team thread
+  static_assert(NB % 4 == 0 && (NORM || GU_ROWS % (NT / 64) == 0), "compile-time GEMV widths are multiples of 128");
   __shared__ __align__(16) int8_t xl[K];
   __shared__ __align__(16) float xsl[NB];
-  __shared__ __align__(16) float t[GU_ROWS * STRIDE];
+  __shared__ __align__(16) float t[NB * RS];
   __shared__ __align__(16) float vals[GU_ROWS];
-  __shared__ __align__(16) float yl[NORM ? NT * C : 4];
+  __shared__ __align__(16) float yl[NORM ? GN_TEAM * CT : 4];
+  __shared__ __align__(16) float xf[NORM ? GN_TEAM * CT : 4];
+  __shared__ __align__(16) float wf[NORM ? GN_TEAM * CT : 4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const bool in_team = NORM && wave < GN_TEAM / 64;  // (wave-uniform) the norm team, as in k_gemv_norm
   const size_t row0 = (size_t)blockIdx.x * GU_ROWS;
-  float nxv[NORM ? C : 1], nwv[NORM ? C : 1];
-  if constexpr (NORM) norm_load<C>(x, nw, K, nxv, nwv);  // ahead of the weights
-  // the wave's weight and scale loads: all up front, or with NORM the first GU_PRE rows
-  // before the norm and the rest after it (a wave stalls when it issues into a full memory
-  // queue, and the norm's barriers would wait for it)
+  float nxv[NORM ? CT : 1], nwv[NORM ? CT : 1];
+  __shared__ NormTeamLds<GN_TEAM> team;
+  CM_GEMV_STAMP(1, 0, 0)
+  if constexpr (NORM) {
+    if (in_team) norm_load_team<CT>(x, nw, K, nxv, nwv);
+    if (tid == 0) {
+      team.ctr = 0u;
+      team.bad = 0u;
+    }
+    __syncthreads();  // the norm's loads ahead of every weight load; the team counter zeroed
+  }
+  // the wave's weight and scale loads: all up front; the norm team's after its norm
   int4 wv[RPW][IT];
   uint16_t dv[RPW][IT];
+  // local row of slot k of this wave (-1: none): rows wave*RPW + k without NORM; with NORM the
+  // weight waves' slots (wave - TW) + NWW k, then the norm team's NWW RPW + wave + TW k
+  auto row_of = [&](int k) {
+    const int r = NORM ? (in_team ? NWW * RPW + wave + TW * k : (wave - TW) + NWW * k) : wave * RPW + k;
+    return r < GU_ROWS ? r : -1;
+  };
   auto load_row = [&](int k) {
-    const size_t row = row0 + wave * RPW + k;
+    const int lr = row_of(k);
+    if (lr < 0) return;  // (wave-uniform)
+    const size_t row = row0 + lr;
     const int4* w4 = reinterpret_cast<const int4*>(wq + row * K);
     const uint16_t* d = wd + row * NB;
 #pragma unroll
@@ -1067,22 +1247,30 @@ __global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ 
       dv[k][i] = d[c >> 1];
     }
   };
-  constexpr int PRE = NORM ? (GU_PRE < RPW ? GU_PRE : RPW) : RPW;
-#pragma unroll
-  for (int k = 0; k < PRE; ++k) load_row(k);
   if constexpr (NORM) {
-    __shared__ FsLds<NT> fs;
-    norm_q8_lds<NT, C>(nxv, nwv, K, eps, xl, xsl, yl, fs);
+    if (in_team) {
+      norm_scale<GN_TEAM, CT>(nxv, nwv, K, eps, xf, wf, yl, team.fs, &team.scale,
+                              TeamBar{&team.ctr, &team.bad, GN_TEAM / 64, 0u}, 1);
+      CM_GEMV_STAMP(1, 1, 0)
+    }
 #pragma unroll
-    for (int k = PRE; k < RPW; ++k) load_row(k);
+    for (int k = 0; k < RPW; ++k) load_row(k);
+    CM_GEMV_STAMP(1, 2, GN_TEAM)
+    __syncthreads();  // the scale and x, w are in LDS for every wave
+    norm_quantize_all<NT>(xf, wf, K, team.scale, xl, xsl);
+    __syncthreads();  // the normalised activation (Q8_0) is in LDS
+    CM_GEMV_STAMP(1, 3, 0)
   } else {
+#pragma unroll
+    for (int k = 0; k < RPW; ++k) load_row(k);
     for (int c = tid; c < CPR; c += NT) reinterpret_cast<int4*>(xl)[c] = reinterpret_cast<const int4*>(xq)[c];
     for (int b = tid; b < NB; b += NT) xsl[b] = xs[b];
     __syncthreads();
   }
 #pragma unroll
   for (int k = 0; k < RPW; ++k) {
-    float* tr = t + (wave * RPW + k) * STRIDE;
+    const int lr = row_of(k);
+    if (lr < 0) continue;  // (wave-uniform)
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       __builtin_amdgcn_sched_barrier(0);
@@ -1090,30 +1278,22 @@ __global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ 
       const int cc = min(c, CPR - 1);
       int sacc = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
       sacc += dpp_xor1(sacc);
-      if ((lane & 1) == 0 && c < CPR) tr[c >> 1] = ((float)sacc * half_bits_to_float(dv[k][i])) * xsl[c >> 1];
+      if ((lane & 1) == 0 && c < CPR)
+        t[(c >> 1) * RS + lr] = ((float)sacc * half_bits_to_float(dv[k][i])) * xsl[c >> 1];
     }
   }
+  CM_GEMV_STAMP(1, 4, 0)
   __syncthreads();
-  if (tid < GU_ROWS) vals[tid] = fold_lds_n<NB>(t + tid * STRIDE);  // one lane per row
+  if (tid < GU_ROWS)  // one lane per row
+    vals[tid] = NORM && team.bad ? __builtin_nanf("") : fold_lds_strided<NB>(t + tid, RS);
   __syncthreads();
-  if (tid < 32) vals[tid] = silu_mul1(vals[tid], vals[32 + tid]);
-  __syncthreads();
-  if (tid == 0) {  // the block's quantization, from registers
-    float y[32];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float4 v = reinterpret_cast<const float4*>(vals)[u];
-      y[u * 4] = v.x;
-      y[u * 4 + 1] = v.y;
-      y[u * 4 + 2] = v.z;
-      y[u * 4 + 3] = v.w;
-    }
-    uint32_t packed[8];
-    as[blockIdx.x] = quantize_block_regs(y, packed);
-    uint4* qp = reinterpret_cast<uint4*>(aq + (size_t)blockIdx.x * 32);
-    qp[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-    qp[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+  if (tid < 32) {  // SwiGLU and the block's Q8_0 quantization, one value per lane
+    int8_t q;
+    const float d = quantize_lane32(silu_mul1(vals[tid], vals[32 + tid]), &q);
+    aq[(size_t)blockIdx.x * 32 + tid] = q;
+    if (tid == 0) as[blockIdx.x] = d;
   }
+  CM_GEMV_STAMP(1, 5, 0)
 }
 
 // Decode-loop state shared by the step's kernels (device memory).
@@ -1495,6 +1675,25 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, i
 }
 
 // ---------------------------------------------------------------------------
+// Phase timestamps of the decode attention, compiled only into the measurement build
+// (-DCM_STAMPS, libcamelid_hip_stamps.so): thread 0 of head h's workgroup in layer l records
+// the 100 MHz real-time counter at each phase boundary into g_att_stamps[l][h][i]
+// (camelid_hip_phase_stamps reads them).  Phases: 0 start, 1 q/k/v built and K/V stored,
+// 2 scores and their maximum, 3 exponentials, 4 denominator, 5 output sums, 6 end.
+constexpr int ATT_NSTAMP = 7;
+constexpr int ATT_STAMP_LAYERS = 64, ATT_STAMP_HEADS = 64;
+#ifdef CM_STAMPS
+__device__ uint64_t g_att_stamps[ATT_STAMP_LAYERS * ATT_STAMP_HEADS * ATT_NSTAMP];
+#endif
+#ifdef CM_STAMPS
+#define CM_ATT_STAMP(i)                                                                                 \
+  if (tid == 0 && layer < ATT_STAMP_LAYERS && h < ATT_STAMP_HEADS)                                      \
+    g_att_stamps[((size_t)layer * ATT_STAMP_HEADS + h) * ATT_NSTAMP + (i)] = __builtin_amdgcn_s_memrealtime();
+#else
+#define CM_ATT_STAMP(i)
+#endif
+
+// ---------------------------------------------------------------------------
 // Decode attention, faithful (inference.rs:23945-24025), one workgroup per query head.
 //   score_p = dot_seq(q, k_p) * scale         one lane per position, d in order
 //   m = max_p score_p                          exact
@@ -1626,6 +1825,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   const uint4* vg = reinterpret_cast<const uint4*>(vc + hbase);  // V granule (g, d): g * HD + d
   const int pos = (int)*d_pos;
   if (kv_pos_bad(pos, kvs)) return;  // (uniform, before any barrier)
+  CM_ATT_STAMP(0)
   const int P = pos + 1;
   const int ncache = pos;
   // Loads in the order they are needed (a wave's loads complete in order): this token's q, k
@@ -1733,6 +1933,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
     }
   }
   __syncthreads();
+  CM_ATT_STAMP(1)
 
   if (P == 1) {
     // inference.rs:23564-23575: a single position copies the V row.
@@ -1782,6 +1983,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
       lmax = fmaxf(lmax, sv);
     }
     const float mx = block_max(lmax, red);
+    CM_ATT_STAMP(2)
     for (int p = tid; p < P; p += ATT_NT) sc[p] = glibc_expf_t(sc[p] - mx, etab);
     // The denominator: the one-pass exact in-order sum; beyond its limit the exact segmented
     // sum (one binade per pass) with its prefix array in the V ring, staged only afterwards,
@@ -1789,6 +1991,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
     const bool seg = !early && att_seg_chunk<ATT_NT>(P) > 0 &&
                      att_seg_bytes<ATT_NT>(P) <= (size_t)R * ATT_RING_GRANULES * 16;
     __syncthreads();
+    CM_ATT_STAMP(3)
     // the first V chunks go out now: the staging waves' issue (a wave stalls while the CU's
     // memory queue is full) overlaps the denominator's serial fold by one lane, and no
     // barrier waits on it before that
@@ -1811,6 +2014,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
       __syncthreads();
       inv = s_inv;
     }
+    CM_ATT_STAMP(4)
     for (int p = tid; p < P; p += ATT_NT) sc[p] = sc[p] * inv;
     // ---- out_d = fold_p prob_p * v_pd: lane d walks the ring chunk by chunk (granules of
     // 8 positions; each product is one mixed-precision FMA on the f16 value).
@@ -1879,6 +2083,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
         }
       }
     }
+    CM_ATT_STAMP(5)
     __syncthreads();  // the normalised probabilities past the ring (and with no chunks at all)
     if (tid < HD) {
 #pragma unroll
@@ -1896,6 +2101,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
     xq[(size_t)h * HD + tid] = q;
     if ((tid & 31) == 0) xs[((size_t)h * HD + tid) >> 5] = dd;
   }
+  CM_ATT_STAMP(6)
 }
 
 // ---------------------------------------------------------------------------

@@ -142,6 +142,16 @@ int camelid_hip_read_hidden(camelid_hip_engine* e, float* out);
 int camelid_hip_profile_begin(camelid_hip_engine* e);
 int camelid_hip_profile_end(camelid_hip_engine* e, double* ms, double* bytes, uint64_t* launches,
                             uint32_t n_cat);
+/* Measurement hook (no reference counterpart): in-kernel phase timestamps (100 MHz counter) of
+ * the last decode step, recorded only by the measurement build of this library
+ * (libcamelid_hip_stamps.so, compiled with -DCM_STAMPS); the product build returns an error.
+ * Layout: the decode attention [layer < 64][head < 64][7] (start, q/k/v built, scores,
+ * exponentials, denominator, output sums, end), then the norm-fused GEMVs of the last layer
+ * [kind 0 qkv, 1 gate/up][workgroup < 256][8] (start, norm done, a weight wave's loads issued,
+ * past the post-norm barrier, block dots done, end, the norm inputs arrived, the sum of squares
+ * known).  Copies min(n, 64*64*7 +
+ * 2*256*8) words; *n_out receives the count. */
+int camelid_hip_phase_stamps(uint64_t* out, size_t n, size_t* n_out);
 /* Device name and compute units. */
 int camelid_hip_device_info(char* name, size_t name_len, int* n_cu);
 
@@ -178,7 +188,7 @@ int camelid_hip_rmsnorm_q8_0_gemv(const int8_t* wq, const uint16_t* wd, uint32_t
 /* Gate/up projection + SwiGLU + Q8_0 quantization of the activation (CPU tensor/mod.rs:1943-1967,
  * inference.rs:16953): W holds gate and up rows interleaved in groups of 32 (group g: gate rows
  * 32g..32g+31, then up rows 32g..32g+31; ffn groups), aq/as = Q8_0(silu(gate.x) * up.x).  The
- * activation is Q8_0(rmsnorm(x; nw)) computed in-kernel when x is given (k in {2048, 3072}),
+ * activation is Q8_0(rmsnorm(x; nw)) computed in-kernel when x is given,
  * else xq/xs.  k in {2048, 3072, 4096}; ffn % 32 == 0. */
 int camelid_hip_gate_up_silu(const int8_t* wq, const uint16_t* wd, uint32_t ffn, uint32_t k, const int8_t* xq,
                              const float* xs, const float* x, const float* nw, float eps, int8_t* aq, float* as,

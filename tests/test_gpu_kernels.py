@@ -267,7 +267,8 @@ def test_rmsnorm_q8_gemv_bit_exact(native, orc, rows, k):
 
 
 @pytest.mark.parametrize("ffn,k,norm", [(8192, 3072, True), (8192, 3072, False), (5632, 2048, True),
-                                        (96, 4096, False), (64, 2048, False), (96, 3072, True)])
+                                        (96, 4096, False), (64, 2048, False), (96, 3072, True),
+                                        (14336, 4096, True), (12288, 4096, True)])
 def test_gate_up_silu_bit_exact(native, orc, ffn, k, norm):
     """Fused gate/up GEMV + SwiGLU + Q8_0 of the activation (rows interleaved by 32)."""
     rng = np.random.default_rng(ffn + k + norm)
