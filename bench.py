@@ -186,10 +186,10 @@ def attention_phases(cfg) -> dict:
     and the launch span (first start to last end), in microseconds."""
     import ctypes as C
     from camelid_amd import _native as N
-    na, ng = 64 * 64 * 7, 2 * 256 * 8
-    buf = (C.c_uint64 * (na + ng))()
+    na, ng, nsp = 64 * 64 * 7, 2 * 256 * 8, 2 * 1024 * 8
+    buf = (C.c_uint64 * (na + ng + nsp))()
     got = C.c_size_t(0)
-    N.check(N.lib().camelid_hip_phase_stamps(buf, na + ng, C.byref(got)))
+    N.check(N.lib().camelid_hip_phase_stamps(buf, na + ng + nsp, C.byref(got)))
     allst = np.frombuffer(buf, np.uint64).astype(np.int64)
     st = allst[:na].reshape(64, 64, 7)[:cfg.n_layers, :cfg.n_heads]
     d = np.diff(st, axis=2) * 0.01  # 100 MHz ticks -> us
@@ -199,7 +199,7 @@ def attention_phases(cfg) -> dict:
     res["launch_span"] = round(float((st[:, :, 6].max(1) - st[:, :, 0].min(1)).mean() * 0.01), 3)
     log("attention phases (us, mean over layers and heads): " + ", ".join(f"{k} {v}" for k, v in res.items()))
     # the norm-fused GEMVs of the last layer (mean over the workgroups that recorded)
-    gs = allst[na:].reshape(2, 256, 8)
+    gs = allst[na:na + ng].reshape(2, 256, 8)
     for kind, name in enumerate(("qkv_norm_gemv", "gate_up_norm_gemv")):
         g = gs[kind]
         g = g[g[:, 0] > 0]
@@ -216,6 +216,21 @@ def attention_phases(cfg) -> dict:
               "start_spread": float((t0.max() - t0.min()) * 0.01),
               "launch_span": float((g[:, 5].max() - t0.min()) * 0.01),
               "workgroups": int(len(g))}
+        res[name] = {k: round(v, 3) for k, v in ph.items()}
+        log(f"{name} phases (us from each workgroup's start): " + ", ".join(f"{k} {v:.3f}" for k, v in ph.items()))
+    # the split attention (when it ran in the last layer)
+    sp = allst[na + ng:].reshape(2, 1024, 8)
+    for kind, name, labels in ((0, "att_scores_split", ("q_built", "scores_done", "end")),
+                               (1, "att_out_split", ("scores_max", "exp", "denominator", "output_sums", "end"))):
+        g = sp[kind]
+        g = g[(g[:, 0] > 0) & (g[:, len(labels)] > 0)]
+        if not len(g):
+            continue
+        t0 = g[:, 0]
+        ph = {lab: float((g[:, i + 1] - t0).mean() * 0.01) for i, lab in enumerate(labels)}
+        ph["start_spread"] = float((t0.max() - t0.min()) * 0.01)
+        ph["launch_span"] = float((g[:, len(labels)].max() - t0.min()) * 0.01)
+        ph["workgroups"] = int(len(g))
         res[name] = {k: round(v, 3) for k, v in ph.items()}
         log(f"{name} phases (us from each workgroup's start): " + ", ".join(f"{k} {v:.3f}" for k, v in ph.items()))
     return res

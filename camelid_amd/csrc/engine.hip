@@ -559,9 +559,10 @@ void launch_attention(uint32_t hd, uint32_t n_heads, int slots, hipStream_t s, c
 #undef CM_ATT
 }
 
-// The split attention for long contexts (k_att_scores + k_att_out): slices of ATT_NT
-// positions for the scores (grid sized for kvs; slices past the position exit), 32-dim
-// output workgroups (+ read-ahead workgroups) for the softmax and output sum.
+// The split attention (k_att_scores + k_att_out): score slices of ATT_SLICE positions (grid
+// sized for kvs; slices past the position exit), 32-dim output workgroups (+ read-ahead
+// workgroups) for the softmax and output sum.
+constexpr int ATT_SLICE = 256;
 template <bool FUSED>
 void launch_attention_split(uint32_t hd, uint32_t n_heads, int slots, hipStream_t s, const float* qsrc, int nh,
                             int nkv, int rope_dim, int split_half, const float* cb, const float* sb, int rs,
@@ -569,7 +570,16 @@ void launch_attention_split(uint32_t hd, uint32_t n_heads, int slots, hipStream_
                             int kvs, const uint32_t* pos, float scale, float* g_sc, float* g_mx, float* att,
                             int8_t* xq, float* xs, cm::Prefetch pf) {
   const size_t lds = (size_t)slots * cm::ATT_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs);
-#define CM_ATTS(HD)                                                                                                 {                                                                                                                   const int nsl = (kvs + cm::att_nt(HD) - 1) / cm::att_nt(HD);                                                     CM_LAUNCH((cm::k_att_scores<HD, FUSED>), dim3(n_heads, nsl), dim3(cm::att_nt(HD)), 0, s, qsrc, nh, nkv,                    rope_dim, split_half, cb, sb, rs, qn, kn, eps, kc, vc, layer, kvs, pos, scale, g_sc, g_mx);            const uint32_t grid = n_heads * (HD / 32) + (pf.a_lines ? PREFETCH_WGS : 0);                                      CM_LAUNCH((cm::k_att_out<HD>), dim3(grid), dim3(cm::att_nt(HD)), lds, s, vc, nh, nkv, layer, kvs, pos, g_sc,               g_mx, nsl, att, xq, xs, slots, pf);                                                                   }
+  const int nsl = (kvs + ATT_SLICE - 1) / ATT_SLICE;
+#define CM_ATTS(HD)                                                                                                \
+  {                                                                                                                \
+    CM_LAUNCH((cm::k_att_scores<HD, FUSED, (HD > ATT_SLICE ? HD : ATT_SLICE)>), dim3(n_heads, nsl),               \
+              dim3(HD > ATT_SLICE ? HD : ATT_SLICE), 0, s, qsrc, nh, nkv, rope_dim, split_half, cb, sb, rs, qn, kn, \
+              eps, kc, vc, layer, kvs, pos, scale, g_sc, g_mx);                                                   \
+    const uint32_t grid = n_heads * (HD / 32) + (pf.a_lines ? PREFETCH_WGS : 0);                                  \
+    CM_LAUNCH((cm::k_att_out<HD>), dim3(grid), dim3(cm::att_nt(HD)), lds, s, vc, nh, nkv, layer, kvs, pos, g_sc,  \
+              g_mx, nsl, (HD > ATT_SLICE ? HD : ATT_SLICE), att, xq, xs, slots, pf);                              \
+  }
   if (hd == 64) CM_ATTS(64)
   else if (hd == 128) CM_ATTS(128)
   else CM_ATTS(256)
@@ -1764,15 +1774,19 @@ int camelid_hip_phase_stamps(uint64_t* out, size_t n, size_t* n_out) {
   if (!out || !n_out) return fail(nullptr, "null argument");
   const size_t na = (size_t)cm::ATT_STAMP_LAYERS * cm::ATT_STAMP_HEADS * cm::ATT_NSTAMP;
   const size_t ng = (size_t)2 * cm::GEMV_STAMP_WGS * cm::GEMV_NSTAMP;
-  const size_t total = na + ng;
+  const size_t nsp = (size_t)2 * cm::SPLIT_STAMP_WGS * cm::SPLIT_NSTAMP;
+  const size_t total = na + ng + nsp;
 #ifdef CM_STAMPS
   G_TRY(hipDeviceSynchronize());
-  const size_t m1 = std::min(n, na), m2 = std::min(n - m1, ng);
+  const size_t m1 = std::min(n, na), m2 = std::min(n - m1, ng), m3 = std::min(n - m1 - m2, nsp);
   G_TRY(hipMemcpyFromSymbol(out, HIP_SYMBOL(cm::g_att_stamps), m1 * sizeof(uint64_t), 0, hipMemcpyDeviceToHost));
   if (m2)
     G_TRY(hipMemcpyFromSymbol(out + m1, HIP_SYMBOL(cm::g_gemv_stamps), m2 * sizeof(uint64_t), 0,
                               hipMemcpyDeviceToHost));
-  *n_out = m1 + m2;
+  if (m3)
+    G_TRY(hipMemcpyFromSymbol(out + m1 + m2, HIP_SYMBOL(cm::g_split_stamps), m3 * sizeof(uint64_t), 0,
+                              hipMemcpyDeviceToHost));
+  *n_out = m1 + m2 + m3;
   return 0;
 #else
   (void)n;

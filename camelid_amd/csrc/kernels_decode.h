@@ -1685,6 +1685,19 @@ constexpr int ATT_STAMP_LAYERS = 64, ATT_STAMP_HEADS = 64;
 #ifdef CM_STAMPS
 __device__ uint64_t g_att_stamps[ATT_STAMP_LAYERS * ATT_STAMP_HEADS * ATT_NSTAMP];
 #endif
+// The split attention's workgroups (measurement build): kind 0 k_att_scores (workgroup index
+// head * slices + slice), 1 k_att_out (head * dim groups + group); per workgroup < 1024 of the
+// last layer: k_att_scores 0 start, 1 q built, 2 scores done, 3 end; k_att_out 0 start,
+// 1 scores loaded and maximum, 2 exponentials, 3 denominator, 4 output sums, 5 end.
+constexpr int SPLIT_NSTAMP = 8, SPLIT_STAMP_WGS = 1024;
+#ifdef CM_STAMPS
+__device__ uint64_t g_split_stamps[2 * SPLIT_STAMP_WGS * SPLIT_NSTAMP];
+#define CM_SPLIT_STAMP(kind, wg, i)                                                                        \
+  if (threadIdx.x == 0 && (wg) < SPLIT_STAMP_WGS)                                                         \
+    g_split_stamps[((kind) * SPLIT_STAMP_WGS + (wg)) * SPLIT_NSTAMP + (i)] = __builtin_amdgcn_s_memrealtime();
+#else
+#define CM_SPLIT_STAMP(kind, wg, i)
+#endif
 #ifdef CM_STAMPS
 #define CM_ATT_STAMP(i)                                                                                 \
   if (tid == 0 && layer < ATT_STAMP_LAYERS && h < ATT_STAMP_HEADS)                                      \
@@ -2105,27 +2118,29 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention for long contexts, split over workgroups: k_attention's arithmetic, in
-// the same order, with a head's K and V streamed through many CUs instead of one (at 8K
-// positions one CU's loads in flight, not the arithmetic, bound the single-workgroup kernel).
-//   k_att_scores  grid (heads, ceil(kvs / ATT_NT)): workgroup (h, s) builds q (and, for s = 0
+// Decode attention split over workgroups: k_attention's arithmetic, in the same order, with
+// a head's K and V streamed through many CUs instead of one (one CU's loads in flight, not the
+// arithmetic, bound the single-workgroup kernel: about 30 GB/s per CU).
+//   k_att_scores  grid (heads, ceil(kvs / NT)): workgroup (h, s) builds q (and, for s = 0
 //                 of a group's first head, stores this position's K/V, as k_attention does),
-//                 then the scores of positions [s ATT_NT, (s + 1) ATT_NT) ∩ [0, pos] into
-//                 g_sc[h][p] and their max into g_max[h][s]; slices past pos exit at once.
+//                 then the scores of positions [s NT, (s + 1) NT) ∩ [0, pos] into g_sc[h][p]
+//                 and their max into g_max[h][s]; slices past pos exit at once.  Each thread's
+//                 K row is issued with the q/k/v loads, so the slice streams while q is built.
 //   k_att_out     grid (heads * HD / 32 [+ read-ahead workgroups]): workgroup (h, w) reads the
 //                 head's scores, softmax as k_attention (max, expf, the in-order denominator,
 //                 normalise), then out_d for d in [32 w, 32 w + 32) through a V ring whose 32 KB
-//                 chunks hold 512 positions of those 32 dims, and quantizes them (one Q8_0
-//                 block).  Every position's V comes from the cache (k_att_scores stored pos).
-template <int HD, bool FUSED>
-__global__ __launch_bounds__(att_nt(HD)) void k_att_scores(
+//                 chunks hold 512 positions of those 32 dims (its first chunks issued behind
+//                 the scores loads), and quantizes them (one Q8_0 block).  Every position's V
+//                 comes from the cache (k_att_scores stored pos).
+template <int HD, bool FUSED, int NT>
+__global__ __launch_bounds__(NT) void k_att_scores(
     const float* __restrict__ qsrc, int n_heads, int n_kv, int rope_dim, int split_half,
     const float* __restrict__ cos_base, const float* __restrict__ sin_base, int rope_stride,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm, float eps, uint16_t* __restrict__ kc,
     uint16_t* __restrict__ vc, int layer, int kvs, const uint32_t* __restrict__ d_pos, float scale,
     float* __restrict__ g_sc, float* __restrict__ g_max) {
-  constexpr int ATT_NT = att_nt(HD);
-  static_assert(HD % 64 == 0 && HD <= 256, "head_dim must be 64, 128 or 256");
+  constexpr int ATT_NT = NT;  // positions per slice, one per thread
+  static_assert(HD % 64 == 0 && HD <= 256 && NT >= HD && NT % 64 == 0, "head_dim must be 64, 128 or 256");
   constexpr int R8 = HD / 8;
   __shared__ __align__(16) float qs[HD];
   __shared__ __align__(16) float kn[HD];
@@ -2142,6 +2157,8 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_scores(
   const int kvh = h / rep;
   const size_t hbase = kv_head_base(layer, n_kv, kvh, HD, kvs);
   const uint4* kg = reinterpret_cast<const uint4*>(kc + hbase);
+  const int wg = h * (int)gridDim.y + s;
+  CM_SPLIT_STAMP(0, wg, 0)
   if (tid < HD) {
     qs[tid] = qsrc[(size_t)h * HD + tid];
     if (FUSED) {
@@ -2150,6 +2167,14 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_scores(
     } else {
       kn[tid] = half_bits_to_float(kc[hbase + kv_k_index(kvs, pos, tid)]);
     }
+  }
+  // this thread's cache position's K row: issued now (behind q/k/v in their waves), so that
+  // the slice's K streams while q is built
+  const int p = p0 + tid;
+  uint4 row[R8];
+  if (p < pos) {
+#pragma unroll
+    for (int u = 0; u < R8; ++u) row[u] = kg[(size_t)u * kvs + p];
   }
   if (FUSED) {
     if (q_norm) {  // per-head RMSNorm of q and k (serial folds, as k_attention)
@@ -2194,12 +2219,9 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_scores(
     }
   }
   __syncthreads();
+  CM_SPLIT_STAMP(0, wg, 1)
   float lmax = -INFINITY;
-  const int p = p0 + tid;
   if (p < pos) {
-    uint4 row[R8];
-#pragma unroll
-    for (int u = 0; u < R8; ++u) row[u] = kg[(size_t)u * kvs + p];
     float acc = 0.0f;
 #pragma unroll
     for (int u = 0; u < R8; ++u) {
@@ -2230,14 +2252,17 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_scores(
     g_sc[(size_t)h * kvs + p] = sv;
     lmax = sv;
   }
+  CM_SPLIT_STAMP(0, wg, 2)
   const float mx = block_max(lmax, red);
   if (tid == 0) g_max[(size_t)h * gridDim.y + s] = mx;
+  CM_SPLIT_STAMP(0, wg, 3)
 }
 
 template <int HD>
 __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
     const uint16_t* __restrict__ vc, int n_heads, int n_kv, int layer, int kvs, const uint32_t* __restrict__ d_pos,
-    const float* __restrict__ g_sc, const float* __restrict__ g_max, int n_slices, float* __restrict__ att_out,
+    const float* __restrict__ g_sc, const float* __restrict__ g_max, int n_slices, int n_slices_pos,
+    float* __restrict__ att_out,
     int8_t* __restrict__ xq, float* __restrict__ xs, int ring_slots, Prefetch pf) {
   constexpr int ATT_NT = att_nt(HD);
   constexpr int NW = ATT_NT / 64;
@@ -2269,20 +2294,26 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
   const int P = pos + 1;
   const int d = w * DW + tid;  // output lanes: tid < DW
   float acc = 0.0f;
+  CM_SPLIT_STAMP(1, (int)blockIdx.x, 0)
   if (P == 1) {
     // inference.rs:23564-23575: a single position copies the V row
     if (tid < DW) acc = half_bits_to_float(vc[hbase + kv_v_index(HD, pos, d)]);
   } else {
+    const int ng = pos >> 3;  // full groups of 8 positions before pos
+    // the output lanes' V values past the full groups (positions ng*8 .. pos, at most 8), loaded
+    // now: the output chain adds them from registers at the end
+    uint16_t vtail[8];
+    if (tid < DW) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) vtail[u] = ng * 8 + u < P ? vc[hbase + kv_v_index(HD, ng * 8 + u, d)] : (uint16_t)0;
+    }
     if (tid < 32) etab[tid] = kExp2Tab[tid];
     const float* gs = g_sc + (size_t)h * kvs;
     for (int p = tid; p < P; p += ATT_NT) sc[p] = gs[p];
     float lm = -INFINITY;
-    const int nsl = (P + ATT_NT - 1) / ATT_NT;
+    const int nsl = (P + n_slices_pos - 1) / n_slices_pos;
     for (int i = tid; i < nsl; i += ATT_NT) lm = fmaxf(lm, g_max[(size_t)h * n_slices + i]);
-    const float mx = block_max(lm, red);  // (its barriers also publish sc and etab)
-    for (int p = tid; p < P; p += ATT_NT) sc[p] = glibc_expf_t(sc[p] - mx, etab);
     const int R = ring_slots;
-    const int ng = pos >> 3;  // full groups of 8 positions before pos
     const int nchunks = (ng + CG - 1) / CG;
     const int hw = (tid >> 6) - 1;
     const bool stager = hw >= 0 && hw < NH;
@@ -2302,10 +2333,16 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
     const bool early = P <= ATT_NT * ATT_ONEPASS_C;
     const bool seg = !early && att_seg_chunk<ATT_NT>(P) > 0 &&
                      att_seg_bytes<ATT_NT>(P) <= (size_t)R * ATT_RING_GRANULES * 16;
-    __syncthreads();
+    // the first V chunks go out behind the scores loads (nothing waits on them before the
+    // output sum; the segmented denominator uses the ring first and stages afterwards)
     if (stager && !seg) {
       for (int c = 0; c < min(R - 1, nchunks); ++c) stage(c);
     }
+    const float mx = block_max(lm, red);  // (its barriers also publish sc and etab)
+    CM_SPLIT_STAMP(1, (int)blockIdx.x, 1)
+    for (int p = tid; p < P; p += ATT_NT) sc[p] = glibc_expf_t(sc[p] - mx, etab);
+    __syncthreads();
+    CM_SPLIT_STAMP(1, (int)blockIdx.x, 2)
     float inv;
     if (onepass) {
       inv = 1.0f / att_onepass_sum<ATT_NT>(sc, P, fs);
@@ -2322,6 +2359,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
       __syncthreads();
       inv = s_inv;
     }
+    CM_SPLIT_STAMP(1, (int)blockIdx.x, 3)
     for (int p = tid; p < P; p += ATT_NT) sc[p] = sc[p] * inv;
     for (int c = 0; c < nchunks; ++c) {
       if (stager) wait_vmcnt(LH * (min(c + R - 2, nchunks - 1) - c));  // chunk c has landed
@@ -2385,9 +2423,12 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
         }
       }
     }
+    CM_SPLIT_STAMP(1, (int)blockIdx.x, 4)
     __syncthreads();  // the normalised probabilities past the ring (and with no chunks at all)
     if (tid < DW) {
-      for (int p = ng * 8; p < P; ++p) acc += sc[p] * half_bits_to_float(vc[hbase + kv_v_index(HD, p, d)]);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (ng * 8 + u < P) acc += sc[ng * 8 + u] * half_bits_to_float(vtail[u]);
     }
   }
   if (tid < DW) {
@@ -2397,6 +2438,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
     xq[(size_t)h * HD + d] = q;
     if (tid == 0) xs[((size_t)h * HD + d) >> 5] = dd;
   }
+  CM_SPLIT_STAMP(1, (int)blockIdx.x, 5)
 }
 
 // ---------------------------------------------------------------------------

@@ -149,8 +149,10 @@ int camelid_hip_profile_end(camelid_hip_engine* e, double* ms, double* bytes, ui
  * exponentials, denominator, output sums, end), then the norm-fused GEMVs of the last layer
  * [kind 0 qkv, 1 gate/up][workgroup < 256][8] (start, norm done, a weight wave's loads issued,
  * past the post-norm barrier, block dots done, end, the norm inputs arrived, the sum of squares
- * known).  Copies min(n, 64*64*7 +
- * 2*256*8) words; *n_out receives the count. */
+ * known), then the split attention of the last layer [kind 0 scores, 1 output][workgroup <
+ * 1024][8] (scores: start, q built, scores done, end; output: start, scores and maximum,
+ * exponentials, denominator, output sums, end).  Copies min(n, 64*64*7 + 2*256*8 + 2*1024*8)
+ * words; *n_out receives the count. */
 int camelid_hip_phase_stamps(uint64_t* out, size_t n, size_t* n_out);
 /* Device name and compute units. */
 int camelid_hip_device_info(char* name, size_t name_len, int* n_cu);
