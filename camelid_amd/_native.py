@@ -113,6 +113,8 @@ SIGNATURES: dict[str, tuple] = {
                                                C.c_uint32, vp, C.c_float, vp, vp, vp, vp]),
     "camelid_hip_attention_decode_split": (C.c_int, [vp, vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                                C.c_uint32, vp, C.c_float, vp, vp, vp, vp]),
+    "camelid_hip_attention_decode_split_noalloc": (C.c_int, [vp, vp, vp, C.c_uint32, C.c_uint32, C.c_uint32,
+                                                             C.c_uint32, C.c_uint32, vp, C.c_float, vp, vp, vp, vp]),
     "camelid_hip_q8_0_gemm": (C.c_int, [vp, vp, C.c_uint32, C.c_uint32, vp, vp, C.c_uint32, vp, vp, vp]),
     "camelid_hip_attention_prefill": (C.c_int, [vp, vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                                 C.c_uint32, C.c_uint32, C.c_uint32, C.c_float, vp, vp, vp, vp]),

@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_ext.h>
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -2021,6 +2022,62 @@ int camelid_hip_attention_decode_split(const float* qrot, const uint16_t* kc, co
   (void)hipFree(g_mx);
   if (!rc && st != hipSuccess) return fail(nullptr, std::string("attention_decode_split: ") + hipGetErrorString(st));
   return rc ? rc : kv_pos_result((hipStream_t)stream, "attention_decode_split");
+}
+
+// ---- the split attention without allocation (camelid_hip_attention_decode_split_noalloc)
+// Its score scratch: a file-scope device array, one copy per GPU, held until the process
+// ends.  Host code never passes the array's name to a kernel (on the host it is a stand-in,
+// not a device address): the first call on each device looks up that device's copy with
+// hipGetSymbolAddress and keeps the address per device.
+constexpr size_t NOALLOC_SCORE_FLOATS = (size_t)1 << 20;  // n_heads * max_pos score words (4 MiB)
+constexpr size_t NOALLOC_MAX_FLOATS = (size_t)1 << 14;    // n_heads * ceil(max_pos / 256) slice maxima
+static __device__ __align__(256) float scratch[NOALLOC_SCORE_FLOATS + NOALLOC_MAX_FLOATS];
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static std::atomic<float*> g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+// This device's copy of `scratch` (looked up once per device, with that device current).
+static int scratch_for_current_device(float** out) {
+  int dev = 0;
+  G_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return fail(nullptr, "attention_decode_split_noalloc: device index out of range");
+  float* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    void* sym = nullptr;
+    const hipError_t st = hipGetSymbolAddress(&sym, HIP_SYMBOL(scratch));
+    if (st != hipSuccess || !sym)
+      return fail(nullptr, std::string("attention_decode_split_noalloc: hipGetSymbolAddress(scratch): ") +
+                               hipGetErrorString(st));
+    p = static_cast<float*>(sym);
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return 0;
+}
+
+int camelid_hip_attention_decode_split_noalloc(const float* qrot, const uint16_t* kc, const uint16_t* vc,
+                                               uint32_t layer, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
+                                               uint32_t max_pos, const uint32_t* d_pos, float scale, float* att_out,
+                                               int8_t* xq, float* xs, void* stream) {
+  if (!qrot || !kc || !vc || !d_pos || !att_out || !xq || !xs) return fail(nullptr, "null argument");
+  if (!n_heads || !n_kv || n_heads % n_kv || !attention_hd_supported(hd)) return fail(nullptr, "invalid head geometry");
+  if (max_pos % 8) return fail(nullptr, "the KV position stride (max_pos) must be a multiple of 8");
+  const size_t n_scores = (size_t)n_heads * max_pos;
+  const size_t n_max = (size_t)n_heads * ((max_pos + ATT_SLICE - 1) / ATT_SLICE);
+  if (n_scores > NOALLOC_SCORE_FLOATS || n_max > NOALLOC_MAX_FLOATS)
+    return fail(nullptr, "attention_decode_split_noalloc: n_heads * max_pos = " + std::to_string(n_scores) +
+                             " exceeds the static scratch (" + std::to_string(NOALLOC_SCORE_FLOATS) + " scores)");
+  const int slots = attn_ring_slots(max_pos);
+  if (slots == 0) return fail(nullptr, "max_pos too large for the decode attention");
+  float* base = nullptr;
+  if (scratch_for_current_device(&base)) return 1;
+  if (kv_pos_check(d_pos, max_pos, (hipStream_t)stream, "attention_decode_split_noalloc")) return 1;
+  // every scratch word the output kernel reads is written by the scores kernel of this call
+  launch_attention_split<false>(hd, n_heads, slots, (hipStream_t)stream, qrot, (int)n_heads, (int)n_kv, (int)hd, 0,
+                                nullptr, nullptr, 0, nullptr, nullptr, 0.0f, const_cast<uint16_t*>(kc),
+                                const_cast<uint16_t*>(vc), (int)layer, (int)max_pos, d_pos, scale, base,
+                                base + NOALLOC_SCORE_FLOATS, att_out, xq, xs, prefetch_of((const Q8Mat*)nullptr));
+  if (launch_status("attention_decode_split_noalloc")) return 1;
+  return kv_pos_result((hipStream_t)stream, "attention_decode_split_noalloc");
 }
 
 int camelid_hip_rmsnorm_q8_0_gemv(const int8_t* wq, const uint16_t* wd, uint32_t rows, uint32_t k, const float* x,

@@ -234,6 +234,19 @@ int camelid_hip_attention_decode_split(const float* qrot, const uint16_t* kc, co
                                        uint32_t layer, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
                                        uint32_t max_pos, const uint32_t* d_pos, float scale,
                                        float* att_out, int8_t* xq, float* xs, void* stream);
+/* No counterpart in the reference: camelid_hip_attention_decode_split for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The same kernels and bits as camelid_hip_attention_decode_split, but the score
+ * scratch is a static device array of the library (4 MiB + 64 KiB per GPU, held until the
+ * process ends) instead of a per-call allocation; no hipMalloc or hipFree is called.  Limit:
+ * n_heads * max_pos <= 2^20 and n_heads * ceil(max_pos / 256) <= 2^14, else an error.  Every
+ * call on one GPU shares that GPU's scratch (it keeps no state between calls: each word read
+ * is written earlier in the same call), so calls that overlap on one GPU (other streams or
+ * threads) race.  Position contract as camelid_hip_rope_kv; synchronizes the stream. */
+int camelid_hip_attention_decode_split_noalloc(const float* qrot, const uint16_t* kc, const uint16_t* vc,
+                                               uint32_t layer, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
+                                               uint32_t max_pos, const uint32_t* d_pos, float scale,
+                                               float* att_out, int8_t* xq, float* xs, void* stream);
 /* q8_gemm_batched (cuda_resident.rs:1494; CPU: the row dot of inference.rs:19871-19905 for
  * each token): y[t][n] = resid[t][n] + W[n].X[t] for T = tokens activation rows X [tokens][k]
  * (Q8_0 quants, f32 block scales [tokens][k/32]); output [tokens][rows]; the same
