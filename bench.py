@@ -35,11 +35,15 @@ INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix-core peak, AMD published
 HEADLINE = "llama-3.2-3b"
 ARCH = {"llama-3.2-3b": "Llama-3.2-3B-arch Q8_0", "tinyllama-1.1b": "TinyLlama-1.1B-arch Q8_0",
         "mistral-7b-v0.3": "Mistral-7B-v0.3-arch Q8_0 (8K context)", "qwen3-8b": "Qwen3-8B-arch Q4_K_M"}
-# Measured HBM bytes per launch of the dominant kernel: rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE passes over `bench.py --probe-traffic`, FETCH_SIZE scaled by 2.0 (what it reads
-# for a 256 MiB device copy: 128 MiB; WRITE_SIZE reads 256 MiB), averaged over the 113 GEMV
-# launches of one C3 step (profiles/traffic_gemv_llama-3.2-3b_q8_0.md).
+# MI355X peak engine clock (AMD published), for the VALU ceiling of the prefill GEMM's fold
+PEAK_CLOCK_HZ = 2.4e9
+# Measured HBM bytes per launch of the dominant kernel class, not measured by this script:
+# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over `bench.py --probe-traffic`, each
+# scaled by what the same counter reads for a device copy of known size, averaged over the
+# GEMV launches of one C3 step (profiles/traffic_gemv_llama-3.2-3b_q8_0.md).
 TRAFFIC: dict = {"llama-3.2-3b": 30571736}
+TRAFFIC_SOURCE = ("profiles/traffic_gemv_llama-3.2-3b_q8_0.md: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE "
+                  "passes, scaled by a copy kernel's reading; a recorded figure, not measured in this run")
 # Q8_0 [N, K] shapes, weights N(0, 0.02) and activations N(0, 1), seed 2
 SWEEP_SHAPES = [(2048, 2048), (5632, 2048), (2048, 5632), (32000, 2048), (128256, 3072)]
 
@@ -48,12 +52,29 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(model, cfg, prompt_len: int, n_steps: int, threads: int) -> dict:
+def host_cpu() -> dict:
+    """The host's CPU as lscpu reports it, and the CPUs this process may run on."""
+    info = {"model": None, "nproc": os.cpu_count(), "physical_cores": None,
+            "allowed_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None}
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = dict(line.split(":", 1) for line in out.splitlines() if ":" in line)
+        kv = {k.strip(): v.strip() for k, v in kv.items()}
+        info["model"] = kv.get("Model name")
+        if kv.get("Core(s) per socket") and kv.get("Socket(s)"):
+            info["physical_cores"] = int(kv["Core(s) per socket"]) * int(kv["Socket(s)"])
+    except (OSError, ValueError):
+        pass
+    return info
+
+
+def cpu_baseline(model, cfg, prompt_len: int, n_steps: int, thread_counts: list) -> dict:
     """Oracle (C++ restatement of Camelid's CPU path) decode steps at the benchmark's
     positions: KV for the prompt is seeded with f16-rounded random rows, then `n_steps`
-    greedy steps run from position prompt_len-1."""
-    from oracle.oracle import OracleModel
-    os.environ.setdefault("OMP_NUM_THREADS", str(threads))
+    greedy steps run from position prompt_len-1, once per thread count (OpenMP threads over
+    output rows; the first count is the reported value)."""
+    from oracle.oracle import OracleModel, set_threads
     orc = OracleModel(model, prompt_len + n_steps + 1)
     rng = np.random.default_rng(0)
     n = prompt_len - 1
@@ -61,16 +82,33 @@ def cpu_baseline(model, cfg, prompt_len: int, n_steps: int, threads: int) -> dic
         k = rng.normal(0, 1, (cfg.n_kv_heads, n, cfg.head_dim)).astype(np.float32)
         v = rng.normal(0, 1, (cfg.n_kv_heads, n, cfg.head_dim)).astype(np.float32)
         orc.seed_kv(layer, k, v)
-    tok = 1
-    t0 = time.perf_counter()
-    for i in range(n_steps):
-        tok, _, _ = orc.forward(tok, n + i)
-    dt = time.perf_counter() - t0
+    runs = []
+    for threads in thread_counts:
+        set_threads(threads)
+        tok = 1
+        t0 = time.perf_counter()
+        for i in range(n_steps):
+            tok, _, _ = orc.forward(tok, n + i)
+        dt = time.perf_counter() - t0
+        runs.append({"threads": threads, "tok_s": round(n_steps / dt, 3), "s": round(dt, 2)})
+        log(f"CPU baseline, {threads} threads: {n_steps / dt:.2f} tok/s")
     orc.close()
-    return {"value": round(n_steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+    return {"value": runs[0]["tok_s"], "unit": "tok/s", "cores": runs[0]["threads"], "kind": "port",
             "sample": f"{n_steps} greedy decode steps of the same {ARCH[cfg.name]} model at positions "
                       f"{n}..{n + n_steps - 1} (KV history seeded), oracle/camelid_oracle.cpp, "
-                      f"{threads} OpenMP threads over output rows"}
+                      f"{runs[0]['threads']} OpenMP threads over output rows",
+            "runs": runs, "host": host_cpu()}
+
+
+def hbm_bandwidth(bytes_per_array: int = 1 << 30, reps: int = 10) -> dict:
+    """Measured HBM bandwidth of this device: STREAM triad and a read-only pass over arrays of
+    1 GiB (well beyond the 256 MB last-level cache), best of `reps` passes."""
+    import ctypes as C
+    from camelid_amd import _native as N
+    t, r = C.c_double(), C.c_double()
+    N.check(N.lib().camelid_hip_hbm_bandwidth(bytes_per_array, reps, C.byref(t), C.byref(r)))
+    return {"triad_GBps": round(t.value, 1), "read_GBps": round(r.value, 1), "spec_GBps": HBM_PEAK_GBS,
+            "bytes_per_array": bytes_per_array, "passes": reps}
 
 
 def run_sweep(iters_min: int = 200) -> dict:
@@ -274,8 +312,9 @@ def main() -> int:
     ap.add_argument("--config", default="llama-3.2-3b")
     ap.add_argument("--prompt", type=int, default=None, help="prompt length (default: the config's)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-steps", type=int, default=6)
+    ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--no-hbm-probe", action="store_true", help="skip the HBM triad/read bandwidth probe")
     ap.add_argument("--sweep", action="store_true", help="run the isolated Q8_0 GEMV/GEMM sweep (configs[1])")
     ap.add_argument("--sweep-kquant", action="store_true",
                     help="time the K-quant prefill projections (Q4_K GEMM, Q6_K multi-token GEMV) of configs[4]")
@@ -398,6 +437,7 @@ def main() -> int:
                  "K-quant GEMV: k_gemv_q4k + k_gemv_q6k (incl. lm_head)")
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get(cfg.name),
+                    "traffic_source": TRAFFIC_SOURCE if cfg.name in TRAFFIC else None,
                     "kernel": kname + ", all launches of K steps (algorithmic bytes / summed dispatch durations)",
                     "avg_launch_us": round(g["ms"] * 1e3 / max(g["launches"], 1), 3),
                     "launches": g["launches"]}
@@ -421,12 +461,45 @@ def main() -> int:
                   "tok_s_if_all_accepted": round(8 / vdt, 1)}
         log(f"verify k=8: {vdt * 1e3:.2f} ms, tokens identical to the decode loop: {verify['tokens_identical']}")
 
+    # prefill projections under the profiler: a second prefill of the same prompt from
+    # position 0 (rewrites the same KV rows), for the matrix-core utilisation
+    prefill_mm = None
+    if not args.no_profile and not args.seed_kv:
+        eng.set_filled(0)
+        eng.profile_begin()
+        sess.prefill(prompt[:-1])
+        pprof = eng.profile_end()
+        g = pprof["prefill_gemm"]
+        tops = g["bytes"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] else 0.0
+        # the bit-exact fold costs 4 unpacked VALU ops (int->f32, two scale products, add) per
+        # output row, token and 32-wide block (64 int8 ops): a ceiling of 64 lanes x clock / 4
+        # x 64 ops per CU
+        fold_ceiling = n_cu * 64 * PEAK_CLOCK_HZ / 4 * 64 / 1e12
+        prefill_mm = {"tokens": P - 1, "gemm_tops": round(tops, 1), "gemm_ms": round(g["ms"], 3),
+                      "gemm_launches": g["launches"], "int8_peak_tops": INT8_PEAK_TOPS,
+                      "mfma_frac": round(tops / INT8_PEAK_TOPS, 4),
+                      "valu_fold_ceiling_tops": round(fold_ceiling, 1),
+                      "frac_of_fold_ceiling": round(tops / fold_ceiling, 4),
+                      "all_kernels_ms": round(sum(v["ms"] for v in pprof.values()), 3)}
+        log(f"prefill projections: {tops:.1f} TOP/s over {g['launches']} launches "
+            f"({tops / INT8_PEAK_TOPS:.3f} of the int8 peak, {tops / fold_ceiling:.3f} of the fold ceiling)")
+
+    hbm = None
+    if not args.no_hbm_probe:
+        hbm = hbm_bandwidth()
+        hbm["decode_frac_of_triad"] = round(total_bytes / dt / 1e9 / hbm["triad_GBps"], 4)
+        hbm["decode_frac_of_read"] = round(total_bytes / dt / 1e9 / hbm["read_GBps"], 4)
+        if roofline:
+            roofline["frac_of_measured_read"] = round(roofline["achieved"] / hbm["read_GBps"], 4)
+        log(f"HBM measured: triad {hbm['triad_GBps']} GB/s, read {hbm['read_GBps']} GB/s (spec {HBM_PEAK_GBS})")
+
     cpu = None
     if not args.no_cpu_baseline:
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-        log(f"CPU baseline: {args.cpu_steps} oracle decode steps on {threads} threads")
-        cpu = cpu_baseline(model, cfg, P, args.cpu_steps, threads)
-        log(f"CPU baseline {cpu['value']} tok/s")
+        share = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+        share = min(share, len(os.sched_getaffinity(0)))
+        counts = [share] + ([1] if share > 1 else [])
+        log(f"CPU baseline: {args.cpu_steps} oracle decode steps at {counts} threads")
+        cpu = cpu_baseline(model, cfg, P, args.cpu_steps, counts)
 
     out = {
         "metric": f"decode tok/s & % of HBM roofline, {ARCH[cfg.name]}, batch 1, 1 MI355X",
@@ -448,6 +521,8 @@ def main() -> int:
         "hbm_roofline_frac": round(hbm_frac, 4),
         "bytes_per_token": round(total_bytes / K),
         "prefill_tok_s": round((P - 1) / prefill_s, 2) if prefill_s else None,
+        "prefill_matrix_cores": prefill_mm,
+        "hbm_measured": hbm,
         "parity": parity,
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -91,6 +91,7 @@ SIGNATURES: dict[str, tuple] = {
     "camelid_hip_generate": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_float, u32p]),
     "camelid_hip_capture_hidden": (C.c_int, [vp, C.c_int]),
     "camelid_hip_read_hidden": (C.c_int, [vp, f32p]),
+    "camelid_hip_hbm_bandwidth": (C.c_int, [C.c_size_t, C.c_uint32, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "camelid_hip_profile_begin": (C.c_int, [vp]),
     "camelid_hip_profile_end": (C.c_int, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                           C.POINTER(C.c_uint64), C.c_uint32]),

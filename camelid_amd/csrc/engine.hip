@@ -80,7 +80,7 @@ struct LayerW {
 };
 
 // Profiling categories (camelid_hip_profile_end).
-enum { P_GEMV = 0, P_NORM, P_ATTN, P_SILU, P_HEAD, P_EMBED, P_NCAT };
+enum { P_GEMV = 0, P_NORM, P_ATTN, P_SILU, P_HEAD, P_EMBED, P_GEMM, P_NCAT };
 
 }  // namespace
 
@@ -1054,6 +1054,8 @@ void prefill_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cosv,
   const uint32_t nq = d.n_heads * d.head_dim, nkv = d.n_kv_heads * d.head_dim, F = d.ffn_dim, H = d.hidden;
   // projection i into rows [T][ldy] at y (+ resid)
   auto proj_rows = [&](const Proj& p, float* y, uint32_t ldy, const float* resid) {
+    ProfScope ps(e, P_GEMM, 2.0 * (p.quant != CAMELID_Q8_0 ? p.kq.rows : p.q8.rows) *
+                                (p.quant != CAMELID_Q8_0 ? p.kq.k : p.q8.k) * T);
     if (p.quant != CAMELID_Q8_0) {
       launch_kgemm(p.kq, T, e->pf_kd, e->pf_kq, y, ldy, resid, s);
     } else if (ldy == p.q8.rows) {
@@ -1096,6 +1098,11 @@ void prefill_chunk(camelid_hip_engine* e, const float* cosv, const float* sinv, 
   const camelid_hip_dims& d = e->d;
   hipStream_t s = e->stream;
   const uint32_t half = d.rope_dim / 2;
+  // a Q8_0 projection of the chunk; int8 ops (2 per weight and token) credited to the profile
+  auto gemm = [&](const Q8Mat& m, float* y, const float* resid) {
+    ProfScope ps(e, P_GEMM, 2.0 * m.rows * m.k * T);
+    launch_gemm(m, T, e->pf_xq, e->pf_xs, y, resid, s);
+  };
   for (uint32_t l = 0; l < d.n_layers; ++l) {
     const LayerW& L = e->layers[l];
     if (L.generic) {
@@ -1103,19 +1110,19 @@ void prefill_chunk(camelid_hip_engine* e, const float* cosv, const float* sinv, 
       continue;
     }
     launch_rmsnorm_quant(e->pf_h, L.attn_norm, d.hidden, d.eps, e->pf_xq, e->pf_xs, nullptr, s, cm::Prefetch{}, T);
-    launch_gemm(L.qkv, T, e->pf_xq, e->pf_xs, e->pf_qkv, nullptr, s);
+    gemm(L.qkv, e->pf_qkv, nullptr);
     CM_LAUNCH(cm::k_rope_kv, dim3(d.n_heads + d.n_kv_heads, T), dim3(64), 0, s, e->pf_qkv, (int)d.n_heads,
               (int)d.n_kv_heads, (int)d.head_dim, (int)d.rope_dim, (int)d.split_half_pairing, cosv, sinv, L.q_norm,
               L.k_norm, d.eps, e->pf_q, e->kc, e->vc, (int)l, (int)e->kvs, (const uint32_t*)nullptr, (int)pos0,
               (int)half);
     launch_attn_prefill(d.head_dim, d.n_heads, d.n_kv_heads, T, e->pf_q, e->kc, e->vc, (int)l, (int)e->kvs,
                         (int)pos0, scale, nullptr, e->pf_xq, e->pf_xs, s);
-    launch_gemm(L.o, T, e->pf_xq, e->pf_xs, e->pf_h, e->pf_h, s);
+    gemm(L.o, e->pf_h, e->pf_h);
     launch_rmsnorm_quant(e->pf_h, L.ffn_norm, d.hidden, d.eps, e->pf_xq, e->pf_xs, nullptr, s, cm::Prefetch{}, T);
-    launch_gemm(L.gu, T, e->pf_xq, e->pf_xs, e->pf_gu, nullptr, s);
+    gemm(L.gu, e->pf_gu, nullptr);
     CM_LAUNCH(cm::k_silu_rows, dim3((d.ffn_dim + 255) / 256, T), dim3(256), 0, s, e->pf_gu, (int)d.ffn_dim,
               (int)e->gu_fused, e->pf_xq, e->pf_xs);
-    launch_gemm(L.down, T, e->pf_xq, e->pf_xs, e->pf_h, e->pf_h, s);
+    gemm(L.down, e->pf_h, e->pf_h);
   }
 }
 
@@ -1806,6 +1813,86 @@ int camelid_hip_device_info(char* name, size_t name_len, int* n_cu) {
   if (name && name_len) std::snprintf(name, name_len, "%s%s%s", p.name, p.name[0] ? " " : "", p.gcnArchName);
   if (n_cu) *n_cu = p.multiProcessorCount;
   return 0;
+}
+
+// HBM bandwidth probe: STREAM's triad a = b + s*c and a read-only pass over one array, each
+// workgroup on a contiguous span, with nontemporal (streaming) loads and stores, the fastest
+// of the forms measured on MI355X for arrays far beyond the caches.
+typedef float bw_v4 __attribute__((ext_vector_type(4)));
+constexpr int BW_TRIAD_U = 4, BW_TRIAD_NT = 256;  // 16-byte elements per thread, threads
+constexpr int BW_READ_U = 16, BW_READ_NT = 512;
+constexpr size_t BW_GRAIN = (size_t)BW_READ_U * BW_READ_NT * 16;  // bytes; a multiple of the triad span
+__global__ __launch_bounds__(BW_TRIAD_NT) void k_bw_triad(bw_v4* __restrict__ a, const bw_v4* __restrict__ b,
+                                                          const bw_v4* __restrict__ c, float sc) {
+  const size_t base = (size_t)blockIdx.x * BW_TRIAD_NT * BW_TRIAD_U + threadIdx.x;
+  bw_v4 x[BW_TRIAD_U], y[BW_TRIAD_U];
+#pragma unroll
+  for (int u = 0; u < BW_TRIAD_U; ++u) {
+    x[u] = __builtin_nontemporal_load(b + base + u * BW_TRIAD_NT);
+    y[u] = __builtin_nontemporal_load(c + base + u * BW_TRIAD_NT);
+  }
+#pragma unroll
+  for (int u = 0; u < BW_TRIAD_U; ++u) __builtin_nontemporal_store(x[u] + sc * y[u], a + base + u * BW_TRIAD_NT);
+}
+__global__ __launch_bounds__(BW_READ_NT) void k_bw_read(const bw_v4* __restrict__ b, float* __restrict__ sink) {
+  const size_t base = (size_t)blockIdx.x * BW_READ_NT * BW_READ_U + threadIdx.x;
+  bw_v4 x[BW_READ_U];
+#pragma unroll
+  for (int u = 0; u < BW_READ_U; ++u) x[u] = __builtin_nontemporal_load(b + base + u * BW_READ_NT);
+  float acc = 0.0f;
+#pragma unroll
+  for (int u = 0; u < BW_READ_U; ++u) acc += (x[u].x + x[u].y) + (x[u].z + x[u].w);
+  if (acc == -1.0f) sink[threadIdx.x] = acc;  // (the arrays hold zeros: never taken, but not provable)
+}
+
+int camelid_hip_hbm_bandwidth(size_t bytes_per_array, uint32_t reps, double* triad_gbs, double* read_gbs) {
+  if (!triad_gbs || !read_gbs || reps == 0) return fail(nullptr, "null argument");
+  if (bytes_per_array == 0 || bytes_per_array % BW_GRAIN)
+    return fail(nullptr, "bytes_per_array must be a positive multiple of " + std::to_string(BW_GRAIN));
+  const size_t n4 = bytes_per_array / 16;
+  bw_v4 *a = nullptr, *b = nullptr, *c = nullptr;
+  float* sink = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = 0;
+  if (hipMalloc(&a, bytes_per_array) != hipSuccess || hipMalloc(&b, bytes_per_array) != hipSuccess ||
+      hipMalloc(&c, bytes_per_array) != hipSuccess || hipMalloc(&sink, BW_READ_NT * 4) != hipSuccess) {
+    rc = fail(nullptr, "hbm_bandwidth: allocation failed");
+  } else if (hipMemset(a, 0, bytes_per_array) != hipSuccess || hipMemset(b, 0, bytes_per_array) != hipSuccess ||
+             hipMemset(c, 0, bytes_per_array) != hipSuccess || hipEventCreate(&e0) != hipSuccess ||
+             hipEventCreate(&e1) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+    rc = fail(nullptr, "hbm_bandwidth: set-up failed");
+  } else {
+    // best of `reps` timed passes after one warm-up pass, the triads first, then the reads
+    auto best_of = [&](auto launch, double moved, double* out) {
+      double best = 0.0;
+      for (uint32_t i = 0; i <= reps; ++i) {
+        float ms = 0.0f;
+        (void)hipEventRecord(e0, nullptr);
+        launch();
+        (void)hipEventRecord(e1, nullptr);
+        if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+          return fail(nullptr, "hbm_bandwidth: timing failed");
+        if (i > 0 && ms > 0.0f) best = std::max(best, moved / (ms * 1e-3) / 1e9);
+      }
+      *out = best;
+      return 0;
+    };
+    rc = best_of([&] { hipLaunchKernelGGL(k_bw_triad, dim3((uint32_t)(n4 / (BW_TRIAD_NT * BW_TRIAD_U))),
+                                          dim3(BW_TRIAD_NT), 0, nullptr, a, b, c, 3.0f); },
+                 3.0 * bytes_per_array, triad_gbs);
+    if (!rc)
+      rc = best_of([&] { hipLaunchKernelGGL(k_bw_read, dim3((uint32_t)(n4 / (BW_READ_NT * BW_READ_U))),
+                                            dim3(BW_READ_NT), 0, nullptr, b, sink); },
+                   1.0 * bytes_per_array, read_gbs);
+    if (!rc && hipGetLastError() != hipSuccess) rc = fail(nullptr, "hbm_bandwidth: launch failed");
+  }
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  (void)hipFree(a);
+  (void)hipFree(b);
+  (void)hipFree(c);
+  (void)hipFree(sink);
+  return rc;
 }
 
 // ------------------------------------------------------------------ kernel-level ABI

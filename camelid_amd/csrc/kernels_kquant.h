@@ -114,8 +114,8 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int cc = min(lane + 64 * i, NC - 1);
-      wv[k][i] = np[cc];
-      hv[k][i] = hp[cc >> 3];
+      wv[k][i] = ld_stream(np + cc);
+      hv[k][i] = ld_stream(hp + (cc >> 3));
     }
   }
   if (xf) {  // the activation given in f32: each wave quantizes blocks wave, wave + 4, ... to Q8_K
@@ -262,10 +262,10 @@ __device__ __forceinline__ void gemv_q6k_body(const int bid, const uint8_t* __re
       const bool valid = u < NU;  // uniform per 4-lane superblock group (NU % 4 == 0)
       const int uu = min(u, NU - 1);
       const int s = uu >> 2, n = (uu >> 1) & 1, q0 = (uu & 1) * 16;
-      const uint4 l0 = *reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + q0);
-      const uint4 l1 = *reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + 32 + q0);
-      const uint4 hh = *reinterpret_cast<const uint4*>(qhr + s * 64 + n * 32 + q0);
-      const uint4 scv = *reinterpret_cast<const uint4*>(scr + s * 16);
+      const uint4 l0 = ld_stream(reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + q0));
+      const uint4 l1 = ld_stream(reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + 32 + q0));
+      const uint4 hh = ld_stream(reinterpret_cast<const uint4*>(qhr + s * 64 + n * 32 + q0));
+      const uint4 scv = ld_stream(reinterpret_cast<const uint4*>(scr + s * 16));
       const uint32_t L0[4] = {l0.x, l0.y, l0.z, l0.w}, L1[4] = {l1.x, l1.y, l1.z, l1.w};
       const uint32_t HH[4] = {hh.x, hh.y, hh.z, hh.w};
       const uint32_t SC[4] = {scv.x, scv.y, scv.z, scv.w};
@@ -648,10 +648,10 @@ __global__ __launch_bounds__(KQ_NT) void k_gemv_q6k_multi(const uint8_t* __restr
       const bool valid = u < NU;  // uniform per 4-lane superblock group (NU % 4 == 0)
       const int uu = min(u, NU - 1);
       const int s = uu >> 2, n = (uu >> 1) & 1, q0 = (uu & 1) * 16;
-      const uint4 l0 = *reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + q0);
-      const uint4 l1 = *reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + 32 + q0);
-      const uint4 hh = *reinterpret_cast<const uint4*>(qhr + s * 64 + n * 32 + q0);
-      const uint4 scv = *reinterpret_cast<const uint4*>(scr + s * 16);
+      const uint4 l0 = ld_stream(reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + q0));
+      const uint4 l1 = ld_stream(reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + 32 + q0));
+      const uint4 hh = ld_stream(reinterpret_cast<const uint4*>(qhr + s * 64 + n * 32 + q0));
+      const uint4 scv = ld_stream(reinterpret_cast<const uint4*>(scr + s * 16));
       const float dsb = half_bits_to_float(dw[(size_t)row * NSB + s]);
       const uint32_t L0[4] = {l0.x, l0.y, l0.z, l0.w}, L1[4] = {l1.x, l1.y, l1.z, l1.w};
       const uint32_t HH[4] = {hh.x, hh.y, hh.z, hh.w};
@@ -887,8 +887,8 @@ __global__ __launch_bounds__(KQ_NT) void k_gemv_q4k_multi(const uint8_t* __restr
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int cc = min(lane + 64 * i, NC - 1);
-      wv[i] = np[cc];
-      hv[i] = hp[cc >> 3];
+      wv[i] = ld_stream(np + cc);
+      hv[i] = ld_stream(hp + (cc >> 3));
     }
   }
   for (int c = tid; c < (T * K) >> 4; c += KQ_NT) reinterpret_cast<int4*>(xq)[c] = reinterpret_cast<const int4*>(yq)[c];

@@ -320,8 +320,8 @@ __global__ __launch_bounds__(256) void k_gemv_multi(const int8_t* __restrict__ w
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int c = min(lane + 64 * i, CPR - 1);
-      wv[k][i] = w4[c];
-      dv[k][i] = d[c >> 1];
+      wv[k][i] = ld_stream(w4 + c);
+      dv[k][i] = ld_stream(d + (c >> 1));
     }
   }
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0): this wave's direct loads have landed

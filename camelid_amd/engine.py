@@ -219,7 +219,8 @@ class HipResidentDecode:
         return out
 
     # -- measurement ------------------------------------------------------------------------
-    PROFILE_CATEGORIES = ("gemv", "rmsnorm_quant", "attention", "silu_quant", "head", "embed")
+    # prefill_gemm: the prefill projections; its "bytes" are int8 operations
+    PROFILE_CATEGORIES = ("gemv", "rmsnorm_quant", "attention", "silu_quant", "head", "embed", "prefill_gemm")
 
     def profile_begin(self) -> None:
         self._chk(self._lib.camelid_hip_profile_begin(self._h))

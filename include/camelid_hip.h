@@ -137,8 +137,9 @@ int camelid_hip_read_hidden(camelid_hip_engine* e, float* out);
  * end every kernel launch is bracketed by events (the device-side loop then runs without
  * its graph); end synchronises and returns, per category (0 Q8_0 GEMV incl. the lm_head +
  * argmax launch, 1 RMSNorm+quantize, 2 attention incl. QK-norm/RoPE/KV store, 3 SwiGLU +
- * quantize, 4 unused, 5 embedding gather), the summed kernel milliseconds, algorithmic bytes
- * and launch count. */
+ * quantize, 4 argmax finish, 5 embedding gather, 6 the prefill projections: matrix-core GEMMs
+ * and multi-token GEMVs, whose "bytes" are int8 operations, 2 per weight and token), the
+ * summed kernel milliseconds, algorithmic bytes and launch count. */
 int camelid_hip_profile_begin(camelid_hip_engine* e);
 int camelid_hip_profile_end(camelid_hip_engine* e, double* ms, double* bytes, uint64_t* launches,
                             uint32_t n_cat);
@@ -154,6 +155,11 @@ int camelid_hip_profile_end(camelid_hip_engine* e, double* ms, double* bytes, ui
  * exponentials, denominator, output sums, end).  Copies min(n, 64*64*7 + 2*256*8 + 2*1024*8)
  * words; *n_out receives the count. */
 int camelid_hip_phase_stamps(uint64_t* out, size_t n, size_t* n_out);
+/* Measurement hook (no reference counterpart): HBM bandwidth of this device, best of `reps`
+ * passes over three device arrays of bytes_per_array each (a multiple of 128 KiB; allocated
+ * and freed here): STREAM's triad a = b + 3c (3 x bytes_per_array moved per pass) and a
+ * read-only pass over b, both with nontemporal loads and stores.  GB/s = 1e9 bytes per second. */
+int camelid_hip_hbm_bandwidth(size_t bytes_per_array, uint32_t reps, double* triad_gbs, double* read_gbs);
 /* Device name and compute units. */
 int camelid_hip_device_info(char* name, size_t name_len, int* n_cu);
 

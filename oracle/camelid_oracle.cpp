@@ -36,6 +36,7 @@
 #include <cstring>
 #include <vector>
 #include <algorithm>
+#include <omp.h>
 
 #define OX extern "C" __attribute__((visibility("default")))
 
@@ -730,3 +731,7 @@ OX void oracle_serial_sum_rows(const float* x, size_t rows, size_t n, float* out
     out[r] = acc;
   }
 }
+
+// OpenMP threads of the row-parallel loops (the baseline timing runs at several counts;
+// the results do not depend on it: every output row is computed by one thread).
+OX void oracle_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }

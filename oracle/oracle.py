@@ -58,6 +58,7 @@ _SIG = {
     "oracle_kquant_gemv": (None, [C.c_int, u8p, C.c_size_t, C.c_size_t, f32p, i8p, f32p]),
     "oracle_model_set_quant": (None, [vp, C.c_uint32, u8p]),
     "oracle_model_set_output_quant": (None, [vp, C.c_int, C.c_int]),
+    "oracle_set_threads": (None, [C.c_int]),
 }
 
 _lib = None
@@ -80,6 +81,11 @@ def lib() -> C.CDLL:
             fn.argtypes = a
         _lib = h
     return _lib
+
+
+def set_threads(n: int) -> None:
+    """OpenMP threads of the oracle's row-parallel loops (no effect on any result)."""
+    lib().oracle_set_threads(int(n))
 
 
 def P(a, t):
