@@ -542,6 +542,7 @@ cm::Prefetch prefetch_of(const KMat* m) {
 
 size_t attn_sc_bytes(uint32_t kvs) { return (((size_t)kvs + 3) & ~(size_t)3) * 4; }
 int attn_ring_slots(uint32_t kvs);
+int attn_out_slots(uint32_t kvs, int slots, int* pb);
 
 template <bool FUSED>
 void launch_attention(uint32_t hd, uint32_t n_heads, int slots, hipStream_t s, const float* qsrc, int nh, int nkv,
@@ -578,8 +579,18 @@ void launch_attention_split(uint32_t hd, uint32_t n_heads, int slots, hipStream_
               dim3(HD > ATT_SLICE ? HD : ATT_SLICE), 0, s, qsrc, nh, nkv, rope_dim, split_half, cb, sb, rs, qn, kn, \
               eps, kc, vc, layer, kvs, pos, scale, g_sc, g_mx);                                                   \
     const uint32_t grid = n_heads * (HD / 32) + (pf.a_lines ? PREFETCH_WGS : 0);                                  \
-    CM_LAUNCH((cm::k_att_out<HD>), dim3(grid), dim3(cm::att_nt(HD)), lds, s, vc, nh, nkv, layer, kvs, pos, g_sc,  \
-              g_mx, nsl, (HD > ATT_SLICE ? HD : ATT_SLICE), att, xq, xs, slots, pf);                              \
+    int pb = 0;                                                                                                    \
+    const int so = attn_out_slots((uint32_t)kvs, slots, &pb);                                                      \
+    const size_t lds_o = (size_t)so * cm::ATT_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs) + cm::avp_bytes(pb); \
+    if (pb == 256)                                                                                                 \
+      CM_LAUNCH((cm::k_att_out<HD, 256>), dim3(grid), dim3(cm::att_nt(HD)), lds_o, s, vc, nh, nkv, layer, kvs, pos, \
+                g_sc, g_mx, nsl, (HD > ATT_SLICE ? HD : ATT_SLICE), att, xq, xs, so, pf);                          \
+    else if (pb == 128)                                                                                            \
+      CM_LAUNCH((cm::k_att_out<HD, 128>), dim3(grid), dim3(cm::att_nt(HD)), lds_o, s, vc, nh, nkv, layer, kvs, pos, \
+                g_sc, g_mx, nsl, (HD > ATT_SLICE ? HD : ATT_SLICE), att, xq, xs, so, pf);                          \
+    else                                                                                                           \
+      CM_LAUNCH((cm::k_att_out<HD, 64>), dim3(grid), dim3(cm::att_nt(HD)), lds_o, s, vc, nh, nkv, layer, kvs, pos,  \
+                g_sc, g_mx, nsl, (HD > ATT_SLICE ? HD : ATT_SLICE), att, xq, xs, so, pf);                          \
   }
   if (hd == 64) CM_ATTS(64)
   else if (hd == 128) CM_ATTS(128)
@@ -635,7 +646,7 @@ long attn_static_lds() {
     CM_ATT_LDS(256, true) CM_ATT_LDS(256, false)
 #undef CM_ATT_LDS
 #define CM_ATTO_LDS(HD)                                                                      \
-  if (hipFuncGetAttributes(&a, reinterpret_cast<const void*>(&cm::k_att_out<HD>)) == hipSuccess) \
+  if (hipFuncGetAttributes(&a, reinterpret_cast<const void*>(&cm::k_att_out<HD, 128>)) == hipSuccess) \
     m = std::max<long>(m, (long)a.sharedSizeBytes);                                           \
   else                                                                                        \
     m = std::max<long>(m, ATT_STATIC_LDS_BOUND);
@@ -646,7 +657,8 @@ long attn_static_lds() {
   return bytes;
 }
 
-int attn_ring_slots(uint32_t kvs) {
+// LDS per workgroup of the device (read once; the gfx950 figure without a device).
+long attn_lds_limit() {
   static int limit = -1;
   if (limit < 0) {
     int dev = 0, v = 0;
@@ -654,9 +666,32 @@ int attn_ring_slots(uint32_t kvs) {
       v = GFX950_LDS_PER_WORKGROUP;
     limit = v;
   }
-  const long room = (long)limit - attn_static_lds() - (long)attn_sc_bytes(kvs);
+  return limit;
+}
+
+int attn_ring_slots(uint32_t kvs) {
+  const long room = attn_lds_limit() - attn_static_lds() - (long)attn_sc_bytes(kvs);
   const long slots = std::min<long>(4, room / (cm::ATT_RING_GRANULES * 16));
-  return slots >= 2 ? (int)slots : 0;
+  // the split output kernel also holds its product buffers (64-position blocks at least),
+  // and two ring chunks beside them
+  const long out_slots = (room - (long)cm::avp_bytes(64)) / (cm::ATT_RING_GRANULES * 16);
+  return slots >= 2 && out_slots >= 2 ? (int)slots : 0;
+}
+
+// Ring slots of the split output kernel: its products and counters take LDS beside the ring.
+// Ring slots and product block of the split output kernel, whose product buffers take LDS
+// beside the V ring: the largest block of 256, 128, 64 positions that leaves two ring chunks
+// (attn_ring_slots admitted kvs only with room for two beside 64-position blocks).
+int attn_out_slots(uint32_t kvs, int slots, int* pb) {
+  const long room = (long)attn_lds_limit() - attn_static_lds() - (long)attn_sc_bytes(kvs);
+  constexpr long chunk = (long)cm::ATT_RING_GRANULES * 16;
+  *pb = 64;
+  for (int b : {256, 128})
+    if ((room - (long)cm::avp_bytes(b)) / chunk >= 2) {
+      *pb = b;
+      break;
+    }
+  return (int)std::min<long>(slots, (room - (long)cm::avp_bytes(*pb)) / chunk);
 }
 
 // Algorithmic bytes of one K-quant GEMV launch: superblocks (144 or 210 B per 256 values),

@@ -1828,6 +1828,19 @@ __device__ __forceinline__ float att_onepass_sum(const float* v, int P, FsLds<NT
 #undef CM_AOP
 }
 
+// Workgroups are dealt to the 8 XCDs round-robin (workgroup b runs on XCD b % 8), and each
+// XCD has an L2 of its own.  The attention workgroups that read the same KV rows (the query
+// heads of one KV head; with `parts` workgroups per head, the same part of them) are mapped
+// to one XCD, so that the rows come from HBM once and from that L2 for the rest.  Workgroup b
+// of n_kv * parts * rep returns its (kv unit, member) as kv_unit * rep + member, where kv unit
+// u = kv_head * parts + part; the identity when the units do not divide over the XCDs.
+constexpr int N_XCD = 8;
+__device__ __forceinline__ int xcd_member(int b, int n_units, int rep) {
+  if (n_units % N_XCD != 0) return b;
+  const int x = b % N_XCD, i = b / N_XCD;
+  return (x + N_XCD * (i / rep)) * rep + i % rep;
+}
+
 template <int HD, bool FUSED>
 __global__ __launch_bounds__(att_nt(HD)) void k_attention(
     const float* __restrict__ qsrc, int n_heads, int n_kv, int rope_dim, int split_half,
@@ -1860,8 +1873,8 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   __shared__ uint64_t etab[32];  // the expf table, read from LDS by the exponentials
   __shared__ FsLds<ATT_NT> fs;
   const int tid = threadIdx.x;
-  const int h = blockIdx.x;
   const int rep = n_heads / n_kv;
+  const int h = xcd_member(blockIdx.x, n_kv, rep);
   const int kvh = h / rep;
   const size_t hbase = kv_head_base(layer, n_kv, kvh, HD, kvs);
   const uint4* kg = reinterpret_cast<const uint4*>(kc + hbase);  // K granule (u, p): u * kvs + p
@@ -2178,7 +2191,8 @@ __global__ __launch_bounds__(NT) void k_att_scores(
   __shared__ __align__(16) float sq[2 * HD];
   __shared__ float red[ATT_NT / 64];
   __shared__ float s_qscale, s_kscale;
-  const int tid = threadIdx.x, h = blockIdx.x, s = blockIdx.y;
+  const int tid = threadIdx.x, s = blockIdx.y;
+  const int h = gridDim.x % N_XCD == 0 ? xcd_member(blockIdx.x, n_kv, n_heads / n_kv) : (int)blockIdx.x;
   const int pos = (int)*d_pos;
   if (kv_pos_bad(pos, kvs)) return;  // (uniform, before any barrier)
   const int p0 = s * ATT_NT;
@@ -2288,7 +2302,13 @@ __global__ __launch_bounds__(NT) void k_att_scores(
   CM_SPLIT_STAMP(0, wg, 3)
 }
 
-template <int HD>
+// The split output kernel's products: two buffers of [32 dims][PB positions + 4] f32 (the
+// row pad keeps the 16-byte LDS reads and writes of consecutive dims on distinct banks),
+// placed after the scores in dynamic LDS.  Larger blocks pay the per-block barrier fewer
+// times; the launch takes the largest of 256, 128, 64 that leaves two V ring chunks.
+__host__ __device__ constexpr size_t avp_bytes(int pb) { return (size_t)2 * 32 * (pb + 4) * 4; }
+
+template <int HD, int PB>
 __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
     const uint16_t* __restrict__ vc, int n_heads, int n_kv, int layer, int kvs, const uint32_t* __restrict__ d_pos,
     const float* __restrict__ g_sc, const float* __restrict__ g_max, int n_slices, int n_slices_pos,
@@ -2302,9 +2322,13 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
   constexpr int LH = ATT_RING_LOADS / NH;      // 1 KB wave loads per staging wave per chunk
   constexpr int CG = ATT_RING_GRANULES / DW;   // 8-position groups per ring chunk
   static_assert(CG % 4 == 0, "ring chunks hold a multiple of 4 granule groups");
+  constexpr int BG = PB / 8;  // groups per product block
+  constexpr int AVP_RS = PB + 4;
+  static_assert(CG % BG == 0, "product blocks tile the ring chunks");
   extern __shared__ __align__(16) float4 dyn[];
   float4* ring = dyn;
   float* sc = reinterpret_cast<float*>(dyn + (size_t)ring_slots * ATT_RING_GRANULES);
+  float* pbuf = sc + ((kvs + 3) & ~3);  // (16-byte aligned)
   const int nwork = n_heads * NDW;
   if ((int)blockIdx.x >= nwork) {  // spare workgroups: read ahead the output projection
     prefetch_lines(pf, blockIdx.x - nwork, gridDim.x - nwork, sc);
@@ -2315,8 +2339,10 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
   __shared__ uint64_t etab[32];
   __shared__ FsLds<ATT_NT> fs;
   const int tid = threadIdx.x;
-  const int h = (int)blockIdx.x / NDW, w = (int)blockIdx.x % NDW;
   const int rep = n_heads / n_kv;
+  // (head, part): unit u = kv head * NDW + w, shared by the group's rep heads
+  const int m = xcd_member(blockIdx.x, n_kv * NDW, rep);
+  const int w = (m / rep) % NDW, h = (m / rep / NDW) * rep + m % rep;
   const size_t hbase = kv_head_base(layer, n_kv, h / rep, HD, kvs);
   const uint4* vg = reinterpret_cast<const uint4*>(vc + hbase);  // V granule (g, d): g * HD + d
   const int pos = (int)*d_pos;
@@ -2391,70 +2417,84 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
     }
     CM_SPLIT_STAMP(1, (int)blockIdx.x, 3)
     for (int p = tid; p < P; p += ATT_NT) sc[p] = sc[p] * inv;
-    for (int c = 0; c < nchunks; ++c) {
-      if (stager) wait_vmcnt(LH * (min(c + R - 2, nchunks - 1) - c));  // chunk c has landed
-      __syncthreads();  // chunk c visible; the slot of chunk c - 1 is free
-      if (stager && c + R - 1 < nchunks) stage(c + R - 1);
-      if (tid < DW) {
-        const uint4* slot = reinterpret_cast<const uint4*>(ring + (size_t)(c % R) * ATT_RING_GRANULES) + tid;
-        const float4* pr4 = reinterpret_cast<const float4*>(sc) + (size_t)c * CG * 2;
-        const int gn = min(CG, ng - c * CG);
-        auto granule = [&](const uint4& g, const float4& q0, const float4& q1, float(&pr)[8]) {
-          pr[0] = mul_f16_lo(q0.x, g.x);
-          pr[1] = mul_f16_hi(q0.y, g.x);
-          pr[2] = mul_f16_lo(q0.z, g.y);
-          pr[3] = mul_f16_hi(q0.w, g.y);
-          pr[4] = mul_f16_lo(q1.x, g.z);
-          pr[5] = mul_f16_hi(q1.y, g.z);
-          pr[6] = mul_f16_lo(q1.z, g.w);
-          pr[7] = mul_f16_hi(q1.w, g.w);
-        };
-        if (gn == CG) {
-          uint4 va[2], vb[2];
-          float4 pa[4], pb[4];
-          auto ld = [&](uint4(&v)[2], float4(&pq)[4], int j0) {
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-              v[u] = slot[(j0 + u) * DW];
-              pq[2 * u] = pr4[2 * (j0 + u)];
-              pq[2 * u + 1] = pr4[2 * (j0 + u) + 1];
-            }
-          };
-          auto mac = [&](const uint4(&v)[2], const float4(&pq)[4]) {
-            float pr[2][8];
-            granule(v[0], pq[0], pq[1], pr[0]);
-            granule(v[1], pq[2], pq[3], pr[1]);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int u = 0; u < 2; ++u)
-#pragma unroll
-              for (int e = 0; e < 8; ++e) acc += pr[u][e];
-          };
-          // blocks of 16 groups, each fully unrolled (the LDS reads run one batch ahead)
-          for (int j0 = 0; j0 < CG; j0 += 16) {
-            ld(va, pa, j0);
-#pragma unroll
-            for (int j = j0; j < j0 + 16; j += 4) {
-              ld(vb, pb, j + 2);
-              __builtin_amdgcn_sched_barrier(0);
-              mac(va, pa);
-              if (j + 4 < j0 + 16) ld(va, pa, j + 4);
-              __builtin_amdgcn_sched_barrier(0);
-              mac(vb, pb);
-            }
-          }
-        } else {
-          for (int j = 0; j < gn; ++j) {
-            float pr[8];
-            granule(slot[j * DW], pr4[2 * j], pr4[2 * j + 1], pr);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc += pr[e];
-          }
+    // ---- out_d = fold_p prob_p * v_pd over the full 8-position groups: the products of a
+    // block of BG groups are formed by all waves but wave 0 (the rounded f32 product of the
+    // probability and the f16 value, as the chain would form it) into one of two LDS buffers,
+    // while wave 0's output lanes (lane d = dim d) add the previous block's in position
+    // order: the chain then only adds.  One barrier per block; the staging waves keep V
+    // chunks landing in the ring on a fixed schedule (chunk c's slot is refilled once the
+    // products of its last block have been formed).
+    constexpr int BPC = CG / BG;  // product blocks per ring chunk
+    const int nb = (ng + BG - 1) / BG;
+    int issued = min(R - 1, nchunks);  // ring chunks issued so far (staging waves)
+    auto products = [&](int b) {
+      const int c = b / BPC;
+      const uint4* slot = reinterpret_cast<const uint4*>(ring + (size_t)(c % R) * ATT_RING_GRANULES);
+      float* dst0 = pbuf + (size_t)(b & 1) * DW * AVP_RS;
+      for (int gi = tid - 64; gi < BG * DW; gi += ATT_NT - 64) {
+        const int gl = gi / DW, dd = gi % DW, g = b * BG + gl;
+        if (g < ng) {
+          const uint4 v = slot[(g - c * CG) * DW + dd];
+          const float4 q0 = reinterpret_cast<const float4*>(sc)[2 * g];
+          const float4 q1 = reinterpret_cast<const float4*>(sc)[2 * g + 1];
+          float4* dst = reinterpret_cast<float4*>(dst0 + (size_t)dd * AVP_RS + gl * 8);
+          dst[0] = make_float4(mul_f16_lo(q0.x, v.x), mul_f16_hi(q0.y, v.x), mul_f16_lo(q0.z, v.y),
+                               mul_f16_hi(q0.w, v.y));
+          dst[1] = make_float4(mul_f16_lo(q1.x, v.z), mul_f16_hi(q1.y, v.z), mul_f16_lo(q1.z, v.w),
+                               mul_f16_hi(q1.w, v.w));
         }
       }
+    };
+    if (nb > 0) {
+      if (stager) {
+        if (issued < min(R, nchunks)) stage(issued++);  // chunk R - 1 into the unused slot
+        wait_vmcnt(LH * (issued - 1));                  // chunk 0 has landed
+      }
+      __syncthreads();  // chunk 0 and the normalised probabilities
+      if (tid >= 64) products(0);
+      __syncthreads();
+    }
+    for (int b = 0; b < nb; ++b) {
+      if (tid < DW) {
+        const float4* row = reinterpret_cast<const float4*>(pbuf + ((size_t)(b & 1) * DW + tid) * AVP_RS);
+        const int n4 = min(BG, ng - b * BG) * 2;  // 4-position pieces of this block
+        if (n4 == BG * 2) {
+          // 8 pieces in flight ahead of the adds (ping-pong), as in fold_lds
+          float4 x[8], y[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) x[i] = row[i];
+#pragma unroll
+          for (int j = 8; j < BG * 2; j += 16) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) y[i] = row[j + i];
+            __builtin_amdgcn_sched_barrier(0);
+            add8(acc, x);
+            if (j + 8 < BG * 2) {
+#pragma unroll
+              for (int i = 0; i < 8; ++i) x[i] = row[j + 8 + i];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            add8(acc, y);
+          }
+        } else {
+          for (int i = 0; i < n4; ++i) add4(acc, row[i]);
+        }
+      } else if (tid >= 64) {
+        if (b + 1 < nb) products(b + 1);
+        if (stager) {
+          // chunk c's last block was formed in the previous iteration: refill its slot
+          if (b % BPC == BPC - 1) {
+            const int c = (b - (BPC - 1)) / BPC;
+            if (c + R < nchunks && c + R >= issued) stage(issued++);
+          }
+          // the products of the next iteration read a new chunk: it must have landed
+          const int q = (b + 2) / BPC;
+          if ((b + 2) % BPC == 0 && q < nchunks) wait_vmcnt(LH * (issued - 1 - q));
+        }
+      }
+      __syncthreads();  // wave 0 is done with buffer b & 1; block b + 1's products are visible
     }
     CM_SPLIT_STAMP(1, (int)blockIdx.x, 4)
-    __syncthreads();  // the normalised probabilities past the ring (and with no chunks at all)
     if (tid < DW) {
 #pragma unroll
       for (int u = 0; u < 8; ++u)
