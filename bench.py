@@ -224,14 +224,18 @@ def attention_phases(cfg) -> dict:
     and the launch span (first start to last end), in microseconds."""
     import ctypes as C
     from camelid_amd import _native as N
-    na, ng, nsp = 64 * 64 * 7, 2 * 256 * 8, 2 * 1024 * 8
+    na, ng, nsp = 64 * 64 * 9, 2 * 256 * 8, 2 * 1024 * 8
     buf = (C.c_uint64 * (na + ng + nsp))()
     got = C.c_size_t(0)
     N.check(N.lib().camelid_hip_phase_stamps(buf, na + ng + nsp, C.byref(got)))
     allst = np.frombuffer(buf, np.uint64).astype(np.int64)
-    st = allst[:na].reshape(64, 64, 7)[:cfg.n_layers, :cfg.n_heads]
-    d = np.diff(st, axis=2) * 0.01  # 100 MHz ticks -> us
+    st = allst[:na].reshape(64, 64, 9)[:cfg.n_layers, :cfg.n_heads]
+    d = np.diff(st[:, :, :7], axis=2) * 0.01  # 100 MHz ticks -> us
     res = {name: round(float(d[:, :, i].mean()), 3) for i, name in enumerate(ATT_PHASES)}
+    # inside the score phase (from its start): thread 0's K-row loads issued, wave 0's scores done
+    for i, name in ((7, "k_rows_issued"), (8, "wave0_scores_done")):
+        v = (st[:, :, i] - st[:, :, 1]) * 0.01
+        res[name] = round(float(v[st[:, :, i] > 0].mean()), 3) if (st[:, :, i] > 0).any() else None
     res["workgroup_total"] = round(float((st[:, :, 6] - st[:, :, 0]).mean() * 0.01), 3)
     res["start_spread"] = round(float((st[:, :, 0].max(1) - st[:, :, 0].min(1)).mean() * 0.01), 3)
     res["launch_span"] = round(float((st[:, :, 6].max(1) - st[:, :, 0].min(1)).mean() * 0.01), 3)

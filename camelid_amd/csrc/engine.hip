@@ -116,6 +116,7 @@ struct camelid_hip_engine {
   float* att_mx = nullptr;
   int att_mode = -1;       // -1: by position; 0 / 1: single / split (graph capture)
   bool read_ahead = true;  // spare workgroups of the norm kernels read ahead the next weights
+  bool kv_ahead = true;    // the qkv GEMV's idle norm waves read the layer's KV rows into L2
   bool gu_fused = false;   // gate/up rows interleaved by 32, SwiGLU fused into their GEMV
   bool norm_fused = true;  // RMSNorms computed inside the qkv and gate/up GEMVs (Q8_0 layers)
   bool qkv_merged = true;  // Q4_K q|k and Q6_K v projections in one launch (k_gemv_qk4_v6)
@@ -464,7 +465,8 @@ void launch_gemv(const Q8Mat& m, const int8_t* xq, const float* xs, float* y, co
 // y = W · rmsnorm(x; nw) for a Q8_0 W whose width is a fused-norm width (2048, 3072, 4096):
 // at most 32 rows per workgroup, spread over up to 256 workgroups; the 8 weight waves hold
 // ceil(rows per workgroup / 8) rows each.
-void launch_gemv_norm(const Q8Mat& m, const float* x, const float* nw, float eps, float* y, hipStream_t s) {
+void launch_gemv_norm(const Q8Mat& m, const float* x, const float* nw, float eps, float* y, hipStream_t s,
+                      cm::KvAhead kva = cm::KvAhead{}) {
   const uint32_t per = std::min(32u, std::max(1u, (m.rows + 255u) / 256u));
   const uint32_t grid = (m.rows + per - 1) / per;
   const uint32_t rpw = (per + 7) / 8;
@@ -472,7 +474,7 @@ void launch_gemv_norm(const Q8Mat& m, const float* x, const float* nw, float eps
 #define CM_GN(K, RPW)                                                                                                 \
   case K * 8 + RPW:                                                                                                   \
     CM_LAUNCH((cm::k_gemv_norm<K, RPW>), dim3(grid), dim3(cm::GN_NT), 0, s, m.q, m.d, (int)m.rows, (int)per, x, nw, \
-              eps, y);                                                                                                \
+              eps, y, kva);                                                                                           \
     return;
     CM_GN(2048, 1) CM_GN(2048, 2) CM_GN(2048, 3) CM_GN(2048, 4)
     CM_GN(3072, 1) CM_GN(3072, 2) CM_GN(3072, 3) CM_GN(3072, 4)
@@ -873,7 +875,12 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const f
   const bool gu_norm = norm_fused && e->gu_fused && cm::gu_norm_k((int)d.hidden);
   if (norm_fused) {
     ProfScope ps(e, P_GEMV, q8_bytes(L.qkv, false) + d.hidden * 8.0);
-    launch_gemv_norm(L.qkv, e->h, L.attn_norm, d.eps, e->qkv, s);
+    // the attention that follows reads this layer's K/V rows from its XCDs' L2
+    cm::KvAhead kva{};
+    if (e->kv_ahead && !att_split(e))
+      kva = cm::KvAhead{e->kc, e->vc, &e->st->pos, (int)l, (int)d.n_heads, (int)d.n_kv_heads, (int)d.head_dim,
+                        (int)e->kvs, 1};
+    launch_gemv_norm(L.qkv, e->h, L.attn_norm, d.eps, e->qkv, s, kva);
   } else {
     rmsnorm(e, L.attn_norm, &L.qkv);
     gemv(e, L.qkv, e->qkv, nullptr);
@@ -1282,7 +1289,8 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   e->d = d;
   if (const char* dev = std::getenv("CAMELID_HIP_DEVICE")) e->device = std::atoi(dev);
   if (const char* g = std::getenv("CAMELID_HIP_GRAPHS")) e->use_graph = std::atoi(g) != 0;
-  if (const char* r = std::getenv("CAMELID_HIP_READ_AHEAD")) e->read_ahead = std::atoi(r) != 0;
+  if (const char* r = std::getenv("CAMELID_HIP_READ_AHEAD")) e->read_ahead = e->kv_ahead = std::atoi(r) != 0;
+  if (const char* r = std::getenv("CAMELID_HIP_KV_AHEAD")) e->kv_ahead = std::atoi(r) != 0;
   if (const char* p = std::getenv("CAMELID_HIP_PREFILL")) e->prefill_batched = std::strcmp(p, "token") != 0;
   hipError_t st = hipSetDevice(e->device);
   if (st != hipSuccess) {

@@ -1116,6 +1116,86 @@ struct NormTeamLds {
   FsLds<NTEAM> fs;
 };
 
+// ---------------------------------------------------------------------------
+// KV cache layout.  Per layer and kv head a region of hd * kvs elements (kvs: the position
+// stride, a multiple of 8) at kv_head_base; inside it, f16 bits,
+//   K: [hd/8][kvs][8]  -- 16-byte granule = 8 dims of one position,
+//   V: [kvs/8][hd][8]  -- 16-byte granule = 8 positions of one dim,
+// so that lanes over consecutive positions (scores) or consecutive dims (the output sum)
+// read consecutive granules.  Both products (q * k, p * v) are one mixed-precision FMA on
+// the f16 value, so each position costs the serial add chain two VALU operations.
+__host__ __device__ __forceinline__ size_t kv_head_base(int layer, int n_kv, int kvh, int hd, int kvs) {
+  return ((size_t)layer * n_kv + kvh) * (size_t)hd * kvs;
+}
+__host__ __device__ __forceinline__ size_t kv_k_index(int kvs, int p, int d) {
+  return ((size_t)(d >> 3) * kvs + p) * 8 + (d & 7);
+}
+__host__ __device__ __forceinline__ size_t kv_v_index(int hd, int p, int d) {
+  return ((size_t)(p >> 3) * hd + d) * 8 + (p & 7);
+}
+
+// Read-ahead of one layer's KV cache into the L2 of the XCD whose attention workgroups will
+// read it.  Workgroup b of a launch runs on XCD b % 8, each XCD has an L2 of its own, and an
+// L2 line stays valid across kernel boundaries (measured on MI355X: a line read by one kernel
+// is hit at ~93 ns by the next kernel's workgroups on the same XCD, ~235 ns from other XCDs,
+// ~370 ns cold).  The single-workgroup decode attention maps its workgroup b to head
+// xcd_member(b, n_kv, rep); the read-ahead workgroups on XCD x touch one word of every
+// 128-byte line of the K and V rows [0, pos) of the KV heads that those heads read, so that
+// the attention's K-row loads and V staging hit the L2 instead of HBM.  Loads only; pos (the
+// row the attention kernel itself writes) and beyond are not touched.  nwg % 8 == 0 workgroups
+// after the owning kernel's own; a position outside the cache reads nothing.
+// Workgroups are dealt to the 8 XCDs round-robin (workgroup b runs on XCD b % 8), and each
+// XCD has an L2 of its own.  The attention workgroups that read the same KV rows (the query
+// heads of one KV head; with `parts` workgroups per head, the same part of them) are mapped
+// to one XCD, so that the rows come from HBM once and from that L2 for the rest.  Workgroup b
+// of n_kv * parts * rep returns its (kv unit, member) as kv_unit * rep + member, where kv unit
+// u = kv_head * parts + part; the identity when the units do not divide over the XCDs.
+constexpr int N_XCD = 8;
+__device__ __forceinline__ int xcd_member(int b, int n_units, int rep) {
+  if (n_units % N_XCD != 0) return b;
+  const int x = b % N_XCD, i = b / N_XCD;
+  return (x + N_XCD * (i / rep)) * rep + i % rep;
+}
+
+struct KvAhead {
+  const uint16_t* kc;
+  const uint16_t* vc;
+  const uint32_t* d_pos;
+  int layer, n_heads, n_kv, hd, kvs;
+  int on;  // 0: no read-ahead
+};
+
+// The read-ahead share of lane `lane` of `nlanes` in workgroup b of a grid of `nwg`
+// workgroups (b runs on XCD b % 8; the workgroups of one XCD split its lines).
+__device__ __forceinline__ void kv_ahead(const KvAhead& a, int b, int nwg, int lane, int nlanes) {
+  const int x = b % N_XCD, member = b / N_XCD, members = (nwg - x + N_XCD - 1) / N_XCD;
+  const int pos = (int)*a.d_pos;
+  if (pos <= 0 || pos >= a.kvs) return;
+  const int rep = a.n_heads / a.n_kv;
+  const size_t kstripe = (size_t)((pos + 7) / 8);         // lines of one K stripe (8 dims, positions [0, pos))
+  const size_t lines_per_head = (size_t)(a.hd / 8) * kstripe;  // of K, and of V
+  const size_t stride = (size_t)members * nlanes;
+  uint32_t acc = 0;
+  int last = -1;
+  for (int w = x; w < a.n_heads; w += N_XCD) {
+    const int kvh = xcd_member(w, a.n_kv, rep) / rep;
+    if (kvh == last) continue;  // (consecutive heads of one group share their rows)
+    last = kvh;
+    const size_t base = kv_head_base(a.layer, a.n_kv, kvh, a.hd, a.kvs);
+    const uint32_t* k32 = reinterpret_cast<const uint32_t*>(a.kc + base);
+    const uint32_t* v32 = reinterpret_cast<const uint32_t*>(a.vc + base);
+    for (size_t l = (size_t)member * nlanes + lane; l < 2 * lines_per_head; l += stride) {
+      if (l < lines_per_head) {
+        const size_t u = l / kstripe, r = l - u * kstripe;  // stripe u (dims 8u..8u+7), line r
+        acc ^= k32[(u * (size_t)a.kvs * 16 + r * 128) / 4];
+      } else {
+        acc ^= v32[(l - lines_per_head) * 32];
+      }
+    }
+  }
+  asm volatile("" ::"v"(acc));  // keeps the loads
+}
+
 // Row stride of the block-major term layout [block][row] of the norm-fused GEMVs: an odd word
 // count, so that the lanes writing one row's terms (one block each) and the lanes folding the
 // rows (one row each) both touch distinct LDS banks.
@@ -1128,7 +1208,8 @@ __host__ __device__ constexpr int gemv_row_stride(int rows) { return rows | 1; }
 template <int K, int RPW>
 __global__ __launch_bounds__(GN_NT) void k_gemv_norm(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                      int rows, int rows_per_wg, const float* __restrict__ x,
-                                                     const float* __restrict__ nw, float eps, float* __restrict__ y) {
+                                                     const float* __restrict__ nw, float eps, float* __restrict__ y,
+                                                     KvAhead kva) {
   constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64;
   constexpr int NT = GN_TEAM_QKV;  // the norm team: waves 0..TW-1; waves TW.. hold the rows
   constexpr int NWV = GN_NT / 64, R = NWV * RPW, C = (K + NT - 1) / NT, TW = NT / 64;
@@ -1184,6 +1265,10 @@ __global__ __launch_bounds__(GN_NT) void k_gemv_norm(const int8_t* __restrict__ 
   norm_quantize_all<GN_NT>(xf, wf, K, team.scale, xl, xsl);
   __syncthreads();  // the normalised activation (Q8_0) is in LDS
   CM_GEMV_STAMP(0, 3, 0)
+  // (the weight scale enters as the raw f16 operand of a mixed-precision multiply, exactly
+  // float(sacc) * f32(scale) rounded once: a separate f16->f32 conversion was placed by the
+  // compiler right behind each row's loads inside the conditional load block, which made the
+  // wave wait for every row before issuing the next one)
 #pragma unroll
   for (int k = 0; k < RPW; ++k) {
     const int sl = slot_of(k);
@@ -1196,12 +1281,16 @@ __global__ __launch_bounds__(GN_NT) void k_gemv_norm(const int8_t* __restrict__ 
       int sacc = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
       sacc += dpp_xor1(sacc);
       if ((lane & 1) == 0 && c < CPR)
-        t[(c >> 1) * RS + sl] = ((float)sacc * half_bits_to_float(dv[k][i])) * xsl[c >> 1];
+        t[(c >> 1) * RS + sl] = mul_f16_lo((float)sacc, dv[k][i]) * xsl[c >> 1];
     }
   }
   CM_GEMV_STAMP(0, 4, 0)
   __syncthreads();
   if (tid < nrows) y[row0 + tid] = team.bad ? __builtin_nanf("") : fold_lds_strided<NB>(t + tid, RS);
+  // the norm team's other waves, idle from here on: the KV rows of the attention that follows
+  // into their XCD's L2 (nothing waits on these loads but the end of the kernel, which the
+  // folds of wave 0 hold up longer)
+  if (kva.on && wave >= 1 && wave < TW) kv_ahead(kva, blockIdx.x, gridDim.x, tid - 64, NT - 64);
   CM_GEMV_STAMP(0, 5, 0)
 }
 
@@ -1309,7 +1398,7 @@ __global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ 
       int sacc = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
       sacc += dpp_xor1(sacc);
       if ((lane & 1) == 0 && c < CPR)
-        t[(c >> 1) * RS + lr] = ((float)sacc * half_bits_to_float(dv[k][i])) * xsl[c >> 1];
+        t[(c >> 1) * RS + lr] = mul_f16_lo((float)sacc, dv[k][i]) * xsl[c >> 1];
     }
   }
   CM_GEMV_STAMP(1, 4, 0)
@@ -1611,24 +1700,6 @@ __global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict_
   if (kd) quantize_q8k_wg256(a, kq + (size_t)blockIdx.x * 256, kbs + (size_t)blockIdx.x * 8, kd + blockIdx.x);
 }
 
-// ---------------------------------------------------------------------------
-// KV cache layout.  Per layer and kv head a region of hd * kvs elements (kvs: the position
-// stride, a multiple of 8) at kv_head_base; inside it, f16 bits,
-//   K: [hd/8][kvs][8]  -- 16-byte granule = 8 dims of one position,
-//   V: [kvs/8][hd][8]  -- 16-byte granule = 8 positions of one dim,
-// so that lanes over consecutive positions (scores) or consecutive dims (the output sum)
-// read consecutive granules.  Both products (q * k, p * v) are one mixed-precision FMA on
-// the f16 value, so each position costs the serial add chain two VALU operations.
-__host__ __device__ __forceinline__ size_t kv_head_base(int layer, int n_kv, int kvh, int hd, int kvs) {
-  return ((size_t)layer * n_kv + kvh) * (size_t)hd * kvs;
-}
-__host__ __device__ __forceinline__ size_t kv_k_index(int kvs, int p, int d) {
-  return ((size_t)(d >> 3) * kvs + p) * 8 + (d & 7);
-}
-__host__ __device__ __forceinline__ size_t kv_v_index(int hd, int p, int d) {
-  return ((size_t)(p >> 3) * hd + d) * 8 + (p & 7);
-}
-
 // Position guard of the decode kernels that read their position from device memory: a
 // position outside the KV cache (pos >= kvs) makes the kernel touch no cache entry and write
 // no output; it sets this word to 1 instead.  The kernel-level entry points clear and read it
@@ -1709,8 +1780,9 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float* __restrict__ qkv, i
 // (-DCM_STAMPS, libcamelid_hip_stamps.so): thread 0 of head h's workgroup in layer l records
 // the 100 MHz real-time counter at each phase boundary into g_att_stamps[l][h][i]
 // (camelid_hip_phase_stamps reads them).  Phases: 0 start, 1 q/k/v built and K/V stored,
-// 2 scores and their maximum, 3 exponentials, 4 denominator, 5 output sums, 6 end.
-constexpr int ATT_NSTAMP = 7;
+// 2 scores and their maximum, 3 exponentials, 4 denominator, 5 output sums, 6 end; 7 the first
+// row wave's K-row loads issued, 8 its scores done (before the maximum's barrier).
+constexpr int ATT_NSTAMP = 9;
 constexpr int ATT_STAMP_LAYERS = 64, ATT_STAMP_HEADS = 64;
 #ifdef CM_STAMPS
 __device__ uint64_t g_att_stamps[ATT_STAMP_LAYERS * ATT_STAMP_HEADS * ATT_NSTAMP];
@@ -1729,12 +1801,13 @@ __device__ uint64_t g_split_stamps[2 * SPLIT_STAMP_WGS * SPLIT_NSTAMP];
 #define CM_SPLIT_STAMP(kind, wg, i)
 #endif
 #ifdef CM_STAMPS
-#define CM_ATT_STAMP(i)                                                                                 \
-  if (tid == 0 && layer < ATT_STAMP_LAYERS && h < ATT_STAMP_HEADS)                                      \
+#define CM_ATT_STAMP_T(i, t)                                                                            \
+  if (tid == (t) && layer < ATT_STAMP_LAYERS && h < ATT_STAMP_HEADS)                                    \
     g_att_stamps[((size_t)layer * ATT_STAMP_HEADS + h) * ATT_NSTAMP + (i)] = __builtin_amdgcn_s_memrealtime();
 #else
-#define CM_ATT_STAMP(i)
+#define CM_ATT_STAMP_T(i, t)
 #endif
+#define CM_ATT_STAMP(i) CM_ATT_STAMP_T(i, 0)
 
 // ---------------------------------------------------------------------------
 // Decode attention, faithful (inference.rs:23945-24025), one workgroup per query head.
@@ -1828,18 +1901,6 @@ __device__ __forceinline__ float att_onepass_sum(const float* v, int P, FsLds<NT
 #undef CM_AOP
 }
 
-// Workgroups are dealt to the 8 XCDs round-robin (workgroup b runs on XCD b % 8), and each
-// XCD has an L2 of its own.  The attention workgroups that read the same KV rows (the query
-// heads of one KV head; with `parts` workgroups per head, the same part of them) are mapped
-// to one XCD, so that the rows come from HBM once and from that L2 for the rest.  Workgroup b
-// of n_kv * parts * rep returns its (kv unit, member) as kv_unit * rep + member, where kv unit
-// u = kv_head * parts + part; the identity when the units do not divide over the XCDs.
-constexpr int N_XCD = 8;
-__device__ __forceinline__ int xcd_member(int b, int n_units, int rep) {
-  if (n_units % N_XCD != 0) return b;
-  const int x = b % N_XCD, i = b / N_XCD;
-  return (x + N_XCD * (i / rep)) * rep + i % rep;
-}
 
 template <int HD, bool FUSED>
 __global__ __launch_bounds__(att_nt(HD)) void k_attention(
@@ -1866,12 +1927,12 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   __shared__ __align__(16) float qs[HD];
   __shared__ __align__(16) float kn[HD];  // this position's k (f16-rounded)
   __shared__ __align__(16) float vn[HD];  // this position's v (f16-rounded)
-  __shared__ __align__(16) float out[HD];
   __shared__ __align__(16) float sq[2 * HD];
   __shared__ float red[ATT_NT / 64];
   __shared__ float s_qscale, s_kscale, s_inv;
   __shared__ uint64_t etab[32];  // the expf table, read from LDS by the exponentials
   __shared__ FsLds<ATT_NT> fs;
+  __shared__ uint32_t team_ctr, team_bad;  // the head team's LDS barrier
   const int tid = threadIdx.x;
   const int rep = n_heads / n_kv;
   const int h = xcd_member(blockIdx.x, n_kv, rep);
@@ -1901,15 +1962,46 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   }
   if (tid < 32) et = kExp2Tab[tid];
   // The output lanes also load now the (up to 7) V values of the positions past the last
-  // full 8-position granule, which their output chain adds from registers at the end.  (The
-  // K rows and V chunks wait for the score phase: a wave issuing hundreds of KB stalls until
-  // the CU's memory queue drains, and the RoPE barriers would wait for it.)
+  // full 8-position granule, which their output chain adds from registers at the end, and
+  // the RoPE table entries and QK-norm weights of this head.
   uint16_t vtail[7];
+  const int half = rope_dim >> 1;
+  float rc = 0.0f, rs = 0.0f, qnw = 0.0f, knw = 0.0f;
   if (tid < HD) {
     const int tail0 = (pos >> 3) << 3;  // first position past the full granules of [0, pos)
 #pragma unroll
     for (int u = 0; u < 7; ++u)
       vtail[u] = tail0 + u < pos ? vc[hbase + kv_v_index(HD, tail0 + u, tid)] : (uint16_t)0;
+    if (FUSED) {
+      if (tid < half) {
+        rc = cos_base[(size_t)pos * rope_stride + tid];
+        rs = sin_base[(size_t)pos * rope_stride + tid];
+      }
+      if (q_norm) {
+        qnw = q_norm[tid];
+        knw = k_norm[tid];
+      }
+    }
+  }
+  if (tid == 0) {
+    team_ctr = 0u;
+    team_bad = 0u;
+  }
+  // Waves 0..CW-1 (the head team) build q and this position's k and v; the other waves hold
+  // the cache rows of the first score pass (score lane lt = tid - HD, positions lt, lt + NT,
+  // ...; the team's lanes take lt = NT - HD + tid).  This barrier puts the team's loads at the
+  // head of the CU's memory queue; then the row waves issue their K rows, which stream while
+  // the team works (it synchronises through an LDS counter, so a row wave stalled issuing
+  // its loads holds up nobody) and are in registers when the score phase starts.
+  __syncthreads();
+  const int lt = tid >= HD ? tid - HD : tid + ATT_NT - HD;
+  uint4 row0[R8];
+  if (tid >= HD && lt < ncache) {
+#pragma unroll
+    for (int u = 0; u < R8; ++u) row0[u] = kg[(size_t)u * kvs + lt];
+    if (lt == 0) {
+      CM_ATT_STAMP_T(7, HD)
+    }
   }
   // V staging: the cache positions' V granules (full 8-position groups) are copied into an
   // LDS ring of ring_slots chunks by NH staging waves with direct global->LDS loads; the
@@ -1936,48 +2028,41 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   // to ATT_NT * ATT_ONEPASS_C, the segmented passes beyond (which use the ring first)
   const bool onepass = P >= ATT_FOLD_MAX && P <= ATT_NT * ATT_ONEPASS_C;
   const bool early = P > 1 && P <= ATT_NT * ATT_ONEPASS_C;
-  if (tid < 32) etab[tid] = et;
-  if (tid < HD) {
+  if (tid < HD) {  // (the head team: whole waves)
+    TeamBar tb{&team_ctr, &team_bad, (uint32_t)CW, 0u};
+    if (tid < 32) etab[tid] = et;
     qs[tid] = qv;
     kn[tid] = kv;
     vn[tid] = vv;
-  }
-
-  if (FUSED) {
-    if (q_norm) {  // per-head RMSNorm of q and k (two serial folds by two lanes)
-      __syncthreads();
-      if (tid < HD) {
+    if (FUSED) {
+      if (q_norm) {  // per-head RMSNorm of q and k (two serial folds by two lanes)
+        tb();
         sq[tid] = qs[tid] * qs[tid];
         sq[HD + tid] = kn[tid] * kn[tid];
+        tb();
+        constexpr int KT = HD >= 128 ? 64 : 32;  // the k fold's lane (another wave when there is one)
+        if (tid == 0 || tid == KT) {
+          const float r = 1.0f / sqrtf(fold_lds_lean(tid == 0 ? sq : sq + HD, HD) / (float)HD + eps);
+          if (tid == 0) s_qscale = r;
+          else s_kscale = r;
+        }
+        tb();
+        qs[tid] = (qs[tid] * s_qscale) * qnw;
+        kn[tid] = (kn[tid] * s_kscale) * knw;
       }
-      __syncthreads();
-      // (lean folds: the first score pass's K rows are in flight in registers)
-      if (tid == 0) s_qscale = 1.0f / sqrtf(fold_lds_lean(sq, HD) / (float)HD + eps);
-      if (tid == 64) s_kscale = 1.0f / sqrtf(fold_lds_lean(sq + HD, HD) / (float)HD + eps);
-      __syncthreads();
-      if (tid < HD) {
-        qs[tid] = (qs[tid] * s_qscale) * q_norm[tid];
-        kn[tid] = (kn[tid] * s_kscale) * k_norm[tid];
+      tb();
+      if (tid < half) {
+        const int d0 = split_half ? tid : 2 * tid;
+        const int d1 = split_half ? tid + half : 2 * tid + 1;
+        float x0 = qs[d0], x1 = qs[d1];
+        qs[d0] = (x0 * rc) - (x1 * rs);
+        qs[d1] = (x0 * rs) + (x1 * rc);
+        x0 = kn[d0];
+        x1 = kn[d1];
+        kn[d0] = (x0 * rc) - (x1 * rs);
+        kn[d1] = (x0 * rs) + (x1 * rc);
       }
-    }
-    __syncthreads();
-    const float* cosv = cos_base + (size_t)pos * rope_stride;
-    const float* sinv = sin_base + (size_t)pos * rope_stride;
-    const int half = rope_dim >> 1;
-    if (tid < half) {
-      const int d0 = split_half ? tid : 2 * tid;
-      const int d1 = split_half ? tid + half : 2 * tid + 1;
-      const float c = cosv[tid], s = sinv[tid];
-      float x0 = qs[d0], x1 = qs[d1];
-      qs[d0] = (x0 * c) - (x1 * s);
-      qs[d1] = (x0 * s) + (x1 * c);
-      x0 = kn[d0];
-      x1 = kn[d1];
-      kn[d0] = (x0 * c) - (x1 * s);
-      kn[d1] = (x0 * s) + (x1 * c);
-    }
-    __syncthreads();
-    if (tid < HD) {
+      tb();
       const uint16_t kb = f32_to_f16_bits(kn[tid]);
       const uint16_t vb = f32_to_f16_bits(vn[tid]);
       kn[tid] = half_bits_to_float(kb);
@@ -1991,26 +2076,79 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   __syncthreads();
   CM_ATT_STAMP(1)
 
+  float res = 0.0f;  // this output lane's value (tid < HD)
   if (P == 1) {
     // inference.rs:23564-23575: a single position copies the V row.
-    if (tid < HD) out[tid] = vn[tid];
+    if (tid < HD) res = vn[tid];
   } else {
     // ---- scores: cache positions 0..pos-1, one lane each
     float lmax = -INFINITY;
     auto score = [&](const uint4(&row)[R8], int p) {
       float acc = 0.0f;
+      // q is read from LDS 8 values at a time (fencing the schedule keeps the whole of q from
+      // being hoisted into registers next to the in-flight row): the next granule's q goes out
+      // after this granule's 8 products and before its 8 dependent adds, so the read latency
+      // overlaps the adds, and no add waits on its product
+      const float4* q4 = reinterpret_cast<const float4*>(qs);
+      float4 qa = q4[0], qb = q4[1];
 #pragma unroll
       for (int u = 0; u < R8; ++u) {
-        // q is read from LDS 8 values at a time (fencing the schedule keeps the whole of
-        // q from being hoisted into registers next to the in-flight row); the 8 products
-        // are formed before the 8 dependent adds, so no add waits on its product
         __builtin_amdgcn_sched_barrier(0);
-        const float4 qa = reinterpret_cast<const float4*>(qs)[2 * u];
-        const float4 qb = reinterpret_cast<const float4*>(qs)[2 * u + 1];
         const float p0 = mul_f16_lo(qa.x, row[u].x), p1 = mul_f16_hi(qa.y, row[u].x);
         const float p2 = mul_f16_lo(qa.z, row[u].y), p3 = mul_f16_hi(qa.w, row[u].y);
         const float p4 = mul_f16_lo(qb.x, row[u].z), p5 = mul_f16_hi(qb.y, row[u].z);
         const float p6 = mul_f16_lo(qb.z, row[u].w), p7 = mul_f16_hi(qb.w, row[u].w);
+        __builtin_amdgcn_sched_barrier(0);
+        if (u + 1 < R8) {
+          qa = q4[2 * u + 2];
+          qb = q4[2 * u + 3];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        acc += p0;
+        acc += p1;
+        acc += p2;
+        acc += p3;
+        acc += p4;
+        acc += p5;
+        acc += p6;
+        acc += p7;
+        asm volatile("" : "+v"(acc));  // this granule's adds stay ahead of the next reads
+      }
+      const float sv = acc * scale;
+      sc[p] = sv;
+      lmax = fmaxf(lmax, sv);
+    };
+    if (lt < ncache) {
+      if (tid >= HD) {
+        score(row0, lt);
+      } else {  // (the team's lanes: positions NT - HD + tid, reached from NT - HD + 1 positions)
+        uint4 row[R8];
+#pragma unroll
+        for (int u = 0; u < R8; ++u) row[u] = kg[(size_t)u * kvs + lt];
+        score(row, lt);
+      }
+    }
+    if (lt == 0) {
+      CM_ATT_STAMP_T(8, HD)
+    }
+    for (int p = lt + ATT_NT; p < ncache; p += ATT_NT) {
+      uint4 row[R8];
+#pragma unroll
+      for (int u = 0; u < R8; ++u) row[u] = kg[(size_t)u * kvs + p];
+      score(row, p);
+    }
+    // this token's own key (from LDS) by the team's last lane, which has no cache row below
+    // NT positions (its chain then runs beside the row waves' instead of after one of them);
+    // 8 products ahead of their 8 dependent adds
+    if (tid == HD - 1) {
+      float acc = 0.0f;
+      const float4* q4 = reinterpret_cast<const float4*>(qs);
+      const float4* k4 = reinterpret_cast<const float4*>(kn);
+#pragma unroll
+      for (int u = 0; u < HD / 8; ++u) {
+        const float4 qa = q4[2 * u], qb = q4[2 * u + 1], ka = k4[2 * u], kb = k4[2 * u + 1];
+        const float p0 = qa.x * ka.x, p1 = qa.y * ka.y, p2 = qa.z * ka.z, p3 = qa.w * ka.w;
+        const float p4 = qb.x * kb.x, p5 = qb.y * kb.y, p6 = qb.z * kb.z, p7 = qb.w * kb.w;
         acc += p0;
         acc += p1;
         acc += p2;
@@ -2020,20 +2158,6 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
         acc += p6;
         acc += p7;
       }
-      const float sv = acc * scale;
-      sc[p] = sv;
-      lmax = fmaxf(lmax, sv);
-    };
-    for (int p = tid; p < ncache; p += ATT_NT) {
-      uint4 row[R8];
-#pragma unroll
-      for (int u = 0; u < R8; ++u) row[u] = kg[(size_t)u * kvs + p];
-      score(row, p);
-    }
-    if (tid == (pos & (ATT_NT - 1))) {  // this token's own key, from LDS
-      float acc = 0.0f;
-#pragma unroll
-      for (int d = 0; d < HD; ++d) acc += qs[d] * kn[d];
       const float sv = acc * scale;
       sc[pos] = sv;
       lmax = fmaxf(lmax, sv);
@@ -2140,20 +2264,24 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
       }
     }
     CM_ATT_STAMP(5)
-    __syncthreads();  // the normalised probabilities past the ring (and with no chunks at all)
+    // the normalised probabilities past the ring were published by the ring loop's first
+    // barrier; with no chunks at all, by this one (uniform)
+    if (nchunks == 0) __syncthreads();
     if (tid < HD) {
 #pragma unroll
       for (int u = 0; u < 7; ++u)
         if (ng * 8 + u < ncache) acc += sc[ng * 8 + u] * half_bits_to_float(vtail[u]);
       acc += sc[pos] * vn[tid];
-      out[tid] = acc;
+      res = acc;
     }
   }
-  __syncthreads();
+  // (each output lane stores and quantizes its own value: no barrier; the Q8_0 block's
+  // scale is formed by lane shuffles within the 32-lane group)
   if (tid < HD) {
-    att_out[(size_t)h * HD + tid] = out[tid];
+    if (team_bad) res = __builtin_nanf("");  // (the team barrier's bound was reached: no result)
+    att_out[(size_t)h * HD + tid] = res;
     int8_t q;
-    const float dd = quantize_lane32(out[tid], &q);
+    const float dd = quantize_lane32(res, &q);
     xq[(size_t)h * HD + tid] = q;
     if ((tid & 31) == 0) xs[((size_t)h * HD + tid) >> 5] = dd;
   }
