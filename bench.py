@@ -224,7 +224,7 @@ def attention_phases(cfg) -> dict:
     and the launch span (first start to last end), in microseconds."""
     import ctypes as C
     from camelid_amd import _native as N
-    na, ng, nsp = 64 * 64 * 9, 2 * 256 * 8, 2 * 1024 * 8
+    na, ng, nsp = 64 * 64 * 9, 2 * 256 * 13, 2 * 1024 * 8
     buf = (C.c_uint64 * (na + ng + nsp))()
     got = C.c_size_t(0)
     N.check(N.lib().camelid_hip_phase_stamps(buf, na + ng + nsp, C.byref(got)))
@@ -241,7 +241,7 @@ def attention_phases(cfg) -> dict:
     res["launch_span"] = round(float((st[:, :, 6].max(1) - st[:, :, 0].min(1)).mean() * 0.01), 3)
     log("attention phases (us, mean over layers and heads): " + ", ".join(f"{k} {v}" for k, v in res.items()))
     # the norm-fused GEMVs of the last layer (mean over the workgroups that recorded)
-    gs = allst[na:na + ng].reshape(2, 256, 8)
+    gs = allst[na:na + ng].reshape(2, 256, 13)
     for kind, name in enumerate(("qkv_norm_gemv", "gate_up_norm_gemv")):
         g = gs[kind]
         g = g[g[:, 0] > 0]
@@ -250,6 +250,11 @@ def attention_phases(cfg) -> dict:
         t0 = g[:, 0]
         ph = {"norm_inputs_arrived": float((g[:, 6] - t0).mean() * 0.01),
               "sum_of_squares_done": float((g[:, 7] - t0).mean() * 0.01),
+              "sum_f64_scan": float((g[:, 8] - t0).mean() * 0.01) if (g[:, 8] > 0).all() else None,
+              "sum_seg_scan": float((g[:, 9] - t0).mean() * 0.01) if (g[:, 9] > 0).all() else None,
+              "sum_specials": float((g[:, 10] - t0).mean() * 0.01) if (g[:, 10] > 0).all() else None,
+              "sum_replay": float((g[:, 11] - t0).mean() * 0.01) if (g[:, 11] > 0).all() else None,
+              "special_steps_mean": float(g[:, 12].mean()), "special_steps_max": float(g[:, 12].max()),
               "norm_done": float((g[:, 1] - t0).mean() * 0.01),
               "weight_loads_issued": float((g[:, 2] - t0).mean() * 0.01),
               "past_norm_barrier": float((g[:, 3] - t0).mean() * 0.01),
@@ -258,8 +263,9 @@ def attention_phases(cfg) -> dict:
               "start_spread": float((t0.max() - t0.min()) * 0.01),
               "launch_span": float((g[:, 5].max() - t0.min()) * 0.01),
               "workgroups": int(len(g))}
-        res[name] = {k: round(v, 3) for k, v in ph.items()}
-        log(f"{name} phases (us from each workgroup's start): " + ", ".join(f"{k} {v:.3f}" for k, v in ph.items()))
+        res[name] = {k: (round(v, 3) if v is not None else None) for k, v in ph.items()}
+        log(f"{name} phases (us from each workgroup's start): " +
+            ", ".join(f"{k} {v:.3f}" for k, v in ph.items() if v is not None))
     # the split attention (when it ran in the last layer)
     sp = allst[na + ng:].reshape(2, 1024, 8)
     for kind, name, labels in ((0, "att_scores_split", ("q_built", "scores_done", "end")),

@@ -110,8 +110,10 @@ struct camelid_hip_engine {
   uint32_t kvs = 0;        // KV position stride: max_pos rounded up to a multiple of 8
   int att_slots = 0;       // V ring chunks of the attention kernel
   // long contexts: the split attention (k_att_scores + k_att_out) from att_split_min positions
-  // on (CAMELID_HIP_ATT_SPLIT; 0 = never); its scores [n_heads][kvs] and slice maxima
-  uint32_t att_split_min = 2048;
+  // on (CAMELID_HIP_ATT_SPLIT; 0 = never); its scores [n_heads][kvs] and slice maxima.
+  // Measured on MI355X: at ~550 positions the single-workgroup kernel is faster (C3 657 vs
+  // 638 tok/s with the split everywhere); from ~1024 on the split is (C5 299.5 vs 293.4 tok/s)
+  uint32_t att_split_min = 1024;
   float* att_sc = nullptr;
   float* att_mx = nullptr;
   int att_mode = -1;       // -1: by position; 0 / 1: single / split (graph capture)

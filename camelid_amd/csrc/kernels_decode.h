@@ -407,13 +407,26 @@ __device__ __forceinline__ float inorder_sum_nonneg(const float* v, uint32_t* ps
 // (the same n terms, in LDS): the result never depends on the prediction being right.
 // Every thread of the workgroup must call; NT * C >= n; fs: the caller's LDS workspace (one
 // per kernel, shared by every chunk size the kernel instantiates).
+// Phase timestamps of the two norm-fused GEMVs (measurement build only, as g_att_stamps):
+// kind 0 k_gemv_norm, 1 k_gemv_gu_silu; per workgroup (< 256; the last launch overwrites):
+// 0 start (thread 0), 1 norm done (thread 0), 2 a weight wave's loads issued (thread 256),
+// 3 past the workgroup barrier after the norm, 4 block dots done, 5 end.
+constexpr int GEMV_NSTAMP = 13, GEMV_STAMP_WGS = 256;
+#ifdef CM_STAMPS
+__device__ uint64_t g_gemv_stamps[2 * GEMV_STAMP_WGS * GEMV_NSTAMP];
+#define CM_GEMV_STAMP(kind, i, t)                                                                        \
+  if (threadIdx.x == (t) && blockIdx.x < GEMV_STAMP_WGS)                                                 \
+    g_gemv_stamps[((kind) * GEMV_STAMP_WGS + blockIdx.x) * GEMV_NSTAMP + (i)] = __builtin_amdgcn_s_memrealtime();
+#else
+#define CM_GEMV_STAMP(kind, i, t)
+#endif
+
 constexpr int FS_CAP = 128;  // special steps the replay takes before falling back
 template <int NT>
 struct FsLds {
+  uint4 ent[FS_CAP];                   // the special steps: (run before it, its check lo, lim, term bits)
   double r[NT / 64];                   // wave totals of the f64 prefix
   uint32_t rs[NT / 64], b[NT / 64], c[NT / 64];  // wave totals of the segmented scan
-  float et[FS_CAP];                    // the special steps: term,
-  uint32_t ev[FS_CAP], lo[FS_CAP], lim[FS_CAP];  // run before it and its check
   uint32_t end[3];                     // the final run and its check
   float sum;
 };
@@ -497,13 +510,14 @@ struct TeamBar {
 
 template <int NT, int C, typename Bar = WgBar>
 __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const float* v, int n, FsLds<NT>& fs,
-                                                     Bar&& bar = Bar{}) {
+                                                     Bar&& bar = Bar{}, int stamp_kind = -1) {
+  (void)stamp_kind;  // (the measurement build: stamps 8..11 of the norm-fused GEMVs after each barrier)
   constexpr int NW = NT / 64;
   static_assert(NT % 64 == 0 && NW <= 16 && C <= 32, "one 16-lane row holds the wave totals");
   double* sh_r = fs.r;
   uint32_t *sh_rs = fs.rs, *sh_b = fs.b, *sh_c = fs.c;
-  float* sh_et = fs.et;
-  uint32_t *sh_ev = fs.ev, *sh_lo = fs.lo, *sh_lim = fs.lim, *sh_end = fs.end;
+  uint4* sh_ent = fs.ent;
+  uint32_t* sh_end = fs.end;
   float& sh_sum = fs.sum;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave: a scalar lane index
@@ -523,6 +537,9 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
   if (lane == 63) sh_r[wave] = incl;
   double R = dpp_f64<0x138, 0xf>(incl);  // wave_shr:1 -> exclusive
   bar();
+  if (stamp_kind >= 0) {
+    CM_GEMV_STAMP(stamp_kind, 8, 0)
+  }
   if (NW > 1) {
     double wt = lane < NW ? sh_r[lane] : 0.0;
     wt += dpp_f64<0x111, 0xf>(wt);
@@ -573,6 +590,9 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
   uint32_t run = CM_DPP(b, 0x138, 0xf), pos = CM_DPP(cnt, 0x138, 0xf);
   const uint32_t rs_x = CM_DPP(rs, 0x138, 0xf);
   bar();
+  if (stamp_kind >= 0) {
+    CM_GEMV_STAMP(stamp_kind, 9, 0)
+  }
   uint32_t total;
   {
     const uint32_t wr = lane < NW ? sh_rs[lane] : 0u, wbv = lane < NW ? sh_b[lane] : 0u,
@@ -597,10 +617,7 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
       if (pos < (uint32_t)FS_CAP) {
         uint32_t lo, lim;
         fs_entry(run, eb_of[c], lo, lim);
-        sh_et[pos] = t[c];
-        sh_ev[pos] = run;
-        sh_lo[pos] = lo;
-        sh_lim[pos] = lim;
+        sh_ent[pos] = make_uint4(run, lo, lim, __float_as_uint(t[c]));
       }
       ++pos;
       run = 0u;
@@ -616,23 +633,42 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
     sh_end[2] = lim;
   }
   bar();
-  if (wave == 0) {  // replay, branch-free per step: the sum's chain is one integer and one f32 add
+  if (stamp_kind >= 0) {
+    CM_GEMV_STAMP(stamp_kind, 10, 0)
+  }
+  if (wave == 0) {
+    // replay, branch-free per step: the sum's chain is one integer and one f32 add.  Every lane
+    // of wave 0 runs the same chain on the same entries (broadcast LDS reads, 8 entries read
+    // ahead of the chain)
     const int tot = __builtin_amdgcn_readfirstlane((int)total);
+#ifdef CM_STAMPS
+    if (stamp_kind >= 0 && threadIdx.x == 0 && blockIdx.x < GEMV_STAMP_WGS)  // (a count, not a time)
+      g_gemv_stamps[(stamp_kind * GEMV_STAMP_WGS + blockIdx.x) * GEMV_NSTAMP + 12] = (uint64_t)tot;
+#endif
     float s = 0.0f;
     uint32_t bad = tot > FS_CAP;
-    for (int base = 0; !bad && base < tot; base += 64) {
-      const int e = min(base + lane, tot - 1);
-      const float et = sh_et[e];
-      const uint32_t ev = sh_ev[e], elo = sh_lo[e], elim = sh_lim[e];
-      const int m = min(64, tot - base);
-      for (int j = 0; j < m; ++j) {
-        const uint32_t V = (uint32_t)__builtin_amdgcn_readlane((int)ev, j);
-        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)elo, j);
-        const uint32_t lim = (uint32_t)__builtin_amdgcn_readlane((int)elim, j);
-        const float tj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(et), j));
+    if (!bad && tot > 0) {
+      auto step = [&](const uint4& q) {
         const uint32_t sb = __float_as_uint(s);
-        bad |= (uint32_t)!(sb - lo < lim);
-        s = __uint_as_float(sb + V) + tj;
+        bad |= (uint32_t)!(sb - q.y < q.z);
+        s = __uint_as_float(sb + q.x) + __uint_as_float(q.w);
+      };
+      const int nb8 = (tot + 7) >> 3;
+      uint4 x[8], y[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = sh_ent[u];
+      for (int k = 0; k < nb8; ++k) {
+        if (k + 1 < nb8) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u) y[u] = sh_ent[min(8 * (k + 1) + u, FS_CAP - 1)];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const int m = min(8, tot - 8 * k);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (u < m) step(x[u]);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = y[u];
       }
     }
     {
@@ -644,6 +680,9 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
     if (lane == 0) sh_sum = s;
   }
   bar();
+  if (stamp_kind >= 0) {
+    CM_GEMV_STAMP(stamp_kind, 11, 0)
+  }
   return sh_sum;
 }
 #undef CM_FS_STEP
@@ -691,13 +730,30 @@ __device__ __forceinline__ float fold_lds_strided(const float* p, int stride) {
 // Lane-pair exchange (xor 1) through DPP quad_perm [1,0,3,2]; all lanes must be active.
 __device__ __forceinline__ int dpp_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
 
+// Maximum over each aligned 32-lane half of the wave, in every lane of the half (fmaxf: order
+// independent): quad and row exchanges by DPP (lane i then holds quads i, i - 4, i - 8, i - 12
+// of its row), then the half's two rows from lanes 0/16 or 32/48.  Whole halves must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float max_half_wave(float a) {
+  a = fmaxf(a, dpp_f32<0xB1>(a));   // quad_perm [1,0,3,2]
+  a = fmaxf(a, dpp_f32<0x4E>(a));   // quad_perm [2,3,0,1]
+  a = fmaxf(a, dpp_f32<0x124>(a));  // row_ror:4
+  a = fmaxf(a, dpp_f32<0x128>(a));  // row_ror:8
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 48));
+  return (threadIdx.x & 32) ? fmaxf(r2, r3) : fmaxf(r0, r1);
+}
+
 // Q8_0 quantization of one 32-value block held one value per lane by a 32-lane group
 // (lanes 0-31 or 32-63 of a wave).  Returns the block's f16-valued scale (same in every
 // lane); *q receives this lane's quant.  inference.rs:16953-16971.
 __device__ __forceinline__ float quantize_lane32(float v, int8_t* q) {
-  float amax = fabsf(v);
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  const float amax = max_half_wave(fabsf(v));
   const float unrounded = amax / 127.0f;
   const float scale = f16_bits_to_f32(f32_to_f16_bits(unrounded));
   const float inv = unrounded == 0.0f ? 0.0f : 1.0f / unrounded;
@@ -778,6 +834,60 @@ __device__ __forceinline__ void amax_pick(float& a, int& i, float& v, float oa, 
   }
 }
 
+// The (|max|, first index) reduction across lanes by DPP exchanges (one VALU move per value,
+// where a __shfl_xor is an LDS permute round trip).  amax_pick is a total order on (a, -i) for
+// the non-NaN a the quantizers produce (a starts at 0 and only grows through '>'), so every
+// reduction tree gives the same pick.
+template <int CTRL>
+__device__ __forceinline__ void amax_dpp(float& a, int& i, float& v, float& oa, int& oi, float& ov) {
+  oa = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), CTRL, 0xf, 0xf, false));
+  oi = __builtin_amdgcn_update_dpp(0, i, CTRL, 0xf, 0xf, false);
+  ov = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ void amax_pick_dpp(float& a, int& i, float& v) {
+  float oa, ov;
+  int oi;
+  amax_dpp<CTRL>(a, i, v, oa, oi, ov);
+  amax_pick(a, i, v, oa, oi, ov);
+}
+// every lane of each aligned quad: the quad's pick (xor-1, then xor-2 partners)
+__device__ __forceinline__ void amax_pick_quad(float& a, int& i, float& v) {
+  amax_pick_dpp<0xB1>(a, i, v);  // quad_perm [1,0,3,2]
+  amax_pick_dpp<0x4E>(a, i, v);  // quad_perm [2,3,0,1]
+}
+// every lane of each aligned group of 8: the quads, then the other quad of the group (lane
+// i ^ 4: row_ror:4 reads lane i - 4, row_ror:12 lane i + 4, within the row of 16)
+__device__ __forceinline__ void amax_pick_group8(float& a, int& i, float& v) {
+  amax_pick_quad(a, i, v);
+  float oa4, ov4, oa12, ov12;
+  int oi4, oi12;
+  amax_dpp<0x124>(a, i, v, oa4, oi4, ov4);
+  amax_dpp<0x12C>(a, i, v, oa12, oi12, ov12);
+  const bool upper = (threadIdx.x & 4) != 0;
+  amax_pick(a, i, v, upper ? oa4 : oa12, upper ? oi4 : oi12, upper ? ov4 : ov12);
+}
+// every lane of the wave: the quads, the row's four quads by rotations (lane i then holds
+// quads i, i - 4, i - 8, i - 12 of its row), then the four rows' picks from lanes 0, 16, 32, 48
+__device__ __forceinline__ void amax_pick_wave(float& a, int& i, float& v) {
+  amax_pick_quad(a, i, v);
+  amax_pick_dpp<0x124>(a, i, v);  // row_ror:4
+  amax_pick_dpp<0x128>(a, i, v);  // row_ror:8
+  float ra[4], rv[4];
+  int ri[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    ra[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 16 * r));
+    ri[r] = __builtin_amdgcn_readlane(i, 16 * r);
+    rv[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16 * r));
+  }
+  a = ra[0];
+  i = ri[0];
+  v = rv[0];
+#pragma unroll
+  for (int r = 1; r < 4; ++r) amax_pick(a, i, v, ra[r], ri[r], rv[r]);
+}
+
 // Q8_K block held as eight 32-value pieces by eight consecutive lanes (piece j = values
 // 32j..32j+31 of the block, in lane j of the group): each lane writes its 32 quants and their
 // sum; the group's first lane writes the block scale.
@@ -793,8 +903,7 @@ __device__ __forceinline__ void quantize_q8k_lanes8(const float (&y)[32], int8_t
       v = y[e];
       idx = 32 * j + e;
     }
-#pragma unroll
-  for (int o = 1; o < 8; o <<= 1) amax_pick(a, idx, v, __shfl_xor(a, o), __shfl_xor(idx, o), __shfl_xor(v, o));
+  amax_pick_group8(a, idx, v);
   const float iscale = a > 0.0f ? -127.0f / v : 0.0f;
   int sum = 0;
 #pragma unroll
@@ -822,8 +931,7 @@ __device__ __forceinline__ void quantize_q8k_wg256(float x, int8_t* __restrict__
   float a = fabsf(x), v = x;
   int idx = tid;
   if (!(a > 0.0f)) a = 0.0f;  // zeros and NaN never win against the scan's initial 0
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) amax_pick(a, idx, v, __shfl_xor(a, o), __shfl_xor(idx, o), __shfl_xor(v, o));
+  amax_pick_wave(a, idx, v);
   if ((tid & 63) == 0) {
     s_a[tid >> 6] = a;
     s_i[tid >> 6] = idx;
@@ -1026,19 +1134,6 @@ constexpr int GN_NT = 1024;
 constexpr int GN_TEAM = 256;      // threads of the gate/up kernel's norm team
 constexpr int GN_TEAM_QKV = 512;  // threads of the qkv kernel's norm team (its weight waves hold every row)
 
-// Phase timestamps of the two norm-fused GEMVs (measurement build only, as g_att_stamps):
-// kind 0 k_gemv_norm, 1 k_gemv_gu_silu; per workgroup (< 256; the last launch overwrites):
-// 0 start (thread 0), 1 norm done (thread 0), 2 a weight wave's loads issued (thread 256),
-// 3 past the workgroup barrier after the norm, 4 block dots done, 5 end.
-constexpr int GEMV_NSTAMP = 8, GEMV_STAMP_WGS = 256;
-#ifdef CM_STAMPS
-__device__ uint64_t g_gemv_stamps[2 * GEMV_STAMP_WGS * GEMV_NSTAMP];
-#define CM_GEMV_STAMP(kind, i, t)                                                                        \
-  if (threadIdx.x == (t) && blockIdx.x < GEMV_STAMP_WGS)                                                 \
-    g_gemv_stamps[((kind) * GEMV_STAMP_WGS + blockIdx.x) * GEMV_NSTAMP + (i)] = __builtin_amdgcn_s_memrealtime();
-#else
-#define CM_GEMV_STAMP(kind, i, t)
-#endif
 
 // The norm team's share of x and w: thread t holds the C consecutive values t*C.. (the layout
 // of inorder_sum_onepass).
@@ -1079,7 +1174,7 @@ __device__ __forceinline__ void norm_scale(const float (&xv)[C], const float (&w
   if (stamp_kind >= 0) {
     CM_GEMV_STAMP(stamp_kind, 6, 0)  // (the measurement build: x and w have arrived)
   }
-  const float ss = inorder_sum_onepass<NT, C>(t, yl, n, fs, bar);
+  const float ss = inorder_sum_onepass<NT, C>(t, yl, n, fs, bar, stamp_kind);
   if (tid == 0) *s_scale = 1.0f / sqrtf(ss / (float)n + eps);
   if (stamp_kind >= 0) {
     CM_GEMV_STAMP(stamp_kind, 7, 0)  // the sum of squares is known

@@ -23,13 +23,23 @@ __global__ __launch_bounds__(256) void k_quantize_q8k(const float* __restrict__ 
   quantize_q8k_wg256(x[s * 256 + threadIdx.x], yq + s * 256, ybs + s * 8, yd + s);
 }
 
-// Integer sum over lane groups of 2^m consecutive lanes (xor butterflies; exact).
-template <int W>
-__device__ __forceinline__ int group_sum(int v) {
-#pragma unroll
-  for (int o = 1; o < W; o <<= 1) v += __shfl_xor(v, o);
+// Integer sums over lane groups (exact in any order), by DPP lane exchanges inside each row
+// of 16 lanes: one VALU add per step, where a __shfl_xor is an LDS permute round trip.
+//   quad_sum: every lane of each aligned quad gets the quad's sum (xor-1 then xor-2 partners).
+//   group8_sum_lead: lane 8g (the first of each aligned group of 8) gets the group's sum: the
+//   quad sums, then lane 8g adds lane 8g + 4's (row_ror:12: lane i reads lane i - 12 mod 16 of
+//   its row); the other lanes hold partials.
+#define CM_DPP_ADD(v, ctrl) ((v) + __builtin_amdgcn_update_dpp(0, (v), (ctrl), 0xf, 0xf, false))
+__device__ __forceinline__ int quad_sum(int v) {
+  v = CM_DPP_ADD(v, 0xB1);  // quad_perm [1,0,3,2]
+  v = CM_DPP_ADD(v, 0x4E);  // quad_perm [2,3,0,1]
   return v;
 }
+__device__ __forceinline__ int group8_sum_lead(int v) {
+  v = quad_sum(v);
+  return CM_DPP_ADD(v, 0x12C);  // row_ror:12
+}
+#undef CM_DPP_ADD
 
 // Q8_K quantization of one 256-value block by one wave (lane l holds values 4l..4l+3) into
 // LDS: quants, per-32 sums and the scale (inference.rs:17564-17599, as quantize_q8k_wg256).
@@ -46,8 +56,7 @@ __device__ __forceinline__ void quantize_q8k_wave(const float* __restrict__ x, i
       v = vals[e];
       idx = 4 * lane + e;
     }
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) amax_pick(a, idx, v, __shfl_xor(a, o), __shfl_xor(idx, o), __shfl_xor(v, o));
+  amax_pick_wave(a, idx, v);
   const float iscale = a > 0.0f ? -127.0f / v : 0.0f;
   uint32_t word = 0;
   int sum = 0;
@@ -58,7 +67,7 @@ __device__ __forceinline__ void quantize_q8k_wave(const float* __restrict__ x, i
     word |= ((uint32_t)qv & 0xffu) << (8 * e);
   }
   reinterpret_cast<uint32_t*>(q)[lane] = word;
-  sum = group_sum<8>(sum);
+  sum = group8_sum_lead(sum);
   if ((lane & 7) == 0) bs[lane >> 3] = sum;
   if (lane == 0) *d = a > 0.0f ? 1.0f / iscale : 0.0f;
 }
@@ -155,8 +164,8 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
       hi = __builtin_amdgcn_sdot4((int)((w.y >> 4) & K2), qb.y, hi, false);
       hi = __builtin_amdgcn_sdot4((int)((w.z >> 4) & K2), qb.z, hi, false);
       hi = __builtin_amdgcn_sdot4((int)((w.w >> 4) & K2), qb.w, hi, false);
-      const int sumi = group_sum<8>(lo * sc_lo + hi * sc_hi);
-      const int prod = group_sum<8>(xbs[s * 8 + j] * mn);
+      const int sumi = group8_sum_lead(lo * sc_lo + hi * sc_hi);
+      const int prod = group8_sum_lead(xbs[s * 8 + j] * mn);
       if (valid && j == 0) {
         const float ydv = xd[s];
         const float dw = half_bits_to_float((uint16_t)(hd.x & 0xffffu));
@@ -292,7 +301,7 @@ __device__ __forceinline__ void gemv_q6k_body(const int bid, const uint8_t* __re
         }
       }
 #pragma unroll
-      for (int l = 0; l < 8; ++l) aux[l] = group_sum<4>(aux[l]);
+      for (int l = 0; l < 8; ++l) aux[l] = quad_sum(aux[l]);
       if (valid && (uu & 3) == 0) {
         const float d = half_bits_to_float(dw[(size_t)row * NSB + s]) * xd[s];
         float* tp = terms + ((size_t)rl * NSB + s) * 8;
@@ -694,7 +703,7 @@ __global__ __launch_bounds__(KQ_NT) void k_gemv_q6k_multi(const uint8_t* __restr
           }
         }
 #pragma unroll
-        for (int l = 0; l < 8; ++l) aux[l] = group_sum<4>(aux[l]);
+        for (int l = 0; l < 8; ++l) aux[l] = quad_sum(aux[l]);
         if (valid && (uu & 3) == 0) {
           const float d = dsb * xd[t * NSB + s];
           float* tp = terms + (((size_t)rl * T + t) * NSB + s) * 8;
@@ -940,8 +949,8 @@ __global__ __launch_bounds__(KQ_NT) void k_gemv_q4k_multi(const uint8_t* __restr
       hi = __builtin_amdgcn_sdot4(wh[1], qb.y, hi, false);
       hi = __builtin_amdgcn_sdot4(wh[2], qb.z, hi, false);
       hi = __builtin_amdgcn_sdot4(wh[3], qb.w, hi, false);
-      const int sumi = group_sum<8>(lo * sc_lo + hi * sc_hi);
-      const int prod = group_sum<8>(xbs[t * NC + s * 8 + j] * mn);
+      const int sumi = group8_sum_lead(lo * sc_lo + hi * sc_hi);
+      const int prod = group8_sum_lead(xbs[t * NC + s * 8 + j] * mn);
       if (valid && j == 0) {
         const float ydv = xd[t * NSB + s];
         terms[((size_t)wave * T + t) * NSB + s] = make_float4(-(ydv * dmw), (float)prod, ydv * dw, (float)sumi);
