@@ -748,6 +748,28 @@ __device__ __forceinline__ float max_half_wave(float a) {
   const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 48));
   return (threadIdx.x & 32) ? fmaxf(r2, r3) : fmaxf(r0, r1);
 }
+// maximum over the whole wave, in every lane (as max_half_wave; the whole wave active)
+__device__ __forceinline__ float max_wave(float a) {
+  a = fmaxf(a, dpp_f32<0xB1>(a));
+  a = fmaxf(a, dpp_f32<0x4E>(a));
+  a = fmaxf(a, dpp_f32<0x124>(a));
+  a = fmaxf(a, dpp_f32<0x128>(a));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+// integer sum over each aligned 32-lane half, in every lane of the half (exact)
+__device__ __forceinline__ int sum_half_wave(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false);
+  const int lo = __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16);
+  const int hi = __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
+  return (threadIdx.x & 32) ? hi : lo;
+}
 
 // Q8_0 quantization of one 32-value block held one value per lane by a 32-lane group
 // (lanes 0-31 or 32-63 of a wave).  Returns the block's f16-valued scale (same in every
@@ -946,16 +968,13 @@ __device__ __forceinline__ void quantize_q8k_wg256(float x, int8_t* __restrict__
   const int q = a > 0.0f ? min(nearest_int_ref(iscale * x), 127) : 0;
   const int8_t q8 = (int8_t)q;
   yq[tid] = q8;
-  int bs = q8;
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) bs += __shfl_xor(bs, o);
+  const int bs = sum_half_wave(q8);
   if ((tid & 31) == 0) ybs[tid >> 5] = bs;
   if (tid == 0) *yd = a > 0.0f ? 1.0f / iscale : 0.0f;
 }
 
 __device__ __forceinline__ float block_max(float v, float* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  v = max_wave(v);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
   __syncthreads();
   if (lane == 0) red[wave] = v;
@@ -1529,6 +1548,30 @@ __device__ __forceinline__ void argmax_pair(float& bv, uint32_t& bi, float ov, u
     bi = oi;
   }
 }
+// argmax_pair over the whole wave, in every lane: a total order on (value, -index) for the
+// non-NaN values it admits (NaN never replaces the running pair), so any reduction tree gives
+// the first index of the maximum; DPP quad and row exchanges, then the four rows' pairs
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp(float& bv, uint32_t& bi) {
+  argmax_pair(bv, bi, dpp_f32<CTRL>(bv), (uint32_t)__builtin_amdgcn_update_dpp(0, (int)bi, CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ void argmax_wave(float& bv, uint32_t& bi) {
+  argmax_dpp<0xB1>(bv, bi);
+  argmax_dpp<0x4E>(bv, bi);
+  argmax_dpp<0x124>(bv, bi);
+  argmax_dpp<0x128>(bv, bi);
+  float rv[4];
+  uint32_t ri[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    rv[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), 16 * r));
+    ri[r] = (uint32_t)__builtin_amdgcn_readlane((int)bi, 16 * r);
+  }
+  bv = rv[0];
+  bi = ri[0];
+#pragma unroll
+  for (int r = 1; r < 4; ++r) argmax_pair(bv, bi, rv[r], ri[r]);
+}
 
 // lm_head: the GEMV writes the logits and, per workgroup, its (value, index) argmax
 // partial; k_argmax_finish (one workgroup, the next launch) reduces the partials, writes
@@ -1557,8 +1600,7 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv_argmax(const int8_t* __restric
       logits[row0 + tid] = acc;
       argmax_pair(bv, bi, acc, (uint32_t)(row0 + tid));
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) argmax_pair(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
+    argmax_wave(bv, bi);
     if (tid == 0) {
       part_v[blockIdx.x] = bv;
       part_i[blockIdx.x] = bi;
@@ -1586,8 +1628,7 @@ __global__ __launch_bounds__(1024) void k_argmax_finish(const float* __restrict_
 #pragma unroll
     for (int u = 0; u < 8; ++u) argmax_pair(bv, bi, v[u], ix[u]);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) argmax_pair(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
+  argmax_wave(bv, bi);
   if ((tid & 63) == 0) {
     rv[tid >> 6] = bv;
     ri[tid >> 6] = bi;

@@ -191,8 +191,7 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
     if (part_v) {  // lm_head: this workgroup's argmax partial (first index of the max)
       float bv = live ? acc : -INFINITY;
       uint32_t bi = live ? (uint32_t)row : 0xffffffffu;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) argmax_pair(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
+      argmax_wave(bv, bi);
       if (tid == 0) {
         part_v[bid] = bv;
         part_i[bid] = bi;
@@ -330,8 +329,7 @@ __device__ __forceinline__ void gemv_q6k_body(const int bid, const uint8_t* __re
     if (part_v) {  // lm_head: this workgroup's argmax partial (first index of the max)
       float bv = live ? acc : -INFINITY;
       uint32_t bi = live ? (uint32_t)row : 0xffffffffu;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) argmax_pair(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
+      argmax_wave(bv, bi);
       if (tid == 0) {
         part_v[bid] = bv;
         part_i[bid] = bi;
