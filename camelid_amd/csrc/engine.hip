@@ -122,6 +122,12 @@ struct camelid_hip_engine {
   bool gu_fused = false;   // gate/up rows interleaved by 32, SwiGLU fused into their GEMV
   bool norm_fused = true;  // RMSNorms computed inside the qkv and gate/up GEMVs (Q8_0 layers)
   bool qkv_merged = true;  // Q4_K q|k and Q6_K v projections in one launch (k_gemv_qk4_v6)
+  // K-quant layers with the RMSNorm inside the q|k+v and gate|up launches (cm::k_norm_qk4_v6,
+  // cm::k_norm_gemv_q4k; CAMELID_HIP_KQ_NORM_FUSED): on when every layer has that shape
+  bool kq_norm_fused = true;
+  int nf_state = -1;              // -1 unknown, 0 off, 1 on (every layer fusable)
+  uint32_t* nf_slots = nullptr;   // the launches' flag words (cm::NF_WORDS)
+  uint32_t* p_err = nullptr;      // host copy of the handoff error word
   float *h = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr;
   float *logits = nullptr, *hidden_cap = nullptr, *xs = nullptr;
   float *cos_cur = nullptr, *sin_cur = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
@@ -794,6 +800,54 @@ void decode_attention(camelid_hip_engine* e, uint32_t l, const float* cos_base, 
                            scale, e->att, e->xq, e->xs, pf);
 }
 
+// The K-quant layer shape the norm-fused launches take: hidden 4096 (the norm workgroup's 256 x
+// 16 values), q|k stacked Q4_K + v Q6_K as k_gemv_qk4_v6 takes them, gate|up stacked Q4_K.
+bool nf_layer_ok(const camelid_hip_engine* e, const LayerW& L) {
+  const camelid_hip_dims& d = e->d;
+  if (!L.generic || d.hidden != (uint32_t)cm::KQ_NT * cm::NQ_C) return false;
+  const KMat& qk = L.p[0].kq;
+  const KMat& v6 = L.p[2].kq;
+  const KMat& gu = L.p[4].kq;
+  return e->qkv_merged && L.qk_stacked && L.p[0].quant == CAMELID_Q4_K && L.p[2].quant == CAMELID_Q6_K &&
+         qk.rows < 16384 && v6.rows < 16384 && qk.k == d.hidden && v6.k == d.hidden && L.gu_stacked &&
+         L.p[4].quant == CAMELID_Q4_K && gu.k == d.hidden;
+}
+
+// Whether the decode layers run the norm-fused launches: every layer must (their two flag
+// slots rely on the launches of the two kinds strictly alternating).
+bool nf_enabled(camelid_hip_engine* e) {
+  if (e->nf_state < 0) {
+    bool ok = e->kq_norm_fused && e->d.n_layers > 0;
+    for (uint32_t l = 0; ok && l < e->d.n_layers; ++l) ok = e->layers[l].set && nf_layer_ok(e, e->layers[l]);
+    e->nf_state = ok ? 1 : 0;
+  }
+  return e->nf_state == 1;
+}
+
+// Before a call's decode steps (not inside a captured graph): the flag slots start cleared (a
+// step cut short by an error leaves one set) and the handoff error word is cleared.
+int nf_begin(camelid_hip_engine* e) {
+  if (!nf_enabled(e)) return 0;
+  static const uint32_t zero = 0;
+  HIP_TRY(e, hipMemsetAsync(e->nf_slots, 0, cm::NF_WORDS * 4, e->stream));
+  HIP_TRY(e, hipMemcpyToSymbolAsync(HIP_SYMBOL(cm::g_handoff_error), &zero, 4, 0, hipMemcpyHostToDevice, e->stream));
+  return 0;
+}
+// After the call's work is enqueued: the error word comes back with the call's own sync.
+int nf_end(camelid_hip_engine* e) {
+  if (e->nf_state != 1) return 0;
+  HIP_TRY(e, hipMemcpyFromSymbolAsync(e->p_err, HIP_SYMBOL(cm::g_handoff_error), 4, 0, hipMemcpyDeviceToHost,
+                                      e->stream));
+  return 0;
+}
+int nf_failed(camelid_hip_engine* e) {
+  if (e->nf_state == 1 && *e->p_err) {
+    e->filled = 0;
+    return fail(e, "norm-fused GEMV: a workgroup's wait for the norm workgroup timed out");
+  }
+  return 0;
+}
+
 // A layer with K-quant projections (forward_layer_timed, inference.rs:6228-6807): the same
 // order as run_layer, with each projection in its own format; the RMSNorm kernel also writes
 // the normalized row, which is quantized to Q8_K when a K-quant projection reads it.
@@ -815,9 +869,25 @@ void run_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cos_base,
     launch_rmsnorm_quant(e->h, w, d.hidden, d.eps, e->xq, e->xs, nullptr, s, pf, 1, k8 ? e->kd : nullptr,
                          k8 ? e->kq : nullptr, k8 ? e->kbs : nullptr);
   };
-  norm(L.attn_norm, is_k(0) || is_k(1) || is_k(2), ahead(L.p[0]));
+  const bool nf = e->nf_state == 1;  // (decided by nf_begin before the call's steps)
   const KMat& qk = L.p[0].kq;
   const KMat& v6 = L.p[2].kq;
+  if (nf) {
+    // the attention RMSNorm inside the q|k + v launch (workgroup 0), flag slot 0
+    ProfScope ps(e, P_GEMV, kq_bytes(qk, false) + kq_bytes(v6, false) - qk.k * (1.0 + 4.0 / 256 + 4.0 / 32) +
+                                d.hidden * 8.0);
+    const uint32_t g4 = (qk.rows + 3) / 4, g6 = (v6.rows + 3) / 4;
+    const size_t lds = std::max({cm::kq4_lds_bytes((int)qk.k, 4), cm::kq6_lds_bytes((int)qk.k, 4),
+                                 cm::norm_q8k_lds_bytes((int)qk.k)});
+    const int it = (int)(qk.k / 32 + 63) / 64;
+    if (it == 2)
+      CM_LAUNCH(cm::k_norm_qk4_v6<2>, dim3(1 + g4 + g6), dim3(cm::KQ_NT), lds, s, e->h, L.attn_norm, d.eps,
+                e->nf_slots, 0, e->kd, e->kq, e->kbs, qk.a, qk.b, (int)qk.rows, e->qkv, (int)g4, v6.a, v6.b, v6.sc,
+                v6.d, (int)v6.rows, e->qkv + nq + nkv, (int)qk.k);
+    else
+      g_launch_error = "norm-fused q|k+v GEMV: row width " + std::to_string(qk.k) + " has no instantiation";
+  } else {
+  norm(L.attn_norm, is_k(0) || is_k(1) || is_k(2), ahead(L.p[0]));
   if (e->qkv_merged && L.qk_stacked && L.p[0].quant == CAMELID_Q4_K && L.p[2].quant == CAMELID_Q6_K &&
       qk.rows < 16384 && v6.rows < 16384 && qk.k == v6.k && qk.k / 32 <= 8 * 64) {
     // q|k and v in one launch (both from the Q8_K activation the norm wrote)
@@ -842,14 +912,33 @@ void run_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cos_base,
     if (!L.qk_stacked) proj(e, L.p[1], e->qkv + nq, nullptr);
     proj(e, L.p[2], e->qkv + nq + nkv, nullptr);
   }
+  }
   {
     ProfScope ps(e, P_ATTN, (nq + 2.0 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0));
     decode_attention(e, l, cos_base, sin_base, rope_stride, scale, ahead(L.p[3]));
   }
   proj(e, L.p[3], e->h, e->h, is_k(3) ? e->att : nullptr);
-  norm(L.ffn_norm, is_k(4) || is_k(5), ahead(L.p[4]));
-  proj(e, L.p[4], e->gu, nullptr);  // gate, or gate|up stacked
-  if (!L.gu_stacked) proj(e, L.p[5], e->gu + d.ffn_dim, nullptr);
+  if (nf) {
+    // the FFN RMSNorm inside the gate|up launch (workgroup 0), flag slot 1
+    const KMat& gu = L.p[4].kq;
+    ProfScope ps(e, P_GEMV, kq_bytes(gu, false) - gu.k * (1.0 + 4.0 / 256 + 4.0 / 32) + d.hidden * 8.0);
+    const int rpw = gu.rows >= 16384 ? 2 : 1;
+    const uint32_t R = 4 * rpw, grid = (gu.rows + R - 1) / R;
+    const size_t lds = std::max(cm::kq4_lds_bytes((int)gu.k, (int)R), cm::norm_q8k_lds_bytes((int)gu.k));
+    const int it = (int)(gu.k / 32 + 63) / 64;
+    if (it == 2 && rpw == 2)
+      CM_LAUNCH((cm::k_norm_gemv_q4k<2, 2>), dim3(1 + grid), dim3(cm::KQ_NT), lds, s, e->h, L.ffn_norm, d.eps,
+                e->nf_slots, 1, e->kd, e->kq, e->kbs, gu.a, gu.b, (int)gu.rows, (int)gu.k, e->gu);
+    else if (it == 2)
+      CM_LAUNCH((cm::k_norm_gemv_q4k<2, 1>), dim3(1 + grid), dim3(cm::KQ_NT), lds, s, e->h, L.ffn_norm, d.eps,
+                e->nf_slots, 1, e->kd, e->kq, e->kbs, gu.a, gu.b, (int)gu.rows, (int)gu.k, e->gu);
+    else
+      g_launch_error = "norm-fused gate|up GEMV: row width " + std::to_string(gu.k) + " has no instantiation";
+  } else {
+    norm(L.ffn_norm, is_k(4) || is_k(5), ahead(L.p[4]));
+    proj(e, L.p[4], e->gu, nullptr);  // gate, or gate|up stacked
+    if (!L.gu_stacked) proj(e, L.p[5], e->gu + d.ffn_dim, nullptr);
+  }
   {
     ProfScope ps(e, P_SILU, d.ffn_dim * 12.0 + d.ffn_dim * 34.0 / 32.0);
     const cm::Prefetch pf = ahead(L.p[6]);
@@ -1312,6 +1401,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   if (const char* f = std::getenv("CAMELID_HIP_FUSED_GU")) e->gu_fused = e->gu_fused && std::atoi(f) != 0;
   if (const char* f = std::getenv("CAMELID_HIP_FUSED_NORM")) e->norm_fused = std::atoi(f) != 0;
   if (const char* f = std::getenv("CAMELID_HIP_QKV_MERGED")) e->qkv_merged = std::atoi(f) != 0;
+  if (const char* f = std::getenv("CAMELID_HIP_KQ_NORM_FUSED")) e->kq_norm_fused = std::atoi(f) != 0;
   e->att_slots = attn_ring_slots(e->kvs);
   if (const char* f = std::getenv("CAMELID_HIP_ATT_SPLIT")) e->att_split_min = (uint32_t)std::strtoul(f, nullptr, 10);
   const size_t nq = (size_t)d.n_heads * d.head_dim, nkv = (size_t)d.n_kv_heads * d.head_dim;
@@ -1333,7 +1423,8 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
            dev_alloc(e, &e->att_mx, (size_t)d.n_heads * ((e->kvs + 255) / 256)) ||
            host_alloc(e, &e->p_emb, d.hidden) ||
            host_alloc(e, &e->p_cos, half) || host_alloc(e, &e->p_sin, half) || host_alloc(e, &e->p_logits, d.vocab) ||
-           host_alloc(e, &e->p_st, 1);
+           host_alloc(e, &e->p_st, 1) || host_alloc(e, &e->p_err, 1) ||
+           dev_alloc(e, &e->nf_slots, (size_t)cm::NF_WORDS);
   if (rc) {
     std::string m = e->err;
     camelid_hip_engine_free(e);
@@ -1341,7 +1432,8 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   }
   // A fresh cache reads as zeros (K/V past `filled` are never read); StepState starts at 0.
   if (hipMemset(e->kc, 0, kv_elems * 2) != hipSuccess || hipMemset(e->vc, 0, kv_elems * 2) != hipSuccess ||
-      hipMemset(e->st, 0, sizeof(cm::StepState)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+      hipMemset(e->st, 0, sizeof(cm::StepState)) != hipSuccess ||
+      hipMemset(e->nf_slots, 0, cm::NF_WORDS * 4) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
     camelid_hip_engine_free(e);
     return fail(nullptr, "initial device memset failed");
   }
@@ -1364,6 +1456,7 @@ void camelid_hip_engine_free(camelid_hip_engine* e) {
 int camelid_hip_set_layer(camelid_hip_engine* e, uint32_t layer, const uint8_t* const w[7], const size_t len[7],
                           const uint8_t quant[7], uint8_t q8_layout, const float* attn_norm, const float* ffn_norm,
                           const float* q_norm, const float* k_norm) {
+  if (e) e->nf_state = -1;  // (the fused-norm decision is taken again for the new weights)
   if (!e) return fail(nullptr, "null engine");
   if (layer >= e->d.n_layers) return fail(e, "layer index out of range");
   if (!w || !len || !quant || !attn_norm || !ffn_norm) return fail(e, "null argument");
@@ -1570,12 +1663,14 @@ int camelid_hip_forward_token(camelid_hip_engine* e, const float* emb, const flo
   HIP_TRY(e, hipMemcpyAsync(e->cos_cur, e->p_cos, half * 4, hipMemcpyHostToDevice, e->stream));
   HIP_TRY(e, hipMemcpyAsync(e->sin_cur, e->p_sin, half * 4, hipMemcpyHostToDevice, e->stream));
   HIP_TRY(e, hipMemcpyAsync(e->st, e->p_st, sizeof(cm::StepState), hipMemcpyHostToDevice, e->stream));
+  if (nf_begin(e)) return 1;
   run_stack(e, e->cos_cur, e->sin_cur, 0, scale);
   run_head(e, nullptr, 0);
   if (check_launch(e)) {
     e->filled = 0;
     return 1;
   }
+  if (nf_end(e)) return 1;
   HIP_TRY(e, hipMemcpyAsync(e->p_st, e->st, sizeof(cm::StepState), hipMemcpyDeviceToHost, e->stream));
   if (want_logits && logits_out)
     HIP_TRY(e, hipMemcpyAsync(e->p_logits, e->logits, (size_t)d.vocab * 4, hipMemcpyDeviceToHost, e->stream));
@@ -1584,6 +1679,7 @@ int camelid_hip_forward_token(camelid_hip_engine* e, const float* emb, const flo
     e->filled = 0;
     return fail(e, std::string("forward_token: ") + hipGetErrorString(st));
   }
+  if (nf_failed(e)) return 1;
   if (tok_out) *tok_out = e->p_st->tok;
   if (want_logits && logits_out) std::memcpy(logits_out, e->p_logits, (size_t)d.vocab * 4);
   e->filled = position + 1;
@@ -1633,11 +1729,19 @@ int camelid_hip_prefill(camelid_hip_engine* e, const float* embs, const float* c
     } else {
       // one decode step per token (CAMELID_HIP_PREFILL=token; the reference's CPU prefill of
       // K-quant layers is likewise a per-token loop of row dots, inference.rs:2462-2473)
+      if (nf_begin(e)) {
+        rc = 1;
+        break;
+      }
       for (uint32_t t = 0; t < n; ++t) {
         (void)hipMemcpyAsync(e->h, d_embs + (size_t)t * d.hidden, d.hidden * 4, hipMemcpyDeviceToDevice, e->stream);
         (void)hipMemcpyAsync(e->st, d_sts + t, sizeof(cm::StepState), hipMemcpyDeviceToDevice, e->stream);
         e->cur_pos = sv[t].pos;
         run_stack(e, d_cos + (size_t)t * half, d_sin + (size_t)t * half, 0, scale);
+      }
+      if (nf_end(e)) {
+        rc = 1;
+        break;
       }
     }
     if (check_launch(e)) {
@@ -1647,6 +1751,10 @@ int camelid_hip_prefill(camelid_hip_engine* e, const float* embs, const float* c
     hipError_t st = hipStreamSynchronize(e->stream);
     if (st != hipSuccess) {
       rc = fail(e, std::string("prefill: ") + hipGetErrorString(st));
+      break;
+    }
+    if (nf_failed(e)) {
+      rc = 1;
       break;
     }
   } while (0);
@@ -1704,6 +1812,7 @@ int camelid_hip_verify(camelid_hip_engine* e, const float* embs, const float* co
     // k single-token steps; the head writes each greedy token to v_tok[step]
     *e->p_st = cm::StepState{base_position, 0u, 0u, 0u};
     HIP_TRY(e, hipMemcpyAsync(e->st, e->p_st, sizeof(cm::StepState), hipMemcpyHostToDevice, e->stream));
+    if (nf_begin(e)) return 1;
     for (uint32_t t = 0; t < k; ++t) {
       HIP_TRY(e, hipMemcpyAsync(e->h, e->v_embs + (size_t)t * d.hidden, d.hidden * 4, hipMemcpyDeviceToDevice,
                                 e->stream));
@@ -1711,6 +1820,7 @@ int camelid_hip_verify(camelid_hip_engine* e, const float* embs, const float* co
       run_stack(e, e->v_cos + (size_t)t * half, e->v_sin + (size_t)t * half, 0, scale);
       run_head(e, e->v_tok, k);
     }
+    if (nf_end(e)) return 1;
   }
   if (check_launch(e)) {
     e->filled = 0;
@@ -1721,6 +1831,7 @@ int camelid_hip_verify(camelid_hip_engine* e, const float* embs, const float* co
     e->filled = 0;
     return fail(e, std::string("verify: ") + hipGetErrorString(st));
   }
+  if (nf_failed(e)) return 1;
   HIP_TRY(e, hipMemcpy(tokens_out, e->v_tok, (size_t)k * 4, hipMemcpyDeviceToHost));
   return 0;
 }
@@ -1740,6 +1851,7 @@ int camelid_hip_generate(camelid_hip_engine* e, uint32_t token, uint32_t positio
   const bool graph = e->use_graph && !e->profiling && !e->capture;
   *e->p_st = cm::StepState{position, token, 0u, 0u};
   HIP_TRY(e, hipMemcpyAsync(e->st, e->p_st, sizeof(cm::StepState), hipMemcpyHostToDevice, e->stream));
+  if (nf_begin(e)) return 1;
   if (graph) {  // the graphs this call's positions need (the split attention from att_split_min on)
     const uint64_t first = (uint64_t)position + 1, last = (uint64_t)position + n_steps;
     const bool split_used = e->att_split_min && last >= e->att_split_min;
@@ -1763,11 +1875,13 @@ int camelid_hip_generate(camelid_hip_engine* e, uint32_t token, uint32_t positio
     e->filled = 0;
     return 1;
   }
+  if (nf_end(e)) return 1;
   hipError_t st = hipStreamSynchronize(e->stream);
   if (st != hipSuccess) {
     e->filled = 0;
     return fail(e, std::string("generate: ") + hipGetErrorString(st));
   }
+  if (nf_failed(e)) return 1;
   HIP_TRY(e, hipMemcpy(tokens_out, e->tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost));
   e->filled = position + n_steps;
   return 0;

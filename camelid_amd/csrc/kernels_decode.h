@@ -552,7 +552,9 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
   }
   // classify the steps; d = ulps of an in-binade step, 0 for a special one
   uint32_t d[C];
-  int eb_of[C];
+  uint32_t ebp[(C + 3) / 4];  // the predicted binade before each step (an exponent field: a byte each)
+#pragma unroll
+  for (int c = 0; c < (C + 3) / 4; ++c) ebp[c] = 0u;
   uint32_t spm = 0;
   int eb = fs_binade(R, i0), e_end = 1;
 #pragma unroll
@@ -565,7 +567,7 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
     const bool special = i < n && dc == SEG_FLAG;
     d[c] = (i < n && !special) ? dc : 0u;
     spm |= (uint32_t)special << c;
-    eb_of[c] = eb;
+    ebp[c >> 2] |= (uint32_t)eb << (8 * (c & 3));
     if (i == n - 1) e_end = ea;
     eb = ea;
     R = Ra;
@@ -616,7 +618,7 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
     if ((spm >> c) & 1u) {
       if (pos < (uint32_t)FS_CAP) {
         uint32_t lo, lim;
-        fs_entry(run, eb_of[c], lo, lim);
+        fs_entry(run, (int)((ebp[c >> 2] >> (8 * (c & 3))) & 0xffu), lo, lim);
         sh_ent[pos] = make_uint4(run, lo, lim, __float_as_uint(t[c]));
       }
       ++pos;

@@ -76,6 +76,48 @@ constexpr int KQ_NT = 256;  // 4 waves
 __host__ __device__ inline int kq_rows_per_wg(int rpw) { return 4 * rpw; }
 
 // ---------------------------------------------------------------------------
+// In-launch handoff of a norm-fused K-quant GEMV: workgroup 0 computes the RMSNorm and its
+// Q8_K quantization and publishes it with agent-scope (XCD-coherent) stores, waits for them
+// to complete, then sets a flag word (one copy per XCD, 128 bytes apart); every other
+// workgroup issues its weight loads, waits for the copy of its own XCD (workgroup b runs on
+// XCD b % 8) and reads the activation with agent-scope loads.  Two flag slots, one per norm
+// of a layer: a launch resets the other slot (whose launch has completed: the launches of the
+// two kinds strictly alternate) and uses its own, which the previous launch reset.  The wait
+// is bounded (about a second): past it the workgroup sets g_handoff_error and goes on.
+constexpr int NF_XCD = 8, NF_STRIDE = 32;  // flag copies per slot, words between copies
+constexpr int NF_WORDS = 2 * NF_XCD * NF_STRIDE;
+__device__ uint32_t g_handoff_error;
+
+__device__ __forceinline__ uint64_t ld_agent64(const void* p) {
+  return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_agent32(const void* p) {
+  return __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent64(void* p, uint64_t v) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent32(void* p, uint32_t v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The waiting side: thread 0 polls its XCD's copy of the slot, then the workgroup barrier.
+__device__ __forceinline__ void handoff_wait(const uint32_t* slot) {
+  if (threadIdx.x == 0) {
+    const uint32_t* f = slot + (blockIdx.x % NF_XCD) * NF_STRIDE;
+    uint32_t polls = 0;
+    while (ld_agent32(f) == 0u) {
+      __builtin_amdgcn_s_sleep(2);
+      if (++polls == (1u << 20)) {
+        g_handoff_error = 1u;
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
 // Q4_K GEMV (q4k_gemv, cuda_resident.rs:601; CPU: q4_k_dot_arm, refmath.rs:424-561, the
 // Q4_K decode dot of inference.rs:17906-17965), faithful:
 //   per superblock s: prod = sum_g bsum32_g * min_g, sumi = sum_j (lo_j*sc_2j + hi_j*sc_2j+1)
@@ -102,7 +144,9 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
                                                     int rows, int K, const float* __restrict__ yd,
                                                     const int8_t* __restrict__ yq, const int32_t* __restrict__ ybs,
                                                     float* y, const float* resid, float* __restrict__ part_v,
-                                                    uint32_t* __restrict__ part_i, const float* __restrict__ xf) {
+                                                    uint32_t* __restrict__ part_i, const float* __restrict__ xf,
+                                                    const uint32_t* ready = nullptr, int sk = -1) {
+  (void)sk;  // (the measurement build's stamp kind)
   constexpr int R = 4 * RPW;
   extern __shared__ __align__(16) unsigned char smem[];
   const int NSB = K >> 8, NC = K >> 5;
@@ -127,7 +171,15 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
       hv[k][i] = ld_stream(hp + (cc >> 3));
     }
   }
-  if (xf) {  // the activation given in f32: each wave quantizes blocks wave, wave + 4, ... to Q8_K
+  if (ready) {  // the activation published by workgroup 0 of this launch (agent-scope loads)
+    handoff_wait(ready);
+    for (int c = tid; c < (K >> 3); c += KQ_NT) reinterpret_cast<uint64_t*>(xq)[c] = ld_agent64(yq + 8 * c);
+    for (int i = tid; i < NSB; i += KQ_NT) xd[i] = __uint_as_float(ld_agent32(yd + i));
+    for (int i = tid; i < NC; i += KQ_NT) xbs[i] = (int)ld_agent32(ybs + i);
+    if (sk >= 0) {
+      CM_GEMV_STAMP(sk, 3, 0)
+    }
+  } else if (xf) {  // the activation given in f32: each wave quantizes blocks wave, wave + 4, ... to Q8_K
     for (int b = wave; b < NSB; b += KQ_NT / 64) quantize_q8k_wave(xf + 256 * b, xq + 256 * b, xbs + 8 * b, xd + b);
   } else {
     for (int c = tid; c < (K >> 4); c += KQ_NT) reinterpret_cast<int4*>(xq)[c] = reinterpret_cast<const int4*>(yq)[c];
@@ -198,6 +250,9 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
       }
     }
   }
+  if (sk >= 0) {
+    CM_GEMV_STAMP(sk, 5, 0)
+  }
 }
 
 template <int IT, int RPW>
@@ -236,7 +291,8 @@ __device__ __forceinline__ void gemv_q6k_body(const int bid, const uint8_t* __re
                                                     const int8_t* __restrict__ scl, const uint16_t* __restrict__ dw,
                                                     int rows, int K, const float* __restrict__ yd,
                                                     const int8_t* __restrict__ yq, float* y, const float* resid,
-                                                    float* __restrict__ part_v, uint32_t* __restrict__ part_i) {
+                                                    float* __restrict__ part_v, uint32_t* __restrict__ part_i,
+                                                    const uint32_t* ready = nullptr) {
   constexpr int R = 4 * RPW;
   extern __shared__ __align__(16) unsigned char smem[];
   const int NSB = K >> 8, NU = K >> 6;
@@ -246,16 +302,19 @@ __device__ __forceinline__ void gemv_q6k_body(const int bid, const uint8_t* __re
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int row0 = bid * R;
   // activation pairs: entry (s, j, l) = bytes (q[16j+l], q[16j+8+l], q[16j+l], q[16j+8+l])
+  // (published by workgroup 0 of this launch: agent-scope loads after the handoff)
+  if (ready) handoff_wait(ready);
   for (int e = tid; e < NSB * 128; e += KQ_NT) {
     const int l = e & 7, g = e >> 3;  // g = s * 16 + j
     const uint32_t* src = reinterpret_cast<const uint32_t*>(yq + (size_t)g * 16);
-    const uint32_t a = src[l >> 2], b = src[(l >> 2) + 2];
+    const uint32_t a = ready ? ld_agent32(src + (l >> 2)) : src[l >> 2];
+    const uint32_t b = ready ? ld_agent32(src + (l >> 2) + 2) : src[(l >> 2) + 2];
     const uint32_t bl = l & 3;
     // bytes: 0 <- a.byte(bl), 1 <- b.byte(bl), 2 <- a.byte(bl), 3 <- b.byte(bl)
     const uint32_t sel = bl | ((4 + bl) << 8) | (bl << 16) | ((4 + bl) << 24);
     xp[e] = __builtin_amdgcn_perm(b, a, sel);
   }
-  for (int i = tid; i < NSB; i += KQ_NT) xd[i] = yd[i];
+  for (int i = tid; i < NSB; i += KQ_NT) xd[i] = ready ? __uint_as_float(ld_agent32(yd + i)) : yd[i];
   __syncthreads();
   const uint32_t M4 = 0x0f0f0f0fu, M2 = 0x03030303u;
 #pragma unroll
@@ -364,6 +423,147 @@ __global__ __launch_bounds__(KQ_NT) void k_gemv_qk4_v6(const uint8_t* __restrict
     gemv_q4k_body<IT, 1>((int)blockIdx.x, nib, hdr, rows4, K, yd, yq, ybs, y4, nullptr, nullptr, nullptr, nullptr);
   else
     gemv_q6k_body<1>((int)blockIdx.x - g4, ql, qh, scl, dw, rows6, K, yd, yq, y6, nullptr, nullptr, nullptr);
+}
+
+// ---------------------------------------------------------------------------
+// Norm-fused K-quant decode GEMVs (hidden 4096 = 256 threads x 16 values).  Workgroup 0 of
+// the launch computes the layer's RMSNorm (tensor/mod.rs:2083-2106: the in-order sum of
+// squares, scale = 1/sqrt(ss/n + eps), y = (x * scale) * w) and its Q8_K quantization
+// (inference.rs:17564-17599, as k_rmsnorm_quant: the same operations, so the same bits) and
+// publishes the activation (see handoff_wait); the other workgroups run the GEMV bodies,
+// whose weight loads go out before they wait for it.  The RMSNorm launch of the unfused
+// layer and its dependency gap disappear; its latency overlaps the weight stream.
+constexpr int NQ_C = 16;  // values per thread of the norm workgroup
+__host__ __device__ inline size_t norm_q8k_lds_bytes(int n) { return (size_t)n * 4 + sizeof(FsLds<KQ_NT>); }
+
+// Thread t holds values 16t..16t+15 (the one-pass sum's layout); a Q8_K block is one row of 16
+// lanes (the (|max|, first index) pick by DPP within the row; block position 16 j + e).
+// smem: the n squares (the sum's fallback) + FsLds<256>.  n == 16 * 256.
+// (measurement build: stamps of workgroup 0 in g_gemv_stamps[kind][0]: 0 start, 6 x and w
+// loaded, 7 sum of squares, 1 published; of the other workgroups b < 256: 0 start, 3 flag
+// seen and activation staged, 5 end)
+__device__ __forceinline__ void norm_q8k_publish(const float* __restrict__ x, const float* __restrict__ w, int n,
+                                                 float eps, float* __restrict__ kd, int8_t* __restrict__ kq,
+                                                 int32_t* __restrict__ kbs, uint32_t* slot_set,
+                                                 uint32_t* slot_reset, unsigned char* smem, int kind) {
+  (void)kind;
+  constexpr int C = NQ_C;
+  CM_GEMV_STAMP(kind, 0, 0)
+  const int tid = threadIdx.x, j = tid & 15;
+  float* sq = reinterpret_cast<float*>(smem);
+  FsLds<KQ_NT>& fs = *reinterpret_cast<FsLds<KQ_NT>*>(smem + (size_t)n * 4);
+  if (tid == 0) {  // the other kind's slot: its launch has completed
+#pragma unroll
+    for (int c = 0; c < NF_XCD; ++c) st_agent32(slot_reset + c * NF_STRIDE, 0u);
+  }
+  // (x and w are read again after the sum, not held across it: the kernel's register count
+  // is this workgroup's, and it sets how many GEMV workgroups are resident)
+  float tv[C];
+#pragma unroll
+  for (int u = 0; u < C / 4; ++u) {
+    const float4 a = reinterpret_cast<const float4*>(x + tid * C)[u];
+    tv[4 * u] = a.x * a.x, tv[4 * u + 1] = a.y * a.y, tv[4 * u + 2] = a.z * a.z, tv[4 * u + 3] = a.w * a.w;
+  }
+#pragma unroll
+  for (int u = 0; u < C / 4; ++u)
+    reinterpret_cast<float4*>(sq + tid * C)[u] = make_float4(tv[4 * u], tv[4 * u + 1], tv[4 * u + 2], tv[4 * u + 3]);
+  CM_GEMV_STAMP(kind, 6, 0)
+  __syncthreads();
+  const float ss = inorder_sum_onepass<KQ_NT, C>(tv, sq, n, fs);
+  CM_GEMV_STAMP(kind, 7, 0)
+  const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+  float y[C];
+#pragma unroll
+  for (int u = 0; u < C / 4; ++u) {
+    const float4 a = reinterpret_cast<const float4*>(x + tid * C)[u];
+    const float4 b = reinterpret_cast<const float4*>(w + tid * C)[u];
+    y[4 * u] = (a.x * scale) * b.x;
+    y[4 * u + 1] = (a.y * scale) * b.y;
+    y[4 * u + 2] = (a.z * scale) * b.z;
+    y[4 * u + 3] = (a.w * scale) * b.w;
+  }
+  float a = 0.0f, v = 0.0f;
+  int idx = 0x7fffffff;
+#pragma unroll
+  for (int e = 0; e < C; ++e)
+    if (fabsf(y[e]) > a) {
+      a = fabsf(y[e]);
+      v = y[e];
+      idx = C * j + e;
+    }
+  amax_pick_quad(a, idx, v);
+  amax_pick_dpp<0x124>(a, idx, v);  // row_ror:4
+  amax_pick_dpp<0x128>(a, idx, v);  // row_ror:8: every lane of the row holds the block's pick
+  const float iscale = a > 0.0f ? -127.0f / v : 0.0f;
+  uint32_t words[C / 4];
+  int sum = 0;
+#pragma unroll
+  for (int w4 = 0; w4 < C / 4; ++w4) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int q = a > 0.0f ? min(nearest_int_ref(iscale * y[w4 * 4 + e]), 127) : 0;
+      sum += (int8_t)q;
+      word |= ((uint32_t)q & 0xffu) << (8 * e);
+    }
+    words[w4] = word;
+  }
+  // lanes 2m and 2m + 1 hold values 32m..32m+31 of the block: the per-32 sum
+  const int s2 = sum + __builtin_amdgcn_update_dpp(0, sum, 0xB1, 0xf, 0xf, false);
+  st_agent64(kq + tid * C, (uint64_t)words[0] | ((uint64_t)words[1] << 32));
+  st_agent64(kq + tid * C + 8, (uint64_t)words[2] | ((uint64_t)words[3] << 32));
+  if ((tid & 1) == 0) st_agent32(kbs + (tid >> 1), (uint32_t)s2);
+  if (j == 0) st_agent32(kd + (tid >> 4), __float_as_uint(a > 0.0f ? 1.0f / iscale : 0.0f));
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
+  __syncthreads();
+  if (tid == 0) {
+#pragma unroll
+    for (int c = 0; c < NF_XCD; ++c) st_agent32(slot_set + c * NF_STRIDE, 1u);
+  }
+  CM_GEMV_STAMP(kind, 1, 0)
+}
+
+// q|k (Q4_K) + v (Q6_K) with the attention RMSNorm: grid 1 + g4 + g6 (k_gemv_qk4_v6's
+// workgroups after the norm workgroup); slot `kind` of the flag words (slots: 2 x NF_XCD x
+// NF_STRIDE words).
+template <int IT>
+__global__ __launch_bounds__(KQ_NT) void k_norm_qk4_v6(const float* __restrict__ x, const float* __restrict__ nw,
+                                                       float eps, uint32_t* slots, int kind, float* __restrict__ kd,
+                                                       int8_t* __restrict__ kq, int32_t* __restrict__ kbs,
+                                                       const uint8_t* __restrict__ nib, const uint8_t* __restrict__ hdr,
+                                                       int rows4, float* y4, int g4, const uint8_t* __restrict__ ql,
+                                                       const uint8_t* __restrict__ qh, const int8_t* __restrict__ scl,
+                                                       const uint16_t* __restrict__ dw, int rows6, float* y6, int K) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint32_t* mine = slots + kind * NF_XCD * NF_STRIDE;
+  if (blockIdx.x == 0) {
+    norm_q8k_publish(x, nw, K, eps, kd, kq, kbs, mine, slots + (1 - kind) * NF_XCD * NF_STRIDE, smem, kind);
+    return;
+  }
+  CM_GEMV_STAMP(kind, 0, 0)
+  const int b = (int)blockIdx.x - 1;
+  if (b < g4)
+    gemv_q4k_body<IT, 1>(b, nib, hdr, rows4, K, kd, kq, kbs, y4, nullptr, nullptr, nullptr, nullptr, mine, kind);
+  else
+    gemv_q6k_body<1>(b - g4, ql, qh, scl, dw, rows6, K, kd, kq, y6, nullptr, nullptr, nullptr, mine);
+}
+
+// A Q4_K projection (gate|up stacked) with the FFN RMSNorm: grid 1 + the GEMV's workgroups.
+template <int IT, int RPW>
+__global__ __launch_bounds__(KQ_NT) void k_norm_gemv_q4k(const float* __restrict__ x, const float* __restrict__ nw,
+                                                         float eps, uint32_t* slots, int kind, float* __restrict__ kd,
+                                                         int8_t* __restrict__ kq, int32_t* __restrict__ kbs,
+                                                         const uint8_t* __restrict__ nib,
+                                                         const uint8_t* __restrict__ hdr, int rows, int K, float* y) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint32_t* mine = slots + kind * NF_XCD * NF_STRIDE;
+  if (blockIdx.x == 0) {
+    norm_q8k_publish(x, nw, K, eps, kd, kq, kbs, mine, slots + (1 - kind) * NF_XCD * NF_STRIDE, smem, kind);
+    return;
+  }
+  CM_GEMV_STAMP(kind, 0, 0)
+  gemv_q4k_body<IT, RPW>((int)blockIdx.x - 1, nib, hdr, rows, K, kd, kq, kbs, y, nullptr, nullptr, nullptr, nullptr,
+                         mine, kind);
 }
 
 // ---------------------------------------------------------------------------

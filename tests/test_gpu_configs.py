@@ -9,7 +9,7 @@ CPU<->GPU stream parity (tests/cuda_cpu_parity.rs:32-62) and full-forward parity
 (src/cuda_resident/tests.rs:354).
 
 Also here: the engine's documented switches (CAMELID_HIP_FUSED_GU, _FUSED_NORM, _READ_AHEAD,
-_GRAPHS, _QKV_MERGED) each switched off against the same golden / oracle, and greedy ties
+_GRAPHS, _KV_AHEAD, _QKV_MERGED, _KQ_NORM_FUSED) each switched off against the same golden / oracle, and greedy ties
 (duplicated lm_head rows) through the product argmax paths.
 """
 import importlib.util
@@ -73,19 +73,23 @@ def test_config_stream_matches_golden(name):
 
 
 @pytest.mark.parametrize("switch", ["CAMELID_HIP_FUSED_GU", "CAMELID_HIP_FUSED_NORM", "CAMELID_HIP_READ_AHEAD",
-                                    "CAMELID_HIP_GRAPHS"])
+                                    "CAMELID_HIP_GRAPHS", "CAMELID_HIP_KV_AHEAD"])
 def test_switch_off_keeps_tinyllama_stream(monkeypatch, switch):
     """Each documented switch of the Q8_0 decode path set to 0 (the separate RMSNorm launch,
-    the separate SwiGLU launch, no weight read-ahead, launches without a graph): the TinyLlama
-    golden stream (configs[0], 128 + 128) is still reproduced by the device loop."""
+    the separate SwiGLU launch, no weight read-ahead, launches without a graph, no KV read into
+    L2 by the qkv launch): the TinyLlama golden stream (configs[0], 128 + 128) is still
+    reproduced by the device loop."""
     monkeypatch.setenv(switch, "0")
     test_config_stream_matches_golden("tinyllama-1.1b")
 
 
 def test_switch_off_qkv_merged_kquant_matches_oracle(monkeypatch):
-    """CAMELID_HIP_QKV_MERGED=0 (separate Q4_K q|k and Q6_K v launches) and the default merged
-    launch, at the C5 layer shape (hidden 4096, 32/8 heads of 128, ffn 12288, Q4_K_M): per-layer
-    hidden states, logits and tokens of both are bit-identical to the CPU oracle."""
+    """At the C5 layer shape (hidden 4096, 32/8 heads of 128, ffn 12288, Q4_K_M), three K-quant
+    decode layouts: the default (each RMSNorm inside the q|k+v and gate|up launches, whose other
+    workgroups wait for it), CAMELID_HIP_KQ_NORM_FUSED=0 (a separate RMSNorm + Q8_K launch before
+    the merged q|k+v launch and the gate|up launch) and CAMELID_HIP_QKV_MERGED=0 (separate Q4_K
+    q|k and Q6_K v launches, which also leaves the norm unfused): per-layer hidden states, logits
+    and tokens of each are bit-identical to the CPU oracle."""
     from oracle.oracle import OracleModel
     cfg = tiny_config(n_layers=2, hidden=4096, ffn_dim=12288, n_heads=32, n_kv_heads=8, head_dim=128, vocab=2048,
                       qk_norm=True, split_half=True, rope_theta=1e6, quant_scheme="q4_k_m", prompt_len=12)
@@ -99,8 +103,9 @@ def test_switch_off_qkv_merged_kquant_matches_oracle(monkeypatch):
         tok, hid, lg = orc.forward(tok, pos, hidden=True, logits=True)
         want.append((tok, hid, lg))
         pos += 1
-    for merged in ("1", "0"):
+    for merged, fused in (("1", "1"), ("1", "0"), ("0", "1")):
         monkeypatch.setenv("CAMELID_HIP_QKV_MERGED", merged)
+        monkeypatch.setenv("CAMELID_HIP_KQ_NORM_FUSED", fused)
         sess = ResidentSession(model, 32)
         sess.engine.capture_hidden(True)
         sess.prefill(prompt[:-1])
@@ -108,8 +113,8 @@ def test_switch_off_qkv_merged_kquant_matches_oracle(monkeypatch):
         for step, (t_o, hid_o, lg_o) in enumerate(want):
             tok = sess.step(tok, pos, logits=True)
             hid = sess.engine.read_hidden()
-            assert np.array_equal(hid.view(np.uint32), hid_o.view(np.uint32)), (merged, step)
-            assert np.array_equal(sess.engine.last_logits.view(np.uint32), lg_o.view(np.uint32)), (merged, step)
+            assert np.array_equal(hid.view(np.uint32), hid_o.view(np.uint32)), (merged, fused, step)
+            assert np.array_equal(sess.engine.last_logits.view(np.uint32), lg_o.view(np.uint32)), (merged, fused, step)
             assert tok == t_o
             pos += 1
         sess.close()
