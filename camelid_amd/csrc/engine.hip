@@ -800,11 +800,11 @@ void decode_attention(camelid_hip_engine* e, uint32_t l, const float* cos_base, 
                            scale, e->att, e->xq, e->xs, pf);
 }
 
-// The K-quant layer shape the norm-fused launches take: hidden 4096 (the norm workgroup's 256 x
-// 16 values), q|k stacked Q4_K + v Q6_K as k_gemv_qk4_v6 takes them, gate|up stacked Q4_K.
+// The K-quant layer shape the norm-fused launches take: hidden 4096 (the norm workgroup's 512 x
+// 8 values), q|k stacked Q4_K + v Q6_K as k_gemv_qk4_v6 takes them, gate|up stacked Q4_K.
 bool nf_layer_ok(const camelid_hip_engine* e, const LayerW& L) {
   const camelid_hip_dims& d = e->d;
-  if (!L.generic || d.hidden != (uint32_t)cm::KQ_NT * cm::NQ_C) return false;
+  if (!L.generic || d.hidden != (uint32_t)cm::NF_NT * cm::NQ_C) return false;
   const KMat& qk = L.p[0].kq;
   const KMat& v6 = L.p[2].kq;
   const KMat& gu = L.p[4].kq;
@@ -876,12 +876,13 @@ void run_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cos_base,
     // the attention RMSNorm inside the q|k + v launch (workgroup 0), flag slot 0
     ProfScope ps(e, P_GEMV, kq_bytes(qk, false) + kq_bytes(v6, false) - qk.k * (1.0 + 4.0 / 256 + 4.0 / 32) +
                                 d.hidden * 8.0);
-    const uint32_t g4 = (qk.rows + 3) / 4, g6 = (v6.rows + 3) / 4;
-    const size_t lds = std::max({cm::kq4_lds_bytes((int)qk.k, 4), cm::kq6_lds_bytes((int)qk.k, 4),
+    constexpr uint32_t R = cm::NF_NT / 64;  // rows per workgroup: one per wave
+    const uint32_t g4 = (qk.rows + R - 1) / R, g6 = (v6.rows + R - 1) / R;
+    const size_t lds = std::max({cm::kq4_lds_bytes((int)qk.k, R), cm::kq6_lds_bytes((int)qk.k, R),
                                  cm::norm_q8k_lds_bytes((int)qk.k)});
     const int it = (int)(qk.k / 32 + 63) / 64;
     if (it == 2)
-      CM_LAUNCH(cm::k_norm_qk4_v6<2>, dim3(1 + g4 + g6), dim3(cm::KQ_NT), lds, s, e->h, L.attn_norm, d.eps,
+      CM_LAUNCH(cm::k_norm_qk4_v6<2>, dim3(1 + g4 + g6), dim3(cm::NF_NT), lds, s, e->h, L.attn_norm, d.eps,
                 e->nf_slots, 0, e->kd, e->kq, e->kbs, qk.a, qk.b, (int)qk.rows, e->qkv, (int)g4, v6.a, v6.b, v6.sc,
                 v6.d, (int)v6.rows, e->qkv + nq + nkv, (int)qk.k);
     else
@@ -923,14 +924,14 @@ void run_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cos_base,
     const KMat& gu = L.p[4].kq;
     ProfScope ps(e, P_GEMV, kq_bytes(gu, false) - gu.k * (1.0 + 4.0 / 256 + 4.0 / 32) + d.hidden * 8.0);
     const int rpw = gu.rows >= 16384 ? 2 : 1;
-    const uint32_t R = 4 * rpw, grid = (gu.rows + R - 1) / R;
+    const uint32_t R = (cm::NF_NT / 64) * rpw, grid = (gu.rows + R - 1) / R;
     const size_t lds = std::max(cm::kq4_lds_bytes((int)gu.k, (int)R), cm::norm_q8k_lds_bytes((int)gu.k));
     const int it = (int)(gu.k / 32 + 63) / 64;
     if (it == 2 && rpw == 2)
-      CM_LAUNCH((cm::k_norm_gemv_q4k<2, 2>), dim3(1 + grid), dim3(cm::KQ_NT), lds, s, e->h, L.ffn_norm, d.eps,
+      CM_LAUNCH((cm::k_norm_gemv_q4k<2, 2>), dim3(1 + grid), dim3(cm::NF_NT), lds, s, e->h, L.ffn_norm, d.eps,
                 e->nf_slots, 1, e->kd, e->kq, e->kbs, gu.a, gu.b, (int)gu.rows, (int)gu.k, e->gu);
     else if (it == 2)
-      CM_LAUNCH((cm::k_norm_gemv_q4k<2, 1>), dim3(1 + grid), dim3(cm::KQ_NT), lds, s, e->h, L.ffn_norm, d.eps,
+      CM_LAUNCH((cm::k_norm_gemv_q4k<2, 1>), dim3(1 + grid), dim3(cm::NF_NT), lds, s, e->h, L.ffn_norm, d.eps,
                 e->nf_slots, 1, e->kd, e->kq, e->kbs, gu.a, gu.b, (int)gu.rows, (int)gu.k, e->gu);
     else
       g_launch_error = "norm-fused gate|up GEMV: row width " + std::to_string(gu.k) + " has no instantiation";

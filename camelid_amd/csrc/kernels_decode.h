@@ -417,8 +417,14 @@ __device__ uint64_t g_gemv_stamps[2 * GEMV_STAMP_WGS * GEMV_NSTAMP];
 #define CM_GEMV_STAMP(kind, i, t)                                                                        \
   if (threadIdx.x == (t) && blockIdx.x < GEMV_STAMP_WGS)                                                 \
     g_gemv_stamps[((kind) * GEMV_STAMP_WGS + blockIdx.x) * GEMV_NSTAMP + (i)] = __builtin_amdgcn_s_memrealtime();
+// (workgroups spread over the whole grid: every ceil(grid / 256)-th, in slot blockIdx / that)
+#define CM_GEMV_STAMP_SAMPLED(kind, i, t)                                                                \
+  if (threadIdx.x == (t) && blockIdx.x % ((gridDim.x + GEMV_STAMP_WGS - 1) / GEMV_STAMP_WGS) == 0)       \
+    g_gemv_stamps[((kind) * GEMV_STAMP_WGS + blockIdx.x / ((gridDim.x + GEMV_STAMP_WGS - 1) / GEMV_STAMP_WGS)) * \
+                      GEMV_NSTAMP + (i)] = __builtin_amdgcn_s_memrealtime();
 #else
 #define CM_GEMV_STAMP(kind, i, t)
+#define CM_GEMV_STAMP_SAMPLED(kind, i, t)
 #endif
 
 constexpr int FS_CAP = 128;  // special steps the replay takes before falling back

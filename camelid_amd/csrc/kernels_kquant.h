@@ -139,7 +139,7 @@ __host__ __device__ inline size_t kq4_lds_bytes(int K, int R) {
   return kq4_terms_offset(K) + (size_t)R * (K / 256) * 16;
 }
 
-template <int IT, int RPW>
+template <int IT, int RPW, int NT = KQ_NT>
 __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __restrict__ nib, const uint8_t* __restrict__ hdr,
                                                     int rows, int K, const float* __restrict__ yd,
                                                     const int8_t* __restrict__ yq, const int32_t* __restrict__ ybs,
@@ -147,7 +147,8 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
                                                     uint32_t* __restrict__ part_i, const float* __restrict__ xf,
                                                     const uint32_t* ready = nullptr, int sk = -1) {
   (void)sk;  // (the measurement build's stamp kind)
-  constexpr int R = 4 * RPW;
+  constexpr int R = (NT / 64) * RPW;
+  static_assert(R <= 64, "one lane per row folds the terms");
   extern __shared__ __align__(16) unsigned char smem[];
   const int NSB = K >> 8, NC = K >> 5;
   int8_t* xq = reinterpret_cast<int8_t*>(smem);
@@ -173,18 +174,18 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
   }
   if (ready) {  // the activation published by workgroup 0 of this launch (agent-scope loads)
     handoff_wait(ready);
-    for (int c = tid; c < (K >> 3); c += KQ_NT) reinterpret_cast<uint64_t*>(xq)[c] = ld_agent64(yq + 8 * c);
-    for (int i = tid; i < NSB; i += KQ_NT) xd[i] = __uint_as_float(ld_agent32(yd + i));
-    for (int i = tid; i < NC; i += KQ_NT) xbs[i] = (int)ld_agent32(ybs + i);
+    for (int c = tid; c < (K >> 3); c += NT) reinterpret_cast<uint64_t*>(xq)[c] = ld_agent64(yq + 8 * c);
+    for (int i = tid; i < NSB; i += NT) xd[i] = __uint_as_float(ld_agent32(yd + i));
+    for (int i = tid; i < NC; i += NT) xbs[i] = (int)ld_agent32(ybs + i);
     if (sk >= 0) {
-      CM_GEMV_STAMP(sk, 3, 0)
+      CM_GEMV_STAMP_SAMPLED(sk, 3, 0)
     }
   } else if (xf) {  // the activation given in f32: each wave quantizes blocks wave, wave + 4, ... to Q8_K
-    for (int b = wave; b < NSB; b += KQ_NT / 64) quantize_q8k_wave(xf + 256 * b, xq + 256 * b, xbs + 8 * b, xd + b);
+    for (int b = wave; b < NSB; b += NT / 64) quantize_q8k_wave(xf + 256 * b, xq + 256 * b, xbs + 8 * b, xd + b);
   } else {
-    for (int c = tid; c < (K >> 4); c += KQ_NT) reinterpret_cast<int4*>(xq)[c] = reinterpret_cast<const int4*>(yq)[c];
-    for (int i = tid; i < NSB; i += KQ_NT) xd[i] = yd[i];
-    for (int i = tid; i < NC; i += KQ_NT) xbs[i] = ybs[i];
+    for (int c = tid; c < (K >> 4); c += NT) reinterpret_cast<int4*>(xq)[c] = reinterpret_cast<const int4*>(yq)[c];
+    for (int i = tid; i < NSB; i += NT) xd[i] = yd[i];
+    for (int i = tid; i < NC; i += NT) xbs[i] = ybs[i];
   }
   __syncthreads();
   const uint32_t K1 = 0x3f3f3f3fu, K2 = 0x0f0f0f0fu, K3 = 0x03030303u;
@@ -251,7 +252,7 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
     }
   }
   if (sk >= 0) {
-    CM_GEMV_STAMP(sk, 5, 0)
+    CM_GEMV_STAMP_SAMPLED(sk, 5, 0)
   }
 }
 
@@ -286,14 +287,15 @@ __host__ __device__ inline size_t kq6_lds_bytes(int K, int R) {
   return kq6_terms_offset(K) + (size_t)R * (K / 256) * 32;
 }
 
-template <int RPW>
+template <int RPW, int NT = KQ_NT>
 __device__ __forceinline__ void gemv_q6k_body(const int bid, const uint8_t* __restrict__ ql, const uint8_t* __restrict__ qh,
                                                     const int8_t* __restrict__ scl, const uint16_t* __restrict__ dw,
                                                     int rows, int K, const float* __restrict__ yd,
                                                     const int8_t* __restrict__ yq, float* y, const float* resid,
                                                     float* __restrict__ part_v, uint32_t* __restrict__ part_i,
                                                     const uint32_t* ready = nullptr) {
-  constexpr int R = 4 * RPW;
+  constexpr int R = (NT / 64) * RPW;
+  static_assert(R <= 8, "eight lanes per row run the class chains");
   extern __shared__ __align__(16) unsigned char smem[];
   const int NSB = K >> 8, NU = K >> 6;
   uint32_t* xp = reinterpret_cast<uint32_t*>(smem);  // [s][group j][class l] activation pairs
@@ -304,7 +306,7 @@ __device__ __forceinline__ void gemv_q6k_body(const int bid, const uint8_t* __re
   // activation pairs: entry (s, j, l) = bytes (q[16j+l], q[16j+8+l], q[16j+l], q[16j+8+l])
   // (published by workgroup 0 of this launch: agent-scope loads after the handoff)
   if (ready) handoff_wait(ready);
-  for (int e = tid; e < NSB * 128; e += KQ_NT) {
+  for (int e = tid; e < NSB * 128; e += NT) {
     const int l = e & 7, g = e >> 3;  // g = s * 16 + j
     const uint32_t* src = reinterpret_cast<const uint32_t*>(yq + (size_t)g * 16);
     const uint32_t a = ready ? ld_agent32(src + (l >> 2)) : src[l >> 2];
@@ -314,7 +316,7 @@ __device__ __forceinline__ void gemv_q6k_body(const int bid, const uint8_t* __re
     const uint32_t sel = bl | ((4 + bl) << 8) | (bl << 16) | ((4 + bl) << 24);
     xp[e] = __builtin_amdgcn_perm(b, a, sel);
   }
-  for (int i = tid; i < NSB; i += KQ_NT) xd[i] = ready ? __uint_as_float(ld_agent32(yd + i)) : yd[i];
+  for (int i = tid; i < NSB; i += NT) xd[i] = ready ? __uint_as_float(ld_agent32(yd + i)) : yd[i];
   __syncthreads();
   const uint32_t M4 = 0x0f0f0f0fu, M2 = 0x03030303u;
 #pragma unroll
@@ -426,22 +428,48 @@ __global__ __launch_bounds__(KQ_NT) void k_gemv_qk4_v6(const uint8_t* __restrict
 }
 
 // ---------------------------------------------------------------------------
-// Norm-fused K-quant decode GEMVs (hidden 4096 = 256 threads x 16 values).  Workgroup 0 of
+// Norm-fused K-quant decode GEMVs (hidden 4096 = 512 threads x 8 values).  Workgroup 0 of
 // the launch computes the layer's RMSNorm (tensor/mod.rs:2083-2106: the in-order sum of
 // squares, scale = 1/sqrt(ss/n + eps), y = (x * scale) * w) and its Q8_K quantization
 // (inference.rs:17564-17599, as k_rmsnorm_quant: the same operations, so the same bits) and
-// publishes the activation (see handoff_wait); the other workgroups run the GEMV bodies,
-// whose weight loads go out before they wait for it.  The RMSNorm launch of the unfused
-// layer and its dependency gap disappear; its latency overlaps the weight stream.
-constexpr int NQ_C = 16;  // values per thread of the norm workgroup
-__host__ __device__ inline size_t norm_q8k_lds_bytes(int n) { return (size_t)n * 4 + sizeof(FsLds<KQ_NT>); }
+// publishes the activation (see handoff_wait); the other workgroups run the GEMV bodies with
+// eight waves, whose weight loads go out before they wait for it.  The RMSNorm launch of the
+// unfused layer and its dependency gap disappear; its latency overlaps the weight stream.
+// Eight waves per workgroup (where the plain K-quant GEMVs run four): the norm workgroup's
+// eight values per thread keep the kernel within 64 VGPRs, so as many GEMV waves stay
+// resident as in the plain launches, and the one-pass sum is shorter at 512 threads.
+constexpr int NF_NT = 512;  // threads of a norm-fused launch's workgroups
+constexpr int NQ_C = 8;     // values per thread of the norm workgroup
+__host__ __device__ inline size_t norm_q8k_lds_bytes(int n) { return (size_t)n * 4 + sizeof(FsLds<NF_NT>); }
 
-// Thread t holds values 16t..16t+15 (the one-pass sum's layout); a Q8_K block is one row of 16
-// lanes (the (|max|, first index) pick by DPP within the row; block position 16 j + e).
-// smem: the n squares (the sum's fallback) + FsLds<256>.  n == 16 * 256.
-// (measurement build: stamps of workgroup 0 in g_gemv_stamps[kind][0]: 0 start, 6 x and w
-// loaded, 7 sum of squares, 1 published; of the other workgroups b < 256: 0 start, 3 flag
-// seen and activation staged, 5 end)
+// (|max|, first index) of each half wave (lanes 0-31, 32-63) in every lane of the half: the
+// row's pick by DPP (quads, then rotations by 4 and 8 within the row of 16), then the two rows'
+// picks from lanes 0/16 or 32/48.
+__device__ __forceinline__ void amax_pick_half_wave(float& a, int& i, float& v) {
+  amax_pick_quad(a, i, v);
+  amax_pick_dpp<0x124>(a, i, v);  // row_ror:4
+  amax_pick_dpp<0x128>(a, i, v);  // row_ror:8
+  float ra[4], rv[4];
+  int ri[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    ra[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 16 * r));
+    ri[r] = __builtin_amdgcn_readlane(i, 16 * r);
+    rv[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16 * r));
+  }
+  const bool hi = (threadIdx.x & 32) != 0;
+  a = hi ? ra[2] : ra[0];
+  i = hi ? ri[2] : ri[0];
+  v = hi ? rv[2] : rv[0];
+  amax_pick(a, i, v, hi ? ra[3] : ra[1], hi ? ri[3] : ri[1], hi ? rv[3] : rv[1]);
+}
+
+// Thread t holds values 8t..8t+7 (the one-pass sum's layout); a Q8_K block is one half wave
+// (block position 8 l + e for lane l of the half).  smem: the n squares (the sum's fallback)
+// + FsLds<512>.  n == 8 * 512.
+// (measurement build: stamps of workgroup 0 in g_gemv_stamps[kind][0]: 0 start, 6 squares
+// stored, 7 sum of squares, 1 published; of a sample of the other workgroups (every
+// ceil(grid / 256)-th): 0 start, 3 flag seen and activation staged, 5 end)
 __device__ __forceinline__ void norm_q8k_publish(const float* __restrict__ x, const float* __restrict__ w, int n,
                                                  float eps, float* __restrict__ kd, int8_t* __restrict__ kq,
                                                  int32_t* __restrict__ kbs, uint32_t* slot_set,
@@ -449,9 +477,9 @@ __device__ __forceinline__ void norm_q8k_publish(const float* __restrict__ x, co
   (void)kind;
   constexpr int C = NQ_C;
   CM_GEMV_STAMP(kind, 0, 0)
-  const int tid = threadIdx.x, j = tid & 15;
+  const int tid = threadIdx.x, l = tid & 31;
   float* sq = reinterpret_cast<float*>(smem);
-  FsLds<KQ_NT>& fs = *reinterpret_cast<FsLds<KQ_NT>*>(smem + (size_t)n * 4);
+  FsLds<NF_NT>& fs = *reinterpret_cast<FsLds<NF_NT>*>(smem + (size_t)n * 4);
   if (tid == 0) {  // the other kind's slot: its launch has completed
 #pragma unroll
     for (int c = 0; c < NF_XCD; ++c) st_agent32(slot_reset + c * NF_STRIDE, 0u);
@@ -469,7 +497,7 @@ __device__ __forceinline__ void norm_q8k_publish(const float* __restrict__ x, co
     reinterpret_cast<float4*>(sq + tid * C)[u] = make_float4(tv[4 * u], tv[4 * u + 1], tv[4 * u + 2], tv[4 * u + 3]);
   CM_GEMV_STAMP(kind, 6, 0)
   __syncthreads();
-  const float ss = inorder_sum_onepass<KQ_NT, C>(tv, sq, n, fs);
+  const float ss = inorder_sum_onepass<NF_NT, C>(tv, sq, n, fs, WgBar{}, kind);
   CM_GEMV_STAMP(kind, 7, 0)
   const float scale = 1.0f / sqrtf(ss / (float)n + eps);
   float y[C];
@@ -489,11 +517,9 @@ __device__ __forceinline__ void norm_q8k_publish(const float* __restrict__ x, co
     if (fabsf(y[e]) > a) {
       a = fabsf(y[e]);
       v = y[e];
-      idx = C * j + e;
+      idx = C * l + e;
     }
-  amax_pick_quad(a, idx, v);
-  amax_pick_dpp<0x124>(a, idx, v);  // row_ror:4
-  amax_pick_dpp<0x128>(a, idx, v);  // row_ror:8: every lane of the row holds the block's pick
+  amax_pick_half_wave(a, idx, v);
   const float iscale = a > 0.0f ? -127.0f / v : 0.0f;
   uint32_t words[C / 4];
   int sum = 0;
@@ -508,12 +534,11 @@ __device__ __forceinline__ void norm_q8k_publish(const float* __restrict__ x, co
     }
     words[w4] = word;
   }
-  // lanes 2m and 2m + 1 hold values 32m..32m+31 of the block: the per-32 sum
-  const int s2 = sum + __builtin_amdgcn_update_dpp(0, sum, 0xB1, 0xf, 0xf, false);
+  // the lanes of a quad hold 32 consecutive values: the per-32 sum
+  const int s4 = quad_sum(sum);
   st_agent64(kq + tid * C, (uint64_t)words[0] | ((uint64_t)words[1] << 32));
-  st_agent64(kq + tid * C + 8, (uint64_t)words[2] | ((uint64_t)words[3] << 32));
-  if ((tid & 1) == 0) st_agent32(kbs + (tid >> 1), (uint32_t)s2);
-  if (j == 0) st_agent32(kd + (tid >> 4), __float_as_uint(a > 0.0f ? 1.0f / iscale : 0.0f));
+  if ((tid & 3) == 0) st_agent32(kbs + (tid >> 2), (uint32_t)s4);
+  if (l == 0) st_agent32(kd + (tid >> 5), __float_as_uint(a > 0.0f ? 1.0f / iscale : 0.0f));
   __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
   __syncthreads();
   if (tid == 0) {
@@ -523,11 +548,11 @@ __device__ __forceinline__ void norm_q8k_publish(const float* __restrict__ x, co
   CM_GEMV_STAMP(kind, 1, 0)
 }
 
-// q|k (Q4_K) + v (Q6_K) with the attention RMSNorm: grid 1 + g4 + g6 (k_gemv_qk4_v6's
-// workgroups after the norm workgroup); slot `kind` of the flag words (slots: 2 x NF_XCD x
-// NF_STRIDE words).
+// q|k (Q4_K) + v (Q6_K) with the attention RMSNorm: grid 1 + g4 + g6 (eight rows per
+// workgroup, one per wave, as k_gemv_qk4_v6's workgroups with twice the waves) after the norm
+// workgroup; slot `kind` of the flag words (slots: 2 x NF_XCD x NF_STRIDE words).
 template <int IT>
-__global__ __launch_bounds__(KQ_NT) void k_norm_qk4_v6(const float* __restrict__ x, const float* __restrict__ nw,
+__global__ __launch_bounds__(NF_NT, 8) void k_norm_qk4_v6(const float* __restrict__ x, const float* __restrict__ nw,
                                                        float eps, uint32_t* slots, int kind, float* __restrict__ kd,
                                                        int8_t* __restrict__ kq, int32_t* __restrict__ kbs,
                                                        const uint8_t* __restrict__ nib, const uint8_t* __restrict__ hdr,
@@ -540,17 +565,19 @@ __global__ __launch_bounds__(KQ_NT) void k_norm_qk4_v6(const float* __restrict__
     norm_q8k_publish(x, nw, K, eps, kd, kq, kbs, mine, slots + (1 - kind) * NF_XCD * NF_STRIDE, smem, kind);
     return;
   }
-  CM_GEMV_STAMP(kind, 0, 0)
+  CM_GEMV_STAMP_SAMPLED(kind, 0, 0)
   const int b = (int)blockIdx.x - 1;
   if (b < g4)
-    gemv_q4k_body<IT, 1>(b, nib, hdr, rows4, K, kd, kq, kbs, y4, nullptr, nullptr, nullptr, nullptr, mine, kind);
+    gemv_q4k_body<IT, 1, NF_NT>(b, nib, hdr, rows4, K, kd, kq, kbs, y4, nullptr, nullptr, nullptr, nullptr, mine,
+                                kind);
   else
-    gemv_q6k_body<1>(b - g4, ql, qh, scl, dw, rows6, K, kd, kq, y6, nullptr, nullptr, nullptr, mine);
+    gemv_q6k_body<1, NF_NT>(b - g4, ql, qh, scl, dw, rows6, K, kd, kq, y6, nullptr, nullptr, nullptr, mine);
 }
 
-// A Q4_K projection (gate|up stacked) with the FFN RMSNorm: grid 1 + the GEMV's workgroups.
+// A Q4_K projection (gate|up stacked) with the FFN RMSNorm: grid 1 + the GEMV's workgroups
+// (8 RPW rows each).
 template <int IT, int RPW>
-__global__ __launch_bounds__(KQ_NT) void k_norm_gemv_q4k(const float* __restrict__ x, const float* __restrict__ nw,
+__global__ __launch_bounds__(NF_NT, 8) void k_norm_gemv_q4k(const float* __restrict__ x, const float* __restrict__ nw,
                                                          float eps, uint32_t* slots, int kind, float* __restrict__ kd,
                                                          int8_t* __restrict__ kq, int32_t* __restrict__ kbs,
                                                          const uint8_t* __restrict__ nib,
@@ -561,9 +588,9 @@ __global__ __launch_bounds__(KQ_NT) void k_norm_gemv_q4k(const float* __restrict
     norm_q8k_publish(x, nw, K, eps, kd, kq, kbs, mine, slots + (1 - kind) * NF_XCD * NF_STRIDE, smem, kind);
     return;
   }
-  CM_GEMV_STAMP(kind, 0, 0)
-  gemv_q4k_body<IT, RPW>((int)blockIdx.x - 1, nib, hdr, rows, K, kd, kq, kbs, y, nullptr, nullptr, nullptr, nullptr,
-                         mine, kind);
+  CM_GEMV_STAMP_SAMPLED(kind, 0, 0)
+  gemv_q4k_body<IT, RPW, NF_NT>((int)blockIdx.x - 1, nib, hdr, rows, K, kd, kq, kbs, y, nullptr, nullptr, nullptr,
+                                nullptr, mine, kind);
 }
 
 // ---------------------------------------------------------------------------
