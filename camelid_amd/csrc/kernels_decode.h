@@ -768,6 +768,16 @@ __device__ __forceinline__ float max_wave(float a) {
   const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 48));
   return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
+// unsigned minimum over each aligned 32-lane half, in every lane of the half
+__device__ __forceinline__ uint32_t min_half_wave(uint32_t v) {
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0xB1, 0xf, 0xf, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x4E, 0xf, 0xf, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x124, 0xf, 0xf, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x128, 0xf, 0xf, false));
+  const uint32_t lo = min((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
+  const uint32_t hi = min((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+  return (threadIdx.x & 32) ? hi : lo;
+}
 // integer sum over each aligned 32-lane half, in every lane of the half (exact)
 __device__ __forceinline__ int sum_half_wave(int v) {
   v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);

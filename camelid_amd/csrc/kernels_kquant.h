@@ -287,13 +287,14 @@ __host__ __device__ inline size_t kq6_lds_bytes(int K, int R) {
   return kq6_terms_offset(K) + (size_t)R * (K / 256) * 32;
 }
 
-template <int RPW, int NT = KQ_NT>
+template <int RPW, int NT = KQ_NT, bool PRE = false>
 __device__ __forceinline__ void gemv_q6k_body(const int bid, const uint8_t* __restrict__ ql, const uint8_t* __restrict__ qh,
                                                     const int8_t* __restrict__ scl, const uint16_t* __restrict__ dw,
                                                     int rows, int K, const float* __restrict__ yd,
                                                     const int8_t* __restrict__ yq, float* y, const float* resid,
                                                     float* __restrict__ part_v, uint32_t* __restrict__ part_i,
-                                                    const uint32_t* ready = nullptr) {
+                                                    const uint32_t* ready = nullptr, int sk = -1) {
+  (void)sk;  // (the measurement build's stamp kind)
   constexpr int R = (NT / 64) * RPW;
   static_assert(R <= 8, "eight lanes per row run the class chains");
   extern __shared__ __align__(16) unsigned char smem[];
@@ -303,6 +304,28 @@ __device__ __forceinline__ void gemv_q6k_body(const int bid, const uint8_t* __re
   float* terms = reinterpret_cast<float*>(smem + kq6_terms_offset(K));  // [row][s][l]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int row0 = bid * R;
+  // the weight pieces of one lane work unit (row rl of this workgroup, unit u0 + lane)
+  struct Unit6 {
+    uint4 l0, l1, hh, sc;
+    uint32_t d;  // the superblock's f16 scale bits
+  };
+  auto load_unit = [&](int rl, int u0) {
+    const int row = min(row0 + rl, rows - 1);
+    const int uu = min(u0 + lane, NU - 1);
+    const int s = uu >> 2, n = (uu >> 1) & 1, q0 = (uu & 1) * 16;
+    const uint8_t* qlr = ql + (size_t)row * (K >> 1);
+    Unit6 w;
+    w.l0 = ld_stream(reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + q0));
+    w.l1 = ld_stream(reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + 32 + q0));
+    w.hh = ld_stream(reinterpret_cast<const uint4*>(qh + (size_t)row * (K >> 2) + s * 64 + n * 32 + q0));
+    w.sc = ld_stream(reinterpret_cast<const uint4*>(scl + ((size_t)row * NSB + s) * 16));
+    w.d = dw[(size_t)row * NSB + s];
+    return w;
+  };
+  // PRE (the norm-fused launch): the first unit's loads go out before the wait for the
+  // activation (16 more registers live across it, which the plain launches do not spend)
+  Unit6 first;
+  if (PRE) first = load_unit(wave * RPW, 0);
   // activation pairs: entry (s, j, l) = bytes (q[16j+l], q[16j+8+l], q[16j+l], q[16j+8+l])
   // (published by workgroup 0 of this launch: agent-scope loads after the handoff)
   if (ready) handoff_wait(ready);
@@ -317,60 +340,58 @@ __device__ __forceinline__ void gemv_q6k_body(const int bid, const uint8_t* __re
     xp[e] = __builtin_amdgcn_perm(b, a, sel);
   }
   for (int i = tid; i < NSB; i += NT) xd[i] = ready ? __uint_as_float(ld_agent32(yd + i)) : yd[i];
+  if (sk >= 0) {
+    CM_GEMV_STAMP_SAMPLED(sk, 3, 0)
+  }
   __syncthreads();
   const uint32_t M4 = 0x0f0f0f0fu, M2 = 0x03030303u;
+  auto unit = [&](int rl, int u0, const Unit6& w) {
+    const int u = u0 + lane;
+    const bool valid = u < NU;  // uniform per 4-lane superblock group (NU % 4 == 0)
+    const int uu = min(u, NU - 1);
+    const int s = uu >> 2, n = (uu >> 1) & 1, q0 = (uu & 1) * 16;
+    const uint32_t L0[4] = {w.l0.x, w.l0.y, w.l0.z, w.l0.w}, L1[4] = {w.l1.x, w.l1.y, w.l1.z, w.l1.w};
+    const uint32_t HH[4] = {w.hh.x, w.hh.y, w.hh.z, w.hh.w};
+    int aux[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int j = n * 8 + (q0 >> 4) + 2 * kk;  // the group's index (scale index)
+      // scale word j / 4 = 2n + kk / 2 (a select, not an indexed register array)
+      const uint32_t scw = n ? (kk < 2 ? w.sc.z : w.sc.w) : (kk < 2 ? w.sc.x : w.sc.y);
+      const int sc = (int)(int8_t)((scw >> (8 * (j & 3))) & 0xff);
+      uint32_t v[4];
+#pragma unroll
+      for (int t4 = 0; t4 < 4; ++t4) {
+        const uint32_t lq = (kk & 1) ? L1[t4] : L0[t4];
+        const uint32_t lo = (kk < 2) ? (lq & M4) : ((lq >> 4) & M4);
+        v[t4] = lo | (((HH[t4] >> (2 * kk)) & M2) << 4);
+      }
+      const uint32_t* xg = xp + (size_t)(s * 16 + j) * 8;
+#pragma unroll
+      for (int l = 0; l < 8; ++l) {
+        const uint32_t bl = l & 3;
+        const uint32_t a = v[l >> 2], b = v[(l >> 2) + 2];
+        const uint32_t wpair = __builtin_amdgcn_perm(b, a, bl | ((4 + bl) << 8) | (0x0c << 16) | (0x0cu << 24)) |
+                               0xe0e00000u;
+        aux[l] += sc * __builtin_amdgcn_sdot4((int)wpair, (int)xg[l], 0, false);
+      }
+    }
+#pragma unroll
+    for (int l = 0; l < 8; ++l) aux[l] = quad_sum(aux[l]);
+    if (valid && (uu & 3) == 0) {
+      const float d = half_bits_to_float((uint16_t)w.d) * xd[s];
+      float* tp = terms + ((size_t)rl * NSB + s) * 8;
+      *reinterpret_cast<float4*>(tp) = make_float4(d * (float)aux[0], d * (float)aux[1], d * (float)aux[2],
+                                                   d * (float)aux[3]);
+      *reinterpret_cast<float4*>(tp + 4) = make_float4(d * (float)aux[4], d * (float)aux[5], d * (float)aux[6],
+                                                       d * (float)aux[7]);
+    }
+  };
 #pragma unroll
   for (int k = 0; k < RPW; ++k) {
     const int rl = wave * RPW + k;
-    const int row = min(row0 + rl, rows - 1);
-    const uint8_t* qlr = ql + (size_t)row * (K >> 1);
-    const uint8_t* qhr = qh + (size_t)row * (K >> 2);
-    const int8_t* scr = scl + (size_t)row * NSB * 16;
-    for (int u0 = 0; u0 < NU; u0 += 64) {
-      const int u = u0 + lane;
-      const bool valid = u < NU;  // uniform per 4-lane superblock group (NU % 4 == 0)
-      const int uu = min(u, NU - 1);
-      const int s = uu >> 2, n = (uu >> 1) & 1, q0 = (uu & 1) * 16;
-      const uint4 l0 = ld_stream(reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + q0));
-      const uint4 l1 = ld_stream(reinterpret_cast<const uint4*>(qlr + s * 128 + n * 64 + 32 + q0));
-      const uint4 hh = ld_stream(reinterpret_cast<const uint4*>(qhr + s * 64 + n * 32 + q0));
-      const uint4 scv = ld_stream(reinterpret_cast<const uint4*>(scr + s * 16));
-      const uint32_t L0[4] = {l0.x, l0.y, l0.z, l0.w}, L1[4] = {l1.x, l1.y, l1.z, l1.w};
-      const uint32_t HH[4] = {hh.x, hh.y, hh.z, hh.w};
-      const uint32_t SC[4] = {scv.x, scv.y, scv.z, scv.w};
-      int aux[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int j = n * 8 + (q0 >> 4) + 2 * kk;  // the group's index (scale index)
-        const int sc = (int)(int8_t)((SC[j >> 2] >> (8 * (j & 3))) & 0xff);
-        uint32_t v[4];
-#pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4) {
-          const uint32_t lq = (kk & 1) ? L1[t4] : L0[t4];
-          const uint32_t lo = (kk < 2) ? (lq & M4) : ((lq >> 4) & M4);
-          v[t4] = lo | (((HH[t4] >> (2 * kk)) & M2) << 4);
-        }
-        const uint32_t* xg = xp + (size_t)(s * 16 + j) * 8;
-#pragma unroll
-        for (int l = 0; l < 8; ++l) {
-          const uint32_t bl = l & 3;
-          const uint32_t a = v[l >> 2], b = v[(l >> 2) + 2];
-          const uint32_t wpair = __builtin_amdgcn_perm(b, a, bl | ((4 + bl) << 8) | (0x0c << 16) | (0x0cu << 24)) |
-                                 0xe0e00000u;
-          aux[l] += sc * __builtin_amdgcn_sdot4((int)wpair, (int)xg[l], 0, false);
-        }
-      }
-#pragma unroll
-      for (int l = 0; l < 8; ++l) aux[l] = quad_sum(aux[l]);
-      if (valid && (uu & 3) == 0) {
-        const float d = half_bits_to_float(dw[(size_t)row * NSB + s]) * xd[s];
-        float* tp = terms + ((size_t)rl * NSB + s) * 8;
-        *reinterpret_cast<float4*>(tp) = make_float4(d * (float)aux[0], d * (float)aux[1], d * (float)aux[2],
-                                                     d * (float)aux[3]);
-        *reinterpret_cast<float4*>(tp + 4) = make_float4(d * (float)aux[4], d * (float)aux[5], d * (float)aux[6],
-                                                         d * (float)aux[7]);
-      }
-    }
+    if (PRE && k == 0) unit(rl, 0, first);
+    for (int u0 = PRE && k == 0 ? 64 : 0; u0 < NU; u0 += 64) unit(rl, u0, load_unit(rl, u0));
   }
   __syncthreads();
   if (tid < 64) {
@@ -396,6 +417,9 @@ __device__ __forceinline__ void gemv_q6k_body(const int bid, const uint8_t* __re
         part_i[bid] = bi;
       }
     }
+  }
+  if (sk >= 0) {
+    CM_GEMV_STAMP_SAMPLED(sk, 5, 0)
   }
 }
 
@@ -442,33 +466,11 @@ constexpr int NF_NT = 512;  // threads of a norm-fused launch's workgroups
 constexpr int NQ_C = 8;     // values per thread of the norm workgroup
 __host__ __device__ inline size_t norm_q8k_lds_bytes(int n) { return (size_t)n * 4 + sizeof(FsLds<NF_NT>); }
 
-// (|max|, first index) of each half wave (lanes 0-31, 32-63) in every lane of the half: the
-// row's pick by DPP (quads, then rotations by 4 and 8 within the row of 16), then the two rows'
-// picks from lanes 0/16 or 32/48.
-__device__ __forceinline__ void amax_pick_half_wave(float& a, int& i, float& v) {
-  amax_pick_quad(a, i, v);
-  amax_pick_dpp<0x124>(a, i, v);  // row_ror:4
-  amax_pick_dpp<0x128>(a, i, v);  // row_ror:8
-  float ra[4], rv[4];
-  int ri[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    ra[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 16 * r));
-    ri[r] = __builtin_amdgcn_readlane(i, 16 * r);
-    rv[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16 * r));
-  }
-  const bool hi = (threadIdx.x & 32) != 0;
-  a = hi ? ra[2] : ra[0];
-  i = hi ? ri[2] : ri[0];
-  v = hi ? rv[2] : rv[0];
-  amax_pick(a, i, v, hi ? ra[3] : ra[1], hi ? ri[3] : ri[1], hi ? rv[3] : rv[1]);
-}
-
 // Thread t holds values 8t..8t+7 (the one-pass sum's layout); a Q8_K block is one half wave
 // (block position 8 l + e for lane l of the half).  smem: the n squares (the sum's fallback)
 // + FsLds<512>.  n == 8 * 512.
 // (measurement build: stamps of workgroup 0 in g_gemv_stamps[kind][0]: 0 start, 6 squares
-// stored, 7 sum of squares, 1 published; of a sample of the other workgroups (every
+// stored, 7 sum of squares, 2 y, 3 block maxima, 4 quants, 5 stores completed, 1 published; of a sample of the other workgroups (every
 // ceil(grid / 256)-th): 0 start, 3 flag seen and activation staged, 5 end)
 __device__ __forceinline__ void norm_q8k_publish(const float* __restrict__ x, const float* __restrict__ w, int n,
                                                  float eps, float* __restrict__ kd, int8_t* __restrict__ kq,
@@ -510,16 +512,20 @@ __device__ __forceinline__ void norm_q8k_publish(const float* __restrict__ x, co
     y[4 * u + 2] = (a.z * scale) * b.z;
     y[4 * u + 3] = (a.w * scale) * b.w;
   }
-  float a = 0.0f, v = 0.0f;
-  int idx = 0x7fffffff;
+  CM_GEMV_STAMP(kind, 2, 0)
+  // the block's (|max|, first index) pick needs only |max| and the sign of its first
+  // occurrence: a max, then a min over (index << 1 | sign) of the lanes holding |max|
+  float a = 0.0f;
 #pragma unroll
-  for (int e = 0; e < C; ++e)
-    if (fabsf(y[e]) > a) {
-      a = fabsf(y[e]);
-      v = y[e];
-      idx = C * l + e;
-    }
-  amax_pick_half_wave(a, idx, v);
+  for (int e = 0; e < C; ++e) a = fabsf(y[e]) > a ? fabsf(y[e]) : a;
+  a = max_half_wave(a);
+  uint32_t key = 0xffffffffu;
+#pragma unroll
+  for (int e = C - 1; e >= 0; --e)
+    key = fabsf(y[e]) == a ? ((uint32_t)(C * l + e) << 1) | (__float_as_uint(y[e]) >> 31) : key;
+  key = min_half_wave(key);
+  const float v = (key & 1u) ? -a : a;  // y at the first index of the maximum (a > 0)
+  CM_GEMV_STAMP(kind, 3, 0)
   const float iscale = a > 0.0f ? -127.0f / v : 0.0f;
   uint32_t words[C / 4];
   int sum = 0;
@@ -536,10 +542,12 @@ __device__ __forceinline__ void norm_q8k_publish(const float* __restrict__ x, co
   }
   // the lanes of a quad hold 32 consecutive values: the per-32 sum
   const int s4 = quad_sum(sum);
+  CM_GEMV_STAMP(kind, 4, 0)
   st_agent64(kq + tid * C, (uint64_t)words[0] | ((uint64_t)words[1] << 32));
   if ((tid & 3) == 0) st_agent32(kbs + (tid >> 2), (uint32_t)s4);
   if (l == 0) st_agent32(kd + (tid >> 5), __float_as_uint(a > 0.0f ? 1.0f / iscale : 0.0f));
   __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
+  CM_GEMV_STAMP(kind, 5, 0)
   __syncthreads();
   if (tid == 0) {
 #pragma unroll
@@ -571,7 +579,8 @@ __global__ __launch_bounds__(NF_NT, 8) void k_norm_qk4_v6(const float* __restric
     gemv_q4k_body<IT, 1, NF_NT>(b, nib, hdr, rows4, K, kd, kq, kbs, y4, nullptr, nullptr, nullptr, nullptr, mine,
                                 kind);
   else
-    gemv_q6k_body<1, NF_NT>(b - g4, ql, qh, scl, dw, rows6, K, kd, kq, y6, nullptr, nullptr, nullptr, mine);
+    gemv_q6k_body<1, NF_NT, true>(b - g4, ql, qh, scl, dw, rows6, K, kd, kq, y6, nullptr, nullptr, nullptr, mine,
+                                  kind);
 }
 
 // A Q4_K projection (gate|up stacked) with the FFN RMSNorm: grid 1 + the GEMV's workgroups
