@@ -640,14 +640,19 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
     sh_end[1] = lo;
     sh_end[2] = lim;
   }
+  if (tid < 3) {  // the entries padded to a multiple of 4 with steps that change nothing
+    const uint32_t p = total + (uint32_t)tid;
+    if (p < ((total + 3u) & ~3u) && p < (uint32_t)FS_CAP) sh_ent[p] = make_uint4(0u, 0u, 0xffffffffu, 0u);
+  }
   bar();
   if (stamp_kind >= 0) {
     CM_GEMV_STAMP(stamp_kind, 10, 0)
   }
   if (wave == 0) {
-    // replay, branch-free per step: the sum's chain is one integer and one f32 add.  Every lane
-    // of wave 0 runs the same chain on the same entries (broadcast LDS reads, 8 entries read
-    // ahead of the chain)
+    // replay: the sum's chain is one integer and one f32 add per special step.  Every lane
+    // of wave 0 runs the same chain on the same entries: broadcast LDS reads of 4 entries, the
+    // next 4 read while these are applied (two register sets, no moves; no step is skipped:
+    // the padding steps add 0 ulps and +0.0, which leave a sum >= +0 unchanged)
     const int tot = __builtin_amdgcn_readfirstlane((int)total);
 #ifdef CM_STAMPS
     if (stamp_kind >= 0 && threadIdx.x == 0 && blockIdx.x < GEMV_STAMP_WGS)  // (a count, not a time)
@@ -661,22 +666,26 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
         bad |= (uint32_t)!(sb - q.y < q.z);
         s = __uint_as_float(sb + q.x) + __uint_as_float(q.w);
       };
-      const int nb8 = (tot + 7) >> 3;
-      uint4 x[8], y[8];
+      const int nb = (tot + 3) >> 2;  // blocks of 4 entries (nb <= FS_CAP / 4)
+      uint4 A[4], B[4];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) x[u] = sh_ent[u];
-      for (int k = 0; k < nb8; ++k) {
-        if (k + 1 < nb8) {
+      for (int u = 0; u < 4; ++u) A[u] = sh_ent[u];
+      for (int k = 0; k < nb; k += 2) {
+        if (k + 1 < nb) {
 #pragma unroll
-          for (int u = 0; u < 8; ++u) y[u] = sh_ent[min(8 * (k + 1) + u, FS_CAP - 1)];
+          for (int u = 0; u < 4; ++u) B[u] = sh_ent[4 * (k + 1) + u];
         }
         __builtin_amdgcn_sched_barrier(0);
-        const int m = min(8, tot - 8 * k);
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (u < m) step(x[u]);
+        for (int u = 0; u < 4; ++u) step(A[u]);
+        if (k + 1 >= nb) break;
+        if (k + 2 < nb) {
 #pragma unroll
-        for (int u = 0; u < 8; ++u) x[u] = y[u];
+          for (int u = 0; u < 4; ++u) A[u] = sh_ent[4 * (k + 2) + u];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) step(B[u]);
       }
     }
     {

@@ -387,11 +387,15 @@ __device__ __forceinline__ void gemv_q6k_body(const int bid, const uint8_t* __re
                                                        d * (float)aux[7]);
     }
   };
+  if constexpr (PRE) {  // (one unit per lane: K <= 4096, as the norm-fused launch's callers check)
+    static_assert(RPW == 1, "the preloaded unit is the wave's only one");
+    unit(wave, 0, first);
+  } else {
 #pragma unroll
-  for (int k = 0; k < RPW; ++k) {
-    const int rl = wave * RPW + k;
-    if (PRE && k == 0) unit(rl, 0, first);
-    for (int u0 = PRE && k == 0 ? 64 : 0; u0 < NU; u0 += 64) unit(rl, u0, load_unit(rl, u0));
+    for (int k = 0; k < RPW; ++k) {
+      const int rl = wave * RPW + k;
+      for (int u0 = 0; u0 < NU; u0 += 64) unit(rl, u0, load_unit(rl, u0));
+    }
   }
   __syncthreads();
   if (tid < 64) {
