@@ -117,8 +117,13 @@ struct camelid_hip_engine {
   float* att_sc = nullptr;
   float* att_mx = nullptr;
   int att_mode = -1;       // -1: by position; 0 / 1: single / split (graph capture)
-  bool read_ahead = true;  // spare workgroups of the norm kernels read ahead the next weights
-  bool kv_ahead = true;    // the qkv GEMV's idle norm waves read the layer's KV rows into L2
+  // Read-ahead (off by default): spare workgroups of the norm and attention kernels read the
+  // next projection's weights towards the caches; the qkv GEMV's idle norm waves read the
+  // layer's KV rows.  Measured on the three big configs with the current kernels: no gain
+  // (C3 663.5 -> 664.8, C4 213.0 -> 214.2, C5 355.7 -> 359.7 tok/s with it off), and the
+  // counters show attention fetching its K/V rows again either way, so it is opt-in.
+  bool read_ahead = false;
+  bool kv_ahead = false;
   bool gu_fused = false;   // gate/up rows interleaved by 32, SwiGLU fused into their GEMV
   bool norm_fused = true;  // RMSNorms computed inside the qkv and gate/up GEMVs (Q8_0 layers)
   bool qkv_merged = true;  // Q4_K q|k and Q6_K v projections in one launch (k_gemv_qk4_v6)

@@ -8,9 +8,10 @@ replayed HIP graph per token, on-device embedding gather and argmax).  Mirrors t
 CPU<->GPU stream parity (tests/cuda_cpu_parity.rs:32-62) and full-forward parity at real dims
 (src/cuda_resident/tests.rs:354).
 
-Also here: the engine's documented switches (CAMELID_HIP_FUSED_GU, _FUSED_NORM, _READ_AHEAD,
-_GRAPHS, _KV_AHEAD, _QKV_MERGED, _KQ_NORM_FUSED) each switched off against the same golden / oracle, and greedy ties
-(duplicated lm_head rows) through the product argmax paths.
+Also here: the engine's documented switches (CAMELID_HIP_FUSED_GU, _FUSED_NORM, _GRAPHS,
+_QKV_MERGED, _KQ_NORM_FUSED switched off; the opt-in _READ_AHEAD, _KV_AHEAD switched on) each
+against the same golden / oracle, and greedy ties (duplicated lm_head rows) through the
+product argmax paths.
 """
 import importlib.util
 import json
@@ -72,24 +73,26 @@ def test_config_stream_matches_golden(name):
     assert toks == g["tokens"], f"{name}: first differing step {first_bad} of {g['decode_len']}"
 
 
-@pytest.mark.parametrize("switch", ["CAMELID_HIP_FUSED_GU", "CAMELID_HIP_FUSED_NORM", "CAMELID_HIP_READ_AHEAD",
-                                    "CAMELID_HIP_GRAPHS", "CAMELID_HIP_KV_AHEAD"])
-def test_switch_off_keeps_tinyllama_stream(monkeypatch, switch):
-    """Each documented switch of the Q8_0 decode path set to 0 (the separate RMSNorm launch,
-    the separate SwiGLU launch, no weight read-ahead, launches without a graph, no KV read into
-    L2 by the qkv launch): the TinyLlama golden stream (configs[0], 128 + 128) is still
-    reproduced by the device loop."""
-    monkeypatch.setenv(switch, "0")
+@pytest.mark.parametrize("switch,value", [("CAMELID_HIP_FUSED_GU", "0"), ("CAMELID_HIP_FUSED_NORM", "0"),
+                                          ("CAMELID_HIP_READ_AHEAD", "1"), ("CAMELID_HIP_GRAPHS", "0"),
+                                          ("CAMELID_HIP_KV_AHEAD", "1")])
+def test_switch_off_keeps_tinyllama_stream(monkeypatch, switch, value):
+    """Each documented switch of the Q8_0 decode path set away from its default (the separate
+    RMSNorm launch, the separate SwiGLU launch, the weight read-ahead workgroups, launches
+    without a graph, the KV rows read by the qkv launch's idle waves): the TinyLlama golden
+    stream (configs[0], 128 + 128) is still reproduced by the device loop."""
+    monkeypatch.setenv(switch, value)
     test_config_stream_matches_golden("tinyllama-1.1b")
 
 
 def test_switch_off_qkv_merged_kquant_matches_oracle(monkeypatch):
-    """At the C5 layer shape (hidden 4096, 32/8 heads of 128, ffn 12288, Q4_K_M), three K-quant
+    """At the C5 layer shape (hidden 4096, 32/8 heads of 128, ffn 12288, Q4_K_M), four K-quant
     decode layouts: the default (each RMSNorm inside the q|k+v and gate|up launches, whose other
     workgroups wait for it), CAMELID_HIP_KQ_NORM_FUSED=0 (a separate RMSNorm + Q8_K launch before
-    the merged q|k+v launch and the gate|up launch) and CAMELID_HIP_QKV_MERGED=0 (separate Q4_K
-    q|k and Q6_K v launches, which also leaves the norm unfused): per-layer hidden states, logits
-    and tokens of each are bit-identical to the CPU oracle."""
+    the merged q|k+v launch and the gate|up launch), CAMELID_HIP_QKV_MERGED=0 (separate Q4_K
+    q|k and Q6_K v launches, which also leaves the norm unfused) and the unfused layout with
+    CAMELID_HIP_READ_AHEAD=1 (the norm launches' spare workgroups read the next weights ahead):
+    per-layer hidden states, logits and tokens of each are bit-identical to the CPU oracle."""
     from oracle.oracle import OracleModel
     cfg = tiny_config(n_layers=2, hidden=4096, ffn_dim=12288, n_heads=32, n_kv_heads=8, head_dim=128, vocab=2048,
                       qk_norm=True, split_half=True, rope_theta=1e6, quant_scheme="q4_k_m", prompt_len=12)
@@ -103,9 +106,10 @@ def test_switch_off_qkv_merged_kquant_matches_oracle(monkeypatch):
         tok, hid, lg = orc.forward(tok, pos, hidden=True, logits=True)
         want.append((tok, hid, lg))
         pos += 1
-    for merged, fused in (("1", "1"), ("1", "0"), ("0", "1")):
+    for merged, fused, ahead in (("1", "1", "0"), ("1", "0", "0"), ("0", "1", "0"), ("1", "0", "1")):
         monkeypatch.setenv("CAMELID_HIP_QKV_MERGED", merged)
         monkeypatch.setenv("CAMELID_HIP_KQ_NORM_FUSED", fused)
+        monkeypatch.setenv("CAMELID_HIP_READ_AHEAD", ahead)
         sess = ResidentSession(model, 32)
         sess.engine.capture_hidden(True)
         sess.prefill(prompt[:-1])
@@ -113,8 +117,9 @@ def test_switch_off_qkv_merged_kquant_matches_oracle(monkeypatch):
         for step, (t_o, hid_o, lg_o) in enumerate(want):
             tok = sess.step(tok, pos, logits=True)
             hid = sess.engine.read_hidden()
-            assert np.array_equal(hid.view(np.uint32), hid_o.view(np.uint32)), (merged, fused, step)
-            assert np.array_equal(sess.engine.last_logits.view(np.uint32), lg_o.view(np.uint32)), (merged, fused, step)
+            assert np.array_equal(hid.view(np.uint32), hid_o.view(np.uint32)), (merged, fused, ahead, step)
+            assert np.array_equal(sess.engine.last_logits.view(np.uint32), lg_o.view(np.uint32)), (
+                merged, fused, ahead, step)
             assert tok == t_o
             pos += 1
         sess.close()
