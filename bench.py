@@ -41,7 +41,7 @@ PEAK_CLOCK_HZ = 2.4e9
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over `bench.py --probe-traffic`, each
 # scaled by what the same counter reads for a device copy of known size, averaged over the
 # GEMV launches of one C3 step (profiles/traffic_gemv_llama-3.2-3b_q8_0.md).
-TRAFFIC: dict = {"llama-3.2-3b": 30571736}
+TRAFFIC: dict = {"llama-3.2-3b": 30583110}
 TRAFFIC_SOURCE = ("profiles/traffic_gemv_llama-3.2-3b_q8_0.md: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE "
                   "passes, scaled by a copy kernel's reading; a recorded figure, not measured in this run")
 # Q8_0 [N, K] shapes, weights N(0, 0.02) and activations N(0, 1), seed 2
@@ -217,6 +217,58 @@ def run_sweep_kquant(tokens: int = 512, iters: int = 20) -> dict:
 ATT_PHASES = ("qkv_rope_kvstore", "scores_max", "exp", "denominator", "output_sums", "quantize_store")
 
 
+def kquant_norm_phases(cfg, gs) -> dict:
+    """The norm-fused K-quant launches of the last layer (k_norm_qk4_v6: kind 0, k_norm_gemv_q4k:
+    kind 1), from the measurement build's stamps: workgroup 0 (the RMSNorm + Q8_K row) in slot
+    0 -- 0 start, 6 squares stored, 8..11 after the one-pass sum's f64 scan, segmented scan,
+    special-step entries and replay, 12 the special-step count, 7 sum done, 2 y, 3 block maxima,
+    4 quants, 5 stores completed, 1 published; every ceil(grid / 256)-th other workgroup in slot
+    blockIdx / that -- 0 start, 3 flag seen and activation staged, 5 end.  Times in us from
+    workgroup 0's start."""
+    res = {}
+    hd, nq, nkv = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    gu_r = 16 if 2 * cfg.ffn_dim >= 16384 else 8  # (rows per gate|up workgroup, as the engine launches it)
+    wgs = {0: ((nq + nkv) * hd + 7) // 8 + (nkv * hd + 7) // 8, 1: (2 * cfg.ffn_dim + gu_r - 1) // gu_r}
+    for kind, name in enumerate(("norm_qk4_v6", "norm_gemv_q4k_gate_up")):
+        g = gs[kind]
+        w0 = g[0]
+        if w0[0] <= 0:
+            continue
+        t0 = w0[0]
+        us = lambda v: round(float(v - t0) * 0.01, 3)
+        ph = {"squares_stored": us(w0[6]), "sum_f64_scan": us(w0[8]), "sum_seg_scan": us(w0[9]),
+              "sum_specials": us(w0[10]), "sum_replay": us(w0[11]), "special_steps": int(w0[12]),
+              "sum_done": us(w0[7]), "y": us(w0[2]), "block_maxima": us(w0[3]), "quants": us(w0[4]),
+              "stores_completed": us(w0[5]), "published": us(w0[1])}
+        every = (1 + wgs[kind] + 255) // 256
+        ws = g[1:]
+        ok = (ws[:, 0] > 0) & (ws[:, 3] > 0) & (ws[:, 5] > 0)
+        ws = ws[ok]
+        if len(ws):
+            ph.update({"waiters_sampled": int(len(ws)), "waiters_every": every,
+                       "waiter_start_mean": us(ws[:, 0].mean()), "waiter_start_max": us(ws[:, 0].max()),
+                       "staged_mean": us(ws[:, 3].mean()), "staged_min": us(ws[:, 3].min()),
+                       "end_mean": us(ws[:, 5].mean()), "end_max": us(ws[:, 5].max())})
+        res[name] = ph
+        log(f"{name} phases (us from workgroup 0's start): " + ", ".join(f"{k} {v}" for k, v in ph.items()))
+    return res
+
+
+def fused_attention_phases(st) -> dict:
+    """The single-workgroup attention's phases from its stamps st[layer][head][9]."""
+    d = np.diff(st[:, :, :7], axis=2) * 0.01  # 100 MHz ticks -> us
+    res = {name: round(float(d[:, :, i].mean()), 3) for i, name in enumerate(ATT_PHASES)}
+    # inside the score phase (from its start): thread 0's K-row loads issued, wave 0's scores done
+    for i, name in ((7, "k_rows_issued"), (8, "wave0_scores_done")):
+        v = (st[:, :, i] - st[:, :, 1]) * 0.01
+        res[name] = round(float(v[st[:, :, i] > 0].mean()), 3) if (st[:, :, i] > 0).any() else None
+    res["workgroup_total"] = round(float((st[:, :, 6] - st[:, :, 0]).mean() * 0.01), 3)
+    res["start_spread"] = round(float((st[:, :, 0].max(1) - st[:, :, 0].min(1)).mean() * 0.01), 3)
+    res["launch_span"] = round(float((st[:, :, 6].max(1) - st[:, :, 0].min(1)).mean() * 0.01), 3)
+    log("attention phases (us, mean over layers and heads): " + ", ".join(f"{k} {v}" for k, v in res.items()))
+    return res
+
+
 def attention_phases(cfg) -> dict:
     """Per-phase times of the decode attention in the last timed step, from the measurement
     build's in-kernel timestamps (100 MHz counter, thread 0 of every head's workgroup): the
@@ -230,19 +282,15 @@ def attention_phases(cfg) -> dict:
     N.check(N.lib().camelid_hip_phase_stamps(buf, na + ng + nsp, C.byref(got)))
     allst = np.frombuffer(buf, np.uint64).astype(np.int64)
     st = allst[:na].reshape(64, 64, 9)[:cfg.n_layers, :cfg.n_heads]
-    d = np.diff(st[:, :, :7], axis=2) * 0.01  # 100 MHz ticks -> us
-    res = {name: round(float(d[:, :, i].mean()), 3) for i, name in enumerate(ATT_PHASES)}
-    # inside the score phase (from its start): thread 0's K-row loads issued, wave 0's scores done
-    for i, name in ((7, "k_rows_issued"), (8, "wave0_scores_done")):
-        v = (st[:, :, i] - st[:, :, 1]) * 0.01
-        res[name] = round(float(v[st[:, :, i] > 0].mean()), 3) if (st[:, :, i] > 0).any() else None
-    res["workgroup_total"] = round(float((st[:, :, 6] - st[:, :, 0]).mean() * 0.01), 3)
-    res["start_spread"] = round(float((st[:, :, 0].max(1) - st[:, :, 0].min(1)).mean() * 0.01), 3)
-    res["launch_span"] = round(float((st[:, :, 6].max(1) - st[:, :, 0].min(1)).mean() * 0.01), 3)
-    log("attention phases (us, mean over layers and heads): " + ", ".join(f"{k} {v}" for k, v in res.items()))
+    res = {}
+    if (st[:, :, 0] > 0).all():  # (the single-workgroup attention ran; else the split one did)
+        res.update(fused_attention_phases(st))
     # the norm-fused GEMVs of the last layer (mean over the workgroups that recorded)
     gs = allst[na:na + ng].reshape(2, 256, 13)
-    for kind, name in enumerate(("qkv_norm_gemv", "gate_up_norm_gemv")):
+    kquant = cfg.quant_scheme != "q8_0"
+    if kquant:
+        res.update(kquant_norm_phases(cfg, gs))
+    for kind, name in enumerate(() if kquant else ("qkv_norm_gemv", "gate_up_norm_gemv")):
         g = gs[kind]
         g = g[g[:, 0] > 0]
         if not len(g):

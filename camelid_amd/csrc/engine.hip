@@ -727,11 +727,27 @@ uint32_t launch_kgemv(const KMat& m, const float* yd, const int8_t* yq, const in
   if (m.quant == CAMELID_Q4_K) {
     const size_t lds = cm::kq4_lds_bytes((int)m.k, (int)R);
     const int it = (int)(m.k / 32 + 63) / 64;  // 16-byte pieces per lane and row (k <= 16384: <= 8)
+    if (xf) {  // (f32 activation: one row per wave)
+      switch (rpw == 1 ? it : 0) {
+#define CM_Q4X(IT)                                                                                               \
+  case IT:                                                                                                       \
+    CM_LAUNCH((cm::k_gemv_q4k<IT, 1, true>), dim3(grid), dim3(cm::KQ_NT), lds, s, m.a, m.b, (int)m.rows, (int)m.k, \
+              yd, yq, ybs, y, resid, part_v, part_i, xf);                                                        \
+    break;
+        CM_Q4X(1) CM_Q4X(2) CM_Q4X(3) CM_Q4X(4) CM_Q4X(5) CM_Q4X(6) CM_Q4X(7) CM_Q4X(8)
+#undef CM_Q4X
+        default:
+          g_launch_error = "Q4_K GEMV of an f32 activation: " + std::to_string(m.rows) + " x " + std::to_string(m.k) +
+                           " has no kernel instantiation";
+          return 0;
+      }
+      return grid;
+    }
     switch (it * 2 + (rpw == 2)) {
 #define CM_Q4(IT, RPW)                                                                                           \
   case IT * 2 + (RPW == 2):                                                                                      \
     CM_LAUNCH((cm::k_gemv_q4k<IT, RPW>), dim3(grid), dim3(cm::KQ_NT), lds, s, m.a, m.b, (int)m.rows, (int)m.k, yd, \
-              yq, ybs, y, resid, part_v, part_i, xf);                                                            \
+              yq, ybs, y, resid, part_v, part_i, nullptr);                                                       \
     break;
       CM_Q4(1, 1) CM_Q4(1, 2) CM_Q4(2, 1) CM_Q4(2, 2) CM_Q4(3, 1) CM_Q4(3, 2) CM_Q4(4, 1) CM_Q4(4, 2)
       CM_Q4(5, 1) CM_Q4(6, 1) CM_Q4(7, 1) CM_Q4(8, 1)
@@ -773,13 +789,14 @@ void quant_q8k(camelid_hip_engine* e, const float* x, uint32_t n) {
 }
 
 // One projection in its own format: Q8_0 from the Q8_0 activation, K-quants from the Q8_K
-// one, or (xf given) from the f32 activation, which a Q4_K GEMV quantizes itself.
+// one, or (xf given) from the f32 activation, which a Q4_K GEMV of one row per wave (rows <
+// 16384) quantizes itself.
 void proj(camelid_hip_engine* e, const Proj& p, float* y, const float* resid, const float* xf = nullptr) {
   if (p.quant == CAMELID_Q8_0) {
     gemv(e, p.q8, y, resid);
     return;
   }
-  if (xf && p.quant == CAMELID_Q6_K) {
+  if (xf && (p.quant == CAMELID_Q6_K || p.kq.rows >= 16384)) {
     quant_q8k(e, xf, p.kq.k);
     xf = nullptr;
   }

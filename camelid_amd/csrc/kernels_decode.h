@@ -777,6 +777,16 @@ __device__ __forceinline__ float max_wave(float a) {
   const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 48));
   return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
+// unsigned minimum over the whole wave, in every lane (the whole wave active)
+__device__ __forceinline__ uint32_t min_wave(uint32_t v) {
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0xB1, 0xf, 0xf, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x4E, 0xf, 0xf, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x124, 0xf, 0xf, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x128, 0xf, 0xf, false));
+  const uint32_t lo = min((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
+  const uint32_t hi = min((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+  return min(lo, hi);
+}
 // unsigned minimum over each aligned 32-lane half, in every lane of the half
 __device__ __forceinline__ uint32_t min_half_wave(uint32_t v) {
   v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0xB1, 0xf, 0xf, false));

@@ -43,20 +43,21 @@ __device__ __forceinline__ int group8_sum_lead(int v) {
 
 // Q8_K quantization of one 256-value block by one wave (lane l holds values 4l..4l+3) into
 // LDS: quants, per-32 sums and the scale (inference.rs:17564-17599, as quantize_q8k_wg256).
-__device__ __forceinline__ void quantize_q8k_wave(const float* __restrict__ x, int8_t* q, int* bs, float* d) {
+// The block's (|max|, first index) pick needs only |max| and the sign of the value at its
+// first occurrence: a wave max, then a wave min over (index << 1 | sign) of the lanes holding it.
+__device__ __forceinline__ void quantize_q8k_wave_vals(const float4 v4, int8_t* q, int* bs, float* d) {
   const int lane = threadIdx.x & 63;
-  const float4 v4 = reinterpret_cast<const float4*>(x)[lane];
   const float vals[4] = {v4.x, v4.y, v4.z, v4.w};
-  float a = 0.0f, v = 0.0f;
-  int idx = 0x7fffffff;
+  float a = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 4; ++e)
-    if (fabsf(vals[e]) > a) {
-      a = fabsf(vals[e]);
-      v = vals[e];
-      idx = 4 * lane + e;
-    }
-  amax_pick_wave(a, idx, v);
+  for (int e = 0; e < 4; ++e) a = fabsf(vals[e]) > a ? fabsf(vals[e]) : a;
+  a = max_wave(a);
+  uint32_t key = 0xffffffffu;
+#pragma unroll
+  for (int e = 3; e >= 0; --e)
+    key = fabsf(vals[e]) == a ? ((uint32_t)(4 * lane + e) << 1) | (__float_as_uint(vals[e]) >> 31) : key;
+  key = min_wave(key);
+  const float v = (key & 1u) ? -a : a;  // the value at the first index of the maximum (a > 0)
   const float iscale = a > 0.0f ? -127.0f / v : 0.0f;
   uint32_t word = 0;
   int sum = 0;
@@ -139,7 +140,7 @@ __host__ __device__ inline size_t kq4_lds_bytes(int K, int R) {
   return kq4_terms_offset(K) + (size_t)R * (K / 256) * 16;
 }
 
-template <int IT, int RPW, int NT = KQ_NT>
+template <int IT, int RPW, int NT = KQ_NT, bool XF = false>
 __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __restrict__ nib, const uint8_t* __restrict__ hdr,
                                                     int rows, int K, const float* __restrict__ yd,
                                                     const int8_t* __restrict__ yq, const int32_t* __restrict__ ybs,
@@ -180,8 +181,22 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
     if (sk >= 0) {
       CM_GEMV_STAMP_SAMPLED(sk, 3, 0)
     }
-  } else if (xf) {  // the activation given in f32: each wave quantizes blocks wave, wave + 4, ... to Q8_K
-    for (int b = wave; b < NSB; b += NT / 64) quantize_q8k_wave(xf + 256 * b, xq + 256 * b, xbs + 8 * b, xd + b);
+  } else if constexpr (XF) {  // the activation given in f32: each wave quantizes blocks wave, wave + NW, ... to Q8_K
+    // (the loads of a wave's first four blocks go out together, ahead of the first pick)
+    constexpr int NW = NT / 64, PB = 4;
+    float4 pre[PB];
+#pragma unroll
+    for (int u = 0; u < PB; ++u) {
+      const int b = wave + NW * u;
+      if (b < NSB) pre[u] = reinterpret_cast<const float4*>(xf + 256 * b)[lane];
+    }
+#pragma unroll
+    for (int u = 0; u < PB; ++u) {
+      const int b = wave + NW * u;
+      if (b < NSB) quantize_q8k_wave_vals(pre[u], xq + 256 * b, xbs + 8 * b, xd + b);
+    }
+    for (int b = wave + NW * PB; b < NSB; b += NW)
+      quantize_q8k_wave_vals(reinterpret_cast<const float4*>(xf + 256 * b)[lane], xq + 256 * b, xbs + 8 * b, xd + b);
   } else {
     for (int c = tid; c < (K >> 4); c += NT) reinterpret_cast<int4*>(xq)[c] = reinterpret_cast<const int4*>(yq)[c];
     for (int i = tid; i < NSB; i += NT) xd[i] = yd[i];
@@ -256,13 +271,15 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
   }
 }
 
-template <int IT, int RPW>
+// XF: the activation comes as f32 in xf (quantized by the workgroup), else as Q8_K in yd/yq/ybs
+// (a separate instantiation: the f32 path's registers would lower every launch's occupancy).
+template <int IT, int RPW, bool XF = false>
 __global__ __launch_bounds__(KQ_NT) void k_gemv_q4k(const uint8_t* __restrict__ nib, const uint8_t* __restrict__ hdr,
                                                     int rows, int K, const float* __restrict__ yd,
                                                     const int8_t* __restrict__ yq, const int32_t* __restrict__ ybs,
                                                     float* y, const float* resid, float* __restrict__ part_v,
                                                     uint32_t* __restrict__ part_i, const float* __restrict__ xf) {
-  gemv_q4k_body<IT, RPW>((int)blockIdx.x, nib, hdr, rows, K, yd, yq, ybs, y, resid, part_v, part_i, xf);
+  gemv_q4k_body<IT, RPW, KQ_NT, XF>((int)blockIdx.x, nib, hdr, rows, K, yd, yq, ybs, y, resid, part_v, part_i, xf);
 }
 
 // ---------------------------------------------------------------------------
