@@ -158,7 +158,19 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
   float4* terms = reinterpret_cast<float4*>(smem + kq4_terms_offset(K));
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int row0 = bid * R;
-  // every weight and header load of this wave first (pieces lane + 64 i of each row; past
+  // XF: the loads of this wave's first four 256-value blocks of the f32 activation go out
+  // first (from L2), so that its Q8_K quantization waits for them only, not for the weight
+  // loads behind them (loads complete in issue order for the wait counter)
+  constexpr int NW = NT / 64, PB = 4;
+  float4 pre[XF ? PB : 1];
+  if constexpr (XF) {
+#pragma unroll
+    for (int u = 0; u < PB; ++u) {
+      const int b = wave + NW * u;
+      if (b < NSB) pre[u] = reinterpret_cast<const float4*>(xf + 256 * b)[lane];
+    }
+  }
+  // every weight and header load of this wave next (pieces lane + 64 i of each row; past
   // NC clamped, their results never stored)
   uint4 wv[RPW][IT], hv[RPW][IT];
 #pragma unroll
@@ -182,14 +194,6 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
       CM_GEMV_STAMP_SAMPLED(sk, 3, 0)
     }
   } else if constexpr (XF) {  // the activation given in f32: each wave quantizes blocks wave, wave + NW, ... to Q8_K
-    // (the loads of a wave's first four blocks go out together, ahead of the first pick)
-    constexpr int NW = NT / 64, PB = 4;
-    float4 pre[PB];
-#pragma unroll
-    for (int u = 0; u < PB; ++u) {
-      const int b = wave + NW * u;
-      if (b < NSB) pre[u] = reinterpret_cast<const float4*>(xf + 256 * b)[lane];
-    }
 #pragma unroll
     for (int u = 0; u < PB; ++u) {
       const int b = wave + NW * u;
