@@ -124,6 +124,9 @@ struct camelid_hip_engine {
   // counters show attention fetching its K/V rows again either way, so it is opt-in.
   bool read_ahead = false;
   bool kv_ahead = false;
+  // workgroups per query head of the decode attention (CAMELID_HIP_ATT_DG; 0: 64 output dims
+  // per workgroup): each stages only its dims' V rows
+  int att_dg = 0;
   bool gu_fused = false;   // gate/up rows interleaved by 32, SwiGLU fused into their GEMV
   bool norm_fused = true;  // RMSNorms computed inside the qkv and gate/up GEMVs (Q8_0 layers)
   bool qkv_merged = true;  // Q4_K q|k and Q6_K v projections in one launch (k_gemv_qk4_v6)
@@ -559,20 +562,37 @@ size_t attn_sc_bytes(uint32_t kvs) { return (((size_t)kvs + 3) & ~(size_t)3) * 4
 int attn_ring_slots(uint32_t kvs);
 int attn_out_slots(uint32_t kvs, int slots, int* pb);
 
+// dg: workgroups per query head (k_attention's DG: 1, 2 or 4, at most hd / 32); 0 takes the
+// default, 64 output dims per workgroup (C3 decode: 671.0 / 675.6 / 668.0 tok/s at 1 / 2 / 4
+// workgroups per head of 128 dims).
 template <bool FUSED>
 void launch_attention(uint32_t hd, uint32_t n_heads, int slots, hipStream_t s, const float* qsrc, int nh, int nkv,
                       int rope_dim, int split_half, const float* cb, const float* sb, int rs, const float* qn,
                       const float* kn, float eps, uint16_t* kc, uint16_t* vc, int layer, int kvs, const uint32_t* pos,
-                      float scale, float* att, int8_t* xq, float* xs, cm::Prefetch pf) {
+                      float scale, float* att, int8_t* xq, float* xs, cm::Prefetch pf, int dg = 1) {
   const size_t lds = (size_t)slots * cm::ATT_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs);
-  const uint32_t grid = n_heads + (pf.a_lines ? PREFETCH_WGS : 0);
-#define CM_ATT(HD)                                                                                                  \
-  CM_LAUNCH((cm::k_attention<HD, FUSED>), dim3(grid), dim3(cm::att_nt(HD)), lds, s, qsrc, nh, nkv,  \
-                     rope_dim, split_half, cb, sb, rs, qn, kn, eps, kc, vc, layer, kvs, pos, scale, att, xq, xs, \
-                     slots, pf)
-  if (hd == 64) CM_ATT(64);
-  else if (hd == 128) CM_ATT(128);
-  else CM_ATT(256);
+  if (dg <= 0) dg = (int)std::max<uint32_t>(1, hd / 64);
+  if (dg > 4 || (dg & (dg - 1)) || hd / (uint32_t)dg < 32) {
+    g_launch_error = "attention: " + std::to_string(dg) + " workgroups per head of " + std::to_string(hd) +
+                     " dims has no instantiation";
+    return;
+  }
+  const uint32_t grid = n_heads * (uint32_t)dg + (pf.a_lines ? PREFETCH_WGS : 0);
+#define CM_ATT(HD, DG)                                                                                         \
+  CM_LAUNCH((cm::k_attention<HD, FUSED, DG>), dim3(grid), dim3(cm::att_nt(HD)), lds, s, qsrc, nh, nkv, rope_dim, \
+            split_half, cb, sb, rs, qn, kn, eps, kc, vc, layer, kvs, pos, scale, att, xq, xs, slots, pf)
+  if (hd == 64) {
+    if (dg == 1) CM_ATT(64, 1);
+    else CM_ATT(64, 2);
+  } else if (hd == 128) {
+    if (dg == 1) CM_ATT(128, 1);
+    else if (dg == 2) CM_ATT(128, 2);
+    else CM_ATT(128, 4);
+  } else {
+    if (dg == 1) CM_ATT(256, 1);
+    else if (dg == 2) CM_ATT(256, 2);
+    else CM_ATT(256, 4);
+  }
 #undef CM_ATT
 }
 
@@ -819,7 +839,7 @@ void decode_attention(camelid_hip_engine* e, uint32_t l, const float* cos_base, 
     launch_attention<true>(d.head_dim, d.n_heads, e->att_slots, e->stream, e->qkv, (int)d.n_heads,
                            (int)d.n_kv_heads, (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base,
                            rope_stride, L.q_norm, L.k_norm, d.eps, e->kc, e->vc, (int)l, (int)e->kvs, &e->st->pos,
-                           scale, e->att, e->xq, e->xs, pf);
+                           scale, e->att, e->xq, e->xs, pf, e->att_dg);
 }
 
 // The K-quant layer shape the norm-fused launches take: hidden 4096 (the norm workgroup's 512 x
@@ -1427,6 +1447,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   if (const char* f = std::getenv("CAMELID_HIP_KQ_NORM_FUSED")) e->kq_norm_fused = std::atoi(f) != 0;
   e->att_slots = attn_ring_slots(e->kvs);
   if (const char* f = std::getenv("CAMELID_HIP_ATT_SPLIT")) e->att_split_min = (uint32_t)std::strtoul(f, nullptr, 10);
+  if (const char* f = std::getenv("CAMELID_HIP_ATT_DG")) e->att_dg = std::atoi(f);
   const size_t nq = (size_t)d.n_heads * d.head_dim, nkv = (size_t)d.n_kv_heads * d.head_dim;
   const size_t kv_elems = (size_t)d.n_layers * d.n_kv_heads * e->kvs * d.head_dim;
   const size_t act = std::max<size_t>({(size_t)d.hidden, (size_t)d.ffn_dim, nq});

@@ -2075,7 +2075,10 @@ __device__ __forceinline__ float att_onepass_sum(const float* v, int P, FsLds<NT
 }
 
 
-template <int HD, bool FUSED>
+// DG workgroups per query head (the grid is n_heads * DG): each computes the head's scores,
+// softmax and denominator (the same bits in every one of them) and the output sums of its
+// HD / DG dims, so that a CU stages 1/DG of the head's V rows; one of them stores the K/V row.
+template <int HD, bool FUSED, int DG = 1>
 __global__ __launch_bounds__(att_nt(HD)) void k_attention(
     const float* __restrict__ qsrc, int n_heads, int n_kv, int rope_dim, int split_half,
     const float* __restrict__ cos_base, const float* __restrict__ sin_base, int rope_stride,
@@ -2089,12 +2092,14 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   constexpr int CW = HD / 64;                        // output waves: one lane per dim
   constexpr int NH = (NW - CW) >= 8 ? 8 : 4;         // V-staging waves (divides the 32 loads)
   constexpr int LH = ATT_RING_LOADS / NH;            // 1 KB wave loads per staging wave per chunk
-  constexpr int CG = ATT_RING_GRANULES / HD;         // 8-position groups per ring chunk
+  constexpr int OD = HD / DG;                        // output dims of this workgroup: [d0, d0 + OD)
+  static_assert(OD % 32 == 0 && OD <= 64 * CW, "whole Q8_0 blocks of output per workgroup");
+  constexpr int CG = ATT_RING_GRANULES / OD;         // 8-position groups per ring chunk
   extern __shared__ __align__(16) float4 dyn[];
   float4* ring = dyn;  // ring_slots chunks of ATT_RING_GRANULES V granules
   float* sc = reinterpret_cast<float*>(dyn + (size_t)ring_slots * ATT_RING_GRANULES);
-  if ((int)blockIdx.x >= n_heads) {  // spare workgroups: read ahead the output projection
-    prefetch_lines(pf, blockIdx.x - n_heads, gridDim.x - n_heads, sc);
+  if ((int)blockIdx.x >= n_heads * DG) {  // spare workgroups: read ahead the output projection
+    prefetch_lines(pf, blockIdx.x - n_heads * DG, gridDim.x - n_heads * DG, sc);
     return;
   }
   __shared__ __align__(16) float qs[HD];
@@ -2108,7 +2113,10 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   __shared__ uint32_t team_ctr, team_bad;  // the head team's LDS barrier
   const int tid = threadIdx.x;
   const int rep = n_heads / n_kv;
-  const int h = xcd_member(blockIdx.x, n_kv, rep);
+  // workgroup (h, dg): the head's DG workgroups and those of the other query heads of its KV
+  // head on one XCD
+  const int hm = xcd_member(blockIdx.x, n_kv, rep * DG);
+  const int h = hm / DG, dg = hm % DG, d0 = dg * OD;
   const int kvh = h / rep;
   const size_t hbase = kv_head_base(layer, n_kv, kvh, HD, kvs);
   const uint4* kg = reinterpret_cast<const uint4*>(kc + hbase);  // K granule (u, p): u * kvs + p
@@ -2142,9 +2150,11 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   float rc = 0.0f, rs = 0.0f, qnw = 0.0f, knw = 0.0f;
   if (tid < HD) {
     const int tail0 = (pos >> 3) << 3;  // first position past the full granules of [0, pos)
+    if (tid < OD) {
 #pragma unroll
-    for (int u = 0; u < 7; ++u)
-      vtail[u] = tail0 + u < pos ? vc[hbase + kv_v_index(HD, tail0 + u, tid)] : (uint16_t)0;
+      for (int u = 0; u < 7; ++u)
+        vtail[u] = tail0 + u < pos ? vc[hbase + kv_v_index(HD, tail0 + u, d0 + tid)] : (uint16_t)0;
+    }
     if (FUSED) {
       if (tid < half) {
         rc = cos_base[(size_t)pos * rope_stride + tid];
@@ -2176,9 +2186,10 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
       CM_ATT_STAMP_T(7, HD)
     }
   }
-  // V staging: the cache positions' V granules (full 8-position groups) are copied into an
-  // LDS ring of ring_slots chunks by NH staging waves with direct global->LDS loads; the
-  // output lanes read them from LDS.  A chunk is contiguous in the cache layout.  The first
+  // V staging: the cache positions' V granules (full 8-position groups) of this workgroup's
+  // dims are copied into an LDS ring of ring_slots chunks by NH staging waves with direct
+  // global->LDS loads; the output lanes read them from LDS.  A chunk holds CG groups of OD
+  // granules (contiguous in the cache layout when DG = 1, else OD-granule runs).  The first
   // chunks go out after the exponentials (longer contexts with the segmented denominator use
   // the ring for its prefix arrays first).
   const int ng = ncache >> 3;  // full groups of 8 cache positions
@@ -2186,13 +2197,14 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   const int R = ring_slots;
   const int hw = (tid >> 6) - CW;
   const bool stager = hw >= 0 && hw < NH;
-  const size_t last_granule = (size_t)max(ng, 1) * HD - 1;
+  const size_t last_group = (size_t)max(ng, 1) - 1;
   auto stage = [&](int c) {  // chunk c into slot c % R
     float4* slot = ring + (size_t)(c % R) * ATT_RING_GRANULES;
 #pragma unroll
     for (int j = 0; j < LH; ++j) {
       const int i = hw + NH * j;  // 1 KB piece of the chunk
-      const size_t gsrc = min((size_t)c * ATT_RING_GRANULES + (size_t)i * 64 + (tid & 63), last_granule);
+      const int q = i * 64 + (tid & 63);  // granule q of the chunk: group q / OD, dim d0 + q % OD
+      const size_t gsrc = min((size_t)c * CG + (size_t)(q / OD), last_group) * HD + d0 + q % OD;
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(vg + gsrc),
                                        (__attribute__((address_space(3))) void*)(slot + i * 64), 16, 0, 0);
     }
@@ -2240,7 +2252,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
       const uint16_t vb = f32_to_f16_bits(vn[tid]);
       kn[tid] = half_bits_to_float(kb);
       vn[tid] = half_bits_to_float(vb);
-      if ((h % rep) == 0) {
+      if ((h % rep) == 0 && dg == 0) {
         kc[hbase + kv_k_index(kvs, pos, tid)] = kb;
         vc[hbase + kv_v_index(HD, pos, tid)] = vb;
       }
@@ -2252,7 +2264,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   float res = 0.0f;  // this output lane's value (tid < HD)
   if (P == 1) {
     // inference.rs:23564-23575: a single position copies the V row.
-    if (tid < HD) res = vn[tid];
+    if (tid < OD) res = vn[d0 + tid];
   } else {
     // ---- scores: cache positions 0..pos-1, one lane each
     float lmax = -INFINITY;
@@ -2376,7 +2388,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
       if (stager) wait_vmcnt(LH * (min(c + R - 2, nchunks - 1) - c));  // chunk c has landed
       __syncthreads();  // chunk c visible; the slot of chunk c - 1 is free
       if (stager && c + R - 1 < nchunks) stage(c + R - 1);
-      if (tid < HD) {
+      if (tid < OD) {
         const uint4* slot = reinterpret_cast<const uint4*>(ring + (size_t)(c % R) * ATT_RING_GRANULES) + tid;
         const float4* pr4 = reinterpret_cast<const float4*>(sc) + (size_t)c * CG * 2;
         const int gn = min(CG, ng - c * CG);
@@ -2392,30 +2404,30 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
           pr[6] = mul_f16_lo(p1.z, g.w);
           pr[7] = mul_f16_hi(p1.w, g.w);
         };
+        // LDS reads ping-pong between two batches of 2 granules (16 positions) so that the
+        // add chain never waits on LDS latency
+        static_assert(CG % 4 == 0, "ring chunks hold a multiple of 4 granule groups");
+        uint4 va[2], vb[2];
+        float4 pa[4], pb[4];
+        auto ld = [&](uint4(&v)[2], float4(&pq)[4], int j0) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            v[u] = slot[(j0 + u) * OD];
+            pq[2 * u] = pr4[2 * (j0 + u)];
+            pq[2 * u + 1] = pr4[2 * (j0 + u) + 1];
+          }
+        };
+        auto mac = [&](const uint4(&v)[2], const float4(&pq)[4]) {
+          float pr[2][8];
+          granule(v[0], pq[0], pq[1], pr[0]);
+          granule(v[1], pq[2], pq[3], pr[1]);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc += pr[u][e];
+        };
         if (gn == CG) {
-          // LDS reads ping-pong between two batches of 2 granules (16 positions) so that
-          // the add chain never waits on LDS latency
-          static_assert(CG % 4 == 0, "ring chunks hold a multiple of 4 granule groups");
-          uint4 va[2], vb[2];
-          float4 pa[4], pb[4];
-          auto ld = [&](uint4(&v)[2], float4(&pq)[4], int j0) {
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-              v[u] = slot[(j0 + u) * HD];
-              pq[2 * u] = pr4[2 * (j0 + u)];
-              pq[2 * u + 1] = pr4[2 * (j0 + u) + 1];
-            }
-          };
-          auto mac = [&](const uint4(&v)[2], const float4(&pq)[4]) {
-            float pr[2][8];
-            granule(v[0], pq[0], pq[1], pr[0]);
-            granule(v[1], pq[2], pq[3], pr[1]);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int u = 0; u < 2; ++u)
-#pragma unroll
-              for (int e = 0; e < 8; ++e) acc += pr[u][e];
-          };
           ld(va, pa, 0);
 #pragma unroll
           for (int j = 0; j < CG; j += 4) {
@@ -2427,9 +2439,20 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
             mac(vb, pb);
           }
         } else {
-          for (int j = 0; j < gn; ++j) {
+          // the last chunk: its whole batches of 4 granules as above, then one at a time
+          const int g4 = gn & ~3;
+          if (g4 > 0) ld(va, pa, 0);
+          for (int j = 0; j < g4; j += 4) {
+            ld(vb, pb, j + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            mac(va, pa);
+            if (j + 4 < g4) ld(va, pa, j + 4);
+            __builtin_amdgcn_sched_barrier(0);
+            mac(vb, pb);
+          }
+          for (int j = g4; j < gn; ++j) {
             float pr[8];
-            granule(slot[j * HD], pr4[2 * j], pr4[2 * j + 1], pr);
+            granule(slot[j * OD], pr4[2 * j], pr4[2 * j + 1], pr);
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc += pr[e];
           }
@@ -2440,23 +2463,23 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
     // the normalised probabilities past the ring were published by the ring loop's first
     // barrier; with no chunks at all, by this one (uniform)
     if (nchunks == 0) __syncthreads();
-    if (tid < HD) {
+    if (tid < OD) {
 #pragma unroll
       for (int u = 0; u < 7; ++u)
         if (ng * 8 + u < ncache) acc += sc[ng * 8 + u] * half_bits_to_float(vtail[u]);
-      acc += sc[pos] * vn[tid];
+      acc += sc[pos] * vn[d0 + tid];
       res = acc;
     }
   }
   // (each output lane stores and quantizes its own value: no barrier; the Q8_0 block's
   // scale is formed by lane shuffles within the 32-lane group)
-  if (tid < HD) {
+  if (tid < OD) {
     if (team_bad) res = __builtin_nanf("");  // (the team barrier's bound was reached: no result)
-    att_out[(size_t)h * HD + tid] = res;
+    att_out[(size_t)h * HD + d0 + tid] = res;
     int8_t q;
     const float dd = quantize_lane32(res, &q);
-    xq[(size_t)h * HD + tid] = q;
-    if ((tid & 31) == 0) xs[((size_t)h * HD + tid) >> 5] = dd;
+    xq[(size_t)h * HD + d0 + tid] = q;
+    if ((tid & 31) == 0) xs[((size_t)h * HD + d0 + tid) >> 5] = dd;
   }
   CM_ATT_STAMP(6)
 }

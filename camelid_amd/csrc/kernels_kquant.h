@@ -491,6 +491,53 @@ constexpr int NF_NT = 512;  // threads of a norm-fused launch's workgroups
 constexpr int NQ_C = 8;     // values per thread of the norm workgroup
 __host__ __device__ inline size_t norm_q8k_lds_bytes(int n) { return (size_t)n * 4 + sizeof(FsLds<NF_NT>); }
 
+// Q8_K quantization of one 256-value block held 8 values per lane by a half wave (lane l of
+// the half: values 8l..8l+7; inference.rs:17564-17599, as k_rmsnorm_quant), stored with
+// agent-scope (XCD-coherent) stores for a reader in the same launch: this lane's 8 quants to
+// q8 (8 bytes), the per-32 sums to bs (by lanes l % 4 == 0), the scale to d (by lane l == 0).
+// The block's (|max|, first index) pick needs only |max| and the sign of its first
+// occurrence: a max, then a min over (index << 1 | sign) of the lanes holding |max|.
+__device__ __forceinline__ void q8k_half_wave_block(const float (&y)[8], int l, int8_t* q8, int32_t* bs, float* d,
+                                                    int kind = -1) {
+  (void)kind;  // (the measurement build's stamp kind)
+  constexpr int C = 8;
+  float a = 0.0f;
+#pragma unroll
+  for (int e = 0; e < C; ++e) a = fabsf(y[e]) > a ? fabsf(y[e]) : a;
+  a = max_half_wave(a);
+  uint32_t key = 0xffffffffu;
+#pragma unroll
+  for (int e = C - 1; e >= 0; --e)
+    key = fabsf(y[e]) == a ? ((uint32_t)(C * l + e) << 1) | (__float_as_uint(y[e]) >> 31) : key;
+  key = min_half_wave(key);
+  const float v = (key & 1u) ? -a : a;  // y at the first index of the maximum (a > 0)
+  if (kind >= 0) {
+    CM_GEMV_STAMP(kind, 3, 0)
+  }
+  const float iscale = a > 0.0f ? -127.0f / v : 0.0f;
+  uint32_t words[C / 4];
+  int sum = 0;
+#pragma unroll
+  for (int w4 = 0; w4 < C / 4; ++w4) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int q = a > 0.0f ? min(nearest_int_ref(iscale * y[w4 * 4 + e]), 127) : 0;
+      sum += (int8_t)q;
+      word |= ((uint32_t)q & 0xffu) << (8 * e);
+    }
+    words[w4] = word;
+  }
+  // the lanes of a quad hold 32 consecutive values: the per-32 sum
+  const int s4 = quad_sum(sum);
+  if (kind >= 0) {
+    CM_GEMV_STAMP(kind, 4, 0)
+  }
+  st_agent64(q8, (uint64_t)words[0] | ((uint64_t)words[1] << 32));
+  if ((l & 3) == 0) st_agent32(bs, (uint32_t)s4);
+  if (l == 0) st_agent32(d, __float_as_uint(a > 0.0f ? 1.0f / iscale : 0.0f));
+}
+
 // Thread t holds values 8t..8t+7 (the one-pass sum's layout); a Q8_K block is one half wave
 // (block position 8 l + e for lane l of the half).  smem: the n squares (the sum's fallback)
 // + FsLds<512>.  n == 8 * 512.
@@ -538,39 +585,7 @@ __device__ __forceinline__ void norm_q8k_publish(const float* __restrict__ x, co
     y[4 * u + 3] = (a.w * scale) * b.w;
   }
   CM_GEMV_STAMP(kind, 2, 0)
-  // the block's (|max|, first index) pick needs only |max| and the sign of its first
-  // occurrence: a max, then a min over (index << 1 | sign) of the lanes holding |max|
-  float a = 0.0f;
-#pragma unroll
-  for (int e = 0; e < C; ++e) a = fabsf(y[e]) > a ? fabsf(y[e]) : a;
-  a = max_half_wave(a);
-  uint32_t key = 0xffffffffu;
-#pragma unroll
-  for (int e = C - 1; e >= 0; --e)
-    key = fabsf(y[e]) == a ? ((uint32_t)(C * l + e) << 1) | (__float_as_uint(y[e]) >> 31) : key;
-  key = min_half_wave(key);
-  const float v = (key & 1u) ? -a : a;  // y at the first index of the maximum (a > 0)
-  CM_GEMV_STAMP(kind, 3, 0)
-  const float iscale = a > 0.0f ? -127.0f / v : 0.0f;
-  uint32_t words[C / 4];
-  int sum = 0;
-#pragma unroll
-  for (int w4 = 0; w4 < C / 4; ++w4) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int q = a > 0.0f ? min(nearest_int_ref(iscale * y[w4 * 4 + e]), 127) : 0;
-      sum += (int8_t)q;
-      word |= ((uint32_t)q & 0xffu) << (8 * e);
-    }
-    words[w4] = word;
-  }
-  // the lanes of a quad hold 32 consecutive values: the per-32 sum
-  const int s4 = quad_sum(sum);
-  CM_GEMV_STAMP(kind, 4, 0)
-  st_agent64(kq + tid * C, (uint64_t)words[0] | ((uint64_t)words[1] << 32));
-  if ((tid & 3) == 0) st_agent32(kbs + (tid >> 2), (uint32_t)s4);
-  if (l == 0) st_agent32(kd + (tid >> 5), __float_as_uint(a > 0.0f ? 1.0f / iscale : 0.0f));
+  q8k_half_wave_block(y, l, kq + tid * C, kbs + (tid >> 2), kd + (tid >> 5), kind);
   __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
   CM_GEMV_STAMP(kind, 5, 0)
   __syncthreads();

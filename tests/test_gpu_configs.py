@@ -9,9 +9,9 @@ CPU<->GPU stream parity (tests/cuda_cpu_parity.rs:32-62) and full-forward parity
 (src/cuda_resident/tests.rs:354).
 
 Also here: the engine's documented switches (CAMELID_HIP_FUSED_GU, _FUSED_NORM, _GRAPHS,
-_QKV_MERGED, _KQ_NORM_FUSED switched off; the opt-in _READ_AHEAD, _KV_AHEAD switched on) each
-against the same golden / oracle, and greedy ties (duplicated lm_head rows) through the
-product argmax paths.
+_QKV_MERGED, _KQ_NORM_FUSED switched off; the opt-in _READ_AHEAD, _KV_AHEAD switched on;
+_ATT_DG at each workgroup count) each against the same golden / oracle, and greedy ties
+(duplicated lm_head rows) through the product argmax paths.
 """
 import importlib.util
 import json
@@ -75,12 +75,13 @@ def test_config_stream_matches_golden(name):
 
 @pytest.mark.parametrize("switch,value", [("CAMELID_HIP_FUSED_GU", "0"), ("CAMELID_HIP_FUSED_NORM", "0"),
                                           ("CAMELID_HIP_READ_AHEAD", "1"), ("CAMELID_HIP_GRAPHS", "0"),
-                                          ("CAMELID_HIP_KV_AHEAD", "1")])
+                                          ("CAMELID_HIP_KV_AHEAD", "1"), ("CAMELID_HIP_ATT_DG", "2")])
 def test_switch_off_keeps_tinyllama_stream(monkeypatch, switch, value):
     """Each documented switch of the Q8_0 decode path set away from its default (the separate
     RMSNorm launch, the separate SwiGLU launch, the weight read-ahead workgroups, launches
-    without a graph, the KV rows read by the qkv launch's idle waves): the TinyLlama golden
-    stream (configs[0], 128 + 128) is still reproduced by the device loop."""
+    without a graph, the KV rows read by the qkv launch's idle waves, two attention workgroups
+    per head of 64 dims instead of one): the TinyLlama golden stream (configs[0], 128 + 128) is
+    still reproduced by the device loop."""
     monkeypatch.setenv(switch, value)
     test_config_stream_matches_golden("tinyllama-1.1b")
 
@@ -123,6 +124,36 @@ def test_switch_off_qkv_merged_kquant_matches_oracle(monkeypatch):
             assert tok == t_o
             pos += 1
         sess.close()
+
+
+@pytest.mark.parametrize("dg", ["1", "2", "4"])
+def test_attention_workgroups_per_head_match_oracle(monkeypatch, dg):
+    """CAMELID_HIP_ATT_DG: the decode attention with 1, 2 or 4 workgroups per query head (each
+    recomputes the head's scores and denominator and sums 128 / DG output dims, staging only
+    their V rows), head_dim 128, GQA 2:1, at positions 583..590 (the V ring's chunks hold 128,
+    256 or 512 positions: several chunks plus a partial one and the 7-position tail): per-layer
+    hidden states, logits and tokens bit-identical to the CPU oracle."""
+    from oracle.oracle import OracleModel
+    monkeypatch.setenv("CAMELID_HIP_ATT_DG", dg)
+    cfg = tiny_config(n_layers=2, hidden=512, ffn_dim=1024, n_heads=4, n_kv_heads=2, head_dim=128, vocab=512,
+                      prompt_len=584)
+    model = SyntheticModel.generate(cfg)
+    prompt = prompt_tokens(cfg)
+    orc = OracleModel(model, 600)
+    orc.prefill(prompt[:-1])
+    sess = ResidentSession(model, 600)
+    sess.engine.capture_hidden(True)
+    sess.prefill(prompt[:-1])
+    tok_o = tok_g = int(prompt[-1])
+    pos = len(prompt) - 1
+    for step in range(8):
+        tok_o, hid_o, lg_o = orc.forward(tok_o, pos, hidden=True, logits=True)
+        tok_g = sess.step(tok_g, pos, logits=True)
+        assert np.array_equal(sess.engine.read_hidden().view(np.uint32), hid_o.view(np.uint32)), (dg, step)
+        assert np.array_equal(sess.engine.last_logits.view(np.uint32), lg_o.view(np.uint32)), (dg, step)
+        assert tok_g == tok_o
+        pos += 1
+    sess.close()
 
 
 def _tied_max_model(cfg, period):
