@@ -135,6 +135,11 @@ struct camelid_hip_engine {
   bool kq_norm_fused = true;
   int nf_state = -1;              // -1 unknown, 0 off, 1 on (every layer fusable)
   uint32_t* nf_slots = nullptr;   // the launches' flag words (cm::NF_WORDS)
+  // Q8_0 layers: the output projection inside the single-workgroup attention launch
+  // (cm::att_oproj; CAMELID_HIP_ATT_O).  Measured on MI355X: see the layer loop.
+  bool att_o_fused = true;
+  int ao_state = -1;              // -1 unknown, 0 off, 1 on
+  uint64_t* ao_words = nullptr;   // the tagged activation words (ao_words())
   uint32_t* p_err = nullptr;      // host copy of the handoff error word
   float *h = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr;
   float *logits = nullptr, *hidden_cap = nullptr, *xs = nullptr;
@@ -569,18 +574,27 @@ template <bool FUSED>
 void launch_attention(uint32_t hd, uint32_t n_heads, int slots, hipStream_t s, const float* qsrc, int nh, int nkv,
                       int rope_dim, int split_half, const float* cb, const float* sb, int rs, const float* qn,
                       const float* kn, float eps, uint16_t* kc, uint16_t* vc, int layer, int kvs, const uint32_t* pos,
-                      float scale, float* att, int8_t* xq, float* xs, cm::Prefetch pf, int dg = 1) {
-  const size_t lds = (size_t)slots * cm::ATT_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs);
+                      float scale, float* att, int8_t* xq, float* xs, cm::Prefetch pf, int dg = 1,
+                      cm::OProj op = cm::OProj{}) {
+  size_t lds = (size_t)slots * cm::ATT_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs);
   if (dg <= 0) dg = (int)std::max<uint32_t>(1, hd / 64);
   if (dg > 4 || (dg & (dg - 1)) || hd / (uint32_t)dg < 32) {
     g_launch_error = "attention: " + std::to_string(dg) + " workgroups per head of " + std::to_string(hd) +
                      " dims has no instantiation";
     return;
   }
-  const uint32_t grid = n_heads * (uint32_t)dg + (pf.a_lines ? PREFETCH_WGS : 0);
+  uint32_t grid = n_heads * (uint32_t)dg + (pf.a_lines ? PREFETCH_WGS : 0);
+  if (op.q) {  // the output projection's workgroups instead of read-ahead ones
+    if (cm::att_nt((int)hd) != cm::AO_ROWS * 64 || !cm::ao_width_ok(op.K) || op.K != (int)(n_heads * hd)) {
+      g_launch_error = "attention: no output projection body for this shape";
+      return;
+    }
+    grid = n_heads * (uint32_t)dg + (uint32_t)(op.rows + cm::AO_ROWS - 1) / cm::AO_ROWS;
+    lds = std::max(lds, cm::ao_lds_bytes(op.K));
+  }
 #define CM_ATT(HD, DG)                                                                                         \
   CM_LAUNCH((cm::k_attention<HD, FUSED, DG>), dim3(grid), dim3(cm::att_nt(HD)), lds, s, qsrc, nh, nkv, rope_dim, \
-            split_half, cb, sb, rs, qn, kn, eps, kc, vc, layer, kvs, pos, scale, att, xq, xs, slots, pf)
+            split_half, cb, sb, rs, qn, kn, eps, kc, vc, layer, kvs, pos, scale, att, xq, xs, slots, pf, op)
   if (hd == 64) {
     if (dg == 1) CM_ATT(64, 1);
     else CM_ATT(64, 2);
@@ -827,7 +841,7 @@ void proj(camelid_hip_engine* e, const Proj& p, float* y, const float* resid, co
 // The decode attention of layer l for the token at StepState.pos (QK-norm, RoPE and the K/V
 // store fused): one workgroup per head, or the split kernels for long contexts.
 void decode_attention(camelid_hip_engine* e, uint32_t l, const float* cos_base, const float* sin_base,
-                      int rope_stride, float scale, cm::Prefetch pf) {
+                      int rope_stride, float scale, cm::Prefetch pf, cm::OProj op = cm::OProj{}) {
   const camelid_hip_dims& d = e->d;
   const LayerW& L = e->layers[l];
   if (att_split(e))
@@ -839,7 +853,33 @@ void decode_attention(camelid_hip_engine* e, uint32_t l, const float* cos_base, 
     launch_attention<true>(d.head_dim, d.n_heads, e->att_slots, e->stream, e->qkv, (int)d.n_heads,
                            (int)d.n_kv_heads, (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base,
                            rope_stride, L.q_norm, L.k_norm, d.eps, e->kc, e->vc, (int)l, (int)e->kvs, &e->st->pos,
-                           scale, e->att, e->xq, e->xs, pf, e->att_dg);
+                           scale, e->att, e->xq, e->xs, pf, e->att_dg, op);
+}
+
+// Tagged activation words of the attention's output projection: K / 4 quant words, K / 32 scales.
+size_t ao_words(const camelid_hip_engine* e) {
+  const size_t nq = (size_t)e->d.n_heads * e->d.head_dim;
+  return nq / 4 + nq / 32 + 1;
+}
+
+// Whether the Q8_0 decode layers compute the output projection inside the single-workgroup
+// attention launch (cm::att_oproj; CAMELID_HIP_ATT_O=0 turns it off): every layer must be a
+// Q8_0 layer whose W_o width has a projection body, with the read-ahead off (its workgroups
+// take the same place in the grid).
+bool ao_enabled(camelid_hip_engine* e) {
+  if (e->ao_state < 0) {
+    const camelid_hip_dims& d = e->d;
+    // (tags: the layer in 8 bits, position + 1 in 24)
+    bool ok = e->att_o_fused && !e->read_ahead && d.n_layers <= 255 && e->kvs < (1u << 24) - 1 &&
+              cm::att_nt((int)d.head_dim) == cm::AO_ROWS * 64 && cm::ao_width_ok((int)(d.n_heads * d.head_dim)) &&
+              e->ao_words != nullptr;
+    for (uint32_t l = 0; ok && l < d.n_layers; ++l) {
+      const LayerW& L = e->layers[l];
+      ok = L.set && !L.generic && L.o.k == d.n_heads * d.head_dim && L.o.rows == d.hidden;
+    }
+    e->ao_state = ok ? 1 : 0;
+  }
+  return e->ao_state == 1;
 }
 
 // The K-quant layer shape the norm-fused launches take: hidden 4096 (the norm workgroup's 512 x
@@ -868,24 +908,27 @@ bool nf_enabled(camelid_hip_engine* e) {
 
 // Before a call's decode steps (not inside a captured graph): the flag slots start cleared (a
 // step cut short by an error leaves one set) and the handoff error word is cleared.
+// The same for the attention's output-projection counters (one per layer).
 int nf_begin(camelid_hip_engine* e) {
-  if (!nf_enabled(e)) return 0;
+  const bool nf = nf_enabled(e), ao = ao_enabled(e);
+  if (!nf && !ao) return 0;
   static const uint32_t zero = 0;
-  HIP_TRY(e, hipMemsetAsync(e->nf_slots, 0, cm::NF_WORDS * 4, e->stream));
+  if (nf) HIP_TRY(e, hipMemsetAsync(e->nf_slots, 0, cm::NF_WORDS * 4, e->stream));
+  if (ao) HIP_TRY(e, hipMemsetAsync(e->ao_words, 0, ao_words(e) * 8, e->stream));
   HIP_TRY(e, hipMemcpyToSymbolAsync(HIP_SYMBOL(cm::g_handoff_error), &zero, 4, 0, hipMemcpyHostToDevice, e->stream));
   return 0;
 }
 // After the call's work is enqueued: the error word comes back with the call's own sync.
 int nf_end(camelid_hip_engine* e) {
-  if (e->nf_state != 1) return 0;
+  if (e->nf_state != 1 && e->ao_state != 1) return 0;
   HIP_TRY(e, hipMemcpyFromSymbolAsync(e->p_err, HIP_SYMBOL(cm::g_handoff_error), 4, 0, hipMemcpyDeviceToHost,
                                       e->stream));
   return 0;
 }
 int nf_failed(camelid_hip_engine* e) {
-  if (e->nf_state == 1 && *e->p_err) {
+  if ((e->nf_state == 1 || e->ao_state == 1) && *e->p_err) {
     e->filled = 0;
-    return fail(e, "norm-fused GEMV: a workgroup's wait for the norm workgroup timed out");
+    return fail(e, "in-launch handoff: a workgroup's wait for another workgroup of its launch timed out");
   }
   return 0;
 }
@@ -1019,11 +1062,20 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const f
     rmsnorm(e, L.attn_norm, &L.qkv);
     gemv(e, L.qkv, e->qkv, nullptr);
   }
-  {
-    ProfScope ps(e, P_ATTN, (nq + 2 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0));
-    decode_attention(e, l, cos_base, sin_base, rope_stride, scale, prefetch_of(e->read_ahead ? &L.o : nullptr));
+  const double att_bytes = (nq + 2 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0);
+  if (ao_enabled(e) && !att_split(e)) {
+    // the output projection's workgroups ride in the attention launch (attention + W_o bytes)
+    ProfScope ps(e, P_ATTN, att_bytes + q8_bytes(L.o, true));
+    const size_t nqw = (size_t)d.n_heads * d.head_dim / 4;
+    const cm::OProj op{L.o.q, L.o.d, (int)L.o.rows, (int)L.o.k, e->h, e->h, e->ao_words, e->ao_words + nqw, (int)l};
+    decode_attention(e, l, cos_base, sin_base, rope_stride, scale, cm::Prefetch{nullptr, 0, nullptr, 0}, op);
+  } else {
+    {
+      ProfScope ps(e, P_ATTN, att_bytes);
+      decode_attention(e, l, cos_base, sin_base, rope_stride, scale, prefetch_of(e->read_ahead ? &L.o : nullptr));
+    }
+    gemv(e, L.o, e->h, e->h);
   }
-  gemv(e, L.o, e->h, e->h);
   if (!gu_norm) rmsnorm(e, L.ffn_norm, &L.gu);
   if (e->gu_fused) {
     ProfScope ps(e, P_GEMV, q8_bytes(L.gu, false) - L.gu.rows * 4.0 + d.ffn_dim * 34.0 / 32.0 +
@@ -1448,6 +1500,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   e->att_slots = attn_ring_slots(e->kvs);
   if (const char* f = std::getenv("CAMELID_HIP_ATT_SPLIT")) e->att_split_min = (uint32_t)std::strtoul(f, nullptr, 10);
   if (const char* f = std::getenv("CAMELID_HIP_ATT_DG")) e->att_dg = std::atoi(f);
+  if (const char* f = std::getenv("CAMELID_HIP_ATT_O")) e->att_o_fused = std::atoi(f) != 0;
   const size_t nq = (size_t)d.n_heads * d.head_dim, nkv = (size_t)d.n_kv_heads * d.head_dim;
   const size_t kv_elems = (size_t)d.n_layers * d.n_kv_heads * e->kvs * d.head_dim;
   const size_t act = std::max<size_t>({(size_t)d.hidden, (size_t)d.ffn_dim, nq});
@@ -1468,7 +1521,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
            host_alloc(e, &e->p_emb, d.hidden) ||
            host_alloc(e, &e->p_cos, half) || host_alloc(e, &e->p_sin, half) || host_alloc(e, &e->p_logits, d.vocab) ||
            host_alloc(e, &e->p_st, 1) || host_alloc(e, &e->p_err, 1) ||
-           dev_alloc(e, &e->nf_slots, (size_t)cm::NF_WORDS);
+           dev_alloc(e, &e->nf_slots, (size_t)cm::NF_WORDS) || dev_alloc(e, &e->ao_words, ao_words(e));
   if (rc) {
     std::string m = e->err;
     camelid_hip_engine_free(e);
@@ -1477,7 +1530,8 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   // A fresh cache reads as zeros (K/V past `filled` are never read); StepState starts at 0.
   if (hipMemset(e->kc, 0, kv_elems * 2) != hipSuccess || hipMemset(e->vc, 0, kv_elems * 2) != hipSuccess ||
       hipMemset(e->st, 0, sizeof(cm::StepState)) != hipSuccess ||
-      hipMemset(e->nf_slots, 0, cm::NF_WORDS * 4) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+      hipMemset(e->nf_slots, 0, cm::NF_WORDS * 4) != hipSuccess || hipMemset(e->ao_words, 0, ao_words(e) * 8) != hipSuccess ||
+      hipDeviceSynchronize() != hipSuccess) {
     camelid_hip_engine_free(e);
     return fail(nullptr, "initial device memset failed");
   }

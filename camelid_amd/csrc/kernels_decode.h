@@ -67,6 +67,25 @@ __device__ __forceinline__ uint16_t ld_stream(const uint16_t* p) {
 #endif
 }
 
+// Agent-scope (device-coherent across XCDs) loads and stores for data handed between the
+// workgroups of one launch: they bypass the XCD-private L2 copies that plain accesses may hit.
+__device__ __forceinline__ uint64_t ld_agent64(const void* p) {
+  return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_agent32(const void* p) {
+  return __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent64(void* p, uint64_t v) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent32(void* p, uint32_t v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Set by a workgroup whose bounded wait for another workgroup of its launch ran out (the
+// in-launch handoffs of the norm-fused K-quant GEMVs and of the attention's output
+// projection); the engine clears it before a call's decode steps and reads it after them.
+__device__ uint32_t g_handoff_error;
+
 __device__ __forceinline__ int dot4x4(int4 w, int4 x, int acc) {
   acc = __builtin_amdgcn_sdot4(w.x, x.x, acc, false);
   acc = __builtin_amdgcn_sdot4(w.y, x.y, acc, false);
@@ -2075,16 +2094,135 @@ __device__ __forceinline__ float att_onepass_sum(const float* v, int P, FsLds<NT
 }
 
 
+// ---------------------------------------------------------------------------
+// The output projection inside the decode attention launch (att . W_o^T + residual, the
+// Q8_0 GEMV k_gemv_k computes after the attention: q8_gemv with the residual add,
+// cuda_resident.rs:230; CPU inference.rs:19871-19905).  The attention occupies one CU per
+// workgroup for its whole duration while the HBM stream idles, so the launch carries
+// ceil(rows / 16) more workgroups that load their W_o rows (one per wave) at once and then
+// read the Q8_0 activation as the attention workgroups publish it, and run k_gemv_k's dots
+// and block-ordered folds: the same terms in the same order, so the same bits.
+// Handoff: the attention workgroups store their quants (four to a word) and block scales as
+// 8-byte words whose high half is a tag, ao_tag(pos, layer), with agent-scope (cross-XCD
+// coherent) stores; a projection workgroup's thread 0 first watches one scale word, then every
+// thread reads its words with agent-scope loads until each carries the tag.  One tag per
+// (position, layer): the engine clears the words before a call's decode steps, and within a
+// call every (position, layer) is computed once.  The wait is bounded: past about 2^18 polls
+// per word the workgroup sets g_handoff_error and computes from whatever it read.
+constexpr int AO_ROWS = 16;  // rows per projection workgroup (one per wave)
+struct OProj {
+  const int8_t* q;      // W_o quants [rows][K] (null: no projection in this launch)
+  const uint16_t* d;    // W_o f16 block scales [rows][K / 32]
+  int rows, K;          // K = n_heads * head_dim
+  float* y;             // y[r] = resid[r] + (W_o att)[r]
+  const float* resid;
+  uint64_t* xq_t;       // [K / 4] tagged quant words
+  uint64_t* xs_t;       // [K / 32] tagged block scales
+  int layer;
+};
+__host__ __device__ constexpr uint32_t ao_tag(uint32_t pos, uint32_t layer) { return ((pos + 1u) << 8) | layer; }
+__host__ __device__ constexpr size_t ao_lds_bytes(int K) {
+  return (size_t)K + (size_t)(K / 32) * 4 + (size_t)AO_ROWS * gemv_term_stride(K / 32) * 4;
+}
+
+__device__ __forceinline__ uint64_t ao_wait_word(const uint64_t* p, uint32_t tag) {
+  uint64_t v = ld_agent64(p);
+  uint32_t polls = 0;
+  while ((uint32_t)(v >> 32) != tag) {
+    __builtin_amdgcn_s_sleep(1);
+    if (++polls == (1u << 18)) {
+      g_handoff_error = 1u;
+      break;
+    }
+    v = ld_agent64(p);
+  }
+  return v;
+}
+
+template <int K, int NT>
+__device__ __forceinline__ void att_oproj_rows(const OProj& op, int wg, uint32_t tag, unsigned char* smem) {
+  constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64, STRIDE = gemv_term_stride(NB);
+  static_assert(NT / 64 == AO_ROWS && K % 128 == 0, "one row per wave, whole 128-value groups");
+  uint32_t* xl = reinterpret_cast<uint32_t*>(smem);
+  float* xsl = reinterpret_cast<float*>(smem + K);
+  float* t = xsl + NB;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int row0 = wg * AO_ROWS;
+  // this wave's row: every weight and scale load first (rows past the end clamped; their
+  // results are never stored)
+  int4 wv[IT];
+  uint16_t dv[IT];
+  {
+    const int row = min(row0 + wave, op.rows - 1);
+    const int4* w4 = reinterpret_cast<const int4*>(op.q + (size_t)row * K);
+    const uint16_t* dp = op.d + (size_t)row * NB;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int c = min(lane + 64 * i, CPR - 1);
+      wv[i] = ld_stream(w4 + c);
+      dv[i] = ld_stream(dp + (c >> 1));
+    }
+  }
+  // one watcher until a scale word carries the tag (the heads finish together), then every
+  // word by its own thread
+  if (tid == 0) (void)ao_wait_word(op.xs_t + (blockIdx.x % NB), tag);
+  __syncthreads();
+  for (int c = tid; c < K / 4 + NB; c += NT) {
+    if (c < K / 4)
+      xl[c] = (uint32_t)ao_wait_word(op.xq_t + c, tag);
+    else
+      xsl[c - K / 4] = __uint_as_float((uint32_t)ao_wait_word(op.xs_t + (c - K / 4), tag));
+  }
+  __syncthreads();
+  float* tr = t + wave * STRIDE;
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int c = lane + 64 * i;
+    const int cc = min(c, CPR - 1);
+    int s = dot4x4(wv[i], reinterpret_cast<const int4*>(xl)[cc], 0);
+    s += dpp_xor1(s);
+    if ((lane & 1) == 0 && c < CPR) tr[c >> 1] = ((float)s * half_bits_to_float(dv[i])) * xsl[c >> 1];
+  }
+  __syncthreads();
+  if (tid < AO_ROWS && row0 + tid < op.rows) {
+    const float acc = fold_lds_n<NB>(t + tid * STRIDE);
+    op.y[row0 + tid] = op.resid[row0 + tid] + acc;
+  }
+}
+
+// The attention's widths n_heads * head_dim with an instantiated projection body.
+__host__ __device__ constexpr bool ao_width_ok(int K) { return K == 2048 || K == 3072 || K == 4096; }
+
+template <int NT>
+__device__ __forceinline__ void att_oproj(const OProj& op, int wg, uint32_t tag, unsigned char* smem) {
+  switch (op.K) {
+    case 2048:
+      att_oproj_rows<2048, NT>(op, wg, tag, smem);
+      break;
+    case 3072:
+      att_oproj_rows<3072, NT>(op, wg, tag, smem);
+      break;
+    case 4096:
+      att_oproj_rows<4096, NT>(op, wg, tag, smem);
+      break;
+    default:
+      break;
+  }
+}
+
 // DG workgroups per query head (the grid is n_heads * DG): each computes the head's scores,
 // softmax and denominator (the same bits in every one of them) and the output sums of its
 // HD / DG dims, so that a CU stages 1/DG of the head's V rows; one of them stores the K/V row.
+// With op.q set, ceil(op.rows / 16) more workgroups compute the output projection (att_oproj).
 template <int HD, bool FUSED, int DG = 1>
 __global__ __launch_bounds__(att_nt(HD)) void k_attention(
     const float* __restrict__ qsrc, int n_heads, int n_kv, int rope_dim, int split_half,
     const float* __restrict__ cos_base, const float* __restrict__ sin_base, int rope_stride,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm, float eps, uint16_t* __restrict__ kc,
     uint16_t* __restrict__ vc, int layer, int kvs, const uint32_t* __restrict__ d_pos, float scale,
-    float* __restrict__ att_out, int8_t* __restrict__ xq, float* __restrict__ xs, int ring_slots, Prefetch pf) {
+    float* __restrict__ att_out, int8_t* __restrict__ xq, float* __restrict__ xs, int ring_slots, Prefetch pf,
+    OProj op) {
   constexpr int ATT_NT = att_nt(HD);
   static_assert(HD % 64 == 0 && HD <= 256, "head_dim must be 64, 128 or 256");
   constexpr int R8 = HD / 8;  // 16-byte granules per K row
@@ -2098,7 +2236,17 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   extern __shared__ __align__(16) float4 dyn[];
   float4* ring = dyn;  // ring_slots chunks of ATT_RING_GRANULES V granules
   float* sc = reinterpret_cast<float*>(dyn + (size_t)ring_slots * ATT_RING_GRANULES);
-  if ((int)blockIdx.x >= n_heads * DG) {  // spare workgroups: read ahead the output projection
+  if ((int)blockIdx.x >= n_heads * DG) {
+    if constexpr (ATT_NT == AO_ROWS * 64) {
+      if (op.q) {  // the output projection's workgroups
+        const int pos = (int)*d_pos;
+        if (kv_pos_bad(pos, kvs)) return;
+        att_oproj<ATT_NT>(op, (int)blockIdx.x - n_heads * DG, ao_tag((uint32_t)pos, (uint32_t)op.layer),
+                          reinterpret_cast<unsigned char*>(dyn));
+        return;
+      }
+    }
+    // spare workgroups: read ahead the output projection
     prefetch_lines(pf, blockIdx.x - n_heads * DG, gridDim.x - n_heads * DG, sc);
     return;
   }
@@ -2473,13 +2621,26 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
   }
   // (each output lane stores and quantizes its own value: no barrier; the Q8_0 block's
   // scale is formed by lane shuffles within the 32-lane group)
+  const bool publish = ATT_NT == AO_ROWS * 64 && op.q != nullptr;
   if (tid < OD) {
     if (team_bad) res = __builtin_nanf("");  // (the team barrier's bound was reached: no result)
-    att_out[(size_t)h * HD + d0 + tid] = res;
+    const size_t o = (size_t)h * HD + d0 + tid;
+    att_out[o] = res;
     int8_t q;
     const float dd = quantize_lane32(res, &q);
-    xq[(size_t)h * HD + d0 + tid] = q;
-    if ((tid & 31) == 0) xs[((size_t)h * HD + d0 + tid) >> 5] = dd;
+    if (publish) {
+      // for the projection workgroups of this launch: four lanes' quants in one word, and the
+      // block scale, each with the tag in its high half, by agent-scope stores
+      const uint64_t tg = (uint64_t)ao_tag((uint32_t)pos, (uint32_t)op.layer) << 32;
+      const uint32_t b = (uint32_t)(uint8_t)q;
+      const uint32_t w = b | ((uint32_t)__shfl_down((int)b, 1) << 8) | ((uint32_t)__shfl_down((int)b, 2) << 16) |
+                         ((uint32_t)__shfl_down((int)b, 3) << 24);
+      if ((tid & 3) == 0) st_agent64(op.xq_t + (o >> 2), tg | w);
+      if ((tid & 31) == 0) st_agent64(op.xs_t + (o >> 5), tg | __float_as_uint(dd));
+    } else {
+      xq[o] = q;
+      if ((tid & 31) == 0) xs[o >> 5] = dd;
+    }
   }
   CM_ATT_STAMP(6)
 }

@@ -87,20 +87,6 @@ __host__ __device__ inline int kq_rows_per_wg(int rpw) { return 4 * rpw; }
 // is bounded (about a second): past it the workgroup sets g_handoff_error and goes on.
 constexpr int NF_XCD = 8, NF_STRIDE = 32;  // flag copies per slot, words between copies
 constexpr int NF_WORDS = 2 * NF_XCD * NF_STRIDE;
-__device__ uint32_t g_handoff_error;
-
-__device__ __forceinline__ uint64_t ld_agent64(const void* p) {
-  return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t ld_agent32(const void* p) {
-  return __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_agent64(void* p, uint64_t v) {
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_agent32(void* p, uint32_t v) {
-  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // The waiting side: thread 0 polls its XCD's copy of the slot, then the workgroup barrier.
 __device__ __forceinline__ void handoff_wait(const uint32_t* slot) {

@@ -75,13 +75,15 @@ def test_config_stream_matches_golden(name):
 
 @pytest.mark.parametrize("switch,value", [("CAMELID_HIP_FUSED_GU", "0"), ("CAMELID_HIP_FUSED_NORM", "0"),
                                           ("CAMELID_HIP_READ_AHEAD", "1"), ("CAMELID_HIP_GRAPHS", "0"),
-                                          ("CAMELID_HIP_KV_AHEAD", "1"), ("CAMELID_HIP_ATT_DG", "2")])
+                                          ("CAMELID_HIP_KV_AHEAD", "1"), ("CAMELID_HIP_ATT_DG", "2"),
+                                          ("CAMELID_HIP_ATT_O", "0")])
 def test_switch_off_keeps_tinyllama_stream(monkeypatch, switch, value):
     """Each documented switch of the Q8_0 decode path set away from its default (the separate
     RMSNorm launch, the separate SwiGLU launch, the weight read-ahead workgroups, launches
     without a graph, the KV rows read by the qkv launch's idle waves, two attention workgroups
-    per head of 64 dims instead of one): the TinyLlama golden stream (configs[0], 128 + 128) is
-    still reproduced by the device loop."""
+    per head of 64 dims instead of one, the output projection as its own launch instead of
+    inside the attention launch): the TinyLlama golden stream (configs[0], 128 + 128) is still
+    reproduced by the device loop."""
     monkeypatch.setenv(switch, value)
     test_config_stream_matches_golden("tinyllama-1.1b")
 
