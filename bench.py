@@ -276,15 +276,27 @@ def attention_phases(cfg) -> dict:
     and the launch span (first start to last end), in microseconds."""
     import ctypes as C
     from camelid_amd import _native as N
-    na, ng, nsp = 64 * 64 * 9, 2 * 256 * 13, 2 * 1024 * 8
-    buf = (C.c_uint64 * (na + ng + nsp))()
+    na, ng, nsp, nao = 64 * 64 * 9, 2 * 256 * 13, 2 * 1024 * 8, 64 * 2 * 4
+    buf = (C.c_uint64 * (na + ng + nsp + nao))()
     got = C.c_size_t(0)
-    N.check(N.lib().camelid_hip_phase_stamps(buf, na + ng + nsp, C.byref(got)))
+    N.check(N.lib().camelid_hip_phase_stamps(buf, na + ng + nsp + nao, C.byref(got)))
     allst = np.frombuffer(buf, np.uint64).astype(np.int64)
     st = allst[:na].reshape(64, 64, 9)[:cfg.n_layers, :cfg.n_heads]
     res = {}
     if (st[:, :, 0] > 0).all():  # (the single-workgroup attention ran; else the split one did)
         res.update(fused_attention_phases(st))
+        # the output projection's workgroups of the same launches (first and last workgroup),
+        # from the attention workgroups' first start and last end of each layer
+        ao = allst[na + ng + nsp:].reshape(64, 2, 4)[:cfg.n_layers]
+        if (ao[:, :, 0] > 0).all():
+            a0, a1 = st[:, :, 0].min(1)[:, None], st[:, :, 6].max(1)[:, None]
+            ph = {"start_from_attention_start": float((ao[:, :, 0] - a0).mean() * 0.01),
+                  "tag_seen_from_attention_end": float((ao[:, :, 1] - a1).mean() * 0.01),
+                  "staged_from_attention_end": float((ao[:, :, 2] - a1).mean() * 0.01),
+                  "end_from_attention_end": float((ao[:, :, 3] - a1).mean() * 0.01),
+                  "last_end_from_attention_start": float((ao[:, :, 3].max(1)[:, None] - a0).mean() * 0.01)}
+            res["output_projection"] = {k: round(v, 3) for k, v in ph.items()}
+            log("output projection workgroups (us): " + ", ".join(f"{k} {v:.3f}" for k, v in ph.items()))
     # the norm-fused GEMVs of the last layer (mean over the workgroups that recorded)
     gs = allst[na:na + ng].reshape(2, 256, 13)
     kquant = cfg.quant_scheme != "q8_0"
@@ -315,7 +327,7 @@ def attention_phases(cfg) -> dict:
         log(f"{name} phases (us from each workgroup's start): " +
             ", ".join(f"{k} {v:.3f}" for k, v in ph.items() if v is not None))
     # the split attention (when it ran in the last layer)
-    sp = allst[na + ng:].reshape(2, 1024, 8)
+    sp = allst[na + ng:na + ng + nsp].reshape(2, 1024, 8)
     for kind, name, labels in ((0, "att_scores_split", ("q_built", "scores_done", "end")),
                                (1, "att_out_split", ("scores_max", "exp", "denominator", "output_sums", "end"))):
         g = sp[kind]

@@ -116,6 +116,12 @@ struct camelid_hip_engine {
   uint32_t att_split_min = 1024;
   float* att_sc = nullptr;
   float* att_mx = nullptr;
+  // the split attention as one launch (cm::k_att_fused: score slices, output workgroups and,
+  // for Q8_0 layers, the output projection, handing over through tagged words;
+  // CAMELID_HIP_ATT_FUSED_SPLIT=0: the two launches) and its tagged scores [n_heads][kvs]
+  bool att_fsplit = true;
+  uint64_t* att_sct = nullptr;
+  uint32_t n_cus = 256;  // compute units of the device (read at creation)
   int att_mode = -1;       // -1: by position; 0 / 1: single / split (graph capture)
   // Read-ahead (off by default): spare workgroups of the norm and attention kernels read the
   // next projection's weights towards the caches; the qkv GEMV's idle norm waves read the
@@ -141,6 +147,7 @@ struct camelid_hip_engine {
   int ao_state = -1;              // -1 unknown, 0 off, 1 on
   uint64_t* ao_words = nullptr;   // the tagged activation words (ao_words())
   uint32_t* p_err = nullptr;      // host copy of the handoff error word
+  bool err_pending = false;       // nf_end enqueued its copy in the current call
   float *h = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr;
   float *logits = nullptr, *hidden_cap = nullptr, *xs = nullptr;
   float *cos_cur = nullptr, *sin_cur = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
@@ -223,8 +230,10 @@ int dev_alloc(camelid_hip_engine* e, T** p, size_t count) {
 template <typename T>
 int host_alloc(camelid_hip_engine* e, T** p, size_t count) {
   void* v = nullptr;
-  hipError_t st = hipHostMalloc(&v, std::max<size_t>(count * sizeof(T), 64), hipHostMallocDefault);
+  const size_t bytes = std::max<size_t>(count * sizeof(T), 64);
+  hipError_t st = hipHostMalloc(&v, bytes, hipHostMallocDefault);
   if (st != hipSuccess) return fail(e, std::string("hipHostMalloc failed: ") + hipGetErrorString(st));
+  std::memset(v, 0, bytes);  // (pinned pages may be reused from an earlier allocation)
   e->host_allocs.push_back(v);
   *p = static_cast<T*>(v);
   return 0;
@@ -647,6 +656,50 @@ void launch_attention_split(uint32_t hd, uint32_t n_heads, int slots, hipStream_
 #undef CM_ATTS
 }
 
+// The one-launch split attention (cm::k_att_fused): score slices of 128 positions up to 1024
+// cache positions (more CUs stream a head's K), of one workgroup's threads beyond; output
+// workgroups as k_att_out's; the output projection's workgroups when op.q is set.
+int fsplit_sl(uint32_t kvs, uint32_t hd) { return kvs <= 1024 ? 128 : cm::att_nt((int)hd); }
+bool fsplit_supported(uint32_t hd) { return hd == 64 || hd == 128; }
+void launch_attention_fused(uint32_t hd, uint32_t n_heads, int slots, hipStream_t s, const float* qsrc, int nh,
+                            int nkv, int rope_dim, int split_half, const float* cb, const float* sb, int rs,
+                            const float* qn, const float* kn, float eps, uint16_t* kc, uint16_t* vc, int layer,
+                            int kvs, const uint32_t* pos, float scale, uint64_t* sct, float* att,
+                            int8_t* xq, float* xs, cm::OProj op) {
+  if (!fsplit_supported(hd)) {
+    g_launch_error = "fused split attention: head_dim " + std::to_string(hd) + " has no instantiation";
+    return;
+  }
+  const int sl = fsplit_sl((uint32_t)kvs, hd);
+  const int nsl = (kvs + sl - 1) / sl;
+  int pb = 0;
+  const int so = attn_out_slots((uint32_t)kvs, slots, &pb);
+  size_t lds = (size_t)so * cm::ATT_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs) + cm::avp_bytes(pb);
+  uint32_t grid = n_heads * (uint32_t)nsl + n_heads * (hd / 32);
+  if (op.q) {
+    if (cm::att_nt((int)hd) != cm::AO_ROWS * 64 || !cm::ao_width_ok(op.K) || op.K != (int)(n_heads * hd)) {
+      g_launch_error = "attention: no output projection body for this shape";
+      return;
+    }
+    grid += (uint32_t)(op.rows + cm::AO_ROWS - 1) / cm::AO_ROWS;
+    lds = std::max(lds, cm::ao_lds_bytes(op.K));
+  }
+#define CM_ATTF(HD, PB, SL)                                                                                    \
+  CM_LAUNCH((cm::k_att_fused<HD, PB, SL>), dim3(grid), dim3(cm::att_nt(HD)), lds, s, qsrc, nh, nkv, rope_dim,    \
+            split_half, cb, sb, rs, qn, kn, eps, kc, vc, layer, kvs, pos, scale, sct, nsl, att, xq, xs, so, op)
+#define CM_ATTF_PB(HD, SL)           \
+  if (pb == 256) CM_ATTF(HD, 256, SL); \
+  else if (pb == 128) CM_ATTF(HD, 128, SL); \
+  else CM_ATTF(HD, 64, SL);
+  if (hd == 64) {
+    if (sl == 128) { CM_ATTF_PB(64, 128) } else { CM_ATTF_PB(64, 1024) }
+  } else {
+    if (sl == 128) { CM_ATTF_PB(128, 128) } else { CM_ATTF_PB(128, 1024) }
+  }
+#undef CM_ATTF_PB
+#undef CM_ATTF
+}
+
 // The attention of this step: the split kernels from att_split_min positions on.
 bool att_split(const camelid_hip_engine* e) {
   if (e->att_mode >= 0) return e->att_mode == 1;
@@ -701,6 +754,13 @@ long attn_static_lds() {
     m = std::max<long>(m, ATT_STATIC_LDS_BOUND);
     CM_ATTO_LDS(64) CM_ATTO_LDS(128) CM_ATTO_LDS(256)
 #undef CM_ATTO_LDS
+#define CM_ATTF_LDS(HD, SL)                                                                                 \
+  if (hipFuncGetAttributes(&a, reinterpret_cast<const void*>(&cm::k_att_fused<HD, 64, SL>)) == hipSuccess) \
+    m = std::max<long>(m, (long)a.sharedSizeBytes);                                                         \
+  else                                                                                                      \
+    m = std::max<long>(m, ATT_STATIC_LDS_BOUND);
+    CM_ATTF_LDS(64, 128) CM_ATTF_LDS(64, 1024) CM_ATTF_LDS(128, 128) CM_ATTF_LDS(128, 1024)
+#undef CM_ATTF_LDS
     bytes = m;
   }
   return bytes;
@@ -838,13 +898,31 @@ void proj(camelid_hip_engine* e, const Proj& p, float* y, const float* resid, co
   launch_kgemv(p.kq, e->kd, e->kq, e->kbs, y, resid, nullptr, nullptr, e->stream, xf);
 }
 
+// Whether the split attention runs as one launch (k_att_fused): on by default where it is
+// instantiated, and only with the read-ahead off (the two-launch path keeps its read-ahead).
+// The launch's score and output workgroups must also fit on the device's CUs at once (one
+// workgroup per CU): with more score slices than that (C4's 8K context: 288 score + 128 output
+// workgroups) the output workgroups start only as score workgroups retire, and the two launches
+// measured faster (212.1 vs 204.1 tok/s); within it the one launch is (C5 372.0 vs 365.3).
+bool att_fused_split(const camelid_hip_engine* e) {
+  if (!(e->att_fsplit && fsplit_supported(e->d.head_dim) && !e->read_ahead && e->att_sct)) return false;
+  const uint32_t sl = (uint32_t)fsplit_sl(e->kvs, e->d.head_dim);
+  const uint32_t wgs = e->d.n_heads * ((e->kvs + sl - 1) / sl) + e->d.n_heads * (e->d.head_dim / 32);
+  return wgs <= e->n_cus;
+}
+
 // The decode attention of layer l for the token at StepState.pos (QK-norm, RoPE and the K/V
 // store fused): one workgroup per head, or the split kernels for long contexts.
 void decode_attention(camelid_hip_engine* e, uint32_t l, const float* cos_base, const float* sin_base,
                       int rope_stride, float scale, cm::Prefetch pf, cm::OProj op = cm::OProj{}) {
   const camelid_hip_dims& d = e->d;
   const LayerW& L = e->layers[l];
-  if (att_split(e))
+  if (att_split(e) && att_fused_split(e))
+    launch_attention_fused(d.head_dim, d.n_heads, e->att_slots, e->stream, e->qkv, (int)d.n_heads, (int)d.n_kv_heads,
+                           (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base, rope_stride, L.q_norm,
+                           L.k_norm, d.eps, e->kc, e->vc, (int)l, (int)e->kvs, &e->st->pos, scale, e->att_sct,
+                           e->att, e->xq, e->xs, op);
+  else if (att_split(e))
     launch_attention_split<true>(d.head_dim, d.n_heads, e->att_slots, e->stream, e->qkv, (int)d.n_heads,
                                  (int)d.n_kv_heads, (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base,
                                  rope_stride, L.q_norm, L.k_norm, d.eps, e->kc, e->vc, (int)l, (int)e->kvs,
@@ -910,8 +988,9 @@ bool nf_enabled(camelid_hip_engine* e) {
 // step cut short by an error leaves one set) and the handoff error word is cleared.
 // The same for the attention's output-projection counters (one per layer).
 int nf_begin(camelid_hip_engine* e) {
-  const bool nf = nf_enabled(e), ao = ao_enabled(e);
-  if (!nf && !ao) return 0;
+  const bool nf = nf_enabled(e), ao = ao_enabled(e), fs = att_fused_split(e);
+  if (fs) HIP_TRY(e, hipMemsetAsync(e->att_sct, 0, (size_t)e->d.n_heads * e->kvs * 8, e->stream));
+  if (!nf && !ao && !fs) return 0;
   static const uint32_t zero = 0;
   if (nf) HIP_TRY(e, hipMemsetAsync(e->nf_slots, 0, cm::NF_WORDS * 4, e->stream));
   if (ao) HIP_TRY(e, hipMemsetAsync(e->ao_words, 0, ao_words(e) * 8, e->stream));
@@ -920,13 +999,17 @@ int nf_begin(camelid_hip_engine* e) {
 }
 // After the call's work is enqueued: the error word comes back with the call's own sync.
 int nf_end(camelid_hip_engine* e) {
-  if (e->nf_state != 1 && e->ao_state != 1) return 0;
+  if (e->nf_state != 1 && e->ao_state != 1 && !att_fused_split(e)) return 0;
   HIP_TRY(e, hipMemcpyFromSymbolAsync(e->p_err, HIP_SYMBOL(cm::g_handoff_error), 4, 0, hipMemcpyDeviceToHost,
                                       e->stream));
+  e->err_pending = true;
   return 0;
 }
+// After the call's sync: only a word that nf_end asked for in this call is read.
 int nf_failed(camelid_hip_engine* e) {
-  if ((e->nf_state == 1 || e->ao_state == 1) && *e->p_err) {
+  const bool pending = e->err_pending;
+  e->err_pending = false;
+  if (pending && *e->p_err) {
     e->filled = 0;
     return fail(e, "in-launch handoff: a workgroup's wait for another workgroup of its launch timed out");
   }
@@ -1063,7 +1146,7 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const f
     gemv(e, L.qkv, e->qkv, nullptr);
   }
   const double att_bytes = (nq + 2 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0);
-  if (ao_enabled(e) && !att_split(e)) {
+  if (ao_enabled(e) && (!att_split(e) || att_fused_split(e))) {
     // the output projection's workgroups ride in the attention launch (attention + W_o bytes)
     ProfScope ps(e, P_ATTN, att_bytes + q8_bytes(L.o, true));
     const size_t nqw = (size_t)d.n_heads * d.head_dim / 4;
@@ -1501,6 +1584,12 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   if (const char* f = std::getenv("CAMELID_HIP_ATT_SPLIT")) e->att_split_min = (uint32_t)std::strtoul(f, nullptr, 10);
   if (const char* f = std::getenv("CAMELID_HIP_ATT_DG")) e->att_dg = std::atoi(f);
   if (const char* f = std::getenv("CAMELID_HIP_ATT_O")) e->att_o_fused = std::atoi(f) != 0;
+  if (const char* f = std::getenv("CAMELID_HIP_ATT_FUSED_SPLIT")) e->att_fsplit = std::atoi(f) != 0;
+  {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device) == hipSuccess && cus > 0)
+      e->n_cus = (uint32_t)cus;
+  }
   const size_t nq = (size_t)d.n_heads * d.head_dim, nkv = (size_t)d.n_kv_heads * d.head_dim;
   const size_t kv_elems = (size_t)d.n_layers * d.n_kv_heads * e->kvs * d.head_dim;
   const size_t act = std::max<size_t>({(size_t)d.hidden, (size_t)d.ffn_dim, nq});
@@ -1518,6 +1607,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
            dev_alloc(e, &e->kd, act / 256 + 1) || dev_alloc(e, &e->kq, act) || dev_alloc(e, &e->kbs, act / 32) ||
            dev_alloc(e, &e->att_sc, (size_t)d.n_heads * e->kvs) ||
            dev_alloc(e, &e->att_mx, (size_t)d.n_heads * ((e->kvs + 255) / 256)) ||
+           dev_alloc(e, &e->att_sct, (size_t)d.n_heads * e->kvs) ||
            host_alloc(e, &e->p_emb, d.hidden) ||
            host_alloc(e, &e->p_cos, half) || host_alloc(e, &e->p_sin, half) || host_alloc(e, &e->p_logits, d.vocab) ||
            host_alloc(e, &e->p_st, 1) || host_alloc(e, &e->p_err, 1) ||
@@ -2040,10 +2130,12 @@ int camelid_hip_phase_stamps(uint64_t* out, size_t n, size_t* n_out) {
   const size_t na = (size_t)cm::ATT_STAMP_LAYERS * cm::ATT_STAMP_HEADS * cm::ATT_NSTAMP;
   const size_t ng = (size_t)2 * cm::GEMV_STAMP_WGS * cm::GEMV_NSTAMP;
   const size_t nsp = (size_t)2 * cm::SPLIT_STAMP_WGS * cm::SPLIT_NSTAMP;
-  const size_t total = na + ng + nsp;
+  const size_t nao = (size_t)cm::ATT_STAMP_LAYERS * 2 * cm::AO_NSTAMP;
+  const size_t total = na + ng + nsp + nao;
 #ifdef CM_STAMPS
   G_TRY(hipDeviceSynchronize());
-  const size_t m1 = std::min(n, na), m2 = std::min(n - m1, ng), m3 = std::min(n - m1 - m2, nsp);
+  const size_t m1 = std::min(n, na), m2 = std::min(n - m1, ng), m3 = std::min(n - m1 - m2, nsp),
+               m4 = std::min(n - m1 - m2 - m3, nao);
   G_TRY(hipMemcpyFromSymbol(out, HIP_SYMBOL(cm::g_att_stamps), m1 * sizeof(uint64_t), 0, hipMemcpyDeviceToHost));
   if (m2)
     G_TRY(hipMemcpyFromSymbol(out + m1, HIP_SYMBOL(cm::g_gemv_stamps), m2 * sizeof(uint64_t), 0,
@@ -2051,7 +2143,10 @@ int camelid_hip_phase_stamps(uint64_t* out, size_t n, size_t* n_out) {
   if (m3)
     G_TRY(hipMemcpyFromSymbol(out + m1 + m2, HIP_SYMBOL(cm::g_split_stamps), m3 * sizeof(uint64_t), 0,
                               hipMemcpyDeviceToHost));
-  *n_out = m1 + m2 + m3;
+  if (m4)
+    G_TRY(hipMemcpyFromSymbol(out + m1 + m2 + m3, HIP_SYMBOL(cm::g_ao_stamps), m4 * sizeof(uint64_t), 0,
+                              hipMemcpyDeviceToHost));
+  *n_out = m1 + m2 + m3 + m4;
   return 0;
 #else
   (void)n;

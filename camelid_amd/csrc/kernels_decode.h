@@ -2073,9 +2073,10 @@ __device__ __forceinline__ float att_seg_sum(const float* v, uint32_t* ps, int P
 }
 
 // Softmax denominator by the one-pass exact in-order sum for ATT_FOLD_MAX <= P <= NT *
-// ATT_ONEPASS_C positions (C = P / NT rounded up to a power of two); below, a serial fold
+// ATT_ONEPASS_C positions (C = P / NT rounded up to a power of two: up to 16 positions per
+// thread, 16384 at 1024 threads); below, a serial fold
 // by one lane is faster (measured: 2.0 us fold vs 2.9 us one-pass at P = 560).
-constexpr int ATT_ONEPASS_C = 8;
+constexpr int ATT_ONEPASS_C = 16;
 constexpr int ATT_FOLD_MAX = 1024;
 template <int NT>
 __device__ __forceinline__ float att_onepass_sum(const float* v, int P, FsLds<NT>& fs) {
@@ -2089,7 +2090,8 @@ __device__ __forceinline__ float att_onepass_sum(const float* v, int P, FsLds<NT
   if (P <= NT) CM_AOP(1)
   if (P <= NT * 2) CM_AOP(2)
   if (P <= NT * 4) CM_AOP(4)
-  CM_AOP(8)
+  if (P <= NT * 8) CM_AOP(8)
+  CM_AOP(16)
 #undef CM_AOP
 }
 
@@ -2110,6 +2112,17 @@ __device__ __forceinline__ float att_onepass_sum(const float* v, int P, FsLds<NT
 // call every (position, layer) is computed once.  The wait is bounded: past about 2^18 polls
 // per word the workgroup sets g_handoff_error and computes from whatever it read.
 constexpr int AO_ROWS = 16;  // rows per projection workgroup (one per wave)
+// (measurement build: thread 0 of the first and the last projection workgroup of layer l
+// records 0 start, 1 watched word tagged, 2 activation staged, 3 end into g_ao_stamps[l][0|1])
+constexpr int AO_NSTAMP = 4;
+#ifdef CM_STAMPS
+__device__ uint64_t g_ao_stamps[64 * 2 * AO_NSTAMP];
+#define CM_AO_STAMP(i)                                                                                  \
+  if (threadIdx.x == 0 && op.layer < 64 && (wg == 0 || wg == (int)gridDim.x - 1 - (int)(blockIdx.x - wg))) \
+    g_ao_stamps[((size_t)op.layer * 2 + (wg != 0)) * AO_NSTAMP + (i)] = __builtin_amdgcn_s_memrealtime();
+#else
+#define CM_AO_STAMP(i)
+#endif
 struct OProj {
   const int8_t* q;      // W_o quants [rows][K] (null: no projection in this launch)
   const uint16_t* d;    // W_o f16 block scales [rows][K / 32]
@@ -2148,6 +2161,7 @@ __device__ __forceinline__ void att_oproj_rows(const OProj& op, int wg, uint32_t
   float* t = xsl + NB;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int row0 = wg * AO_ROWS;
+  CM_AO_STAMP(0)
   // this wave's row: every weight and scale load first (rows past the end clamped; their
   // results are never stored)
   int4 wv[IT];
@@ -2166,6 +2180,7 @@ __device__ __forceinline__ void att_oproj_rows(const OProj& op, int wg, uint32_t
   // one watcher until a scale word carries the tag (the heads finish together), then every
   // word by its own thread
   if (tid == 0) (void)ao_wait_word(op.xs_t + (blockIdx.x % NB), tag);
+  CM_AO_STAMP(1)
   __syncthreads();
   for (int c = tid; c < K / 4 + NB; c += NT) {
     if (c < K / 4)
@@ -2174,6 +2189,7 @@ __device__ __forceinline__ void att_oproj_rows(const OProj& op, int wg, uint32_t
       xsl[c - K / 4] = __uint_as_float((uint32_t)ao_wait_word(op.xs_t + (c - K / 4), tag));
   }
   __syncthreads();
+  CM_AO_STAMP(2)
   float* tr = t + wave * STRIDE;
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
@@ -2189,6 +2205,7 @@ __device__ __forceinline__ void att_oproj_rows(const OProj& op, int wg, uint32_t
     const float acc = fold_lds_n<NB>(t + tid * STRIDE);
     op.y[row0 + tid] = op.resid[row0 + tid] + acc;
   }
+  CM_AO_STAMP(3)
 }
 
 // The attention's widths n_heads * head_dim with an instantiated projection body.
@@ -2660,15 +2677,20 @@ __global__ __launch_bounds__(att_nt(HD)) void k_attention(
 //                 chunks hold 512 positions of those 32 dims (its first chunks issued behind
 //                 the scores loads), and quantizes them (one Q8_0 block).  Every position's V
 //                 comes from the cache (k_att_scores stored pos).
-template <int HD, bool FUSED, int NT>
-__global__ __launch_bounds__(NT) void k_att_scores(
-    const float* __restrict__ qsrc, int n_heads, int n_kv, int rope_dim, int split_half,
+// Score slice s of head h: positions [s SL, (s + 1) SL) by threads 0 .. SL - 1 of the NT
+// threads.  TAG: each score goes out as soon as it is formed, as a tagged word (sc_t[h][p]:
+// the value's bits, tag << 32) by an agent-scope store, for the output workgroups of the same
+// launch (k_att_fused), which take the maximum themselves; else the scores and the slice
+// maximum as plain floats (g_sc, g_max).
+template <int HD, bool FUSED, int NT, int SL, bool TAG>
+__device__ __forceinline__ void att_scores_body(
+    int h, int s, int n_slices, const float* __restrict__ qsrc, int n_heads, int n_kv, int rope_dim, int split_half,
     const float* __restrict__ cos_base, const float* __restrict__ sin_base, int rope_stride,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm, float eps, uint16_t* __restrict__ kc,
     uint16_t* __restrict__ vc, int layer, int kvs, const uint32_t* __restrict__ d_pos, float scale,
-    float* __restrict__ g_sc, float* __restrict__ g_max) {
-  constexpr int ATT_NT = NT;  // positions per slice, one per thread
-  static_assert(HD % 64 == 0 && HD <= 256 && NT >= HD && NT % 64 == 0, "head_dim must be 64, 128 or 256");
+    float* __restrict__ g_sc, float* __restrict__ g_max, uint64_t* __restrict__ sc_t) {
+  constexpr int ATT_NT = NT;
+  static_assert(HD % 64 == 0 && HD <= 256 && NT >= HD && NT % 64 == 0 && SL <= NT, "head_dim must be 64, 128 or 256");
   constexpr int R8 = HD / 8;
   __shared__ __align__(16) float qs[HD];
   __shared__ __align__(16) float kn[HD];
@@ -2676,17 +2698,18 @@ __global__ __launch_bounds__(NT) void k_att_scores(
   __shared__ __align__(16) float sq[2 * HD];
   __shared__ float red[ATT_NT / 64];
   __shared__ float s_qscale, s_kscale;
-  const int tid = threadIdx.x, s = blockIdx.y;
-  const int h = gridDim.x % N_XCD == 0 ? xcd_member(blockIdx.x, n_kv, n_heads / n_kv) : (int)blockIdx.x;
+  const int tid = threadIdx.x;
   const int pos = (int)*d_pos;
   if (kv_pos_bad(pos, kvs)) return;  // (uniform, before any barrier)
-  const int p0 = s * ATT_NT;
+  const int p0 = s * SL;
   if (p0 > pos) return;  // (uniform) a slice past the current position
+  const uint64_t tg = TAG ? (uint64_t)ao_tag((uint32_t)pos, (uint32_t)layer) << 32 : 0;
   const int rep = n_heads / n_kv;
   const int kvh = h / rep;
   const size_t hbase = kv_head_base(layer, n_kv, kvh, HD, kvs);
   const uint4* kg = reinterpret_cast<const uint4*>(kc + hbase);
-  const int wg = h * (int)gridDim.y + s;
+  const int wg = h * n_slices + s;
+  (void)wg;
   CM_SPLIT_STAMP(0, wg, 0)
   if (tid < HD) {
     qs[tid] = qsrc[(size_t)h * HD + tid];
@@ -2699,7 +2722,7 @@ __global__ __launch_bounds__(NT) void k_att_scores(
   }
   // this thread's cache position's K row: issued now (behind q/k/v in their waves), so that
   // the slice's K streams while q is built
-  const int p = p0 + tid;
+  const int p = tid < SL ? p0 + tid : 0x7fffffff;
   uint4 row[R8];
   if (p < pos) {
 #pragma unroll
@@ -2771,20 +2794,41 @@ __global__ __launch_bounds__(NT) void k_att_scores(
       acc += e7;
     }
     const float sv = acc * scale;
-    g_sc[(size_t)h * kvs + p] = sv;
+    if (TAG)
+      st_agent64(sc_t + (size_t)h * kvs + p, tg | __float_as_uint(sv));
+    else
+      g_sc[(size_t)h * kvs + p] = sv;
     lmax = sv;
   } else if (p == pos) {  // this token's own key, from LDS
     float acc = 0.0f;
 #pragma unroll
     for (int d = 0; d < HD; ++d) acc += qs[d] * kn[d];
     const float sv = acc * scale;
-    g_sc[(size_t)h * kvs + p] = sv;
+    if (TAG)
+      st_agent64(sc_t + (size_t)h * kvs + p, tg | __float_as_uint(sv));
+    else
+      g_sc[(size_t)h * kvs + p] = sv;
     lmax = sv;
   }
   CM_SPLIT_STAMP(0, wg, 2)
-  const float mx = block_max(lmax, red);
-  if (tid == 0) g_max[(size_t)h * gridDim.y + s] = mx;
+  if (!TAG) {
+    const float mx = block_max(lmax, red);
+    if (tid == 0) g_max[(size_t)h * n_slices + s] = mx;
+  }
   CM_SPLIT_STAMP(0, wg, 3)
+}
+
+template <int HD, bool FUSED, int NT>
+__global__ __launch_bounds__(NT) void k_att_scores(
+    const float* __restrict__ qsrc, int n_heads, int n_kv, int rope_dim, int split_half,
+    const float* __restrict__ cos_base, const float* __restrict__ sin_base, int rope_stride,
+    const float* __restrict__ q_norm, const float* __restrict__ k_norm, float eps, uint16_t* __restrict__ kc,
+    uint16_t* __restrict__ vc, int layer, int kvs, const uint32_t* __restrict__ d_pos, float scale,
+    float* __restrict__ g_sc, float* __restrict__ g_max) {
+  const int h = gridDim.x % N_XCD == 0 ? xcd_member(blockIdx.x, n_kv, n_heads / n_kv) : (int)blockIdx.x;
+  att_scores_body<HD, FUSED, NT, NT, false>(h, (int)blockIdx.y, (int)gridDim.y, qsrc, n_heads, n_kv, rope_dim,
+                                            split_half, cos_base, sin_base, rope_stride, q_norm, k_norm, eps, kc, vc,
+                                            layer, kvs, d_pos, scale, g_sc, g_max, nullptr);
 }
 
 // The split output kernel's products: two buffers of [32 dims][PB positions + 4] f32 (the
@@ -2793,12 +2837,17 @@ __global__ __launch_bounds__(NT) void k_att_scores(
 // times; the launch takes the largest of 256, 128, 64 that leaves two V ring chunks.
 __host__ __device__ constexpr size_t avp_bytes(int pb) { return (size_t)2 * 32 * (pb + 4) * 4; }
 
-template <int HD, int PB>
-__global__ __launch_bounds__(att_nt(HD)) void k_att_out(
-    const uint16_t* __restrict__ vc, int n_heads, int n_kv, int layer, int kvs, const uint32_t* __restrict__ d_pos,
-    const float* __restrict__ g_sc, const float* __restrict__ g_max, int n_slices, int n_slices_pos,
-    float* __restrict__ att_out,
-    int8_t* __restrict__ xq, float* __restrict__ xs, int ring_slots, Prefetch pf) {
+// Output workgroup `bid` (32 dims of one head).  TAG (k_att_fused): the head's scores are read
+// as tagged words (sc_t) once the score workgroups of the same launch have stored them, and
+// their maximum is taken here; this position's V row comes from qsrc (the cache row is stored
+// by a score workgroup of the same launch); with op.q the Q8_0 output goes out as tagged words
+// for the output projection's workgroups (att_oproj).
+template <int HD, int PB, bool TAG>
+__device__ __forceinline__ void att_out_body(
+    int bid, const uint16_t* __restrict__ vc, int n_heads, int n_kv, int layer, int kvs,
+    const uint32_t* __restrict__ d_pos, const float* __restrict__ g_sc, const float* __restrict__ g_max,
+    int n_slices, int n_slices_pos, float* __restrict__ att_out, int8_t* __restrict__ xq, float* __restrict__ xs,
+    int ring_slots, const uint64_t* __restrict__ sc_t, const float* __restrict__ qsrc, const OProj& op) {
   constexpr int ATT_NT = att_nt(HD);
   constexpr int NW = ATT_NT / 64;
   constexpr int DW = 32;                       // output dims per workgroup: one Q8_0 block
@@ -2814,11 +2863,6 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
   float4* ring = dyn;
   float* sc = reinterpret_cast<float*>(dyn + (size_t)ring_slots * ATT_RING_GRANULES);
   float* pbuf = sc + ((kvs + 3) & ~3);  // (16-byte aligned)
-  const int nwork = n_heads * NDW;
-  if ((int)blockIdx.x >= nwork) {  // spare workgroups: read ahead the output projection
-    prefetch_lines(pf, blockIdx.x - nwork, gridDim.x - nwork, sc);
-    return;
-  }
   __shared__ float red[NW];
   __shared__ float s_inv;
   __shared__ uint64_t etab[32];
@@ -2826,7 +2870,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
   const int tid = threadIdx.x;
   const int rep = n_heads / n_kv;
   // (head, part): unit u = kv head * NDW + w, shared by the group's rep heads
-  const int m = xcd_member(blockIdx.x, n_kv * NDW, rep);
+  const int m = xcd_member(bid, n_kv * NDW, rep);
   const int w = (m / rep) % NDW, h = (m / rep / NDW) * rep + m % rep;
   const size_t hbase = kv_head_base(layer, n_kv, h / rep, HD, kvs);
   const uint4* vg = reinterpret_cast<const uint4*>(vc + hbase);  // V granule (g, d): g * HD + d
@@ -2834,11 +2878,18 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
   if (kv_pos_bad(pos, kvs)) return;  // (uniform, before any barrier)
   const int P = pos + 1;
   const int d = w * DW + tid;  // output lanes: tid < DW
+  const uint32_t tag = TAG ? ao_tag((uint32_t)pos, (uint32_t)layer) : 0u;
+  // this position's V value of output lane d (TAG: from the projection's output, rounded to
+  // f16 as the cache row that a score workgroup of this launch stores)
+  auto v_pos = [&]() -> uint16_t {
+    if (TAG) return f32_to_f16_bits(qsrc[(size_t)(n_heads + n_kv) * HD + (size_t)(h / rep) * HD + d]);
+    return vc[hbase + kv_v_index(HD, pos, d)];
+  };
   float acc = 0.0f;
-  CM_SPLIT_STAMP(1, (int)blockIdx.x, 0)
+  CM_SPLIT_STAMP(1, bid, 0)
   if (P == 1) {
     // inference.rs:23564-23575: a single position copies the V row
-    if (tid < DW) acc = half_bits_to_float(vc[hbase + kv_v_index(HD, pos, d)]);
+    if (tid < DW) acc = half_bits_to_float(v_pos());
   } else {
     const int ng = pos >> 3;  // full groups of 8 positions before pos
     // the output lanes' V values past the full groups (positions ng*8 .. pos, at most 8), loaded
@@ -2846,14 +2897,11 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
     uint16_t vtail[8];
     if (tid < DW) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) vtail[u] = ng * 8 + u < P ? vc[hbase + kv_v_index(HD, ng * 8 + u, d)] : (uint16_t)0;
+      for (int u = 0; u < 8; ++u)
+        vtail[u] = ng * 8 + u < pos ? vc[hbase + kv_v_index(HD, ng * 8 + u, d)]
+                                    : (ng * 8 + u == pos ? v_pos() : (uint16_t)0);
     }
     if (tid < 32) etab[tid] = kExp2Tab[tid];
-    const float* gs = g_sc + (size_t)h * kvs;
-    for (int p = tid; p < P; p += ATT_NT) sc[p] = gs[p];
-    float lm = -INFINITY;
-    const int nsl = (P + n_slices_pos - 1) / n_slices_pos;
-    for (int i = tid; i < nsl; i += ATT_NT) lm = fmaxf(lm, g_max[(size_t)h * n_slices + i]);
     const int R = ring_slots;
     const int nchunks = (ng + CG - 1) / CG;
     const int hw = (tid >> 6) - 1;
@@ -2874,16 +2922,57 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
     const bool early = P <= ATT_NT * ATT_ONEPASS_C;
     const bool seg = !early && att_seg_chunk<ATT_NT>(P) > 0 &&
                      att_seg_bytes<ATT_NT>(P) <= (size_t)R * ATT_RING_GRANULES * 16;
-    // the first V chunks go out behind the scores loads (nothing waits on them before the
-    // output sum; the segmented denominator uses the ring first and stages afterwards)
-    if (stager && !seg) {
-      for (int c = 0; c < min(R - 1, nchunks); ++c) stage(c);
+    float lm = -INFINITY;
+    const int nsl = (P + n_slices_pos - 1) / n_slices_pos;
+    if (TAG) {
+      // the first V chunks go out first (the scores are not there yet); then one watcher until
+      // this position's score carries the tag, then every score word, read by the waves that
+      // stage no V (a wave's loads complete in order: behind its V loads a score word would
+      // wait for them).  (Measured at C3: watching each slice's last cache position instead
+      // starts the reads 0.8 us later.)
+      (void)nsl;
+      if (stager && !seg) {
+        for (int c = 0; c < min(R - 1, nchunks); ++c) stage(c);
+      }
+      const uint64_t* gs = sc_t + (size_t)h * kvs;
+      if (tid == 0) (void)ao_wait_word(gs + pos, tag);
+      __syncthreads();
+      // (with the segmented denominator no V is staged yet: every wave reads)
+      if (!stager || seg) {
+        const int i0 = seg || tid < 64 ? tid : tid - 64 * NH;  // wave 0, then waves NH + 1 ..
+        const int ns = seg ? ATT_NT : ATT_NT - 64 * NH;
+        // eight words in flight per thread; a word not yet tagged is polled on its own
+        for (int b0 = i0; b0 < P; b0 += 8 * ns) {
+          uint64_t v[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) v[u] = b0 + u * ns < P ? ld_agent64(gs + b0 + u * ns) : 0;
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int p = b0 + u * ns;
+            if (p < P) {
+              if ((uint32_t)(v[u] >> 32) != tag) v[u] = ao_wait_word(gs + p, tag);
+              const float f = __uint_as_float((uint32_t)v[u]);
+              sc[p] = f;
+              lm = fmaxf(lm, f);
+            }
+          }
+        }
+      }
+    } else {
+      const float* gs = g_sc + (size_t)h * kvs;
+      for (int p = tid; p < P; p += ATT_NT) sc[p] = gs[p];
+      for (int i = tid; i < nsl; i += ATT_NT) lm = fmaxf(lm, g_max[(size_t)h * n_slices + i]);
+      // the first V chunks go out behind the scores loads (nothing waits on them before the
+      // output sum; the segmented denominator uses the ring first and stages afterwards)
+      if (stager && !seg) {
+        for (int c = 0; c < min(R - 1, nchunks); ++c) stage(c);
+      }
     }
     const float mx = block_max(lm, red);  // (its barriers also publish sc and etab)
-    CM_SPLIT_STAMP(1, (int)blockIdx.x, 1)
+    CM_SPLIT_STAMP(1, bid, 1)
     for (int p = tid; p < P; p += ATT_NT) sc[p] = glibc_expf_t(sc[p] - mx, etab);
     __syncthreads();
-    CM_SPLIT_STAMP(1, (int)blockIdx.x, 2)
+    CM_SPLIT_STAMP(1, bid, 2)
     float inv;
     if (onepass) {
       inv = 1.0f / att_onepass_sum<ATT_NT>(sc, P, fs);
@@ -2900,7 +2989,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
       __syncthreads();
       inv = s_inv;
     }
-    CM_SPLIT_STAMP(1, (int)blockIdx.x, 3)
+    CM_SPLIT_STAMP(1, bid, 3)
     for (int p = tid; p < P; p += ATT_NT) sc[p] = sc[p] * inv;
     // ---- out_d = fold_p prob_p * v_pd over the full 8-position groups: the products of a
     // block of BG groups are formed by all waves but wave 0 (the rounded f32 product of the
@@ -2979,7 +3068,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
       }
       __syncthreads();  // wave 0 is done with buffer b & 1; block b + 1's products are visible
     }
-    CM_SPLIT_STAMP(1, (int)blockIdx.x, 4)
+    CM_SPLIT_STAMP(1, bid, 4)
     if (tid < DW) {
 #pragma unroll
       for (int u = 0; u < 8; ++u)
@@ -2987,13 +3076,76 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
     }
   }
   if (tid < DW) {
-    att_out[(size_t)h * HD + d] = acc;
+    const size_t o = (size_t)h * HD + d;
+    att_out[o] = acc;
     int8_t q;
     const float dd = quantize_lane32(acc, &q);
-    xq[(size_t)h * HD + d] = q;
-    if (tid == 0) xs[((size_t)h * HD + d) >> 5] = dd;
+    if (TAG && op.q) {  // for the output projection's workgroups of this launch (as k_attention)
+      const uint64_t tg = (uint64_t)tag << 32;
+      const uint32_t b = (uint32_t)(uint8_t)q;
+      const uint32_t wq = b | ((uint32_t)__shfl_down((int)b, 1) << 8) | ((uint32_t)__shfl_down((int)b, 2) << 16) |
+                          ((uint32_t)__shfl_down((int)b, 3) << 24);
+      if ((tid & 3) == 0) st_agent64(op.xq_t + (o >> 2), tg | wq);
+      if (tid == 0) st_agent64(op.xs_t + (o >> 5), tg | __float_as_uint(dd));
+    } else {
+      xq[o] = q;
+      if (tid == 0) xs[o >> 5] = dd;
+    }
   }
-  CM_SPLIT_STAMP(1, (int)blockIdx.x, 5)
+  CM_SPLIT_STAMP(1, bid, 5)
+}
+
+template <int HD, int PB>
+__global__ __launch_bounds__(att_nt(HD)) void k_att_out(
+    const uint16_t* __restrict__ vc, int n_heads, int n_kv, int layer, int kvs, const uint32_t* __restrict__ d_pos,
+    const float* __restrict__ g_sc, const float* __restrict__ g_max, int n_slices, int n_slices_pos,
+    float* __restrict__ att_out,
+    int8_t* __restrict__ xq, float* __restrict__ xs, int ring_slots, Prefetch pf) {
+  const int nwork = n_heads * (HD / 32);
+  if ((int)blockIdx.x >= nwork) {  // spare workgroups: read ahead the output projection
+    extern __shared__ __align__(16) float4 dyn[];
+    prefetch_lines(pf, blockIdx.x - nwork, gridDim.x - nwork,
+                   reinterpret_cast<float*>(dyn + (size_t)ring_slots * ATT_RING_GRANULES));
+    return;
+  }
+  att_out_body<HD, PB, false>((int)blockIdx.x, vc, n_heads, n_kv, layer, kvs, d_pos, g_sc, g_max, n_slices,
+                              n_slices_pos, att_out, xq, xs, ring_slots, nullptr, nullptr, OProj{});
+}
+
+// ---------------------------------------------------------------------------
+// The split decode attention in one launch (no round trip of the scores through a launch
+// boundary): workgroups [0, n_heads * n_slices) are score slices of SL positions (slice s of
+// head h at s * n_heads + h: every head's first slices are dispatched first), then n_heads *
+// HD / 32 output workgroups, then (op.q set) the output projection's workgroups.  Every
+// workgroup waits only for workgroups of lower index, which the dispatcher has started
+// before it, so the waits end whatever the number of CUs.  Same arithmetic and order as
+// k_att_scores + k_att_out + k_gemv_k.
+template <int HD, int PB, int SL>
+__global__ __launch_bounds__(att_nt(HD)) void k_att_fused(
+    const float* __restrict__ qsrc, int n_heads, int n_kv, int rope_dim, int split_half,
+    const float* __restrict__ cos_base, const float* __restrict__ sin_base, int rope_stride,
+    const float* __restrict__ q_norm, const float* __restrict__ k_norm, float eps, uint16_t* __restrict__ kc,
+    uint16_t* __restrict__ vc, int layer, int kvs, const uint32_t* __restrict__ d_pos, float scale,
+    uint64_t* __restrict__ sc_t, int n_slices, float* __restrict__ att_out,
+    int8_t* __restrict__ xq, float* __restrict__ xs, int ring_slots, OProj op) {
+  constexpr int NT = att_nt(HD);
+  const int nsw = n_heads * n_slices, now = n_heads * (HD / 32);
+  const int b = (int)blockIdx.x;
+  if (b < nsw) {
+    att_scores_body<HD, true, NT, SL, true>(b % n_heads, b / n_heads, n_slices, qsrc, n_heads, n_kv, rope_dim,
+                                            split_half, cos_base, sin_base, rope_stride, q_norm, k_norm, eps, kc, vc,
+                                            layer, kvs, d_pos, scale, nullptr, nullptr, sc_t);
+  } else if (b < nsw + now) {
+    att_out_body<HD, PB, true>(b - nsw, vc, n_heads, n_kv, layer, kvs, d_pos, nullptr, nullptr, n_slices, SL,
+                               att_out, xq, xs, ring_slots, sc_t, qsrc, op);
+  } else if constexpr (NT == AO_ROWS * 64) {
+    if (op.q) {
+      extern __shared__ __align__(16) float4 dyn[];
+      const int pos = (int)*d_pos;
+      if (kv_pos_bad(pos, kvs)) return;
+      att_oproj<NT>(op, b - nsw - now, ao_tag((uint32_t)pos, (uint32_t)layer), reinterpret_cast<unsigned char*>(dyn));
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------

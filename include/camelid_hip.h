@@ -146,13 +146,16 @@ int camelid_hip_profile_end(camelid_hip_engine* e, double* ms, double* bytes, ui
 /* Measurement hook (no reference counterpart): in-kernel phase timestamps (100 MHz counter) of
  * the last decode step, recorded only by the measurement build of this library
  * (libcamelid_hip_stamps.so, compiled with -DCM_STAMPS); the product build returns an error.
- * Layout: the decode attention [layer < 64][head < 64][7] (start, q/k/v built, scores,
- * exponentials, denominator, output sums, end), then the norm-fused GEMVs of the last layer
- * [kind 0 qkv, 1 gate/up][workgroup < 256][8] (start, norm done, a weight wave's loads issued,
- * past the post-norm barrier, block dots done, end, the norm inputs arrived, the sum of squares
- * known), then the split attention of the last layer [kind 0 scores, 1 output][workgroup <
- * 1024][8] (scores: start, q built, scores done, end; output: start, scores and maximum,
- * exponentials, denominator, output sums, end).  Copies min(n, 64*64*7 + 2*256*8 + 2*1024*8)
+ * Layout: the decode attention [layer < 64][head < 64][9] (start, q/k/v built, scores,
+ * exponentials, denominator, output sums, end, a row wave's K-row loads issued, its scores
+ * done), then the norm-fused GEMVs of the last layer [kind 0 qkv, 1 gate/up][workgroup <
+ * 256][13] (start, norm done, a weight wave's loads issued, past the post-norm barrier, block
+ * dots done, end, the norm inputs arrived, the sum of squares known, the one-pass sum's four
+ * phases, its special-step count), then the split attention of the last layer [kind 0 scores,
+ * 1 output][workgroup < 1024][8] (scores: start, q built, scores done, end; output: start,
+ * scores and maximum, exponentials, denominator, output sums, end), then the output-projection
+ * workgroups of the attention launch [layer < 64][first, last workgroup][4] (start, watched
+ * word tagged, activation staged, end).  Copies min(n, 64*64*9 + 2*256*13 + 2*1024*8 + 64*2*4)
  * words; *n_out receives the count. */
 int camelid_hip_phase_stamps(uint64_t* out, size_t n, size_t* n_out);
 /* Measurement hook (no reference counterpart): HBM bandwidth of this device, best of `reps`

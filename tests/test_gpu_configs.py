@@ -76,15 +76,35 @@ def test_config_stream_matches_golden(name):
 @pytest.mark.parametrize("switch,value", [("CAMELID_HIP_FUSED_GU", "0"), ("CAMELID_HIP_FUSED_NORM", "0"),
                                           ("CAMELID_HIP_READ_AHEAD", "1"), ("CAMELID_HIP_GRAPHS", "0"),
                                           ("CAMELID_HIP_KV_AHEAD", "1"), ("CAMELID_HIP_ATT_DG", "2"),
-                                          ("CAMELID_HIP_ATT_O", "0")])
+                                          ("CAMELID_HIP_ATT_O", "0"), ("CAMELID_HIP_ATT_SPLIT", "1")])
 def test_switch_off_keeps_tinyllama_stream(monkeypatch, switch, value):
     """Each documented switch of the Q8_0 decode path set away from its default (the separate
     RMSNorm launch, the separate SwiGLU launch, the weight read-ahead workgroups, launches
     without a graph, the KV rows read by the qkv launch's idle waves, two attention workgroups
     per head of 64 dims instead of one, the output projection as its own launch instead of
-    inside the attention launch): the TinyLlama golden stream (configs[0], 128 + 128) is still
-    reproduced by the device loop."""
+    inside the attention launch, the one-launch split attention with the output projection at
+    every position instead of from 1024 on): the TinyLlama golden stream (configs[0], 128 + 128)
+    is still reproduced by the device loop."""
     monkeypatch.setenv(switch, value)
+    test_config_stream_matches_golden("tinyllama-1.1b")
+
+
+def test_split_attention_everywhere_keeps_llama3b_stream(monkeypatch):
+    """configs[1] (Llama-3.2-3B-arch, heads of 128) with the one-launch split attention at every
+    position (score slices of 128 positions below 1024 cache positions, the output projection's
+    workgroups in the same launch): the golden stream is still reproduced."""
+    monkeypatch.setenv("CAMELID_HIP_ATT_SPLIT", "1")
+    test_config_stream_matches_golden("llama-3.2-3b")
+
+
+@pytest.mark.parametrize("fused_split,att_o", [("0", "1"), ("1", "0")])
+def test_split_attention_variants_keep_tinyllama_stream(monkeypatch, fused_split, att_o):
+    """The split attention at every position in its other forms: two launches (scores, then
+    outputs) with the output projection as its own launch, and one launch without the output
+    projection's workgroups: the TinyLlama golden stream is still reproduced."""
+    monkeypatch.setenv("CAMELID_HIP_ATT_SPLIT", "1")
+    monkeypatch.setenv("CAMELID_HIP_ATT_FUSED_SPLIT", fused_split)
+    monkeypatch.setenv("CAMELID_HIP_ATT_O", att_o)
     test_config_stream_matches_golden("tinyllama-1.1b")
 
 
