@@ -502,9 +502,10 @@ def main() -> int:
         assert [int(t) for t in toks2] == [int(t) for t in toks], "profiled pass diverged"
         g = prof["gemv"]
         achieved = g["bytes"] / (g["ms"] * 1e-3) / 1e9
-        kname = ("Q8_0 GEMV: k_gemv_norm (RMSNorm + qkv) + k_gemv_k (o, down; + residual) + k_gemv_gu_silu "
-                 "(RMSNorm + gate/up + SwiGLU + Q8_0) + k_gemv_argmax (lm_head)" if cfg.quant_scheme == "q8_0" else
-                 "K-quant GEMV: k_gemv_q4k + k_gemv_q6k (incl. lm_head)")
+        kname = ("Q8_0 GEMV: k_gemv_norm (RMSNorm + qkv) + k_gemv_k (down + residual) + k_gemv_gu_silu "
+                 "(RMSNorm + gate/up + SwiGLU + Q8_0) + k_gemv_argmax (lm_head); the o projection runs inside the "
+                 "attention launch (k_attention / k_att_fused) and is counted with it" if cfg.quant_scheme == "q8_0"
+                 else "K-quant GEMV: k_gemv_q4k + k_gemv_q6k (incl. lm_head)")
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get(cfg.name),
                     "traffic_source": TRAFFIC_SOURCE if cfg.name in TRAFFIC else None,
