@@ -41,7 +41,7 @@ PEAK_CLOCK_HZ = 2.4e9
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over `bench.py --probe-traffic`, each
 # scaled by what the same counter reads for a device copy of known size, averaged over the
 # GEMV launches of one C3 step (profiles/traffic_gemv_llama-3.2-3b_q8_0.md).
-TRAFFIC: dict = {"llama-3.2-3b": 30583110}
+TRAFFIC: dict = {"llama-3.2-3b": 37285133}
 TRAFFIC_SOURCE = ("profiles/traffic_gemv_llama-3.2-3b_q8_0.md: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE "
                   "passes, scaled by a copy kernel's reading; a recorded figure, not measured in this run")
 # Q8_0 [N, K] shapes, weights N(0, 0.02) and activations N(0, 1), seed 2
