@@ -639,7 +639,7 @@ void launch_attention_split(uint32_t hd, uint32_t n_heads, int slots, hipStream_
     const uint32_t grid = n_heads * (HD / 32) + (pf.a_lines ? PREFETCH_WGS : 0);                                  \
     int pb = 0;                                                                                                    \
     const int so = attn_out_slots((uint32_t)kvs, slots, &pb);                                                      \
-    const size_t lds_o = (size_t)so * cm::ATT_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs) + cm::avp_bytes(pb); \
+    const size_t lds_o = (size_t)so * cm::AO_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs) + cm::avp_bytes(pb); \
     if (pb == 256)                                                                                                 \
       CM_LAUNCH((cm::k_att_out<HD, 256>), dim3(grid), dim3(cm::att_nt(HD)), lds_o, s, vc, nh, nkv, layer, kvs, pos, \
                 g_sc, g_mx, nsl, (HD > ATT_SLICE ? HD : ATT_SLICE), att, xq, xs, so, pf);                          \
@@ -674,7 +674,7 @@ void launch_attention_fused(uint32_t hd, uint32_t n_heads, int slots, hipStream_
   const int nsl = (kvs + sl - 1) / sl;
   int pb = 0;
   const int so = attn_out_slots((uint32_t)kvs, slots, &pb);
-  size_t lds = (size_t)so * cm::ATT_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs) + cm::avp_bytes(pb);
+  size_t lds = (size_t)so * cm::AO_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs) + cm::avp_bytes(pb);
   uint32_t grid = n_heads * (uint32_t)nsl + n_heads * (hd / 32);
   if (op.q) {
     if (cm::att_nt((int)hd) != cm::AO_ROWS * 64 || !cm::ao_width_ok(op.K) || op.K != (int)(n_heads * hd)) {
@@ -787,20 +787,23 @@ int attn_ring_slots(uint32_t kvs) {
   return slots >= 2 && out_slots >= 2 ? (int)slots : 0;
 }
 
-// Ring slots of the split output kernel: its products and counters take LDS beside the ring.
 // Ring slots and product block of the split output kernel, whose product buffers take LDS
-// beside the V ring: the largest block of 256, 128, 64 positions that leaves two ring chunks
-// (attn_ring_slots admitted kvs only with room for two beside 64-position blocks).
+// beside the V ring: three 16 KB chunks (more chunks in flight measured slower) beside the
+// largest product block of 256, 128, 64 positions that leaves room for them; the block size
+// sets the number of workgroup barriers of the output chain (C4, 8K positions: 128 -> 256
+// positions per block, 225.8 -> 239.6 tok/s).  attn_ring_slots admitted kvs only with room
+// for two 32 KB chunks beside 64-position blocks, so at least three 16 KB chunks fit.
 int attn_out_slots(uint32_t kvs, int slots, int* pb) {
+  (void)slots;
   const long room = (long)attn_lds_limit() - attn_static_lds() - (long)attn_sc_bytes(kvs);
-  constexpr long chunk = (long)cm::ATT_RING_GRANULES * 16;
+  constexpr long chunk = (long)cm::AO_RING_GRANULES * 16;
   *pb = 64;
   for (int b : {256, 128})
-    if ((room - (long)cm::avp_bytes(b)) / chunk >= 2) {
+    if ((room - (long)cm::avp_bytes(b)) / chunk >= 3) {
       *pb = b;
       break;
     }
-  return (int)std::min<long>(slots, (room - (long)cm::avp_bytes(*pb)) / chunk);
+  return (int)std::min<long>(3, (room - (long)cm::avp_bytes(*pb)) / chunk);
 }
 
 // Algorithmic bytes of one K-quant GEMV launch: superblocks (144 or 210 B per 256 values),

@@ -2028,6 +2028,11 @@ __host__ __device__ constexpr int att_nt(int hd) { return hd <= 128 ? 1024 : 512
 // V staging ring: chunks of 32 KB (2048 16-byte granules), 32 wave-loads of 1 KB each.
 constexpr int ATT_RING_GRANULES = 2048;
 constexpr int ATT_RING_LOADS = 32;
+// The split output workgroups' V ring: chunks of 16 KB (1024 granules, 16 wave-loads), three
+// of them, so that 256-position product blocks (one workgroup barrier per block) fit beside
+// the scores at 8K positions, where 32 KB chunks left room for 128-position blocks only.
+constexpr int AO_RING_GRANULES = 1024;
+constexpr int AO_RING_LOADS = 16;
 
 // Waits until at most n of this wave's vector memory operations are outstanding (gfx9
 // s_waitcnt encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
@@ -2834,7 +2839,7 @@ __global__ __launch_bounds__(NT) void k_att_scores(
 // The split output kernel's products: two buffers of [32 dims][PB positions + 4] f32 (the
 // row pad keeps the 16-byte LDS reads and writes of consecutive dims on distinct banks),
 // placed after the scores in dynamic LDS.  Larger blocks pay the per-block barrier fewer
-// times; the launch takes the largest of 256, 128, 64 that leaves two V ring chunks.
+// times; the launch takes the largest of 256, 128, 64 that leaves three 16 KB V ring chunks.
 __host__ __device__ constexpr size_t avp_bytes(int pb) { return (size_t)2 * 32 * (pb + 4) * 4; }
 
 // Output workgroup `bid` (32 dims of one head).  TAG (k_att_fused): the head's scores are read
@@ -2853,15 +2858,15 @@ __device__ __forceinline__ void att_out_body(
   constexpr int DW = 32;                       // output dims per workgroup: one Q8_0 block
   constexpr int NDW = HD / DW;
   constexpr int NH = (NW - 1) >= 8 ? 8 : 4;    // V-staging waves 1..NH
-  constexpr int LH = ATT_RING_LOADS / NH;      // 1 KB wave loads per staging wave per chunk
-  constexpr int CG = ATT_RING_GRANULES / DW;   // 8-position groups per ring chunk
+  constexpr int LH = AO_RING_LOADS / NH;      // 1 KB wave loads per staging wave per chunk
+  constexpr int CG = AO_RING_GRANULES / DW;   // 8-position groups per ring chunk
   static_assert(CG % 4 == 0, "ring chunks hold a multiple of 4 granule groups");
   constexpr int BG = PB / 8;  // groups per product block
   constexpr int AVP_RS = PB + 4;
   static_assert(CG % BG == 0, "product blocks tile the ring chunks");
   extern __shared__ __align__(16) float4 dyn[];
   float4* ring = dyn;
-  float* sc = reinterpret_cast<float*>(dyn + (size_t)ring_slots * ATT_RING_GRANULES);
+  float* sc = reinterpret_cast<float*>(dyn + (size_t)ring_slots * AO_RING_GRANULES);
   float* pbuf = sc + ((kvs + 3) & ~3);  // (16-byte aligned)
   __shared__ float red[NW];
   __shared__ float s_inv;
@@ -2908,7 +2913,7 @@ __device__ __forceinline__ void att_out_body(
     const bool stager = hw >= 0 && hw < NH;
     const size_t last_group = (size_t)max(ng, 1) - 1;
     auto stage = [&](int c) {  // chunk c into slot c % R: 1 KB wave load i = groups 2i, 2i+1
-      float4* slot = ring + (size_t)(c % R) * ATT_RING_GRANULES;
+      float4* slot = ring + (size_t)(c % R) * AO_RING_GRANULES;
 #pragma unroll
       for (int j = 0; j < LH; ++j) {
         const int i = hw + NH * j;
@@ -2921,7 +2926,7 @@ __device__ __forceinline__ void att_out_body(
     const bool onepass = P >= ATT_FOLD_MAX && P <= ATT_NT * ATT_ONEPASS_C;
     const bool early = P <= ATT_NT * ATT_ONEPASS_C;
     const bool seg = !early && att_seg_chunk<ATT_NT>(P) > 0 &&
-                     att_seg_bytes<ATT_NT>(P) <= (size_t)R * ATT_RING_GRANULES * 16;
+                     att_seg_bytes<ATT_NT>(P) <= (size_t)R * AO_RING_GRANULES * 16;
     float lm = -INFINITY;
     const int nsl = (P + n_slices_pos - 1) / n_slices_pos;
     if (TAG) {
@@ -3003,7 +3008,7 @@ __device__ __forceinline__ void att_out_body(
     int issued = min(R - 1, nchunks);  // ring chunks issued so far (staging waves)
     auto products = [&](int b) {
       const int c = b / BPC;
-      const uint4* slot = reinterpret_cast<const uint4*>(ring + (size_t)(c % R) * ATT_RING_GRANULES);
+      const uint4* slot = reinterpret_cast<const uint4*>(ring + (size_t)(c % R) * AO_RING_GRANULES);
       float* dst0 = pbuf + (size_t)(b & 1) * DW * AVP_RS;
       for (int gi = tid - 64; gi < BG * DW; gi += ATT_NT - 64) {
         const int gl = gi / DW, dd = gi % DW, g = b * BG + gl;
@@ -3105,7 +3110,7 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
   if ((int)blockIdx.x >= nwork) {  // spare workgroups: read ahead the output projection
     extern __shared__ __align__(16) float4 dyn[];
     prefetch_lines(pf, blockIdx.x - nwork, gridDim.x - nwork,
-                   reinterpret_cast<float*>(dyn + (size_t)ring_slots * ATT_RING_GRANULES));
+                   reinterpret_cast<float*>(dyn + (size_t)ring_slots * AO_RING_GRANULES));
     return;
   }
   att_out_body<HD, PB, false>((int)blockIdx.x, vc, n_heads, n_kv, layer, kvs, d_pos, g_sc, g_max, n_slices,
