@@ -19,17 +19,23 @@
 //   f16 conversions        - exhaustive vs F16C semantics + reference fixtures F16.json
 //   Q8_0 dequant           - reference fixtures Q8_0.json (gguf==0.19.0)
 //   quantize_q8_0          - reference KAT q8_0_input_quantization_uses_unrounded_scale
-//                            + brute-force properties (round-half-away, clamp)
+//                            + brute-force properties (round-half-away, clamp); scale and
+//                            x * inv expression known answers
 //   block int dot          - brute force int64 sums
 //   Q8_0 row fold          - exact integer case; order/FMA/association known answers
 //   rms_norm               - closed form on constant rows; float64 bound; sum-order and
-//                            rounded-square known answers
-//   rope                   - pos 0 identity, norm preservation, llama3 KAT
+//                            rounded-square known answers; scale / (x*scale)*w known answer
+//   rope                   - pos 0 identity, norm preservation, llama3 KAT; rotation (no
+//                            FMA), powf frequency and llama3 association known answers
 //   attention              - single-position copy, uniform keys -> mean of V; score-dot,
-//                            softmax-sum and AV order / rounded-product known answers
-//   silu_mul / argmax      - closed forms / brute force incl. ties
+//                            softmax-sum and AV order / rounded-product known answers;
+//                            score scale and e * (1/sum) known answers
+//   silu_mul / argmax      - expression known answer / brute force incl. ties
+//   quantize_q8_k          - properties; iscale product and d = 1/iscale known answers
 //   Q4_K / Q6_K row dots   - fixture-pinned dequant sums; FMA chain and class-chain
 //                            left-fold known answers
+// tests/test_oracle_mutants.py rebuilds this file with 21 single-expression rewrites and
+// requires each to fail one of these pins.
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
@@ -590,6 +596,12 @@ OX void oracle_rope_tables(uint32_t rope_dim, float freq_base, int scaling_kind,
                            float* cos_out, float* sin_out) {
   RopeCfg c{rope_dim, freq_base, scaling_kind, factor, orig_ctx, low, high, rope_freqs};
   rope_tables(c, pos0, n_pos, cos_out, sin_out);
+}
+// The per-pair frequencies theta_i (rope_pair_frequency, rope.rs:526-560) the tables are built from.
+OX void oracle_rope_frequencies(uint32_t rope_dim, float freq_base, int scaling_kind, float factor, float orig_ctx,
+                                float low, float high, const float* rope_freqs, float* theta_out) {
+  RopeCfg c{rope_dim, freq_base, scaling_kind, factor, orig_ctx, low, high, rope_freqs};
+  for (uint32_t p = 0; p < rope_dim / 2; ++p) theta_out[p] = rope_pair_frequency(p, c);
 }
 OX void oracle_apply_rope(float* data, uint32_t heads, uint32_t hd, uint32_t rope_dim, const float* cosv,
                           const float* sinv, int split_half) {

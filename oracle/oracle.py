@@ -6,6 +6,7 @@ wherever the tests run).  The product package never imports this module.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
@@ -13,6 +14,8 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "_build" / "libcamelid_oracle.so"
+# tests/test_oracle_mutants.py points this at deliberately altered builds of the oracle
+LIB_OVERRIDE = os.environ.get("CAMELID_ORACLE_LIB")
 
 f32p = C.POINTER(C.c_float)
 u8p = C.POINTER(C.c_uint8)
@@ -38,6 +41,8 @@ _SIG = {
     "oracle_rms_norm": (None, [f32p, f32p, C.c_size_t, C.c_size_t, C.c_float, f32p]),
     "oracle_rope_tables": (None, [C.c_uint32, C.c_float, C.c_int, C.c_float, C.c_float, C.c_float, C.c_float, f32p,
                                   C.c_uint32, C.c_uint32, f32p, f32p]),
+    "oracle_rope_frequencies": (None, [C.c_uint32, C.c_float, C.c_int, C.c_float, C.c_float, C.c_float, C.c_float,
+                                       f32p, f32p]),
     "oracle_apply_rope": (None, [f32p, C.c_uint32, C.c_uint32, C.c_uint32, f32p, f32p, C.c_int]),
     "oracle_silu_mul": (None, [f32p, f32p, C.c_size_t, f32p]),
     "oracle_argmax": (C.c_uint32, [f32p, C.c_size_t]),
@@ -72,9 +77,12 @@ def build() -> Path:
 def lib() -> C.CDLL:
     global _lib
     if _lib is None:
-        if not LIB_PATH.exists():
-            build()
-        h = C.CDLL(str(LIB_PATH))
+        if LIB_OVERRIDE:
+            h = C.CDLL(LIB_OVERRIDE)
+        else:
+            if not LIB_PATH.exists():
+                build()
+            h = C.CDLL(str(LIB_PATH))
         for n, (r, a) in _SIG.items():
             fn = getattr(h, n)
             fn.restype = r
@@ -220,6 +228,14 @@ def rope_tables(rope_dim, base, kind=0, factor=1.0, orig_ctx=8192.0, low=1.0, hi
     lib().oracle_rope_tables(rope_dim, base, kind, factor, orig_ctx, low, high, fp, pos0, n_pos, P(c, C.c_float),
                              P(s, C.c_float))
     return c, s
+
+
+def rope_frequencies(rope_dim, base, kind=0, factor=1.0, orig_ctx=8192.0, low=1.0, high=4.0, freqs=None):
+    """The per-pair frequencies theta_i that rope_tables() takes cos/sin of."""
+    out = np.empty(rope_dim // 2, np.float32)
+    fp = P(np.ascontiguousarray(freqs, np.float32), C.c_float) if freqs is not None else None
+    lib().oracle_rope_frequencies(rope_dim, base, kind, factor, orig_ctx, low, high, fp, P(out, C.c_float))
+    return out
 
 
 def apply_rope(x, heads, hd, rope_dim, cos, sin, split_half=False) -> np.ndarray:

@@ -11,7 +11,7 @@ oracle therefore fails here, whatever the float64 bounds of test_oracle_pins.py 
 Which order is "the CPU path" (Linux x86-64, the GPU box's host):
   - Q8_0 row fold           inference.rs:20434-20442 (sum += (float(dot) * w_d) * x_d, block order)
   - RMSNorm sum of squares  tensor/mod.rs:2083-2091 (ss += x * x, sequential)
-  - attention score dot     tensor/mod.rs:2632-2648 dot_product (sequential, no FMA): the
+  - attention score dot     tensor/mod.rs:2632-2648 dot_product (sequential, products rounded): the
                             Linux cache is KvDtype::F32 (kv_cache.rs:199-214) and the blocked
                             FMA lane is Windows-only (inference.rs:23932-23938)
   - softmax sum, AV         inference.rs:23988-24016 (score_sum += e, sequential; out[d] +=
@@ -212,6 +212,38 @@ def test_attention_score_dot_order(orc):
         assert s0 != 64.0
         wrong = _softmax_av([F(s0 * F(0.125)), F(0.0)], values)
         assert not np.array_equal(wrong.view(np.uint32), got.view(np.uint32))
+
+
+def test_attention_score_dot_products_are_rounded(orc):
+    """tensor/mod.rs:2632-2648: sum += q_d * k_d, each product rounded before the add (no FMA).
+    hd = 64 (scale 1/8), A = 16 + 2^-8, q = [A, -A, 8, 0...], k_0 = [A, A, 8, 0...], k_1 = 0:
+      A * A = 256 + 2^-3 + 2^-16, a tie at ulp 2^-15, to even -> 256.125; -A * A -> -256.125;
+      0 + 256.125 - 256.125 + 64 = 64, score_0 = 8 exactly, as in the order test above.
+    A fused multiply-add keeps the second product exact: fma(-A, A, 256.125) = -2^-16, then
+    fma(8, 8, -2^-16) = 64 - 2^-16 (exact at ulp 2^-18): score_0 = 8 - 2^-19, which moves
+    e_1 = expf(score_1 - score_0) by about 2^-19 relative, i.e. many ulps."""
+    global _ORC
+    _ORC = orc
+    hd = 64
+    a = F(16 + 2.0 ** -8)
+    q = np.zeros(hd, np.float32)
+    q[:3] = [a, -a, 8]
+    k0 = np.zeros(hd, np.float32)
+    k0[:3] = [a, a, 8]
+    keys = np.stack([k0, np.zeros(hd, np.float32)])
+    values = np.zeros((2, hd), np.float32)
+    values[0, 0] = values[1, 1] = 1.0
+    got = _attend(orc, q, keys, values, hd)
+    prods = [F(x * y) for x, y in zip(q[:3], k0[:3])]
+    assert [float(v) for v in prods] == [256.125, -256.125, 64.0] and fold(prods) == 64.0
+    want = _softmax_av([F(F(64.0) * F(0.125)), F(0.0)], values)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    fused = F(0.0)
+    for x, y in zip(q[:3], k0[:3]):
+        fused = fma32(x, y, fused)
+    assert float(fused) == 64 - 2.0 ** -16
+    wrong = _softmax_av([F(fused * F(0.125)), F(0.0)], values)
+    assert not np.array_equal(wrong.view(np.uint32), got.view(np.uint32))
 
 
 def test_attention_softmax_sum_and_av_order(orc):
