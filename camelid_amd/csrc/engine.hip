@@ -573,7 +573,7 @@ cm::Prefetch prefetch_of(const KMat* m) {
 }
 
 size_t attn_sc_bytes(uint32_t kvs) { return (((size_t)kvs + 3) & ~(size_t)3) * 4; }
-int attn_ring_slots(uint32_t kvs);
+int attn_ring_slots(uint32_t kvs, bool host_only = false);
 int attn_out_slots(uint32_t kvs, int slots, int* pb);
 
 // dg: workgroups per query head (k_attention's DG: 1, 2 or 4, at most hd / 32); 0 takes the
@@ -778,8 +778,12 @@ long attn_lds_limit() {
   return limit;
 }
 
-int attn_ring_slots(uint32_t kvs) {
-  const long room = attn_lds_limit() - attn_static_lds() - (long)attn_sc_bytes(kvs);
+// host_only: the figures of the device-free preflight (gfx950's LDS per workgroup and the
+// bound on the kernels' static LDS), with no HIP call.
+int attn_ring_slots(uint32_t kvs, bool host_only) {
+  const long room = (host_only ? (long)GFX950_LDS_PER_WORKGROUP - ATT_STATIC_LDS_BOUND
+                               : attn_lds_limit() - attn_static_lds()) -
+                    (long)attn_sc_bytes(kvs);
   const long slots = std::min<long>(4, room / (cm::ATT_RING_GRANULES * 16));
   // the split output kernel also holds its product buffers (64-position blocks at least),
   // and two ring chunks beside them
@@ -907,10 +911,16 @@ void proj(camelid_hip_engine* e, const Proj& p, float* y, const float* resid, co
 // workgroup per CU): with more score slices than that (C4's 8K context: 288 score + 128 output
 // workgroups) the output workgroups start only as score workgroups retire, and the two launches
 // measured faster (212.1 vs 204.1 tok/s); within it the one launch is (C5 372.0 vs 365.3).
-bool att_fused_split(const camelid_hip_engine* e) {
+// The count includes the output projection's workgroups when the Q8_0 O projection rides in
+// the launch.  The score words are tagged with (position + 1, layer) in 24 + 8 bits, so the
+// layer count and the cache length must fit those fields, as for the projection's words.
+bool ao_enabled(camelid_hip_engine* e);
+bool att_fused_split(camelid_hip_engine* e) {
   if (!(e->att_fsplit && fsplit_supported(e->d.head_dim) && !e->read_ahead && e->att_sct)) return false;
+  if (e->d.n_layers > 255 || e->kvs >= (1u << 24) - 1) return false;
   const uint32_t sl = (uint32_t)fsplit_sl(e->kvs, e->d.head_dim);
-  const uint32_t wgs = e->d.n_heads * ((e->kvs + sl - 1) / sl) + e->d.n_heads * (e->d.head_dim / 32);
+  uint32_t wgs = e->d.n_heads * ((e->kvs + sl - 1) / sl) + e->d.n_heads * (e->d.head_dim / 32);
+  if (ao_enabled(e)) wgs += (e->d.hidden + cm::AO_ROWS - 1) / cm::AO_ROWS;
   return wgs <= e->n_cus;
 }
 
@@ -1499,9 +1509,11 @@ int ensure_graph(camelid_hip_engine* e, float scale, int mode) {
   return 0;
 }
 
-// Why the engine would refuse these dimensions ("" when it takes them).  Host-only: callable
-// without a device (camelid_hip_check_model).
-std::string dims_problem(const camelid_hip_dims& d) {
+// Why the engine would refuse these dimensions ("" when it takes them).  host_only (the
+// preflight camelid_hip_check_model): no HIP call; the attention's LDS room is judged with the
+// device-free bounds, which decline a max_pos within a few hundred positions of the device's
+// own limit that engine_new would still take.
+std::string dims_problem(const camelid_hip_dims& d, bool host_only) {
   if (!d.n_layers || !d.n_heads || !d.n_kv_heads || !d.head_dim || !d.hidden || !d.ffn_dim || !d.vocab || !d.max_pos)
     return "all dimensions must be nonzero";
   if (d.n_heads % d.n_kv_heads) return "n_heads must be a multiple of n_kv_heads";
@@ -1509,7 +1521,7 @@ std::string dims_problem(const camelid_hip_dims& d) {
   if (!attention_hd_supported(d.head_dim)) return "head_dim must be 64, 128 or 256";
   if (d.hidden > (uint32_t)cm::SEG_MAX_N) return "hidden > 16384 is not supported by the RMSNorm kernel";
   if (d.rope_dim == 0 || d.rope_dim > d.head_dim || d.rope_dim % 2) return "rope_dim must be even and within head_dim";
-  if (attn_ring_slots((d.max_pos + 7u) & ~7u) == 0) return "max_pos too large for the decode attention";
+  if (attn_ring_slots((d.max_pos + 7u) & ~7u, host_only) == 0) return "max_pos too large for the decode attention";
   if (cm::gemv_lds_bytes((int)std::max(d.ffn_dim, d.n_heads * d.head_dim)) > 64 * 1024)
     return "row width too large for the GEMV";
   return "";
@@ -1536,7 +1548,7 @@ const char* camelid_hip_last_error(const camelid_hip_engine* e) { return e ? e->
 int camelid_hip_check_model(const camelid_hip_dims* dims, const uint8_t layer_quant[7], uint8_t out_quant) {
   if (!dims) return fail(nullptr, "null argument");
   const camelid_hip_dims& d = *dims;
-  std::string bad = dims_problem(d);
+  std::string bad = dims_problem(d, true);
   if (!bad.empty()) return fail(nullptr, bad);
   const uint32_t nq = d.n_heads * d.head_dim;
   const uint32_t ks[7] = {d.hidden, d.hidden, d.hidden, nq, d.hidden, d.hidden, d.ffn_dim};
@@ -1555,7 +1567,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   if (!dims || !out) return fail(nullptr, "null argument");
   *out = nullptr;
   const camelid_hip_dims& d = *dims;
-  const std::string bad = dims_problem(d);
+  const std::string bad = dims_problem(d, false);
   if (!bad.empty()) return fail(nullptr, bad);
   auto* e = new camelid_hip_engine();
   e->d = d;

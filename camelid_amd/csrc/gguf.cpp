@@ -34,6 +34,34 @@ int gfail(const std::string& m) {
   return 1;
 }
 
+// IEEE binary16 -> binary32 (exact; subnormal halves normalised), and bfloat16 (the top half
+// of a binary32).
+float camelid_f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1fu, man = h & 0x3ffu, bits;
+  if (exp == 0x1fu) {
+    bits = sign | 0x7f800000u | (man << 13);
+  } else if (exp != 0) {
+    bits = sign | ((exp + 112u) << 23) | (man << 13);
+  } else if (man == 0) {
+    bits = sign;
+  } else {
+    int e = 113;
+    while (!(man & 0x400u)) { man <<= 1; --e; }
+    bits = sign | ((uint32_t)e << 23) | ((man & 0x3ffu) << 13);
+  }
+  float f;
+  std::memcpy(&f, &bits, 4);
+  return f;
+}
+
+float bf16_to_f32(uint16_t b) {
+  const uint32_t bits = (uint32_t)b << 16;
+  float f;
+  std::memcpy(&f, &bits, 4);
+  return f;
+}
+
 // GGML type id -> (values per block, bytes per block) (reader.rs:101-133).
 bool ggml_layout(int32_t t, uint64_t* bs, uint64_t* ts) {
   struct L {
@@ -110,6 +138,9 @@ struct camelid_gguf {
   std::map<std::string, Meta> meta;
   std::vector<std::string> names;
   std::map<std::string, camelid_gguf_tensor> tensors;
+  // rope_freqs.weight widened to f32 when the file stores it as F16 or BF16; the pointer that
+  // camelid_gguf_model hands out stays valid until camelid_gguf_close
+  mutable std::vector<float> rope_freqs_f32;
 };
 
 namespace {
@@ -467,12 +498,41 @@ CX int camelid_gguf_model(const camelid_gguf* g, uint32_t max_pos, camelid_hip_d
   r.orig_ctx = meta_u32(g, key("rope.scaling.original_context_length"), &v) ? (float)v : 8192.0f;
   r.low = meta_f32(g, key("rope.scaling.low_freq_factor"), &f) ? f : 1.0f;
   r.high = meta_f32(g, key("rope.scaling.high_freq_factor"), &f) ? f : 4.0f;
-  const camelid_gguf_tensor* rf = tensor(g, "rope_freqs.weight");
-  // rope_freqs: an F32 tensor holding at least rope_dim/2 factors (its byte count checked too,
-  // so a tensor with a zero trailing dimension is never read past its end)
-  r.freqs = (rf && rf->type == 0 && rf->dims[0] == d.rope_dim / 2 && rf->n_bytes >= (uint64_t)d.rope_dim / 2 * 4)
-                ? reinterpret_cast<const float*>(rf->data)
-                : nullptr;
+  r.freqs = nullptr;
+  if (const camelid_gguf_tensor* rf = tensor(g, "rope_freqs.weight")) {
+    // model.rs:938-944: the RoPE dimension count must be even and within the head dimension,
+    // and the tensor's descriptor shape exactly [rope_dim / 2]
+    if (d.rope_dim == 0 || d.rope_dim > d.head_dim || d.rope_dim % 2 != 0)
+      return gfail("RoPE dimension count " + std::to_string(d.rope_dim) + " must be even and within head dimension " +
+                   std::to_string(d.head_dim));
+    const uint32_t half = d.rope_dim / 2;
+    if (rf->n_dims != 1 || rf->dims[0] != half) {
+      std::string got = "[";
+      for (uint32_t i = 0; i < rf->n_dims; ++i) got += (i ? ", " : "") + std::to_string(rf->dims[i]);
+      return gfail("rope frequencies tensor rope_freqs.weight expected descriptor shape [" + std::to_string(half) +
+                   "], got " + got + "]");
+    }
+    // tensor/mod.rs:3943-3946 load_cpu_f32: F32 as stored, F16 and BF16 widened
+    const uint8_t* p = rf->data;
+    if (rf->type == 0) {
+      r.freqs = reinterpret_cast<const float*>(p);
+    } else if (rf->type == 1 || rf->type == 30) {
+      g->rope_freqs_f32.resize(half);
+      for (uint32_t i = 0; i < half; ++i) {
+        const uint16_t b = (uint16_t)(p[2 * i] | (p[2 * i + 1] << 8));
+        g->rope_freqs_f32[i] = rf->type == 1 ? camelid_f16_to_f32(b) : bf16_to_f32(b);
+      }
+      r.freqs = g->rope_freqs_f32.data();
+    } else {
+      return gfail("rope_freqs.weight of GGML type " + std::to_string(rf->type) +
+                   " is not read by this loader (F32, F16 or BF16 only)");
+    }
+    // rope.rs:303-312 validate_rope_frequency_tensor
+    for (uint32_t i = 0; i < half; ++i)
+      if (!(r.freqs[i] > 0.0f) || !std::isfinite(r.freqs[i]))
+        return gfail("rope_freqs.weight[" + std::to_string(i) + "] frequency factor " + std::to_string(r.freqs[i]) +
+                     " must be finite and positive");
+  }
   *dims = d;
   *rope = r;
   return 0;

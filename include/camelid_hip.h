@@ -60,7 +60,10 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
  * take): 0 when engine_new would accept `dims` and set_layer / set_output would accept a layer
  * whose projections have the formats layer_quant[7] (CAMELID_PROJ_* order; NULL: no layer
  * check) and an lm_head of format out_quant; nonzero otherwise, with the reason in
- * camelid_hip_last_error(NULL).  Needs no device. */
+ * camelid_hip_last_error(NULL).  Makes no HIP call: the decode attention's LDS room is judged
+ * with gfx950's 160 KB per workgroup and a bound on the kernels' static LDS, so a max_pos within
+ * a few hundred positions of the device's own limit may be declined here and still be taken
+ * by engine_new. */
 int camelid_hip_check_model(const camelid_hip_dims* dims, const uint8_t layer_quant[7], uint8_t out_quant);
 /* Drop (cuda_resident.rs:5398 Drop + cuda.rs:485 release_async_pool). */
 void camelid_hip_engine_free(camelid_hip_engine* e);
@@ -244,8 +247,9 @@ int camelid_hip_attention_decode_split(const float* qrot, const uint16_t* kc, co
                                        uint32_t max_pos, const uint32_t* d_pos, float scale,
                                        float* att_out, int8_t* xq, float* xs, void* stream);
 /* No counterpart in the reference: camelid_hip_attention_decode_split for callers that cannot
- * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  The same kernels and bits as camelid_hip_attention_decode_split, but the score
+ * allocate (tight serving loops, harnesses that forbid hipMalloc).  It is not for code under
+ * stream capture: like the allocating entry it reads the position back to the host and
+ * synchronizes the stream.  The same kernels and bits as camelid_hip_attention_decode_split, but the score
  * scratch is a static device array of the library (4 MiB + 64 KiB per GPU, held until the
  * process ends) instead of a per-call allocation; no hipMalloc or hipFree is called.  Limit:
  * n_heads * max_pos <= 2^20 and n_heads * ceil(max_pos / 256) <= 2^14, else an error.  Every

@@ -173,24 +173,50 @@ def test_element_count_overflow_is_refused(tmp_path):
     assert "beyond end of file" in _refusal(tmp_path, gguf_bytes(ok_meta, [("a.weight", [2 ** 32, 2 ** 31], 0, b"")]))
 
 
-def test_short_rope_freqs_is_not_read(tmp_path):
-    """A rope_freqs tensor with the right first dimension but no bytes ([rope_dim/2, 0]) is
-    ignored: the model reader hands out no pointer to read rope_dim/2 factors from."""
+def _model_with_rope_freqs(tmp_path, dims, ggml_type, data):
     cfg = tiny_config()
     model = SyntheticModel.generate(cfg)
-    half = cfg.rope_dim // 2
-    for dims, data, expect in (([half, 0], b"", False), ([half], np.full(half, 2.0, np.float32).tobytes(), True)):
-        p = tmp_path / "rf.gguf"
-        p.write_bytes(model_gguf(model, "llama", extra_tensors=[("rope_freqs.weight", dims, 0, data)]))
-        rc, h, msg = _open(p)
-        assert rc == 0, msg
-        lib = N.lib()
-        try:
-            d, rope = N.Dims(), N.GgufRope()
-            assert lib.camelid_gguf_model(h, 64, C.byref(d), C.byref(rope)) == 0
-            assert bool(rope.freqs) == expect
-            if expect:
-                got = np.ctypeslib.as_array(C.cast(rope.freqs, C.POINTER(C.c_float)), (half,))
-                assert np.all(got == 2.0)
-        finally:
-            lib.camelid_gguf_close(h)
+    p = tmp_path / "rf.gguf"
+    p.write_bytes(model_gguf(model, "llama", extra_tensors=[("rope_freqs.weight", dims, ggml_type, data)]))
+    rc, h, msg = _open(p)
+    assert rc == 0, msg
+    lib = N.lib()
+    d, rope = N.Dims(), N.GgufRope()
+    rc = lib.camelid_gguf_model(h, 64, C.byref(d), C.byref(rope))
+    msg = lib.camelid_gguf_last_error().decode() if rc else ""
+    got = None
+    if rc == 0 and rope.freqs:
+        got = np.ctypeslib.as_array(C.cast(rope.freqs, C.POINTER(C.c_float)), (cfg.rope_dim // 2,)).copy()
+    lib.camelid_gguf_close(h)
+    return rc, msg, got
+
+
+def test_rope_freqs_shape_type_and_values_are_validated(tmp_path):
+    """model.rs:938-944 require_descriptor_shape(rope_freqs, [rope_dim/2]) and rope.rs:287-312
+    validate_rope_frequency_tensor: any other descriptor shape ([half, 0], [half, 2], a short
+    [half - 1]) and any factor that is not finite and positive refuse the model, with the
+    reference's reason; F32 is read in place, F16 and BF16 widened as load_cpu_f32 does
+    (tensor/mod.rs:3943-3946)."""
+    half = tiny_config().rope_dim // 2
+    for dims in ([half, 0], [half, 2], [half - 1]):
+        n = int(np.prod(dims))
+        rc, msg, _ = _model_with_rope_freqs(tmp_path, dims, 0, np.full(n, 2.0, np.float32).tobytes())
+        assert rc != 0 and "expected descriptor shape" in msg, (dims, msg)
+    for bad in (0.0, -1.0, np.inf, np.nan):
+        vals = np.full(half, 2.0, np.float32)
+        vals[3] = bad
+        rc, msg, _ = _model_with_rope_freqs(tmp_path, [half], 0, vals.tobytes())
+        assert rc != 0 and "rope_freqs.weight[3]" in msg and "finite and positive" in msg, (bad, msg)
+    vals = np.linspace(0.5, 8.0, half, dtype=np.float32)
+    rc, msg, got = _model_with_rope_freqs(tmp_path, [half], 0, vals.tobytes())
+    assert rc == 0, msg
+    assert np.array_equal(got, vals)
+    # F16 and BF16 (subnormal and normal halves; every half is exact in f32)
+    h16 = np.array([2.0 ** -20, 6.1e-5, 0.5, 1.0, 1.5, 3.140625, 1000.0, 65504.0] * (half // 8 + 1), np.float16)[:half]
+    rc, msg, got = _model_with_rope_freqs(tmp_path, [half], 1, h16.tobytes())
+    assert rc == 0, msg
+    assert np.array_equal(got, h16.astype(np.float32))
+    b16 = (vals.view(np.uint32) >> 16).astype(np.uint16)
+    rc, msg, got = _model_with_rope_freqs(tmp_path, [half], 30, b16.tobytes())
+    assert rc == 0, msg
+    assert np.array_equal(got, (b16.astype(np.uint32) << 16).view(np.float32))
