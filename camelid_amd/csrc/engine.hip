@@ -173,6 +173,11 @@ struct camelid_hip_engine {
   float *pf_kd = nullptr, *pf_att = nullptr, *pf_tmp = nullptr;
   int8_t* pf_kq = nullptr;
   int32_t* pf_kbs = nullptr;
+  // score rows of the tiled prefill attention (cm::k_attn_prefill_tile; CAMELID_HIP_ATT_TILE=0:
+  // one workgroup per (head, token) instead), sized for a chunk ending at max_pos
+  bool att_tile = true;
+  uint32_t att_tile_pos = 1024;  // chunks ending below this position: per-token kernel (CAMELID_HIP_ATT_TILE_POS)
+  float* pf_sc = nullptr;
   // verify scratch (allocated on first use): inputs of up to CAMELID_MAX_VERIFY_K tokens,
   // their logits and greedy tokens
   float *v_embs = nullptr, *v_cos = nullptr, *v_sin = nullptr, *v_logits = nullptr, *v_pv = nullptr;
@@ -1259,6 +1264,13 @@ void run_embed(camelid_hip_engine* e) {
 // ---------------------------------------------------------------- batched prefill
 constexpr uint32_t PREFILL_CHUNK = 512;  // tokens per pass over the layers
 
+// Scratch floats the tiled prefill attention needs for T tokens up to position pos0 + T - 1
+// (its score rows: 64 per tile, one tile per TQ tokens of each KV head).
+size_t attn_prefill_scratch(uint32_t n_heads, uint32_t n_kv, uint32_t T, uint32_t pos_end) {
+  const uint32_t tq = (uint32_t)cm::apt_tq((int)(n_heads / n_kv));
+  return (size_t)n_kv * ((T + tq - 1) / tq) * cm::APT_R * cm::apt_pitch(pos_end);
+}
+
 int ensure_prefill_buffers(camelid_hip_engine* e) {
   if (e->pf_h) return 0;
   const camelid_hip_dims& d = e->d;
@@ -1268,6 +1280,9 @@ int ensure_prefill_buffers(camelid_hip_engine* e) {
   if (dev_alloc(e, &e->pf_h, tc * d.hidden) || dev_alloc(e, &e->pf_qkv, tc * (nq + 2 * nkv)) ||
       dev_alloc(e, &e->pf_q, tc * nq) || dev_alloc(e, &e->pf_gu, tc * 2 * d.ffn_dim) ||
       dev_alloc(e, &e->pf_xq, tc * act) || dev_alloc(e, &e->pf_xs, tc * act / 32))
+    return 1;
+  if (e->att_tile && cm::apt_hd_ok((int)d.head_dim) && d.n_heads / d.n_kv_heads <= (uint32_t)cm::APT_R &&
+      dev_alloc(e, &e->pf_sc, attn_prefill_scratch(d.n_heads, d.n_kv_heads, PREFILL_CHUNK, e->kvs)))
     return 1;
   if (!e->any_kquant) return 0;
   return dev_alloc(e, &e->pf_kd, tc * act / 256) || dev_alloc(e, &e->pf_kq, tc * act) ||
@@ -1351,9 +1366,31 @@ void launch_gemm(const Q8Mat& m, uint32_t T, const int8_t* xq, const float* xs, 
             (int)m.k, xq, xs, (int)T, y, resid);
 }
 
+// Causal attention of a prefill chunk: the tiled kernel (K/V rows shared by a tile of query
+// tokens and the heads of their KV group) when scratch is given, the geometry has it and the
+// chunk has at least tile_min tokens and reaches position tile_pos, else one workgroup per
+// (head, token): a verify batch of a few tokens spreads wider that way, and below ~1K positions
+// the per-token kernel measured faster (C5 1023-token prefill 0.072 vs 0.076 s, C3 511 tokens
+// 0.016 vs 0.018 s; C4 8191 tokens 1.52 -> 1.03 s tiled).
+constexpr uint32_t APT_TILE_MIN = 32;
+constexpr uint32_t APT_TILE_POS = 1024;
 void launch_attn_prefill(uint32_t hd, uint32_t n_heads, uint32_t n_kv, uint32_t T, const float* q, const uint16_t* kc,
                          const uint16_t* vc, int layer, int kvs, int pos0, float scale, float* att, int8_t* xq, float* xs,
-                         hipStream_t s) {
+                         hipStream_t s, float* scratch = nullptr, uint32_t tile_min = APT_TILE_MIN,
+                         uint32_t tile_pos = APT_TILE_POS) {
+  if (scratch && cm::apt_hd_ok((int)hd) && n_heads / n_kv <= (uint32_t)cm::APT_R && T >= tile_min &&
+      (uint32_t)pos0 + T >= tile_pos) {
+    const uint32_t tq = (uint32_t)cm::apt_tq((int)(n_heads / n_kv));
+    const size_t pitch = cm::apt_pitch((size_t)pos0 + T);
+    const dim3 grid(n_kv, (T + tq - 1) / tq);
+    if (hd == 64)
+      CM_LAUNCH(cm::k_attn_prefill_tile<64>, grid, dim3(cm::APT_NT), cm::apt_lds_bytes(64), s, q, (int)n_heads,
+                (int)n_kv, kc, vc, layer, kvs, pos0, (int)T, scale, scratch, pitch, att, xq, xs);
+    else
+      CM_LAUNCH(cm::k_attn_prefill_tile<128>, grid, dim3(cm::APT_NT), cm::apt_lds_bytes(128), s, q, (int)n_heads,
+                (int)n_kv, kc, vc, layer, kvs, pos0, (int)T, scale, scratch, pitch, att, xq, xs);
+    return;
+  }
   const size_t lds = (((size_t)pos0 + T + 3) & ~(size_t)3) * 4;
 #define CM_AP(HD)                                                                                                  \
   CM_LAUNCH(cm::k_attn_prefill<HD>, dim3(n_heads, T), dim3(cm::AP_NT), lds, s, q, (int)n_heads, (int)n_kv, kc, vc, \
@@ -1401,7 +1438,7 @@ void prefill_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cosv,
             L.k_norm, d.eps, e->pf_q, e->kc, e->vc, (int)l, (int)e->kvs, (const uint32_t*)nullptr, (int)pos0,
             (int)half);
   launch_attn_prefill(d.head_dim, d.n_heads, d.n_kv_heads, T, e->pf_q, e->kc, e->vc, (int)l, (int)e->kvs, (int)pos0,
-                      scale, e->pf_att, e->pf_xq, e->pf_xs, s);
+                      scale, e->pf_att, e->pf_xq, e->pf_xs, s, e->pf_sc, APT_TILE_MIN, e->att_tile_pos);
   if (L.p[3].quant != CAMELID_Q8_0)
     CM_LAUNCH(cm::k_quantize_q8k, dim3(T * nq / 256), dim3(256), 0, s, e->pf_att, e->pf_kd, e->pf_kq,
               e->pf_kbs);
@@ -1440,7 +1477,7 @@ void prefill_chunk(camelid_hip_engine* e, const float* cosv, const float* sinv, 
               L.k_norm, d.eps, e->pf_q, e->kc, e->vc, (int)l, (int)e->kvs, (const uint32_t*)nullptr, (int)pos0,
               (int)half);
     launch_attn_prefill(d.head_dim, d.n_heads, d.n_kv_heads, T, e->pf_q, e->kc, e->vc, (int)l, (int)e->kvs,
-                        (int)pos0, scale, nullptr, e->pf_xq, e->pf_xs, s);
+                        (int)pos0, scale, nullptr, e->pf_xq, e->pf_xs, s, e->pf_sc, APT_TILE_MIN, e->att_tile_pos);
     gemm(L.o, e->pf_h, e->pf_h);
     launch_rmsnorm_quant(e->pf_h, L.ffn_norm, d.hidden, d.eps, e->pf_xq, e->pf_xs, nullptr, s, cm::Prefetch{}, T);
     gemm(L.gu, e->pf_gu, nullptr);
@@ -1599,6 +1636,8 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   if (const char* f = std::getenv("CAMELID_HIP_ATT_SPLIT")) e->att_split_min = (uint32_t)std::strtoul(f, nullptr, 10);
   if (const char* f = std::getenv("CAMELID_HIP_ATT_DG")) e->att_dg = std::atoi(f);
   if (const char* f = std::getenv("CAMELID_HIP_ATT_O")) e->att_o_fused = std::atoi(f) != 0;
+  if (const char* f = std::getenv("CAMELID_HIP_ATT_TILE")) e->att_tile = std::atoi(f) != 0;
+  if (const char* f = std::getenv("CAMELID_HIP_ATT_TILE_POS")) e->att_tile_pos = (uint32_t)std::max(0, std::atoi(f));
   if (const char* f = std::getenv("CAMELID_HIP_ATT_FUSED_SPLIT")) e->att_fsplit = std::atoi(f) != 0;
   {
     int cus = 0;
@@ -1659,7 +1698,7 @@ void camelid_hip_engine_free(camelid_hip_engine* e) {
 int camelid_hip_set_layer(camelid_hip_engine* e, uint32_t layer, const uint8_t* const w[7], const size_t len[7],
                           const uint8_t quant[7], uint8_t q8_layout, const float* attn_norm, const float* ffn_norm,
                           const float* q_norm, const float* k_norm) {
-  if (e) e->nf_state = -1;  // (the fused-norm decision is taken again for the new weights)
+  if (e) e->nf_state = e->ao_state = -1;  // (the fused-launch decisions are taken again for the new weights)
   if (!e) return fail(nullptr, "null engine");
   if (layer >= e->d.n_layers) return fail(e, "layer index out of range");
   if (!w || !len || !quant || !attn_norm || !ffn_norm) return fail(e, "null argument");
@@ -2592,8 +2631,20 @@ int camelid_hip_attention_prefill(const float* qrot, const uint16_t* kc, const u
   if (max_pos % 8) return fail(nullptr, "the KV position stride (max_pos) must be a multiple of 8");
   if (tokens == 0 || (size_t)pos0 + tokens > max_pos) return fail(nullptr, "positions beyond max_pos");
   if (((size_t)pos0 + tokens) * 4 > 64 * 1024) return fail(nullptr, "more than 16384 positions");
+  // the tiled kernel whenever it applies (any token count), unless CAMELID_HIP_ATT_TILE=0;
+  // its score scratch is allocated for the call
+  const char* te = std::getenv("CAMELID_HIP_ATT_TILE");
+  const bool tiled = !(te && std::atoi(te) == 0) && cm::apt_hd_ok((int)hd) && n_heads / n_kv <= (uint32_t)cm::APT_R;
+  float* scratch = nullptr;
+  if (tiled && hipMalloc(&scratch, attn_prefill_scratch(n_heads, n_kv, tokens, pos0 + tokens) * 4) != hipSuccess)
+    return fail(nullptr, "scratch allocation failed");
   launch_attn_prefill(hd, n_heads, n_kv, tokens, qrot, kc, vc, (int)layer, (int)max_pos, (int)pos0, scale, att_out,
-                      xq, xs, (hipStream_t)stream);
+                      xq, xs, (hipStream_t)stream, scratch, 1, 0);
+  if (scratch) {
+    const hipError_t st = hipStreamSynchronize((hipStream_t)stream);
+    (void)hipFree(scratch);
+    if (st != hipSuccess) return fail(nullptr, std::string("attention_prefill: ") + hipGetErrorString(st));
+  }
   return launch_status("attention_prefill");
 }
 

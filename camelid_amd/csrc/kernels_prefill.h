@@ -478,6 +478,329 @@ __global__ __launch_bounds__(AP_NT) void k_attn_prefill(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------
+// Causal attention of a prefill chunk, tiled over query tokens (attention_batched and the
+// flash prefill of cuda_resident.rs:1994, :2523-2757; CPU inference.rs:23945-24025 per token).
+// One workgroup per (KV head g, tile of TQ consecutive tokens).  Its rows are the (query head
+// g*rep + i, token t0 + j) pairs, row r = i*TQ + j, at most 64 of them, so each K and V row of
+// the cache is loaded once per tile and used by every row of it (k_attn_prefill loads it once
+// per (head, token)).  Each row's arithmetic is k_attn_prefill's, in the same order:
+//   A  scores s_p = (sum_d q_d * k_pd, d in order) * scale over 128-position blocks of K
+//      granules in LDS, 4 rows x 4 positions per thread (16 independent chains); the scores go
+//      to the scratch rows sc[r][p]; the row maximum (exact, any order);
+//   B  e_p = expf(s_p - m_r), written back over the score, and folded into the row's sum in
+//      position order by one lane per row (wave 0); inv_r = 1 / sum;
+//   C  prob_p = e_p * inv_r, out_rd = fold_p prob_p * v_pd in position order: the block's V
+//      granules in LDS, 4 rows x DB dims per thread.
+// Every thread reads back only the scratch words it wrote itself (phases A, B and C share one
+// (rows, positions) assignment), so no cache line of another thread's is ever stale.  The next
+// block's global loads (K and V granules, scratch words) go out before the current block is
+// computed.  A row's positions p >= P_r = pos0 + t + 1 contribute e = 0 to its sum and nothing
+// to its outputs (masked adds in the blocks that reach past the tile's first row); a sum that
+// starts at +0 and adds non-negative terms is never -0, so adding +0 leaves it unchanged.  A
+// row with P_r = 1 copies the V row (inference.rs:23564-23575).  Outputs as k_attn_prefill:
+// f32 rows (optional) and Q8_0 per 32-value block.  Scratch: sc + tile_index * 64 * pitch
+// floats, pitch >= P_max rounded up to 128.  Dynamic LDS: apt_lds_bytes(HD).
+constexpr int APT_NT = 512;
+constexpr int APT_R = 64;    // rows per tile
+constexpr int APT_PB = 128;  // positions per block
+constexpr int APT_ES = APT_PB + 4;  // row stride of the exponential / probability block
+__host__ __device__ constexpr int apt_tq(int rep) { return rep >= APT_R ? 1 : APT_R / rep; }
+__host__ __device__ constexpr size_t apt_pitch(size_t pmax) { return (pmax + APT_PB - 1) / APT_PB * APT_PB; }
+__host__ __device__ constexpr size_t apt_lds_bytes(int hd) {
+  return (size_t)hd * APT_R * 4 + (size_t)(hd / 8) * APT_PB * 16 + (size_t)APT_R * APT_ES * 4;
+}
+__host__ __device__ constexpr bool apt_hd_ok(int hd) { return hd == 64 || hd == 128; }
+
+// the f16 value e of the 8 in a 16-byte granule times x, rounded once (v_fma_mix)
+__device__ __forceinline__ float mul_gran(float x, const uint4& g, int e) {
+  const uint32_t w = e < 2 ? g.x : e < 4 ? g.y : e < 6 ? g.z : g.w;
+  return (e & 1) ? mul_f16_hi(x, w) : mul_f16_lo(x, w);
+}
+
+template <int HD>
+__global__ __launch_bounds__(APT_NT) void k_attn_prefill_tile(
+    const float* __restrict__ qrot, int n_heads, int n_kv, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, int layer, int kvs, int pos0, int T, float scale, float* __restrict__ scg,
+    size_t pitch, float* __restrict__ att_out, int8_t* __restrict__ xq, float* __restrict__ xs) {
+  static_assert(apt_hd_ok(HD), "tiled prefill attention: head_dim 64 or 128");
+  constexpr int R8 = HD / 8;            // K granules per position
+  constexpr int DB = HD / 32;           // output dims per thread in phase C (32 dim groups)
+  constexpr int KG = R8 * APT_PB;       // K granules of a block (as many V granules: APT_PB/8 x HD)
+  constexpr int GPT = KG / APT_NT;      // of them per thread
+  static_assert(KG == (APT_PB / 8) * HD && KG % APT_NT == 0, "block staging");
+  extern __shared__ __align__(16) float4 dyn[];
+  float* qs = reinterpret_cast<float*>(dyn);              // [HD][64] q tile; later out rows [64][HD]
+  uint4* kb = reinterpret_cast<uint4*>(qs + HD * APT_R);  // K granules [R8][PB], then V [PB/8][HD]
+  float* eb = reinterpret_cast<float*>(kb + KG);          // [64][APT_ES] exponentials / probabilities
+  __shared__ float mrow[APT_R], irow[APT_R];
+  __shared__ int prow[APT_R];  // P_r (0: no row in this slot)
+  const int tid = threadIdx.x;
+  const int rep = n_heads / n_kv, TQ = apt_tq(rep);
+  const int g = blockIdx.x, ntile = gridDim.y, tile = ntile - 1 - (int)blockIdx.y;  // longest first
+  const int t0 = tile * TQ;
+  const size_t hbase = kv_head_base(layer, n_kv, g, HD, kvs);
+  const uint4* kg = reinterpret_cast<const uint4*>(kc + hbase);
+  const uint4* vg = reinterpret_cast<const uint4*>(vc + hbase);
+  float* sc = scg + ((size_t)g * ntile + tile) * APT_R * pitch;
+  auto row_head = [&](int r) { return g * rep + r / TQ; };
+  auto row_tok = [&](int r) { return t0 + r % TQ; };
+  if (tid < APT_R) {
+    const int i = tid / TQ, t = t0 + tid % TQ;
+    prow[tid] = (i < rep && t < T) ? pos0 + t + 1 : 0;
+  }
+  const int pmax = pos0 + min(t0 + TQ, T);  // the tile's longest row
+  const int pmin = pos0 + t0 + 1;           // its shortest
+  const int nblk = (pmax + APT_PB - 1) / APT_PB;
+  // staging of block b through registers: K granule (u, p) or V granule (group, d) number
+  // i = tid + APT_NT * k (GPT = 2 or 4 named registers: an array here went to scratch memory)
+  const int glast = (pmax - 1) >> 3;
+  uint4 stg0, stg1, stg2, stg3;
+  auto kgran = [&](int b, int k) {
+    const int i = tid + APT_NT * k, u = i / APT_PB, p = i % APT_PB;
+    return kg[(size_t)u * kvs + min(b * APT_PB + p, pmax - 1)];
+  };
+  auto vgran = [&](int b, int k) {
+    const int i = tid + APT_NT * k, gq = i / HD, d = i % HD;
+    return vg[(size_t)min(b * (APT_PB / 8) + gq, glast) * HD + d];
+  };
+#define APT_LOAD_K(b)                                       \
+  stg0 = kgran((b), 0);                                     \
+  stg1 = kgran((b), 1);                                     \
+  if (GPT > 2) {                                            \
+    stg2 = kgran((b), 2);                                   \
+    stg3 = kgran((b), 3);                                   \
+  }
+#define APT_LOAD_V(b)                                       \
+  stg0 = vgran((b), 0);                                     \
+  stg1 = vgran((b), 1);                                     \
+  if (GPT > 2) {                                            \
+    stg2 = vgran((b), 2);                                   \
+    stg3 = vgran((b), 3);                                   \
+  }
+#define APT_PUT()                                           \
+  kb[tid] = stg0;                                           \
+  kb[tid + APT_NT] = stg1;                                  \
+  if (GPT > 2) {                                            \
+    kb[tid + 2 * APT_NT] = stg2;                            \
+    kb[tid + 3 * APT_NT] = stg3;                            \
+  }
+  static_assert(GPT == 2 || GPT == 4, "staging registers");
+  APT_LOAD_K(0)
+  // the q tile, transposed: qs[d][r]
+  for (int i = tid; i < APT_R * HD; i += APT_NT) {
+    const int r = i / HD, d = i % HD;
+    const int t = row_tok(r);
+    const bool ok = r / TQ < rep && t < T;
+    qs[d * APT_R + r] = ok ? qrot[(size_t)t * n_heads * HD + (size_t)row_head(r) * HD + d] : 0.0f;
+  }
+  APT_PUT()
+  __syncthreads();
+  const int rg = tid >> 5, pg = tid & 31;  // rows 4rg .. 4rg+3, block positions 4pg .. 4pg+3
+  int pr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pr[i] = prow[4 * rg + i];
+  auto scw = [&](int i, int b) { return reinterpret_cast<float4*>(sc + (size_t)(4 * rg + i) * pitch + b * APT_PB) + pg; };
+  // ---- A: scores and row maxima
+  float rmax[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  for (int b = 0; b < nblk; ++b) {
+    if (b + 1 < nblk) {
+      APT_LOAD_K(b + 1)
+    }
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+    for (int u = 0; u < R8; ++u) {
+      uint4 k4[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) k4[j] = kb[u * APT_PB + 4 * pg + j];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float4 q4 = reinterpret_cast<const float4*>(qs + (8 * u + e) * APT_R)[rg];
+        const float qv[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] += mul_gran(qv[i], k4[j], e);
+      }
+    }
+    const int p0 = b * APT_PB + 4 * pg;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float sv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        sv[j] = acc[i][j] * scale;
+        if (p0 + j < pr[i]) rmax[i] = fmaxf(rmax[i], sv[j]);
+      }
+      if (pr[i] > p0) *scw(i, b) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+    }
+    __syncthreads();  // every wave is done with this block's K
+    if (b + 1 < nblk) {
+      APT_PUT()
+    }
+    __syncthreads();
+  }
+  APT_LOAD_V(0)  // (the first V block streams during the softmax)
+  // row maxima over the 32 threads of a row group (lanes 32 rg' .. 32 rg' + 31 of a wave)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) rmax[i] = fmaxf(rmax[i], __shfl_xor(rmax[i], o));
+    if (pg == 0) mrow[4 * rg + i] = rmax[i];
+  }
+  __syncthreads();
+  float m[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m[i] = mrow[4 * rg + i];
+  // ---- B: exponentials (over the scores in the scratch), each row's sum in position order
+  float sum = 0.0f;
+  float4 snext[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) snext[i] = pr[i] > 4 * pg ? *scw(i, 0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int b = 0; b < nblk; ++b) {
+    const int p0 = b * APT_PB + 4 * pg;
+    float4 scur[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) scur[i] = snext[i];
+    if (b + 1 < nblk) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) snext[i] = pr[i] > p0 + APT_PB ? *scw(i, b + 1) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float sv[4] = {scur[i].x, scur[i].y, scur[i].z, scur[i].w};
+      float ev[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ev[j] = p0 + j < pr[i] ? glibc_expf(sv[j] - m[i]) : 0.0f;
+      const float4 e4 = make_float4(ev[0], ev[1], ev[2], ev[3]);
+      reinterpret_cast<float4*>(eb + (4 * rg + i) * APT_ES)[pg] = e4;
+      if (pr[i] > p0) *scw(i, b) = e4;
+    }
+    __syncthreads();
+    if (tid < APT_R) {
+      const float* er = eb + tid * APT_ES;
+#pragma unroll 8
+      for (int p = 0; p < APT_PB; ++p) sum += er[p];
+    }
+    __syncthreads();
+  }
+  if (tid < APT_R) irow[tid] = 1.0f / sum;
+  APT_PUT()  // the first V block
+  __syncthreads();
+  float inv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) inv[i] = irow[4 * rg + i];
+  // ---- C: output sums
+  const int dgi = tid & 31;  // dims DB*dgi .. +DB-1 of rows 4rg ..
+  float o[4][DB];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int k = 0; k < DB; ++k) o[i][k] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) snext[i] = pr[i] > 4 * pg ? *scw(i, 0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int b = 0; b < nblk; ++b) {
+    const int pb = b * APT_PB, p0 = pb + 4 * pg;
+    if (b + 1 < nblk) {
+      APT_LOAD_V(b + 1)
+    }
+    float4 ecur[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ecur[i] = snext[i];
+    if (b + 1 < nblk) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) snext[i] = pr[i] > p0 + APT_PB ? *scw(i, b + 1) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float ev[4] = {ecur[i].x, ecur[i].y, ecur[i].z, ecur[i].w};
+      float pv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pv[j] = p0 + j < pr[i] ? ev[j] * inv[i] : 0.0f;
+      reinterpret_cast<float4*>(eb + (4 * rg + i) * APT_ES)[pg] = make_float4(pv[0], pv[1], pv[2], pv[3]);
+    }
+    __syncthreads();
+    const bool masked = pb + APT_PB > pmin;  // a row of the tile ends inside this block
+#pragma unroll 1
+    for (int gq = 0; gq < APT_PB / 8; ++gq) {
+      uint4 v[DB];
+#pragma unroll
+      for (int k = 0; k < DB; ++k) v[k] = kb[gq * HD + DB * dgi + k];
+      float pp[4][8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 a = reinterpret_cast<const float4*>(eb + (4 * rg + i) * APT_ES + 8 * gq)[0];
+        const float4 c = reinterpret_cast<const float4*>(eb + (4 * rg + i) * APT_ES + 8 * gq)[1];
+        pp[i][0] = a.x; pp[i][1] = a.y; pp[i][2] = a.z; pp[i][3] = a.w;
+        pp[i][4] = c.x; pp[i][5] = c.y; pp[i][6] = c.z; pp[i][7] = c.w;
+      }
+      if (!masked) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < DB; ++k) o[i][k] += mul_gran(pp[i][e], v[k], e);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int p = pb + 8 * gq + e;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < DB; ++k) {
+              const float t = mul_gran(pp[i][e], v[k], e);
+              if (p < pr[i]) o[i][k] += t;
+            }
+        }
+      }
+    }
+    __syncthreads();  // every wave is done with this block's V and probabilities
+    if (b + 1 < nblk) {
+      APT_PUT()
+    }
+    // (the next block's probabilities are written after this barrier's successor)
+  }
+  __syncthreads();
+  // ---- outputs: rows to LDS (reusing the q tile), then one (row, 32-value block) per thread
+  float* os = qs;  // [64][HD]
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * rg + i;
+#pragma unroll
+    for (int k = 0; k < DB; ++k) {
+      const int d = DB * dgi + k;
+      // a single position copies the V row (its bits, -0 included)
+      os[r * HD + d] = pr[i] == 1 ? half_bits_to_float(vc[hbase + kv_v_index(HD, 0, d)]) : o[i][k];
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < APT_R * (HD / 32); i += APT_NT) {
+    const int r = i / (HD / 32), blk = i % (HD / 32);
+    if (prow[r] == 0) continue;
+    float y[32];
+#pragma unroll
+    for (int e = 0; e < 32; ++e) y[e] = os[r * HD + 32 * blk + e];
+    const size_t o0 = (size_t)row_tok(r) * n_heads * HD + (size_t)row_head(r) * HD + 32 * blk;
+    if (att_out) {
+#pragma unroll
+      for (int e = 0; e < 32; e += 4)
+        *reinterpret_cast<float4*>(att_out + o0 + e) = make_float4(y[e], y[e + 1], y[e + 2], y[e + 3]);
+    }
+    uint32_t packed[8];
+    xs[o0 >> 5] = quantize_block_regs(y, packed);
+    uint4* qp = reinterpret_cast<uint4*>(xq + o0);
+    qp[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    qp[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+  }
+#undef APT_LOAD_K
+#undef APT_LOAD_V
+#undef APT_PUT
+}
+
+// ---------------------------------------------------------------------------
 // SwiGLU + Q8_0 quantization of T rows (silu_mul_quantize, cuda_resident.rs:1315; CPU
 // tensor/mod.rs:1943-1967).  Row t of gu holds 2F values: [gate | up], or, interleaved,
 // groups of 32 gate values followed by the matching 32 up values.  grid (ceil(F/256), T).

@@ -387,10 +387,16 @@ def test_attention_decode_bit_exact(native, orc, nh, nkv, hd, P):
         assert np.array_equal(xq.download(np.int8, nh * hd), wq)
 
 
+@pytest.mark.parametrize("tiled", [True, False])
 @pytest.mark.parametrize("nh,nkv,hd,pos0,T", [(24, 8, 128, 0, 70), (24, 8, 128, 500, 11), (32, 4, 64, 3, 130),
-                                             (8, 4, 256, 40, 9), (4, 4, 64, 0, 1)])
-def test_attention_prefill_bit_exact(native, orc, nh, nkv, hd, pos0, T):
-    """Causal attention of a prefill chunk == the decode attention of each of its tokens."""
+                                             (8, 4, 256, 40, 9), (4, 4, 64, 0, 1), (32, 8, 128, 8000, 20),
+                                             (24, 8, 128, 700, 64), (4, 4, 64, 0, 200), (32, 8, 128, 61, 33)])
+def test_attention_prefill_bit_exact(native, orc, monkeypatch, nh, nkv, hd, pos0, T, tiled):
+    """Causal attention of a prefill chunk == the decode attention of each of its tokens, for
+    the tiled kernel (a tile's rows sharing K/V blocks, rows ending inside a block, rows of one
+    position) and the one-workgroup-per-(head, token) kernel (CAMELID_HIP_ATT_TILE=0); head_dim
+    256 runs the latter either way."""
+    monkeypatch.setenv("CAMELID_HIP_ATT_TILE", "1" if tiled else "0")
     rng = np.random.default_rng(pos0 * 31 + T + hd)
     L, layer = 2, 1
     max_pos = (pos0 + T + 5 + 7) // 8 * 8
