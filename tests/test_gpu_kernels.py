@@ -111,6 +111,33 @@ def test_q8_gemm_bit_exact(native, orc, rows, k, tokens):
     assert np.array_equal(_bits(dres.download(np.float32, tokens * rows).reshape(tokens, rows)), _bits(resid + want))
 
 
+@pytest.mark.parametrize("rows,k", [(32000, 2048), (128256, 3072)])
+def test_q8_gemm_bit_exact_large(native, orc, rows, k):
+    """The sweep's two largest shapes (TinyLlama's and Llama-3.2-3B's lm_head widths) at the
+    512-token prefill batch: the whole [512, rows] product on the matrix cores, checked against
+    the CPU path's per-token GEMV fold on 384 sampled rows (the first, the last, and rows of
+    every 64-row tile position) for every token."""
+    from camelid_amd.model import synth_q8_0
+    rng = np.random.default_rng(rows + k)
+    tokens = 512
+    wire = synth_q8_0(f"gemm{rows}x{k}", 2, rows, k, 0.02)
+    q, d = _repack(native, wire, rows, k)
+    xs = np.empty((tokens, k // 32), np.float32)
+    xq = np.empty((tokens, k), np.int8)
+    for t in range(tokens):
+        xs[t], xq[t] = orc.quantize_q8_0(rng.normal(0, 1 + t % 5, k).astype(np.float32))
+    wq, wd, dxq, dxs = _dev(q), _dev(d), _dev(xq), _dev(xs)
+    y = _buf(tokens * rows * 4)
+    _ok(native.camelid_hip_q8_0_gemm(wq.ptr, wd.ptr, rows, k, dxq.ptr, dxs.ptr, tokens, y.ptr, None, None))
+    got = y.download(np.float32, tokens * rows).reshape(tokens, rows)
+    sample = np.unique(np.concatenate([[0, rows - 1], np.arange(0, rows, rows // 64)[:64] + np.arange(64) % 64,
+                                       rng.choice(rows, 318, replace=False)]))
+    rb = k // 32 * 34
+    sub = np.ascontiguousarray(wire.reshape(rows, rb)[sample]).ravel()
+    want = np.stack([orc.q8_0_gemv(sub, len(sample), k, xs[t], xq[t]) for t in range(tokens)])
+    assert np.array_equal(_bits(np.ascontiguousarray(got[:, sample])), _bits(want))
+
+
 def test_q8_gemm_extreme_quants(native, orc):
     """All -128 quants (largest |int32| block dot), zero-scale rows, through the matrix cores."""
     rows, k, tokens = 64, 1024, 20
