@@ -558,10 +558,12 @@ def main() -> int:
         pprof = eng.profile_end()
         g = pprof["prefill_gemm"]
         tops = g["bytes"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] else 0.0
-        # the bit-exact fold costs 4 unpacked VALU ops (int->f32, two scale products, add) per
-        # output row, token and 32-wide block (64 int8 ops): a ceiling of 64 lanes x clock / 4
-        # x 64 ops per CU
-        fold_ceiling = n_cu * 64 * PEAK_CLOCK_HZ / 4 * 64 / 1e12
+        # the bit-exact fold costs 3 unpacked VALU ops per output row, token and 32-wide block
+        # (64 int8 ops): float(dot) * w_scale as one mixed FMA on the dot offset by 1.5 * 2^23,
+        # the product with the activation scale, the add; a ceiling of 64 lanes x clock / 3 x 64
+        # ops per CU (the plain form's 4 ops, for matrices with an infinite weight scale, only
+        # lowers it)
+        fold_ceiling = n_cu * 64 * PEAK_CLOCK_HZ / 3 * 64 / 1e12
         prefill_mm = {"tokens": P - 1, "gemm_tops": round(tops, 1), "gemm_ms": round(g["ms"], 3),
                       "gemm_launches": g["launches"], "int8_peak_tops": INT8_PEAK_TOPS,
                       "mfma_frac": round(tops / INT8_PEAK_TOPS, 4),

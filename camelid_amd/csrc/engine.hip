@@ -44,7 +44,17 @@ struct Q8Mat {
   int8_t* q = nullptr;
   uint16_t* d = nullptr;
   uint32_t rows = 0, k = 0;
+  // a weight scale is +-inf (or not known not to be): the prefill GEMM folds with the plain
+  // conversion and product (cm::k_gemm_q8<true>), which gives dot * inf; else with one FMA
+  bool inf_scale = true;
 };
+
+// Whether any of the n f16 values is +-inf.
+bool f16_any_inf(const uint16_t* h, size_t n) {
+  for (size_t i = 0; i < n; ++i)
+    if ((h[i] & 0x7fffu) == 0x7c00u) return true;
+  return false;
+}
 
 // A K-quant matrix as planes split out of its GGUF superblocks (kernels_kquant.h):
 // Q4_K: a = nibbles [rows][k/2], b = headers [rows][k/256][16];
@@ -328,6 +338,7 @@ int upload_q8(camelid_hip_engine* e, Q8Mat* m, const std::vector<Part>& parts, u
   }
   m->rows = rows;
   m->k = k;
+  m->inf_scale = f16_any_inf(d.data(), d.size());
   HIP_TRY(e, hipMemcpy(m->q, q.data(), q.size(), hipMemcpyHostToDevice));
   HIP_TRY(e, hipMemcpy(m->d, d.data(), d.size() * 2, hipMemcpyHostToDevice));
   return 0;
@@ -1362,8 +1373,30 @@ void launch_gemm(const Q8Mat& m, uint32_t T, const int8_t* xq, const float* xs, 
         break;
     }
   }
-  CM_LAUNCH(cm::k_gemm_q8, dim3(cm::gemm_grid((int)m.rows, (int)T)), dim3(cm::GM_NT), 0, s, m.q, m.d, (int)m.rows,
-            (int)m.k, xq, xs, (int)T, y, resid);
+  if (m.inf_scale)
+    CM_LAUNCH(cm::k_gemm_q8<true>, dim3(cm::gemm_grid((int)m.rows, (int)T)), dim3(cm::GM_NT), 0, s, m.q, m.d,
+              (int)m.rows, (int)m.k, xq, xs, (int)T, y, resid);
+  else
+    CM_LAUNCH(cm::k_gemm_q8<false>, dim3(cm::gemm_grid((int)m.rows, (int)T)), dim3(cm::GM_NT), 0, s, m.q, m.d,
+              (int)m.rows, (int)m.k, xq, xs, (int)T, y, resid);
+}
+
+// Q8Mat::inf_scale of weight scales already on the device (the entry points that take device
+// pointers): a scan on the stream, its flag read back (synchronizes the stream).
+int q8_scan_inf_scales(Q8Mat* m, hipStream_t s) {
+  const size_t n = (size_t)m->rows * (m->k / 32);
+  uint32_t* flag = nullptr;
+  uint32_t h = 1;
+  if (hipMalloc(&flag, 4) != hipSuccess) return fail(nullptr, "scale scan: device allocation failed");
+  const uint32_t grid = (uint32_t)std::min<size_t>((n + 255) / 256, 1024);
+  bool ok = hipMemsetAsync(flag, 0, 4, s) == hipSuccess;
+  if (ok) hipLaunchKernelGGL(cm::k_f16_any_inf, dim3(grid), dim3(256), 0, s, m->d, n, flag);
+  ok = ok && hipGetLastError() == hipSuccess && hipMemcpyAsync(&h, flag, 4, hipMemcpyDeviceToHost, s) == hipSuccess &&
+       hipStreamSynchronize(s) == hipSuccess;
+  (void)hipFree(flag);
+  if (!ok) return fail(nullptr, "scale scan failed");
+  m->inf_scale = h != 0;
+  return 0;
 }
 
 // Causal attention of a prefill chunk: the tiled kernel (K/V rows shared by a tile of query
@@ -2619,6 +2652,7 @@ int camelid_hip_q8_0_gemm(const int8_t* wq, const uint16_t* wd, uint32_t rows, u
   m.d = const_cast<uint16_t*>(wd);
   m.rows = rows;
   m.k = k;
+  if (q8_scan_inf_scales(&m, (hipStream_t)stream)) return 1;
   launch_gemm(m, tokens, xq, xs, y, resid, (hipStream_t)stream);
   return launch_status("q8_0_gemm");
 }
@@ -2717,24 +2751,30 @@ int camelid_hip_time_q8_0(int batched, const int8_t* const* wq, const uint16_t* 
   if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) {
     rc = fail(nullptr, "event create failed");
   } else {
+    std::vector<Q8Mat> mats(copies);
+    for (uint32_t c = 0; c < copies && !rc; ++c) {
+      mats[c].q = const_cast<int8_t*>(wq[c]);
+      mats[c].d = const_cast<uint16_t*>(wd[c]);
+      mats[c].rows = rows;
+      mats[c].k = k;
+      if (batched) rc = q8_scan_inf_scales(&mats[c], s);
+    }
     auto launch = [&](uint32_t i) {
-      Q8Mat m;
-      m.q = const_cast<int8_t*>(wq[i % copies]);
-      m.d = const_cast<uint16_t*>(wd[i % copies]);
-      m.rows = rows;
-      m.k = k;
+      const Q8Mat& m = mats[i % copies];
       if (batched)
         launch_gemm(m, tokens, xq, xs, y, nullptr, s);
       else
         launch_gemv(m, xq, xs, y, nullptr, s);
     };
-    for (uint32_t i = 0; i < std::min(copies, 4u); ++i) launch(i);  // warm-up
-    (void)hipEventRecord(a, s);
-    for (uint32_t i = 0; i < iters; ++i) launch(i);
-    (void)hipEventRecord(b, s);
-    if (hipEventSynchronize(b) != hipSuccess || hipEventElapsedTime(ms_out, a, b) != hipSuccess)
-      rc = fail(nullptr, "timing failed");
-    if (!rc && hipGetLastError() != hipSuccess) rc = fail(nullptr, "launch failed");
+    if (!rc) {
+      for (uint32_t i = 0; i < std::min(copies, 4u); ++i) launch(i);  // warm-up
+      (void)hipEventRecord(a, s);
+      for (uint32_t i = 0; i < iters; ++i) launch(i);
+      (void)hipEventRecord(b, s);
+      if (hipEventSynchronize(b) != hipSuccess || hipEventElapsedTime(ms_out, a, b) != hipSuccess)
+        rc = fail(nullptr, "timing failed");
+      if (!rc && hipGetLastError() != hipSuccess) rc = fail(nullptr, "launch failed");
+    }
   }
   if (a) (void)hipEventDestroy(a);
   if (b) (void)hipEventDestroy(b);

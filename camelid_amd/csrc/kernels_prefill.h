@@ -38,26 +38,61 @@ typedef int v4i_t __attribute__((ext_vector_type(4)));
 constexpr int GM_NT = 256;
 constexpr int GM_RN = 64;  // rows per workgroup tile
 constexpr int GM_RT = 64;  // tokens per workgroup tile
-constexpr int GM_BG = 32;  // blocks per scale-staging group
+constexpr int GM_BG = 16;  // blocks per scale-staging group
 constexpr int GM_SB = 4;   // blocks per operand step
 // 8-byte pieces per [block][piece] row of the LDS tile: 64 + 1 pad, so that the planes
 // start 2 banks apart (130 dwords) and the 8 pieces a row's 16-byte chunks scatter to
 // land in different banks (the tile writes are otherwise 8-way bank conflicts)
 constexpr int GM_PS = 65;
+// The block dots start from the bit pattern of 1.5 * 2^23 instead of 0: |dot| <= 32 * 128^2
+// = 2^19 < 2^22, so the int32 sum's bits are those of the f32 value 1.5 * 2^23 + dot (ulp 1
+// in [2^23, 2^24)), and fma(f, w, -(1.5 * 2^23) w) = round(f w - 1.5 * 2^23 w) = round(dot w)
+// exactly (the FMA rounds once, -(1.5 * 2^23) w is exact for every f16 w: 13 significant
+// bits, no overflow).  That is float(dot) * w in one mixed-precision FMA, in place of a
+// conversion and a multiply.  An infinite w (dot * w = +-inf, or NaN at dot = 0) is the one
+// value it does not give: a matrix whose weight scales hold one runs k_gemm_q8<true>, the plain
+// form (the host decides per matrix; q8_scales_have_inf).
+constexpr int32_t GM_MAGIC = 0x4B400000;
+constexpr float GM_MAGIC_F = 12582912.0f;
+
+// a * f32(lo / hi half of w) + c, rounded once: one v_fma_mix_f32.  Written as an fma of the
+// widened half (not inline assembly): the operand a comes straight from a matrix-core result,
+// and only compiler-visible reads get the wait states the hardware needs after an MFMA write.
+__device__ __forceinline__ float fma_f16_lo(float a, uint32_t w, float c) {
+  _Float16 h[2];
+  __builtin_memcpy(h, &w, 4);
+  return __builtin_fmaf(a, (float)h[0], c);
+}
+__device__ __forceinline__ float fma_f16_hi(float a, uint32_t w, float c) {
+  _Float16 h[2];
+  __builtin_memcpy(h, &w, 4);
+  return __builtin_fmaf(a, (float)h[1], c);
+}
+
+template <typename V, V X>
+struct gm_const {
+  static constexpr V value = X;
+};
 
 __host__ __device__ inline int gemm_tiles(int N, int T) {
   return ((N + GM_RN - 1) / GM_RN) * ((T + GM_RT - 1) / GM_RT);
 }
 __host__ __device__ inline int gemm_grid(int N, int T) { return ((gemm_tiles(N, T) + 7) / 8) * 8; }
 
+// PLAIN: the dots from 0, converted and multiplied by the weight scale (two VALU operations);
+// else from the 1.5 * 2^23 pattern, one FMA (GM_MAGIC).  Both give float(dot) * w rounded
+// once, then * xs, then + in block order.
+template <bool PLAIN>
 __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                    int N, int K, const int8_t* __restrict__ xq,
                                                    const float* __restrict__ xs, int T, float* y,
                                                    const float* resid) {
-  static_assert(GM_RN == 64 && GM_RT == 64 && GM_NT == 256 && GM_SB == 4 && GM_BG % GM_SB == 0, "tile layout");
+  static_assert(GM_RN == 64 && GM_RT == 64 && GM_NT == 256 && GM_SB == 4 && GM_BG % GM_SB == 0 &&
+                    GM_NT % GM_BG == 0, "tile layout");
   __shared__ __align__(16) uint2 sa[2][GM_SB][4][GM_PS];
   __shared__ __align__(16) uint2 sb[2][GM_SB][4][GM_PS];
   __shared__ __align__(16) uint16_t swd[GM_BG][GM_RN + 4];
+  __shared__ __align__(16) float snb[GM_BG][GM_RN + 4];  // -(1.5 * 2^23) * f32(wd)
   __shared__ __align__(16) float sxs[GM_BG][GM_RT + 1];
   const int NB = K >> 5;
   const int nsteps = (NB + GM_SB - 1) / GM_SB;
@@ -82,7 +117,7 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq
     gb[j] = xq + (size_t)min(t_base + crow + 32 * j, T - 1) * K;
   }
   uint4 ra[2], rb[2];
-  auto gload = [&](int step) {
+  auto gload = [&](int step) __attribute__((always_inline)) {
     const int off = min(step * 128 + cc * 16, K - 16);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -90,7 +125,7 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq
       rb[j] = *reinterpret_cast<const uint4*>(gb[j] + off);
     }
   };
-  auto lds_put = [&](int buf) {  // bytes 0..7 -> piece 2(cc%2), 8..15 -> piece 2(cc%2)+1
+  auto lds_put = [&](int buf) __attribute__((always_inline)) {  // bytes 0..7 -> piece 2(cc%2), 8..15 -> piece 2(cc%2)+1
     const int bl = cc >> 1, pc = (cc & 1) * 2;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -102,25 +137,26 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq
     }
   };
 
-  // scale staging: thread tid carries block tid % 32 of rows / tokens tid / 32 + 8 i
-  constexpr int SPT = GM_BG * GM_RN / GM_NT;
+  // scale staging: thread tid carries block tid % GM_BG of rows / tokens tid / GM_BG + 16 i
+  constexpr int SPT = GM_BG * GM_RN / GM_NT, SRS = GM_NT / GM_BG;
   uint32_t pw[SPT];
   float px[SPT];
-  auto stage_load = [&](int g0) {
-    const int blk = min(g0 + (tid & 31), NB - 1);
+  auto stage_load = [&](int g0) __attribute__((always_inline)) {
+    const int blk = min(g0 + (tid % GM_BG), NB - 1);
 #pragma unroll
     for (int i = 0; i < SPT; ++i) {
-      const int row = (tid >> 5) + 8 * i;
+      const int row = tid / GM_BG + SRS * i;
       pw[i] = wd[(size_t)min(n_base + row, N - 1) * NB + blk];
       px[i] = xs[(size_t)min(t_base + row, T - 1) * NB + blk];
     }
   };
-  auto stage_store = [&]() {
-    const int bb = tid & 31;
+  auto stage_store = [&]() __attribute__((always_inline)) {
+    const int bb = tid % GM_BG;
 #pragma unroll
     for (int i = 0; i < SPT; ++i) {
-      const int row = (tid >> 5) + 8 * i;
+      const int row = tid / GM_BG + SRS * i;
       swd[bb][row] = (uint16_t)pw[i];
+      if (!PLAIN) snb[bb][row] = -GM_MAGIC_F * half_bits_to_float((uint16_t)pw[i]);
       sxs[bb][row] = px[i];
     }
   };
@@ -133,35 +169,82 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[nf][tf][i] = 0.0f;
 
-  auto block = [&](int buf, int bl, int b) {  // block b = step block bl, from LDS buffer buf
+  // block b = step block bl, from LDS buffer buf
+  auto block = [&](int buf, int bl, int b) __attribute__((always_inline)) {
+    constexpr bool plain = PLAIN;
     long av[2], bv[2];
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
       av[f] = *reinterpret_cast<const long*>(&sa[buf][bl][g][wn + 16 * f + r]);
       bv[f] = *reinterpret_cast<const long*>(&sb[buf][bl][g][wt + 16 * f + r]);
     }
+    const int32_t c0 = plain ? 0 : GM_MAGIC;
     v4i_t c[2][2];
 #pragma unroll
     for (int nf = 0; nf < 2; ++nf)
 #pragma unroll
       for (int tf = 0; tf < 2; ++tf)
-        c[nf][tf] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[nf], bv[tf], v4i_t{0, 0, 0, 0}, 0, 0, 0);
+        c[nf][tf] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[nf], bv[tf], v4i_t{c0, c0, c0, c0}, 0, 0, 0);
     const int sl = b & (GM_BG - 1);
     uint2 w2[2];
+    float4 nb[2];
     float xv[2];
 #pragma unroll
-    for (int nf = 0; nf < 2; ++nf) w2[nf] = *reinterpret_cast<const uint2*>(&swd[sl][wn + 16 * nf + 4 * g]);
+    for (int nf = 0; nf < 2; ++nf) {
+      w2[nf] = *reinterpret_cast<const uint2*>(&swd[sl][wn + 16 * nf + 4 * g]);
+      if (!plain) nb[nf] = *reinterpret_cast<const float4*>(&snb[sl][wn + 16 * nf + 4 * g]);
+    }
 #pragma unroll
     for (int tf = 0; tf < 2; ++tf) xv[tf] = sxs[sl][wt + 16 * tf + r];
 #pragma unroll
     for (int nf = 0; nf < 2; ++nf)
 #pragma unroll
       for (int tf = 0; tf < 2; ++tf) {
-        acc[nf][tf][0] += mul_f16_lo((float)c[nf][tf][0], w2[nf].x) * xv[tf];
-        acc[nf][tf][1] += mul_f16_hi((float)c[nf][tf][1], w2[nf].x) * xv[tf];
-        acc[nf][tf][2] += mul_f16_lo((float)c[nf][tf][2], w2[nf].y) * xv[tf];
-        acc[nf][tf][3] += mul_f16_hi((float)c[nf][tf][3], w2[nf].y) * xv[tf];
+        if (plain) {
+          acc[nf][tf][0] += mul_f16_lo((float)c[nf][tf][0], w2[nf].x) * xv[tf];
+          acc[nf][tf][1] += mul_f16_hi((float)c[nf][tf][1], w2[nf].x) * xv[tf];
+          acc[nf][tf][2] += mul_f16_lo((float)c[nf][tf][2], w2[nf].y) * xv[tf];
+          acc[nf][tf][3] += mul_f16_hi((float)c[nf][tf][3], w2[nf].y) * xv[tf];
+        } else {
+          acc[nf][tf][0] += fma_f16_lo(__int_as_float(c[nf][tf][0]), w2[nf].x, nb[nf].x) * xv[tf];
+          acc[nf][tf][1] += fma_f16_hi(__int_as_float(c[nf][tf][1]), w2[nf].x, nb[nf].y) * xv[tf];
+          acc[nf][tf][2] += fma_f16_lo(__int_as_float(c[nf][tf][2]), w2[nf].y, nb[nf].z) * xv[tf];
+          acc[nf][tf][3] += fma_f16_hi(__int_as_float(c[nf][tf][3]), w2[nf].y, nb[nf].w) * xv[tf];
+        }
       }
+    // the folds stay in this block (not sunk past the staging branch with 16 dots held live)
+#pragma unroll
+    for (int nf = 0; nf < 2; ++nf)
+#pragma unroll
+      for (int tf = 0; tf < 2; ++tf)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[nf][tf][i]));
+  };
+  // operand step s from LDS buffer s % 2, GM_SB blocks (FULL) or the NB % GM_SB of the last
+  // step; then the next step's operands into the other buffer
+  auto run_step = [&](int s, auto fullc) __attribute__((always_inline)) {
+    constexpr bool full = decltype(fullc)::value;
+    const int buf = s & 1, b0 = s * GM_SB;
+    if (s + 1 < nsteps) gload(s + 1);
+    if (full) {
+      block(buf, 0, b0);
+      block(buf, 1, b0 + 1);
+      block(buf, 2, b0 + 2);
+      block(buf, 3, b0 + 3);
+    } else {
+      for (int bl = 0; bl < NB - b0; ++bl) block(buf, bl, b0 + bl);
+    }
+    if (s + 1 < nsteps && ((s + 1) * GM_SB) % GM_BG == 0) {  // next step opens a new scale group
+      lds_put(buf ^ 1);
+      __syncthreads();  // every wave is done with this group's scales
+      stage_store();
+      const int g_next = (s + 1) * GM_SB + GM_BG;
+      if (g_next < NB) stage_load(g_next);
+      __syncthreads();
+    } else {
+      if (s + 1 < nsteps) lds_put(buf ^ 1);
+      __syncthreads();
+    }
   };
 
   stage_load(0);
@@ -170,29 +253,9 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq
   if (GM_BG < NB) stage_load(GM_BG);
   lds_put(0);
   __syncthreads();
-  for (int s = 0; s < nsteps; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < nsteps) gload(s + 1);
-    const int b0 = s * GM_SB;
-    if (b0 + GM_SB <= NB) {
-      block(buf, 0, b0);
-      block(buf, 1, b0 + 1);
-      block(buf, 2, b0 + 2);
-      block(buf, 3, b0 + 3);
-    } else {  // the last, partial step
-      for (int bl = 0; bl < NB - b0; ++bl) block(buf, bl, b0 + bl);
-    }
-    if (s + 1 < nsteps) {
-      lds_put(buf ^ 1);
-      if (((s + 1) * GM_SB) % GM_BG == 0) {  // next step opens a new scale group
-        __syncthreads();  // every wave is done with this group's scales
-        stage_store();
-        const int g_next = (s + 1) * GM_SB + GM_BG;
-        if (g_next < NB) stage_load(g_next);
-      }
-    }
-    __syncthreads();
-  }
+  const int nfull = NB / GM_SB;
+  for (int s = 0; s < nfull; ++s) run_step(s, gm_const<bool, true>{});
+  if (nfull < nsteps) run_step(nfull, gm_const<bool, false>{});  // the partial last step
 #pragma unroll
   for (int nf = 0; nf < 2; ++nf)
 #pragma unroll
@@ -208,6 +271,15 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq
         *reinterpret_cast<float4*>(y + o) = v;
       }
     }
+}
+
+// Sets *flag (cleared by the caller) when one of the n f16 values is +-inf: which fold form a
+// matrix of device-resident weight scales needs (k_gemm_q8<true> if set).
+__global__ __launch_bounds__(256) void k_f16_any_inf(const uint16_t* __restrict__ h, size_t n, uint32_t* flag) {
+  bool inf = false;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    inf |= (h[i] & 0x7fffu) == 0x7c00u;
+  if (inf) *flag = 1u;  // every writer stores the same value
 }
 
 // ---------------------------------------------------------------------------

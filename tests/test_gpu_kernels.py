@@ -157,6 +157,48 @@ def test_q8_gemm_extreme_quants(native, orc):
     assert np.array_equal(_bits(y.download(np.float32, rows * tokens).reshape(tokens, rows)), _bits(want))
 
 
+def test_q8_gemm_special_scales(native, orc):
+    """Weight scales across the f16 range through the GEMM's one-FMA fold (the block dots start
+    from the bits of 1.5 * 2^23, and fma(f, w, -(1.5 * 2^23) w) gives float(dot) * w): subnormal,
+    largest, negative and signed-zero scales, and x scales from f32 subnormals to 1e30.  An
+    infinite weight scale (which the one-FMA form cannot give) switches its 16-block staging
+    group to the plain conversion and product; the expected +-inf and NaN (dot 0 times inf)
+    results come from the CPU fold, compared bit for bit except that any NaN matches any NaN."""
+    rows, k, tokens = 128, 2048, 70
+    nb = k // 32
+    rng = np.random.default_rng(7)
+    quants = rng.integers(-128, 128, (rows, nb, 32), dtype=np.int64).astype(np.int8)
+    wbits = orc.f32_to_f16(rng.normal(0, 0.02, (rows, nb)).astype(np.float32)).view(np.uint16).copy()
+    wbits[5] = rng.integers(1, 0x400, nb)  # f16 subnormals
+    wbits[6, ::2], wbits[6, 1::2] = 0x7BFF, 0xFBFF  # +-65504
+    wbits[7] |= 0x8000  # negative
+    wbits[8, ::2], wbits[8, 1::2] = 0x0000, 0x8000  # +0, -0
+    wbits[9, 20] = 0x7C00  # +inf: tile 0, staging group 1
+    wbits[70, 40] = 0xFC00  # -inf: tile 1, staging group 2
+    wbits[71, 3] = 0x7E00  # NaN (the one-FMA form gives NaN too)
+    wire = np.zeros((rows, nb, 34), np.uint8)
+    wire[:, :, :2] = wbits.view(np.uint8).reshape(rows, nb, 2)
+    wire[:, :, 2:] = quants.view(np.uint8)
+    wire = wire.ravel()
+    q, d = _repack(native, wire, rows, k)
+    xs = np.empty((tokens, nb), np.float32)
+    xq = np.empty((tokens, k), np.int8)
+    for t in range(tokens):
+        xs[t], xq[t] = orc.quantize_q8_0(rng.normal(0, 1 + t % 5, k).astype(np.float32))
+    xq[0, 20 * 32:21 * 32] = 0  # dot 0 against the +inf scale: NaN
+    xs[1] = np.float32(1e-40)  # f32 subnormal
+    xs[2] = np.float32(1e30)
+    xs[3, ::3] = 0.0
+    wq, wd, dxq, dxs = _dev(q), _dev(d), _dev(xq), _dev(xs)
+    y = _buf(rows * tokens * 4)
+    _ok(native.camelid_hip_q8_0_gemm(wq.ptr, wd.ptr, rows, k, dxq.ptr, dxs.ptr, tokens, y.ptr, None, None))
+    got = y.download(np.float32, rows * tokens).reshape(tokens, rows)
+    want = np.stack([orc.q8_0_gemv(wire, rows, k, xs[t], xq[t]) for t in range(tokens)])
+    assert np.isnan(want[0, 9]) and np.isinf(want[1:, 9]).any() and np.isinf(want[:, 70]).any()
+    diff = (_bits(got) != _bits(want)) & ~(np.isnan(got) & np.isnan(want))
+    assert not diff.any(), f"{np.count_nonzero(diff)} mismatches, first at {np.argwhere(diff)[:4].tolist()}"
+
+
 def test_q8_gemv_extreme_quants(native, orc):
     """All -128 quants on both sides (largest |int32| block dot) and zero scales."""
     rows, k = 64, 1024
