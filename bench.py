@@ -336,6 +336,9 @@ def attention_phases(cfg) -> dict:
             continue
         t0 = g[:, 0]
         ph = {lab: float((g[:, i + 1] - t0).mean() * 0.01) for i, lab in enumerate(labels)}
+        if kind == 1 and (g[:, 6] > 0).any():  # the output chain's time in its adds / at barriers
+            ph["chain_adds"] = float(g[:, 6].mean() * 0.01)
+            ph["chain_barrier_wait"] = float(g[:, 7].mean() * 0.01)
         ph["start_spread"] = float((t0.max() - t0.min()) * 0.01)
         ph["launch_span"] = float((g[:, len(labels)].max() - t0.min()) * 0.01)
         ph["workgroups"] = int(len(g))

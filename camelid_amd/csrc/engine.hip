@@ -45,7 +45,7 @@ struct Q8Mat {
   uint16_t* d = nullptr;
   uint32_t rows = 0, k = 0;
   // a weight scale is +-inf (or not known not to be): the prefill GEMM folds with the plain
-  // conversion and product (cm::k_gemm_q8<true>), which gives dot * inf; else with one FMA
+  // conversion and product (cm::k_gemm_q8<true, NF>), which gives dot * inf; else with one FMA
   bool inf_scale = true;
 };
 
@@ -1357,6 +1357,7 @@ void launch_kgemm(const KMat& m, uint32_t T, const float* kd, const int8_t* kq, 
   }
 }
 
+constexpr int GEMM_NF1_BELOW = 512;
 void launch_gemm(const Q8Mat& m, uint32_t T, const int8_t* xq, const float* xs, float* y, const float* resid,
                  hipStream_t s) {
   if (T <= (uint32_t)cm::GMT_MAX && m.k <= 8192) {  // a few tokens: weights streamed once by GEMV-shaped workgroups
@@ -1373,12 +1374,26 @@ void launch_gemm(const Q8Mat& m, uint32_t T, const int8_t* xq, const float* xs, 
         break;
     }
   }
-  if (m.inf_scale)
-    CM_LAUNCH(cm::k_gemm_q8<true>, dim3(cm::gemm_grid((int)m.rows, (int)T)), dim3(cm::GM_NT), 0, s, m.q, m.d,
-              (int)m.rows, (int)m.k, xq, xs, (int)T, y, resid);
-  else
-    CM_LAUNCH(cm::k_gemm_q8<false>, dim3(cm::gemm_grid((int)m.rows, (int)T)), dim3(cm::GM_NT), 0, s, m.q, m.d,
-              (int)m.rows, (int)m.k, xq, xs, (int)T, y, resid);
+  // 32-row tiles when 64-row ones give fewer than two workgroups per CU of the 256 (measured
+  // at 512 tokens: [2048 x 2048] 20.5 -> 18.1 us, [2048 x 5632] 52.8 -> 46.2 us with them; at
+  // 704 tiles, [5632 x 2048], 36.3 -> 40.4 us, so not there).  CAMELID_HIP_GEMM_NF=1 / 2
+  // forces either tile height.
+  int nf = cm::gemm_tiles((int)m.rows, (int)T, 2) < GEMM_NF1_BELOW ? 1 : 2;
+  if (const char* f = std::getenv("CAMELID_HIP_GEMM_NF")) {
+    if (f[0] == '1') nf = 1;
+    if (f[0] == '2') nf = 2;
+  }
+#define CM_GEMM(PLAIN, NF)                                                                                      \
+  CM_LAUNCH((cm::k_gemm_q8<PLAIN, NF>), dim3(cm::gemm_grid((int)m.rows, (int)T, NF)), dim3(cm::GM_NT), 0, s, m.q, \
+            m.d, (int)m.rows, (int)m.k, xq, xs, (int)T, y, resid)
+  if (m.inf_scale) {
+    if (nf == 1) CM_GEMM(true, 1);
+    else CM_GEMM(true, 2);
+  } else {
+    if (nf == 1) CM_GEMM(false, 1);
+    else CM_GEMM(false, 2);
+  }
+#undef CM_GEMM
 }
 
 // Q8Mat::inf_scale of weight scales already on the device (the entry points that take device

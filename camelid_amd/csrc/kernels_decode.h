@@ -1982,7 +1982,8 @@ __device__ uint64_t g_att_stamps[ATT_STAMP_LAYERS * ATT_STAMP_HEADS * ATT_NSTAMP
 // The split attention's workgroups (measurement build): kind 0 k_att_scores (workgroup index
 // head * slices + slice), 1 k_att_out (head * dim groups + group); per workgroup < 1024 of the
 // last layer: k_att_scores 0 start, 1 q built, 2 scores done, 3 end; k_att_out 0 start,
-// 1 scores loaded and maximum, 2 exponentials, 3 denominator, 4 output sums, 5 end.
+// 1 scores loaded and maximum, 2 exponentials, 3 denominator, 4 output sums, 5 end, and the
+// output chain's time summed over its product blocks: 6 in its adds, 7 at the block barriers.
 constexpr int SPLIT_NSTAMP = 8, SPLIT_STAMP_WGS = 1024;
 #ifdef CM_STAMPS
 __device__ uint64_t g_split_stamps[2 * SPLIT_STAMP_WGS * SPLIT_NSTAMP];
@@ -3033,7 +3034,13 @@ __device__ __forceinline__ void att_out_body(
       if (tid >= 64) products(0);
       __syncthreads();
     }
+#ifdef CM_STAMPS
+    uint64_t t_adds = 0, t_wait = 0, t_mark = 0;  // (thread 0: time in the adds, at the barriers)
+#endif
     for (int b = 0; b < nb; ++b) {
+#ifdef CM_STAMPS
+      if (tid == 0) t_mark = __builtin_amdgcn_s_memrealtime();
+#endif
       if (tid < DW) {
         const float4* row = reinterpret_cast<const float4*>(pbuf + ((size_t)(b & 1) * DW + tid) * AVP_RS);
         const int n4 = min(BG, ng - b * BG) * 2;  // 4-position pieces of this block
@@ -3071,8 +3078,24 @@ __device__ __forceinline__ void att_out_body(
           if ((b + 2) % BPC == 0 && q < nchunks) wait_vmcnt(LH * (issued - 1 - q));
         }
       }
+#ifdef CM_STAMPS
+      if (tid == 0) {
+        const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+        t_adds += t1 - t_mark;
+        t_mark = t1;
+      }
+#endif
       __syncthreads();  // wave 0 is done with buffer b & 1; block b + 1's products are visible
+#ifdef CM_STAMPS
+      if (tid == 0) t_wait += __builtin_amdgcn_s_memrealtime() - t_mark;
+#endif
     }
+#ifdef CM_STAMPS
+    if (tid == 0 && bid < SPLIT_STAMP_WGS) {  // slots 6, 7: sums over the blocks, not times
+      g_split_stamps[(SPLIT_STAMP_WGS + bid) * SPLIT_NSTAMP + 6] = t_adds;
+      g_split_stamps[(SPLIT_STAMP_WGS + bid) * SPLIT_NSTAMP + 7] = t_wait;
+    }
+#endif
     CM_SPLIT_STAMP(1, bid, 4)
     if (tid < DW) {
 #pragma unroll

@@ -24,34 +24,37 @@ typedef int v4i_t __attribute__((ext_vector_type(4)));
 // tokens) fragment and block; its K = 32 is exactly one Q8_0 block, so every block's int32
 // dot comes out separately (any assignment of the 32 byte positions to lanes gives the same
 // integer, as long as the weight and activation operands use the same one).
-// Workgroup: 4 waves over a 64-row x 64-token tile, each wave 32 x 32 (2 x 2 fragments).
+// Workgroup: 4 waves over a (32 NF)-row x 64-token tile, each wave 16 NF x 32 (NF x 2 fragments).
 // Lane l of a fragment supplies row / token l % 16, bytes 8*(l/16) .. +7 of the block, and
 // receives the outputs of rows 4*(l/16) + i (i = 0..3) for token l % 16.
 // Operands move in steps of 4 blocks (128 bytes of every row and token): coalesced 16-byte
 // global loads into registers one step ahead, then into a double-buffered LDS tile laid out
 // [block][8-byte piece][row] (a fragment read is 16 consecutive 8-byte pieces per piece
-// index: no bank conflicts).  Scales are staged in LDS 32 blocks at a time (transposed:
+// index: no bank conflicts).  Scales are staged in LDS 16 blocks at a time (transposed:
 // [block][row], [block][token]), the next group's held in registers meanwhile.
 // Tiles are dealt so that each XCD (workgroup id mod 8) runs a contiguous range of tiles,
 // token tiles innermost: the row tile's weights are read once per XCD and re-read from its L2.
 // N % 4 == 0 (16-byte output stores); K % 32 == 0; y may alias resid.
 constexpr int GM_NT = 256;
-constexpr int GM_RN = 64;  // rows per workgroup tile
 constexpr int GM_RT = 64;  // tokens per workgroup tile
 constexpr int GM_BG = 16;  // blocks per scale-staging group
 constexpr int GM_SB = 4;   // blocks per operand step
-// 8-byte pieces per [block][piece] row of the LDS tile: 64 + 1 pad, so that the planes
-// start 2 banks apart (130 dwords) and the 8 pieces a row's 16-byte chunks scatter to
-// land in different banks (the tile writes are otherwise 8-way bank conflicts)
-constexpr int GM_PS = 65;
+// Rows per workgroup tile: 32 * NF, NF = 2 (64) or 1 (32, for small grids: a [3072 x 3072] x 511
+// product has 384 tiles of 64 x 64, one or two 4-wave workgroups per CU, and a single wave
+// issues one VALU instruction per ~7 clocks, so each SIMD then idles half the time).
+__host__ __device__ constexpr int gm_rows(int NF) { return 32 * NF; }
+// 8-byte pieces per [block][piece] row of an LDS operand tile: rows + 1 pad, so that the
+// planes start 2 banks apart (2 * rows + 2 dwords) and the 8 pieces a row's 16-byte chunks
+// scatter to land in different banks (the tile writes are otherwise 8-way bank conflicts)
+__host__ __device__ constexpr int gm_ps(int rows) { return rows + 1; }
 // The block dots start from the bit pattern of 1.5 * 2^23 instead of 0: |dot| <= 32 * 128^2
 // = 2^19 < 2^22, so the int32 sum's bits are those of the f32 value 1.5 * 2^23 + dot (ulp 1
 // in [2^23, 2^24)), and fma(f, w, -(1.5 * 2^23) w) = round(f w - 1.5 * 2^23 w) = round(dot w)
 // exactly (the FMA rounds once, -(1.5 * 2^23) w is exact for every f16 w: 13 significant
 // bits, no overflow).  That is float(dot) * w in one mixed-precision FMA, in place of a
 // conversion and a multiply.  An infinite w (dot * w = +-inf, or NaN at dot = 0) is the one
-// value it does not give: a matrix whose weight scales hold one runs k_gemm_q8<true>, the plain
-// form (the host decides per matrix; q8_scales_have_inf).
+// value it does not give: a matrix whose weight scales hold one runs k_gemm_q8<true, NF>, the
+// plain form (the host decides per matrix).
 constexpr int32_t GM_MAGIC = 0x4B400000;
 constexpr float GM_MAGIC_F = 12582912.0f;
 
@@ -74,96 +77,98 @@ struct gm_const {
   static constexpr V value = X;
 };
 
-__host__ __device__ inline int gemm_tiles(int N, int T) {
-  return ((N + GM_RN - 1) / GM_RN) * ((T + GM_RT - 1) / GM_RT);
+__host__ __device__ inline int gemm_tiles(int N, int T, int NF = 2) {
+  return ((N + gm_rows(NF) - 1) / gm_rows(NF)) * ((T + GM_RT - 1) / GM_RT);
 }
-__host__ __device__ inline int gemm_grid(int N, int T) { return ((gemm_tiles(N, T) + 7) / 8) * 8; }
+__host__ __device__ inline int gemm_grid(int N, int T, int NF = 2) { return ((gemm_tiles(N, T, NF) + 7) / 8) * 8; }
 
 // PLAIN: the dots from 0, converted and multiplied by the weight scale (two VALU operations);
 // else from the 1.5 * 2^23 pattern, one FMA (GM_MAGIC).  Both give float(dot) * w rounded
 // once, then * xs, then + in block order.
-template <bool PLAIN>
+// Waves: 2 (rows) x 2 (tokens), each 16 NF rows x 32 tokens (NF x 2 fragments).
+template <bool PLAIN, int NF>
 __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                    int N, int K, const int8_t* __restrict__ xq,
                                                    const float* __restrict__ xs, int T, float* y,
                                                    const float* resid) {
-  static_assert(GM_RN == 64 && GM_RT == 64 && GM_NT == 256 && GM_SB == 4 && GM_BG % GM_SB == 0 &&
+  constexpr int RN = gm_rows(NF), PSA = gm_ps(RN), PSB = gm_ps(GM_RT);
+  constexpr int AJ = RN / 32, BJ = GM_RT / 32;  // 16-byte global loads per thread and step
+  static_assert((NF == 1 || NF == 2) && GM_RT == 64 && GM_NT == 256 && GM_SB == 4 && GM_BG % GM_SB == 0 &&
                     GM_NT % GM_BG == 0, "tile layout");
-  __shared__ __align__(16) uint2 sa[2][GM_SB][4][GM_PS];
-  __shared__ __align__(16) uint2 sb[2][GM_SB][4][GM_PS];
-  __shared__ __align__(16) uint16_t swd[GM_BG][GM_RN + 4];
-  __shared__ __align__(16) float snb[GM_BG][GM_RN + 4];  // -(1.5 * 2^23) * f32(wd)
+  __shared__ __align__(16) uint2 sa[2][GM_SB][4][PSA];
+  __shared__ __align__(16) uint2 sb[2][GM_SB][4][PSB];
+  __shared__ __align__(16) uint16_t swd[GM_BG][RN + 4];
+  __shared__ __align__(16) float snb[GM_BG][RN + 4];  // -(1.5 * 2^23) * f32(wd)
   __shared__ __align__(16) float sxs[GM_BG][GM_RT + 1];
   const int NB = K >> 5;
   const int nsteps = (NB + GM_SB - 1) / GM_SB;
   const int ntt = (T + GM_RT - 1) / GM_RT;
-  const int tiles = gemm_tiles(N, T);
+  const int tiles = gemm_tiles(N, T, NF);
   const int per = (tiles + 7) >> 3;
   const int L = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
   if (L >= tiles) return;
-  const int n_base = (L / ntt) * GM_RN, t_base = (L % ntt) * GM_RT;
+  const int n_base = (L / ntt) * RN, t_base = (L % ntt) * GM_RT;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int r = lane & 15, g = lane >> 4;
-  const int wn = (wave & 1) * 32, wt = (wave >> 1) * 32;
+  const int wn = (wave & 1) * 16 * NF, wt = (wave >> 1) * 32;
 
   // global -> register loads of one step: chunk j of thread tid is 16 bytes of row / token
   // (tid + 256 j) / 8 at byte (tid % 8) * 16 of the step's 128
   const int crow = tid >> 3, cc = tid & 7;
-  const int8_t* ga[2];
-  const int8_t* gb[2];
+  const int8_t* ga[AJ];
+  const int8_t* gb[BJ];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    ga[j] = wq + (size_t)min(n_base + crow + 32 * j, N - 1) * K;
-    gb[j] = xq + (size_t)min(t_base + crow + 32 * j, T - 1) * K;
-  }
-  uint4 ra[2], rb[2];
+  for (int j = 0; j < AJ; ++j) ga[j] = wq + (size_t)min(n_base + crow + 32 * j, N - 1) * K;
+#pragma unroll
+  for (int j = 0; j < BJ; ++j) gb[j] = xq + (size_t)min(t_base + crow + 32 * j, T - 1) * K;
+  uint4 ra[AJ], rb[BJ];
   auto gload = [&](int step) __attribute__((always_inline)) {
     const int off = min(step * 128 + cc * 16, K - 16);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      ra[j] = *reinterpret_cast<const uint4*>(ga[j] + off);
-      rb[j] = *reinterpret_cast<const uint4*>(gb[j] + off);
-    }
+    for (int j = 0; j < AJ; ++j) ra[j] = *reinterpret_cast<const uint4*>(ga[j] + off);
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) rb[j] = *reinterpret_cast<const uint4*>(gb[j] + off);
   };
   auto lds_put = [&](int buf) __attribute__((always_inline)) {  // bytes 0..7 -> piece 2(cc%2), 8..15 -> piece 2(cc%2)+1
     const int bl = cc >> 1, pc = (cc & 1) * 2;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int row = crow + 32 * j;
-      sa[buf][bl][pc][row] = make_uint2(ra[j].x, ra[j].y);
-      sa[buf][bl][pc + 1][row] = make_uint2(ra[j].z, ra[j].w);
-      sb[buf][bl][pc][row] = make_uint2(rb[j].x, rb[j].y);
-      sb[buf][bl][pc + 1][row] = make_uint2(rb[j].z, rb[j].w);
+    for (int j = 0; j < AJ; ++j) {
+      sa[buf][bl][pc][crow + 32 * j] = make_uint2(ra[j].x, ra[j].y);
+      sa[buf][bl][pc + 1][crow + 32 * j] = make_uint2(ra[j].z, ra[j].w);
+    }
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) {
+      sb[buf][bl][pc][crow + 32 * j] = make_uint2(rb[j].x, rb[j].y);
+      sb[buf][bl][pc + 1][crow + 32 * j] = make_uint2(rb[j].z, rb[j].w);
     }
   };
 
   // scale staging: thread tid carries block tid % GM_BG of rows / tokens tid / GM_BG + 16 i
-  constexpr int SPT = GM_BG * GM_RN / GM_NT, SRS = GM_NT / GM_BG;
-  uint32_t pw[SPT];
-  float px[SPT];
+  constexpr int SPW = GM_BG * RN / GM_NT, SPX = GM_BG * GM_RT / GM_NT, SRS = GM_NT / GM_BG;
+  uint32_t pw[SPW];
+  float px[SPX];
   auto stage_load = [&](int g0) __attribute__((always_inline)) {
     const int blk = min(g0 + (tid % GM_BG), NB - 1);
 #pragma unroll
-    for (int i = 0; i < SPT; ++i) {
-      const int row = tid / GM_BG + SRS * i;
-      pw[i] = wd[(size_t)min(n_base + row, N - 1) * NB + blk];
-      px[i] = xs[(size_t)min(t_base + row, T - 1) * NB + blk];
-    }
+    for (int i = 0; i < SPW; ++i) pw[i] = wd[(size_t)min(n_base + tid / GM_BG + SRS * i, N - 1) * NB + blk];
+#pragma unroll
+    for (int i = 0; i < SPX; ++i) px[i] = xs[(size_t)min(t_base + tid / GM_BG + SRS * i, T - 1) * NB + blk];
   };
   auto stage_store = [&]() __attribute__((always_inline)) {
     const int bb = tid % GM_BG;
 #pragma unroll
-    for (int i = 0; i < SPT; ++i) {
+    for (int i = 0; i < SPW; ++i) {
       const int row = tid / GM_BG + SRS * i;
       swd[bb][row] = (uint16_t)pw[i];
       if (!PLAIN) snb[bb][row] = -GM_MAGIC_F * half_bits_to_float((uint16_t)pw[i]);
-      sxs[bb][row] = px[i];
     }
+#pragma unroll
+    for (int i = 0; i < SPX; ++i) sxs[bb][tid / GM_BG + SRS * i] = px[i];
   };
 
-  float acc[2][2][4];
+  float acc[NF][2][4];
 #pragma unroll
-  for (int nf = 0; nf < 2; ++nf)
+  for (int nf = 0; nf < NF; ++nf)
 #pragma unroll
     for (int tf = 0; tf < 2; ++tf)
 #pragma unroll
@@ -172,32 +177,31 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq
   // block b = step block bl, from LDS buffer buf
   auto block = [&](int buf, int bl, int b) __attribute__((always_inline)) {
     constexpr bool plain = PLAIN;
-    long av[2], bv[2];
+    long av[NF], bv[2];
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
-      av[f] = *reinterpret_cast<const long*>(&sa[buf][bl][g][wn + 16 * f + r]);
-      bv[f] = *reinterpret_cast<const long*>(&sb[buf][bl][g][wt + 16 * f + r]);
-    }
+    for (int f = 0; f < NF; ++f) av[f] = *reinterpret_cast<const long*>(&sa[buf][bl][g][wn + 16 * f + r]);
+#pragma unroll
+    for (int f = 0; f < 2; ++f) bv[f] = *reinterpret_cast<const long*>(&sb[buf][bl][g][wt + 16 * f + r]);
     const int32_t c0 = plain ? 0 : GM_MAGIC;
-    v4i_t c[2][2];
+    v4i_t c[NF][2];
 #pragma unroll
-    for (int nf = 0; nf < 2; ++nf)
+    for (int nf = 0; nf < NF; ++nf)
 #pragma unroll
       for (int tf = 0; tf < 2; ++tf)
         c[nf][tf] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[nf], bv[tf], v4i_t{c0, c0, c0, c0}, 0, 0, 0);
     const int sl = b & (GM_BG - 1);
-    uint2 w2[2];
-    float4 nb[2];
+    uint2 w2[NF];
+    float4 nb[NF];
     float xv[2];
 #pragma unroll
-    for (int nf = 0; nf < 2; ++nf) {
+    for (int nf = 0; nf < NF; ++nf) {
       w2[nf] = *reinterpret_cast<const uint2*>(&swd[sl][wn + 16 * nf + 4 * g]);
       if (!plain) nb[nf] = *reinterpret_cast<const float4*>(&snb[sl][wn + 16 * nf + 4 * g]);
     }
 #pragma unroll
     for (int tf = 0; tf < 2; ++tf) xv[tf] = sxs[sl][wt + 16 * tf + r];
 #pragma unroll
-    for (int nf = 0; nf < 2; ++nf)
+    for (int nf = 0; nf < NF; ++nf)
 #pragma unroll
       for (int tf = 0; tf < 2; ++tf) {
         if (plain) {
@@ -212,9 +216,9 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq
           acc[nf][tf][3] += fma_f16_hi(__int_as_float(c[nf][tf][3]), w2[nf].y, nb[nf].w) * xv[tf];
         }
       }
-    // the folds stay in this block (not sunk past the staging branch with 16 dots held live)
+    // the folds stay in this block (not sunk past the staging branch with the dots held live)
 #pragma unroll
-    for (int nf = 0; nf < 2; ++nf)
+    for (int nf = 0; nf < NF; ++nf)
 #pragma unroll
       for (int tf = 0; tf < 2; ++tf)
 #pragma unroll
@@ -257,7 +261,7 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq
   for (int s = 0; s < nfull; ++s) run_step(s, gm_const<bool, true>{});
   if (nfull < nsteps) run_step(nfull, gm_const<bool, false>{});  // the partial last step
 #pragma unroll
-  for (int nf = 0; nf < 2; ++nf)
+  for (int nf = 0; nf < NF; ++nf)
 #pragma unroll
     for (int tf = 0; tf < 2; ++tf) {
       const int t = t_base + wt + 16 * tf + r, n = n_base + wn + 16 * nf + 4 * g;

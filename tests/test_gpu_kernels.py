@@ -111,6 +111,26 @@ def test_q8_gemm_bit_exact(native, orc, rows, k, tokens):
     assert np.array_equal(_bits(dres.download(np.float32, tokens * rows).reshape(tokens, rows)), _bits(resid + want))
 
 
+@pytest.mark.parametrize("rows,k,tokens,nf", [(5120, 3072, 130, "2"), (36, 96, 70, "2"), (2048, 5632, 65, "2"),
+                                              (32000, 2048, 200, "1"), (4100, 5632, 300, "1")])
+def test_q8_gemm_forced_tile_height(native, orc, monkeypatch, rows, k, tokens, nf):
+    """The GEMM at the tile height its size would not pick (64 rows for small grids, 32 for a
+    large one): the same bits as the CPU fold."""
+    monkeypatch.setenv("CAMELID_HIP_GEMM_NF", nf)
+    rng = np.random.default_rng(rows + 5 * k + tokens)
+    wire = orc.quantize_q8_0_wire(rng.normal(0, 0.02, rows * k).astype(np.float32))
+    q, d = _repack(native, wire, rows, k)
+    xs = np.empty((tokens, k // 32), np.float32)
+    xq = np.empty((tokens, k), np.int8)
+    for t in range(tokens):
+        xs[t], xq[t] = orc.quantize_q8_0(rng.normal(0, 1 + t % 5, k).astype(np.float32))
+    resid = rng.normal(0, 1, (tokens, rows)).astype(np.float32)
+    wq, wd, dxq, dxs, dres = _dev(q), _dev(d), _dev(xq), _dev(xs), _dev(resid)
+    _ok(native.camelid_hip_q8_0_gemm(wq.ptr, wd.ptr, rows, k, dxq.ptr, dxs.ptr, tokens, dres.ptr, dres.ptr, None))
+    want = np.stack([orc.q8_0_gemv(wire, rows, k, xs[t], xq[t]) for t in range(tokens)])
+    assert np.array_equal(_bits(dres.download(np.float32, tokens * rows).reshape(tokens, rows)), _bits(resid + want))
+
+
 @pytest.mark.parametrize("rows,k", [(32000, 2048), (128256, 3072)])
 def test_q8_gemm_bit_exact_large(native, orc, rows, k):
     """The sweep's two largest shapes (TinyLlama's and Llama-3.2-3B's lm_head widths) at the
@@ -157,13 +177,16 @@ def test_q8_gemm_extreme_quants(native, orc):
     assert np.array_equal(_bits(y.download(np.float32, rows * tokens).reshape(tokens, rows)), _bits(want))
 
 
-def test_q8_gemm_special_scales(native, orc):
+@pytest.mark.parametrize("nf", ["1", "2"])
+def test_q8_gemm_special_scales(native, orc, monkeypatch, nf):
     """Weight scales across the f16 range through the GEMM's one-FMA fold (the block dots start
     from the bits of 1.5 * 2^23, and fma(f, w, -(1.5 * 2^23) w) gives float(dot) * w): subnormal,
     largest, negative and signed-zero scales, and x scales from f32 subnormals to 1e30.  An
     infinite weight scale (which the one-FMA form cannot give) switches its 16-block staging
     group to the plain conversion and product; the expected +-inf and NaN (dot 0 times inf)
-    results come from the CPU fold, compared bit for bit except that any NaN matches any NaN."""
+    results come from the CPU fold, compared bit for bit except that any NaN matches any NaN.
+    Both tile heights (32 and 64 rows) run."""
+    monkeypatch.setenv("CAMELID_HIP_GEMM_NF", nf)
     rows, k, tokens = 128, 2048, 70
     nb = k // 32
     rng = np.random.default_rng(7)
