@@ -1431,12 +1431,23 @@ void launch_attn_prefill(uint32_t hd, uint32_t n_heads, uint32_t n_kv, uint32_t 
     const uint32_t tq = (uint32_t)cm::apt_tq((int)(n_heads / n_kv));
     const size_t pitch = cm::apt_pitch((size_t)pos0 + T);
     const dim3 grid(n_kv, (T + tq - 1) / tq);
-    if (hd == 64)
-      CM_LAUNCH(cm::k_attn_prefill_tile<64>, grid, dim3(cm::APT_NT), cm::apt_lds_bytes(64), s, q, (int)n_heads,
-                (int)n_kv, kc, vc, layer, kvs, pos0, (int)T, scale, scratch, pitch, att, xq, xs);
-    else
-      CM_LAUNCH(cm::k_attn_prefill_tile<128>, grid, dim3(cm::APT_NT), cm::apt_lds_bytes(128), s, q, (int)n_heads,
-                (int)n_kv, kc, vc, layer, kvs, pos0, (int)T, scale, scratch, pitch, att, xq, xs);
+    // 1024 threads (2 rows per thread, 110 VGPRs: four waves per SIMD) by default; 512 (4 rows
+    // per thread, 155 VGPRs, two waves per SIMD) with CAMELID_HIP_APT_NT=512.  C4's 8191-token
+    // prefill: 1.004 s at 512, 0.915 s at 1024 (a single wave issues one VALU instruction per
+    // ~7 clocks, so two waves leave a SIMD idle between their issues)
+    const char* nt = std::getenv("CAMELID_HIP_APT_NT");
+    const bool wide = !(nt && std::atoi(nt) == 512);
+#define CM_APT(HD, NT)                                                                                        \
+  CM_LAUNCH((cm::k_attn_prefill_tile<HD, NT>), grid, dim3(NT), cm::apt_lds_bytes(HD), s, q, (int)n_heads,     \
+            (int)n_kv, kc, vc, layer, kvs, pos0, (int)T, scale, scratch, pitch, att, xq, xs)
+    if (hd == 64) {
+      if (wide) CM_APT(64, 1024);
+      else CM_APT(64, 512);
+    } else {
+      if (wide) CM_APT(128, 1024);
+      else CM_APT(128, 512);
+    }
+#undef CM_APT
     return;
   }
   const size_t lds = (((size_t)pos0 + T + 3) & ~(size_t)3) * 4;

@@ -576,7 +576,7 @@ __global__ __launch_bounds__(AP_NT) void k_attn_prefill(const float* __restrict_
 // row with P_r = 1 copies the V row (inference.rs:23564-23575).  Outputs as k_attn_prefill:
 // f32 rows (optional) and Q8_0 per 32-value block.  Scratch: sc + tile_index * 64 * pitch
 // floats, pitch >= P_max rounded up to 128.  Dynamic LDS: apt_lds_bytes(HD).
-constexpr int APT_NT = 512;
+constexpr int APT_NT = 1024;  // threads (the kernel is also instantiated at 512)
 constexpr int APT_R = 64;    // rows per tile
 constexpr int APT_PB = 128;  // positions per block
 constexpr int APT_ES = APT_PB + 4;  // row stride of the exponential / probability block
@@ -593,8 +593,8 @@ __device__ __forceinline__ float mul_gran(float x, const uint4& g, int e) {
   return (e & 1) ? mul_f16_hi(x, w) : mul_f16_lo(x, w);
 }
 
-template <int HD>
-__global__ __launch_bounds__(APT_NT) void k_attn_prefill_tile(
+template <int HD, int NT = APT_NT>
+__global__ __launch_bounds__(NT) void k_attn_prefill_tile(
     const float* __restrict__ qrot, int n_heads, int n_kv, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int layer, int kvs, int pos0, int T, float scale, float* __restrict__ scg,
     size_t pitch, float* __restrict__ att_out, int8_t* __restrict__ xq, float* __restrict__ xs) {
@@ -602,8 +602,10 @@ __global__ __launch_bounds__(APT_NT) void k_attn_prefill_tile(
   constexpr int R8 = HD / 8;            // K granules per position
   constexpr int DB = HD / 32;           // output dims per thread in phase C (32 dim groups)
   constexpr int KG = R8 * APT_PB;       // K granules of a block (as many V granules: APT_PB/8 x HD)
-  constexpr int GPT = KG / APT_NT;      // of them per thread
-  static_assert(KG == (APT_PB / 8) * HD && KG % APT_NT == 0, "block staging");
+  constexpr int GPT = KG / NT;          // of them per thread
+  constexpr int NRG = NT / 32;          // row groups: 32 threads each (4 positions / DB dims a thread)
+  constexpr int RPT = APT_R / NRG;      // rows per thread: 4 at 512 threads, 2 at 1024
+  static_assert(KG == (APT_PB / 8) * HD && KG % NT == 0 && (RPT == 2 || RPT == 4), "block staging");
   extern __shared__ __align__(16) float4 dyn[];
   float* qs = reinterpret_cast<float*>(dyn);              // [HD][64] q tile; later out rows [64][HD]
   uint4* kb = reinterpret_cast<uint4*>(qs + HD * APT_R);  // K granules [R8][PB], then V [PB/8][HD]
@@ -628,42 +630,42 @@ __global__ __launch_bounds__(APT_NT) void k_attn_prefill_tile(
   const int pmin = pos0 + t0 + 1;           // its shortest
   const int nblk = (pmax + APT_PB - 1) / APT_PB;
   // staging of block b through registers: K granule (u, p) or V granule (group, d) number
-  // i = tid + APT_NT * k (GPT = 2 or 4 named registers: an array here went to scratch memory)
+  // i = tid + NT * k (GPT = 1, 2 or 4 named registers: an array here went to scratch memory)
   const int glast = (pmax - 1) >> 3;
   uint4 stg0, stg1, stg2, stg3;
   auto kgran = [&](int b, int k) {
-    const int i = tid + APT_NT * k, u = i / APT_PB, p = i % APT_PB;
+    const int i = tid + NT * k, u = i / APT_PB, p = i % APT_PB;
     return kg[(size_t)u * kvs + min(b * APT_PB + p, pmax - 1)];
   };
   auto vgran = [&](int b, int k) {
-    const int i = tid + APT_NT * k, gq = i / HD, d = i % HD;
+    const int i = tid + NT * k, gq = i / HD, d = i % HD;
     return vg[(size_t)min(b * (APT_PB / 8) + gq, glast) * HD + d];
   };
 #define APT_LOAD_K(b)                                       \
   stg0 = kgran((b), 0);                                     \
-  stg1 = kgran((b), 1);                                     \
+  if (GPT > 1) stg1 = kgran((b), 1);                        \
   if (GPT > 2) {                                            \
     stg2 = kgran((b), 2);                                   \
     stg3 = kgran((b), 3);                                   \
   }
 #define APT_LOAD_V(b)                                       \
   stg0 = vgran((b), 0);                                     \
-  stg1 = vgran((b), 1);                                     \
+  if (GPT > 1) stg1 = vgran((b), 1);                        \
   if (GPT > 2) {                                            \
     stg2 = vgran((b), 2);                                   \
     stg3 = vgran((b), 3);                                   \
   }
 #define APT_PUT()                                           \
   kb[tid] = stg0;                                           \
-  kb[tid + APT_NT] = stg1;                                  \
+  if (GPT > 1) kb[tid + NT] = stg1;                         \
   if (GPT > 2) {                                            \
-    kb[tid + 2 * APT_NT] = stg2;                            \
-    kb[tid + 3 * APT_NT] = stg3;                            \
+    kb[tid + 2 * NT] = stg2;                                \
+    kb[tid + 3 * NT] = stg3;                                \
   }
-  static_assert(GPT == 2 || GPT == 4, "staging registers");
+  static_assert(GPT == 1 || GPT == 2 || GPT == 4, "staging registers");
   APT_LOAD_K(0)
   // the q tile, transposed: qs[d][r]
-  for (int i = tid; i < APT_R * HD; i += APT_NT) {
+  for (int i = tid; i < APT_R * HD; i += NT) {
     const int r = i / HD, d = i % HD;
     const int t = row_tok(r);
     const bool ok = r / TQ < rep && t < T;
@@ -671,20 +673,36 @@ __global__ __launch_bounds__(APT_NT) void k_attn_prefill_tile(
   }
   APT_PUT()
   __syncthreads();
-  const int rg = tid >> 5, pg = tid & 31;  // rows 4rg .. 4rg+3, block positions 4pg .. 4pg+3
-  int pr[4];
+  const int rg = tid >> 5, pg = tid & 31;  // rows RPT rg .. +RPT-1, block positions 4pg .. 4pg+3
+  int pr[RPT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) pr[i] = prow[4 * rg + i];
-  auto scw = [&](int i, int b) { return reinterpret_cast<float4*>(sc + (size_t)(4 * rg + i) * pitch + b * APT_PB) + pg; };
+  for (int i = 0; i < RPT; ++i) pr[i] = prow[RPT * rg + i];
+  auto scw = [&](int i, int b) { return reinterpret_cast<float4*>(sc + (size_t)(RPT * rg + i) * pitch + b * APT_PB) + pg; };
+  // the q values of this thread's RPT rows for dim d (one LDS read)
+  auto qrows = [&](int d, float (&qv)[RPT]) {
+    if constexpr (RPT == 4) {
+      const float4 q4 = reinterpret_cast<const float4*>(qs + d * APT_R)[rg];
+      qv[0] = q4.x;
+      qv[1] = q4.y;
+      qv[2] = q4.z;
+      qv[3] = q4.w;
+    } else {
+      const float2 q2 = reinterpret_cast<const float2*>(qs + d * APT_R)[rg];
+      qv[0] = q2.x;
+      qv[1] = q2.y;
+    }
+  };
   // ---- A: scores and row maxima
-  float rmax[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  float rmax[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) rmax[i] = -INFINITY;
   for (int b = 0; b < nblk; ++b) {
     if (b + 1 < nblk) {
       APT_LOAD_K(b + 1)
     }
-    float acc[4][4];
+    float acc[RPT][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RPT; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
     for (int u = 0; u < R8; ++u) {
@@ -693,17 +711,17 @@ __global__ __launch_bounds__(APT_NT) void k_attn_prefill_tile(
       for (int j = 0; j < 4; ++j) k4[j] = kb[u * APT_PB + 4 * pg + j];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float4 q4 = reinterpret_cast<const float4*>(qs + (8 * u + e) * APT_R)[rg];
-        const float qv[4] = {q4.x, q4.y, q4.z, q4.w};
+        float qv[RPT];
+        qrows(8 * u + e, qv);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < RPT; ++i)
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[i][j] += mul_gran(qv[i], k4[j], e);
       }
     }
     const int p0 = b * APT_PB + 4 * pg;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < RPT; ++i) {
       float sv[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -721,37 +739,37 @@ __global__ __launch_bounds__(APT_NT) void k_attn_prefill_tile(
   APT_LOAD_V(0)  // (the first V block streams during the softmax)
   // row maxima over the 32 threads of a row group (lanes 32 rg' .. 32 rg' + 31 of a wave)
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < RPT; ++i) {
 #pragma unroll
     for (int o = 16; o >= 1; o >>= 1) rmax[i] = fmaxf(rmax[i], __shfl_xor(rmax[i], o));
-    if (pg == 0) mrow[4 * rg + i] = rmax[i];
+    if (pg == 0) mrow[RPT * rg + i] = rmax[i];
   }
   __syncthreads();
-  float m[4];
+  float m[RPT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) m[i] = mrow[4 * rg + i];
+  for (int i = 0; i < RPT; ++i) m[i] = mrow[RPT * rg + i];
   // ---- B: exponentials (over the scores in the scratch), each row's sum in position order
   float sum = 0.0f;
-  float4 snext[4];
+  float4 snext[RPT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) snext[i] = pr[i] > 4 * pg ? *scw(i, 0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int i = 0; i < RPT; ++i) snext[i] = pr[i] > 4 * pg ? *scw(i, 0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   for (int b = 0; b < nblk; ++b) {
     const int p0 = b * APT_PB + 4 * pg;
-    float4 scur[4];
+    float4 scur[RPT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) scur[i] = snext[i];
+    for (int i = 0; i < RPT; ++i) scur[i] = snext[i];
     if (b + 1 < nblk) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) snext[i] = pr[i] > p0 + APT_PB ? *scw(i, b + 1) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      for (int i = 0; i < RPT; ++i) snext[i] = pr[i] > p0 + APT_PB ? *scw(i, b + 1) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < RPT; ++i) {
       const float sv[4] = {scur[i].x, scur[i].y, scur[i].z, scur[i].w};
       float ev[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) ev[j] = p0 + j < pr[i] ? glibc_expf(sv[j] - m[i]) : 0.0f;
       const float4 e4 = make_float4(ev[0], ev[1], ev[2], ev[3]);
-      reinterpret_cast<float4*>(eb + (4 * rg + i) * APT_ES)[pg] = e4;
+      reinterpret_cast<float4*>(eb + (RPT * rg + i) * APT_ES)[pg] = e4;
       if (pr[i] > p0) *scw(i, b) = e4;
     }
     __syncthreads();
@@ -765,37 +783,37 @@ __global__ __launch_bounds__(APT_NT) void k_attn_prefill_tile(
   if (tid < APT_R) irow[tid] = 1.0f / sum;
   APT_PUT()  // the first V block
   __syncthreads();
-  float inv[4];
+  float inv[RPT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) inv[i] = irow[4 * rg + i];
+  for (int i = 0; i < RPT; ++i) inv[i] = irow[RPT * rg + i];
   // ---- C: output sums
-  const int dgi = tid & 31;  // dims DB*dgi .. +DB-1 of rows 4rg ..
-  float o[4][DB];
+  const int dgi = tid & 31;  // dims DB*dgi .. +DB-1 of rows RPT rg ..
+  float o[RPT][DB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < RPT; ++i)
 #pragma unroll
     for (int k = 0; k < DB; ++k) o[i][k] = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) snext[i] = pr[i] > 4 * pg ? *scw(i, 0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int i = 0; i < RPT; ++i) snext[i] = pr[i] > 4 * pg ? *scw(i, 0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   for (int b = 0; b < nblk; ++b) {
     const int pb = b * APT_PB, p0 = pb + 4 * pg;
     if (b + 1 < nblk) {
       APT_LOAD_V(b + 1)
     }
-    float4 ecur[4];
+    float4 ecur[RPT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ecur[i] = snext[i];
+    for (int i = 0; i < RPT; ++i) ecur[i] = snext[i];
     if (b + 1 < nblk) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) snext[i] = pr[i] > p0 + APT_PB ? *scw(i, b + 1) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      for (int i = 0; i < RPT; ++i) snext[i] = pr[i] > p0 + APT_PB ? *scw(i, b + 1) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < RPT; ++i) {
       const float ev[4] = {ecur[i].x, ecur[i].y, ecur[i].z, ecur[i].w};
       float pv[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) pv[j] = p0 + j < pr[i] ? ev[j] * inv[i] : 0.0f;
-      reinterpret_cast<float4*>(eb + (4 * rg + i) * APT_ES)[pg] = make_float4(pv[0], pv[1], pv[2], pv[3]);
+      reinterpret_cast<float4*>(eb + (RPT * rg + i) * APT_ES)[pg] = make_float4(pv[0], pv[1], pv[2], pv[3]);
     }
     __syncthreads();
     const bool masked = pb + APT_PB > pmin;  // a row of the tile ends inside this block
@@ -804,11 +822,11 @@ __global__ __launch_bounds__(APT_NT) void k_attn_prefill_tile(
       uint4 v[DB];
 #pragma unroll
       for (int k = 0; k < DB; ++k) v[k] = kb[gq * HD + DB * dgi + k];
-      float pp[4][8];
+      float pp[RPT][8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float4 a = reinterpret_cast<const float4*>(eb + (4 * rg + i) * APT_ES + 8 * gq)[0];
-        const float4 c = reinterpret_cast<const float4*>(eb + (4 * rg + i) * APT_ES + 8 * gq)[1];
+      for (int i = 0; i < RPT; ++i) {
+        const float4 a = reinterpret_cast<const float4*>(eb + (RPT * rg + i) * APT_ES + 8 * gq)[0];
+        const float4 c = reinterpret_cast<const float4*>(eb + (RPT * rg + i) * APT_ES + 8 * gq)[1];
         pp[i][0] = a.x; pp[i][1] = a.y; pp[i][2] = a.z; pp[i][3] = a.w;
         pp[i][4] = c.x; pp[i][5] = c.y; pp[i][6] = c.z; pp[i][7] = c.w;
       }
@@ -816,7 +834,7 @@ __global__ __launch_bounds__(APT_NT) void k_attn_prefill_tile(
 #pragma unroll
         for (int e = 0; e < 8; ++e)
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < RPT; ++i)
 #pragma unroll
             for (int k = 0; k < DB; ++k) o[i][k] += mul_gran(pp[i][e], v[k], e);
       } else {
@@ -824,7 +842,7 @@ __global__ __launch_bounds__(APT_NT) void k_attn_prefill_tile(
         for (int e = 0; e < 8; ++e) {
           const int p = pb + 8 * gq + e;
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < RPT; ++i)
 #pragma unroll
             for (int k = 0; k < DB; ++k) {
               const float t = mul_gran(pp[i][e], v[k], e);
@@ -843,8 +861,8 @@ __global__ __launch_bounds__(APT_NT) void k_attn_prefill_tile(
   // ---- outputs: rows to LDS (reusing the q tile), then one (row, 32-value block) per thread
   float* os = qs;  // [64][HD]
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 4 * rg + i;
+  for (int i = 0; i < RPT; ++i) {
+    const int r = RPT * rg + i;
 #pragma unroll
     for (int k = 0; k < DB; ++k) {
       const int d = DB * dgi + k;
@@ -853,7 +871,7 @@ __global__ __launch_bounds__(APT_NT) void k_attn_prefill_tile(
     }
   }
   __syncthreads();
-  for (int i = tid; i < APT_R * (HD / 32); i += APT_NT) {
+  for (int i = tid; i < APT_R * (HD / 32); i += NT) {
     const int r = i / (HD / 32), blk = i % (HD / 32);
     if (prow[r] == 0) continue;
     float y[32];
