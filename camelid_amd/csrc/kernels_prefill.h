@@ -30,14 +30,14 @@ typedef int v4i_t __attribute__((ext_vector_type(4)));
 // Operands move in steps of 4 blocks (128 bytes of every row and token): coalesced 16-byte
 // global loads into registers one step ahead, then into a double-buffered LDS tile laid out
 // [block][8-byte piece][row] (a fragment read is 16 consecutive 8-byte pieces per piece
-// index: no bank conflicts).  Scales are staged in LDS 16 blocks at a time (transposed:
+// index: no bank conflicts).  Scales are staged in LDS 8 blocks at a time (transposed:
 // [block][row], [block][token]), the next group's held in registers meanwhile.
 // Tiles are dealt so that each XCD (workgroup id mod 8) runs a contiguous range of tiles,
 // token tiles innermost: the row tile's weights are read once per XCD and re-read from its L2.
 // N % 4 == 0 (16-byte output stores); K % 32 == 0; y may alias resid.
 constexpr int GM_NT = 256;
 constexpr int GM_RT = 64;  // tokens per workgroup tile
-constexpr int GM_BG = 16;  // blocks per scale-staging group
+constexpr int GM_BG = 8;   // blocks per scale-staging group
 constexpr int GM_SB = 4;   // blocks per operand step
 // Rows per workgroup tile: 32 * NF, NF = 2 (64) or 1 (32, for small grids: a [3072 x 3072] x 511
 // product has 384 tiles of 64 x 64, one or two 4-wave workgroups per CU, and a single wave
@@ -86,8 +86,9 @@ __host__ __device__ inline int gemm_grid(int N, int T, int NF = 2) { return ((ge
 // else from the 1.5 * 2^23 pattern, one FMA (GM_MAGIC).  Both give float(dot) * w rounded
 // once, then * xs, then + in block order.
 // Waves: 2 (rows) x 2 (tokens), each 16 NF rows x 32 tokens (NF x 2 fragments).
+// (at most 128 VGPRs and, with 8-block scale groups, under 40 KB of LDS: four workgroups per CU)
 template <bool PLAIN, int NF>
-__global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+__global__ __launch_bounds__(GM_NT, 4) void k_gemm_q8(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                    int N, int K, const int8_t* __restrict__ xq,
                                                    const float* __restrict__ xs, int T, float* y,
                                                    const float* resid) {
