@@ -3028,7 +3028,10 @@ __device__ __forceinline__ void att_out_body(
     if (nb > 0) {
       if (stager) {
         if (issued < min(R, nchunks)) stage(issued++);  // chunk R - 1 into the unused slot
-        wait_vmcnt(LH * (issued - 1));                  // chunk 0 has landed
+        // chunk 0 has landed, and the chunk of block 1 (chunk 1 when a chunk holds one block):
+        // block 1's products are formed in the loop's first iteration, before its first wait
+        const int q1 = min(nchunks - 1, 1 / BPC);
+        wait_vmcnt(LH * (issued - 1 - q1));
       }
       __syncthreads();  // chunk 0 and the normalised probabilities
       if (tid >= 64) products(0);
