@@ -567,11 +567,15 @@ def main() -> int:
         # ops per CU (the plain form's 4 ops, for matrices with an infinite weight scale, only
         # lowers it)
         fold_ceiling = n_cu * 64 * PEAK_CLOCK_HZ / 3 * 64 / 1e12
+        # (the same rate over the ceiling of the 4-operation fold -- convert, x w_scale, x x_scale,
+        # add -- which the GEMM used before the offset accumulator: the figure earlier builds reported)
+        fold4_ceiling = fold_ceiling * 3 / 4
         prefill_mm = {"tokens": P - 1, "gemm_tops": round(tops, 1), "gemm_ms": round(g["ms"], 3),
                       "gemm_launches": g["launches"], "int8_peak_tops": INT8_PEAK_TOPS,
                       "mfma_frac": round(tops / INT8_PEAK_TOPS, 4),
                       "valu_fold_ceiling_tops": round(fold_ceiling, 1),
-                      "frac_of_fold_ceiling": round(tops / fold_ceiling, 4),
+                      "frac_of_fold_ceiling": round(tops / fold_ceiling, 4), "fold_valu_ops": 3,
+                      "frac_of_4op_fold_ceiling": round(tops / fold4_ceiling, 4),
                       "all_kernels_ms": round(sum(v["ms"] for v in pprof.values()), 3)}
         log(f"prefill projections: {tops:.1f} TOP/s over {g['launches']} launches "
             f"({tops / INT8_PEAK_TOPS:.3f} of the int8 peak, {tops / fold_ceiling:.3f} of the fold ceiling)")
