@@ -66,6 +66,9 @@ struct KMat {
   int8_t* sc = nullptr;
   uint16_t* d = nullptr;
   uint32_t rows = 0, k = 0;
+  // Q6_K projections: the scaled weights as class-major int8 planes [rows][k/256][512] for the
+  // prefill GEMM (cm::k_gemm_q6k2, built by cm::k_q6k_w2); null: the sparse-MFMA GEMM
+  int8_t* w2 = nullptr;
 };
 
 // One projection in its own format (the layers with any K-quant projection keep all seven
@@ -149,6 +152,7 @@ struct camelid_hip_engine {
   // K-quant layers with the RMSNorm inside the q|k+v and gate|up launches (cm::k_norm_qk4_v6,
   // cm::k_norm_gemv_q4k; CAMELID_HIP_KQ_NORM_FUSED): on when every layer has that shape
   bool kq_norm_fused = true;
+  bool q6_gemm2 = true;  // Q6_K projections get the class-major prefill GEMM's planes (CAMELID_HIP_Q6K_GEMM2)
   int nf_state = -1;              // -1 unknown, 0 off, 1 on (every layer fusable)
   uint32_t* nf_slots = nullptr;   // the launches' flag words (cm::NF_WORDS)
   // Q8_0 layers: the output projection inside the single-workgroup attention launch
@@ -375,7 +379,7 @@ constexpr uint32_t KQ_MAX_K = 16384;
 thread_local std::string g_launch_error;
 
 int upload_kq(camelid_hip_engine* e, KMat* m, const uint8_t* src, size_t len, uint32_t rows, uint32_t k,
-              uint8_t quant) {
+              uint8_t quant, bool gemm_planes = false) {
   if (quant != CAMELID_Q4_K && quant != CAMELID_Q6_K) return fail(e, "unknown weight format");
   if (!src) return fail(e, "missing projection bytes");
   if (k % 256) return fail(e, "K-quant row width must be a multiple of 256");
@@ -410,6 +414,13 @@ int upload_kq(camelid_hip_engine* e, KMat* m, const uint8_t* src, size_t len, ui
   if (quant == CAMELID_Q6_K) {
     HIP_TRY(e, hipMemcpy(m->sc, sc.data(), sc.size(), hipMemcpyHostToDevice));
     HIP_TRY(e, hipMemcpy(m->d, d.data(), d.size() * 2, hipMemcpyHostToDevice));
+    if (gemm_planes && e->q6_gemm2) {  // the prefill GEMM's weight planes, built on the device
+      if (!m->w2 && dev_alloc(e, &m->w2, (size_t)rows * nsb * cm::Q6G_W2)) return 1;
+      hipLaunchKernelGGL(cm::k_q6k_w2, dim3((uint32_t)nsb, rows), dim3(256), 0, e->stream, m->a, m->b, m->sc, (int)k,
+                         m->w2);
+      HIP_TRY(e, hipGetLastError());
+      HIP_TRY(e, hipStreamSynchronize(e->stream));
+    }
   }
   return 0;
 }
@@ -1342,7 +1353,12 @@ void launch_kgemm(const KMat& m, uint32_t T, const float* kd, const int8_t* kq, 
               (int)m.rows, (int)m.k, kd, kq, (int)T, y, (int)ldy, resid);
     return;
   }
-  if (T > (uint32_t)cm::Q6M_MAX) {  // a chunk: the matrix-core GEMM
+  if (T > (uint32_t)cm::Q6M_MAX && m.w2 && m.rows % 4 == 0 && ldy % 4 == 0) {  // a chunk: class-major GEMM
+    CM_LAUNCH(cm::k_gemm_q6k2, dim3(cm::gemm_q6k2_grid((int)m.rows, (int)T)), dim3(cm::Q6G_NT), 0, s, m.w2, m.d,
+              (int)m.rows, (int)m.k, kd, kq, (int)T, y, (int)ldy, resid);
+    return;
+  }
+  if (T > (uint32_t)cm::Q6M_MAX) {  // a chunk: the sparse-MFMA GEMM
     CM_LAUNCH(cm::k_gemm_q6k, dim3((m.rows + cm::G6_RN - 1) / cm::G6_RN, (T + cm::G6_RT - 1) / cm::G6_RT),
               dim3(cm::G6_NT), 0, s, m.a, m.b, m.sc, m.d, (int)m.rows, (int)m.k, kd, kq, (int)T, y, (int)ldy, resid);
     return;
@@ -1691,6 +1707,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   if (const char* f = std::getenv("CAMELID_HIP_FUSED_NORM")) e->norm_fused = std::atoi(f) != 0;
   if (const char* f = std::getenv("CAMELID_HIP_QKV_MERGED")) e->qkv_merged = std::atoi(f) != 0;
   if (const char* f = std::getenv("CAMELID_HIP_KQ_NORM_FUSED")) e->kq_norm_fused = std::atoi(f) != 0;
+  if (const char* f = std::getenv("CAMELID_HIP_Q6K_GEMM2")) e->q6_gemm2 = std::atoi(f) != 0;
   e->att_slots = attn_ring_slots(e->kvs);
   if (const char* f = std::getenv("CAMELID_HIP_ATT_SPLIT")) e->att_split_min = (uint32_t)std::strtoul(f, nullptr, 10);
   if (const char* f = std::getenv("CAMELID_HIP_ATT_DG")) e->att_dg = std::atoi(f);
@@ -1799,10 +1816,10 @@ int camelid_hip_set_layer(camelid_hip_engine* e, uint32_t layer, const uint8_t* 
         const size_t per_row = (size_t)(ks[i] / 256) * kq_block_bytes(quant[i]);
         if (len[i] != (size_t)rows[i] * per_row || len[i + 1] != (size_t)rows[i + 1] * per_row)
           return fail(e, "K-quant byte length does not match the projection shape");
-        rc = upload_kq(e, &P.kq, both.data(), both.size(), rows[i] + rows[i + 1], ks[i], quant[i]);
+        rc = upload_kq(e, &P.kq, both.data(), both.size(), rows[i] + rows[i + 1], ks[i], quant[i], true);
       } else {
         rc = quant[i] == CAMELID_Q8_0 ? upload_q8(e, &P.q8, {{w[i], len[i], rows[i]}}, ks[i], q8_layout)
-                                      : upload_kq(e, &P.kq, w[i], len[i], rows[i], ks[i], quant[i]);
+                                      : upload_kq(e, &P.kq, w[i], len[i], rows[i], ks[i], quant[i], true);
       }
       if (rc) return 1;
     }
@@ -2760,8 +2777,25 @@ int camelid_hip_kquant_gemm(uint8_t quant, const uint8_t* a, const uint8_t* b, c
   m.d = const_cast<uint16_t*>(d);
   m.rows = rows;
   m.k = k;
+  // Q6_K chunks: the class-major GEMM with its weight planes built for this call (a temporary
+  // allocation; the stream is synchronized before it is freed) unless CAMELID_HIP_Q6K_GEMM2=0
+  const char* g2 = std::getenv("CAMELID_HIP_Q6K_GEMM2");
+  const bool planes = quant == CAMELID_Q6_K && tokens > (uint32_t)cm::Q6M_MAX && rows % 4 == 0 && ldy % 4 == 0 &&
+                      !(g2 && std::atoi(g2) == 0);
+  if (planes) {
+    if (hipMalloc(&m.w2, (size_t)rows * (k / 256) * cm::Q6G_W2) != hipSuccess)
+      return fail(nullptr, "kquant_gemm: weight plane allocation failed");
+    hipLaunchKernelGGL(cm::k_q6k_w2, dim3(k / 256, rows), dim3(256), 0, (hipStream_t)stream, m.a, m.b, m.sc, (int)k,
+                       m.w2);
+  }
   launch_kgemm(m, tokens, yd, yq, y, ldy, resid, (hipStream_t)stream);
-  return launch_status("kquant_gemm");
+  const int rc = launch_status("kquant_gemm");
+  if (planes) {
+    const bool synced = hipStreamSynchronize((hipStream_t)stream) == hipSuccess;
+    (void)hipFree(m.w2);
+    if (!synced && !rc) return fail(nullptr, "kquant_gemm: stream synchronization failed");
+  }
+  return rc;
 }
 
 int camelid_hip_time_q8_0(int batched, const int8_t* const* wq, const uint16_t* const* wd, uint32_t copies,

@@ -1122,6 +1122,181 @@ __global__ __launch_bounds__(G6_NT) void k_gemm_q6k(const uint8_t* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
+// Q6_K GEMM, class-major form (prefill chunks).  The Q6_K dot's integer part per superblock,
+// aux[l] = sum over the 32 positions p = l (mod 8) of sc[p/16] * w[p] * q8[p] (inference.rs:
+// 19148-19195; exact, so any summation order gives it), is a K = 32 dot once the weights carry
+// their scale: w'[p] = sc[p/16] * w[p] lies in [-4096, 4096], so it is stored as two int8
+// planes w' = 128 h + lo (h in [-32, 32], lo in [-64, 63]) and aux[l] = 128 * (h . q8) +
+// (lo . q8): two v_mfma_i32_16x16x32_i8 per class, K = the class's 32 positions.
+// k_q6k_w2 builds the weight planes once per matrix, class-major per (row, superblock):
+// [class l][h | lo][m], m = 2 (p / 16) + (p / 8) % 2 for p = 16 (m / 2) + 8 (m % 2) + l.
+// k_gemm_q6k2 stages each superblock's activations in the same order (an 8 x 8 byte transpose
+// of every 64 positions: position 64 g + 8 i + l is class l's m = 8 g + i), then per class and
+// output: sums[l] += (f16(d) * y.d) * float(aux[l]) in superblock order, and the result is the
+// left fold of sums[0..8] from -0.0 -- k_gemv_q6k's arithmetic, in its order.
+// Workgroup: 4 waves over 32 rows x 64 tokens, each wave 16 x 32 (1 x 2 fragments, 8 class
+// chains per output); one superblock per step through double-buffered LDS tiles
+// [class plane][8-byte piece][row or token] (rows + 1 pieces per plane).
+constexpr int Q6G_NT = 256;
+constexpr int Q6G_RN = 32;
+constexpr int Q6G_RT = 64;
+constexpr int Q6G_W2 = 512;  // bytes of the weight planes per (row, superblock)
+__host__ __device__ inline int gemm_q6k2_tiles(int N, int T) {
+  return ((N + Q6G_RN - 1) / Q6G_RN) * ((T + Q6G_RT - 1) / Q6G_RT);
+}
+__host__ __device__ inline int gemm_q6k2_grid(int N, int T) { return ((gemm_q6k2_tiles(N, T) + 7) / 8) * 8; }
+
+// grid (K / 256, N), 256 threads: thread p of workgroup (s, row) writes position p's h and lo.
+__global__ __launch_bounds__(256) void k_q6k_w2(const uint8_t* __restrict__ ql, const uint8_t* __restrict__ qh,
+                                                const int8_t* __restrict__ scl, int K, int8_t* __restrict__ w2) {
+  const int s = blockIdx.x, p = threadIdx.x, NSB = K >> 8;
+  const size_t row = blockIdx.y;
+  const uint8_t* l8 = ql + row * (size_t)(K >> 1) + (size_t)s * 128;
+  const uint8_t* h8 = qh + row * (size_t)(K >> 2) + (size_t)s * 64;
+  const int n = p >> 7, q = p & 127, l32 = q & 31, quarter = q >> 5;  // (q6_k_values' order)
+  const uint8_t lq = l8[64 * n + l32 + (quarter & 1) * 32];
+  const int lo4 = (quarter < 2) ? (lq & 0xf) : (lq >> 4);
+  const int hi2 = (h8[32 * n + l32] >> (2 * quarter)) & 3;
+  const int w = (lo4 | (hi2 << 4)) - 32;
+  const int wp = (int)scl[(row * NSB + s) * 16 + (p >> 4)] * w;
+  const int h = (wp + 64) >> 7;  // floor((w' + 64) / 128): w' = 128 h + lo, lo in [-64, 63]
+  const int lo = wp - 128 * h;
+  const int cls = p & 7, m = 2 * (p >> 4) + ((p >> 3) & 1);
+  int8_t* o = w2 + (row * NSB + s) * Q6G_W2 + cls * 64;
+  o[m] = (int8_t)h;
+  o[32 + m] = (int8_t)lo;
+}
+
+// bytes b of a0..a3 as one dword (a0's in byte 0)
+template <int B>
+__device__ __forceinline__ uint32_t byte_col4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3) {
+  constexpr uint32_t s01 = (uint32_t)B | ((4u + B) << 8) | (0x0cu << 16) | (0x0cu << 24);
+  constexpr uint32_t s23 = 0x0cu | (0x0cu << 8) | ((uint32_t)B << 16) | ((4u + B) << 24);
+  return __builtin_amdgcn_perm(a1, a0, s01) | __builtin_amdgcn_perm(a3, a2, s23);
+}
+
+__global__ __launch_bounds__(Q6G_NT) void k_gemm_q6k2(const int8_t* __restrict__ w2,
+                                                      const uint16_t* __restrict__ dw, int N, int K,
+                                                      const float* __restrict__ xd,
+                                                      const int8_t* __restrict__ xq, int T, float* y, int ldy,
+                                                      const float* resid) {
+  constexpr int PSA = Q6G_RN + 1, PSB = Q6G_RT + 1;
+  __shared__ __align__(16) uint2 sw[2][16][4][PSA];  // [buf][class * 2 + (h | lo)][piece][row]
+  __shared__ __align__(16) uint2 sx[2][8][4][PSB];   // [buf][class][piece][token]
+  __shared__ float sd[2][Q6G_RN], syd[2][Q6G_RT];
+  const int NSB = K >> 8;
+  const int ntt = (T + Q6G_RT - 1) / Q6G_RT;
+  const int tiles = gemm_q6k2_tiles(N, T);
+  const int per = (tiles + 7) >> 3;
+  const int L = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (L >= tiles) return;
+  const int n_base = (L / ntt) * Q6G_RN, t_base = (L % ntt) * Q6G_RT;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int r = lane & 15, g = lane >> 4;
+  const int wn = (wave & 1) * 16, wt = (wave >> 1) * 32;
+  // staging: thread tid carries class tid % 8 of weight row tid / 8 (64 bytes: h, lo) and
+  // positions 64 (tid % 4) .. +63 of token tid / 4
+  const int wrow = tid >> 3, wcls = tid & 7, xtok = tid >> 2, xseg = tid & 3;
+  const int8_t* gw = w2 + (size_t)min(n_base + wrow, N - 1) * NSB * Q6G_W2 + wcls * 64;
+  const int8_t* gx = xq + (size_t)min(t_base + xtok, T - 1) * K + xseg * 64;
+  uint4 rw[4], rx[4];
+  float rd = 0.0f, ryd = 0.0f;
+  auto gload = [&](int s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      rw[u] = reinterpret_cast<const uint4*>(gw + (size_t)s * Q6G_W2)[u];
+      rx[u] = reinterpret_cast<const uint4*>(gx + (size_t)s * 256)[u];
+    }
+    if (tid < Q6G_RN) rd = half_bits_to_float(dw[(size_t)min(n_base + tid, N - 1) * NSB + s]);
+    if (tid < Q6G_RT) ryd = xd[(size_t)min(t_base + tid, T - 1) * NSB + s];
+  };
+  auto lds_put = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {  // h: rw[0..1] (m 0..31), lo: rw[2..3]
+      sw[buf][2 * wcls][2 * u][wrow] = make_uint2(rw[u].x, rw[u].y);
+      sw[buf][2 * wcls][2 * u + 1][wrow] = make_uint2(rw[u].z, rw[u].w);
+      sw[buf][2 * wcls + 1][2 * u][wrow] = make_uint2(rw[2 + u].x, rw[2 + u].y);
+      sw[buf][2 * wcls + 1][2 * u + 1][wrow] = make_uint2(rw[2 + u].z, rw[2 + u].w);
+    }
+    // rows i = 0..7 of the 8 x 8 byte block: dwords 2i (positions 8i .. 8i+3), 2i + 1 (+4 .. +7)
+    const uint32_t d[16] = {rx[0].x, rx[0].y, rx[0].z, rx[0].w, rx[1].x, rx[1].y, rx[1].z, rx[1].w,
+                            rx[2].x, rx[2].y, rx[2].z, rx[2].w, rx[3].x, rx[3].y, rx[3].z, rx[3].w};
+#define CM_Q6T(C)                                                                                             \
+  sx[buf][C][xseg][xtok] = make_uint2(byte_col4<(C) & 3>(d[(C) >> 2], d[2 + ((C) >> 2)], d[4 + ((C) >> 2)],  \
+                                                          d[6 + ((C) >> 2)]),                                \
+                                      byte_col4<(C) & 3>(d[8 + ((C) >> 2)], d[10 + ((C) >> 2)],               \
+                                                          d[12 + ((C) >> 2)], d[14 + ((C) >> 2)]));
+    CM_Q6T(0) CM_Q6T(1) CM_Q6T(2) CM_Q6T(3) CM_Q6T(4) CM_Q6T(5) CM_Q6T(6) CM_Q6T(7)
+#undef CM_Q6T
+    if (tid < Q6G_RN) sd[buf][tid] = rd;
+    if (tid < Q6G_RT) syd[buf][tid] = ryd;
+  };
+
+  float sums[8][2][4];
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+#pragma unroll
+    for (int tf = 0; tf < 2; ++tf)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sums[c][tf][i] = 0.0f;
+
+  gload(0);
+  lds_put(0);
+  __syncthreads();
+  for (int s = 0; s < NSB; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < NSB) gload(s + 1);
+    float dd[2][4];  // (f16(d) * y.d) of this lane's outputs
+#pragma unroll
+    for (int tf = 0; tf < 2; ++tf)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dd[tf][i] = sd[buf][wn + 4 * g + i] * syd[buf][wt + 16 * tf + r];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const long ah = *reinterpret_cast<const long*>(&sw[buf][2 * c][g][wn + r]);
+      const long al = *reinterpret_cast<const long*>(&sw[buf][2 * c + 1][g][wn + r]);
+#pragma unroll
+      for (int tf = 0; tf < 2; ++tf) {
+        const long bv = *reinterpret_cast<const long*>(&sx[buf][c][g][wt + 16 * tf + r]);
+        const v4i_t ch = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bv, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+        const v4i_t cl = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, bv, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sums[c][tf][i] += dd[tf][i] * (float)(ch[i] * 128 + cl[i]);
+      }
+      // one class at a time (its dots consumed before the next class's are formed: registers)
+#pragma unroll
+      for (int tf = 0; tf < 2; ++tf)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(sums[c][tf][i]));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (s + 1 < NSB) lds_put(buf ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int tf = 0; tf < 2; ++tf) {
+    const int t = t_base + wt + 16 * tf + r, n = n_base + wn + 4 * g;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float a = -0.0f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) a += sums[c][tf][i];
+      v[i] = a;
+    }
+    if (t < T && n < N) {
+      const size_t o = (size_t)t * ldy + n;
+      float4 out = make_float4(v[0], v[1], v[2], v[3]);
+      if (resid) {
+        const float4 rr = *reinterpret_cast<const float4*>(resid + o);
+        out = make_float4(rr.x + v[0], rr.y + v[1], rr.z + v[2], rr.w + v[3]);
+      }
+      *reinterpret_cast<float4*>(y + o) = out;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Q4_K GEMV over T tokens at once (speculative verify): each token's result is k_gemv_q4k's,
 // in the same order; a lane's weight pieces and their headers are loaded once and dotted with
 // every token's Q8_K activation, staged in LDS ([T][K] quants, [T][K/256] scales, and the
