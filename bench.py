@@ -165,10 +165,10 @@ KQUANT_SWEEP_SHAPES = [(1, 4096, 4096), (1, 5120, 4096), (1, 24576, 4096), (1, 4
 
 def run_sweep_kquant(tokens: int = 512, iters: int = 20) -> dict:
     """The K-quant prefill projections of configs[4] (Qwen3-8B Q4_K_M: q, q|k, gate|up, down as
-    Q4_K; v as Q6_K) over a 512-token chunk: k_gemm_q4k / k_gemm_q6k on the int8 matrix cores,
-    timed on the host over `iters` launches after one warm-up (each
-    launch is 0.1-3 ms, launch overhead is below 1 %).  int8 TOP/s = 2 N K T / time, against
-    the matrix-core peak."""
+    Q4_K; v as Q6_K) over a 512-token chunk: k_gemm_q4k / k_gemm_q6k2 on the int8 matrix cores,
+    `iters` back-to-back launches after one warm-up timed with HIP events on the launching stream
+    (Q6_K's class-major weight planes built once beforehand, as at model upload).  int8 TOP/s =
+    2 N K T / time, against the matrix-core peak."""
     import ctypes as C
     from camelid_amd import _native as N
     from camelid_amd.engine import DeviceBuffer
@@ -191,18 +191,13 @@ def run_sweep_kquant(tokens: int = 512, iters: int = 20) -> dict:
         N.check(L.camelid_hip_quantize_q8_k(x.ptr, T * k, yd.ptr, yq.ptr, ybs.ptr, None))
         y = DeviceBuffer(T * rows * 4)
 
-        def launch():
-            N.check(L.camelid_hip_kquant_gemm(quant, da.ptr, db.ptr, dsc.ptr, dd.ptr, rows, k, T, yd.ptr, yq.ptr,
-                                              y.ptr, rows, None, None))
-        launch()
-        N.check(L.camelid_hip_synchronize())
-        t0 = time.perf_counter()
-        for _ in range(iters):
-            launch()
-        N.check(L.camelid_hip_synchronize())
-        us = (time.perf_counter() - t0) / iters * 1e6
+        ms = C.c_float(0.0)
+        N.check(L.camelid_hip_time_kquant(quant, da.ptr, db.ptr, dsc.ptr, dd.ptr, rows, k, T, yd.ptr, yq.ptr,
+                                          y.ptr, iters, C.byref(ms)))
+        us = ms.value / iters * 1e3
         ops = 2.0 * rows * k * T
-        name = "k_gemm_q4k" if quant == 1 else ("k_gemm_q6k" if T > 8 else "k_gemv_q6k_multi")
+        q6 = "k_gemm_q6k" if os.environ.get("CAMELID_HIP_Q6K_GEMM2") == "0" else "k_gemm_q6k2"
+        name = "k_gemm_q4k" if quant == 1 else (q6 if T > 8 else "k_gemv_q6k_multi")
         out.append({"quant": "Q4_K" if quant == 1 else "Q6_K", "kernel": name, "shape": [rows, k], "tokens": T,
                     "us": round(us, 1), "tops": round(ops / us / 1e6, 1),
                     "mfma_frac": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4)})

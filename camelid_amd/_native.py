@@ -140,6 +140,8 @@ SIGNATURES: dict[str, tuple] = {
     "camelid_hip_load_gguf": (C.c_int, [vp, vp, C.c_int]),
     "camelid_hip_kquant_gemm": (C.c_int, [C.c_uint8, vp, vp, vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp,
                                           vp, C.c_uint32, vp, vp]),
+    "camelid_hip_time_kquant": (C.c_int, [C.c_uint8, vp, vp, vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp,
+                                          vp, C.c_uint32, C.POINTER(C.c_float)]),
     "camelid_hip_time_q8_0": (C.c_int, [C.c_int, C.POINTER(vp), C.POINTER(vp), C.c_uint32, C.c_uint32,
                                         C.c_uint32, vp, vp, C.c_uint32, vp, C.c_uint32, C.POINTER(C.c_float)]),
     "camelid_hip_argmax": (C.c_int, [vp, C.c_uint32, vp, vp]),

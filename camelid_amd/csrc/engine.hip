@@ -66,8 +66,8 @@ struct KMat {
   int8_t* sc = nullptr;
   uint16_t* d = nullptr;
   uint32_t rows = 0, k = 0;
-  // Q6_K projections: the scaled weights as class-major int8 planes [rows][k/256][512] for the
-  // prefill GEMM (cm::k_gemm_q6k2, built by cm::k_q6k_w2); null: the sparse-MFMA GEMM
+  // Q6_K projections: the scaled weights as class-major int8 planes for the prefill GEMM
+  // (cm::k_gemm_q6k2; cm::q6g_planes_bytes, built by cm::k_q6k_w2); null: the sparse-MFMA GEMM
   int8_t* w2 = nullptr;
 };
 
@@ -186,6 +186,7 @@ struct camelid_hip_engine {
   // a Q8_0 projection before they are scattered into the QKV / gate|up rows
   float *pf_kd = nullptr, *pf_att = nullptr, *pf_tmp = nullptr;
   int8_t* pf_kq = nullptr;
+  int8_t* pf_kqt = nullptr;  // the chunk's Q8_K quants in the class-major order of the Q6_K GEMM
   int32_t* pf_kbs = nullptr;
   // score rows of the tiled prefill attention (cm::k_attn_prefill_tile; CAMELID_HIP_ATT_TILE=0:
   // one workgroup per (head, token) instead), sized for a chunk ending at max_pos
@@ -415,9 +416,9 @@ int upload_kq(camelid_hip_engine* e, KMat* m, const uint8_t* src, size_t len, ui
     HIP_TRY(e, hipMemcpy(m->sc, sc.data(), sc.size(), hipMemcpyHostToDevice));
     HIP_TRY(e, hipMemcpy(m->d, d.data(), d.size() * 2, hipMemcpyHostToDevice));
     if (gemm_planes && e->q6_gemm2) {  // the prefill GEMM's weight planes, built on the device
-      if (!m->w2 && dev_alloc(e, &m->w2, (size_t)rows * nsb * cm::Q6G_W2)) return 1;
-      hipLaunchKernelGGL(cm::k_q6k_w2, dim3((uint32_t)nsb, rows), dim3(256), 0, e->stream, m->a, m->b, m->sc, (int)k,
-                         m->w2);
+      if (!m->w2 && dev_alloc(e, &m->w2, cm::q6g_planes_bytes((int)rows, (int)k))) return 1;
+      hipLaunchKernelGGL(cm::k_q6k_w2, dim3((uint32_t)nsb, (rows + cm::Q6G_R - 1) / cm::Q6G_R * cm::Q6G_R), dim3(256),
+                         0, e->stream, m->a, m->b, m->sc, (int)rows, (int)k, m->w2);
       HIP_TRY(e, hipGetLastError());
       HIP_TRY(e, hipStreamSynchronize(e->stream));
     }
@@ -1309,7 +1310,7 @@ int ensure_prefill_buffers(camelid_hip_engine* e) {
   if (!e->any_kquant) return 0;
   return dev_alloc(e, &e->pf_kd, tc * act / 256) || dev_alloc(e, &e->pf_kq, tc * act) ||
          dev_alloc(e, &e->pf_kbs, tc * act / 32) || dev_alloc(e, &e->pf_att, tc * nq) ||
-         dev_alloc(e, &e->pf_tmp, tc * act);
+         dev_alloc(e, &e->pf_tmp, tc * act) || dev_alloc(e, &e->pf_kqt, cm::q6g_act_bytes((int)tc, (int)act));
 }
 
 // Tokens per launch of the multi-token Q6_K GEMV at width K (its activations and terms
@@ -1321,10 +1322,11 @@ uint32_t q6m_tokens(uint32_t K) {
 }
 
 // A K-quant projection over T tokens with Q8_K activation rows (kd [T][k/256], kq [T][k]):
-// y[t * ldy + row] (+ resid, same stride).  Q4_K: the matrix-core GEMM; Q6_K: the matrix-core
-// GEMM for more than Q6M_MAX tokens, else the multi-token GEMV.
+// y[t * ldy + row] (+ resid, same stride).  Q4_K: the matrix-core GEMM; Q6_K: for more than
+// Q6M_MAX tokens the class-major GEMM (needs m.w2 and xt, cm::q6g_act_bytes(T, k) bytes for
+// the class-major copy of kq) or else the sparse-MFMA GEMM, for fewer the multi-token GEMV.
 void launch_kgemm(const KMat& m, uint32_t T, const float* kd, const int8_t* kq, float* y, uint32_t ldy,
-                  const float* resid, hipStream_t s) {
+                  const float* resid, hipStream_t s, int8_t* xt) {
   if (m.quant == CAMELID_Q4_K && T <= (uint32_t)cm::Q4M_MAX) {  // a few tokens (verify)
     uint32_t tt = T;
     while (tt > 1 && cm::gemv_q4k_multi_lds_bytes((int)m.k, (int)tt) > 65536) --tt;
@@ -1353,9 +1355,12 @@ void launch_kgemm(const KMat& m, uint32_t T, const float* kd, const int8_t* kq, 
               (int)m.rows, (int)m.k, kd, kq, (int)T, y, (int)ldy, resid);
     return;
   }
-  if (T > (uint32_t)cm::Q6M_MAX && m.w2 && m.rows % 4 == 0 && ldy % 4 == 0) {  // a chunk: class-major GEMM
+  if (T > (uint32_t)cm::Q6M_MAX && m.w2 && xt && m.rows % 4 == 0 && ldy % 4 == 0) {  // a chunk: class-major GEMM
+    const size_t threads = cm::q6g_act_bytes((int)T, (int)m.k) / 64;
+    CM_LAUNCH(cm::k_q8k_classmajor, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, s, kq, (int)T, (int)m.k,
+              xt);
     CM_LAUNCH(cm::k_gemm_q6k2, dim3(cm::gemm_q6k2_grid((int)m.rows, (int)T)), dim3(cm::Q6G_NT), 0, s, m.w2, m.d,
-              (int)m.rows, (int)m.k, kd, kq, (int)T, y, (int)ldy, resid);
+              (int)m.rows, (int)m.k, kd, xt, (int)T, y, (int)ldy, resid);
     return;
   }
   if (T > (uint32_t)cm::Q6M_MAX) {  // a chunk: the sparse-MFMA GEMM
@@ -1493,7 +1498,7 @@ void prefill_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cosv,
     ProfScope ps(e, P_GEMM, 2.0 * (p.quant != CAMELID_Q8_0 ? p.kq.rows : p.q8.rows) *
                                 (p.quant != CAMELID_Q8_0 ? p.kq.k : p.q8.k) * T);
     if (p.quant != CAMELID_Q8_0) {
-      launch_kgemm(p.kq, T, e->pf_kd, e->pf_kq, y, ldy, resid, s);
+      launch_kgemm(p.kq, T, e->pf_kd, e->pf_kq, y, ldy, resid, s, e->pf_kqt);
     } else if (ldy == p.q8.rows) {
       launch_gemm(p.q8, T, e->pf_xq, e->pf_xs, y, resid, s);
     } else {  // (no residual on the strided projections)
@@ -2120,7 +2125,7 @@ int camelid_hip_verify(camelid_hip_engine* e, const float* embs, const float* co
                          cm::Prefetch{}, k, kout ? e->pf_kd : nullptr, kout ? e->pf_kq : nullptr,
                          kout ? e->pf_kbs : nullptr);
     if (kout)
-      launch_kgemm(e->out_k, k, e->pf_kd, e->pf_kq, e->v_logits, d.vocab, nullptr, e->stream);
+      launch_kgemm(e->out_k, k, e->pf_kd, e->pf_kq, e->v_logits, d.vocab, nullptr, e->stream, e->pf_kqt);
     else
       launch_gemm(e->out, k, e->pf_xq, e->pf_xs, e->v_logits, nullptr, e->stream);
     CM_LAUNCH(cm::k_argmax_rows_part, dim3(cm::AMR_PARTS, k), dim3(256), 0, e->stream, e->v_logits, (int)d.vocab,
@@ -2777,22 +2782,31 @@ int camelid_hip_kquant_gemm(uint8_t quant, const uint8_t* a, const uint8_t* b, c
   m.d = const_cast<uint16_t*>(d);
   m.rows = rows;
   m.k = k;
-  // Q6_K chunks: the class-major GEMM with its weight planes built for this call (a temporary
-  // allocation; the stream is synchronized before it is freed) unless CAMELID_HIP_Q6K_GEMM2=0
+  // Q6_K chunks: the class-major GEMM with its weight planes and activation copy in temporary
+  // allocations for this call (the stream is synchronized before they are freed) unless
+  // CAMELID_HIP_Q6K_GEMM2=0
   const char* g2 = std::getenv("CAMELID_HIP_Q6K_GEMM2");
   const bool planes = quant == CAMELID_Q6_K && tokens > (uint32_t)cm::Q6M_MAX && rows % 4 == 0 && ldy % 4 == 0 &&
                       !(g2 && std::atoi(g2) == 0);
+  int8_t* xt = nullptr;
   if (planes) {
-    if (hipMalloc(&m.w2, (size_t)rows * (k / 256) * cm::Q6G_W2) != hipSuccess)
+    if (hipMalloc(&m.w2, cm::q6g_planes_bytes((int)rows, (int)k)) != hipSuccess) {
+      m.w2 = nullptr;
       return fail(nullptr, "kquant_gemm: weight plane allocation failed");
-    hipLaunchKernelGGL(cm::k_q6k_w2, dim3(k / 256, rows), dim3(256), 0, (hipStream_t)stream, m.a, m.b, m.sc, (int)k,
-                       m.w2);
+    }
+    if (hipMalloc(&xt, cm::q6g_act_bytes((int)tokens, (int)k)) != hipSuccess) {
+      (void)hipFree(m.w2);
+      return fail(nullptr, "kquant_gemm: activation copy allocation failed");
+    }
+    hipLaunchKernelGGL(cm::k_q6k_w2, dim3(k / 256, (rows + cm::Q6G_R - 1) / cm::Q6G_R * cm::Q6G_R), dim3(256), 0,
+                       (hipStream_t)stream, m.a, m.b, m.sc, (int)rows, (int)k, m.w2);
   }
-  launch_kgemm(m, tokens, yd, yq, y, ldy, resid, (hipStream_t)stream);
+  launch_kgemm(m, tokens, yd, yq, y, ldy, resid, (hipStream_t)stream, xt);
   const int rc = launch_status("kquant_gemm");
   if (planes) {
     const bool synced = hipStreamSynchronize((hipStream_t)stream) == hipSuccess;
     (void)hipFree(m.w2);
+    (void)hipFree(xt);
     if (!synced && !rc) return fail(nullptr, "kquant_gemm: stream synchronization failed");
   }
   return rc;
@@ -2838,6 +2852,61 @@ int camelid_hip_time_q8_0(int batched, const int8_t* const* wq, const uint16_t* 
   }
   if (a) (void)hipEventDestroy(a);
   if (b) (void)hipEventDestroy(b);
+  (void)hipStreamDestroy(s);
+  return rc;
+}
+
+int camelid_hip_time_kquant(uint8_t quant, const uint8_t* a, const uint8_t* b, const int8_t* sc, const uint16_t* d,
+                            uint32_t rows, uint32_t k, uint32_t tokens, const float* yd, const int8_t* yq, float* y,
+                            uint32_t iters, float* ms_out) {
+  if (!a || !b || !yd || !yq || !y || !ms_out || iters == 0) return fail(nullptr, "null argument");
+  if (quant != CAMELID_Q4_K && quant != CAMELID_Q6_K) return fail(nullptr, "quant must be Q4_K or Q6_K");
+  if (quant == CAMELID_Q6_K && (!sc || !d)) return fail(nullptr, "null argument");
+  if (rows == 0 || k == 0 || k % 256 || k > 16384 || tokens == 0) return fail(nullptr, "invalid shape");
+  hipStream_t s = nullptr;
+  if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return fail(nullptr, "stream create failed");
+  hipEvent_t ea = nullptr, eb = nullptr;
+  KMat m;
+  m.quant = quant;
+  m.a = const_cast<uint8_t*>(a);
+  m.b = const_cast<uint8_t*>(b);
+  m.sc = const_cast<int8_t*>(sc);
+  m.d = const_cast<uint16_t*>(d);
+  m.rows = rows;
+  m.k = k;
+  int rc = 0;
+  // the Q6_K weight planes are built once, outside the timed launches (as at model upload);
+  // each timed launch includes the activations' class-major copy (as in a prefill chunk)
+  const char* g2 = std::getenv("CAMELID_HIP_Q6K_GEMM2");
+  int8_t* xt = nullptr;
+  if (quant == CAMELID_Q6_K && tokens > (uint32_t)cm::Q6M_MAX && rows % 4 == 0 && !(g2 && std::atoi(g2) == 0)) {
+    if (hipMalloc(&m.w2, cm::q6g_planes_bytes((int)rows, (int)k)) != hipSuccess) {
+      m.w2 = nullptr;
+      rc = fail(nullptr, "time_kquant: weight plane allocation failed");
+    } else if (hipMalloc(&xt, cm::q6g_act_bytes((int)tokens, (int)k)) != hipSuccess) {
+      xt = nullptr;
+      rc = fail(nullptr, "time_kquant: activation copy allocation failed");
+    } else {
+      hipLaunchKernelGGL(cm::k_q6k_w2, dim3(k / 256, (rows + cm::Q6G_R - 1) / cm::Q6G_R * cm::Q6G_R), dim3(256), 0,
+                         s, m.a, m.b, m.sc, (int)rows, (int)k, m.w2);
+    }
+  }
+  if (!rc && (hipEventCreate(&ea) != hipSuccess || hipEventCreate(&eb) != hipSuccess))
+    rc = fail(nullptr, "event create failed");
+  if (!rc) {
+    launch_kgemm(m, tokens, yd, yq, y, rows, nullptr, s, xt);  // warm-up
+    (void)hipEventRecord(ea, s);
+    for (uint32_t i = 0; i < iters; ++i) launch_kgemm(m, tokens, yd, yq, y, rows, nullptr, s, xt);
+    (void)hipEventRecord(eb, s);
+    if (hipEventSynchronize(eb) != hipSuccess || hipEventElapsedTime(ms_out, ea, eb) != hipSuccess)
+      rc = fail(nullptr, "timing failed");
+    if (!rc && hipGetLastError() != hipSuccess) rc = fail(nullptr, "launch failed");
+  }
+  (void)hipStreamSynchronize(s);
+  if (m.w2) (void)hipFree(m.w2);
+  if (xt) (void)hipFree(xt);
+  if (ea) (void)hipEventDestroy(ea);
+  if (eb) (void)hipEventDestroy(eb);
   (void)hipStreamDestroy(s);
   return rc;
 }

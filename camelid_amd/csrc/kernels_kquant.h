@@ -1123,48 +1123,65 @@ __global__ __launch_bounds__(G6_NT) void k_gemm_q6k(const uint8_t* __restrict__ 
 
 // ---------------------------------------------------------------------------
 // Q6_K GEMM, class-major form (prefill chunks).  The Q6_K dot's integer part per superblock,
-// aux[l] = sum over the 32 positions p = l (mod 8) of sc[p/16] * w[p] * q8[p] (inference.rs:
-// 19148-19195; exact, so any summation order gives it), is a K = 32 dot once the weights carry
-// their scale: w'[p] = sc[p/16] * w[p] lies in [-4096, 4096], so it is stored as two int8
-// planes w' = 128 h + lo (h in [-32, 32], lo in [-64, 63]) and aux[l] = 128 * (h . q8) +
-// (lo . q8): two v_mfma_i32_16x16x32_i8 per class, K = the class's 32 positions.
-// k_q6k_w2 builds the weight planes once per matrix, class-major per (row, superblock):
-// [class l][h | lo][m], m = 2 (p / 16) + (p / 8) % 2 for p = 16 (m / 2) + 8 (m % 2) + l.
-// k_gemm_q6k2 stages each superblock's activations in the same order (an 8 x 8 byte transpose
-// of every 64 positions: position 64 g + 8 i + l is class l's m = 8 g + i), then per class and
-// output: sums[l] += (f16(d) * y.d) * float(aux[l]) in superblock order, and the result is the
+// aux[l] = sum over the 32 positions p = 8 j + l (j = 0..31) of sc[p/16] * w[p] * q8[p]
+// (inference.rs:19148-19195; exact, so any summation order gives it), is a K = 32 dot once
+// the weights carry their scale: w'[p] = sc[p/16] * w[p] lies in [-4096, 4096], so it is stored
+// as two int8 planes w' = 128 h + lo (h in [-32, 32], lo in [-64, 63]) and aux[l] =
+// 128 (h . q8) + (lo . q8): two v_mfma_i32_16x16x32_i8 per class, K = j.  Then per class and
+// output sums[l] += (f16(d) * y.d) * float(aux[l]) in superblock order, and the result is the
 // left fold of sums[0..8] from -0.0 -- k_gemv_q6k's arithmetic, in its order.
-// Workgroup: 4 waves over 32 rows x 64 tokens, each wave 16 x 32 (1 x 2 fragments, 8 class
-// chains per output); one superblock per step through double-buffered LDS tiles
-// [class plane][8-byte piece][row or token] (rows + 1 pieces per plane).
-constexpr int Q6G_NT = 256;
-constexpr int Q6G_RN = 32;
-constexpr int Q6G_RT = 64;
-constexpr int Q6G_W2 = 512;  // bytes of the weight planes per (row, superblock)
+// The eight class chains are independent, so wave l of a workgroup folds class l of its
+// 32-row x 32-token tile (2 x 2 MFMA fragments, 16 chains per lane) and the class sums meet in
+// LDS for the final fold: 8 waves per tile where one wave per tile holding all classes would
+// leave the SIMDs issue-bound at one wave each.
+// Both operands sit in HBM in the order the waves read them from LDS, so a superblock step
+// stages each tile with one straight 16-byte copy per thread:
+//   weights (k_q6k_w2, once per matrix): [32-row tile][superblock] blocks of 16 KB, each
+//     [class l][plane h | lo][row half][k group g][row r][j % 8] (rows padded to 32 with zeros);
+//   activations (k_q8k_classmajor, once per call): [32-token tile][superblock] blocks of 8 KB,
+//     [class l][token half][k group g][token r][j % 8], j = 8 g + (j % 8).
+constexpr int Q6G_NT = 512;   // 8 waves, wave l folds position class l
+constexpr int Q6G_R = 32;     // rows and tokens per tile
+constexpr int Q6G_WB = 16384; // weight-plane bytes per (32-row tile, superblock)
+constexpr int Q6G_XB = 8192;  // activation bytes per (32-token tile, superblock)
+constexpr int Q6G_DP = 36;    // floats per token row of the LDS scale-product and class-sum tables
+constexpr int Q6G_LDS = 2 * (Q6G_WB + Q6G_XB) + 2 * Q6G_R * Q6G_DP * 4;
+static_assert(8 * Q6G_R * Q6G_DP * 4 <= Q6G_LDS, "class sums fit the staging LDS");
+__host__ __device__ inline size_t q6g_planes_bytes(int N, int K) {
+  return (size_t)((N + Q6G_R - 1) / Q6G_R) * (K / 256) * Q6G_WB;
+}
+__host__ __device__ inline size_t q6g_act_bytes(int T, int K) {
+  return (size_t)((T + Q6G_R - 1) / Q6G_R) * (K / 256) * Q6G_XB;
+}
 __host__ __device__ inline int gemm_q6k2_tiles(int N, int T) {
-  return ((N + Q6G_RN - 1) / Q6G_RN) * ((T + Q6G_RT - 1) / Q6G_RT);
+  return ((N + Q6G_R - 1) / Q6G_R) * ((T + Q6G_R - 1) / Q6G_R);
 }
 __host__ __device__ inline int gemm_q6k2_grid(int N, int T) { return ((gemm_q6k2_tiles(N, T) + 7) / 8) * 8; }
 
-// grid (K / 256, N), 256 threads: thread p of workgroup (s, row) writes position p's h and lo.
+// grid (K / 256, N rounded up to 32), 256 threads: thread p of workgroup (s, row) writes
+// position p's h and lo (zeros for the padding rows >= N).
 __global__ __launch_bounds__(256) void k_q6k_w2(const uint8_t* __restrict__ ql, const uint8_t* __restrict__ qh,
-                                                const int8_t* __restrict__ scl, int K, int8_t* __restrict__ w2) {
+                                                const int8_t* __restrict__ scl, int N, int K,
+                                                int8_t* __restrict__ w2) {
   const int s = blockIdx.x, p = threadIdx.x, NSB = K >> 8;
-  const size_t row = blockIdx.y;
-  const uint8_t* l8 = ql + row * (size_t)(K >> 1) + (size_t)s * 128;
-  const uint8_t* h8 = qh + row * (size_t)(K >> 2) + (size_t)s * 64;
-  const int n = p >> 7, q = p & 127, l32 = q & 31, quarter = q >> 5;  // (q6_k_values' order)
-  const uint8_t lq = l8[64 * n + l32 + (quarter & 1) * 32];
-  const int lo4 = (quarter < 2) ? (lq & 0xf) : (lq >> 4);
-  const int hi2 = (h8[32 * n + l32] >> (2 * quarter)) & 3;
-  const int w = (lo4 | (hi2 << 4)) - 32;
-  const int wp = (int)scl[(row * NSB + s) * 16 + (p >> 4)] * w;
-  const int h = (wp + 64) >> 7;  // floor((w' + 64) / 128): w' = 128 h + lo, lo in [-64, 63]
-  const int lo = wp - 128 * h;
-  const int cls = p & 7, m = 2 * (p >> 4) + ((p >> 3) & 1);
-  int8_t* o = w2 + (row * NSB + s) * Q6G_W2 + cls * 64;
-  o[m] = (int8_t)h;
-  o[32 + m] = (int8_t)lo;
+  const int row = blockIdx.y;
+  int h = 0, lo = 0;
+  if (row < N) {
+    const uint8_t* l8 = ql + (size_t)row * (K >> 1) + (size_t)s * 128;
+    const uint8_t* h8 = qh + (size_t)row * (K >> 2) + (size_t)s * 64;
+    const int n = p >> 7, q = p & 127, l32 = q & 31, quarter = q >> 5;  // (q6_k_values' order)
+    const uint8_t lq = l8[64 * n + l32 + (quarter & 1) * 32];
+    const int lo4 = (quarter < 2) ? (lq & 0xf) : (lq >> 4);
+    const int hi2 = (h8[32 * n + l32] >> (2 * quarter)) & 3;
+    const int w = (lo4 | (hi2 << 4)) - 32;
+    const int wp = (int)scl[((size_t)row * NSB + s) * 16 + (p >> 4)] * w;
+    h = (wp + 64) >> 7;  // floor((w' + 64) / 128): w' = 128 h + lo, lo in [-64, 63]
+    lo = wp - 128 * h;
+  }
+  const int cls = p & 7, j = p >> 3, g = j >> 3, b = j & 7, rf = (row >> 4) & 1, r = row & 15;
+  int8_t* o = w2 + ((size_t)(row / Q6G_R) * NSB + s) * Q6G_WB;
+  o[(((cls * 2 + 0) * 2 + rf) * 4 + g) * 128 + r * 8 + b] = (int8_t)h;
+  o[(((cls * 2 + 1) * 2 + rf) * 4 + g) * 128 + r * 8 + b] = (int8_t)lo;
 }
 
 // bytes b of a0..a3 as one dword (a0's in byte 0)
@@ -1175,124 +1192,180 @@ __device__ __forceinline__ uint32_t byte_col4(uint32_t a0, uint32_t a1, uint32_t
   return __builtin_amdgcn_perm(a1, a0, s01) | __builtin_amdgcn_perm(a3, a2, s23);
 }
 
-__global__ __launch_bounds__(Q6G_NT) void k_gemm_q6k2(const int8_t* __restrict__ w2,
-                                                      const uint16_t* __restrict__ dw, int N, int K,
-                                                      const float* __restrict__ xd,
-                                                      const int8_t* __restrict__ xq, int T, float* y, int ldy,
-                                                      const float* resid) {
-  constexpr int PSA = Q6G_RN + 1, PSB = Q6G_RT + 1;
-  __shared__ __align__(16) uint2 sw[2][16][4][PSA];  // [buf][class * 2 + (h | lo)][piece][row]
-  __shared__ __align__(16) uint2 sx[2][8][4][PSB];   // [buf][class][piece][token]
-  __shared__ float sd[2][Q6G_RN], syd[2][Q6G_RT];
+// Q8_K quants [T][K] -> the class-major blocks above (zeros for the padding tokens >= T):
+// thread (tile, superblock, g, token of the tile) moves positions 64 g .. 64 g + 63 of one
+// token, an 8 x 8 byte transpose (position 64 g + 8 i + l is class l's j = 8 g + i).
+__global__ __launch_bounds__(256) void k_q8k_classmajor(const int8_t* __restrict__ xq, int T, int K,
+                                                        int8_t* __restrict__ xt) {
   const int NSB = K >> 8;
-  const int ntt = (T + Q6G_RT - 1) / Q6G_RT;
+  const size_t id = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t total = (size_t)((T + Q6G_R - 1) / Q6G_R) * NSB * 128;
+  if (id >= total) return;
+  const int rr = (int)(id & 31), g = (int)((id >> 5) & 3);
+  const size_t rest = id >> 7;
+  const int s = (int)(rest % NSB), tt = (int)(rest / NSB);
+  const int tok = tt * Q6G_R + rr;
+  uint4 v[4] = {};
+  if (tok < T) {
+    const uint4* src = reinterpret_cast<const uint4*>(xq + (size_t)tok * K + (size_t)s * 256 + 64 * g);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = src[u];
+  }
+  // d[2 i] = positions 64 g + 8 i .. +3, d[2 i + 1] = +4 .. +7
+  const uint32_t d[16] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w,
+                          v[2].x, v[2].y, v[2].z, v[2].w, v[3].x, v[3].y, v[3].z, v[3].w};
+  uint2* o = reinterpret_cast<uint2*>(xt + ((size_t)tt * NSB + s) * Q6G_XB) + (rr >> 4) * 64 + g * 16 + (rr & 15);
+#define CM_Q6T(C)                                                                                               \
+  o[(C) * 128] = make_uint2(byte_col4<(C) & 3>(d[(C) >> 2], d[2 + ((C) >> 2)], d[4 + ((C) >> 2)], d[6 + ((C) >> 2)]), \
+                            byte_col4<(C) & 3>(d[8 + ((C) >> 2)], d[10 + ((C) >> 2)], d[12 + ((C) >> 2)],           \
+                                               d[14 + ((C) >> 2)]));
+  CM_Q6T(0) CM_Q6T(1) CM_Q6T(2) CM_Q6T(3) CM_Q6T(4) CM_Q6T(5) CM_Q6T(6) CM_Q6T(7)
+#undef CM_Q6T
+}
+
+// y[t * ldy + n] (+ resid, same stride) for N % 4 == 0, ldy % 4 == 0; w2 and xt in the
+// layouts above; grid gemm_q6k2_grid(N, T), Q6G_NT threads.
+__global__ __launch_bounds__(Q6G_NT, 4) void k_gemm_q6k2(const int8_t* __restrict__ w2,
+                                                         const uint16_t* __restrict__ dw, int N, int K,
+                                                         const float* __restrict__ xd,
+                                                         const int8_t* __restrict__ xt, int T, float* y, int ldy,
+                                                         const float* resid) {
+  // buffer b: weights at b * WB, activations at 2 WB + b * XB, scale products (f16(d) * y.d,
+  // [token][row]) after both; the class sums [class][token][row] reuse it all at the end
+  __shared__ __align__(16) unsigned char smem[Q6G_LDS];
+  const int NSB = K >> 8;
+  const int ntt = (T + Q6G_R - 1) / Q6G_R;
   const int tiles = gemm_q6k2_tiles(N, T);
   const int per = (tiles + 7) >> 3;
-  const int L = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  const int L = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);  // contiguous tiles per XCD
   if (L >= tiles) return;
-  const int n_base = (L / ntt) * Q6G_RN, t_base = (L % ntt) * Q6G_RT;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int r = lane & 15, g = lane >> 4;
-  const int wn = (wave & 1) * 16, wt = (wave >> 1) * 32;
-  // staging: thread tid carries class tid % 8 of weight row tid / 8 (64 bytes: h, lo) and
-  // positions 64 (tid % 4) .. +63 of token tid / 4
-  const int wrow = tid >> 3, wcls = tid & 7, xtok = tid >> 2, xseg = tid & 3;
-  const int8_t* gw = w2 + (size_t)min(n_base + wrow, N - 1) * NSB * Q6G_W2 + wcls * 64;
-  const int8_t* gx = xq + (size_t)min(t_base + xtok, T - 1) * K + xseg * 64;
-  uint4 rw[4], rx[4];
-  float rd = 0.0f, ryd = 0.0f;
-  auto gload = [&](int s) __attribute__((always_inline)) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      rw[u] = reinterpret_cast<const uint4*>(gw + (size_t)s * Q6G_W2)[u];
-      rx[u] = reinterpret_cast<const uint4*>(gx + (size_t)s * 256)[u];
-    }
-    if (tid < Q6G_RN) rd = half_bits_to_float(dw[(size_t)min(n_base + tid, N - 1) * NSB + s]);
-    if (tid < Q6G_RT) ryd = xd[(size_t)min(t_base + tid, T - 1) * NSB + s];
-  };
-  auto lds_put = [&](int buf) __attribute__((always_inline)) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {  // h: rw[0..1] (m 0..31), lo: rw[2..3]
-      sw[buf][2 * wcls][2 * u][wrow] = make_uint2(rw[u].x, rw[u].y);
-      sw[buf][2 * wcls][2 * u + 1][wrow] = make_uint2(rw[u].z, rw[u].w);
-      sw[buf][2 * wcls + 1][2 * u][wrow] = make_uint2(rw[2 + u].x, rw[2 + u].y);
-      sw[buf][2 * wcls + 1][2 * u + 1][wrow] = make_uint2(rw[2 + u].z, rw[2 + u].w);
-    }
-    // rows i = 0..7 of the 8 x 8 byte block: dwords 2i (positions 8i .. 8i+3), 2i + 1 (+4 .. +7)
-    const uint32_t d[16] = {rx[0].x, rx[0].y, rx[0].z, rx[0].w, rx[1].x, rx[1].y, rx[1].z, rx[1].w,
-                            rx[2].x, rx[2].y, rx[2].z, rx[2].w, rx[3].x, rx[3].y, rx[3].z, rx[3].w};
-#define CM_Q6T(C)                                                                                             \
-  sx[buf][C][xseg][xtok] = make_uint2(byte_col4<(C) & 3>(d[(C) >> 2], d[2 + ((C) >> 2)], d[4 + ((C) >> 2)],  \
-                                                          d[6 + ((C) >> 2)]),                                \
-                                      byte_col4<(C) & 3>(d[8 + ((C) >> 2)], d[10 + ((C) >> 2)],               \
-                                                          d[12 + ((C) >> 2)], d[14 + ((C) >> 2)]));
-    CM_Q6T(0) CM_Q6T(1) CM_Q6T(2) CM_Q6T(3) CM_Q6T(4) CM_Q6T(5) CM_Q6T(6) CM_Q6T(7)
-#undef CM_Q6T
-    if (tid < Q6G_RN) sd[buf][tid] = rd;
-    if (tid < Q6G_RT) syd[buf][tid] = ryd;
-  };
+  const int rt = L / ntt, tt = L % ntt;
+  const int tid = threadIdx.x, cls = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
+  const uint4* gw = reinterpret_cast<const uint4*>(w2 + (size_t)rt * NSB * Q6G_WB);
+  const uint4* gx = reinterpret_cast<const uint4*>(xt + (size_t)tt * NSB * Q6G_XB);
+  // thread tid forms the scale products of token tid / 16, rows 2 (tid % 16) and + 1
+  const int dtok = tid >> 4, drow = 2 * (tid & 15);
+  const uint16_t* gd0 = dw + (size_t)min(rt * Q6G_R + drow, N - 1) * NSB;
+  const uint16_t* gd1 = dw + (size_t)min(rt * Q6G_R + drow + 1, N - 1) * NSB;
+  const float* gyd = xd + (size_t)min(tt * Q6G_R + dtok, T - 1) * NSB;
+  // the tiles of the next two steps, held raw in registers (set j % 2 for step j) until they
+  // are stored: a step's loads are issued two steps before its tile is folded, and the f16
+  // scales are converted only at the store, so no use of a load waits inside its own step
+  uint4 rw0_0, rw1_0, rx_0, rw0_1, rw1_1, rx_1;
+  uint16_t rh0_0, rh1_0, rh0_1, rh1_1;
+  float ryd_0, ryd_1;
+#define CM_Q6G_LOAD(S, P)                                  \
+  rw0_##P = gw[(size_t)(S) * (Q6G_WB / 16) + tid];         \
+  rw1_##P = gw[(size_t)(S) * (Q6G_WB / 16) + Q6G_NT + tid]; \
+  rx_##P = gx[(size_t)(S) * (Q6G_XB / 16) + tid];          \
+  rh0_##P = gd0[S];                                        \
+  rh1_##P = gd1[S];                                        \
+  ryd_##P = gyd[S];
+#define CM_Q6G_STORE(P)                                                                                     \
+  {                                                                                                         \
+    uint4* sw_ = reinterpret_cast<uint4*>(smem + (P) * Q6G_WB);                                           \
+    sw_[tid] = rw0_##P;                                                                                     \
+    sw_[Q6G_NT + tid] = rw1_##P;                                                                            \
+    reinterpret_cast<uint4*>(smem + 2 * Q6G_WB + (P) * Q6G_XB)[tid] = rx_##P;                             \
+    float* sdd_ = reinterpret_cast<float*>(smem + 2 * (Q6G_WB + Q6G_XB)) + (P) * Q6G_R * Q6G_DP;          \
+    *reinterpret_cast<float2*>(sdd_ + dtok * Q6G_DP + drow) = make_float2(                                 \
+        half_bits_to_float(rh0_##P) * ryd_##P, half_bits_to_float(rh1_##P) * ryd_##P);                     \
+  }
 
-  float sums[8][2][4];
+  float sums[2][2][4];  // [row half][token half][i]: rows 16 rf + 4 g + i, token 16 tf + r
 #pragma unroll
-  for (int c = 0; c < 8; ++c)
+  for (int rf = 0; rf < 2; ++rf)
 #pragma unroll
     for (int tf = 0; tf < 2; ++tf)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sums[c][tf][i] = 0.0f;
+      for (int i = 0; i < 4; ++i) sums[rf][tf][i] = 0.0f;
 
-  gload(0);
-  lds_put(0);
-  __syncthreads();
-  for (int s = 0; s < NSB; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < NSB) gload(s + 1);
-    float dd[2][4];  // (f16(d) * y.d) of this lane's outputs
+  // fold of LDS buffer p: 8 MFMAs, then the 16 chains in superblock order
+  auto fold = [&](int p) __attribute__((always_inline)) {
+    const uint2* sw = reinterpret_cast<const uint2*>(smem + p * Q6G_WB) + cls * 256 + g * 16 + r;
+    const uint2* sx = reinterpret_cast<const uint2*>(smem + 2 * Q6G_WB + p * Q6G_XB) + cls * 128 + g * 16 + r;
+    const float* sdd = reinterpret_cast<const float*>(smem + 2 * (Q6G_WB + Q6G_XB)) + p * Q6G_R * Q6G_DP;
+    long ah[2], al[2], bx[2];
 #pragma unroll
-    for (int tf = 0; tf < 2; ++tf)
+    for (int f = 0; f < 2; ++f) {
+      ah[f] = *reinterpret_cast<const long*>(sw + f * 64);        // plane h, row half f
+      al[f] = *reinterpret_cast<const long*>(sw + 128 + f * 64);  // plane lo
+      bx[f] = *reinterpret_cast<const long*>(sx + f * 64);        // token half f
+    }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dd[tf][i] = sd[buf][wn + 4 * g + i] * syd[buf][wt + 16 * tf + r];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const long ah = *reinterpret_cast<const long*>(&sw[buf][2 * c][g][wn + r]);
-      const long al = *reinterpret_cast<const long*>(&sw[buf][2 * c + 1][g][wn + r]);
+    for (int rf = 0; rf < 2; ++rf)
 #pragma unroll
       for (int tf = 0; tf < 2; ++tf) {
-        const long bv = *reinterpret_cast<const long*>(&sx[buf][c][g][wt + 16 * tf + r]);
-        const v4i_t ch = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bv, v4i_t{0, 0, 0, 0}, 0, 0, 0);
-        const v4i_t cl = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, bv, v4i_t{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sums[c][tf][i] += dd[tf][i] * (float)(ch[i] * 128 + cl[i]);
+        const v4i_t ch = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah[rf], bx[tf], v4i_t{0, 0, 0, 0}, 0, 0, 0);
+        const v4i_t cl = __builtin_amdgcn_mfma_i32_16x16x32_i8(al[rf], bx[tf], v4i_t{0, 0, 0, 0}, 0, 0, 0);
+        const float4 dd = *reinterpret_cast<const float4*>(sdd + (16 * tf + r) * Q6G_DP + 16 * rf + 4 * g);
+        sums[rf][tf][0] += dd.x * (float)(ch[0] * 128 + cl[0]);
+        sums[rf][tf][1] += dd.y * (float)(ch[1] * 128 + cl[1]);
+        sums[rf][tf][2] += dd.z * (float)(ch[2] * 128 + cl[2]);
+        sums[rf][tf][3] += dd.w * (float)(ch[3] * 128 + cl[3]);
       }
-      // one class at a time (its dots consumed before the next class's are formed: registers)
+    // the fold before the next tile's LDS stores (which wait for its global loads)
+#pragma unroll
+    for (int rf = 0; rf < 2; ++rf)
 #pragma unroll
       for (int tf = 0; tf < 2; ++tf)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(sums[c][tf][i]));
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (s + 1 < NSB) lds_put(buf ^ 1);
+        for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(sums[rf][tf][i]));
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // step s (LDS buffer and register set s % 2): issue step s + 2's loads into that set (its
+  // tile went to LDS at step s - 1 or before the loop), fold the buffer, store the other set
+  // (step s + 1's tile, loaded at step s - 1) into the other buffer.  The loop body is two
+  // whole steps with no branch: loads past the end re-read the last superblock and their
+  // stores fill a buffer no step folds, so the loads in flight at each store are the same on
+  // every path and a store waits only for its own set; an odd last step runs after the loop.
+  const int last = NSB - 1;
+  CM_Q6G_LOAD(0, 0)
+  CM_Q6G_LOAD(min(1, last), 1)
+  CM_Q6G_STORE(0)
+  __syncthreads();
+  int s = 0;
+  for (; s + 1 < NSB; s += 2) {
+    CM_Q6G_LOAD(min(s + 2, last), 0)
+    fold(0);
+    CM_Q6G_STORE(1)
+    __syncthreads();
+    CM_Q6G_LOAD(min(s + 3, last), 1)
+    fold(1);
+    CM_Q6G_STORE(0)  // step s + 2's tile (unused when s + 2 == NSB)
     __syncthreads();
   }
+  if (s < NSB) {  // odd NSB: the last step, in buffer 0
+    fold(0);
+    __syncthreads();
+  }
+#undef CM_Q6G_LOAD
+#undef CM_Q6G_STORE
+  float* sf = reinterpret_cast<float*>(smem);  // [class][token][row]
 #pragma unroll
-  for (int tf = 0; tf < 2; ++tf) {
-    const int t = t_base + wt + 16 * tf + r, n = n_base + wn + 4 * g;
-    float v[4];
+  for (int rf = 0; rf < 2; ++rf)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float a = -0.0f;
+    for (int tf = 0; tf < 2; ++tf)
+      *reinterpret_cast<float4*>(sf + (cls * Q6G_R + 16 * tf + r) * Q6G_DP + 16 * rf + 4 * g) =
+          make_float4(sums[rf][tf][0], sums[rf][tf][1], sums[rf][tf][2], sums[rf][tf][3]);
+  __syncthreads();
+  float a0 = -0.0f, a1 = -0.0f;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) a += sums[c][tf][i];
-      v[i] = a;
+  for (int c = 0; c < 8; ++c) {
+    const float2 v = *reinterpret_cast<const float2*>(sf + (c * Q6G_R + dtok) * Q6G_DP + drow);
+    a0 += v.x;
+    a1 += v.y;
+  }
+  const int t = tt * Q6G_R + dtok, n = rt * Q6G_R + drow;
+  if (t < T && n < N) {  // N even: n + 1 < N too
+    const size_t o = (size_t)t * ldy + n;
+    float2 out = make_float2(a0, a1);
+    if (resid) {
+      const float2 rr = *reinterpret_cast<const float2*>(resid + o);
+      out = make_float2(rr.x + a0, rr.y + a1);
     }
-    if (t < T && n < N) {
-      const size_t o = (size_t)t * ldy + n;
-      float4 out = make_float4(v[0], v[1], v[2], v[3]);
-      if (resid) {
-        const float4 rr = *reinterpret_cast<const float4*>(resid + o);
-        out = make_float4(rr.x + v[0], rr.y + v[1], rr.z + v[2], rr.w + v[3]);
-      }
-      *reinterpret_cast<float4*>(y + o) = out;
-    }
+    *reinterpret_cast<float2*>(y + o) = out;
   }
 }
 

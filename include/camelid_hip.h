@@ -307,9 +307,12 @@ int camelid_hip_kquant_gemv(uint8_t quant, const uint8_t* a, const uint8_t* b, c
 /* K-quant projection over `tokens` Q8_K activation rows (yd [tokens][k/256], yq [tokens][k]):
  * y[t * ldy + r] = resid[t * ldy + r] + W[r].x[t], each (token, row) bit-identical to
  * camelid_hip_kquant_gemv on that token.  Replaces the reference's per-token K-quant prefill
- * loop (inference.rs:2462-2473; the reference has no K-quant GEMM): Q4_K on the int8 matrix
- * cores, Q6_K by a multi-token GEMV.  k % 256 == 0, k <= 16384, ldy >= rows; resid may be
- * NULL; y may alias resid. */
+ * loop (inference.rs:2462-2473; the reference has no K-quant GEMM), on the int8 matrix cores.
+ * Q6_K over more than 8 tokens with rows % 4 == 0 and ldy % 4 == 0 builds the matrix's
+ * class-major weight planes and a class-major copy of yq for the call (temporary device
+ * allocations, freed after the stream is synchronized; the engine builds the planes once at
+ * upload).  k % 256 == 0,
+ * k <= 16384, ldy >= rows; resid may be NULL; y may alias resid. */
 int camelid_hip_kquant_gemm(uint8_t quant, const uint8_t* a, const uint8_t* b, const int8_t* sc,
                             const uint16_t* d, uint32_t rows, uint32_t k, uint32_t tokens,
                             const float* yd, const int8_t* yq, float* y, uint32_t ldy,
@@ -322,6 +325,15 @@ int camelid_hip_time_q8_0(int batched, const int8_t* const* wq, const uint16_t* 
                           uint32_t copies, uint32_t rows, uint32_t k, const int8_t* xq,
                           const float* xs, uint32_t tokens, float* y, uint32_t iters,
                           float* ms_out);
+/* Measurement hook (no reference counterpart; the kernel sweep of the benchmark): `iters`
+ * launches of the K-quant prefill GEMM over `tokens` Q8_K activation rows (ldy = rows), timed
+ * with HIP events on a stream of its own; Q6_K's weight planes are built once before the
+ * timed launches, each of which includes the activations' class-major copy; *ms_out = total
+ * milliseconds. */
+int camelid_hip_time_kquant(uint8_t quant, const uint8_t* a, const uint8_t* b, const int8_t* sc,
+                            const uint16_t* d, uint32_t rows, uint32_t k, uint32_t tokens,
+                            const float* yd, const int8_t* yq, float* y, uint32_t iters,
+                            float* ms_out);
 /* argmax_f32 (cuda_resident.rs:1847; CPU inference.rs:5912). */
 int camelid_hip_argmax(const float* x, uint32_t n, uint32_t* out, void* stream);
 /* Sequential-order f32 sums of rows [rows][n] (n <= 16384), evaluated by a workgroup-parallel

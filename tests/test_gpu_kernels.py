@@ -650,6 +650,50 @@ def test_kquant_gemm_bit_exact(native, orc, quant, rows, k, T, ldy):
             assert np.array_equal(_bits(want), _bits(orc.kquant_gemv(quant, wire, rows, k, ydh[t], yqh[t])))
 
 
+@pytest.mark.parametrize("case", ["min", "max", "mixed"])
+def test_q6k_gemm_extreme_products(native, orc, case):
+    """Q6_K chunk GEMM at the ends of its integer range: scaled weights sc * w of +4096 (sc =
+    -128, w = -32) and 127 * 31 against Q8_K quants of -127 and +127, so a class's integer dot
+    reaches 32 * 4096 * 127 (just under 2^24); every (token, row) equals the single-token GEMV
+    and the CPU dot bit for bit."""
+    rows, k, T = 64, 512, 40
+    rng = np.random.default_rng(7)
+    wire = _kquant_wire(orc, rng, 2, rows, k).reshape(rows, k // 256, 210)
+    if case == "min":  # ql = qh = 0: w = -32 everywhere; sc = -128
+        wire[:, :, 0:192] = 0
+        wire[:, :, 192:208] = np.uint8(0x80)
+    elif case == "max":  # ql = qh = all ones: w = 31; sc = 127
+        wire[:, :, 0:192] = 0xFF
+        wire[:, :, 192:208] = 127
+    else:  # per superblock one of the two extremes, scales at +-127 / -128
+        wire[::2, :, 0:192] = 0
+        wire[1::2, :, 0:192] = 0xFF
+        wire[:, :, 192:208] = rng.choice(np.array([0x80, 0x7F, 0x81], np.uint8), (rows, k // 256, 16))
+    wire = wire.ravel()
+    a, b, sc, d = _kquant_planes(native, 2, wire, rows, k)
+    x = np.ones((T, k), np.float32)  # quants of -127 (a block's max maps to -127 whatever its sign)
+    x[1::3] = -1.0
+    x[1::3, ::256] = 1.0  # each block's first element is its max: the -1 entries give +127
+    x[2::5, ::7] = 0.5
+    yds, yqs = zip(*(orc.quantize_q8_k(x[t]) for t in range(T)))
+    ydh, yqh = np.stack(yds).astype(np.float32), np.stack(yqs).astype(np.int8)
+    assert (yqh == -127).any() and (yqh == 127).any()
+    yd, yq, y = _dev(ydh), _dev(yqh), _buf(T * rows * 4)
+    _ok(native.camelid_hip_kquant_gemm(2, a.ptr, b.ptr, sc.ptr, d.ptr, rows, k, T, yd.ptr, yq.ptr, y.ptr, rows,
+                                       None, None))
+    got = y.download(np.float32, T * rows).reshape(T, rows)
+    one, ybs = _buf(rows * 4), _buf(k // 32 * 4)
+    for t in range(T):
+        tyd, tyq = _dev(ydh[t]), _dev(yqh[t])
+        dbs = _dev(yqh[t].astype(np.int32).reshape(-1, 32).sum(1).astype(np.int32))
+        _ok(native.camelid_hip_kquant_gemv(2, a.ptr, b.ptr, sc.ptr, d.ptr, rows, k, tyd.ptr, tyq.ptr, dbs.ptr,
+                                           one.ptr, None, None))
+        want = one.download(np.float32, rows)
+        assert np.array_equal(_bits(got[t]), _bits(want)), f"token {t}"
+        if t in (0, 1, T - 1):
+            assert np.array_equal(_bits(want), _bits(orc.kquant_gemv(2, wire, rows, k, ydh[t], yqh[t])))
+
+
 @pytest.mark.parametrize("n", [1, 1000, 32000, 128256, 151936])
 def test_argmax_matches_first_max(native, orc, n):
     rng = np.random.default_rng(n)
