@@ -688,31 +688,32 @@ __global__ __launch_bounds__(256) void k_embed_q6k(const uint8_t* __restrict__ q
 // superblock.  Lane l of a fragment supplies token / row l % 16, values 8*(l/16) .. +7 of
 // the sub-block; 8 nibble bytes of a row give the row operands of both sub-blocks of a
 // 64-value chunk (low nibbles: sub-block 2c, high: 2c + 1).
-// Workgroup: 4 waves over a 64-row x 64-token tile, each wave 32 x 32 (2 x 2 fragments).
+// Workgroup: 8 waves over a 64-row x 64-token tile, each wave 16 rows x 32 tokens (1 x 2
+// fragments: a row's nibbles are unpacked once per 32 tokens; 24 accumulators per lane, so
+// two workgroups share a CU at four waves per SIMD).
 // One superblock per step: 128 nibble bytes of every row and 256 activation bytes of every
 // token, loaded one step ahead into registers, then into a double-buffered LDS tile
 // [chunk or sub-block][8-byte piece][row or token] (65-entry planes: no bank conflicts);
-// headers and activation scales go straight to registers one step ahead.
+// headers and activation scales go the same way one step ahead.
 // Tiles are dealt so that each XCD runs a contiguous range, token tiles innermost.
 // K % 256 == 0; y may alias resid (same row stride ldy).
-constexpr int G4_NT = 256;
+constexpr int G4_NT = 512;
 constexpr int G4_RN = 64;
 constexpr int G4_RT = 64;
 constexpr int G4_PS = 65;
-constexpr int G4_MAX_SB = 64;  // K <= 16384
 __host__ __device__ inline int gemm_q4k_tiles(int N, int T) {
   return ((N + G4_RN - 1) / G4_RN) * ((T + G4_RT - 1) / G4_RT);
 }
 __host__ __device__ inline int gemm_q4k_grid(int N, int T) { return ((gemm_q4k_tiles(N, T) + 7) / 8) * 8; }
 
-__global__ __launch_bounds__(G4_NT, 2) void k_gemm_q4k(const uint8_t* __restrict__ nib,
+__global__ __launch_bounds__(G4_NT, 4) void k_gemm_q4k(const uint8_t* __restrict__ nib,
                                                        const uint8_t* __restrict__ hdr, int N, int K,
                                                        const float* __restrict__ xd,
                                                        const int8_t* __restrict__ xq, int T, float* y, int ldy,
                                                        const float* resid) {
   __shared__ __align__(16) uint2 sw[2][4][4][G4_PS];  // weights: [buf][64-value chunk][piece][row]
   __shared__ __align__(16) uint2 sx[2][8][4][G4_PS];  // activations: [buf][sub-block][piece][token]
-  __shared__ __align__(16) float sxd[G4_MAX_SB][G4_RT];  // activation scales: [superblock][token]
+  __shared__ __align__(16) float sxd[2][G4_RT];       // activation scales: [buf][token]
   const int NSB = K >> 8;
   const int ntt = (T + G4_RT - 1) / G4_RT;
   const int tiles = gemm_q4k_tiles(N, T);
@@ -722,123 +723,99 @@ __global__ __launch_bounds__(G4_NT, 2) void k_gemm_q4k(const uint8_t* __restrict
   const int n_base = (L / ntt) * G4_RN, t_base = (L % ntt) * G4_RT;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int r = lane & 15, g = lane >> 4;
-  const int wn = (wave & 1) * 32, wt = (wave >> 1) * 32;
-  for (int i = tid; i < NSB * G4_RT; i += G4_NT) {
-    const int sb = i / G4_RT, t = i - sb * G4_RT;
-    sxd[sb][t] = xd[(size_t)min(t_base + t, T - 1) * NSB + sb];
-  }
+  const int wn = (wave & 3) * 16, wt = (wave >> 2) * 32;
 
   // global -> register loads of one superblock step (32-bit offsets from the matrix bases)
-  const int wrow = tid >> 3, wc = tid & 7;   // weights: rows wrow + 32 j, 16 bytes at wc * 16
-  const int xrow = tid >> 4, xc = tid & 15;  // activations: tokens xrow + 16 j, 16 bytes at xc * 16
-  uint32_t ow[2], ox[4], oh[2];
+  const int wrow = tid >> 3, wc = tid & 7;   // weights: row wrow, 16 bytes at wc * 16
+  const int xrow = tid >> 4, xc = tid & 15;  // activations: tokens xrow + 32 j, 16 bytes at xc * 16
+  const uint32_t ow = (uint32_t)min(n_base + wrow, N - 1) * (uint32_t)(K >> 1) + wc * 16;
+  uint32_t ox[2];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) ow[j] = (uint32_t)min(n_base + wrow + 32 * j, N - 1) * (uint32_t)(K >> 1) + wc * 16;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) ox[j] = (uint32_t)min(t_base + xrow + 16 * j, T - 1) * (uint32_t)K + xc * 16;
-#pragma unroll
-  for (int f = 0; f < 2; ++f) oh[f] = (uint32_t)min(n_base + wn + 16 * f + r, N - 1) * (uint32_t)NSB;
-  uint4 rw[2], rx[4], rh[2];
+  for (int j = 0; j < 2; ++j) ox[j] = (uint32_t)min(t_base + xrow + 32 * j, T - 1) * (uint32_t)K + xc * 16;
+  const uint32_t oh = (uint32_t)min(n_base + wn + r, N - 1) * (uint32_t)NSB;
+  const float* gxd = xd + (size_t)min(t_base + (tid & (G4_RT - 1)), T - 1) * NSB;  // (threads < 64)
+  uint4 rw, rx[2], rh;
+  float rxd = 0.0f;
   auto gload = [&](int s) {
+    if (tid < G4_RT) rxd = gxd[s];
+    rw = *reinterpret_cast<const uint4*>(nib + (ow + (uint32_t)s * 128u));
 #pragma unroll
-    for (int j = 0; j < 2; ++j) rw[j] = *reinterpret_cast<const uint4*>(nib + ow[j] + (size_t)s * 128);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) rx[j] = *reinterpret_cast<const uint4*>(xq + ox[j] + (size_t)s * 256);
-#pragma unroll
-    for (int f = 0; f < 2; ++f) rh[f] = reinterpret_cast<const uint4*>(hdr)[oh[f] + s];
+    for (int j = 0; j < 2; ++j) rx[j] = *reinterpret_cast<const uint4*>(xq + (ox[j] + (uint32_t)s * 256u));
+    rh = reinterpret_cast<const uint4*>(hdr)[oh + (uint32_t)s];
   };
   auto lds_put = [&](int buf) {
     const int wchunk = wc >> 1, wp = (wc & 1) * 2;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      sw[buf][wchunk][wp][wrow + 32 * j] = make_uint2(rw[j].x, rw[j].y);
-      sw[buf][wchunk][wp + 1][wrow + 32 * j] = make_uint2(rw[j].z, rw[j].w);
-    }
+    sw[buf][wchunk][wp][wrow] = make_uint2(rw.x, rw.y);
+    sw[buf][wchunk][wp + 1][wrow] = make_uint2(rw.z, rw.w);
     const int xsb = xc >> 1, xp = (xc & 1) * 2;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      sx[buf][xsb][xp][xrow + 16 * j] = make_uint2(rx[j].x, rx[j].y);
-      sx[buf][xsb][xp + 1][xrow + 16 * j] = make_uint2(rx[j].z, rx[j].w);
+    for (int j = 0; j < 2; ++j) {
+      sx[buf][xsb][xp][xrow + 32 * j] = make_uint2(rx[j].x, rx[j].y);
+      sx[buf][xsb][xp + 1][xrow + 32 * j] = make_uint2(rx[j].z, rx[j].w);
     }
+    if (tid < G4_RT) sxd[buf][tid] = rxd;
   };
 
-  float acc[2][2][4];  // [token fragment][row fragment][token 4g + i]
+  float acc[2][4];  // [token fragment][token 4g + i]
 #pragma unroll
   for (int tf = 0; tf < 2; ++tf)
 #pragma unroll
-    for (int nf = 0; nf < 2; ++nf)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[tf][nf][i] = 0.0f;
+    for (int i = 0; i < 4; ++i) acc[tf][i] = 0.0f;
 
   const uint32_t K1 = 0x3f3f3f3fu, K2 = 0x0f0f0f0fu, K3 = 0x03030303u;
-  auto step = [&](int buf, int sb, const uint4 (&hd)[2]) {
-    // the rows' 6-bit scales and mins, 4 per dword (sub-blocks 0-3, 4-7)
-    uint32_t scp[2][2], mnp[2][2];
+  auto step = [&](int buf, const uint4& hd) {
+    // the row's 6-bit scales and mins, 4 per dword (sub-blocks 0-3, 4-7)
+    uint32_t scp[2], mnp[2];
+    scp[0] = hd.y & K1;
+    scp[1] = (hd.w & K2) | (((hd.y >> 6) & K3) << 4);
+    mnp[0] = hd.z & K1;
+    mnp[1] = ((hd.w >> 4) & K2) | (((hd.z >> 6) & K3) << 4);
+    int sumi[2][4];
+    v4i_t cmn[2];
 #pragma unroll
-    for (int nf = 0; nf < 2; ++nf) {
-      scp[nf][0] = hd[nf].y & K1;
-      scp[nf][1] = (hd[nf].w & K2) | (((hd[nf].y >> 6) & K3) << 4);
-      mnp[nf][0] = hd[nf].z & K1;
-      mnp[nf][1] = ((hd[nf].w >> 4) & K2) | (((hd[nf].z >> 6) & K3) << 4);
+    for (int tf = 0; tf < 2; ++tf) {
+      cmn[tf] = v4i_t{0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sumi[tf][i] = 0;
     }
-    int sumi[2][2][4];
-    v4i_t cmn[2][2];
-#pragma unroll
-    for (int tf = 0; tf < 2; ++tf)
-#pragma unroll
-      for (int nf = 0; nf < 2; ++nf) {
-        cmn[tf][nf] = v4i_t{0, 0, 0, 0};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sumi[tf][nf][i] = 0;
-      }
 #pragma unroll
     for (int c4 = 0; c4 < 4; ++c4) {
       __builtin_amdgcn_sched_barrier(0);  // one 64-value chunk at a time (register pressure)
-      uint2 wv[2];
-#pragma unroll
-      for (int nf = 0; nf < 2; ++nf) wv[nf] = sw[buf][c4][g][wn + 16 * nf + r];
+      const uint2 wv = sw[buf][c4][g][wn + r];
 #pragma unroll
       for (int hb = 0; hb < 2; ++hb) {
+        if (hb) __builtin_amdgcn_sched_barrier(0);  // one sub-block's products live at a time
         const int j = 2 * c4 + hb;
-        long av[2], bw[2], bm[2];
-        int scj[2];
+        long av[2];
 #pragma unroll
         for (int tf = 0; tf < 2; ++tf) av[tf] = *reinterpret_cast<const long*>(&sx[buf][j][g][wt + 16 * tf + r]);
+        const uint32_t lo = hb ? ((wv.x >> 4) & K2) : (wv.x & K2);
+        const uint32_t hi = hb ? ((wv.y >> 4) & K2) : (wv.y & K2);
+        const long bw = (long)(((uint64_t)hi << 32) | lo);
+        const uint32_t sel = (uint32_t)(j & 3) * 0x01010101u;  // byte j % 4 into all four bytes
+        const uint32_t mrep = __builtin_amdgcn_perm(0u, mnp[j >> 2], sel);
+        const long bm = (long)(((uint64_t)mrep << 32) | mrep);
+        const int scj = (int)((scp[j >> 2] >> (8 * (j & 3))) & 0xffu);
 #pragma unroll
-        for (int nf = 0; nf < 2; ++nf) {
-          const uint32_t lo = hb ? ((wv[nf].x >> 4) & K2) : (wv[nf].x & K2);
-          const uint32_t hi = hb ? ((wv[nf].y >> 4) & K2) : (wv[nf].y & K2);
-          bw[nf] = (long)(((uint64_t)hi << 32) | lo);
-          const uint32_t sel = (uint32_t)(j & 3) * 0x01010101u;  // byte j % 4 into all four bytes
-          const uint32_t mrep = __builtin_amdgcn_perm(0u, mnp[nf][j >> 2], sel);
-          bm[nf] = (long)(((uint64_t)mrep << 32) | mrep);
-          scj[nf] = (int)((scp[nf][j >> 2] >> (8 * (j & 3))) & 0xffu);
+        for (int tf = 0; tf < 2; ++tf) {
+          const v4i_t c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[tf], bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+          cmn[tf] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[tf], bm, cmn[tf], 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sumi[tf][i] += scj * c[i];
         }
-#pragma unroll
-        for (int tf = 0; tf < 2; ++tf)
-#pragma unroll
-          for (int nf = 0; nf < 2; ++nf) {
-            const v4i_t c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[tf], bw[nf], v4i_t{0, 0, 0, 0}, 0, 0, 0);
-            cmn[tf][nf] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[tf], bm[nf], cmn[tf][nf], 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sumi[tf][nf][i] += scj[nf] * c[i];
-          }
       }
     }
     __builtin_amdgcn_sched_barrier(0);
+    const float dw = half_bits_to_float((uint16_t)(hd.x & 0xffffu));
+    const float dmw = half_bits_to_float((uint16_t)(hd.x >> 16));
 #pragma unroll
     for (int tf = 0; tf < 2; ++tf) {
-      const float4 y4 = *reinterpret_cast<const float4*>(&sxd[sb][wt + 16 * tf + 4 * g]);
+      const float4 y4 = *reinterpret_cast<const float4*>(&sxd[buf][wt + 16 * tf + 4 * g]);
       const float ydv[4] = {y4.x, y4.y, y4.z, y4.w};
 #pragma unroll
-      for (int nf = 0; nf < 2; ++nf) {
-        const float dw = half_bits_to_float((uint16_t)(hd[nf].x & 0xffffu));
-        const float dmw = half_bits_to_float((uint16_t)(hd[nf].x >> 16));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc[tf][nf][i] = fmaf(-(ydv[i] * dmw), (float)cmn[tf][nf][i], acc[tf][nf][i]);
-          acc[tf][nf][i] = fmaf(ydv[i] * dw, (float)sumi[tf][nf][i], acc[tf][nf][i]);
-        }
+      for (int i = 0; i < 4; ++i) {
+        acc[tf][i] = fmaf(-(ydv[i] * dmw), (float)cmn[tf][i], acc[tf][i]);
+        acc[tf][i] = fmaf(ydv[i] * dw, (float)sumi[tf][i], acc[tf][i]);
       }
     }
   };
@@ -848,24 +825,21 @@ __global__ __launch_bounds__(G4_NT, 2) void k_gemm_q4k(const uint8_t* __restrict
   __syncthreads();
   for (int sb = 0; sb < NSB; ++sb) {
     const int buf = sb & 1;
-    const uint4 hd[2] = {rh[0], rh[1]};
+    const uint4 hd = rh;
     if (sb + 1 < NSB) gload(sb + 1);
-    step(buf, sb, hd);
+    step(buf, hd);
     if (sb + 1 < NSB) lds_put(buf ^ 1);
     __syncthreads();
   }
+  const int n = n_base + wn + r;
 #pragma unroll
   for (int tf = 0; tf < 2; ++tf)
 #pragma unroll
-    for (int nf = 0; nf < 2; ++nf) {
-      const int n = n_base + wn + 16 * nf + r;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = t_base + wt + 16 * tf + 4 * g + i;
-        if (t < T && n < N) {
-          const size_t o = (size_t)t * ldy + n;
-          y[o] = resid ? resid[o] + acc[tf][nf][i] : acc[tf][nf][i];
-        }
+    for (int i = 0; i < 4; ++i) {
+      const int t = t_base + wt + 16 * tf + 4 * g + i;
+      if (t < T && n < N) {
+        const size_t o = (size_t)t * ldy + n;
+        y[o] = resid ? resid[o] + acc[tf][i] : acc[tf][i];
       }
     }
 }
