@@ -697,6 +697,7 @@ __global__ __launch_bounds__(256) void k_embed_q6k(const uint8_t* __restrict__ q
 // headers and activation scales go the same way one step ahead.
 // Tiles are dealt so that each XCD runs a contiguous range, token tiles innermost.
 // K % 256 == 0; y may alias resid (same row stride ldy).
+typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
 constexpr int G4_NT = 512;
 constexpr int G4_RN = 64;
 constexpr int G4_RT = 64;
@@ -711,8 +712,10 @@ __global__ __launch_bounds__(G4_NT, 4) void k_gemm_q4k(const uint8_t* __restrict
                                                        const float* __restrict__ xd,
                                                        const int8_t* __restrict__ xq, int T, float* y, int ldy,
                                                        const float* resid) {
-  __shared__ __align__(16) uint2 sw[2][4][4][G4_PS];  // weights: [buf][64-value chunk][piece][row]
-  __shared__ __align__(16) uint2 sx[2][8][4][G4_PS];  // activations: [buf][sub-block][piece][token]
+  // 16-byte units: weights [buf][64-value chunk][half][row] (chunk bytes 16 h .. 16 h + 15),
+  // activations [buf][sub-block][half][token] (positions 16 h .. 16 h + 15); 65-unit planes
+  __shared__ __align__(16) uint4 sw[2][4][2][G4_PS];
+  __shared__ __align__(16) uint4 sx[2][8][2][G4_PS];
   __shared__ __align__(16) float sxd[2][G4_RT];       // activation scales: [buf][token]
   const int NSB = K >> 8;
   const int ntt = (T + G4_RT - 1) / G4_RT;
@@ -734,25 +737,19 @@ __global__ __launch_bounds__(G4_NT, 4) void k_gemm_q4k(const uint8_t* __restrict
   for (int j = 0; j < 2; ++j) ox[j] = (uint32_t)min(t_base + xrow + 32 * j, T - 1) * (uint32_t)K + xc * 16;
   const uint32_t oh = (uint32_t)min(n_base + wn + r, N - 1) * (uint32_t)NSB;
   const float* gxd = xd + (size_t)min(t_base + (tid & (G4_RT - 1)), T - 1) * NSB;  // (threads < 64)
-  uint4 rw, rx[2], rh;
+  uint4 rw, rx0, rx1, rh;
   float rxd = 0.0f;
   auto gload = [&](int s) {
     if (tid < G4_RT) rxd = gxd[s];
     rw = *reinterpret_cast<const uint4*>(nib + (ow + (uint32_t)s * 128u));
-#pragma unroll
-    for (int j = 0; j < 2; ++j) rx[j] = *reinterpret_cast<const uint4*>(xq + (ox[j] + (uint32_t)s * 256u));
+    rx0 = *reinterpret_cast<const uint4*>(xq + (ox[0] + (uint32_t)s * 256u));
+    rx1 = *reinterpret_cast<const uint4*>(xq + (ox[1] + (uint32_t)s * 256u));
     rh = reinterpret_cast<const uint4*>(hdr)[oh + (uint32_t)s];
   };
   auto lds_put = [&](int buf) {
-    const int wchunk = wc >> 1, wp = (wc & 1) * 2;
-    sw[buf][wchunk][wp][wrow] = make_uint2(rw.x, rw.y);
-    sw[buf][wchunk][wp + 1][wrow] = make_uint2(rw.z, rw.w);
-    const int xsb = xc >> 1, xp = (xc & 1) * 2;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      sx[buf][xsb][xp][xrow + 32 * j] = make_uint2(rx[j].x, rx[j].y);
-      sx[buf][xsb][xp + 1][xrow + 32 * j] = make_uint2(rx[j].z, rx[j].w);
-    }
+    sw[buf][wc >> 1][wc & 1][wrow] = make_uint4(rw.x, rw.y, rw.z, rw.w);
+    sx[buf][xc >> 1][xc & 1][xrow] = make_uint4(rx0.x, rx0.y, rx0.z, rx0.w);
+    sx[buf][xc >> 1][xc & 1][xrow + 32] = make_uint4(rx1.x, rx1.y, rx1.z, rx1.w);
     if (tid < G4_RT) sxd[buf][tid] = rxd;
   };
 
@@ -770,39 +767,39 @@ __global__ __launch_bounds__(G4_NT, 4) void k_gemm_q4k(const uint8_t* __restrict
     scp[1] = (hd.w & K2) | (((hd.y >> 6) & K3) << 4);
     mnp[0] = hd.z & K1;
     mnp[1] = ((hd.w >> 4) & K2) | (((hd.z >> 6) & K3) << 4);
-    int sumi[2][4];
-    v4i_t cmn[2];
+    // sumi = sum_j sc_j D_j as one K = 256 integer dot per plane: sc_j = 8 sh_j + sl_j (3 bits
+    // each), so sh_j * q and sl_j * q (<= 105) are int8 weights: sumi = 8 (H . x) + (L . x);
+    // prod = sum_k mn_j(k) x_k.  Per 64-value chunk one v_mfma_i32_16x16x64_i8 per plane and
+    // token fragment; lane (r, g) supplies positions 16 (g % 2) .. +15 of sub-block
+    // 2 chunk + g / 2 (the high nibbles for odd sub-blocks), the same positions of x.
+    const int gb = g >> 1, gh = g & 1;
+    v4i_t ch[2], cl[2], cm[2];
 #pragma unroll
-    for (int tf = 0; tf < 2; ++tf) {
-      cmn[tf] = v4i_t{0, 0, 0, 0};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sumi[tf][i] = 0;
-    }
+    for (int tf = 0; tf < 2; ++tf) ch[tf] = cl[tf] = cm[tf] = v4i_t{0, 0, 0, 0};
 #pragma unroll
     for (int c4 = 0; c4 < 4; ++c4) {
       __builtin_amdgcn_sched_barrier(0);  // one 64-value chunk at a time (register pressure)
-      const uint2 wv = sw[buf][c4][g][wn + r];
+      const int sh8 = 16 * (c4 & 1) + 8 * gb;  // byte of sub-block 2 c4 + gb in scp / mnp[c4 / 2]
+      const uint32_t sc = (scp[c4 >> 1] >> sh8) & 0xffu, mn = (mnp[c4 >> 1] >> sh8) & 0xffu;
+      const u16x2_t shp = {(uint16_t)(sc >> 3), (uint16_t)(sc >> 3)}, slp = {(uint16_t)(sc & 7u), (uint16_t)(sc & 7u)};
+      const uint32_t mrep = __builtin_amdgcn_perm(0u, mn, 0u);  // mn's byte 0 (selector 0: second operand) x 4
+      const uint4 w = sw[buf][c4][gh][wn + r];
+      const uint32_t ns = 4 * gb;
+      const uint32_t nb[4] = {(w.x >> ns) & K2, (w.y >> ns) & K2, (w.z >> ns) & K2, (w.w >> ns) & K2};
+      v4i_t wh, wl;
 #pragma unroll
-      for (int hb = 0; hb < 2; ++hb) {
-        if (hb) __builtin_amdgcn_sched_barrier(0);  // one sub-block's products live at a time
-        const int j = 2 * c4 + hb;
-        long av[2];
+      for (int u = 0; u < 4; ++u) {  // bytes <= 15 times <= 7: no carry between the bytes of a half
+        const u16x2_t q = __builtin_bit_cast(u16x2_t, nb[u]);
+        wh[u] = __builtin_bit_cast(int, q * shp);
+        wl[u] = __builtin_bit_cast(int, q * slp);
+      }
+      const v4i_t wm = v4i_t{(int)mrep, (int)mrep, (int)mrep, (int)mrep};
 #pragma unroll
-        for (int tf = 0; tf < 2; ++tf) av[tf] = *reinterpret_cast<const long*>(&sx[buf][j][g][wt + 16 * tf + r]);
-        const uint32_t lo = hb ? ((wv.x >> 4) & K2) : (wv.x & K2);
-        const uint32_t hi = hb ? ((wv.y >> 4) & K2) : (wv.y & K2);
-        const long bw = (long)(((uint64_t)hi << 32) | lo);
-        const uint32_t sel = (uint32_t)(j & 3) * 0x01010101u;  // byte j % 4 into all four bytes
-        const uint32_t mrep = __builtin_amdgcn_perm(0u, mnp[j >> 2], sel);
-        const long bm = (long)(((uint64_t)mrep << 32) | mrep);
-        const int scj = (int)((scp[j >> 2] >> (8 * (j & 3))) & 0xffu);
-#pragma unroll
-        for (int tf = 0; tf < 2; ++tf) {
-          const v4i_t c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[tf], bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
-          cmn[tf] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[tf], bm, cmn[tf], 0, 0, 0);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sumi[tf][i] += scj * c[i];
-        }
+      for (int tf = 0; tf < 2; ++tf) {
+        const v4i_t xa = __builtin_bit_cast(v4i_t, sx[buf][2 * c4 + gb][gh][wt + 16 * tf + r]);
+        ch[tf] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wh, ch[tf], 0, 0, 0);
+        cl[tf] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wl, cl[tf], 0, 0, 0);
+        cm[tf] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wm, cm[tf], 0, 0, 0);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -814,8 +811,8 @@ __global__ __launch_bounds__(G4_NT, 4) void k_gemm_q4k(const uint8_t* __restrict
       const float ydv[4] = {y4.x, y4.y, y4.z, y4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        acc[tf][i] = fmaf(-(ydv[i] * dmw), (float)cmn[tf][i], acc[tf][i]);
-        acc[tf][i] = fmaf(ydv[i] * dw, (float)sumi[tf][i], acc[tf][i]);
+        acc[tf][i] = fmaf(-(ydv[i] * dmw), (float)cm[tf][i], acc[tf][i]);
+        acc[tf][i] = fmaf(ydv[i] * dw, (float)(ch[tf][i] * 8 + cl[tf][i]), acc[tf][i]);
       }
     }
   };
