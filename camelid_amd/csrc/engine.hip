@@ -417,7 +417,7 @@ int upload_kq(camelid_hip_engine* e, KMat* m, const uint8_t* src, size_t len, ui
     HIP_TRY(e, hipMemcpy(m->d, d.data(), d.size() * 2, hipMemcpyHostToDevice));
     if (gemm_planes && e->q6_gemm2) {  // the prefill GEMM's weight planes, built on the device
       if (!m->w2 && dev_alloc(e, &m->w2, cm::q6g_planes_bytes((int)rows, (int)k))) return 1;
-      hipLaunchKernelGGL(cm::k_q6k_w2, dim3((uint32_t)nsb, (rows + cm::Q6G_R - 1) / cm::Q6G_R * cm::Q6G_R), dim3(256),
+      hipLaunchKernelGGL(cm::k_q6k_w2, dim3((rows + cm::Q6G_R - 1) / cm::Q6G_R * cm::Q6G_R, (uint32_t)nsb), dim3(256),
                          0, e->stream, m->a, m->b, m->sc, (int)rows, (int)k, m->w2);
       HIP_TRY(e, hipGetLastError());
       HIP_TRY(e, hipStreamSynchronize(e->stream));
@@ -2774,6 +2774,8 @@ int camelid_hip_kquant_gemm(uint8_t quant, const uint8_t* a, const uint8_t* b, c
   if (quant == CAMELID_Q6_K && (!sc || !d)) return fail(nullptr, "null argument");
   if (rows == 0 || k == 0 || k % 256 || k > 16384) return fail(nullptr, "k must be a multiple of 256, at most 16384");
   if (tokens == 0 || ldy < rows) return fail(nullptr, "tokens must be nonzero and ldy >= rows");
+  if ((uint64_t)tokens * k >= (1ull << 31) || (uint64_t)rows * k >= (1ull << 32))
+    return fail(nullptr, "kquant_gemm: tokens * k must be below 2^31 and rows * k below 2^32 (32-bit GEMM offsets)");
   KMat m;
   m.quant = quant;
   m.a = const_cast<uint8_t*>(a);
@@ -2798,7 +2800,7 @@ int camelid_hip_kquant_gemm(uint8_t quant, const uint8_t* a, const uint8_t* b, c
       (void)hipFree(m.w2);
       return fail(nullptr, "kquant_gemm: activation copy allocation failed");
     }
-    hipLaunchKernelGGL(cm::k_q6k_w2, dim3(k / 256, (rows + cm::Q6G_R - 1) / cm::Q6G_R * cm::Q6G_R), dim3(256), 0,
+    hipLaunchKernelGGL(cm::k_q6k_w2, dim3((rows + cm::Q6G_R - 1) / cm::Q6G_R * cm::Q6G_R, k / 256), dim3(256), 0,
                        (hipStream_t)stream, m.a, m.b, m.sc, (int)rows, (int)k, m.w2);
   }
   launch_kgemm(m, tokens, yd, yq, y, ldy, resid, (hipStream_t)stream, xt);
@@ -2887,7 +2889,7 @@ int camelid_hip_time_kquant(uint8_t quant, const uint8_t* a, const uint8_t* b, c
       xt = nullptr;
       rc = fail(nullptr, "time_kquant: activation copy allocation failed");
     } else {
-      hipLaunchKernelGGL(cm::k_q6k_w2, dim3(k / 256, (rows + cm::Q6G_R - 1) / cm::Q6G_R * cm::Q6G_R), dim3(256), 0,
+      hipLaunchKernelGGL(cm::k_q6k_w2, dim3((rows + cm::Q6G_R - 1) / cm::Q6G_R * cm::Q6G_R, k / 256), dim3(256), 0,
                          s, m.a, m.b, m.sc, (int)rows, (int)k, m.w2);
     }
   }

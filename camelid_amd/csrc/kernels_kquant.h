@@ -1129,13 +1129,13 @@ __host__ __device__ inline int gemm_q6k2_tiles(int N, int T) {
 }
 __host__ __device__ inline int gemm_q6k2_grid(int N, int T) { return ((gemm_q6k2_tiles(N, T) + 7) / 8) * 8; }
 
-// grid (K / 256, N rounded up to 32), 256 threads: thread p of workgroup (s, row) writes
+// grid (N rounded up to 32, K / 256), 256 threads: thread p of workgroup (row, s) writes
 // position p's h and lo (zeros for the padding rows >= N).
 __global__ __launch_bounds__(256) void k_q6k_w2(const uint8_t* __restrict__ ql, const uint8_t* __restrict__ qh,
                                                 const int8_t* __restrict__ scl, int N, int K,
                                                 int8_t* __restrict__ w2) {
-  const int s = blockIdx.x, p = threadIdx.x, NSB = K >> 8;
-  const int row = blockIdx.y;
+  const int s = blockIdx.y, p = threadIdx.x, NSB = K >> 8;
+  const int row = blockIdx.x;
   int h = 0, lo = 0;
   if (row < N) {
     const uint8_t* l8 = ql + (size_t)row * (K >> 1) + (size_t)s * 128;

@@ -312,7 +312,8 @@ int camelid_hip_kquant_gemv(uint8_t quant, const uint8_t* a, const uint8_t* b, c
  * class-major weight planes and a class-major copy of yq for the call (temporary device
  * allocations, freed after the stream is synchronized; the engine builds the planes once at
  * upload).  k % 256 == 0,
- * k <= 16384, ldy >= rows; resid may be NULL; y may alias resid. */
+ * k <= 16384, ldy >= rows, tokens * k < 2^31, rows * k < 2^32; resid may be NULL; y may
+ * alias resid. */
 int camelid_hip_kquant_gemm(uint8_t quant, const uint8_t* a, const uint8_t* b, const int8_t* sc,
                             const uint16_t* d, uint32_t rows, uint32_t k, uint32_t tokens,
                             const float* yd, const int8_t* yq, float* y, uint32_t ldy,
