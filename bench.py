@@ -339,6 +339,21 @@ def attention_phases(cfg) -> dict:
         ph["workgroups"] = int(len(g))
         res[name] = {k: round(v, 3) for k, v in ph.items()}
         log(f"{name} phases (us from each workgroup's start): " + ", ".join(f"{k} {v:.3f}" for k, v in ph.items()))
+    # the Q4_K output projection's workgroups of the last split launch (first and last
+    # workgroup), from the split output workgroups' first start and last end
+    ao = allst[na + ng + nsp:].reshape(64, 2, 4)[cfg.n_layers - 1]
+    g = sp[1]
+    g = g[(g[:, 0] > 0) & (g[:, 5] > 0)]
+    if (ao[:, 0] > 0).all() and (ao[:, 3] > 0).all() and len(g) and "output_projection" not in res:
+        a0, a1 = g[:, 0].min(), g[:, 5].max()
+        ph = {"start_from_output_start": float((ao[:, 0] - a0).mean() * 0.01),
+              "tag_seen_from_output_end": float((ao[:, 1] - a1).mean() * 0.01),
+              "staged_from_output_end": float((ao[:, 2] - a1).mean() * 0.01),
+              "end_from_output_end": float((ao[:, 3] - a1).mean() * 0.01),
+              "last_end_from_output_start": float((ao[:, 3].max() - a0) * 0.01)}
+        res["output_projection_q4k"] = {k: round(v, 3) for k, v in ph.items()}
+        log("Q4_K output projection workgroups, last layer (us): " +
+            ", ".join(f"{k} {v:.3f}" for k, v in ph.items()))
     return res
 
 

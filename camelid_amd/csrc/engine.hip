@@ -159,6 +159,7 @@ struct camelid_hip_engine {
   // (cm::att_oproj; CAMELID_HIP_ATT_O).  Measured on MI355X: see the layer loop.
   bool att_o_fused = true;
   int ao_state = -1;              // -1 unknown, 0 off, 1 on
+  int ao4_state = -1;             // the Q4_K output projection in the split attention launch (ao4_enabled)
   uint64_t* ao_words = nullptr;   // the tagged activation words (ao_words())
   uint32_t* p_err = nullptr;      // host copy of the handoff error word
   bool err_pending = false;       // nf_end enqueued its copy in the current call
@@ -711,6 +712,13 @@ void launch_attention_fused(uint32_t hd, uint32_t n_heads, int slots, hipStream_
     }
     grid += (uint32_t)(op.rows + cm::AO_ROWS - 1) / cm::AO_ROWS;
     lds = std::max(lds, cm::ao_lds_bytes(op.K));
+  } else if (op.k4nib) {
+    if (cm::att_nt((int)hd) != cm::AO_ROWS * 64 || !cm::aoq_width_ok(op.K) || op.K != (int)(n_heads * hd)) {
+      g_launch_error = "attention: no Q4_K output projection body for this shape";
+      return;
+    }
+    grid += (uint32_t)(op.rows + cm::AOQ_ROWS - 1) / cm::AOQ_ROWS;
+    lds = std::max(lds, cm::kq4_lds_bytes(op.K, cm::AOQ_ROWS));
   }
 #define CM_ATTF(HD, PB, SL)                                                                                    \
   CM_LAUNCH((cm::k_att_fused<HD, PB, SL>), dim3(grid), dim3(cm::att_nt(HD)), lds, s, qsrc, nh, nkv, rope_dim,    \
@@ -975,10 +983,11 @@ void decode_attention(camelid_hip_engine* e, uint32_t l, const float* cos_base, 
                            scale, e->att, e->xq, e->xs, pf, e->att_dg, op);
 }
 
-// Tagged activation words of the attention's output projection: K / 4 quant words, K / 32 scales.
+// Tagged activation words of the attention's output projection: K / 4 quant words and K / 32
+// scales (Q8_0 W_o), or K f32 values (Q4_K W_o).
 size_t ao_words(const camelid_hip_engine* e) {
   const size_t nq = (size_t)e->d.n_heads * e->d.head_dim;
-  return nq / 4 + nq / 32 + 1;
+  return std::max(nq / 4 + nq / 32 + 1, nq);
 }
 
 // Whether the Q8_0 decode layers compute the output projection inside the single-workgroup
@@ -999,6 +1008,38 @@ bool ao_enabled(camelid_hip_engine* e) {
     e->ao_state = ok ? 1 : 0;
   }
   return e->ao_state == 1;
+}
+
+// Whether the K-quant decode layers compute a Q4_K output projection inside the one-launch
+// split attention (cm::att_oproj_q4k; CAMELID_HIP_ATT_O=0 turns it off): every layer must be a
+// K-quant layer whose W_o is Q4_K of width n_heads * head_dim = 4096 and hidden rows, with the
+// read-ahead off.  It rides only in launches where it fits the CUs (ao4_rides).
+bool ao4_enabled(camelid_hip_engine* e) {
+  if (e->ao4_state < 0) {
+    const camelid_hip_dims& d = e->d;
+    bool ok = e->att_o_fused && !e->read_ahead && d.n_layers <= 255 && e->kvs < (1u << 24) - 1 &&
+              cm::att_nt((int)d.head_dim) == cm::AO_ROWS * 64 && cm::aoq_width_ok((int)(d.n_heads * d.head_dim)) &&
+              e->ao_words != nullptr && d.n_layers > 0;
+    for (uint32_t l = 0; ok && l < d.n_layers; ++l) {
+      const LayerW& L = e->layers[l];
+      ok = L.set && L.generic && L.p[3].quant == CAMELID_Q4_K && L.p[3].kq.k == d.n_heads * d.head_dim &&
+           L.p[3].kq.rows == d.hidden;
+    }
+    e->ao4_state = ok ? 1 : 0;
+  }
+  return e->ao4_state == 1;
+}
+// The one-launch split attention takes the Q4_K projection's workgroups where they fit the CUs
+// once the score slices retire (those come first and finish long before the output sums: the
+// projection workgroups that find no free CU start then, and still have their weights in
+// registers before the attention output is ready).
+bool ao4_rides(camelid_hip_engine* e) {
+  if (!ao4_enabled(e) || !att_fused_split(e)) return false;
+  const uint32_t sl = (uint32_t)fsplit_sl(e->kvs, e->d.head_dim);
+  const uint32_t outs = e->d.n_heads * (e->d.head_dim / 32);
+  const uint32_t wgs = outs + (e->d.hidden + cm::AOQ_ROWS - 1) / cm::AOQ_ROWS;
+  (void)sl;
+  return wgs <= e->n_cus;
 }
 
 // The K-quant layer shape the norm-fused launches take: hidden 4096 (the norm workgroup's 512 x
@@ -1029,12 +1070,12 @@ bool nf_enabled(camelid_hip_engine* e) {
 // step cut short by an error leaves one set) and the handoff error word is cleared.
 // The same for the attention's output-projection counters (one per layer).
 int nf_begin(camelid_hip_engine* e) {
-  const bool nf = nf_enabled(e), ao = ao_enabled(e), fs = att_fused_split(e);
+  const bool nf = nf_enabled(e), ao = ao_enabled(e), fs = att_fused_split(e), ao4 = ao4_rides(e);
   if (fs) HIP_TRY(e, hipMemsetAsync(e->att_sct, 0, (size_t)e->d.n_heads * e->kvs * 8, e->stream));
   if (!nf && !ao && !fs) return 0;
   static const uint32_t zero = 0;
   if (nf) HIP_TRY(e, hipMemsetAsync(e->nf_slots, 0, cm::NF_WORDS * 4, e->stream));
-  if (ao) HIP_TRY(e, hipMemsetAsync(e->ao_words, 0, ao_words(e) * 8, e->stream));
+  if (ao || ao4) HIP_TRY(e, hipMemsetAsync(e->ao_words, 0, ao_words(e) * 8, e->stream));
   HIP_TRY(e, hipMemcpyToSymbolAsync(HIP_SYMBOL(cm::g_handoff_error), &zero, 4, 0, hipMemcpyHostToDevice, e->stream));
   return 0;
 }
@@ -1123,11 +1164,22 @@ void run_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cos_base,
     proj(e, L.p[2], e->qkv + nq + nkv, nullptr);
   }
   }
-  {
-    ProfScope ps(e, P_ATTN, (nq + 2.0 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0));
-    decode_attention(e, l, cos_base, sin_base, rope_stride, scale, ahead(L.p[3]));
+  const double att_bytes = (nq + 2.0 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0);
+  if (att_split(e) && ao4_rides(e)) {
+    // the Q4_K output projection's workgroups ride in the split attention launch
+    ProfScope ps(e, P_ATTN, att_bytes + kq_bytes(L.p[3].kq, true));
+    cm::OProj op{nullptr, nullptr, (int)L.p[3].kq.rows, (int)L.p[3].kq.k, e->h, e->h, nullptr, nullptr, (int)l};
+    op.k4nib = L.p[3].kq.a;
+    op.k4hdr = L.p[3].kq.b;
+    op.xf_t = e->ao_words;
+    decode_attention(e, l, cos_base, sin_base, rope_stride, scale, cm::Prefetch{nullptr, 0, nullptr, 0}, op);
+  } else {
+    {
+      ProfScope ps(e, P_ATTN, att_bytes);
+      decode_attention(e, l, cos_base, sin_base, rope_stride, scale, ahead(L.p[3]));
+    }
+    proj(e, L.p[3], e->h, e->h, is_k(3) ? e->att : nullptr);
   }
-  proj(e, L.p[3], e->h, e->h, is_k(3) ? e->att : nullptr);
   if (nf) {
     // the FFN RMSNorm inside the gate|up launch (workgroup 0), flag slot 1
     const KMat& gu = L.p[4].kq;
@@ -1779,7 +1831,7 @@ void camelid_hip_engine_free(camelid_hip_engine* e) {
 int camelid_hip_set_layer(camelid_hip_engine* e, uint32_t layer, const uint8_t* const w[7], const size_t len[7],
                           const uint8_t quant[7], uint8_t q8_layout, const float* attn_norm, const float* ffn_norm,
                           const float* q_norm, const float* k_norm) {
-  if (e) e->nf_state = e->ao_state = -1;  // (the fused-launch decisions are taken again for the new weights)
+  if (e) e->nf_state = e->ao_state = e->ao4_state = -1;  // (the fused-launch decisions are taken again for the new weights)
   if (!e) return fail(nullptr, "null engine");
   if (layer >= e->d.n_layers) return fail(e, "layer index out of range");
   if (!w || !len || !quant || !attn_norm || !ffn_norm) return fail(e, "null argument");

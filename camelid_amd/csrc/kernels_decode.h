@@ -66,6 +66,13 @@ __device__ __forceinline__ uint16_t ld_stream(const uint16_t* p) {
   return *p;
 #endif
 }
+__device__ __forceinline__ uint32_t ld_stream(const uint32_t* p) {
+#if CM_STREAM_LOADS
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
 
 // Agent-scope (device-coherent across XCDs) loads and stores for data handed between the
 // workgroups of one launch: they bypass the XCD-private L2 copies that plain accesses may hit.
@@ -2130,7 +2137,7 @@ __device__ uint64_t g_ao_stamps[64 * 2 * AO_NSTAMP];
 #define CM_AO_STAMP(i)
 #endif
 struct OProj {
-  const int8_t* q;      // W_o quants [rows][K] (null: no projection in this launch)
+  const int8_t* q;      // W_o quants [rows][K] (null: no Q8_0 projection in this launch)
   const uint16_t* d;    // W_o f16 block scales [rows][K / 32]
   int rows, K;          // K = n_heads * head_dim
   float* y;             // y[r] = resid[r] + (W_o att)[r]
@@ -2138,6 +2145,11 @@ struct OProj {
   uint64_t* xq_t;       // [K / 4] tagged quant words
   uint64_t* xs_t;       // [K / 32] tagged block scales
   int layer;
+  // a Q4_K W_o instead (k_att_fused only; q null): its nibble and header planes, and the
+  // attention output as [K] tagged f32 words, quantized to Q8_K by the projection workgroups
+  const uint8_t* k4nib = nullptr;
+  const uint8_t* k4hdr = nullptr;
+  uint64_t* xf_t = nullptr;
 };
 __host__ __device__ constexpr uint32_t ao_tag(uint32_t pos, uint32_t layer) { return ((pos + 1u) << 8) | layer; }
 __host__ __device__ constexpr size_t ao_lds_bytes(int K) {
@@ -3109,6 +3121,8 @@ __device__ __forceinline__ void att_out_body(
   if (tid < DW) {
     const size_t o = (size_t)h * HD + d;
     att_out[o] = acc;
+    if (TAG && op.xf_t)  // the f32 value, tagged, for the Q4_K projection's workgroups of this launch
+      st_agent64(op.xf_t + o, ((uint64_t)tag << 32) | __float_as_uint(acc));
     int8_t q;
     const float dd = quantize_lane32(acc, &q);
     if (TAG && op.q) {  // for the output projection's workgroups of this launch (as k_attention)
@@ -3143,6 +3157,10 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
                               n_slices_pos, att_out, xq, xs, ring_slots, nullptr, nullptr, OProj{});
 }
 
+// The Q4_K output projection's workgroups of k_att_fused (defined with the K-quant kernels).
+template <int NT>
+__device__ __forceinline__ void att_oproj_q4k(const OProj& op, int wg, uint32_t tag);
+
 // ---------------------------------------------------------------------------
 // The split decode attention in one launch (no round trip of the scores through a launch
 // boundary): workgroups [0, n_heads * n_slices) are score slices of SL positions (slice s of
@@ -3175,6 +3193,10 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_fused(
       const int pos = (int)*d_pos;
       if (kv_pos_bad(pos, kvs)) return;
       att_oproj<NT>(op, b - nsw - now, ao_tag((uint32_t)pos, (uint32_t)layer), reinterpret_cast<unsigned char*>(dyn));
+    } else if (op.k4nib) {
+      const int pos = (int)*d_pos;
+      if (kv_pos_bad(pos, kvs)) return;
+      att_oproj_q4k<NT>(op, b - nsw - now, ao_tag((uint32_t)pos, (uint32_t)layer));
     }
   }
 }

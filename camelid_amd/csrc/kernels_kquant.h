@@ -126,13 +126,32 @@ __host__ __device__ inline size_t kq4_lds_bytes(int K, int R) {
   return kq4_terms_offset(K) + (size_t)R * (K / 256) * 16;
 }
 
-template <int IT, int RPW, int NT = KQ_NT, bool XF = false>
+// TAGF (with XF): the f32 activation arrives as [K] tagged words from other workgroups of the
+// launch (xf_t, ao_tag in the high half, agent-scope): the waves wait for their blocks' words
+// instead of loading xf, then quantize as with XF.
+// HQ: lane j of a superblock's 8 lanes loads only dword j % 4 of the 16-byte header, and each
+// 4-lane quad rebuilds the whole header with DPP broadcasts where it is used (5 instead of 8
+// registers per row and piece).
+template <int IT, int RPW, int NT = KQ_NT, bool XF = false, bool TAGF = false, bool HQ = false>
 __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __restrict__ nib, const uint8_t* __restrict__ hdr,
                                                     int rows, int K, const float* __restrict__ yd,
                                                     const int8_t* __restrict__ yq, const int32_t* __restrict__ ybs,
                                                     float* y, const float* resid, float* __restrict__ part_v,
                                                     uint32_t* __restrict__ part_i, const float* __restrict__ xf,
-                                                    const uint32_t* ready = nullptr, int sk = -1) {
+                                                    const uint32_t* ready = nullptr, int sk = -1,
+                                                    const uint64_t* xf_t = nullptr, uint32_t tag = 0,
+                                                    int ao_layer = -1) {
+  static_assert(!TAGF || XF, "tagged f32 words are an f32 activation");
+  (void)ao_layer;  // (the measurement build: TAGF phase stamps of the first and last workgroup, g_ao_stamps)
+#ifdef CM_STAMPS
+#define CM_AOQ_STAMP(i)                                                                                        \
+  if (TAGF && threadIdx.x == 0 && ao_layer >= 0 && ao_layer < 64 &&                                           \
+      (bid == 0 || bid == (int)gridDim.x - 1 - ((int)blockIdx.x - bid)))                                      \
+    g_ao_stamps[((size_t)ao_layer * 2 + (bid != 0)) * AO_NSTAMP + (i)] = __builtin_amdgcn_s_memrealtime();
+#else
+#define CM_AOQ_STAMP(i)
+#endif
+  CM_AOQ_STAMP(0)
   (void)sk;  // (the measurement build's stamp kind)
   constexpr int R = (NT / 64) * RPW;
   static_assert(R <= 64, "one lane per row folds the terms");
@@ -149,7 +168,7 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
   // loads behind them (loads complete in issue order for the wait counter)
   constexpr int NW = NT / 64, PB = 4;
   float4 pre[XF ? PB : 1];
-  if constexpr (XF) {
+  if constexpr (XF && !TAGF) {
 #pragma unroll
     for (int u = 0; u < PB; ++u) {
       const int b = wave + NW * u;
@@ -158,7 +177,8 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
   }
   // every weight and header load of this wave next (pieces lane + 64 i of each row; past
   // NC clamped, their results never stored)
-  uint4 wv[RPW][IT], hv[RPW][IT];
+  uint4 wv[RPW][IT], hv[HQ ? 1 : RPW][HQ ? 1 : IT];
+  uint32_t hw[HQ ? RPW : 1][HQ ? IT : 1];
 #pragma unroll
   for (int k = 0; k < RPW; ++k) {
     const int row = min(row0 + wave * RPW + k, rows - 1);
@@ -168,7 +188,10 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
     for (int i = 0; i < IT; ++i) {
       const int cc = min(lane + 64 * i, NC - 1);
       wv[k][i] = ld_stream(np + cc);
-      hv[k][i] = ld_stream(hp + (cc >> 3));
+      if constexpr (HQ)
+        hw[k][i] = ld_stream(reinterpret_cast<const uint32_t*>(hp + (cc >> 3)) + (lane & 3));
+      else
+        hv[k][i] = ld_stream(hp + (cc >> 3));
     }
   }
   if (ready) {  // the activation published by workgroup 0 of this launch (agent-scope loads)
@@ -178,6 +201,24 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
     for (int i = tid; i < NC; i += NT) xbs[i] = (int)ld_agent32(ybs + i);
     if (sk >= 0) {
       CM_GEMV_STAMP_SAMPLED(sk, 3, 0)
+    }
+  } else if constexpr (TAGF) {  // the f32 activation as tagged words: one watcher, then every lane its own
+    if (threadIdx.x == 0) (void)ao_wait_word(xf_t + (blockIdx.x * 97u) % (uint32_t)K, tag);
+    __syncthreads();
+    CM_AOQ_STAMP(1)
+    for (int b = wave; b < NSB; b += NW) {
+      // the lane's four words in one round trip (issued together), then a poll of any whose
+      // tag is not there yet
+      const uint64_t* wp = xf_t + 256 * b + 4 * lane;
+      uint64_t v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = ld_agent64(wp + u);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if ((uint32_t)(v[u] >> 32) != tag) v[u] = ao_wait_word(wp + u, tag);
+      const float4 f = make_float4(__uint_as_float((uint32_t)v[0]), __uint_as_float((uint32_t)v[1]),
+                                   __uint_as_float((uint32_t)v[2]), __uint_as_float((uint32_t)v[3]));
+      quantize_q8k_wave_vals(f, xq + 256 * b, xbs + 8 * b, xd + b);
     }
   } else if constexpr (XF) {  // the activation given in f32: each wave quantizes blocks wave, wave + NW, ... to Q8_K
 #pragma unroll
@@ -193,6 +234,7 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
     for (int i = tid; i < NC; i += NT) xbs[i] = ybs[i];
   }
   __syncthreads();
+  CM_AOQ_STAMP(2)
   const uint32_t K1 = 0x3f3f3f3fu, K2 = 0x0f0f0f0fu, K3 = 0x03030303u;
 #pragma unroll
   for (int k = 0; k < RPW; ++k) {
@@ -203,7 +245,17 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
       const int c = lane + 64 * i;
       const bool valid = c < NC;  // uniform per 8-lane superblock group (NC % 8 == 0)
       const int cc = min(c, NC - 1);
-      const uint4 w = wv[k][i], hd = hv[k][i];
+      const uint4 w = wv[k][i];
+      uint4 hd;
+      if constexpr (HQ) {  // quad_perm broadcasts of lanes 0..3 of this lane's quad (whole quads clamp alike)
+        const int hq = (int)hw[k][i];
+        hd = make_uint4((uint32_t)__builtin_amdgcn_update_dpp(0, hq, 0x00, 0xf, 0xf, false),
+                        (uint32_t)__builtin_amdgcn_update_dpp(0, hq, 0x55, 0xf, 0xf, false),
+                        (uint32_t)__builtin_amdgcn_update_dpp(0, hq, 0xaa, 0xf, 0xf, false),
+                        (uint32_t)__builtin_amdgcn_update_dpp(0, hq, 0xff, 0xf, 0xf, false));
+      } else {
+        hd = hv[k][i];
+      }
       const int s = cc >> 3, j = cc & 7, c4 = j >> 1, h = j & 1;
       const uint32_t scw = (c4 < 2) ? (hd.y & K1) : ((hd.w & K2) | (((hd.y >> 6) & K3) << 4));
       const uint32_t mnw = (j < 4) ? (hd.z & K1) : (((hd.w >> 4) & K2) | (((hd.z >> 6) & K3) << 4));
@@ -228,7 +280,7 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
         const float ydv = xd[s];
         const float dw = half_bits_to_float((uint16_t)(hd.x & 0xffffu));
         const float dmw = half_bits_to_float((uint16_t)(hd.x >> 16));
-        terms[rl * NSB + s] = make_float4(-(ydv * dmw), (float)prod, ydv * dw, (float)sumi);
+        terms[s * R + rl] = make_float4(-(ydv * dmw), (float)prod, ydv * dw, (float)sumi);
       }
     }
   }
@@ -236,9 +288,9 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
   if (tid < 64) {
     float acc = 0.0f;
     if (tid < R) {
-      const float4* t = terms + tid * NSB;
+      const float4* t = terms + tid;  // superblock-major: the fold lanes read consecutive entries
       for (int s = 0; s < NSB; ++s) {
-        const float4 v = t[s];
+        const float4 v = t[s * R];
         acc = fmaf(v.x, v.y, acc);
         acc = fmaf(v.z, v.w, acc);
       }
@@ -246,6 +298,7 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
     const int row = row0 + tid;
     const bool live = tid < R && row < rows;
     if (live) y[row] = resid ? resid[row] + acc : acc;
+    CM_AOQ_STAMP(3)
     if (part_v) {  // lm_head: this workgroup's argmax partial (first index of the max)
       float bv = live ? acc : -INFINITY;
       uint32_t bi = live ? (uint32_t)row : 0xffffffffu;
@@ -260,6 +313,7 @@ __device__ __forceinline__ void gemv_q4k_body(const int bid, const uint8_t* __re
     CM_GEMV_STAMP_SAMPLED(sk, 5, 0)
   }
 }
+#undef CM_AOQ_STAMP
 
 // XF: the activation comes as f32 in xf (quantized by the workgroup), else as Q8_K in yd/yq/ybs
 // (a separate instantiation: the f32 path's registers would lower every launch's occupancy).
@@ -432,6 +486,23 @@ __device__ __forceinline__ void gemv_q6k_body(const int bid, const uint8_t* __re
   if (sk >= 0) {
     CM_GEMV_STAMP_SAMPLED(sk, 5, 0)
   }
+}
+
+// The Q4_K output projection inside the split decode attention launch (k_att_fused): 32 rows
+// per 1024-thread workgroup (2 per wave), their weight loads issued as the workgroup starts (at
+// the launch's start on the CUs the attention leaves free, the rest as the score slices retire);
+// the attention output is read as tagged f32 words as the output workgroups store them,
+// quantized to Q8_K by the workgroup (one wave per 256-value block) and dotted exactly as by
+// k_gemv_q4k<IT, RPW, true> on the f32 activation: the same bits.  y = resid + W_o att.
+constexpr int AOQ_RPW = 2;
+constexpr int AOQ_ROWS = AOQ_RPW * 16;  // rows per projection workgroup
+__host__ __device__ constexpr bool aoq_width_ok(int K) { return K == 4096; }
+template <int NT>
+__device__ __forceinline__ void att_oproj_q4k(const OProj& op, int wg, uint32_t tag) {
+  static_assert(NT == 1024, "sixteen waves, AOQ_RPW rows each");
+  gemv_q4k_body<2, AOQ_RPW, NT, true, true, true>(wg, op.k4nib, op.k4hdr, op.rows, op.K, nullptr, nullptr, nullptr,
+                                                  op.y, op.resid, nullptr, nullptr, nullptr, nullptr, -1, op.xf_t,
+                                                  tag, op.layer);
 }
 
 template <int RPW>
