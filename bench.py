@@ -519,7 +519,8 @@ def main() -> int:
         kname = ("Q8_0 GEMV: k_gemv_norm (RMSNorm + qkv) + k_gemv_k (down + residual) + k_gemv_gu_silu "
                  "(RMSNorm + gate/up + SwiGLU + Q8_0) + k_gemv_argmax (lm_head); the o projection runs inside the "
                  "attention launch (k_attention / k_att_fused) and is counted with it" if cfg.quant_scheme == "q8_0"
-                 else "K-quant GEMV: k_gemv_q4k + k_gemv_q6k (incl. lm_head)")
+                 else "K-quant GEMV: k_gemv_q4k + k_gemv_q6k (incl. lm_head); from the split attention's first "
+                 "position on, the Q4_K o projection runs inside that launch (k_att_fused) and is counted with it")
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get(cfg.name),
                     "traffic_source": TRAFFIC_SOURCE if cfg.name in TRAFFIC else None,
@@ -527,7 +528,7 @@ def main() -> int:
                     "avg_launch_us": round(g["ms"] * 1e3 / max(g["launches"], 1), 3),
                     "launches": g["launches"]}
         # the costliest single launch per step: the decode attention (with the o projection's
-        # workgroups on the Q8_0 path), reported against the same HBM peak; its time is set by
+        # workgroups where they ride in it), reported against the same HBM peak; its time is set by
         # the CPU-order serial f32 chains (scores, softmax denominator, output sums), not by bytes
         a = prof["attention"]
         if a["launches"]:
@@ -536,8 +537,10 @@ def main() -> int:
                 "bound": "hbm", "achieved": round(att_achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(att_achieved / HBM_PEAK_GBS, 4),
                 "kernel": ("decode attention + o projection (k_attention / k_att_fused with the W_o workgroups)"
-                           if cfg.quant_scheme == "q8_0" else "decode attention (k_attention / k_att_fused)")
-                + ": K/V read and written, q/k/v in, output and (Q8_0) W_o + residual bytes / summed dispatch durations",
+                           if cfg.quant_scheme == "q8_0" else
+                           "decode attention (k_attention; k_att_fused with the Q4_K W_o workgroups)")
+                + ": K/V read and written, q/k/v in, output and (where its workgroups ride in the launch) W_o + "
+                  "residual bytes / summed dispatch durations",
                 "avg_launch_us": round(a["ms"] * 1e3 / a["launches"], 3), "launches": a["launches"],
                 "share_of_step": round(a["ms"] / (sum(v["ms"] for v in prof.values()) or 1.0), 4),
                 "note": "latency-bound: the in-order f32 chains the CPU reference fixes, not HBM bytes"}
