@@ -657,27 +657,34 @@ void launch_attention_split(uint32_t hd, uint32_t n_heads, int slots, hipStream_
                             int nkv, int rope_dim, int split_half, const float* cb, const float* sb, int rs,
                             const float* qn, const float* kn, float eps, uint16_t* kc, uint16_t* vc, int layer,
                             int kvs, const uint32_t* pos, float scale, float* g_sc, float* g_mx, float* att,
-                            int8_t* xq, float* xs, cm::Prefetch pf) {
+                            int8_t* xq, float* xs, cm::Prefetch pf, cm::OProj op = cm::OProj{}) {
   const size_t lds = (size_t)slots * cm::ATT_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs);
   const int nsl = (kvs + ATT_SLICE - 1) / ATT_SLICE;
+  constexpr int AOR = cm::AO_ROWS * cm::AO_SPLIT_RPW;  // rows per projection workgroup
+  if (op.q && (cm::att_nt((int)hd) != cm::AO_ROWS * 64 || !cm::ao_width_ok(op.K) || op.K != (int)(n_heads * hd))) {
+    g_launch_error = "split attention: no output projection body for this shape";
+    return;
+  }
 #define CM_ATTS(HD)                                                                                                \
   {                                                                                                                \
     CM_LAUNCH((cm::k_att_scores<HD, FUSED, (HD > ATT_SLICE ? HD : ATT_SLICE)>), dim3(n_heads, nsl),               \
               dim3(HD > ATT_SLICE ? HD : ATT_SLICE), 0, s, qsrc, nh, nkv, rope_dim, split_half, cb, sb, rs, qn, kn, \
               eps, kc, vc, layer, kvs, pos, scale, g_sc, g_mx);                                                   \
-    const uint32_t grid = n_heads * (HD / 32) + (pf.a_lines ? PREFETCH_WGS : 0);                                  \
+    const uint32_t grid = n_heads * (HD / 32) +                                                                    \
+                          (op.q ? (uint32_t)(op.rows + AOR - 1) / AOR : (pf.a_lines ? PREFETCH_WGS : 0));           \
     int pb = 0;                                                                                                    \
     const int so = attn_out_slots((uint32_t)kvs, slots, &pb);                                                      \
-    const size_t lds_o = (size_t)so * cm::AO_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs) + cm::avp_bytes(pb); \
+    size_t lds_o = (size_t)so * cm::AO_RING_GRANULES * 16 + attn_sc_bytes((uint32_t)kvs) + cm::avp_bytes(pb);     \
+    if (op.q) lds_o = std::max(lds_o, cm::ao_lds_bytes(op.K, AOR));                                               \
     if (pb == 256)                                                                                                 \
       CM_LAUNCH((cm::k_att_out<HD, 256>), dim3(grid), dim3(cm::att_nt(HD)), lds_o, s, vc, nh, nkv, layer, kvs, pos, \
-                g_sc, g_mx, nsl, (HD > ATT_SLICE ? HD : ATT_SLICE), att, xq, xs, so, pf);                          \
+                g_sc, g_mx, nsl, (HD > ATT_SLICE ? HD : ATT_SLICE), att, xq, xs, so, pf, op);                      \
     else if (pb == 128)                                                                                            \
       CM_LAUNCH((cm::k_att_out<HD, 128>), dim3(grid), dim3(cm::att_nt(HD)), lds_o, s, vc, nh, nkv, layer, kvs, pos, \
-                g_sc, g_mx, nsl, (HD > ATT_SLICE ? HD : ATT_SLICE), att, xq, xs, so, pf);                          \
+                g_sc, g_mx, nsl, (HD > ATT_SLICE ? HD : ATT_SLICE), att, xq, xs, so, pf, op);                      \
     else                                                                                                           \
       CM_LAUNCH((cm::k_att_out<HD, 64>), dim3(grid), dim3(cm::att_nt(HD)), lds_o, s, vc, nh, nkv, layer, kvs, pos,  \
-                g_sc, g_mx, nsl, (HD > ATT_SLICE ? HD : ATT_SLICE), att, xq, xs, so, pf);                          \
+                g_sc, g_mx, nsl, (HD > ATT_SLICE ? HD : ATT_SLICE), att, xq, xs, so, pf, op);                      \
   }
   if (hd == 64) CM_ATTS(64)
   else if (hd == 128) CM_ATTS(128)
@@ -975,7 +982,7 @@ void decode_attention(camelid_hip_engine* e, uint32_t l, const float* cos_base, 
     launch_attention_split<true>(d.head_dim, d.n_heads, e->att_slots, e->stream, e->qkv, (int)d.n_heads,
                                  (int)d.n_kv_heads, (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base,
                                  rope_stride, L.q_norm, L.k_norm, d.eps, e->kc, e->vc, (int)l, (int)e->kvs,
-                                 &e->st->pos, scale, e->att_sc, e->att_mx, e->att, e->xq, e->xs, pf);
+                                 &e->st->pos, scale, e->att_sc, e->att_mx, e->att, e->xq, e->xs, pf, op);
   else
     launch_attention<true>(d.head_dim, d.n_heads, e->att_slots, e->stream, e->qkv, (int)d.n_heads,
                            (int)d.n_kv_heads, (int)d.rope_dim, (int)d.split_half_pairing, cos_base, sin_base,
@@ -1008,6 +1015,13 @@ bool ao_enabled(camelid_hip_engine* e) {
     e->ao_state = ok ? 1 : 0;
   }
   return e->ao_state == 1;
+}
+
+// The two-launch split attention takes the Q8_0 output projection's workgroups in its output
+// launch where they fit beside the output workgroups (cm::k_att_out, AO_SPLIT_RPW rows per wave).
+bool ao_split_fits(camelid_hip_engine* e) {
+  const uint32_t aor = (uint32_t)(cm::AO_ROWS * cm::AO_SPLIT_RPW);
+  return ao_enabled(e) && e->d.n_heads * (e->d.head_dim / 32) + (e->d.hidden + aor - 1) / aor <= e->n_cus;
 }
 
 // Whether the K-quant decode layers compute a Q4_K output projection inside the one-launch
@@ -1239,7 +1253,7 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const f
     gemv(e, L.qkv, e->qkv, nullptr);
   }
   const double att_bytes = (nq + 2 * nkv) * 4 + 2.0 * nkv * 2 * (e->cur_pos + 1) + nq * (4 + 34.0 / 32.0);
-  if (ao_enabled(e) && (!att_split(e) || att_fused_split(e))) {
+  if (ao_enabled(e) && (!att_split(e) || att_fused_split(e) || ao_split_fits(e))) {
     // the output projection's workgroups ride in the attention launch (attention + W_o bytes)
     ProfScope ps(e, P_ATTN, att_bytes + q8_bytes(L.o, true));
     const size_t nqw = (size_t)d.n_heads * d.head_dim / 4;

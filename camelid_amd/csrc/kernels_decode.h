@@ -2125,6 +2125,10 @@ __device__ __forceinline__ float att_onepass_sum(const float* v, int P, FsLds<NT
 // call every (position, layer) is computed once.  The wait is bounded: past about 2^18 polls
 // per word the workgroup sets g_handoff_error and computes from whatever it read.
 constexpr int AO_ROWS = 16;  // rows per projection workgroup (one per wave)
+// rows per wave of the projection workgroups in the split output launch (k_att_out), which
+// take the CUs its 32-dim output workgroups leave free: 2, so that a [4096 x 4096] W_o fits
+// 128 workgroups beside the 128 output workgroups of 32 heads of 128
+constexpr int AO_SPLIT_RPW = 2;
 // (measurement build: thread 0 of the first and the last projection workgroup of layer l
 // records 0 start, 1 watched word tagged, 2 activation staged, 3 end into g_ao_stamps[l][0|1])
 constexpr int AO_NSTAMP = 4;
@@ -2152,8 +2156,8 @@ struct OProj {
   uint64_t* xf_t = nullptr;
 };
 __host__ __device__ constexpr uint32_t ao_tag(uint32_t pos, uint32_t layer) { return ((pos + 1u) << 8) | layer; }
-__host__ __device__ constexpr size_t ao_lds_bytes(int K) {
-  return (size_t)K + (size_t)(K / 32) * 4 + (size_t)AO_ROWS * gemv_term_stride(K / 32) * 4;
+__host__ __device__ constexpr size_t ao_lds_bytes(int K, int rows = AO_ROWS) {
+  return (size_t)K + (size_t)(K / 32) * 4 + (size_t)rows * gemv_term_stride(K / 32) * 4;
 }
 
 __device__ __forceinline__ uint64_t ao_wait_word(const uint64_t* p, uint32_t tag) {
@@ -2170,29 +2174,32 @@ __device__ __forceinline__ uint64_t ao_wait_word(const uint64_t* p, uint32_t tag
   return v;
 }
 
-template <int K, int NT>
+// RPW rows per wave (AO_ROWS * RPW per workgroup).
+template <int K, int NT, int RPW = 1>
 __device__ __forceinline__ void att_oproj_rows(const OProj& op, int wg, uint32_t tag, unsigned char* smem) {
   constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64, STRIDE = gemv_term_stride(NB);
-  static_assert(NT / 64 == AO_ROWS && K % 128 == 0, "one row per wave, whole 128-value groups");
+  constexpr int R = AO_ROWS * RPW;
+  static_assert(NT / 64 == AO_ROWS && K % 128 == 0, "sixteen waves, whole 128-value groups");
   uint32_t* xl = reinterpret_cast<uint32_t*>(smem);
   float* xsl = reinterpret_cast<float*>(smem + K);
   float* t = xsl + NB;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int row0 = wg * AO_ROWS;
+  const int row0 = wg * R;
   CM_AO_STAMP(0)
-  // this wave's row: every weight and scale load first (rows past the end clamped; their
+  // this wave's rows: every weight and scale load first (rows past the end clamped; their
   // results are never stored)
-  int4 wv[IT];
-  uint16_t dv[IT];
-  {
-    const int row = min(row0 + wave, op.rows - 1);
+  int4 wv[RPW][IT];
+  uint16_t dv[RPW][IT];
+#pragma unroll
+  for (int k = 0; k < RPW; ++k) {
+    const int row = min(row0 + wave * RPW + k, op.rows - 1);
     const int4* w4 = reinterpret_cast<const int4*>(op.q + (size_t)row * K);
     const uint16_t* dp = op.d + (size_t)row * NB;
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int c = min(lane + 64 * i, CPR - 1);
-      wv[i] = ld_stream(w4 + c);
-      dv[i] = ld_stream(dp + (c >> 1));
+      wv[k][i] = ld_stream(w4 + c);
+      dv[k][i] = ld_stream(dp + (c >> 1));
     }
   }
   // one watcher until a scale word carries the tag (the heads finish together), then every
@@ -2208,18 +2215,21 @@ __device__ __forceinline__ void att_oproj_rows(const OProj& op, int wg, uint32_t
   }
   __syncthreads();
   CM_AO_STAMP(2)
-  float* tr = t + wave * STRIDE;
 #pragma unroll
-  for (int i = 0; i < IT; ++i) {
-    __builtin_amdgcn_sched_barrier(0);
-    const int c = lane + 64 * i;
-    const int cc = min(c, CPR - 1);
-    int s = dot4x4(wv[i], reinterpret_cast<const int4*>(xl)[cc], 0);
-    s += dpp_xor1(s);
-    if ((lane & 1) == 0 && c < CPR) tr[c >> 1] = ((float)s * half_bits_to_float(dv[i])) * xsl[c >> 1];
+  for (int k = 0; k < RPW; ++k) {
+    float* tr = t + (wave * RPW + k) * STRIDE;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int c = lane + 64 * i;
+      const int cc = min(c, CPR - 1);
+      int s = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
+      s += dpp_xor1(s);
+      if ((lane & 1) == 0 && c < CPR) tr[c >> 1] = ((float)s * half_bits_to_float(dv[k][i])) * xsl[c >> 1];
+    }
   }
   __syncthreads();
-  if (tid < AO_ROWS && row0 + tid < op.rows) {
+  if (tid < R && row0 + tid < op.rows) {
     const float acc = fold_lds_n<NB>(t + tid * STRIDE);
     op.y[row0 + tid] = op.resid[row0 + tid] + acc;
   }
@@ -2229,17 +2239,17 @@ __device__ __forceinline__ void att_oproj_rows(const OProj& op, int wg, uint32_t
 // The attention's widths n_heads * head_dim with an instantiated projection body.
 __host__ __device__ constexpr bool ao_width_ok(int K) { return K == 2048 || K == 3072 || K == 4096; }
 
-template <int NT>
+template <int NT, int RPW = 1>
 __device__ __forceinline__ void att_oproj(const OProj& op, int wg, uint32_t tag, unsigned char* smem) {
   switch (op.K) {
     case 2048:
-      att_oproj_rows<2048, NT>(op, wg, tag, smem);
+      att_oproj_rows<2048, NT, RPW>(op, wg, tag, smem);
       break;
     case 3072:
-      att_oproj_rows<3072, NT>(op, wg, tag, smem);
+      att_oproj_rows<3072, NT, RPW>(op, wg, tag, smem);
       break;
     case 4096:
-      att_oproj_rows<4096, NT>(op, wg, tag, smem);
+      att_oproj_rows<4096, NT, RPW>(op, wg, tag, smem);
       break;
     default:
       break;
@@ -2896,7 +2906,7 @@ __device__ __forceinline__ void att_out_body(
   if (kv_pos_bad(pos, kvs)) return;  // (uniform, before any barrier)
   const int P = pos + 1;
   const int d = w * DW + tid;  // output lanes: tid < DW
-  const uint32_t tag = TAG ? ao_tag((uint32_t)pos, (uint32_t)layer) : 0u;
+  const uint32_t tag = (TAG || op.q) ? ao_tag((uint32_t)pos, (uint32_t)layer) : 0u;
   // this position's V value of output lane d (TAG: from the projection's output, rounded to
   // f16 as the cache row that a score workgroup of this launch stores)
   auto v_pos = [&]() -> uint16_t {
@@ -3125,7 +3135,7 @@ __device__ __forceinline__ void att_out_body(
       st_agent64(op.xf_t + o, ((uint64_t)tag << 32) | __float_as_uint(acc));
     int8_t q;
     const float dd = quantize_lane32(acc, &q);
-    if (TAG && op.q) {  // for the output projection's workgroups of this launch (as k_attention)
+    if (op.q) {  // for the output projection's workgroups of this launch (as k_attention)
       const uint64_t tg = (uint64_t)tag << 32;
       const uint32_t b = (uint32_t)(uint8_t)q;
       const uint32_t wq = b | ((uint32_t)__shfl_down((int)b, 1) << 8) | ((uint32_t)__shfl_down((int)b, 2) << 16) |
@@ -3145,16 +3155,26 @@ __global__ __launch_bounds__(att_nt(HD)) void k_att_out(
     const uint16_t* __restrict__ vc, int n_heads, int n_kv, int layer, int kvs, const uint32_t* __restrict__ d_pos,
     const float* __restrict__ g_sc, const float* __restrict__ g_max, int n_slices, int n_slices_pos,
     float* __restrict__ att_out,
-    int8_t* __restrict__ xq, float* __restrict__ xs, int ring_slots, Prefetch pf) {
+    int8_t* __restrict__ xq, float* __restrict__ xs, int ring_slots, Prefetch pf, OProj op) {
   const int nwork = n_heads * (HD / 32);
-  if ((int)blockIdx.x >= nwork) {  // spare workgroups: read ahead the output projection
+  if ((int)blockIdx.x >= nwork) {
     extern __shared__ __align__(16) float4 dyn[];
+    if constexpr (att_nt(HD) == AO_ROWS * 64) {
+      if (op.q) {  // the output projection's workgroups (AO_SPLIT_RPW rows per wave)
+        const int pos = (int)*d_pos;
+        if (kv_pos_bad(pos, kvs)) return;
+        att_oproj<att_nt(HD), AO_SPLIT_RPW>(op, (int)blockIdx.x - nwork, ao_tag((uint32_t)pos, (uint32_t)layer),
+                                            reinterpret_cast<unsigned char*>(dyn));
+        return;
+      }
+    }
+    // spare workgroups: read ahead the output projection
     prefetch_lines(pf, blockIdx.x - nwork, gridDim.x - nwork,
                    reinterpret_cast<float*>(dyn + (size_t)ring_slots * AO_RING_GRANULES));
     return;
   }
   att_out_body<HD, PB, false>((int)blockIdx.x, vc, n_heads, n_kv, layer, kvs, d_pos, g_sc, g_max, n_slices,
-                              n_slices_pos, att_out, xq, xs, ring_slots, nullptr, nullptr, OProj{});
+                              n_slices_pos, att_out, xq, xs, ring_slots, nullptr, nullptr, op);
 }
 
 // The Q4_K output projection's workgroups of k_att_fused (defined with the K-quant kernels).

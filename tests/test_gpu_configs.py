@@ -184,6 +184,43 @@ def test_split_attention_q4k_oproj_matches_oracle(monkeypatch):
         sess.close()
 
 
+def test_split_attention_q8_oproj_in_output_launch_matches_oracle(monkeypatch):
+    """At the C4 layer shape (hidden 4096 = 32 heads of 128, 8 KV heads, Q8_0), the decode
+    attention split from the first position on as two launches (scores, then output sums):
+    with the Q8_0 output projection's workgroups in the output launch (2 rows per wave, reading
+    the Q8_0 attention output as tagged words) and, with CAMELID_HIP_ATT_O=0, as a GEMV launch of
+    its own; per-layer hidden states, logits and tokens of both equal the CPU oracle's."""
+    from oracle.oracle import OracleModel
+    cfg = tiny_config(n_layers=2, hidden=4096, ffn_dim=4096, n_heads=32, n_kv_heads=8, head_dim=128, vocab=2048,
+                      rope_theta=1e6, prompt_len=12)
+    model = SyntheticModel.generate(cfg)
+    prompt = prompt_tokens(cfg)
+    orc = OracleModel(model, 32)
+    orc.prefill(prompt[:-1])
+    want = []
+    tok, pos = int(prompt[-1]), len(prompt) - 1
+    for _ in range(4):
+        tok, hid, lg = orc.forward(tok, pos, hidden=True, logits=True)
+        want.append((tok, hid, lg))
+        pos += 1
+    monkeypatch.setenv("CAMELID_HIP_ATT_SPLIT", "1")
+    monkeypatch.setenv("CAMELID_HIP_ATT_FUSED_SPLIT", "0")
+    for att_o in ("1", "0"):
+        monkeypatch.setenv("CAMELID_HIP_ATT_O", att_o)
+        sess = ResidentSession(model, 32)
+        sess.engine.capture_hidden(True)
+        sess.prefill(prompt[:-1])
+        tok, pos = int(prompt[-1]), len(prompt) - 1
+        for step, (t_o, hid_o, lg_o) in enumerate(want):
+            tok = sess.step(tok, pos, logits=True)
+            hid = sess.engine.read_hidden()
+            assert np.array_equal(hid.view(np.uint32), hid_o.view(np.uint32)), (att_o, step)
+            assert np.array_equal(sess.engine.last_logits.view(np.uint32), lg_o.view(np.uint32)), (att_o, step)
+            assert tok == t_o
+            pos += 1
+        sess.close()
+
+
 @pytest.mark.parametrize("dg",["1", "2", "4"])
 def test_attention_workgroups_per_head_match_oracle(monkeypatch, dg):
     """CAMELID_HIP_ATT_DG: the decode attention with 1, 2 or 4 workgroups per query head (each
