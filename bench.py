@@ -339,8 +339,9 @@ def attention_phases(cfg) -> dict:
         ph["workgroups"] = int(len(g))
         res[name] = {k: round(v, 3) for k, v in ph.items()}
         log(f"{name} phases (us from each workgroup's start): " + ", ".join(f"{k} {v:.3f}" for k, v in ph.items()))
-    # the Q4_K output projection's workgroups of the last split launch (first and last
-    # workgroup), from the split output workgroups' first start and last end
+    # the output projection's workgroups of the last split launch (first and last workgroup:
+    # the Q4_K ones of k_att_fused or the Q8_0 ones of k_att_out), from the split output
+    # workgroups' first start and last end
     ao = allst[na + ng + nsp:].reshape(64, 2, 4)[cfg.n_layers - 1]
     g = sp[1]
     g = g[(g[:, 0] > 0) & (g[:, 5] > 0)]
@@ -351,8 +352,8 @@ def attention_phases(cfg) -> dict:
               "staged_from_output_end": float((ao[:, 2] - a1).mean() * 0.01),
               "end_from_output_end": float((ao[:, 3] - a1).mean() * 0.01),
               "last_end_from_output_start": float((ao[:, 3].max() - a0) * 0.01)}
-        res["output_projection_q4k"] = {k: round(v, 3) for k, v in ph.items()}
-        log("Q4_K output projection workgroups, last layer (us): " +
+        res["output_projection_split"] = {k: round(v, 3) for k, v in ph.items()}
+        log("output projection workgroups of the split launch, last layer (us): " +
             ", ".join(f"{k} {v:.3f}" for k, v in ph.items()))
     return res
 
