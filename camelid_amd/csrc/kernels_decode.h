@@ -2086,8 +2086,10 @@ __device__ __forceinline__ float att_seg_sum(const float* v, uint32_t* ps, int P
 }
 
 // Softmax denominator by the one-pass exact in-order sum for ATT_FOLD_MAX <= P <= NT *
-// ATT_ONEPASS_C positions (C = P / NT rounded up to a power of two: up to 16 positions per
-// thread, 16384 at 1024 threads); below, a serial fold
+// ATT_ONEPASS_C positions (C = P / NT rounded up to the next of 1, 2, 3, 4, 6, 8, 9, 12, 16
+// positions per thread, 16384 at 1024 threads: the classification pass costs C steps per
+// thread, so a context just past a power-of-two multiple of NT does not pay for twice its
+// terms); below, a serial fold
 // by one lane is faster (measured: 2.0 us fold vs 2.9 us one-pass at P = 560).
 constexpr int ATT_ONEPASS_C = 16;
 constexpr int ATT_FOLD_MAX = 1024;
@@ -2102,8 +2104,12 @@ __device__ __forceinline__ float att_onepass_sum(const float* v, int P, FsLds<NT
   }
   if (P <= NT) CM_AOP(1)
   if (P <= NT * 2) CM_AOP(2)
+  if (P <= NT * 3) CM_AOP(3)
   if (P <= NT * 4) CM_AOP(4)
+  if (P <= NT * 6) CM_AOP(6)
   if (P <= NT * 8) CM_AOP(8)
+  if (P <= NT * 9) CM_AOP(9)
+  if (P <= NT * 12) CM_AOP(12)
   CM_AOP(16)
 #undef CM_AOP
 }

@@ -455,7 +455,8 @@ def test_rope_kv_bit_exact(native, orc, nh, nkv, hd, split, qk):
                                          (24, 8, 128, 767), (32, 4, 64, 129), (8, 8, 64, 300), (32, 8, 128, 1280),
                                          (32, 8, 128, 2100), (8, 4, 256, 700), (8, 4, 256, 40),
                                          (32, 8, 128, 5000), (32, 8, 128, 8448), (8, 4, 256, 3000),
-                                         (32, 8, 64, 12000)])
+                                         (32, 8, 64, 12000), (32, 8, 128, 4000), (32, 8, 128, 6200),
+                                         (8, 4, 128, 13000)])
 def test_attention_decode_bit_exact(native, orc, nh, nkv, hd, P):
     rng = np.random.default_rng(P + nh)
     L, layer, max_pos = 2, 1, (max(P, 2) + 3 + 7) // 8 * 8  # position stride: multiple of 8
