@@ -153,6 +153,7 @@ struct camelid_hip_engine {
   // cm::k_norm_gemv_q4k; CAMELID_HIP_KQ_NORM_FUSED): on when every layer has that shape
   bool kq_norm_fused = true;
   bool q6_gemm2 = true;  // Q6_K projections get the class-major prefill GEMM's planes (CAMELID_HIP_Q6K_GEMM2)
+  bool gu_loop = true;   // norm-fused Q8_0 gate/up: workgroups loop over row groups (CAMELID_HIP_GU_LOOP)
   int nf_state = -1;              // -1 unknown, 0 off, 1 on (every layer fusable)
   uint32_t* nf_slots = nullptr;   // the launches' flag words (cm::NF_WORDS)
   // Q8_0 layers: the output projection inside the single-workgroup attention launch
@@ -1271,16 +1272,27 @@ void run_layer(camelid_hip_engine* e, uint32_t l, const float* cos_base, const f
     ProfScope ps(e, P_GEMV, q8_bytes(L.gu, false) - L.gu.rows * 4.0 + d.ffn_dim * 34.0 / 32.0 +
                                 (gu_norm ? d.hidden * 8.0 - d.hidden * 34.0 / 32.0 : 0.0));
     const uint32_t groups = d.ffn_dim / 32;
+    // norm-fused: one 1024-thread workgroup fits a CU, so where the groups exceed the CUs one
+    // workgroup per CU takes groups b, b + CUs, ... in turn (the next group's weights streaming
+    // during the current one's fold; CAMELID_HIP_GU_LOOP=0: one group per workgroup, in rounds).
+    // Measured on the Mistral-7B shape (448 groups): 256 workgroups 253.1, 224 of two groups each
+    // 252.0, two rounds 250.8 tok/s.
+    const uint32_t ngrid = (e->gu_loop && groups > e->n_cus) ? e->n_cus : groups;
+    const bool loop = ngrid < groups;  // (the looping instantiation)
     switch (d.hidden) {
 #define CM_GU(K)                                                                                                 \
   case K:                                                                                                        \
-    if (cm::gu_norm_k(K) && gu_norm)                                                                           \
+    if (cm::gu_norm_k(K) && gu_norm && loop)                                                                    \
+      CM_LAUNCH((cm::k_gemv_gu_silu<K, cm::GN_NT, cm::gu_norm_k(K), true>), dim3(ngrid), dim3(cm::GN_NT), 0, s,  \
+                L.gu.q, L.gu.d, (const int8_t*)nullptr, (const float*)nullptr, e->h, L.ffn_norm, d.eps, e->aq,  \
+                e->as, (int)groups);                                                                           \
+    else if (cm::gu_norm_k(K) && gu_norm)                                                                      \
       CM_LAUNCH((cm::k_gemv_gu_silu<K, cm::GN_NT, cm::gu_norm_k(K)>), dim3(groups), dim3(cm::GN_NT), 0, s,       \
                 L.gu.q, L.gu.d, (const int8_t*)nullptr, (const float*)nullptr, e->h, L.ffn_norm, d.eps, e->aq,  \
-                e->as);                                                                                        \
+                e->as, (int)groups);                                                                           \
     else                                                                                                       \
       CM_LAUNCH((cm::k_gemv_gu_silu<K, cm::GU_NT, false>), dim3(groups), dim3(cm::GU_NT), 0, s, L.gu.q, L.gu.d,  \
-                e->xq, e->xs, (const float*)nullptr, (const float*)nullptr, 0.0f, e->aq, e->as);               \
+                e->xq, e->xs, (const float*)nullptr, (const float*)nullptr, 0.0f, e->aq, e->as, (int)groups);  \
     break;
       CM_GU(2048) CM_GU(3072) CM_GU(4096)
 #undef CM_GU
@@ -1779,6 +1791,7 @@ int camelid_hip_engine_new(const camelid_hip_dims* dims, camelid_hip_engine** ou
   if (const char* f = std::getenv("CAMELID_HIP_QKV_MERGED")) e->qkv_merged = std::atoi(f) != 0;
   if (const char* f = std::getenv("CAMELID_HIP_KQ_NORM_FUSED")) e->kq_norm_fused = std::atoi(f) != 0;
   if (const char* f = std::getenv("CAMELID_HIP_Q6K_GEMM2")) e->q6_gemm2 = std::atoi(f) != 0;
+  if (const char* f = std::getenv("CAMELID_HIP_GU_LOOP")) e->gu_loop = std::atoi(f) != 0;
   e->att_slots = attn_ring_slots(e->kvs);
   if (const char* f = std::getenv("CAMELID_HIP_ATT_SPLIT")) e->att_split_min = (uint32_t)std::strtoul(f, nullptr, 10);
   if (const char* f = std::getenv("CAMELID_HIP_ATT_DG")) e->att_dg = std::atoi(f);
@@ -2745,10 +2758,11 @@ int camelid_hip_gate_up_silu(const int8_t* wq, const uint16_t* wd, uint32_t ffn,
   case K:                                                                                                          \
     if (x && cm::gu_norm_k(K))                                                                                     \
       hipLaunchKernelGGL((cm::k_gemv_gu_silu<K, cm::GN_NT, cm::gu_norm_k(K)>), dim3(ffn / 32), dim3(cm::GN_NT), 0, \
-                         s, wq, wd, (const int8_t*)nullptr, (const float*)nullptr, x, nw, eps, aq, as);            \
+                         s, wq, wd, (const int8_t*)nullptr, (const float*)nullptr, x, nw, eps, aq, as,             \
+                         (int)(ffn / 32));                                                                         \
     else                                                                                                           \
       hipLaunchKernelGGL((cm::k_gemv_gu_silu<K, cm::GU_NT, false>), dim3(ffn / 32), dim3(cm::GU_NT), 0, s, wq, wd, \
-                         xq, xs, (const float*)nullptr, (const float*)nullptr, 0.0f, aq, as);                      \
+                         xq, xs, (const float*)nullptr, (const float*)nullptr, 0.0f, aq, as, (int)(ffn / 32));     \
     break;
     CM_GU(2048) CM_GU(3072) CM_GU(4096)
 #undef CM_GU

@@ -1485,11 +1485,19 @@ __host__ __device__ constexpr bool gu_norm_k(int K) { return K == 2048 || K == 3
 // NORM: the activation is the RMSNorm of x (weights nw), computed by every workgroup in its
 // prologue (norm_scale by the norm team, norm_quantize_all) instead of read quantized from
 // xq/xs.
-template <int K, int NT, bool NORM>
+// groups: the 64-row groups of the matrix (ffn / 32), one per workgroup.  LOOP: workgroup b takes
+// groups b, b + grid, ... (a grid of fewer workgroups than groups, where the groups do not all
+// fit the CUs at once): each workgroup forms the activation once and issues the next group's
+// weight loads as soon as the current group's block dots have consumed its registers, so that
+// they stream while the current group's rows are folded, instead of a second round of
+// workgroups starting behind the first one's fold tails.  (Its own instantiation: the loop's
+// live state costs registers that the one-group launches do not pay.)
+template <int K, int NT, bool NORM, bool LOOP = false>
 __global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                     const int8_t* __restrict__ xq, const float* __restrict__ xs,
                                                     const float* __restrict__ x, const float* __restrict__ nw,
-                                                    float eps, int8_t* __restrict__ aq, float* __restrict__ as) {
+                                                    float eps, int8_t* __restrict__ aq, float* __restrict__ as,
+                                                    int groups) {
   constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64;
   constexpr int RS = gemv_row_stride(GU_ROWS);  // terms block-major: t[block * RS + row]
   // row slots per wave: 8 at 512 threads; with NORM the weight waves' slots come first (up to
@@ -1509,7 +1517,11 @@ __global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ 
   __shared__ __align__(16) float wf[NORM ? GN_TEAM * CT : 4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const bool in_team = NORM && wave < GN_TEAM / 64;  // (wave-uniform) the norm team, as in k_gemv_norm
-  const size_t row0 = (size_t)blockIdx.x * GU_ROWS;
+  uint32_t g = blockIdx.x;  // this workgroup's current group
+  if constexpr (LOOP) {
+    if (g >= (uint32_t)groups) return;  // (uniform; the engine's grid has none such)
+  }
+  size_t row0 = (size_t)g * GU_ROWS;
   float nxv[NORM ? CT : 1], nwv[NORM ? CT : 1];
   __shared__ NormTeamLds<GN_TEAM> team;
   CM_GEMV_STAMP(1, 0, 0)
@@ -1563,33 +1575,44 @@ __global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ 
     for (int b = tid; b < NB; b += NT) xsl[b] = xs[b];
     __syncthreads();
   }
+  for (;;) {
 #pragma unroll
-  for (int k = 0; k < RPW; ++k) {
-    const int lr = row_of(k);
-    if (lr < 0) continue;  // (wave-uniform)
+    for (int k = 0; k < RPW; ++k) {
+      const int lr = row_of(k);
+      if (lr < 0) continue;  // (wave-uniform)
 #pragma unroll
-    for (int i = 0; i < IT; ++i) {
-      __builtin_amdgcn_sched_barrier(0);
-      const int c = lane + 64 * i;
-      const int cc = min(c, CPR - 1);
-      int sacc = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
-      sacc += dpp_xor1(sacc);
-      if ((lane & 1) == 0 && c < CPR)
-        t[(c >> 1) * RS + lr] = mul_f16_lo((float)sacc, dv[k][i]) * xsl[c >> 1];
+      for (int i = 0; i < IT; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int c = lane + 64 * i;
+        const int cc = min(c, CPR - 1);
+        int sacc = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
+        sacc += dpp_xor1(sacc);
+        if ((lane & 1) == 0 && c < CPR)
+          t[(c >> 1) * RS + lr] = mul_f16_lo((float)sacc, dv[k][i]) * xsl[c >> 1];
+      }
     }
+    CM_GEMV_STAMP(1, 4, 0)
+    // the next group's weights (every wave's slots, the team's included) go out now
+    const uint32_t gn = g + gridDim.x;
+    if (LOOP && gn < (uint32_t)groups) {
+      row0 = (size_t)gn * GU_ROWS;
+#pragma unroll
+      for (int k = 0; k < RPW; ++k) load_row(k);
+    }
+    __syncthreads();
+    if (tid < GU_ROWS)  // one lane per row
+      vals[tid] = NORM && team.bad ? __builtin_nanf("") : fold_lds_strided<NB>(t + tid, RS);
+    __syncthreads();  // (also: every fold has read t, which the next group's dots rewrite)
+    if (tid < 32) {  // SwiGLU and the block's Q8_0 quantization, one value per lane
+      int8_t q;
+      const float d = quantize_lane32(silu_mul1(vals[tid], vals[32 + tid]), &q);
+      aq[(size_t)g * 32 + tid] = q;
+      if (tid == 0) as[g] = d;
+    }
+    CM_GEMV_STAMP(1, 5, 0)
+    if (!LOOP || gn >= (uint32_t)groups) break;
+    g = gn;
   }
-  CM_GEMV_STAMP(1, 4, 0)
-  __syncthreads();
-  if (tid < GU_ROWS)  // one lane per row
-    vals[tid] = NORM && team.bad ? __builtin_nanf("") : fold_lds_strided<NB>(t + tid, RS);
-  __syncthreads();
-  if (tid < 32) {  // SwiGLU and the block's Q8_0 quantization, one value per lane
-    int8_t q;
-    const float d = quantize_lane32(silu_mul1(vals[tid], vals[32 + tid]), &q);
-    aq[(size_t)blockIdx.x * 32 + tid] = q;
-    if (tid == 0) as[blockIdx.x] = d;
-  }
-  CM_GEMV_STAMP(1, 5, 0)
 }
 
 // Decode-loop state shared by the step's kernels (device memory).

@@ -184,6 +184,47 @@ def test_split_attention_q4k_oproj_matches_oracle(monkeypatch):
         sess.close()
 
 
+def test_gate_up_group_loop_matches_oracle(monkeypatch):
+    """At the C4 FFN shape (hidden 4096, ffn 14336: 448 gate/up row groups, more than the CUs
+    hold 1024-thread workgroups at once), the norm-fused gate/up launch as one workgroup per CU,
+    each taking its groups in turn (the next group's weights loaded during the current one's
+    fold) and, with
+    CAMELID_HIP_GU_LOOP=0, as 448 workgroups in two rounds; per-layer hidden states, logits and
+    tokens of both equal the CPU oracle's, and so do the device loop's tokens."""
+    from oracle.oracle import OracleModel
+    cfg = tiny_config(n_layers=2, hidden=4096, ffn_dim=14336, n_heads=32, n_kv_heads=8, head_dim=128, vocab=2048,
+                      rope_theta=1e6, prompt_len=12)
+    model = SyntheticModel.generate(cfg)
+    prompt = prompt_tokens(cfg)
+    orc = OracleModel(model, 32)
+    orc.prefill(prompt[:-1])
+    want = []
+    tok, pos = int(prompt[-1]), len(prompt) - 1
+    for _ in range(4):
+        tok, hid, lg = orc.forward(tok, pos, hidden=True, logits=True)
+        want.append((tok, hid, lg))
+        pos += 1
+    for loop in ("1", "0"):
+        monkeypatch.setenv("CAMELID_HIP_GU_LOOP", loop)
+        sess = ResidentSession(model, 32)
+        sess.engine.capture_hidden(True)
+        sess.prefill(prompt[:-1])
+        tok, pos = int(prompt[-1]), len(prompt) - 1
+        for step, (t_o, hid_o, lg_o) in enumerate(want):
+            tok = sess.step(tok, pos, logits=True)
+            hid = sess.engine.read_hidden()
+            assert np.array_equal(hid.view(np.uint32), hid_o.view(np.uint32)), (loop, step)
+            assert np.array_equal(sess.engine.last_logits.view(np.uint32), lg_o.view(np.uint32)), (loop, step)
+            assert tok == t_o
+            pos += 1
+        sess.close()
+    # the device-side loop (graph replay) over the same steps
+    monkeypatch.setenv("CAMELID_HIP_GU_LOOP", "1")
+    sess = ResidentSession(model, 32, device_loop=True)
+    assert sess.generate(prompt, len(want)) == [w[0] for w in want]
+    sess.close()
+
+
 def test_split_attention_q8_oproj_in_output_launch_matches_oracle(monkeypatch):
     """At the C4 layer shape (hidden 4096 = 32 heads of 128, 8 KV heads, Q8_0), the decode
     attention split from the first position on as two launches (scores, then output sums):
