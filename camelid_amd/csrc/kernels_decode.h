@@ -464,29 +464,30 @@ struct FsLds {
 };
 
 // Predicted binade (f32 exponent field, at least 1) of a running sum estimated as R after b
-// terms; 0 when the sum may lie in a neighbouring binade (or R is negative or huge).
+// terms; 0 when the sum may lie in a neighbouring binade (or R is negative or huge).  Written
+// without branches (bitwise tests, one select): it runs C times per thread in the
+// classification pass, whose length is set by each wave's instruction issue.
 __device__ __forceinline__ int fs_binade(double R, int b) {
   const uint32_t hi = (uint32_t)__double2hiint(R);
   const int field = (int)(hi >> 20) - 896;  // f64 exponent rebased to f32's
   const uint32_t m20 = hi & 0xfffffu;       // leading 20 mantissa bits
   const uint32_t slack = ((uint32_t)(b + 1) >> 3) + 2;  // (b+1) * 2^-23 relative, in 2^-20 units
-  if (field <= 0) return 1;  // below 2^-126: one binade (ulp 2^-149) down to zero
-  if (field >= 254 || m20 >= 0xfffffu - slack || (field >= 2 && m20 < slack)) return 0;
-  return field;
+  const bool unsure = (field >= 254) | (m20 >= 0xfffffu - slack) | ((field >= 2) & (m20 < slack));
+  // below 2^-126 (field <= 0): one binade (ulp 2^-149) down to zero
+  return field <= 0 ? 1 : (unsure ? 0 : field);
 }
 
 // A special step's replay data: the run of V ulps before it is valid iff the running sum's
 // bits sb satisfy (sb - lo) < lim (unsigned), i.e. sb lies in the run's predicted binade
 // E and sb + V stays below its top; the run then moves the sum to the bits sb + V.
+// (Selects, no branches: it runs for every term of the entries pass.)
 __device__ __forceinline__ void fs_entry(uint32_t V, int E, uint32_t& lo, uint32_t& lim) {
-  if (V == 0u) {  // nothing to apply, nothing to check
-    lo = 0u;
-    lim = 0xffffffffu;
-    return;
-  }
-  lo = E <= 1 ? 0u : (uint32_t)E << 23;            // lowest bits of the binade (E = 0: invalid)
-  const uint32_t span = ((uint32_t)(E + 1) << 23) - lo;  // bits in the binade
-  lim = (E >= 1 && V < span) ? span - V : 0u;
+  const uint32_t lo0 = E <= 1 ? 0u : (uint32_t)E << 23;    // lowest bits of the binade (E = 0: invalid)
+  const uint32_t span = ((uint32_t)(E + 1) << 23) - lo0;  // bits in the binade
+  const uint32_t lim0 = ((E >= 1) & (V < span)) ? span - V : 0u;
+  // V == 0: nothing to apply, nothing to check
+  lo = V == 0u ? 0u : lo0;
+  lim = V == 0u ? 0xffffffffu : lim0;
 }
 
 template <int CTRL, int RMASK>
@@ -594,8 +595,9 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
     const int i = i0 + c;
     const double Ra = R + (double)t[c];
     const int ea = fs_binade(Ra, i + 1);
-    uint32_t dc = SEG_FLAG;
-    if (eb != 0 && eb == ea) dc = seg_d(t[c], eb);
+    // (seg_d unconditionally, then a select: no branch per term)
+    const uint32_t sd = seg_d(t[c], eb > 0 ? eb : 1);
+    const uint32_t dc = ((eb != 0) & (eb == ea)) ? sd : SEG_FLAG;
     const bool special = i < n && dc == SEG_FLAG;
     d[c] = (i < n && !special) ? dc : 0u;
     spm |= (uint32_t)special << c;
@@ -644,20 +646,16 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
       run = rs_x ? run : sat_add(bw, run);
     }
   }
-  // the special steps, in order: the term, and the run before it with its check
+  // the special steps, in order: the term, and the run before it with its check (the entry
+  // formed for every term, one guarded store: no nested branches per term)
 #pragma unroll
   for (int c = 0; c < C; ++c) {
-    if ((spm >> c) & 1u) {
-      if (pos < (uint32_t)FS_CAP) {
-        uint32_t lo, lim;
-        fs_entry(run, (int)((ebp[c >> 2] >> (8 * (c & 3))) & 0xffu), lo, lim);
-        sh_ent[pos] = make_uint4(run, lo, lim, __float_as_uint(t[c]));
-      }
-      ++pos;
-      run = 0u;
-    } else {
-      run = sat_add(run, d[c]);
-    }
+    const bool sp = (spm >> c) & 1u;
+    uint32_t lo, lim;
+    fs_entry(run, (int)((ebp[c >> 2] >> (8 * (c & 3))) & 0xffu), lo, lim);
+    if (sp & (pos < (uint32_t)FS_CAP)) sh_ent[pos] = make_uint4(run, lo, lim, __float_as_uint(t[c]));
+    pos += (uint32_t)sp;
+    run = sp ? 0u : sat_add(run, d[c]);
   }
   if (i0 <= n - 1 && n - 1 < i0 + C) {
     uint32_t lo, lim;
