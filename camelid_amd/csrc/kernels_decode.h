@@ -739,35 +739,6 @@ __device__ __forceinline__ float fold_lds_n(const float* p, float acc = 0.0f) {
   return fold_lds(p, n, acc);
 }
 
-// Serial fold in index order of N terms spaced `stride` floats apart in LDS (one lane; the
-// block-major term layout [block][row] of the norm-fused GEMVs, whose lanes - one per row -
-// then read consecutive words).  Reads run 8 terms ahead of the dependent add chain.
-template <int N>
-__device__ __forceinline__ float fold_lds_strided(const float* p, int stride) {
-  static_assert(N % 8 == 0 && N >= 8, "strided fold length must be a multiple of 8");
-  float a[8], b[8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u) a[u] = p[u * stride];
-  float acc = 0.0f;
-  int n = N;
-  asm volatile("" : "+s"(n));  // keep the fold a loop (registers set the occupancy)
-#pragma unroll 1
-  for (int base = 8; base < n; base += 8) {
-#pragma unroll
-    for (int u = 0; u < 8; ++u) b[u] = p[(base + u) * stride];
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      acc += a[u];
-      a[u] = b[u];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-#pragma unroll
-  for (int u = 0; u < 8; ++u) acc += a[u];
-  return acc;
-}
-
 // Lane-pair exchange (xor 1) through DPP quad_perm [1,0,3,2]; all lanes must be active.
 __device__ __forceinline__ int dpp_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
 
@@ -1202,6 +1173,37 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv(const int8_t* __restrict__ wq,
   }
 }
 
+// Serial fold in index order of N terms spaced `stride` floats apart in LDS (one lane; a
+// block-major term layout [block][row], whose fold lanes - one per row - then read consecutive
+// words), one 4-byte read per term, 8 terms ahead of the dependent add chain: 16 registers
+// where the 16-byte reads of fold_lds take 64 (the looping gate/up GEMV folds with the next
+// group's weights in flight).
+template <int N>
+__device__ __forceinline__ float fold_lds_strided(const float* p, int stride) {
+  static_assert(N % 8 == 0 && N >= 8, "strided fold length must be a multiple of 8");
+  float a[8], b[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) a[u] = p[u * stride];
+  float acc = 0.0f;
+  int n = N;
+  asm volatile("" : "+s"(n));  // keep the fold a loop (registers set the occupancy)
+#pragma unroll 1
+  for (int base = 8; base < n; base += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) b[u] = p[(base + u) * stride];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      acc += a[u];
+      a[u] = b[u];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int u = 0; u < 8; ++u) acc += a[u];
+  return acc;
+}
+
 // ---------------------------------------------------------------------------
 // RMSNorm fused into the GEMV that consumes it: every workgroup normalises the activation
 // itself (the arithmetic of k_rmsnorm_quant) into LDS, so the norm needs no launch of its own.
@@ -1371,9 +1373,9 @@ __device__ __forceinline__ void kv_ahead(const KvAhead& a, int b, int nwg, int l
   asm volatile("" ::"v"(acc));  // keeps the loads
 }
 
-// Row stride of the block-major term layout [block][row] of the norm-fused GEMVs: an odd word
-// count, so that the lanes writing one row's terms (one block each) and the lanes folding the
-// rows (one row each) both touch distinct LDS banks.
+// Row stride of a block-major term layout [block][row]: an odd word count, so that the lanes
+// writing one row's terms (one block each) and the lanes folding the rows (one row each) both
+// touch distinct LDS banks.
 __host__ __device__ constexpr int gemv_row_stride(int rows) { return rows | 1; }
 
 // y = W · rmsnorm(x) for a Q8_0 W [rows][K]: workgroup b takes rows b*rows_per_wg .. (at most
@@ -1388,10 +1390,10 @@ __global__ __launch_bounds__(GN_NT) void k_gemv_norm(const int8_t* __restrict__ 
   constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64;
   constexpr int NT = GN_TEAM_QKV;  // the norm team: waves 0..TW-1; waves TW.. hold the rows
   constexpr int NWV = GN_NT / 64, R = NWV * RPW, C = (K + NT - 1) / NT, TW = NT / 64;
-  constexpr int RS = gemv_row_stride(R);  // terms block-major: t[block * RS + slot]
+  constexpr int ST = gemv_term_stride(NB);  // terms row-major: t[slot * ST + block]
   __shared__ __align__(16) int8_t xl[K];
   __shared__ __align__(16) float xsl[NB];
-  __shared__ __align__(16) float t[NB * RS];
+  __shared__ __align__(16) float t[R * ST];
   __shared__ __align__(16) float yl[NT * C];
   __shared__ __align__(16) float xf[NT * C];
   __shared__ __align__(16) float wf[NT * C];
@@ -1456,12 +1458,12 @@ __global__ __launch_bounds__(GN_NT) void k_gemv_norm(const int8_t* __restrict__ 
       int sacc = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
       sacc += dpp_xor1(sacc);
       if ((lane & 1) == 0 && c < CPR)
-        t[(c >> 1) * RS + sl] = mul_f16_lo((float)sacc, dv[k][i]) * xsl[c >> 1];
+        t[sl * ST + (c >> 1)] = mul_f16_lo((float)sacc, dv[k][i]) * xsl[c >> 1];
     }
   }
   CM_GEMV_STAMP(0, 4, 0)
   __syncthreads();
-  if (tid < nrows) y[row0 + tid] = team.bad ? __builtin_nanf("") : fold_lds_strided<NB>(t + tid, RS);
+  if (tid < nrows) y[row0 + tid] = team.bad ? __builtin_nanf("") : fold_lds_n<NB>(t + tid * ST);
   // the norm team's other waves, idle from here on: the KV rows of the attention that follows
   // into their XCD's L2 (nothing waits on these loads but the end of the kernel, which the
   // folds of wave 0 hold up longer)
@@ -1497,7 +1499,10 @@ __global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ 
                                                     float eps, int8_t* __restrict__ aq, float* __restrict__ as,
                                                     int groups) {
   constexpr int NB = K / 32, CPR = K / 16, IT = (CPR + 63) / 64;
-  constexpr int RS = gemv_row_stride(GU_ROWS);  // terms block-major: t[block * RS + row]
+  // terms row-major, t[row * ST + block], folded with 16-byte reads (fold_lds_n: 1.25
+  // instructions per term); LOOP: block-major, t[block * ST + row], folded with 4-byte reads
+  // (fold_lds_strided: 16 registers, where the next group's weights are in flight)
+  constexpr int ST = LOOP ? gemv_row_stride(GU_ROWS) : gemv_term_stride(NB);
   // row slots per wave: 8 at 512 threads; with NORM the weight waves' slots come first (up to
   // K = 3072 six each: all 64 rows stream during the norm; at 4096, where six rows of
   // registers do not fit, four each and the norm team's slots take the last 16 rows)
@@ -1508,7 +1513,7 @@ __global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ 
   static_assert(NB % 4 == 0 && (NORM || GU_ROWS % (NT / 64) == 0), "compile-time GEMV widths are multiples of 128");
   __shared__ __align__(16) int8_t xl[K];
   __shared__ __align__(16) float xsl[NB];
-  __shared__ __align__(16) float t[NB * RS];
+  __shared__ __align__(16) float t[LOOP ? NB * ST : GU_ROWS * ST];
   __shared__ __align__(16) float vals[GU_ROWS];
   __shared__ __align__(16) float yl[NORM ? GN_TEAM * CT : 4];
   __shared__ __align__(16) float xf[NORM ? GN_TEAM * CT : 4];
@@ -1586,7 +1591,7 @@ __global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ 
         int sacc = dot4x4(wv[k][i], reinterpret_cast<const int4*>(xl)[cc], 0);
         sacc += dpp_xor1(sacc);
         if ((lane & 1) == 0 && c < CPR)
-          t[(c >> 1) * RS + lr] = mul_f16_lo((float)sacc, dv[k][i]) * xsl[c >> 1];
+          t[LOOP ? (c >> 1) * ST + lr : lr * ST + (c >> 1)] = mul_f16_lo((float)sacc, dv[k][i]) * xsl[c >> 1];
       }
     }
     CM_GEMV_STAMP(1, 4, 0)
@@ -1599,7 +1604,8 @@ __global__ __launch_bounds__(NT) void k_gemv_gu_silu(const int8_t* __restrict__ 
     }
     __syncthreads();
     if (tid < GU_ROWS)  // one lane per row
-      vals[tid] = NORM && team.bad ? __builtin_nanf("") : fold_lds_strided<NB>(t + tid, RS);
+      vals[tid] = NORM && team.bad ? __builtin_nanf("")
+                                   : (LOOP ? fold_lds_strided<NB>(t + tid, ST) : fold_lds_n<NB>(t + tid * ST));
     __syncthreads();  // (also: every fold has read t, which the next group's dots rewrite)
     if (tid < 32) {  // SwiGLU and the block's Q8_0 quantization, one value per lane
       int8_t q;
