@@ -2860,10 +2860,24 @@ __device__ __forceinline__ void att_scores_body(
     else
       g_sc[(size_t)h * kvs + p] = sv;
     lmax = sv;
-  } else if (p == pos) {  // this token's own key, from LDS
+  } else if (p == pos) {  // this token's own key, from LDS (16-byte reads, 8 products ahead of their adds)
     float acc = 0.0f;
+    const float4* q4 = reinterpret_cast<const float4*>(qs);
+    const float4* k4 = reinterpret_cast<const float4*>(kn);
 #pragma unroll
-    for (int d = 0; d < HD; ++d) acc += qs[d] * kn[d];
+    for (int u = 0; u < HD / 8; ++u) {
+      const float4 qa = q4[2 * u], qb = q4[2 * u + 1], ka = k4[2 * u], kb = k4[2 * u + 1];
+      const float p0 = qa.x * ka.x, p1 = qa.y * ka.y, p2 = qa.z * ka.z, p3 = qa.w * ka.w;
+      const float p4 = qb.x * kb.x, p5 = qb.y * kb.y, p6 = qb.z * kb.z, p7 = qb.w * kb.w;
+      acc += p0;
+      acc += p1;
+      acc += p2;
+      acc += p3;
+      acc += p4;
+      acc += p5;
+      acc += p6;
+      acc += p7;
+    }
     const float sv = acc * scale;
     if (TAG)
       st_agent64(sc_t + (size_t)h * kvs + p, tg | __float_as_uint(sv));
