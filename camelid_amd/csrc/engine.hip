@@ -1221,8 +1221,8 @@ void run_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cos_base,
     const cm::Prefetch pf = ahead(L.p[6]);
     const bool k8 = is_k(6);
     CM_LAUNCH(cm::k_silu_mul_quant, dim3((d.ffn_dim + 255) / 256 + (pf.a_lines ? PREFETCH_WGS : 0)), dim3(256), 0, s,
-              e->gu, (int)d.ffn_dim, e->xq,
-              e->xs, (float*)nullptr, pf, k8 ? e->kd : nullptr, k8 ? e->kq : nullptr, k8 ? e->kbs : nullptr);
+              e->gu, (int)d.ffn_dim, k8 ? (int8_t*)nullptr : e->xq, k8 ? (float*)nullptr : e->xs, (float*)nullptr,
+              pf, k8 ? e->kd : nullptr, k8 ? e->kq : nullptr, k8 ? e->kbs : nullptr);
   }
   proj(e, L.p[6], e->h, e->h);
 }
@@ -1606,9 +1606,9 @@ void prefill_layer_generic(camelid_hip_engine* e, uint32_t l, const float* cosv,
   proj_rows(L.p[4], e->pf_gu, 2 * F, nullptr);
   if (!L.gu_stacked) proj_rows(L.p[5], e->pf_gu + F, 2 * F, nullptr);
   const bool k8 = L.p[6].quant != CAMELID_Q8_0;
-  CM_LAUNCH(cm::k_silu_mul_quant, dim3((F + 255) / 256, T), dim3(256), 0, s, e->pf_gu, (int)F, e->pf_xq, e->pf_xs,
-            (float*)nullptr, cm::Prefetch{}, k8 ? e->pf_kd : nullptr, k8 ? e->pf_kq : nullptr,
-            k8 ? e->pf_kbs : nullptr);
+  CM_LAUNCH(cm::k_silu_mul_quant, dim3((F + 255) / 256, T), dim3(256), 0, s, e->pf_gu, (int)F,
+            k8 ? (int8_t*)nullptr : e->pf_xq, k8 ? (float*)nullptr : e->pf_xs, (float*)nullptr, cm::Prefetch{},
+            k8 ? e->pf_kd : nullptr, k8 ? e->pf_kq : nullptr, k8 ? e->pf_kbs : nullptr);
   proj_rows(L.p[6], e->pf_h, H, e->pf_h);
 }
 
@@ -2578,19 +2578,10 @@ int camelid_hip_rmsnorm_q8_k(const float* x, const float* w, uint32_t n, float e
 int camelid_hip_silu_mul_q8_k(const float* gu, uint32_t n, float* yd, int8_t* yq, int32_t* ybs, void* stream) {
   if (!gu || !yd || !yq || !ybs) return fail(nullptr, "null argument");
   if (n == 0 || n % 256) return fail(nullptr, "n must be a multiple of 256");
-  int8_t* xq = nullptr;
-  float* xs = nullptr;
-  if (hipMalloc(&xq, n) != hipSuccess || hipMalloc(&xs, n / 32 * 4) != hipSuccess) {
-    (void)hipFree(xq);
-    return fail(nullptr, "scratch allocation failed");
-  }
-  hipLaunchKernelGGL(cm::k_silu_mul_quant, dim3(n / 256), dim3(256), 0, (hipStream_t)stream, gu, (int)n, xq, xs,
-                     (float*)nullptr, prefetch_of((const Q8Mat*)nullptr), yd, yq, ybs);
-  const int rc = launch_status("silu_mul_q8_k");
-  (void)hipStreamSynchronize((hipStream_t)stream);
-  (void)hipFree(xq);
-  (void)hipFree(xs);
-  return rc;
+  hipLaunchKernelGGL(cm::k_silu_mul_quant, dim3(n / 256), dim3(256), 0, (hipStream_t)stream, gu, (int)n,
+                     (int8_t*)nullptr, (float*)nullptr, (float*)nullptr, prefetch_of((const Q8Mat*)nullptr), yd, yq,
+                     ybs);
+  return launch_status("silu_mul_q8_k");
 }
 
 // The kernel-level entry points that read the position from device memory (d_pos): the

@@ -1890,7 +1890,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float* __restrict__
   if ((i & 31) == 0) xs[i >> 5] = d;
 }
 
-// SwiGLU (tensor/mod.rs:1943-1967) + Q8_0 quantization.  gu = [gate(n) | up(n)].
+// SwiGLU (tensor/mod.rs:1943-1967) + Q8_0 quantization (skipped with xq null).  gu = [gate(n) | up(n)].
 // kd (optional, n % 256 == 0): also the Q8_K quantization of the activation, one block per
 // workgroup.  gridDim.y rows (prefill chunks): row y at gu + y * 2n, outputs likewise.
 __global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict__ gu, int n, int8_t* __restrict__ xq,
@@ -1919,10 +1919,12 @@ __global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict_
   if (i >= n) return;  // uniform per 32-lane group
   const float a = silu_mul1(gu[i], gu[n + i]);
   if (act_out) act_out[i] = a;
-  int8_t q;
-  const float d = quantize_lane32(a, &q);
-  xq[i] = q;
-  if ((i & 31) == 0) xs[i >> 5] = d;
+  if (xq) {  // (null: only the Q8_K activation is read next)
+    int8_t q;
+    const float d = quantize_lane32(a, &q);
+    xq[i] = q;
+    if ((i & 31) == 0) xs[i >> 5] = d;
+  }
   if (kd) quantize_q8k_wg256(a, kq + (size_t)blockIdx.x * 256, kbs + (size_t)blockIdx.x * 8, kd + blockIdx.x);
 }
 

@@ -286,7 +286,7 @@ int camelid_hip_quantize_q8_k(const float* x, uint32_t n, float* yd, int8_t* yq,
 int camelid_hip_rmsnorm_q8_k(const float* x, const float* w, uint32_t n, float eps, float* yd,
                              int8_t* yq, int32_t* ybs, void* stream);
 /* silu_mul + quantize_q8k (CPU tensor/mod.rs:1943-1967 then inference.rs:17564-17599), gu =
- * [gate|up], n % 256 == 0.  (Test hook; allocates its own Q8_0 scratch.) */
+ * [gate|up], n % 256 == 0.  (Test hook; asynchronous on stream, allocates nothing.) */
 int camelid_hip_silu_mul_q8_k(const float* gu, uint32_t n, float* yd, int8_t* yq, int32_t* ybs,
                               void* stream);
 /* Host split of K-quant wire rows [rows][k/256 superblocks] into the device planes the
