@@ -14,6 +14,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include "device_math.h"
+#include <type_traits>
 
 namespace cm {
 
@@ -541,7 +542,7 @@ struct TeamBar {
   }
 };
 
-template <int NT, int C, typename Bar = WgBar>
+template <int NT, int C, bool LINE = false, typename Bar = WgBar>
 __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const float* v, int n, FsLds<NT>& fs,
                                                      Bar&& bar = Bar{}, int stamp_kind = -1) {
   (void)stamp_kind;  // (the measurement build: stamps 8..11 of the norm-fused GEMVs after each barrier)
@@ -683,18 +684,22 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
       g_gemv_stamps[(stamp_kind * GEMV_STAMP_WGS + blockIdx.x) * GEMV_NSTAMP + 12] = (uint64_t)tot;
 #endif
     float s = 0.0f;
-    uint32_t bad = tot > FS_CAP;
+    // (a mask flag for the straight-line replay; a 0/1 word for the loop, as that form measured
+    // faster in the attention and K-quant norm sums)
+    typename std::conditional<LINE, bool, uint32_t>::type bad = tot > FS_CAP;
     if (!bad && tot > 0) {
       auto step = [&](const uint4& q) {
         const uint32_t sb = __float_as_uint(s);
-        bad |= (uint32_t)!(sb - q.y < q.z);
+        bad |= sb - q.y >= q.z;
         s = __uint_as_float(sb + q.x) + __uint_as_float(q.w);
       };
       const int nb = (tot + 3) >> 2;  // blocks of 4 entries (nb <= FS_CAP / 4)
       uint4 A[4], B[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) A[u] = sh_ent[u];
-      for (int k = 0; k < nb; k += 2) {
+      // two blocks: A's steps while B's entries are read, B's while the next A's are; false
+      // once the last block is applied
+      auto pair = [&](int k) -> bool {
         if (k + 1 < nb) {
 #pragma unroll
           for (int u = 0; u < 4; ++u) B[u] = sh_ent[4 * (k + 1) + u];
@@ -702,7 +707,7 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < 4; ++u) step(A[u]);
-        if (k + 1 >= nb) break;
+        if (k + 1 >= nb) return false;
         if (k + 2 < nb) {
 #pragma unroll
           for (int u = 0; u < 4; ++u) A[u] = sh_ent[4 * (k + 2) + u];
@@ -710,11 +715,26 @@ __device__ __forceinline__ float inorder_sum_onepass(const float (&t)[C], const 
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < 4; ++u) step(B[u]);
+        return k + 2 < nb;
+      };
+      // LINE: the first 32 entries as straight-line code (the two register sets alternate
+      // without copies), any beyond as a loop; else all as a loop (less code where the sum is
+      // not on the launch's critical path)
+      bool more = true;
+      int k0 = 0;
+      if constexpr (LINE) {
+#pragma unroll
+        for (int k = 0; k < 8; k += 2)
+          if (more) more = pair(k);
+        k0 = 8;
       }
+      if (more)
+        for (int k = k0; k < nb && pair(k); k += 2) {
+        }
     }
     {
       const uint32_t sb = __float_as_uint(s);
-      bad |= (uint32_t)!(sb - sh_end[1] < sh_end[2]);
+      bad |= sb - sh_end[1] >= sh_end[2];
       s = __uint_as_float(sb + sh_end[0]);
     }
     if (bad) s = fold_lds_lean(v, n);
@@ -1256,7 +1276,7 @@ __device__ __forceinline__ void norm_scale(const float (&xv)[C], const float (&w
   if (stamp_kind >= 0) {
     CM_GEMV_STAMP(stamp_kind, 6, 0)  // (the measurement build: x and w have arrived)
   }
-  const float ss = inorder_sum_onepass<NT, C>(t, yl, n, fs, bar, stamp_kind);
+  const float ss = inorder_sum_onepass<NT, C, true>(t, yl, n, fs, bar, stamp_kind);
   if (tid == 0) *s_scale = 1.0f / sqrtf(ss / (float)n + eps);
   if (stamp_kind >= 0) {
     CM_GEMV_STAMP(stamp_kind, 7, 0)  // the sum of squares is known
